@@ -1,0 +1,146 @@
+/*
+ * tl_attn.h -- C ABI of the MI355X (gfx950) attention hot path of
+ * truellm-engine: paged-attention decode (single pass and split-K with a
+ * log-sum-exp reduce), reshape_and_cache into the block-table KV pool, the
+ * FP8 E4M3 KV variant, the reference KIVI vector codec, paged KIVI INT4 KV
+ * and chunked prefill.
+ *
+ * Conventions
+ *  - Plain pointers and sizes; every pointer is device memory unless noted.
+ *  - `stream` is a hipStream_t passed as void* (NULL = default stream).
+ *    Every call is asynchronous on that stream; nothing here allocates,
+ *    frees or synchronises.
+ *  - Return value: tl_status (0 = ok).  Bad shapes, NULL pointers, misaligned
+ *    buffers and unsupported combinations are reported, never asserted;
+ *    tl_last_error_string() describes the last failure of the calling thread.
+ *  - KV pools use the reference layout [num_blocks, num_kv_heads, head_size,
+ *    block_size] (cache_kernels.cu:74-83), block tables are int32
+ *    [num_seqs, max_blocks_per_seq] with -1 for holes, seq_lens int32.
+ */
+#ifndef TL_ATTN_H
+#define TL_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TL_ABI_VERSION 1
+
+/* Mirrors truellm::ErrorCode (include/truellm/types.h:20-32). */
+typedef enum tl_status {
+  TL_OK = 0,
+  TL_ERR_INVALID_ARGUMENT = 1,
+  TL_ERR_NOT_IMPLEMENTED = 3,
+  TL_ERR_BACKEND = 5,
+  TL_ERR_INTERNAL = 99
+} tl_status;
+
+/* F32/F16/BF16 mirror truellm::DataType (include/truellm/types.h:47-60);
+ * FP8_E4M3 is OCP E4M3 (max 448), which the reference only sizes for
+ * (cuda_allocator.h:179-182). */
+typedef enum tl_dtype {
+  TL_DTYPE_F32 = 0,
+  TL_DTYPE_F16 = 1,
+  TL_DTYPE_BF16 = 2,
+  TL_DTYPE_FP8_E4M3 = 32
+} tl_dtype;
+
+/* Which KV head a q head reads.  MODULO is the reference kernels' mapping
+ * (paged_attention_v1.cu:46); GROUPED is the model's (megakernel.cu:271-277). */
+typedef enum tl_gqa_map { TL_GQA_MODULO = 0, TL_GQA_GROUPED = 1 } tl_gqa_map;
+
+int tl_abi_version(void);
+const char* tl_last_error_string(void);
+
+/* ------------------------------------------------------------------------
+ * Paged-attention decode
+ * --------------------------------------------------------------------- */
+
+typedef struct tl_decode_desc {
+  int32_t num_seqs;            /* S */
+  int32_t num_heads;           /* H (q heads); H % num_kv_heads == 0 */
+  int32_t num_kv_heads;
+  int32_t head_size;           /* 64, 128 or 256 (128 for FP8/F32 KV) */
+  int32_t block_size;          /* 16, or 32 with head_size 128 */
+  int32_t max_blocks_per_seq;  /* row stride of block_tables */
+  int32_t num_blocks;          /* pool capacity N; table entries >= N are holes */
+  int32_t q_dtype;             /* q and out: F16, BF16 (or F32 with F32 KV) */
+  int32_t kv_dtype;            /* F16, BF16, F32 (= q_dtype) or FP8_E4M3 */
+  int32_t gqa_map;             /* tl_gqa_map */
+  int32_t partition_tokens;    /* 0 = choose, -1 = single pass, else k*512 */
+  float scale;                 /* softmax scale, normally 1/sqrt(head_size) */
+  float k_scale, v_scale;      /* FP8 dequant scales (x = code * scale); else ignored */
+} tl_decode_desc;
+
+/* Bytes of fp32 workspace tl_paged_attention_decode needs for split-K at
+ * max_context_len (0 when it will run single pass). */
+size_t tl_paged_attention_workspace_bytes(const tl_decode_desc* desc, int32_t max_context_len);
+
+/* out[s, h, :] = softmax(scale * q[s, h] . K^T) V over seq_lens[s] tokens.
+ * q, out: [S, H, head_size] in q_dtype.  A sequence of length 0 gets zeros.
+ * workspace may be NULL when the query above returned 0. */
+int tl_paged_attention_decode(const tl_decode_desc* desc, void* out, const void* q,
+                              const void* k_cache, const void* v_cache,
+                              const int32_t* block_tables, const int32_t* seq_lens,
+                              int32_t max_context_len, void* workspace,
+                              size_t workspace_bytes, void* stream);
+
+/* Replaces paged_attention_v1 (paged_attention_v1.cu:177-213): single pass,
+ * same arguments plus the explicit sizes a TrueBuffer carried. */
+int tl_paged_attention_v1(void* out, const void* q, const void* k_cache, const void* v_cache,
+                          const int32_t* block_tables, const int32_t* seq_lens,
+                          int32_t num_seqs, int32_t num_heads, int32_t num_kv_heads,
+                          int32_t head_size, int32_t block_size, int32_t max_blocks_per_seq,
+                          int32_t num_blocks, float scale, int32_t dtype, int32_t gqa_map,
+                          void* stream);
+
+/* Replaces paged_attention_v2 (paged_attention_v2.cu:176-251): split-K over
+ * partitions of 32 blocks with caller scratch exp_sums / max_logits
+ * [S, H, P] fp32 and tmp_out [S, H, P, head_size] in dtype, where
+ * P = ceil(max_context_len / (32 * block_size)) (the caller's sizing,
+ * cuda_engine.cpp:276-285). */
+int tl_paged_attention_v2(void* out, float* exp_sums, float* max_logits, void* tmp_out,
+                          const void* q, const void* k_cache, const void* v_cache,
+                          const int32_t* block_tables, const int32_t* seq_lens,
+                          int32_t num_seqs, int32_t num_heads, int32_t num_kv_heads,
+                          int32_t head_size, int32_t block_size, int32_t max_blocks_per_seq,
+                          int32_t num_blocks, float scale, int32_t dtype, int32_t gqa_map,
+                          int32_t max_context_len, void* stream);
+
+/* ------------------------------------------------------------------------
+ * KV-cache writes
+ * --------------------------------------------------------------------- */
+
+/* Replaces reshape_and_cache (cache_kernels.cu:202-232): key/value
+ * [T, n_kv, head_size] -> k_cache/v_cache [N, n_kv, head_size, block_size]
+ * at slot_mapping[t] (int32, < 0 skipped, block >= N skipped).  dtype F16,
+ * BF16 or F32, same for sources and pools (bit copy).  head_size % 8 == 0. */
+int tl_reshape_and_cache(const void* key, const void* value, void* k_cache, void* v_cache,
+                         const int32_t* slot_mapping, int32_t num_tokens, int32_t num_kv_heads,
+                         int32_t head_size, int32_t block_size, int32_t num_blocks,
+                         int32_t dtype, void* stream);
+
+/* FP8 pool variant (the engine's use_fp8_kv, cuda_allocator.h:179-182, with
+ * the quantisation of convert_fp8, cache_kernels.cu:181-193):
+ * code = e4m3_rne_satfinite(x * (1/scale)), scale 0 treated as 1.
+ * src_dtype F16 or BF16. */
+int tl_reshape_and_cache_fp8(const void* key, const void* value, int32_t src_dtype,
+                             uint8_t* k_cache, uint8_t* v_cache, const int32_t* slot_mapping,
+                             int32_t num_tokens, int32_t num_kv_heads, int32_t head_size,
+                             int32_t block_size, int32_t num_blocks, float k_scale,
+                             float v_scale, void* stream);
+
+/* Per-tensor E4M3 scale: *scale_out (device fp32) = absmax(x) / 448, the
+ * convention of per_token_fp8_quant_kernel (fp8_gemm.cu:80-84) applied to a
+ * whole tensor.  x: n elements of dtype F16, BF16 or F32. */
+int tl_fp8_absmax_scale(const void* x, int32_t dtype, int64_t n, float* scale_out,
+                        void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TL_ATTN_H */

@@ -1,0 +1,731 @@
+/*
+ * tl_oracle.c -- CPU oracle for the truellm-engine attention hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY (see tl_oracle.h): the checker for tests/,
+ * __graft_entry__.smoke() and bench.py's cpu_baseline leg.  Never linked into
+ * or called by the product library.
+ *
+ * Built with -ffp-contract=off so every fp32 operation below rounds exactly
+ * where it is written; the one fused multiply-add the reference relies on
+ * (kivi_cache.cu:190, contracted by nvcc's default -fmad=true) is an explicit
+ * fmaf().
+ */
+#include "tl_oracle.h"
+
+#include <float.h>
+#include <math.h>
+#include <pthread.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ========================================================================
+ * Scalar conversions
+ * ====================================================================== */
+
+static uint32_t f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+static float u2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+
+/* IEEE binary16, round to nearest even, overflow to inf, NaN kept quiet. */
+uint16_t orc_f32_to_f16(float f)
+{
+    uint32_t x = f2u(f);
+    uint16_t sign = (uint16_t)((x >> 16) & 0x8000u);
+    uint32_t ax = x & 0x7fffffffu;
+    if (ax > 0x7f800000u) return (uint16_t)(sign | 0x7e00u | ((ax >> 13) & 0x3ffu));
+    if (ax >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u);   /* >= 65520 */
+    if (ax >= 0x38800000u) {                                     /* >= 2^-14 */
+        uint32_t mant = ax & 0x7fffffu;
+        uint32_t e = (ax >> 23) - 127 + 15;
+        uint32_t h = (e << 10) | (mant >> 13);
+        uint32_t rem = mant & 0x1fffu;
+        if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) h++;
+        return (uint16_t)(sign | h);
+    }
+    /* subnormal: units of 2^-24; the product is exact in double and rint
+     * rounds half to even under the default rounding mode. */
+    double v = rint((double)u2f(ax) * 16777216.0);
+    return (uint16_t)(sign | (uint16_t)v);
+}
+
+float orc_f16_to_f32(uint16_t h)
+{
+    uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    uint32_t e = (h >> 10) & 0x1fu, m = h & 0x3ffu;
+    if (e == 0) {
+        float v = (float)m * (1.0f / 16777216.0f);
+        return sign ? -v : v;
+    }
+    if (e == 31) return u2f(sign | 0x7f800000u | (m << 13));
+    return u2f(sign | ((e - 15 + 127) << 23) | (m << 13));
+}
+
+uint16_t orc_f32_to_bf16(float f)
+{
+    uint32_t x = f2u(f);
+    if ((x & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((x >> 16) | 0x40u);
+    x += 0x7fffu + ((x >> 16) & 1u);
+    return (uint16_t)(x >> 16);
+}
+
+float orc_bf16_to_f32(uint16_t h) { return u2f((uint32_t)h << 16); }
+
+/* OCP 8-bit E4M3 ("E4M3FN"): bias 7, no infinities, S.1111.111 = NaN,
+ * max finite 0x7E = 448.  Round to nearest even; magnitudes >= 448 (and
+ * infinities) saturate to 448. */
+uint8_t orc_f32_to_e4m3(float f)
+{
+    uint8_t sign = (f2u(f) >> 24) & 0x80u;
+    if (isnan(f)) return (uint8_t)(sign | 0x7fu);
+    double a = fabs((double)f);
+    if (a >= 448.0) return (uint8_t)(sign | 0x7eu);
+    if (a < 0.015625) {                        /* below 2^-6: subnormal grid 2^-9 */
+        double q = rint(a * 512.0);            /* 0..8; 8 encodes 2^-6 exactly */
+        return (uint8_t)(sign | (uint8_t)q);
+    }
+    int e;
+    double fr = frexp(a, &e);                  /* a = fr * 2^e, fr in [0.5, 1) */
+    int ue = e - 1;                            /* a = 1.m * 2^ue */
+    double m = rint((fr * 2.0 - 1.0) * 8.0);   /* 0..8 */
+    if (m >= 8.0) { m = 0.0; ue++; }
+    return (uint8_t)(sign | (uint8_t)((ue + 7) << 3) | (uint8_t)m);
+}
+
+float orc_e4m3_to_f32(uint8_t v)
+{
+    float s = (v & 0x80u) ? -1.0f : 1.0f;
+    int e = (v >> 3) & 0xf, m = v & 7;
+    if (e == 15 && m == 7) return NAN;
+    if (e == 0) return s * ldexpf((float)m, -9);
+    return s * ldexpf(1.0f + (float)m / 8.0f, e - 7);
+}
+
+static double load_elem(const void* base, int dtype, int64_t i)
+{
+    switch (dtype) {
+    case ORC_F32:  return ((const float*)base)[i];
+    case ORC_F16:  return orc_f16_to_f32(((const uint16_t*)base)[i]);
+    case ORC_BF16: return orc_bf16_to_f32(((const uint16_t*)base)[i]);
+    case ORC_FP8:  return orc_e4m3_to_f32(((const uint8_t*)base)[i]);
+    default:       return NAN;
+    }
+}
+
+static float load_f32(const void* base, int dtype, int64_t i)
+{
+    return (float)load_elem(base, dtype, i);
+}
+
+static void store_elem(void* base, int dtype, int64_t i, float v)
+{
+    switch (dtype) {
+    case ORC_F32:  ((float*)base)[i] = v; break;
+    case ORC_F16:  ((uint16_t*)base)[i] = orc_f32_to_f16(v); break;
+    case ORC_BF16: ((uint16_t*)base)[i] = orc_f32_to_bf16(v); break;
+    case ORC_FP8:  ((uint8_t*)base)[i] = orc_f32_to_e4m3(v); break;
+    default: break;
+    }
+}
+
+void orc_convert(const void* src, int src_dtype, void* dst, int dst_dtype,
+                 int64_t n, float mul)
+{
+    for (int64_t i = 0; i < n; ++i) {
+        float v = load_f32(src, src_dtype, i);
+        if (src_dtype == ORC_FP8 || dst_dtype == ORC_FP8) v = v * mul;
+        store_elem(dst, dst_dtype, i, v);
+    }
+}
+
+/* ========================================================================
+ * reshape_and_cache  (cache_kernels.cu:47-94)
+ *   blk = slot / bs, off = slot % bs
+ *   cache[blk][h][e][off] = src[t][h][e]
+ * ====================================================================== */
+
+void orc_reshape_and_cache(const void* key, const void* value,
+                           void* k_cache, void* v_cache,
+                           const int32_t* slot_mapping, int num_tokens,
+                           int num_kv_heads, int head_size, int block_size,
+                           int elem_bytes)
+{
+    for (int t = 0; t < num_tokens; ++t) {
+        int32_t slot = slot_mapping[t];
+        if (slot < 0) continue;                       /* cache_kernels.cu:68-69 */
+        int64_t blk = slot / block_size, off = slot % block_size;
+        for (int h = 0; h < num_kv_heads; ++h)
+            for (int e = 0; e < head_size; ++e) {
+                int64_t dst = ((blk * num_kv_heads + h) * head_size + e) * block_size + off;
+                int64_t src = ((int64_t)t * num_kv_heads + h) * head_size + e;
+                memcpy((char*)k_cache + dst * elem_bytes, (const char*)key + src * elem_bytes, elem_bytes);
+                memcpy((char*)v_cache + dst * elem_bytes, (const char*)value + src * elem_bytes, elem_bytes);
+            }
+    }
+}
+
+void orc_reshape_and_cache_fp8(const void* key, const void* value, int src_dtype,
+                               uint8_t* k_cache, uint8_t* v_cache,
+                               const int32_t* slot_mapping, int num_tokens,
+                               int num_kv_heads, int head_size, int block_size,
+                               float k_scale, float v_scale)
+{
+    /* multiplier = 1/scale in fp32, as fp8_gemm.cu:89-93 (scale 0 -> 1) */
+    float km = 1.0f / (k_scale == 0.0f ? 1.0f : k_scale);
+    float vm = 1.0f / (v_scale == 0.0f ? 1.0f : v_scale);
+    for (int t = 0; t < num_tokens; ++t) {
+        int32_t slot = slot_mapping[t];
+        if (slot < 0) continue;
+        int64_t blk = slot / block_size, off = slot % block_size;
+        for (int h = 0; h < num_kv_heads; ++h)
+            for (int e = 0; e < head_size; ++e) {
+                int64_t dst = ((blk * num_kv_heads + h) * head_size + e) * block_size + off;
+                int64_t src = ((int64_t)t * num_kv_heads + h) * head_size + e;
+                k_cache[dst] = orc_f32_to_e4m3(load_f32(key, src_dtype, src) * km);
+                v_cache[dst] = orc_f32_to_e4m3(load_f32(value, src_dtype, src) * vm);
+            }
+    }
+}
+
+/* ========================================================================
+ * Paged attention, intended semantics (double accumulation)
+ * ====================================================================== */
+
+static int kv_head_of(int head, int num_heads, int num_kv_heads, int gqa_map)
+{
+    if (gqa_map == ORC_GQA_GROUPED) return head / (num_heads / num_kv_heads);
+    return head % num_kv_heads;
+}
+
+/* Element (token position t, dim e) of one sequence's gathered K or V;
+ * returns 0 when the table entry is negative (token skipped). */
+static int gather_ok(const int32_t* row, int t, int block_size, int64_t* phys)
+{
+    int32_t p = row[t / block_size];
+    if (p < 0) return 0;
+    *phys = p;
+    return 1;
+}
+
+void orc_paged_attention(double* out, const void* q, int q_dtype,
+                         const void* k_cache, const void* v_cache, int kv_dtype,
+                         float k_scale, float v_scale,
+                         const int32_t* block_tables, int max_blocks_per_seq,
+                         const int32_t* seq_lens, int num_seqs, int num_heads,
+                         int num_kv_heads, int head_size, int block_size,
+                         float scale, int gqa_map, int partition_tokens)
+{
+    double ks = (kv_dtype == ORC_FP8) ? (double)k_scale : 1.0;
+    double vs = (kv_dtype == ORC_FP8) ? (double)v_scale : 1.0;
+    int max_len = 0;
+    for (int s = 0; s < num_seqs; ++s) if (seq_lens[s] > max_len) max_len = seq_lens[s];
+    double* sc = (double*)malloc(sizeof(double) * (max_len > 0 ? max_len : 1));
+    unsigned char* ok = (unsigned char*)malloc(max_len > 0 ? max_len : 1);
+    double* acc = (double*)malloc(sizeof(double) * head_size);
+    double* pacc = (double*)malloc(sizeof(double) * head_size);
+
+    for (int s = 0; s < num_seqs; ++s) {
+        int L = seq_lens[s];
+        const int32_t* row = block_tables + (int64_t)s * max_blocks_per_seq;
+        for (int h = 0; h < num_heads; ++h) {
+            int kvh = kv_head_of(h, num_heads, num_kv_heads, gqa_map);
+            const int64_t qoff = ((int64_t)s * num_heads + h) * head_size;
+            double* o = out + qoff;
+            for (int t = 0; t < L; ++t) {
+                int64_t phys;
+                ok[t] = (unsigned char)gather_ok(row, t, block_size, &phys);
+                if (!ok[t]) continue;
+                int64_t base = (phys * num_kv_heads + kvh) * head_size * block_size + t % block_size;
+                double dot = 0.0;
+                for (int e = 0; e < head_size; ++e)
+                    dot += load_elem(q, q_dtype, qoff + e) *
+                           (load_elem(k_cache, kv_dtype, base + (int64_t)e * block_size) * ks);
+                sc[t] = dot * (double)scale;
+            }
+            int P = (partition_tokens > 0) ? (L + partition_tokens - 1) / partition_tokens : 1;
+            int PT = (partition_tokens > 0) ? partition_tokens : (L > 0 ? L : 1);
+            /* global accumulators for the LSE merge */
+            double gm = -INFINITY, gl = 0.0;
+            for (int e = 0; e < head_size; ++e) acc[e] = 0.0;
+            for (int p = 0; p < P; ++p) {
+                int t0 = p * PT, t1 = t0 + PT < L ? t0 + PT : L;
+                double m = -INFINITY, l = 0.0;
+                for (int t = t0; t < t1; ++t) if (ok[t] && sc[t] > m) m = sc[t];
+                if (m == -INFINITY) continue;               /* empty partition */
+                for (int e = 0; e < head_size; ++e) pacc[e] = 0.0;
+                for (int t = t0; t < t1; ++t) {
+                    if (!ok[t]) continue;
+                    int64_t phys = 0; gather_ok(row, t, block_size, &phys);
+                    int64_t base = (phys * num_kv_heads + kvh) * head_size * block_size + t % block_size;
+                    double w = exp(sc[t] - m);
+                    l += w;
+                    for (int e = 0; e < head_size; ++e)
+                        pacc[e] += w * (load_elem(v_cache, kv_dtype, base + (int64_t)e * block_size) * vs);
+                }
+                /* partition result (m, l, pacc/l) merged by log-sum-exp */
+                double nm = m > gm ? m : gm;
+                double a = (gm == -INFINITY) ? 0.0 : exp(gm - nm);
+                double b = exp(m - nm);
+                for (int e = 0; e < head_size; ++e)
+                    acc[e] = acc[e] * a + (pacc[e] / l) * (l * b);
+                gl = gl * a + l * b;
+                gm = nm;
+            }
+            for (int e = 0; e < head_size; ++e) o[e] = (gl > 0.0) ? acc[e] / gl : 0.0;
+        }
+    }
+    free(sc); free(ok); free(acc); free(pacc);
+}
+
+/* ---- literal v1 (paged_attention_v1.cu:31-135, attention_utils.cuh:47-68,
+ *      reduce_kernel_utils.cuh:41-73) -------------------------------------
+ * Only warp-0 lanes t < tokens_in_block (<= 32) carry tokens.  After each
+ * block every warp-0 lane holds (M_b, S_b) with
+ *   S_b = 32 * S_{b-1} * e^{M_{b-1}-M_b} + sum_t e^{qk_t - M_b}
+ * and thread d writes only its own out_acc[d]:
+ *   out[d] = sum_b [d%128 < T_b] e^{qk_{b,d%128}-M_b}/S_b * V[b][d][d%128]. */
+void orc_paged_attention_literal_v1(float* out, const void* q, const void* k_cache,
+                                    const void* v_cache, int dtype,
+                                    const int32_t* block_tables, int max_blocks_per_seq,
+                                    const int32_t* seq_lens, int num_seqs, int num_heads,
+                                    int num_kv_heads, int head_size, int block_size,
+                                    float scale)
+{
+    float qk[128];
+    for (int s = 0; s < num_seqs; ++s) {
+        int L = seq_lens[s];
+        if (L == 0) continue;
+        for (int h = 0; h < num_heads; ++h) {
+            int kvh = h % num_kv_heads;
+            const int64_t qoff = ((int64_t)s * num_heads + h) * head_size;
+            float M = -1e20f, S = 0.f;
+            float* o = out + qoff;
+            for (int d = 0; d < head_size; ++d) o[d] = 0.f;
+            int nb = (L + block_size - 1) / block_size;
+            for (int b = 0; b < nb; ++b) {
+                int32_t p = block_tables[(int64_t)s * max_blocks_per_seq + b];
+                if (p < 0) continue;
+                int T = (L - b * block_size) < block_size ? (L - b * block_size) : block_size;
+                int64_t base = ((int64_t)p * num_kv_heads + kvh) * head_size * block_size;
+                float Mb = M;
+                for (int t = 0; t < T; ++t) {
+                    float a = 0.f;
+                    for (int e = 0; e < head_size; ++e)
+                        a += load_f32(q, dtype, qoff + e) * load_f32(k_cache, dtype, base + (int64_t)e * block_size + t);
+                    qk[t] = a * scale;
+                    if (qk[t] > Mb) Mb = qk[t];
+                }
+                float Sb = 32.f * S * expf(M - Mb);
+                for (int t = 0; t < T; ++t) Sb += expf(qk[t] - Mb);
+                M = Mb; S = Sb;
+                for (int d = 0; d < head_size; ++d) {
+                    int t = d % 128;
+                    if (t < T)
+                        o[d] += expf(qk[t] - M) / S * load_f32(v_cache, dtype, base + (int64_t)d * block_size + t);
+                }
+            }
+        }
+    }
+}
+
+/* ========================================================================
+ * Chunked prefill, intended semantics
+ * ====================================================================== */
+
+void orc_chunked_prefill(double* out, const void* q, int q_dtype,
+                         const int32_t* cu_q_lens, const void* k_cache,
+                         const void* v_cache, int kv_dtype,
+                         const int32_t* block_tables, int max_blocks_per_seq,
+                         const int32_t* seq_lens, int num_seqs, int num_heads,
+                         int num_kv_heads, int head_size, int block_size,
+                         float scale, int gqa_map)
+{
+    int max_len = 0;
+    for (int s = 0; s < num_seqs; ++s) if (seq_lens[s] > max_len) max_len = seq_lens[s];
+    double* sc = (double*)malloc(sizeof(double) * (max_len > 0 ? max_len : 1));
+    for (int s = 0; s < num_seqs; ++s) {
+        int L = seq_lens[s];
+        int q0 = cu_q_lens[s], ql = cu_q_lens[s + 1] - cu_q_lens[s];
+        const int32_t* row = block_tables + (int64_t)s * max_blocks_per_seq;
+        for (int i = 0; i < ql; ++i) {
+            int pos = L - ql + i;
+            for (int h = 0; h < num_heads; ++h) {
+                int kvh = kv_head_of(h, num_heads, num_kv_heads, gqa_map);
+                int64_t qoff = ((int64_t)(q0 + i) * num_heads + h) * head_size;
+                double m = -INFINITY;
+                for (int t = 0; t <= pos; ++t) {
+                    int64_t phys;
+                    if (!gather_ok(row, t, block_size, &phys)) { sc[t] = -INFINITY; continue; }
+                    int64_t base = (phys * num_kv_heads + kvh) * head_size * block_size + t % block_size;
+                    double dot = 0.0;
+                    for (int e = 0; e < head_size; ++e)
+                        dot += load_elem(q, q_dtype, qoff + e) * load_elem(k_cache, kv_dtype, base + (int64_t)e * block_size);
+                    sc[t] = dot * (double)scale;
+                    if (sc[t] > m) m = sc[t];
+                }
+                double l = 0.0;
+                double* o = out + qoff;
+                for (int e = 0; e < head_size; ++e) o[e] = 0.0;
+                if (m == -INFINITY) continue;
+                for (int t = 0; t <= pos; ++t) {
+                    if (sc[t] == -INFINITY) continue;
+                    int64_t phys = 0; gather_ok(row, t, block_size, &phys);
+                    int64_t base = (phys * num_kv_heads + kvh) * head_size * block_size + t % block_size;
+                    double w = exp(sc[t] - m);
+                    l += w;
+                    for (int e = 0; e < head_size; ++e)
+                        o[e] += w * load_elem(v_cache, kv_dtype, base + (int64_t)e * block_size);
+                }
+                for (int e = 0; e < head_size; ++e) o[e] /= l;
+            }
+        }
+    }
+    free(sc);
+}
+
+/* ========================================================================
+ * Reference KIVI vector codec (kivi_cache.cu:23-198, kivi_cache.cuh:32-43)
+ * ====================================================================== */
+
+#define KIVI_MAX_HEAD_DIM 128
+#define KIVI_MAX_OUTLIERS 64
+
+size_t orc_kivi_compressed_bytes(int head_dim, int n_outliers, int group_size)
+{
+    int n_res = head_dim - n_outliers;
+    int n_groups = (n_res + group_size - 1) / group_size;
+    return (size_t)n_outliers * 3 + (size_t)n_groups * (size_t)(group_size / 2 + 4);
+}
+
+int orc_kivi_params_supported(int head_dim, int n_outliers, int group_size)
+{
+    return head_dim > 0 && head_dim <= KIVI_MAX_HEAD_DIM && n_outliers >= 0 &&
+           n_outliers <= KIVI_MAX_OUTLIERS && group_size > 0 && n_outliers <= head_dim;
+}
+
+/* __float2int_rn then the clamp of kivi_cache.cu:109-112 */
+static int quant_nibble(float v)
+{
+    float r = rintf(v);
+    if (!(r >= 0.0f)) return 0;          /* negative or NaN */
+    if (r > 15.0f) return 15;
+    return (int)r;
+}
+
+void orc_kivi_quant_group(const float* x, int n, uint8_t* q, uint16_t* step, uint16_t* zero)
+{
+    float gmin = FLT_MAX, gmax = -FLT_MAX;
+    for (int i = 0; i < n; ++i) {
+        if (x[i] < gmin) gmin = x[i];
+        if (x[i] > gmax) gmax = x[i];
+    }
+    float range = gmax - gmin;
+    int degenerate = !(range > 1e-6f);
+    float scale = degenerate ? 0.0f : (15.0f / range);
+    for (int i = 0; i < n; ++i) {
+        float d = x[i] - gmin;           /* rounded separately ... */
+        q[i] = (uint8_t)quant_nibble(d * scale);  /* ... from the multiply */
+    }
+    float st = degenerate ? 0.0f : (1.0f / scale);
+    int gmin_ok = (gmin == gmin) && (gmin > -FLT_MAX) && (gmin < FLT_MAX);
+    *step = orc_f32_to_f16(st);
+    *zero = orc_f32_to_f16(gmin_ok ? gmin : 0.0f);
+}
+
+void orc_kivi_compress(const uint16_t* in, uint8_t* out, int n_vecs,
+                       int head_dim, int n_outliers, int group_size)
+{
+    if (n_vecs <= 0 || !orc_kivi_params_supported(head_dim, n_outliers, group_size)) return;
+    size_t stride = orc_kivi_compressed_bytes(head_dim, n_outliers, group_size);
+    int n_out = n_outliers;
+    for (int v = 0; v < n_vecs; ++v) {
+        const uint16_t* src = in + (int64_t)v * head_dim;
+        uint8_t* p = out + (size_t)v * stride;
+        uint8_t oidx[KIVI_MAX_OUTLIERS];
+        float omag[KIVI_MAX_OUTLIERS];
+        for (int i = 0; i < n_out; ++i) { oidx[i] = 0; omag[i] = -1.f; }
+        float min_mag = -1.f;
+        int min_pos = 0;
+        for (int d = 0; d < head_dim; ++d) {
+            float a = fabsf(orc_f16_to_f32(src[d]));
+            if (a > min_mag) {
+                if (n_out > 0) { oidx[min_pos] = (uint8_t)d; omag[min_pos] = a; }
+                min_mag = (n_out > 0) ? omag[0] : a;   /* n_out == 0: slot 0 scribble */
+                min_pos = 0;
+                for (int i = 1; i < n_out; ++i)
+                    if (omag[i] < min_mag) { min_mag = omag[i]; min_pos = i; }
+            }
+        }
+        unsigned char is_out[KIVI_MAX_HEAD_DIM];
+        memset(is_out, 0, sizeof is_out);
+        for (int i = 0; i < n_out; ++i) is_out[oidx[i]] = 1;
+        for (int i = 0; i < n_out; ++i) {
+            *p++ = oidx[i];
+            uint16_t hv = src[oidx[i]];
+            memcpy(p, &hv, 2); p += 2;
+        }
+        int n_res = head_dim - n_out;
+        int n_groups = (n_res + group_size - 1) / group_size;
+        float res[KIVI_MAX_HEAD_DIM];
+        int r = 0;
+        for (int d = 0; d < head_dim && r < n_res; ++d)
+            if (!is_out[d]) res[r++] = orc_f16_to_f32(src[d]);
+        for (int g = 0; g < n_groups; ++g) {
+            int g0 = g * group_size, g1 = g0 + group_size < n_res ? g0 + group_size : n_res;
+            uint8_t qn[KIVI_MAX_HEAD_DIM];
+            uint16_t st, ze;
+            orc_kivi_quant_group(res + g0, g1 - g0, qn, &st, &ze);
+            for (int i = 0; i < g1 - g0; i += 2) {
+                int q0 = qn[i];
+                int q1 = (i + 1 < g1 - g0) ? qn[i + 1] : 0;
+                *p++ = (uint8_t)((q1 << 4) | q0);
+            }
+            memcpy(p, &st, 2); p += 2;
+            memcpy(p, &ze, 2); p += 2;
+        }
+    }
+}
+
+void orc_kivi_decompress(const uint8_t* in, uint16_t* out, int n_vecs,
+                         int head_dim, int n_outliers, int group_size)
+{
+    if (n_vecs <= 0 || !orc_kivi_params_supported(head_dim, n_outliers, group_size)) return;
+    size_t stride = orc_kivi_compressed_bytes(head_dim, n_outliers, group_size);
+    int n_out = n_outliers;
+    for (int v = 0; v < n_vecs; ++v) {
+        const uint8_t* p = in + (size_t)v * stride;
+        uint16_t* dst = out + (int64_t)v * head_dim;
+        float result[KIVI_MAX_HEAD_DIM];
+        unsigned char written[KIVI_MAX_HEAD_DIM];
+        for (int d = 0; d < head_dim; ++d) { result[d] = 0.f; written[d] = 0; }
+        for (int i = 0; i < n_out; ++i) {
+            uint8_t ch = *p++;
+            uint16_t hv; memcpy(&hv, p, 2); p += 2;
+            if (ch < head_dim) { result[ch] = orc_f16_to_f32(hv); written[ch] = 1; }
+        }
+        int n_res = head_dim - n_out;
+        int n_groups = (n_res + group_size - 1) / group_size;
+        int rch[KIVI_MAX_HEAD_DIM];
+        int r = 0;
+        for (int d = 0; d < head_dim && r < n_res; ++d)
+            if (!written[d]) rch[r++] = d;
+        for (int g = 0; g < n_groups; ++g) {
+            int g0 = g * group_size, g1 = g0 + group_size < n_res ? g0 + group_size : n_res;
+            const uint8_t* pack = p;
+            p += (g1 - g0 + 1) / 2;
+            uint16_t hs, hz;
+            memcpy(&hs, p, 2); p += 2;
+            memcpy(&hz, p, 2); p += 2;
+            float st = orc_f16_to_f32(hs), ze = orc_f16_to_f32(hz);
+            for (int i = g0; i < g1; ++i) {
+                int k = i - g0;
+                int nib = (k % 2 == 0) ? (pack[k / 2] & 0x0f) : (pack[k / 2] >> 4);
+                float val = fmaf((float)nib, st, ze);
+                if (i < r) result[rch[i]] = val;
+            }
+        }
+        for (int d = 0; d < head_dim; ++d) dst[d] = orc_f32_to_f16(result[d]);
+    }
+}
+
+/* ========================================================================
+ * Paged KIVI INT4 page format (head_size 128, 32 tokens per page, per kv head)
+ *
+ *   [   0, 2048) K nibbles, 128 chunks of 16 B.  Chunk c = tt*64 + j*16 + u
+ *                holds token t = tt*16 + u; its dword m (0..3) holds channel
+ *                octet o = j + 4m: channel 8o + 2i + hb at bit 16*hb + 4i.
+ *   [2048, 2560) K params: octet o -> 32 B = 8 fp16 steps then 8 fp16 zeros
+ *                for channels 8o..8o+7 (one (step, zero) per channel over the
+ *                page's 32 tokens).
+ *   [2560, 4608) V nibbles, 128 chunks of 16 B.  Chunk c = hh*64 + r*16 + u;
+ *                dword m holds channel (4hh + m)*16 + u for the eight tokens
+ *                of slot s = 0..7: token 4r + s (s < 4) or 16 + 4r + s - 4
+ *                (s >= 4), at bit 16*(s&1) + 4*(s>>1).
+ *   [4608, 5120) V params: (g, r) -> 32 B = 8 fp16 steps then 8 fp16 zeros
+ *                in slot order, for channel group g (32 channels) of the
+ *                tokens of lane group r.
+ * ====================================================================== */
+
+#define PG_T 32
+#define PG_D 128
+
+static int64_t kn_bitpos(int t, int ch, int* byte)    /* K nibble position */
+{
+    int tt = t / 16, u = t % 16;
+    int o = ch / 8, j = o % 4, m = o / 4;
+    int i = (ch % 8) / 2, hb = ch % 2;
+    int c = tt * 64 + j * 16 + u;
+    int bit = 16 * hb + 4 * i;
+    *byte = c * 16 + m * 4 + bit / 8;
+    return bit % 8;
+}
+
+static void v_slot_of(int t, int* r, int* s)
+{
+    if (t < 16) { *r = t / 4; *s = t % 4; }
+    else { *r = (t - 16) / 4; *s = 4 + (t - 16) % 4; }
+}
+
+static int64_t vn_bitpos(int t, int ch, int* byte)    /* V nibble position */
+{
+    int r, s; v_slot_of(t, &r, &s);
+    int nt = ch / 16, u = ch % 16, hh = nt / 4, m = nt % 4;
+    int c = hh * 64 + r * 16 + u;
+    int bit = 16 * (s & 1) + 4 * (s >> 1);
+    *byte = 2560 + c * 16 + m * 4 + bit / 8;
+    return bit % 8;
+}
+
+static int kparam_off(int ch, int zero) { return 2048 + (ch / 8) * 32 + zero * 16 + 2 * (ch % 8); }
+static int vparam_off(int t, int g, int zero)
+{
+    int r, s; v_slot_of(t, &r, &s);
+    return 4608 + (g * 4 + r) * 32 + zero * 16 + 2 * s;
+}
+
+void orc_kivi_page_quantize(const uint16_t* k_tok, const uint16_t* v_tok, uint8_t* page)
+{
+    memset(page, 0, ORC_KIVI_PAGE_BYTES);
+    float x[PG_D];
+    uint8_t q[PG_D];
+    uint16_t st, ze;
+    /* K: per channel over the 32 tokens */
+    for (int ch = 0; ch < PG_D; ++ch) {
+        for (int t = 0; t < PG_T; ++t) x[t] = orc_f16_to_f32(k_tok[t * PG_D + ch]);
+        orc_kivi_quant_group(x, PG_T, q, &st, &ze);
+        for (int t = 0; t < PG_T; ++t) {
+            int byte; int sh = (int)kn_bitpos(t, ch, &byte);
+            page[byte] |= (uint8_t)(q[t] << sh);
+        }
+        memcpy(page + kparam_off(ch, 0), &st, 2);
+        memcpy(page + kparam_off(ch, 1), &ze, 2);
+    }
+    /* V: per token over groups of 32 channels */
+    for (int t = 0; t < PG_T; ++t)
+        for (int g = 0; g < PG_D / 32; ++g) {
+            for (int i = 0; i < 32; ++i) x[i] = orc_f16_to_f32(v_tok[t * PG_D + g * 32 + i]);
+            orc_kivi_quant_group(x, 32, q, &st, &ze);
+            for (int i = 0; i < 32; ++i) {
+                int byte; int sh = (int)vn_bitpos(t, g * 32 + i, &byte);
+                page[byte] |= (uint8_t)(q[i] << sh);
+            }
+            memcpy(page + vparam_off(t, g, 0), &st, 2);
+            memcpy(page + vparam_off(t, g, 1), &ze, 2);
+        }
+}
+
+void orc_kivi_page_dequant(const uint8_t* page, uint16_t* k_tok, uint16_t* v_tok)
+{
+    for (int t = 0; t < PG_T; ++t)
+        for (int ch = 0; ch < PG_D; ++ch) {
+            int byte; int sh = (int)kn_bitpos(t, ch, &byte);
+            int n = (page[byte] >> sh) & 0xf;
+            uint16_t st, ze;
+            memcpy(&st, page + kparam_off(ch, 0), 2);
+            memcpy(&ze, page + kparam_off(ch, 1), 2);
+            k_tok[t * PG_D + ch] = orc_f32_to_f16(fmaf((float)n, orc_f16_to_f32(st), orc_f16_to_f32(ze)));
+            sh = (int)vn_bitpos(t, ch, &byte);
+            n = (page[byte] >> sh) & 0xf;
+            memcpy(&st, page + vparam_off(t, ch / 32, 0), 2);
+            memcpy(&ze, page + vparam_off(t, ch / 32, 1), 2);
+            v_tok[t * PG_D + ch] = orc_f32_to_f16(fmaf((float)n, orc_f16_to_f32(st), orc_f16_to_f32(ze)));
+        }
+}
+
+int orc_kivi_quantized_len(int seq_len, int residual_length)
+{
+    if (seq_len <= residual_length) return 0;
+    return ((seq_len - residual_length) / PG_T) * PG_T;
+}
+
+static void gather_tok_f16(const uint16_t* cache, const int32_t* row, int t, int kvh,
+                           int num_kv_heads, int block_size, uint16_t* dst)
+{
+    int32_t p = row[t / block_size];
+    for (int e = 0; e < PG_D; ++e)
+        dst[e] = (p < 0) ? 0 : cache[(((int64_t)p * num_kv_heads + kvh) * PG_D + e) * block_size + t % block_size];
+}
+
+void orc_kivi_build_pages(const uint16_t* k_cache, const uint16_t* v_cache,
+                          const int32_t* block_tables, int max_blocks_per_seq,
+                          const int32_t* seq_lens, int num_seqs, int num_kv_heads,
+                          int block_size, int residual_length,
+                          uint8_t* pages, const int32_t* page_tables, int max_pages)
+{
+    uint16_t kt[PG_T * PG_D], vt[PG_T * PG_D];
+    for (int s = 0; s < num_seqs; ++s) {
+        int Lq = orc_kivi_quantized_len(seq_lens[s], residual_length);
+        const int32_t* row = block_tables + (int64_t)s * max_blocks_per_seq;
+        for (int p = 0; p < Lq / PG_T; ++p) {
+            int32_t pid = page_tables[(int64_t)s * max_pages + p];
+            if (pid < 0) continue;
+            for (int h = 0; h < num_kv_heads; ++h) {
+                for (int t = 0; t < PG_T; ++t) {
+                    gather_tok_f16(k_cache, row, p * PG_T + t, h, num_kv_heads, block_size, kt + t * PG_D);
+                    gather_tok_f16(v_cache, row, p * PG_T + t, h, num_kv_heads, block_size, vt + t * PG_D);
+                }
+                orc_kivi_page_quantize(kt, vt, pages + ((int64_t)pid * num_kv_heads + h) * ORC_KIVI_PAGE_BYTES);
+            }
+        }
+    }
+}
+
+void orc_kivi_paged_attention(double* out, const void* q, int q_dtype,
+                              const uint8_t* pages, const int32_t* page_tables,
+                              int max_pages, const uint16_t* k_cache,
+                              const uint16_t* v_cache, const int32_t* block_tables,
+                              int max_blocks_per_seq, const int32_t* seq_lens,
+                              int num_seqs, int num_heads, int num_kv_heads,
+                              int block_size, int residual_length, float scale,
+                              int gqa_map)
+{
+    int max_len = 0;
+    for (int s = 0; s < num_seqs; ++s) if (seq_lens[s] > max_len) max_len = seq_lens[s];
+    if (max_len == 0) max_len = 1;
+    float* K = (float*)malloc(sizeof(float) * (size_t)max_len * PG_D);
+    float* V = (float*)malloc(sizeof(float) * (size_t)max_len * PG_D);
+    double* sc = (double*)malloc(sizeof(double) * (size_t)max_len);
+    uint16_t kt[PG_T * PG_D], vt[PG_T * PG_D];
+    for (int s = 0; s < num_seqs; ++s) {
+        int L = seq_lens[s];
+        int Lq = orc_kivi_quantized_len(L, residual_length);
+        const int32_t* row = block_tables + (int64_t)s * max_blocks_per_seq;
+        for (int kvh = 0; kvh < num_kv_heads; ++kvh) {
+            for (int p = 0; p < Lq / PG_T; ++p) {
+                int32_t pid = page_tables[(int64_t)s * max_pages + p];
+                orc_kivi_page_dequant(pages + ((int64_t)pid * num_kv_heads + kvh) * ORC_KIVI_PAGE_BYTES, kt, vt);
+                for (int i = 0; i < PG_T * PG_D; ++i) {
+                    K[(size_t)p * PG_T * PG_D + i] = orc_f16_to_f32(kt[i]);
+                    V[(size_t)p * PG_T * PG_D + i] = orc_f16_to_f32(vt[i]);
+                }
+            }
+            for (int t = Lq; t < L; ++t) {
+                gather_tok_f16(k_cache, row, t, kvh, num_kv_heads, block_size, kt);
+                gather_tok_f16(v_cache, row, t, kvh, num_kv_heads, block_size, vt);
+                for (int e = 0; e < PG_D; ++e) {
+                    K[(size_t)t * PG_D + e] = orc_f16_to_f32(kt[e]);
+                    V[(size_t)t * PG_D + e] = orc_f16_to_f32(vt[e]);
+                }
+            }
+            for (int h = 0; h < num_heads; ++h) {
+                if (kv_head_of(h, num_heads, num_kv_heads, gqa_map) != kvh) continue;
+                int64_t qoff = ((int64_t)s * num_heads + h) * PG_D;
+                double m = -INFINITY;
+                for (int t = 0; t < L; ++t) {
+                    double d = 0.0;
+                    for (int e = 0; e < PG_D; ++e) d += load_elem(q, q_dtype, qoff + e) * (double)K[(size_t)t * PG_D + e];
+                    sc[t] = d * (double)scale;
+                    if (sc[t] > m) m = sc[t];
+                }
+                double l = 0.0;
+                double* o = out + qoff;
+                for (int e = 0; e < PG_D; ++e) o[e] = 0.0;
+                for (int t = 0; t < L; ++t) {
+                    double w = exp(sc[t] - m);
+                    l += w;
+                    for (int e = 0; e < PG_D; ++e) o[e] += w * (double)V[(size_t)t * PG_D + e];
+                }
+                for (int e = 0; e < PG_D; ++e) o[e] = (l > 0.0) ? o[e] / l : 0.0;
+            }
+        }
+    }
+    free(K); free(V); free(sc);
+}

@@ -1,0 +1,112 @@
+"""C ABI checks that need no GPU: the library loads, exports every function
+include/*.h declares, and rejects bad calls with an error code before any
+HIP call is made."""
+import ctypes
+
+import pytest
+
+import tl_attn as tla
+
+
+def test_exports_every_declared_function():
+    names = tla.header_functions()
+    assert len(names) >= 9
+    missing = [n for n in names if not hasattr(tla.lib, n)]
+    assert not missing, missing
+
+
+def test_abi_version():
+    assert tla.lib.tl_abi_version() == 1
+
+
+def _desc(**kw):
+    d = tla.DecodeDesc()
+    d.num_seqs, d.num_heads, d.num_kv_heads, d.head_size, d.block_size = 4, 32, 8, 128, 16
+    d.max_blocks_per_seq, d.num_blocks = 64, 512
+    d.q_dtype = d.kv_dtype = tla.F16
+    d.gqa_map, d.partition_tokens = tla.GQA_GROUPED, 0
+    d.scale, d.k_scale, d.v_scale = 0.088, 1.0, 1.0
+    for k, v in kw.items():
+        setattr(d, k, v)
+    return d
+
+
+FAKE = ctypes.c_void_p(0x1000)  # never dereferenced: every call below fails validation
+
+
+def _decode(d, out=FAKE, ws=None, ws_bytes=0, max_ctx=1024):
+    return tla.lib.tl_paged_attention_decode(ctypes.byref(d), out, FAKE, FAKE, FAKE, FAKE, FAKE,
+                                             max_ctx, ws, ws_bytes, None)
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(num_heads=30), tla.ERR_INVALID_ARGUMENT),
+    (dict(num_kv_heads=0), tla.ERR_INVALID_ARGUMENT),
+    (dict(head_size=80), tla.ERR_NOT_IMPLEMENTED),
+    (dict(block_size=8), tla.ERR_NOT_IMPLEMENTED),
+    (dict(q_dtype=7), tla.ERR_INVALID_ARGUMENT),
+    (dict(kv_dtype=tla.BF16), tla.ERR_NOT_IMPLEMENTED),
+    (dict(kv_dtype=tla.FP8_E4M3, q_dtype=tla.F32), tla.ERR_NOT_IMPLEMENTED),
+    (dict(gqa_map=5), tla.ERR_INVALID_ARGUMENT),
+    (dict(partition_tokens=100), tla.ERR_INVALID_ARGUMENT),
+    (dict(num_blocks=0), tla.ERR_INVALID_ARGUMENT),
+])
+def test_decode_rejects_bad_descriptors(kw, code):
+    assert _decode(_desc(**kw)) == code
+    assert tla.last_error()
+
+
+def test_decode_rejects_null_and_missing_workspace():
+    assert tla.lib.tl_paged_attention_decode(None, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 10, None, 0,
+                                             None) == tla.ERR_INVALID_ARGUMENT
+    assert _decode(_desc(), out=None) == tla.ERR_INVALID_ARGUMENT
+    d = _desc(partition_tokens=512)
+    need = tla.workspace_bytes(d, 4096)
+    assert need == 4 * 32 * 8 * (128 * 4 + 8)
+    assert _decode(d, max_ctx=4096) == tla.ERR_INVALID_ARGUMENT
+    assert "workspace" in tla.last_error()
+
+
+def test_workspace_is_zero_for_single_pass():
+    assert tla.workspace_bytes(_desc(partition_tokens=-1), 32768) == 0
+    assert tla.workspace_bytes(_desc(), 512) == 0
+
+
+def test_auto_partitioning_targets_many_workgroups():
+    # 64 x 8 work items at 4096 tokens -> 4 partitions of 1024
+    d = _desc(num_seqs=64)
+    assert tla.workspace_bytes(d, 4096) == 64 * 32 * 4 * (128 * 4 + 8)
+
+
+def test_empty_batch_is_a_no_op():
+    d = _desc(num_seqs=0)
+    assert tla.lib.tl_paged_attention_decode(ctypes.byref(d), None, None, None, None, None, None,
+                                             0, None, 0, None) == tla.OK
+    assert tla.lib.tl_reshape_and_cache(None, None, None, None, None, 0, 8, 128, 16, 10,
+                                        tla.F16, None) == tla.OK
+
+
+def test_v1_v2_reject_like_decode():
+    rc = tla.lib.tl_paged_attention_v1(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 4, 32, 8, 96, 16, 64,
+                                       512, 0.1, tla.F16, 0, None)
+    assert rc == tla.ERR_NOT_IMPLEMENTED
+    rc = tla.lib.tl_paged_attention_v2(FAKE, None, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 4, 32,
+                                       8, 128, 16, 64, 512, 0.1, tla.F16, 0, 4096, None)
+    assert rc == tla.ERR_INVALID_ARGUMENT
+    # misaligned pool
+    rc = tla.lib.tl_paged_attention_v1(FAKE, FAKE, ctypes.c_void_p(0x1002), FAKE, FAKE, FAKE, 4,
+                                       32, 8, 128, 16, 64, 512, 0.1, tla.F16, 0, None)
+    assert rc == tla.ERR_INVALID_ARGUMENT
+
+
+def test_reshape_rejects_bad_arguments():
+    L = tla.lib
+    assert L.tl_reshape_and_cache(FAKE, FAKE, FAKE, FAKE, FAKE, 4, 8, 100, 16, 10, tla.F16,
+                                  None) == tla.ERR_INVALID_ARGUMENT
+    assert L.tl_reshape_and_cache(FAKE, FAKE, FAKE, FAKE, FAKE, 4, 8, 128, 16, 10, 9,
+                                  None) == tla.ERR_INVALID_ARGUMENT
+    assert L.tl_reshape_and_cache(None, FAKE, FAKE, FAKE, FAKE, 4, 8, 128, 16, 10, tla.F16,
+                                  None) == tla.ERR_INVALID_ARGUMENT
+    assert L.tl_reshape_and_cache_fp8(FAKE, FAKE, tla.F32, FAKE, FAKE, FAKE, 4, 8, 128, 16, 10,
+                                      1.0, 1.0, None) == tla.ERR_NOT_IMPLEMENTED
+    assert L.tl_fp8_absmax_scale(FAKE, tla.F16, -1, FAKE, None) == tla.ERR_INVALID_ARGUMENT

@@ -1,0 +1,479 @@
+"""Pins the CPU oracle before it is trusted as the checker.
+
+Each check is chosen so that a plausible mistake in the oracle (a wrong
+rounding rule, a swapped index in the block-table gather, a dropped
+softmax term, a wrong GQA mapping, a mis-packed nibble) fails it:
+  - conversions against independent implementations (numpy float16, torch
+    bfloat16 / float8_e4m3fn) and brute force over every code;
+  - attention against a vectorised numpy float64 implementation on small
+    inputs, plus closed forms (L = 1 gives v, constant K gives mean(V)) and
+    invariants (split-K + LSE = single pass, physical-block permutation,
+    holes = removed tokens);
+  - the KIVI codec against the known answers and bounds of the reference's
+    own tests (test_kivi_bounds.cpp, test_kivi_roundtrip.cpp) and a
+    hand-derived record.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import inputs
+import oracle_lib as orc
+
+
+# ---------------------------------------------------------------------------
+# conversions
+# ---------------------------------------------------------------------------
+
+def test_f16_decode_all_codes_matches_numpy():
+    codes = np.arange(65536, dtype=np.uint16)
+    got = orc.bits_to_f32(codes, orc.F16)
+    want = codes.view(np.float16).astype(np.float32)
+    same = (got.view(np.uint32) == want.view(np.uint32)) | (np.isnan(got) & np.isnan(want))
+    assert same.all()
+
+
+def test_f16_encode_matches_numpy_rne():
+    rng = np.random.default_rng(1)
+    x = np.concatenate([
+        rng.standard_normal(200000).astype(np.float32) * 10,
+        (rng.standard_normal(50000) * 1e-5).astype(np.float32),      # subnormal range
+        np.array([65504, 65519.99, 65520, 1e6, -1e6, 0.0, -0.0, np.inf, -np.inf], np.float32),
+        # exact halfway points between adjacent fp16 values (ties to even)
+        ((np.arange(1024, 2048, dtype=np.float32) + 0.5) * 2.0 ** -10),
+        ((np.arange(0, 1024, dtype=np.float32) + 0.5) * 2.0 ** -24),
+    ]).astype(np.float32)
+    got = orc.f32_to_f16_bits(x)
+    with np.errstate(over="ignore"):
+        want = x.astype(np.float16).view(np.uint16)
+    assert np.array_equal(got, want)
+
+
+def test_bf16_encode_matches_torch_rne():
+    rng = np.random.default_rng(2)
+    x = np.concatenate([
+        rng.standard_normal(200000).astype(np.float32) * 100,
+        np.array([0.0, -0.0, np.inf, -np.inf, 3.3895314e38], np.float32),
+        (np.arange(0, 4096, dtype=np.uint32) * 65536 + 32768).view(np.float32),  # ties
+    ]).astype(np.float32)
+    got = orc.f32_to_bf16_bits(x)
+    want = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(got, want)
+
+
+def _e4m3_values():
+    return torch.arange(256, dtype=torch.uint8).view(torch.float8_e4m3fn).float().numpy()
+
+
+def test_e4m3_decode_all_codes_matches_torch():
+    got = orc.bits_to_f32(np.arange(256, dtype=np.uint8), orc.FP8)
+    want = _e4m3_values()
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    ok = ~np.isnan(want)
+    assert np.array_equal(got[ok], want[ok])
+    assert got[0x7E] == 448.0 and np.isnan(got[0x7F]) and np.isnan(got[0xFF])
+
+
+def test_e4m3_encode_every_f16_brute_force():
+    """RNE to the nearest finite E4M3 value (ties to even code), saturate at
+    448: brute force over all 256 codes for every fp16 input."""
+    x = np.arange(65536, dtype=np.uint16).view(np.float16).astype(np.float32)
+    x = x[np.isfinite(x)]
+    vals = orc.bits_to_f32(np.arange(256, dtype=np.uint8), orc.FP8).astype(np.float64)
+    finite = np.where(~np.isnan(vals))[0]
+    got = orc.f32_to_e4m3(x)
+    # nearest by distance, ties to the even mantissa (code with bit0 == 0)
+    xv = x.astype(np.float64)[:, None]
+    dist = np.abs(xv - vals[finite][None, :])
+    dmin = dist.min(axis=1, keepdims=True)
+    cand = (dist == dmin)
+    codes = finite[None, :].repeat(len(x), 0)
+    even = cand & ((codes & 1) == 0)
+    pick_even = even.any(axis=1)
+    idx = np.where(pick_even, np.argmax(even, axis=1), np.argmax(cand, axis=1))
+    want = finite[idx].astype(np.uint8)
+    # a result of zero keeps the sign of the input (IEEE rounding)
+    want = np.where((vals[want] == 0) & np.signbit(x), 0x80, want).astype(np.uint8)
+    sat = np.abs(x) >= 448
+    want = np.where(sat, np.where(x < 0, 0xFE, 0x7E), want).astype(np.uint8)
+    assert np.array_equal(got, want)
+
+
+def test_e4m3_encode_matches_torch_in_range():
+    x = np.arange(65536, dtype=np.uint16).view(np.float16).astype(np.float32)
+    x = x[np.isfinite(x) & (np.abs(x) < 464)]
+    got = orc.f32_to_e4m3(x)
+    want = torch.from_numpy(x).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    assert np.array_equal(got, want)
+    assert orc.lib.orc_f32_to_e4m3(float("inf")) == 0x7E
+    assert orc.lib.orc_f32_to_e4m3(-1e9) == 0xFE
+    assert orc.lib.orc_f32_to_e4m3(float("nan")) & 0x7F == 0x7F
+
+
+# ---------------------------------------------------------------------------
+# reshape_and_cache
+# ---------------------------------------------------------------------------
+
+def test_reshape_and_cache_index_map():
+    T, n_kv, D, BS, N = 5, 3, 8, 4, 6
+    key = np.arange(T * n_kv * D, dtype=np.uint16).reshape(T, n_kv, D)
+    val = (key + 1000).astype(np.uint16)
+    kc = np.zeros((N, n_kv, D, BS), np.uint16)
+    vc = np.zeros_like(kc)
+    slots = np.array([0, 7, -1, 23, 13], np.int32)
+    orc.reshape_and_cache(key, val, kc, vc, slots)
+    for t, s in enumerate(slots):
+        if s < 0:
+            continue
+        assert np.array_equal(kc[s // BS, :, :, s % BS], key[t])
+        assert np.array_equal(vc[s // BS, :, :, s % BS], val[t])
+    # nothing else written: the skipped token's data appears nowhere
+    assert not np.isin(key[2], kc).any()
+    assert (kc != 0).sum() == 4 * n_kv * D - 1  # element 0 of token 0 is 0 itself
+
+
+def test_reshape_then_gather_roundtrip():
+    """gather(scatter(x)) == x through slot = table[pos // BS] * BS + pos % BS
+    (cuda_allocator.cpp:270-274)."""
+    rng = np.random.default_rng(3)
+    n_kv, D, BS, N, L = 2, 16, 16, 20, 70
+    table = rng.permutation(N)[: (L + BS - 1) // BS].astype(np.int32)
+    pos = np.arange(L)
+    slots = (table[pos // BS] * BS + pos % BS).astype(np.int32)
+    key = rng.integers(0, 65535, (L, n_kv, D), dtype=np.uint16)
+    kc = np.zeros((N, n_kv, D, BS), np.uint16)
+    vc = np.zeros_like(kc)
+    orc.reshape_and_cache(key, key, kc, vc, slots)
+    back = kc[table[pos // BS], :, :, pos % BS]
+    assert np.array_equal(back, key)
+
+
+# ---------------------------------------------------------------------------
+# paged attention
+# ---------------------------------------------------------------------------
+
+def numpy_attention(case: inputs.PagedCase, gqa_map):
+    """Vectorised float64 restatement used to cross-check the C loops."""
+    S, H, D, BS = case.shape
+    q = orc.bits_to_f32(case.q, case.code).astype(np.float64) if case.code != orc.F32 else case.q.astype(np.float64)
+    kc = orc.bits_to_f32(case.k_cache, case.code).astype(np.float64) if case.code != orc.F32 else case.k_cache.astype(np.float64)
+    vc = orc.bits_to_f32(case.v_cache, case.code).astype(np.float64) if case.code != orc.F32 else case.v_cache.astype(np.float64)
+    G = H // case.num_kv_heads
+    out = np.zeros((S, H, D))
+    for s in range(S):
+        L = int(case.seq_lens[s])
+        if L == 0:
+            continue
+        pos = np.arange(L)
+        phys = case.tables[s][pos // BS]
+        keep = phys >= 0
+        pos, phys = pos[keep], phys[keep]
+        for h in range(H):
+            kvh = h // G if gqa_map == orc.GROUPED else h % case.num_kv_heads
+            K = kc[phys, kvh, :, pos % BS]          # [L, D]
+            V = vc[phys, kvh, :, pos % BS]
+            sc = K @ q[s, h] * float(np.float32(case.scale))
+            w = np.exp(sc - sc.max())
+            out[s, h] = (w / w.sum()) @ V
+    return out
+
+
+@pytest.mark.parametrize("gqa_map", [orc.MODULO, orc.GROUPED])
+@pytest.mark.parametrize("code", [orc.F16, orc.BF16, orc.F32])
+def test_attention_matches_numpy(gqa_map, code):
+    case = inputs.make_paged_case(11, S=3, H=8, n_kv=2, D=32, BS=16, lens=[1, 40, 77], code=code)
+    got = orc.paged_attention(case.q, code, case.k_cache, case.v_cache, code, case.tables,
+                              case.seq_lens, 2, case.scale, gqa_map)
+    np.testing.assert_allclose(got, numpy_attention(case, gqa_map), rtol=0, atol=1e-12)
+
+
+def test_attention_single_token_returns_v():
+    case = inputs.make_paged_case(12, S=2, H=4, n_kv=4, D=16, BS=16, lens=[1, 1], code=orc.F16)
+    got = orc.paged_attention(case.q, orc.F16, case.k_cache, case.v_cache, orc.F16, case.tables,
+                              case.seq_lens, 4, case.scale, orc.GROUPED)
+    for s in range(2):
+        b = case.tables[s, 0]
+        want = orc.bits_to_f32(case.v_cache[b, :, :, 0], orc.F16)
+        np.testing.assert_array_equal(got[s], want)
+
+
+def test_attention_constant_keys_give_mean_of_values():
+    case = inputs.make_paged_case(13, S=1, H=2, n_kv=1, D=16, BS=16, lens=[37], code=orc.F32)
+    case.k_cache[:] = 0.25                          # every score equal
+    got = orc.paged_attention(case.q, orc.F32, case.k_cache, case.v_cache, orc.F32, case.tables,
+                              case.seq_lens, 1, case.scale, orc.GROUPED)
+    pos = np.arange(37)
+    V = case.v_cache[case.tables[0][pos // 16], 0, :, pos % 16].astype(np.float64)
+    np.testing.assert_allclose(got[0, 0], V.mean(0), atol=1e-12)
+    np.testing.assert_allclose(got[0, 1], V.mean(0), atol=1e-12)
+
+
+@pytest.mark.parametrize("pt", [16, 48, 512])
+def test_split_k_lse_equals_single_pass(pt):
+    lens = inputs.uniform_lens(5, 4, 1, 1200)
+    case = inputs.make_paged_case(14, S=4, H=4, n_kv=2, D=32, BS=16, lens=lens, code=orc.BF16)
+    a = orc.paged_attention(case.q, orc.BF16, case.k_cache, case.v_cache, orc.BF16, case.tables,
+                            case.seq_lens, 2, case.scale, orc.GROUPED, 0)
+    b = orc.paged_attention(case.q, orc.BF16, case.k_cache, case.v_cache, orc.BF16, case.tables,
+                            case.seq_lens, 2, case.scale, orc.GROUPED, pt)
+    np.testing.assert_allclose(a, b, atol=1e-12)
+
+
+def test_physical_block_permutation_invariance():
+    case = inputs.make_paged_case(15, S=2, H=4, n_kv=2, D=16, BS=16, lens=[100, 33], code=orc.F16)
+    a = orc.paged_attention(case.q, orc.F16, case.k_cache, case.v_cache, orc.F16, case.tables,
+                            case.seq_lens, 2, case.scale, orc.GROUPED)
+    N = case.k_cache.shape[0]
+    perm = np.random.default_rng(0).permutation(N)
+    inv = np.argsort(perm)
+    k2 = np.ascontiguousarray(case.k_cache[perm])    # new block i holds old block perm[i]
+    v2 = np.ascontiguousarray(case.v_cache[perm])
+    t2 = np.where(case.tables >= 0, inv[np.maximum(case.tables, 0)], -1).astype(np.int32)
+    b = orc.paged_attention(case.q, orc.F16, k2, v2, orc.F16, t2, case.seq_lens, 2, case.scale,
+                            orc.GROUPED)
+    np.testing.assert_array_equal(a, b)
+
+
+def test_table_hole_equals_removed_tokens():
+    case = inputs.make_paged_case(16, S=1, H=2, n_kv=1, D=16, BS=16, lens=[48], code=orc.F32)
+    with_hole = case.tables.copy()
+    with_hole[0, 1] = -1
+    a = orc.paged_attention(case.q, orc.F32, case.k_cache, case.v_cache, orc.F32, with_hole,
+                            case.seq_lens, 1, case.scale, orc.GROUPED)
+    # same tokens without the hole: move block 2 into slot 1 and shorten
+    packed = np.full_like(case.tables, -1)
+    packed[0, 0], packed[0, 1] = case.tables[0, 0], case.tables[0, 2]
+    b = orc.paged_attention(case.q, orc.F32, case.k_cache, case.v_cache, orc.F32, packed,
+                            np.array([32], np.int32), 1, case.scale, orc.GROUPED)
+    np.testing.assert_allclose(a, b, atol=1e-12)
+
+
+def test_gqa_mappings_pick_the_right_kv_head():
+    case = inputs.make_paged_case(17, S=1, H=8, n_kv=2, D=16, BS=16, lens=[20], code=orc.F32)
+    case.v_cache[:, 0] = 1.0
+    case.v_cache[:, 1] = 2.0
+    g = orc.paged_attention(case.q, orc.F32, case.k_cache, case.v_cache, orc.F32, case.tables,
+                            case.seq_lens, 2, case.scale, orc.GROUPED)
+    m = orc.paged_attention(case.q, orc.F32, case.k_cache, case.v_cache, orc.F32, case.tables,
+                            case.seq_lens, 2, case.scale, orc.MODULO)
+    np.testing.assert_allclose(g[0, :, 0], [1, 1, 1, 1, 2, 2, 2, 2])
+    np.testing.assert_allclose(m[0, :, 0], [1, 2, 1, 2, 1, 2, 1, 2])
+
+
+def test_empty_sequence_gives_zeros():
+    case = inputs.make_paged_case(18, S=2, H=2, n_kv=1, D=16, BS=16, lens=[0, 5], code=orc.F16)
+    got = orc.paged_attention(case.q, orc.F16, case.k_cache, case.v_cache, orc.F16, case.tables,
+                              case.seq_lens, 1, case.scale, orc.GROUPED)
+    assert (got[0] == 0).all() and (got[1] != 0).any()
+
+
+def test_fp8_attention_is_attention_on_dequantised_pool():
+    case = inputs.make_paged_case(19, S=2, H=4, n_kv=2, D=32, BS=16, lens=[50, 17], code=orc.F32)
+    ks, vs = 0.01, 0.02
+    k8 = orc.f32_to_e4m3(case.k_cache, 1 / ks)
+    v8 = orc.f32_to_e4m3(case.v_cache, 1 / vs)
+    got = orc.paged_attention(case.q, orc.F32, k8, v8, orc.FP8, case.tables, case.seq_lens, 2,
+                              case.scale, orc.GROUPED, 0, ks, vs)
+    kd = (orc.bits_to_f32(k8, orc.FP8).astype(np.float64) * ks).astype(np.float32)
+    vd = (orc.bits_to_f32(v8, orc.FP8).astype(np.float64) * vs).astype(np.float32)
+    want = orc.paged_attention(case.q, orc.F32, kd, vd, orc.F32, case.tables, case.seq_lens, 2,
+                               case.scale, orc.GROUPED)
+    np.testing.assert_allclose(got, want, atol=1e-6)
+
+
+def test_cpu_baseline_f32_matches_oracle():
+    lens = inputs.uniform_lens(6, 3, 1, 700)
+    case = inputs.make_paged_case(20, S=3, H=8, n_kv=2, D=128, BS=16, lens=lens, code=orc.BF16)
+    a = orc.paged_attention(case.q, orc.BF16, case.k_cache, case.v_cache, orc.BF16, case.tables,
+                            case.seq_lens, 2, case.scale, orc.GROUPED)
+    b = orc.paged_attention_f32(case.q, orc.BF16, case.k_cache, case.v_cache, orc.BF16,
+                                case.tables, case.seq_lens, 2, case.scale, orc.GROUPED, threads=4)
+    np.testing.assert_allclose(b, a, atol=2e-5)
+
+
+def test_literal_v1_documents_reference_divergence():
+    """The reference kernel's literal output (Appendix-C semantics): dims >=
+    block_size are never written (per-thread accumulators are not reduced),
+    so it is not attention."""
+    case = inputs.make_paged_case(21, S=2, H=4, n_kv=2, D=64, BS=16, lens=[40, 100], code=orc.F16)
+    lit = orc.paged_attention_literal_v1(case.q, case.k_cache, case.v_cache, orc.F16, case.tables,
+                                         case.seq_lens, 2, case.scale)
+    assert (lit[:, :, 16:] == 0).all()
+    want = orc.paged_attention(case.q, orc.F16, case.k_cache, case.v_cache, orc.F16, case.tables,
+                               case.seq_lens, 2, case.scale, orc.MODULO)
+    assert np.abs(lit - want).max() > 0.05
+
+
+# ---------------------------------------------------------------------------
+# chunked prefill
+# ---------------------------------------------------------------------------
+
+def test_prefill_last_row_equals_decode_and_chunks_equal_whole():
+    rng = np.random.default_rng(22)
+    case = inputs.make_paged_case(22, S=1, H=4, n_kv=2, D=32, BS=16, lens=[96], code=orc.BF16)
+    qp = inputs.encode(rng.standard_normal((96, 4, 32), dtype=np.float32), orc.BF16)
+    whole = orc.chunked_prefill(qp, orc.BF16, np.array([0, 96], np.int32), case.k_cache,
+                                case.v_cache, orc.BF16, case.tables, case.seq_lens, 2, case.scale)
+    # second half as its own chunk over the full context
+    half = orc.chunked_prefill(np.ascontiguousarray(qp[48:]), orc.BF16, np.array([0, 48], np.int32),
+                               case.k_cache, case.v_cache, orc.BF16, case.tables, case.seq_lens, 2,
+                               case.scale)
+    np.testing.assert_allclose(half, whole[48:], atol=1e-12)
+    dec = orc.paged_attention(np.ascontiguousarray(qp[95:96]), orc.BF16, case.k_cache,
+                              case.v_cache, orc.BF16, case.tables, case.seq_lens, 2, case.scale,
+                              orc.GROUPED)
+    np.testing.assert_allclose(whole[95:96], dec, atol=1e-12)
+    # the first row sees only token 0: its output is v[0]
+    b = case.tables[0, 0]
+    v0 = orc.bits_to_f32(case.v_cache[b, :, :, 0], orc.BF16)
+    np.testing.assert_allclose(whole[0, 0], v0[0], atol=1e-12)
+    np.testing.assert_allclose(whole[0, 3], v0[1], atol=1e-12)
+
+
+# ---------------------------------------------------------------------------
+# reference KIVI vector codec
+# ---------------------------------------------------------------------------
+
+def test_kivi_known_answers_from_reference_tests():
+    # test_kivi_bounds.cpp:27-29, 37-56, 67-68
+    assert orc.kivi_compressed_bytes(128, 8, 16) == 24 + 8 * 12
+    assert orc.kivi_compressed_bytes(64, 0, 16) == 4 * 12
+    assert orc.kivi_compressed_bytes(64, 64, 16) == 64 * 3
+    assert orc.kivi_params_supported(128, 8, 16)
+    assert orc.kivi_params_supported(64, 4, 16)
+    assert orc.kivi_params_supported(128, 64, 16)
+    assert not orc.kivi_params_supported(129, 8, 16)
+    assert not orc.kivi_params_supported(128, 65, 16)
+    assert not orc.kivi_params_supported(16, 32, 16)
+    assert not orc.kivi_params_supported(128, 8, 0)
+    assert not orc.kivi_params_supported(128, 8, -4)
+    assert not orc.kivi_params_supported(0, 0, 16)
+    assert not orc.kivi_params_supported(-1, 0, 16)
+
+
+def _f16(x):
+    return np.atleast_1d(np.asarray(x, np.float32)).astype(np.float16).view(np.uint16)
+
+
+def _roundtrip(x, D, O, G):
+    n = x.size // D
+    rec = orc.kivi_compress(_f16(x), D, O, G)
+    return orc.kivi_decompress(rec, n, D, O, G).view(np.float16).astype(np.float32)
+
+
+def test_kivi_roundtrip_int4_granularity():
+    # test_kivi_roundtrip.cpp:83-113
+    x = np.array([[0.1 * d + 0.5 * v for d in range(64)] for v in range(3)], np.float32).ravel()
+    got = _roundtrip(x, 64, 0, 16)
+    assert np.abs(got - x).max() <= 0.15
+
+
+def test_kivi_roundtrip_outliers_preserved():
+    # test_kivi_roundtrip.cpp:121-170
+    x = np.array([0.01 * (i % 64) for i in range(128)], np.float32)
+    for v in range(2):
+        for k, ch in enumerate([3, 17, 33, 55]):
+            x[v * 64 + ch] = 50.0 + k + v
+    got = _roundtrip(x, 64, 4, 16)
+    assert np.abs(got - x).max() <= 0.1
+
+
+def test_kivi_degenerate_group_is_constant():
+    # test_kivi_roundtrip.cpp:178-200
+    got = _roundtrip(np.full(32, 2.5, np.float32), 32, 0, 16)
+    assert np.abs(got - 2.5).max() <= 1e-2
+
+
+def test_kivi_unsupported_params_no_op():
+    # test_kivi_roundtrip.cpp:207-229
+    stride = orc.kivi_compressed_bytes(256, 0, 16)
+    out = np.full(stride, 0xAB, np.uint8)
+    orc.kivi_compress(_f16(np.ones(256)), 256, 0, 16, out=out)
+    assert (out == 0xAB).all()
+
+
+def test_kivi_hand_derived_record():
+    """x = [1, -3, 0.5, 2], one outlier, group 4: outlier (1, -3); residual
+    [1, 0.5, 2] -> gmin 0.5, range 1.5, scale 10 -> q = 5, 0, 15; step
+    fp16(0.1) = 0x2E66, zero fp16(0.5) = 0x3800."""
+    rec = orc.kivi_compress(_f16([1, -3, 0.5, 2]), 4, 1, 4)
+    assert list(rec) == [0x01, 0x00, 0xC2, 0x05, 0x0F, 0x66, 0x2E, 0x00, 0x38]
+    back = orc.kivi_decompress(rec, 1, 4, 1, 4).view(np.float16).astype(np.float32)
+    assert list(back) == [1.0, -3.0, 0.5, 2.0]
+
+
+def test_kivi_quant_group_nibbles_follow_rne():
+    q, st, ze = orc.kivi_quant_group(np.arange(16, dtype=np.float32))
+    assert list(q) == list(range(16))
+    assert st == int(_f16(1.0)[0]) and ze == 0
+    q, st, ze = orc.kivi_quant_group(np.array([0.0, 0.5, 1.0, 2.0], np.float32) * 2)
+    # scale = 15/4: (1*3.75 = 3.75 -> 4), (2*3.75 = 7.5 -> 8 even), (4*3.75 = 15)
+    assert list(q) == [0, 4, 8, 15]
+
+
+# ---------------------------------------------------------------------------
+# paged KIVI page format
+# ---------------------------------------------------------------------------
+
+def test_kivi_page_nibble_positions_are_a_bijection():
+    # mark one token/channel at a time: exactly one nibble of the K (V) area moves
+    base_k = np.zeros((32, 128), np.float32)
+    base_k[0, :] = 1.0                                   # gmin 0, gmax 1 everywhere
+    base_v = np.zeros((32, 128), np.float32)
+    base_v[:, 0::32] = 1.0
+    seen_k, seen_v = set(), set()
+    p0 = orc.kivi_page_quantize(_f16(base_k).reshape(32, 128), _f16(base_v).reshape(32, 128))
+    for t in range(0, 32, 7):
+        for ch in range(1, 128, 13):
+            k = base_k.copy(); k[t, ch] = 1.0 if t != 0 else 0.0
+            p = orc.kivi_page_quantize(_f16(k).reshape(32, 128), _f16(base_v).reshape(32, 128))
+            diff = np.nonzero(p[:2048] != p0[:2048])[0]
+            assert len(diff) == 1
+            seen_k.add((int(diff[0]), int(p[diff[0]] ^ p0[diff[0]])))
+    assert len(seen_k) == len(range(0, 32, 7)) * len(range(1, 128, 13))
+
+
+def test_kivi_page_roundtrip_error_bound():
+    rng = np.random.default_rng(23)
+    k = rng.standard_normal((32, 128)).astype(np.float32)
+    k[:, [3, 40, 77, 100]] *= 8                          # outlier channels
+    v = rng.standard_normal((32, 128)).astype(np.float32)
+    kb, vb = _f16(k).reshape(32, 128), _f16(v).reshape(32, 128)
+    page = orc.kivi_page_quantize(kb, vb)
+    kd, vd = orc.kivi_page_dequant(page)
+    kd = kd.view(np.float16).astype(np.float32)
+    vd = vd.view(np.float16).astype(np.float32)
+    kx, vx = kb.view(np.float16).astype(np.float32), vb.view(np.float16).astype(np.float32)
+    # per-channel K groups over tokens; per-token V groups over 32 channels
+    kstep = (kx.max(0) - kx.min(0)) / 15
+    assert (np.abs(kd - kx) <= kstep[None, :] * 0.5 + np.abs(kx) * 2e-3 + 1e-3).all()
+    vg = vx.reshape(32, 4, 32)
+    vstep = (vg.max(2) - vg.min(2)) / 15
+    err = np.abs(vd - vx).reshape(32, 4, 32)
+    assert (err <= vstep[:, :, None] * 0.5 + np.abs(vg) * 2e-3 + 1e-3).all()
+
+
+def test_kivi_page_constant_is_exact_and_params_land_in_place():
+    k = np.full((32, 128), 1.5, np.float32)
+    v = np.full((32, 128), -0.75, np.float32)
+    page = orc.kivi_page_quantize(_f16(k).reshape(32, 128), _f16(v).reshape(32, 128))
+    kd, vd = orc.kivi_page_dequant(page)
+    assert (kd.view(np.float16) == 1.5).all() and (vd.view(np.float16) == -0.75).all()
+    assert (page[:2048] == 0).all() and (page[2560:4608] == 0).all()
+    kp = page[2048:2560].view(np.uint16).reshape(16, 2, 8)
+    assert (kp[:, 0] == 0).all() and (kp[:, 1] == _f16(1.5)[0]).all()
+    vp = page[4608:5120].view(np.uint16).reshape(16, 2, 8)
+    assert (vp[:, 0] == 0).all() and (vp[:, 1] == _f16(-0.75)[0]).all()
+
+
+def test_kivi_quantized_len():
+    assert orc.kivi_quantized_len(0, 128) == 0
+    assert orc.kivi_quantized_len(128, 128) == 0
+    assert orc.kivi_quantized_len(159, 128) == 0
+    assert orc.kivi_quantized_len(160, 128) == 32
+    assert orc.kivi_quantized_len(4096, 128) == 3968
+    for L in range(0, 600, 7):
+        lq = orc.kivi_quantized_len(L, 128)
+        assert lq % 32 == 0 and (L < 160 or 128 <= L - lq < 160)

@@ -1,0 +1,280 @@
+// tl_api.cpp -- the C ABI (include/tl_attn.h): argument checks, split-K
+// planning and dispatch to the HIP launchers.  Every check runs on the host
+// before any HIP call, so a bad call returns an error code and leaves the
+// device untouched.
+#include "tl_attn.h"
+#include "tl_internal.hpp"
+
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof g_err, fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int ok() {
+  g_err[0] = '\0';
+  return TL_OK;
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+bool is_float_kind(int32_t d) {
+  return d == TL_DTYPE_F32 || d == TL_DTYPE_F16 || d == TL_DTYPE_BF16;
+}
+
+int check_decode(const tl_decode_desc* d) {
+  if (!d) return fail(TL_ERR_INVALID_ARGUMENT, "desc is NULL");
+  if (d->num_seqs < 0) return fail(TL_ERR_INVALID_ARGUMENT, "num_seqs=%d < 0", d->num_seqs);
+  if (d->num_kv_heads <= 0 || d->num_heads <= 0 || d->num_heads % d->num_kv_heads)
+    return fail(TL_ERR_INVALID_ARGUMENT, "num_heads=%d must be a positive multiple of num_kv_heads=%d",
+                d->num_heads, d->num_kv_heads);
+  if (d->max_blocks_per_seq <= 0 || d->num_blocks <= 0)
+    return fail(TL_ERR_INVALID_ARGUMENT, "max_blocks_per_seq=%d and num_blocks=%d must be > 0",
+                d->max_blocks_per_seq, d->num_blocks);
+  if (d->gqa_map != TL_GQA_MODULO && d->gqa_map != TL_GQA_GROUPED)
+    return fail(TL_ERR_INVALID_ARGUMENT, "gqa_map=%d", d->gqa_map);
+  if (!is_float_kind(d->q_dtype))
+    return fail(TL_ERR_INVALID_ARGUMENT, "q_dtype=%d is not F32/F16/BF16", d->q_dtype);
+  if (!is_float_kind(d->kv_dtype) && d->kv_dtype != TL_DTYPE_FP8_E4M3)
+    return fail(TL_ERR_INVALID_ARGUMENT, "kv_dtype=%d", d->kv_dtype);
+  if (d->kv_dtype != TL_DTYPE_FP8_E4M3 && d->kv_dtype != d->q_dtype)
+    return fail(TL_ERR_NOT_IMPLEMENTED, "kv_dtype=%d with q_dtype=%d (q and a 16/32-bit pool must match)",
+                d->kv_dtype, d->q_dtype);
+  if (d->kv_dtype == TL_DTYPE_FP8_E4M3 && d->q_dtype == TL_DTYPE_F32)
+    return fail(TL_ERR_NOT_IMPLEMENTED, "FP8 KV needs F16 or BF16 q");
+  const bool shape_ok =
+      (d->block_size == 16 && (d->head_size == 64 || d->head_size == 128 || d->head_size == 256)) ||
+      (d->block_size == 32 && d->head_size == 128);
+  if (!shape_ok)
+    return fail(TL_ERR_NOT_IMPLEMENTED, "head_size=%d block_size=%d (built: 64/128/256 x 16, 128 x 32)",
+                d->head_size, d->block_size);
+  if (d->kv_dtype == TL_DTYPE_F32 && !(d->head_size == 128 && d->block_size == 16))
+    return fail(TL_ERR_NOT_IMPLEMENTED, "F32 KV is built for head_size 128, block_size 16 only");
+  if (d->partition_tokens != 0 && d->partition_tokens != -1 &&
+      (d->partition_tokens <= 0 || d->partition_tokens % tl::kDecodeChunk))
+    return fail(TL_ERR_INVALID_ARGUMENT, "partition_tokens=%d must be 0, -1 or a multiple of %d",
+                d->partition_tokens, tl::kDecodeChunk);
+  return TL_OK;
+}
+
+// Split-K plan: partition size and count for a batch whose longest sequence
+// is max_ctx.  Aim for >= 2048 workgroups (8 per CU on 256 CUs).
+void plan_partitions(const tl_decode_desc* d, int32_t max_ctx, int* P, int* PT) {
+  const int chunks = max_ctx > 0 ? (max_ctx + tl::kDecodeChunk - 1) / tl::kDecodeChunk : 1;
+  int pt_chunks;
+  if (d->partition_tokens == -1) {
+    pt_chunks = chunks;
+  } else if (d->partition_tokens > 0) {
+    pt_chunks = d->partition_tokens / tl::kDecodeChunk;
+  } else {
+    const int group = d->num_heads / d->num_kv_heads;
+    const int slices = group == 1 ? 1 : (group + 3) / 4;
+    const long items = (long)d->num_seqs * d->num_kv_heads * slices;
+    long want = items > 0 ? (2048 + items - 1) / items : 1;
+    if (want < 1) want = 1;
+    if (want > chunks) want = chunks;
+    pt_chunks = (int)((chunks + want - 1) / want);
+  }
+  if (pt_chunks < 1) pt_chunks = 1;
+  *P = (chunks + pt_chunks - 1) / pt_chunks;
+  *PT = pt_chunks * tl::kDecodeChunk;
+}
+
+tl::DecodeLaunch make_launch(const tl_decode_desc* d, void* out, const void* q,
+                             const void* k_cache, const void* v_cache, const int32_t* bt,
+                             const int32_t* sl, void* stream) {
+  tl::DecodeLaunch a;
+  memset(&a, 0, sizeof a);
+  a.out = out; a.q = q; a.k_cache = k_cache; a.v_cache = v_cache;
+  a.block_tables = bt; a.seq_lens = sl;
+  a.num_seqs = d->num_seqs; a.num_heads = d->num_heads; a.num_kv_heads = d->num_kv_heads;
+  a.head_size = d->head_size; a.block_size = d->block_size;
+  a.max_blocks_per_seq = d->max_blocks_per_seq; a.num_blocks = d->num_blocks;
+  a.q_dtype = d->q_dtype; a.kv_dtype = d->kv_dtype; a.gqa_map = d->gqa_map;
+  a.scale = d->scale; a.k_scale = d->k_scale; a.v_scale = d->v_scale;
+  a.num_partitions = 1; a.partition_tokens = 0;
+  a.stream = (hipStream_t)stream;
+  return a;
+}
+
+int run(const tl::DecodeLaunch& a) {
+  const int rc = tl::launch_decode(a);
+  if (rc == 3) return fail(TL_ERR_NOT_IMPLEMENTED, "no decode kernel for this dtype/shape");
+  if (rc != 0) return fail(TL_ERR_BACKEND, "decode launch failed: %s", hipGetErrorString(hipGetLastError()));
+  return ok();
+}
+
+size_t ws_bytes(const tl_decode_desc* d, int P) {
+  if (P <= 1) return 0;
+  const size_t sh = (size_t)d->num_seqs * d->num_heads * P;
+  return sh * d->head_size * 4 + 2 * sh * 4;
+}
+
+}  // namespace
+
+extern "C" {
+
+int tl_abi_version(void) { return TL_ABI_VERSION; }
+
+const char* tl_last_error_string(void) { return g_err; }
+
+size_t tl_paged_attention_workspace_bytes(const tl_decode_desc* desc, int32_t max_context_len) {
+  if (check_decode(desc) != TL_OK || max_context_len < 0) return 0;
+  int P, PT;
+  plan_partitions(desc, max_context_len, &P, &PT);
+  return ws_bytes(desc, P);
+}
+
+int tl_paged_attention_decode(const tl_decode_desc* desc, void* out, const void* q,
+                              const void* k_cache, const void* v_cache,
+                              const int32_t* block_tables, const int32_t* seq_lens,
+                              int32_t max_context_len, void* workspace, size_t workspace_bytes,
+                              void* stream) {
+  int rc = check_decode(desc);
+  if (rc) return rc;
+  if (max_context_len < 0) return fail(TL_ERR_INVALID_ARGUMENT, "max_context_len < 0");
+  if (desc->num_seqs == 0) return ok();
+  if (!out || !q || !k_cache || !v_cache || !block_tables || !seq_lens)
+    return fail(TL_ERR_INVALID_ARGUMENT, "NULL tensor pointer");
+  if (!aligned16(k_cache) || !aligned16(v_cache))
+    return fail(TL_ERR_INVALID_ARGUMENT, "k_cache/v_cache must be 16-byte aligned");
+  int P, PT;
+  plan_partitions(desc, max_context_len, &P, &PT);
+  tl::DecodeLaunch a = make_launch(desc, out, q, k_cache, v_cache, block_tables, seq_lens, stream);
+  if (P > 1) {
+    const size_t need = ws_bytes(desc, P);
+    if (!workspace || workspace_bytes < need)
+      return fail(TL_ERR_INVALID_ARGUMENT, "workspace of %zu bytes needed, %zu given", need,
+                  workspace_bytes);
+    if (!aligned16(workspace)) return fail(TL_ERR_INVALID_ARGUMENT, "workspace must be 16-byte aligned");
+    const size_t sh = (size_t)desc->num_seqs * desc->num_heads * P;
+    a.part_o = workspace;
+    a.part_m = (float*)((char*)workspace + sh * desc->head_size * 4);
+    a.part_l = a.part_m + sh;
+    a.part_o_dtype = 0;
+    a.num_partitions = P;
+    a.partition_tokens = PT;
+  }
+  return run(a);
+}
+
+int tl_paged_attention_v1(void* out, const void* q, const void* k_cache, const void* v_cache,
+                          const int32_t* block_tables, const int32_t* seq_lens, int32_t num_seqs,
+                          int32_t num_heads, int32_t num_kv_heads, int32_t head_size,
+                          int32_t block_size, int32_t max_blocks_per_seq, int32_t num_blocks,
+                          float scale, int32_t dtype, int32_t gqa_map, void* stream) {
+  tl_decode_desc d = {num_seqs, num_heads, num_kv_heads, head_size, block_size, max_blocks_per_seq,
+                      num_blocks, dtype, dtype, gqa_map, -1, scale, 1.f, 1.f};
+  int rc = check_decode(&d);
+  if (rc) return rc;
+  if (num_seqs == 0) return ok();
+  if (!out || !q || !k_cache || !v_cache || !block_tables || !seq_lens)
+    return fail(TL_ERR_INVALID_ARGUMENT, "NULL tensor pointer");
+  if (!aligned16(k_cache) || !aligned16(v_cache))
+    return fail(TL_ERR_INVALID_ARGUMENT, "k_cache/v_cache must be 16-byte aligned");
+  return run(make_launch(&d, out, q, k_cache, v_cache, block_tables, seq_lens, stream));
+}
+
+int tl_paged_attention_v2(void* out, float* exp_sums, float* max_logits, void* tmp_out,
+                          const void* q, const void* k_cache, const void* v_cache,
+                          const int32_t* block_tables, const int32_t* seq_lens, int32_t num_seqs,
+                          int32_t num_heads, int32_t num_kv_heads, int32_t head_size,
+                          int32_t block_size, int32_t max_blocks_per_seq, int32_t num_blocks,
+                          float scale, int32_t dtype, int32_t gqa_map, int32_t max_context_len,
+                          void* stream) {
+  tl_decode_desc d = {num_seqs, num_heads, num_kv_heads, head_size, block_size, max_blocks_per_seq,
+                      num_blocks, dtype, dtype, gqa_map, 0, scale, 1.f, 1.f};
+  int rc = check_decode(&d);
+  if (rc) return rc;
+  if (max_context_len < 0) return fail(TL_ERR_INVALID_ARGUMENT, "max_context_len < 0");
+  if (num_seqs == 0) return ok();
+  if (!out || !q || !k_cache || !v_cache || !block_tables || !seq_lens || !exp_sums ||
+      !max_logits || !tmp_out)
+    return fail(TL_ERR_INVALID_ARGUMENT, "NULL tensor pointer");
+  if (!aligned16(k_cache) || !aligned16(v_cache))
+    return fail(TL_ERR_INVALID_ARGUMENT, "k_cache/v_cache must be 16-byte aligned");
+  // Partitions of 32 blocks as the reference (PARTITION_SIZE, paged_attention_v2.cu:25);
+  // the count is taken with ceil so the tail block is kept.
+  const int PT = 32 * block_size;
+  if (PT % tl::kDecodeChunk)
+    return fail(TL_ERR_NOT_IMPLEMENTED, "block_size=%d: partitions of 32 blocks must be multiples of %d tokens",
+                block_size, tl::kDecodeChunk);
+  const int P = max_context_len > 0 ? (max_context_len + PT - 1) / PT : 1;
+  tl::DecodeLaunch a = make_launch(&d, out, q, k_cache, v_cache, block_tables, seq_lens, stream);
+  a.num_partitions = P;
+  a.partition_tokens = PT;
+  a.part_m = max_logits;
+  a.part_l = exp_sums;
+  a.part_o = tmp_out;
+  a.part_o_dtype = dtype;  // tmp_out holds q-dtype partials, as the caller sized it
+  // With one partition the kernel writes out directly and the scratch is unused.
+  return run(a);
+}
+
+int tl_reshape_and_cache(const void* key, const void* value, void* k_cache, void* v_cache,
+                         const int32_t* slot_mapping, int32_t num_tokens, int32_t num_kv_heads,
+                         int32_t head_size, int32_t block_size, int32_t num_blocks, int32_t dtype,
+                         void* stream) {
+  if (num_tokens < 0 || num_kv_heads <= 0 || head_size <= 0 || block_size <= 0 || num_blocks <= 0)
+    return fail(TL_ERR_INVALID_ARGUMENT, "num_tokens=%d num_kv_heads=%d head_size=%d block_size=%d num_blocks=%d",
+                num_tokens, num_kv_heads, head_size, block_size, num_blocks);
+  if (!is_float_kind(dtype)) return fail(TL_ERR_INVALID_ARGUMENT, "dtype=%d", dtype);
+  const int run = dtype == TL_DTYPE_F32 ? 4 : 8;
+  if (head_size % run) return fail(TL_ERR_INVALID_ARGUMENT, "head_size=%d must be a multiple of %d", head_size, run);
+  if (num_tokens == 0) return ok();
+  if (!key || !value || !k_cache || !v_cache || !slot_mapping)
+    return fail(TL_ERR_INVALID_ARGUMENT, "NULL tensor pointer");
+  if (!aligned16(key) || !aligned16(value))
+    return fail(TL_ERR_INVALID_ARGUMENT, "key/value must be 16-byte aligned");
+  tl::CacheLaunch a = {key, value, k_cache, v_cache, slot_mapping, num_tokens, num_kv_heads,
+                       head_size, block_size, num_blocks, dtype, dtype, 1.f, 1.f,
+                       (hipStream_t)stream};
+  const int rc = tl::launch_reshape_and_cache(a);
+  if (rc) return fail(TL_ERR_BACKEND, "reshape_and_cache launch failed");
+  return ok();
+}
+
+int tl_reshape_and_cache_fp8(const void* key, const void* value, int32_t src_dtype,
+                             uint8_t* k_cache, uint8_t* v_cache, const int32_t* slot_mapping,
+                             int32_t num_tokens, int32_t num_kv_heads, int32_t head_size,
+                             int32_t block_size, int32_t num_blocks, float k_scale, float v_scale,
+                             void* stream) {
+  if (num_tokens < 0 || num_kv_heads <= 0 || head_size <= 0 || block_size <= 0 || num_blocks <= 0)
+    return fail(TL_ERR_INVALID_ARGUMENT, "bad sizes");
+  if (src_dtype != TL_DTYPE_F16 && src_dtype != TL_DTYPE_BF16)
+    return fail(TL_ERR_NOT_IMPLEMENTED, "src_dtype=%d (F16 or BF16 sources)", src_dtype);
+  if (head_size % 8) return fail(TL_ERR_INVALID_ARGUMENT, "head_size=%d must be a multiple of 8", head_size);
+  if (num_tokens == 0) return ok();
+  if (!key || !value || !k_cache || !v_cache || !slot_mapping)
+    return fail(TL_ERR_INVALID_ARGUMENT, "NULL tensor pointer");
+  if (!aligned16(key) || !aligned16(value))
+    return fail(TL_ERR_INVALID_ARGUMENT, "key/value must be 16-byte aligned");
+  tl::CacheLaunch a = {key, value, k_cache, v_cache, slot_mapping, num_tokens, num_kv_heads,
+                       head_size, block_size, num_blocks, src_dtype, TL_DTYPE_FP8_E4M3, k_scale,
+                       v_scale, (hipStream_t)stream};
+  const int rc = tl::launch_reshape_and_cache(a);
+  if (rc == 3) return fail(TL_ERR_NOT_IMPLEMENTED, "no fp8 cache kernel for src_dtype=%d", src_dtype);
+  if (rc) return fail(TL_ERR_BACKEND, "reshape_and_cache_fp8 launch failed");
+  return ok();
+}
+
+int tl_fp8_absmax_scale(const void* x, int32_t dtype, int64_t n, float* scale_out, void* stream) {
+  if (n < 0 || !scale_out || (n > 0 && !x)) return fail(TL_ERR_INVALID_ARGUMENT, "bad arguments");
+  if (!is_float_kind(dtype)) return fail(TL_ERR_INVALID_ARGUMENT, "dtype=%d", dtype);
+  if (((uintptr_t)scale_out & 3u) != 0) return fail(TL_ERR_INVALID_ARGUMENT, "scale_out misaligned");
+  const int rc = tl::launch_fp8_scale(x, dtype, n, scale_out, (hipStream_t)stream);
+  if (rc) return fail(TL_ERR_BACKEND, "fp8 scale launch failed");
+  return ok();
+}
+
+}  // extern "C"

@@ -1,0 +1,170 @@
+// tl_cache.hip -- KV-cache writes for gfx950.
+//
+// reshape_and_cache (cache_kernels.cu:47-94, :202-232): scatter the new
+// tokens' K and V rows [T, n_kv, D] into the paged pools [N, n_kv, D, BS] at
+// slot = block * BS + offset; slot < 0 is a padded token and is skipped.
+// Each thread moves one 16-byte run of 8 head dims (one load per source
+// tensor) and writes them with stride BS into the block, converting to E4M3
+// on the way when the pool is FP8 (multiplier 1/scale, fp8_gemm.cu:89-93).
+//
+// fp8 scale: per-tensor absmax(x)/448, the E4M3 scale convention of
+// fp8_gemm.cu:82-84, as a grid-wide max.
+#include "tl_device.hpp"
+#include "tl_internal.hpp"
+
+namespace tl {
+
+namespace {
+
+template <Kind SRC> __device__ __forceinline__ void load8(const void* p, int64_t i, float* f);
+template <> __device__ __forceinline__ void load8<Kind::F16>(const void* p, int64_t i, float* f) {
+  const u32x4 c = load16((const uint16_t*)p + i);
+  Unpack<Kind::F16>::run(c.x, f); Unpack<Kind::F16>::run(c.y, f + 2);
+  Unpack<Kind::F16>::run(c.z, f + 4); Unpack<Kind::F16>::run(c.w, f + 6);
+}
+template <> __device__ __forceinline__ void load8<Kind::BF16>(const void* p, int64_t i, float* f) {
+  const u32x4 c = load16((const uint16_t*)p + i);
+  Unpack<Kind::BF16>::run(c.x, f); Unpack<Kind::BF16>::run(c.y, f + 2);
+  Unpack<Kind::BF16>::run(c.z, f + 4); Unpack<Kind::BF16>::run(c.w, f + 6);
+}
+
+// Same-type copy: move raw element bits (bit-exact, NaN payloads included).
+template <int E>
+__global__ __launch_bounds__(256) void reshape_copy_kernel(
+    const char* __restrict__ key, const char* __restrict__ value, char* __restrict__ k_cache,
+    char* __restrict__ v_cache, const int32_t* __restrict__ slots, int num_tokens,
+    int num_kv_heads, int head_size, int block_size, int num_blocks) {
+  constexpr int RUN = 16 / E;                       // elements per 16-byte run
+  const int runs = head_size / RUN;
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t total = (int64_t)num_tokens * num_kv_heads * runs;
+  if (idx >= total) return;
+  const int r = (int)(idx % runs);
+  const int h = (int)((idx / runs) % num_kv_heads);
+  const int t = (int)(idx / ((int64_t)runs * num_kv_heads));
+  const int32_t slot = slots[t];
+  if (slot < 0) return;
+  const int blk = slot / block_size, off = slot % block_size;
+  if (blk >= num_blocks) return;
+  const int64_t src = ((int64_t)t * num_kv_heads + h) * head_size + (int64_t)r * RUN;
+  const int64_t dst = (((int64_t)blk * num_kv_heads + h) * head_size + (int64_t)r * RUN) * block_size + off;
+  const u32x4 kk = load16(key + src * E), vv = load16(value + src * E);
+  const uint32_t kw[4] = {kk.x, kk.y, kk.z, kk.w}, vw[4] = {vv.x, vv.y, vv.z, vv.w};
+#pragma unroll
+  for (int i = 0; i < RUN; ++i) {
+    const int64_t o = (dst + (int64_t)i * block_size) * E;
+    if constexpr (E == 2) {
+      const int wi = i / 2, sh = (i % 2) * 16;
+      *(uint16_t*)(k_cache + o) = (uint16_t)(kw[wi] >> sh);
+      *(uint16_t*)(v_cache + o) = (uint16_t)(vw[wi] >> sh);
+    } else {
+      *(uint32_t*)(k_cache + o) = kw[i];
+      *(uint32_t*)(v_cache + o) = vw[i];
+    }
+  }
+}
+
+template <Kind SRC>
+__global__ __launch_bounds__(256) void reshape_fp8_kernel(
+    const void* __restrict__ key, const void* __restrict__ value, uint8_t* __restrict__ k_cache,
+    uint8_t* __restrict__ v_cache, const int32_t* __restrict__ slots, int num_tokens,
+    int num_kv_heads, int head_size, int block_size, int num_blocks, float k_mul, float v_mul) {
+  const int runs = head_size / 8;
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t total = (int64_t)num_tokens * num_kv_heads * runs;
+  if (idx >= total) return;
+  const int r = (int)(idx % runs);
+  const int h = (int)((idx / runs) % num_kv_heads);
+  const int t = (int)(idx / ((int64_t)runs * num_kv_heads));
+  const int32_t slot = slots[t];
+  if (slot < 0) return;
+  const int blk = slot / block_size, off = slot % block_size;
+  if (blk >= num_blocks) return;
+  const int64_t src = ((int64_t)t * num_kv_heads + h) * head_size + (int64_t)r * 8;
+  const int64_t dst = (((int64_t)blk * num_kv_heads + h) * head_size + (int64_t)r * 8) * block_size + off;
+  float kf[8], vf[8];
+  load8<SRC>(key, src, kf);
+  load8<SRC>(value, src, vf);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    k_cache[dst + (int64_t)i * block_size] = f32_to_fp8(kf[i] * k_mul);
+    v_cache[dst + (int64_t)i * block_size] = f32_to_fp8(vf[i] * v_mul);
+  }
+}
+
+__global__ void fill_u32_kernel(uint32_t* p, uint32_t v) { *p = v; }
+
+template <Kind SRC>
+__global__ __launch_bounds__(256) void absmax_kernel(const void* __restrict__ x, int64_t n,
+                                                     uint32_t* __restrict__ out_bits) {
+  float m = 0.f;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    m = fmaxf(m, fabsf(load_scalar<SRC>(x, i)));
+  m = wave_max<32, 1>(m);
+  if ((threadIdx.x % kWave) == 0) atomicMax(out_bits, __builtin_bit_cast(uint32_t, m));
+}
+
+__global__ void scale_finish_kernel(uint32_t* bits) {
+  const float amax = __builtin_bit_cast(float, *bits);
+  *reinterpret_cast<float*>(bits) = amax / 448.0f;
+}
+
+}  // namespace
+
+int launch_reshape_and_cache(const CacheLaunch& a) {
+  const int64_t runs_per_tok = (int64_t)a.num_kv_heads * (a.head_size / 8);
+  if (a.num_tokens == 0) return 0;
+  if (a.cache_dtype == (int)Kind::FP8) {
+    const int64_t total = (int64_t)a.num_tokens * runs_per_tok;
+    const dim3 grid((unsigned)((total + 255) / 256));
+    const float km = 1.0f / (a.k_scale == 0.f ? 1.f : a.k_scale);
+    const float vm = 1.0f / (a.v_scale == 0.f ? 1.f : a.v_scale);
+    if (a.src_dtype == (int)Kind::F16)
+      hipLaunchKernelGGL(reshape_fp8_kernel<Kind::F16>, grid, dim3(256), 0, a.stream, a.key,
+                         a.value, (uint8_t*)a.k_cache, (uint8_t*)a.v_cache, a.slot_mapping,
+                         a.num_tokens, a.num_kv_heads, a.head_size, a.block_size, a.num_blocks, km, vm);
+    else if (a.src_dtype == (int)Kind::BF16)
+      hipLaunchKernelGGL(reshape_fp8_kernel<Kind::BF16>, grid, dim3(256), 0, a.stream, a.key,
+                         a.value, (uint8_t*)a.k_cache, (uint8_t*)a.v_cache, a.slot_mapping,
+                         a.num_tokens, a.num_kv_heads, a.head_size, a.block_size, a.num_blocks, km, vm);
+    else
+      return 3;
+  } else {
+    const int E = (a.cache_dtype == (int)Kind::F32) ? 4 : 2;
+    const int64_t total = (int64_t)a.num_tokens * a.num_kv_heads * (a.head_size / (16 / E));
+    const dim3 grid((unsigned)((total + 255) / 256));
+    if (E == 2)
+      hipLaunchKernelGGL(reshape_copy_kernel<2>, grid, dim3(256), 0, a.stream,
+                         (const char*)a.key, (const char*)a.value, (char*)a.k_cache,
+                         (char*)a.v_cache, a.slot_mapping, a.num_tokens, a.num_kv_heads,
+                         a.head_size, a.block_size, a.num_blocks);
+    else
+      hipLaunchKernelGGL(reshape_copy_kernel<4>, grid, dim3(256), 0, a.stream,
+                         (const char*)a.key, (const char*)a.value, (char*)a.k_cache,
+                         (char*)a.v_cache, a.slot_mapping, a.num_tokens, a.num_kv_heads,
+                         a.head_size, a.block_size, a.num_blocks);
+  }
+  return hipGetLastError() == hipSuccess ? 0 : 5;
+}
+
+int launch_fp8_scale(const void* x, int dtype, int64_t n, float* scale_out, hipStream_t stream) {
+  uint32_t* bits = reinterpret_cast<uint32_t*>(scale_out);
+  hipLaunchKernelGGL(fill_u32_kernel, dim3(1), dim3(1), 0, stream, bits, 0u);
+  if (n > 0) {
+    const int64_t want = (n + 255) / 256;
+    const dim3 grid((unsigned)(want < 4096 ? want : 4096));
+    if (dtype == (int)Kind::F16)
+      hipLaunchKernelGGL(absmax_kernel<Kind::F16>, grid, dim3(256), 0, stream, x, n, bits);
+    else if (dtype == (int)Kind::BF16)
+      hipLaunchKernelGGL(absmax_kernel<Kind::BF16>, grid, dim3(256), 0, stream, x, n, bits);
+    else if (dtype == (int)Kind::F32)
+      hipLaunchKernelGGL(absmax_kernel<Kind::F32>, grid, dim3(256), 0, stream, x, n, bits);
+    else
+      return 3;
+  }
+  hipLaunchKernelGGL(scale_finish_kernel, dim3(1), dim3(1), 0, stream, bits);
+  return hipGetLastError() == hipSuccess ? 0 : 5;
+}
+
+}  // namespace tl

@@ -1,0 +1,225 @@
+"""Python host mirror of truellm-engine's attention operator interface over
+the gfx950 C ABI (include/tl_attn.h, libtlattn.so).
+
+The reference exposes free C++ functions taking TrueBuffer views
+(paged_attention_v1.cu:177, paged_attention_v2.cu:176, cache_kernels.cu:202,
+kivi_cache.cu:205-239).  The functions here take torch tensors on the GPU in
+the same roles and with the same argument meaning; shapes are read from the
+tensors the way the reference reads TrueBuffer.shape.  They launch on the
+current torch stream and raise TLError when the library reports an error.
+
+torch is only the device-memory and stream plumbing: every computation runs
+in the HIP kernels of libtlattn.so.  There is no fallback: importing this
+module without the built library raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libtlattn.so")
+HEADER_DIR = os.path.join(os.path.dirname(_HERE), "include")
+
+# tl_dtype (mirrors truellm::DataType for the first three)
+F32, F16, BF16, FP8_E4M3 = 0, 1, 2, 32
+# tl_gqa_map
+GQA_MODULO, GQA_GROUPED = 0, 1
+# tl_status
+OK, ERR_INVALID_ARGUMENT, ERR_NOT_IMPLEMENTED, ERR_BACKEND, ERR_INTERNAL = 0, 1, 3, 5, 99
+
+KIVI_MAX_HEAD_DIM = 128
+KIVI_MAX_OUTLIERS = 64
+
+
+class TLError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"tl_status {code}: {msg}")
+        self.code = code
+
+
+class DecodeDesc(ctypes.Structure):
+    _fields_ = [
+        ("num_seqs", ctypes.c_int32),
+        ("num_heads", ctypes.c_int32),
+        ("num_kv_heads", ctypes.c_int32),
+        ("head_size", ctypes.c_int32),
+        ("block_size", ctypes.c_int32),
+        ("max_blocks_per_seq", ctypes.c_int32),
+        ("num_blocks", ctypes.c_int32),
+        ("q_dtype", ctypes.c_int32),
+        ("kv_dtype", ctypes.c_int32),
+        ("gqa_map", ctypes.c_int32),
+        ("partition_tokens", ctypes.c_int32),
+        ("scale", ctypes.c_float),
+        ("k_scale", ctypes.c_float),
+        ("v_scale", ctypes.c_float),
+    ]
+
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int32
+_F = ctypes.c_float
+_SIG = {
+    "tl_abi_version": (ctypes.c_int, []),
+    "tl_last_error_string": (ctypes.c_char_p, []),
+    "tl_paged_attention_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(DecodeDesc), _I]),
+    "tl_paged_attention_decode": (ctypes.c_int, [ctypes.POINTER(DecodeDesc), _P, _P, _P, _P, _P, _P, _I, _P, ctypes.c_size_t, _P]),
+    "tl_paged_attention_v1": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F, _I, _I, _P]),
+    "tl_paged_attention_v2": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F, _I, _I, _I, _P]),
+    "tl_reshape_and_cache": (ctypes.c_int, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P]),
+    "tl_reshape_and_cache_fp8": (ctypes.c_int, [_P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _I, _F, _F, _P]),
+    "tl_fp8_absmax_scale": (ctypes.c_int, [_P, _I, ctypes.c_int64, _P, _P]),
+}
+
+
+def _load() -> ctypes.CDLL:
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(f"{LIB_PATH} is not built; run __graft_entry__.build() (make -C truellm-engine_amd)")
+    lib = ctypes.CDLL(LIB_PATH)
+    for name, (res, args) in _SIG.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
+lib = _load()
+
+
+def header_functions() -> list[str]:
+    """Names of every function declared in include/*.h."""
+    names = []
+    for fn in sorted(os.listdir(HEADER_DIR)):
+        if not fn.endswith(".h"):
+            continue
+        text = open(os.path.join(HEADER_DIR, fn)).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        names += re.findall(r"^[A-Za-z_][\w \*]*?\b(tl_\w+)\s*\(", text, flags=re.M)
+    return names
+
+
+def last_error() -> str:
+    return lib.tl_last_error_string().decode()
+
+
+def check(rc: int) -> None:
+    if rc != OK:
+        raise TLError(rc, last_error())
+
+
+# ---------------------------------------------------------------------------
+# torch helpers (import lazily so ABI tests run without touching the GPU)
+# ---------------------------------------------------------------------------
+
+def _torch():
+    import torch
+    return torch
+
+
+def dtype_code(t) -> int:
+    torch = _torch()
+    m = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16, torch.uint8: FP8_E4M3}
+    if t.dtype not in m:
+        raise TLError(ERR_INVALID_ARGUMENT, f"unsupported tensor dtype {t.dtype}")
+    return m[t.dtype]
+
+
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(stream=None):
+    torch = _torch()
+    s = torch.cuda.current_stream() if stream is None else stream
+    return ctypes.c_void_p(s.cuda_stream)
+
+
+# ---------------------------------------------------------------------------
+# Reference operator interface (same names, same argument roles)
+# ---------------------------------------------------------------------------
+
+def paged_attention_v1(out, q, k_cache, v_cache, block_tables, seq_lens, num_kv_heads, scale,
+                       head_size, block_size, stream=None, gqa_map=GQA_MODULO):
+    """paged_attention_v1.cu:177: q/out [S, H, D]; k/v_cache [N, n_kv, D, BS]."""
+    S, H = q.shape[0], q.shape[1]
+    check(lib.tl_paged_attention_v1(
+        _ptr(out), _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(block_tables), _ptr(seq_lens),
+        S, H, num_kv_heads, head_size, block_size, block_tables.shape[1], k_cache.shape[0],
+        scale, dtype_code(q), gqa_map, _stream(stream)))
+
+
+def paged_attention_v2(out, exp_sums, max_logits, tmp_out, q, k_cache, v_cache, block_tables,
+                       seq_lens, num_kv_heads, scale, head_size, block_size, max_context_len,
+                       stream=None, gqa_map=GQA_MODULO):
+    """paged_attention_v2.cu:176: scratch exp_sums/max_logits [S, H, P] fp32,
+    tmp_out [S, H, P, D] in q's dtype, P = ceil(max_context_len / (32 * BS))."""
+    S, H = q.shape[0], q.shape[1]
+    check(lib.tl_paged_attention_v2(
+        _ptr(out), _ptr(exp_sums), _ptr(max_logits), _ptr(tmp_out), _ptr(q), _ptr(k_cache),
+        _ptr(v_cache), _ptr(block_tables), _ptr(seq_lens), S, H, num_kv_heads, head_size,
+        block_size, block_tables.shape[1], k_cache.shape[0], scale, dtype_code(q), gqa_map,
+        max_context_len, _stream(stream)))
+
+
+def v2_num_partitions(max_context_len: int, block_size: int) -> int:
+    pt = 32 * block_size
+    return max(1, (max_context_len + pt - 1) // pt)
+
+
+def reshape_and_cache(key, value, kv_cache, slot_mapping, stream=None):
+    """cache_kernels.cu:202: key/value [T, n_kv, D]; kv_cache [2N, n_kv, D, BS]
+    holding the K pool then the V pool."""
+    T, n_kv, D = key.shape
+    N = kv_cache.shape[0] // 2
+    k_cache, v_cache = kv_cache[:N], kv_cache[N:]
+    reshape_and_cache_split(key, value, k_cache, v_cache, slot_mapping, stream)
+
+
+def reshape_and_cache_split(key, value, k_cache, v_cache, slot_mapping, stream=None):
+    T, n_kv, D = key.shape
+    check(lib.tl_reshape_and_cache(
+        _ptr(key), _ptr(value), _ptr(k_cache), _ptr(v_cache), _ptr(slot_mapping), T, n_kv, D,
+        k_cache.shape[3], k_cache.shape[0], dtype_code(key), _stream(stream)))
+
+
+def reshape_and_cache_fp8(key, value, k_cache, v_cache, slot_mapping, k_scale, v_scale,
+                          stream=None):
+    T, n_kv, D = key.shape
+    check(lib.tl_reshape_and_cache_fp8(
+        _ptr(key), _ptr(value), dtype_code(key), _ptr(k_cache), _ptr(v_cache), _ptr(slot_mapping),
+        T, n_kv, D, k_cache.shape[3], k_cache.shape[0], k_scale, v_scale, _stream(stream)))
+
+
+def fp8_absmax_scale(x, scale_out, stream=None):
+    check(lib.tl_fp8_absmax_scale(_ptr(x), dtype_code(x), x.numel(), _ptr(scale_out),
+                                  _stream(stream)))
+
+
+def make_decode_desc(q, k_cache, block_tables, num_kv_heads, scale, *, kv_dtype=None,
+                     gqa_map=GQA_GROUPED, partition_tokens=0, k_scale=1.0, v_scale=1.0):
+    S, H, D = q.shape
+    d = DecodeDesc()
+    d.num_seqs, d.num_heads, d.num_kv_heads, d.head_size = S, H, num_kv_heads, D
+    d.block_size = k_cache.shape[3]
+    d.max_blocks_per_seq = block_tables.shape[1]
+    d.num_blocks = k_cache.shape[0]
+    d.q_dtype = dtype_code(q)
+    d.kv_dtype = dtype_code(k_cache) if kv_dtype is None else kv_dtype
+    d.gqa_map = gqa_map
+    d.partition_tokens = partition_tokens
+    d.scale, d.k_scale, d.v_scale = scale, k_scale, v_scale
+    return d
+
+
+def workspace_bytes(desc: DecodeDesc, max_context_len: int) -> int:
+    return lib.tl_paged_attention_workspace_bytes(ctypes.byref(desc), max_context_len)
+
+
+def paged_attention_decode(desc: DecodeDesc, out, q, k_cache, v_cache, block_tables, seq_lens,
+                           max_context_len, workspace=None, stream=None):
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    check(lib.tl_paged_attention_decode(
+        ctypes.byref(desc), _ptr(out), _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(block_tables),
+        _ptr(seq_lens), max_context_len, _ptr(workspace), ws_bytes, _stream(stream)))
