@@ -74,10 +74,25 @@ _SIG = {
 }
 
 
+def _hip_runtimes() -> set:
+    try:
+        with open("/proc/self/maps") as f:
+            return {ln.split()[-1] for ln in f if "libamdhip64" in ln}
+    except OSError:
+        return set()
+
+
 def _load() -> ctypes.CDLL:
     if not os.path.exists(LIB_PATH):
         raise RuntimeError(f"{LIB_PATH} is not built; run __graft_entry__.build() (make -C truellm-engine_amd)")
+    # torch ships its own libamdhip64 with the same SONAME as /opt/rocm's.  Loading
+    # torch first makes libtlattn.so bind to that runtime, so torch's allocations and
+    # streams and our launches share one HIP runtime.  Importing torch does not
+    # initialise the GPU.
+    import torch  # noqa: F401
     lib = ctypes.CDLL(LIB_PATH)
+    if len(_hip_runtimes()) > 1:
+        raise RuntimeError(f"two HIP runtimes loaded in one process: {sorted(_hip_runtimes())}")
     for name, (res, args) in _SIG.items():
         fn = getattr(lib, name)
         fn.restype = res
