@@ -109,6 +109,24 @@ def test_edge_lengths_and_holes(runner):
     assert (host_f64(out[0]) == 0).all()                     # empty sequence -> zeros
 
 
+@pytest.mark.parametrize("H,n_kv", [(8, 2), (4, 4)])
+@pytest.mark.parametrize("code", [orc.F16, orc.BF16])
+@pytest.mark.parametrize("runner", ["v1", "pt512"])
+def test_unused_slots_holding_nan_are_ignored(code, runner, H, n_kv):
+    """Slots past seq_len in a sequence's last block (and blocks past it) may
+    hold anything, NaN included; they must not reach the output."""
+    lens = [33, 500, 1031]
+    case = inputs.make_paged_case(34, 3, H, n_kv, 128, 16, lens, code)
+    nan = np.uint16(0x7E00 if code == orc.F16 else 0x7FC0)
+    for s, L in enumerate(lens):
+        last = case.tables[s, (L - 1) // 16]
+        case.k_cache[last, :, :, L % 16 or 16:] = nan
+        case.v_cache[last, :, :, L % 16 or 16:] = nan
+    print(f"case nan-slots code={code} runner={runner}", flush=True)
+    assert_close(RUNNERS[runner](case, tla.GQA_GROUPED), _ref(case, tla.GQA_GROUPED), code, ATOL,
+                 runner)
+
+
 @pytest.mark.parametrize("H,n_kv", [(4, 4), (6, 2), (16, 2), (8, 1)])
 @pytest.mark.parametrize("runner", ["v1", "pt512"])
 def test_gqa_group_sizes(H, n_kv, runner):

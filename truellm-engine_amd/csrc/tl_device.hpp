@@ -169,6 +169,74 @@ __device__ __forceinline__ int transpose_reduce(float* v, int lane) {
   return base;
 }
 
+// ---- cross-lane steps that stay in the VALU ---------------------------------
+// gfx950 v_permlane16_swap / v_permlane32_swap exchange half-rows between two
+// registers.  Fed (lo, hi) they give every lane (own, partner) copies of the
+// half it keeps (lo for lanes with bit 4 / bit 5 clear, hi otherwise), so a
+// transpose-reduce level is one swap and one add, with no select.
+__device__ __forceinline__ float swap16_add(float lo, float hi) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(unsigned, lo),
+                                                  __builtin_bit_cast(unsigned, hi), false, false);
+  return __builtin_bit_cast(float, (unsigned)r[0]) + __builtin_bit_cast(float, (unsigned)r[1]);
+}
+__device__ __forceinline__ float swap32_add(float lo, float hi) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, lo),
+                                                  __builtin_bit_cast(unsigned, hi), false, false);
+  return __builtin_bit_cast(float, (unsigned)r[0]) + __builtin_bit_cast(float, (unsigned)r[1]);
+}
+
+// DPP lane reads within a row of 16 lanes.
+constexpr int kDppXor1 = 0xB1;         // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;         // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141;  // lane i <- 7 - i within each 8 lanes
+constexpr int kDppMirror = 0x140;      // lane i <- 15 - i within each row
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+// Max / sum over the 16 lanes of a row (masks 1, 2, 7, 15 span the 4 bits).
+__device__ __forceinline__ float row_max(float v) {
+  v = __builtin_fmaxf(v, dpp<kDppXor1>(v));
+  v = __builtin_fmaxf(v, dpp<kDppXor2>(v));
+  v = __builtin_fmaxf(v, dpp<kDppHalfMirror>(v));
+  return __builtin_fmaxf(v, dpp<kDppMirror>(v));
+}
+__device__ __forceinline__ float row_sum(float v) {
+  v += dpp<kDppXor1>(v);
+  v += dpp<kDppXor2>(v);
+  v += dpp<kDppHalfMirror>(v);
+  return v + dpp<kDppMirror>(v);
+}
+
+// Transpose-reduce of N values over lane bits 5, 4, 1, 0 (in that order).
+// Afterwards v[0 .. N/16) of each lane hold the sums of value indices
+// base + i with base = (N/2)*b5 + (N/4)*b4 + (N/8)*b1 + (N/16)*b0.
+template <int N>
+__device__ __forceinline__ void transpose_reduce_5410(float* v, int lane) {
+  static_assert(N >= 16 && N % 16 == 0, "16 lanes share the values");
+#pragma unroll
+  for (int i = 0; i < N / 2; ++i) v[i] = swap32_add(v[i], v[i + N / 2]);
+#pragma unroll
+  for (int i = 0; i < N / 4; ++i) v[i] = swap16_add(v[i], v[i + N / 4]);
+  {
+    const bool up = (lane & 2) != 0;
+#pragma unroll
+    for (int i = 0; i < N / 8; ++i) {
+      const float keep = up ? v[i + N / 8] : v[i], give = up ? v[i] : v[i + N / 8];
+      v[i] = keep + dpp<kDppXor2>(give);
+    }
+  }
+  {
+    const bool up = (lane & 1) != 0;
+#pragma unroll
+    for (int i = 0; i < N / 16; ++i) {
+      const float keep = up ? v[i + N / 16] : v[i], give = up ? v[i] : v[i + N / 16];
+      v[i] = keep + dpp<kDppXor1>(give);
+    }
+  }
+}
+
 // Number of values a lane keeps after transpose_reduce<N, HI, LO>.
 template <int N, int MASK_HI, int MASK_LO>
 constexpr int transpose_kept() {

@@ -29,6 +29,7 @@ struct DecodeLaunch {
   int partition_tokens;         // multiple of kDecodeChunk when P > 1
   int q_dtype, kv_dtype, gqa_map;
   float scale, k_scale, v_scale;
+  int use_generic;              // 1 = force the generic (FMA) decode kernel
   hipStream_t stream;
 };
 
