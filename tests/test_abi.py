@@ -73,9 +73,12 @@ def test_workspace_is_zero_for_single_pass():
 
 
 def test_auto_partitioning_targets_many_workgroups():
-    # 64 x 8 work items at 4096 tokens -> 4 partitions of 1024
-    d = _desc(num_seqs=64)
-    assert tla.workspace_bytes(d, 4096) == 64 * 32 * 4 * (128 * 4 + 8)
+    # 64 x 8 work items already fill the GPU: single pass
+    assert tla.workspace_bytes(_desc(num_seqs=64), 4096) == 0
+    # 4 x 8 items at 4096 tokens -> 8 partitions of 512
+    assert tla.workspace_bytes(_desc(num_seqs=4), 4096) == 4 * 32 * 8 * (128 * 4 + 8)
+    # 16 x 8 items at 32768 tokens -> 4 partitions of 8192
+    assert tla.workspace_bytes(_desc(num_seqs=16), 32768) == 16 * 32 * 4 * (128 * 4 + 8)
 
 
 def test_empty_batch_is_a_no_op():

@@ -68,7 +68,9 @@ int check_decode(const tl_decode_desc* d) {
 }
 
 // Split-K plan: partition size and count for a batch whose longest sequence
-// is max_ctx.  Aim for >= 2048 workgroups (8 per CU on 256 CUs).
+// is max_ctx.  Aim for >= 512 workgroups (two per CU on 256 CUs, which is
+// what the single-pass kernels' occupancy admits); a batch that already
+// provides that many (sequence, kv head) items runs single pass.
 void plan_partitions(const tl_decode_desc* d, int32_t max_ctx, int* P, int* PT) {
   const int chunks = max_ctx > 0 ? (max_ctx + tl::kDecodeChunk - 1) / tl::kDecodeChunk : 1;
   int pt_chunks;
@@ -80,7 +82,7 @@ void plan_partitions(const tl_decode_desc* d, int32_t max_ctx, int* P, int* PT) 
     const int group = d->num_heads / d->num_kv_heads;
     const int slices = group == 1 ? 1 : (group + 3) / 4;
     const long items = (long)d->num_seqs * d->num_kv_heads * slices;
-    long want = items > 0 ? (2048 + items - 1) / items : 1;
+    long want = items > 0 ? (512 + items - 1) / items : 1;
     if (want < 1) want = 1;
     if (want > chunks) want = chunks;
     pt_chunks = (int)((chunks + want - 1) / want);

@@ -370,8 +370,8 @@ __device__ __forceinline__ void load_k_pairs(u32x4 (&kr)[KP][2], const char* blk
 #pragma unroll
   for (int j = 0; j < KP; ++j) {
     const int c = 2 * (dl + 16 * j) * CPR + th;
-    kr[j][0] = load16(blk + c * 16);
-    kr[j][1] = load16(blk + (c + CPR) * 16);
+    kr[j][0] = load16_stream(blk + c * 16);
+    kr[j][1] = load16_stream(blk + (c + CPR) * 16);
   }
 }
 
@@ -379,7 +379,7 @@ __device__ __forceinline__ void load_k_pairs(u32x4 (&kr)[KP][2], const char* blk
 template <int VD, int CPR>
 __device__ __forceinline__ void load_v_rows(u32x4 (&vr)[VD], const char* blk, int dl, int th) {
 #pragma unroll
-  for (int j = 0; j < VD; ++j) vr[j] = load16(blk + ((16 * j + dl) * CPR + th) * 16);
+  for (int j = 0; j < VD; ++j) vr[j] = load16_stream(blk + ((16 * j + dl) * CPR + th) * 16);
 }
 
 template <Kind KV, Kind PO, int HEAD, int BS, int NW, bool FINAL>

@@ -115,6 +115,14 @@ __device__ __forceinline__ u32x4 load16(const void* p) {
   return *reinterpret_cast<const u32x4*>(p);
 }
 
+// Streaming 16-byte load (non-temporal hint): KV bytes are read once per
+// decode step, so they should not displace reusable lines in L2 / MALL.
+typedef unsigned u32v4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ u32x4 load16_stream(const void* p) {
+  const u32v4 v = __builtin_nontemporal_load(reinterpret_cast<const u32v4*>(p));
+  return u32x4{v.x, v.y, v.z, v.w};
+}
+
 // ---- wavefront reductions ----------------------------------------------------
 __device__ __forceinline__ float shfl_xor(float v, int mask) {
   return __shfl_xor(v, mask, kWave);
