@@ -139,6 +139,92 @@ int tl_reshape_and_cache_fp8(const void* key, const void* value, int32_t src_dty
 int tl_fp8_absmax_scale(const void* x, int32_t dtype, int64_t n, float* scale_out,
                         void* stream);
 
+/* ------------------------------------------------------------------------
+ * Reference KIVI vector codec (kivi_cache.cuh:27-84, kivi_cache.cu:23-239)
+ * --------------------------------------------------------------------- */
+
+#define TL_KIVI_MAX_HEAD_DIM 128
+#define TL_KIVI_MAX_OUTLIERS 64
+
+/* Record stride of one compressed vector: 3*n_outliers +
+ * ceil((head_dim - n_outliers) / group_size) * (group_size/2 + 4)
+ * (kivi_compressed_bytes, kivi_cache.cuh:32-43). */
+size_t tl_kivi_compressed_bytes(int32_t head_dim, int32_t n_outliers, int32_t group_size);
+
+/* 1 iff 0 < head_dim <= 128, 0 <= n_outliers <= 64, n_outliers <= head_dim
+ * and group_size > 0 (kivi_params_supported, kivi_cache.cu:205-211). */
+int tl_kivi_params_supported(int32_t head_dim, int32_t n_outliers, int32_t group_size);
+
+/* Replace kivi_compress / kivi_decompress (kivi_cache.cu:213-239): kv fp16
+ * [n_vecs, head_dim] <-> records u8 [n_vecs, stride], bit-exact with the
+ * reference.  Unsupported parameters and odd group sizes (whose records
+ * overrun the reference's stride) return TL_ERR_INVALID_ARGUMENT and touch
+ * nothing; n_vecs == 0 is a no-op. */
+int tl_kivi_compress(const void* kv_in, uint8_t* out, int32_t n_vecs, int32_t head_dim,
+                     int32_t n_outliers, int32_t group_size, void* stream);
+int tl_kivi_decompress(const uint8_t* in, void* kv_out, int32_t n_vecs, int32_t head_dim,
+                       int32_t n_outliers, int32_t group_size, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Paged KIVI INT4 KV: K per channel and V per token, groups of 32, fp16
+ * step/zero, nibbles two per byte, the most recent residual_length tokens
+ * (plus up to 31 more) kept in the fp16 pool (KiviConfig, config_schema.h:
+ * 122-129, which the reference declares but never implements).
+ * A sequence of length L holds its first
+ *   Lq = L <= R ? 0 : floor((L - R) / 32) * 32
+ * tokens in pages; page p covers tokens [32p, 32p + 32).  Pages live in a
+ * pool [num_pages, num_kv_heads, 5120 B] addressed by page_tables
+ * [num_seqs, max_pages_per_seq]; the fp16 pool keeps every token.
+ * --------------------------------------------------------------------- */
+
+#define TL_KIVI_PAGE_TOKENS 32
+#define TL_KIVI_PAGE_BYTES 5120   /* per kv head, head_size 128 */
+
+typedef struct tl_kivi_desc {
+  int32_t num_seqs;
+  int32_t num_heads;
+  int32_t num_kv_heads;
+  int32_t head_size;           /* 128 */
+  int32_t block_size;          /* 16 (fp16 pool) */
+  int32_t max_blocks_per_seq;
+  int32_t num_blocks;
+  int32_t max_pages_per_seq;
+  int32_t num_pages;
+  int32_t residual_length;     /* R >= 0 */
+  int32_t gqa_map;
+  int32_t partition_pages;     /* 0 = choose, -1 = single pass, else pages per partition */
+  float scale;
+} tl_kivi_desc;
+
+int32_t tl_kivi_quantized_len(int32_t seq_len, int32_t residual_length);
+
+/* Quantise every page of every sequence's prefix (tokens < Lq(seq_lens[s]))
+ * from the fp16 pools.  Bit-exact with the reference quantiser. */
+int tl_kivi_build_pages(const tl_kivi_desc* desc, const void* k_cache, const void* v_cache,
+                        const int32_t* block_tables, const int32_t* seq_lens,
+                        const int32_t* page_tables, void* pages, int32_t max_context_len,
+                        void* stream);
+
+/* Append one token per sequence: key/value fp16 [S, n_kv, 128] go to the
+ * fp16 pools at slot_mapping[s] (as tl_reshape_and_cache), then every
+ * sequence whose new length seq_lens[s] completes a page (Lq grows) has that
+ * page quantised. */
+int tl_kivi_append(const tl_kivi_desc* desc, const void* key, const void* value, void* k_cache,
+                   void* v_cache, const int32_t* slot_mapping, const int32_t* block_tables,
+                   const int32_t* seq_lens, const int32_t* page_tables, void* pages,
+                   void* stream);
+
+size_t tl_kivi_workspace_bytes(const tl_kivi_desc* desc, int32_t max_context_len);
+
+/* Decode attention over pages (tokens < Lq) and the fp16 pool (tokens >= Lq).
+ * q, out fp16 [S, H, 128]. */
+int tl_kivi_paged_attention_decode(const tl_kivi_desc* desc, void* out, const void* q,
+                                   const void* pages, const int32_t* page_tables,
+                                   const void* k_cache, const void* v_cache,
+                                   const int32_t* block_tables, const int32_t* seq_lens,
+                                   int32_t max_context_len, void* workspace,
+                                   size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

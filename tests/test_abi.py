@@ -113,3 +113,56 @@ def test_reshape_rejects_bad_arguments():
     assert L.tl_reshape_and_cache_fp8(FAKE, FAKE, tla.F32, FAKE, FAKE, FAKE, 4, 8, 128, 16, 10,
                                       1.0, 1.0, None) == tla.ERR_NOT_IMPLEMENTED
     assert L.tl_fp8_absmax_scale(FAKE, tla.F16, -1, FAKE, None) == tla.ERR_INVALID_ARGUMENT
+
+
+def test_kivi_host_helpers_match_reference_known_answers():
+    # test_kivi_bounds.cpp:25-69, through the library
+    assert tla.kivi_compressed_bytes(128, 8, 16) == 24 + 8 * 12
+    assert tla.kivi_compressed_bytes(64, 0, 16) == 4 * 12
+    assert tla.kivi_compressed_bytes(64, 64, 16) == 64 * 3
+    assert tla.kivi_params_supported(128, 8, 16)
+    assert tla.kivi_params_supported(64, 4, 16)
+    assert tla.kivi_params_supported(tla.KIVI_MAX_HEAD_DIM, tla.KIVI_MAX_OUTLIERS, 16)
+    for bad in [(129, 8, 16), (128, 65, 16), (16, 32, 16), (128, 8, 0), (128, 8, -4), (0, 0, 16),
+                (-1, 0, 16)]:
+        assert not tla.kivi_params_supported(*bad)
+    assert tla.KIVI_MAX_HEAD_DIM == 128 and tla.KIVI_MAX_OUTLIERS == 64
+
+
+def test_kivi_quantized_len():
+    assert tla.kivi_quantized_len(4096, 128) == 3968
+    assert tla.kivi_quantized_len(159, 128) == 0
+    assert tla.kivi_quantized_len(160, 128) == 32
+    assert tla.kivi_quantized_len(5, 0) == 0 and tla.kivi_quantized_len(64, 0) == 64
+
+
+def test_kivi_codec_rejects_unsupported_and_odd_groups():
+    L = tla.lib
+    assert L.tl_kivi_compress(FAKE, FAKE, 1, 256, 0, 16, None) == tla.ERR_INVALID_ARGUMENT
+    assert L.tl_kivi_compress(FAKE, FAKE, 1, 128, 8, 5, None) == tla.ERR_INVALID_ARGUMENT
+    assert L.tl_kivi_decompress(FAKE, FAKE, -1, 128, 8, 16, None) == tla.ERR_INVALID_ARGUMENT
+    assert L.tl_kivi_compress(None, None, 0, 128, 8, 16, None) == tla.OK
+
+
+def _kdesc(**kw):
+    d = tla.KiviDesc()
+    d.num_seqs, d.num_heads, d.num_kv_heads, d.head_size, d.block_size = 64, 32, 8, 128, 16
+    d.max_blocks_per_seq, d.num_blocks, d.max_pages_per_seq, d.num_pages = 256, 20480, 128, 8192
+    d.residual_length, d.gqa_map, d.partition_pages, d.scale = 128, 1, 0, 0.088
+    for k, v in kw.items():
+        setattr(d, k, v)
+    return d
+
+
+def test_kivi_decode_descriptor_checks_and_planning():
+    L = tla.lib
+    call = lambda d: L.tl_kivi_paged_attention_decode(ctypes.byref(d), FAKE, FAKE, FAKE, FAKE,
+                                                      FAKE, FAKE, FAKE, FAKE, 4096, None, 0, None)
+    assert call(_kdesc(head_size=64)) == tla.ERR_NOT_IMPLEMENTED
+    assert call(_kdesc(block_size=32)) == tla.ERR_NOT_IMPLEMENTED
+    assert call(_kdesc(residual_length=-1)) == tla.ERR_INVALID_ARGUMENT
+    assert call(_kdesc(num_pages=0)) == tla.ERR_INVALID_ARGUMENT
+    assert tla.kivi_workspace_bytes(_kdesc(), 4096) == 0               # 512 items: single pass
+    # 4 x 8 items, 124 pages -> 16 partitions of 8 pages
+    assert tla.kivi_workspace_bytes(_kdesc(num_seqs=4), 4096) == 4 * 32 * 16 * (128 * 4 + 8)
+    assert call(_kdesc(num_seqs=4)) == tla.ERR_INVALID_ARGUMENT        # workspace missing

@@ -1,0 +1,239 @@
+"""KIVI INT4 on the GPU against the oracle.
+
+Codec bytes (records, pages, nibbles, scales, zeros) must be bit-exact;
+decode attention is compared with attention on the oracle's dequantised
+pages plus the fp16 residual window, max-abs 1e-2 (plus half an fp16 ulp)."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import inputs
+import oracle_lib as orc
+import tl_attn as tla
+from gpu_util import assert_close, dev, host_bits
+
+pytestmark = pytest.mark.gpu
+
+ATOL_KIVI = 1e-2
+
+
+def _f16(x):
+    return np.asarray(x, np.float32).astype(np.float16).view(np.uint16)
+
+
+# ---------------------------------------------------------------------------
+# reference vector codec
+# ---------------------------------------------------------------------------
+
+def _special_vectors(rng, n, D):
+    x = rng.standard_normal((n, D)).astype(np.float32)
+    x[0] = 2.5                                   # degenerate groups
+    x[1, : D // 2] = 0.0                         # constant halves
+    x[2] = np.round(x[2] * 4) / 4                # many exact ties
+    x[3, 5] = 60000.0                            # large outlier
+    x[4] *= 1e-4                                 # tiny values
+    x[5, 0::2] = -x[5, 1::2]                   # +-pairs of equal magnitude
+    return x
+
+
+@pytest.mark.parametrize("D,O,G", [(128, 8, 16), (64, 4, 16), (64, 0, 16), (32, 0, 16),
+                                   (100, 3, 10), (128, 64, 16), (64, 64, 16), (128, 0, 32),
+                                   (96, 13, 8)])
+def test_vector_codec_bit_exact(D, O, G):
+    rng = np.random.default_rng(D * 131 + O * 7 + G)
+    n = 300
+    xb = _f16(_special_vectors(rng, n, D)).reshape(n, D)
+    stride = orc.kivi_compressed_bytes(D, O, G)
+    want = np.full(n * stride, 0xAB, np.uint8)
+    orc.kivi_compress(xb, D, O, G, out=want)
+    rec = torch.full((n * stride,), 0xAB, dtype=torch.uint8, device="cuda")
+    print(f"case vec codec D={D} O={O} G={G}", flush=True)
+    tla.kivi_compress(dev(xb, orc.F16), rec, n, D, O, G)
+    torch.cuda.synchronize()
+    got = rec.cpu().numpy()
+    assert np.array_equal(got, want)
+    back = torch.zeros(n, D, dtype=torch.float16, device="cuda")
+    tla.kivi_decompress(rec, back, n, D, O, G)
+    torch.cuda.synchronize()
+    assert np.array_equal(host_bits(back).ravel(), orc.kivi_decompress(want, n, D, O, G))
+
+
+def test_vector_codec_reference_roundtrips():
+    """test_kivi_roundtrip.cpp:83-200 on the GPU path."""
+    def rt(x, D, O, G):
+        n = x.size // D
+        xd = dev(_f16(x).reshape(n, D), orc.F16)
+        rec = torch.zeros(n * tla.kivi_compressed_bytes(D, O, G), dtype=torch.uint8, device="cuda")
+        out = torch.zeros(n, D, dtype=torch.float16, device="cuda")
+        tla.kivi_compress(xd, rec, n, D, O, G)
+        tla.kivi_decompress(rec, out, n, D, O, G)
+        torch.cuda.synchronize()
+        return out.float().cpu().numpy().ravel()
+
+    x = np.array([[0.1 * d + 0.5 * v for d in range(64)] for v in range(3)], np.float32).ravel()
+    assert np.abs(rt(x, 64, 0, 16) - x).max() <= 0.15
+    x = np.array([0.01 * (i % 64) for i in range(128)], np.float32)
+    for v in range(2):
+        for k, ch in enumerate([3, 17, 33, 55]):
+            x[v * 64 + ch] = 50.0 + k + v
+    assert np.abs(rt(x, 64, 4, 16) - x).max() <= 0.1
+    assert np.abs(rt(np.full(32, 2.5, np.float32), 32, 0, 16) - 2.5).max() <= 1e-2
+
+
+def test_vector_codec_unsupported_params_leave_output_untouched():
+    """test_kivi_roundtrip.cpp:207-229: head_dim 256 is refused, sentinel stays."""
+    stride = tla.kivi_compressed_bytes(256, 0, 16)
+    rec = torch.full((stride,), 0xAB, dtype=torch.uint8, device="cuda")
+    x = torch.ones(1, 256, dtype=torch.float16, device="cuda")
+    with pytest.raises(tla.TLError):
+        tla.kivi_compress(x, rec, 1, 256, 0, 16)
+    torch.cuda.synchronize()
+    assert (rec.cpu().numpy() == 0xAB).all()
+
+
+# ---------------------------------------------------------------------------
+# paged KIVI
+# ---------------------------------------------------------------------------
+
+class KiviCase:
+    """fp16 pools for the given lengths plus a page table over a page pool."""
+
+    def __init__(self, seed, lens, H=32, n_kv=8, R=128, outliers=4, extra_blocks=4):
+        self.lens = np.asarray(lens, np.int32)
+        self.R = R
+        S, D, BS = len(lens), 128, 16
+        self.case = inputs.make_paged_case(seed, S, H, n_kv, D, BS,
+                                           [L + extra_blocks * BS for L in lens], orc.F32)
+        rng = np.random.default_rng(seed + 1)
+        # outlier K channels per kv head scaled x8
+        for h in range(n_kv):
+            ch = rng.choice(D, size=outliers, replace=False)
+            self.case.k_cache[:, h, ch, :] *= 8
+        self.k = inputs.encode(self.case.k_cache, orc.F16)
+        self.v = inputs.encode(self.case.v_cache, orc.F16)
+        self.q = inputs.encode(orc.bits_to_f32(self.case.q, orc.F32), orc.F16)
+        self.tables = self.case.tables
+        self.n_kv, self.H, self.S = n_kv, H, S
+        max_pages = max(1, (int(self.lens.max()) + extra_blocks * BS) // 32 + 1)
+        self.num_pages = S * max_pages + 3
+        perm = rng.permutation(self.num_pages).astype(np.int32)
+        self.page_tables = perm[: S * max_pages].reshape(S, max_pages).copy()
+        self.scale = 1 / math.sqrt(D)
+
+    def oracle_pages(self, lens=None):
+        pages = np.zeros((self.num_pages, self.n_kv, orc.KIVI_PAGE_BYTES), np.uint8)
+        orc.kivi_build_pages(self.k, self.v, self.tables, self.lens if lens is None else lens, self.R,
+                             pages, self.page_tables)
+        return pages
+
+    def desc(self, qd, kd, btd, ptd, partition_pages=0, gqa=tla.GQA_GROUPED):
+        return tla.make_kivi_desc(qd, kd, btd, ptd, self.num_pages, self.n_kv, self.scale,
+                                  residual_length=self.R, gqa_map=gqa,
+                                  partition_pages=partition_pages)
+
+
+def _used_pages(kc, lens):
+    used = set()
+    for s, L in enumerate(lens):
+        for p in range(orc.kivi_quantized_len(int(L), kc.R) // 32):
+            used.add(int(kc.page_tables[s, p]))
+    return sorted(used)
+
+
+@pytest.mark.parametrize("R", [128, 0, 40])
+def test_build_pages_bit_exact(R):
+    kc = KiviCase(51, [300, 1000, 161, 159, 0, 4096], R=R)
+    want = kc.oracle_pages()
+    qd, kd, vd = dev(kc.q, orc.F16), dev(kc.k, orc.F16), dev(kc.v, orc.F16)
+    btd, sld, ptd = dev(kc.tables), dev(kc.lens), dev(kc.page_tables)
+    pages = torch.zeros(kc.num_pages, kc.n_kv, tla.KIVI_PAGE_BYTES, dtype=torch.uint8, device="cuda")
+    print(f"case build pages R={R}", flush=True)
+    tla.kivi_build_pages(kc.desc(qd, kd, btd, ptd), kd, vd, btd, sld, ptd, pages, int(kc.lens.max()))
+    torch.cuda.synchronize()
+    got = pages.cpu().numpy()
+    used = _used_pages(kc, kc.lens)
+    assert used, "case builds no page"
+    assert np.array_equal(got[used], want[used])
+    unused = sorted(set(range(kc.num_pages)) - set(used))
+    assert (got[unused] == 0).all()
+
+
+def test_append_quantises_on_page_boundaries():
+    """Append one token per step for 70 steps; pages and the fp16 pool match
+    a rebuild from the final pool, and pages appear exactly when Lq grows."""
+    start = np.array([150, 159, 160, 191, 200], np.int32)
+    steps = 70
+    kc = KiviCase(52, start + steps, extra_blocks=1)
+    qd, kd, vd = dev(kc.q, orc.F16), dev(kc.k, orc.F16), dev(kc.v, orc.F16)
+    btd, ptd = dev(kc.tables), dev(kc.page_tables)
+    pages = torch.zeros(kc.num_pages, kc.n_kv, tla.KIVI_PAGE_BYTES, dtype=torch.uint8, device="cuda")
+    desc = kc.desc(qd, kd, btd, ptd)
+    tla.kivi_build_pages(desc, kd, vd, btd, dev(start), ptd, pages, int(start.max()))
+    rng = np.random.default_rng(9)
+    lens = start.copy()
+    k_host, v_host = kc.k.copy(), kc.v.copy()
+    for _ in range(steps):
+        lens = lens + 1
+        pos = lens - 1
+        slots = (kc.tables[np.arange(kc.S), pos // 16] * 16 + pos % 16).astype(np.int32)
+        knew = inputs.encode(rng.standard_normal((kc.S, kc.n_kv, 128), dtype=np.float32), orc.F16)
+        vnew = inputs.encode(rng.standard_normal((kc.S, kc.n_kv, 128), dtype=np.float32), orc.F16)
+        tla.kivi_append(desc, dev(knew, orc.F16), dev(vnew, orc.F16), kd, vd, dev(slots), btd,
+                        dev(lens), ptd, pages)
+        orc.reshape_and_cache(knew, vnew, k_host, v_host, slots)
+    torch.cuda.synchronize()
+    assert np.array_equal(host_bits(kd), k_host) and np.array_equal(host_bits(vd), v_host)
+    kc.k, kc.v = k_host, v_host
+    want = kc.oracle_pages(lens)
+    used = _used_pages(kc, lens)
+    got = pages.cpu().numpy()
+    assert np.array_equal(got[used], want[used])
+
+
+def _run_decode(kc, pages_np, partition_pages=0, gqa=tla.GQA_GROUPED):
+    qd, kd, vd = dev(kc.q, orc.F16), dev(kc.k, orc.F16), dev(kc.v, orc.F16)
+    btd, sld, ptd = dev(kc.tables), dev(kc.lens), dev(kc.page_tables)
+    pages = torch.from_numpy(pages_np).cuda()
+    desc = kc.desc(qd, kd, btd, ptd, partition_pages, gqa)
+    max_ctx = int(kc.lens.max())
+    ws = torch.empty(max(16, tla.kivi_workspace_bytes(desc, max_ctx)), dtype=torch.uint8, device="cuda")
+    out = torch.full_like(qd, float("nan"))
+    tla.kivi_paged_attention_decode(desc, out, qd, pages, ptd, kd, vd, btd, sld, max_ctx, ws)
+    torch.cuda.synchronize()
+    return out
+
+
+def _kivi_ref(kc, pages_np, gqa=orc.GROUPED):
+    return orc.kivi_paged_attention(kc.q, orc.F16, pages_np, kc.page_tables, kc.k, kc.v, kc.tables,
+                                    kc.lens, kc.n_kv, kc.R, kc.scale, gqa)
+
+
+@pytest.mark.parametrize("pp", [-1, 0, 4, 1])
+def test_kivi_decode_matches_oracle(pp):
+    kc = KiviCase(53, [4096, 1000, 161, 159, 0, 1, 2047, 3000])
+    pages = kc.oracle_pages()
+    print(f"case kivi decode pp={pp}", flush=True)
+    assert_close(_run_decode(kc, pages, pp), _kivi_ref(kc, pages), orc.F16, ATOL_KIVI, f"pp={pp}")
+
+
+@pytest.mark.parametrize("H,n_kv", [(16, 8), (64, 8), (8, 8)])
+@pytest.mark.parametrize("gqa", [tla.GQA_GROUPED, tla.GQA_MODULO])
+def test_kivi_decode_group_sizes(H, n_kv, gqa):
+    kc = KiviCase(54, [700, 300, 2000], H=H, n_kv=n_kv)
+    pages = kc.oracle_pages()
+    print(f"case kivi H={H} n_kv={n_kv} gqa={gqa}", flush=True)
+    assert_close(_run_decode(kc, pages, 0, gqa), _kivi_ref(kc, pages, gqa), orc.F16, ATOL_KIVI,
+                 f"H={H}")
+
+
+def test_kivi_decode_residual_zero_and_nan_slots():
+    """R = 0 (every whole page quantised) and NaN in unused fp16 slots."""
+    kc = KiviCase(55, [96, 100, 33], R=0)
+    for s, L in enumerate(kc.lens):
+        last = kc.tables[s, (L - 1) // 16]
+        kc.v[last, :, :, L % 16 or 16:] = 0x7E00
+        kc.k[last, :, :, L % 16 or 16:] = 0x7E00
+    pages = kc.oracle_pages()
+    assert_close(_run_decode(kc, pages, -1), _kivi_ref(kc, pages), orc.F16, ATOL_KIVI, "R=0")

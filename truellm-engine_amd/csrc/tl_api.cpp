@@ -4,6 +4,7 @@
 // device untouched.
 #include "tl_attn.h"
 #include "tl_internal.hpp"
+#include "tl_kivi.hpp"
 
 #include <stdarg.h>
 #include <stdio.h>
@@ -276,6 +277,195 @@ int tl_fp8_absmax_scale(const void* x, int32_t dtype, int64_t n, float* scale_ou
   if (((uintptr_t)scale_out & 3u) != 0) return fail(TL_ERR_INVALID_ARGUMENT, "scale_out misaligned");
   const int rc = tl::launch_fp8_scale(x, dtype, n, scale_out, (hipStream_t)stream);
   if (rc) return fail(TL_ERR_BACKEND, "fp8 scale launch failed");
+  return ok();
+}
+
+// ---------------------------------------------------------------------------
+// KIVI
+// ---------------------------------------------------------------------------
+
+size_t tl_kivi_compressed_bytes(int32_t head_dim, int32_t n_outliers, int32_t group_size) {
+  if (group_size <= 0) return 0;
+  const int n_res = head_dim - n_outliers;
+  const int n_groups = (n_res + group_size - 1) / group_size;
+  return (size_t)n_outliers * 3 + (size_t)n_groups * (size_t)(group_size / 2 + 4);
+}
+
+int tl_kivi_params_supported(int32_t head_dim, int32_t n_outliers, int32_t group_size) {
+  return head_dim > 0 && head_dim <= TL_KIVI_MAX_HEAD_DIM && n_outliers >= 0 &&
+         n_outliers <= TL_KIVI_MAX_OUTLIERS && group_size > 0 && n_outliers <= head_dim;
+}
+
+static int kivi_vec(const void* in, void* out, int32_t n_vecs, int32_t head_dim, int32_t n_outliers,
+                    int32_t group_size, bool compress, void* stream) {
+  if (n_vecs < 0) return fail(TL_ERR_INVALID_ARGUMENT, "n_vecs=%d", n_vecs);
+  if (!tl_kivi_params_supported(head_dim, n_outliers, group_size))
+    return fail(TL_ERR_INVALID_ARGUMENT, "unsupported KIVI params head_dim=%d n_outliers=%d group_size=%d",
+                head_dim, n_outliers, group_size);
+  if (group_size % 2)
+    return fail(TL_ERR_INVALID_ARGUMENT, "odd group_size=%d: records would overrun the stride", group_size);
+  if (n_vecs == 0) return ok();
+  if (!in || !out) return fail(TL_ERR_INVALID_ARGUMENT, "NULL pointer");
+  const int stride = (int)tl_kivi_compressed_bytes(head_dim, n_outliers, group_size);
+  if (tl::launch_kivi_vec(in, out, n_vecs, head_dim, n_outliers, group_size, stride, compress,
+                          (hipStream_t)stream))
+    return fail(TL_ERR_BACKEND, "KIVI codec launch failed");
+  return ok();
+}
+
+int tl_kivi_compress(const void* kv_in, uint8_t* out, int32_t n_vecs, int32_t head_dim,
+                     int32_t n_outliers, int32_t group_size, void* stream) {
+  return kivi_vec(kv_in, out, n_vecs, head_dim, n_outliers, group_size, true, stream);
+}
+
+int tl_kivi_decompress(const uint8_t* in, void* kv_out, int32_t n_vecs, int32_t head_dim,
+                       int32_t n_outliers, int32_t group_size, void* stream) {
+  return kivi_vec(in, kv_out, n_vecs, head_dim, n_outliers, group_size, false, stream);
+}
+
+int32_t tl_kivi_quantized_len(int32_t seq_len, int32_t residual_length) {
+  if (seq_len < 0 || residual_length < 0) return 0;
+  return tl::kivi_quantized_len(seq_len, residual_length);
+}
+
+static int check_kivi(const tl_kivi_desc* d) {
+  if (!d) return fail(TL_ERR_INVALID_ARGUMENT, "desc is NULL");
+  if (d->num_seqs < 0) return fail(TL_ERR_INVALID_ARGUMENT, "num_seqs=%d", d->num_seqs);
+  if (d->num_kv_heads <= 0 || d->num_heads <= 0 || d->num_heads % d->num_kv_heads)
+    return fail(TL_ERR_INVALID_ARGUMENT, "num_heads=%d / num_kv_heads=%d", d->num_heads, d->num_kv_heads);
+  if (d->head_size != tl::kKiviHead || d->block_size != 16)
+    return fail(TL_ERR_NOT_IMPLEMENTED, "paged KIVI is built for head_size 128, block_size 16");
+  if (d->max_blocks_per_seq <= 0 || d->num_blocks <= 0 || d->max_pages_per_seq <= 0 || d->num_pages <= 0)
+    return fail(TL_ERR_INVALID_ARGUMENT, "table and pool sizes must be > 0");
+  if (d->residual_length < 0) return fail(TL_ERR_INVALID_ARGUMENT, "residual_length=%d", d->residual_length);
+  if (d->gqa_map != TL_GQA_MODULO && d->gqa_map != TL_GQA_GROUPED)
+    return fail(TL_ERR_INVALID_ARGUMENT, "gqa_map=%d", d->gqa_map);
+  if (d->partition_pages < -1) return fail(TL_ERR_INVALID_ARGUMENT, "partition_pages=%d", d->partition_pages);
+  return TL_OK;
+}
+
+static tl::KiviPageLaunch page_launch(const tl_kivi_desc* d, const void* k_cache, const void* v_cache,
+                                      const int32_t* bt, const int32_t* sl, const int32_t* pt,
+                                      void* pages, void* stream) {
+  tl::KiviPageLaunch a;
+  memset(&a, 0, sizeof a);
+  a.k_cache = k_cache; a.v_cache = v_cache; a.block_tables = bt; a.seq_lens = sl;
+  a.page_tables = pt; a.pages = pages;
+  a.num_seqs = d->num_seqs; a.num_kv_heads = d->num_kv_heads; a.block_size = d->block_size;
+  a.max_blocks_per_seq = d->max_blocks_per_seq; a.num_blocks = d->num_blocks;
+  a.max_pages_per_seq = d->max_pages_per_seq; a.num_pages = d->num_pages;
+  a.residual_length = d->residual_length;
+  a.stream = (hipStream_t)stream;
+  return a;
+}
+
+int tl_kivi_build_pages(const tl_kivi_desc* desc, const void* k_cache, const void* v_cache,
+                        const int32_t* block_tables, const int32_t* seq_lens,
+                        const int32_t* page_tables, void* pages, int32_t max_context_len,
+                        void* stream) {
+  int rc = check_kivi(desc);
+  if (rc) return rc;
+  if (max_context_len < 0) return fail(TL_ERR_INVALID_ARGUMENT, "max_context_len < 0");
+  if (desc->num_seqs == 0) return ok();
+  if (!k_cache || !v_cache || !block_tables || !seq_lens || !page_tables || !pages)
+    return fail(TL_ERR_INVALID_ARGUMENT, "NULL pointer");
+  if (!aligned16(pages)) return fail(TL_ERR_INVALID_ARGUMENT, "pages must be 16-byte aligned");
+  tl::KiviPageLaunch a = page_launch(desc, k_cache, v_cache, block_tables, seq_lens, page_tables, pages, stream);
+  a.max_pages_to_build = tl::kivi_quantized_len(max_context_len, desc->residual_length) / tl::kKiviPageTokens;
+  if (a.max_pages_to_build > desc->max_pages_per_seq) a.max_pages_to_build = desc->max_pages_per_seq;
+  if (tl::launch_kivi_pages(a)) return fail(TL_ERR_BACKEND, "KIVI page launch failed");
+  return ok();
+}
+
+int tl_kivi_append(const tl_kivi_desc* desc, const void* key, const void* value, void* k_cache,
+                   void* v_cache, const int32_t* slot_mapping, const int32_t* block_tables,
+                   const int32_t* seq_lens, const int32_t* page_tables, void* pages, void* stream) {
+  int rc = check_kivi(desc);
+  if (rc) return rc;
+  if (desc->num_seqs == 0) return ok();
+  if (!key || !value || !k_cache || !v_cache || !slot_mapping || !block_tables || !seq_lens ||
+      !page_tables || !pages)
+    return fail(TL_ERR_INVALID_ARGUMENT, "NULL pointer");
+  if (!aligned16(key) || !aligned16(value) || !aligned16(pages))
+    return fail(TL_ERR_INVALID_ARGUMENT, "key/value/pages must be 16-byte aligned");
+  tl::CacheLaunch c = {key, value, k_cache, v_cache, slot_mapping, desc->num_seqs, desc->num_kv_heads,
+                       desc->head_size, desc->block_size, desc->num_blocks, TL_DTYPE_F16, TL_DTYPE_F16,
+                       1.f, 1.f, (hipStream_t)stream};
+  if (tl::launch_reshape_and_cache(c)) return fail(TL_ERR_BACKEND, "append launch failed");
+  tl::KiviPageLaunch a = page_launch(desc, k_cache, v_cache, block_tables, seq_lens, page_tables, pages, stream);
+  a.append = 1;
+  if (tl::launch_kivi_pages(a)) return fail(TL_ERR_BACKEND, "KIVI page launch failed");
+  return ok();
+}
+
+static void kivi_plan(const tl_kivi_desc* d, int32_t max_ctx, int* P, int* PP) {
+  const int pages = tl::kivi_quantized_len(max_ctx, d->residual_length) / tl::kKiviPageTokens;
+  int pp;
+  if (d->partition_pages == -1 || pages == 0) {
+    pp = pages > 0 ? pages : 1;
+  } else if (d->partition_pages > 0) {
+    pp = d->partition_pages;
+  } else {
+    const int group = d->num_heads / d->num_kv_heads;
+    const long items = (long)d->num_seqs * d->num_kv_heads * ((group + 3) / 4);
+    long want = items > 0 ? (512 + items - 1) / items : 1;
+    if (want < 1) want = 1;
+    if (want > pages) want = pages;
+    pp = (int)((pages + want - 1) / want);
+  }
+  *PP = pp;
+  *P = pages > 0 ? (pages + pp - 1) / pp : 1;
+}
+
+size_t tl_kivi_workspace_bytes(const tl_kivi_desc* desc, int32_t max_context_len) {
+  if (check_kivi(desc) != TL_OK || max_context_len < 0) return 0;
+  int P, PP;
+  kivi_plan(desc, max_context_len, &P, &PP);
+  if (P <= 1) return 0;
+  const size_t sh = (size_t)desc->num_seqs * desc->num_heads * P;
+  return sh * desc->head_size * 4 + 2 * sh * 4;
+}
+
+int tl_kivi_paged_attention_decode(const tl_kivi_desc* desc, void* out, const void* q,
+                                   const void* pages, const int32_t* page_tables,
+                                   const void* k_cache, const void* v_cache,
+                                   const int32_t* block_tables, const int32_t* seq_lens,
+                                   int32_t max_context_len, void* workspace,
+                                   size_t workspace_bytes, void* stream) {
+  int rc = check_kivi(desc);
+  if (rc) return rc;
+  if (max_context_len < 0) return fail(TL_ERR_INVALID_ARGUMENT, "max_context_len < 0");
+  if (desc->num_seqs == 0) return ok();
+  if (!out || !q || !pages || !page_tables || !k_cache || !v_cache || !block_tables || !seq_lens)
+    return fail(TL_ERR_INVALID_ARGUMENT, "NULL pointer");
+  if (!aligned16(q) || !aligned16(pages) || !aligned16(k_cache) || !aligned16(v_cache))
+    return fail(TL_ERR_INVALID_ARGUMENT, "q, pages and pools must be 16-byte aligned");
+  int P, PP;
+  kivi_plan(desc, max_context_len, &P, &PP);
+  tl::KiviDecodeLaunch a;
+  memset(&a, 0, sizeof a);
+  a.out = out; a.q = q; a.pages = pages; a.page_tables = page_tables;
+  a.k_cache = k_cache; a.v_cache = v_cache; a.block_tables = block_tables; a.seq_lens = seq_lens;
+  a.num_seqs = desc->num_seqs; a.num_heads = desc->num_heads; a.num_kv_heads = desc->num_kv_heads;
+  a.max_blocks_per_seq = desc->max_blocks_per_seq; a.num_blocks = desc->num_blocks;
+  a.max_pages_per_seq = desc->max_pages_per_seq; a.num_pages = desc->num_pages;
+  a.residual_length = desc->residual_length; a.gqa_map = desc->gqa_map;
+  a.num_partitions = P; a.partition_pages = PP;
+  a.scale = desc->scale;
+  a.stream = (hipStream_t)stream;
+  if (P > 1) {
+    const size_t sh = (size_t)desc->num_seqs * desc->num_heads * P;
+    const size_t need = sh * desc->head_size * 4 + 2 * sh * 4;
+    if (!workspace || workspace_bytes < need)
+      return fail(TL_ERR_INVALID_ARGUMENT, "workspace of %zu bytes needed, %zu given", need, workspace_bytes);
+    if (!aligned16(workspace)) return fail(TL_ERR_INVALID_ARGUMENT, "workspace must be 16-byte aligned");
+    a.part_o = workspace;
+    a.part_m = (float*)((char*)workspace + sh * desc->head_size * 4);
+    a.part_l = a.part_m + sh;
+  }
+  rc = tl::launch_kivi_decode(a);
+  if (rc == 3) return fail(TL_ERR_NOT_IMPLEMENTED, "no KIVI decode kernel for this shape");
+  if (rc) return fail(TL_ERR_BACKEND, "KIVI decode launch failed");
   return ok();
 }
 

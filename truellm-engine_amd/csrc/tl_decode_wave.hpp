@@ -1,0 +1,306 @@
+// tl_decode_wave.hpp -- the per-wavefront decode of 2-byte (f16 / bf16) KV
+// shared by the paged decode kernel and the fp16 residual window of the
+// KIVI decode kernel.
+//
+// A wavefront runs its own online softmax over the 32-token iterations it
+// owns (tokens first_it, first_it + step, ... below t1), so the callers'
+// main loops have no workgroup barrier; the loads of the next iteration are
+// issued while the current one computes.  Lane bits 2-3 pick the token
+// group tg (one 8-token run of a block row), bits 0-1 and 4-5 the head dims
+// dl.  Both contractions use the packed dot-product instruction
+// (v_dot2_f32_bf16 / v_dot2_f32_f16):
+//   q.k over head-dim pairs (2m, 2m+1): two 16-byte loads per pair and one
+//       v_perm_b32 per token build the (K[2m][t], K[2m+1][t]) operand;
+//   p.v over token pairs (t, t+1), adjacent in the [d][bs] layout, with the
+//       weights packed to the KV type.
+// The q.k partials are finished by a transpose-reduce over the 16 lanes of
+// a token group (v_permlane32/16_swap for bits 5 and 4, DPP for bits 1 and
+// 0); each lane then owns head lane>>4, tokens 2*(lane&3) and +1, and the
+// per-head softmax reductions run inside one 16-lane row on DPP.
+#pragma once
+
+#include "tl_device.hpp"
+
+#include <math.h>
+
+namespace tl {
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kWaveHeads = 4;   // q heads served per wavefront
+
+struct Params {
+  void* out;
+  const void* q;
+  const char* k_cache;
+  const char* v_cache;
+  const int32_t* block_tables;
+  const int32_t* seq_lens;
+  float* part_m;
+  float* part_l;
+  void* part_o;
+  int num_heads, num_kv_heads, max_blocks_per_seq, num_blocks;
+  int num_partitions, partition_tokens;
+  int group, head_slices, gqa_map;
+  float qk_scale;  // softmax scale * k dequant scale * log2(e)
+  float v_scale;
+};
+
+__device__ __forceinline__ int head_of(const Params& p, int kvh, int gi) {
+  return p.gqa_map ? kvh * p.group + gi : kvh + gi * p.num_kv_heads;
+}
+
+template <Kind KV> struct Dot2;
+template <> struct Dot2<Kind::BF16> {
+  typedef __bf16 v2 __attribute__((ext_vector_type(2)));
+  __device__ __forceinline__ static float dot(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(v2, a), __builtin_bit_cast(v2, b), c, false);
+  }
+  __device__ __forceinline__ static uint32_t pack(float x, float y) {
+    const v2 p = {(__bf16)x, (__bf16)y};
+    return __builtin_bit_cast(uint32_t, p);
+  }
+};
+template <> struct Dot2<Kind::F16> {
+  typedef _Float16 v2 __attribute__((ext_vector_type(2)));
+  __device__ __forceinline__ static float dot(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(v2, a), __builtin_bit_cast(v2, b), c, false);
+  }
+  __device__ __forceinline__ static uint32_t pack(float x, float y) {
+    const v2 p = {(_Float16)x, (_Float16)y};
+    return __builtin_bit_cast(uint32_t, p);
+  }
+};
+
+__device__ __forceinline__ uint32_t word(const u32x4& c, int w) {
+  return w == 0 ? c.x : w == 1 ? c.y : w == 2 ? c.z : c.w;
+}
+
+// Physical block holding token blk_tok (a block start) of a sequence, or -1
+// for a hole, a block past the partition end t1 or an entry outside the pool.
+template <int BS>
+__device__ __forceinline__ int table_entry_bs(const Params& p, const int32_t* table, int blk_tok, int t1) {
+  const int lb = blk_tok / BS;
+  int ph = -1;
+  if (blk_tok < t1 && lb < p.max_blocks_per_seq) ph = table[lb];
+  return (ph >= p.num_blocks) ? -1 : ph;
+}
+
+// K of head-dim pairs (2m, 2m+1), m = dl + 16 j: rows 2m and 2m+1 of the
+// lane's 8-token run th of one block ([D][BS] layout, 16-byte chunks).
+template <int KP, int CPR>
+__device__ __forceinline__ void load_k_pairs(u32x4 (&kr)[KP][2], const char* blk, int dl, int th) {
+#pragma unroll
+  for (int j = 0; j < KP; ++j) {
+    const int c = 2 * (dl + 16 * j) * CPR + th;
+    kr[j][0] = load16_stream(blk + c * 16);
+    kr[j][1] = load16_stream(blk + (c + CPR) * 16);
+  }
+}
+
+// V rows d = 16 j + dl of the lane's 8-token run th of one block.
+template <int VD, int CPR>
+__device__ __forceinline__ void load_v_rows(u32x4 (&vr)[VD], const char* blk, int dl, int th) {
+#pragma unroll
+  for (int j = 0; j < VD; ++j) vr[j] = load16_stream(blk + ((16 * j + dl) * CPR + th) * 16);
+}
+
+// Runs one wavefront over its iterations and leaves its state in LDS:
+// s_acc_w [4][HEAD] unnormalised outputs, s_m_w [4] running max (log2 units),
+// s_l_w [4] sums.  s_p_w is the wavefront's [4][4][4] weight exchange area.
+template <Kind KV, int HEAD, int BS>
+__device__ __forceinline__ void decode2_wave(const Params& p, int seq, int kvh, int hs, int first_it,
+                                             int t1, int step, uint32_t* s_p_w, float* s_acc_w,
+                                             float* s_m_w, float* s_l_w) {
+  constexpr int GT = kWaveHeads;
+  constexpr int CPR = BS / 8;             // 16-byte chunks per head-dim row of a block
+  constexpr int BPI = 4 / CPR;            // blocks per wave iteration
+  constexpr int TPI = BPI * BS;           // tokens per wave iteration
+  constexpr int KP = HEAD / 32;           // head-dim pairs per lane (q.k)
+  constexpr int VD = HEAD / 16;           // head dims per lane (p.v)
+  constexpr int BLOCK_BYTES = HEAD * BS * 2;
+  static_assert(TPI == 32, "four 8-token groups per wave iteration");
+  using D2 = Dot2<KV>;
+
+  const int lane = threadIdx.x % kWave;
+  const int tg = (lane >> 2) & 3, dl = (lane & 3) | ((lane >> 4) << 2);
+  const int blk_in = tg / CPR, th = tg % CPR;
+  const int g_lane = lane >> 4, tp = lane & 3;
+
+  // q as (dim 2m, 2m+1) pairs, m = dl + 16 j, straight from [S, H, D]
+  uint32_t qp[GT][KP];
+#pragma unroll
+  for (int g = 0; g < GT; ++g) {
+    const int gi = hs * GT + g;
+    const uint32_t* qrow = (const uint32_t*)p.q +
+        ((int64_t)seq * p.num_heads + (gi < p.group ? head_of(p, kvh, gi) : 0)) * (HEAD / 2);
+#pragma unroll
+    for (int j = 0; j < KP; ++j) qp[g][j] = (gi < p.group) ? qrow[dl + 16 * j] : 0u;
+  }
+
+  float m_run[GT], acc[GT][VD], l_lane = 0.f;
+#pragma unroll
+  for (int g = 0; g < GT; ++g) {
+    m_run[g] = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < VD; ++j) acc[g][j] = 0.f;
+  }
+
+  const int32_t* table = p.block_tables + (int64_t)seq * p.max_blocks_per_seq;
+  const int64_t pool_stride = (int64_t)p.num_kv_heads * BLOCK_BYTES;
+  const char* kbase0 = p.k_cache + (int64_t)kvh * BLOCK_BYTES;
+  const char* vbase0 = p.v_cache + (int64_t)kvh * BLOCK_BYTES;
+
+  // Pipeline: the K loads of iteration i+1 are issued as soon as the scores
+  // of iteration i are formed, the V loads of i+1 once p.v of i is done, and
+  // block-table entries are read two iterations ahead, so each wavefront
+  // keeps one iteration of K/V in flight while it computes.  Holes load
+  // block 0 and are masked.
+  int it = first_it;
+  int ph_cur = table_entry_bs<BS>(p, table, it + blk_in * BS, t1);
+  int ph_next = table_entry_bs<BS>(p, table, it + step + blk_in * BS, t1);
+  u32x4 kr[KP][2], vr[VD];
+  if (it < t1) {
+    load_k_pairs<KP, CPR>(kr, kbase0 + (int64_t)max(ph_cur, 0) * pool_stride, dl, th);
+    load_v_rows<VD, CPR>(vr, vbase0 + (int64_t)max(ph_cur, 0) * pool_stride, dl, th);
+  }
+
+#pragma unroll 1
+  for (; it < t1; it += step) {
+    const int ph_nn = table_entry_bs<BS>(p, table, it + 2 * step + blk_in * BS, t1);
+    const bool has_next = it + step < t1;
+    const int blk_tok = it + blk_in * BS;                // first token of this lane's block
+
+    // ---- q.k partials over this lane's dim pairs, 8 tokens x 4 heads ----
+    float s[GT * 8];
+#pragma unroll
+    for (int j = 0; j < KP; ++j)
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const uint32_t a = word(kr[j][0], w), b = word(kr[j][1], w);
+        const uint32_t k_lo = __builtin_amdgcn_perm(b, a, 0x05040100u);  // token 2w
+        const uint32_t k_hi = __builtin_amdgcn_perm(b, a, 0x07060302u);  // token 2w+1
+#pragma unroll
+        for (int g = 0; g < GT; ++g) {
+          const int i0 = g * 8 + 2 * w;
+          s[i0] = D2::dot(k_lo, qp[g][j], j == 0 ? 0.f : s[i0]);
+          s[i0 + 1] = D2::dot(k_hi, qp[g][j], j == 0 ? 0.f : s[i0 + 1]);
+        }
+      }
+    if (has_next)
+      load_k_pairs<KP, CPR>(kr, kbase0 + (int64_t)max(ph_next, 0) * pool_stride, dl, th);
+    transpose_reduce_5410<GT * 8>(s, lane);             // -> (head g_lane, tokens 2tp, 2tp+1)
+
+    const int tok = blk_tok + th * 8 + 2 * tp;
+    const bool ok0 = ph_cur >= 0 && tok < t1, ok1 = ph_cur >= 0 && tok + 1 < t1;
+    const float sc0 = ok0 ? s[0] * p.qk_scale : -INFINITY;
+    const float sc1 = ok1 ? s[1] * p.qk_scale : -INFINITY;
+
+    // ---- online softmax, one running max per head for the wavefront ----
+    const float mx = row_max(fmaxf(sc0, sc1));
+    float m_lane = 0.f;
+#pragma unroll
+    for (int g = 0; g < GT; ++g) {
+      const float mg = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mx), 16 * g));
+      const float m_new = fmaxf(m_run[g], mg);
+      if (m_new != m_run[g]) {
+        const float alpha = (m_run[g] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_run[g] - m_new);
+#pragma unroll
+        for (int j = 0; j < VD; ++j) acc[g][j] *= alpha;
+        if (g == g_lane) l_lane *= alpha;
+        m_run[g] = m_new;
+      }
+      if (g == g_lane) m_lane = m_run[g];
+    }
+    const float p0 = ok0 ? __builtin_amdgcn_exp2f(sc0 - m_lane) : 0.f;
+    const float p1 = ok1 ? __builtin_amdgcn_exp2f(sc1 - m_lane) : 0.f;
+    l_lane += p0 + p1;
+    s_p_w[(tg * GT + g_lane) * 4 + tp] = D2::pack(p0, p1);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    // ---- holes, and slots past the end of a partial block, may hold anything ----
+    if (ph_cur < 0 || blk_tok + BS > t1) {
+#pragma unroll
+      for (int j = 0; j < VD; ++j) {
+        uint32_t w4[4] = {vr[j].x, vr[j].y, vr[j].z, vr[j].w};
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          const int t = blk_tok + th * 8 + 2 * w;
+          if (ph_cur < 0 || t >= t1) w4[w] = 0u;
+          else if (t + 1 >= t1) w4[w] &= 0xffffu;
+        }
+        vr[j] = u32x4{w4[0], w4[1], w4[2], w4[3]};
+      }
+    }
+
+    // ---- p.v over token pairs ----
+    u32x4 pp[GT];
+#pragma unroll
+    for (int g = 0; g < GT; ++g) pp[g] = *reinterpret_cast<const u32x4*>(&s_p_w[(tg * GT + g) * 4]);
+#pragma unroll
+    for (int j = 0; j < VD; ++j)
+#pragma unroll
+      for (int g = 0; g < GT; ++g) {
+        float a = acc[g][j];
+#pragma unroll
+        for (int w = 0; w < 4; ++w) a = D2::dot(word(pp[g], w), word(vr[j], w), a);
+        acc[g][j] = a;
+      }
+    if (has_next)
+      load_v_rows<VD, CPR>(vr, vbase0 + (int64_t)max(ph_next, 0) * pool_stride, dl, th);
+    ph_cur = ph_next;
+    ph_next = ph_nn;
+  }
+
+  // ---- wavefront totals: sums per head, acc reduced over token groups ----
+  const float l_tot = row_sum(l_lane);
+  float* accf = &acc[0][0];
+  transpose_reduce<GT * VD, 8, 4>(accf, lane);         // -> head tg, dims 16 j + dl
+#pragma unroll
+  for (int j = 0; j < VD; ++j) s_acc_w[tg * HEAD + 16 * j + dl] = accf[j];
+  if (lane == 0) {
+#pragma unroll
+    for (int g = 0; g < GT; ++g) s_m_w[g] = m_run[g];
+  }
+  if ((lane & 15) == 0) s_l_w[g_lane] = l_tot;
+}
+
+// Merges the nw wavefront states (s_m [nw][4], s_l [nw][4], s_acc [nw][4][HEAD])
+// and writes the workgroup's result: the normalised output (FINAL) or the
+// partition's (max, sum, normalised partial) for the log-sum-exp merge.
+template <Kind QK, Kind PO, int HEAD, bool FINAL>
+__device__ __forceinline__ void combine_waves(const Params& p, int nw, const float* s_m,
+                                              const float* s_l, const float* s_acc, int seq, int kvh,
+                                              int hs, int part, int tid, int nthreads) {
+  constexpr int GT = kWaveHeads;
+  for (int i = tid; i < GT * HEAD; i += nthreads) {
+    const int g = i / HEAD, d = i % HEAD, gi = hs * GT + g;
+    if (gi >= p.group) continue;
+    float M = -INFINITY;
+    for (int w = 0; w < nw; ++w) M = fmaxf(M, s_m[w * GT + g]);
+    float num = 0.f, den = 0.f;
+    if (M != -INFINITY) {
+      for (int w = 0; w < nw; ++w) {
+        const float mw = s_m[w * GT + g];
+        const float f = (mw == -INFINITY) ? 0.f : exp2f(mw - M);
+        num += f * s_acc[(w * GT + g) * HEAD + d];
+        den += f * s_l[w * GT + g];
+      }
+    }
+    const float val = (den > 0.f) ? num / den : 0.f;
+    const int head = head_of(p, kvh, gi);
+    if constexpr (FINAL) {
+      store_scalar<QK>(p.out, ((int64_t)seq * p.num_heads + head) * HEAD + d, val);
+    } else {
+      const int64_t pi = ((int64_t)seq * p.num_heads + head) * p.num_partitions + part;
+      store_scalar<PO>(p.part_o, pi * HEAD + d, val);
+      if (d == 0) {
+        p.part_m[pi] = (den > 0.f) ? M * (1.0f / kLog2e) : -INFINITY;
+        p.part_l[pi] = den;
+      }
+    }
+  }
+}
+
+}  // namespace tl

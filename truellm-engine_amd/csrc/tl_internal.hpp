@@ -50,6 +50,51 @@ struct CacheLaunch {
 };
 int launch_reshape_and_cache(const CacheLaunch& a);
 
+// Log-sum-exp merge of split-K partials into out.  The partitions a sequence
+// has are ceil(L / partition_tokens), or, for KIVI (kivi_pages > 0),
+// max(1, ceil(pages(L) / kivi_pages)).
+int launch_lse_reduce(void* out, int q_dtype, const float* part_m, const float* part_l,
+                      const void* part_o, int part_o_dtype, const int32_t* seq_lens, int num_seqs,
+                      int num_heads, int head_size, int num_partitions, int partition_tokens,
+                      int kivi_residual, int kivi_pages, hipStream_t stream);
+
+// ---- KIVI ------------------------------------------------------------------
+int launch_kivi_vec(const void* in, void* out, int n_vecs, int head_dim, int n_outliers,
+                    int group_size, int stride, bool compress, hipStream_t stream);
+
+struct KiviPageLaunch {
+  const void* k_cache;          // fp16 pools [N, n_kv, 128, BS]
+  const void* v_cache;
+  const int32_t* block_tables;
+  const int32_t* seq_lens;
+  const int32_t* page_tables;   // [S, max_pages_per_seq]
+  void* pages;                  // [num_pages, n_kv, 5120]
+  int num_seqs, num_kv_heads, block_size, max_blocks_per_seq, num_blocks;
+  int max_pages_per_seq, num_pages, residual_length;
+  int max_pages_to_build;       // prefix build: page slots per sequence in the grid
+  int append;                   // 1: build only the page that length L just completed
+  hipStream_t stream;
+};
+int launch_kivi_pages(const KiviPageLaunch& a);
+
+struct KiviDecodeLaunch {
+  void* out;                    // [S, H, 128] fp16
+  const void* q;                // [S, H, 128] fp16
+  const void* pages;
+  const int32_t* page_tables;
+  const void* k_cache;          // fp16 residual window, [N, n_kv, 128, 16]
+  const void* v_cache;
+  const int32_t* block_tables;
+  const int32_t* seq_lens;
+  float* part_m; float* part_l; void* part_o;   // fp32 split-K partials
+  int num_seqs, num_heads, num_kv_heads, max_blocks_per_seq, num_blocks;
+  int max_pages_per_seq, num_pages, residual_length, gqa_map;
+  int num_partitions, partition_pages;
+  float scale;
+  hipStream_t stream;
+};
+int launch_kivi_decode(const KiviDecodeLaunch& a);
+
 // absmax(x)/448 into *scale_out (1 when absmax is 0).
 int launch_fp8_scale(const void* x, int dtype, int64_t n, float* scale_out,
                      hipStream_t stream);

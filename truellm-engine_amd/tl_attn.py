@@ -58,6 +58,27 @@ class DecodeDesc(ctypes.Structure):
     ]
 
 
+class KiviDesc(ctypes.Structure):
+    _fields_ = [
+        ("num_seqs", ctypes.c_int32),
+        ("num_heads", ctypes.c_int32),
+        ("num_kv_heads", ctypes.c_int32),
+        ("head_size", ctypes.c_int32),
+        ("block_size", ctypes.c_int32),
+        ("max_blocks_per_seq", ctypes.c_int32),
+        ("num_blocks", ctypes.c_int32),
+        ("max_pages_per_seq", ctypes.c_int32),
+        ("num_pages", ctypes.c_int32),
+        ("residual_length", ctypes.c_int32),
+        ("gqa_map", ctypes.c_int32),
+        ("partition_pages", ctypes.c_int32),
+        ("scale", ctypes.c_float),
+    ]
+
+
+KIVI_PAGE_TOKENS = 32
+KIVI_PAGE_BYTES = 5120
+
 _P = ctypes.c_void_p
 _I = ctypes.c_int32
 _F = ctypes.c_float
@@ -71,6 +92,15 @@ _SIG = {
     "tl_reshape_and_cache": (ctypes.c_int, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P]),
     "tl_reshape_and_cache_fp8": (ctypes.c_int, [_P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _I, _F, _F, _P]),
     "tl_fp8_absmax_scale": (ctypes.c_int, [_P, _I, ctypes.c_int64, _P, _P]),
+    "tl_kivi_compressed_bytes": (ctypes.c_size_t, [_I, _I, _I]),
+    "tl_kivi_params_supported": (ctypes.c_int, [_I, _I, _I]),
+    "tl_kivi_compress": (ctypes.c_int, [_P, _P, _I, _I, _I, _I, _P]),
+    "tl_kivi_decompress": (ctypes.c_int, [_P, _P, _I, _I, _I, _I, _P]),
+    "tl_kivi_quantized_len": (ctypes.c_int32, [_I, _I]),
+    "tl_kivi_build_pages": (ctypes.c_int, [ctypes.POINTER(KiviDesc), _P, _P, _P, _P, _P, _P, _I, _P]),
+    "tl_kivi_append": (ctypes.c_int, [ctypes.POINTER(KiviDesc), _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
+    "tl_kivi_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(KiviDesc), _I]),
+    "tl_kivi_paged_attention_decode": (ctypes.c_int, [ctypes.POINTER(KiviDesc), _P, _P, _P, _P, _P, _P, _P, _P, _I, _P, ctypes.c_size_t, _P]),
 }
 
 
@@ -238,3 +268,74 @@ def paged_attention_decode(desc: DecodeDesc, out, q, k_cache, v_cache, block_tab
     check(lib.tl_paged_attention_decode(
         ctypes.byref(desc), _ptr(out), _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(block_tables),
         _ptr(seq_lens), max_context_len, _ptr(workspace), ws_bytes, _stream(stream)))
+
+
+# ---------------------------------------------------------------------------
+# Reference KIVI vector codec (kivi_cache.cuh:32-84): same names and roles
+# ---------------------------------------------------------------------------
+
+def kivi_compressed_bytes(head_dim, n_outliers, group_size) -> int:
+    return lib.tl_kivi_compressed_bytes(head_dim, n_outliers, group_size)
+
+
+def kivi_params_supported(head_dim, n_outliers, group_size) -> bool:
+    return bool(lib.tl_kivi_params_supported(head_dim, n_outliers, group_size))
+
+
+def kivi_compress(kv_in, out, n_vecs, head_dim, n_outliers, group_size, stream=None):
+    """kv_in fp16 [n_vecs, head_dim] -> out uint8 records."""
+    check(lib.tl_kivi_compress(_ptr(kv_in), _ptr(out), n_vecs, head_dim, n_outliers, group_size,
+                               _stream(stream)))
+
+
+def kivi_decompress(rec, kv_out, n_vecs, head_dim, n_outliers, group_size, stream=None):
+    check(lib.tl_kivi_decompress(_ptr(rec), _ptr(kv_out), n_vecs, head_dim, n_outliers,
+                                 group_size, _stream(stream)))
+
+
+# ---------------------------------------------------------------------------
+# Paged KIVI INT4
+# ---------------------------------------------------------------------------
+
+def kivi_quantized_len(seq_len, residual_length) -> int:
+    return lib.tl_kivi_quantized_len(seq_len, residual_length)
+
+
+def make_kivi_desc(q, k_cache, block_tables, page_tables, num_pages, num_kv_heads, scale, *,
+                   residual_length=128, gqa_map=GQA_GROUPED, partition_pages=0):
+    S, H, D = q.shape
+    d = KiviDesc()
+    d.num_seqs, d.num_heads, d.num_kv_heads, d.head_size = S, H, num_kv_heads, D
+    d.block_size = k_cache.shape[3]
+    d.max_blocks_per_seq, d.num_blocks = block_tables.shape[1], k_cache.shape[0]
+    d.max_pages_per_seq, d.num_pages = page_tables.shape[1], num_pages
+    d.residual_length, d.gqa_map, d.partition_pages = residual_length, gqa_map, partition_pages
+    d.scale = scale
+    return d
+
+
+def kivi_build_pages(desc, k_cache, v_cache, block_tables, seq_lens, page_tables, pages,
+                     max_context_len, stream=None):
+    check(lib.tl_kivi_build_pages(ctypes.byref(desc), _ptr(k_cache), _ptr(v_cache),
+                                  _ptr(block_tables), _ptr(seq_lens), _ptr(page_tables),
+                                  _ptr(pages), max_context_len, _stream(stream)))
+
+
+def kivi_append(desc, key, value, k_cache, v_cache, slot_mapping, block_tables, seq_lens,
+                page_tables, pages, stream=None):
+    check(lib.tl_kivi_append(ctypes.byref(desc), _ptr(key), _ptr(value), _ptr(k_cache),
+                             _ptr(v_cache), _ptr(slot_mapping), _ptr(block_tables),
+                             _ptr(seq_lens), _ptr(page_tables), _ptr(pages), _stream(stream)))
+
+
+def kivi_workspace_bytes(desc, max_context_len) -> int:
+    return lib.tl_kivi_workspace_bytes(ctypes.byref(desc), max_context_len)
+
+
+def kivi_paged_attention_decode(desc, out, q, pages, page_tables, k_cache, v_cache, block_tables,
+                                seq_lens, max_context_len, workspace=None, stream=None):
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    check(lib.tl_kivi_paged_attention_decode(
+        ctypes.byref(desc), _ptr(out), _ptr(q), _ptr(pages), _ptr(page_tables), _ptr(k_cache),
+        _ptr(v_cache), _ptr(block_tables), _ptr(seq_lens), max_context_len, _ptr(workspace),
+        ws_bytes, _stream(stream)))
