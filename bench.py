@@ -1,22 +1,29 @@
 """Paged-attention decode benchmark on one MI355X.
 
-Workload (one "step" = one decode step of one attention layer for the whole
-batch): Llama-3-8B-shape decode, batch 64, 32 q heads / 8 KV heads (GQA 4),
-head_dim 128, block_size 16, every context 4096 tokens, bf16 KV in a
-shuffled pool of 1.25x the blocks needed, q/K/V ~ N(0,1) (synthetic,
-seeded).  Two pool copies are rotated between steps so the 256 MiB
-Infinity Cache cannot serve a re-timed step.
+One "step" is one decode step of one attention layer for the whole batch.
+Workloads (synthetic, seeded; q/K/V ~ N(0,1)):
+  * headline: Llama-3-8B-shape decode, batch 64, 32 q heads / 8 KV heads
+    (GQA 4), head_dim 128, block_size 16, every context 4096 tokens, bf16 KV
+    in a shuffled pool of 1.25x the blocks needed;
+  * the same shape with fp16 KV (the reference for the KIVI speed-up);
+  * KIVI INT4 at the same shape: per-channel K / per-token V groups of 32,
+    fp16 residual window of 128+ tokens, 4 outlier K channels per kv head
+    scaled x8; each step appends one token per sequence (fp16 write plus
+    quantise-on-append when a page completes) and then decodes.
+Two copies of every pool are rotated between steps so the 256 MiB Infinity
+Cache cannot serve a re-timed step.
 
-Prints one JSON line: value = GB/s of algorithmic bytes (KV read once +
-q read + out write + block tables + seq_lens) per step over the timed
-steps; tok/s = batch / step time; roofline of the decode step against 8 TB/s;
-cpu_baseline = the oracle's multithreaded fp32 decode on the host cores over
-a bounded sample (4 of the 64 sequences).
+Prints one JSON line.  value = GB/s of algorithmic bytes (KV read once + q
+read + out write + block tables + seq_lens) per bf16 step over the timed
+steps; roofline = the same bytes over the decode kernel's average duration
+(HIP events on the launch stream) against 8 TB/s; cpu_baseline = the
+oracle's multithreaded fp32 decode on the host cores over a bounded sample.
 """
 import argparse
 import json
 import math
 import os
+import re
 import sys
 import time
 
@@ -26,13 +33,32 @@ sys.path.insert(0, os.path.join(ROOT, "tests"))
 
 HBM_PEAK_GBS = 8000.0
 METRIC = "paged-attn decode GB/s (% HBM peak) + tok/s, B=64 ctx4k, fp16 & KIVI-INT4 KV"
+S, H, NKV, D, BS, CTX = 64, 32, 8, 128, 16, 4096
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "decode_bf16_b64_ctx4096_hbm_traffic.md")
 
 
-def algorithmic_bytes(S, H, n_kv, D, BS, lens, elem):
-    kv = sum(lens) * n_kv * D * 2 * elem
+def algorithmic_bytes(lens, elem):
+    kv = sum(lens) * NKV * D * 2 * elem
     qo = S * H * D * elem * 2
     tables = sum((L + BS - 1) // BS for L in lens) * 4 + 4 * S
     return kv + qo + tables
+
+
+def kivi_bytes(lens, R, appended_page):
+    """KIVI bytes of one step: pages (160 B/token/kv head) + fp16 window
+    (512 B/token/kv head) + q/out + tables, plus the appended token and,
+    when a page completes, its quantisation (32 fp16 tokens read, 5 KiB
+    written per kv head)."""
+    tot = 0
+    for L in lens:
+        lq = 0 if L <= R else ((L - R) // 32) * 32
+        tot += NKV * (lq * 160 + (L - lq) * 512)
+        tot += (lq // 32 + (L - lq + BS - 1) // BS) * 4 + 4
+    tot += S * H * D * 2 * 2
+    tot += S * NKV * D * 2 * 2
+    if appended_page:
+        tot += S * NKV * (32 * 512 + 5120)
+    return tot
 
 
 def parse():
@@ -41,38 +67,173 @@ def parse():
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--partition-tokens", type=int, default=0)
-    p.add_argument("--dtype", default="bf16", choices=["bf16", "fp16"])
     p.add_argument("--cpu-seconds", type=float, default=15.0)
     p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--only", default="all", choices=["all", "bf16", "fp16", "kivi"])
     return p.parse_args()
 
 
-def cpu_baseline(seconds, S_sample, H, n_kv, D, BS, L, threads):
-    import numpy as np
+def timed(step, steps, warmup, stream):
+    import torch
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    ev[0].record(stream)
+    for i in range(steps):
+        step(warmup + i)
+        ev[i + 1].record(stream)
+    torch.cuda.synchronize()
+    per = [ev[i].elapsed_time(ev[i + 1]) for i in range(steps)]
+    return ev[0].elapsed_time(ev[-1]) / steps, per
 
+
+def bench_decode(args, dtype):
+    import torch
+
+    import tl_attn as tla
+
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float16
+    nb = CTX // BS
+    N = math.ceil(1.25 * S * nb)
+    g = torch.Generator(device="cuda").manual_seed(0x7E5E0002)
+    pools = []
+    for _ in range(2):
+        k = torch.randn(N, NKV, D, BS, generator=g, device="cuda", dtype=tdt)
+        v = torch.randn(N, NKV, D, BS, generator=g, device="cuda", dtype=tdt)
+        perm = torch.randperm(N, generator=g, device="cuda").to(torch.int32)
+        pools.append((k, v, perm[: S * nb].view(S, nb).contiguous()))
+    q = torch.randn(S, H, D, generator=g, device="cuda", dtype=tdt)
+    sl = torch.full((S,), CTX, dtype=torch.int32, device="cuda")
+    out = torch.empty_like(q)
+    desc = tla.make_decode_desc(q, pools[0][0], pools[0][2], NKV, 1.0 / math.sqrt(D),
+                                gqa_map=tla.GQA_GROUPED, partition_tokens=args.partition_tokens)
+    ws = torch.empty(max(16, tla.workspace_bytes(desc, CTX)), dtype=torch.uint8, device="cuda")
+    stream = torch.cuda.current_stream()
+
+    def step(i):
+        k, v, tables = pools[i % 2]
+        tla.paged_attention_decode(desc, out, q, k, v, tables, sl, CTX, ws, stream)
+
+    ms, per = timed(step, args.steps, args.warmup, stream)
+    nbytes = algorithmic_bytes([CTX] * S, 2)
+    launch_ms = sum(per) / len(per)
+    return {
+        "ms_per_step": ms, "gbs": nbytes / (ms * 1e-3) / 1e9, "tok_s": S / (ms * 1e-3),
+        "bytes": nbytes, "launch_ms": launch_ms, "pool_blocks": N,
+        "workspace_bytes": tla.workspace_bytes(desc, CTX),
+    }
+
+
+def bench_kivi(args, R=128):
+    import torch
+
+    import tl_attn as tla
+
+    total_steps = args.warmup + args.steps
+    L0 = CTX
+    Lmax = L0 + total_steps
+    nb = (Lmax + BS - 1) // BS
+    N = S * nb + 8
+    max_pages = Lmax // 32 + 1
+    g = torch.Generator(device="cuda").manual_seed(0x7E5E0003)
+    reps = []
+    for _ in range(2):
+        k = torch.randn(N, NKV, D, BS, generator=g, device="cuda", dtype=torch.float16)
+        v = torch.randn(N, NKV, D, BS, generator=g, device="cuda", dtype=torch.float16)
+        for h in range(NKV):                                  # 4 outlier K channels x8
+            ch = torch.randperm(D, generator=g, device="cuda")[:4]
+            k[:, h, ch, :] *= 8
+        perm = torch.randperm(N, generator=g, device="cuda").to(torch.int32)
+        tables = perm[: S * nb].view(S, nb).contiguous()
+        num_pages = S * max_pages + 8
+        pperm = torch.randperm(num_pages, generator=g, device="cuda").to(torch.int32)
+        ptables = pperm[: S * max_pages].view(S, max_pages).contiguous()
+        pages = torch.zeros(num_pages, NKV, tla.KIVI_PAGE_BYTES, dtype=torch.uint8, device="cuda")
+        reps.append([k, v, tables, ptables, pages, num_pages])
+    q = torch.randn(S, H, D, generator=g, device="cuda", dtype=torch.float16)
+    knew = torch.randn(S, NKV, D, generator=g, device="cuda", dtype=torch.float16)
+    vnew = torch.randn(S, NKV, D, generator=g, device="cuda", dtype=torch.float16)
+    out = torch.empty_like(q)
+    scale = 1.0 / math.sqrt(D)
+    # per replica: lengths before each of its appends, slots of the new token
+    lens_host = {0: L0, 1: L0}
+    plan = []
+    for i in range(total_steps):
+        r = i % 2
+        L = lens_host[r] + 1
+        lens_host[r] = L
+        plan.append((r, L))
+    sl_dev, slot_dev = [], []
+    tables_host = [rep[2].cpu() for rep in reps]
+    for r, L in plan:
+        sl_dev.append(torch.full((S,), L, dtype=torch.int32, device="cuda"))
+        pos = L - 1
+        slot = tables_host[r][:, pos // BS] * BS + pos % BS
+        slot_dev.append(slot.to(torch.int32).cuda())
+    desc0 = tla.make_kivi_desc(q, reps[0][0], reps[0][2], reps[0][3], reps[0][5], NKV, scale,
+                               residual_length=R, gqa_map=tla.GQA_GROUPED)
+    ws = torch.empty(max(16, tla.kivi_workspace_bytes(desc0, Lmax)), dtype=torch.uint8, device="cuda")
+    stream = torch.cuda.current_stream()
+    for rep in reps:
+        d = tla.make_kivi_desc(q, rep[0], rep[2], rep[3], rep[5], NKV, scale, residual_length=R)
+        sl0 = torch.full((S,), L0, dtype=torch.int32, device="cuda")
+        tla.kivi_build_pages(d, rep[0], rep[1], rep[2], sl0, rep[3], rep[4], L0)
+    descs = [tla.make_kivi_desc(q, rep[0], rep[2], rep[3], rep[5], NKV, scale, residual_length=R)
+             for rep in reps]
+
+    def step(i):
+        r, L = plan[i]
+        k, v, tables, ptables, pages, _ = reps[r]
+        tla.kivi_append(descs[r], knew, vnew, k, v, slot_dev[i], tables, sl_dev[i], ptables, pages,
+                        stream)
+        tla.kivi_paged_attention_decode(descs[r], out, q, pages, ptables, k, v, tables, sl_dev[i], L,
+                                        ws, stream)
+
+    ms, per = timed(step, args.steps, args.warmup, stream)
+    nbytes = []
+    for i in range(args.warmup, total_steps):
+        _, L = plan[i]
+        lq = lambda x: 0 if x <= R else ((x - R) // 32) * 32
+        nbytes.append(kivi_bytes([L] * S, R, lq(L) > lq(L - 1)))
+    avg_bytes = sum(nbytes) / len(nbytes)
+    return {"ms_per_step": ms, "gbs": avg_bytes / (ms * 1e-3) / 1e9, "tok_s": S / (ms * 1e-3),
+            "bytes_per_step": avg_bytes, "residual_length": R, "group": 32}
+
+
+def traffic_from_profile():
+    """HBM bytes per decode launch measured with rocprofv3 --pmc (FETCH_SIZE,
+    WRITE_SIZE) and recorded in the profile summary, if present."""
+    try:
+        text = open(TRAFFIC_PROFILE).read()
+    except OSError:
+        return None
+    m = re.search(r"traffic_bytes_per_launch:\s*([0-9]+)", text)
+    return int(m.group(1)) if m else None
+
+
+def cpu_baseline(seconds, S_sample, threads):
     import inputs
     import oracle_lib as orc
 
-    lens = [L] * S_sample
-    case = inputs.make_paged_case(inputs.SEEDS[1], S_sample, H, n_kv, D, BS, lens, orc.BF16)
-    nbytes = algorithmic_bytes(S_sample, H, n_kv, D, BS, lens, 2)
+    lens = [CTX] * S_sample
+    case = inputs.make_paged_case(inputs.SEEDS[1], S_sample, H, NKV, D, BS, lens, orc.BF16)
+    kv = sum(lens) * NKV * D * 2 * 2
+    nbytes = kv + S_sample * H * D * 2 * 2 + sum(L // BS for L in lens) * 4 + 4 * S_sample
     reps, t_total = 0, 0.0
     while t_total < seconds or reps < 2:
         t0 = time.perf_counter()
         orc.paged_attention_f32(case.q, orc.BF16, case.k_cache, case.v_cache, orc.BF16,
-                                case.tables, case.seq_lens, n_kv, case.scale, orc.GROUPED,
+                                case.tables, case.seq_lens, NKV, case.scale, orc.GROUPED,
                                 threads=threads)
         t_total += time.perf_counter() - t0
         reps += 1
     per = t_total / reps
     return {
-        "value": round(nbytes / per / 1e9, 3),
-        "unit": "GB/s",
-        "tok_s": round(S_sample / per, 2),
-        "cores": threads,
-        "kind": "port",
-        "sample": f"{S_sample} of the 64 sequences (ctx {L}, 32/8 heads, d 128, bf16 pool), "
-                  f"{reps} runs of the oracle's fp32 pthread decode, {per * 1e3:.1f} ms each",
+        "value": round(nbytes / per / 1e9, 3), "unit": "GB/s", "tok_s": round(S_sample / per, 2),
+        "cores": threads, "kind": "port",
+        "sample": f"{S_sample} of the 64 sequences (ctx {CTX}, 32/8 heads, d 128, bf16 pool), "
+                  f"{reps} runs of the oracle's fp32 pthread decode, {per * 1e3:.2f} ms each",
     }
 
 
@@ -84,83 +245,57 @@ def main():
 
     import torch
 
-    import tl_attn as tla
-
     torch.cuda.set_device(0)
-    S, H, n_kv, D, BS, L = 64, 32, 8, 128, 16, 4096
-    tdt = torch.bfloat16 if args.dtype == "bf16" else torch.float16
-    nb = L // BS
-    N = math.ceil(1.25 * S * nb)
-    g = torch.Generator(device="cuda").manual_seed(0x7E5E0002)
-    pools = []
-    for _ in range(2):
-        k = torch.randn(N, n_kv, D, BS, generator=g, device="cuda", dtype=tdt)
-        v = torch.randn(N, n_kv, D, BS, generator=g, device="cuda", dtype=tdt)
-        perm = torch.randperm(N, generator=g, device="cuda").to(torch.int32)
-        tables = perm[: S * nb].view(S, nb).contiguous()
-        pools.append((k, v, tables))
-    q = torch.randn(S, H, D, generator=g, device="cuda", dtype=tdt)
-    sl = torch.full((S,), L, dtype=torch.int32, device="cuda")
-    out = torch.empty_like(q)
-    scale = 1.0 / math.sqrt(D)
-    desc = tla.make_decode_desc(q, pools[0][0], pools[0][2], n_kv, scale,
-                                gqa_map=tla.GQA_GROUPED, partition_tokens=args.partition_tokens)
-    ws = torch.empty(max(16, tla.workspace_bytes(desc, L)), dtype=torch.uint8, device="cuda")
-    stream = torch.cuda.current_stream()
-
-    def step(i):
-        k, v, tables = pools[i % 2]
-        tla.paged_attention_decode(desc, out, q, k, v, tables, sl, L, ws, stream)
-
-    for i in range(args.warmup):
-        step(i)
-    torch.cuda.synchronize()
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
-    ev[0].record(stream)
-    for i in range(args.steps):
-        step(i)
-        ev[i + 1].record(stream)
-    torch.cuda.synchronize()
-    per_step = [ev[i].elapsed_time(ev[i + 1]) for i in range(args.steps)]
-    total_ms = ev[0].elapsed_time(ev[-1])
-    ms = total_ms / args.steps
-    nbytes = algorithmic_bytes(S, H, n_kv, D, BS, [L] * S, 2)
-    gbs = nbytes / (ms * 1e-3) / 1e9
-    avg_launch_ms = sum(per_step) / len(per_step)
-    achieved = nbytes / (avg_launch_ms * 1e-3) / 1e9
-
-    res = {
-        "metric": METRIC,
-        "value": round(gbs, 2),
-        "unit": "GB/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms, 5),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": args.dtype,
-        "data": "synthetic",
-        "config": {
-            "workload": "paged-attention decode, Llama-3-8B shape",
-            "batch": S, "q_heads": H, "kv_heads": n_kv, "head_dim": D, "block_size": BS,
-            "context": L, "kv_dtype": args.dtype, "pool_blocks": N, "pools_rotated": 2,
-            "partition_tokens": args.partition_tokens or "auto",
-        },
-        "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
-        "tok_s": round(S / (ms * 1e-3), 1),
-        "tok_s_32_layers": round(S / (ms * 1e-3) / 32, 1),
-        "roofline": {
-            "kernel": "paged decode step (decode_kernel + lse_reduce_kernel)",
-            "bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
-            "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "bytes_per_launch": nbytes, "traffic": None,
-        },
+    res = {"metric": METRIC, "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+           "warmup": args.warmup, "higher_is_better": True, "scaling": "weak",
+           "vs_baseline": None, "dtype": "bf16", "data": "synthetic"}
+    bf = fp = kv = None
+    if args.only in ("all", "bf16"):
+        bf = bench_decode(args, "bf16")
+    if args.only in ("all", "fp16"):
+        fp = bench_decode(args, "fp16")
+    if args.only in ("all", "kivi"):
+        kv = bench_kivi(args)
+    head = bf or fp
+    if head is not None:
+        res["dtype"] = "bf16" if bf else "fp16"
+        res["value"] = round(head["gbs"], 2)
+        res["ms_per_step"] = round(head["ms_per_step"], 5)
+        res["pct_hbm_peak"] = round(100 * head["gbs"] / HBM_PEAK_GBS, 2)
+        res["tok_s"] = round(head["tok_s"], 1)
+        res["tok_s_32_layers"] = round(head["tok_s"] / 32, 1)
+        achieved = head["bytes"] / (head["launch_ms"] * 1e-3) / 1e9
+        res["roofline"] = {
+            "kernel": "decode2_kernel (paged decode, single pass)" if head["workspace_bytes"] == 0
+                      else "decode2_kernel + lse_reduce_kernel (split-K)",
+            "bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "bytes_per_launch": head["bytes"],
+            "traffic": traffic_from_profile(),
+        }
+    else:
+        res["value"] = round(kv["gbs"], 2)
+        res["ms_per_step"] = round(kv["ms_per_step"], 5)
+        res["dtype"] = "f16 x int4"
+    res["config"] = {
+        "workload": "paged-attention decode, Llama-3-8B shape, one layer, batch 64, ctx 4096",
+        "batch": S, "q_heads": H, "kv_heads": NKV, "head_dim": D, "block_size": BS, "context": CTX,
+        "kv_dtype": res["dtype"], "pools_rotated": 2,
+        "partition_tokens": args.partition_tokens or "auto",
     }
+    if fp is not None:
+        res["fp16"] = {"gbs": round(fp["gbs"], 2), "ms_per_step": round(fp["ms_per_step"], 5),
+                       "tok_s": round(fp["tok_s"], 1),
+                       "pct_hbm_peak": round(100 * fp["gbs"] / HBM_PEAK_GBS, 2)}
+    if kv is not None:
+        res["kivi_int4"] = {"gbs": round(kv["gbs"], 2), "ms_per_step": round(kv["ms_per_step"], 5),
+                            "tok_s": round(kv["tok_s"], 1),
+                            "pct_hbm_peak": round(100 * kv["gbs"] / HBM_PEAK_GBS, 2),
+                            "bytes_per_step": int(kv["bytes_per_step"]),
+                            "includes": "append of 1 token/seq with quantise-on-append + decode"}
+        if fp is not None:
+            res["kivi_int4"]["speedup_vs_fp16_tok_s"] = round(kv["tok_s"] / fp["tok_s"], 3)
     if not args.no_cpu:
-        threads = min(16, os.cpu_count() or 1)
-        res["cpu_baseline"] = cpu_baseline(args.cpu_seconds, 4, H, n_kv, D, BS, L, threads)
+        res["cpu_baseline"] = cpu_baseline(args.cpu_seconds, 4, min(16, os.cpu_count() or 1))
     print(json.dumps(res), flush=True)
 
 

@@ -349,7 +349,8 @@ static tl::KiviPageLaunch page_launch(const tl_kivi_desc* d, const void* k_cache
                                       void* pages, void* stream) {
   tl::KiviPageLaunch a;
   memset(&a, 0, sizeof a);
-  a.k_cache = k_cache; a.v_cache = v_cache; a.block_tables = bt; a.seq_lens = sl;
+  a.k_cache = const_cast<void*>(k_cache); a.v_cache = const_cast<void*>(v_cache);
+  a.block_tables = bt; a.seq_lens = sl;
   a.page_tables = pt; a.pages = pages;
   a.num_seqs = d->num_seqs; a.num_kv_heads = d->num_kv_heads; a.block_size = d->block_size;
   a.max_blocks_per_seq = d->max_blocks_per_seq; a.num_blocks = d->num_blocks;
@@ -388,12 +389,9 @@ int tl_kivi_append(const tl_kivi_desc* desc, const void* key, const void* value,
     return fail(TL_ERR_INVALID_ARGUMENT, "NULL pointer");
   if (!aligned16(key) || !aligned16(value) || !aligned16(pages))
     return fail(TL_ERR_INVALID_ARGUMENT, "key/value/pages must be 16-byte aligned");
-  tl::CacheLaunch c = {key, value, k_cache, v_cache, slot_mapping, desc->num_seqs, desc->num_kv_heads,
-                       desc->head_size, desc->block_size, desc->num_blocks, TL_DTYPE_F16, TL_DTYPE_F16,
-                       1.f, 1.f, (hipStream_t)stream};
-  if (tl::launch_reshape_and_cache(c)) return fail(TL_ERR_BACKEND, "append launch failed");
   tl::KiviPageLaunch a = page_launch(desc, k_cache, v_cache, block_tables, seq_lens, page_tables, pages, stream);
   a.append = 1;
+  a.knew = key; a.vnew = value; a.slots = slot_mapping;
   if (tl::launch_kivi_pages(a)) return fail(TL_ERR_BACKEND, "KIVI page launch failed");
   return ok();
 }

@@ -63,8 +63,8 @@ int launch_kivi_vec(const void* in, void* out, int n_vecs, int head_dim, int n_o
                     int group_size, int stride, bool compress, hipStream_t stream);
 
 struct KiviPageLaunch {
-  const void* k_cache;          // fp16 pools [N, n_kv, 128, BS]
-  const void* v_cache;
+  void* k_cache;                // fp16 pools [N, n_kv, 128, BS] (append writes the new token)
+  void* v_cache;
   const int32_t* block_tables;
   const int32_t* seq_lens;
   const int32_t* page_tables;   // [S, max_pages_per_seq]
@@ -72,7 +72,10 @@ struct KiviPageLaunch {
   int num_seqs, num_kv_heads, block_size, max_blocks_per_seq, num_blocks;
   int max_pages_per_seq, num_pages, residual_length;
   int max_pages_to_build;       // prefix build: page slots per sequence in the grid
-  int append;                   // 1: build only the page that length L just completed
+  int append;                   // 1: write the new token, then build the page L completes
+  const void* knew;             // append: new token per sequence [S, n_kv, 128] fp16
+  const void* vnew;
+  const int32_t* slots;         // append: its slot in the fp16 pool
   hipStream_t stream;
 };
 int launch_kivi_pages(const KiviPageLaunch& a);

@@ -160,8 +160,8 @@ __global__ __launch_bounds__(128) void kivi_vec_decompress_kernel(
 // the fp16 pool [N, n_kv, 128, BS].
 // ---------------------------------------------------------------------------
 struct PageJob {
-  const uint16_t* k_cache;
-  const uint16_t* v_cache;
+  uint16_t* k_cache;        // written only by append (the new token)
+  uint16_t* v_cache;
   const int32_t* block_tables;
   const int32_t* seq_lens;
   const int32_t* page_tables;
@@ -169,7 +169,10 @@ struct PageJob {
   int num_kv_heads, block_size, max_blocks_per_seq, num_blocks;
   int max_pages_per_seq, num_pages, residual_length;
   int pages_per_seq_grid;   // grid stride over page index (prefix build)
-  int append;               // 1: only the page that length L completes, if any
+  int append;               // 1: write the new token, then the page that L completes, if any
+  const uint16_t* knew;     // append: new token per sequence [S, n_kv, 128]
+  const uint16_t* vnew;
+  const int32_t* slots;     // append: its slot in the fp16 pool
 };
 
 __global__ __launch_bounds__(128) void kivi_page_kernel(PageJob j) {
@@ -188,7 +191,16 @@ __global__ __launch_bounds__(128) void kivi_page_kernel(PageJob j) {
   const int L = j.seq_lens[seq];
   const int lq = kivi_quantized_len(L, j.residual_length);
   int page;
+  const int64_t new_off = ((int64_t)seq * j.num_kv_heads + kvh) * D;
   if (j.append) {
+    // the new token (position L - 1) into the fp16 pool, one channel per thread
+    const int32_t slot = j.slots[seq];
+    const int blk = slot >= 0 ? slot / j.block_size : -1;
+    if (blk >= 0 && blk < j.num_blocks) {
+      const int64_t off = (((int64_t)blk * j.num_kv_heads + kvh) * D + tid) * j.block_size + slot % j.block_size;
+      j.k_cache[off] = j.knew[new_off + tid];
+      j.v_cache[off] = j.vnew[new_off + tid];
+    }
     if (lq == 0 || lq == kivi_quantized_len(L - 1, j.residual_length)) return;
     page = lq / T - 1;
   } else {
@@ -207,7 +219,10 @@ __global__ __launch_bounds__(128) void kivi_page_kernel(PageJob j) {
     int phys = (lb < j.max_blocks_per_seq) ? j.block_tables[(int64_t)seq * j.max_blocks_per_seq + lb] : -1;
     if (phys >= j.num_blocks) phys = -1;
     uint16_t kv = 0, vv = 0;
-    if (phys >= 0) {
+    if (j.append && tok == L - 1) {          // just written by this workgroup: take it from the input
+      kv = j.knew[new_off + c];
+      vv = j.vnew[new_off + c];
+    } else if (phys >= 0) {
       const int64_t off = (((int64_t)phys * j.num_kv_heads + kvh) * D + c) * j.block_size + tok % j.block_size;
       kv = j.k_cache[off];
       vv = j.v_cache[off];
@@ -295,7 +310,7 @@ int launch_kivi_vec(const void* in, void* out, int n_vecs, int head_dim, int n_o
 
 int launch_kivi_pages(const KiviPageLaunch& a) {
   PageJob j;
-  j.k_cache = (const uint16_t*)a.k_cache; j.v_cache = (const uint16_t*)a.v_cache;
+  j.k_cache = (uint16_t*)a.k_cache; j.v_cache = (uint16_t*)a.v_cache;
   j.block_tables = a.block_tables; j.seq_lens = a.seq_lens; j.page_tables = a.page_tables;
   j.pages = (uint8_t*)a.pages;
   j.num_kv_heads = a.num_kv_heads; j.block_size = a.block_size;
@@ -303,6 +318,7 @@ int launch_kivi_pages(const KiviPageLaunch& a) {
   j.max_pages_per_seq = a.max_pages_per_seq; j.num_pages = a.num_pages;
   j.residual_length = a.residual_length;
   j.append = a.append;
+  j.knew = (const uint16_t*)a.knew; j.vnew = (const uint16_t*)a.vnew; j.slots = a.slots;
   j.pages_per_seq_grid = a.append ? 1 : (a.max_pages_to_build > 0 ? a.max_pages_to_build : 1);
   if (!a.append && a.max_pages_to_build <= 0) return 0;
   const dim3 grid((unsigned)(a.num_seqs * j.pages_per_seq_grid * a.num_kv_heads));

@@ -42,20 +42,16 @@ struct KiviParams {
   int max_pages_per_seq, num_pages, residual_length, partition_pages;
 };
 
-// Eight nibbles (pairs at bits 4i and 16 + 4i) to eight fp16 values
-// n * step + zero, step / zero given as four fp16 pairs.
-__device__ __forceinline__ h8 dequant8(uint32_t w, const u32x4& step, const u32x4& zero) {
-  h8 r;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint32_t x = ((w >> (4 * i)) & 0x000F000Fu) | 0x64006400u;   // 1024 + n
-    const h2 n = __builtin_bit_cast(h2, x) - (h2){(_Float16)1024.0f, (_Float16)1024.0f};
-    const h2 v = __builtin_elementwise_fma(n, __builtin_bit_cast(h2, word(step, i)),
-                                           __builtin_bit_cast(h2, word(zero, i)));
-    r[2 * i] = v.x;
-    r[2 * i + 1] = v.y;
-  }
-  return r;
+// Eight nibbles n_j (slot j at bit 16 (j & 1) + 4 (j >> 1)) to the fp16
+// values base_j + n_j, base = {1024, 1024, 64, 64, 1024, 1024, 64, 64}:
+// 0x6400 | n is 1024 + n and 0x5400 | n << 4 is 64 + n, so one shift and
+// four v_and_or_b32 cover a dword (the magic words arrive in registers, so
+// the (x & mask) | magic pattern selects v_and_or_b32).  The bases are
+// removed exactly by one more MFMA against -base (fp32 accumulation).
+__device__ __forceinline__ u32x4 nib8(uint32_t w, uint32_t m1024, uint32_t m64) {
+  const uint32_t y = w >> 8;
+  return u32x4{(w & 0x000F000Fu) | m1024, (w & 0x00F000F0u) | m64,
+               (y & 0x000F000Fu) | m1024, (y & 0x00F000F0u) | m64};
 }
 
 __device__ __forceinline__ h8 as_h8(const u32x4& c) {
@@ -75,106 +71,220 @@ __device__ __forceinline__ float swap32_max(float x) {
   return fmaxf(__builtin_bit_cast(float, (unsigned)r[0]), __builtin_bit_cast(float, (unsigned)r[1]));
 }
 
-// One wavefront over pages pg_begin, pg_begin + pg_step, ... < pg_end.
+// One page's raw bytes as a lane loads them: its K and V nibble chunks and
+// one 16-byte slice of the page's 1 KiB of (step, zero) parameters.
+struct PageRaw {
+  u32x4 kn[2], vn[2], par;
+};
+
+__device__ __forceinline__ void load_page(PageRaw& r, const uint8_t* base, int lane) {
+  r.kn[0] = load16_stream(base + lane * 16);
+  r.kn[1] = load16_stream(base + (64 + lane) * 16);
+  r.vn[0] = load16_stream(base + kKiviVNibOff + lane * 16);
+  r.vn[1] = load16_stream(base + kKiviVNibOff + (64 + lane) * 16);
+  // lanes 0-31: K params [2048, 2560); lanes 32-63: V params [4608, 5120)
+  r.par = load16_stream(base + (lane < 32 ? kKiviKParamOff + lane * 16 : kKiviVParamOff + (lane - 32) * 16));
+}
+
+// Physical page of page index pg, or -1 (hole / past the end / outside the pool).
+__device__ __forceinline__ int page_id(const KiviParams& k, const int32_t* ptab, int pg, int pg_end) {
+  if (pg >= pg_end) return -1;
+  const int pid = ptab[pg];
+  return (pid < 0 || pid >= k.num_pages) ? -1 : pid;
+}
+
+__device__ __forceinline__ h8 hmul(const h8& a, const u32x4& b) { return a * as_h8(b); }
+
+__device__ __forceinline__ f4 mfma(const h8& a, const h8& b, const f4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// Running state of one page wavefront.
+struct PageState {
+  f4 acc[8];       // rows: heads 4 grp + r, columns: channels 16 nt + u
+  float m_run;     // running max (log2 units) of head u
+  float l_lane;    // this lane's share of the running sum of head u
+};
+
+// One pair of pages (a, b) for a wavefront whose lane (grp, u) holds
+// qsc = q[head u] * scale * log2(e) at channels 32 m + 8 grp .. +7.
+//
+// q.k, per page and token tile tt:  S^T[t][u] = sum_c (n_tc step_c + zero_c) qsc_uc
+//   = sum_c (base_c + n_tc) q2_uc + [sum_c zero_c qsc_uc - sum_c base_c q2_uc],
+// q2 = qsc * step (packed fp16); the bracket is one tile per page, formed by
+// MFMAs with A = zeros / A = -base, and seeds both token tiles.
+// p.v, per page and channel group g (32 channels, per-token step/zero):
+//   O[u][c] += sum_t p_ut (n_tc step_tg + zero_tg)
+//            = sum_t (p_ut step_tg) (base_t + n_tc) - sum_t (p_ut step_tg) base_t
+//              + sum_t p_ut zero_tg,
+// three MFMAs per channel tile.
+__device__ __forceinline__ void page_pair(PageState& st, const PageRaw& ra, const PageRaw& rb, bool oka,
+                                          bool okb, const u32x4 (&qsc)[4], uint32_t* s_par_w, int lane,
+                                          uint32_t m1024, uint32_t m64, const h8& neg_base) {
+  constexpr int GT = kWaveHeads;
+  const int grp = lane >> 4;
+
+  *reinterpret_cast<u32x4*>(s_par_w + lane * 4) = ra.par;
+  *reinterpret_cast<u32x4*>(s_par_w + 256 + lane * 4) = rb.par;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+  // ---- q.k ----
+  f4 s[2][2];
+#pragma unroll
+  for (int pi = 0; pi < 2; ++pi) {
+    const PageRaw& r = pi ? rb : ra;
+    const uint32_t* par = s_par_w + pi * 256;
+    h8 q2[4];
+    f4 corr = (f4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const u32x4* kp = reinterpret_cast<const u32x4*>(par + (grp + 4 * m) * 8);
+      const h8 qm = as_h8(qsc[m]);
+      q2[m] = hmul(qm, kp[0]);
+      corr = mfma(as_h8(kp[1]), qm, corr);
+      corr = mfma(neg_base, q2[m], corr);
+    }
+    f4 t0 = corr, t1 = corr;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      t0 = mfma(as_h8(nib8(word(r.kn[0], m), m1024, m64)), q2[m], t0);
+      t1 = mfma(as_h8(nib8(word(r.kn[1], m), m1024, m64)), q2[m], t1);
+    }
+    s[pi][0] = t0;
+    s[pi][1] = t1;
+  }
+
+  // ---- online softmax: lane holds head u, tokens 4 grp + r and 16 + 4 grp + r of each page ----
+  float mx = -INFINITY;
+  if (oka) mx = fmaxf(fmaxf(fmaxf(s[0][0][0], s[0][0][1]), fmaxf(s[0][0][2], s[0][0][3])),
+                      fmaxf(fmaxf(s[0][1][0], s[0][1][1]), fmaxf(s[0][1][2], s[0][1][3])));
+  if (okb) mx = fmaxf(mx, fmaxf(fmaxf(fmaxf(s[1][0][0], s[1][0][1]), fmaxf(s[1][0][2], s[1][0][3])),
+                                fmaxf(fmaxf(s[1][1][0], s[1][1][1]), fmaxf(s[1][1][2], s[1][1][3]))));
+  mx = swap32_max(swap16_max(mx));
+  const float m_new = fmaxf(st.m_run, mx);
+  const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+  const float alpha = __builtin_amdgcn_exp2f(st.m_run - m_use);
+  st.m_run = m_new;
+  h8 pw[2];
+  float lsum = 0.f;
+#pragma unroll
+  for (int pi = 0; pi < 2; ++pi) {
+    const bool ok = pi ? okb : oka;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float e = ok ? __builtin_amdgcn_exp2f(s[pi][i >> 2][i & 3] - m_use) : 0.f;
+      lsum += e;
+      pw[pi][i] = (_Float16)e;
+    }
+  }
+  st.l_lane = st.l_lane * alpha + lsum;
+
+  // rows of acc are heads 4 grp + r: rescale with those heads' alpha
+#pragma unroll
+  for (int r = 0; r < GT; ++r) {
+    const float a_r = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, alpha), r));
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) st.acc[nt][r] *= a_r;
+  }
+
+  // ---- p.v (a hole's weights are zero; its bytes are block 0's) ----
+#pragma unroll
+  for (int pi = 0; pi < 2; ++pi) {
+    const PageRaw& r = pi ? rb : ra;
+    const uint32_t* par = s_par_w + pi * 256 + 128;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const u32x4* vp = reinterpret_cast<const u32x4*>(par + (g * 4 + grp) * 8);
+      const h8 ps = hmul(pw[pi], vp[0]);
+      const h8 vz = as_h8(vp[1]);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int nt = 2 * g + h;
+        f4 a = mfma(pw[pi], vz, st.acc[nt]);
+        a = mfma(ps, neg_base, a);
+        st.acc[nt] = mfma(ps, as_h8(nib8(word(r.vn[nt / 4], nt % 4), m1024, m64)), a);
+      }
+    }
+  }
+}
+
+// One wavefront over its pages: page pairs (pg, pg + pg_step) at
+// pg = pg_begin, pg_begin + 2 pg_step, ... below pg_end, the next pair's
+// loads in flight while a pair is computed (two register sets, alternating).
+// The pair's parameters go through the wavefront's 2 KiB LDS slot s_par_w
+// (page a at 0, page b at 256 dwords; K params first, V params at 128).
 __device__ __forceinline__ void kivi_pages_wave(const KiviParams& k, int seq, int kvh, int hs,
                                                 int pg_begin, int pg_end, int pg_step,
-                                                float* s_acc_w, float* s_m_w, float* s_l_w) {
+                                                uint32_t* s_par_w, float* s_acc_w, float* s_m_w,
+                                                float* s_l_w) {
   constexpr int GT = kWaveHeads;
   const Params& p = k.base;
   const int lane = threadIdx.x % kWave;
   const int grp = lane >> 4, u = lane & 15;     // lane group (k slots), row / column index
 
-  // B operand of q.k: head u (real for u < GT), channels 32 m + 8 grp .. +7
-  u32x4 qb[4];
+  // B operand of q.k: head u (real for u < GT), channels 32 m + 8 grp .. +7,
+  // times scale * log2(e); zero for the padding heads
+  u32x4 qsc[4];
   const int gi = hs * GT + u;
   const bool real = u < GT && gi < p.group;
   const uint16_t* qrow = (const uint16_t*)p.q +
       ((int64_t)seq * p.num_heads + (real ? head_of(p, kvh, gi) : 0)) * kKiviHead;
+  const _Float16 qs = (_Float16)p.qk_scale;
 #pragma unroll
-  for (int m = 0; m < 4; ++m)
-    qb[m] = real ? load16(qrow + 32 * m + 8 * grp) : u32x4{0u, 0u, 0u, 0u};
+  for (int m = 0; m < 4; ++m) {
+    const u32x4 raw = real ? load16(qrow + 32 * m + 8 * grp) : u32x4{0u, 0u, 0u, 0u};
+    const h8 v = as_h8(raw) * qs;
+    qsc[m] = __builtin_bit_cast(u32x4, v);
+  }
+  // magic words held opaque in registers (an empty asm, no instruction)
+  uint32_t m1024 = 0x64006400u, m64 = 0x54005400u;
+  asm volatile("" : "+v"(m1024), "+v"(m64));
+  const _Float16 nb1024 = (_Float16)-1024.0f, nb64 = (_Float16)-64.0f;
+  const h8 neg_base = {nb1024, nb1024, nb64, nb64, nb1024, nb1024, nb64, nb64};
 
-  float m_run = -INFINITY, l_lane = 0.f;       // for head u
-  f4 acc[8];                                   // rows: heads 4 grp + r, columns: channels 16 nt + u
+  PageState st;
+  st.m_run = -INFINITY;
+  st.l_lane = 0.f;
 #pragma unroll
-  for (int nt = 0; nt < 8; ++nt) acc[nt] = (f4){0.f, 0.f, 0.f, 0.f};
+  for (int nt = 0; nt < 8; ++nt) st.acc[nt] = (f4){0.f, 0.f, 0.f, 0.f};
 
   const int32_t* ptab = k.page_tables + (int64_t)seq * k.max_pages_per_seq;
+  const uint8_t* pool = k.pages + (int64_t)kvh * kKiviPageBytes;
+  const int64_t pid_stride = (int64_t)p.num_kv_heads * kKiviPageBytes;
+  const int pair = 2 * pg_step;
+  auto pid = [&](int pg) { return __builtin_amdgcn_readfirstlane(page_id(k, ptab, pg, pg_end)); };
+  auto load = [&](PageRaw& ra, PageRaw& rb, int ia, int ib) {
+    load_page(ra, pool + (int64_t)max(ia, 0) * pid_stride, lane);
+    load_page(rb, pool + (int64_t)max(ib, 0) * pid_stride, lane);
+  };
+
+  int ia = pid(pg_begin), ib = pid(pg_begin + pg_step);                // pair being computed
+  int ja = pid(pg_begin + pair), jb = pid(pg_begin + pair + pg_step);  // next pair
+  PageRaw r0a, r0b, r1a, r1b;
+  if (pg_begin < pg_end) load(r0a, r0b, ia, ib);
+
 #pragma unroll 1
-  for (int pg = pg_begin; pg < pg_end; pg += pg_step) {
-    const int pid = ptab[pg];
-    if (pid < 0 || pid >= k.num_pages) continue;
-    const uint8_t* base = k.pages + ((int64_t)pid * p.num_kv_heads + kvh) * kKiviPageBytes;
-    u32x4 kn[2], ks[4], kz[4], vn[2], vs[4], vz[4];
-#pragma unroll
-    for (int tt = 0; tt < 2; ++tt) kn[tt] = load16_stream(base + (tt * 64 + lane) * 16);
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      const uint8_t* kp = base + kKiviKParamOff + (grp + 4 * m) * 32;
-      ks[m] = load16(kp);
-      kz[m] = load16(kp + 16);
+  for (int pg = pg_begin; pg < pg_end; pg += 2 * pair) {
+    {
+      const int na = pid(pg + 2 * pair), nb = pid(pg + 2 * pair + pg_step);
+      if (pg + pair < pg_end) load(r1a, r1b, ja, jb);
+      page_pair(st, r0a, r0b, ia >= 0, ib >= 0, qsc, s_par_w, lane, m1024, m64, neg_base);
+      ia = ja; ib = jb; ja = na; jb = nb;
     }
-#pragma unroll
-    for (int hh = 0; hh < 2; ++hh) vn[hh] = load16_stream(base + kKiviVNibOff + (hh * 64 + lane) * 16);
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const uint8_t* vp = base + kKiviVParamOff + (g * 4 + grp) * 32;
-      vs[g] = load16(vp);
-      vz[g] = load16(vp + 16);
-    }
-
-    // ---- q.k: S^T[token][head], token tiles 0 and 1 ----
-    f4 s0 = (f4){0.f, 0.f, 0.f, 0.f}, s1 = s0;
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      const h8 qm = as_h8(qb[m]);
-      s0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(dequant8(word(kn[0], m), ks[m], kz[m]), qm, s0, 0, 0, 0);
-      s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(dequant8(word(kn[1], m), ks[m], kz[m]), qm, s1, 0, 0, 0);
-    }
-    // lane holds head u, tokens 4 grp + r (tile 0) and 16 + 4 grp + r (tile 1)
-    float sc[8];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      sc[r] = real ? s0[r] * p.qk_scale : -INFINITY;
-      sc[4 + r] = real ? s1[r] * p.qk_scale : -INFINITY;
-    }
-    float mx = sc[0];
-#pragma unroll
-    for (int i = 1; i < 8; ++i) mx = fmaxf(mx, sc[i]);
-    mx = swap32_max(swap16_max(mx));
-    const float m_new = fmaxf(m_run, mx);
-    const float alpha = (m_run == m_new) ? 1.f : (m_run == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new));
-    m_run = m_new;
-    float pw[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) pw[i] = real ? __builtin_amdgcn_exp2f(sc[i] - m_new) : 0.f;
-    l_lane = l_lane * alpha;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) l_lane += pw[i];
-    h8 pa;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) pa[i] = (_Float16)pw[i];
-
-    // rows of acc are heads 4 grp + r: rescale with those heads' alpha
-#pragma unroll
-    for (int r = 0; r < GT; ++r) {
-      const float a_r = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, alpha), r));
-      if (a_r != 1.f) {
-#pragma unroll
-        for (int nt = 0; nt < 8; ++nt) acc[nt][r] *= a_r;
-      }
-    }
-
-    // ---- p.v over the page's 32 tokens, 8 channel tiles ----
-#pragma unroll
-    for (int nt = 0; nt < 8; ++nt) {
-      const h8 vb = dequant8(word(vn[nt / 4], nt % 4), vs[nt / 2], vz[nt / 2]);
-      acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, vb, acc[nt], 0, 0, 0);
+    if (pg + pair >= pg_end) break;
+    {
+      const int na = pid(pg + 3 * pair), nb = pid(pg + 3 * pair + pg_step);
+      if (pg + 2 * pair < pg_end) load(r0a, r0b, ja, jb);
+      page_pair(st, r1a, r1b, ia >= 0, ib >= 0, qsc, s_par_w, lane, m1024, m64, neg_base);
+      ia = ja; ib = jb; ja = na; jb = nb;
     }
   }
 
   // sums over the four lane groups for head u
   {
+    const float l_lane = st.l_lane;
     const auto r16 = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(unsigned, l_lane),
                                                       __builtin_bit_cast(unsigned, l_lane), false, false);
     const float l2 = __builtin_bit_cast(float, (unsigned)r16[0]) + __builtin_bit_cast(float, (unsigned)r16[1]);
@@ -182,7 +292,7 @@ __device__ __forceinline__ void kivi_pages_wave(const KiviParams& k, int seq, in
                                                       __builtin_bit_cast(unsigned, l2), false, false);
     const float l4 = __builtin_bit_cast(float, (unsigned)r32[0]) + __builtin_bit_cast(float, (unsigned)r32[1]);
     if (lane < GT) {
-      s_m_w[lane] = m_run;
+      s_m_w[lane] = st.m_run;
       s_l_w[lane] = l4;
     }
   }
@@ -190,14 +300,14 @@ __device__ __forceinline__ void kivi_pages_wave(const KiviParams& k, int seq, in
 #pragma unroll
     for (int nt = 0; nt < 8; ++nt)
 #pragma unroll
-      for (int r = 0; r < GT; ++r) s_acc_w[r * kKiviHead + nt * 16 + u] = acc[nt][r];
+      for (int r = 0; r < GT; ++r) s_acc_w[r * kKiviHead + nt * 16 + u] = st.acc[nt][r];
   }
 }
 
 template <int NW, bool FINAL>
 __global__ __launch_bounds__(NW * kWave) void kivi_decode_kernel(KiviParams k) {
   constexpr int GT = kWaveHeads;
-  __shared__ __attribute__((aligned(16))) uint32_t s_p[NW][4][GT][4];
+  __shared__ __attribute__((aligned(16))) uint32_t s_p[NW][512];   // per wave: weights or page params
   __shared__ float s_m[NW][GT], s_l[NW][GT];
   __shared__ float s_acc[NW][GT][kKiviHead];
 
@@ -219,10 +329,10 @@ __global__ __launch_bounds__(NW * kWave) void kivi_decode_kernel(KiviParams k) {
   const int page_waves = has_res ? NW - 1 : NW;
 
   if (wave < page_waves) {
-    kivi_pages_wave(k, seq, kvh, hs, pg0 + wave, pg1, page_waves, &s_acc[wave][0][0], &s_m[wave][0],
-                    &s_l[wave][0]);
+    kivi_pages_wave(k, seq, kvh, hs, pg0 + wave, pg1, page_waves, &s_p[wave][0], &s_acc[wave][0][0],
+                    &s_m[wave][0], &s_l[wave][0]);
   } else {
-    decode2_wave<Kind::F16, kKiviHead, 16>(p, seq, kvh, hs, lq, L, 32, &s_p[wave][0][0][0],
+    decode2_wave<Kind::F16, kKiviHead, 16>(p, seq, kvh, hs, lq, L, 32, &s_p[wave][0],
                                            &s_acc[wave][0][0], &s_m[wave][0], &s_l[wave][0]);
   }
   __syncthreads();
