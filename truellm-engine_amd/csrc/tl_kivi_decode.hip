@@ -42,17 +42,18 @@ struct KiviParams {
   int max_pages_per_seq, num_pages, residual_length, partition_pages;
 };
 
-// Eight nibbles n_j (slot j at bit 16 (j & 1) + 4 (j >> 1)) to the fp16
-// values base_j + n_j, base = {1024, 1024, 64, 64, 1024, 1024, 64, 64}:
-// 0x6400 | n is 1024 + n and 0x5400 | n << 4 is 64 + n, so one shift and
-// four v_and_or_b32 cover a dword (the magic words arrive in registers, so
-// the (x & mask) | magic pattern selects v_and_or_b32).  The bases are
-// removed exactly by one more MFMA against -base (fp32 accumulation).
-__device__ __forceinline__ u32x4 nib8(uint32_t w, uint32_t m1024, uint32_t m64) {
+// Eight nibbles n_j (slot j at bit 16 (j & 1) + 4 (j >> 1)) as fp16
+// denormals: a masked nibble pair is the fp16 pair (n * 2^-24, n' * 2^-24),
+// or 16 n * 2^-24 for the pairs at bits 4 and 20 (slots 2, 3, 6, 7; the
+// factor 16 is taken out of the other MFMA operand: slot_scale).  One shift
+// and four ands per dword; the MFMA takes denormal fp16 inputs exactly and
+// the 2^24 is restored in fp32.
+__device__ __forceinline__ u32x4 nib8(uint32_t w) {
   const uint32_t y = w >> 8;
-  return u32x4{(w & 0x000F000Fu) | m1024, (w & 0x00F000F0u) | m64,
-               (y & 0x000F000Fu) | m1024, (y & 0x00F000F0u) | m64};
+  return u32x4{w & 0x000F000Fu, w & 0x00F000F0u, y & 0x000F000Fu, y & 0x00F000F0u};
 }
+
+constexpr float kTwo24 = 16777216.0f, kTwoM24 = 1.0f / 16777216.0f;
 
 __device__ __forceinline__ h8 as_h8(const u32x4& c) {
   typedef unsigned u4 __attribute__((ext_vector_type(4)));
@@ -101,7 +102,8 @@ __device__ __forceinline__ f4 mfma(const h8& a, const h8& b, const f4& c) {
 
 // Running state of one page wavefront.
 struct PageState {
-  f4 acc[8];       // rows: heads 4 grp + r, columns: channels 16 nt + u
+  f4 acc[8];       // 2^-24 * sum p step n:  rows heads 4 grp + r, columns channels 16 nt + u
+  f4 cz;           // sum p zero:  rows heads 4 grp + r, column u = channel group (u < 4)
   float m_run;     // running max (log2 units) of head u
   float l_lane;    // this lane's share of the running sum of head u
 };
@@ -109,20 +111,19 @@ struct PageState {
 // One pair of pages (a, b) for a wavefront whose lane (grp, u) holds
 // qsc = q[head u] * scale * log2(e) at channels 32 m + 8 grp .. +7.
 //
-// q.k, per page and token tile tt:  S^T[t][u] = sum_c (n_tc step_c + zero_c) qsc_uc
-//   = sum_c (base_c + n_tc) q2_uc + [sum_c zero_c qsc_uc - sum_c base_c q2_uc],
-// q2 = qsc * step (packed fp16); the bracket is one tile per page, formed by
-// MFMAs with A = zeros / A = -base, and seeds both token tiles.
+// q.k, per page and token tile:  S^T[t][u] = sum_c (n_tc step_c + zero_c) qsc_uc
+//   = 2^24 sum_c (n_tc 2^-24) (qsc_uc step_c slot_scale) + sum_c zero_c qsc_uc;
+// the zero term is one tile per page (A = zeros, rows all alike) scaled by
+// 2^-24 to seed both token tiles, so the tiles hold 2^-24 S^T.
 // p.v, per page and channel group g (32 channels, per-token step/zero):
-//   O[u][c] += sum_t p_ut (n_tc step_tg + zero_tg)
-//            = sum_t (p_ut step_tg) (base_t + n_tc) - sum_t (p_ut step_tg) base_t
-//              + sum_t p_ut zero_tg,
-// three MFMAs per channel tile.
+//   O[u][c] = 2^24 sum_t (p_ut slot_scale step_tg) (n_tc 2^-24) + sum_t p_ut zero_tg;
+// the first sum goes to acc (one MFMA per channel tile), the second to cz
+// (one MFMA per page: B column g holds zero_tg).
 __device__ __forceinline__ void page_pair(PageState& st, const PageRaw& ra, const PageRaw& rb, bool oka,
                                           bool okb, const u32x4 (&qsc)[4], uint32_t* s_par_w, int lane,
-                                          uint32_t m1024, uint32_t m64, const h8& neg_base) {
+                                          const h8& slot_scale) {
   constexpr int GT = kWaveHeads;
-  const int grp = lane >> 4;
+  const int grp = lane >> 4, u = lane & 15;
 
   *reinterpret_cast<u32x4*>(s_par_w + lane * 4) = ra.par;
   *reinterpret_cast<u32x4*>(s_par_w + 256 + lane * 4) = rb.par;
@@ -130,39 +131,39 @@ __device__ __forceinline__ void page_pair(PageState& st, const PageRaw& ra, cons
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-  // ---- q.k ----
+  // ---- q.k (tiles hold 2^-24 S^T) ----
   f4 s[2][2];
 #pragma unroll
   for (int pi = 0; pi < 2; ++pi) {
     const PageRaw& r = pi ? rb : ra;
     const uint32_t* par = s_par_w + pi * 256;
-    h8 q2[4];
-    f4 corr = (f4){0.f, 0.f, 0.f, 0.f};
+    f4 zt = (f4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
       const u32x4* kp = reinterpret_cast<const u32x4*>(par + (grp + 4 * m) * 8);
-      const h8 qm = as_h8(qsc[m]);
-      q2[m] = hmul(qm, kp[0]);
-      corr = mfma(as_h8(kp[1]), qm, corr);
-      corr = mfma(neg_base, q2[m], corr);
+      zt = mfma(as_h8(kp[1]), as_h8(qsc[m]), zt);
     }
-    f4 t0 = corr, t1 = corr;
+    f4 t0 = zt * kTwoM24, t1 = t0;
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
-      t0 = mfma(as_h8(nib8(word(r.kn[0], m), m1024, m64)), q2[m], t0);
-      t1 = mfma(as_h8(nib8(word(r.kn[1], m), m1024, m64)), q2[m], t1);
+      const u32x4* kp = reinterpret_cast<const u32x4*>(par + (grp + 4 * m) * 8);
+      const h8 q2 = hmul(as_h8(qsc[m]), kp[0]) * slot_scale;
+      t0 = mfma(as_h8(nib8(word(r.kn[0], m))), q2, t0);
+      t1 = mfma(as_h8(nib8(word(r.kn[1], m))), q2, t1);
     }
     s[pi][0] = t0;
     s[pi][1] = t1;
   }
+  // a hole's scores (block 0's bytes) are dropped
+  if (!oka) s[0][0] = s[0][1] = (f4){-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+  if (!okb) s[1][0] = s[1][1] = (f4){-INFINITY, -INFINITY, -INFINITY, -INFINITY};
 
   // ---- online softmax: lane holds head u, tokens 4 grp + r and 16 + 4 grp + r of each page ----
-  float mx = -INFINITY;
-  if (oka) mx = fmaxf(fmaxf(fmaxf(s[0][0][0], s[0][0][1]), fmaxf(s[0][0][2], s[0][0][3])),
-                      fmaxf(fmaxf(s[0][1][0], s[0][1][1]), fmaxf(s[0][1][2], s[0][1][3])));
-  if (okb) mx = fmaxf(mx, fmaxf(fmaxf(fmaxf(s[1][0][0], s[1][0][1]), fmaxf(s[1][0][2], s[1][0][3])),
-                                fmaxf(fmaxf(s[1][1][0], s[1][1][1]), fmaxf(s[1][1][2], s[1][1][3]))));
-  mx = swap32_max(swap16_max(mx));
+  float mx = fmaxf(fmaxf(fmaxf(s[0][0][0], s[0][0][1]), fmaxf(s[0][0][2], s[0][0][3])),
+                   fmaxf(fmaxf(s[0][1][0], s[0][1][1]), fmaxf(s[0][1][2], s[0][1][3])));
+  mx = fmaxf(mx, fmaxf(fmaxf(fmaxf(s[1][0][0], s[1][0][1]), fmaxf(s[1][0][2], s[1][0][3])),
+                       fmaxf(fmaxf(s[1][1][0], s[1][1][1]), fmaxf(s[1][1][2], s[1][1][3]))));
+  mx = swap32_max(swap16_max(mx)) * kTwo24;
   const float m_new = fmaxf(st.m_run, mx);
   const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
   const float alpha = __builtin_amdgcn_exp2f(st.m_run - m_use);
@@ -171,40 +172,41 @@ __device__ __forceinline__ void page_pair(PageState& st, const PageRaw& ra, cons
   float lsum = 0.f;
 #pragma unroll
   for (int pi = 0; pi < 2; ++pi) {
-    const bool ok = pi ? okb : oka;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const float e = ok ? __builtin_amdgcn_exp2f(s[pi][i >> 2][i & 3] - m_use) : 0.f;
+      const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(s[pi][i >> 2][i & 3], kTwo24, -m_use));
       lsum += e;
       pw[pi][i] = (_Float16)e;
     }
   }
   st.l_lane = st.l_lane * alpha + lsum;
 
-  // rows of acc are heads 4 grp + r: rescale with those heads' alpha
+  // rows of acc / cz are heads 4 grp + r: rescale with those heads' alpha
+  if (__builtin_amdgcn_ballot_w64(alpha != 1.f)) {
 #pragma unroll
-  for (int r = 0; r < GT; ++r) {
-    const float a_r = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, alpha), r));
+    for (int r = 0; r < GT; ++r) {
+      const float a_r = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, alpha), r));
 #pragma unroll
-    for (int nt = 0; nt < 8; ++nt) st.acc[nt][r] *= a_r;
+      for (int nt = 0; nt < 8; ++nt) st.acc[nt][r] *= a_r;
+      st.cz[r] *= a_r;
+    }
   }
 
-  // ---- p.v (a hole's weights are zero; its bytes are block 0's) ----
+  // ---- p.v (a hole's weights are zero) ----
 #pragma unroll
   for (int pi = 0; pi < 2; ++pi) {
     const PageRaw& r = pi ? rb : ra;
     const uint32_t* par = s_par_w + pi * 256 + 128;
+    // zero term: B column u < 4 holds zero_tg of group g = u
+    st.cz = mfma(pw[pi], as_h8(reinterpret_cast<const u32x4*>(par + ((u & 3) * 4 + grp) * 8)[1]), st.cz);
+    const h8 pws = pw[pi] * slot_scale;
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
-      const u32x4* vp = reinterpret_cast<const u32x4*>(par + (g * 4 + grp) * 8);
-      const h8 ps = hmul(pw[pi], vp[0]);
-      const h8 vz = as_h8(vp[1]);
+      const h8 ps = hmul(pws, reinterpret_cast<const u32x4*>(par + (g * 4 + grp) * 8)[0]);
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const int nt = 2 * g + h;
-        f4 a = mfma(pw[pi], vz, st.acc[nt]);
-        a = mfma(ps, neg_base, a);
-        st.acc[nt] = mfma(ps, as_h8(nib8(word(r.vn[nt / 4], nt % 4), m1024, m64)), a);
+        st.acc[nt] = mfma(ps, as_h8(nib8(word(r.vn[nt / 4], nt % 4))), st.acc[nt]);
       }
     }
   }
@@ -226,6 +228,8 @@ __device__ __forceinline__ void kivi_pages_wave(const KiviParams& k, int seq, in
 
   // B operand of q.k: head u (real for u < GT), channels 32 m + 8 grp .. +7,
   // times scale * log2(e); zero for the padding heads
+  const _Float16 one = (_Float16)1.0f, sixteenth = (_Float16)0.0625f;
+  const h8 slot_scale = {one, one, sixteenth, sixteenth, one, one, sixteenth, sixteenth};
   u32x4 qsc[4];
   const int gi = hs * GT + u;
   const bool real = u < GT && gi < p.group;
@@ -238,15 +242,11 @@ __device__ __forceinline__ void kivi_pages_wave(const KiviParams& k, int seq, in
     const h8 v = as_h8(raw) * qs;
     qsc[m] = __builtin_bit_cast(u32x4, v);
   }
-  // magic words held opaque in registers (an empty asm, no instruction)
-  uint32_t m1024 = 0x64006400u, m64 = 0x54005400u;
-  asm volatile("" : "+v"(m1024), "+v"(m64));
-  const _Float16 nb1024 = (_Float16)-1024.0f, nb64 = (_Float16)-64.0f;
-  const h8 neg_base = {nb1024, nb1024, nb64, nb64, nb1024, nb1024, nb64, nb64};
 
   PageState st;
   st.m_run = -INFINITY;
   st.l_lane = 0.f;
+  st.cz = (f4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int nt = 0; nt < 8; ++nt) st.acc[nt] = (f4){0.f, 0.f, 0.f, 0.f};
 
@@ -270,14 +270,14 @@ __device__ __forceinline__ void kivi_pages_wave(const KiviParams& k, int seq, in
     {
       const int na = pid(pg + 2 * pair), nb = pid(pg + 2 * pair + pg_step);
       if (pg + pair < pg_end) load(r1a, r1b, ja, jb);
-      page_pair(st, r0a, r0b, ia >= 0, ib >= 0, qsc, s_par_w, lane, m1024, m64, neg_base);
+      page_pair(st, r0a, r0b, ia >= 0, ib >= 0, qsc, s_par_w, lane, slot_scale);
       ia = ja; ib = jb; ja = na; jb = nb;
     }
     if (pg + pair >= pg_end) break;
     {
       const int na = pid(pg + 3 * pair), nb = pid(pg + 3 * pair + pg_step);
       if (pg + 2 * pair < pg_end) load(r0a, r0b, ja, jb);
-      page_pair(st, r1a, r1b, ia >= 0, ib >= 0, qsc, s_par_w, lane, m1024, m64, neg_base);
+      page_pair(st, r1a, r1b, ia >= 0, ib >= 0, qsc, s_par_w, lane, slot_scale);
       ia = ja; ib = jb; ja = na; jb = nb;
     }
   }
@@ -296,11 +296,22 @@ __device__ __forceinline__ void kivi_pages_wave(const KiviParams& k, int seq, in
       s_l_w[lane] = l4;
     }
   }
+  // O = 2^24 acc + cz[group]; cz of (head r, group g) sits in lane g of
+  // group 0 and goes through the (now free) parameter slot
+  float* s_cz = reinterpret_cast<float*>(s_par_w);
+  if (lane < 4) {
+#pragma unroll
+    for (int r = 0; r < GT; ++r) s_cz[r * 4 + lane] = st.cz[r];
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   if (grp == 0) {
 #pragma unroll
     for (int nt = 0; nt < 8; ++nt)
 #pragma unroll
-      for (int r = 0; r < GT; ++r) s_acc_w[r * kKiviHead + nt * 16 + u] = st.acc[nt][r];
+      for (int r = 0; r < GT; ++r)
+        s_acc_w[r * kKiviHead + nt * 16 + u] = __builtin_fmaf(st.acc[nt][r], kTwo24, s_cz[r * 4 + nt / 2]);
   }
 }
 
