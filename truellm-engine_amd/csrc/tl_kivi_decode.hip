@@ -78,13 +78,22 @@ struct PageRaw {
   u32x4 kn[2], vn[2], par;
 };
 
-__device__ __forceinline__ void load_page(PageRaw& r, const uint8_t* base, int lane) {
-  r.kn[0] = load16_stream(base + lane * 16);
-  r.kn[1] = load16_stream(base + (64 + lane) * 16);
-  r.vn[0] = load16_stream(base + kKiviVNibOff + lane * 16);
-  r.vn[1] = load16_stream(base + kKiviVNibOff + (64 + lane) * 16);
-  // lanes 0-31: K params [2048, 2560); lanes 32-63: V params [4608, 5120)
-  r.par = load16_stream(base + (lane < 32 ? kKiviKParamOff + lane * 16 : kKiviVParamOff + (lane - 32) * 16));
+// One page through a buffer descriptor built in scalar registers (base =
+// the page, 5120 bytes in range, so the hardware also bounds every access)
+// and per-lane 32-bit offsets: the loads need no per-lane address registers.
+// aux 2 = non-temporal (the page is read once per decode step).
+constexpr int kBufferWord3 = 0x00020000;   // raw buffer, CDNA dword 3
+__device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t r, unsigned off) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 2));
+}
+__device__ __forceinline__ void load_page(PageRaw& r, const uint8_t* page, unsigned off, unsigned par_off) {
+  const __amdgpu_buffer_rsrc_t rs =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(page), (short)0, kKiviPageBytes, kBufferWord3);
+  r.kn[0] = buffer_load16(rs, off);
+  r.kn[1] = buffer_load16(rs, 1024u + off);
+  r.vn[0] = buffer_load16(rs, unsigned(kKiviVNibOff) + off);
+  r.vn[1] = buffer_load16(rs, unsigned(kKiviVNibOff) + 1024u + off);
+  r.par = buffer_load16(rs, par_off);
 }
 
 // Physical page of page index pg, or -1 (hole / past the end / outside the pool).
@@ -252,33 +261,38 @@ __device__ __forceinline__ void kivi_pages_wave(const KiviParams& k, int seq, in
 
   const int32_t* ptab = k.page_tables + (int64_t)seq * k.max_pages_per_seq;
   const uint8_t* pool = k.pages + (int64_t)kvh * kKiviPageBytes;
-  const int64_t pid_stride = (int64_t)p.num_kv_heads * kKiviPageBytes;
-  const int pair = 2 * pg_step;
-  auto pid = [&](int pg) { return __builtin_amdgcn_readfirstlane(page_id(k, ptab, pg, pg_end)); };
+  const uint32_t pid_stride = uint32_t(p.num_kv_heads) * uint32_t(kKiviPageBytes);
+  // lane's 16 bytes of each 1 KiB nibble block; lanes 0-31 take the K params
+  // [2048, 2560), lanes 32-63 the V params [4608, 5120)
+  const unsigned off = unsigned(lane) * 16u;
+  const unsigned par_off = lane < 32 ? unsigned(kKiviKParamOff) + off : unsigned(kKiviVParamOff) + off - 512u;
   auto load = [&](PageRaw& ra, PageRaw& rb, int ia, int ib) {
-    load_page(ra, pool + (int64_t)max(ia, 0) * pid_stride, lane);
-    load_page(rb, pool + (int64_t)max(ib, 0) * pid_stride, lane);
+    // 32 x 32 -> 64-bit products keep the page base in scalar registers
+    load_page(ra, pool + uint64_t(uint32_t(max(ia, 0))) * pid_stride, off, par_off);
+    load_page(rb, pool + uint64_t(uint32_t(max(ib, 0))) * pid_stride, off, par_off);
   };
 
-  int ia = pid(pg_begin), ib = pid(pg_begin + pg_step);                // pair being computed
-  int ja = pid(pg_begin + pair), jb = pid(pg_begin + pair + pg_step);  // next pair
+  // The wavefront's pages are pg_begin + o * pg_step, o = 0 .. n_mine - 1.
+  // Their physical ids are read 64 at a time into one register (lane i: page
+  // o = c0 + i) and taken out with readlane, so the loop issues no table
+  // loads.  Page loads are unconditional (past the end they fetch page 0
+  // again, an L2 hit): a fixed number of loads per iteration lets the
+  // compiler wait only for the pair about to be used, not for the prefetch.
+  const int n_mine = pg_begin < pg_end ? (pg_end - pg_begin + pg_step - 1) / pg_step : 0;
   PageRaw r0a, r0b, r1a, r1b;
-  if (pg_begin < pg_end) load(r0a, r0b, ia, ib);
-
 #pragma unroll 1
-  for (int pg = pg_begin; pg < pg_end; pg += 2 * pair) {
-    {
-      const int na = pid(pg + 2 * pair), nb = pid(pg + 2 * pair + pg_step);
-      if (pg + pair < pg_end) load(r1a, r1b, ja, jb);
-      page_pair(st, r0a, r0b, ia >= 0, ib >= 0, qsc, s_par_w, lane, slot_scale);
-      ia = ja; ib = jb; ja = na; jb = nb;
-    }
-    if (pg + pair >= pg_end) break;
-    {
-      const int na = pid(pg + 3 * pair), nb = pid(pg + 3 * pair + pg_step);
-      if (pg + 2 * pair < pg_end) load(r0a, r0b, ja, jb);
-      page_pair(st, r1a, r1b, ia >= 0, ib >= 0, qsc, s_par_w, lane, slot_scale);
-      ia = ja; ib = jb; ja = na; jb = nb;
+  for (int c0 = 0; c0 < n_mine; c0 += kWave) {
+    const int cn = min(kWave, n_mine - c0);
+    const int idv = page_id(k, ptab, pg_begin + (c0 + lane) * pg_step, pg_end);
+    auto id = [&](int o) { return o < cn ? __builtin_amdgcn_readlane(idv, o) : -1; };
+    load(r0a, r0b, id(0), id(1));
+#pragma unroll 1
+    for (int o = 0; o < cn; o += 4) {
+      load(r1a, r1b, id(o + 2), id(o + 3));
+      page_pair(st, r0a, r0b, id(o) >= 0, id(o + 1) >= 0, qsc, s_par_w, lane, slot_scale);
+      if (o + 2 >= cn) break;
+      load(r0a, r0b, id(o + 4), id(o + 5));
+      page_pair(st, r1a, r1b, id(o + 2) >= 0, id(o + 3) >= 0, qsc, s_par_w, lane, slot_scale);
     }
   }
 
@@ -323,7 +337,8 @@ __global__ __launch_bounds__(NW * kWave) void kivi_decode_kernel(KiviParams k) {
   __shared__ float s_acc[NW][GT][kKiviHead];
 
   const Params& p = k.base;
-  const int tid = threadIdx.x, wave = tid / kWave;
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);   // wave-uniform (SGPR)
   int bid = blockIdx.x;
   const int part = bid % p.num_partitions; bid /= p.num_partitions;
   const int hs = bid % p.head_slices;      bid /= p.head_slices;
