@@ -13,11 +13,14 @@ Workloads (synthetic, seeded; q/K/V ~ N(0,1)):
 Two copies of every pool are rotated between steps so the 256 MiB Infinity
 Cache cannot serve a re-timed step.
 
+The timed steps are captured into one HIP graph and replayed (events on the
+replay stream), as a serving decode loop runs; warmup steps run eagerly.
+
 Prints one JSON line.  value = GB/s of algorithmic bytes (KV read once + q
 read + out write + block tables + seq_lens) per bf16 step over the timed
-steps; roofline = the same bytes over the decode kernel's average duration
-(HIP events on the launch stream) against 8 TB/s; cpu_baseline = the
-oracle's multithreaded fp32 decode on the host cores over a bounded sample.
+steps; roofline = the same bytes over the decode launch's average duration
+(one launch per step) against 8 TB/s; cpu_baseline = the oracle's
+multithreaded fp32 decode on the host cores over a bounded sample.
 """
 import argparse
 import json
@@ -73,19 +76,30 @@ def parse():
     return p.parse_args()
 
 
-def timed(step, steps, warmup, stream):
+def timed(step, steps, warmup):
+    """Run `warmup` eager steps, capture the next `steps` steps into one HIP
+    graph, replay it once untimed, then time one replay with events on the
+    replay stream.  Returns ms per step.  A serving decode loop runs the same
+    way: the graph removes the per-launch host cost, which otherwise exceeds a
+    short step's GPU time."""
     import torch
+    stream = torch.cuda.current_stream()
     for i in range(warmup):
-        step(i)
+        step(i, stream)
     torch.cuda.synchronize()
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
-    ev[0].record(stream)
-    for i in range(steps):
-        step(warmup + i)
-        ev[i + 1].record(stream)
+    graph = torch.cuda.CUDAGraph()
+    cap = torch.cuda.Stream()
+    with torch.cuda.graph(graph, stream=cap):
+        for i in range(steps):
+            step(warmup + i, cap)
+    graph.replay()
     torch.cuda.synchronize()
-    per = [ev[i].elapsed_time(ev[i + 1]) for i in range(steps)]
-    return ev[0].elapsed_time(ev[-1]) / steps, per
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    graph.replay()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
 
 
 def bench_decode(args, dtype):
@@ -109,15 +123,14 @@ def bench_decode(args, dtype):
     desc = tla.make_decode_desc(q, pools[0][0], pools[0][2], NKV, 1.0 / math.sqrt(D),
                                 gqa_map=tla.GQA_GROUPED, partition_tokens=args.partition_tokens)
     ws = torch.empty(max(16, tla.workspace_bytes(desc, CTX)), dtype=torch.uint8, device="cuda")
-    stream = torch.cuda.current_stream()
 
-    def step(i):
+    def step(i, stream):
         k, v, tables = pools[i % 2]
         tla.paged_attention_decode(desc, out, q, k, v, tables, sl, CTX, ws, stream)
 
-    ms, per = timed(step, args.steps, args.warmup, stream)
+    ms = timed(step, args.steps, args.warmup)
     nbytes = algorithmic_bytes([CTX] * S, 2)
-    launch_ms = sum(per) / len(per)
+    launch_ms = ms                      # one decode launch per step
     return {
         "ms_per_step": ms, "gbs": nbytes / (ms * 1e-3) / 1e9, "tok_s": S / (ms * 1e-3),
         "bytes": nbytes, "launch_ms": launch_ms, "pool_blocks": N,
@@ -174,7 +187,6 @@ def bench_kivi(args, R=128):
     desc0 = tla.make_kivi_desc(q, reps[0][0], reps[0][2], reps[0][3], reps[0][5], NKV, scale,
                                residual_length=R, gqa_map=tla.GQA_GROUPED)
     ws = torch.empty(max(16, tla.kivi_workspace_bytes(desc0, Lmax)), dtype=torch.uint8, device="cuda")
-    stream = torch.cuda.current_stream()
     for rep in reps:
         d = tla.make_kivi_desc(q, rep[0], rep[2], rep[3], rep[5], NKV, scale, residual_length=R)
         sl0 = torch.full((S,), L0, dtype=torch.int32, device="cuda")
@@ -182,7 +194,7 @@ def bench_kivi(args, R=128):
     descs = [tla.make_kivi_desc(q, rep[0], rep[2], rep[3], rep[5], NKV, scale, residual_length=R)
              for rep in reps]
 
-    def step(i):
+    def step(i, stream):
         r, L = plan[i]
         k, v, tables, ptables, pages, _ = reps[r]
         tla.kivi_append(descs[r], knew, vnew, k, v, slot_dev[i], tables, sl_dev[i], ptables, pages,
@@ -190,7 +202,7 @@ def bench_kivi(args, R=128):
         tla.kivi_paged_attention_decode(descs[r], out, q, pages, ptables, k, v, tables, sl_dev[i], L,
                                         ws, stream)
 
-    ms, per = timed(step, args.steps, args.warmup, stream)
+    ms = timed(step, args.steps, args.warmup)
     nbytes = []
     for i in range(args.warmup, total_steps):
         _, L = plan[i]

@@ -244,3 +244,33 @@ def test_full_size_single_pass_equals_split_k_and_spot_checks():
                                   np.arange(nb, dtype=np.int32)[None], np.array([L], np.int32),
                                   n_kv, scale, orc.GROUPED)
         assert_close(outs[-1][s:s + 1].to(torch.bfloat16), ref, orc.BF16, ATOL, f"seq {s}")
+
+
+@pytest.mark.parametrize("pt", [-1, 512])
+def test_decode_graph_replay_matches_eager(pt):
+    """Decode (single pass and split-K + reduce) captured in a HIP graph and
+    replayed three times with eager work between: every replay is bit-equal
+    to the eager launch."""
+    case = inputs.make_paged_case(inputs.SEEDS[2], 8, 32, 8, 128, 16,
+                                  [4096, 1000, 17, 1, 0, 2047, 3000, 511], orc.BF16)
+    q, k, v, bt, sl = _gpu_case(case)
+    max_ctx = int(case.seq_lens.max())
+    desc = tla.make_decode_desc(q, k, bt, case.num_kv_heads, case.scale, partition_tokens=pt)
+    ws = torch.empty(max(16, tla.workspace_bytes(desc, max_ctx)), dtype=torch.uint8, device="cuda")
+    out = torch.zeros_like(q)
+    print(f"case decode graph replay pt={pt}", flush=True)
+    tla.paged_attention_decode(desc, out, q, k, v, bt, sl, max_ctx, ws)
+    torch.cuda.synchronize()
+    eager = out.clone()
+    graph = torch.cuda.CUDAGraph()
+    cap = torch.cuda.Stream()
+    with torch.cuda.graph(graph, stream=cap):
+        tla.paged_attention_decode(desc, out, q, k, v, bt, sl, max_ctx, ws, cap)
+    for _ in range(3):
+        out.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
+        tla.paged_attention_decode(desc, out, q, k, v, bt, sl, max_ctx, ws)
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)

@@ -237,3 +237,49 @@ def test_kivi_decode_residual_zero_and_nan_slots():
         kc.k[last, :, :, L % 16 or 16:] = 0x7E00
     pages = kc.oracle_pages()
     assert_close(_run_decode(kc, pages, -1), _kivi_ref(kc, pages), orc.F16, ATOL_KIVI, "R=0")
+
+
+def test_kivi_step_graph_replay_matches_eager():
+    """One append + decode step captured in a HIP graph and replayed three
+    times, with eager work between replays: every replay matches the eager
+    step bit for bit (the append is idempotent: same token, same slot)."""
+    start = np.array([700, 159, 2000, 129], np.int32)
+    kc = KiviCase(57, start + 1, extra_blocks=1)
+    qd, kd, vd = dev(kc.q, orc.F16), dev(kc.k, orc.F16), dev(kc.v, orc.F16)
+    btd, ptd = dev(kc.tables), dev(kc.page_tables)
+    pages = torch.zeros(kc.num_pages, kc.n_kv, tla.KIVI_PAGE_BYTES, dtype=torch.uint8, device="cuda")
+    desc = kc.desc(qd, kd, btd, ptd)
+    tla.kivi_build_pages(desc, kd, vd, btd, dev(start), ptd, pages, int(start.max()))
+    lens = start + 1
+    pos = lens - 1
+    slots = dev((kc.tables[np.arange(kc.S), pos // 16] * 16 + pos % 16).astype(np.int32))
+    rng = np.random.default_rng(10)
+    knew = dev(inputs.encode(rng.standard_normal((kc.S, kc.n_kv, 128), dtype=np.float32), orc.F16), orc.F16)
+    vnew = dev(inputs.encode(rng.standard_normal((kc.S, kc.n_kv, 128), dtype=np.float32), orc.F16), orc.F16)
+    sld = dev(lens)
+    max_ctx = int(lens.max())
+    ws = torch.empty(max(16, tla.kivi_workspace_bytes(desc, max_ctx)), dtype=torch.uint8, device="cuda")
+    out = torch.zeros_like(qd)
+
+    def step(stream):
+        tla.kivi_append(desc, knew, vnew, kd, vd, slots, btd, sld, ptd, pages, stream)
+        tla.kivi_paged_attention_decode(desc, out, qd, pages, ptd, kd, vd, btd, sld, max_ctx, ws, stream)
+
+    print("case kivi graph replay", flush=True)
+    step(torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    eager, eager_pages = out.clone(), pages.clone()
+    graph = torch.cuda.CUDAGraph()
+    cap = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    with torch.cuda.graph(graph, stream=cap):
+        step(cap)
+    for _ in range(3):
+        out.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
+        assert torch.equal(pages, eager_pages)
+        step(torch.cuda.current_stream())            # eager work between replays
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
