@@ -225,6 +225,35 @@ int tl_kivi_paged_attention_decode(const tl_kivi_desc* desc, void* out, const vo
                                    int32_t max_context_len, void* workspace,
                                    size_t workspace_bytes, void* stream);
 
+/* ---- chunked prefill (causal) + decode rows in one launch ---------------
+ * No reference counterpart: the reference's prefill runs per token
+ * (cuda_engine.cpp:842-860) or densely in the megakernel
+ * (megakernel.cu:267-351).  Mixed batch: sequence s owns query rows
+ * cu_q_lens[s] .. cu_q_lens[s+1]-1 of q/out [total_q, H, 128]; its length
+ * after the chunk is seq_lens[s] (the chunk's own K/V already written to the
+ * pool with tl_reshape_and_cache); query i sits at position
+ * seq_lens[s] - q_len + i and attends causally to keys 0 .. that position.
+ * q_len == 1 rows are decode rows.  head_size 128, block_size 16 or 32,
+ * dtype F16 or BF16 for q, out and the pool.  max_q_len (host) bounds the
+ * grid. */
+typedef struct tl_prefill_desc {
+  int32_t num_seqs;
+  int32_t num_heads;
+  int32_t num_kv_heads;
+  int32_t head_size;           /* 128 */
+  int32_t block_size;          /* 16 or 32 */
+  int32_t max_blocks_per_seq;
+  int32_t num_blocks;
+  int32_t dtype;               /* TL_DTYPE_F16 or TL_DTYPE_BF16 */
+  int32_t gqa_map;
+  float scale;
+} tl_prefill_desc;
+
+int tl_chunked_prefill(const tl_prefill_desc* desc, void* out, const void* q,
+                       const int32_t* cu_q_lens, const void* k_cache, const void* v_cache,
+                       const int32_t* block_tables, const int32_t* seq_lens,
+                       int32_t total_q, int32_t max_q_len, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,161 @@
+"""Chunked prefill (+ decode rows in the same launch) on the GPU against the
+oracle's fp64 causal attention (oracle/tl_oracle.c orc_chunked_prefill).
+
+Tolerance: max-abs 2e-3 plus half an output ulp (fp16 weights enter the PV
+MFMA as one fp16 term, bf16 weights as a hi + lo pair of bf16 terms)."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import inputs
+import oracle_lib as orc
+import tl_attn as tla
+from gpu_util import assert_close, dev
+
+pytestmark = pytest.mark.gpu
+
+ATOL = 2e-3
+
+
+class PrefillCase:
+    """Sequences given as (q_len, seq_len) pairs over one shuffled pool."""
+
+    def __init__(self, seed, shape, H, n_kv, code, BS=16, holes=0, nan_unused=False):
+        self.q_lens = np.array([a for a, _ in shape], np.int32)
+        self.lens = np.array([b for _, b in shape], np.int32)
+        assert (self.q_lens <= self.lens).all()
+        S = len(shape)
+        self.case = inputs.make_paged_case(seed, S, H, n_kv, 128, BS, self.lens, code, holes=holes)
+        if nan_unused:
+            nan = 0x7FC0 if code == orc.BF16 else 0x7E00
+            for s, L in enumerate(self.lens):
+                if L % BS:
+                    last = self.case.tables[s, (L - 1) // BS]
+                    if last >= 0:
+                        self.case.k_cache[last, :, :, L % BS:] = nan
+                        self.case.v_cache[last, :, :, L % BS:] = nan
+        self.cu = np.concatenate([[0], np.cumsum(self.q_lens)]).astype(np.int32)
+        rng = np.random.default_rng(seed + 7)
+        self.q = inputs.encode(rng.standard_normal((int(self.cu[-1]), H, 128), dtype=np.float32), code)
+        self.code, self.H, self.n_kv, self.S = code, H, n_kv, S
+
+    def run(self, gqa=tla.GQA_GROUPED):
+        c = self.case
+        q = dev(self.q, self.code)
+        k, v = dev(c.k_cache, self.code), dev(c.v_cache, self.code)
+        bt, sl, cu = dev(c.tables), dev(self.lens), dev(self.cu)
+        out = torch.full_like(q, float("nan"))
+        desc = tla.make_prefill_desc(q, k, bt, self.S, self.n_kv, c.scale, gqa_map=gqa)
+        tla.chunked_prefill(desc, out, q, cu, k, v, bt, sl, int(self.q_lens.max()))
+        torch.cuda.synchronize()
+        return out
+
+    def ref(self, gqa=orc.GROUPED):
+        c = self.case
+        return orc.chunked_prefill(self.q, self.code, self.cu, c.k_cache, c.v_cache, self.code, c.tables,
+                                   self.lens, self.n_kv, c.scale, gqa)
+
+
+MIXED = [(96, 96), (130, 400), (1, 700), (33, 33), (2, 50), (1, 1), (257, 300), (1, 129)]
+
+
+@pytest.mark.parametrize("code", [orc.BF16, orc.F16])
+@pytest.mark.parametrize("gqa", [tla.GQA_GROUPED, tla.GQA_MODULO])
+def test_mixed_batch_matches_oracle(code, gqa):
+    pc = PrefillCase(inputs.SEEDS[4], MIXED, 16, 4, code)
+    print(f"case prefill mixed code={code} gqa={gqa}", flush=True)
+    assert_close(pc.run(gqa), pc.ref(gqa), code, ATOL, "mixed")
+
+
+@pytest.mark.parametrize("H,n_kv", [(16, 2), (4, 4), (12, 4)])
+def test_group_sizes(H, n_kv):
+    pc = PrefillCase(inputs.SEEDS[4] + 1, [(70, 200), (1, 333), (40, 40)], H, n_kv, orc.BF16)
+    print(f"case prefill H={H} n_kv={n_kv}", flush=True)
+    assert_close(pc.run(), pc.ref(), orc.BF16, ATOL, f"H={H}")
+
+
+def test_block_size_32_holes_and_nan_unused_slots():
+    pc = PrefillCase(inputs.SEEDS[4] + 2, [(50, 300), (1, 250), (17, 77)], 16, 4, orc.F16, BS=32, holes=3,
+                     nan_unused=True)
+    print("case prefill bs32 holes nan", flush=True)
+    assert_close(pc.run(), pc.ref(), orc.F16, ATOL, "bs32")
+
+
+def test_nan_in_unused_slots_bs16():
+    pc = PrefillCase(inputs.SEEDS[4] + 3, [(45, 45), (1, 90), (20, 100)], 8, 2, orc.BF16, nan_unused=True)
+    print("case prefill nan bs16", flush=True)
+    assert_close(pc.run(), pc.ref(), orc.BF16, ATOL, "nan")
+
+
+def test_chunked_equals_whole_prompt():
+    """A 256-token prompt as one chunk and as four 64-token chunks (each chunk
+    sees the previous ones through the pool) gives the same rows."""
+    whole = PrefillCase(inputs.SEEDS[4] + 4, [(256, 256)], 16, 2, orc.BF16)
+    out_whole = whole.run()
+    c = whole.case
+    k, v = dev(c.k_cache, orc.BF16), dev(c.v_cache, orc.BF16)
+    bt = dev(c.tables)
+    parts = []
+    for i in range(4):
+        q = dev(np.ascontiguousarray(whole.q[64 * i: 64 * (i + 1)]), orc.BF16)
+        out = torch.full_like(q, float("nan"))
+        desc = tla.make_prefill_desc(q, k, bt, 1, 2, c.scale)
+        tla.chunked_prefill(desc, out, q, dev(np.array([0, 64], np.int32)), k, v, bt,
+                            dev(np.array([64 * (i + 1)], np.int32)), 64)
+        parts.append(out)
+    torch.cuda.synchronize()
+    chunked = torch.cat(parts)
+    assert torch.equal(chunked.view(torch.int16), out_whole.view(torch.int16))
+
+
+def test_decode_rows_match_decode_kernel():
+    """q_len == 1 rows of the prefill launch agree with the decode entry point
+    (same wavefront code, tokens split over 4 instead of 8 wavefronts)."""
+    pc = PrefillCase(inputs.SEEDS[4] + 5, [(1, 1000), (1, 4096), (1, 17)], 32, 8, orc.BF16)
+    got = pc.run()
+    c = pc.case
+    q = dev(pc.q, orc.BF16)
+    k, v, bt, sl = dev(c.k_cache, orc.BF16), dev(c.v_cache, orc.BF16), dev(c.tables), dev(pc.lens)
+    desc = tla.make_decode_desc(q, k, bt, 8, c.scale, partition_tokens=-1)
+    out = torch.full_like(q, float("nan"))
+    tla.paged_attention_decode(desc, out, q, k, v, bt, sl, int(pc.lens.max()), None)
+    torch.cuda.synchronize()
+    assert (got.float() - out.float()).abs().max().item() <= 2 * ATOL
+    assert_close(got, pc.ref(), orc.BF16, ATOL, "decode rows")
+
+
+def test_config5_shape_spot_checks():
+    """H=64, n_kv=8, bf16: two 512-row chunks (prefixes 0 and 1536) plus 8
+    decode rows at 2048 in one launch; decode rows and the last 4 queries of
+    each chunk against the oracle."""
+    shape = [(512, 512), (512, 2048)] + [(1, 2048)] * 8
+    pc = PrefillCase(inputs.SEEDS[4] + 6, shape, 64, 8, orc.BF16)
+    got = pc.run().float().cpu().numpy()
+    c = pc.case
+    for s in range(len(shape)):
+        ql, L = int(pc.q_lens[s]), int(pc.lens[s])
+        take = min(ql, 4)
+        rows = slice(int(pc.cu[s]) + ql - take, int(pc.cu[s + 1]))
+        qs = np.ascontiguousarray(pc.q[rows])
+        ref = orc.chunked_prefill(qs, orc.BF16, np.array([0, take], np.int32), c.k_cache, c.v_cache, orc.BF16,
+                                  np.ascontiguousarray(c.tables[s:s + 1]), np.array([L], np.int32), 8, c.scale)
+        g = torch.from_numpy(got[rows]).to(torch.bfloat16)
+        assert_close(g, ref, orc.BF16, ATOL, f"seq {s}")
+
+
+def test_empty_and_invalid_arguments():
+    q = torch.zeros(4, 8, 128, dtype=torch.bfloat16, device="cuda")
+    k = torch.zeros(4, 2, 128, 16, dtype=torch.bfloat16, device="cuda")
+    bt = torch.zeros(1, 4, dtype=torch.int32, device="cuda")
+    desc = tla.make_prefill_desc(q, k, bt, 1, 2, 0.1)
+    cu = torch.tensor([0, 0], dtype=torch.int32, device="cuda")
+    sl = torch.tensor([0], dtype=torch.int32, device="cuda")
+    out = torch.zeros_like(q)
+    tla.chunked_prefill(desc, out, q[:0], cu, k, k, bt, sl, 0)          # nothing to do
+    bad = tla.make_prefill_desc(q, k, bt, 1, 2, 0.1)
+    bad.head_size = 64
+    with pytest.raises(tla.TLError) as e:
+        tla.chunked_prefill(bad, out, q, cu, k, k, bt, sl, 4)
+    assert e.value.code == tla.ERR_NOT_IMPLEMENTED

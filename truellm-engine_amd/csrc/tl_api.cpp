@@ -467,4 +467,44 @@ int tl_kivi_paged_attention_decode(const tl_kivi_desc* desc, void* out, const vo
   return ok();
 }
 
+int tl_chunked_prefill(const tl_prefill_desc* d, void* out, const void* q, const int32_t* cu_q_lens,
+                       const void* k_cache, const void* v_cache, const int32_t* block_tables,
+                       const int32_t* seq_lens, int32_t total_q, int32_t max_q_len, void* stream) {
+  if (!d) return fail(TL_ERR_INVALID_ARGUMENT, "desc is NULL");
+  if (d->num_seqs < 0 || total_q < 0 || max_q_len < 0)
+    return fail(TL_ERR_INVALID_ARGUMENT, "num_seqs=%d total_q=%d max_q_len=%d must be >= 0",
+                d->num_seqs, total_q, max_q_len);
+  if (d->num_kv_heads <= 0 || d->num_heads <= 0 || d->num_heads % d->num_kv_heads)
+    return fail(TL_ERR_INVALID_ARGUMENT, "num_heads=%d must be a positive multiple of num_kv_heads=%d",
+                d->num_heads, d->num_kv_heads);
+  if (d->max_blocks_per_seq <= 0 || d->num_blocks <= 0)
+    return fail(TL_ERR_INVALID_ARGUMENT, "max_blocks_per_seq=%d and num_blocks=%d must be > 0",
+                d->max_blocks_per_seq, d->num_blocks);
+  if (d->gqa_map != TL_GQA_MODULO && d->gqa_map != TL_GQA_GROUPED)
+    return fail(TL_ERR_INVALID_ARGUMENT, "gqa_map=%d", d->gqa_map);
+  if (d->dtype != TL_DTYPE_F16 && d->dtype != TL_DTYPE_BF16)
+    return fail(TL_ERR_NOT_IMPLEMENTED, "prefill dtype=%d (built: F16, BF16)", d->dtype);
+  if (d->head_size != 128 || (d->block_size != 16 && d->block_size != 32))
+    return fail(TL_ERR_NOT_IMPLEMENTED, "prefill head_size=%d block_size=%d (built: 128 x 16/32)",
+                d->head_size, d->block_size);
+  if (d->num_seqs == 0 || total_q == 0) return ok();
+  if (max_q_len > total_q)
+    return fail(TL_ERR_INVALID_ARGUMENT, "max_q_len=%d > total_q=%d", max_q_len, total_q);
+  if (!out || !q || !cu_q_lens || !k_cache || !v_cache || !block_tables || !seq_lens)
+    return fail(TL_ERR_INVALID_ARGUMENT, "NULL pointer");
+  if (!aligned16(q) || !aligned16(k_cache) || !aligned16(v_cache))
+    return fail(TL_ERR_INVALID_ARGUMENT, "q and the pools must be 16-byte aligned");
+  tl::PrefillLaunch a;
+  memset(&a, 0, sizeof a);
+  a.out = out; a.q = q; a.cu_q_lens = cu_q_lens; a.k_cache = k_cache; a.v_cache = v_cache;
+  a.block_tables = block_tables; a.seq_lens = seq_lens;
+  a.num_seqs = d->num_seqs; a.num_heads = d->num_heads; a.num_kv_heads = d->num_kv_heads;
+  a.block_size = d->block_size; a.max_blocks_per_seq = d->max_blocks_per_seq; a.num_blocks = d->num_blocks;
+  a.dtype = d->dtype;   // TL_DTYPE_F16 / TL_DTYPE_BF16 share the kernels' Kind codes
+  a.gqa_map = d->gqa_map; a.max_q_len = max_q_len; a.scale = d->scale;
+  a.stream = (hipStream_t)stream;
+  if (tl::launch_prefill(a)) return fail(TL_ERR_BACKEND, "prefill launch failed");
+  return ok();
+}
+
 }  // extern "C"

@@ -98,6 +98,21 @@ struct KiviDecodeLaunch {
 };
 int launch_kivi_decode(const KiviDecodeLaunch& a);
 
+struct PrefillLaunch {
+  void* out;                    // [total_q, H, 128], dtype
+  const void* q;                // [total_q, H, 128], dtype
+  const int32_t* cu_q_lens;     // [num_seqs + 1]
+  const void* k_cache;          // [N, n_kv, 128, bs], dtype
+  const void* v_cache;
+  const int32_t* block_tables;
+  const int32_t* seq_lens;
+  int num_seqs, num_heads, num_kv_heads, block_size, max_blocks_per_seq, num_blocks;
+  int dtype, gqa_map, max_q_len;
+  float scale;
+  hipStream_t stream;
+};
+int launch_prefill(const PrefillLaunch& a);
+
 // absmax(x)/448 into *scale_out (1 when absmax is 0).
 int launch_fp8_scale(const void* x, int dtype, int64_t n, float* scale_out,
                      hipStream_t stream);

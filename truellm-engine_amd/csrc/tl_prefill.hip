@@ -1,0 +1,383 @@
+// tl_prefill.hip -- chunked-prefill paged attention on MFMA (gfx950).
+//
+// One launch serves a mixed batch: sequences with q_len > 1 are prefill
+// chunks (causal: query i of a chunk sits at position L - q_len + i and sees
+// keys 0 .. that position, its own chunk included, all read from the paged
+// pool), sequences with q_len == 1 are decode rows.
+//
+// Prefill work item: one workgroup per (sequence, kv head, tile of NW * 32
+// rows), a row being one (query, q head of the GQA group) pair, so every K/V
+// block fetched serves all q heads of the group.  Per 32-key iteration:
+//   * the workgroup copies the keys' K (transposed to [key][channel], rows
+//     padded to 136 halves) and V ([block][channel][slot], as in the pool)
+//     into a double-buffered LDS stage;
+//   * each wavefront (32 rows) forms S^T = K Q^T with
+//     v_mfma_f32_32x32x16_{bf16,f16}: A = K (rows: keys, k: channels) read
+//     from LDS, B = Q^T held in registers for the whole launch.  Lane l then
+//     holds 16 keys of row l % 32, so the row max needs one permlane32 swap;
+//   * online softmax with lazy rescaling: the running max is only raised
+//     when a row's new max exceeds it by more than 8 (log2 units), so the
+//     weights stay below 2^8 and the O accumulators are rescaled rarely;
+//   * O += P V on the same MFMA: the weights leave the S^T accumulator as
+//     keys {16 st + 4 g + i, 16 st + 8 + 4 g + i} for lane group g, which is
+//     used as the k order of step st; V is read from LDS in that order.
+// Decode rows run the 2-byte decode wavefront (tl_decode_wave.hpp), one
+// workgroup per (sequence, kv head, head slice).
+//
+// Nearest reference analogues: the per-token prefill of cuda_engine.cpp:842-860
+// and the dense attention of megakernel.cu:267-351; the reference has no
+// chunked prefill over the paged pool.
+#include "tl_decode_wave.hpp"
+#include "tl_device.hpp"
+#include "tl_internal.hpp"
+
+namespace tl {
+
+namespace {
+
+typedef float f16v __attribute__((ext_vector_type(16)));
+typedef unsigned u4v __attribute__((ext_vector_type(4)));
+
+constexpr int kPfHead = 128;
+constexpr int kPfRows = 32;          // rows per wavefront
+constexpr int kPfKeys = 32;          // keys per iteration
+constexpr int kKtStride = 136;       // halves per key row of the transposed K stage
+constexpr float kLazyRescale = 8.f;  // log2 units
+
+template <Kind KV> struct Mfma32;
+// bf16 keeps 8 mantissa bits: the weights go to the PV product as two bf16
+// terms (hi = bf16(p), lo = bf16(p - hi)), fp16 weights (11 bits) as one.
+template <> struct Mfma32<Kind::BF16> {
+  static constexpr bool kSplitP = true;
+  typedef __bf16 v8 __attribute__((ext_vector_type(8)));
+  typedef __bf16 v2 __attribute__((ext_vector_type(2)));
+  __device__ __forceinline__ static float hi(float x) { return (float)(__bf16)x; }
+  __device__ __forceinline__ static f16v mma(const u32x4& a, const u32x4& b, const f16v& c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8, a), __builtin_bit_cast(v8, b), c,
+                                                   0, 0, 0);
+  }
+  __device__ __forceinline__ static uint32_t pack(float x, float y) {
+    const v2 v = {(__bf16)x, (__bf16)y};
+    return __builtin_bit_cast(uint32_t, v);
+  }
+};
+template <> struct Mfma32<Kind::F16> {
+  static constexpr bool kSplitP = false;
+  typedef _Float16 v8 __attribute__((ext_vector_type(8)));
+  typedef _Float16 v2 __attribute__((ext_vector_type(2)));
+  __device__ __forceinline__ static float hi(float x) { return (float)(_Float16)x; }
+  __device__ __forceinline__ static f16v mma(const u32x4& a, const u32x4& b, const f16v& c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8, a), __builtin_bit_cast(v8, b), c,
+                                                  0, 0, 0);
+  }
+  __device__ __forceinline__ static uint32_t pack(float x, float y) {
+    const v2 v = {(_Float16)x, (_Float16)y};
+    return __builtin_bit_cast(uint32_t, v);
+  }
+};
+
+struct PrefillParams {
+  Params base;                 // q, out, pools, tables, seq_lens, heads, group, qk_scale
+  const int32_t* cu_q_lens;    // [num_seqs + 1]
+  int num_seqs, row_tiles;
+};
+
+template <int NW, int BS>
+struct PrefillSmem {
+  union {
+    struct {
+      uint16_t kt[2][kPfKeys * kKtStride];        // [key][channel] (+8 pad)
+      uint16_t v[2][kPfHead * kPfKeys];           // [block][channel][slot]
+      float row[NW][kPfRows];                     // per-row exchange (alpha, l)
+    } pf;
+    struct {
+      uint32_t p[NW][4][kWaveHeads][4];
+      float m[NW][kWaveHeads], l[NW][kWaveHeads];
+      float acc[NW][kWaveHeads][kPfHead];
+    } dc;
+  };
+};
+
+// Physical block of block index lb of a table row, or -1.
+__device__ __forceinline__ int block_of(const Params& p, const int32_t* table, int lb) {
+  if (lb >= p.max_blocks_per_seq) return -1;
+  const int b = table[lb];
+  return (b < 0 || b >= p.num_blocks) ? -1 : b;
+}
+
+template <Kind KV, int BS, int NW>
+__global__ __launch_bounds__(NW * kWave) void prefill_kernel(PrefillParams pp) {
+  static_assert(BS == 16 || BS == 32, "block size");
+  constexpr int BPI = kPfKeys / BS;                    // pool blocks per iteration
+  constexpr int CPB = kPfHead * BS / 8;                // 16-byte chunks per block (K or V)
+  constexpr int CHUNKS = BPI * CPB;                    // per tensor per iteration (512)
+  constexpr int NT = NW * kWave;
+  static_assert(CHUNKS % NT == 0, "whole chunks per thread");
+  constexpr int CPT = CHUNKS / NT;                     // K (and V) chunks per thread
+  using M = Mfma32<KV>;
+  __shared__ __attribute__((aligned(16))) PrefillSmem<NW, BS> sm;
+
+  const Params& p = pp.base;
+  const int tid = threadIdx.x, lane = tid % kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int g = lane >> 5, c32 = lane & 31;
+
+  int b = blockIdx.x;
+  const int items = pp.num_seqs * p.num_kv_heads;
+  const int tile = pp.row_tiles - 1 - b / items;       // longest (latest) tiles first
+  b %= items;
+  const int seq = b / p.num_kv_heads, kvh = b % p.num_kv_heads;
+  const int q0 = pp.cu_q_lens[seq], ql = pp.cu_q_lens[seq + 1] - q0;
+  const int L = p.seq_lens[seq];
+  if (ql <= 0) return;
+
+  if (ql == 1) {
+    // ---- decode row: the 2-byte decode wavefront over one head slice ----
+    if (tile >= p.head_slices) return;
+    Params pd = p;
+    const int64_t shift = (int64_t)(q0 - seq) * p.num_heads * kPfHead * 2;   // q / out row q0
+    pd.q = (const char*)p.q + shift;
+    pd.out = (char*)p.out + shift;
+    decode2_wave<KV, kPfHead, BS>(pd, seq, kvh, tile, wave * 32, L, NW * 32, &sm.dc.p[wave][0][0][0],
+                                  &sm.dc.acc[wave][0][0], &sm.dc.m[wave][0], &sm.dc.l[wave][0]);
+    __syncthreads();
+    combine_waves<KV, Kind::F32, kPfHead, true>(pd, NW, &sm.dc.m[0][0], &sm.dc.l[0][0],
+                                                &sm.dc.acc[0][0][0], seq, kvh, tile, 0, tid, NT);
+    return;
+  }
+
+  // ---- prefill tile ----
+  const int rows = ql * p.group;
+  const int row0 = tile * NW * kPfRows;
+  if (row0 >= rows) return;
+  const int wrow0 = row0 + wave * kPfRows;
+  const int my_row = wrow0 + c32;
+  const bool row_ok = my_row < rows;
+  const int qi = row_ok ? my_row / p.group : 0, gi = row_ok ? my_row % p.group : 0;
+  const int pos = row_ok ? L - ql + qi : -1;           // keys 0 .. pos
+  const int last_row = min(rows, row0 + NW * kPfRows) - 1;
+  const int kend = max(0, L - ql + last_row / p.group + 1);           // keys of the workgroup
+  const int wlast = min(rows, wrow0 + kPfRows) - 1;
+  const int wkend = wrow0 < rows ? max(0, L - ql + wlast / p.group + 1) : 0;
+  const int n_it = (kend + kPfKeys - 1) / kPfKeys;
+
+  // B operand of S^T: row my_row, channels 16 ks + 8 g .. +7 (zero for padding rows)
+  u32x4 qb[8];
+  {
+    const uint16_t* qrow = (const uint16_t*)p.q +
+        ((int64_t)(q0 + qi) * p.num_heads + head_of(p, kvh, gi)) * kPfHead + 8 * g;
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) qb[ks] = row_ok ? load16(qrow + 16 * ks) : u32x4{0u, 0u, 0u, 0u};
+  }
+
+  const int32_t* table = p.block_tables + (int64_t)seq * p.max_blocks_per_seq;
+  const int64_t head_stride = (int64_t)kPfHead * BS;                  // elements per (block, kv head)
+  const uint16_t* kpool = (const uint16_t*)p.k_cache;
+  const uint16_t* vpool = (const uint16_t*)p.v_cache;
+
+  // this thread's chunks: chunk ci = tid + NT * j -> block ci / CPB, channel
+  // (ci % CPB) / (BS / 8), slots 8 * (ci % (BS / 8)) .. +7
+  u32x4 kr[CPT], vr[CPT];
+  auto fetch = [&](int it) {
+#pragma unroll
+    for (int j = 0; j < CPT; ++j) {
+      const int ci = tid + NT * j;
+      const int blk = ci / CPB, ch = (ci % CPB) / (BS / 8), s8 = 8 * (ci % (BS / 8));
+      const int key0 = it * kPfKeys + blk * BS + s8;
+      const int pb = key0 < kend ? block_of(p, table, it * BPI + blk) : -1;
+      if (pb >= 0) {
+        const int64_t off = ((int64_t)pb * p.num_kv_heads + kvh) * head_stride + (int64_t)ch * BS + s8;
+        kr[j] = load16_stream(kpool + off);
+        u4v v = __builtin_bit_cast(u4v, load16_stream(vpool + off));
+        // slots at or past the sequence end may hold anything: zero their V
+        if (key0 + 8 > L) {
+#pragma unroll
+          for (int w = 0; w < 4; ++w)
+            if (key0 + 2 * w >= L) v[w] = 0u;
+            else if (key0 + 2 * w + 1 >= L) v[w] &= 0xFFFFu;
+        }
+        vr[j] = __builtin_bit_cast(u32x4, v);
+      } else {
+        kr[j] = u32x4{0u, 0u, 0u, 0u};
+        vr[j] = u32x4{0u, 0u, 0u, 0u};
+      }
+    }
+  };
+  auto stage = [&](int st) {
+#pragma unroll
+    for (int j = 0; j < CPT; ++j) {
+      const int ci = tid + NT * j;
+      const int blk = ci / CPB, ch = (ci % CPB) / (BS / 8), s8 = 8 * (ci % (BS / 8));
+      uint16_t* kt = &sm.pf.kt[st][(blk * BS + s8) * kKtStride + ch];
+      const u4v kv = __builtin_bit_cast(u4v, kr[j]);
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        kt[(2 * w) * kKtStride] = (uint16_t)(kv[w] & 0xFFFFu);
+        kt[(2 * w + 1) * kKtStride] = (uint16_t)(kv[w] >> 16);
+      }
+      *reinterpret_cast<u32x4*>(&sm.pf.v[st][(blk * kPfHead + ch) * BS + s8]) = vr[j];
+    }
+  };
+
+  f16v o[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) o[c] = f16v{};
+  float m_used = -INFINITY, l_part = 0.f;
+  float* s_row = &sm.pf.row[wave][0];
+
+  if (n_it > 0) {
+    fetch(0);
+    stage(0);
+  }
+  __syncthreads();
+#pragma unroll 1
+  for (int it = 0; it < n_it; ++it) {
+    const int st = it & 1;
+    if (it + 1 < n_it) fetch(it + 1);
+    const int k0 = it * kPfKeys;
+    if (k0 < wkend) {
+      // ---- S^T = K Q^T (lane: keys 8 j + 4 g + i of row my_row) ----
+      f16v s = f16v{};
+      const uint16_t* ktw = &sm.pf.kt[st][c32 * kKtStride + 8 * g];
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks)
+        s = M::mma(*reinterpret_cast<const u32x4*>(ktw + 16 * ks), qb[ks], s);
+      // ---- mask, row max, lazy rescale ----
+      float sc[16];
+      float mx = -INFINITY;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int kk = 8 * (r >> 2) + 4 * g + (r & 3);
+        const int key = k0 + kk;
+        const bool ok = key <= pos && block_of(p, table, (k0 + kk) / BS) >= 0;
+        sc[r] = ok ? s[r] * p.qk_scale : -INFINITY;
+        mx = fmaxf(mx, sc[r]);
+      }
+      {
+        const auto sw = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, mx),
+                                                         __builtin_bit_cast(unsigned, mx), false, false);
+        mx = fmaxf(__builtin_bit_cast(float, (unsigned)sw[0]), __builtin_bit_cast(float, (unsigned)sw[1]));
+      }
+      const bool raise = mx > m_used + kLazyRescale || (m_used == -INFINITY && mx != -INFINITY);
+      if (__builtin_amdgcn_ballot_w64(raise)) {
+        const float m_new = raise ? mx : m_used;
+        const float alpha = (m_new == m_used) ? 1.f : (m_used == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_used - m_new));
+        m_used = m_new;
+        l_part *= alpha;
+        if (g == 0) s_row[c32] = alpha;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        // O rows of this lane: 8 j + 4 g + i
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float4 a4 = *reinterpret_cast<const float4*>(&s_row[8 * j + 4 * g]);
+          const float a[4] = {a4.x, a4.y, a4.z, a4.w};
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) o[c][4 * j + i] *= a[i];
+        }
+        __builtin_amdgcn_wave_barrier();
+      }
+      const float m_use = (m_used == -INFINITY) ? 0.f : m_used;
+      float pw[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        pw[r] = __builtin_amdgcn_exp2f(sc[r] - m_use);
+        l_part += pw[r];
+      }
+      // ---- O += P V, step st2 = keys {16 st2 + 4 g + i, 16 st2 + 8 + 4 g + i} ----
+#pragma unroll
+      for (int st2 = 0; st2 < 2; ++st2) {
+        const int r0 = 8 * st2;
+        const u32x4 pa = {M::pack(pw[r0 + 0], pw[r0 + 1]), M::pack(pw[r0 + 2], pw[r0 + 3]),
+                          M::pack(pw[r0 + 4], pw[r0 + 5]), M::pack(pw[r0 + 6], pw[r0 + 7])};
+        u32x4 pl = {0u, 0u, 0u, 0u};
+        if constexpr (M::kSplitP) {
+          float lo[8];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) lo[i] = pw[r0 + i] - M::hi(pw[r0 + i]);
+          pl = u32x4{M::pack(lo[0], lo[1]), M::pack(lo[2], lo[3]), M::pack(lo[4], lo[5]), M::pack(lo[6], lo[7])};
+        }
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const int ch = 32 * c + c32;
+          const int ka = 16 * st2 + 4 * g;                 // first key of the step's slots 0-3
+          const uint16_t* vrow = &sm.pf.v[st][((ka / BS) * kPfHead + ch) * BS + (ka % BS)];
+          const uint2 lo = *reinterpret_cast<const uint2*>(vrow);
+          const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 8);
+          const u32x4 vb = {lo.x, lo.y, hi.x, hi.y};
+          o[c] = M::mma(pa, vb, o[c]);
+          if constexpr (M::kSplitP) o[c] = M::mma(pl, vb, o[c]);
+        }
+      }
+    }
+    if (it + 1 < n_it) stage(st ^ 1);
+    __syncthreads();
+  }
+
+  // ---- normalise and store: lane holds rows 8 j + 4 g + i, channels 32 c + c32 ----
+  {
+    const auto sw = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, l_part),
+                                                     __builtin_bit_cast(unsigned, l_part), false, false);
+    const float l = __builtin_bit_cast(float, (unsigned)sw[0]) + __builtin_bit_cast(float, (unsigned)sw[1]);
+    if (g == 0) s_row[c32] = l;
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int rl = 8 * j + 4 * g + i, row = wrow0 + rl;
+      if (row >= rows) continue;
+      const float l = s_row[rl];
+      const float inv = l > 0.f ? 1.f / l : 0.f;
+      const int qr = row / p.group, gr = row % p.group;
+      const int64_t base = ((int64_t)(q0 + qr) * p.num_heads + head_of(p, kvh, gr)) * kPfHead;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) store_scalar<KV>(p.out, base + 32 * c + c32, o[c][4 * j + i] * inv);
+    }
+  }
+}
+
+template <Kind KV, int BS>
+int launch_prefill_t(const PrefillParams& pp, unsigned grid, hipStream_t stream) {
+  constexpr int NW = 4;
+  hipLaunchKernelGGL((prefill_kernel<KV, BS, NW>), dim3(grid), dim3(NW * kWave), 0, stream, pp);
+  return hipGetLastError() == hipSuccess ? 0 : 5;
+}
+
+}  // namespace
+
+int launch_prefill(const PrefillLaunch& a) {
+  constexpr int NW = 4;
+  PrefillParams pp;
+  Params& p = pp.base;
+  p.out = a.out; p.q = a.q;
+  p.k_cache = (const char*)a.k_cache; p.v_cache = (const char*)a.v_cache;
+  p.block_tables = a.block_tables; p.seq_lens = a.seq_lens;
+  p.part_m = nullptr; p.part_l = nullptr; p.part_o = nullptr;
+  p.num_heads = a.num_heads; p.num_kv_heads = a.num_kv_heads;
+  p.max_blocks_per_seq = a.max_blocks_per_seq; p.num_blocks = a.num_blocks;
+  p.num_partitions = 1; p.partition_tokens = 0;
+  p.group = a.num_heads / a.num_kv_heads;
+  p.head_slices = (p.group + kWaveHeads - 1) / kWaveHeads;
+  p.gqa_map = a.gqa_map;
+  p.qk_scale = a.scale * kLog2e;
+  p.v_scale = 1.f;
+  pp.cu_q_lens = a.cu_q_lens;
+  pp.num_seqs = a.num_seqs;
+  const int row_tiles_pf = (a.max_q_len * p.group + NW * kPfRows - 1) / (NW * kPfRows);
+  pp.row_tiles = max(row_tiles_pf, p.head_slices);
+  const unsigned grid = (unsigned)(pp.row_tiles * a.num_seqs * a.num_kv_heads);
+  if (grid == 0) return 0;
+  const bool bf16 = a.dtype == (int)Kind::BF16;
+  if (a.block_size == 16)
+    return bf16 ? launch_prefill_t<Kind::BF16, 16>(pp, grid, a.stream) : launch_prefill_t<Kind::F16, 16>(pp, grid, a.stream);
+  return bf16 ? launch_prefill_t<Kind::BF16, 32>(pp, grid, a.stream) : launch_prefill_t<Kind::F16, 32>(pp, grid, a.stream);
+}
+
+}  // namespace tl

@@ -79,6 +79,21 @@ class KiviDesc(ctypes.Structure):
 KIVI_PAGE_TOKENS = 32
 KIVI_PAGE_BYTES = 5120
 
+
+class PrefillDesc(ctypes.Structure):
+    _fields_ = [
+        ("num_seqs", ctypes.c_int32),
+        ("num_heads", ctypes.c_int32),
+        ("num_kv_heads", ctypes.c_int32),
+        ("head_size", ctypes.c_int32),
+        ("block_size", ctypes.c_int32),
+        ("max_blocks_per_seq", ctypes.c_int32),
+        ("num_blocks", ctypes.c_int32),
+        ("dtype", ctypes.c_int32),
+        ("gqa_map", ctypes.c_int32),
+        ("scale", ctypes.c_float),
+    ]
+
 _P = ctypes.c_void_p
 _I = ctypes.c_int32
 _F = ctypes.c_float
@@ -100,6 +115,7 @@ _SIG = {
     "tl_kivi_build_pages": (ctypes.c_int, [ctypes.POINTER(KiviDesc), _P, _P, _P, _P, _P, _P, _I, _P]),
     "tl_kivi_append": (ctypes.c_int, [ctypes.POINTER(KiviDesc), _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
     "tl_kivi_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(KiviDesc), _I]),
+    "tl_chunked_prefill": (ctypes.c_int, [ctypes.POINTER(PrefillDesc), _P, _P, _P, _P, _P, _P, _P, _I, _I, _P]),
     "tl_kivi_paged_attention_decode": (ctypes.c_int, [ctypes.POINTER(KiviDesc), _P, _P, _P, _P, _P, _P, _P, _P, _I, _P, ctypes.c_size_t, _P]),
 }
 
@@ -339,3 +355,29 @@ def kivi_paged_attention_decode(desc, out, q, pages, page_tables, k_cache, v_cac
         ctypes.byref(desc), _ptr(out), _ptr(q), _ptr(pages), _ptr(page_tables), _ptr(k_cache),
         _ptr(v_cache), _ptr(block_tables), _ptr(seq_lens), max_context_len, _ptr(workspace),
         ws_bytes, _stream(stream)))
+
+
+# ---------------------------------------------------------------------------
+# chunked prefill + decode rows (no reference counterpart)
+# ---------------------------------------------------------------------------
+
+def make_prefill_desc(q, k_cache, block_tables, num_seqs, num_kv_heads, scale, *,
+                      gqa_map=GQA_GROUPED):
+    """q [total_q, H, 128]; k_cache [N, n_kv, 128, bs]; block_tables [S, max_blocks]."""
+    d = PrefillDesc()
+    d.num_seqs, d.num_heads, d.num_kv_heads, d.head_size = num_seqs, q.shape[1], num_kv_heads, q.shape[2]
+    d.block_size = k_cache.shape[3]
+    d.max_blocks_per_seq, d.num_blocks = block_tables.shape[1], k_cache.shape[0]
+    d.dtype = dtype_code(q)
+    d.gqa_map = gqa_map
+    d.scale = scale
+    return d
+
+
+def chunked_prefill(desc, out, q, cu_q_lens, k_cache, v_cache, block_tables, seq_lens, max_q_len,
+                    stream=None):
+    """Causal attention of each sequence's query rows (cu_q_lens) against its
+    paged keys 0 .. seq_lens[s] - q_len + i; q_len == 1 rows are decode rows."""
+    check(lib.tl_chunked_prefill(ctypes.byref(desc), _ptr(out), _ptr(q), _ptr(cu_q_lens),
+                                 _ptr(k_cache), _ptr(v_cache), _ptr(block_tables), _ptr(seq_lens),
+                                 q.shape[0], max_q_len, _stream(stream)))
