@@ -23,6 +23,7 @@ steps; roofline = the same bytes over the decode launch's average duration
 multithreaded fp32 decode on the host cores over a bounded sample.
 """
 import argparse
+import itertools
 import json
 import math
 import os
@@ -72,7 +73,7 @@ def parse():
     p.add_argument("--partition-tokens", type=int, default=0)
     p.add_argument("--cpu-seconds", type=float, default=15.0)
     p.add_argument("--no-cpu", action="store_true")
-    p.add_argument("--only", default="all", choices=["all", "bf16", "fp16", "kivi"])
+    p.add_argument("--only", default="all", choices=["all", "bf16", "fp16", "kivi", "prefill"])
     return p.parse_args()
 
 
@@ -213,6 +214,61 @@ def bench_kivi(args, R=128):
             "bytes_per_step": avg_bytes, "residual_length": R, "group": 32}
 
 
+PF_H, PF_NKV, PF_SEQS, PF_PROMPT, PF_CHUNK, PF_DEC, PF_DEC_L = 64, 8, 8, 2048, 512, 32, 2048
+
+
+def prefill_flops():
+    """4 d multiply-add FLOPs per unmasked (query, key) pair, QK^T plus PV,
+    over the 4 causal chunks of every prompt and every q head."""
+    per_head = 0
+    for c in range(PF_PROMPT // PF_CHUNK):
+        per_head += 4 * D * (PF_CHUNK * PF_CHUNK * c + PF_CHUNK * (PF_CHUNK + 1) // 2)
+    return per_head * PF_H * PF_SEQS
+
+
+def bench_prefill(args):
+    """Chunked prefill, Llama-3-70B attention shape (64 q / 8 kv heads, d 128,
+    bf16): 8 prompts of 2048 tokens as 4 launches of 512-token causal chunks
+    (chunk c sees the 512 c tokens before it), every launch also carrying 32
+    decode rows at context 2048.  One step = the 4 launches."""
+    import torch
+
+    import tl_attn as tla
+
+    S = PF_SEQS + PF_DEC
+    nb = PF_PROMPT // BS
+    N = math.ceil(1.25 * S * nb)
+    g = torch.Generator(device="cuda").manual_seed(0x7E5E0005)
+    pools = []
+    for _ in range(2):
+        k = torch.randn(N, PF_NKV, D, BS, generator=g, device="cuda", dtype=torch.bfloat16)
+        v = torch.randn(N, PF_NKV, D, BS, generator=g, device="cuda", dtype=torch.bfloat16)
+        perm = torch.randperm(N, generator=g, device="cuda").to(torch.int32)
+        pools.append((k, v, perm[: S * nb].view(S, nb).contiguous()))
+    nq = PF_SEQS * PF_CHUNK + PF_DEC
+    q = torch.randn(nq, PF_H, D, generator=g, device="cuda", dtype=torch.bfloat16)
+    out = torch.empty_like(q)
+    q_lens = [PF_CHUNK] * PF_SEQS + [1] * PF_DEC
+    cu = torch.tensor([0] + list(itertools.accumulate(q_lens)), dtype=torch.int32, device="cuda")
+    lens = []
+    for c in range(PF_PROMPT // PF_CHUNK):
+        lens.append(torch.tensor([PF_CHUNK * (c + 1)] * PF_SEQS + [PF_DEC_L] * PF_DEC, dtype=torch.int32,
+                                 device="cuda"))
+    desc = tla.make_prefill_desc(q, pools[0][0], pools[0][2], S, PF_NKV, 1.0 / math.sqrt(D),
+                                 num_prefill_seqs=PF_SEQS)
+
+    def step(i, stream):
+        k, v, tables = pools[i % 2]
+        for c in range(PF_PROMPT // PF_CHUNK):
+            tla.chunked_prefill(desc, out, q, cu, k, v, tables, lens[c], PF_CHUNK, stream)
+
+    ms = timed(step, max(4, args.steps // 5), max(2, args.warmup // 5))
+    flops = prefill_flops()
+    dec_bytes = (PF_PROMPT // PF_CHUNK) * PF_DEC * PF_DEC_L * PF_NKV * D * 2 * 2
+    return {"ms_per_step": ms, "tflops": flops / (ms * 1e-3) / 1e12, "flops": flops,
+            "ms_per_launch": ms / (PF_PROMPT // PF_CHUNK), "decode_row_bytes": dec_bytes}
+
+
 def traffic_from_profile():
     """HBM bytes per decode launch measured with rocprofv3 --pmc (FETCH_SIZE,
     WRITE_SIZE) and recorded in the profile summary, if present."""
@@ -268,6 +324,7 @@ def main():
         fp = bench_decode(args, "fp16")
     if args.only in ("all", "kivi"):
         kv = bench_kivi(args)
+    pf = bench_prefill(args) if args.only in ("all", "prefill") else None
     head = bf or fp
     if head is not None:
         res["dtype"] = "bf16" if bf else "fp16"
@@ -284,10 +341,13 @@ def main():
             "frac": round(achieved / HBM_PEAK_GBS, 4), "bytes_per_launch": head["bytes"],
             "traffic": traffic_from_profile(),
         }
-    else:
+    elif kv is not None:
         res["value"] = round(kv["gbs"], 2)
         res["ms_per_step"] = round(kv["ms_per_step"], 5)
         res["dtype"] = "f16 x int4"
+    else:
+        res["value"] = None
+        res["unit"] = "GB/s (decode benches not run)"
     res["config"] = {
         "workload": "paged-attention decode, Llama-3-8B shape, one layer, batch 64, ctx 4096",
         "batch": S, "q_heads": H, "kv_heads": NKV, "head_dim": D, "block_size": BS, "context": CTX,
@@ -306,6 +366,13 @@ def main():
                             "includes": "append of 1 token/seq with quantise-on-append + decode"}
         if fp is not None:
             res["kivi_int4"]["speedup_vs_fp16_tok_s"] = round(kv["tok_s"] / fp["tok_s"], 3)
+    if pf is not None:
+        res["prefill"] = {
+            "workload": "chunked prefill, 64 q / 8 kv heads, d 128, bf16: 8 prompts x 2048 tokens as 4 "
+                        "causal 512-token chunk launches, each with 32 decode rows at ctx 2048",
+            "tflops": round(pf["tflops"], 2), "pct_mfma_peak_bf16": round(100 * pf["tflops"] / 2500.0, 2),
+            "ms_per_4_launches": round(pf["ms_per_step"], 5), "ms_per_launch": round(pf["ms_per_launch"], 5),
+            "flops_per_4_launches": pf["flops"]}
     if not args.no_cpu:
         res["cpu_baseline"] = cpu_baseline(args.cpu_seconds, 4, min(16, os.cpu_count() or 1))
     print(json.dumps(res), flush=True)

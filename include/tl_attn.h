@@ -225,7 +225,7 @@ int tl_kivi_paged_attention_decode(const tl_kivi_desc* desc, void* out, const vo
                                    int32_t max_context_len, void* workspace,
                                    size_t workspace_bytes, void* stream);
 
-/* ---- chunked prefill (causal) + decode rows in one launch ---------------
+/* ---- chunked prefill (causal) + decode rows in one call -----------------
  * No reference counterpart: the reference's prefill runs per token
  * (cuda_engine.cpp:842-860) or densely in the megakernel
  * (megakernel.cu:267-351).  Mixed batch: sequence s owns query rows
@@ -233,7 +233,8 @@ int tl_kivi_paged_attention_decode(const tl_kivi_desc* desc, void* out, const vo
  * after the chunk is seq_lens[s] (the chunk's own K/V already written to the
  * pool with tl_reshape_and_cache); query i sits at position
  * seq_lens[s] - q_len + i and attends causally to keys 0 .. that position.
- * q_len == 1 rows are decode rows.  head_size 128, block_size 16 or 32,
+ * q_len == 1 rows are decode rows (a second kernel on the same stream).
+ * head_size 128, block_size 16 or 32,
  * dtype F16 or BF16 for q, out and the pool.  max_q_len (host) bounds the
  * grid. */
 typedef struct tl_prefill_desc {
@@ -246,6 +247,8 @@ typedef struct tl_prefill_desc {
   int32_t num_blocks;
   int32_t dtype;               /* TL_DTYPE_F16 or TL_DTYPE_BF16 */
   int32_t gqa_map;
+  int32_t num_prefill_seqs;    /* 0: any sequence may be either kind; n > 0: sequences
+                                  0..n-1 hold every q_len > 1 row, n.. only q_len <= 1 */
   float scale;
 } tl_prefill_desc;
 

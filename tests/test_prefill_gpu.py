@@ -111,8 +111,8 @@ def test_chunked_equals_whole_prompt():
 
 
 def test_decode_rows_match_decode_kernel():
-    """q_len == 1 rows of the prefill launch agree with the decode entry point
-    (same wavefront code, tokens split over 4 instead of 8 wavefronts)."""
+    """q_len == 1 rows of a prefill call agree with the decode entry point
+    (same wavefront code and split)."""
     pc = PrefillCase(inputs.SEEDS[4] + 5, [(1, 1000), (1, 4096), (1, 17)], 32, 8, orc.BF16)
     got = pc.run()
     c = pc.case
@@ -126,14 +126,36 @@ def test_decode_rows_match_decode_kernel():
     assert_close(got, pc.ref(), orc.BF16, ATOL, "decode rows")
 
 
+def test_prefill_first_ordering_matches_unordered():
+    """num_prefill_seqs (prefill sequences first) gives the same rows as the
+    scan of every sequence."""
+    pc = PrefillCase(inputs.SEEDS[4] + 7, [(90, 300), (33, 33), (1, 500), (1, 64), (0, 10)], 16, 4, orc.BF16)
+    a = pc.run()
+    c = pc.case
+    q = dev(pc.q, orc.BF16)
+    k, v, bt, sl, cu = dev(c.k_cache, orc.BF16), dev(c.v_cache, orc.BF16), dev(c.tables), dev(pc.lens), dev(pc.cu)
+    out = torch.full_like(q, float("nan"))
+    desc = tla.make_prefill_desc(q, k, bt, pc.S, 4, c.scale, num_prefill_seqs=2)
+    tla.chunked_prefill(desc, out, q, cu, k, v, bt, sl, 90)
+    torch.cuda.synchronize()
+    assert torch.equal(a.view(torch.int16), out.view(torch.int16))
+    assert_close(out, pc.ref(), orc.BF16, ATOL, "ordered")
+
+
 def test_config5_shape_spot_checks():
     """H=64, n_kv=8, bf16: two 512-row chunks (prefixes 0 and 1536) plus 8
     decode rows at 2048 in one launch; decode rows and the last 4 queries of
     each chunk against the oracle."""
     shape = [(512, 512), (512, 2048)] + [(1, 2048)] * 8
     pc = PrefillCase(inputs.SEEDS[4] + 6, shape, 64, 8, orc.BF16)
-    got = pc.run().float().cpu().numpy()
     c = pc.case
+    q = dev(pc.q, orc.BF16)
+    k, v, bt, sl, cu = dev(c.k_cache, orc.BF16), dev(c.v_cache, orc.BF16), dev(c.tables), dev(pc.lens), dev(pc.cu)
+    out = torch.full_like(q, float("nan"))
+    desc = tla.make_prefill_desc(q, k, bt, pc.S, 8, c.scale, num_prefill_seqs=2)
+    tla.chunked_prefill(desc, out, q, cu, k, v, bt, sl, 512)
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy()
     for s in range(len(shape)):
         ql, L = int(pc.q_lens[s]), int(pc.lens[s])
         take = min(ql, 4)

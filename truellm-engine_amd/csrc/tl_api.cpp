@@ -487,6 +487,9 @@ int tl_chunked_prefill(const tl_prefill_desc* d, void* out, const void* q, const
   if (d->head_size != 128 || (d->block_size != 16 && d->block_size != 32))
     return fail(TL_ERR_NOT_IMPLEMENTED, "prefill head_size=%d block_size=%d (built: 128 x 16/32)",
                 d->head_size, d->block_size);
+  if (d->num_prefill_seqs < 0 || d->num_prefill_seqs > d->num_seqs)
+    return fail(TL_ERR_INVALID_ARGUMENT, "num_prefill_seqs=%d outside [0, %d]", d->num_prefill_seqs,
+                d->num_seqs);
   if (d->num_seqs == 0 || total_q == 0) return ok();
   if (max_q_len > total_q)
     return fail(TL_ERR_INVALID_ARGUMENT, "max_q_len=%d > total_q=%d", max_q_len, total_q);
@@ -502,6 +505,7 @@ int tl_chunked_prefill(const tl_prefill_desc* d, void* out, const void* q, const
   a.block_size = d->block_size; a.max_blocks_per_seq = d->max_blocks_per_seq; a.num_blocks = d->num_blocks;
   a.dtype = d->dtype;   // TL_DTYPE_F16 / TL_DTYPE_BF16 share the kernels' Kind codes
   a.gqa_map = d->gqa_map; a.max_q_len = max_q_len; a.scale = d->scale;
+  a.num_prefill_seqs = d->num_prefill_seqs;
   a.stream = (hipStream_t)stream;
   if (tl::launch_prefill(a)) return fail(TL_ERR_BACKEND, "prefill launch failed");
   return ok();

@@ -107,7 +107,7 @@ struct PrefillLaunch {
   const int32_t* block_tables;
   const int32_t* seq_lens;
   int num_seqs, num_heads, num_kv_heads, block_size, max_blocks_per_seq, num_blocks;
-  int dtype, gqa_map, max_q_len;
+  int dtype, gqa_map, max_q_len, num_prefill_seqs;
   float scale;
   hipStream_t stream;
 };

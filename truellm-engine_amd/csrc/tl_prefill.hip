@@ -22,7 +22,9 @@
 //     keys {16 st + 4 g + i, 16 st + 8 + 4 g + i} for lane group g, which is
 //     used as the k order of step st; V is read from LDS in that order.
 // Decode rows run the 2-byte decode wavefront (tl_decode_wave.hpp), one
-// workgroup per (sequence, kv head, head slice).
+// workgroup per (sequence, kv head, head slice), as a second kernel of the
+// same call on the same stream (one kernel for both would be sized by the
+// decode path's registers on top of the prefill path's).
 //
 // Nearest reference analogues: the per-token prefill of cuda_engine.cpp:842-860
 // and the dense attention of megakernel.cu:267-351; the reference has no
@@ -80,22 +82,17 @@ struct PrefillParams {
   Params base;                 // q, out, pools, tables, seq_lens, heads, group, qk_scale
   const int32_t* cu_q_lens;    // [num_seqs + 1]
   int num_seqs, row_tiles;
+  int pf_seqs;                 // sequences [0, pf_seqs) may be prefill rows
+  int dec_first;               // sequences [dec_first, num_seqs) may be decode rows
 };
 
 template <int NW, int BS>
 struct PrefillSmem {
-  union {
-    struct {
-      uint16_t kt[2][kPfKeys * kKtStride];        // [key][channel] (+8 pad)
-      uint16_t v[2][kPfHead * kPfKeys];           // [block][channel][slot]
-      float row[NW][kPfRows];                     // per-row exchange (alpha, l)
-    } pf;
-    struct {
-      uint32_t p[NW][4][kWaveHeads][4];
-      float m[NW][kWaveHeads], l[NW][kWaveHeads];
-      float acc[NW][kWaveHeads][kPfHead];
-    } dc;
-  };
+  struct {
+    uint16_t kt[2][kPfKeys * kKtStride];          // [key][channel] (+8 pad)
+    uint16_t v[2][kPfHead * kPfKeys];             // [block][channel][slot]
+    float row[NW][kPfRows];                       // per-row exchange (alpha, l)
+  } pf;
 };
 
 // Physical block of block index lb of a table row, or -1.
@@ -123,7 +120,7 @@ __global__ __launch_bounds__(NW * kWave) void prefill_kernel(PrefillParams pp) {
   const int g = lane >> 5, c32 = lane & 31;
 
   int b = blockIdx.x;
-  const int items = pp.num_seqs * p.num_kv_heads;
+  const int items = pp.pf_seqs * p.num_kv_heads;
   const int tile = pp.row_tiles - 1 - b / items;       // longest (latest) tiles first
   b %= items;
   const int seq = b / p.num_kv_heads, kvh = b % p.num_kv_heads;
@@ -131,20 +128,7 @@ __global__ __launch_bounds__(NW * kWave) void prefill_kernel(PrefillParams pp) {
   const int L = p.seq_lens[seq];
   if (ql <= 0) return;
 
-  if (ql == 1) {
-    // ---- decode row: the 2-byte decode wavefront over one head slice ----
-    if (tile >= p.head_slices) return;
-    Params pd = p;
-    const int64_t shift = (int64_t)(q0 - seq) * p.num_heads * kPfHead * 2;   // q / out row q0
-    pd.q = (const char*)p.q + shift;
-    pd.out = (char*)p.out + shift;
-    decode2_wave<KV, kPfHead, BS>(pd, seq, kvh, tile, wave * 32, L, NW * 32, &sm.dc.p[wave][0][0][0],
-                                  &sm.dc.acc[wave][0][0], &sm.dc.m[wave][0], &sm.dc.l[wave][0]);
-    __syncthreads();
-    combine_waves<KV, Kind::F32, kPfHead, true>(pd, NW, &sm.dc.m[0][0], &sm.dc.l[0][0],
-                                                &sm.dc.acc[0][0][0], seq, kvh, tile, 0, tid, NT);
-    return;
-  }
+  if (ql == 1) return;                                  // decode rows: prefill_decode_kernel
 
   // ---- prefill tile ----
   const int rows = ql * p.group;
@@ -237,20 +221,22 @@ __global__ __launch_bounds__(NW * kWave) void prefill_kernel(PrefillParams pp) {
     const int k0 = it * kPfKeys;
     if (k0 < wkend) {
       // ---- S^T = K Q^T (lane: keys 8 j + 4 g + i of row my_row) ----
-      f16v s = f16v{};
+      f16v sa = f16v{};
       const uint16_t* ktw = &sm.pf.kt[st][c32 * kKtStride + 8 * g];
 #pragma unroll
       for (int ks = 0; ks < 8; ++ks)
-        s = M::mma(*reinterpret_cast<const u32x4*>(ktw + 16 * ks), qb[ks], s);
-      // ---- mask, row max, lazy rescale ----
+        sa = M::mma(*reinterpret_cast<const u32x4*>(ktw + 16 * ks), qb[ks], sa);
+      // ---- mask (causal; table holes), row max, lazy rescale ----
+      bool blk_ok[BPI];
+#pragma unroll
+      for (int bi = 0; bi < BPI; ++bi) blk_ok[bi] = block_of(p, table, it * BPI + bi) >= 0;
       float sc[16];
       float mx = -INFINITY;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int kk = 8 * (r >> 2) + 4 * g + (r & 3);
-        const int key = k0 + kk;
-        const bool ok = key <= pos && block_of(p, table, (k0 + kk) / BS) >= 0;
-        sc[r] = ok ? s[r] * p.qk_scale : -INFINITY;
+        const bool ok = k0 + kk <= pos && blk_ok[(8 * (r >> 2)) / BS];
+        sc[r] = ok ? sa[r] * p.qk_scale : -INFINITY;
         mx = fmaxf(mx, sc[r]);
       }
       {
@@ -343,17 +329,48 @@ __global__ __launch_bounds__(NW * kWave) void prefill_kernel(PrefillParams pp) {
   }
 }
 
+// Decode rows (q_len == 1) of a mixed batch: the 2-byte decode wavefronts,
+// one workgroup per (sequence, kv head, head slice), q / out row cu_q_lens[s].
+template <Kind KV, int BS, int NW>
+__global__ __launch_bounds__(NW * kWave) void prefill_decode_kernel(PrefillParams pp) {
+  __shared__ __attribute__((aligned(16))) uint32_t s_p[NW][4][kWaveHeads][4];
+  __shared__ float s_m[NW][kWaveHeads], s_l[NW][kWaveHeads];
+  __shared__ float s_acc[NW][kWaveHeads][kPfHead];
+  const Params& p = pp.base;
+  const int tid = threadIdx.x, wave = tid / kWave;
+  int b = blockIdx.x;
+  const int hs = b % p.head_slices; b /= p.head_slices;
+  const int kvh = b % p.num_kv_heads, seq = pp.dec_first + b / p.num_kv_heads;
+  const int q0 = pp.cu_q_lens[seq];
+  if (pp.cu_q_lens[seq + 1] - q0 != 1) return;
+  const int L = p.seq_lens[seq];
+  Params pd = p;
+  const int64_t shift = (int64_t)(q0 - seq) * p.num_heads * kPfHead * 2;   // q / out row q0
+  pd.q = (const char*)p.q + shift;
+  pd.out = (char*)p.out + shift;
+  decode2_wave<KV, kPfHead, BS>(pd, seq, kvh, hs, wave * 32, L, NW * 32, &s_p[wave][0][0][0],
+                                &s_acc[wave][0][0], &s_m[wave][0], &s_l[wave][0]);
+  __syncthreads();
+  combine_waves<KV, Kind::F32, kPfHead, true>(pd, NW, &s_m[0][0], &s_l[0][0], &s_acc[0][0][0], seq, kvh,
+                                              hs, 0, tid, NW * kWave);
+}
+
 template <Kind KV, int BS>
 int launch_prefill_t(const PrefillParams& pp, unsigned grid, hipStream_t stream) {
-  constexpr int NW = 4;
-  hipLaunchKernelGGL((prefill_kernel<KV, BS, NW>), dim3(grid), dim3(NW * kWave), 0, stream, pp);
+  constexpr int NW = 8, NWD = 8;
+  const Params& p = pp.base;
+  const unsigned dgrid = (unsigned)((pp.num_seqs - pp.dec_first) * p.num_kv_heads * p.head_slices);
+  if (dgrid > 0)
+    hipLaunchKernelGGL((prefill_decode_kernel<KV, BS, NWD>), dim3(dgrid), dim3(NWD * kWave), 0, stream, pp);
+  if (grid > 0)
+    hipLaunchKernelGGL((prefill_kernel<KV, BS, NW>), dim3(grid), dim3(NW * kWave), 0, stream, pp);
   return hipGetLastError() == hipSuccess ? 0 : 5;
 }
 
 }  // namespace
 
 int launch_prefill(const PrefillLaunch& a) {
-  constexpr int NW = 4;
+  constexpr int NW = 8;
   PrefillParams pp;
   Params& p = pp.base;
   p.out = a.out; p.q = a.q;
@@ -370,10 +387,13 @@ int launch_prefill(const PrefillLaunch& a) {
   p.v_scale = 1.f;
   pp.cu_q_lens = a.cu_q_lens;
   pp.num_seqs = a.num_seqs;
-  const int row_tiles_pf = (a.max_q_len * p.group + NW * kPfRows - 1) / (NW * kPfRows);
-  pp.row_tiles = max(row_tiles_pf, p.head_slices);
-  const unsigned grid = (unsigned)(pp.row_tiles * a.num_seqs * a.num_kv_heads);
-  if (grid == 0) return 0;
+  // with the prefill sequences first (num_prefill_seqs > 0) each kernel's grid
+  // covers only its own sequences; otherwise both scan every sequence
+  pp.pf_seqs = a.num_prefill_seqs > 0 ? a.num_prefill_seqs : a.num_seqs;
+  pp.dec_first = a.num_prefill_seqs > 0 ? a.num_prefill_seqs : 0;
+  // prefill tiles exist only for q_len > 1
+  pp.row_tiles = a.max_q_len > 1 ? (a.max_q_len * p.group + NW * kPfRows - 1) / (NW * kPfRows) : 0;
+  const unsigned grid = (unsigned)(pp.row_tiles * pp.pf_seqs * a.num_kv_heads);
   const bool bf16 = a.dtype == (int)Kind::BF16;
   if (a.block_size == 16)
     return bf16 ? launch_prefill_t<Kind::BF16, 16>(pp, grid, a.stream) : launch_prefill_t<Kind::F16, 16>(pp, grid, a.stream);

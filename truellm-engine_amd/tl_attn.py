@@ -91,6 +91,7 @@ class PrefillDesc(ctypes.Structure):
         ("num_blocks", ctypes.c_int32),
         ("dtype", ctypes.c_int32),
         ("gqa_map", ctypes.c_int32),
+        ("num_prefill_seqs", ctypes.c_int32),
         ("scale", ctypes.c_float),
     ]
 
@@ -362,14 +363,17 @@ def kivi_paged_attention_decode(desc, out, q, pages, page_tables, k_cache, v_cac
 # ---------------------------------------------------------------------------
 
 def make_prefill_desc(q, k_cache, block_tables, num_seqs, num_kv_heads, scale, *,
-                      gqa_map=GQA_GROUPED):
-    """q [total_q, H, 128]; k_cache [N, n_kv, 128, bs]; block_tables [S, max_blocks]."""
+                      gqa_map=GQA_GROUPED, num_prefill_seqs=0):
+    """q [total_q, H, 128]; k_cache [N, n_kv, 128, bs]; block_tables [S, max_blocks].
+    num_prefill_seqs > 0 declares sequences 0..n-1 the prefill ones (q_len > 1
+    only there), which keeps the decode rows out of the prefill grid."""
     d = PrefillDesc()
     d.num_seqs, d.num_heads, d.num_kv_heads, d.head_size = num_seqs, q.shape[1], num_kv_heads, q.shape[2]
     d.block_size = k_cache.shape[3]
     d.max_blocks_per_seq, d.num_blocks = block_tables.shape[1], k_cache.shape[0]
     d.dtype = dtype_code(q)
     d.gqa_map = gqa_map
+    d.num_prefill_seqs = num_prefill_seqs
     d.scale = scale
     return d
 
