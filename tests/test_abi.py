@@ -166,3 +166,59 @@ def test_kivi_decode_descriptor_checks_and_planning():
     # 4 x 8 items, 124 pages -> 16 partitions of 8 pages
     assert tla.kivi_workspace_bytes(_kdesc(num_seqs=4), 4096) == 4 * 32 * 16 * (128 * 4 + 8)
     assert call(_kdesc(num_seqs=4)) == tla.ERR_INVALID_ARGUMENT        # workspace missing
+
+
+# ---- reference-named C++ operators (include/tl_truellm_ops.h) -------------
+
+def _demangled_exports():
+    import subprocess
+    out = subprocess.run(["nm", "-DC", "--defined-only", tla.LIB_PATH], check=True, capture_output=True,
+                         text=True).stdout
+    return {ln.split(" ", 2)[2] for ln in out.splitlines() if len(ln.split(" ", 2)) == 3}
+
+
+def test_exports_reference_named_operators():
+    exp = _demangled_exports()
+    want = [
+        "reshape_and_cache(truellm::TrueBuffer const&, truellm::TrueBuffer const&, truellm::TrueBuffer&, "
+        "truellm::TrueBuffer const&, ihipStream_t*)",
+        "paged_attention_v1(truellm::TrueBuffer&, truellm::TrueBuffer const&, truellm::TrueBuffer const&, "
+        "truellm::TrueBuffer const&, truellm::TrueBuffer const&, truellm::TrueBuffer const&, int, float, int, "
+        "int, ihipStream_t*)",
+        "paged_attention_v2(truellm::TrueBuffer&, truellm::TrueBuffer&, truellm::TrueBuffer&, "
+        "truellm::TrueBuffer&, truellm::TrueBuffer const&, truellm::TrueBuffer const&, truellm::TrueBuffer "
+        "const&, truellm::TrueBuffer const&, truellm::TrueBuffer const&, int, float, int, int, int, "
+        "ihipStream_t*)",
+        "truellm::kivi_params_supported(int, int, int)",
+        "truellm::kivi_compress(__half const*, unsigned char*, int, int, int, int, ihipStream_t*)",
+        "truellm::kivi_decompress(unsigned char const*, __half*, int, int, int, int, ihipStream_t*)",
+        "truellm_kernel_init",
+    ]
+    missing = [w for w in want if w not in exp]
+    assert not missing, missing
+
+
+class _Manifest(ctypes.Structure):
+    _fields_ = [("abi_version", ctypes.c_uint32), ("name", ctypes.c_char_p), ("version", ctypes.c_char_p),
+                ("category", ctypes.c_int), ("min_sm_major", ctypes.c_uint32), ("min_sm_minor", ctypes.c_uint32),
+                ("initialize", ctypes.c_void_p), ("shutdown", ctypes.c_void_p), ("kernel_state", ctypes.c_void_p)]
+
+
+def test_kernel_manifest():
+    """kernel.h:23-57: ABI version 1, category ATTENTION, both hooks set."""
+    fn = tla.lib.truellm_kernel_init
+    fn.restype = ctypes.POINTER(_Manifest)
+    m = fn().contents
+    assert m.abi_version == 1 and m.category == 0
+    assert m.name == b"tlattn_paged_attention_gfx950" and m.version
+    assert (m.min_sm_major, m.min_sm_minor) == (9, 5)
+    assert m.initialize and m.shutdown
+
+
+def test_kivi_params_supported_shim_matches_reference_rule():
+    f = tla.lib["_ZN7truellm21kivi_params_supportedEiii"]
+    f.restype = ctypes.c_bool
+    f.argtypes = [ctypes.c_int] * 3
+    for args, want in [((128, 8, 16), True), ((129, 0, 16), False), ((64, 65, 16), False), ((64, 0, 0), False),
+                       ((64, 64, 16), True), ((0, 0, 16), False), ((16, 17, 16), False), ((128, 8, 15), True)]:
+        assert f(*args) == want, args
