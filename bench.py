@@ -74,7 +74,15 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=15.0)
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--only", default="all", choices=["all", "bf16", "fp16", "kivi", "prefill"])
+    p.add_argument("--no-graph", action="store_true",
+                   help="launch the timed steps eagerly (for counter passes that cannot follow graphs)")
+    p.add_argument("--copy-calibration", action="store_true",
+                   help="only run a plain 1 GiB device-to-device copy 5 times (HBM byte counters of a "
+                        "kernel of known traffic) and exit")
     return p.parse_args()
+
+
+USE_GRAPH = True
 
 
 def timed(step, steps, warmup):
@@ -88,6 +96,14 @@ def timed(step, steps, warmup):
     for i in range(warmup):
         step(i, stream)
     torch.cuda.synchronize()
+    if not USE_GRAPH:
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for i in range(steps):
+            step(warmup + i, stream)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / steps
     graph = torch.cuda.CUDAGraph()
     cap = torch.cuda.Stream()
     with torch.cuda.graph(graph, stream=cap):
@@ -314,6 +330,17 @@ def main():
     import torch
 
     torch.cuda.set_device(0)
+    global USE_GRAPH
+    USE_GRAPH = not args.no_graph
+    if args.copy_calibration:
+        n = 1 << 30
+        a = torch.empty(n, dtype=torch.uint8, device="cuda")
+        b = torch.empty_like(a)
+        for _ in range(5):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes_read": n, "bytes_written": n, "launches": 5}), flush=True)
+        return
     res = {"metric": METRIC, "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
            "warmup": args.warmup, "higher_is_better": True, "scaling": "weak",
            "vs_baseline": None, "dtype": "bf16", "data": "synthetic"}
