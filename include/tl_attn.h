@@ -225,6 +225,35 @@ int tl_kivi_paged_attention_decode(const tl_kivi_desc* desc, void* out, const vo
                                    int32_t max_context_len, void* workspace,
                                    size_t workspace_bytes, void* stream);
 
+/* ---- host-side helpers of the path's callers (no device work) ----------- */
+
+/* The engine's attention dispatch (cuda_engine.cpp:1138-1160): v2 iff
+ * max_context_len / block_size > 32, with ceil(max_context_len / (32 bs))
+ * partitions; scale = 1/sqrt(head_size). */
+int tl_attention_plan(int32_t max_context_len, int32_t block_size, int32_t head_size,
+                      int32_t* use_v2, int32_t* num_partitions, float* scale);
+
+/* The allocator's bounds and tables (cuda_allocator.cpp:76, :231-253, :255-280):
+ * max_blocks_per_seq = min(num_blocks, 2048); a block-table row is the
+ * sequence's blocks followed by -1 up to max_blocks_per_seq; token
+ * seq_start_pos + i of a sequence goes to slot blocks[pos / bs] * bs + pos % bs.
+ * tl_build_block_tables fills a [num_seqs, max_blocks_per_seq] batch from
+ * the concatenated per-sequence lists (block_offsets[num_seqs + 1]). */
+int32_t tl_max_blocks_per_seq(int32_t num_blocks);
+int tl_build_block_tables(const int32_t* blocks, const int32_t* block_offsets, int32_t num_seqs,
+                          int32_t max_blocks_per_seq, int32_t* tables);
+int tl_build_slot_mapping(const int32_t* blocks, int32_t num_blocks_of_seq, int32_t block_size,
+                          int32_t seq_start_pos, int32_t num_tokens, int32_t* slots);
+
+/* KvCompressionPass's KIVI settings (kv_compression_pass.cpp:29-66, :184-216):
+ * n_outliers = residual_length, group_size = bits == 4 ? 16 : 8, enabled only
+ * when kivi_params_supported; a layer is compressed in place only when
+ * seq_len > 0 and seq_len * n_kv_heads records fit the scratch bytes. */
+int tl_kivi_pass_params(int32_t residual_length, int32_t bits, int32_t head_dim, int32_t* n_outliers,
+                        int32_t* group_size, int32_t* enabled);
+int32_t tl_kivi_pass_runs(int32_t seq_len, int32_t n_kv_heads, int32_t head_dim, int32_t n_outliers,
+                          int32_t group_size, size_t scratch_bytes);
+
 /* ---- chunked prefill (causal) + decode rows in one call -----------------
  * No reference counterpart: the reference's prefill runs per token
  * (cuda_engine.cpp:842-860) or densely in the megakernel

@@ -222,3 +222,51 @@ def test_kivi_params_supported_shim_matches_reference_rule():
     for args, want in [((128, 8, 16), True), ((129, 0, 16), False), ((64, 65, 16), False), ((64, 0, 0), False),
                        ((64, 64, 16), True), ((0, 0, 16), False), ((16, 17, 16), False), ((128, 8, 15), True)]:
         assert f(*args) == want, args
+
+
+# ---- host-side callers: engine dispatch, allocator tables, compression pass --
+
+def test_attention_plan_matches_engine_dispatch():
+    """cuda_engine.cpp:1138-1160: v1 up to 32 blocks of context, else v2 with
+    ceil(ctx / (32 bs)) partitions; scale 1/sqrt(d)."""
+    assert tla.attention_plan(512, 16, 128)[:2] == (False, 1)
+    assert tla.attention_plan(527, 16, 128)[:2] == (False, 1)       # 527 // 16 == 32
+    assert tla.attention_plan(528, 16, 128)[:2] == (True, 2)
+    assert tla.attention_plan(4096, 16, 128)[:2] == (True, 8)
+    assert tla.attention_plan(32768, 16, 128)[:2] == (True, 64)
+    assert tla.attention_plan(1055, 32, 128)[:2] == (False, 1)      # 1055 // 32 == 32
+    assert tla.attention_plan(1056, 32, 128)[:2] == (True, 2)
+    assert abs(tla.attention_plan(10, 16, 128)[2] - 1 / 128 ** 0.5) < 1e-7
+    with pytest.raises(tla.TLError):
+        tla.attention_plan(10, 0, 128)
+
+
+def test_allocator_tables_and_slots():
+    import numpy as np
+    assert tla.max_blocks_per_seq(512) == 512 and tla.max_blocks_per_seq(100000) == 2048
+    t = tla.build_block_tables([[7, 3, 9], [], [1]], 5)
+    assert t.tolist() == [[7, 3, 9, -1, -1], [-1] * 5, [1, -1, -1, -1, -1]]
+    with pytest.raises(tla.TLError):
+        tla.build_block_tables([[1, 2, 3]], 2)
+    blocks = np.array([5, 2, 11], np.int32)
+    s = tla.build_slot_mapping(blocks, 16, 14, 5)
+    assert s.tolist() == [5 * 16 + 14, 5 * 16 + 15, 2 * 16, 2 * 16 + 1, 2 * 16 + 2]
+    # the decode step's single token at position L - 1
+    assert tla.build_slot_mapping(blocks, 16, 47, 1).tolist() == [11 * 16 + 15]
+    with pytest.raises(tla.TLError):
+        tla.build_slot_mapping(blocks, 16, 47, 2)                      # needs a 4th block
+
+
+def test_kivi_compression_pass_settings():
+    """kv_compression_pass.cpp:29-66 (test_kv_compression_pass.cpp:40-108):
+    residual_length -> n_outliers, bits 4 -> group 16 else 8, disabled when
+    the parameters are unsupported; run_kivi skips empty layers and layers
+    whose records exceed the scratch."""
+    assert tla.kivi_pass_params(8, 4, 128) == (8, 16, True)
+    assert tla.kivi_pass_params(8, 2, 128) == (8, 8, True)
+    assert tla.kivi_pass_params(128, 4, 128) == (128, 16, False)       # > 64 outliers
+    assert tla.kivi_pass_params(0, 4, 256) == (0, 16, False)           # head_dim > 128
+    rec = tla.kivi_compressed_bytes(128, 8, 16)
+    assert tla.kivi_pass_runs(10, 8, 128, 8, 16, 10 * 8 * rec)
+    assert not tla.kivi_pass_runs(11, 8, 128, 8, 16, 10 * 8 * rec)
+    assert not tla.kivi_pass_runs(0, 8, 128, 8, 16, 1 << 30)

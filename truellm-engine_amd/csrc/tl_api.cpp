@@ -6,6 +6,7 @@
 #include "tl_internal.hpp"
 #include "tl_kivi.hpp"
 
+#include <math.h>
 #include <stdarg.h>
 #include <stdio.h>
 #include <string.h>
@@ -465,6 +466,76 @@ int tl_kivi_paged_attention_decode(const tl_kivi_desc* desc, void* out, const vo
   if (rc == 3) return fail(TL_ERR_NOT_IMPLEMENTED, "no KIVI decode kernel for this shape");
   if (rc) return fail(TL_ERR_BACKEND, "KIVI decode launch failed");
   return ok();
+}
+
+int tl_attention_plan(int32_t max_context_len, int32_t block_size, int32_t head_size, int32_t* use_v2,
+                      int32_t* num_partitions, float* scale) {
+  if (block_size <= 0 || head_size <= 0 || max_context_len < 0)
+    return fail(TL_ERR_INVALID_ARGUMENT, "block_size=%d head_size=%d max_context_len=%d", block_size, head_size,
+                max_context_len);
+  if (!use_v2 || !num_partitions || !scale) return fail(TL_ERR_INVALID_ARGUMENT, "NULL pointer");
+  *use_v2 = (max_context_len / block_size) > 32;
+  *num_partitions = *use_v2 ? (max_context_len + 32 * block_size - 1) / (32 * block_size) : 1;
+  *scale = 1.f / sqrtf((float)head_size);
+  return ok();
+}
+
+int32_t tl_max_blocks_per_seq(int32_t num_blocks) { return num_blocks < 2048 ? num_blocks : 2048; }
+
+int tl_build_block_tables(const int32_t* blocks, const int32_t* block_offsets, int32_t num_seqs,
+                          int32_t max_blocks_per_seq, int32_t* tables) {
+  if (num_seqs < 0 || max_blocks_per_seq <= 0)
+    return fail(TL_ERR_INVALID_ARGUMENT, "num_seqs=%d max_blocks_per_seq=%d", num_seqs, max_blocks_per_seq);
+  if (num_seqs == 0) return ok();
+  if (!block_offsets || !tables) return fail(TL_ERR_INVALID_ARGUMENT, "NULL pointer");
+  for (int32_t s = 0; s < num_seqs; ++s) {
+    const int32_t n = block_offsets[s + 1] - block_offsets[s];
+    if (n < 0 || n > max_blocks_per_seq)
+      return fail(TL_ERR_INVALID_ARGUMENT, "sequence %d has %d blocks (max %d)", s, n, max_blocks_per_seq);
+    if (n > 0 && !blocks) return fail(TL_ERR_INVALID_ARGUMENT, "NULL blocks");
+  }
+  for (int32_t s = 0; s < num_seqs; ++s) {
+    const int32_t n = block_offsets[s + 1] - block_offsets[s];
+    int32_t* row = tables + (size_t)s * max_blocks_per_seq;
+    if (n > 0) memcpy(row, blocks + block_offsets[s], (size_t)n * sizeof(int32_t));
+    memset(row + n, 0xFF, (size_t)(max_blocks_per_seq - n) * sizeof(int32_t));   // -1 padding
+  }
+  return ok();
+}
+
+int tl_build_slot_mapping(const int32_t* blocks, int32_t num_blocks_of_seq, int32_t block_size,
+                          int32_t seq_start_pos, int32_t num_tokens, int32_t* slots) {
+  if (block_size <= 0 || seq_start_pos < 0 || num_tokens < 0 || num_blocks_of_seq < 0)
+    return fail(TL_ERR_INVALID_ARGUMENT, "block_size=%d seq_start_pos=%d num_tokens=%d", block_size,
+                seq_start_pos, num_tokens);
+  if (num_tokens == 0) return ok();
+  if (!blocks || !slots) return fail(TL_ERR_INVALID_ARGUMENT, "NULL pointer");
+  const int64_t last = (int64_t)seq_start_pos + num_tokens - 1;
+  if (last / block_size >= num_blocks_of_seq)
+    return fail(TL_ERR_INVALID_ARGUMENT, "position %lld needs block %lld of %d", (long long)last,
+                (long long)(last / block_size), num_blocks_of_seq);
+  for (int32_t i = 0; i < num_tokens; ++i) {
+    const int32_t pos = seq_start_pos + i;
+    slots[i] = blocks[pos / block_size] * block_size + pos % block_size;
+  }
+  return ok();
+}
+
+int tl_kivi_pass_params(int32_t residual_length, int32_t bits, int32_t head_dim, int32_t* n_outliers,
+                        int32_t* group_size, int32_t* enabled) {
+  if (!n_outliers || !group_size || !enabled) return fail(TL_ERR_INVALID_ARGUMENT, "NULL pointer");
+  *n_outliers = residual_length;
+  *group_size = bits == 4 ? 16 : 8;
+  *enabled = tl_kivi_params_supported(head_dim, *n_outliers, *group_size);
+  return ok();
+}
+
+int32_t tl_kivi_pass_runs(int32_t seq_len, int32_t n_kv_heads, int32_t head_dim, int32_t n_outliers,
+                          int32_t group_size, size_t scratch_bytes) {
+  if (seq_len <= 0 || n_kv_heads <= 0) return 0;
+  if (!tl_kivi_params_supported(head_dim, n_outliers, group_size)) return 0;
+  const size_t need = (size_t)seq_len * n_kv_heads * tl_kivi_compressed_bytes(head_dim, n_outliers, group_size);
+  return need <= scratch_bytes;
 }
 
 int tl_chunked_prefill(const tl_prefill_desc* d, void* out, const void* q, const int32_t* cu_q_lens,

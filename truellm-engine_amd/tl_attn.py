@@ -116,6 +116,12 @@ _SIG = {
     "tl_kivi_build_pages": (ctypes.c_int, [ctypes.POINTER(KiviDesc), _P, _P, _P, _P, _P, _P, _I, _P]),
     "tl_kivi_append": (ctypes.c_int, [ctypes.POINTER(KiviDesc), _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
     "tl_kivi_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(KiviDesc), _I]),
+    "tl_attention_plan": (ctypes.c_int, [_I, _I, _I, ctypes.POINTER(_I), ctypes.POINTER(_I), ctypes.POINTER(ctypes.c_float)]),
+    "tl_max_blocks_per_seq": (_I, [_I]),
+    "tl_build_block_tables": (ctypes.c_int, [_P, _P, _I, _I, _P]),
+    "tl_build_slot_mapping": (ctypes.c_int, [_P, _I, _I, _I, _I, _P]),
+    "tl_kivi_pass_params": (ctypes.c_int, [_I, _I, _I, ctypes.POINTER(_I), ctypes.POINTER(_I), ctypes.POINTER(_I)]),
+    "tl_kivi_pass_runs": (_I, [_I, _I, _I, _I, _I, ctypes.c_size_t]),
     "tl_chunked_prefill": (ctypes.c_int, [ctypes.POINTER(PrefillDesc), _P, _P, _P, _P, _P, _P, _P, _I, _I, _P]),
     "tl_kivi_paged_attention_decode": (ctypes.c_int, [ctypes.POINTER(KiviDesc), _P, _P, _P, _P, _P, _P, _P, _P, _I, _P, ctypes.c_size_t, _P]),
 }
@@ -385,3 +391,55 @@ def chunked_prefill(desc, out, q, cu_q_lens, k_cache, v_cache, block_tables, seq
     check(lib.tl_chunked_prefill(ctypes.byref(desc), _ptr(out), _ptr(q), _ptr(cu_q_lens),
                                  _ptr(k_cache), _ptr(v_cache), _ptr(block_tables), _ptr(seq_lens),
                                  q.shape[0], max_q_len, _stream(stream)))
+
+
+# ---------------------------------------------------------------------------
+# host-side helpers of the path's callers (numpy in, numpy out; no GPU)
+# ---------------------------------------------------------------------------
+
+def attention_plan(max_context_len, block_size, head_size):
+    """cuda_engine.cpp:1138-1160: (use_v2, num_partitions, scale)."""
+    v2, P, sc = _I(), _I(), ctypes.c_float()
+    check(lib.tl_attention_plan(max_context_len, block_size, head_size, ctypes.byref(v2), ctypes.byref(P),
+                                ctypes.byref(sc)))
+    return bool(v2.value), P.value, sc.value
+
+
+def max_blocks_per_seq(num_blocks):
+    return lib.tl_max_blocks_per_seq(num_blocks)
+
+
+def build_block_tables(seq_blocks, max_blocks):
+    """cuda_allocator.cpp:231-253 for a batch: rows of block ids padded with -1."""
+    import numpy as np
+    flat = np.ascontiguousarray(np.concatenate([np.asarray(b, np.int32) for b in seq_blocks])
+                                if seq_blocks else np.zeros(0, np.int32), dtype=np.int32)
+    offs = np.zeros(len(seq_blocks) + 1, np.int32)
+    offs[1:] = np.cumsum([len(b) for b in seq_blocks])
+    out = np.empty((len(seq_blocks), max_blocks), np.int32)
+    check(lib.tl_build_block_tables(flat.ctypes.data if flat.size else None, offs.ctypes.data, len(seq_blocks),
+                                    max_blocks, out.ctypes.data))
+    return out
+
+
+def build_slot_mapping(blocks, block_size, seq_start_pos, num_tokens):
+    """cuda_allocator.cpp:255-280."""
+    import numpy as np
+    b = np.ascontiguousarray(blocks, np.int32)
+    out = np.empty(num_tokens, np.int32)
+    check(lib.tl_build_slot_mapping(b.ctypes.data if b.size else None, b.size, block_size, seq_start_pos,
+                                    num_tokens, out.ctypes.data if num_tokens else None))
+    return out
+
+
+def kivi_pass_params(residual_length, bits, head_dim):
+    """kv_compression_pass.cpp:29-66: (n_outliers, group_size, enabled)."""
+    o, g, e = _I(), _I(), _I()
+    check(lib.tl_kivi_pass_params(residual_length, bits, head_dim, ctypes.byref(o), ctypes.byref(g),
+                                  ctypes.byref(e)))
+    return o.value, g.value, bool(e.value)
+
+
+def kivi_pass_runs(seq_len, n_kv_heads, head_dim, n_outliers, group_size, scratch_bytes):
+    """kv_compression_pass.cpp:184-216: does run_kivi compress this layer?"""
+    return bool(lib.tl_kivi_pass_runs(seq_len, n_kv_heads, head_dim, n_outliers, group_size, scratch_bytes))
