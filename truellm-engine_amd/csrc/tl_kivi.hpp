@@ -5,10 +5,12 @@
 //   [   0, 2048) K nibbles, 128 chunks of 16 B.  Chunk c = tt*64 + j*16 + u
 //                holds token t = tt*16 + u; its dword m (0..3) holds channel
 //                octet o = j + 4m, channel 8o + 2i + hb at bit 16*hb + 4i.
-//                Unpacked with (w >> 4i) & 0x000F000F, a dword gives the
-//                eight channels of the octet as fp16 pairs in order: the A
-//                operand of v_mfma_f32_16x16x32_f16 for (token t, k-block m)
-//                held by lane group j.
+//                Masked with 0x000F000F and 0x00F000F0 (and the same after a
+//                shift by 8), a dword gives the octet's eight channels in
+//                order as fp16 denormal pairs n * 2^-24 (16 n * 2^-24 for
+//                channels 2, 3, 6, 7): the A operand of
+//                v_mfma_f32_16x16x32_f16 for (token t, k-block m) held by
+//                lane group j.
 //   [2048, 2560) K (step, zero): octet o -> 8 fp16 steps then 8 fp16 zeros
 //                for channels 8o..8o+7 (per channel over the page's tokens).
 //   [2560, 4608) V nibbles, 128 chunks of 16 B.  Chunk c = hh*64 + r*16 + u;
