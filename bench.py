@@ -214,10 +214,8 @@ def bench_kivi(args, R=128):
     def step(i, stream):
         r, L = plan[i]
         k, v, tables, ptables, pages, _ = reps[r]
-        tla.kivi_append(descs[r], knew, vnew, k, v, slot_dev[i], tables, sl_dev[i], ptables, pages,
-                        stream)
-        tla.kivi_paged_attention_decode(descs[r], out, q, pages, ptables, k, v, tables, sl_dev[i], L,
-                                        ws, stream)
+        tla.kivi_decode_step(descs[r], out, q, knew, vnew, slot_dev[i], pages, ptables, k, v, tables,
+                             sl_dev[i], L, ws, stream)
 
     ms = timed(step, args.steps, args.warmup)
     nbytes = []

@@ -225,6 +225,15 @@ int tl_kivi_paged_attention_decode(const tl_kivi_desc* desc, void* out, const vo
                                    int32_t max_context_len, void* workspace,
                                    size_t workspace_bytes, void* stream);
 
+/* One KIVI decode step in one call: tl_kivi_append then
+ * tl_kivi_paged_attention_decode (seq_lens are the lengths after the
+ * append), two launches on the stream. */
+int tl_kivi_decode_step(const tl_kivi_desc* desc, void* out, const void* q, const void* key,
+                        const void* value, const int32_t* slot_mapping, void* pages,
+                        const int32_t* page_tables, void* k_cache, void* v_cache,
+                        const int32_t* block_tables, const int32_t* seq_lens, int32_t max_context_len,
+                        void* workspace, size_t workspace_bytes, void* stream);
+
 /* ---- host-side helpers of the path's callers (no device work) ----------- */
 
 /* The engine's attention dispatch (cuda_engine.cpp:1138-1160): v2 iff

@@ -283,3 +283,43 @@ def test_kivi_step_graph_replay_matches_eager():
         step(torch.cuda.current_stream())            # eager work between replays
         torch.cuda.synchronize()
         assert torch.equal(out, eager)
+
+
+@pytest.mark.parametrize("H,R,pp", [(32, 128, 0), (32, 0, 0), (64, 128, 0), (32, 128, 4)])
+def test_decode_step_equals_append_then_decode(H, R, pp):
+    """tl_kivi_decode_step gives the bytes of tl_kivi_append followed by
+    tl_kivi_paged_attention_decode, over 40 steps that complete pages."""
+    start = np.array([150, 159, 160, 191, 33, 1000], np.int32)
+    steps = 40
+    runs = []
+    for fused in (False, True):
+        kc = KiviCase(58, start + steps, H=H, R=R, extra_blocks=1)
+        qd, kd, vd = dev(kc.q, orc.F16), dev(kc.k, orc.F16), dev(kc.v, orc.F16)
+        btd, ptd = dev(kc.tables), dev(kc.page_tables)
+        pages = torch.zeros(kc.num_pages, kc.n_kv, tla.KIVI_PAGE_BYTES, dtype=torch.uint8, device="cuda")
+        desc = kc.desc(qd, kd, btd, ptd, pp)
+        tla.kivi_build_pages(desc, kd, vd, btd, dev(start), ptd, pages, int(start.max()))
+        rng = np.random.default_rng(11)
+        max_ctx = int(start.max()) + steps
+        ws = torch.empty(max(16, tla.kivi_workspace_bytes(desc, max_ctx)), dtype=torch.uint8, device="cuda")
+        lens = start.copy()
+        outs = []
+        print(f"case kivi step H={H} R={R} pp={pp} fused={fused}", flush=True)
+        for _ in range(steps):
+            lens = lens + 1
+            pos = lens - 1
+            slots = dev((kc.tables[np.arange(kc.S), pos // 16] * 16 + pos % 16).astype(np.int32))
+            knew = dev(inputs.encode(rng.standard_normal((kc.S, kc.n_kv, 128), dtype=np.float32), orc.F16), orc.F16)
+            vnew = dev(inputs.encode(rng.standard_normal((kc.S, kc.n_kv, 128), dtype=np.float32), orc.F16), orc.F16)
+            sld = dev(lens)
+            out = torch.full_like(qd, float("nan"))
+            if fused:
+                tla.kivi_decode_step(desc, out, qd, knew, vnew, slots, pages, ptd, kd, vd, btd, sld, max_ctx, ws)
+            else:
+                tla.kivi_append(desc, knew, vnew, kd, vd, slots, btd, sld, ptd, pages)
+                tla.kivi_paged_attention_decode(desc, out, qd, pages, ptd, kd, vd, btd, sld, max_ctx, ws)
+            outs.append(out)
+        torch.cuda.synchronize()
+        runs.append((torch.stack(outs), pages.clone(), kd.clone(), vd.clone()))
+    for a, b in zip(runs[0], runs[1]):
+        assert torch.equal(a.view(torch.uint8), b.view(torch.uint8))

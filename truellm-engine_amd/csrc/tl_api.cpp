@@ -412,6 +412,7 @@ static void kivi_plan(const tl_kivi_desc* d, int32_t max_ctx, int* P, int* PP) {
     if (want > pages) want = pages;
     pp = (int)((pages + want - 1) / want);
   }
+  if (pp > tl::kKiviMaxWgPages) pp = tl::kKiviMaxWgPages;   // a workgroup stages its page ids in LDS
   *PP = pp;
   *P = pages > 0 ? (pages + pp - 1) / pp : 1;
 }
@@ -425,12 +426,44 @@ size_t tl_kivi_workspace_bytes(const tl_kivi_desc* desc, int32_t max_context_len
   return sh * desc->head_size * 4 + 2 * sh * 4;
 }
 
+static int kivi_decode_impl(const tl_kivi_desc* desc, void* out, const void* q, const void* pages,
+                            const int32_t* page_tables, const void* k_cache, const void* v_cache,
+                            const int32_t* block_tables, const int32_t* seq_lens, int32_t max_context_len,
+                            void* workspace, size_t workspace_bytes, void* stream,
+                            const tl::KiviPageLaunch* append);
+
 int tl_kivi_paged_attention_decode(const tl_kivi_desc* desc, void* out, const void* q,
                                    const void* pages, const int32_t* page_tables,
                                    const void* k_cache, const void* v_cache,
                                    const int32_t* block_tables, const int32_t* seq_lens,
                                    int32_t max_context_len, void* workspace,
                                    size_t workspace_bytes, void* stream) {
+  return kivi_decode_impl(desc, out, q, pages, page_tables, k_cache, v_cache, block_tables, seq_lens,
+                          max_context_len, workspace, workspace_bytes, stream, nullptr);
+}
+
+int tl_kivi_decode_step(const tl_kivi_desc* desc, void* out, const void* q, const void* key,
+                        const void* value, const int32_t* slot_mapping, void* pages,
+                        const int32_t* page_tables, void* k_cache, void* v_cache,
+                        const int32_t* block_tables, const int32_t* seq_lens, int32_t max_context_len,
+                        void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = check_kivi(desc);
+  if (rc) return rc;
+  if (desc->num_seqs == 0) return ok();
+  if (!key || !value || !slot_mapping) return fail(TL_ERR_INVALID_ARGUMENT, "NULL pointer");
+  if (!aligned16(key) || !aligned16(value)) return fail(TL_ERR_INVALID_ARGUMENT, "key/value must be 16-byte aligned");
+  tl::KiviPageLaunch a = page_launch(desc, k_cache, v_cache, block_tables, seq_lens, page_tables, pages, stream);
+  a.append = 1;
+  a.knew = key; a.vnew = value; a.slots = slot_mapping;
+  return kivi_decode_impl(desc, out, q, pages, page_tables, k_cache, v_cache, block_tables, seq_lens,
+                          max_context_len, workspace, workspace_bytes, stream, &a);
+}
+
+static int kivi_decode_impl(const tl_kivi_desc* desc, void* out, const void* q, const void* pages,
+                            const int32_t* page_tables, const void* k_cache, const void* v_cache,
+                            const int32_t* block_tables, const int32_t* seq_lens, int32_t max_context_len,
+                            void* workspace, size_t workspace_bytes, void* stream,
+                            const tl::KiviPageLaunch* append) {
   int rc = check_kivi(desc);
   if (rc) return rc;
   if (max_context_len < 0) return fail(TL_ERR_INVALID_ARGUMENT, "max_context_len < 0");
@@ -451,6 +484,7 @@ int tl_kivi_paged_attention_decode(const tl_kivi_desc* desc, void* out, const vo
   a.residual_length = desc->residual_length; a.gqa_map = desc->gqa_map;
   a.num_partitions = P; a.partition_pages = PP;
   a.scale = desc->scale;
+  a.append = append;
   a.stream = (hipStream_t)stream;
   if (P > 1) {
     const size_t sh = (size_t)desc->num_seqs * desc->num_heads * P;

@@ -94,6 +94,8 @@ struct KiviDecodeLaunch {
   int max_pages_per_seq, num_pages, residual_length, gqa_map;
   int num_partitions, partition_pages;
   float scale;
+  const KiviPageLaunch* append;  // non-null: the step's append first (fused when one workgroup
+                                 // owns each (seq, kv head), else as its own launch)
   hipStream_t stream;
 };
 int launch_kivi_decode(const KiviDecodeLaunch& a);

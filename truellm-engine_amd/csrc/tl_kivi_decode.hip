@@ -118,10 +118,11 @@ struct PageState {
 };
 
 // One pair of pages (a, b) for a wavefront whose lane (grp, u) holds
-// qsc = q[head u] * scale * log2(e) at channels 32 m + 8 grp .. +7.
+// qsc = q[head u] * scale * log2(e) at channels 32 m + 8 grp .. +7 and
+// qss = qsc * slot_scale.
 //
 // q.k, per page and token tile:  S^T[t][u] = sum_c (n_tc step_c + zero_c) qsc_uc
-//   = 2^24 sum_c (n_tc 2^-24) (qsc_uc step_c slot_scale) + sum_c zero_c qsc_uc;
+//   = 2^24 sum_c (n_tc 2^-24) (qss_uc step_c) + sum_c zero_c qsc_uc;
 // the zero term is one tile per page (A = zeros, rows all alike) scaled by
 // 2^-24 to seed both token tiles, so the tiles hold 2^-24 S^T.
 // p.v, per page and channel group g (32 channels, per-token step/zero):
@@ -129,8 +130,8 @@ struct PageState {
 // the first sum goes to acc (one MFMA per channel tile), the second to cz
 // (one MFMA per page: B column g holds zero_tg).
 __device__ __forceinline__ void page_pair(PageState& st, const PageRaw& ra, const PageRaw& rb, bool oka,
-                                          bool okb, const u32x4 (&qsc)[4], uint32_t* s_par_w, int lane,
-                                          const h8& slot_scale) {
+                                          bool okb, const u32x4 (&qsc)[4], const u32x4 (&qss)[4],
+                                          uint32_t* s_par_w, int lane, const h8& slot_scale) {
   constexpr int GT = kWaveHeads;
   const int grp = lane >> 4, u = lane & 15;
 
@@ -156,7 +157,7 @@ __device__ __forceinline__ void page_pair(PageState& st, const PageRaw& ra, cons
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
       const u32x4* kp = reinterpret_cast<const u32x4*>(par + (grp + 4 * m) * 8);
-      const h8 q2 = hmul(as_h8(qsc[m]), kp[0]) * slot_scale;
+      const h8 q2 = hmul(as_h8(qss[m]), kp[0]);
       t0 = mfma(as_h8(nib8(word(r.kn[0], m))), q2, t0);
       t1 = mfma(as_h8(nib8(word(r.kn[1], m))), q2, t1);
     }
@@ -239,7 +240,7 @@ __device__ __forceinline__ void kivi_pages_wave(const KiviParams& k, int seq, in
   // times scale * log2(e); zero for the padding heads
   const _Float16 one = (_Float16)1.0f, sixteenth = (_Float16)0.0625f;
   const h8 slot_scale = {one, one, sixteenth, sixteenth, one, one, sixteenth, sixteenth};
-  u32x4 qsc[4];
+  u32x4 qsc[4], qss[4];   // q * scale * log2(e); the same times slot_scale
   const int gi = hs * GT + u;
   const bool real = u < GT && gi < p.group;
   const uint16_t* qrow = (const uint16_t*)p.q +
@@ -250,6 +251,7 @@ __device__ __forceinline__ void kivi_pages_wave(const KiviParams& k, int seq, in
     const u32x4 raw = real ? load16(qrow + 32 * m + 8 * grp) : u32x4{0u, 0u, 0u, 0u};
     const h8 v = as_h8(raw) * qs;
     qsc[m] = __builtin_bit_cast(u32x4, v);
+    qss[m] = __builtin_bit_cast(u32x4, v * slot_scale);
   }
 
   PageState st;
@@ -289,10 +291,10 @@ __device__ __forceinline__ void kivi_pages_wave(const KiviParams& k, int seq, in
 #pragma unroll 1
     for (int o = 0; o < cn; o += 4) {
       load(r1a, r1b, id(o + 2), id(o + 3));
-      page_pair(st, r0a, r0b, id(o) >= 0, id(o + 1) >= 0, qsc, s_par_w, lane, slot_scale);
+      page_pair(st, r0a, r0b, id(o) >= 0, id(o + 1) >= 0, qsc, qss, s_par_w, lane, slot_scale);
       if (o + 2 >= cn) break;
       load(r0a, r0b, id(o + 4), id(o + 5));
-      page_pair(st, r1a, r1b, id(o + 2) >= 0, id(o + 3) >= 0, qsc, s_par_w, lane, slot_scale);
+      page_pair(st, r1a, r1b, id(o + 2) >= 0, id(o + 3) >= 0, qsc, qss, s_par_w, lane, slot_scale);
     }
   }
 
@@ -386,6 +388,10 @@ int launch_kivi_decode(const KiviDecodeLaunch& a) {
   k.pages = (const uint8_t*)a.pages; k.page_tables = a.page_tables;
   k.max_pages_per_seq = a.max_pages_per_seq; k.num_pages = a.num_pages;
   k.residual_length = a.residual_length; k.partition_pages = a.partition_pages;
+  // the step's append (token write, quantise-on-append) runs as its own launch
+  // before the decode: folding it into the decode workgroups' prologue cost
+  // them as much as the separate launch
+  if (a.append && launch_kivi_pages(*a.append)) return 5;
   const unsigned items = (unsigned)(a.num_seqs * a.num_kv_heads * p.head_slices);
   if (a.num_partitions == 1) {
     hipLaunchKernelGGL((kivi_decode_kernel<8, true>), dim3(items), dim3(8 * kWave), 0, a.stream, k);

@@ -116,6 +116,7 @@ _SIG = {
     "tl_kivi_build_pages": (ctypes.c_int, [ctypes.POINTER(KiviDesc), _P, _P, _P, _P, _P, _P, _I, _P]),
     "tl_kivi_append": (ctypes.c_int, [ctypes.POINTER(KiviDesc), _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
     "tl_kivi_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(KiviDesc), _I]),
+    "tl_kivi_decode_step": (ctypes.c_int, [ctypes.POINTER(KiviDesc), _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _P, ctypes.c_size_t, _P]),
     "tl_attention_plan": (ctypes.c_int, [_I, _I, _I, ctypes.POINTER(_I), ctypes.POINTER(_I), ctypes.POINTER(ctypes.c_float)]),
     "tl_max_blocks_per_seq": (_I, [_I]),
     "tl_build_block_tables": (ctypes.c_int, [_P, _P, _I, _I, _P]),
@@ -353,6 +354,16 @@ def kivi_append(desc, key, value, k_cache, v_cache, slot_mapping, block_tables, 
 
 def kivi_workspace_bytes(desc, max_context_len) -> int:
     return lib.tl_kivi_workspace_bytes(ctypes.byref(desc), max_context_len)
+
+
+def kivi_decode_step(desc, out, q, key, value, slot_mapping, pages, page_tables, k_cache, v_cache,
+                     block_tables, seq_lens, max_context_len, workspace=None, stream=None):
+    """kivi_append then kivi_paged_attention_decode (seq_lens after the append) in one call."""
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    check(lib.tl_kivi_decode_step(
+        ctypes.byref(desc), _ptr(out), _ptr(q), _ptr(key), _ptr(value), _ptr(slot_mapping), _ptr(pages),
+        _ptr(page_tables), _ptr(k_cache), _ptr(v_cache), _ptr(block_tables), _ptr(seq_lens), max_context_len,
+        _ptr(workspace), ws_bytes, _stream(stream)))
 
 
 def kivi_paged_attention_decode(desc, out, q, pages, page_tables, k_cache, v_cache, block_tables,
