@@ -73,7 +73,7 @@ def parse():
     p.add_argument("--partition-tokens", type=int, default=0)
     p.add_argument("--cpu-seconds", type=float, default=15.0)
     p.add_argument("--no-cpu", action="store_true")
-    p.add_argument("--only", default="all", choices=["all", "bf16", "fp16", "kivi", "prefill"])
+    p.add_argument("--only", default="all", choices=["all", "bf16", "fp16", "kivi", "fp8", "prefill"])
     p.add_argument("--no-graph", action="store_true",
                    help="launch the timed steps eagerly (for counter passes that cannot follow graphs)")
     p.add_argument("--copy-calibration", action="store_true",
@@ -228,6 +228,53 @@ def bench_kivi(args, R=128):
             "bytes_per_step": avg_bytes, "residual_length": R, "group": 32}
 
 
+F8_S, F8_CTX = 16, 32768
+
+
+def bench_fp8(args):
+    """FP8 E4M3 KV long-context decode: batch 16, 32 q / 8 kv heads, d 128,
+    bs 16, every context 32768, per-tensor fp32 scales absmax/448 (K/V drawn
+    N(0,1) in fp16 and cast), bf16 q/out.  The library's own split-K plan
+    (partition_tokens 0) picks the partitions; the log-sum-exp reduce is in
+    the timed step."""
+    import torch
+
+    import tl_attn as tla
+
+    nb = F8_CTX // BS
+    N = math.ceil(1.25 * F8_S * nb)
+    g = torch.Generator(device="cuda").manual_seed(0x7E5E0004)
+    pools = []
+    for _ in range(2):
+        kv = []
+        for _t in range(2):
+            x = torch.randn(N, NKV, D, BS, generator=g, device="cuda", dtype=torch.float16)
+            s = x.abs().max().float() / 448.0
+            kv.append(((x.float() / s).to(torch.float8_e4m3fn).view(torch.uint8), float(s)))
+        perm = torch.randperm(N, generator=g, device="cuda").to(torch.int32)
+        pools.append((kv[0], kv[1], perm[: F8_S * nb].view(F8_S, nb).contiguous()))
+    q = torch.randn(F8_S, H, D, generator=g, device="cuda", dtype=torch.bfloat16)
+    sl = torch.full((F8_S,), F8_CTX, dtype=torch.int32, device="cuda")
+    out = torch.empty_like(q)
+    descs = []
+    for (kq, ks), (vq, vs), tables in pools:
+        descs.append(tla.make_decode_desc(q, kq, tables, NKV, 1.0 / math.sqrt(D), gqa_map=tla.GQA_GROUPED,
+                                          partition_tokens=0, k_scale=ks, v_scale=vs))
+    ws = torch.empty(max(16, tla.workspace_bytes(descs[0], F8_CTX)), dtype=torch.uint8, device="cuda")
+
+    def step(i, stream):
+        (kq, _), (vq, _), tables = pools[i % 2]
+        tla.paged_attention_decode(descs[i % 2], out, q, kq, vq, tables, sl, F8_CTX, ws, stream)
+
+    ms = timed(step, args.steps, args.warmup)
+    kv_bytes = F8_S * F8_CTX * NKV * D * 2
+    nbytes = kv_bytes + F8_S * H * D * 2 * 2 + F8_S * nb * 4 + F8_S * 4
+    P = max(1, tla.workspace_bytes(descs[0], F8_CTX) // (F8_S * H * (D + 2) * 4))
+    part = F8_S * H * P * (D + 2) * 4 * 2
+    return {"ms_per_step": ms, "gbs": nbytes / (ms * 1e-3) / 1e9, "tok_s": F8_S / (ms * 1e-3),
+            "bytes": nbytes, "partial_bytes": part, "partitions": P}
+
+
 PF_H, PF_NKV, PF_SEQS, PF_PROMPT, PF_CHUNK, PF_DEC, PF_DEC_L = 64, 8, 8, 2048, 512, 32, 2048
 
 
@@ -349,6 +396,7 @@ def main():
         fp = bench_decode(args, "fp16")
     if args.only in ("all", "kivi"):
         kv = bench_kivi(args)
+    f8 = bench_fp8(args) if args.only in ("all", "fp8") else None
     pf = bench_prefill(args) if args.only in ("all", "prefill") else None
     head = bf or fp
     if head is not None:
@@ -391,6 +439,14 @@ def main():
                             "includes": "append of 1 token/seq with quantise-on-append + decode"}
         if fp is not None:
             res["kivi_int4"]["speedup_vs_fp16_tok_s"] = round(kv["tok_s"] / fp["tok_s"], 3)
+    if f8 is not None:
+        res["fp8_e4m3_long_context"] = {
+            "workload": "decode, batch 16, ctx 32768, 32 q / 8 kv heads, d 128, FP8 E4M3 KV with per-tensor "
+                        f"scales, bf16 q, split-K {f8['partitions']} x {F8_CTX // f8['partitions']} tokens "
+                        "(library plan) + LSE reduce",
+            "gbs": round(f8["gbs"], 2), "pct_hbm_peak": round(100 * f8["gbs"] / HBM_PEAK_GBS, 2),
+            "ms_per_step": round(f8["ms_per_step"], 5), "tok_s": round(f8["tok_s"], 1),
+            "bytes_per_step": f8["bytes"], "split_k_partial_bytes_not_counted": f8["partial_bytes"]}
     if pf is not None:
         res["prefill"] = {
             "workload": "chunked prefill, 64 q / 8 kv heads, d 128, bf16: 8 prompts x 2048 tokens as 4 "

@@ -432,6 +432,12 @@ int launch_decode2(const DecodeLaunch& a) {
 template <Kind KV, Kind QK, int HEAD, int BS>
 int launch_gt(const DecodeLaunch& a) {
   const int group = a.num_heads / a.num_kv_heads;
+  if constexpr (KV == Kind::FP8 && HEAD == 128 && BS == 16) {
+    if (a.use_generic == 0) {
+      const int rc = launch_decode_fp8_mfma(a);
+      if (rc != 3) return rc;
+    }
+  }
   if (group == 1) return launch_typed<KV, QK, HEAD, BS, 1>(a);
   if constexpr ((KV == Kind::F16 || KV == Kind::BF16) && QK == KV && (HEAD == 64 || HEAD == 128)) {
     if (a.use_generic == 0) return launch_decode2<KV, HEAD, BS>(a);

@@ -266,14 +266,14 @@ __device__ __forceinline__ void decode2_wave(const Params& p, int seq, int kvh, 
   if ((lane & 15) == 0) s_l_w[g_lane] = l_tot;
 }
 
-// Merges the nw wavefront states (s_m [nw][4], s_l [nw][4], s_acc [nw][4][HEAD])
-// and writes the workgroup's result: the normalised output (FINAL) or the
-// partition's (max, sum, normalised partial) for the log-sum-exp merge.
-template <Kind QK, Kind PO, int HEAD, bool FINAL>
+// Merges the nw wavefront states (s_m [nw][GT], s_l [nw][GT], s_acc
+// [nw][GT][HEAD], GT q heads per wavefront) and writes the workgroup's
+// result: the normalised output (FINAL) or the partition's (max, sum,
+// normalised partial) for the log-sum-exp merge.
+template <Kind QK, Kind PO, int HEAD, bool FINAL, int GT = kWaveHeads>
 __device__ __forceinline__ void combine_waves(const Params& p, int nw, const float* s_m,
                                               const float* s_l, const float* s_acc, int seq, int kvh,
                                               int hs, int part, int tid, int nthreads) {
-  constexpr int GT = kWaveHeads;
   for (int i = tid; i < GT * HEAD; i += nthreads) {
     const int g = i / HEAD, d = i % HEAD, gi = hs * GT + g;
     if (gi >= p.group) continue;

@@ -37,6 +37,11 @@ struct DecodeLaunch {
 // 5 on a launch error.
 int launch_decode(const DecodeLaunch& a);
 
+// The matrix-core decode of FP8 KV (head_size 128, block_size 16, f16 / bf16
+// q, fp32 split-K partials).  Returns 3 for anything else, so the caller can
+// fall back to the generic kernel.
+int launch_decode_fp8_mfma(const DecodeLaunch& a);
+
 struct CacheLaunch {
   const void* key;              // [T, n_kv, D]
   const void* value;
