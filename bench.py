@@ -408,8 +408,8 @@ def main():
         res["tok_s_32_layers"] = round(head["tok_s"] / 32, 1)
         achieved = head["bytes"] / (head["launch_ms"] * 1e-3) / 1e9
         res["roofline"] = {
-            "kernel": "decode2_kernel (paged decode, single pass)" if head["workspace_bytes"] == 0
-                      else "decode2_kernel + lse_reduce_kernel (split-K)",
+            "kernel": "mfma2_decode_kernel (paged decode, single pass)" if head["workspace_bytes"] == 0
+                      else "mfma2_decode_kernel + lse_reduce_kernel (split-K)",
             "bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4), "bytes_per_launch": head["bytes"],
             "traffic": traffic_from_profile(),

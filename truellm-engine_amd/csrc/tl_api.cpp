@@ -82,8 +82,9 @@ void plan_partitions(const tl_decode_desc* d, int32_t max_ctx, int* P, int* PT) 
     pt_chunks = d->partition_tokens / tl::kDecodeChunk;
   } else {
     const int group = d->num_heads / d->num_kv_heads;
-    // q heads per workgroup: 16 for the FP8 matrix-core kernel, 4 otherwise
-    const int per = (d->kv_dtype == TL_DTYPE_FP8_E4M3 && d->head_size == 128 && d->block_size == 16) ? 16 : 4;
+    // q heads per workgroup: 16 for the matrix-core kernels, 4 otherwise
+    const int per = tl::decode_uses_mfma(d->kv_dtype, d->num_heads, d->num_kv_heads, d->head_size, d->block_size)
+                        ? 16 : 4;
     const int slices = group == 1 ? 1 : (group + per - 1) / per;
     const long items = (long)d->num_seqs * d->num_kv_heads * slices;
     long want = items > 0 ? (512 + items - 1) / items : 1;

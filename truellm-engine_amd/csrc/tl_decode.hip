@@ -432,11 +432,10 @@ int launch_decode2(const DecodeLaunch& a) {
 template <Kind KV, Kind QK, int HEAD, int BS>
 int launch_gt(const DecodeLaunch& a) {
   const int group = a.num_heads / a.num_kv_heads;
-  if constexpr (KV == Kind::FP8 && HEAD == 128 && BS == 16) {
-    if (a.use_generic == 0) {
-      const int rc = launch_decode_fp8_mfma(a);
-      if (rc != 3) return rc;
-    }
+  if (a.use_generic == 0 &&
+      decode_uses_mfma(a.kv_dtype, a.num_heads, a.num_kv_heads, a.head_size, a.block_size)) {
+    const int rc = launch_decode_mfma(a);
+    if (rc != 3) return rc;
   }
   if (group == 1) return launch_typed<KV, QK, HEAD, BS, 1>(a);
   if constexpr ((KV == Kind::F16 || KV == Kind::BF16) && QK == KV && (HEAD == 64 || HEAD == 128)) {

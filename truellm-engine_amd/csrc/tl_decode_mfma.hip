@@ -1,0 +1,113 @@
+// tl_decode_mfma.hip -- paged-attention decode on the matrix cores
+// (head_size 128, block_size 16), for FP8 E4M3 KV and for 2-byte KV.
+//
+// The wavefronts are in tl_mfma_wave.hpp.  Why matrix cores for decode:
+//   * FP8: a byte is one element, so per byte of HBM traffic there are twice
+//     the multiply-adds of 2-byte KV, which the packed dot products of the
+//     2-byte wavefront cannot keep up with;
+//   * 2-byte KV with more than 4 q heads per kv head (GQA group 8 or 16):
+//     the 16 MFMA columns serve the whole group from one KV read, where the
+//     dot-product wavefront reads the KV once per 4 heads.
+// The dequant scales of FP8 fold into the score scale (k_scale) and the
+// output (v_scale), as the reference's dequantise-then-multiply does (the
+// scaled K/V are k_scale * code and v_scale * code).  Workgroups and the
+// split-K / log-sum-exp protocol are those of the 2-byte decode (NW
+// wavefronts stride over a partition's iterations and merge in LDS).
+#include "tl_device.hpp"
+#include "tl_internal.hpp"
+#include "tl_mfma_wave.hpp"
+
+namespace tl {
+
+namespace {
+
+// Work item of a decode workgroup: (sequence, kv head, head slice,
+// partition) and the partition's token range [t0, t1); false when the
+// partition starts past the sequence (split-K only).
+struct Item {
+  int seq, kvh, hs, part, t0, t1;
+};
+__device__ __forceinline__ bool item_of(const Params& p, bool final, Item& w) {
+  int bid = blockIdx.x;
+  w.part = bid % p.num_partitions; bid /= p.num_partitions;
+  w.hs = bid % p.head_slices;      bid /= p.head_slices;
+  w.kvh = bid % p.num_kv_heads;
+  w.seq = bid / p.num_kv_heads;
+  const int L = p.seq_lens[w.seq];
+  w.t0 = w.part * p.partition_tokens;
+  if (!final && w.t0 >= L) return false;
+  w.t1 = min(w.t0 + p.partition_tokens, L);
+  return true;
+}
+
+template <Kind QK, Kind PO, int NW, bool FINAL>
+__global__ __launch_bounds__(NW * kWave) void fp8_decode_kernel(Params p) {
+  __shared__ __attribute__((aligned(16))) float s_acc[NW * mw::kHeads * mw::kHead];
+  __shared__ float s_m[NW * mw::kHeads], s_l[NW * mw::kHeads];
+  Item w;
+  if (!item_of(p, FINAL, w)) return;
+  mw::decode_workgroup<Kind::FP8, QK, PO, NW, FINAL>(p, w.seq, w.kvh, w.hs, w.part, w.t0, w.t1, s_acc, s_m, s_l);
+}
+
+template <Kind KV, Kind PO, int NW, bool FINAL>
+__global__ __launch_bounds__(NW * kWave) void mfma2_decode_kernel(Params p) {
+  __shared__ __attribute__((aligned(16))) float s_acc[NW * mw::kHeads * mw::kHead];
+  __shared__ float s_m[NW * mw::kHeads], s_l[NW * mw::kHeads];
+  Item w;
+  if (!item_of(p, FINAL, w)) return;
+  mw::decode_workgroup<KV, KV, PO, NW, FINAL>(p, w.seq, w.kvh, w.hs, w.part, w.t0, w.t1, s_acc, s_m, s_l);
+}
+
+template <Kind KV, Kind QK, int NW, bool FINAL>
+void launch_kernel(const Params& p, unsigned grid, hipStream_t stream) {
+  constexpr Kind PO = FINAL ? QK : Kind::F32;
+  if constexpr (KV == Kind::FP8)
+    hipLaunchKernelGGL((fp8_decode_kernel<QK, PO, NW, FINAL>), dim3(grid), dim3(NW * kWave), 0, stream, p);
+  else
+    hipLaunchKernelGGL((mfma2_decode_kernel<KV, PO, NW, FINAL>), dim3(grid), dim3(NW * kWave), 0, stream, p);
+}
+
+template <Kind KV, Kind QK>
+int launch_typed(const DecodeLaunch& a) {
+  Params p;
+  p.out = a.out; p.q = a.q;
+  p.k_cache = (const char*)a.k_cache; p.v_cache = (const char*)a.v_cache;
+  p.block_tables = a.block_tables; p.seq_lens = a.seq_lens;
+  p.part_m = a.part_m; p.part_l = a.part_l; p.part_o = a.part_o;
+  p.num_heads = a.num_heads; p.num_kv_heads = a.num_kv_heads;
+  p.max_blocks_per_seq = a.max_blocks_per_seq; p.num_blocks = a.num_blocks;
+  p.num_partitions = a.num_partitions; p.partition_tokens = a.partition_tokens;
+  p.group = a.num_heads / a.num_kv_heads;
+  p.head_slices = (p.group + mw::kHeads - 1) / mw::kHeads;
+  p.gqa_map = a.gqa_map;
+  const bool fp8 = KV == Kind::FP8;
+  p.qk_scale = a.scale * (fp8 ? a.k_scale : 1.f) * kLog2e;
+  p.v_scale = fp8 ? a.v_scale : 1.f;
+  const int P = a.num_partitions;
+  const unsigned items = (unsigned)(a.num_seqs * a.num_kv_heads * p.head_slices);
+  if (P == 1) {
+    p.partition_tokens = 0x7fffffff;
+    launch_kernel<KV, QK, 8, true>(p, items, a.stream);
+    return hipGetLastError() == hipSuccess ? 0 : 5;
+  }
+  launch_kernel<KV, QK, 4, false>(p, items * P, a.stream);
+  if (hipGetLastError() != hipSuccess) return 5;
+  return launch_lse_reduce(a.out, a.q_dtype, a.part_m, a.part_l, a.part_o, a.part_o_dtype, a.seq_lens,
+                           a.num_seqs, a.num_heads, mw::kHead, P, a.partition_tokens, 0, 0, a.stream);
+}
+
+}  // namespace
+
+int launch_decode_mfma(const DecodeLaunch& a) {
+  const Kind kv = (Kind)a.kv_dtype, qk = (Kind)a.q_dtype;
+  if (a.head_size != mw::kHead || a.block_size != 16) return 3;
+  const int tpi = kv == Kind::FP8 ? mw::tokens_per_iteration<Kind::FP8>() : mw::tokens_per_iteration<Kind::F16>();
+  if (a.num_partitions > 1 && (a.partition_tokens % tpi || a.part_o_dtype != 0)) return 3;
+  if (kv == Kind::FP8 && qk == Kind::F16) return launch_typed<Kind::FP8, Kind::F16>(a);
+  if (kv == Kind::FP8 && qk == Kind::BF16) return launch_typed<Kind::FP8, Kind::BF16>(a);
+  if (kv == Kind::F16 && qk == Kind::F16) return launch_typed<Kind::F16, Kind::F16>(a);
+  if (kv == Kind::BF16 && qk == Kind::BF16) return launch_typed<Kind::BF16, Kind::BF16>(a);
+  return 3;
+}
+
+}  // namespace tl

@@ -37,10 +37,22 @@ struct DecodeLaunch {
 // 5 on a launch error.
 int launch_decode(const DecodeLaunch& a);
 
-// The matrix-core decode of FP8 KV (head_size 128, block_size 16, f16 / bf16
-// q, fp32 split-K partials).  Returns 3 for anything else, so the caller can
-// fall back to the generic kernel.
-int launch_decode_fp8_mfma(const DecodeLaunch& a);
+// The matrix-core decode (head_size 128, block_size 16, fp32 split-K
+// partials): FP8 KV with f16 / bf16 q, or 2-byte KV with q of the same type.
+// Returns 3 for anything else, so the caller can fall back.
+int launch_decode_mfma(const DecodeLaunch& a);
+
+// Whether launch_decode sends a decode to the matrix-core kernels, which
+// serve 16 q heads per workgroup (the other kernels serve 4): FP8, f16 and
+// bf16 KV with head_size 128 and block_size 16.  They beat the dot-product
+// wavefront at every GQA group measured (group 4: 6.38 against 5.94 TB/s;
+// group 8, where the dot-product wavefront reads KV twice: 5.8 against
+// 3.0 TB/s).
+inline bool decode_uses_mfma(int kv_dtype, int num_heads, int num_kv_heads, int head_size, int block_size) {
+  (void)num_heads;
+  if (head_size != 128 || block_size != 16 || num_kv_heads <= 0) return false;
+  return kv_dtype == 32 || kv_dtype == 1 || kv_dtype == 2;   // FP8 E4M3, f16, bf16
+}
 
 struct CacheLaunch {
   const void* key;              // [T, n_kv, D]

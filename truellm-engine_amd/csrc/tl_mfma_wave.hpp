@@ -1,0 +1,459 @@
+// tl_mfma_wave.hpp -- decode wavefronts on the matrix cores for head_size
+// 128, block_size 16: FP8 E4M3 KV (fp8_wave) and 2-byte KV (mfma2_wave).
+//
+// Both put the q heads on the 16 columns of v_mfma_f32_16x16x32_{f16,bf16},
+// so one KV read serves up to 16 heads of a GQA group, and both keep the
+// same accumulator layout: lane (m = lane & 15, kg = lane >> 4) holds head
+// m, head dims 16 dt + 4 kg + r of O^T tile dt.
+//   q.k, S^T[token][head] = K^T q^T.  The contraction runs over head dims,
+//     the pool keeps tokens contiguous ([D][BS] per block), so K is
+//     transposed in registers: a lane reads dwords of rows d = 4 j + kg
+//     (j < 32; for each j the wavefront reads rows 4 j .. 4 j + 3, 64 or 128
+//     contiguous bytes per block), and one v_perm_b32 per output dword pairs
+//     two rows per token.  MFMA step s (k = 32) holds head dim
+//     32 s + 4 e + kg in slot e of lane group kg; q is loaded in that order.
+//   p.v, O^T[d][head] = V P^T.  A lane's score registers hold its head's
+//     weights for a contiguous run of tokens that is exactly one k group of
+//     the V operand (rows of V as loaded, no conversion for 2-byte KV), so
+//     P^T needs no cross-lane move.
+// Online softmax per lane (= head): running max with lazy rescaling (the
+// weights exp2(s - m) stay below 2^8), fp32 sums and accumulators.
+#pragma once
+
+#include "tl_decode_wave.hpp"
+#include "tl_device.hpp"
+
+#include <math.h>
+
+namespace tl {
+namespace mw {
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef __bf16 b8 __attribute__((ext_vector_type(8)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef unsigned u4v __attribute__((ext_vector_type(4)));
+
+constexpr int kHead = 128;
+constexpr int kHeads = 16;          // q heads per wavefront: the MFMA columns
+constexpr float kLazyRescale = 8.f; // rescale once the max grows by more than 2^8
+
+template <Kind KV> constexpr int tokens_per_iteration() { return KV == Kind::FP8 ? 64 : 32; }
+
+// Two E4M3 codes (bytes 0,1 or 2,3 of w) to two f16, exactly.
+template <bool HI>
+__device__ __forceinline__ uint32_t f8x2(uint32_t w) {
+  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, HI));
+}
+
+// 16x16x32 MFMA on four dwords of packed f16 / bf16 pairs per operand.
+template <Kind T>
+__device__ __forceinline__ f4 mma(uint32_t a0, uint32_t a1, uint32_t a2, uint32_t a3, const u4v& b, f4 c) {
+  const u4v a = {a0, a1, a2, a3};
+  if constexpr (T == Kind::BF16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(b8, a), __builtin_bit_cast(b8, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, a), __builtin_bit_cast(h8, b), c, 0, 0, 0);
+}
+
+__device__ __forceinline__ uint32_t ld_nt(const char* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(p));
+}
+
+// Max / sum over the lanes l, l ^ 16, l ^ 32, l ^ 48.
+__device__ __forceinline__ float max_kg(float v) {
+  auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, v), __builtin_bit_cast(unsigned, v),
+                                            false, false);
+  v = fmaxf(__builtin_bit_cast(float, (unsigned)r[0]), __builtin_bit_cast(float, (unsigned)r[1]));
+  r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(unsigned, v), __builtin_bit_cast(unsigned, v), false,
+                                       false);
+  return fmaxf(__builtin_bit_cast(float, (unsigned)r[0]), __builtin_bit_cast(float, (unsigned)r[1]));
+}
+__device__ __forceinline__ float sum_kg(float v) {
+  v = swap32_add(v, v);
+  return swap16_add(v, v);
+}
+
+// Physical blocks of the NB blocks starting at token it (-1: hole, past t1
+// or outside the pool).
+template <int NB> struct Blocks { int e[NB]; };
+template <int NB>
+__device__ __forceinline__ Blocks<NB> table_blocks(const Params& p, const int32_t* table, int it, int t1) {
+  Blocks<NB> b;
+#pragma unroll
+  for (int i = 0; i < NB; ++i) b.e[i] = table_entry_bs<16>(p, table, it + 16 * i, t1);
+  return b;
+}
+// Entry i (per lane) of a wave-uniform set.  Written as one nested select:
+// a select loop over k is turned back into an indexed load, which puts the
+// set in LDS.
+template <int NB>
+__device__ __forceinline__ int pick(const Blocks<NB>& b, int i) {
+  static_assert(NB == 2 || NB == 4, "2 or 4 blocks per iteration");
+  if constexpr (NB == 4) return i == 0 ? b.e[0] : i == 1 ? b.e[1] : i == 2 ? b.e[2] : b.e[3];
+  else return i == 0 ? b.e[0] : b.e[1];
+}
+
+// Zeroes the bytes of tokens >= n (0 <= n <= 16) of a 16-token FP8 row.
+__device__ __forceinline__ u32x4 keep_bytes(const u32x4& v, int n) {
+  uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int k = n - 4 * i;   // bytes of this word to keep
+    const uint32_t mask = k >= 4 ? 0xffffffffu : k <= 0 ? 0u : (0xffffffffu >> (32 - 8 * k));
+    w[i] &= mask;
+  }
+  return u32x4{w[0], w[1], w[2], w[3]};
+}
+// Zeroes the 2-byte elements >= n (0 <= n <= 8) of an 8-token run.
+__device__ __forceinline__ u32x4 keep_halves(const u32x4& v, int n) {
+  uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int k = n - 2 * i;
+    w[i] &= k >= 2 ? 0xffffffffu : k == 1 ? 0xffffu : 0u;
+  }
+  return u32x4{w[0], w[1], w[2], w[3]};
+}
+
+// The running softmax state of a wavefront and its hand-over to LDS
+// (s_acc_w [16][128] unnormalised, times v_scale; s_m_w [16] in log2 units;
+// s_l_w [16]).
+struct State {
+  f4 o[8];
+  float m_run, l_lane;
+  __device__ __forceinline__ void init() {
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) o[dt] = f4{0.f, 0.f, 0.f, 0.f};
+    m_run = -INFINITY;
+    l_lane = 0.f;
+  }
+  // Raises the running max to the wavefront's new max mx when it grew by
+  // more than 2^8 for some head.
+  __device__ __forceinline__ void update_max(float mx) {
+    const float m_new = fmaxf(m_run, max_kg(mx));
+    if (__builtin_amdgcn_ballot_w64(m_new > m_run + kLazyRescale) != 0) {
+      const float alpha = (m_run == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new);
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) o[dt] *= alpha;
+      l_lane *= alpha;
+      m_run = m_new;
+    }
+  }
+  __device__ __forceinline__ void store(float v_scale, int m, int kg, float* s_acc_w, float* s_m_w,
+                                        float* s_l_w) const {
+    const float l_tot = sum_kg(l_lane);
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt)
+      *reinterpret_cast<f4*>(&s_acc_w[m * kHead + 16 * dt + 4 * kg]) = o[dt] * v_scale;
+    if (kg == 0) {
+      s_m_w[m] = m_run;
+      s_l_w[m] = l_tot;
+    }
+  }
+};
+
+// ---- FP8 E4M3 KV, f16 / bf16 q: 64 tokens (4 blocks) per iteration ----
+//
+// K: the A row m is token quad m (block m >> 2, tokens 4 (m & 3) .. +3) and
+// tile i takes token i of every quad.  Lane (m, kg) reads 32 dwords (64
+// contiguous bytes per block for each j); one v_perm_b32 stage pairs the
+// bytes of two rows per token, and the converter's (bytes 0,1) / (bytes
+// 2,3) halves are then exactly the f16 (d, d') pairs of one token: 1 perm
+// and 2 converts per 4 bytes.  v_cvt_scalef32_pk_f16_fp8 with scale 1 is
+// exact: every E4M3 value, subnormals and NaN included, is an f16 value.
+// Scores: lane (m, kg) holds head m, token 4 r + i of block kg.
+// V: lane (m, kg) loads 16 bytes, row d = 16 dt + m of block kg; MFMA h
+// takes its tokens 8 h .. 8 h + 7.
+// bf16 q is brought into f16 range by a power of two per head (exact: max
+// |q| in [2^14, 2^15)); the factor returns in the score scale.  The
+// dequant scales fold into the score scale (k_scale) and the output
+// (v_scale).
+template <Kind QK>
+__device__ __forceinline__ void fp8_wave(const Params& p, int seq, int kvh, int hs, int first_it, int t1,
+                                         int step, float* s_acc_w, float* s_m_w, float* s_l_w) {
+  constexpr int kBlockBytes = kHead * 16;
+  const int lane = threadIdx.x % kWave;
+  const int m = lane & 15, kg = lane >> 4;
+
+  // ---- q of head column m in MFMA order: slot (s, e) = dim 32 s + 4 e + kg ----
+  const int gi = hs * kHeads + m;
+  const bool hv = gi < p.group;
+  const int head = hv ? head_of(p, kvh, gi) : 0;
+  const uint16_t* qrow = (const uint16_t*)p.q + ((int64_t)seq * p.num_heads + head) * kHead;
+  float qf[32];
+  float qmax = 0.f;
+#pragma unroll
+  for (int s = 0; s < 4; ++s)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const uint16_t bits = hv ? qrow[32 * s + 4 * e + kg] : (uint16_t)0;
+      const float v = QK == Kind::BF16 ? bf16_to_f32(bits) : f16_to_f32(bits);
+      qf[8 * s + e] = v;
+      qmax = fmaxf(qmax, fabsf(v));
+    }
+  int sh = 0;
+  if constexpr (QK == Kind::BF16) {
+    qmax = max_kg(qmax);
+    if (qmax > 0.f && qmax < INFINITY) {
+      int ex;
+      frexpf(qmax, &ex);
+      sh = 15 - ex;
+    }
+  }
+  u4v qb[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    h8 v;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = (_Float16)ldexpf(qf[8 * s + e], sh);
+    qb[s] = __builtin_bit_cast(u4v, v);
+  }
+  const float qk_scale = p.qk_scale * ldexpf(1.f, -sh);
+
+  State st;
+  st.init();
+
+  const int32_t* table = p.block_tables + (int64_t)seq * p.max_blocks_per_seq;
+  const int64_t pool_stride = (int64_t)p.num_kv_heads * kBlockBytes;
+  const char* kbase0 = p.k_cache + (int64_t)kvh * kBlockBytes + 16 * kg + 4 * (m & 3);
+  const char* vbase0 = p.v_cache + (int64_t)kvh * kBlockBytes + 16 * m;
+  const int kb = m >> 2;   // the block of this lane's K quad
+  auto load_k = [&](uint32_t (&kw)[32], const char* base) {
+#pragma unroll
+    for (int j = 0; j < 32; ++j) kw[j] = ld_nt(base + 64 * j);
+  };
+  auto load_v = [&](u32x4 (&vr)[8], const char* base) {
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) vr[dt] = load16_stream(base + 256 * dt);
+  };
+
+  int it = first_it;
+  Blocks<4> cur = table_blocks<4>(p, table, it, t1);
+  Blocks<4> nxt = table_blocks<4>(p, table, it + step, t1);
+  uint32_t kw[32];
+  u32x4 vr[8];
+  if (it < t1) {
+    load_k(kw, kbase0 + (int64_t)max(pick(cur, kb), 0) * pool_stride);
+    load_v(vr, vbase0 + (int64_t)max(pick(cur, kg), 0) * pool_stride);
+  }
+
+#pragma unroll 1
+  for (; it < t1; it += step) {
+    const Blocks<4> nn = table_blocks<4>(p, table, it + 2 * step, t1);
+    const bool has_next = it + step < t1;
+
+    // ---- q.k: 4 tiles (token i of each quad) x 4 MFMA steps ----
+    f4 s[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s[i] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int sk = 0; sk < 4; ++sk) {
+      uint32_t a[4][4];   // [tile][f16 pair]
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf) {
+        const uint32_t* w = &kw[8 * sk + 4 * hf];   // rows 32 sk + 16 hf + 4 c + kg
+        const uint32_t x0 = __builtin_amdgcn_perm(w[1], w[0], 0x05010400u);  // tokens 0, 1
+        const uint32_t x1 = __builtin_amdgcn_perm(w[1], w[0], 0x07030602u);  // tokens 2, 3
+        const uint32_t y0 = __builtin_amdgcn_perm(w[3], w[2], 0x05010400u);
+        const uint32_t y1 = __builtin_amdgcn_perm(w[3], w[2], 0x07030602u);
+        a[0][2 * hf] = f8x2<false>(x0); a[0][2 * hf + 1] = f8x2<false>(y0);
+        a[1][2 * hf] = f8x2<true>(x0);  a[1][2 * hf + 1] = f8x2<true>(y0);
+        a[2][2 * hf] = f8x2<false>(x1); a[2][2 * hf + 1] = f8x2<false>(y1);
+        a[3][2 * hf] = f8x2<true>(x1);  a[3][2 * hf + 1] = f8x2<true>(y1);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) s[i] = mma<Kind::F16>(a[i][0], a[i][1], a[i][2], a[i][3], qb[sk], s[i]);
+    }
+    if (has_next) load_k(kw, kbase0 + (int64_t)max(pick(nxt, kb), 0) * pool_stride);
+
+    // ---- softmax: lane (m, kg) owns head m, tokens 4 r + i of block kg ----
+    const int ph_v = pick(cur, kg);
+    const int n_ok = ph_v < 0 ? 0 : min(max(t1 - (it + 16 * kg), 0), 16);
+    float sc[4][4];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        sc[i][r] = (4 * r + i < n_ok) ? s[i][r] * qk_scale : -INFINITY;
+        mx = fmaxf(mx, sc[i][r]);
+      }
+    st.update_max(mx);
+    float pw[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        pw[i][r] = (4 * r + i < n_ok) ? __builtin_amdgcn_exp2f(sc[i][r] - st.m_run) : 0.f;
+        st.l_lane += pw[i][r];
+      }
+    // P^T operands: MFMA h takes tokens 8 h .. 8 h + 7 = (r = 2 h, 2 h + 1) x (i = 0 .. 3)
+    u4v pb[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      h8 v;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = (_Float16)pw[e & 3][2 * h + (e >> 2)];
+      pb[h] = __builtin_bit_cast(u4v, v);
+    }
+
+    // ---- p.v: tokens past t1 and holes may hold any byte (NaN codes too) ----
+    if (__builtin_amdgcn_ballot_w64(n_ok < 16) != 0) {
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) vr[dt] = keep_bytes(vr[dt], n_ok);
+    }
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+      const u32x4 v = vr[dt];
+      st.o[dt] = mma<Kind::F16>(f8x2<false>(v.x), f8x2<true>(v.x), f8x2<false>(v.y), f8x2<true>(v.y), pb[0],
+                                st.o[dt]);
+      st.o[dt] = mma<Kind::F16>(f8x2<false>(v.z), f8x2<true>(v.z), f8x2<false>(v.w), f8x2<true>(v.w), pb[1],
+                                st.o[dt]);
+    }
+    if (has_next) load_v(vr, vbase0 + (int64_t)max(pick(nxt, kg), 0) * pool_stride);
+    cur = nxt;
+    nxt = nn;
+  }
+  st.store(p.v_scale, m, kg, s_acc_w, s_m_w, s_l_w);
+}
+
+// ---- 2-byte KV (f16 / bf16, q of the same type): 32 tokens (2 blocks) per iteration ----
+//
+// K: the A row m is token pair m (block m >> 3, tokens 2 (m & 7), +1) and
+// tile i takes token i of every pair.  Lane (m, kg) reads 32 dwords (128
+// contiguous bytes per block for each j); v_perm_b32 of the dwords of rows
+// (e, e + 1) gives the (d, d') pair of the pair's first (low halves) or
+// second (high halves) token: 1 perm per operand dword.
+// Scores: lane (m, kg) holds head m, tokens 8 (kg & 1) + 2 r + i of block
+// kg >> 1, i.e. the run of 8 tokens that is k group kg of the p.v MFMA.
+// V: lane (m, kg) loads the 16 bytes of that run, row d = 16 dt + m.
+template <Kind KV>
+__device__ __forceinline__ void mfma2_wave(const Params& p, int seq, int kvh, int hs, int first_it, int t1,
+                                           int step, float* s_acc_w, float* s_m_w, float* s_l_w) {
+  constexpr int kBlockBytes = kHead * 16 * 2;
+  const int lane = threadIdx.x % kWave;
+  const int m = lane & 15, kg = lane >> 4;
+
+  // ---- q of head column m: dword e2 of step s = dims (32 s + 8 e2 + kg, +4) ----
+  const int gi = hs * kHeads + m;
+  const bool hv = gi < p.group;
+  const int head = hv ? head_of(p, kvh, gi) : 0;
+  const uint16_t* qrow = (const uint16_t*)p.q + ((int64_t)seq * p.num_heads + head) * kHead;
+  u4v qb[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s)
+#pragma unroll
+    for (int e2 = 0; e2 < 4; ++e2) {
+      const uint32_t lo = hv ? qrow[32 * s + 8 * e2 + kg] : 0u;
+      const uint32_t hi = hv ? qrow[32 * s + 8 * e2 + 4 + kg] : 0u;
+      qb[s][e2] = lo | (hi << 16);
+    }
+
+  State st;
+  st.init();
+
+  const int32_t* table = p.block_tables + (int64_t)seq * p.max_blocks_per_seq;
+  const int64_t pool_stride = (int64_t)p.num_kv_heads * kBlockBytes;
+  const char* kbase0 = p.k_cache + (int64_t)kvh * kBlockBytes + 32 * kg + 4 * (m & 7);
+  const char* vbase0 = p.v_cache + (int64_t)kvh * kBlockBytes + 32 * m + 16 * (kg & 1);
+  const int kb = m >> 3, vb = kg >> 1;   // blocks of this lane's K pair and V run
+  auto load_k = [&](uint32_t (&kw)[32], const char* base) {
+#pragma unroll
+    for (int j = 0; j < 32; ++j) kw[j] = ld_nt(base + 128 * j);
+  };
+  auto load_v = [&](u32x4 (&vr)[8], const char* base) {
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) vr[dt] = load16_stream(base + 512 * dt);
+  };
+
+  int it = first_it;
+  Blocks<2> cur = table_blocks<2>(p, table, it, t1);
+  Blocks<2> nxt = table_blocks<2>(p, table, it + step, t1);
+  uint32_t kw[32];
+  u32x4 vr[8];
+  if (it < t1) {
+    load_k(kw, kbase0 + (int64_t)max(pick(cur, kb), 0) * pool_stride);
+    load_v(vr, vbase0 + (int64_t)max(pick(cur, vb), 0) * pool_stride);
+  }
+
+#pragma unroll 1
+  for (; it < t1; it += step) {
+    const Blocks<2> nn = table_blocks<2>(p, table, it + 2 * step, t1);
+    const bool has_next = it + step < t1;
+
+    // ---- q.k: 2 tiles (token i of each pair) x 4 MFMA steps ----
+    f4 s[2] = {f4{0.f, 0.f, 0.f, 0.f}, f4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int sk = 0; sk < 4; ++sk) {
+      const uint32_t* w = &kw[8 * sk];            // rows 32 sk + 4 e + kg
+      uint32_t a[2][4];
+#pragma unroll
+      for (int e2 = 0; e2 < 4; ++e2) {
+        a[0][e2] = __builtin_amdgcn_perm(w[2 * e2 + 1], w[2 * e2], 0x05040100u);  // first token
+        a[1][e2] = __builtin_amdgcn_perm(w[2 * e2 + 1], w[2 * e2], 0x07060302u);  // second token
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i) s[i] = mma<KV>(a[i][0], a[i][1], a[i][2], a[i][3], qb[sk], s[i]);
+    }
+    if (has_next) load_k(kw, kbase0 + (int64_t)max(pick(nxt, kb), 0) * pool_stride);
+
+    // ---- softmax: lane (m, kg) owns head m, tokens 8 (kg & 1) + 2 r + i of block kg >> 1 ----
+    const int ph_v = pick(cur, vb);
+    const int n_ok = ph_v < 0 ? 0 : min(max(t1 - (it + 16 * vb), 0), 16);
+    const int run0 = 8 * (kg & 1);
+    float sc[2][4];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        sc[i][r] = (run0 + 2 * r + i < n_ok) ? s[i][r] * p.qk_scale : -INFINITY;
+        mx = fmaxf(mx, sc[i][r]);
+      }
+    st.update_max(mx);
+    u4v pb;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float p0 = (run0 + 2 * r < n_ok) ? __builtin_amdgcn_exp2f(sc[0][r] - st.m_run) : 0.f;
+      const float p1 = (run0 + 2 * r + 1 < n_ok) ? __builtin_amdgcn_exp2f(sc[1][r] - st.m_run) : 0.f;
+      st.l_lane += p0 + p1;
+      pb[r] = Dot2<KV>::pack(p0, p1);
+    }
+
+    // ---- p.v: slots past t1 and holes may hold anything, NaN included ----
+    if (__builtin_amdgcn_ballot_w64(n_ok < 16) != 0) {
+      const int keep = min(max(n_ok - run0, 0), 8);
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) vr[dt] = keep_halves(vr[dt], keep);
+    }
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt)
+      st.o[dt] = mma<KV>(vr[dt].x, vr[dt].y, vr[dt].z, vr[dt].w, pb, st.o[dt]);
+    if (has_next) load_v(vr, vbase0 + (int64_t)max(pick(nxt, vb), 0) * pool_stride);
+    cur = nxt;
+    nxt = nn;
+  }
+  st.store(1.f, m, kg, s_acc_w, s_m_w, s_l_w);
+}
+
+// One workgroup of NW wavefronts over (sequence, kv head, 16-head slice,
+// partition): the wavefronts stride over the partition's iterations and
+// are merged in LDS (smem: NW x 16 x 128 + 2 x NW x 16 floats).
+template <Kind KV, Kind QK, Kind PO, int NW, bool FINAL>
+__device__ __forceinline__ void decode_workgroup(const Params& p, int seq, int kvh, int hs, int part, int t0,
+                                                 int t1, float* s_acc, float* s_m, float* s_l) {
+  constexpr int TPI = tokens_per_iteration<KV>();
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+  float* acc_w = s_acc + wave * kHeads * kHead;
+  if constexpr (KV == Kind::FP8)
+    fp8_wave<QK>(p, seq, kvh, hs, t0 + wave * TPI, t1, NW * TPI, acc_w, s_m + wave * kHeads, s_l + wave * kHeads);
+  else
+    mfma2_wave<KV>(p, seq, kvh, hs, t0 + wave * TPI, t1, NW * TPI, acc_w, s_m + wave * kHeads,
+                   s_l + wave * kHeads);
+  __syncthreads();
+  combine_waves<QK, PO, kHead, FINAL, kHeads>(p, NW, s_m, s_l, s_acc, seq, kvh, hs, part, tid, NW * kWave);
+}
+
+}  // namespace mw
+}  // namespace tl

@@ -21,10 +21,11 @@
 //   * O += P V on the same MFMA: the weights leave the S^T accumulator as
 //     keys {16 st + 4 g + i, 16 st + 8 + 4 g + i} for lane group g, which is
 //     used as the k order of step st; V is read from LDS in that order.
-// Decode rows run the 2-byte decode wavefront (tl_decode_wave.hpp), one
-// workgroup per (sequence, kv head, head slice), as a second kernel of the
-// same call on the same stream (one kernel for both would be sized by the
-// decode path's registers on top of the prefill path's).
+// Decode rows run the decode wavefronts (tl_mfma_wave.hpp for block_size 16,
+// tl_decode_wave.hpp otherwise), one workgroup per (sequence, kv head, head
+// slice), as a second kernel of the same call on the same stream (one
+// kernel for both would be sized by the decode path's registers on top of
+// the prefill path's).
 //
 // Nearest reference analogues: the per-token prefill of cuda_engine.cpp:842-860
 // and the dense attention of megakernel.cu:267-351; the reference has no
@@ -32,6 +33,7 @@
 #include "tl_decode_wave.hpp"
 #include "tl_device.hpp"
 #include "tl_internal.hpp"
+#include "tl_mfma_wave.hpp"
 
 namespace tl {
 
@@ -329,17 +331,23 @@ __global__ __launch_bounds__(NW * kWave) void prefill_kernel(PrefillParams pp) {
   }
 }
 
-// Decode rows (q_len == 1) of a mixed batch: the 2-byte decode wavefronts,
-// one workgroup per (sequence, kv head, head slice), q / out row cu_q_lens[s].
+// q heads per decode-row workgroup: the matrix-core wavefronts serve 16
+// (block_size 16), the dot-product wavefronts 4.
+template <int BS> constexpr int decode_row_heads() { return BS == 16 ? mw::kHeads : kWaveHeads; }
+
+// Decode rows (q_len == 1) of a mixed batch, one workgroup per (sequence,
+// kv head, head slice), q / out row cu_q_lens[s]: the matrix-core decode
+// wavefronts (tl_mfma_wave.hpp) for block_size 16, so a GQA group of up to
+// 16 heads reads its KV once, the 2-byte dot-product wavefronts otherwise.
 template <Kind KV, int BS, int NW>
 __global__ __launch_bounds__(NW * kWave) void prefill_decode_kernel(PrefillParams pp) {
-  __shared__ __attribute__((aligned(16))) uint32_t s_p[NW][4][kWaveHeads][4];
-  __shared__ float s_m[NW][kWaveHeads], s_l[NW][kWaveHeads];
-  __shared__ float s_acc[NW][kWaveHeads][kPfHead];
+  constexpr int GT = decode_row_heads<BS>();
+  __shared__ __attribute__((aligned(16))) float s_acc[NW * GT * kPfHead];
+  __shared__ float s_m[NW * GT], s_l[NW * GT];
   const Params& p = pp.base;
-  const int tid = threadIdx.x, wave = tid / kWave;
+  const int slices = (p.group + GT - 1) / GT;
   int b = blockIdx.x;
-  const int hs = b % p.head_slices; b /= p.head_slices;
+  const int hs = b % slices; b /= slices;
   const int kvh = b % p.num_kv_heads, seq = pp.dec_first + b / p.num_kv_heads;
   const int q0 = pp.cu_q_lens[seq];
   if (pp.cu_q_lens[seq + 1] - q0 != 1) return;
@@ -348,18 +356,25 @@ __global__ __launch_bounds__(NW * kWave) void prefill_decode_kernel(PrefillParam
   const int64_t shift = (int64_t)(q0 - seq) * p.num_heads * kPfHead * 2;   // q / out row q0
   pd.q = (const char*)p.q + shift;
   pd.out = (char*)p.out + shift;
-  decode2_wave<KV, kPfHead, BS>(pd, seq, kvh, hs, wave * 32, L, NW * 32, &s_p[wave][0][0][0],
-                                &s_acc[wave][0][0], &s_m[wave][0], &s_l[wave][0]);
-  __syncthreads();
-  combine_waves<KV, Kind::F32, kPfHead, true>(pd, NW, &s_m[0][0], &s_l[0][0], &s_acc[0][0][0], seq, kvh,
-                                              hs, 0, tid, NW * kWave);
+  pd.head_slices = slices;
+  if constexpr (BS == 16) {
+    mw::decode_workgroup<KV, KV, Kind::F32, NW, true>(pd, seq, kvh, hs, 0, 0, L, s_acc, s_m, s_l);
+  } else {
+    __shared__ __attribute__((aligned(16))) uint32_t s_p[NW][4][kWaveHeads][4];
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+    decode2_wave<KV, kPfHead, BS>(pd, seq, kvh, hs, wave * 32, L, NW * 32, &s_p[wave][0][0][0],
+                                  &s_acc[wave * GT * kPfHead], &s_m[wave * GT], &s_l[wave * GT]);
+    __syncthreads();
+    combine_waves<KV, Kind::F32, kPfHead, true>(pd, NW, s_m, s_l, s_acc, seq, kvh, hs, 0, tid, NW * kWave);
+  }
 }
 
 template <Kind KV, int BS>
 int launch_prefill_t(const PrefillParams& pp, unsigned grid, hipStream_t stream) {
   constexpr int NW = 8, NWD = 8;
   const Params& p = pp.base;
-  const unsigned dgrid = (unsigned)((pp.num_seqs - pp.dec_first) * p.num_kv_heads * p.head_slices);
+  constexpr int GT = decode_row_heads<BS>();
+  const unsigned dgrid = (unsigned)((pp.num_seqs - pp.dec_first) * p.num_kv_heads * ((p.group + GT - 1) / GT));
   if (dgrid > 0)
     hipLaunchKernelGGL((prefill_decode_kernel<KV, BS, NWD>), dim3(dgrid), dim3(NWD * kWave), 0, stream, pp);
   if (grid > 0)
