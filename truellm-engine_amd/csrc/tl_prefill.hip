@@ -9,8 +9,11 @@
 // rows), a row being one (query, q head of the GQA group) pair, so every K/V
 // block fetched serves all q heads of the group.  Per 32-key iteration:
 //   * the workgroup copies the keys' K (transposed to [key][channel], rows
-//     padded to 136 halves) and V ([block][channel][slot], as in the pool)
-//     into a double-buffered LDS stage;
+//     padded to 136 halves) and V ([channel][key slot], the key order of the
+//     PV operand, rows padded to 40 halves) into a double-buffered LDS
+//     stage; each wavefront copies one 8-key run for half of the channels,
+//     laid out so its LDS writes and the MFMA operand reads are free of bank
+//     conflicts;
 //   * each wavefront (32 rows) forms S^T = K Q^T with
 //     v_mfma_f32_32x32x16_{bf16,f16}: A = K (rows: keys, k: channels) read
 //     from LDS, B = Q^T held in registers for the whole launch.  Lane l then
@@ -46,6 +49,17 @@ constexpr int kPfHead = 128;
 constexpr int kPfRows = 32;          // rows per wavefront
 constexpr int kPfKeys = 32;          // keys per iteration
 constexpr int kKtStride = 136;       // halves per key row of the transposed K stage
+constexpr int kVStride = 40;         // halves per channel row of the V stage (32 keys + pad)
+
+// Slot of key k (of an iteration's 32) in a V stage row: the middle two
+// 4-key quarters of every 16 keys are swapped, so the 8 keys a PV MFMA step
+// takes from lane group g (16 st + 4 g + i and 16 st + 8 + 4 g + i) sit
+// together at 16 st + 8 g and are one 16-byte read.  With 80-byte rows the
+// 16 lanes of one ds_read_b128 cycle hit 16 distinct 4-bank groups.
+__device__ __forceinline__ int v_slot(int k) {
+  const int q = (k >> 2) & 3;
+  return (k & ~15) + 4 * (((q & 1) << 1) | (q >> 1)) + (k & 3);
+}
 constexpr float kLazyRescale = 8.f;  // log2 units
 
 template <Kind KV> struct Mfma32;
@@ -92,7 +106,7 @@ template <int NW, int BS>
 struct PrefillSmem {
   struct {
     uint16_t kt[2][kPfKeys * kKtStride];          // [key][channel] (+8 pad)
-    uint16_t v[2][kPfHead * kPfKeys];             // [block][channel][slot]
+    uint16_t v[2][kPfHead * kVStride];            // [channel][v_slot(key)] (+8 pad)
     float row[NW][kPfRows];                       // per-row exchange (alpha, l)
   } pf;
 };
@@ -108,11 +122,6 @@ template <Kind KV, int BS, int NW>
 __global__ __launch_bounds__(NW * kWave) void prefill_kernel(PrefillParams pp) {
   static_assert(BS == 16 || BS == 32, "block size");
   constexpr int BPI = kPfKeys / BS;                    // pool blocks per iteration
-  constexpr int CPB = kPfHead * BS / 8;                // 16-byte chunks per block (K or V)
-  constexpr int CHUNKS = BPI * CPB;                    // per tensor per iteration (512)
-  constexpr int NT = NW * kWave;
-  static_assert(CHUNKS % NT == 0, "whole chunks per thread");
-  constexpr int CPT = CHUNKS / NT;                     // K (and V) chunks per thread
   using M = Mfma32<KV>;
   __shared__ __attribute__((aligned(16))) PrefillSmem<NW, BS> sm;
 
@@ -161,48 +170,47 @@ __global__ __launch_bounds__(NW * kWave) void prefill_kernel(PrefillParams pp) {
   const uint16_t* kpool = (const uint16_t*)p.k_cache;
   const uint16_t* vpool = (const uint16_t*)p.v_cache;
 
-  // this thread's chunks: chunk ci = tid + NT * j -> block ci / CPB, channel
-  // (ci % CPB) / (BS / 8), slots 8 * (ci % (BS / 8)) .. +7
-  u32x4 kr[CPT], vr[CPT];
-  auto fetch = [&](int it) {
+  // Staging: wavefront w copies the 8-key run (block s_blk, keys s8 .. s8+7)
+  // of the iteration with run index w >> 1, for half of the channels.  K:
+  // channel 2 lane + (w & 1), so each transposed 2-byte LDS write of a
+  // wavefront hits 64 consecutive dwords; V: channel lane + 64 (w & 1).  The
+  // run's block id is wave-uniform (a scalar table read).
+  static_assert(2 * BPI * (BS / 8) == NW, "one (run, channel half) per wavefront");
+  const int run_id = wave >> 1;
+  const int s_blk = run_id / (BS / 8), s8 = 8 * (run_id % (BS / 8));
+  const int k_ch = 2 * lane + (wave & 1), v_ch = lane + 64 * (wave & 1);
+  auto fetch = [&](int it, u32x4& kr, u32x4& vr) {
+    const int key0 = it * kPfKeys + s_blk * BS + s8;
+    const int pb = key0 < kend ? block_of(p, table, it * BPI + s_blk) : -1;
+    if (pb >= 0) {
+      const int64_t base = ((int64_t)pb * p.num_kv_heads + kvh) * head_stride + s8;
+      kr = load16_stream(kpool + base + (int64_t)k_ch * BS);
+      u4v v = __builtin_bit_cast(u4v, load16_stream(vpool + base + (int64_t)v_ch * BS));
+      // slots at or past the sequence end may hold anything: zero their V
+      if (key0 + 8 > L) {
 #pragma unroll
-    for (int j = 0; j < CPT; ++j) {
-      const int ci = tid + NT * j;
-      const int blk = ci / CPB, ch = (ci % CPB) / (BS / 8), s8 = 8 * (ci % (BS / 8));
-      const int key0 = it * kPfKeys + blk * BS + s8;
-      const int pb = key0 < kend ? block_of(p, table, it * BPI + blk) : -1;
-      if (pb >= 0) {
-        const int64_t off = ((int64_t)pb * p.num_kv_heads + kvh) * head_stride + (int64_t)ch * BS + s8;
-        kr[j] = load16_stream(kpool + off);
-        u4v v = __builtin_bit_cast(u4v, load16_stream(vpool + off));
-        // slots at or past the sequence end may hold anything: zero their V
-        if (key0 + 8 > L) {
-#pragma unroll
-          for (int w = 0; w < 4; ++w)
-            if (key0 + 2 * w >= L) v[w] = 0u;
-            else if (key0 + 2 * w + 1 >= L) v[w] &= 0xFFFFu;
-        }
-        vr[j] = __builtin_bit_cast(u32x4, v);
-      } else {
-        kr[j] = u32x4{0u, 0u, 0u, 0u};
-        vr[j] = u32x4{0u, 0u, 0u, 0u};
+        for (int w = 0; w < 4; ++w)
+          if (key0 + 2 * w >= L) v[w] = 0u;
+          else if (key0 + 2 * w + 1 >= L) v[w] &= 0xFFFFu;
       }
+      vr = __builtin_bit_cast(u32x4, v);
+    } else {
+      kr = u32x4{0u, 0u, 0u, 0u};
+      vr = u32x4{0u, 0u, 0u, 0u};
     }
   };
-  auto stage = [&](int st) {
+  auto stage = [&](int st, const u32x4& kr, const u32x4& vr) {
+    const int kb = s_blk * BS + s8;                      // the run's first key in the iteration
+    uint16_t* kt = &sm.pf.kt[st][kb * kKtStride + k_ch];
+    const u4v kv = __builtin_bit_cast(u4v, kr);
 #pragma unroll
-    for (int j = 0; j < CPT; ++j) {
-      const int ci = tid + NT * j;
-      const int blk = ci / CPB, ch = (ci % CPB) / (BS / 8), s8 = 8 * (ci % (BS / 8));
-      uint16_t* kt = &sm.pf.kt[st][(blk * BS + s8) * kKtStride + ch];
-      const u4v kv = __builtin_bit_cast(u4v, kr[j]);
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        kt[(2 * w) * kKtStride] = (uint16_t)(kv[w] & 0xFFFFu);
-        kt[(2 * w + 1) * kKtStride] = (uint16_t)(kv[w] >> 16);
-      }
-      *reinterpret_cast<u32x4*>(&sm.pf.v[st][(blk * kPfHead + ch) * BS + s8]) = vr[j];
+    for (int w = 0; w < 4; ++w) {
+      kt[(2 * w) * kKtStride] = (uint16_t)(kv[w] & 0xFFFFu);
+      kt[(2 * w + 1) * kKtStride] = (uint16_t)(kv[w] >> 16);
     }
+    uint16_t* vrow = &sm.pf.v[st][v_ch * kVStride];
+    *reinterpret_cast<uint2*>(vrow + v_slot(kb)) = uint2{vr.x, vr.y};
+    *reinterpret_cast<uint2*>(vrow + v_slot(kb + 4)) = uint2{vr.z, vr.w};
   };
 
   f16v o[4];
@@ -211,15 +219,21 @@ __global__ __launch_bounds__(NW * kWave) void prefill_kernel(PrefillParams pp) {
   float m_used = -INFINITY, l_part = 0.f;
   float* s_row = &sm.pf.row[wave][0];
 
+  // Two register sets hold fetched, not yet staged iterations: iteration
+  // it + 2 is fetched while it computes and it + 1 waits to be staged.
+  // Keys of an iteration entirely at or below the wavefront's first query
+  // position, in blocks that exist, need no mask.
+  const int wmin_pos = L - ql + wrow0 / p.group;
+  u32x4 k_set0, v_set0, k_set1, v_set1;
   if (n_it > 0) {
-    fetch(0);
-    stage(0);
+    fetch(0, k_set0, v_set0);
+    stage(0, k_set0, v_set0);
   }
+  if (n_it > 1) fetch(1, k_set1, v_set1);
   __syncthreads();
-#pragma unroll 1
-  for (int it = 0; it < n_it; ++it) {
+  auto iteration = [&](int it, u32x4& k_free, u32x4& v_free, const u32x4& k_next, const u32x4& v_next) {
     const int st = it & 1;
-    if (it + 1 < n_it) fetch(it + 1);
+    if (it + 2 < n_it) fetch(it + 2, k_free, v_free);
     const int k0 = it * kPfKeys;
     if (k0 < wkend) {
       // ---- S^T = K Q^T (lane: keys 8 j + 4 g + i of row my_row) ----
@@ -230,16 +244,28 @@ __global__ __launch_bounds__(NW * kWave) void prefill_kernel(PrefillParams pp) {
         sa = M::mma(*reinterpret_cast<const u32x4*>(ktw + 16 * ks), qb[ks], sa);
       // ---- mask (causal; table holes), row max, lazy rescale ----
       bool blk_ok[BPI];
+      bool all_ok = true;
 #pragma unroll
-      for (int bi = 0; bi < BPI; ++bi) blk_ok[bi] = block_of(p, table, it * BPI + bi) >= 0;
+      for (int bi = 0; bi < BPI; ++bi) {
+        blk_ok[bi] = block_of(p, table, it * BPI + bi) >= 0;
+        all_ok = all_ok && blk_ok[bi];
+      }
       float sc[16];
       float mx = -INFINITY;
+      if (all_ok && k0 + kPfKeys - 1 <= wmin_pos) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int kk = 8 * (r >> 2) + 4 * g + (r & 3);
-        const bool ok = k0 + kk <= pos && blk_ok[(8 * (r >> 2)) / BS];
-        sc[r] = ok ? sa[r] * p.qk_scale : -INFINITY;
-        mx = fmaxf(mx, sc[r]);
+        for (int r = 0; r < 16; ++r) {
+          sc[r] = sa[r] * p.qk_scale;
+          mx = fmaxf(mx, sc[r]);
+        }
+      } else {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int kk = 8 * (r >> 2) + 4 * g + (r & 3);
+          const bool ok = k0 + kk <= pos && blk_ok[(8 * (r >> 2)) / BS];
+          sc[r] = ok ? sa[r] * p.qk_scale : -INFINITY;
+          mx = fmaxf(mx, sc[r]);
+        }
       }
       {
         const auto sw = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, mx),
@@ -291,18 +317,21 @@ __global__ __launch_bounds__(NW * kWave) void prefill_kernel(PrefillParams pp) {
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
           const int ch = 32 * c + c32;
-          const int ka = 16 * st2 + 4 * g;                 // first key of the step's slots 0-3
-          const uint16_t* vrow = &sm.pf.v[st][((ka / BS) * kPfHead + ch) * BS + (ka % BS)];
-          const uint2 lo = *reinterpret_cast<const uint2*>(vrow);
-          const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 8);
-          const u32x4 vb = {lo.x, lo.y, hi.x, hi.y};
+          // slots 0-3: keys 16 st2 + 4 g + i, slots 4-7: keys 16 st2 + 8 + 4 g + i
+          const u32x4 vb = *reinterpret_cast<const u32x4*>(&sm.pf.v[st][ch * kVStride + 16 * st2 + 8 * g]);
           o[c] = M::mma(pa, vb, o[c]);
           if constexpr (M::kSplitP) o[c] = M::mma(pl, vb, o[c]);
         }
       }
     }
-    if (it + 1 < n_it) stage(st ^ 1);
+    if (it + 1 < n_it) stage(st ^ 1, k_next, v_next);
     __syncthreads();
+  };
+#pragma unroll 1
+  for (int it = 0; it < n_it; it += 2) {
+    iteration(it, k_set0, v_set0, k_set1, v_set1);
+    if (it + 1 >= n_it) break;
+    iteration(it + 1, k_set1, v_set1, k_set0, v_set0);
   }
 
   // ---- normalise and store: lane holds rows 8 j + 4 g + i, channels 32 c + c32 ----
