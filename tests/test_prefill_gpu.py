@@ -181,3 +181,8 @@ def test_empty_and_invalid_arguments():
     with pytest.raises(tla.TLError) as e:
         tla.chunked_prefill(bad, out, q, cu, k, k, bt, sl, 4)
     assert e.value.code == tla.ERR_NOT_IMPLEMENTED
+    for scale in (0.0, -0.1, float("inf"), float("nan")):
+        neg = tla.make_prefill_desc(q, k, bt, 1, 2, scale)
+        with pytest.raises(tla.TLError) as e:
+            tla.chunked_prefill(neg, out, q, cu, k, k, bt, sl, 4)
+        assert e.value.code == tla.ERR_INVALID_ARGUMENT

@@ -598,6 +598,9 @@ int tl_chunked_prefill(const tl_prefill_desc* d, void* out, const void* q, const
   if (d->num_prefill_seqs < 0 || d->num_prefill_seqs > d->num_seqs)
     return fail(TL_ERR_INVALID_ARGUMENT, "num_prefill_seqs=%d outside [0, %d]", d->num_prefill_seqs,
                 d->num_seqs);
+  // the prefill kernel takes the row max of unscaled scores
+  if (!(d->scale > 0.f) || !(d->scale < INFINITY))
+    return fail(TL_ERR_INVALID_ARGUMENT, "scale=%g must be positive and finite", (double)d->scale);
   if (d->num_seqs == 0 || total_q == 0) return ok();
   if (max_q_len > total_q)
     return fail(TL_ERR_INVALID_ARGUMENT, "max_q_len=%d > total_q=%d", max_q_len, total_q);

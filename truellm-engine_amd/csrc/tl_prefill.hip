@@ -7,23 +7,25 @@
 //
 // Prefill work item: one workgroup per (sequence, kv head, tile of NW * 32
 // rows), a row being one (query, q head of the GQA group) pair, so every K/V
-// block fetched serves all q heads of the group.  Per 32-key iteration:
+// block fetched serves all q heads of the group.  Per 64-key iteration:
 //   * the workgroup copies the keys' K (transposed to [key][channel], rows
 //     padded to 136 halves) and V ([channel][key slot], the key order of the
-//     PV operand, rows padded to 40 halves) into a double-buffered LDS
-//     stage; each wavefront copies one 8-key run for half of the channels,
+//     PV operand, rows padded to 72 halves) into a double-buffered LDS
+//     stage; each wavefront copies two 8-key runs for half of the channels,
 //     laid out so its LDS writes and the MFMA operand reads are free of bank
 //     conflicts;
-//   * each wavefront (32 rows) forms S^T = K Q^T with
+//   * each wavefront (32 rows) forms two 32-key tiles of S^T = K Q^T with
 //     v_mfma_f32_32x32x16_{bf16,f16}: A = K (rows: keys, k: channels) read
 //     from LDS, B = Q^T held in registers for the whole launch.  Lane l then
-//     holds 16 keys of row l % 32, so the row max needs one permlane32 swap;
+//     holds 16 keys per tile of row l % 32, so the row max needs one
+//     permlane32 swap;
 //   * online softmax with lazy rescaling: the running max is only raised
 //     when a row's new max exceeds it by more than 8 (log2 units), so the
 //     weights stay below 2^8 and the O accumulators are rescaled rarely;
-//   * O += P V on the same MFMA: the weights leave the S^T accumulator as
-//     keys {16 st + 4 g + i, 16 st + 8 + 4 g + i} for lane group g, which is
-//     used as the k order of step st; V is read from LDS in that order.
+//   * O += P V on the same MFMA: the weights leave the S^T accumulator of
+//     tile t as keys {32 t + 16 s + 4 g + i, 32 t + 16 s + 8 + 4 g + i} for
+//     lane group g, which is used as the k order of step s; V is read from
+//     LDS in that order.
 // Decode rows run the decode wavefronts (tl_mfma_wave.hpp for block_size 16,
 // tl_decode_wave.hpp otherwise), one workgroup per (sequence, kv head, head
 // slice), as a second kernel of the same call on the same stream (one
@@ -47,14 +49,15 @@ typedef unsigned u4v __attribute__((ext_vector_type(4)));
 
 constexpr int kPfHead = 128;
 constexpr int kPfRows = 32;          // rows per wavefront
-constexpr int kPfKeys = 32;          // keys per iteration
+constexpr int kPfKeys = 64;          // keys per iteration
+constexpr int KT = kPfKeys / 32;     // 32-key S tiles per iteration
 constexpr int kKtStride = 136;       // halves per key row of the transposed K stage
-constexpr int kVStride = 40;         // halves per channel row of the V stage (32 keys + pad)
+constexpr int kVStride = 72;         // halves per channel row of the V stage (64 keys + pad)
 
-// Slot of key k (of an iteration's 32) in a V stage row: the middle two
+// Slot of key k (of an iteration's 64) in a V stage row: the middle two
 // 4-key quarters of every 16 keys are swapped, so the 8 keys a PV MFMA step
-// takes from lane group g (16 st + 4 g + i and 16 st + 8 + 4 g + i) sit
-// together at 16 st + 8 g and are one 16-byte read.  With 80-byte rows the
+// takes from lane group g (16 s + 4 g + i and 16 s + 8 + 4 g + i) sit
+// together at 16 s + 8 g and are one 16-byte read.  With 144-byte rows the
 // 16 lanes of one ds_read_b128 cycle hit 16 distinct 4-bank groups.
 __device__ __forceinline__ int v_slot(int k) {
   const int q = (k >> 2) & 3;
@@ -170,47 +173,56 @@ __global__ __launch_bounds__(NW * kWave) void prefill_kernel(PrefillParams pp) {
   const uint16_t* kpool = (const uint16_t*)p.k_cache;
   const uint16_t* vpool = (const uint16_t*)p.v_cache;
 
-  // Staging: wavefront w copies the 8-key run (block s_blk, keys s8 .. s8+7)
-  // of the iteration with run index w >> 1, for half of the channels.  K:
-  // channel 2 lane + (w & 1), so each transposed 2-byte LDS write of a
-  // wavefront hits 64 consecutive dwords; V: channel lane + 64 (w & 1).  The
-  // run's block id is wave-uniform (a scalar table read).
-  static_assert(2 * BPI * (BS / 8) == NW, "one (run, channel half) per wavefront");
-  const int run_id = wave >> 1;
-  const int s_blk = run_id / (BS / 8), s8 = 8 * (run_id % (BS / 8));
+  // Staging: an iteration's 64 keys are 8 runs of 8 (run r: keys 8 r .. 8 r
+  // + 7 of the iteration).  Wavefront w copies runs (w >> 1) and (w >> 1) + 4
+  // for half of the channels.  K: channel 2 lane + (w & 1), so each
+  // transposed 2-byte LDS write of a wavefront hits 64 consecutive dwords;
+  // V: channel lane + 64 (w & 1).  Block ids are wave-uniform (scalar table
+  // reads).
+  constexpr int RPW = 2 * (kPfKeys / 8) / NW;          // runs per wavefront
+  static_assert(RPW * NW == 2 * (kPfKeys / 8), "runs x channel halves per wavefront");
   const int k_ch = 2 * lane + (wave & 1), v_ch = lane + 64 * (wave & 1);
-  auto fetch = [&](int it, u32x4& kr, u32x4& vr) {
-    const int key0 = it * kPfKeys + s_blk * BS + s8;
-    const int pb = key0 < kend ? block_of(p, table, it * BPI + s_blk) : -1;
-    if (pb >= 0) {
-      const int64_t base = ((int64_t)pb * p.num_kv_heads + kvh) * head_stride + s8;
-      kr = load16_stream(kpool + base + (int64_t)k_ch * BS);
-      u4v v = __builtin_bit_cast(u4v, load16_stream(vpool + base + (int64_t)v_ch * BS));
-      // slots at or past the sequence end may hold anything: zero their V
-      if (key0 + 8 > L) {
+  struct Fetched { u32x4 k[RPW], v[RPW]; };
+  auto run_key = [&](int j) { return 8 * ((wave >> 1) + (NW / 2) * j); };   // first key of run j
+  auto fetch = [&](int it, Fetched& f) {
 #pragma unroll
-        for (int w = 0; w < 4; ++w)
-          if (key0 + 2 * w >= L) v[w] = 0u;
-          else if (key0 + 2 * w + 1 >= L) v[w] &= 0xFFFFu;
+    for (int j = 0; j < RPW; ++j) {
+      const int kb = run_key(j);
+      const int key0 = it * kPfKeys + kb;
+      const int pb = key0 < kend ? block_of(p, table, it * BPI + kb / BS) : -1;
+      if (pb >= 0) {
+        const int64_t base = ((int64_t)pb * p.num_kv_heads + kvh) * head_stride + kb % BS;
+        f.k[j] = load16_stream(kpool + base + (int64_t)k_ch * BS);
+        u4v v = __builtin_bit_cast(u4v, load16_stream(vpool + base + (int64_t)v_ch * BS));
+        // slots at or past the sequence end may hold anything: zero their V
+        if (key0 + 8 > L) {
+#pragma unroll
+          for (int w = 0; w < 4; ++w)
+            if (key0 + 2 * w >= L) v[w] = 0u;
+            else if (key0 + 2 * w + 1 >= L) v[w] &= 0xFFFFu;
+        }
+        f.v[j] = __builtin_bit_cast(u32x4, v);
+      } else {
+        f.k[j] = u32x4{0u, 0u, 0u, 0u};
+        f.v[j] = u32x4{0u, 0u, 0u, 0u};
       }
-      vr = __builtin_bit_cast(u32x4, v);
-    } else {
-      kr = u32x4{0u, 0u, 0u, 0u};
-      vr = u32x4{0u, 0u, 0u, 0u};
     }
   };
-  auto stage = [&](int st, const u32x4& kr, const u32x4& vr) {
-    const int kb = s_blk * BS + s8;                      // the run's first key in the iteration
-    uint16_t* kt = &sm.pf.kt[st][kb * kKtStride + k_ch];
-    const u4v kv = __builtin_bit_cast(u4v, kr);
+  auto stage = [&](int st, const Fetched& f) {
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      kt[(2 * w) * kKtStride] = (uint16_t)(kv[w] & 0xFFFFu);
-      kt[(2 * w + 1) * kKtStride] = (uint16_t)(kv[w] >> 16);
+    for (int j = 0; j < RPW; ++j) {
+      const int kb = run_key(j);
+      uint16_t* kt = &sm.pf.kt[st][kb * kKtStride + k_ch];
+      const u4v kv = __builtin_bit_cast(u4v, f.k[j]);
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        kt[(2 * w) * kKtStride] = (uint16_t)(kv[w] & 0xFFFFu);
+        kt[(2 * w + 1) * kKtStride] = (uint16_t)(kv[w] >> 16);
+      }
+      uint16_t* vrow = &sm.pf.v[st][v_ch * kVStride];
+      *reinterpret_cast<uint2*>(vrow + v_slot(kb)) = uint2{f.v[j].x, f.v[j].y};
+      *reinterpret_cast<uint2*>(vrow + v_slot(kb + 4)) = uint2{f.v[j].z, f.v[j].w};
     }
-    uint16_t* vrow = &sm.pf.v[st][v_ch * kVStride];
-    *reinterpret_cast<uint2*>(vrow + v_slot(kb)) = uint2{vr.x, vr.y};
-    *reinterpret_cast<uint2*>(vrow + v_slot(kb + 4)) = uint2{vr.z, vr.w};
   };
 
   f16v o[4];
@@ -222,26 +234,31 @@ __global__ __launch_bounds__(NW * kWave) void prefill_kernel(PrefillParams pp) {
   // Two register sets hold fetched, not yet staged iterations: iteration
   // it + 2 is fetched while it computes and it + 1 waits to be staged.
   // Keys of an iteration entirely at or below the wavefront's first query
-  // position, in blocks that exist, need no mask.
+  // position, in blocks that exist, need no mask.  The scores stay unscaled
+  // until the exponent (qk_scale > 0, so the max commutes with the scale).
   const int wmin_pos = L - ql + wrow0 / p.group;
-  u32x4 k_set0, v_set0, k_set1, v_set1;
+  Fetched fs0, fs1;
   if (n_it > 0) {
-    fetch(0, k_set0, v_set0);
-    stage(0, k_set0, v_set0);
+    fetch(0, fs0);
+    stage(0, fs0);
   }
-  if (n_it > 1) fetch(1, k_set1, v_set1);
+  if (n_it > 1) fetch(1, fs1);
   __syncthreads();
-  auto iteration = [&](int it, u32x4& k_free, u32x4& v_free, const u32x4& k_next, const u32x4& v_next) {
+  auto iteration = [&](int it, Fetched& f_free, const Fetched& f_next) {
     const int st = it & 1;
-    if (it + 2 < n_it) fetch(it + 2, k_free, v_free);
+    if (it + 2 < n_it) fetch(it + 2, f_free);
     const int k0 = it * kPfKeys;
     if (k0 < wkend) {
-      // ---- S^T = K Q^T (lane: keys 8 j + 4 g + i of row my_row) ----
-      f16v sa = f16v{};
-      const uint16_t* ktw = &sm.pf.kt[st][c32 * kKtStride + 8 * g];
+      // ---- S^T = K Q^T; tile t, lane: keys 32 t + 8 j + 4 g + i of row my_row ----
+      f16v sa[KT];
 #pragma unroll
-      for (int ks = 0; ks < 8; ++ks)
-        sa = M::mma(*reinterpret_cast<const u32x4*>(ktw + 16 * ks), qb[ks], sa);
+      for (int t = 0; t < KT; ++t) {
+        sa[t] = f16v{};
+        const uint16_t* ktw = &sm.pf.kt[st][(32 * t + c32) * kKtStride + 8 * g];
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks)
+          sa[t] = M::mma(*reinterpret_cast<const u32x4*>(ktw + 16 * ks), qb[ks], sa[t]);
+      }
       // ---- mask (causal; table holes), row max, lazy rescale ----
       bool blk_ok[BPI];
       bool all_ok = true;
@@ -250,28 +267,29 @@ __global__ __launch_bounds__(NW * kWave) void prefill_kernel(PrefillParams pp) {
         blk_ok[bi] = block_of(p, table, it * BPI + bi) >= 0;
         all_ok = all_ok && blk_ok[bi];
       }
-      float sc[16];
       float mx = -INFINITY;
       if (all_ok && k0 + kPfKeys - 1 <= wmin_pos) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          sc[r] = sa[r] * p.qk_scale;
-          mx = fmaxf(mx, sc[r]);
-        }
+        for (int t = 0; t < KT; ++t)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sa[t][r]);
       } else {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int kk = 8 * (r >> 2) + 4 * g + (r & 3);
-          const bool ok = k0 + kk <= pos && blk_ok[(8 * (r >> 2)) / BS];
-          sc[r] = ok ? sa[r] * p.qk_scale : -INFINITY;
-          mx = fmaxf(mx, sc[r]);
-        }
+        for (int t = 0; t < KT; ++t)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int kk = 32 * t + 8 * (r >> 2) + 4 * g + (r & 3);
+            const bool ok = k0 + kk <= pos && blk_ok[kk / BS];
+            sa[t][r] = ok ? sa[t][r] : -INFINITY;
+            mx = fmaxf(mx, sa[t][r]);
+          }
       }
       {
         const auto sw = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, mx),
                                                          __builtin_bit_cast(unsigned, mx), false, false);
         mx = fmaxf(__builtin_bit_cast(float, (unsigned)sw[0]), __builtin_bit_cast(float, (unsigned)sw[1]));
       }
+      mx *= p.qk_scale;
       const bool raise = mx > m_used + kLazyRescale || (m_used == -INFINITY && mx != -INFINITY);
       if (__builtin_amdgcn_ballot_w64(raise)) {
         const float m_new = raise ? mx : m_used;
@@ -295,43 +313,47 @@ __global__ __launch_bounds__(NW * kWave) void prefill_kernel(PrefillParams pp) {
         __builtin_amdgcn_wave_barrier();
       }
       const float m_use = (m_used == -INFINITY) ? 0.f : m_used;
-      float pw[16];
+      // ---- O += P V per tile t and step st2: keys {32 t + 16 st2 + 4 g + i, +8} ----
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        pw[r] = __builtin_amdgcn_exp2f(sc[r] - m_use);
-        l_part += pw[r];
-      }
-      // ---- O += P V, step st2 = keys {16 st2 + 4 g + i, 16 st2 + 8 + 4 g + i} ----
+      for (int t = 0; t < KT; ++t) {
+        float pw[16];
 #pragma unroll
-      for (int st2 = 0; st2 < 2; ++st2) {
-        const int r0 = 8 * st2;
-        const u32x4 pa = {M::pack(pw[r0 + 0], pw[r0 + 1]), M::pack(pw[r0 + 2], pw[r0 + 3]),
-                          M::pack(pw[r0 + 4], pw[r0 + 5]), M::pack(pw[r0 + 6], pw[r0 + 7])};
-        u32x4 pl = {0u, 0u, 0u, 0u};
-        if constexpr (M::kSplitP) {
-          float lo[8];
-#pragma unroll
-          for (int i = 0; i < 8; ++i) lo[i] = pw[r0 + i] - M::hi(pw[r0 + i]);
-          pl = u32x4{M::pack(lo[0], lo[1]), M::pack(lo[2], lo[3]), M::pack(lo[4], lo[5]), M::pack(lo[6], lo[7])};
+        for (int r = 0; r < 16; ++r) {
+          pw[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sa[t][r], p.qk_scale, -m_use));
+          l_part += pw[r];
         }
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const int ch = 32 * c + c32;
-          // slots 0-3: keys 16 st2 + 4 g + i, slots 4-7: keys 16 st2 + 8 + 4 g + i
-          const u32x4 vb = *reinterpret_cast<const u32x4*>(&sm.pf.v[st][ch * kVStride + 16 * st2 + 8 * g]);
-          o[c] = M::mma(pa, vb, o[c]);
-          if constexpr (M::kSplitP) o[c] = M::mma(pl, vb, o[c]);
+        for (int st2 = 0; st2 < 2; ++st2) {
+          const int r0 = 8 * st2;
+          const u32x4 pa = {M::pack(pw[r0 + 0], pw[r0 + 1]), M::pack(pw[r0 + 2], pw[r0 + 3]),
+                            M::pack(pw[r0 + 4], pw[r0 + 5]), M::pack(pw[r0 + 6], pw[r0 + 7])};
+          u32x4 pl = {0u, 0u, 0u, 0u};
+          if constexpr (M::kSplitP) {
+            float lo[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) lo[i] = pw[r0 + i] - M::hi(pw[r0 + i]);
+            pl = u32x4{M::pack(lo[0], lo[1]), M::pack(lo[2], lo[3]), M::pack(lo[4], lo[5]), M::pack(lo[6], lo[7])};
+          }
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            const int ch = 32 * c + c32;
+            // slots 0-3: keys 32 t + 16 st2 + 4 g + i, slots 4-7: the same + 8
+            const u32x4 vb = *reinterpret_cast<const u32x4*>(
+                &sm.pf.v[st][ch * kVStride + 32 * t + 16 * st2 + 8 * g]);
+            o[c] = M::mma(pa, vb, o[c]);
+            if constexpr (M::kSplitP) o[c] = M::mma(pl, vb, o[c]);
+          }
         }
       }
     }
-    if (it + 1 < n_it) stage(st ^ 1, k_next, v_next);
+    if (it + 1 < n_it) stage(st ^ 1, f_next);
     __syncthreads();
   };
 #pragma unroll 1
   for (int it = 0; it < n_it; it += 2) {
-    iteration(it, k_set0, v_set0, k_set1, v_set1);
+    iteration(it, fs0, fs1);
     if (it + 1 >= n_it) break;
-    iteration(it + 1, k_set1, v_set1, k_set0, v_set0);
+    iteration(it + 1, fs1, fs0);
   }
 
   // ---- normalise and store: lane holds rows 8 j + 4 g + i, channels 32 c + c32 ----
