@@ -86,9 +86,13 @@ constexpr int kBufferWord3 = 0x00020000;   // raw buffer, CDNA dword 3
 __device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t r, unsigned off) {
   return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 2));
 }
-__device__ __forceinline__ void load_page(PageRaw& r, const uint8_t* page, unsigned off, unsigned par_off) {
-  const __amdgpu_buffer_rsrc_t rs =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(page), (short)0, kKiviPageBytes, kBufferWord3);
+// A page that is not there (a hole, or a prefetch past the wavefront's last
+// page) gets an empty range: its loads return zeros without a memory request,
+// while the number of loads per iteration stays fixed.
+__device__ __forceinline__ void load_page(PageRaw& r, const uint8_t* page, bool there, unsigned off,
+                                          unsigned par_off) {
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t*>(page), (short)0, there ? kKiviPageBytes : 0, kBufferWord3);
   r.kn[0] = buffer_load16(rs, off);
   r.kn[1] = buffer_load16(rs, 1024u + off);
   r.vn[0] = buffer_load16(rs, unsigned(kKiviVNibOff) + off);
@@ -164,7 +168,7 @@ __device__ __forceinline__ void page_pair(PageState& st, const PageRaw& ra, cons
     s[pi][0] = t0;
     s[pi][1] = t1;
   }
-  // a hole's scores (block 0's bytes) are dropped
+  // a hole's scores (its loads returned zeros) are dropped
   if (!oka) s[0][0] = s[0][1] = (f4){-INFINITY, -INFINITY, -INFINITY, -INFINITY};
   if (!okb) s[1][0] = s[1][1] = (f4){-INFINITY, -INFINITY, -INFINITY, -INFINITY};
 
@@ -270,15 +274,15 @@ __device__ __forceinline__ void kivi_pages_wave(const KiviParams& k, int seq, in
   const unsigned par_off = lane < 32 ? unsigned(kKiviKParamOff) + off : unsigned(kKiviVParamOff) + off - 512u;
   auto load = [&](PageRaw& ra, PageRaw& rb, int ia, int ib) {
     // 32 x 32 -> 64-bit products keep the page base in scalar registers
-    load_page(ra, pool + uint64_t(uint32_t(max(ia, 0))) * pid_stride, off, par_off);
-    load_page(rb, pool + uint64_t(uint32_t(max(ib, 0))) * pid_stride, off, par_off);
+    load_page(ra, pool + uint64_t(uint32_t(max(ia, 0))) * pid_stride, ia >= 0, off, par_off);
+    load_page(rb, pool + uint64_t(uint32_t(max(ib, 0))) * pid_stride, ib >= 0, off, par_off);
   };
 
   // The wavefront's pages are pg_begin + o * pg_step, o = 0 .. n_mine - 1.
   // Their physical ids are read 64 at a time into one register (lane i: page
   // o = c0 + i) and taken out with readlane, so the loop issues no table
-  // loads.  Page loads are unconditional (past the end they fetch page 0
-  // again, an L2 hit): a fixed number of loads per iteration lets the
+  // loads.  Page loads are unconditional (past the end, and for holes, with
+  // an empty range): a fixed number of loads per iteration lets the
   // compiler wait only for the pair about to be used, not for the prefetch.
   const int n_mine = pg_begin < pg_end ? (pg_end - pg_begin + pg_step - 1) / pg_step : 0;
   PageRaw r0a, r0b, r1a, r1b;
