@@ -10,10 +10,10 @@
 // block fetched serves all q heads of the group.  Per 64-key iteration:
 //   * the workgroup copies the keys' K (transposed to [key][channel], rows
 //     padded to 136 halves) and V ([channel][key slot], the key order of the
-//     PV operand, rows padded to 72 halves) into a double-buffered LDS
-//     stage; each wavefront copies two 8-key runs for half of the channels,
-//     laid out so its LDS writes and the MFMA operand reads are free of bank
-//     conflicts;
+//     PV operand, rows padded to 72 halves) into one of three LDS stages,
+//     two iterations ahead; each wavefront copies two 8-key runs for half
+//     of the channels, laid out so its LDS writes and the MFMA operand reads
+//     are free of bank conflicts;
 //   * each wavefront (32 rows) forms two 32-key tiles of S^T = K Q^T with
 //     v_mfma_f32_32x32x16_{bf16,f16}: A = K (rows: keys, k: channels) read
 //     from LDS, B = Q^T held in registers for the whole launch.  Lane l then
@@ -25,7 +25,9 @@
 //   * O += P V on the same MFMA: the weights leave the S^T accumulator of
 //     tile t as keys {32 t + 16 s + 4 g + i, 32 t + 16 s + 8 + 4 g + i} for
 //     lane group g, which is used as the k order of step s; V is read from
-//     LDS in that order.
+//     LDS in that order;
+//   * the q.k MFMAs of the next iteration share a basic block with the
+//     exponentials and P V of the current one (software pipeline).
 // Decode rows run the decode wavefronts (tl_mfma_wave.hpp for block_size 16,
 // tl_decode_wave.hpp otherwise), one workgroup per (sequence, kv head, head
 // slice), as a second kernel of the same call on the same stream (one
@@ -64,6 +66,9 @@ __device__ __forceinline__ int v_slot(int k) {
   return (k & ~15) + 4 * (((q & 1) << 1) | (q >> 1)) + (k & 3);
 }
 constexpr float kLazyRescale = 8.f;  // log2 units
+// LDS stages: iteration i is staged in stage i % 3 two iterations ahead, so
+// its K is already visible during iteration i - 1
+constexpr int kStages = 3;
 
 template <Kind KV> struct Mfma32;
 // bf16 keeps 8 mantissa bits: the weights go to the PV product as two bf16
@@ -108,8 +113,8 @@ struct PrefillParams {
 template <int NW, int BS>
 struct PrefillSmem {
   struct {
-    uint16_t kt[2][kPfKeys * kKtStride];          // [key][channel] (+8 pad)
-    uint16_t v[2][kPfHead * kVStride];            // [channel][v_slot(key)] (+8 pad)
+    uint16_t kt[kStages][kPfKeys * kKtStride];    // [key][channel] (+8 pad)
+    uint16_t v[kStages][kPfHead * kVStride];      // [channel][v_slot(key)] (+8 pad)
     float row[NW][kPfRows];                       // per-row exchange (alpha, l)
   } pf;
 };
@@ -231,129 +236,146 @@ __global__ __launch_bounds__(NW * kWave) void prefill_kernel(PrefillParams pp) {
   float m_used = -INFINITY, l_part = 0.f;
   float* s_row = &sm.pf.row[wave][0];
 
-  // Two register sets hold fetched, not yet staged iterations: iteration
-  // it + 2 is fetched while it computes and it + 1 waits to be staged.
-  // Keys of an iteration entirely at or below the wavefront's first query
+  // Software pipeline.  Iteration it first masks its scores (computed
+  // during it - 1) and decides the rescale; then one branch-free block
+  // holds the q.k MFMAs of it + 1 (its K is staged two iterations ahead),
+  // the exponentials and weight packing of it and its P V MFMAs, which the
+  // compiler interleaves so the matrix cores and the VALU work at once.  A wavefront
+  // past its last keys runs the block on masked scores (weights 0).  Keys
+  // of an iteration entirely at or below the wavefront's first query
   // position, in blocks that exist, need no mask.  The scores stay unscaled
   // until the exponent (qk_scale > 0, so the max commutes with the scale).
   const int wmin_pos = L - ql + wrow0 / p.group;
+  auto qk = [&](int it, f16v (&sa)[KT]) {
+    const uint16_t* kst = sm.pf.kt[it % kStages];
+#pragma unroll
+    for (int t = 0; t < KT; ++t) {
+      sa[t] = f16v{};
+      const uint16_t* ktw = kst + (32 * t + c32) * kKtStride + 8 * g;
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks)
+        sa[t] = M::mma(*reinterpret_cast<const u32x4*>(ktw + 16 * ks), qb[ks], sa[t]);
+    }
+  };
+  // mask, row max and lazy rescale of iteration it; returns the exponent offset
+  auto prepare = [&](int it, f16v (&sa)[KT]) {
+    const int k0 = it * kPfKeys;
+    bool blk_ok[BPI];
+    bool all_ok = true;
+#pragma unroll
+    for (int bi = 0; bi < BPI; ++bi) {
+      blk_ok[bi] = block_of(p, table, it * BPI + bi) >= 0;
+      all_ok = all_ok && blk_ok[bi];
+    }
+    float mx = -INFINITY;
+    if (all_ok && k0 + kPfKeys - 1 <= wmin_pos) {
+#pragma unroll
+      for (int t = 0; t < KT; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sa[t][r]);
+    } else {
+#pragma unroll
+      for (int t = 0; t < KT; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int kk = 32 * t + 8 * (r >> 2) + 4 * g + (r & 3);
+          const bool ok = k0 + kk <= pos && blk_ok[kk / BS];
+          sa[t][r] = ok ? sa[t][r] : -INFINITY;
+          mx = fmaxf(mx, sa[t][r]);
+        }
+    }
+    {
+      const auto sw = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, mx),
+                                                       __builtin_bit_cast(unsigned, mx), false, false);
+      mx = fmaxf(__builtin_bit_cast(float, (unsigned)sw[0]), __builtin_bit_cast(float, (unsigned)sw[1]));
+    }
+    mx *= p.qk_scale;
+    const bool raise = mx > m_used + kLazyRescale || (m_used == -INFINITY && mx != -INFINITY);
+    if (__builtin_amdgcn_ballot_w64(raise)) {
+      const float m_new = raise ? mx : m_used;
+      const float alpha = (m_new == m_used) ? 1.f : (m_used == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_used - m_new));
+      m_used = m_new;
+      l_part *= alpha;
+      if (g == 0) s_row[c32] = alpha;
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      // O rows of this lane: 8 j + 4 g + i
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float4 a4 = *reinterpret_cast<const float4*>(&s_row[8 * j + 4 * g]);
+        const float a[4] = {a4.x, a4.y, a4.z, a4.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int c = 0; c < 4; ++c) o[c][4 * j + i] *= a[i];
+      }
+      __builtin_amdgcn_wave_barrier();
+    }
+    return (m_used == -INFINITY) ? 0.f : m_used;
+  };
+  auto exp_pv = [&](int it, const f16v (&sa)[KT], float m_use) {
+    const uint16_t* vst = sm.pf.v[it % kStages];
+#pragma unroll
+    for (int t = 0; t < KT; ++t) {
+      float pw[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        pw[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sa[t][r], p.qk_scale, -m_use));
+        l_part += pw[r];
+      }
+#pragma unroll
+      for (int st2 = 0; st2 < 2; ++st2) {
+        const int r0 = 8 * st2;
+        const u32x4 pa = {M::pack(pw[r0 + 0], pw[r0 + 1]), M::pack(pw[r0 + 2], pw[r0 + 3]),
+                          M::pack(pw[r0 + 4], pw[r0 + 5]), M::pack(pw[r0 + 6], pw[r0 + 7])};
+        u32x4 pl = {0u, 0u, 0u, 0u};
+        if constexpr (M::kSplitP) {
+          float lo[8];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) lo[i] = pw[r0 + i] - M::hi(pw[r0 + i]);
+          pl = u32x4{M::pack(lo[0], lo[1]), M::pack(lo[2], lo[3]), M::pack(lo[4], lo[5]), M::pack(lo[6], lo[7])};
+        }
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const int ch = 32 * c + c32;
+          // slots 0-3: keys 32 t + 16 st2 + 4 g + i, slots 4-7: the same + 8
+          const u32x4 vb = *reinterpret_cast<const u32x4*>(vst + ch * kVStride + 32 * t + 16 * st2 + 8 * g);
+          o[c] = M::mma(pa, vb, o[c]);
+          if constexpr (M::kSplitP) o[c] = M::mma(pl, vb, o[c]);
+        }
+      }
+    }
+  };
+
   Fetched fs0, fs1;
+  f16v sa0[KT], sa1[KT];
   if (n_it > 0) {
     fetch(0, fs0);
     stage(0, fs0);
   }
-  if (n_it > 1) fetch(1, fs1);
+  if (n_it > 1) {
+    fetch(1, fs1);
+    stage(1, fs1);
+  }
+  if (n_it > 2) fetch(2, fs0);
   __syncthreads();
-  auto iteration = [&](int it, Fetched& f_free, const Fetched& f_next) {
-    const int st = it & 1;
-    if (it + 2 < n_it) fetch(it + 2, f_free);
-    const int k0 = it * kPfKeys;
-    if (k0 < wkend) {
-      // ---- S^T = K Q^T; tile t, lane: keys 32 t + 8 j + 4 g + i of row my_row ----
-      f16v sa[KT];
-#pragma unroll
-      for (int t = 0; t < KT; ++t) {
-        sa[t] = f16v{};
-        const uint16_t* ktw = &sm.pf.kt[st][(32 * t + c32) * kKtStride + 8 * g];
-#pragma unroll
-        for (int ks = 0; ks < 8; ++ks)
-          sa[t] = M::mma(*reinterpret_cast<const u32x4*>(ktw + 16 * ks), qb[ks], sa[t]);
-      }
-      // ---- mask (causal; table holes), row max, lazy rescale ----
-      bool blk_ok[BPI];
-      bool all_ok = true;
-#pragma unroll
-      for (int bi = 0; bi < BPI; ++bi) {
-        blk_ok[bi] = block_of(p, table, it * BPI + bi) >= 0;
-        all_ok = all_ok && blk_ok[bi];
-      }
-      float mx = -INFINITY;
-      if (all_ok && k0 + kPfKeys - 1 <= wmin_pos) {
-#pragma unroll
-        for (int t = 0; t < KT; ++t)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sa[t][r]);
-      } else {
-#pragma unroll
-        for (int t = 0; t < KT; ++t)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int kk = 32 * t + 8 * (r >> 2) + 4 * g + (r & 3);
-            const bool ok = k0 + kk <= pos && blk_ok[kk / BS];
-            sa[t][r] = ok ? sa[t][r] : -INFINITY;
-            mx = fmaxf(mx, sa[t][r]);
-          }
-      }
-      {
-        const auto sw = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, mx),
-                                                         __builtin_bit_cast(unsigned, mx), false, false);
-        mx = fmaxf(__builtin_bit_cast(float, (unsigned)sw[0]), __builtin_bit_cast(float, (unsigned)sw[1]));
-      }
-      mx *= p.qk_scale;
-      const bool raise = mx > m_used + kLazyRescale || (m_used == -INFINITY && mx != -INFINITY);
-      if (__builtin_amdgcn_ballot_w64(raise)) {
-        const float m_new = raise ? mx : m_used;
-        const float alpha = (m_new == m_used) ? 1.f : (m_used == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_used - m_new));
-        m_used = m_new;
-        l_part *= alpha;
-        if (g == 0) s_row[c32] = alpha;
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        // O rows of this lane: 8 j + 4 g + i
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const float4 a4 = *reinterpret_cast<const float4*>(&s_row[8 * j + 4 * g]);
-          const float a[4] = {a4.x, a4.y, a4.z, a4.w};
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int c = 0; c < 4; ++c) o[c][4 * j + i] *= a[i];
-        }
-        __builtin_amdgcn_wave_barrier();
-      }
-      const float m_use = (m_used == -INFINITY) ? 0.f : m_used;
-      // ---- O += P V per tile t and step st2: keys {32 t + 16 st2 + 4 g + i, +8} ----
-#pragma unroll
-      for (int t = 0; t < KT; ++t) {
-        float pw[16];
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          pw[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sa[t][r], p.qk_scale, -m_use));
-          l_part += pw[r];
-        }
-#pragma unroll
-        for (int st2 = 0; st2 < 2; ++st2) {
-          const int r0 = 8 * st2;
-          const u32x4 pa = {M::pack(pw[r0 + 0], pw[r0 + 1]), M::pack(pw[r0 + 2], pw[r0 + 3]),
-                            M::pack(pw[r0 + 4], pw[r0 + 5]), M::pack(pw[r0 + 6], pw[r0 + 7])};
-          u32x4 pl = {0u, 0u, 0u, 0u};
-          if constexpr (M::kSplitP) {
-            float lo[8];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) lo[i] = pw[r0 + i] - M::hi(pw[r0 + i]);
-            pl = u32x4{M::pack(lo[0], lo[1]), M::pack(lo[2], lo[3]), M::pack(lo[4], lo[5]), M::pack(lo[6], lo[7])};
-          }
-#pragma unroll
-          for (int c = 0; c < 4; ++c) {
-            const int ch = 32 * c + c32;
-            // slots 0-3: keys 32 t + 16 st2 + 4 g + i, slots 4-7: the same + 8
-            const u32x4 vb = *reinterpret_cast<const u32x4*>(
-                &sm.pf.v[st][ch * kVStride + 32 * t + 16 * st2 + 8 * g]);
-            o[c] = M::mma(pa, vb, o[c]);
-            if constexpr (M::kSplitP) o[c] = M::mma(pl, vb, o[c]);
-          }
-        }
-      }
-    }
-    if (it + 1 < n_it) stage(st ^ 1, f_next);
+  if (n_it > 0) qk(0, sa0);
+  // f_stage holds it + 2 (staged at the end of it), f_free receives it + 3;
+  // s_cur holds the scores of it, s_next receives those of it + 1
+  auto iteration = [&](int it, Fetched& f_stage, Fetched& f_free, f16v (&s_cur)[KT], f16v (&s_next)[KT]) {
+    if (it + 3 < n_it) fetch(it + 3, f_free);
+    const float m_use = prepare(it, s_cur);
+    qk(it + 1, s_next);
+    exp_pv(it, s_cur, m_use);
+    if (it + 2 < n_it) stage((it + 2) % kStages, f_stage);
     __syncthreads();
   };
 #pragma unroll 1
   for (int it = 0; it < n_it; it += 2) {
-    iteration(it, fs0, fs1);
+    iteration(it, fs0, fs1, sa0, sa1);
     if (it + 1 >= n_it) break;
-    iteration(it + 1, fs1, fs0);
+    iteration(it + 1, fs1, fs0, sa1, sa0);
   }
 
   // ---- normalise and store: lane holds rows 8 j + 4 g + i, channels 32 c + c32 ----
