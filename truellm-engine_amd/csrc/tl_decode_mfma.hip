@@ -5,9 +5,10 @@
 //   * FP8: a byte is one element, so per byte of HBM traffic there are twice
 //     the multiply-adds of 2-byte KV, which the packed dot products of the
 //     2-byte wavefront cannot keep up with;
-//   * 2-byte KV with more than 4 q heads per kv head (GQA group 8 or 16):
-//     the 16 MFMA columns serve the whole group from one KV read, where the
-//     dot-product wavefront reads the KV once per 4 heads.
+//   * 2-byte KV: the MFMA formulation needs half the VALU work of the
+//     packed dot products per byte (6.38 against 5.94 TB/s at GQA group 4),
+//     and its 16 columns serve a whole group of up to 16 heads from one KV
+//     read, where the dot-product wavefront reads the KV once per 4 heads.
 // The dequant scales of FP8 fold into the score scale (k_scale) and the
 // output (v_scale), as the reference's dequantise-then-multiply does (the
 // scaled K/V are k_scale * code and v_scale * code).  Workgroups and the
@@ -86,8 +87,11 @@ int launch_typed(const DecodeLaunch& a) {
   const int P = a.num_partitions;
   const unsigned items = (unsigned)(a.num_seqs * a.num_kv_heads * p.head_slices);
   if (P == 1) {
+    // 4 wavefronts per workgroup: at 2-3 workgroups per CU the single-pass
+    // grid of a large batch is resident in one round (B=64, ctx 4096:
+    // 6.69 against 6.64 TB/s with 8)
     p.partition_tokens = 0x7fffffff;
-    launch_kernel<KV, QK, 8, true>(p, items, a.stream);
+    launch_kernel<KV, QK, 4, true>(p, items, a.stream);
     return hipGetLastError() == hipSuccess ? 0 : 5;
   }
   launch_kernel<KV, QK, 4, false>(p, items * P, a.stream);
