@@ -225,9 +225,14 @@ int tl_kivi_paged_attention_decode(const tl_kivi_desc* desc, void* out, const vo
                                    int32_t max_context_len, void* workspace,
                                    size_t workspace_bytes, void* stream);
 
-/* One KIVI decode step in one call: tl_kivi_append then
- * tl_kivi_paged_attention_decode (seq_lens are the lengths after the
- * append), two launches on the stream. */
+/* One KIVI decode step in one call, with the result of tl_kivi_append then
+ * tl_kivi_paged_attention_decode (seq_lens are the lengths after the append)
+ * byte for byte, in one decode launch (plus the log-sum-exp reduce when
+ * split): the new token's attention reads it from key/value, and the page it
+ * completes is built in the same launch.  slot_mapping[s] must be the pool
+ * slot of position seq_lens[s] - 1 in block_tables, as an append step's slot
+ * is; a negative slot writes nothing and that position is read from the
+ * pool, as the two calls would. */
 int tl_kivi_decode_step(const tl_kivi_desc* desc, void* out, const void* q, const void* key,
                         const void* value, const int32_t* slot_mapping, void* pages,
                         const int32_t* page_tables, void* k_cache, void* v_cache,

@@ -239,10 +239,13 @@ def test_kivi_decode_residual_zero_and_nan_slots():
     assert_close(_run_decode(kc, pages, -1), _kivi_ref(kc, pages), orc.F16, ATOL_KIVI, "R=0")
 
 
-def test_kivi_step_graph_replay_matches_eager():
-    """One append + decode step captured in a HIP graph and replayed three
-    times, with eager work between replays: every replay matches the eager
-    step bit for bit (the append is idempotent: same token, same slot)."""
+@pytest.mark.parametrize("fused", [False, True])
+def test_kivi_step_graph_replay_matches_eager(fused):
+    """One append + decode step (two calls, or the fused tl_kivi_decode_step)
+    captured in a HIP graph and replayed three times, with eager work between
+    replays: every replay matches the eager step bit for bit (the append is
+    idempotent: same token, same slot).  Sequence 1 (159 -> 160 tokens)
+    completes a page in the step."""
     start = np.array([700, 159, 2000, 129], np.int32)
     kc = KiviCase(57, start + 1, extra_blocks=1)
     qd, kd, vd = dev(kc.q, orc.F16), dev(kc.k, orc.F16), dev(kc.v, orc.F16)
@@ -262,10 +265,14 @@ def test_kivi_step_graph_replay_matches_eager():
     out = torch.zeros_like(qd)
 
     def step(stream):
+        if fused:
+            tla.kivi_decode_step(desc, out, qd, knew, vnew, slots, pages, ptd, kd, vd, btd, sld, max_ctx, ws,
+                                 stream)
+            return
         tla.kivi_append(desc, knew, vnew, kd, vd, slots, btd, sld, ptd, pages, stream)
         tla.kivi_paged_attention_decode(desc, out, qd, pages, ptd, kd, vd, btd, sld, max_ctx, ws, stream)
 
-    print("case kivi graph replay", flush=True)
+    print(f"case kivi graph replay fused={fused}", flush=True)
     step(torch.cuda.current_stream())
     torch.cuda.synchronize()
     eager, eager_pages = out.clone(), pages.clone()
@@ -285,7 +292,8 @@ def test_kivi_step_graph_replay_matches_eager():
         assert torch.equal(out, eager)
 
 
-@pytest.mark.parametrize("H,R,pp", [(32, 128, 0), (32, 0, 0), (64, 128, 0), (32, 128, 4)])
+@pytest.mark.parametrize("H,R,pp", [(32, 128, 0), (32, 0, 0), (64, 128, 0), (32, 128, 4), (64, 0, 4),
+                                    (32, 20, 0)])
 def test_decode_step_equals_append_then_decode(H, R, pp):
     """tl_kivi_decode_step gives the bytes of tl_kivi_append followed by
     tl_kivi_paged_attention_decode, over 40 steps that complete pages."""

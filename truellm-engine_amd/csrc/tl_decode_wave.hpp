@@ -71,10 +71,6 @@ template <> struct Dot2<Kind::F16> {
   }
 };
 
-__device__ __forceinline__ uint32_t word(const u32x4& c, int w) {
-  return w == 0 ? c.x : w == 1 ? c.y : w == 2 ? c.z : c.w;
-}
-
 // Physical block holding token blk_tok (a block start) of a sequence, or -1
 // for a hole, a block past the partition end t1 or an entry outside the pool.
 template <int BS>

@@ -111,6 +111,11 @@ template <> struct Unpack<Kind::FP8> {
 // ---- 16-byte global loads ---------------------------------------------------
 struct alignas(16) u32x4 { uint32_t x, y, z, w; };
 
+// Dword w (0..3) of a 16-byte chunk.
+__device__ __forceinline__ uint32_t word(const u32x4& c, int w) {
+  return w == 0 ? c.x : w == 1 ? c.y : w == 2 ? c.z : c.w;
+}
+
 __device__ __forceinline__ u32x4 load16(const void* p) {
   return *reinterpret_cast<const u32x4*>(p);
 }

@@ -111,8 +111,8 @@ struct KiviDecodeLaunch {
   int max_pages_per_seq, num_pages, residual_length, gqa_map;
   int num_partitions, partition_pages;
   float scale;
-  const KiviPageLaunch* append;  // non-null: the step's append first (fused when one workgroup
-                                 // owns each (seq, kv head), else as its own launch)
+  const KiviPageLaunch* append;  // non-null: the step's append (token write, page build),
+                                 // fused into the decode launch
   hipStream_t stream;
 };
 int launch_kivi_decode(const KiviDecodeLaunch& a);

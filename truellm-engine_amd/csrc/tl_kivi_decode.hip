@@ -26,6 +26,7 @@
 #include "tl_device.hpp"
 #include "tl_internal.hpp"
 #include "tl_kivi.hpp"
+#include "tl_kivi_page.hpp"
 
 namespace tl {
 
@@ -40,6 +41,7 @@ struct KiviParams {
   const uint8_t* pages;
   const int32_t* page_tables;
   int max_pages_per_seq, num_pages, residual_length, partition_pages;
+  PageJob job;                 // the step's append (kernels with APPEND)
 };
 
 // Eight nibbles n_j (slot j at bit 16 (j & 1) + 4 (j >> 1)) as fp16
@@ -335,12 +337,110 @@ __device__ __forceinline__ void kivi_pages_wave(const KiviParams& k, int seq, in
   }
 }
 
-template <int NW, bool FINAL>
-__global__ __launch_bounds__(NW * kWave) void kivi_decode_kernel(KiviParams k) {
+// The window's newest token (position L - 1) as a state of its own: lane l
+// holds channels 2l and 2l + 1 of its K and V (fp16 pairs).
+struct NewestToken {
+  uint32_t k, v;
+  bool ok;      // false: a hole in the block table (the token is masked)
+};
+
+// From the fp16 pool, at the token's block-table position.
+__device__ __forceinline__ NewestToken newest_from_pool(const Params& p, int seq, int kvh, int pos, int lane) {
+  constexpr int BS = 16;
+  const int lb = pos / BS;
+  int ph = (pos >= 0 && lb < p.max_blocks_per_seq) ? p.block_tables[(int64_t)seq * p.max_blocks_per_seq + lb] : -1;
+  if (ph >= p.num_blocks) ph = -1;
+  NewestToken t{0u, 0u, ph >= 0};
+  if (ph >= 0) {
+    const int64_t off = (((int64_t)ph * p.num_kv_heads + kvh) * kKiviHead + 2 * lane) * BS + pos % BS;
+    const uint16_t* kp = (const uint16_t*)p.k_cache + off;
+    const uint16_t* vp = (const uint16_t*)p.v_cache + off;
+    t.k = uint32_t(kp[0]) | (uint32_t(kp[BS]) << 16);
+    t.v = uint32_t(vp[0]) | (uint32_t(vp[BS]) << 16);
+  }
+  return t;
+}
+
+// From the step's input row (the token that this launch appends).
+__device__ __forceinline__ NewestToken newest_from_row(const PageJob& j, int seq, int kvh, int lane) {
+  const int64_t row = ((int64_t)seq * j.num_kv_heads + kvh) * (kKiviHead / 2);
+  return NewestToken{reinterpret_cast<const uint32_t*>(j.knew)[row + lane],
+                     reinterpret_cast<const uint32_t*>(j.vnew)[row + lane], true};
+}
+
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) x += __shfl_xor(x, o, kWave);
+  return x;
+}
+
+// The single-token state of the wavefront's q heads: max = the score
+// (log2 units), sum = 1, unnormalised output = V.
+__device__ __forceinline__ void newest_state(const Params& p, const NewestToken& t, int seq, int kvh, int hs,
+                                             int lane, float* s_acc_w, float* s_m_w, float* s_l_w) {
   constexpr int GT = kWaveHeads;
-  __shared__ __attribute__((aligned(16))) uint32_t s_p[NW][512];   // per wave: weights or page params
-  __shared__ float s_m[NW][GT], s_l[NW][GT];
-  __shared__ float s_acc[NW][GT][kKiviHead];
+#pragma unroll
+  for (int g = 0; g < GT; ++g) {
+    const int gi = hs * GT + g;
+    const bool real = gi < p.group;
+    const uint32_t q2 = real ? reinterpret_cast<const uint32_t*>(p.q)
+                                   [((int64_t)seq * p.num_heads + head_of(p, kvh, gi)) * (kKiviHead / 2) + lane]
+                             : 0u;
+    const float sc = wave_sum(Dot2<Kind::F16>::dot(t.k, q2, 0.f)) * p.qk_scale;
+    if (lane == 0) {
+      s_m_w[g] = (t.ok && real) ? sc : -INFINITY;
+      s_l_w[g] = (t.ok && real) ? 1.f : 0.f;
+    }
+    s_acc_w[g * kKiviHead + 2 * lane] = f16_to_f32(uint16_t(t.v));
+    s_acc_w[g * kKiviHead + 2 * lane + 1] = f16_to_f32(uint16_t(t.v >> 16));
+  }
+}
+
+// The new token into the fp16 pool from the wavefront's registers (stores
+// written through L2, as kivi_append_token's).
+__device__ __forceinline__ void store_newest(const PageJob& j, const NewestToken& t, int seq, int kvh, int lane) {
+  const int32_t slot = j.slots[seq];
+  const int blk = slot >= 0 ? slot / j.block_size : -1;
+  if (blk < 0 || blk >= j.num_blocks) return;
+  const int64_t off = (((int64_t)blk * j.num_kv_heads + kvh) * kKiviHead + 2 * lane) * j.block_size + slot % j.block_size;
+  store_through(j.k_cache + off, uint16_t(t.k));
+  store_through(j.k_cache + off + j.block_size, uint16_t(t.k >> 16));
+  store_through(j.v_cache + off, uint16_t(t.v));
+  store_through(j.v_cache + off + j.block_size, uint16_t(t.v >> 16));
+}
+
+// Slots 0 .. NW-1: one per wavefront; slot NW: the newest token.
+template <int NW>
+struct KiviDecodeSmem {
+  uint32_t p[NW][512];                       // per wave: weights or page params
+  float m[NW + 1][kWaveHeads], l[NW + 1][kWaveHeads];
+  float acc[NW + 1][kWaveHeads][kKiviHead];
+};
+
+// One decode workgroup.  The residual wavefront runs the window [lq, L - 1)
+// from the pool and then the newest token (L - 1) as a state of its own.
+// With APPEND the workgroup also does the step's append for its (sequence,
+// kv head), and nothing in the launch reads a byte that it writes:
+//   * the page that the new token completes (if any) is built first, by the
+//     workgroup of the last partition, whose page range holds that page; the
+//     page never holds the new token's pool slot (with R = 0 the new token
+//     is in the page and is read from the input row);
+//   * the newest-token state takes K and V from the input row (when the
+//     slot is >= 0, i.e. the token is written), and the residual wavefront
+//     stores the token to its slot after its window (wavefront 0 of the
+//     last partition when the sequence has no window).  The slot must be the
+//     token's block-table position, as an append step's slot is.
+// With a GQA group over several head slices each slice's workgroup writes
+// the same bytes.
+// Two wavefronts per SIMD (at most 256 registers, VGPRs and AGPRs together):
+// with 4-wavefront workgroups the compiler would otherwise take more and
+// halve the occupancy.
+template <int NW, bool FINAL, bool APPEND>
+__global__ __launch_bounds__(NW * kWave, 2) void kivi_decode_kernel(KiviParams k) {
+  using Smem = KiviDecodeSmem<NW>;
+  constexpr size_t kLds = (APPEND && sizeof(KiviBuildSmem) > sizeof(Smem)) ? sizeof(KiviBuildSmem) : sizeof(Smem);
+  __shared__ __attribute__((aligned(16))) unsigned char s_raw[kLds];
+  Smem& sd = *reinterpret_cast<Smem*>(s_raw);
 
   const Params& p = k.base;
   const int tid = threadIdx.x;
@@ -357,19 +457,46 @@ __global__ __launch_bounds__(NW * kWave) void kivi_decode_kernel(KiviParams k) {
   if (part >= n_parts) return;
   const int pg0 = FINAL ? 0 : part * k.partition_pages;
   const int pg1 = FINAL ? n_pages : min(pg0 + k.partition_pages, n_pages);
-  const bool has_res = (part == n_parts - 1) && L > lq;
+  const bool last = part == n_parts - 1;
+  const bool has_res = last && L > lq;
   const int page_waves = has_res ? NW - 1 : NW;
 
+  if constexpr (APPEND) {
+    if (last && lq > 0 && lq != kivi_quantized_len(L - 1, k.residual_length)) {
+      kivi_build_page<NW * kWave>(*reinterpret_cast<KiviBuildSmem*>(s_raw), k.job, seq, kvh,
+                                  lq / kKiviPageTokens - 1, L, tid);
+      __syncthreads();   // the page is visible to the workgroup; the LDS is free again
+    }
+    if (last && !has_res && wave == 0) kivi_append_token<kWave>(k.job, seq, kvh, tid);
+  }
   if (wave < page_waves) {
-    kivi_pages_wave(k, seq, kvh, hs, pg0 + wave, pg1, page_waves, &s_p[wave][0], &s_acc[wave][0][0],
-                    &s_m[wave][0], &s_l[wave][0]);
+    kivi_pages_wave(k, seq, kvh, hs, pg0 + wave, pg1, page_waves, &sd.p[wave][0], &sd.acc[wave][0][0],
+                    &sd.m[wave][0], &sd.l[wave][0]);
   } else {
-    decode2_wave<Kind::F16, kKiviHead, 16>(p, seq, kvh, hs, lq, L, 32, &s_p[wave][0],
-                                           &s_acc[wave][0][0], &s_m[wave][0], &s_l[wave][0]);
+    const int lane = tid % kWave;
+    NewestToken nt;
+    if constexpr (APPEND)
+      nt = k.job.slots[seq] >= 0 ? newest_from_row(k.job, seq, kvh, lane) : newest_from_pool(p, seq, kvh, L - 1, lane);
+    else
+      nt = newest_from_pool(p, seq, kvh, L - 1, lane);
+    decode2_wave<Kind::F16, kKiviHead, 16>(p, seq, kvh, hs, lq, L - 1, 32, &sd.p[wave][0],
+                                           &sd.acc[wave][0][0], &sd.m[wave][0], &sd.l[wave][0]);
+    newest_state(p, nt, seq, kvh, hs, lane, &sd.acc[NW][0][0], &sd.m[NW][0], &sd.l[NW][0]);
+    // the token's store, at the end of the window: issued earlier (in its
+    // first iteration) it cost the step 6 us more at batch 64, ctx 4096
+    if constexpr (APPEND) store_newest(k.job, nt, seq, kvh, lane);
   }
   __syncthreads();
-  combine_waves<Kind::F16, Kind::F32, kKiviHead, FINAL>(p, NW, &s_m[0][0], &s_l[0][0], &s_acc[0][0][0],
-                                                        seq, kvh, hs, part, tid, NW * kWave);
+  combine_waves<Kind::F16, Kind::F32, kKiviHead, FINAL>(p, has_res ? NW + 1 : NW, &sd.m[0][0], &sd.l[0][0],
+                                                        &sd.acc[0][0][0], seq, kvh, hs, part, tid, NW * kWave);
+}
+
+template <int NW, bool FINAL>
+void launch_decode(const KiviParams& k, bool append, unsigned grid, hipStream_t stream) {
+  if (append)
+    hipLaunchKernelGGL((kivi_decode_kernel<NW, FINAL, true>), dim3(grid), dim3(NW * kWave), 0, stream, k);
+  else
+    hipLaunchKernelGGL((kivi_decode_kernel<NW, FINAL, false>), dim3(grid), dim3(NW * kWave), 0, stream, k);
 }
 
 }  // namespace
@@ -392,16 +519,15 @@ int launch_kivi_decode(const KiviDecodeLaunch& a) {
   k.pages = (const uint8_t*)a.pages; k.page_tables = a.page_tables;
   k.max_pages_per_seq = a.max_pages_per_seq; k.num_pages = a.num_pages;
   k.residual_length = a.residual_length; k.partition_pages = a.partition_pages;
-  // the step's append (token write, quantise-on-append) runs as its own launch
-  // before the decode: folding it into the decode workgroups' prologue cost
-  // them as much as the separate launch
-  if (a.append && launch_kivi_pages(*a.append)) return 5;
+  // the step's append (token write, quantise-on-append) is fused into the
+  // decode launch
+  const bool append = a.append != nullptr;
+  if (append) k.job = make_page_job(*a.append);
   const unsigned items = (unsigned)(a.num_seqs * a.num_kv_heads * p.head_slices);
   if (a.num_partitions == 1) {
-    hipLaunchKernelGGL((kivi_decode_kernel<8, true>), dim3(items), dim3(8 * kWave), 0, a.stream, k);
+    launch_decode<8, true>(k, append, items, a.stream);
   } else {
-    hipLaunchKernelGGL((kivi_decode_kernel<4, false>), dim3(items * a.num_partitions), dim3(4 * kWave),
-                       0, a.stream, k);
+    launch_decode<4, false>(k, append, items * a.num_partitions, a.stream);
     if (hipGetLastError() != hipSuccess) return 5;
     return launch_lse_reduce(a.out, (int)Kind::F16, a.part_m, a.part_l, a.part_o, 0, a.seq_lens,
                              a.num_seqs, a.num_heads, kKiviHead, a.num_partitions, 0,

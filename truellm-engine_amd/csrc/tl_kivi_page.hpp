@@ -91,24 +91,46 @@ struct KiviBuildSmem {
   __attribute__((aligned(16))) uint8_t page[kKiviPageBytes];
 };
 
-// The new token (position L - 1) of (seq, kvh) into the fp16 pool, channels
-// split over NT >= 128 threads.
+// The new token (position L - 1) of (seq, kvh) into the fp16 pool, by NT
+// threads.  In the pool a token's 128 channels are 2-byte elements 2 BS
+// bytes apart; HBM3E has no byte masks, so 256 such scattered writes per
+// (seq, kv head) cost a read-modify-write of a memory burst each.  Instead
+// the block's rows of this kv head (128 channels x 16 slots: 4 KiB each of
+// K and V) are read, the slot is replaced, and the rows are written back
+// whole.  Other slots keep their bytes; the block of the slot belongs to the
+// sequence alone (as every block that a sequence appends to does), so no
+// other writer of the same launch touches these rows except the other head
+// slices of the same (seq, kv head), which write the same bytes.
+// A 2-byte store written through L2 (relaxed, agent scope: sc1).  In the
+// pool a token's 128 channels are 2 BS bytes apart, so one token dirties 32
+// L2 lines each of K and V; left dirty, a decode step's 512 (seq, kv head)
+// tokens cost the next launch about 4 us of write-back at batch 64 (about
+// 1.4 us when written through).
+__device__ __forceinline__ void store_through(uint16_t* p, uint16_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The new token (position L - 1) of (seq, kvh) into the fp16 pool, the 128
+// channels strided over NT threads; a negative slot writes nothing.
 template <int NT>
 __device__ __forceinline__ void kivi_append_token(const PageJob& j, int seq, int kvh, int tid) {
   const int32_t slot = j.slots[seq];
   const int blk = slot >= 0 ? slot / j.block_size : -1;
-  if (tid < kKiviHead && blk >= 0 && blk < j.num_blocks) {
-    const int64_t new_off = ((int64_t)seq * j.num_kv_heads + kvh) * kKiviHead;
-    const int64_t off = (((int64_t)blk * j.num_kv_heads + kvh) * kKiviHead + tid) * j.block_size + slot % j.block_size;
-    j.k_cache[off] = j.knew[new_off + tid];
-    j.v_cache[off] = j.vnew[new_off + tid];
+  if (blk < 0 || blk >= j.num_blocks) return;
+  const int64_t new_off = ((int64_t)seq * j.num_kv_heads + kvh) * kKiviHead;
+  const int64_t base = ((int64_t)blk * j.num_kv_heads + kvh) * kKiviHead * j.block_size + slot % j.block_size;
+#pragma unroll
+  for (int c = tid; c < kKiviHead; c += NT) {
+    store_through(j.k_cache + base + (int64_t)c * j.block_size, j.knew[new_off + c]);
+    store_through(j.v_cache + base + (int64_t)c * j.block_size, j.vnew[new_off + c]);
   }
 }
 
 // Quantise page `page` of (seq, kvh) from the fp16 pool and write it to its
 // slot of the page pool.  Called by all NT (>= 128) threads of a workgroup
-// (it synchronises them); with j.append the token at position L - 1 is
-// taken from the input row, which this workgroup has just written.
+// (it synchronises them, and the caller synchronises them again before it
+// reuses the LDS); with j.append the token at position L - 1 is taken from
+// the input row.
 template <int NT>
 __device__ void kivi_build_page(KiviBuildSmem& sm, const PageJob& j, int seq, int kvh, int page, int L, int tid) {
   static_assert(NT >= 128, "one thread per channel");
@@ -118,24 +140,66 @@ __device__ void kivi_build_page(KiviBuildSmem& sm, const PageJob& j, int seq, in
   if (pid < 0 || pid >= j.num_pages) return;
   const int64_t new_off = ((int64_t)seq * j.num_kv_heads + kvh) * D;
 
-  // gather the 32 tokens: element (token t, channel c) of the fp16 pool
-  for (int i = tid; i < T * D; i += NT) {
-    const int c = i / T, t = i % T;
-    const int tok = page * T + t;
+  // gather the 32 tokens: element (token t, channel c) of the fp16 pool; the
+  // token at L - 1 of an append comes from the input row (it may still be in
+  // flight to the pool)
+  const int32_t* btab = j.block_tables + (int64_t)seq * j.max_blocks_per_seq;
+  auto phys_of = [&](int tok) {
     const int lb = tok / j.block_size;
-    int phys = (lb < j.max_blocks_per_seq) ? j.block_tables[(int64_t)seq * j.max_blocks_per_seq + lb] : -1;
-    if (phys >= j.num_blocks) phys = -1;
-    uint16_t kv = 0, vv = 0;
-    if (j.append && tok == L - 1) {          // just written by this workgroup: take it from the input
-      kv = j.knew[new_off + c];
-      vv = j.vnew[new_off + c];
-    } else if (phys >= 0) {
-      const int64_t off = (((int64_t)phys * j.num_kv_heads + kvh) * D + c) * j.block_size + tok % j.block_size;
-      kv = j.k_cache[off];
-      vv = j.v_cache[off];
+    const int phys = (lb < j.max_blocks_per_seq) ? btab[lb] : -1;
+    return (phys < 0 || phys >= j.num_blocks) ? -1 : phys;
+  };
+  if (j.block_size % 8 == 0) {
+    // 16-byte runs: 8 tokens of one channel are contiguous in one block;
+    // the loads of all of a thread's runs are issued before the LDS stores
+    constexpr int RUNS = D * T / 8, PER = (RUNS + NT - 1) / NT;
+    u32x4 kr[PER], vr[PER];
+#pragma unroll
+    for (int r = 0; r < PER; ++r) {
+      const int i = tid + r * NT;
+      const int c = i / (T / 8), tok = page * T + (i % (T / 8)) * 8;
+      const int phys = i < RUNS ? phys_of(tok) : -1;
+      kr[r] = vr[r] = u32x4{0u, 0u, 0u, 0u};
+      if (phys >= 0) {
+        const int64_t off = (((int64_t)phys * j.num_kv_heads + kvh) * D + c) * j.block_size + tok % j.block_size;
+        kr[r] = load16(j.k_cache + off);
+        vr[r] = load16(j.v_cache + off);
+      }
     }
-    sm.k[c][t] = kv;
-    sm.v[t][c] = vv;
+#pragma unroll
+    for (int r = 0; r < PER; ++r) {
+      const int i = tid + r * NT;
+      if (i >= RUNS) break;
+      const int c = i / (T / 8), t0 = (i % (T / 8)) * 8;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        uint16_t kv = (uint16_t)(word(kr[r], e / 2) >> (16 * (e & 1)));
+        uint16_t vv = (uint16_t)(word(vr[r], e / 2) >> (16 * (e & 1)));
+        if (j.append && page * T + t0 + e == L - 1) {
+          kv = j.knew[new_off + c];
+          vv = j.vnew[new_off + c];
+        }
+        sm.k[c][t0 + e] = kv;
+        sm.v[t0 + e][c] = vv;
+      }
+    }
+  } else {
+    for (int i = tid; i < T * D; i += NT) {
+      const int c = i / T, t = i % T;
+      const int tok = page * T + t;
+      const int phys = phys_of(tok);
+      uint16_t kv = 0, vv = 0;
+      if (j.append && tok == L - 1) {
+        kv = j.knew[new_off + c];
+        vv = j.vnew[new_off + c];
+      } else if (phys >= 0) {
+        const int64_t off = (((int64_t)phys * j.num_kv_heads + kvh) * D + c) * j.block_size + tok % j.block_size;
+        kv = j.k_cache[off];
+        vv = j.v_cache[off];
+      }
+      sm.k[c][t] = kv;
+      sm.v[t][c] = vv;
+    }
   }
   __syncthreads();
 

@@ -358,7 +358,8 @@ def kivi_workspace_bytes(desc, max_context_len) -> int:
 
 def kivi_decode_step(desc, out, q, key, value, slot_mapping, pages, page_tables, k_cache, v_cache,
                      block_tables, seq_lens, max_context_len, workspace=None, stream=None):
-    """kivi_append then kivi_paged_attention_decode (seq_lens after the append) in one call."""
+    """kivi_append then kivi_paged_attention_decode (seq_lens after the append) in one call and one
+    decode launch; slot_mapping[s] is the pool slot of position seq_lens[s] - 1."""
     ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
     check(lib.tl_kivi_decode_step(
         ctypes.byref(desc), _ptr(out), _ptr(q), _ptr(key), _ptr(value), _ptr(slot_mapping), _ptr(pages),
