@@ -85,12 +85,17 @@ def parse():
 USE_GRAPH = True
 
 
+WARM_MS = 30.0
+
+
 def timed(step, steps, warmup):
     """Run `warmup` eager steps, capture the next `steps` steps into one HIP
-    graph, replay it once untimed, then time one replay with events on the
-    replay stream.  Returns ms per step.  A serving decode loop runs the same
-    way: the graph removes the per-launch host cost, which otherwise exceeds a
-    short step's GPU time."""
+    graph, replay it untimed until about WARM_MS of GPU work has run, then
+    time one replay with events on the replay stream.  Returns ms per step.
+    A serving decode loop runs the same way: the graph removes the per-launch
+    host cost, which otherwise exceeds a short step's GPU time, and the GPU
+    runs at the clocks of sustained load (from an idle GPU the first ~10 ms
+    of the KIVI decode ran up to 10 % slower)."""
     import torch
     stream = torch.cuda.current_stream()
     for i in range(warmup):
@@ -109,9 +114,14 @@ def timed(step, steps, warmup):
     with torch.cuda.graph(graph, stream=cap):
         for i in range(steps):
             step(warmup + i, cap)
-    graph.replay()
-    torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    graph.replay()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    for _ in range(min(50, int(WARM_MS / max(e0.elapsed_time(e1), 1e-3)))):
+        graph.replay()
+    torch.cuda.synchronize()
     e0.record(stream)
     graph.replay()
     e1.record(stream)

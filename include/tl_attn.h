@@ -232,7 +232,10 @@ int tl_kivi_paged_attention_decode(const tl_kivi_desc* desc, void* out, const vo
  * completes is built in the same launch.  slot_mapping[s] must be the pool
  * slot of position seq_lens[s] - 1 in block_tables, as an append step's slot
  * is; a negative slot writes nothing and that position is read from the
- * pool, as the two calls would. */
+ * pool, as the two calls would.  The token is stored by rewriting its
+ * block's rows of each kv head (128 channels x 16 slots; the other slots
+ * keep their bytes), so no other writer may touch that block during the
+ * call: a block that a sequence appends to belongs to that sequence. */
 int tl_kivi_decode_step(const tl_kivi_desc* desc, void* out, const void* q, const void* key,
                         const void* value, const int32_t* slot_mapping, void* pages,
                         const int32_t* page_tables, void* k_cache, void* v_cache,

@@ -396,17 +396,49 @@ __device__ __forceinline__ void newest_state(const Params& p, const NewestToken&
   }
 }
 
-// The new token into the fp16 pool from the wavefront's registers (stores
-// written through L2, as kivi_append_token's).
+// Replace 16-bit element e (0..7) of a 16-byte chunk.
+__device__ __forceinline__ void put_half(u32x4& c, int e, uint32_t v) {
+  const uint32_t sh = 16 * (e & 1), keep = ~(0xFFFFu << sh), ins = (v & 0xFFFFu) << sh;
+  const int w = e / 2;
+  c.x = w == 0 ? (c.x & keep) | ins : c.x;
+  c.y = w == 1 ? (c.y & keep) | ins : c.y;
+  c.z = w == 2 ? (c.z & keep) | ins : c.z;
+  c.w = w == 3 ? (c.w & keep) | ins : c.w;
+}
+
+// The new token into the fp16 pool, by one wavefront holding its channels
+// 2 lane and 2 lane + 1 (t).  A token's 128 channels are 2-byte elements
+// 32 bytes apart, and HBM3E has no byte masks: scattered 2-byte stores cost
+// a step at batch 64 about 4 us (left in L2) or 1.4 us (written through),
+// mostly in the memory's read-modify-writes.  So the block's rows of this
+// kv head (128 channels x 16 slots, 4 KiB each of K and V) are read, the
+// slot replaced, and the rows written back whole (about 0.3 us).  The other
+// slots keep their bytes; no other writer may touch the block during the
+// call (a block that a sequence appends to belongs to that sequence; the
+// other head slices of the same (seq, kv head) write the same bytes).
 __device__ __forceinline__ void store_newest(const PageJob& j, const NewestToken& t, int seq, int kvh, int lane) {
+  constexpr int BS = 16;   // the paged KIVI calls take block_size 16 only
   const int32_t slot = j.slots[seq];
-  const int blk = slot >= 0 ? slot / j.block_size : -1;
+  const int blk = slot >= 0 ? slot / BS : -1;
   if (blk < 0 || blk >= j.num_blocks) return;
-  const int64_t off = (((int64_t)blk * j.num_kv_heads + kvh) * kKiviHead + 2 * lane) * j.block_size + slot % j.block_size;
-  store_through(j.k_cache + off, uint16_t(t.k));
-  store_through(j.k_cache + off + j.block_size, uint16_t(t.k >> 16));
-  store_through(j.v_cache + off, uint16_t(t.v));
-  store_through(j.v_cache + off + j.block_size, uint16_t(t.v >> 16));
+  const int64_t base = ((int64_t)blk * j.num_kv_heads + kvh) * kKiviHead * BS;
+  const int s = slot % BS;
+  // chunk i = 4 lane + r: channel i / 2 (= 2 lane + r / 2), slots 8 (i % 2) .. +7
+  u32x4 kr[4], vr[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    kr[r] = load16(j.k_cache + base + 8 * (4 * lane + r));
+    vr[r] = load16(j.v_cache + base + 8 * (4 * lane + r));
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    if ((r & 1) == s / 8) {
+      put_half(kr[r], s % 8, (r & 2) ? t.k >> 16 : t.k);
+      put_half(vr[r], s % 8, (r & 2) ? t.v >> 16 : t.v);
+    }
+    *reinterpret_cast<u32x4*>(j.k_cache + base + 8 * (4 * lane + r)) = kr[r];
+    *reinterpret_cast<u32x4*>(j.v_cache + base + 8 * (4 * lane + r)) = vr[r];
+  }
 }
 
 // Slots 0 .. NW-1: one per wavefront; slot NW: the newest token.
@@ -467,7 +499,7 @@ __global__ __launch_bounds__(NW * kWave, 2) void kivi_decode_kernel(KiviParams k
                                   lq / kKiviPageTokens - 1, L, tid);
       __syncthreads();   // the page is visible to the workgroup; the LDS is free again
     }
-    if (last && !has_res && wave == 0) kivi_append_token<kWave>(k.job, seq, kvh, tid);
+    if (last && !has_res && wave == 0) store_newest(k.job, newest_from_row(k.job, seq, kvh, tid), seq, kvh, tid);
   }
   if (wave < page_waves) {
     kivi_pages_wave(k, seq, kvh, hs, pg0 + wave, pg1, page_waves, &sd.p[wave][0], &sd.acc[wave][0][0],
@@ -482,8 +514,8 @@ __global__ __launch_bounds__(NW * kWave, 2) void kivi_decode_kernel(KiviParams k
     decode2_wave<Kind::F16, kKiviHead, 16>(p, seq, kvh, hs, lq, L - 1, 32, &sd.p[wave][0],
                                            &sd.acc[wave][0][0], &sd.m[wave][0], &sd.l[wave][0]);
     newest_state(p, nt, seq, kvh, hs, lane, &sd.acc[NW][0][0], &sd.m[NW][0], &sd.l[NW][0]);
-    // the token's store, at the end of the window: issued earlier (in its
-    // first iteration) it cost the step 6 us more at batch 64, ctx 4096
+    // the token's store, at the end of the window, off the page wavefronts'
+    // path (the window ends halfway through the launch)
     if constexpr (APPEND) store_newest(k.job, nt, seq, kvh, lane);
   }
   __syncthreads();
@@ -525,7 +557,9 @@ int launch_kivi_decode(const KiviDecodeLaunch& a) {
   if (append) k.job = make_page_job(*a.append);
   const unsigned items = (unsigned)(a.num_seqs * a.num_kv_heads * p.head_slices);
   if (a.num_partitions == 1) {
-    launch_decode<8, true>(k, append, items, a.stream);
+    // 4 wavefronts per workgroup, two workgroups per CU: at batch 64 the
+    // grid is resident in one round (65.1 against 67.1 us with 8)
+    launch_decode<4, true>(k, append, items, a.stream);
   } else {
     launch_decode<4, false>(k, append, items * a.num_partitions, a.stream);
     if (hipGetLastError() != hipSuccess) return 5;
