@@ -73,7 +73,7 @@ def parse():
     p.add_argument("--partition-tokens", type=int, default=0)
     p.add_argument("--cpu-seconds", type=float, default=15.0)
     p.add_argument("--no-cpu", action="store_true")
-    p.add_argument("--only", default="all", choices=["all", "bf16", "fp16", "kivi", "fp8", "prefill"])
+    p.add_argument("--only", default="all", choices=["all", "bf16", "fp16", "kivi", "fp8", "prefill", "blocks"])
     p.add_argument("--no-graph", action="store_true",
                    help="launch the timed steps eagerly (for counter passes that cannot follow graphs)")
     p.add_argument("--copy-calibration", action="store_true",
@@ -251,6 +251,32 @@ def bench_kivi(args, R=128):
 F8_S, F8_CTX = 16, 32768
 
 
+CB_BLOCKS, CB_PAIRS = 8192, 2048
+
+
+def bench_copy_blocks(args):
+    """copy_blocks: 2048 (src, dst) pairs out of an 8192-block fp16 pool pair
+    (8 kv heads, d 128, bs 16: 32 KiB per block and pool), the shape of a
+    prefix-cache fork of 2048 blocks.  Bytes moved = 2 pools x pairs x block
+    read + written."""
+    import torch
+
+    import tl_attn as tla
+
+    g = torch.Generator(device="cuda").manual_seed(0x7E5E0006)
+    k = torch.randn(CB_BLOCKS, NKV, D, BS, generator=g, device="cuda", dtype=torch.float16)
+    v = torch.randn_like(k)
+    perm = torch.randperm(CB_BLOCKS, generator=g, device="cuda")
+    m = torch.stack([perm[:CB_PAIRS], perm[CB_PAIRS:2 * CB_PAIRS]], 1).to(torch.int32).contiguous()
+
+    def step(i, stream):
+        tla.copy_blocks(k, v, m, stream)
+
+    ms = timed(step, args.steps, args.warmup)
+    nbytes = 2 * 2 * CB_PAIRS * k[0].numel() * k.element_size()
+    return {"ms": ms, "bytes": nbytes, "gbs": nbytes / (ms * 1e-3) / 1e9}
+
+
 def bench_fp8(args):
     """FP8 E4M3 KV long-context decode: batch 16, 32 q / 8 kv heads, d 128,
     bs 16, every context 32768, per-tensor fp32 scales absmax/448 (K/V drawn
@@ -418,6 +444,7 @@ def main():
         kv = bench_kivi(args)
     f8 = bench_fp8(args) if args.only in ("all", "fp8") else None
     pf = bench_prefill(args) if args.only in ("all", "prefill") else None
+    cb = bench_copy_blocks(args) if args.only in ("all", "blocks") else None
     head = bf or fp
     if head is not None:
         res["dtype"] = "bf16" if bf else "fp16"
@@ -476,6 +503,12 @@ def main():
             "tflops": round(pf["tflops"], 2), "pct_mfma_peak_bf16": round(100 * pf["tflops"] / 2500.0, 2),
             "ms_per_4_launches": round(pf["ms_per_step"], 5), "ms_per_launch": round(pf["ms_per_launch"], 5),
             "flops_per_4_launches": pf["flops"]}
+    if cb is not None:
+        res["copy_blocks"] = {
+            "workload": f"copy_blocks, {CB_PAIRS} pairs of {NKV} x {D} x {BS} fp16 blocks (K and V pools of "
+                        f"{CB_BLOCKS} blocks)",
+            "gbs": round(cb["gbs"], 2), "pct_hbm_peak": round(100 * cb["gbs"] / HBM_PEAK_GBS, 2),
+            "us_per_call": round(cb["ms"] * 1e3, 2), "bytes_per_call": cb["bytes"]}
     if not args.no_cpu:
         res["cpu_baseline"] = cpu_baseline(args.cpu_seconds, 4, min(16, os.cpu_count() or 1))
     print(json.dumps(res), flush=True)

@@ -140,6 +140,31 @@ int tl_fp8_absmax_scale(const void* x, int32_t dtype, int64_t n, float* scale_ou
                         void* stream);
 
 /* ------------------------------------------------------------------------
+ * KV-cache block management
+ * --------------------------------------------------------------------- */
+
+/* Replaces copy_blocks (cache_kernels.cu:234-262, kernel :107-131): for each
+ * pair p of block_mapping (device int32 [num_pairs, 2] = {src, dst}), block
+ * src of k_cache and of v_cache is copied to block dst of the same pool.  A
+ * block is block_bytes bytes (num_kv_heads * head_size * block_size *
+ * element size; any dtype, bytes are moved as they are).  Pairs with an id
+ * outside [0, num_blocks) are skipped (the reference's kernel writes out of
+ * bounds).  A dst must not be the src or dst of another pair of the call
+ * (the pairs run concurrently, as in the reference). */
+int tl_copy_blocks(void* k_cache, void* v_cache, const int32_t* block_mapping, int32_t num_pairs,
+                   int32_t num_blocks, int64_t block_bytes, void* stream);
+
+/* Replaces swap_blocks (cache_kernels.cu:264-284, kernel :133-167): whole
+ * blocks between a device pool and a host buffer in pinned memory
+ * (hipHostMalloc).  direction 0: device block src -> host block dst; 1: host
+ * block src -> device block dst.  block_bytes as for tl_copy_blocks (the
+ * reference sizes it from shape[4] of a 4-D view, defect D16).  Ids outside
+ * [0, num_device_blocks) / [0, num_host_blocks) skip the pair. */
+int tl_swap_blocks(void* cache, void* host_cache, const int32_t* block_mapping, int32_t num_pairs,
+                   int32_t num_device_blocks, int32_t num_host_blocks, int64_t block_bytes,
+                   int32_t direction, void* stream);
+
+/* ------------------------------------------------------------------------
  * Reference KIVI vector codec (kivi_cache.cuh:27-84, kivi_cache.cu:23-239)
  * --------------------------------------------------------------------- */
 

@@ -84,6 +84,17 @@ void reshape_and_cache(const truellm::TrueBuffer& key, const truellm::TrueBuffer
                        truellm::TrueBuffer& kv_cache, const truellm::TrueBuffer& slot_mapping,
                        hipStream_t stream);
 
+/* cache_kernels.cu:234-238.  kv_cache [2N, n_kv, d, bs] (K blocks, then V);
+ * block_mapping int32 [num_pairs, 2] on the device.  Any element type. */
+void copy_blocks(truellm::TrueBuffer& kv_cache, const truellm::TrueBuffer& block_mapping, hipStream_t stream);
+
+/* cache_kernels.cu:264-269.  kv_cache [M, n_kv, d, bs] on the device,
+ * host_cache [M', n_kv, d, bs] in pinned host memory; block ids index dim 0
+ * of each; direction 0: device -> host, 1: host -> device.  The block size
+ * is dims 1-3 times the element size (the reference reads shape[4], D16). */
+void swap_blocks(truellm::TrueBuffer& kv_cache, truellm::TrueBuffer& host_cache,
+                 const truellm::TrueBuffer& block_mapping, int direction, hipStream_t stream);
+
 /* paged_attention_v1.cu:177-189 */
 void paged_attention_v1(truellm::TrueBuffer& out, const truellm::TrueBuffer& q,
                         const truellm::TrueBuffer& k_cache, const truellm::TrueBuffer& v_cache,

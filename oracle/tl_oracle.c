@@ -186,6 +186,39 @@ void orc_reshape_and_cache_fp8(const void* key, const void* value, int src_dtype
 }
 
 /* ========================================================================
+ * copy_blocks  (cache_kernels.cu:107-131, :234-262)
+ *   for each pair {src, dst}: pool[dst] = pool[src], for the K and the V
+ *   pool; pairs with an id outside [0, num_blocks) are skipped
+ * swap_blocks  (cache_kernels.cu:133-167, :264-284)
+ *   direction 0: host[dst] = dev[src]; 1: dev[dst] = host[src]
+ * ====================================================================== */
+
+void orc_copy_blocks(void* k_cache, void* v_cache, const int32_t* mapping, int num_pairs,
+                     int num_blocks, int64_t block_bytes)
+{
+    for (int p = 0; p < num_pairs; ++p) {
+        int32_t src = mapping[2 * p], dst = mapping[2 * p + 1];
+        if (src < 0 || src >= num_blocks || dst < 0 || dst >= num_blocks) continue;
+        memmove((char*)k_cache + dst * block_bytes, (const char*)k_cache + src * block_bytes, (size_t)block_bytes);
+        memmove((char*)v_cache + dst * block_bytes, (const char*)v_cache + src * block_bytes, (size_t)block_bytes);
+    }
+}
+
+void orc_swap_blocks(void* cache, void* host_cache, const int32_t* mapping, int num_pairs,
+                     int num_device_blocks, int num_host_blocks, int64_t block_bytes, int direction)
+{
+    for (int p = 0; p < num_pairs; ++p) {
+        int32_t src = mapping[2 * p], dst = mapping[2 * p + 1];
+        const char* from = direction == 0 ? (const char*)cache : (const char*)host_cache;
+        char* to = direction == 0 ? (char*)host_cache : (char*)cache;
+        int nf = direction == 0 ? num_device_blocks : num_host_blocks;
+        int nt = direction == 0 ? num_host_blocks : num_device_blocks;
+        if (src < 0 || src >= nf || dst < 0 || dst >= nt) continue;
+        memcpy(to + dst * block_bytes, from + src * block_bytes, (size_t)block_bytes);
+    }
+}
+
+/* ========================================================================
  * Paged attention, intended semantics (double accumulation)
  * ====================================================================== */
 

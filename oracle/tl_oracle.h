@@ -50,6 +50,10 @@ void orc_reshape_and_cache(const void* key, const void* value,
                            int num_kv_heads, int head_size, int block_size,
                            int elem_bytes);
 /* FP8 variant: e4m3(float(x) * (1/k_scale)) from f16/bf16 sources. */
+void orc_copy_blocks(void* k_cache, void* v_cache, const int32_t* mapping, int num_pairs,
+                     int num_blocks, int64_t block_bytes);
+void orc_swap_blocks(void* cache, void* host_cache, const int32_t* mapping, int num_pairs,
+                     int num_device_blocks, int num_host_blocks, int64_t block_bytes, int direction);
 void orc_reshape_and_cache_fp8(const void* key, const void* value, int src_dtype,
                                uint8_t* k_cache, uint8_t* v_cache,
                                const int32_t* slot_mapping, int num_tokens,

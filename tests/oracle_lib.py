@@ -36,6 +36,8 @@ _lib.orc_e4m3_to_f32.argtypes = [ctypes.c_uint8]
 _lib.orc_convert.argtypes = [_P, _I, _P, _I, ctypes.c_int64, _F]
 _lib.orc_reshape_and_cache.argtypes = [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I]
 _lib.orc_reshape_and_cache_fp8.argtypes = [_P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _F, _F]
+_lib.orc_copy_blocks.argtypes = [_P, _P, _P, _I, _I, ctypes.c_int64]
+_lib.orc_swap_blocks.argtypes = [_P, _P, _P, _I, _I, _I, ctypes.c_int64, _I]
 _lib.orc_paged_attention.argtypes = [_P, _P, _I, _P, _P, _I, _F, _F, _P, _I, _P, _I, _I, _I, _I, _I, _F, _I, _I]
 _lib.orc_paged_attention_f32.argtypes = [_P, _I, _P, _I, _P, _P, _I, _F, _F, _P, _I, _P, _I, _I, _I, _I, _I, _F, _I, _I]
 _lib.orc_paged_attention_literal_v1.argtypes = [_P, _P, _P, _P, _I, _P, _I, _P, _I, _I, _I, _I, _I, _F]
@@ -108,6 +110,18 @@ def reshape_and_cache(key, value, k_cache, v_cache, slots):
     T, n_kv, D = key.shape
     _lib.orc_reshape_and_cache(ptr(key), ptr(value), ptr(k_cache), ptr(v_cache), ptr(slots), T,
                                n_kv, D, k_cache.shape[3], key.dtype.itemsize)
+
+
+def copy_blocks(k_cache, v_cache, mapping):
+    """In place on numpy pools [N, ...]; mapping int32 [P, 2]."""
+    nb = k_cache.shape[0]
+    _lib.orc_copy_blocks(ptr(k_cache), ptr(v_cache), ptr(mapping), mapping.shape[0], nb,
+                         k_cache[0].nbytes)
+
+
+def swap_blocks(cache, host_cache, mapping, direction):
+    _lib.orc_swap_blocks(ptr(cache), ptr(host_cache), ptr(mapping), mapping.shape[0], cache.shape[0],
+                         host_cache.shape[0], cache[0].nbytes, direction)
 
 
 def reshape_and_cache_fp8(key, value, src_code, k_cache, v_cache, slots, k_scale, v_scale):

@@ -115,6 +115,19 @@ def test_reshape_rejects_bad_arguments():
     assert L.tl_fp8_absmax_scale(FAKE, tla.F16, -1, FAKE, None) == tla.ERR_INVALID_ARGUMENT
 
 
+def test_block_ops_reject_bad_arguments_and_empty_is_a_no_op():
+    L = tla.lib
+    assert L.tl_copy_blocks(FAKE, FAKE, FAKE, 3, 0, 4096, None) == tla.ERR_INVALID_ARGUMENT
+    assert L.tl_copy_blocks(FAKE, FAKE, FAKE, -1, 8, 4096, None) == tla.ERR_INVALID_ARGUMENT
+    assert L.tl_copy_blocks(FAKE, FAKE, FAKE, 3, 8, 0, None) == tla.ERR_INVALID_ARGUMENT
+    assert L.tl_copy_blocks(None, FAKE, FAKE, 3, 8, 4096, None) == tla.ERR_INVALID_ARGUMENT
+    assert L.tl_copy_blocks(None, None, None, 0, 8, 4096, None) == tla.OK
+    assert L.tl_swap_blocks(FAKE, FAKE, FAKE, 3, 8, 8, 4096, 2, None) == tla.ERR_INVALID_ARGUMENT
+    assert L.tl_swap_blocks(FAKE, FAKE, FAKE, 3, 8, 0, 4096, 0, None) == tla.ERR_INVALID_ARGUMENT
+    assert L.tl_swap_blocks(FAKE, None, FAKE, 3, 8, 8, 4096, 1, None) == tla.ERR_INVALID_ARGUMENT
+    assert L.tl_swap_blocks(None, None, None, 0, 8, 8, 4096, 0, None) == tla.OK
+
+
 def test_kivi_host_helpers_match_reference_known_answers():
     # test_kivi_bounds.cpp:25-69, through the library
     assert tla.kivi_compressed_bytes(128, 8, 16) == 24 + 8 * 12
@@ -192,6 +205,8 @@ def test_exports_reference_named_operators():
         "truellm::kivi_params_supported(int, int, int)",
         "truellm::kivi_compress(__half const*, unsigned char*, int, int, int, int, ihipStream_t*)",
         "truellm::kivi_decompress(unsigned char const*, __half*, int, int, int, int, ihipStream_t*)",
+        "copy_blocks(truellm::TrueBuffer&, truellm::TrueBuffer const&, ihipStream_t*)",
+        "swap_blocks(truellm::TrueBuffer&, truellm::TrueBuffer&, truellm::TrueBuffer const&, int, ihipStream_t*)",
         "truellm_kernel_init",
     ]
     missing = [w for w in want if w not in exp]

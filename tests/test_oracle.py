@@ -477,3 +477,65 @@ def test_kivi_quantized_len():
     for L in range(0, 600, 7):
         lq = orc.kivi_quantized_len(L, 128)
         assert lq % 32 == 0 and (L < 160 or 128 <= L - lq < 160)
+
+
+# ---------------------------------------------------------------------------
+# block management (copy_blocks / swap_blocks)
+# ---------------------------------------------------------------------------
+
+def _pools(rng, n, shape, dtype):
+    k = rng.integers(0, 256, size=(n,) + shape + (np.dtype(dtype).itemsize,), dtype=np.uint8)
+    v = rng.integers(0, 256, size=k.shape, dtype=np.uint8)
+    return k.view(dtype).reshape((n,) + shape), v.view(dtype).reshape((n,) + shape)
+
+
+@pytest.mark.parametrize("dtype", [np.float16, np.float32, np.uint8])
+def test_copy_blocks_oracle_matches_fancy_indexing(dtype):
+    """orc_copy_blocks against numpy's pool[dst] = pool[src] for distinct
+    destinations that are not sources; K and V move independently, other
+    blocks keep their bytes, out-of-range pairs are skipped."""
+    rng = np.random.default_rng(21)
+    N = 24
+    k, v = _pools(rng, N, (2, 8, 16), dtype)
+    perm = rng.permutation(N)
+    src, dst = perm[:8], perm[8:16]
+    mapping = np.stack([src, dst], 1).astype(np.int32)
+    bad = np.array([[-1, 3], [2, N], [N + 5, 0]], np.int32)
+    full = np.concatenate([mapping, bad]).copy()
+    ek, ev = k.copy(), v.copy()
+    ek[dst] = k[src]
+    ev[dst] = v[src]
+    orc.copy_blocks(k, v, full)
+    assert np.array_equal(k.view(np.uint8), ek.view(np.uint8))
+    assert np.array_equal(v.view(np.uint8), ev.view(np.uint8))
+
+
+def test_copy_blocks_oracle_identity_is_a_no_op():
+    rng = np.random.default_rng(22)
+    k, v = _pools(rng, 6, (4, 4), np.float16)
+    k0, v0 = k.copy(), v.copy()
+    orc.copy_blocks(k, v, np.array([[i, i] for i in range(6)], np.int32))
+    assert np.array_equal(k.view(np.uint16), k0.view(np.uint16))
+    assert np.array_equal(v.view(np.uint16), v0.view(np.uint16))
+
+
+def test_swap_blocks_oracle_round_trip():
+    """Out to the host buffer (direction 0) and back (direction 1) restores
+    the evicted blocks; each direction matches numpy indexing."""
+    rng = np.random.default_rng(23)
+    dev_pool, _ = _pools(rng, 20, (8, 16), np.float16)
+    host = np.zeros((10,) + dev_pool.shape[1:], np.float16)
+    src = np.array([3, 17, 0, 9], np.int32)
+    slots = np.array([7, 0, 2, 9], np.int32)
+    out_map = np.stack([src, slots], 1).astype(np.int32).copy()
+    orc.swap_blocks(dev_pool, host, out_map, 0)
+    assert np.array_equal(host[slots].view(np.uint16), dev_pool[src].view(np.uint16))
+    saved = dev_pool[src].copy()
+    dev_pool[src] = 0
+    back = np.stack([slots, src], 1).astype(np.int32).copy()
+    orc.swap_blocks(dev_pool, host, back, 1)
+    assert np.array_equal(dev_pool[src].view(np.uint16), saved.view(np.uint16))
+    # ids outside either pool skip the pair
+    before = host.copy()
+    orc.swap_blocks(dev_pool, host, np.array([[20, 0], [0, 10], [-1, 1]], np.int32), 0)
+    assert np.array_equal(host.view(np.uint16), before.view(np.uint16))

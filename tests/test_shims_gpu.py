@@ -54,6 +54,8 @@ V1 = _fn("_Z18paged_attention_v1RN7truellm10TrueBufferERKS0_S3_S3_S3_S3_ifiiP12i
 V2 = _fn("_Z18paged_attention_v2RN7truellm10TrueBufferES1_S1_S1_RKS0_S3_S3_S3_S3_ifiiiP12ihipStream_t",
          [_R] * 9 + [ctypes.c_int, ctypes.c_float, ctypes.c_int, ctypes.c_int, ctypes.c_int, _S])
 RC = _fn("_Z17reshape_and_cacheRKN7truellm10TrueBufferES2_RS0_S2_P12ihipStream_t", [_R] * 4 + [_S])
+CB = _fn("_Z11copy_blocksRN7truellm10TrueBufferERKS0_P12ihipStream_t", [_R] * 2 + [_S])
+SB = _fn("_Z11swap_blocksRN7truellm10TrueBufferES1_RKS0_iP12ihipStream_t", [_R] * 3 + [ctypes.c_int, _S])
 KC = _fn("_ZN7truellm13kivi_compressEPK6__halfPhiiiiP12ihipStream_t",
          [_S, _S] + [ctypes.c_int] * 4 + [_S])
 KD = _fn("_ZN7truellm15kivi_decompressEPKhP6__halfiiiiP12ihipStream_t",
@@ -152,3 +154,25 @@ def test_manifest_initialize_accepts_this_device():
     torch.cuda.synchronize()
     assert m.initialize(None) == 0
     m.shutdown(None)
+
+
+def test_block_shims_equal_c_abi():
+    """copy_blocks on the [2N, n_kv, d, bs] buffer (K blocks then V) and
+    swap_blocks to a pinned host buffer, by their reference names."""
+    g = torch.Generator(device="cuda").manual_seed(5)
+    N, n_kv, D, BS = 48, 8, 128, 16
+    kv_a = torch.randn(2 * N, n_kv, D, BS, generator=g, device="cuda", dtype=torch.float16)
+    kv_b = kv_a.clone()
+    m = torch.tensor([[3, 40], [7, 1], [12, 13], [47, 0]], dtype=torch.int32, device="cuda")
+    print("case shim copy_blocks", flush=True)
+    CB(tb(kv_a), tb(m), _stream())
+    tla.copy_blocks(kv_b[:N], kv_b[N:], m)
+    torch.cuda.synchronize()
+    assert torch.equal(kv_a.view(torch.int16), kv_b.view(torch.int16))
+    assert torch.equal(kv_a[40], kv_a[3]) and torch.equal(kv_a[N + 40], kv_a[N + 3])
+    host = torch.zeros(6, n_kv, D, BS, dtype=torch.float16, pin_memory=True)
+    sm = torch.tensor([[5, 2], [90, 4]], dtype=torch.int32, device="cuda")
+    print("case shim swap_blocks", flush=True)
+    SB(tb(kv_a), tb(host), tb(sm), 0, _stream())
+    torch.cuda.synchronize()
+    assert torch.equal(host[2], kv_a[5].cpu()) and torch.equal(host[4], kv_a[90].cpu())

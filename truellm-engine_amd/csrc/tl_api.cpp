@@ -251,6 +251,40 @@ int tl_reshape_and_cache(const void* key, const void* value, void* k_cache, void
   return ok();
 }
 
+int tl_copy_blocks(void* k_cache, void* v_cache, const int32_t* block_mapping, int32_t num_pairs,
+                   int32_t num_blocks, int64_t block_bytes, void* stream) {
+  if (num_pairs < 0 || num_blocks <= 0 || block_bytes <= 0)
+    return fail(TL_ERR_INVALID_ARGUMENT, "num_pairs=%d num_blocks=%d block_bytes=%lld", num_pairs, num_blocks,
+                (long long)block_bytes);
+  if (num_pairs == 0) return ok();
+  if (!k_cache || !v_cache || !block_mapping) return fail(TL_ERR_INVALID_ARGUMENT, "NULL pointer");
+  tl::BlockCopy c = {(const char*)k_cache, (const char*)v_cache, (char*)k_cache, (char*)v_cache,
+                     block_mapping, num_pairs, 2, num_blocks, num_blocks, block_bytes, 0};
+  const int rc = tl::launch_block_copy(c, (hipStream_t)stream);
+  if (rc == 3) return fail(TL_ERR_NOT_IMPLEMENTED, "copy_blocks grid too large: %d pairs", num_pairs);
+  if (rc) return fail(TL_ERR_BACKEND, "copy_blocks launch failed");
+  return ok();
+}
+
+int tl_swap_blocks(void* cache, void* host_cache, const int32_t* block_mapping, int32_t num_pairs,
+                   int32_t num_device_blocks, int32_t num_host_blocks, int64_t block_bytes,
+                   int32_t direction, void* stream) {
+  if (num_pairs < 0 || num_device_blocks <= 0 || num_host_blocks <= 0 || block_bytes <= 0)
+    return fail(TL_ERR_INVALID_ARGUMENT, "num_pairs=%d num_device_blocks=%d num_host_blocks=%d block_bytes=%lld",
+                num_pairs, num_device_blocks, num_host_blocks, (long long)block_bytes);
+  if (direction != 0 && direction != 1) return fail(TL_ERR_INVALID_ARGUMENT, "direction=%d", direction);
+  if (num_pairs == 0) return ok();
+  if (!cache || !host_cache || !block_mapping) return fail(TL_ERR_INVALID_ARGUMENT, "NULL pointer");
+  const bool out = direction == 0;
+  tl::BlockCopy c = {(const char*)(out ? cache : host_cache), nullptr, (char*)(out ? host_cache : cache), nullptr,
+                     block_mapping, num_pairs, 1, out ? num_device_blocks : num_host_blocks,
+                     out ? num_host_blocks : num_device_blocks, block_bytes, 0};
+  const int rc = tl::launch_block_copy(c, (hipStream_t)stream);
+  if (rc == 3) return fail(TL_ERR_NOT_IMPLEMENTED, "swap_blocks grid too large: %d pairs", num_pairs);
+  if (rc) return fail(TL_ERR_BACKEND, "swap_blocks launch failed");
+  return ok();
+}
+
 int tl_reshape_and_cache_fp8(const void* key, const void* value, int32_t src_dtype,
                              uint8_t* k_cache, uint8_t* v_cache, const int32_t* slot_mapping,
                              int32_t num_tokens, int32_t num_kv_heads, int32_t head_size,

@@ -9,6 +9,12 @@
 //
 // fp8 scale: per-tensor absmax(x)/448, the E4M3 scale convention of
 // fp8_gemm.cu:82-84, as a grid-wide max.
+//
+// Block copies (copy_blocks, cache_kernels.cu:107-131, :234-262; swap_blocks,
+// :133-167, :264-284): whole blocks between block ids of a mapping {src,
+// dst}; a workgroup moves a slice of one block of one pool in 16-byte
+// chunks (bytes when the block or a base is not 16-byte aligned).  Ids
+// outside their pool skip the pair.
 #include "tl_device.hpp"
 #include "tl_internal.hpp"
 
@@ -92,6 +98,27 @@ __global__ __launch_bounds__(256) void reshape_fp8_kernel(
   }
 }
 
+// grid.x = pairs x pools x slices; pool 1 is the second (V) pool of a copy.
+template <bool VEC>
+__global__ __launch_bounds__(256) void block_copy_kernel(BlockCopy c) {
+  int64_t b = blockIdx.x;
+  const int slice = (int)(b % c.slices); b /= c.slices;
+  const int pool = (int)(b % c.pools);
+  const int pair = (int)(b / c.pools);
+  const int32_t src = c.mapping[2 * pair], dst = c.mapping[2 * pair + 1];
+  if (src < 0 || src >= c.src_blocks || dst < 0 || dst >= c.dst_blocks) return;
+  const char* from = (pool ? c.src1 : c.src0) + (int64_t)src * c.block_bytes;
+  char* to = (pool ? c.dst1 : c.dst0) + (int64_t)dst * c.block_bytes;
+  const int64_t n = VEC ? c.block_bytes / 16 : c.block_bytes;
+  const int64_t step = (int64_t)c.slices * blockDim.x;
+  for (int64_t i = (int64_t)slice * blockDim.x + threadIdx.x; i < n; i += step) {
+    if constexpr (VEC)
+      reinterpret_cast<u32x4*>(to)[i] = reinterpret_cast<const u32x4*>(from)[i];
+    else
+      to[i] = from[i];
+  }
+}
+
 __global__ void fill_u32_kernel(uint32_t* p, uint32_t v) { *p = v; }
 
 template <Kind SRC>
@@ -145,6 +172,25 @@ int launch_reshape_and_cache(const CacheLaunch& a) {
                          (char*)a.v_cache, a.slot_mapping, a.num_tokens, a.num_kv_heads,
                          a.head_size, a.block_size, a.num_blocks);
   }
+  return hipGetLastError() == hipSuccess ? 0 : 5;
+}
+
+int launch_block_copy(const BlockCopy& c, hipStream_t stream) {
+  if (c.num_pairs <= 0) return 0;
+  const auto al = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
+  const bool vec = c.block_bytes % 16 == 0 && al(c.src0) && al(c.dst0) &&
+                   (c.pools == 1 || (al(c.src1) && al(c.dst1)));
+  BlockCopy k = c;
+  // up to 16 workgroups of 256 x 16 bytes per block: a 32 KiB block is 8
+  const int64_t units = vec ? c.block_bytes / 16 : c.block_bytes;
+  const int64_t want = (units + 255) / 256;
+  k.slices = (int)(want < 16 ? (want > 0 ? want : 1) : 16);
+  const int64_t grid = (int64_t)c.num_pairs * c.pools * k.slices;
+  if (grid > 0x7fffffff) return 3;
+  if (vec)
+    hipLaunchKernelGGL(block_copy_kernel<true>, dim3((unsigned)grid), dim3(256), 0, stream, k);
+  else
+    hipLaunchKernelGGL(block_copy_kernel<false>, dim3((unsigned)grid), dim3(256), 0, stream, k);
   return hipGetLastError() == hipSuccess ? 0 : 5;
 }
 

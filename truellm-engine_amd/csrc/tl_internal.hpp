@@ -67,6 +67,19 @@ struct CacheLaunch {
 };
 int launch_reshape_and_cache(const CacheLaunch& a);
 
+// Whole-block copies: for pair p of mapping [num_pairs][2] = {src, dst},
+// block src of src0 (and of src1 when pools == 2) to block dst of dst0
+// (dst1).  Ids outside [0, src_blocks) / [0, dst_blocks) skip the pair.
+struct BlockCopy {
+  const char* src0; const char* src1;
+  char* dst0; char* dst1;
+  const int32_t* mapping;
+  int num_pairs, pools, src_blocks, dst_blocks;
+  int64_t block_bytes;
+  int slices;                   // set by the launcher
+};
+int launch_block_copy(const BlockCopy& c, hipStream_t stream);
+
 // Log-sum-exp merge of split-K partials into out.  The partitions a sequence
 // has are ceil(L / partition_tokens), or, for KIVI (kivi_pages > 0),
 // max(1, ceil(pages(L) / kivi_pages)).

@@ -160,8 +160,6 @@ __global__ __launch_bounds__(NW * kWave) void prefill_kernel(PrefillParams pp) {
   const int pos = row_ok ? L - ql + qi : -1;           // keys 0 .. pos
   const int last_row = min(rows, row0 + NW * kPfRows) - 1;
   const int kend = max(0, L - ql + last_row / p.group + 1);           // keys of the workgroup
-  const int wlast = min(rows, wrow0 + kPfRows) - 1;
-  const int wkend = wrow0 < rows ? max(0, L - ql + wlast / p.group + 1) : 0;
   const int n_it = (kend + kPfKeys - 1) / kPfKeys;
 
   // B operand of S^T: row my_row, channels 16 ks + 8 g .. +7 (zero for padding rows)

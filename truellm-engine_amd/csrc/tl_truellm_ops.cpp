@@ -36,6 +36,16 @@ void report(const char* op, int rc) {
 
 int32_t dim(const TrueBuffer& b, int i) { return i < b.ndim ? (int32_t)b.shape[i] : 1; }
 
+// Bytes per element of a pool view: the attention dtypes, and 1 for the
+// byte-sized types (an FP8 pool is viewed as I8 / Q8 by its owner).
+int64_t elem_bytes(const TrueBuffer& b) {
+  switch (b.dtype) {
+    case DataType::F32: case DataType::I32: return 4;
+    case DataType::F16: case DataType::BF16: case DataType::I16: return 2;
+    default: return 1;
+  }
+}
+
 }  // namespace
 
 void reshape_and_cache(const TrueBuffer& key, const TrueBuffer& value, TrueBuffer& kv_cache,
@@ -49,6 +59,23 @@ void reshape_and_cache(const TrueBuffer& key, const TrueBuffer& value, TrueBuffe
   report("reshape_and_cache",
          tl_reshape_and_cache(key.data, value.data, kv_cache.data, v_cache, (const int32_t*)slot_mapping.data,
                               T, n_kv, d, bs, N, dt, stream));
+}
+
+void copy_blocks(TrueBuffer& kv_cache, const TrueBuffer& block_mapping, hipStream_t stream) {
+  // kv_cache [2N, n_kv, d, bs]: K blocks then V blocks (cache_kernels.cu:234-262)
+  const int32_t N = dim(kv_cache, 0) / 2;
+  const int64_t bytes = (int64_t)dim(kv_cache, 1) * dim(kv_cache, 2) * dim(kv_cache, 3) * elem_bytes(kv_cache);
+  report("copy_blocks", tl_copy_blocks(kv_cache.data, (char*)kv_cache.data + (int64_t)N * bytes,
+                                       (const int32_t*)block_mapping.data, dim(block_mapping, 0), N, bytes,
+                                       stream));
+}
+
+void swap_blocks(TrueBuffer& kv_cache, TrueBuffer& host_cache, const TrueBuffer& block_mapping, int direction,
+                 hipStream_t stream) {
+  const int64_t bytes = (int64_t)dim(kv_cache, 1) * dim(kv_cache, 2) * dim(kv_cache, 3) * elem_bytes(kv_cache);
+  report("swap_blocks", tl_swap_blocks(kv_cache.data, host_cache.data, (const int32_t*)block_mapping.data,
+                                       dim(block_mapping, 0), dim(kv_cache, 0), dim(host_cache, 0), bytes,
+                                       direction, stream));
 }
 
 void paged_attention_v1(TrueBuffer& out, const TrueBuffer& q, const TrueBuffer& k_cache,

@@ -107,6 +107,8 @@ _SIG = {
     "tl_paged_attention_v2": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F, _I, _I, _I, _P]),
     "tl_reshape_and_cache": (ctypes.c_int, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P]),
     "tl_reshape_and_cache_fp8": (ctypes.c_int, [_P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _I, _F, _F, _P]),
+    "tl_copy_blocks": (ctypes.c_int, [_P, _P, _P, _I, _I, ctypes.c_int64, _P]),
+    "tl_swap_blocks": (ctypes.c_int, [_P, _P, _P, _I, _I, _I, ctypes.c_int64, _I, _P]),
     "tl_fp8_absmax_scale": (ctypes.c_int, [_P, _I, ctypes.c_int64, _P, _P]),
     "tl_kivi_compressed_bytes": (ctypes.c_size_t, [_I, _I, _I]),
     "tl_kivi_params_supported": (ctypes.c_int, [_I, _I, _I]),
@@ -251,6 +253,25 @@ def reshape_and_cache_split(key, value, k_cache, v_cache, slot_mapping, stream=N
     check(lib.tl_reshape_and_cache(
         _ptr(key), _ptr(value), _ptr(k_cache), _ptr(v_cache), _ptr(slot_mapping), T, n_kv, D,
         k_cache.shape[3], k_cache.shape[0], dtype_code(key), _stream(stream)))
+
+
+def _block_bytes(pool):
+    return pool[0].numel() * pool.element_size()
+
+
+def copy_blocks(k_cache, v_cache, block_mapping, stream=None):
+    """cache_kernels.cu:234: block_mapping int32 [P, 2] = {src, dst} on the
+    device; block src of each pool is copied to block dst."""
+    check(lib.tl_copy_blocks(_ptr(k_cache), _ptr(v_cache), _ptr(block_mapping), block_mapping.shape[0],
+                             k_cache.shape[0], _block_bytes(k_cache), _stream(stream)))
+
+
+def swap_blocks(cache, host_cache, block_mapping, direction, stream=None):
+    """cache_kernels.cu:264: whole blocks between a device pool and a pinned
+    host tensor; direction 0: device -> host, 1: host -> device."""
+    check(lib.tl_swap_blocks(_ptr(cache), _ptr(host_cache), _ptr(block_mapping), block_mapping.shape[0],
+                             cache.shape[0], host_cache.shape[0], _block_bytes(cache), direction,
+                             _stream(stream)))
 
 
 def reshape_and_cache_fp8(key, value, k_cache, v_cache, slot_mapping, k_scale, v_scale,
