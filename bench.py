@@ -73,7 +73,7 @@ def parse():
     p.add_argument("--partition-tokens", type=int, default=0)
     p.add_argument("--cpu-seconds", type=float, default=15.0)
     p.add_argument("--no-cpu", action="store_true")
-    p.add_argument("--only", default="all", choices=["all", "bf16", "fp16", "kivi", "fp8", "prefill", "blocks"])
+    p.add_argument("--only", default="all", choices=["all", "bf16", "fp16", "kivi", "fp8", "prefill", "blocks", "rope"])
     p.add_argument("--no-graph", action="store_true",
                    help="launch the timed steps eagerly (for counter passes that cannot follow graphs)")
     p.add_argument("--copy-calibration", action="store_true",
@@ -249,6 +249,37 @@ def bench_kivi(args, R=128):
 
 
 F8_S, F8_CTX = 16, 32768
+
+
+def bench_rope(args):
+    """The write side of one decode step at batch 64 (Llama-3-8B shape):
+    RoPE (adjacent pairs, fp32 tables [8192, 64]) on q [64, 32, 128] and k
+    [64, 8, 128], then k and v into the bf16 pools, one launch."""
+    import torch
+
+    import tl_attn as tla
+
+    g = torch.Generator(device="cuda").manual_seed(0x7E5E0007)
+    N = S * (CTX // BS + 1)
+    q = torch.randn(S, H, D, generator=g, device="cuda", dtype=torch.bfloat16)
+    k = torch.randn(S, NKV, D, generator=g, device="cuda", dtype=torch.bfloat16)
+    v = torch.randn(S, NKV, D, generator=g, device="cuda", dtype=torch.bfloat16)
+    kc = torch.zeros(N, NKV, D, BS, device="cuda", dtype=torch.bfloat16)
+    vc = torch.zeros_like(kc)
+    slots = (torch.arange(S, device="cuda", dtype=torch.int32) * (CTX // BS + 1)) * BS + CTX % BS
+    pos = torch.full((S,), CTX, device="cuda", dtype=torch.int32)
+    i = torch.arange(D // 2, device="cuda", dtype=torch.float32)
+    theta = torch.arange(8192, device="cuda", dtype=torch.float32)[:, None] / torch.pow(10000.0, 2 * i / D)
+    cos_t, sin_t = torch.cos(theta).contiguous(), torch.sin(theta).contiguous()
+    q_out = torch.empty_like(q)
+
+    def step(i_, stream):
+        tla.rope_reshape_and_cache(q, k, v, kc, vc, slots, pos, cos_t, sin_t, tla.ROPE_ADJACENT, q_out=q_out,
+                                   stream=stream)
+
+    ms = timed(step, args.steps, args.warmup)
+    nbytes = 2 * q.numel() * 2 + 4 * k.numel() * 2 + 2 * S * (D // 2) * 4 + 2 * S * 4
+    return {"us": ms * 1e3, "bytes": nbytes}
 
 
 CB_BLOCKS, CB_PAIRS = 8192, 2048
@@ -445,6 +476,7 @@ def main():
     f8 = bench_fp8(args) if args.only in ("all", "fp8") else None
     pf = bench_prefill(args) if args.only in ("all", "prefill") else None
     cb = bench_copy_blocks(args) if args.only in ("all", "blocks") else None
+    rp = bench_rope(args) if args.only in ("all", "rope") else None
     head = bf or fp
     if head is not None:
         res["dtype"] = "bf16" if bf else "fp16"
@@ -509,6 +541,12 @@ def main():
                         f"{CB_BLOCKS} blocks)",
             "gbs": round(cb["gbs"], 2), "pct_hbm_peak": round(100 * cb["gbs"] / HBM_PEAK_GBS, 2),
             "us_per_call": round(cb["ms"] * 1e3, 2), "bytes_per_call": cb["bytes"]}
+    if rp is not None:
+        res["rope_reshape_and_cache"] = {
+            "workload": f"decode-step append, batch {S}: RoPE on q [{S}, {H}, {D}] and k, k and v into the bf16 "
+                        "pools, one launch",
+            "us_per_call": round(rp["us"], 2), "bytes_per_call": rp["bytes"],
+            "gbs": round(rp["bytes"] / (rp["us"] * 1e-6) / 1e9, 2)}
     if not args.no_cpu:
         res["cpu_baseline"] = cpu_baseline(args.cpu_seconds, 4, min(16, os.cpu_count() or 1))
     print(json.dumps(res), flush=True)

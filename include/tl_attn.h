@@ -139,6 +139,30 @@ int tl_reshape_and_cache_fp8(const void* key, const void* value, int32_t src_dty
 int tl_fp8_absmax_scale(const void* x, int32_t dtype, int64_t n, float* scale_out,
                         void* stream);
 
+/* Rotary embedding styles.  ADJACENT rotates the pairs (x[2i], x[2i+1]):
+ * ggml's LLAMA_ROPE_TYPE_NORM, the engine's rope (cuda_engine.cpp:1100-1108).
+ * HALVES rotates (x[i], x[i + d/2]): rope_device.cuh:24-36 (the megakernel). */
+typedef enum tl_rope_style { TL_ROPE_ADJACENT = 0, TL_ROPE_HALVES = 1 } tl_rope_style;
+
+/* The write side of a step in one launch: RoPE on q and key with the
+ * model's fp32 tables cos_table / sin_table [max_positions, head_size/2]
+ * (cuda_model.cpp:269-295: theta = pos / base^(2i/d)), then key and value
+ * into the pools as tl_reshape_and_cache does.  Token t sits at position
+ * positions[t]; each pair (a, b) becomes, in fp32,
+ *   (fmaf(a, c, -(b*s)), fmaf(a, s, b*c)),  c, s = tables[pos][i],
+ * rounded once to dtype (F16, BF16 or F32, the dtype of q, key, value and
+ * the pools).  q [T, num_heads, d] -> q_out (may be q itself); key/value
+ * [T, n_kv, d]; pools [N, n_kv, d, bs]; slot < 0 or past the pool skips the
+ * token's pool write.  A token whose position is outside [0, max_positions)
+ * is not written at all (q_out rows and pool).  head_size a multiple of 16;
+ * num_heads 0 rotates and writes key / value only. */
+int tl_rope_reshape_and_cache(const void* q, void* q_out, const void* key, const void* value,
+                              void* k_cache, void* v_cache, const int32_t* slot_mapping,
+                              const int32_t* positions, const float* cos_table, const float* sin_table,
+                              int32_t max_positions, int32_t num_tokens, int32_t num_heads,
+                              int32_t num_kv_heads, int32_t head_size, int32_t block_size,
+                              int32_t num_blocks, int32_t dtype, int32_t style, void* stream);
+
 /* ------------------------------------------------------------------------
  * KV-cache block management
  * --------------------------------------------------------------------- */

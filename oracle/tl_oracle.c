@@ -186,6 +186,65 @@ void orc_reshape_and_cache_fp8(const void* key, const void* value, int src_dtype
 }
 
 /* ========================================================================
+ * RoPE + reshape_and_cache
+ *   style 0 (ggml LLAMA_ROPE_TYPE_NORM, cuda_engine.cpp:1100-1108): pairs
+ *   (2i, 2i+1); style 1 (rope_device.cuh:24-36): pairs (i, i + d/2);
+ *   c, s = cos/sin_table[pos][i] (cuda_model.cpp:269-295);
+ *   (a, b) -> (fmaf(a, c, -(b*s)), fmaf(a, s, b*c)) in fp32, rounded once.
+ *   Then key/value into the pool as orc_reshape_and_cache.
+ * ====================================================================== */
+
+static int rope_dim(int style, int i, int j, int half) { return style == 0 ? 2 * i + j : i + j * half; }
+
+static void rope_row(const void* src, void* dst, int dtype, int64_t base, int head_size, int style,
+                     const float* cs, const float* sn)
+{
+    int half = head_size / 2;
+    for (int i = 0; i < half; ++i) {
+        int d0 = rope_dim(style, i, 0, half), d1 = rope_dim(style, i, 1, half);
+        float a = load_f32(src, dtype, base + d0), b = load_f32(src, dtype, base + d1);
+        float c = cs[i], s = sn[i];
+        float r0 = fmaf(a, c, -(b * s)), r1 = fmaf(a, s, b * c);
+        store_elem(dst, dtype, base + d0, r0);
+        store_elem(dst, dtype, base + d1, r1);
+    }
+}
+
+void orc_rope_reshape_and_cache(const void* q, void* q_out, const void* key, const void* value,
+                                void* k_cache, void* v_cache, const int32_t* slot_mapping,
+                                const int32_t* positions, const float* cos_table, const float* sin_table,
+                                int max_positions, int num_tokens, int num_heads, int num_kv_heads,
+                                int head_size, int block_size, int num_blocks, int dtype, int style)
+{
+    int half = head_size / 2, eb = dtype == ORC_F32 ? 4 : 2;
+    char* tmp = (char*)malloc((size_t)head_size * eb);
+    for (int t = 0; t < num_tokens; ++t) {
+        int pos = positions[t];
+        if (pos < 0 || pos >= max_positions) continue;
+        const float* cs = cos_table + (int64_t)pos * half;
+        const float* sn = sin_table + (int64_t)pos * half;
+        for (int h = 0; h < num_heads; ++h)
+            rope_row(q, q_out, dtype, ((int64_t)t * num_heads + h) * head_size, head_size, style, cs, sn);
+        int32_t slot = slot_mapping[t];
+        if (slot < 0) continue;
+        int64_t blk = slot / block_size, off = slot % block_size;
+        if (blk >= num_blocks) continue;
+        for (int h = 0; h < num_kv_heads; ++h) {
+            int64_t src = ((int64_t)t * num_kv_heads + h) * head_size;
+            /* rotate the key row into a scratch row, then scatter both rows */
+            memcpy(tmp, (const char*)key + src * eb, (size_t)head_size * eb);
+            rope_row(tmp, tmp, dtype, 0, head_size, style, cs, sn);
+            for (int e = 0; e < head_size; ++e) {
+                int64_t dst = ((blk * num_kv_heads + h) * head_size + e) * block_size + off;
+                memcpy((char*)k_cache + dst * eb, tmp + (int64_t)e * eb, eb);
+                memcpy((char*)v_cache + dst * eb, (const char*)value + (src + e) * eb, eb);
+            }
+        }
+    }
+    free(tmp);
+}
+
+/* ========================================================================
  * copy_blocks  (cache_kernels.cu:107-131, :234-262)
  *   for each pair {src, dst}: pool[dst] = pool[src], for the K and the V
  *   pool; pairs with an id outside [0, num_blocks) are skipped

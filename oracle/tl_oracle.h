@@ -50,6 +50,11 @@ void orc_reshape_and_cache(const void* key, const void* value,
                            int num_kv_heads, int head_size, int block_size,
                            int elem_bytes);
 /* FP8 variant: e4m3(float(x) * (1/k_scale)) from f16/bf16 sources. */
+void orc_rope_reshape_and_cache(const void* q, void* q_out, const void* key, const void* value,
+                                void* k_cache, void* v_cache, const int32_t* slot_mapping,
+                                const int32_t* positions, const float* cos_table, const float* sin_table,
+                                int max_positions, int num_tokens, int num_heads, int num_kv_heads,
+                                int head_size, int block_size, int num_blocks, int dtype, int style);
 void orc_copy_blocks(void* k_cache, void* v_cache, const int32_t* mapping, int num_pairs,
                      int num_blocks, int64_t block_bytes);
 void orc_swap_blocks(void* cache, void* host_cache, const int32_t* mapping, int num_pairs,

@@ -36,6 +36,7 @@ _lib.orc_e4m3_to_f32.argtypes = [ctypes.c_uint8]
 _lib.orc_convert.argtypes = [_P, _I, _P, _I, ctypes.c_int64, _F]
 _lib.orc_reshape_and_cache.argtypes = [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I]
 _lib.orc_reshape_and_cache_fp8.argtypes = [_P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _F, _F]
+_lib.orc_rope_reshape_and_cache.argtypes = [_P] * 10 + [_I] * 9
 _lib.orc_copy_blocks.argtypes = [_P, _P, _P, _I, _I, ctypes.c_int64]
 _lib.orc_swap_blocks.argtypes = [_P, _P, _P, _I, _I, _I, ctypes.c_int64, _I]
 _lib.orc_paged_attention.argtypes = [_P, _P, _I, _P, _P, _I, _F, _F, _P, _I, _P, _I, _I, _I, _I, _I, _F, _I, _I]
@@ -110,6 +111,17 @@ def reshape_and_cache(key, value, k_cache, v_cache, slots):
     T, n_kv, D = key.shape
     _lib.orc_reshape_and_cache(ptr(key), ptr(value), ptr(k_cache), ptr(v_cache), ptr(slots), T,
                                n_kv, D, k_cache.shape[3], key.dtype.itemsize)
+
+
+def rope_reshape_and_cache(q, q_out, key, value, k_cache, v_cache, slots, positions, cos_t, sin_t, code,
+                           style):
+    """In place on q_out and the pools (numpy, dtype code F16 / BF16 as uint16, F32)."""
+    T, n_kv, D = key.shape
+    H = 0 if q is None else q.shape[1]
+    _lib.orc_rope_reshape_and_cache(None if q is None else ptr(q), None if q_out is None else ptr(q_out),
+                                    ptr(key), ptr(value), ptr(k_cache), ptr(v_cache), ptr(slots),
+                                    ptr(positions), ptr(cos_t), ptr(sin_t), cos_t.shape[0], T, H, n_kv, D,
+                                    k_cache.shape[3], k_cache.shape[0], code, style)
 
 
 def copy_blocks(k_cache, v_cache, mapping):

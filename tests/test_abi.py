@@ -128,6 +128,22 @@ def test_block_ops_reject_bad_arguments_and_empty_is_a_no_op():
     assert L.tl_swap_blocks(None, None, None, 0, 8, 8, 4096, 0, None) == tla.OK
 
 
+def test_rope_rejects_bad_arguments():
+    L = tla.lib
+    args = lambda **kw: [kw.get(k, v) for k, v in [
+        ("q", FAKE), ("q_out", FAKE), ("key", FAKE), ("value", FAKE), ("kc", FAKE), ("vc", FAKE),
+        ("slots", FAKE), ("pos", FAKE), ("cos", FAKE), ("sin", FAKE), ("max_pos", 4096), ("T", 4), ("H", 32),
+        ("n_kv", 8), ("D", 128), ("BS", 16), ("N", 64), ("dtype", tla.F16), ("style", 0), ("stream", None)]]
+    f = L.tl_rope_reshape_and_cache
+    assert f(*args(D=120)) == tla.ERR_INVALID_ARGUMENT
+    assert f(*args(style=2)) == tla.ERR_INVALID_ARGUMENT
+    assert f(*args(dtype=9)) == tla.ERR_INVALID_ARGUMENT
+    assert f(*args(max_pos=0)) == tla.ERR_INVALID_ARGUMENT
+    assert f(*args(cos=None)) == tla.ERR_INVALID_ARGUMENT
+    assert f(*args(q=None)) == tla.ERR_INVALID_ARGUMENT
+    assert f(*args(T=0, q=None, key=None)) == tla.OK
+
+
 def test_kivi_host_helpers_match_reference_known_answers():
     # test_kivi_bounds.cpp:25-69, through the library
     assert tla.kivi_compressed_bytes(128, 8, 16) == 24 + 8 * 12

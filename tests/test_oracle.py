@@ -539,3 +539,124 @@ def test_swap_blocks_oracle_round_trip():
     before = host.copy()
     orc.swap_blocks(dev_pool, host, np.array([[20, 0], [0, 10], [-1, 1]], np.int32), 0)
     assert np.array_equal(host.view(np.uint16), before.view(np.uint16))
+
+
+# ---------------------------------------------------------------------------
+# RoPE + reshape_and_cache
+# ---------------------------------------------------------------------------
+
+def rope_tables(max_pos, D, base=10000.0):
+    """cuda_model.cpp:269-295: theta = pos / base^(2i/D), fp32 tables [max_pos, D/2]."""
+    i = np.arange(D // 2, dtype=np.float32)
+    pos = np.arange(max_pos, dtype=np.float32)[:, None]
+    theta = pos / np.power(np.float32(base), np.float32(2.0) * i / np.float32(D))
+    return np.cos(theta).astype(np.float32), np.sin(theta).astype(np.float32)
+
+
+def _pair_mag(x, style):
+    """|a| + |b| of each element's pair: the scale of the fp32 rounding error."""
+    D = x.shape[-1]
+    half = D // 2
+    i = np.arange(half)
+    d0, d1 = (2 * i, 2 * i + 1) if style == 0 else (i, i + half)
+    m = np.zeros(x.shape, np.float64)
+    pm = np.abs(x[..., d0]).astype(np.float64) + np.abs(x[..., d1])
+    m[..., d0] = pm
+    m[..., d1] = pm
+    return m
+
+
+def _rope_np(x, pos, cos_t, sin_t, style):
+    """float64 rotation of rows x [..., D] at positions pos (one per leading row)."""
+    D = x.shape[-1]
+    half = D // 2
+    i = np.arange(half)
+    d0, d1 = (2 * i, 2 * i + 1) if style == 0 else (i, i + half)
+    c = cos_t[pos].astype(np.float64)[..., None, :] if x.ndim == 3 else cos_t[pos].astype(np.float64)
+    s = sin_t[pos].astype(np.float64)[..., None, :] if x.ndim == 3 else sin_t[pos].astype(np.float64)
+    a, b = x[..., d0].astype(np.float64), x[..., d1].astype(np.float64)
+    out = x.astype(np.float64).copy()
+    out[..., d0] = a * c - b * s
+    out[..., d1] = a * s + b * c
+    return out
+
+
+def _rope_case(seed, T, H, n_kv, D, BS, N, code, max_pos=4096):
+    rng = np.random.default_rng(seed)
+    q = inputs.encode(rng.standard_normal((T, H, D), dtype=np.float32), code)
+    key = inputs.encode(rng.standard_normal((T, n_kv, D), dtype=np.float32), code)
+    val = inputs.encode(rng.standard_normal((T, n_kv, D), dtype=np.float32), code)
+    slots = rng.choice(N * BS, size=T, replace=False).astype(np.int32)
+    pos = rng.integers(0, max_pos, size=T).astype(np.int32)
+    kc = inputs.encode(np.zeros((N, n_kv, D, BS), np.float32), code)
+    vc = inputs.encode(np.zeros((N, n_kv, D, BS), np.float32), code)
+    return q, key, val, slots, pos, kc, vc
+
+
+@pytest.mark.parametrize("style", [0, 1])
+@pytest.mark.parametrize("code", [orc.F16, orc.BF16, orc.F32])
+def test_rope_oracle_matches_float64_rotation(style, code):
+    """Each style's pairing against a float64 rotation with the same fp32
+    tables: within one unit in the last place of the dtype (a wrong pairing
+    or a sign error is off by O(1)); values pass through the pool unchanged."""
+    T, H, n_kv, D, BS, N = 9, 4, 2, 64, 16, 8
+    q, key, val, slots, pos, kc, vc = _rope_case(40 + style, T, H, n_kv, D, BS, N, code)
+    cos_t, sin_t = rope_tables(4096, D)
+    q_out = np.zeros_like(q)
+    orc.rope_reshape_and_cache(q, q_out, key, val, kc, vc, slots, pos, cos_t, sin_t, code, style)
+    qf = orc.bits_to_f32(q, code) if code != orc.F32 else q
+    kf = orc.bits_to_f32(key, code) if code != orc.F32 else key
+    want_q = _rope_np(qf, pos, cos_t, sin_t, style)
+    want_k = _rope_np(kf, pos, cos_t, sin_t, style)
+    got_q = orc.bits_to_f32(q_out, code) if code != orc.F32 else q_out
+    # one unit in the last place of the dtype at the result, plus the fp32
+    # rounding of the two products (relative to the pair's magnitude)
+    ulp = {orc.F16: 2.0 ** -10, orc.BF16: 2.0 ** -7, orc.F32: 2.0 ** -23}[code]
+    tol = ulp * np.maximum(np.abs(want_q), 2.0 ** -14) + 2.0 ** -22 * _pair_mag(qf, style)
+    assert np.all(np.abs(got_q - want_q) <= tol)
+    blk, off = slots // BS, slots % BS
+    got_k = np.stack([(orc.bits_to_f32(kc, code) if code != orc.F32 else kc)[blk[t], :, :, off[t]]
+                      for t in range(T)])
+    assert np.all(np.abs(got_k - want_k) <= ulp * np.maximum(np.abs(want_k), 2.0 ** -14)
+                  + 2.0 ** -22 * _pair_mag(kf, style))
+    got_v = np.stack([vc[blk[t], :, :, off[t]] for t in range(T)])
+    assert np.array_equal(got_v, val)
+
+
+def test_rope_oracle_position_zero_is_identity_and_skips():
+    """Position 0 (cos 1, sin 0) leaves q and k as they are, so the pools
+    equal a plain reshape_and_cache; slot -1 writes no pool; a position past
+    the tables writes nothing."""
+    T, H, n_kv, D, BS, N = 6, 3, 2, 32, 16, 4
+    q, key, val, slots, pos, kc, vc = _rope_case(44, T, H, n_kv, D, BS, N, orc.F16)
+    cos_t, sin_t = rope_tables(64, D)
+    pos[:] = 0
+    slots[2] = -1
+    pos[4] = 64
+    q_out = np.zeros_like(q)
+    orc.rope_reshape_and_cache(q, q_out, key, val, kc, vc, slots, pos, cos_t, sin_t, orc.F16, 0)
+    keep = np.ones(T, bool)
+    keep[4] = False
+    assert np.array_equal(q_out[keep], q[keep]) and not q_out[4].any()
+    ek, ev = np.zeros_like(kc), np.zeros_like(vc)
+    s2 = slots.copy()
+    s2[4] = -1
+    orc.reshape_and_cache(key, val, ek, ev, s2)
+    assert np.array_equal(kc, ek) and np.array_equal(vc, ev)
+
+
+def test_rope_oracle_preserves_pair_norms_with_reference_tables():
+    """Rotation keeps |(a, b)| of every pair (fp32 data, reference tables at
+    positions up to 4095)."""
+    T, H, n_kv, D, BS, N = 16, 2, 1, 128, 16, 2
+    q, key, val, slots, pos, kc, vc = _rope_case(45, T, H, n_kv, D, BS, N, orc.F32)
+    cos_t, sin_t = rope_tables(4096, D)
+    for style in (0, 1):
+        q_out = np.zeros_like(q)
+        orc.rope_reshape_and_cache(q, q_out, key, val, kc.copy(), vc.copy(), slots, pos, cos_t, sin_t,
+                                   orc.F32, style)
+        i = np.arange(D // 2)
+        d0, d1 = (2 * i, 2 * i + 1) if style == 0 else (i, i + D // 2)
+        n_in = np.hypot(q[..., d0], q[..., d1])
+        n_out = np.hypot(q_out[..., d0], q_out[..., d1])
+        assert np.allclose(n_in, n_out, rtol=1e-6, atol=1e-6)

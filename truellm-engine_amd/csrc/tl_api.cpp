@@ -251,6 +251,33 @@ int tl_reshape_and_cache(const void* key, const void* value, void* k_cache, void
   return ok();
 }
 
+int tl_rope_reshape_and_cache(const void* q, void* q_out, const void* key, const void* value,
+                              void* k_cache, void* v_cache, const int32_t* slot_mapping,
+                              const int32_t* positions, const float* cos_table, const float* sin_table,
+                              int32_t max_positions, int32_t num_tokens, int32_t num_heads,
+                              int32_t num_kv_heads, int32_t head_size, int32_t block_size,
+                              int32_t num_blocks, int32_t dtype, int32_t style, void* stream) {
+  if (num_tokens < 0 || num_heads < 0 || num_kv_heads <= 0 || head_size <= 0 || block_size <= 0 ||
+      num_blocks <= 0 || max_positions <= 0)
+    return fail(TL_ERR_INVALID_ARGUMENT,
+                "num_tokens=%d num_heads=%d num_kv_heads=%d head_size=%d block_size=%d num_blocks=%d "
+                "max_positions=%d", num_tokens, num_heads, num_kv_heads, head_size, block_size, num_blocks,
+                max_positions);
+  if (head_size % 16) return fail(TL_ERR_INVALID_ARGUMENT, "head_size=%d must be a multiple of 16", head_size);
+  if (!is_float_kind(dtype)) return fail(TL_ERR_INVALID_ARGUMENT, "dtype=%d", dtype);
+  if (style != TL_ROPE_ADJACENT && style != TL_ROPE_HALVES) return fail(TL_ERR_INVALID_ARGUMENT, "style=%d", style);
+  if (num_tokens == 0) return ok();
+  if (!key || !value || !k_cache || !v_cache || !slot_mapping || !positions || !cos_table || !sin_table ||
+      (num_heads > 0 && (!q || !q_out)))
+    return fail(TL_ERR_INVALID_ARGUMENT, "NULL pointer");
+  tl::RopeCache a = {q, q_out, key, value, k_cache, v_cache, slot_mapping, positions, cos_table, sin_table,
+                     num_tokens, num_heads, num_kv_heads, head_size, block_size, num_blocks, max_positions,
+                     dtype, style};
+  const int rc = tl::launch_rope_cache(a, (hipStream_t)stream);
+  if (rc) return fail(TL_ERR_BACKEND, "rope_reshape_and_cache launch failed");
+  return ok();
+}
+
 int tl_copy_blocks(void* k_cache, void* v_cache, const int32_t* block_mapping, int32_t num_pairs,
                    int32_t num_blocks, int64_t block_bytes, void* stream) {
   if (num_pairs < 0 || num_blocks <= 0 || block_bytes <= 0)

@@ -10,6 +10,16 @@
 // fp8 scale: per-tensor absmax(x)/448, the E4M3 scale convention of
 // fp8_gemm.cu:82-84, as a grid-wide max.
 //
+// RoPE + reshape_and_cache: the write side of a step in one launch.  A
+// thread owns 8 rotation pairs of one (token, head) of q, of k (rotated, then
+// scattered into the pool) or of v (copied into the pool).  Pairs are
+// (2i, 2i+1) for the ADJACENT style (ggml's LLAMA_ROPE_TYPE_NORM, the
+// engine's rope, cuda_engine.cpp:1100-1108) and (i, i + d/2) for HALVES
+// (rope_device.cuh:24-36); cos/sin come from the model's fp32 tables
+// [max_pos, d/2] (cuda_model.cpp:269-295).  In fp32:
+//   r0 = fmaf(a, c, -(b s)),  r1 = fmaf(a, s, b c),
+// rounded once to the dtype.
+//
 // Block copies (copy_blocks, cache_kernels.cu:107-131, :234-262; swap_blocks,
 // :133-167, :264-284): whole blocks between block ids of a mapping {src,
 // dst}; a workgroup moves a slice of one block of one pool in 16-byte
@@ -98,6 +108,76 @@ __global__ __launch_bounds__(256) void reshape_fp8_kernel(
   }
 }
 
+// Element j of pair i within one head row: ADJACENT (2i + j), HALVES (i + j d/2).
+template <int STYLE>
+__device__ __forceinline__ int rope_dim(int i, int j, int half) {
+  return STYLE == 0 ? 2 * i + j : i + j * half;
+}
+
+template <Kind K, int STYLE>
+__global__ __launch_bounds__(256) void rope_cache_kernel(RopeCache a) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int half = a.head_size / 2, units = half / 8;           // 8 pairs per thread
+  const int rows = a.num_heads + 2 * a.num_kv_heads;            // q heads, k heads, v heads
+  const int64_t total = (int64_t)a.num_tokens * rows * units;
+  if (idx >= total) return;
+  const int u = (int)(idx % units);
+  const int row = (int)((idx / units) % rows);
+  const int t = (int)(idx / ((int64_t)units * rows));
+  const int pos = a.positions[t];
+  if (pos < 0 || pos >= a.max_positions) return;               // token left as it is
+  const int i0 = 8 * u;
+  float x[16];
+  const void* src;
+  int64_t base;
+  if (row < a.num_heads) {
+    src = a.q;
+    base = ((int64_t)t * a.num_heads + row) * a.head_size;
+  } else if (row < a.num_heads + a.num_kv_heads) {
+    src = a.key;
+    base = ((int64_t)t * a.num_kv_heads + (row - a.num_heads)) * a.head_size;
+  } else {
+    src = a.value;
+    base = ((int64_t)t * a.num_kv_heads + (row - a.num_heads - a.num_kv_heads)) * a.head_size;
+  }
+#pragma unroll
+  for (int p = 0; p < 8; ++p) {
+    x[2 * p] = load_scalar<K>(src, base + rope_dim<STYLE>(i0 + p, 0, half));
+    x[2 * p + 1] = load_scalar<K>(src, base + rope_dim<STYLE>(i0 + p, 1, half));
+  }
+  const bool is_v = row >= a.num_heads + a.num_kv_heads;
+  if (!is_v) {
+    const float* cs = a.cos_table + (int64_t)pos * half + i0;
+    const float* sn = a.sin_table + (int64_t)pos * half + i0;
+#pragma unroll
+    for (int p = 0; p < 8; ++p) {
+      const float c = cs[p], sv = sn[p], x0 = x[2 * p], x1 = x[2 * p + 1];
+      x[2 * p] = __builtin_fmaf(x0, c, -(x1 * sv));
+      x[2 * p + 1] = __builtin_fmaf(x0, sv, x1 * c);
+    }
+  }
+  if (row < a.num_heads) {
+#pragma unroll
+    for (int p = 0; p < 8; ++p) {
+      store_scalar<K>(a.q_out, base + rope_dim<STYLE>(i0 + p, 0, half), x[2 * p]);
+      store_scalar<K>(a.q_out, base + rope_dim<STYLE>(i0 + p, 1, half), x[2 * p + 1]);
+    }
+    return;
+  }
+  const int32_t slot = a.slot_mapping[t];
+  if (slot < 0) return;
+  const int blk = slot / a.block_size, off = slot % a.block_size;
+  if (blk >= a.num_blocks) return;
+  const int h = is_v ? row - a.num_heads - a.num_kv_heads : row - a.num_heads;
+  void* pool = is_v ? a.v_cache : a.k_cache;
+  const int64_t pbase = ((int64_t)blk * a.num_kv_heads + h) * a.head_size;
+#pragma unroll
+  for (int p = 0; p < 8; ++p)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      store_scalar<K>(pool, (pbase + rope_dim<STYLE>(i0 + p, j, half)) * a.block_size + off, x[2 * p + j]);
+}
+
 // grid.x = pairs x pools x slices; pool 1 is the second (V) pool of a copy.
 template <bool VEC>
 __global__ __launch_bounds__(256) void block_copy_kernel(BlockCopy c) {
@@ -172,6 +252,20 @@ int launch_reshape_and_cache(const CacheLaunch& a) {
                          (char*)a.v_cache, a.slot_mapping, a.num_tokens, a.num_kv_heads,
                          a.head_size, a.block_size, a.num_blocks);
   }
+  return hipGetLastError() == hipSuccess ? 0 : 5;
+}
+
+int launch_rope_cache(const RopeCache& a, hipStream_t stream) {
+  if (a.num_tokens == 0) return 0;
+  const int64_t total = (int64_t)a.num_tokens * (a.num_heads + 2 * a.num_kv_heads) * (a.head_size / 16);
+  const dim3 grid((unsigned)((total + 255) / 256));
+  const Kind k = (Kind)a.dtype;
+#define TL_ROPE_LAUNCH(K, S) hipLaunchKernelGGL((rope_cache_kernel<K, S>), grid, dim3(256), 0, stream, a)
+  if (k == Kind::F16) { if (a.style) TL_ROPE_LAUNCH(Kind::F16, 1); else TL_ROPE_LAUNCH(Kind::F16, 0); }
+  else if (k == Kind::BF16) { if (a.style) TL_ROPE_LAUNCH(Kind::BF16, 1); else TL_ROPE_LAUNCH(Kind::BF16, 0); }
+  else if (k == Kind::F32) { if (a.style) TL_ROPE_LAUNCH(Kind::F32, 1); else TL_ROPE_LAUNCH(Kind::F32, 0); }
+  else return 3;
+#undef TL_ROPE_LAUNCH
   return hipGetLastError() == hipSuccess ? 0 : 5;
 }
 

@@ -67,6 +67,19 @@ struct CacheLaunch {
 };
 int launch_reshape_and_cache(const CacheLaunch& a);
 
+// RoPE on q and key, then key and value into the pools (one launch).
+struct RopeCache {
+  const void* q; void* q_out;   // [T, H, d]
+  const void* key; const void* value;   // [T, n_kv, d]
+  void* k_cache; void* v_cache; // [N, n_kv, d, BS]
+  const int32_t* slot_mapping;  // [T]
+  const int32_t* positions;     // [T]
+  const float* cos_table; const float* sin_table;   // [max_positions, d/2]
+  int num_tokens, num_heads, num_kv_heads, head_size, block_size, num_blocks, max_positions;
+  int dtype, style;             // style 0: pairs (2i, 2i+1); 1: (i, i + d/2)
+};
+int launch_rope_cache(const RopeCache& a, hipStream_t stream);
+
 // Whole-block copies: for pair p of mapping [num_pairs][2] = {src, dst},
 // block src of src0 (and of src1 when pools == 2) to block dst of dst0
 // (dst1).  Ids outside [0, src_blocks) / [0, dst_blocks) skip the pair.

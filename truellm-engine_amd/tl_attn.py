@@ -107,6 +107,7 @@ _SIG = {
     "tl_paged_attention_v2": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F, _I, _I, _I, _P]),
     "tl_reshape_and_cache": (ctypes.c_int, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P]),
     "tl_reshape_and_cache_fp8": (ctypes.c_int, [_P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _I, _F, _F, _P]),
+    "tl_rope_reshape_and_cache": (ctypes.c_int, [_P] * 10 + [_I] * 9 + [_P]),
     "tl_copy_blocks": (ctypes.c_int, [_P, _P, _P, _I, _I, ctypes.c_int64, _P]),
     "tl_swap_blocks": (ctypes.c_int, [_P, _P, _P, _I, _I, _I, ctypes.c_int64, _I, _P]),
     "tl_fp8_absmax_scale": (ctypes.c_int, [_P, _I, ctypes.c_int64, _P, _P]),
@@ -253,6 +254,22 @@ def reshape_and_cache_split(key, value, k_cache, v_cache, slot_mapping, stream=N
     check(lib.tl_reshape_and_cache(
         _ptr(key), _ptr(value), _ptr(k_cache), _ptr(v_cache), _ptr(slot_mapping), T, n_kv, D,
         k_cache.shape[3], k_cache.shape[0], dtype_code(key), _stream(stream)))
+
+
+ROPE_ADJACENT, ROPE_HALVES = 0, 1
+
+
+def rope_reshape_and_cache(q, key, value, k_cache, v_cache, slot_mapping, positions, cos_table, sin_table,
+                           style=ROPE_ADJACENT, q_out=None, stream=None):
+    """RoPE on q (into q_out, default in place) and key, then key/value into
+    the pools [N, n_kv, D, BS].  Tables fp32 [max_positions, D/2]."""
+    T, n_kv, D = key.shape
+    H = 0 if q is None else q.shape[1]
+    q_out = q if q_out is None else q_out
+    check(lib.tl_rope_reshape_and_cache(
+        _ptr(q), _ptr(q_out), _ptr(key), _ptr(value), _ptr(k_cache), _ptr(v_cache), _ptr(slot_mapping),
+        _ptr(positions), _ptr(cos_table), _ptr(sin_table), cos_table.shape[0], T, H, n_kv, D,
+        k_cache.shape[3], k_cache.shape[0], dtype_code(key), style, _stream(stream)))
 
 
 def _block_bytes(pool):
