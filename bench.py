@@ -73,7 +73,7 @@ def parse():
     p.add_argument("--partition-tokens", type=int, default=0)
     p.add_argument("--cpu-seconds", type=float, default=15.0)
     p.add_argument("--no-cpu", action="store_true")
-    p.add_argument("--only", default="all", choices=["all", "bf16", "fp16", "kivi", "fp8", "prefill", "blocks", "rope"])
+    p.add_argument("--only", default="all", choices=["all", "bf16", "fp16", "kivi", "fp8", "prefill", "blocks", "rope", "vq"])
     p.add_argument("--no-graph", action="store_true",
                    help="launch the timed steps eagerly (for counter passes that cannot follow graphs)")
     p.add_argument("--copy-calibration", action="store_true",
@@ -282,6 +282,30 @@ def bench_rope(args):
     return {"us": ms * 1e3, "bytes": nbytes}
 
 
+VQ_N, VQ_K = 2048 * 8, 256
+
+
+def bench_vq(args):
+    """VQ encode of one 2048-token layer (8 kv heads, d 128: 16384 fp16
+    vectors) against a 256-entry codebook: 3 fp32 flops (subtract, fma) per
+    (vector, entry, dim), in the reference's exact order."""
+    import torch
+
+    import tl_attn as tla
+
+    g = torch.Generator(device="cuda").manual_seed(0x7E5E0008)
+    kv = torch.randn(VQ_N, D, generator=g, device="cuda", dtype=torch.float16)
+    book = torch.randn(VQ_K, D, generator=g, device="cuda", dtype=torch.float16)
+    idx = torch.zeros(VQ_N, dtype=torch.int16, device="cuda")
+
+    def step(i, stream):
+        tla.vq_encode(kv, book, idx, stream)
+
+    ms = timed(step, max(4, args.steps // 5), max(2, args.warmup // 5))
+    flops = 3 * VQ_N * VQ_K * D
+    return {"ms": ms, "flops": flops, "tflops": flops / (ms * 1e-3) / 1e12}
+
+
 CB_BLOCKS, CB_PAIRS = 8192, 2048
 
 
@@ -477,6 +501,7 @@ def main():
     pf = bench_prefill(args) if args.only in ("all", "prefill") else None
     cb = bench_copy_blocks(args) if args.only in ("all", "blocks") else None
     rp = bench_rope(args) if args.only in ("all", "rope") else None
+    vq = bench_vq(args) if args.only in ("all", "vq") else None
     head = bf or fp
     if head is not None:
         res["dtype"] = "bf16" if bf else "fp16"
@@ -547,6 +572,11 @@ def main():
                         "pools, one launch",
             "us_per_call": round(rp["us"], 2), "bytes_per_call": rp["bytes"],
             "gbs": round(rp["bytes"] / (rp["us"] * 1e-6) / 1e9, 2)}
+    if vq is not None:
+        res["vq_encode"] = {
+            "workload": f"VQ encode, {VQ_N} fp16 vectors of d {D} against {VQ_K} entries (exact fp32 distances)",
+            "us_per_call": round(vq["ms"] * 1e3, 2), "tflops_fp32": round(vq["tflops"], 2),
+            "pct_fp32_vector_peak": round(100 * vq["tflops"] / 157.3, 2), "flops_per_call": vq["flops"]}
     if not args.no_cpu:
         res["cpu_baseline"] = cpu_baseline(args.cpu_seconds, 4, min(16, os.cpu_count() or 1))
     print(json.dumps(res), flush=True)

@@ -189,6 +189,44 @@ int tl_swap_blocks(void* cache, void* host_cache, const int32_t* block_mapping, 
                    int32_t direction, void* stream);
 
 /* ------------------------------------------------------------------------
+ * VQ codec of the KV cache (vq_cache.cu, codebook_init.cu)
+ * --------------------------------------------------------------------- */
+
+#define TL_VQ_MAX_HEAD_DIM 256
+
+/* Replaces vq_encode (vq_cache.cu:74-86, kernel :18-43): idx[v] (uint16) =
+ * the codebook entry nearest to vector v of kv [num_vecs, head_dim] fp16
+ * (num_vecs = seq_len * n_kv_heads), by the reference's fp32 distance
+ * (sequential over d, fma per term); the lowest index wins ties, NaN and
+ * >= FLT_MAX distances never win (all of them: 0).  book [codebook_size,
+ * head_dim] fp16.  head_dim a multiple of 8, at most TL_VQ_MAX_HEAD_DIM;
+ * 1 <= codebook_size <= 65536. */
+int tl_vq_encode(const void* kv, const void* book, uint16_t* idx, int32_t num_vecs, int32_t head_dim,
+                 int32_t codebook_size, void* stream);
+
+/* Replaces vq_decode (vq_cache.cu:88-100, kernel :48-69): kv_out[v] =
+ * book[idx[v]] (bit copies; kv_out may be the encoded tensor).  A row whose
+ * index is >= codebook_size is left as it is (the reference reads past the
+ * codebook). */
+int tl_vq_decode(void* kv_out, const void* book, const uint16_t* idx, int32_t num_vecs, int32_t head_dim,
+                 int32_t codebook_size, void* stream);
+
+/* Workspace of tl_vq_kmeans (caller-owned; the reference allocates and frees
+ * temporaries on every call). */
+size_t tl_vq_kmeans_workspace_bytes(int32_t n_samples, int32_t codebook_size, int32_t head_dim);
+
+/* Replaces codebook_init_kmeans (codebook_init.cu:100-145): n_iterations
+ * Lloyd iterations over data [n_samples, head_dim] fp16, updating the
+ * pre-seeded book in place: assign as tl_vq_encode; each centroid becomes
+ * fp16(fp32(sum) * (1/count)) of its members, an empty cluster keeps its
+ * centroid.  The sums are exact (int64 fixed point in units of 2^-24, NaN /
+ * +inf / -inf tracked with IEEE sum rules), so the result does not depend on
+ * the order of the atomic adds, unlike the reference's fp32 atomics.
+ * Asynchronous; no allocation. */
+int tl_vq_kmeans(const void* data, void* book, int32_t n_samples, int32_t codebook_size, int32_t head_dim,
+                 int32_t n_iterations, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
  * Reference KIVI vector codec (kivi_cache.cuh:27-84, kivi_cache.cu:23-239)
  * --------------------------------------------------------------------- */
 

@@ -111,6 +111,16 @@ void paged_attention_v2(truellm::TrueBuffer& out, truellm::TrueBuffer& exp_sums,
                         int head_size, int block_size, int max_context_len, hipStream_t stream);
 
 namespace truellm {
+/* vq_cache.cu:74-86 */
+void vq_encode(const __half* d_kv, const __half* d_book, uint16_t* d_idx, int seq_len, int n_kv_heads,
+               int head_dim, int codebook_size, hipStream_t stream);
+/* vq_cache.cu:88-100 (no codebook size: indices are trusted, as in the reference) */
+void vq_decode(__half* d_kv, const __half* d_book, const uint16_t* d_idx, int seq_len, int n_kv_heads,
+               int head_dim, hipStream_t stream);
+/* codebook_init.cu:100-145: allocates its workspace and synchronises the
+ * stream, as the reference does (tl_vq_kmeans does neither) */
+void codebook_init_kmeans(const void* d_data, void* d_book, int n_samples, int codebook_size, int head_dim,
+                          int n_iterations, hipStream_t stream);
 /* kivi_cache.cu:205-211 */
 bool kivi_params_supported(int head_dim, int n_outliers, int group_size);
 /* kivi_cache.cu:213-224: no-op for n_vecs <= 0 or unsupported parameters */

@@ -245,6 +245,89 @@ void orc_rope_reshape_and_cache(const void* q, void* q_out, const void* key, con
 }
 
 /* ========================================================================
+ * VQ codec  (vq_cache.cu:18-69, codebook_init.cu:23-145)
+ *   encode: dist_c = fold_d fmaf(x_d - b_cd, x_d - b_cd, dist) (fp32, d in
+ *   order); the first c with dist_c < best (best = FLT_MAX at the start)
+ *   decode: out[v] = book[idx[v]]
+ *   k-means: assign, then per cluster the exact sum of its members (each
+ *   fp16 value is a multiple of 2^-24: int64 fixed point), non-finite
+ *   values by IEEE sum rules, centroid = fp16(fp32(sum) * (1/count)),
+ *   empty clusters unchanged
+ * ====================================================================== */
+
+static int vq_nearest(const uint16_t* x, const uint16_t* book, int head_dim, int codebook_size)
+{
+    float best = FLT_MAX;
+    int best_c = 0;
+    for (int c = 0; c < codebook_size; ++c) {
+        const uint16_t* e = book + (int64_t)c * head_dim;
+        float dist = 0.f;
+        for (int d = 0; d < head_dim; ++d) {
+            float diff = orc_f16_to_f32(x[d]) - orc_f16_to_f32(e[d]);
+            dist = fmaf(diff, diff, dist);
+        }
+        if (dist < best) { best = dist; best_c = c; }
+    }
+    return best_c;
+}
+
+void orc_vq_encode(const uint16_t* kv, const uint16_t* book, uint16_t* idx, int64_t num_vecs, int head_dim,
+                   int codebook_size)
+{
+    for (int64_t v = 0; v < num_vecs; ++v)
+        idx[v] = (uint16_t)vq_nearest(kv + v * head_dim, book, head_dim, codebook_size);
+}
+
+void orc_vq_decode(uint16_t* out, const uint16_t* book, const uint16_t* idx, int64_t num_vecs, int head_dim,
+                   int codebook_size)
+{
+    for (int64_t v = 0; v < num_vecs; ++v)
+        if (idx[v] < codebook_size)
+            memcpy(out + v * head_dim, book + (int64_t)idx[v] * head_dim, (size_t)head_dim * 2);
+}
+
+void orc_vq_kmeans(const uint16_t* data, uint16_t* book, int64_t n, int codebook_size, int head_dim,
+                   int iterations)
+{
+    size_t kd = (size_t)codebook_size * head_dim;
+    int* assign = (int*)malloc(sizeof(int) * (size_t)(n > 0 ? n : 1));
+    long long* sums = (long long*)malloc(sizeof(long long) * kd);
+    int* flags = (int*)malloc(sizeof(int) * kd);
+    int* counts = (int*)malloc(sizeof(int) * (size_t)codebook_size);
+    for (int it = 0; it < iterations; ++it) {
+        for (int64_t s = 0; s < n; ++s) assign[s] = vq_nearest(data + s * head_dim, book, head_dim, codebook_size);
+        memset(sums, 0, sizeof(long long) * kd);
+        memset(flags, 0, sizeof(int) * kd);
+        memset(counts, 0, sizeof(int) * (size_t)codebook_size);
+        for (int64_t s = 0; s < n; ++s) {
+            int c = assign[s];
+            counts[c]++;
+            for (int d = 0; d < head_dim; ++d) {
+                float x = orc_f16_to_f32(data[s * head_dim + d]);
+                size_t k = (size_t)c * head_dim + d;
+                if (isnan(x)) flags[k] |= 1;
+                else if (isinf(x)) flags[k] |= x > 0 ? 2 : 4;
+                else sums[k] += (long long)(x * 16777216.0f);
+            }
+        }
+        for (int c = 0; c < codebook_size; ++c) {
+            if (counts[c] == 0) continue;
+            float inv = 1.f / (float)counts[c];
+            for (int d = 0; d < head_dim; ++d) {
+                size_t k = (size_t)c * head_dim + d;
+                float sum;
+                if ((flags[k] & 1) || (flags[k] & 6) == 6) sum = NAN;
+                else if (flags[k] & 2) sum = INFINITY;
+                else if (flags[k] & 4) sum = -INFINITY;
+                else sum = (float)sums[k] * (1.0f / 16777216.0f);
+                book[k] = orc_f32_to_f16(sum * inv);
+            }
+        }
+    }
+    free(assign); free(sums); free(flags); free(counts);
+}
+
+/* ========================================================================
  * copy_blocks  (cache_kernels.cu:107-131, :234-262)
  *   for each pair {src, dst}: pool[dst] = pool[src], for the K and the V
  *   pool; pairs with an id outside [0, num_blocks) are skipped

@@ -55,6 +55,12 @@ void orc_rope_reshape_and_cache(const void* q, void* q_out, const void* key, con
                                 const int32_t* positions, const float* cos_table, const float* sin_table,
                                 int max_positions, int num_tokens, int num_heads, int num_kv_heads,
                                 int head_size, int block_size, int num_blocks, int dtype, int style);
+void orc_vq_encode(const uint16_t* kv, const uint16_t* book, uint16_t* idx, int64_t num_vecs, int head_dim,
+                   int codebook_size);
+void orc_vq_decode(uint16_t* out, const uint16_t* book, const uint16_t* idx, int64_t num_vecs, int head_dim,
+                   int codebook_size);
+void orc_vq_kmeans(const uint16_t* data, uint16_t* book, int64_t n, int codebook_size, int head_dim,
+                   int iterations);
 void orc_copy_blocks(void* k_cache, void* v_cache, const int32_t* mapping, int num_pairs,
                      int num_blocks, int64_t block_bytes);
 void orc_swap_blocks(void* cache, void* host_cache, const int32_t* mapping, int num_pairs,

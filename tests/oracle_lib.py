@@ -37,6 +37,9 @@ _lib.orc_convert.argtypes = [_P, _I, _P, _I, ctypes.c_int64, _F]
 _lib.orc_reshape_and_cache.argtypes = [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I]
 _lib.orc_reshape_and_cache_fp8.argtypes = [_P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _F, _F]
 _lib.orc_rope_reshape_and_cache.argtypes = [_P] * 10 + [_I] * 9
+_lib.orc_vq_encode.argtypes = [_P, _P, _P, ctypes.c_int64, _I, _I]
+_lib.orc_vq_decode.argtypes = [_P, _P, _P, ctypes.c_int64, _I, _I]
+_lib.orc_vq_kmeans.argtypes = [_P, _P, ctypes.c_int64, _I, _I, _I]
 _lib.orc_copy_blocks.argtypes = [_P, _P, _P, _I, _I, ctypes.c_int64]
 _lib.orc_swap_blocks.argtypes = [_P, _P, _P, _I, _I, _I, ctypes.c_int64, _I]
 _lib.orc_paged_attention.argtypes = [_P, _P, _I, _P, _P, _I, _F, _F, _P, _I, _P, _I, _I, _I, _I, _I, _F, _I, _I]
@@ -122,6 +125,29 @@ def rope_reshape_and_cache(q, q_out, key, value, k_cache, v_cache, slots, positi
                                     ptr(key), ptr(value), ptr(k_cache), ptr(v_cache), ptr(slots),
                                     ptr(positions), ptr(cos_t), ptr(sin_t), cos_t.shape[0], T, H, n_kv, D,
                                     k_cache.shape[3], k_cache.shape[0], code, style)
+
+
+def vq_encode(kv_bits, book_bits):
+    """fp16 bits kv [..., D], book [K, D] -> uint16 indices [n]."""
+    D = book_bits.shape[1]
+    kv = np.ascontiguousarray(kv_bits, np.uint16)
+    idx = np.zeros(kv.size // D, np.uint16)
+    _lib.orc_vq_encode(ptr(kv), ptr(np.ascontiguousarray(book_bits, np.uint16)), ptr(idx), idx.size, D,
+                       book_bits.shape[0])
+    return idx
+
+
+def vq_decode(out_bits, book_bits, idx):
+    D = book_bits.shape[1]
+    _lib.orc_vq_decode(ptr(out_bits), ptr(np.ascontiguousarray(book_bits, np.uint16)),
+                       ptr(np.ascontiguousarray(idx, np.uint16)), idx.size, D, book_bits.shape[0])
+
+
+def vq_kmeans(data_bits, book_bits, iterations):
+    """In place on book_bits (uint16 [K, D])."""
+    D = book_bits.shape[1]
+    data = np.ascontiguousarray(data_bits, np.uint16)
+    _lib.orc_vq_kmeans(ptr(data), ptr(book_bits), data.size // D, book_bits.shape[0], D, iterations)
 
 
 def copy_blocks(k_cache, v_cache, mapping):

@@ -144,6 +144,22 @@ def test_rope_rejects_bad_arguments():
     assert f(*args(T=0, q=None, key=None)) == tla.OK
 
 
+def test_vq_rejects_bad_arguments():
+    L = tla.lib
+    assert L.tl_vq_encode(FAKE, FAKE, FAKE, 4, 12, 256, None) == tla.ERR_INVALID_ARGUMENT     # head_dim % 8
+    assert L.tl_vq_encode(FAKE, FAKE, FAKE, 4, 264, 256, None) == tla.ERR_INVALID_ARGUMENT    # > 256
+    assert L.tl_vq_encode(FAKE, FAKE, FAKE, 4, 128, 0, None) == tla.ERR_INVALID_ARGUMENT
+    assert L.tl_vq_encode(FAKE, FAKE, FAKE, 4, 128, 65537, None) == tla.ERR_INVALID_ARGUMENT
+    assert L.tl_vq_encode(FAKE, ctypes.c_void_p(0x1002), FAKE, 4, 128, 256, None) == tla.ERR_INVALID_ARGUMENT
+    assert L.tl_vq_decode(None, FAKE, FAKE, 4, 128, 256, None) == tla.ERR_INVALID_ARGUMENT
+    assert L.tl_vq_encode(None, None, None, 0, 128, 256, None) == tla.OK
+    need = L.tl_vq_kmeans_workspace_bytes(1000, 256, 128)
+    assert need >= 1000 * 4 + 256 * 128 * 12
+    assert L.tl_vq_kmeans(FAKE, FAKE, 1000, 256, 128, 5, FAKE, need - 1, None) == tla.ERR_INVALID_ARGUMENT
+    assert L.tl_vq_kmeans(FAKE, FAKE, 1000, 256, 128, -1, FAKE, need, None) == tla.ERR_INVALID_ARGUMENT
+    assert L.tl_vq_kmeans(FAKE, FAKE, 1000, 256, 128, 0, FAKE, need, None) == tla.OK
+
+
 def test_kivi_host_helpers_match_reference_known_answers():
     # test_kivi_bounds.cpp:25-69, through the library
     assert tla.kivi_compressed_bytes(128, 8, 16) == 24 + 8 * 12
@@ -223,6 +239,9 @@ def test_exports_reference_named_operators():
         "truellm::kivi_decompress(unsigned char const*, __half*, int, int, int, int, ihipStream_t*)",
         "copy_blocks(truellm::TrueBuffer&, truellm::TrueBuffer const&, ihipStream_t*)",
         "swap_blocks(truellm::TrueBuffer&, truellm::TrueBuffer&, truellm::TrueBuffer const&, int, ihipStream_t*)",
+        "truellm::vq_encode(__half const*, __half const*, unsigned short*, int, int, int, int, ihipStream_t*)",
+        "truellm::vq_decode(__half*, __half const*, unsigned short const*, int, int, int, ihipStream_t*)",
+        "truellm::codebook_init_kmeans(void const*, void*, int, int, int, int, ihipStream_t*)",
         "truellm_kernel_init",
     ]
     missing = [w for w in want if w not in exp]

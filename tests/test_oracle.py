@@ -660,3 +660,81 @@ def test_rope_oracle_preserves_pair_norms_with_reference_tables():
         n_in = np.hypot(q[..., d0], q[..., d1])
         n_out = np.hypot(q_out[..., d0], q_out[..., d1])
         assert np.allclose(n_in, n_out, rtol=1e-6, atol=1e-6)
+
+
+# ---------------------------------------------------------------------------
+# VQ codec
+# ---------------------------------------------------------------------------
+
+def _f16(x):
+    return orc.f32_to_f16_bits(np.asarray(x, np.float32))
+
+
+def test_vq_oracle_reference_known_answers():
+    """test_vq_kernels.cpp:96-204: exact copies encode to their own entry and
+    decode back; perturbations of +-1 around entries 1000 apart pick the
+    nearest; decode of synthetic indices reads those rows."""
+    book = _f16([[c * 10 + d for d in range(8)] for c in range(4)])
+    want = np.array([(t * 2 + h) % 4 for t in range(4) for h in range(2)], np.uint16)
+    kv = book[want]
+    idx = orc.vq_encode(kv, book)
+    assert np.array_equal(idx, want)
+    out = np.zeros_like(kv)
+    orc.vq_decode(out, book, idx)
+    assert np.array_equal(out, kv)
+    book2 = _f16([[0] * 4, [1000] * 4, [2000] * 4])
+    kv2 = _f16([[0.5, -0.5, 0.2, -0.2], [1001, 999, 1000.5, 999.5], [1999, 2001, 1999.5, 2000.5]])
+    assert np.array_equal(orc.vq_encode(kv2, book2), np.array([0, 1, 2], np.uint16))
+    book3 = _f16([[100 * c + d for d in range(4)] for c in range(5)])
+    idx3 = np.array([4, 0, 2, 3], np.uint16)
+    out3 = np.zeros((4, 4), np.uint16)
+    orc.vq_decode(out3, book3, idx3)
+    assert np.array_equal(out3, book3[idx3])
+
+
+def test_vq_oracle_nearest_ties_and_nan():
+    """Against float64 brute force: the chosen entry's distance is the
+    minimum (up to fp32 rounding); among equal rows the lowest index wins;
+    a vector holding NaN gets index 0."""
+    rng = np.random.default_rng(50)
+    K, D, n = 64, 32, 200
+    book = _f16(rng.standard_normal((K, D)))
+    book[40] = book[7]                                   # a duplicated entry: 7 must win
+    kv = _f16(rng.standard_normal((n, D)))
+    kv[5] = book[7]
+    idx = orc.vq_encode(kv, book)
+    bf, xf = orc.bits_to_f32(book, orc.F16).astype(np.float64), orc.bits_to_f32(kv, orc.F16).astype(np.float64)
+    d64 = ((xf[:, None, :] - bf[None, :, :]) ** 2).sum(-1)
+    chosen = d64[np.arange(n), idx.astype(int)]
+    assert np.all(chosen <= d64.min(1) * (1 + 1e-5) + 1e-6)
+    assert idx[5] == 7 and not np.any(idx == 40)
+    kv[9, 3] = 0x7E00                                    # NaN
+    assert orc.vq_encode(kv, book)[9] == 0
+
+
+def test_vq_kmeans_oracle_exact_means_order_independent_and_empty_clusters():
+    """One Lloyd step on three well-separated groups: each centroid is its
+    members' mean (to one fp16 ulp); the book does not depend on the order
+    of the samples (exact sums); an entry that attracts no sample keeps its
+    value."""
+    rng = np.random.default_rng(51)
+    D = 16
+    centres = np.array([0.0, 50.0, -80.0])
+    data = np.concatenate([c + rng.standard_normal((30, D)) for c in centres]).astype(np.float32)
+    bits = _f16(data)
+    book0 = _f16(np.stack([np.full(D, c + 0.3) for c in centres] + [np.full(D, 1e4)]))
+    book = book0.copy()
+    orc.vq_kmeans(bits, book, 1)
+    xf = orc.bits_to_f32(bits, orc.F16).astype(np.float64)
+    for g in range(3):
+        want = xf[30 * g:30 * (g + 1)].mean(0)
+        got = orc.bits_to_f32(book[g], orc.F16)
+        assert np.all(np.abs(got - want) <= 2.0 ** -10 * np.maximum(np.abs(want), 2.0 ** -14))
+    assert np.array_equal(book[3], book0[3])
+    perm = rng.permutation(len(bits))
+    book_p = book0.copy()
+    orc.vq_kmeans(bits[perm].copy(), book_p, 1)
+    assert np.array_equal(book, book_p)
+    book3 = book0.copy()
+    orc.vq_kmeans(bits, book3, 3)
+    assert np.array_equal(book3[:3], book[:3])          # converged after one step

@@ -278,6 +278,61 @@ int tl_rope_reshape_and_cache(const void* q, void* q_out, const void* key, const
   return ok();
 }
 
+static int check_vq(int32_t num_vecs, int32_t head_dim, int32_t codebook_size) {
+  if (num_vecs < 0 || head_dim <= 0 || head_dim % 8 || head_dim > TL_VQ_MAX_HEAD_DIM || codebook_size < 1 ||
+      codebook_size > 65536)
+    return fail(TL_ERR_INVALID_ARGUMENT, "num_vecs=%d head_dim=%d codebook_size=%d", num_vecs, head_dim,
+                codebook_size);
+  return TL_OK;
+}
+
+int tl_vq_encode(const void* kv, const void* book, uint16_t* idx, int32_t num_vecs, int32_t head_dim,
+                 int32_t codebook_size, void* stream) {
+  int rc = check_vq(num_vecs, head_dim, codebook_size);
+  if (rc) return rc;
+  if (num_vecs == 0) return ok();
+  if (!kv || !book || !idx) return fail(TL_ERR_INVALID_ARGUMENT, "NULL pointer");
+  if (!aligned16(book)) return fail(TL_ERR_INVALID_ARGUMENT, "book must be 16-byte aligned");
+  tl::VqArgs a = {(const uint16_t*)kv, (const uint16_t*)book, idx, nullptr, num_vecs, head_dim, codebook_size};
+  if (tl::launch_vq_assign(a, (hipStream_t)stream)) return fail(TL_ERR_BACKEND, "vq_encode launch failed");
+  return ok();
+}
+
+int tl_vq_decode(void* kv_out, const void* book, const uint16_t* idx, int32_t num_vecs, int32_t head_dim,
+                 int32_t codebook_size, void* stream) {
+  int rc = check_vq(num_vecs, head_dim, codebook_size);
+  if (rc) return rc;
+  if (num_vecs == 0) return ok();
+  if (!kv_out || !book || !idx) return fail(TL_ERR_INVALID_ARGUMENT, "NULL pointer");
+  if (!aligned16(book) || !aligned16(kv_out))
+    return fail(TL_ERR_INVALID_ARGUMENT, "kv_out and book must be 16-byte aligned");
+  if (tl::launch_vq_decode(kv_out, book, idx, num_vecs, head_dim, codebook_size, (hipStream_t)stream))
+    return fail(TL_ERR_BACKEND, "vq_decode launch failed");
+  return ok();
+}
+
+size_t tl_vq_kmeans_workspace_bytes(int32_t n_samples, int32_t codebook_size, int32_t head_dim) {
+  if (n_samples < 0 || check_vq(0, head_dim, codebook_size) != TL_OK) return 0;
+  return tl::vq_kmeans_workspace(n_samples, codebook_size, head_dim);
+}
+
+int tl_vq_kmeans(const void* data, void* book, int32_t n_samples, int32_t codebook_size, int32_t head_dim,
+                 int32_t n_iterations, void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = check_vq(n_samples, head_dim, codebook_size);
+  if (rc) return rc;
+  if (n_iterations < 0) return fail(TL_ERR_INVALID_ARGUMENT, "n_iterations=%d", n_iterations);
+  if (n_samples == 0 || n_iterations == 0) return ok();
+  if (!data || !book || !workspace) return fail(TL_ERR_INVALID_ARGUMENT, "NULL pointer");
+  if (!aligned16(book)) return fail(TL_ERR_INVALID_ARGUMENT, "book must be 16-byte aligned");
+  const size_t need = tl::vq_kmeans_workspace(n_samples, codebook_size, head_dim);
+  if (workspace_bytes < need)
+    return fail(TL_ERR_INVALID_ARGUMENT, "workspace of %zu bytes needed, %zu given", need, workspace_bytes);
+  if (tl::launch_vq_kmeans(data, book, n_samples, codebook_size, head_dim, n_iterations, workspace,
+                           (hipStream_t)stream))
+    return fail(TL_ERR_BACKEND, "vq_kmeans launch failed");
+  return ok();
+}
+
 int tl_copy_blocks(void* k_cache, void* v_cache, const int32_t* block_mapping, int32_t num_pairs,
                    int32_t num_blocks, int64_t block_bytes, void* stream) {
   if (num_pairs < 0 || num_blocks <= 0 || block_bytes <= 0)

@@ -80,6 +80,23 @@ struct RopeCache {
 };
 int launch_rope_cache(const RopeCache& a, hipStream_t stream);
 
+// VQ codec.  Encode / assign: the nearest codebook entry of each fp16
+// vector, as uint16 (idx16) or int32 (idx32).
+constexpr int kVqMaxDim = 256;
+struct VqArgs {
+  const uint16_t* vecs;         // [n, head_size] fp16
+  const uint16_t* book;         // [codebook_size, head_size] fp16
+  uint16_t* idx16; int32_t* idx32;
+  int64_t num_vecs;
+  int head_size, codebook_size;
+};
+int launch_vq_assign(const VqArgs& a, hipStream_t stream);
+int launch_vq_decode(void* out, const void* book, const uint16_t* idx, int64_t num_vecs, int head_size,
+                     int codebook_size, hipStream_t stream);
+size_t vq_kmeans_workspace(int64_t n, int codebook_size, int head_size);
+int launch_vq_kmeans(const void* data, void* book, int64_t n, int codebook_size, int head_size, int iterations,
+                     void* workspace, hipStream_t stream);
+
 // Whole-block copies: for pair p of mapping [num_pairs][2] = {src, dst},
 // block src of src0 (and of src1 when pools == 2) to block dst of dst0
 // (dst1).  Ids outside [0, src_blocks) / [0, dst_blocks) skip the pair.

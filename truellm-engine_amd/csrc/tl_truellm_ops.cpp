@@ -105,6 +105,30 @@ void paged_attention_v2(TrueBuffer& out, TrueBuffer& exp_sums, TrueBuffer& max_l
 
 namespace truellm {
 
+void vq_encode(const __half* d_kv, const __half* d_book, uint16_t* d_idx, int seq_len, int n_kv_heads,
+               int head_dim, int codebook_size, hipStream_t stream) {
+  report("vq_encode", tl_vq_encode(d_kv, d_book, d_idx, seq_len * n_kv_heads, head_dim, codebook_size, stream));
+}
+
+void vq_decode(__half* d_kv, const __half* d_book, const uint16_t* d_idx, int seq_len, int n_kv_heads,
+               int head_dim, hipStream_t stream) {
+  report("vq_decode", tl_vq_decode(d_kv, d_book, d_idx, seq_len * n_kv_heads, head_dim, 65536, stream));
+}
+
+void codebook_init_kmeans(const void* d_data, void* d_book, int n_samples, int codebook_size, int head_dim,
+                          int n_iterations, hipStream_t stream) {
+  const size_t ws = tl_vq_kmeans_workspace_bytes(n_samples, codebook_size, head_dim);
+  void* work = nullptr;
+  if (ws == 0 || hipMalloc(&work, ws) != hipSuccess) {
+    fprintf(stderr, "[tlattn] codebook_init_kmeans: no workspace (%zu bytes)\n", ws);
+    return;
+  }
+  report("codebook_init_kmeans",
+         tl_vq_kmeans(d_data, d_book, n_samples, codebook_size, head_dim, n_iterations, work, ws, stream));
+  (void)hipStreamSynchronize(stream);
+  (void)hipFree(work);
+}
+
 bool kivi_params_supported(int head_dim, int n_outliers, int group_size) {
   return tl_kivi_params_supported(head_dim, n_outliers, group_size) != 0;
 }

@@ -108,6 +108,10 @@ _SIG = {
     "tl_reshape_and_cache": (ctypes.c_int, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P]),
     "tl_reshape_and_cache_fp8": (ctypes.c_int, [_P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _I, _F, _F, _P]),
     "tl_rope_reshape_and_cache": (ctypes.c_int, [_P] * 10 + [_I] * 9 + [_P]),
+    "tl_vq_encode": (ctypes.c_int, [_P, _P, _P, _I, _I, _I, _P]),
+    "tl_vq_decode": (ctypes.c_int, [_P, _P, _P, _I, _I, _I, _P]),
+    "tl_vq_kmeans_workspace_bytes": (ctypes.c_size_t, [_I, _I, _I]),
+    "tl_vq_kmeans": (ctypes.c_int, [_P, _P, _I, _I, _I, _I, _P, ctypes.c_size_t, _P]),
     "tl_copy_blocks": (ctypes.c_int, [_P, _P, _P, _I, _I, ctypes.c_int64, _P]),
     "tl_swap_blocks": (ctypes.c_int, [_P, _P, _P, _I, _I, _I, ctypes.c_int64, _I, _P]),
     "tl_fp8_absmax_scale": (ctypes.c_int, [_P, _I, ctypes.c_int64, _P, _P]),
@@ -254,6 +258,29 @@ def reshape_and_cache_split(key, value, k_cache, v_cache, slot_mapping, stream=N
     check(lib.tl_reshape_and_cache(
         _ptr(key), _ptr(value), _ptr(k_cache), _ptr(v_cache), _ptr(slot_mapping), T, n_kv, D,
         k_cache.shape[3], k_cache.shape[0], dtype_code(key), _stream(stream)))
+
+
+def vq_encode(kv, book, idx, stream=None):
+    """vq_cache.cu:74: idx (uint16 / int16 [n]) = nearest entry of book
+    [K, D] for each fp16 row of kv [..., D]."""
+    D = book.shape[1]
+    check(lib.tl_vq_encode(_ptr(kv), _ptr(book), _ptr(idx), kv.numel() // D, D, book.shape[0], _stream(stream)))
+
+
+def vq_decode(out, book, idx, stream=None):
+    D = book.shape[1]
+    check(lib.tl_vq_decode(_ptr(out), _ptr(book), _ptr(idx), out.numel() // D, D, book.shape[0], _stream(stream)))
+
+
+def vq_kmeans_workspace_bytes(n_samples, codebook_size, head_dim):
+    return lib.tl_vq_kmeans_workspace_bytes(n_samples, codebook_size, head_dim)
+
+
+def vq_kmeans(data, book, n_iterations, workspace, stream=None):
+    """codebook_init.cu:100: Lloyd iterations over data [n, D] on book [K, D] in place."""
+    D = book.shape[1]
+    check(lib.tl_vq_kmeans(_ptr(data), _ptr(book), data.numel() // D, book.shape[0], D, n_iterations,
+                           _ptr(workspace), workspace.numel() * workspace.element_size(), _stream(stream)))
 
 
 ROPE_ADJACENT, ROPE_HALVES = 0, 1
