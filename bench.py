@@ -73,7 +73,7 @@ def parse():
     p.add_argument("--partition-tokens", type=int, default=0)
     p.add_argument("--cpu-seconds", type=float, default=15.0)
     p.add_argument("--no-cpu", action="store_true")
-    p.add_argument("--only", default="all", choices=["all", "bf16", "fp16", "kivi", "fp8", "prefill", "blocks", "rope", "vq"])
+    p.add_argument("--only", default="all", choices=["all", "bf16", "fp16", "kivi", "fp8", "prefill", "blocks", "rope", "vq", "norm"])
     p.add_argument("--no-graph", action="store_true",
                    help="launch the timed steps eagerly (for counter passes that cannot follow graphs)")
     p.add_argument("--copy-calibration", action="store_true",
@@ -280,6 +280,40 @@ def bench_rope(args):
     ms = timed(step, args.steps, args.warmup)
     nbytes = 2 * q.numel() * 2 + 4 * k.numel() * 2 + 2 * S * (D // 2) * 4 + 2 * S * 4
     return {"us": ms * 1e3, "bytes": nbytes}
+
+
+NA_ROWS, NA_HID, NA_FFN = 4096, 4096, 14336
+
+
+def bench_norm_act(args):
+    """A 4096-token prefill chunk of Llama-3-8B's layer edges, bf16:
+    fused_add_rms_norm over [4096, 4096] (read x and the residual, write the
+    residual and out) and silu_and_mul over [4096, 14336] (read gate and up,
+    write out)."""
+    import torch
+
+    import tl_attn as tla
+
+    g = torch.Generator(device="cuda").manual_seed(0x7E5E0009)
+    x = torch.randn(NA_ROWS, NA_HID, generator=g, device="cuda", dtype=torch.bfloat16)
+    res = torch.randn_like(x)
+    w = torch.randn(NA_HID, generator=g, device="cuda", dtype=torch.bfloat16)
+    out = torch.empty_like(x)
+    gate = torch.randn(NA_ROWS, NA_FFN, generator=g, device="cuda", dtype=torch.bfloat16)
+    up = torch.randn_like(gate)
+    act = torch.empty_like(gate)
+
+    def norm_step(i, stream):
+        tla.fused_add_rms_norm(out, res, x, w, 1e-5, stream)
+
+    def act_step(i, stream):
+        tla.act_and_mul(act, gate, up, tla.ACT_SILU, stream)
+
+    ms_n = timed(norm_step, args.steps, args.warmup)
+    ms_a = timed(act_step, args.steps, args.warmup)
+    bn = 4 * x.numel() * 2 + w.numel() * 2
+    ba = 3 * gate.numel() * 2
+    return {"norm_us": ms_n * 1e3, "norm_bytes": bn, "act_us": ms_a * 1e3, "act_bytes": ba}
 
 
 VQ_N, VQ_K = 2048 * 8, 256
@@ -502,6 +536,7 @@ def main():
     cb = bench_copy_blocks(args) if args.only in ("all", "blocks") else None
     rp = bench_rope(args) if args.only in ("all", "rope") else None
     vq = bench_vq(args) if args.only in ("all", "vq") else None
+    na = bench_norm_act(args) if args.only in ("all", "norm") else None
     head = bf or fp
     if head is not None:
         res["dtype"] = "bf16" if bf else "fp16"
@@ -577,6 +612,14 @@ def main():
             "workload": f"VQ encode, {VQ_N} fp16 vectors of d {D} against {VQ_K} entries (exact fp32 distances)",
             "us_per_call": round(vq["ms"] * 1e3, 2), "tflops_fp32": round(vq["tflops"], 2),
             "pct_fp32_vector_peak": round(100 * vq["tflops"] / 157.3, 2), "flops_per_call": vq["flops"]}
+    if na is not None:
+        res["norm_act"] = {
+            "workload": f"bf16, {NA_ROWS} rows: fused_add_rms_norm [{NA_ROWS}, {NA_HID}], silu_and_mul "
+                        f"[{NA_ROWS}, {NA_FFN}]",
+            "fused_add_rms_norm_us": round(na["norm_us"], 2),
+            "fused_add_rms_norm_gbs": round(na["norm_bytes"] / (na["norm_us"] * 1e-6) / 1e9, 2),
+            "silu_and_mul_us": round(na["act_us"], 2),
+            "silu_and_mul_gbs": round(na["act_bytes"] / (na["act_us"] * 1e-6) / 1e9, 2)}
     if not args.no_cpu:
         res["cpu_baseline"] = cpu_baseline(args.cpu_seconds, 4, min(16, os.cpu_count() or 1))
     print(json.dumps(res), flush=True)

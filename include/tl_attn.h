@@ -189,6 +189,41 @@ int tl_swap_blocks(void* cache, void* host_cache, const int32_t* block_mapping, 
                    int32_t direction, void* stream);
 
 /* ------------------------------------------------------------------------
+ * Norms and gated activations (layernorm_kernels.cu, activation_kernels.cu)
+ * --------------------------------------------------------------------- */
+
+/* Replaces rms_norm (layernorm_kernels.cu:149-167, kernel :28-56): for each
+ * of num_tokens rows of x [num_tokens, hidden_size], out = x *
+ * (1 / sqrt(sum(x^2) / hidden_size + eps)) * weight, in fp32, rounded once
+ * to dtype (F16, BF16 or F32 for x, weight and out).  The total is taken
+ * over the whole row for every element (the reference's block reduction
+ * leaves it in warp 0 only, defect D4). */
+int tl_rms_norm(void* out, const void* x, const void* weight, int32_t num_tokens, int32_t hidden_size,
+                float eps, int32_t dtype, void* stream);
+
+/* Replaces fused_add_rms_norm (layernorm_kernels.cu:169-189, kernel
+ * :64-94): r = residual + x; residual = dtype(r) in place; the mean square
+ * over the fp32 r; out = float(residual) * (1 / sqrt(...)) * weight. */
+int tl_fused_add_rms_norm(void* out, void* residual, const void* x, const void* weight, int32_t num_tokens,
+                          int32_t hidden_size, float eps, int32_t dtype, void* stream);
+
+/* Replaces layer_norm (layernorm_kernels.cu:191-211, kernel :102-139):
+ * out = (x - mean) * (1 / sqrt(var + eps)) * weight + bias, var the mean of
+ * (x - mean)^2 (two passes over the row). */
+int tl_layer_norm(void* out, const void* x, const void* weight, const void* bias, int32_t num_tokens,
+                  int32_t hidden_size, float eps, int32_t dtype, void* stream);
+
+/* Gated activations (activation_kernels.cu:57-132). */
+typedef enum tl_activation { TL_ACT_SILU = 0, TL_ACT_GELU = 1, TL_ACT_GELU_TANH = 2 } tl_activation;
+
+/* Replaces silu_and_mul / gelu_and_mul / gelu_tanh_and_mul: out[i] =
+ * dtype(act(gate[i])) * up[i], over n elements of gate, up and out; the
+ * activation is rounded to dtype before the product, as the reference's
+ * act() returns the storage type. */
+int tl_act_and_mul(void* out, const void* gate, const void* up, int64_t n, int32_t activation, int32_t dtype,
+                   void* stream);
+
+/* ------------------------------------------------------------------------
  * VQ codec of the KV cache (vq_cache.cu, codebook_init.cu)
  * --------------------------------------------------------------------- */
 

@@ -95,6 +95,22 @@ void copy_blocks(truellm::TrueBuffer& kv_cache, const truellm::TrueBuffer& block
 void swap_blocks(truellm::TrueBuffer& kv_cache, truellm::TrueBuffer& host_cache,
                  const truellm::TrueBuffer& block_mapping, int direction, hipStream_t stream);
 
+/* layernorm_kernels.cu:149-211 and activation_kernels.cu:104-132: x / out
+ * [num_tokens, hidden] (shape[0], shape[1]), F32, F16 or BF16 (the
+ * reference runs anything but F16 as f32). */
+void rms_norm(truellm::TrueBuffer& out, const truellm::TrueBuffer& x, const truellm::TrueBuffer& weight, float eps,
+              hipStream_t stream);
+void fused_add_rms_norm(truellm::TrueBuffer& out, truellm::TrueBuffer& residual, const truellm::TrueBuffer& x,
+                        const truellm::TrueBuffer& weight, float eps, hipStream_t stream);
+void layer_norm(truellm::TrueBuffer& out, const truellm::TrueBuffer& x, const truellm::TrueBuffer& weight,
+                const truellm::TrueBuffer& bias, float eps, hipStream_t stream);
+void silu_and_mul(truellm::TrueBuffer& out, const truellm::TrueBuffer& gate, const truellm::TrueBuffer& up,
+                  hipStream_t stream);
+void gelu_and_mul(truellm::TrueBuffer& out, const truellm::TrueBuffer& gate, const truellm::TrueBuffer& up,
+                  hipStream_t stream);
+void gelu_tanh_and_mul(truellm::TrueBuffer& out, const truellm::TrueBuffer& gate, const truellm::TrueBuffer& up,
+                       hipStream_t stream);
+
 /* paged_attention_v1.cu:177-189 */
 void paged_attention_v1(truellm::TrueBuffer& out, const truellm::TrueBuffer& q,
                         const truellm::TrueBuffer& k_cache, const truellm::TrueBuffer& v_cache,

@@ -245,6 +245,69 @@ void orc_rope_reshape_and_cache(const void* q, void* q_out, const void* key, con
 }
 
 /* ========================================================================
+ * Norms and gated activations  (layernorm_kernels.cu:28-139,
+ * activation_kernels.cu:57-100), intended semantics; the row sums in
+ * double (the device's fp32 tree sum differs from any order by a few fp32
+ * ulps, far below the output dtype's)
+ * ====================================================================== */
+
+void orc_rms_norm(void* out, void* residual, const void* x, const void* w, int rows, int hidden, float eps,
+                  int dtype)
+{
+    for (int r = 0; r < rows; ++r) {
+        int64_t base = (int64_t)r * hidden;
+        double ss = 0.0;
+        for (int i = 0; i < hidden; ++i) {
+            float v = load_f32(x, dtype, base + i);
+            if (residual) {
+                v = v + load_f32(residual, dtype, base + i);
+                store_elem(residual, dtype, base + i, v);
+            }
+            ss += (double)v * v;
+        }
+        float inv = (float)(1.0 / sqrt(ss / hidden + eps));
+        const void* src = residual ? residual : x;
+        for (int i = 0; i < hidden; ++i)
+            store_elem(out, dtype, base + i, load_f32(src, dtype, base + i) * inv * load_f32(w, dtype, i));
+    }
+}
+
+void orc_layer_norm(void* out, const void* x, const void* w, const void* b, int rows, int hidden, float eps,
+                    int dtype)
+{
+    for (int r = 0; r < rows; ++r) {
+        int64_t base = (int64_t)r * hidden;
+        double s = 0.0, var = 0.0;
+        for (int i = 0; i < hidden; ++i) s += load_f32(x, dtype, base + i);
+        double mean = s / hidden;
+        for (int i = 0; i < hidden; ++i) {
+            double d = load_f32(x, dtype, base + i) - mean;
+            var += d * d;
+        }
+        double inv = 1.0 / sqrt(var / hidden + eps);
+        for (int i = 0; i < hidden; ++i)
+            store_elem(out, dtype, base + i,
+                       (float)((load_f32(x, dtype, base + i) - mean) * inv * load_f32(w, dtype, i) +
+                               load_f32(b, dtype, i)));
+    }
+}
+
+void orc_act_and_mul(void* out, const void* gate, const void* up, int64_t n, int act, int dtype)
+{
+    for (int64_t i = 0; i < n; ++i) {
+        float g = load_f32(gate, dtype, i), a;
+        if (act == 0) a = g / (1.f + expf(-g));
+        else if (act == 1) a = 0.5f * g * (1.f + erff(g * 0.70710678118f));
+        else a = 0.5f * g * (1.f + tanhf(0.79788456f * (g + 0.044715f * g * g * g)));
+        /* the activation rounded to the storage type, then the product */
+        uint16_t bits;
+        if (dtype == ORC_F16) { bits = orc_f32_to_f16(a); a = orc_f16_to_f32(bits); }
+        else if (dtype == ORC_BF16) { bits = orc_f32_to_bf16(a); a = orc_bf16_to_f32(bits); }
+        store_elem(out, dtype, i, a * load_f32(up, dtype, i));
+    }
+}
+
+/* ========================================================================
  * VQ codec  (vq_cache.cu:18-69, codebook_init.cu:23-145)
  *   encode: dist_c = fold_d fmaf(x_d - b_cd, x_d - b_cd, dist) (fp32, d in
  *   order); the first c with dist_c < best (best = FLT_MAX at the start)

@@ -55,6 +55,11 @@ void orc_rope_reshape_and_cache(const void* q, void* q_out, const void* key, con
                                 const int32_t* positions, const float* cos_table, const float* sin_table,
                                 int max_positions, int num_tokens, int num_heads, int num_kv_heads,
                                 int head_size, int block_size, int num_blocks, int dtype, int style);
+void orc_rms_norm(void* out, void* residual, const void* x, const void* w, int rows, int hidden, float eps,
+                  int dtype);
+void orc_layer_norm(void* out, const void* x, const void* w, const void* b, int rows, int hidden, float eps,
+                    int dtype);
+void orc_act_and_mul(void* out, const void* gate, const void* up, int64_t n, int act, int dtype);
 void orc_vq_encode(const uint16_t* kv, const uint16_t* book, uint16_t* idx, int64_t num_vecs, int head_dim,
                    int codebook_size);
 void orc_vq_decode(uint16_t* out, const uint16_t* book, const uint16_t* idx, int64_t num_vecs, int head_dim,

@@ -37,6 +37,9 @@ _lib.orc_convert.argtypes = [_P, _I, _P, _I, ctypes.c_int64, _F]
 _lib.orc_reshape_and_cache.argtypes = [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I]
 _lib.orc_reshape_and_cache_fp8.argtypes = [_P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _F, _F]
 _lib.orc_rope_reshape_and_cache.argtypes = [_P] * 10 + [_I] * 9
+_lib.orc_rms_norm.argtypes = [_P, _P, _P, _P, _I, _I, _F, _I]
+_lib.orc_layer_norm.argtypes = [_P, _P, _P, _P, _I, _I, _F, _I]
+_lib.orc_act_and_mul.argtypes = [_P, _P, _P, ctypes.c_int64, _I, _I]
 _lib.orc_vq_encode.argtypes = [_P, _P, _P, ctypes.c_int64, _I, _I]
 _lib.orc_vq_decode.argtypes = [_P, _P, _P, ctypes.c_int64, _I, _I]
 _lib.orc_vq_kmeans.argtypes = [_P, _P, ctypes.c_int64, _I, _I, _I]
@@ -125,6 +128,26 @@ def rope_reshape_and_cache(q, q_out, key, value, k_cache, v_cache, slots, positi
                                     ptr(key), ptr(value), ptr(k_cache), ptr(v_cache), ptr(slots),
                                     ptr(positions), ptr(cos_t), ptr(sin_t), cos_t.shape[0], T, H, n_kv, D,
                                     k_cache.shape[3], k_cache.shape[0], code, style)
+
+
+def rms_norm(x, w, eps, code, residual=None):
+    """Returns out (same storage as x); residual (if given) is updated in place."""
+    out = np.zeros_like(x)
+    _lib.orc_rms_norm(ptr(out), None if residual is None else ptr(residual), ptr(x), ptr(w), x.shape[0],
+                      x.shape[1], eps, code)
+    return out
+
+
+def layer_norm(x, w, b, eps, code):
+    out = np.zeros_like(x)
+    _lib.orc_layer_norm(ptr(out), ptr(x), ptr(w), ptr(b), x.shape[0], x.shape[1], eps, code)
+    return out
+
+
+def act_and_mul(gate, up, act, code):
+    out = np.zeros_like(gate)
+    _lib.orc_act_and_mul(ptr(out), ptr(gate), ptr(up), gate.size, act, code)
+    return out
 
 
 def vq_encode(kv_bits, book_bits):

@@ -160,6 +160,19 @@ def test_vq_rejects_bad_arguments():
     assert L.tl_vq_kmeans(FAKE, FAKE, 1000, 256, 128, 0, FAKE, need, None) == tla.OK
 
 
+def test_norm_act_reject_bad_arguments():
+    L = tla.lib
+    assert L.tl_rms_norm(FAKE, FAKE, FAKE, 4, 0, 1e-5, tla.F16, None) == tla.ERR_INVALID_ARGUMENT
+    assert L.tl_rms_norm(FAKE, FAKE, FAKE, 4, 128, 1e-5, 9, None) == tla.ERR_INVALID_ARGUMENT
+    assert L.tl_rms_norm(None, FAKE, FAKE, 4, 128, 1e-5, tla.F16, None) == tla.ERR_INVALID_ARGUMENT
+    assert L.tl_fused_add_rms_norm(FAKE, None, FAKE, FAKE, 4, 128, 1e-5, tla.F16, None) == tla.ERR_INVALID_ARGUMENT
+    assert L.tl_layer_norm(FAKE, FAKE, FAKE, None, 4, 128, 1e-5, tla.F16, None) == tla.ERR_INVALID_ARGUMENT
+    assert L.tl_act_and_mul(FAKE, FAKE, FAKE, 16, 3, tla.F16, None) == tla.ERR_INVALID_ARGUMENT
+    assert L.tl_act_and_mul(FAKE, FAKE, FAKE, -1, 0, tla.F16, None) == tla.ERR_INVALID_ARGUMENT
+    assert L.tl_act_and_mul(None, None, None, 0, 0, tla.F16, None) == tla.OK
+    assert L.tl_rms_norm(None, None, None, 0, 128, 1e-5, tla.F16, None) == tla.OK
+
+
 def test_kivi_host_helpers_match_reference_known_answers():
     # test_kivi_bounds.cpp:25-69, through the library
     assert tla.kivi_compressed_bytes(128, 8, 16) == 24 + 8 * 12
@@ -242,6 +255,15 @@ def test_exports_reference_named_operators():
         "truellm::vq_encode(__half const*, __half const*, unsigned short*, int, int, int, int, ihipStream_t*)",
         "truellm::vq_decode(__half*, __half const*, unsigned short const*, int, int, int, ihipStream_t*)",
         "truellm::codebook_init_kmeans(void const*, void*, int, int, int, int, ihipStream_t*)",
+        "rms_norm(truellm::TrueBuffer&, truellm::TrueBuffer const&, truellm::TrueBuffer const&, float, ihipStream_t*)",
+        "fused_add_rms_norm(truellm::TrueBuffer&, truellm::TrueBuffer&, truellm::TrueBuffer const&, "
+        "truellm::TrueBuffer const&, float, ihipStream_t*)",
+        "layer_norm(truellm::TrueBuffer&, truellm::TrueBuffer const&, truellm::TrueBuffer const&, "
+        "truellm::TrueBuffer const&, float, ihipStream_t*)",
+        "silu_and_mul(truellm::TrueBuffer&, truellm::TrueBuffer const&, truellm::TrueBuffer const&, ihipStream_t*)",
+        "gelu_and_mul(truellm::TrueBuffer&, truellm::TrueBuffer const&, truellm::TrueBuffer const&, ihipStream_t*)",
+        "gelu_tanh_and_mul(truellm::TrueBuffer&, truellm::TrueBuffer const&, truellm::TrueBuffer const&, "
+        "ihipStream_t*)",
         "truellm_kernel_init",
     ]
     missing = [w for w in want if w not in exp]

@@ -738,3 +738,72 @@ def test_vq_kmeans_oracle_exact_means_order_independent_and_empty_clusters():
     book3 = book0.copy()
     orc.vq_kmeans(bits, book3, 3)
     assert np.array_equal(book3[:3], book[:3])          # converged after one step
+
+
+# ---------------------------------------------------------------------------
+# norms and gated activations
+# ---------------------------------------------------------------------------
+
+def test_norm_act_oracle_reference_known_answers():
+    """test_vllm_kernels.cpp:128-253: RMSNorm of a 2 x 8 ramp against the
+    double reference (1e-4), uniform input with eps 0 gives 1, silu_and_mul
+    of ramps against x / (1 + exp(-x)) * up (1e-5), up = 0 gives 0."""
+    T, H = 2, 8
+    x = (0.1 * (np.arange(T * H) + 1)).astype(np.float32).reshape(T, H)
+    w = (1.0 - 0.05 * np.arange(H)).astype(np.float32)
+    got = orc.rms_norm(x, w, 1e-5, orc.F32)
+    xd = x.astype(np.float64)
+    want = xd / np.sqrt((xd ** 2).mean(1, keepdims=True) + 1e-5) * w
+    assert np.allclose(got, want, atol=1e-4, rtol=0)
+    u = np.full((1, 32), 2.5, np.float32)
+    assert np.allclose(orc.rms_norm(u, np.ones(32, np.float32), 0.0, orc.F32), 1.0, atol=1e-4)
+    g = (-1.0 + 0.07 * np.arange(64)).astype(np.float32).reshape(4, 16)
+    up = (0.25 + 0.03 * np.arange(64)).astype(np.float32).reshape(4, 16)
+    got = orc.act_and_mul(g, up, 0, orc.F32)
+    gd = g.astype(np.float64)
+    assert np.allclose(got, gd / (1 + np.exp(-gd)) * up, atol=1e-5, rtol=0)
+    g2 = (np.arange(128) - 64).astype(np.float32).reshape(2, 64)
+    assert not np.any(orc.act_and_mul(g2, np.zeros_like(g2), 0, orc.F32))
+
+
+def test_fused_add_rms_norm_and_layer_norm_oracle_closed_forms():
+    """fused_add_rms_norm = residual update (res + x rounded) followed by the
+    mean square of the unrounded sums applied to the rounded residual;
+    layer_norm against float64 mean / variance, and a constant row gives the
+    bias."""
+    rng = np.random.default_rng(70)
+    T, H = 5, 96
+    code = orc.BF16
+    x = inputs.encode(rng.standard_normal((T, H), dtype=np.float32), code)
+    res = inputs.encode(rng.standard_normal((T, H), dtype=np.float32), code)
+    w = inputs.encode(1 + 0.1 * rng.standard_normal(H, dtype=np.float32), code)
+    r = res.copy()
+    out = orc.rms_norm(x, w, 1e-6, code, residual=r)
+    s32 = orc.bits_to_f32(res, code) + orc.bits_to_f32(x, code)
+    assert np.array_equal(r, orc.f32_to_bf16_bits(s32))
+    inv = 1.0 / np.sqrt((s32.astype(np.float64) ** 2).mean(1, keepdims=True) + 1e-6)
+    want = orc.bits_to_f32(r, code) * inv * orc.bits_to_f32(w, code)
+    got = orc.bits_to_f32(out, code)
+    assert np.all(np.abs(got - want) <= 2.0 ** -7 * np.abs(want) + 1e-6)
+    xf = rng.standard_normal((T, H)).astype(np.float32)
+    wf = rng.standard_normal(H).astype(np.float32)
+    bf = rng.standard_normal(H).astype(np.float32)
+    got = orc.layer_norm(xf, wf, bf, 1e-5, orc.F32)
+    xd = xf.astype(np.float64)
+    want = (xd - xd.mean(1, keepdims=True)) / np.sqrt(xd.var(1, keepdims=True) + 1e-5) * wf + bf
+    assert np.allclose(got, want, atol=1e-5, rtol=1e-5)
+    const = np.full((2, H), 3.0, np.float32)
+    assert np.allclose(orc.layer_norm(const, wf, bf, 1e-5, orc.F32), bf, atol=1e-6)
+
+
+def test_gelu_oracle_matches_float64_formulas():
+    import math
+    g = np.linspace(-6, 6, 241).astype(np.float32).reshape(1, -1)
+    up = np.ones_like(g)
+    got = orc.act_and_mul(g, up, 1, orc.F32)
+    want = np.array([0.5 * v * (1 + math.erf(v / math.sqrt(2))) for v in g.ravel().astype(np.float64)])
+    assert np.allclose(got.ravel(), want, atol=1e-6, rtol=1e-5)
+    got = orc.act_and_mul(g, up, 2, orc.F32)
+    gd = g.ravel().astype(np.float64)
+    want = 0.5 * gd * (1 + np.tanh(0.79788456 * (gd + 0.044715 * gd ** 3)))
+    assert np.allclose(got.ravel(), want, atol=1e-6, rtol=1e-5)

@@ -278,6 +278,56 @@ int tl_rope_reshape_and_cache(const void* q, void* q_out, const void* key, const
   return ok();
 }
 
+static int check_norm(const void* out, const void* x, const void* weight, int32_t rows, int32_t hidden,
+                      int32_t dtype) {
+  if (rows < 0 || hidden <= 0) return fail(TL_ERR_INVALID_ARGUMENT, "num_tokens=%d hidden_size=%d", rows, hidden);
+  if (!is_float_kind(dtype)) return fail(TL_ERR_INVALID_ARGUMENT, "dtype=%d", dtype);
+  if (rows > 0 && (!out || !x || !weight)) return fail(TL_ERR_INVALID_ARGUMENT, "NULL pointer");
+  return TL_OK;
+}
+
+int tl_rms_norm(void* out, const void* x, const void* weight, int32_t num_tokens, int32_t hidden_size,
+                float eps, int32_t dtype, void* stream) {
+  int rc = check_norm(out, x, weight, num_tokens, hidden_size, dtype);
+  if (rc) return rc;
+  if (tl::launch_rms_norm(out, nullptr, x, weight, num_tokens, hidden_size, eps, dtype, (hipStream_t)stream))
+    return fail(TL_ERR_BACKEND, "rms_norm launch failed");
+  return ok();
+}
+
+int tl_fused_add_rms_norm(void* out, void* residual, const void* x, const void* weight, int32_t num_tokens,
+                          int32_t hidden_size, float eps, int32_t dtype, void* stream) {
+  int rc = check_norm(out, x, weight, num_tokens, hidden_size, dtype);
+  if (rc) return rc;
+  if (num_tokens > 0 && !residual) return fail(TL_ERR_INVALID_ARGUMENT, "NULL residual");
+  if (tl::launch_rms_norm(out, residual, x, weight, num_tokens, hidden_size, eps, dtype, (hipStream_t)stream))
+    return fail(TL_ERR_BACKEND, "fused_add_rms_norm launch failed");
+  return ok();
+}
+
+int tl_layer_norm(void* out, const void* x, const void* weight, const void* bias, int32_t num_tokens,
+                  int32_t hidden_size, float eps, int32_t dtype, void* stream) {
+  int rc = check_norm(out, x, weight, num_tokens, hidden_size, dtype);
+  if (rc) return rc;
+  if (num_tokens > 0 && !bias) return fail(TL_ERR_INVALID_ARGUMENT, "NULL bias");
+  if (tl::launch_layer_norm(out, x, weight, bias, num_tokens, hidden_size, eps, dtype, (hipStream_t)stream))
+    return fail(TL_ERR_BACKEND, "layer_norm launch failed");
+  return ok();
+}
+
+int tl_act_and_mul(void* out, const void* gate, const void* up, int64_t n, int32_t activation, int32_t dtype,
+                   void* stream) {
+  if (n < 0 || n > ((int64_t)1 << 40)) return fail(TL_ERR_INVALID_ARGUMENT, "n=%lld", (long long)n);
+  if (activation < TL_ACT_SILU || activation > TL_ACT_GELU_TANH)
+    return fail(TL_ERR_INVALID_ARGUMENT, "activation=%d", activation);
+  if (!is_float_kind(dtype)) return fail(TL_ERR_INVALID_ARGUMENT, "dtype=%d", dtype);
+  if (n == 0) return ok();
+  if (!out || !gate || !up) return fail(TL_ERR_INVALID_ARGUMENT, "NULL pointer");
+  if (tl::launch_act_and_mul(out, gate, up, n, activation, dtype, (hipStream_t)stream))
+    return fail(TL_ERR_BACKEND, "act_and_mul launch failed");
+  return ok();
+}
+
 static int check_vq(int32_t num_vecs, int32_t head_dim, int32_t codebook_size) {
   if (num_vecs < 0 || head_dim <= 0 || head_dim % 8 || head_dim > TL_VQ_MAX_HEAD_DIM || codebook_size < 1 ||
       codebook_size > 65536)

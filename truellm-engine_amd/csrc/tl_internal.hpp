@@ -80,6 +80,14 @@ struct RopeCache {
 };
 int launch_rope_cache(const RopeCache& a, hipStream_t stream);
 
+// Norms and gated activations (residual == nullptr: plain RMSNorm).
+int launch_rms_norm(void* out, void* residual, const void* x, const void* w, int rows, int hidden, float eps,
+                    int dtype, hipStream_t stream);
+int launch_layer_norm(void* out, const void* x, const void* w, const void* b, int rows, int hidden, float eps,
+                      int dtype, hipStream_t stream);
+int launch_act_and_mul(void* out, const void* gate, const void* up, int64_t n, int act, int dtype,
+                       hipStream_t stream);
+
 // VQ codec.  Encode / assign: the nearest codebook entry of each fp16
 // vector, as uint16 (idx16) or int32 (idx32).
 constexpr int kVqMaxDim = 256;

@@ -78,6 +78,41 @@ void swap_blocks(TrueBuffer& kv_cache, TrueBuffer& host_cache, const TrueBuffer&
                                        direction, stream));
 }
 
+void rms_norm(TrueBuffer& out, const TrueBuffer& x, const TrueBuffer& weight, float eps, hipStream_t stream) {
+  report("rms_norm", tl_rms_norm(out.data, x.data, weight.data, dim(x, 0), dim(x, 1), eps, tl_dtype_of(x), stream));
+}
+
+void fused_add_rms_norm(TrueBuffer& out, TrueBuffer& residual, const TrueBuffer& x, const TrueBuffer& weight,
+                        float eps, hipStream_t stream) {
+  report("fused_add_rms_norm", tl_fused_add_rms_norm(out.data, residual.data, x.data, weight.data, dim(x, 0),
+                                                     dim(x, 1), eps, tl_dtype_of(x), stream));
+}
+
+void layer_norm(TrueBuffer& out, const TrueBuffer& x, const TrueBuffer& weight, const TrueBuffer& bias, float eps,
+                hipStream_t stream) {
+  report("layer_norm", tl_layer_norm(out.data, x.data, weight.data, bias.data, dim(x, 0), dim(x, 1), eps,
+                                     tl_dtype_of(x), stream));
+}
+
+static void act_and_mul(const char* name, TrueBuffer& out, const TrueBuffer& gate, const TrueBuffer& up, int act,
+                        hipStream_t stream) {
+  int64_t n = 1;
+  for (int i = 0; i < gate.ndim && i < 4; ++i) n *= gate.shape[i];
+  report(name, tl_act_and_mul(out.data, gate.data, up.data, n, act, tl_dtype_of(gate), stream));
+}
+
+void silu_and_mul(TrueBuffer& out, const TrueBuffer& gate, const TrueBuffer& up, hipStream_t stream) {
+  act_and_mul("silu_and_mul", out, gate, up, TL_ACT_SILU, stream);
+}
+
+void gelu_and_mul(TrueBuffer& out, const TrueBuffer& gate, const TrueBuffer& up, hipStream_t stream) {
+  act_and_mul("gelu_and_mul", out, gate, up, TL_ACT_GELU, stream);
+}
+
+void gelu_tanh_and_mul(TrueBuffer& out, const TrueBuffer& gate, const TrueBuffer& up, hipStream_t stream) {
+  act_and_mul("gelu_tanh_and_mul", out, gate, up, TL_ACT_GELU_TANH, stream);
+}
+
 void paged_attention_v1(TrueBuffer& out, const TrueBuffer& q, const TrueBuffer& k_cache,
                         const TrueBuffer& v_cache, const TrueBuffer& block_tables,
                         const TrueBuffer& seq_lens, int num_kv_heads, float scale, int head_size,

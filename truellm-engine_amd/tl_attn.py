@@ -108,6 +108,10 @@ _SIG = {
     "tl_reshape_and_cache": (ctypes.c_int, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P]),
     "tl_reshape_and_cache_fp8": (ctypes.c_int, [_P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _I, _F, _F, _P]),
     "tl_rope_reshape_and_cache": (ctypes.c_int, [_P] * 10 + [_I] * 9 + [_P]),
+    "tl_rms_norm": (ctypes.c_int, [_P, _P, _P, _I, _I, _F, _I, _P]),
+    "tl_fused_add_rms_norm": (ctypes.c_int, [_P, _P, _P, _P, _I, _I, _F, _I, _P]),
+    "tl_layer_norm": (ctypes.c_int, [_P, _P, _P, _P, _I, _I, _F, _I, _P]),
+    "tl_act_and_mul": (ctypes.c_int, [_P, _P, _P, ctypes.c_int64, _I, _I, _P]),
     "tl_vq_encode": (ctypes.c_int, [_P, _P, _P, _I, _I, _I, _P]),
     "tl_vq_decode": (ctypes.c_int, [_P, _P, _P, _I, _I, _I, _P]),
     "tl_vq_kmeans_workspace_bytes": (ctypes.c_size_t, [_I, _I, _I]),
@@ -258,6 +262,31 @@ def reshape_and_cache_split(key, value, k_cache, v_cache, slot_mapping, stream=N
     check(lib.tl_reshape_and_cache(
         _ptr(key), _ptr(value), _ptr(k_cache), _ptr(v_cache), _ptr(slot_mapping), T, n_kv, D,
         k_cache.shape[3], k_cache.shape[0], dtype_code(key), _stream(stream)))
+
+
+ACT_SILU, ACT_GELU, ACT_GELU_TANH = 0, 1, 2
+
+
+def rms_norm(out, x, weight, eps, stream=None):
+    """layernorm_kernels.cu:149: x / out [T, H]."""
+    check(lib.tl_rms_norm(_ptr(out), _ptr(x), _ptr(weight), x.shape[0], x.shape[1], eps, dtype_code(x),
+                          _stream(stream)))
+
+
+def fused_add_rms_norm(out, residual, x, weight, eps, stream=None):
+    check(lib.tl_fused_add_rms_norm(_ptr(out), _ptr(residual), _ptr(x), _ptr(weight), x.shape[0], x.shape[1], eps,
+                                    dtype_code(x), _stream(stream)))
+
+
+def layer_norm(out, x, weight, bias, eps, stream=None):
+    check(lib.tl_layer_norm(_ptr(out), _ptr(x), _ptr(weight), _ptr(bias), x.shape[0], x.shape[1], eps,
+                            dtype_code(x), _stream(stream)))
+
+
+def act_and_mul(out, gate, up, activation=ACT_SILU, stream=None):
+    """activation_kernels.cu:57: out = act(gate) * up, elementwise."""
+    check(lib.tl_act_and_mul(_ptr(out), _ptr(gate), _ptr(up), gate.numel(), activation, dtype_code(gate),
+                             _stream(stream)))
 
 
 def vq_encode(kv, book, idx, stream=None):
