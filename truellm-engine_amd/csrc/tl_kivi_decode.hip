@@ -233,10 +233,12 @@ __device__ __forceinline__ void page_pair(PageState& st, const PageRaw& ra, cons
 // loads in flight while a pair is computed (two register sets, alternating).
 // The pair's parameters go through the wavefront's 2 KiB LDS slot s_par_w
 // (page a at 0, page b at 256 dwords; K params first, V params at 128).
+// share_simd: raise the wavefront's priority on every other page pair (see
+// kivi_decode_kernel).
 __device__ __forceinline__ void kivi_pages_wave(const KiviParams& k, int seq, int kvh, int hs,
                                                 int pg_begin, int pg_end, int pg_step,
                                                 uint32_t* s_par_w, float* s_acc_w, float* s_m_w,
-                                                float* s_l_w) {
+                                                float* s_l_w, bool share_simd) {
   constexpr int GT = kWaveHeads;
   const Params& p = k.base;
   const int lane = threadIdx.x % kWave;
@@ -297,9 +299,11 @@ __device__ __forceinline__ void kivi_pages_wave(const KiviParams& k, int seq, in
 #pragma unroll 1
     for (int o = 0; o < cn; o += 4) {
       load(r1a, r1b, id(o + 2), id(o + 3));
+      if (share_simd) __builtin_amdgcn_s_setprio(1);
       page_pair(st, r0a, r0b, id(o) >= 0, id(o + 1) >= 0, qsc, qss, s_par_w, lane, slot_scale);
       if (o + 2 >= cn) break;
       load(r0a, r0b, id(o + 4), id(o + 5));
+      if (share_simd) __builtin_amdgcn_s_setprio(0);
       page_pair(st, r1a, r1b, id(o + 2) >= 0, id(o + 3) >= 0, qsc, qss, s_par_w, lane, slot_scale);
     }
   }
@@ -502,8 +506,14 @@ __global__ __launch_bounds__(NW * kWave, 2) void kivi_decode_kernel(KiviParams k
     if (last && !has_res && wave == 0) store_newest(k.job, newest_from_row(k.job, seq, kvh, tid), seq, kvh, tid);
   }
   if (wave < page_waves) {
+    // Single pass runs two workgroups per CU, b and b + grid/2 (dispatch
+    // order), and the SIMDs issue the oldest wavefront first: left alone
+    // workgroup b finishes about 10 us before b + grid/2 (48.5 against 59.4
+    // us at batch 64).  The second half's page wavefronts take the higher
+    // priority on every other page pair, so both progress together (55.5
+    // and 58.5 us).
     kivi_pages_wave(k, seq, kvh, hs, pg0 + wave, pg1, page_waves, &sd.p[wave][0], &sd.acc[wave][0][0],
-                    &sd.m[wave][0], &sd.l[wave][0]);
+                    &sd.m[wave][0], &sd.l[wave][0], FINAL && blockIdx.x >= gridDim.x / 2);
   } else {
     const int lane = tid % kWave;
     NewestToken nt;
