@@ -234,11 +234,13 @@ __device__ __forceinline__ void page_pair(PageState& st, const PageRaw& ra, cons
 // The pair's parameters go through the wavefront's 2 KiB LDS slot s_par_w
 // (page a at 0, page b at 256 dwords; K params first, V params at 128).
 // share_simd: raise the wavefront's priority on every other page pair (see
-// kivi_decode_kernel).
+// kivi_decode_kernel).  early_ok: early_id is the table entry of page
+// pg_begin + lane * pg_step, read by the caller ahead of time (unchecked;
+// pages at or past pg_end and ids outside the pool are dropped here).
 __device__ __forceinline__ void kivi_pages_wave(const KiviParams& k, int seq, int kvh, int hs,
                                                 int pg_begin, int pg_end, int pg_step,
                                                 uint32_t* s_par_w, float* s_acc_w, float* s_m_w,
-                                                float* s_l_w, bool share_simd) {
+                                                float* s_l_w, bool share_simd, bool early_ok, int early_id) {
   constexpr int GT = kWaveHeads;
   const Params& p = k.base;
   const int lane = threadIdx.x % kWave;
@@ -293,16 +295,24 @@ __device__ __forceinline__ void kivi_pages_wave(const KiviParams& k, int seq, in
 #pragma unroll 1
   for (int c0 = 0; c0 < n_mine; c0 += kWave) {
     const int cn = min(kWave, n_mine - c0);
-    const int idv = page_id(k, ptab, pg_begin + (c0 + lane) * pg_step, pg_end);
+    int idv;
+    if (c0 == 0 && early_ok) {
+      const bool in = pg_begin + lane * pg_step < pg_end && early_id >= 0 && early_id < k.num_pages;
+      idv = in ? early_id : -1;
+    } else {
+      idv = page_id(k, ptab, pg_begin + (c0 + lane) * pg_step, pg_end);
+    }
     auto id = [&](int o) { return o < cn ? __builtin_amdgcn_readlane(idv, o) : -1; };
-    load(r0a, r0b, id(0), id(1));
+    // the loads of pages o and o + 1
+    auto fetch = [&](PageRaw& ra, PageRaw& rb, int o) { load(ra, rb, id(o), id(o + 1)); };
+    fetch(r0a, r0b, 0);
 #pragma unroll 1
     for (int o = 0; o < cn; o += 4) {
-      load(r1a, r1b, id(o + 2), id(o + 3));
+      fetch(r1a, r1b, o + 2);
       if (share_simd) __builtin_amdgcn_s_setprio(1);
       page_pair(st, r0a, r0b, id(o) >= 0, id(o + 1) >= 0, qsc, qss, s_par_w, lane, slot_scale);
       if (o + 2 >= cn) break;
-      load(r0a, r0b, id(o + 4), id(o + 5));
+      fetch(r0a, r0b, o + 4);
       if (share_simd) __builtin_amdgcn_s_setprio(0);
       page_pair(st, r1a, r1b, id(o + 2) >= 0, id(o + 3) >= 0, qsc, qss, s_par_w, lane, slot_scale);
     }
@@ -486,6 +496,15 @@ __global__ __launch_bounds__(NW * kWave, 2) void kivi_decode_kernel(KiviParams k
   const int hs = bid % p.head_slices;      bid /= p.head_slices;
   const int kvh = bid % p.num_kv_heads;
   const int seq = bid / p.num_kv_heads;
+  // Single pass: the page table entries of this wavefront's first 64 pages
+  // are read before L is known, for the usual split (NW - 1 page
+  // wavefronts, the last one on the window), so the first page loads wait
+  // for one memory round trip instead of two.
+  int early_id = -1;
+  if constexpr (FINAL) {
+    const int pg = wave + (tid % kWave) * (NW - 1);
+    if (pg < k.max_pages_per_seq) early_id = k.page_tables[(int64_t)seq * k.max_pages_per_seq + pg];
+  }
   const int L = p.seq_lens[seq];
   const int lq = kivi_quantized_len(L, k.residual_length);
   const int n_pages = min(lq / kKiviPageTokens, k.max_pages_per_seq);
@@ -497,6 +516,11 @@ __global__ __launch_bounds__(NW * kWave, 2) void kivi_decode_kernel(KiviParams k
   const bool has_res = last && L > lq;
   const int page_waves = has_res ? NW - 1 : NW;
 
+  // The page that L completes, if any (APPEND), by the whole workgroup
+  // before the page wavefronts start.  (Built by the residual wavefront
+  // alone, overlapped with the page wavefronts, the step was 0.2 us slower
+  // on average: one wavefront takes far longer over the build and then
+  // ends after the page wavefronts.)
   if constexpr (APPEND) {
     if (last && lq > 0 && lq != kivi_quantized_len(L - 1, k.residual_length)) {
       kivi_build_page<NW * kWave>(*reinterpret_cast<KiviBuildSmem*>(s_raw), k.job, seq, kvh,
@@ -513,7 +537,8 @@ __global__ __launch_bounds__(NW * kWave, 2) void kivi_decode_kernel(KiviParams k
     // priority on every other page pair, so both progress together (55.5
     // and 58.5 us).
     kivi_pages_wave(k, seq, kvh, hs, pg0 + wave, pg1, page_waves, &sd.p[wave][0], &sd.acc[wave][0][0],
-                    &sd.m[wave][0], &sd.l[wave][0], FINAL && blockIdx.x >= gridDim.x / 2);
+                    &sd.m[wave][0], &sd.l[wave][0], FINAL && blockIdx.x >= gridDim.x / 2,
+                    FINAL && page_waves == NW - 1, early_id);
   } else {
     const int lane = tid % kWave;
     NewestToken nt;

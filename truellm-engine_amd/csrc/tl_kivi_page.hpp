@@ -126,14 +126,63 @@ __device__ __forceinline__ void kivi_append_token(const PageJob& j, int seq, int
   }
 }
 
+// Orders the LDS accesses of the NT threads of a page build: a workgroup
+// barrier, or, when one wavefront builds, a wavefront barrier.
+template <int NT>
+__device__ __forceinline__ void build_barrier() {
+  if constexpr (NT == kWave) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  } else {
+    __syncthreads();
+  }
+}
+
+// The group quantiser over unit u of a page: u < 128 is K channel u (its 32
+// tokens in order), u >= 128 is V (token, group of 32 channels) u - 128
+// (channels in order).  Nibbles go to qk / qv, step and zero to the page.
+__device__ __forceinline__ void quantise_unit(KiviBuildSmem& sm, int u) {
+  constexpr int T = kKiviPageTokens, D = kKiviHead;
+  if (u < D) {
+    const int c = u;
+    float gmin = FLT_MAX, gmax = -FLT_MAX;
+    for (int t = 0; t < T; ++t) {
+      const float x = f16_to_f32(sm.k[c][t]);
+      if (x < gmin) gmin = x;
+      if (x > gmax) gmax = x;
+    }
+    const GroupQ q = group_params(gmin, gmax);
+    for (int t = 0; t < T; ++t) sm.qk[c][t] = (uint8_t)quantise(f16_to_f32(sm.k[c][t]), q);
+    uint16_t* kp = reinterpret_cast<uint16_t*>(sm.page + kKiviKParamOff + (c / 8) * 32);
+    kp[c % 8] = q.step;
+    kp[8 + c % 8] = q.zero;
+  } else {
+    const int t = (u - D) / 4, g = (u - D) % 4;
+    float gmin = FLT_MAX, gmax = -FLT_MAX;
+    for (int i = 0; i < 32; ++i) {
+      const float x = f16_to_f32(sm.v[t][g * 32 + i]);
+      if (x < gmin) gmin = x;
+      if (x > gmax) gmax = x;
+    }
+    const GroupQ q = group_params(gmin, gmax);
+    for (int i = 0; i < 32; ++i) sm.qv[t][g * 32 + i] = (uint8_t)quantise(f16_to_f32(sm.v[t][g * 32 + i]), q);
+    const int r = kivi_v_group(t), s = kivi_v_slot(t);
+    uint16_t* vp = reinterpret_cast<uint16_t*>(sm.page + kKiviVParamOff + (g * 4 + r) * 32);
+    vp[s] = q.step;
+    vp[8 + s] = q.zero;
+  }
+}
+
 // Quantise page `page` of (seq, kvh) from the fp16 pool and write it to its
-// slot of the page pool.  Called by all NT (>= 128) threads of a workgroup
-// (it synchronises them, and the caller synchronises them again before it
-// reuses the LDS); with j.append the token at position L - 1 is taken from
-// the input row.
+// slot of the page pool.  Called by NT threads (a multiple of the
+// wavefront: all of a workgroup's, or one wavefront's), which it
+// synchronises; the caller synchronises them again before it reuses the
+// LDS.  With j.append the token at position L - 1 is taken from the input
+// row.
 template <int NT>
 __device__ void kivi_build_page(KiviBuildSmem& sm, const PageJob& j, int seq, int kvh, int page, int L, int tid) {
-  static_assert(NT >= 128, "one thread per channel");
+  static_assert(NT % kWave == 0, "whole wavefronts");
   constexpr int T = kKiviPageTokens, D = kKiviHead;
   if (page >= j.max_pages_per_seq) return;
   const int pid = j.page_tables[(int64_t)seq * j.max_pages_per_seq + page];
@@ -201,57 +250,10 @@ __device__ void kivi_build_page(KiviBuildSmem& sm, const PageJob& j, int seq, in
       sm.v[t][c] = vv;
     }
   }
-  __syncthreads();
+  build_barrier<NT>();
 
-  if (tid < D) {
-    // K: one thread per channel, its 32 tokens in order
-    const int c = tid;
-    float gmin = FLT_MAX, gmax = -FLT_MAX;
-    for (int t = 0; t < T; ++t) {
-      const float x = f16_to_f32(sm.k[c][t]);
-      if (x < gmin) gmin = x;
-      if (x > gmax) gmax = x;
-    }
-    const GroupQ q = group_params(gmin, gmax);
-    for (int t = 0; t < T; ++t) sm.qk[c][t] = (uint8_t)quantise(f16_to_f32(sm.k[c][t]), q);
-    uint16_t* kp = reinterpret_cast<uint16_t*>(sm.page + kKiviKParamOff + (c / 8) * 32);
-    kp[c % 8] = q.step;
-    kp[8 + c % 8] = q.zero;
-  } else if (tid < 2 * D) {
-    // V: one thread per (token, group of 32 channels), channels in order
-    const int t = (tid - D) / 4, g = (tid - D) % 4;
-    float gmin = FLT_MAX, gmax = -FLT_MAX;
-    for (int i = 0; i < 32; ++i) {
-      const float x = f16_to_f32(sm.v[t][g * 32 + i]);
-      if (x < gmin) gmin = x;
-      if (x > gmax) gmax = x;
-    }
-    const GroupQ q = group_params(gmin, gmax);
-    for (int i = 0; i < 32; ++i) sm.qv[t][g * 32 + i] = (uint8_t)quantise(f16_to_f32(sm.v[t][g * 32 + i]), q);
-    const int r = kivi_v_group(t), s = kivi_v_slot(t);
-    uint16_t* vp = reinterpret_cast<uint16_t*>(sm.page + kKiviVParamOff + (g * 4 + r) * 32);
-    vp[s] = q.step;
-    vp[8 + s] = q.zero;
-  }
-  if (NT < 2 * D) {
-    // with fewer threads the V groups follow the K channels
-    const int t = tid / 4, g = tid % 4;
-    if (tid < D) {
-      float gmin = FLT_MAX, gmax = -FLT_MAX;
-      for (int i = 0; i < 32; ++i) {
-        const float x = f16_to_f32(sm.v[t][g * 32 + i]);
-        if (x < gmin) gmin = x;
-        if (x > gmax) gmax = x;
-      }
-      const GroupQ q = group_params(gmin, gmax);
-      for (int i = 0; i < 32; ++i) sm.qv[t][g * 32 + i] = (uint8_t)quantise(f16_to_f32(sm.v[t][g * 32 + i]), q);
-      const int r = kivi_v_group(t), s = kivi_v_slot(t);
-      uint16_t* vp = reinterpret_cast<uint16_t*>(sm.page + kKiviVParamOff + (g * 4 + r) * 32);
-      vp[s] = q.step;
-      vp[8 + s] = q.zero;
-    }
-  }
-  __syncthreads();
+  for (int u = tid; u < 2 * D; u += NT) quantise_unit(sm, u);
+  build_barrier<NT>();
 
   // nibble dwords: 512 for K then 512 for V
   uint32_t* pw = reinterpret_cast<uint32_t*>(sm.page);
@@ -275,7 +277,7 @@ __device__ void kivi_build_page(KiviBuildSmem& sm, const PageJob& j, int seq, in
       y |= (uint32_t)sm.qv[kivi_v_token(r, s)][d] << (16 * (s & 1) + 4 * (s >> 1));
     pw[kKiviVNibOff / 4 + w] = y;
   }
-  __syncthreads();
+  build_barrier<NT>();
 
   uint8_t* dst = j.pages + ((int64_t)pid * j.num_kv_heads + kvh) * kKiviPageBytes;
   for (int i = tid; i < kKiviPageBytes / 16; i += NT)
