@@ -128,6 +128,19 @@ __device__ __forceinline__ u32x4 load16_stream(const void* p) {
   return u32x4{v.x, v.y, v.z, v.w};
 }
 
+// Loads through a buffer descriptor built in scalar registers: base and
+// byte range are wave-uniform, offsets per lane, and the hardware returns
+// zeros without a memory request for offsets at or past the range (an
+// empty range: a load that may be issued unconditionally).  Word 3 is the
+// raw-buffer format of CDNA; aux 2 = non-temporal.
+constexpr int kBufferWord3 = 0x00020000;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, unsigned bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, kBufferWord3);
+}
+__device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t r, unsigned off) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 2));
+}
+
 // ---- wavefront reductions ----------------------------------------------------
 __device__ __forceinline__ float shfl_xor(float v, int mask) {
   return __shfl_xor(v, mask, kWave);

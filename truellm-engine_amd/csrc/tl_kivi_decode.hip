@@ -80,21 +80,16 @@ struct PageRaw {
   u32x4 kn[2], vn[2], par;
 };
 
-// One page through a buffer descriptor built in scalar registers (base =
-// the page, 5120 bytes in range, so the hardware also bounds every access)
-// and per-lane 32-bit offsets: the loads need no per-lane address registers.
-// aux 2 = non-temporal (the page is read once per decode step).
-constexpr int kBufferWord3 = 0x00020000;   // raw buffer, CDNA dword 3
-__device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t r, unsigned off) {
-  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 2));
-}
-// A page that is not there (a hole, or a prefetch past the wavefront's last
-// page) gets an empty range: its loads return zeros without a memory request,
-// while the number of loads per iteration stays fixed.
+// One page through a buffer descriptor (base = the page, 5120 bytes in
+// range, so the hardware also bounds every access) and per-lane 32-bit
+// offsets: the loads need no per-lane address registers; non-temporal (the
+// page is read once per decode step).  A page that is not there (a hole,
+// or a prefetch past the wavefront's last page) gets an empty range: its
+// loads return zeros without a memory request, while the number of loads
+// per iteration stays fixed.
 __device__ __forceinline__ void load_page(PageRaw& r, const uint8_t* page, bool there, unsigned off,
                                           unsigned par_off) {
-  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint8_t*>(page), (short)0, there ? kKiviPageBytes : 0, kBufferWord3);
+  const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(page, there ? kKiviPageBytes : 0);
   r.kn[0] = buffer_load16(rs, off);
   r.kn[1] = buffer_load16(rs, 1024u + off);
   r.vn[0] = buffer_load16(rs, unsigned(kKiviVNibOff) + off);

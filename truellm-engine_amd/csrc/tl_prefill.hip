@@ -119,8 +119,14 @@ struct PrefillSmem {
   } pf;
 };
 
+// A block-table row read through the constant address space: the table is
+// not written during the kernel, and with a wave-uniform index the reads
+// are scalar loads, which are waited for on their own counter instead of
+// behind every K/V load in flight.
+typedef const __attribute__((address_space(4))) int32_t* TableRow;
+
 // Physical block of block index lb of a table row, or -1.
-__device__ __forceinline__ int block_of(const Params& p, const int32_t* table, int lb) {
+__device__ __forceinline__ int block_of(const Params& p, TableRow table, int lb) {
   if (lb >= p.max_blocks_per_seq) return -1;
   const int b = table[lb];
   return (b < 0 || b >= p.num_blocks) ? -1 : b;
@@ -169,9 +175,14 @@ __global__ __launch_bounds__(NW * kWave) void prefill_kernel(PrefillParams pp) {
         ((int64_t)(q0 + qi) * p.num_heads + head_of(p, kvh, gi)) * kPfHead + 8 * g;
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) qb[ks] = row_ok ? load16(qrow + 16 * ks) : u32x4{0u, 0u, 0u, 0u};
+    // q is waited for here, on every path: otherwise the loop's first use
+    // of it waits for every load in flight, the K/V loads of later
+    // iterations included
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) asm volatile("" ::"v"(qb[ks].x), "v"(qb[ks].y), "v"(qb[ks].z), "v"(qb[ks].w));
   }
 
-  const int32_t* table = p.block_tables + (int64_t)seq * p.max_blocks_per_seq;
+  const TableRow table = (TableRow)(p.block_tables + (int64_t)seq * p.max_blocks_per_seq);
   const int64_t head_stride = (int64_t)kPfHead * BS;                  // elements per (block, kv head)
   const uint16_t* kpool = (const uint16_t*)p.k_cache;
   const uint16_t* vpool = (const uint16_t*)p.v_cache;
@@ -185,30 +196,24 @@ __global__ __launch_bounds__(NW * kWave) void prefill_kernel(PrefillParams pp) {
   constexpr int RPW = 2 * (kPfKeys / 8) / NW;          // runs per wavefront
   static_assert(RPW * NW == 2 * (kPfKeys / 8), "runs x channel halves per wavefront");
   const int k_ch = 2 * lane + (wave & 1), v_ch = lane + 64 * (wave & 1);
-  struct Fetched { u32x4 k[RPW], v[RPW]; };
+  // nv: keys of the run that exist (the rest of its V is zeroed when staged,
+  // so that the loads are waited for only there)
+  struct Fetched { u32x4 k[RPW], v[RPW]; int nv[RPW]; };
   auto run_key = [&](int j) { return 8 * ((wave >> 1) + (NW / 2) * j); };   // first key of run j
   auto fetch = [&](int it, Fetched& f) {
 #pragma unroll
     for (int j = 0; j < RPW; ++j) {
       const int kb = run_key(j);
       const int key0 = it * kPfKeys + kb;
-      const int pb = key0 < kend ? block_of(p, table, it * BPI + kb / BS) : -1;
-      if (pb >= 0) {
-        const int64_t base = ((int64_t)pb * p.num_kv_heads + kvh) * head_stride + kb % BS;
-        f.k[j] = load16_stream(kpool + base + (int64_t)k_ch * BS);
-        u4v v = __builtin_bit_cast(u4v, load16_stream(vpool + base + (int64_t)v_ch * BS));
-        // slots at or past the sequence end may hold anything: zero their V
-        if (key0 + 8 > L) {
-#pragma unroll
-          for (int w = 0; w < 4; ++w)
-            if (key0 + 2 * w >= L) v[w] = 0u;
-            else if (key0 + 2 * w + 1 >= L) v[w] &= 0xFFFFu;
-        }
-        f.v[j] = __builtin_bit_cast(u32x4, v);
-      } else {
-        f.k[j] = u32x4{0u, 0u, 0u, 0u};
-        f.v[j] = u32x4{0u, 0u, 0u, 0u};
-      }
+      // wave-uniform (the descriptor is built in scalar registers)
+      const int pb = __builtin_amdgcn_readfirstlane(key0 < kend ? block_of(p, table, it * BPI + kb / BS) : -1);
+      f.nv[j] = pb >= 0 ? min(max(L - key0, 0), 8) : 0;
+      // unconditional loads (a missing block has an empty range and reads
+      // zeros): no branch, so nothing waits for them before the staging
+      const int64_t row = pb >= 0 ? ((int64_t)pb * p.num_kv_heads + kvh) * head_stride : 0;
+      const unsigned bytes = pb >= 0 ? unsigned(head_stride * 2) : 0u;
+      f.k[j] = buffer_load16(buffer_rsrc(kpool + row, bytes), unsigned(2 * (k_ch * BS + kb % BS)));
+      f.v[j] = buffer_load16(buffer_rsrc(vpool + row, bytes), unsigned(2 * (v_ch * BS + kb % BS)));
     }
   };
   auto stage = [&](int st, const Fetched& f) {
@@ -222,9 +227,17 @@ __global__ __launch_bounds__(NW * kWave) void prefill_kernel(PrefillParams pp) {
         kt[(2 * w) * kKtStride] = (uint16_t)(kv[w] & 0xFFFFu);
         kt[(2 * w + 1) * kKtStride] = (uint16_t)(kv[w] >> 16);
       }
+      // V slots at or past the sequence end may hold anything (NaN codes
+      // too, and a zero weight times NaN is NaN): zero them
+      u4v v = __builtin_bit_cast(u4v, f.v[j]);
+      const int nv = f.nv[j];
+      if (nv < 8) {
+#pragma unroll
+        for (int w = 0; w < 4; ++w) v[w] = 2 * w >= nv ? 0u : (2 * w + 1 >= nv ? v[w] & 0xFFFFu : v[w]);
+      }
       uint16_t* vrow = &sm.pf.v[st][v_ch * kVStride];
-      *reinterpret_cast<uint2*>(vrow + v_slot(kb)) = uint2{f.v[j].x, f.v[j].y};
-      *reinterpret_cast<uint2*>(vrow + v_slot(kb + 4)) = uint2{f.v[j].z, f.v[j].w};
+      *reinterpret_cast<uint2*>(vrow + v_slot(kb)) = uint2{v[0], v[1]};
+      *reinterpret_cast<uint2*>(vrow + v_slot(kb + 4)) = uint2{v[2], v[3]};
     }
   };
 
@@ -346,27 +359,28 @@ __global__ __launch_bounds__(NW * kWave) void prefill_kernel(PrefillParams pp) {
     }
   };
 
+  // Fetches and stages run unconditionally: past the last iteration the
+  // blocks are missing (empty ranges, zeros), and a stage that no
+  // iteration reads takes them.  A conditional fetch would leave the loop's
+  // waits for one stage's loads unable to tell how many newer loads are in
+  // flight, and they would wait for all of them.
   Fetched fs0, fs1;
   f16v sa0[KT], sa1[KT];
-  if (n_it > 0) {
-    fetch(0, fs0);
-    stage(0, fs0);
-  }
-  if (n_it > 1) {
-    fetch(1, fs1);
-    stage(1, fs1);
-  }
-  if (n_it > 2) fetch(2, fs0);
+  fetch(0, fs0);
+  stage(0, fs0);
+  fetch(1, fs1);
+  stage(1, fs1);
+  fetch(2, fs0);
   __syncthreads();
-  if (n_it > 0) qk(0, sa0);
+  qk(0, sa0);
   // f_stage holds it + 2 (staged at the end of it), f_free receives it + 3;
   // s_cur holds the scores of it, s_next receives those of it + 1
   auto iteration = [&](int it, Fetched& f_stage, Fetched& f_free, f16v (&s_cur)[KT], f16v (&s_next)[KT]) {
-    if (it + 3 < n_it) fetch(it + 3, f_free);
+    fetch(it + 3, f_free);
     const float m_use = prepare(it, s_cur);
     qk(it + 1, s_next);
     exp_pv(it, s_cur, m_use);
-    if (it + 2 < n_it) stage((it + 2) % kStages, f_stage);
+    stage((it + 2) % kStages, f_stage);
     __syncthreads();
   };
 #pragma unroll 1
