@@ -129,7 +129,12 @@ def timed(step, steps, warmup):
     return e0.elapsed_time(e1) / steps
 
 
-def bench_decode(args, dtype):
+def bench_decode(args, dtype, append=False):
+    """Single-pass (or split-K with --partition-tokens) decode at batch 64,
+    ctx 4096.  With append, every step first writes each sequence's newest
+    token (position ctx - 1) into the pool with reshape_and_cache, as an
+    engine's decode step does before attention: the fp16 counterpart of the
+    KIVI step, whose append is fused into its launch."""
     import torch
 
     import tl_attn as tla
@@ -151,8 +156,16 @@ def bench_decode(args, dtype):
                                 gqa_map=tla.GQA_GROUPED, partition_tokens=args.partition_tokens)
     ws = torch.empty(max(16, tla.workspace_bytes(desc, CTX)), dtype=torch.uint8, device="cuda")
 
+    if append:
+        knew = torch.randn(S, NKV, D, generator=g, device="cuda", dtype=tdt)
+        vnew = torch.randn(S, NKV, D, generator=g, device="cuda", dtype=tdt)
+        pos = CTX - 1
+        slots = [(tables[:, pos // BS] * BS + pos % BS).to(torch.int32).contiguous() for _k, _v, tables in pools]
+
     def step(i, stream):
         k, v, tables = pools[i % 2]
+        if append:
+            tla.reshape_and_cache_split(knew, vnew, k, v, slots[i % 2], stream)
         tla.paged_attention_decode(desc, out, q, k, v, tables, sl, CTX, ws, stream)
 
     ms = timed(step, args.steps, args.warmup)
@@ -531,6 +544,7 @@ def main():
         fp = bench_decode(args, "fp16")
     if args.only in ("all", "kivi"):
         kv = bench_kivi(args)
+    fpa = bench_decode(args, "fp16", append=True) if args.only in ("all", "kivi") else None
     f8 = bench_fp8(args) if args.only in ("all", "fp8") else None
     pf = bench_prefill(args) if args.only in ("all", "prefill") else None
     cb = bench_copy_blocks(args) if args.only in ("all", "blocks") else None
@@ -580,6 +594,12 @@ def main():
                                         "fp16 window through its whole 128..159-token cycle"}
         if fp is not None:
             res["kivi_int4"]["speedup_vs_fp16_tok_s"] = round(kv["tok_s"] / fp["tok_s"], 3)
+        if fpa is not None:
+            # like for like: the fp16 step with its append (reshape_and_cache,
+            # then decode), as the KIVI step holds its own
+            res["fp16_with_append"] = {"ms_per_step": round(fpa["ms_per_step"], 5),
+                                       "tok_s": round(fpa["tok_s"], 1)}
+            res["kivi_int4"]["speedup_vs_fp16_step_with_append"] = round(kv["tok_s"] / fpa["tok_s"], 3)
     if f8 is not None:
         res["fp8_e4m3_long_context"] = {
             "workload": "decode, batch 16, ctx 32768, 32 q / 8 kv heads, d 128, FP8 E4M3 KV with per-tensor "

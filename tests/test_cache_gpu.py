@@ -37,6 +37,32 @@ def test_reshape_and_cache_bit_exact(code, T, n_kv, D, BS):
     assert np.array_equal(host_bits(vcd), vc)
 
 
+@pytest.mark.parametrize("code", [orc.F16, orc.BF16, orc.F32])
+@pytest.mark.parametrize("T,n_kv,D,BS", [(64, 8, 128, 16), (33, 2, 64, 32), (256, 4, 128, 16), (300, 2, 128, 16)])
+def test_reshape_and_cache_decode_append_bit_exact(code, T, n_kv, D, BS):
+    """One token per block (a decode step's append: the whole-row path for
+    up to 256 tokens, element stores past that), over a pool of random
+    bytes that every other slot must keep; a few tokens share a block or
+    are padded."""
+    N = 2 * T + 8
+    rng = np.random.default_rng(T + D)
+    blocks = rng.permutation(N)[:T]
+    slots = (blocks * BS + rng.integers(0, BS, size=T)).astype(np.int32)
+    slots[7] = slots[3] - slots[3] % BS + (slots[3] % BS + 1) % BS   # token 7 shares token 3's block
+    slots[11] = -1
+    key = inputs.encode(rng.standard_normal((T, n_kv, D), dtype=np.float32), code)
+    val = inputs.encode(rng.standard_normal((T, n_kv, D), dtype=np.float32), code)
+    kc = inputs.encode(rng.standard_normal((N, n_kv, D, BS), dtype=np.float32), code)
+    vc = inputs.encode(rng.standard_normal((N, n_kv, D, BS), dtype=np.float32), code)
+    kd, vd, kcd, vcd = dev(key, code), dev(val, code), dev(kc, code), dev(vc, code)
+    print(f"case reshape append code={code} T={T} D={D} BS={BS}", flush=True)
+    tla.reshape_and_cache_split(kd, vd, kcd, vcd, dev(slots))
+    torch.cuda.synchronize()
+    orc.reshape_and_cache(key, val, kc, vc, slots)
+    assert np.array_equal(host_bits(kcd), kc)
+    assert np.array_equal(host_bits(vcd), vc)
+
+
 def test_reshape_and_cache_reference_layout_and_out_of_pool_slots():
     """kv_cache [2N, n_kv, D, BS] = K pool then V pool (cache_kernels.cu:27-33);
     slots past the pool are skipped instead of written out of bounds."""

@@ -80,6 +80,85 @@ __global__ __launch_bounds__(256) void reshape_copy_kernel(
   }
 }
 
+// Decode appends: few tokens, each in a block that no other token of the
+// call writes.  HBM3E has no byte masks, so the element stores of
+// reshape_copy_kernel (one token's D elements lie BS elements apart) leave
+// partly written lines whose write-back is a read-modify-write of a memory
+// burst each: 17 us for one token of each of 64 sequences (8 kv heads,
+// d 128, bs 16).  Here a wavefront per (token, kv head) reads the block's
+// row of that kv head (D x BS elements, 4 KiB for f16 at bs 16), replaces
+// the token's slot and writes the row back whole.  The other slots are
+// rewritten with their own bytes, so the block must have no other writer
+// during the call (a block that a sequence appends to belongs to that
+// sequence); a token whose block another token of this call also writes
+// is stored element by element instead.
+template <int E> struct Elem;
+template <> struct Elem<2> { typedef uint16_t T; };
+template <> struct Elem<4> { typedef uint32_t T; };
+
+// Replace element e (PER = 16 / E per chunk) of a 16-byte chunk.
+template <int E>
+__device__ __forceinline__ void put_elem(u32x4& c, int e, uint32_t v) {
+  constexpr int PER = 16 / E;
+  const int w = e / (PER / 4);
+  const uint32_t sh = E == 2 ? 16u * (e & 1) : 0u;
+  const uint32_t keep = E == 2 ? ~(0xFFFFu << sh) : 0u, ins = (E == 2 ? (v & 0xFFFFu) : v) << sh;
+  c.x = w == 0 ? (c.x & keep) | ins : c.x;
+  c.y = w == 1 ? (c.y & keep) | ins : c.y;
+  c.z = w == 2 ? (c.z & keep) | ins : c.z;
+  c.w = w == 3 ? (c.w & keep) | ins : c.w;
+}
+
+template <int E>
+__global__ __launch_bounds__(64) void reshape_rows_kernel(
+    const char* __restrict__ key, const char* __restrict__ value, char* __restrict__ k_cache,
+    char* __restrict__ v_cache, const int32_t* __restrict__ slots, int num_tokens,
+    int num_kv_heads, int head_size, int block_size, int num_blocks) {
+  using T = typename Elem<E>::T;
+  constexpr int PER = 16 / E;                        // elements per 16-byte chunk
+  const int t = blockIdx.x / num_kv_heads, h = blockIdx.x % num_kv_heads;
+  const int lane = threadIdx.x;
+  const int32_t slot = slots[t];
+  if (slot < 0) return;
+  const int blk = slot / block_size, off = slot % block_size;
+  if (blk >= num_blocks) return;
+  bool shared = false;
+  for (int i = lane; i < num_tokens; i += kWave) {
+    const int32_t s2 = slots[i];
+    shared |= i != t && s2 >= 0 && s2 / block_size == blk;
+  }
+  const int64_t src = ((int64_t)t * num_kv_heads + h) * head_size;
+  const int64_t row = ((int64_t)blk * num_kv_heads + h) * head_size * block_size;   // elements
+  const T* ks = reinterpret_cast<const T*>(key) + src;
+  const T* vs = reinterpret_cast<const T*>(value) + src;
+  T* kr = reinterpret_cast<T*>(k_cache) + row;
+  T* vr = reinterpret_cast<T*>(v_cache) + row;
+  if (__builtin_amdgcn_ballot_w64(shared) != 0) {
+    for (int c = lane; c < head_size; c += kWave) {
+      kr[(int64_t)c * block_size + off] = ks[c];
+      vr[(int64_t)c * block_size + off] = vs[c];
+    }
+    return;
+  }
+  const int cpc = block_size / PER;                  // chunks per channel
+  const int chunks = head_size * cpc;
+#pragma unroll 4
+  for (int j = lane; j < chunks; j += kWave) {
+    u32x4 kc = load16(kr + (int64_t)j * PER), vc = load16(vr + (int64_t)j * PER);
+    const int c = j / cpc, e = off - (j % cpc) * PER;
+    if (e >= 0 && e < PER) {
+      put_elem<E>(kc, e, (uint32_t)ks[c]);
+      put_elem<E>(vc, e, (uint32_t)vs[c]);
+    }
+    *reinterpret_cast<u32x4*>(kr + (int64_t)j * PER) = kc;
+    *reinterpret_cast<u32x4*>(vr + (int64_t)j * PER) = vc;
+  }
+}
+
+// The row kernel serves calls of at most this many tokens (each wavefront
+// scans the call's slots for a shared block).
+constexpr int kRowAppendMaxTokens = 256;
+
 template <Kind SRC>
 __global__ __launch_bounds__(256) void reshape_fp8_kernel(
     const void* __restrict__ key, const void* __restrict__ value, uint8_t* __restrict__ k_cache,
@@ -241,7 +320,20 @@ int launch_reshape_and_cache(const CacheLaunch& a) {
     const int E = (a.cache_dtype == (int)Kind::F32) ? 4 : 2;
     const int64_t total = (int64_t)a.num_tokens * a.num_kv_heads * (a.head_size / (16 / E));
     const dim3 grid((unsigned)((total + 255) / 256));
-    if (E == 2)
+    const bool aligned = (((uintptr_t)a.k_cache | (uintptr_t)a.v_cache) % 16) == 0;
+    if (a.num_tokens <= kRowAppendMaxTokens && (a.block_size * E) % 16 == 0 && aligned) {
+      const dim3 rgrid((unsigned)(a.num_tokens * a.num_kv_heads));
+      if (E == 2)
+        hipLaunchKernelGGL(reshape_rows_kernel<2>, rgrid, dim3(kWave), 0, a.stream,
+                           (const char*)a.key, (const char*)a.value, (char*)a.k_cache,
+                           (char*)a.v_cache, a.slot_mapping, a.num_tokens, a.num_kv_heads,
+                           a.head_size, a.block_size, a.num_blocks);
+      else
+        hipLaunchKernelGGL(reshape_rows_kernel<4>, rgrid, dim3(kWave), 0, a.stream,
+                           (const char*)a.key, (const char*)a.value, (char*)a.k_cache,
+                           (char*)a.v_cache, a.slot_mapping, a.num_tokens, a.num_kv_heads,
+                           a.head_size, a.block_size, a.num_blocks);
+    } else if (E == 2)
       hipLaunchKernelGGL(reshape_copy_kernel<2>, grid, dim3(256), 0, a.stream,
                          (const char*)a.key, (const char*)a.value, (char*)a.k_cache,
                          (char*)a.v_cache, a.slot_mapping, a.num_tokens, a.num_kv_heads,
