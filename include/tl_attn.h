@@ -117,7 +117,12 @@ int tl_paged_attention_v2(void* out, float* exp_sums, float* max_logits, void* t
 /* Replaces reshape_and_cache (cache_kernels.cu:202-232): key/value
  * [T, n_kv, head_size] -> k_cache/v_cache [N, n_kv, head_size, block_size]
  * at slot_mapping[t] (int32, < 0 skipped, block >= N skipped).  dtype F16,
- * BF16 or F32, same for sources and pools (bit copy).  head_size % 8 == 0. */
+ * BF16 or F32, same for sources and pools (bit copy).  head_size % 8 == 0.
+ * Calls of at most 256 tokens on 16-byte aligned pools rewrite the whole
+ * row (head_size x block_size elements) of a block that only one token of
+ * the call writes, the other slots with their own bytes: no other writer
+ * may touch such a block during the call (a block that a sequence appends
+ * to belongs to that sequence). */
 int tl_reshape_and_cache(const void* key, const void* value, void* k_cache, void* v_cache,
                          const int32_t* slot_mapping, int32_t num_tokens, int32_t num_kv_heads,
                          int32_t head_size, int32_t block_size, int32_t num_blocks,
