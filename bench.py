@@ -292,7 +292,28 @@ def bench_rope(args):
 
     ms = timed(step, args.steps, args.warmup)
     nbytes = 2 * q.numel() * 2 + 4 * k.numel() * 2 + 2 * S * (D // 2) * 4 + 2 * S * 4
-    return {"us": ms * 1e3, "bytes": nbytes}
+    # the append's full cost shows in the decode that follows it (lines the
+    # append left partly written are written back during the decode): the
+    # append + decode step against the decode alone, over the same pools
+    # (sequence s owns blocks s (ctx/bs + 1) .. +ctx/bs, ctx + 1 tokens)
+    nbs = CTX // BS + 1
+    tables = (torch.arange(S, device="cuda", dtype=torch.int32)[:, None] * nbs +
+              torch.arange(nbs, device="cuda", dtype=torch.int32)[None, :]).contiguous()
+    sl = torch.full((S,), CTX + 1, dtype=torch.int32, device="cuda")
+    out = torch.empty_like(q)
+    desc = tla.make_decode_desc(q_out, kc, tables, NKV, 1.0 / math.sqrt(D), gqa_map=tla.GQA_GROUPED,
+                                partition_tokens=-1)
+
+    def decode(i_, stream):
+        tla.paged_attention_decode(desc, out, q_out, kc, vc, tables, sl, CTX + 1, None, stream)
+
+    def both(i_, stream):
+        step(i_, stream)
+        decode(i_, stream)
+
+    ms_d = timed(decode, args.steps, args.warmup)
+    ms_b = timed(both, args.steps, args.warmup)
+    return {"us": ms * 1e3, "bytes": nbytes, "us_decode": ms_d * 1e3, "us_append_then_decode": ms_b * 1e3}
 
 
 NA_ROWS, NA_HID, NA_FFN = 4096, 4096, 14336
@@ -626,7 +647,9 @@ def main():
             "workload": f"decode-step append, batch {S}: RoPE on q [{S}, {H}, {D}] and k, k and v into the bf16 "
                         "pools, one launch",
             "us_per_call": round(rp["us"], 2), "bytes_per_call": rp["bytes"],
-            "gbs": round(rp["bytes"] / (rp["us"] * 1e-6) / 1e9, 2)}
+            "gbs": round(rp["bytes"] / (rp["us"] * 1e-6) / 1e9, 2),
+            "bf16_decode_us": round(rp["us_decode"], 2),
+            "append_then_decode_us": round(rp["us_append_then_decode"], 2)}
     if vq is not None:
         res["vq_encode"] = {
             "workload": f"VQ encode, {VQ_N} fp16 vectors of d {D} against {VQ_K} entries (exact fp32 distances)",

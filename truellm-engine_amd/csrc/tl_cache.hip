@@ -197,7 +197,7 @@ template <Kind K, int STYLE>
 __global__ __launch_bounds__(256) void rope_cache_kernel(RopeCache a) {
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int half = a.head_size / 2, units = half / 8;           // 8 pairs per thread
-  const int rows = a.num_heads + 2 * a.num_kv_heads;            // q heads, k heads, v heads
+  const int rows = a.num_heads + (a.q_only ? 0 : 2 * a.num_kv_heads);   // q heads, k heads, v heads
   const int64_t total = (int64_t)a.num_tokens * rows * units;
   if (idx >= total) return;
   const int u = (int)(idx % units);
@@ -255,6 +255,98 @@ __global__ __launch_bounds__(256) void rope_cache_kernel(RopeCache a) {
 #pragma unroll
     for (int j = 0; j < 2; ++j)
       store_scalar<K>(pool, (pbase + rope_dim<STYLE>(i0 + p, j, half)) * a.block_size + off, x[2 * p + j]);
+}
+
+// An fp32 result as computed, before its conversion to a 2-byte type: the
+// compiler would otherwise fuse the last fma with the conversion
+// (v_fma_mix*, one rounding), where rope_cache_kernel and the reference
+// round to fp32 first.
+__device__ __forceinline__ float fp32_result(float r) {
+  asm volatile("" : "+v"(r));
+  return r;
+}
+
+// The element's bits in the pool's type (the rounding of store_scalar).
+template <Kind K> __device__ __forceinline__ uint32_t scalar_bits(float v);
+template <> __device__ __forceinline__ uint32_t scalar_bits<Kind::F32>(float v) { return __float_as_uint(v); }
+template <> __device__ __forceinline__ uint32_t scalar_bits<Kind::F16>(float v) { return f32_to_f16(v); }
+template <> __device__ __forceinline__ uint32_t scalar_bits<Kind::BF16>(float v) { return f32_to_bf16(v); }
+
+// The RoPE append for decode-sized calls (at most kRowAppendMaxTokens
+// tokens, 16-byte aligned pools, num_heads a multiple of num_kv_heads), in
+// one launch: a wavefront per (token, kv head) rotates the q heads
+// h G .. h G + G - 1 (G = num_heads / num_kv_heads) and writes k and v as
+// reshape_rows_kernel does: the block's K and V rows rewritten whole, with
+// the rotated key and the value in the token's slot, when no other token
+// of the call writes the block, element by element otherwise.  The
+// rotation is that of rope_cache_kernel.
+template <Kind K, int STYLE>
+__global__ __launch_bounds__(64) void rope_rows_kernel(RopeCache a) {
+  constexpr int E = KindInfo<K>::bytes, PER = 16 / E;
+  const int t = blockIdx.x / a.num_kv_heads, h = blockIdx.x % a.num_kv_heads;
+  const int lane = threadIdx.x;
+  const int pos = a.positions[t];
+  if (pos < 0 || pos >= a.max_positions) return;               // token left as it is
+  {
+    const int G = a.num_heads / a.num_kv_heads, hh = a.head_size / 2;
+    const float* cq = a.cos_table + (int64_t)pos * hh;
+    const float* sq = a.sin_table + (int64_t)pos * hh;
+    for (int hq = h * G; hq < h * G + G; ++hq) {
+      const int64_t qb = ((int64_t)t * a.num_heads + hq) * a.head_size;
+      for (int i = lane; i < hh; i += kWave) {
+        const float x0 = load_scalar<K>(a.q, qb + rope_dim<STYLE>(i, 0, hh));
+        const float x1 = load_scalar<K>(a.q, qb + rope_dim<STYLE>(i, 1, hh));
+        const float c0 = cq[i], s0 = sq[i];
+        store_scalar<K>(a.q_out, qb + rope_dim<STYLE>(i, 0, hh), fp32_result(__builtin_fmaf(x0, c0, -(x1 * s0))));
+        store_scalar<K>(a.q_out, qb + rope_dim<STYLE>(i, 1, hh), fp32_result(__builtin_fmaf(x0, s0, x1 * c0)));
+      }
+    }
+  }
+  const int32_t slot = a.slot_mapping[t];
+  if (slot < 0) return;
+  const int blk = slot / a.block_size, off = slot % a.block_size;
+  if (blk >= a.num_blocks) return;
+  bool shared = false;
+  for (int i = lane; i < a.num_tokens; i += kWave) {
+    const int32_t s2 = a.slot_mapping[i];
+    const int p2 = a.positions[i];
+    shared |= i != t && s2 >= 0 && s2 / a.block_size == blk && p2 >= 0 && p2 < a.max_positions;
+  }
+  const int half = a.head_size / 2;
+  const int64_t src = ((int64_t)t * a.num_kv_heads + h) * a.head_size;
+  const float* cs = a.cos_table + (int64_t)pos * half;
+  const float* sn = a.sin_table + (int64_t)pos * half;
+  // channel c of the rotated key
+  auto rot = [&](int c) {
+    const int i = STYLE == 0 ? c / 2 : c % half, r = STYLE == 0 ? c % 2 : c / half;
+    const float x0 = load_scalar<K>(a.key, src + rope_dim<STYLE>(i, 0, half));
+    const float x1 = load_scalar<K>(a.key, src + rope_dim<STYLE>(i, 1, half));
+    const float c0 = cs[i], s0 = sn[i];
+    return fp32_result(r == 0 ? __builtin_fmaf(x0, c0, -(x1 * s0)) : __builtin_fmaf(x0, s0, x1 * c0));
+  };
+  const int64_t row = ((int64_t)blk * a.num_kv_heads + h) * a.head_size * a.block_size;   // elements
+  char* kr = (char*)a.k_cache + row * E;
+  char* vr = (char*)a.v_cache + row * E;
+  if (__builtin_amdgcn_ballot_w64(shared) != 0) {
+    for (int c = lane; c < a.head_size; c += kWave) {
+      store_scalar<K>(kr, (int64_t)c * a.block_size + off, rot(c));
+      store_scalar<K>(vr, (int64_t)c * a.block_size + off, load_scalar<K>(a.value, src + c));
+    }
+    return;
+  }
+  const int cpc = a.block_size / PER;                  // chunks per channel
+  const int chunks = a.head_size * cpc;
+#pragma unroll 4
+  for (int j = lane; j < chunks; j += kWave) {
+    u32x4 kc = load16(kr + (int64_t)j * 16), vc = load16(vr + (int64_t)j * 16);
+    const int c = j / cpc, e = off - (j % cpc) * PER;
+    if (e >= 0 && e < PER) {
+      put_elem<E>(kc, e, scalar_bits<K>(rot(c)));
+      put_elem<E>(vc, e, scalar_bits<K>(load_scalar<K>(a.value, src + c)));
+    }
+    *reinterpret_cast<u32x4*>(kr + (int64_t)j * 16) = kc;
+    *reinterpret_cast<u32x4*>(vr + (int64_t)j * 16) = vc;
+  }
 }
 
 // grid.x = pairs x pools x slices; pool 1 is the second (V) pool of a copy.
@@ -347,12 +439,24 @@ int launch_reshape_and_cache(const CacheLaunch& a) {
   return hipGetLastError() == hipSuccess ? 0 : 5;
 }
 
-int launch_rope_cache(const RopeCache& a, hipStream_t stream) {
-  if (a.num_tokens == 0) return 0;
+int launch_rope_cache(const RopeCache& a_in, hipStream_t stream) {
+  if (a_in.num_tokens == 0) return 0;
+  RopeCache a = a_in;
+  a.q_only = 0;
+  const Kind k = (Kind)a.dtype;
+  const int E = k == Kind::F32 ? 4 : 2;
+  const bool aligned = (((uintptr_t)a.k_cache | (uintptr_t)a.v_cache) % 16) == 0;
+  // decode-sized calls: one wavefront per (token, kv head), whole block rows
+  const bool rows = a.num_tokens <= kRowAppendMaxTokens && (a.block_size * E) % 16 == 0 && aligned &&
+                    a.num_heads % a.num_kv_heads == 0;
   const int64_t total = (int64_t)a.num_tokens * (a.num_heads + 2 * a.num_kv_heads) * (a.head_size / 16);
   const dim3 grid((unsigned)((total + 255) / 256));
-  const Kind k = (Kind)a.dtype;
-#define TL_ROPE_LAUNCH(K, S) hipLaunchKernelGGL((rope_cache_kernel<K, S>), grid, dim3(256), 0, stream, a)
+  const dim3 rgrid((unsigned)(a.num_tokens * a.num_kv_heads));
+#define TL_ROPE_LAUNCH(K, S)                                                                    \
+  do {                                                                                          \
+    if (rows) hipLaunchKernelGGL((rope_rows_kernel<K, S>), rgrid, dim3(kWave), 0, stream, a);  \
+    else hipLaunchKernelGGL((rope_cache_kernel<K, S>), grid, dim3(256), 0, stream, a);         \
+  } while (0)
   if (k == Kind::F16) { if (a.style) TL_ROPE_LAUNCH(Kind::F16, 1); else TL_ROPE_LAUNCH(Kind::F16, 0); }
   else if (k == Kind::BF16) { if (a.style) TL_ROPE_LAUNCH(Kind::BF16, 1); else TL_ROPE_LAUNCH(Kind::BF16, 0); }
   else if (k == Kind::F32) { if (a.style) TL_ROPE_LAUNCH(Kind::F32, 1); else TL_ROPE_LAUNCH(Kind::F32, 0); }

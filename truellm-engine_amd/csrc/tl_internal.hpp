@@ -77,6 +77,7 @@ struct RopeCache {
   const float* cos_table; const float* sin_table;   // [max_positions, d/2]
   int num_tokens, num_heads, num_kv_heads, head_size, block_size, num_blocks, max_positions;
   int dtype, style;             // style 0: pairs (2i, 2i+1); 1: (i, i + d/2)
+  int q_only;                   // set by the launcher: k and v go through the row kernel
 };
 int launch_rope_cache(const RopeCache& a, hipStream_t stream);
 
