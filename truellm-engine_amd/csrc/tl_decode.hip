@@ -321,6 +321,23 @@ __global__ __launch_bounds__(64) void lse_reduce_kernel(
     const int32_t* seq_lens, int num_heads, int num_partitions, int partition_tokens,
     int kivi_residual, int kivi_pages) {
   const int sh = blockIdx.x, seq = sh / num_heads;
+  const int64_t pb = (int64_t)sh * num_partitions;
+  // The partials are read for every partition slot (all in the workspace)
+  // before the sequence length arrives; slots past the sequence's
+  // partitions hold anything and are dropped by the conditions below.
+  // (head sizes that are a multiple of 64: a thread owns channels
+  // threadIdx.x + 64 c)
+  constexpr int kEarly = HEAD % 64 == 0 ? 8 : 0, CH = HEAD / 64 > 0 ? HEAD / 64 : 1;
+  float em[kEarly > 0 ? kEarly : 1], el[kEarly > 0 ? kEarly : 1], eo[kEarly > 0 ? kEarly : 1][CH];
+#pragma unroll
+  for (int i = 0; i < kEarly; ++i) {
+    const bool in = i < num_partitions;
+    em[i] = in ? part_m[pb + i] : 0.f;
+    el[i] = in ? part_l[pb + i] : 0.f;
+#pragma unroll
+    for (int c = 0; c < CH; ++c)
+      eo[i][c] = in ? load_scalar<PO>(part_o, (pb + i) * HEAD + threadIdx.x + 64 * c) : 0.f;
+  }
   const int L = seq_lens[seq];
   int np;
   if (kivi_pages > 0) {
@@ -330,7 +347,25 @@ __global__ __launch_bounds__(64) void lse_reduce_kernel(
     np = (L + partition_tokens - 1) / partition_tokens;
   }
   np = min(np, num_partitions);
-  const int64_t pb = (int64_t)sh * num_partitions;
+  if (kEarly > 0 && np <= kEarly) {
+    float M = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < kEarly; ++i)
+      if (i < np && el[i] > 0.f) M = fmaxf(M, em[i]);
+    float W = 0.f;
+#pragma unroll
+    for (int i = 0; i < kEarly; ++i)
+      if (i < np && el[i] > 0.f) W += el[i] * __expf(em[i] - M);
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      float o = 0.f;
+#pragma unroll
+      for (int i = 0; i < kEarly; ++i)
+        if (i < np && el[i] > 0.f) o += el[i] * __expf(em[i] - M) * eo[i][c];
+      store_scalar<QK>(out, (int64_t)sh * HEAD + threadIdx.x + 64 * c, (W > 0.f) ? o / W : 0.f);
+    }
+    return;
+  }
   // every partition's (max, sum) and this thread's partial outputs in one go
   float M = -INFINITY;
   for (int i = 0; i < np; ++i)
