@@ -160,7 +160,10 @@ typedef enum tl_rope_style { TL_ROPE_ADJACENT = 0, TL_ROPE_HALVES = 1 } tl_rope_
  * [T, n_kv, d]; pools [N, n_kv, d, bs]; slot < 0 or past the pool skips the
  * token's pool write.  A token whose position is outside [0, max_positions)
  * is not written at all (q_out rows and pool).  head_size a multiple of 16;
- * num_heads 0 rotates and writes key / value only. */
+ * num_heads 0 rotates and writes key / value only.  Calls of at most 256
+ * tokens on 16-byte aligned pools write key / value as tl_reshape_and_cache
+ * does for such calls (whole block rows: no other writer may touch those
+ * blocks during the call). */
 int tl_rope_reshape_and_cache(const void* q, void* q_out, const void* key, const void* value,
                               void* k_cache, void* v_cache, const int32_t* slot_mapping,
                               const int32_t* positions, const float* cos_table, const float* sin_table,
