@@ -19,7 +19,8 @@
 // Online softmax per wavefront; running max per head from a permlane swap
 // max over the four lane groups.
 // Residual wavefront: the last wavefront of the partition that ends the
-// sequence runs the fp16 window with the 2-byte decode (tl_decode_wave.hpp).
+// sequence runs the fp16 window with the 2-byte decode (tl_decode_wave.hpp),
+// the newest token, and then the partition's last 1/30 of the pages.
 // The wavefront states are merged in LDS; several partitions are merged by
 // the log-sum-exp reduce.
 #include "tl_decode_wave.hpp"
@@ -450,16 +451,18 @@ __device__ __forceinline__ void store_newest(const PageJob& j, const NewestToken
   }
 }
 
-// Slots 0 .. NW-1: one per wavefront; slot NW: the newest token.
+// Slots 0 .. NW-1: one per wavefront; slot NW: the newest token; slot
+// NW + 1: the residual wavefront's pages.
 template <int NW>
 struct KiviDecodeSmem {
   uint32_t p[NW][512];                       // per wave: weights or page params
-  float m[NW + 1][kWaveHeads], l[NW + 1][kWaveHeads];
-  float acc[NW + 1][kWaveHeads][kKiviHead];
+  float m[NW + 2][kWaveHeads], l[NW + 2][kWaveHeads];
+  float acc[NW + 2][kWaveHeads][kKiviHead];
 };
 
 // One decode workgroup.  The residual wavefront runs the window [lq, L - 1)
-// from the pool and then the newest token (L - 1) as a state of its own.
+// from the pool, the newest token (L - 1) as a state of its own, and then
+// the range's last pages (slot NW + 1).
 // With APPEND the workgroup also does the step's append for its (sequence,
 // kv head), and nothing in the launch reads a byte that it writes:
 //   * the page that the new token completes (if any) is built first, by the
@@ -510,6 +513,11 @@ __global__ __launch_bounds__(NW * kWave, 2) void kivi_decode_kernel(KiviParams k
   const bool last = part == n_parts - 1;
   const bool has_res = last && L > lq;
   const int page_waves = has_res ? NW - 1 : NW;
+  // The residual wavefront ends its window about 10 us before the page
+  // wavefronts end their pages (batch 64, ctx 4096), so it also runs the
+  // range's last pages, 1/30 of them: 4 of 124 at ctx 4096 gave 63.9 us
+  // per step against 64.5 us (2 pages: 64.7, 3: 64.1, 6: 64.9).
+  const int res_pages = has_res ? (pg1 - pg0) / 30 : 0;
 
   // The page that L completes, if any (APPEND), by the whole workgroup
   // before the page wavefronts start.  (Built by the residual wavefront
@@ -531,7 +539,7 @@ __global__ __launch_bounds__(NW * kWave, 2) void kivi_decode_kernel(KiviParams k
     // us at batch 64).  The second half's page wavefronts take the higher
     // priority on every other page pair, so both progress together (55.5
     // and 58.5 us).
-    kivi_pages_wave(k, seq, kvh, hs, pg0 + wave, pg1, page_waves, &sd.p[wave][0], &sd.acc[wave][0][0],
+    kivi_pages_wave(k, seq, kvh, hs, pg0 + wave, pg1 - res_pages, page_waves, &sd.p[wave][0], &sd.acc[wave][0][0],
                     &sd.m[wave][0], &sd.l[wave][0], FINAL && blockIdx.x >= gridDim.x / 2,
                     FINAL && page_waves == NW - 1, early_id);
   } else {
@@ -547,9 +555,11 @@ __global__ __launch_bounds__(NW * kWave, 2) void kivi_decode_kernel(KiviParams k
     // the token's store, at the end of the window, off the page wavefronts'
     // path (the window ends halfway through the launch)
     if constexpr (APPEND) store_newest(k.job, nt, seq, kvh, lane);
+    kivi_pages_wave(k, seq, kvh, hs, pg1 - res_pages, pg1, 1, &sd.p[wave][0], &sd.acc[NW + 1][0][0],
+                    &sd.m[NW + 1][0], &sd.l[NW + 1][0], false, false, -1);
   }
   __syncthreads();
-  combine_waves<Kind::F16, Kind::F32, kKiviHead, FINAL>(p, has_res ? NW + 1 : NW, &sd.m[0][0], &sd.l[0][0],
+  combine_waves<Kind::F16, Kind::F32, kKiviHead, FINAL>(p, has_res ? NW + 2 : NW, &sd.m[0][0], &sd.l[0][0],
                                                         &sd.acc[0][0][0], seq, kvh, hs, part, tid, NW * kWave);
 }
 
