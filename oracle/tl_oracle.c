@@ -886,15 +886,16 @@ void orc_kivi_build_pages(const uint16_t* k_cache, const uint16_t* v_cache,
                           const int32_t* block_tables, int max_blocks_per_seq,
                           const int32_t* seq_lens, int num_seqs, int num_kv_heads,
                           int block_size, int residual_length,
-                          uint8_t* pages, const int32_t* page_tables, int max_pages)
+                          uint8_t* pages, const int32_t* page_tables, int max_pages,
+                          int num_pages)
 {
     uint16_t kt[PG_T * PG_D], vt[PG_T * PG_D];
     for (int s = 0; s < num_seqs; ++s) {
         int Lq = orc_kivi_quantized_len(seq_lens[s], residual_length);
         const int32_t* row = block_tables + (int64_t)s * max_blocks_per_seq;
-        for (int p = 0; p < Lq / PG_T; ++p) {
+        for (int p = 0; p < Lq / PG_T && p < max_pages; ++p) {
             int32_t pid = page_tables[(int64_t)s * max_pages + p];
-            if (pid < 0) continue;
+            if (pid < 0 || pid >= num_pages) continue;
             for (int h = 0; h < num_kv_heads; ++h) {
                 for (int t = 0; t < PG_T; ++t) {
                     gather_tok_f16(k_cache, row, p * PG_T + t, h, num_kv_heads, block_size, kt + t * PG_D);
@@ -906,9 +907,16 @@ void orc_kivi_build_pages(const uint16_t* k_cache, const uint16_t* v_cache,
     }
 }
 
+/* Attention over the KIVI cache.  Tokens below Lq come from their page
+ * (dequantised by the page format); a page-table entry that is negative or
+ * past the pool (num_pages) is a hole and its 32 tokens are skipped.  Tokens
+ * from Lq on come from the fp16 pool through the block table; a negative
+ * block-table entry is a hole and its tokens are skipped, as in
+ * orc_paged_attention (paged_attention_v1.cu:76).  A (sequence, head) with no
+ * valid token yields zeros. */
 void orc_kivi_paged_attention(double* out, const void* q, int q_dtype,
                               const uint8_t* pages, const int32_t* page_tables,
-                              int max_pages, const uint16_t* k_cache,
+                              int max_pages, int num_pages, const uint16_t* k_cache,
                               const uint16_t* v_cache, const int32_t* block_tables,
                               int max_blocks_per_seq, const int32_t* seq_lens,
                               int num_seqs, int num_heads, int num_kv_heads,
@@ -921,6 +929,7 @@ void orc_kivi_paged_attention(double* out, const void* q, int q_dtype,
     float* K = (float*)malloc(sizeof(float) * (size_t)max_len * PG_D);
     float* V = (float*)malloc(sizeof(float) * (size_t)max_len * PG_D);
     double* sc = (double*)malloc(sizeof(double) * (size_t)max_len);
+    unsigned char* ok = (unsigned char*)malloc((size_t)max_len);
     uint16_t kt[PG_T * PG_D], vt[PG_T * PG_D];
     for (int s = 0; s < num_seqs; ++s) {
         int L = seq_lens[s];
@@ -928,7 +937,10 @@ void orc_kivi_paged_attention(double* out, const void* q, int q_dtype,
         const int32_t* row = block_tables + (int64_t)s * max_blocks_per_seq;
         for (int kvh = 0; kvh < num_kv_heads; ++kvh) {
             for (int p = 0; p < Lq / PG_T; ++p) {
-                int32_t pid = page_tables[(int64_t)s * max_pages + p];
+                int32_t pid = p < max_pages ? page_tables[(int64_t)s * max_pages + p] : -1;
+                int there = pid >= 0 && pid < num_pages;
+                for (int t = 0; t < PG_T; ++t) ok[p * PG_T + t] = (unsigned char)there;
+                if (!there) continue;
                 orc_kivi_page_dequant(pages + ((int64_t)pid * num_kv_heads + kvh) * ORC_KIVI_PAGE_BYTES, kt, vt);
                 for (int i = 0; i < PG_T * PG_D; ++i) {
                     K[(size_t)p * PG_T * PG_D + i] = orc_f16_to_f32(kt[i]);
@@ -936,6 +948,9 @@ void orc_kivi_paged_attention(double* out, const void* q, int q_dtype,
                 }
             }
             for (int t = Lq; t < L; ++t) {
+                int64_t phys;
+                ok[t] = (unsigned char)gather_ok(row, t, block_size, &phys);
+                if (!ok[t]) continue;
                 gather_tok_f16(k_cache, row, t, kvh, num_kv_heads, block_size, kt);
                 gather_tok_f16(v_cache, row, t, kvh, num_kv_heads, block_size, vt);
                 for (int e = 0; e < PG_D; ++e) {
@@ -948,6 +963,7 @@ void orc_kivi_paged_attention(double* out, const void* q, int q_dtype,
                 int64_t qoff = ((int64_t)s * num_heads + h) * PG_D;
                 double m = -INFINITY;
                 for (int t = 0; t < L; ++t) {
+                    if (!ok[t]) continue;
                     double d = 0.0;
                     for (int e = 0; e < PG_D; ++e) d += load_elem(q, q_dtype, qoff + e) * (double)K[(size_t)t * PG_D + e];
                     sc[t] = d * (double)scale;
@@ -956,14 +972,16 @@ void orc_kivi_paged_attention(double* out, const void* q, int q_dtype,
                 double l = 0.0;
                 double* o = out + qoff;
                 for (int e = 0; e < PG_D; ++e) o[e] = 0.0;
+                if (m == -INFINITY) continue;               /* no valid token */
                 for (int t = 0; t < L; ++t) {
+                    if (!ok[t]) continue;
                     double w = exp(sc[t] - m);
                     l += w;
                     for (int e = 0; e < PG_D; ++e) o[e] += w * (double)V[(size_t)t * PG_D + e];
                 }
-                for (int e = 0; e < PG_D; ++e) o[e] = (l > 0.0) ? o[e] / l : 0.0;
+                for (int e = 0; e < PG_D; ++e) o[e] /= l;
             }
         }
     }
-    free(K); free(V); free(sc);
+    free(K); free(V); free(sc); free(ok);
 }

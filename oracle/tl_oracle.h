@@ -145,19 +145,24 @@ void orc_kivi_page_dequant(const uint8_t* page, uint16_t* k_tok, uint16_t* v_tok
 /* Number of tokens held in pages for a sequence of length L. */
 int  orc_kivi_quantized_len(int seq_len, int residual_length);
 
-/* Build every page of a batch from an fp16/bf16-free fp16 paged cache:
- * pages [P_pool][n_kv][5120]; page_tables [S, max_pages]. */
+/* Build every page of a batch from an fp16 paged cache: pages
+ * [num_pages][n_kv][5120]; page_tables [S, max_pages].  Page-table entries
+ * outside [0, num_pages) are skipped; tokens whose block-table entry is
+ * negative are quantised as zeros. */
 void orc_kivi_build_pages(const uint16_t* k_cache, const uint16_t* v_cache,
                           const int32_t* block_tables, int max_blocks_per_seq,
                           const int32_t* seq_lens, int num_seqs, int num_kv_heads,
                           int block_size, int residual_length,
-                          uint8_t* pages, const int32_t* page_tables, int max_pages);
+                          uint8_t* pages, const int32_t* page_tables, int max_pages,
+                          int num_pages);
 
 /* Attention over the KIVI cache: pages (dequantized per the format) for
- * tokens < Lq, the fp16 paged cache for tokens >= Lq.  out double. */
+ * tokens < Lq, the fp16 paged cache for tokens >= Lq.  Page-table entries
+ * outside [0, num_pages) and negative block-table entries are holes whose
+ * tokens are skipped.  out double. */
 void orc_kivi_paged_attention(double* out, const void* q, int q_dtype,
                               const uint8_t* pages, const int32_t* page_tables,
-                              int max_pages, const uint16_t* k_cache,
+                              int max_pages, int num_pages, const uint16_t* k_cache,
                               const uint16_t* v_cache, const int32_t* block_tables,
                               int max_blocks_per_seq, const int32_t* seq_lens,
                               int num_seqs, int num_heads, int num_kv_heads,

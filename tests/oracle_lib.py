@@ -60,8 +60,8 @@ _lib.orc_kivi_page_quantize.argtypes = [_P, _P, _P]
 _lib.orc_kivi_page_dequant.argtypes = [_P, _P, _P]
 _lib.orc_kivi_quantized_len.restype = _I
 _lib.orc_kivi_quantized_len.argtypes = [_I, _I]
-_lib.orc_kivi_build_pages.argtypes = [_P, _P, _P, _I, _P, _I, _I, _I, _I, _P, _P, _I]
-_lib.orc_kivi_paged_attention.argtypes = [_P, _P, _I, _P, _P, _I, _P, _P, _P, _I, _P, _I, _I, _I, _I, _I, _F, _I]
+_lib.orc_kivi_build_pages.argtypes = [_P, _P, _P, _I, _P, _I, _I, _I, _I, _P, _P, _I, _I]
+_lib.orc_kivi_paged_attention.argtypes = [_P, _P, _I, _P, _P, _I, _I, _P, _P, _P, _I, _P, _I, _I, _I, _I, _I, _F, _I]
 
 lib = _lib
 
@@ -285,7 +285,8 @@ def kivi_quantized_len(seq_len, residual_length) -> int:
 def kivi_build_pages(k_cache, v_cache, tables, seq_lens, residual_length, pages, page_tables):
     _lib.orc_kivi_build_pages(ptr(k_cache), ptr(v_cache), ptr(tables), tables.shape[1],
                               ptr(seq_lens), len(seq_lens), k_cache.shape[1], k_cache.shape[3],
-                              residual_length, ptr(pages), ptr(page_tables), page_tables.shape[1])
+                              residual_length, ptr(pages), ptr(page_tables), page_tables.shape[1],
+                              pages.size // (k_cache.shape[1] * KIVI_PAGE_BYTES))
 
 
 def kivi_paged_attention(q, q_code, pages, page_tables, k_cache, v_cache, tables, seq_lens,
@@ -293,7 +294,8 @@ def kivi_paged_attention(q, q_code, pages, page_tables, k_cache, v_cache, tables
     S, H, D = q.shape
     out = np.zeros((S, H, D), np.float64)
     _lib.orc_kivi_paged_attention(ptr(out), ptr(q), q_code, ptr(pages), ptr(page_tables),
-                                  page_tables.shape[1], ptr(k_cache), ptr(v_cache), ptr(tables),
+                                  page_tables.shape[1], pages.size // (num_kv_heads * KIVI_PAGE_BYTES),
+                                  ptr(k_cache), ptr(v_cache), ptr(tables),
                                   tables.shape[1], ptr(seq_lens), S, H, num_kv_heads,
                                   k_cache.shape[3], residual_length, scale, gqa_map)
     return out

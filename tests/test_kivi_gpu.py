@@ -228,6 +228,120 @@ def test_kivi_decode_group_sizes(H, n_kv, gqa):
                  f"H={H}")
 
 
+def _punch_holes(kc):
+    """Holes of every kind on a KiviCase with lengths [4096, 1000, 300, 161,
+    2047, 700] (R = 128): block-table holes in the fp16 window (one on the
+    newest token), a block hole inside a page's range (the page then holds
+    quantised zeros), page-table entries that are negative or past the page
+    pool, and a sequence whose every page is a hole."""
+    t = kc.tables
+    t[0, (4096 - 50) // 16] = -1            # window of sequence 0 (Lq = 3968)
+    t[1, (1000 - 1) // 16] = -1             # the newest token's block of sequence 1
+    t[2, 3] = -1                            # inside page 1 of sequence 2 (Lq = 160)
+    t[4, (2047 - 140) // 16] = -1           # a window block of sequence 4 (Lq = 1888)
+    pt = kc.page_tables
+    pt[0, 7] = -1
+    pt[0, 100] = kc.num_pages               # past the pool: a hole
+    pt[4, 0] = -1
+    pt[5, :] = -1                           # sequence 5: every page a hole (Lq = 544)
+
+
+@pytest.mark.parametrize("pp", [0, 4, -1])
+def test_kivi_decode_table_and_page_holes(pp):
+    """Holes in the block table (fp16 window) and the page table are skipped
+    by the decode, as the oracle skips them; a hole inside a page's block
+    range only zeroes the tokens the page was built from."""
+    kc = KiviCase(59, [4096, 1000, 300, 161, 2047, 700])
+    _punch_holes(kc)
+    pages = kc.oracle_pages()
+    print(f"case kivi holes pp={pp}", flush=True)
+    assert_close(_run_decode(kc, pages, pp), _kivi_ref(kc, pages), orc.F16, ATOL_KIVI, f"holes pp={pp}")
+
+
+def test_kivi_split_k_page_table_narrower_than_sequence():
+    """A page table with fewer columns than a sequence has pages: the pages
+    past its width are dropped by the decode and by the log-sum-exp merge
+    alike (the merge counts the partitions the decode wrote, not those of
+    the full length); the workspace starts as finite values a merge of
+    unwritten partitions would pick up."""
+    kc = KiviCase(62, [4096, 3000, 700, 161])
+    kc.page_tables = np.ascontiguousarray(kc.page_tables[:, :20])
+    pages = kc.oracle_pages()
+    qd, kd, vd = dev(kc.q, orc.F16), dev(kc.k, orc.F16), dev(kc.v, orc.F16)
+    btd, sld, ptd = dev(kc.tables), dev(kc.lens), dev(kc.page_tables)
+    desc = kc.desc(qd, kd, btd, ptd, 4)
+    max_ctx = int(kc.lens.max())
+    nbytes = tla.kivi_workspace_bytes(desc, max_ctx)
+    assert nbytes > 0 and nbytes % 4 == 0
+    ws = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    ws.view(torch.float32).fill_(1.0)
+    out = torch.full_like(qd, float("nan"))
+    print("case kivi narrow page table pp=4", flush=True)
+    tla.kivi_paged_attention_decode(desc, out, qd, torch.from_numpy(pages).cuda(), ptd, kd, vd, btd, sld,
+                                    max_ctx, ws)
+    torch.cuda.synchronize()
+    assert_close(out, _kivi_ref(kc, pages), orc.F16, ATOL_KIVI, "narrow page table")
+
+
+def test_build_pages_with_holes_bit_exact():
+    """The GPU page build skips page-table holes (negative or past the pool)
+    and quantises a block-table hole as zeros, byte for byte as the oracle."""
+    kc = KiviCase(60, [4096, 1000, 300, 161, 2047, 700])
+    _punch_holes(kc)
+    want = kc.oracle_pages()
+    qd, kd, vd = dev(kc.q, orc.F16), dev(kc.k, orc.F16), dev(kc.v, orc.F16)
+    btd, sld, ptd = dev(kc.tables), dev(kc.lens), dev(kc.page_tables)
+    pages = torch.zeros(kc.num_pages, kc.n_kv, tla.KIVI_PAGE_BYTES, dtype=torch.uint8, device="cuda")
+    print("case build pages with holes", flush=True)
+    tla.kivi_build_pages(kc.desc(qd, kd, btd, ptd), kd, vd, btd, sld, ptd, pages, int(kc.lens.max()))
+    torch.cuda.synchronize()
+    assert np.array_equal(pages.cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("H,pp", [(32, 0), (64, 4)])
+def test_kivi_decode_step_matches_oracle_each_step(H, pp):
+    """The fused tl_kivi_decode_step checked against the oracle itself at
+    every step: the host pools receive each token through
+    orc.reshape_and_cache, the pages are rebuilt by orc.kivi_build_pages at
+    the step's lengths and the expected output is orc.kivi_paged_attention.
+    Sequences complete pages during the run; sequence 0's first page and a
+    window block of sequence 5 are holes."""
+    start = np.array([150, 159, 160, 191, 33, 1000], np.int32)
+    steps = 36
+    kc = KiviCase(61, start + steps, H=H, extra_blocks=1)
+    kc.page_tables[0, 0] = -1
+    kc.tables[5, (1000 - 60) // 16] = -1
+    qd, kd, vd = dev(kc.q, orc.F16), dev(kc.k, orc.F16), dev(kc.v, orc.F16)
+    btd, ptd = dev(kc.tables), dev(kc.page_tables)
+    pages = torch.zeros(kc.num_pages, kc.n_kv, tla.KIVI_PAGE_BYTES, dtype=torch.uint8, device="cuda")
+    desc = kc.desc(qd, kd, btd, ptd, pp)
+    tla.kivi_build_pages(desc, kd, vd, btd, dev(start), ptd, pages, int(start.max()))
+    rng = np.random.default_rng(12)
+    max_ctx = int(start.max()) + steps
+    ws = torch.empty(max(16, tla.kivi_workspace_bytes(desc, max_ctx)), dtype=torch.uint8, device="cuda")
+    lens = start.copy()
+    k_host, v_host = kc.k.copy(), kc.v.copy()
+    print(f"case kivi step vs oracle H={H} pp={pp}", flush=True)
+    for step in range(steps):
+        lens = lens + 1
+        pos = lens - 1
+        slots = (kc.tables[np.arange(kc.S), pos // 16] * 16 + pos % 16).astype(np.int32)
+        knew = inputs.encode(rng.standard_normal((kc.S, kc.n_kv, 128), dtype=np.float32), orc.F16)
+        vnew = inputs.encode(rng.standard_normal((kc.S, kc.n_kv, 128), dtype=np.float32), orc.F16)
+        out = torch.full_like(qd, float("nan"))
+        tla.kivi_decode_step(desc, out, qd, dev(knew, orc.F16), dev(vnew, orc.F16), dev(slots), pages, ptd,
+                             kd, vd, btd, dev(lens), max_ctx, ws)
+        torch.cuda.synchronize()
+        orc.reshape_and_cache(knew, vnew, k_host, v_host, slots)
+        kc.k, kc.v, kc.lens = k_host, v_host, lens
+        want_pages = kc.oracle_pages()
+        want = _kivi_ref(kc, want_pages)
+        assert_close(out, want, orc.F16, ATOL_KIVI, f"step {step}")
+    used = _used_pages(kc, lens)
+    used = [p for p in used if p >= 0]
+    assert np.array_equal(pages.cpu().numpy()[used], want_pages[used])
+
+
 def test_kivi_decode_residual_zero_and_nan_slots():
     """R = 0 (every whole page quantised) and NaN in unused fp16 slots."""
     kc = KiviCase(55, [96, 100, 33], R=0)

@@ -479,6 +479,183 @@ def test_kivi_quantized_len():
         assert lq % 32 == 0 and (L < 160 or 128 <= L - lq < 160)
 
 
+def _kivi_small_case(seed, lens, n_kv=2, H=4):
+    """fp16 pools (d 128, bs 16) with a page pool and a shuffled page table."""
+    case = inputs.make_paged_case(seed, S=len(lens), H=H, n_kv=n_kv, D=128, BS=16, lens=lens,
+                                  code=orc.F16)
+    max_pages = max(1, max(lens) // 32 + 1)
+    num_pages = len(lens) * max_pages + 2
+    rng = np.random.default_rng(seed + 9)
+    ptab = rng.permutation(num_pages)[: len(lens) * max_pages].astype(np.int32).reshape(len(lens), -1)
+    return case, np.ascontiguousarray(ptab), num_pages
+
+
+def _gather_tokens(pool, tables, s, t0, t1, kvh, BS=16):
+    """[t1 - t0, 128] fp16 bits of tokens t0..t1-1 through the block table;
+    zeros for a hole (numpy fancy indexing, independent of the oracle)."""
+    pos = np.arange(t0, t1)
+    phys = tables[s][pos // BS]
+    out = pool[np.maximum(phys, 0), kvh, :, pos % BS].copy()
+    out[phys < 0] = 0
+    return out
+
+
+def test_kivi_build_pages_equals_page_quantize_of_gathered_tokens():
+    """orc_kivi_build_pages = orc_kivi_page_quantize (pinned above) applied to
+    the tokens gathered through the block table, zeros for a block hole;
+    page-table holes (negative or past the pool) are left untouched."""
+    R = 128
+    lens = [300, 161, 100, 223]
+    case, ptab, num_pages = _kivi_small_case(31, lens)
+    case.tables[0, 3] = -1                 # tokens 48..63: page 1 of sequence 0
+    ptab[0, 2] = -1                        # page holes: negative and past the pool
+    ptab[0, 4] = num_pages
+    n_kv = 2
+    pages = np.full((num_pages, n_kv, orc.KIVI_PAGE_BYTES), 0xA5, np.uint8)
+    orc.kivi_build_pages(case.k_cache, case.v_cache, case.tables, case.seq_lens, R, pages, ptab)
+    want = np.full_like(pages, 0xA5)
+    built = 0
+    for s, L in enumerate(lens):
+        for p in range(orc.kivi_quantized_len(L, R) // 32):
+            pid = int(ptab[s, p])
+            if pid < 0 or pid >= num_pages:
+                continue
+            for h in range(n_kv):
+                kt = _gather_tokens(case.k_cache, case.tables, s, 32 * p, 32 * p + 32, h)
+                vt = _gather_tokens(case.v_cache, case.tables, s, 32 * p, 32 * p + 32, h)
+                want[pid, h] = orc.kivi_page_quantize(np.ascontiguousarray(kt), np.ascontiguousarray(vt))
+                built += 1
+    assert built == (5 - 2 + 1 + 0 + 2) * n_kv     # Lq: 160, 32, 0, 64 tokens
+    assert np.array_equal(pages, want)
+
+
+def _kivi_as_paged_pool(case, pages, ptab, num_pages, R):
+    """The pool a KIVI cache stands for: tokens below Lq dequantised from
+    their page (a page hole: both of its blocks are table holes), the rest
+    copied from the fp16 pool through the block table.  Each sequence gets
+    contiguous blocks of a fresh pool."""
+    S, H, D = case.q.shape
+    n_kv, BS = case.k_cache.shape[1], 16
+    nblk = [(int(L) + BS - 1) // BS for L in case.seq_lens]
+    kp = np.zeros((sum(nblk) + 1, n_kv, D, BS), np.uint16)
+    vp = np.zeros_like(kp)
+    tables = np.full((S, max(nblk)), -1, np.int32)
+    nxt = 0
+    for s, L in enumerate(case.seq_lens):
+        L = int(L)
+        Lq = orc.kivi_quantized_len(L, R)
+        for b in range(nblk[s]):
+            t0, t1 = b * BS, min(L, b * BS + BS)
+            if t0 < Lq:
+                pid = int(ptab[s, t0 // 32])
+                if pid < 0 or pid >= num_pages:
+                    continue
+                for h in range(n_kv):
+                    kd, vd = orc.kivi_page_dequant(np.ascontiguousarray(pages[pid, h]))
+                    o = t0 % 32
+                    kp[nxt, h] = kd[o:o + BS].T
+                    vp[nxt, h] = vd[o:o + BS].T
+            else:
+                if case.tables[s, b] < 0:
+                    continue
+                for h in range(n_kv):
+                    kp[nxt, h, :, : t1 - t0] = _gather_tokens(case.k_cache, case.tables, s, t0, t1, h).T
+                    vp[nxt, h, :, : t1 - t0] = _gather_tokens(case.v_cache, case.tables, s, t0, t1, h).T
+            tables[s, b] = nxt
+            nxt += 1
+    return kp, vp, tables
+
+
+@pytest.mark.parametrize("gqa_map", [orc.MODULO, orc.GROUPED])
+def test_kivi_attention_equals_paged_attention_on_dequantised_prefix(gqa_map):
+    """orc_kivi_paged_attention = orc_paged_attention (pinned above) over the
+    pool it stands for: pages dequantised by orc_kivi_page_dequant below Lq,
+    the fp16 window above; page-table holes and block-table holes in the
+    window drop their tokens, a block hole inside a built page does not (the
+    page holds its quantised zeros)."""
+    R = 128
+    lens = [300, 161, 100, 223]
+    case, ptab, num_pages = _kivi_small_case(32, lens)
+    case.tables[0, 3] = -1                 # inside page 1 of sequence 0
+    case.tables[0, 12] = -1                # in the window of sequence 0 (Lq = 160)
+    case.tables[3, 9] = -1                 # in the window of sequence 3 (Lq = 64)
+    ptab[0, 2] = -1
+    ptab[3, 1] = num_pages                 # past the pool: a hole too
+    pages = np.zeros((num_pages, 2, orc.KIVI_PAGE_BYTES), np.uint8)
+    orc.kivi_build_pages(case.k_cache, case.v_cache, case.tables, case.seq_lens, R, pages, ptab)
+    got = orc.kivi_paged_attention(case.q, orc.F16, pages, ptab, case.k_cache, case.v_cache,
+                                   case.tables, case.seq_lens, 2, R, case.scale, gqa_map)
+    kp, vp, t2 = _kivi_as_paged_pool(case, pages, ptab, num_pages, R)
+    want = orc.paged_attention(case.q, orc.F16, kp, vp, orc.F16, t2, case.seq_lens, 2, case.scale,
+                               gqa_map)
+    np.testing.assert_allclose(got, want, rtol=0, atol=1e-12)
+    # the holes matter: without them the result changes
+    full = orc.kivi_paged_attention(case.q, orc.F16, pages, np.where(ptab >= num_pages, 0, np.abs(ptab)).astype(np.int32),
+                                    case.k_cache, case.v_cache, case.tables, case.seq_lens, 2, R, case.scale,
+                                    gqa_map)
+    assert np.abs(full[0] - got[0]).max() > 1e-3 and np.abs(full[3] - got[3]).max() > 1e-3
+
+
+def test_kivi_attention_without_pages_is_paged_attention_with_holes():
+    """R >= L: no token is quantised, so KIVI attention is paged attention on
+    the fp16 pool, holes skipped in both."""
+    lens = [300, 161, 100, 1]
+    case, ptab, num_pages = _kivi_small_case(33, lens)
+    case.tables[0, 5] = -1
+    case.tables[2, 0] = -1
+    pages = np.zeros((num_pages, 2, orc.KIVI_PAGE_BYTES), np.uint8)
+    got = orc.kivi_paged_attention(case.q, orc.F16, pages, ptab, case.k_cache, case.v_cache,
+                                   case.tables, case.seq_lens, 2, 512, case.scale, orc.GROUPED)
+    want = orc.paged_attention(case.q, orc.F16, case.k_cache, case.v_cache, orc.F16, case.tables,
+                               case.seq_lens, 2, case.scale, orc.GROUPED)
+    np.testing.assert_allclose(got, want, rtol=0, atol=1e-12)
+    np.testing.assert_allclose(got, numpy_attention(case, orc.GROUPED), rtol=0, atol=1e-12)
+
+
+def test_kivi_attention_all_holes_gives_zeros():
+    lens = [200, 40]
+    case, ptab, num_pages = _kivi_small_case(34, lens)
+    ptab[0, :] = -1                        # both pages of sequence 0 (Lq = 64)
+    case.tables[0, 4:] = -1                # and its whole window
+    case.tables[1, :] = -1
+    pages = np.zeros((num_pages, 2, orc.KIVI_PAGE_BYTES), np.uint8)
+    got = orc.kivi_paged_attention(case.q, orc.F16, pages, ptab, case.k_cache, case.v_cache,
+                                   case.tables, case.seq_lens, 2, 128, case.scale, orc.GROUPED)
+    assert (got == 0).all()
+
+
+@pytest.mark.parametrize("code", [orc.F16, orc.BF16])
+def test_reshape_and_cache_fp8_is_scatter_of_e4m3_codes(code):
+    """orc_reshape_and_cache_fp8 = torch's float8_e4m3fn encode of
+    x * fp32(1 / scale) (an independent RNE implementation) scattered by the
+    slot map with numpy indexing; slot < 0 skipped, other slots untouched."""
+    rng = np.random.default_rng(35)
+    T, n_kv, D, BS, N = 37, 4, 64, 16, 9
+    xk = rng.standard_normal((T, n_kv, D), dtype=np.float32)
+    xv = rng.standard_normal((T, n_kv, D), dtype=np.float32) * 3
+    kb, vb = inputs.encode(xk, code), inputs.encode(xv, code)
+    kf, vf = orc.bits_to_f32(kb, code), orc.bits_to_f32(vb, code)
+    ks, vs = float(np.abs(kf).max()) / 448, float(np.abs(vf).max()) / 448
+    slots = rng.permutation(N * BS)[:T].astype(np.int32)
+    slots[[4, 20]] = -1
+    kc = rng.integers(0, 256, (N, n_kv, D, BS), dtype=np.uint8)
+    vc = rng.integers(0, 256, (N, n_kv, D, BS), dtype=np.uint8)
+    want_k, want_v = kc.copy(), vc.copy()
+    orc.reshape_and_cache_fp8(kb, vb, code, kc, vc, slots, ks, vs)
+
+    def e4m3(x, s):
+        mul = np.float32(1.0) / np.float32(s)
+        return torch.from_numpy(x * mul).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+
+    ck, cv = e4m3(kf, ks), e4m3(vf, vs)
+    for t, sl in enumerate(slots):
+        if sl < 0:
+            continue
+        want_k[sl // BS, :, :, sl % BS] = ck[t]
+        want_v[sl // BS, :, :, sl % BS] = cv[t]
+    assert np.array_equal(kc, want_k) and np.array_equal(vc, want_v)
+
+
 # ---------------------------------------------------------------------------
 # block management (copy_blocks / swap_blocks)
 # ---------------------------------------------------------------------------

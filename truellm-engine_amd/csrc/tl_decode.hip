@@ -319,7 +319,7 @@ template <Kind QK, Kind PO, int HEAD>
 __global__ __launch_bounds__(64) void lse_reduce_kernel(
     void* out, const float* part_m, const float* part_l, const void* part_o,
     const int32_t* seq_lens, int num_heads, int num_partitions, int partition_tokens,
-    int kivi_residual, int kivi_pages) {
+    int kivi_residual, int kivi_pages, int kivi_max_pages) {
   const int sh = blockIdx.x, seq = sh / num_heads;
   const int64_t pb = (int64_t)sh * num_partitions;
   // The partials are read for every partition slot (all in the workspace)
@@ -341,7 +341,8 @@ __global__ __launch_bounds__(64) void lse_reduce_kernel(
   const int L = seq_lens[seq];
   int np;
   if (kivi_pages > 0) {
-    const int pages = kivi_quantized_len(L, kivi_residual) / kKiviPageTokens;
+    // the page count of the decode kernel: clamped to the page table's width
+    const int pages = min(kivi_quantized_len(L, kivi_residual) / kKiviPageTokens, kivi_max_pages);
     np = max(1, (pages + kivi_pages - 1) / kivi_pages);
   } else {
     np = (L + partition_tokens - 1) / partition_tokens;
@@ -412,13 +413,13 @@ int launch_typed(const DecodeLaunch& a) {
                          dim3(kThreads), 0, a.stream, p);
       hipLaunchKernelGGL((lse_reduce_kernel<QK, Kind::F32, HEAD>), rgrid, dim3(64), 0, a.stream,
                          a.out, a.part_m, a.part_l, a.part_o, a.seq_lens, a.num_heads, P,
-                         a.partition_tokens, 0, 0);
+                         a.partition_tokens, 0, 0, 0);
     } else {
       hipLaunchKernelGGL((decode_kernel<KV, QK, QK, HEAD, BS, GT, false>), grid, dim3(kThreads),
                          0, a.stream, p);
       hipLaunchKernelGGL((lse_reduce_kernel<QK, QK, HEAD>), rgrid, dim3(64), 0, a.stream, a.out,
                          a.part_m, a.part_l, a.part_o, a.seq_lens, a.num_heads, P,
-                         a.partition_tokens, 0, 0);
+                         a.partition_tokens, 0, 0, 0);
     }
   }
   return hipGetLastError() == hipSuccess ? 0 : 5;
@@ -452,13 +453,13 @@ int launch_decode2(const DecodeLaunch& a) {
                          dim3(4 * kWave), 0, a.stream, p);
       hipLaunchKernelGGL((lse_reduce_kernel<KV, Kind::F32, HEAD>), rgrid, dim3(64), 0, a.stream,
                          a.out, a.part_m, a.part_l, a.part_o, a.seq_lens, a.num_heads, P,
-                         a.partition_tokens, 0, 0);
+                         a.partition_tokens, 0, 0, 0);
     } else {
       hipLaunchKernelGGL((decode2_kernel<KV, KV, HEAD, BS, 4, false>), dim3(items * P),
                          dim3(4 * kWave), 0, a.stream, p);
       hipLaunchKernelGGL((lse_reduce_kernel<KV, KV, HEAD>), rgrid, dim3(64), 0, a.stream, a.out,
                          a.part_m, a.part_l, a.part_o, a.seq_lens, a.num_heads, P,
-                         a.partition_tokens, 0, 0);
+                         a.partition_tokens, 0, 0, 0);
     }
   }
   return hipGetLastError() == hipSuccess ? 0 : 5;
@@ -496,17 +497,17 @@ int launch_shape(const DecodeLaunch& a) {
 int launch_lse_reduce(void* out, int q_dtype, const float* part_m, const float* part_l,
                       const void* part_o, int part_o_dtype, const int32_t* seq_lens, int num_seqs,
                       int num_heads, int head_size, int num_partitions, int partition_tokens,
-                      int kivi_residual, int kivi_pages, hipStream_t stream) {
+                      int kivi_residual, int kivi_pages, int kivi_max_pages, hipStream_t stream) {
   if (head_size != 128 || part_o_dtype != 0) return 3;
   const dim3 grid((unsigned)(num_seqs * num_heads));
   if (q_dtype == (int)Kind::F16)
     hipLaunchKernelGGL((lse_reduce_kernel<Kind::F16, Kind::F32, 128>), grid, dim3(64), 0, stream, out,
                        part_m, part_l, part_o, seq_lens, num_heads, num_partitions, partition_tokens,
-                       kivi_residual, kivi_pages);
+                       kivi_residual, kivi_pages, kivi_max_pages);
   else if (q_dtype == (int)Kind::BF16)
     hipLaunchKernelGGL((lse_reduce_kernel<Kind::BF16, Kind::F32, 128>), grid, dim3(64), 0, stream, out,
                        part_m, part_l, part_o, seq_lens, num_heads, num_partitions, partition_tokens,
-                       kivi_residual, kivi_pages);
+                       kivi_residual, kivi_pages, kivi_max_pages);
   else
     return 3;
   return hipGetLastError() == hipSuccess ? 0 : 5;

@@ -97,7 +97,7 @@ int launch_typed(const DecodeLaunch& a) {
   launch_kernel<KV, QK, 4, false>(p, items * P, a.stream);
   if (hipGetLastError() != hipSuccess) return 5;
   return launch_lse_reduce(a.out, a.q_dtype, a.part_m, a.part_l, a.part_o, a.part_o_dtype, a.seq_lens,
-                           a.num_seqs, a.num_heads, mw::kHead, P, a.partition_tokens, 0, 0, a.stream);
+                           a.num_seqs, a.num_heads, mw::kHead, P, a.partition_tokens, 0, 0, 0, a.stream);
 }
 
 }  // namespace

@@ -121,11 +121,11 @@ int launch_block_copy(const BlockCopy& c, hipStream_t stream);
 
 // Log-sum-exp merge of split-K partials into out.  The partitions a sequence
 // has are ceil(L / partition_tokens), or, for KIVI (kivi_pages > 0),
-// max(1, ceil(pages(L) / kivi_pages)).
+// max(1, ceil(min(pages(L), kivi_max_pages) / kivi_pages)).
 int launch_lse_reduce(void* out, int q_dtype, const float* part_m, const float* part_l,
                       const void* part_o, int part_o_dtype, const int32_t* seq_lens, int num_seqs,
                       int num_heads, int head_size, int num_partitions, int partition_tokens,
-                      int kivi_residual, int kivi_pages, hipStream_t stream);
+                      int kivi_residual, int kivi_pages, int kivi_max_pages, hipStream_t stream);
 
 // ---- KIVI ------------------------------------------------------------------
 int launch_kivi_vec(const void* in, void* out, int n_vecs, int head_dim, int n_outliers,
