@@ -88,6 +88,21 @@ int tl_paged_attention_decode(const tl_decode_desc* desc, void* out, const void*
                               int32_t max_context_len, void* workspace,
                               size_t workspace_bytes, void* stream);
 
+/* No counterpart in the reference.  tl_paged_attention_decode for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc): the split-K workspace is
+ * a library-owned device array of TL_NOALLOC_SCRATCH_BYTES that each GPU
+ * holds until the process ends; the call allocates nothing.  A plan whose
+ * workspace exceeds it returns TL_ERR_INVALID_ARGUMENT (query the size
+ * with tl_paged_attention_workspace_bytes).  Every call on one GPU shares
+ * that GPU's array: calls that overlap on one GPU (two streams or two
+ * threads) race. */
+#define TL_NOALLOC_SCRATCH_BYTES (32u << 20)
+int tl_paged_attention_decode_noalloc(const tl_decode_desc* desc, void* out, const void* q,
+                                      const void* k_cache, const void* v_cache,
+                                      const int32_t* block_tables, const int32_t* seq_lens,
+                                      int32_t max_context_len, void* stream);
+
 /* Replaces paged_attention_v1 (paged_attention_v1.cu:177-213): single pass,
  * same arguments plus the explicit sizes a TrueBuffer carried. */
 int tl_paged_attention_v1(void* out, const void* q, const void* k_cache, const void* v_cache,

@@ -129,6 +129,8 @@ size_t ws_bytes(const tl_decode_desc* d, int P) {
 
 }  // namespace
 
+int tl::report_error(int code, const char* msg) { return fail(code, "%s", msg); }
+
 extern "C" {
 
 int tl_abi_version(void) { return TL_ABI_VERSION; }

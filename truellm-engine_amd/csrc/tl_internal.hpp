@@ -188,4 +188,8 @@ int launch_prefill(const PrefillLaunch& a);
 int launch_fp8_scale(const void* x, int dtype, int64_t n, float* scale_out,
                      hipStream_t stream);
 
+// Sets the message tl_last_error_string() returns (this thread) and
+// returns code; for entry points defined outside tl_api.cpp.
+int report_error(int code, const char* msg);
+
 }  // namespace tl

@@ -103,6 +103,7 @@ _SIG = {
     "tl_last_error_string": (ctypes.c_char_p, []),
     "tl_paged_attention_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(DecodeDesc), _I]),
     "tl_paged_attention_decode": (ctypes.c_int, [ctypes.POINTER(DecodeDesc), _P, _P, _P, _P, _P, _P, _I, _P, ctypes.c_size_t, _P]),
+    "tl_paged_attention_decode_noalloc": (ctypes.c_int, [ctypes.POINTER(DecodeDesc), _P, _P, _P, _P, _P, _P, _I, _P]),
     "tl_paged_attention_v1": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F, _I, _I, _P]),
     "tl_paged_attention_v2": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F, _I, _I, _I, _P]),
     "tl_reshape_and_cache": (ctypes.c_int, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P]),
@@ -386,6 +387,17 @@ def paged_attention_decode(desc: DecodeDesc, out, q, k_cache, v_cache, block_tab
     check(lib.tl_paged_attention_decode(
         ctypes.byref(desc), _ptr(out), _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(block_tables),
         _ptr(seq_lens), max_context_len, _ptr(workspace), ws_bytes, _stream(stream)))
+
+
+NOALLOC_SCRATCH_BYTES = 32 << 20
+
+
+def paged_attention_decode_noalloc(desc: DecodeDesc, out, q, k_cache, v_cache, block_tables, seq_lens,
+                                   max_context_len, stream=None):
+    """tl_paged_attention_decode with the library's own split-K scratch (no allocation)."""
+    check(lib.tl_paged_attention_decode_noalloc(
+        ctypes.byref(desc), _ptr(out), _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(block_tables),
+        _ptr(seq_lens), max_context_len, _stream(stream)))
 
 
 # ---------------------------------------------------------------------------
