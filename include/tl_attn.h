@@ -63,8 +63,9 @@ typedef struct tl_decode_desc {
   int32_t num_seqs;            /* S */
   int32_t num_heads;           /* H (q heads); H % num_kv_heads == 0 */
   int32_t num_kv_heads;
-  int32_t head_size;           /* 64, 128 or 256 (128 for FP8/F32 KV) */
-  int32_t block_size;          /* 16, or 32 with head_size 128 */
+  int32_t head_size;           /* 128; 64 / 256 (and 80 / 96 for F16 / BF16 KV) */
+  int32_t block_size;          /* head 128: a power of two 8..256 (FP8: 16..256),
+                                  F32 KV and other heads: 16 */
   int32_t max_blocks_per_seq;  /* row stride of block_tables */
   int32_t num_blocks;          /* pool capacity N; table entries >= N are holes */
   int32_t q_dtype;             /* q and out: F16, BF16 (or F32 with F32 KV) */
@@ -112,11 +113,15 @@ int tl_paged_attention_v1(void* out, const void* q, const void* k_cache, const v
                           int32_t num_blocks, float scale, int32_t dtype, int32_t gqa_map,
                           void* stream);
 
-/* Replaces paged_attention_v2 (paged_attention_v2.cu:176-251): split-K over
- * partitions of 32 blocks with caller scratch exp_sums / max_logits
- * [S, H, P] fp32 and tmp_out [S, H, P, head_size] in dtype, where
- * P = ceil(max_context_len / (32 * block_size)) (the caller's sizing,
- * cuda_engine.cpp:276-285). */
+/* Replaces paged_attention_v2 (paged_attention_v2.cu:176-251).  The caller
+ * provides scratch exp_sums / max_logits [S, H, P] fp32 and tmp_out
+ * [S, H, P, head_size] in dtype, P = ceil(max_context_len / (32 *
+ * block_size)) (the engine's sizing, cuda_engine.cpp:276-285,1144), and
+ * reads none of it afterwards.  The call runs the library's own plan (as
+ * tl_paged_attention_decode with partition_tokens 0): single pass when the
+ * batch fills the GPU, else split-K with fp32 partials kept in that scratch
+ * (at most P * sizeof(dtype) / 4 partitions).  The scratch's contents after
+ * the call are not the reference's partials. */
 int tl_paged_attention_v2(void* out, float* exp_sums, float* max_logits, void* tmp_out,
                           const void* q, const void* k_cache, const void* v_cache,
                           const int32_t* block_tables, const int32_t* seq_lens,

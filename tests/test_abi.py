@@ -42,8 +42,14 @@ def _decode(d, out=FAKE, ws=None, ws_bytes=0, max_ctx=1024):
 @pytest.mark.parametrize("kw,code", [
     (dict(num_heads=30), tla.ERR_INVALID_ARGUMENT),
     (dict(num_kv_heads=0), tla.ERR_INVALID_ARGUMENT),
-    (dict(head_size=80), tla.ERR_NOT_IMPLEMENTED),
-    (dict(block_size=8), tla.ERR_NOT_IMPLEMENTED),
+    (dict(head_size=72), tla.ERR_NOT_IMPLEMENTED),
+    (dict(head_size=80, block_size=32), tla.ERR_NOT_IMPLEMENTED),
+    (dict(head_size=80, kv_dtype=tla.FP8_E4M3), tla.ERR_NOT_IMPLEMENTED),
+    (dict(head_size=64, block_size=8), tla.ERR_NOT_IMPLEMENTED),
+    (dict(block_size=12), tla.ERR_NOT_IMPLEMENTED),
+    (dict(block_size=512), tla.ERR_NOT_IMPLEMENTED),
+    (dict(block_size=8, kv_dtype=tla.FP8_E4M3), tla.ERR_NOT_IMPLEMENTED),
+    (dict(block_size=32, q_dtype=tla.F32, kv_dtype=tla.F32), tla.ERR_NOT_IMPLEMENTED),
     (dict(q_dtype=7), tla.ERR_INVALID_ARGUMENT),
     (dict(kv_dtype=tla.BF16), tla.ERR_NOT_IMPLEMENTED),
     (dict(kv_dtype=tla.FP8_E4M3, q_dtype=tla.F32), tla.ERR_NOT_IMPLEMENTED),
@@ -54,6 +60,22 @@ def _decode(d, out=FAKE, ws=None, ws_bytes=0, max_ctx=1024):
 def test_decode_rejects_bad_descriptors(kw, code):
     assert _decode(_desc(**kw)) == code
     assert tla.last_error()
+
+
+@pytest.mark.parametrize("kw", [
+    dict(block_size=8), dict(block_size=32), dict(block_size=64), dict(block_size=128),
+    dict(block_size=256), dict(block_size=16, kv_dtype=tla.FP8_E4M3),
+    dict(block_size=256, kv_dtype=tla.FP8_E4M3, q_dtype=tla.BF16), dict(head_size=80), dict(head_size=96),
+    dict(head_size=96, q_dtype=tla.BF16, kv_dtype=tla.BF16), dict(head_size=64, q_dtype=tla.F32, kv_dtype=tla.F32),
+    dict(head_size=256, q_dtype=tla.F32, kv_dtype=tla.F32), dict(head_size=256, kv_dtype=tla.FP8_E4M3),
+])
+def test_decode_accepts_the_built_shapes(kw):
+    """Head 128 with any power-of-two block size 8..256 (FP8 16..256), the
+    reference's F16 heads 64/80/96/256 and F32 heads 64/128/256 at block
+    size 16 (paged_attention_v1.cu:198-209): validation passes, so the
+    split-K plan has a workspace size."""
+    d = _desc(partition_tokens=512, **kw)
+    assert tla.workspace_bytes(d, 4096) == 4 * 32 * 8 * (d.head_size * 4 + 8), tla.last_error()
 
 
 def test_decode_rejects_null_and_missing_workspace():
@@ -90,7 +112,7 @@ def test_empty_batch_is_a_no_op():
 
 
 def test_v1_v2_reject_like_decode():
-    rc = tla.lib.tl_paged_attention_v1(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 4, 32, 8, 96, 16, 64,
+    rc = tla.lib.tl_paged_attention_v1(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 4, 32, 8, 72, 16, 64,
                                        512, 0.1, tla.F16, 0, None)
     assert rc == tla.ERR_NOT_IMPLEMENTED
     rc = tla.lib.tl_paged_attention_v2(FAKE, None, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 4, 32,

@@ -1,0 +1,219 @@
+"""Decode shapes beyond the headline one, and the paged_attention_v2 drop-in.
+
+- Head size 128 with every power-of-two block size the engine's
+  `paged_kv_block_size` may take (config_schema.h:68): 8 .. 256 for 2-byte
+  pools, 16 .. 256 for FP8 pools.
+- The reference's other dispatch shapes (paged_attention_v1.cu:198-209): F16
+  heads 80 and 96, F32 heads 64 and 256, at block size 16.
+- tl_paged_attention_v2 runs the library's plan inside the caller's scratch:
+  equal to the auto plan where that is single pass, never writing past the
+  scratch the engine sizes (cuda_engine.cpp:273-285,1144).
+
+Tolerance: max-abs 2e-3 (fp16 / bf16 / fp32 KV) or 1e-2 (FP8 KV, against
+attention on the dequantised pool), each plus half an output ulp."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import inputs
+import oracle_lib as orc
+import tl_attn as tla
+from gpu_util import assert_close, dev, host_f64
+
+pytestmark = pytest.mark.gpu
+
+ATOL = 2e-3
+ATOL_FP8 = 1e-2
+NAN_BITS = {orc.F16: 0x7E00, orc.BF16: 0x7FC0}
+
+
+def _ref(case, gqa):
+    return orc.paged_attention(case.q, case.code, case.k_cache, case.v_cache, case.code, case.tables,
+                               case.seq_lens, case.num_kv_heads, case.scale, gqa)
+
+
+def _poison_tails(case, code):
+    """NaN in the slots past each sequence's length in its last block."""
+    BS = case.k_cache.shape[3]
+    for s, L in enumerate(case.seq_lens):
+        L = int(L)
+        if L == 0:
+            continue
+        last = case.tables[s, (L - 1) // BS]
+        if last >= 0 and L % BS:
+            case.k_cache[last, :, :, L % BS:] = NAN_BITS[code]
+            case.v_cache[last, :, :, L % BS:] = NAN_BITS[code]
+
+
+def _decode(case, gqa, pt, kv_dtype=None, k_scale=1.0, v_scale=1.0, q=None, k=None, v=None):
+    q = dev(case.q, case.code) if q is None else q
+    k = dev(case.k_cache, case.code) if k is None else k
+    v = dev(case.v_cache, case.code) if v is None else v
+    bt, sl = dev(case.tables), dev(case.seq_lens)
+    max_ctx = int(case.seq_lens.max())
+    desc = tla.make_decode_desc(q, k, bt, case.num_kv_heads, case.scale, kv_dtype=kv_dtype, gqa_map=gqa,
+                                partition_tokens=pt, k_scale=k_scale, v_scale=v_scale)
+    ws = torch.empty(max(16, tla.workspace_bytes(desc, max_ctx)), dtype=torch.uint8, device="cuda")
+    out = torch.full_like(q, float("nan"))
+    tla.paged_attention_decode(desc, out, q, k, v, bt, sl, max_ctx, ws)
+    torch.cuda.synchronize()
+    return out
+
+
+LENS = [0, 1, 7, 8, 9, 31, 33, 255, 257, 513, 1500, 4100]
+
+
+@pytest.mark.parametrize("BS", [8, 16, 32, 64, 128, 256])
+@pytest.mark.parametrize("code", [orc.F16, orc.BF16])
+@pytest.mark.parametrize("pt", [-1, 512, 0])
+def test_head128_block_sizes(BS, code, pt):
+    """Ragged lengths across block and iteration edges, table holes, NaN in
+    the unused slots of the last blocks.  The short sequences (1 .. 9
+    tokens) also pin the precision of the bf16 softmax weights in p.v: one
+    bf16 rounding of the weights misses 2e-3 there."""
+    case = inputs.make_paged_case(70 + BS, len(LENS), 32, 8, 128, BS, LENS, code, holes=3)
+    _poison_tails(case, code)
+    for gqa in (tla.GQA_GROUPED, tla.GQA_MODULO):
+        print(f"case bs={BS} code={code} pt={pt} gqa={gqa}", flush=True)
+        out = _decode(case, gqa, pt)
+        assert_close(out, _ref(case, gqa), code, ATOL, f"bs={BS} pt={pt}")
+        assert (host_f64(out[0]) == 0).all()
+
+
+@pytest.mark.parametrize("BS", [8, 32, 256])
+def test_head128_block_sizes_group_8_and_mha(BS):
+    lens = [700, 2049, 65]
+    for H, n_kv in ((64, 8), (8, 8)):
+        case = inputs.make_paged_case(80 + BS, 3, H, n_kv, 128, BS, lens, orc.BF16, holes=1)
+        print(f"case bs={BS} H={H} n_kv={n_kv}", flush=True)
+        assert_close(_decode(case, tla.GQA_GROUPED, 512), _ref(case, tla.GQA_GROUPED), orc.BF16, ATOL,
+                     f"bs={BS} H={H}")
+
+
+@pytest.mark.parametrize("BS", [32, 64, 128, 256])
+@pytest.mark.parametrize("q_code", [orc.F16, orc.BF16])
+@pytest.mark.parametrize("pt", [-1, 512])
+def test_fp8_block_sizes(BS, q_code, pt):
+    lens = [1, 63, 65, 511, 2000, 4097]
+    base = inputs.make_paged_case(90 + BS, len(lens), 32, 8, 128, BS, lens, orc.F32, holes=2)
+    ks = float(np.abs(base.k_cache).max()) / 448.0
+    vs = float(np.abs(base.v_cache).max()) / 448.0
+    k8 = orc.f32_to_e4m3(base.k_cache, np.float32(1.0) / np.float32(ks))
+    v8 = orc.f32_to_e4m3(base.v_cache, np.float32(1.0) / np.float32(vs))
+    q = inputs.encode(orc.bits_to_f32(base.q, orc.F32), q_code)
+    for s, L in enumerate(lens):                  # NaN codes past the lengths
+        last = base.tables[s, (L - 1) // BS]
+        if last >= 0 and L % BS:
+            k8[last, :, :, L % BS:] = 0x7F
+            v8[last, :, :, L % BS:] = 0xFF
+    ref = orc.paged_attention(q, q_code, k8, v8, orc.FP8, base.tables, base.seq_lens, 8, base.scale,
+                              orc.GROUPED, 0, ks, vs)
+    print(f"case fp8 bs={BS} q={q_code} pt={pt}", flush=True)
+    out = _decode(base, tla.GQA_GROUPED, pt, kv_dtype=tla.FP8_E4M3, k_scale=ks, v_scale=vs, q=dev(q, q_code),
+                  k=torch.from_numpy(k8).cuda(), v=torch.from_numpy(v8).cuda())
+    assert_close(out, ref, q_code, ATOL_FP8, f"fp8 bs={BS}")
+
+
+@pytest.mark.parametrize("D,code", [(80, orc.F16), (96, orc.F16), (80, orc.BF16), (96, orc.BF16),
+                                    (64, orc.F32), (256, orc.F32), (64, orc.BF16), (256, orc.BF16)])
+@pytest.mark.parametrize("H,n_kv", [(8, 2), (4, 4)])
+def test_reference_dispatch_shapes(D, code, H, n_kv):
+    """F16 heads 80 / 96 and F32 heads 64 / 256 at block size 16, through
+    the v1 operator (single pass) and split-K; bf16 at the same heads (the
+    short sequences check the bf16 weights' precision)."""
+    lens = [1, 3, 7, 17, 600, 1300]
+    case = inputs.make_paged_case(100 + D, len(lens), H, n_kv, D, 16, lens, code, holes=1)
+    if code != orc.F32:
+        _poison_tails(case, code)
+    q, k, v, bt, sl = (dev(case.q, code), dev(case.k_cache, code), dev(case.v_cache, code), dev(case.tables),
+                       dev(case.seq_lens))
+    for gqa in (tla.GQA_MODULO, tla.GQA_GROUPED):
+        ref = _ref(case, gqa)
+        out = torch.full_like(q, float("nan"))
+        print(f"case v1 D={D} code={code} H={H} n_kv={n_kv} gqa={gqa}", flush=True)
+        tla.paged_attention_v1(out, q, k, v, bt, sl, n_kv, case.scale, D, 16, gqa_map=gqa)
+        torch.cuda.synchronize()
+        assert_close(out, ref, code, ATOL, f"v1 D={D}")
+        print(f"case split-K D={D} code={code} H={H} n_kv={n_kv} gqa={gqa}", flush=True)
+        assert_close(_decode(case, gqa, 512), ref, code, ATOL, f"split-K D={D}")
+
+
+# ---------------------------------------------------------------------------
+# paged_attention_v2 drop-in
+# ---------------------------------------------------------------------------
+
+GUARD = 4096
+
+
+def _v2_guarded(case, code, stream=None):
+    """tl_paged_attention_v2 with the engine's scratch sizes followed by
+    sentinel guards; returns (out, guards intact)."""
+    q, k, v, bt, sl = (dev(case.q, code), dev(case.k_cache, code), dev(case.v_cache, code), dev(case.tables),
+                       dev(case.seq_lens))
+    S, H, D = q.shape
+    BS = k.shape[3]
+    max_ctx = int(case.seq_lens.max())
+    P = tla.v2_num_partitions(max_ctx, BS)
+    n = S * H * P
+    es = torch.full((n + GUARD,), 7.25, dtype=torch.float32, device="cuda")
+    ml = torch.full((n + GUARD,), -3.5, dtype=torch.float32, device="cuda")
+    tmp = torch.full((n * D + GUARD,), 1.5, dtype=q.dtype, device="cuda")
+    out = torch.full_like(q, float("nan"))
+    tla.paged_attention_v2(out, es, ml, tmp, q, k, v, bt, sl, case.num_kv_heads, case.scale, D, BS, max_ctx,
+                           stream, gqa_map=tla.GQA_MODULO)
+    torch.cuda.synchronize()
+    intact = bool((es[n:] == 7.25).all() and (ml[n:] == -3.5).all() and (tmp[n * D:] == 1.5).all())
+    return out, intact
+
+
+def test_v2_at_batch_64_is_the_single_pass_kernel():
+    """Batch 64, ctx 4096, 32/8 heads, bf16: the plan is single pass, so v2
+    gives the bytes of tl_paged_attention_decode's auto plan."""
+    case = inputs.make_paged_case(inputs.SEEDS[1], 64, 32, 8, 128, 16, [4096] * 64, orc.BF16)
+    print("case v2 B=64 ctx 4096", flush=True)
+    a, intact = _v2_guarded(case, orc.BF16)
+    assert intact
+    b = _decode(case, tla.GQA_MODULO, 0)
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+    for s in (0, 63):
+        sub = inputs.PagedCase(case.q[s:s + 1], case.k_cache, case.v_cache, case.tables[s:s + 1],
+                               case.seq_lens[s:s + 1], case.code, 8, case.scale)
+        assert_close(a[s:s + 1], _ref(sub, orc.MODULO), orc.BF16, ATOL, f"seq {s}")
+
+
+@pytest.mark.parametrize("lens,code,BS", [
+    ([5000], orc.F16, 16),            # the engine's one-sequence call: capped partitions
+    ([529], orc.F16, 16),             # just past the engine's v2 threshold
+    ([16384], orc.BF16, 16),
+    ([3000, 700, 9000, 1], orc.F16, 16),
+    ([6000, 100], orc.F32, 16),       # 4-byte tmp_out: as many fp32 partitions as the engine's
+    ([5000, 33], orc.BF16, 64),
+])
+def test_v2_split_k_stays_inside_the_callers_scratch(lens, code, BS):
+    D = 128
+    case = inputs.make_paged_case(110 + len(lens), len(lens), 32, 8, D, BS, lens, code)
+    print(f"case v2 lens={lens} code={code} bs={BS}", flush=True)
+    out, intact = _v2_guarded(case, code)
+    assert intact, "v2 wrote past the caller's scratch"
+    assert_close(out, _ref(case, orc.MODULO), code, ATOL, f"v2 {lens}")
+
+
+def test_v2_misaligned_scratch_runs_single_pass():
+    """A tmp_out that is not 16-byte aligned is not used: the call runs
+    single pass and leaves the scratch as it was."""
+    case = inputs.make_paged_case(120, 2, 32, 8, 128, 16, [3000, 4000], orc.F16)
+    q, k, v, bt, sl = (dev(case.q, orc.F16), dev(case.k_cache, orc.F16), dev(case.v_cache, orc.F16),
+                       dev(case.tables), dev(case.seq_lens))
+    P = tla.v2_num_partitions(4000, 16)
+    es = torch.full((2 * 32 * P,), 7.25, dtype=torch.float32, device="cuda")
+    ml = torch.full((2 * 32 * P,), -3.5, dtype=torch.float32, device="cuda")
+    big = torch.full((2 * 32 * P * 128 + 8,), 1.5, dtype=torch.float16, device="cuda")
+    tmp = big[1:]                                  # 2-byte offset
+    out = torch.full_like(q, float("nan"))
+    print("case v2 misaligned tmp_out", flush=True)
+    tla.paged_attention_v2(out, es, ml, tmp, q, k, v, bt, sl, 8, case.scale, 128, 16, 4000, gqa_map=tla.GQA_MODULO)
+    torch.cuda.synchronize()
+    assert (es == 7.25).all() and (ml == -3.5).all() and (big == 1.5).all()
+    assert_close(out, _ref(case, orc.MODULO), orc.F16, ATOL, "v2 misaligned")

@@ -12,7 +12,7 @@ import torch
 import inputs
 import oracle_lib as orc
 import tl_attn as tla
-from gpu_util import dev
+from gpu_util import assert_close, dev
 
 pytestmark = pytest.mark.gpu
 
@@ -90,14 +90,33 @@ def test_v1_v2_shims_equal_c_abi():
 
 
 def test_v1_shim_unsupported_is_a_no_op():
-    case = inputs.make_paged_case(inputs.SEEDS[0], 2, 8, 2, 128, 16, [100, 50], orc.F16)
+    """Head size 72 is in no dispatch table (the reference asserts,
+    paged_attention_v1.cu:212): the operator leaves out untouched."""
+    case = inputs.make_paged_case(inputs.SEEDS[0], 2, 8, 2, 72, 16, [100, 50], orc.F16)
     q, k, v = dev(case.q, orc.F16), dev(case.k_cache, orc.F16), dev(case.v_cache, orc.F16)
+    bt, sl = dev(case.tables), dev(case.seq_lens)     # held: a view of a freed tensor may alias the next
     out = torch.full_like(q, 7.0)
-    V1(tb(out), tb(q), tb(k), tb(v), tb(dev(case.tables)), tb(dev(case.seq_lens)), 2, case.scale, 96, 16,
-       _stream())
+    V1(tb(out), tb(q), tb(k), tb(v), tb(bt), tb(sl), 2, case.scale, 72, 16, _stream())
     torch.cuda.synchronize()
     assert (out == 7.0).all()
-    assert "head_size=96" in tla.last_error()
+    assert "head_size=72" in tla.last_error()
+
+
+@pytest.mark.parametrize("D", [80, 96])
+def test_v1_shim_heads_80_and_96(D):
+    """The reference's F16 heads 80 and 96 (paged_attention_v1.cu:200-201)
+    through the C++ operator, against the oracle (MODULO map, as the
+    reference indexes)."""
+    case = inputs.make_paged_case(inputs.SEEDS[0] + D, 3, 8, 2, D, 16, [100, 50, 700], orc.F16)
+    q, k, v = dev(case.q, orc.F16), dev(case.k_cache, orc.F16), dev(case.v_cache, orc.F16)
+    bt, sl = dev(case.tables), dev(case.seq_lens)
+    out = torch.full_like(q, float("nan"))
+    print(f"case v1 shim D={D}", flush=True)
+    V1(tb(out), tb(q), tb(k), tb(v), tb(bt), tb(sl), 2, case.scale, D, 16, _stream())
+    torch.cuda.synchronize()
+    ref = orc.paged_attention(case.q, orc.F16, case.k_cache, case.v_cache, orc.F16, case.tables, case.seq_lens,
+                              2, case.scale, orc.MODULO)
+    assert_close(out, ref, orc.F16, 2e-3, f"v1 shim D={D}")
 
 
 def test_reshape_and_cache_shim_equals_c_abi():

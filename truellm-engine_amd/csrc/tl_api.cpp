@@ -54,14 +54,28 @@ int check_decode(const tl_decode_desc* d) {
                 d->kv_dtype, d->q_dtype);
   if (d->kv_dtype == TL_DTYPE_FP8_E4M3 && d->q_dtype == TL_DTYPE_F32)
     return fail(TL_ERR_NOT_IMPLEMENTED, "FP8 KV needs F16 or BF16 q");
-  const bool shape_ok =
-      (d->block_size == 16 && (d->head_size == 64 || d->head_size == 128 || d->head_size == 256)) ||
-      (d->block_size == 32 && d->head_size == 128);
+  // head size 128: the matrix-core decode, any power-of-two block size
+  // 8 .. 256 (16 .. 256 for FP8); the FMA decode: head sizes 64 / 256 (and
+  // 80 / 96 for 2-byte pools) at block size 16; F32 pools: head sizes 64 /
+  // 128 / 256 at block size 16 (the shapes of paged_attention_v1.cu:198-209)
+  const int hs = d->head_size, bs = d->block_size;
+  bool shape_ok;
+  if (d->kv_dtype == TL_DTYPE_F32)
+    shape_ok = bs == 16 && (hs == 64 || hs == 128 || hs == 256);
+  else if (hs == 128)
+    shape_ok = tl::decode_uses_mfma(d->kv_dtype, d->num_heads, d->num_kv_heads, hs, bs);
+  else if (hs == 64 || hs == 256)
+    shape_ok = bs == 16;
+  else if (hs == 80 || hs == 96)
+    shape_ok = bs == 16 && d->kv_dtype != TL_DTYPE_FP8_E4M3;
+  else
+    shape_ok = false;
   if (!shape_ok)
-    return fail(TL_ERR_NOT_IMPLEMENTED, "head_size=%d block_size=%d (built: 64/128/256 x 16, 128 x 32)",
-                d->head_size, d->block_size);
-  if (d->kv_dtype == TL_DTYPE_F32 && !(d->head_size == 128 && d->block_size == 16))
-    return fail(TL_ERR_NOT_IMPLEMENTED, "F32 KV is built for head_size 128, block_size 16 only");
+    return fail(TL_ERR_NOT_IMPLEMENTED,
+                "head_size=%d block_size=%d kv_dtype=%d (built: head 128 with block sizes 8..256, FP8 16..256; "
+                "heads 64/256, and 80/96 for 2-byte KV, with block size 16; F32 KV heads 64/128/256 with "
+                "block size 16)",
+                hs, bs, d->kv_dtype);
   if (d->partition_tokens != 0 && d->partition_tokens != -1 &&
       (d->partition_tokens <= 0 || d->partition_tokens % tl::kDecodeChunk))
     return fail(TL_ERR_INVALID_ARGUMENT, "partition_tokens=%d must be 0, -1 or a multiple of %d",
@@ -170,7 +184,6 @@ int tl_paged_attention_decode(const tl_decode_desc* desc, void* out, const void*
     a.part_o = workspace;
     a.part_m = (float*)((char*)workspace + sh * desc->head_size * 4);
     a.part_l = a.part_m + sh;
-    a.part_o_dtype = 0;
     a.num_partitions = P;
     a.partition_tokens = PT;
   }
@@ -212,21 +225,38 @@ int tl_paged_attention_v2(void* out, float* exp_sums, float* max_logits, void* t
     return fail(TL_ERR_INVALID_ARGUMENT, "NULL tensor pointer");
   if (!aligned16(k_cache) || !aligned16(v_cache))
     return fail(TL_ERR_INVALID_ARGUMENT, "k_cache/v_cache must be 16-byte aligned");
-  // Partitions of 32 blocks as the reference (PARTITION_SIZE, paged_attention_v2.cu:25);
-  // the count is taken with ceil so the tail block is kept.
-  const int PT = 32 * block_size;
-  if (PT % tl::kDecodeChunk)
-    return fail(TL_ERR_NOT_IMPLEMENTED, "block_size=%d: partitions of 32 blocks must be multiples of %d tokens",
-                block_size, tl::kDecodeChunk);
-  const int P = max_context_len > 0 ? (max_context_len + PT - 1) / PT : 1;
+  // The caller's scratch holds Pc = ceil(max_context_len / (32 block_size))
+  // partitions (the engine's sizing, cuda_engine.cpp:273-285,1144):
+  // exp_sums / max_logits fp32 [S, H, Pc], tmp_out [S, H, Pc, head_size]
+  // in the call's dtype.  The engine reads none of it after the call, so
+  // it is used as the workspace of the library's own plan: fp32 partials,
+  // the (max, sum) pairs in max_logits / exp_sums and the partial outputs
+  // in tmp_out's bytes, which hold Pc * elem / 4 fp32 partitions.  Where the
+  // plan wants more partitions than that, they are made longer; where it
+  // wants one (a large batch), the call runs single pass.
+  const int64_t part_tokens = 32LL * block_size;
+  const int Pc = max_context_len > 0 ? (int)((max_context_len + part_tokens - 1) / part_tokens) : 1;
+  const int elem = dtype == TL_DTYPE_F32 ? 4 : 2;
+  const int cap = aligned16(tmp_out) ? Pc * elem / 4 : 1;
+  int P, PT;
+  plan_partitions(&d, max_context_len, &P, &PT);
+  if (P > cap) {
+    if (cap <= 1) {
+      P = 1;
+    } else {
+      const int chunks = (max_context_len + tl::kDecodeChunk - 1) / tl::kDecodeChunk;
+      d.partition_tokens = (chunks + cap - 1) / cap * tl::kDecodeChunk;
+      plan_partitions(&d, max_context_len, &P, &PT);
+    }
+  }
   tl::DecodeLaunch a = make_launch(&d, out, q, k_cache, v_cache, block_tables, seq_lens, stream);
-  a.num_partitions = P;
-  a.partition_tokens = PT;
-  a.part_m = max_logits;
-  a.part_l = exp_sums;
-  a.part_o = tmp_out;
-  a.part_o_dtype = dtype;  // tmp_out holds q-dtype partials, as the caller sized it
-  // With one partition the kernel writes out directly and the scratch is unused.
+  if (P > 1) {
+    a.num_partitions = P;
+    a.partition_tokens = PT;
+    a.part_m = max_logits;
+    a.part_l = exp_sums;
+    a.part_o = tmp_out;
+  }
   return run(a);
 }
 

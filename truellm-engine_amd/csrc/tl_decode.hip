@@ -37,20 +37,35 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / kWave;
 
+// Lanes that share one block's chunks: CPB / 8 (8 loads per lane) when
+// that divides the wavefront, else the largest power of two up to 64 that
+// divides CPB (head sizes 80 and 96, 4-byte elements at head size 256).
+constexpr int lanes_per_block(int cpb) {
+  if (cpb % 8 == 0 && cpb / 8 <= kWave && kWave % (cpb / 8) == 0) return cpb / 8;
+  int l = kWave;
+  while (l > 1 && cpb % l) l >>= 1;
+  return l;
+}
+constexpr int pow2_ceil(int n) {
+  int p = 1;
+  while (p < n) p <<= 1;
+  return p;
+}
+
 template <Kind KV, int HEAD, int BS>
 struct Geometry {
   static constexpr int E = KindInfo<KV>::bytes;
   static constexpr int CT = 16 / E;            // tokens per 16-byte chunk
   static constexpr int CPR = BS / CT;          // chunks per head-dim row of a block
   static constexpr int CPB = HEAD * CPR;       // chunks per block (one kv head)
-  static constexpr int DPL = 8;                // loads per lane per wave iteration
-  static constexpr int LPB = CPB / DPL;        // lanes per block
+  static constexpr int LPB = lanes_per_block(CPB);  // lanes per block
+  static constexpr int DPL = CPB / LPB;        // loads per lane per wave iteration
   static constexpr int BPI = kWave / LPB;      // blocks per wave iteration
   static constexpr int TPI = BPI * BS;         // tokens per wave iteration
   static constexpr int NI = kDecodeChunk / (kWaves * TPI);  // iterations per chunk
   static constexpr int R = LPB / CPR;          // lanes sharing one token set
   static_assert(BS % CT == 0, "block size must hold whole 16-byte chunks");
-  static_assert(LPB >= 1 && LPB <= kWave && kWave % LPB == 0, "lane map");
+  static_assert(LPB >= CPR && LPB <= kWave && kWave % LPB == 0 && LPB * DPL == CPB, "lane map");
   static_assert(NI >= 1 && kDecodeChunk % (kWaves * TPI) == 0, "chunk split");
 };
 
@@ -89,6 +104,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(Params p) {
   constexpr int NV = GT * CT;                  // partial scores per lane
   constexpr int KEPT = transpose_kept<NV, LPB / 2, CPR>();
   constexpr int NA = GT * DPL;                 // output accumulators per lane
+  constexpr int NAP = pow2_ceil(NA);           // padded with zeros for the transpose-reduce
   constexpr int BLOCK_BYTES = HEAD * BS * Geo::E;
 
   __shared__ float s_q[GT][HEAD];
@@ -130,9 +146,9 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(Params p) {
 #pragma unroll
     for (int j = 0; j < DPL; ++j) qr[g][j] = s_q[g][j * R + dl];
 
-  float acc[NA];
+  float acc[NAP];
 #pragma unroll
-  for (int i = 0; i < NA; ++i) acc[i] = 0.f;
+  for (int i = 0; i < NAP; ++i) acc[i] = 0.f;
 
   const int32_t* table = p.block_tables + (int64_t)seq * p.max_blocks_per_seq;
   const int64_t head_off = (int64_t)kvh * BLOCK_BYTES + (int64_t)li * 16;
@@ -255,14 +271,14 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(Params p) {
 
   // ------------- reduce acc over lanes (block slot, token half) ------------
   int ab = 0;
-  constexpr int N1 = transpose_kept<NA, 32, LPB>();
-  if constexpr (LPB < kWave) ab += transpose_reduce<NA, 32, LPB>(acc, lane);
+  constexpr int N1 = (LPB < kWave) ? transpose_kept<NAP, 32, LPB>() : NAP;
+  if constexpr (LPB < kWave) ab += transpose_reduce<NAP, 32, LPB>(acc, lane);
   constexpr int N2 = (CPR > 1) ? transpose_kept<N1, CPR / 2, 1>() : N1;
   if constexpr (CPR > 1) ab += transpose_reduce<N1, CPR / 2, 1>(acc, lane);
 #pragma unroll
   for (int i = 0; i < N2; ++i) {
     const int a = ab + i, g = a / DPL, j = a % DPL;
-    s_u.red[wave][g][j * R + dl] = acc[i];
+    if (a < NA) s_u.red[wave][g][j * R + dl] = acc[i];
   }
   __syncthreads();
 
@@ -291,7 +307,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(Params p) {
 template <Kind KV, Kind PO, int HEAD, int BS, int NW, bool FINAL>
 __global__ __launch_bounds__(NW * kWave) void decode2_kernel(Params p) {
   constexpr int GT = kWaveHeads;
-  __shared__ __attribute__((aligned(16))) uint32_t s_p[NW][4][GT][4];
+  __shared__ __attribute__((aligned(16))) uint32_t s_p[NW][2][4][GT][4];   // weights (bf16: high, low)
   __shared__ float s_m[NW][GT], s_l[NW][GT];
   __shared__ float s_acc[NW][GT][HEAD];
 
@@ -306,7 +322,7 @@ __global__ __launch_bounds__(NW * kWave) void decode2_kernel(Params p) {
   if (!FINAL && t0 >= L) return;
   const int t1 = min(t0 + p.partition_tokens, L);
 
-  decode2_wave<KV, HEAD, BS>(p, seq, kvh, hs, t0 + wave * 32, t1, NW * 32, &s_p[wave][0][0][0],
+  decode2_wave<KV, HEAD, BS>(p, seq, kvh, hs, t0 + wave * 32, t1, NW * 32, &s_p[wave][0][0][0][0],
                              &s_acc[wave][0][0], &s_m[wave][0], &s_l[wave][0]);
   __syncthreads();
   combine_waves<KV, PO, HEAD, FINAL>(p, NW, &s_m[0][0], &s_l[0][0], &s_acc[0][0][0], seq, kvh, hs,
@@ -408,19 +424,11 @@ int launch_typed(const DecodeLaunch& a) {
   } else {
     dim3 grid((unsigned)(a.num_seqs * a.num_kv_heads * p.head_slices * P));
     dim3 rgrid((unsigned)(a.num_seqs * a.num_heads));
-    if (a.part_o_dtype == 0) {
-      hipLaunchKernelGGL((decode_kernel<KV, QK, Kind::F32, HEAD, BS, GT, false>), grid,
-                         dim3(kThreads), 0, a.stream, p);
-      hipLaunchKernelGGL((lse_reduce_kernel<QK, Kind::F32, HEAD>), rgrid, dim3(64), 0, a.stream,
-                         a.out, a.part_m, a.part_l, a.part_o, a.seq_lens, a.num_heads, P,
-                         a.partition_tokens, 0, 0, 0);
-    } else {
-      hipLaunchKernelGGL((decode_kernel<KV, QK, QK, HEAD, BS, GT, false>), grid, dim3(kThreads),
-                         0, a.stream, p);
-      hipLaunchKernelGGL((lse_reduce_kernel<QK, QK, HEAD>), rgrid, dim3(64), 0, a.stream, a.out,
-                         a.part_m, a.part_l, a.part_o, a.seq_lens, a.num_heads, P,
-                         a.partition_tokens, 0, 0, 0);
-    }
+    hipLaunchKernelGGL((decode_kernel<KV, QK, Kind::F32, HEAD, BS, GT, false>), grid,
+                       dim3(kThreads), 0, a.stream, p);
+    hipLaunchKernelGGL((lse_reduce_kernel<QK, Kind::F32, HEAD>), rgrid, dim3(64), 0, a.stream,
+                       a.out, a.part_m, a.part_l, a.part_o, a.seq_lens, a.num_heads, P,
+                       a.partition_tokens, 0, 0, 0);
   }
   return hipGetLastError() == hipSuccess ? 0 : 5;
 }
@@ -448,19 +456,11 @@ int launch_decode2(const DecodeLaunch& a) {
                        a.stream, p);
   } else {
     dim3 rgrid((unsigned)(a.num_seqs * a.num_heads));
-    if (a.part_o_dtype == 0) {
-      hipLaunchKernelGGL((decode2_kernel<KV, Kind::F32, HEAD, BS, 4, false>), dim3(items * P),
-                         dim3(4 * kWave), 0, a.stream, p);
-      hipLaunchKernelGGL((lse_reduce_kernel<KV, Kind::F32, HEAD>), rgrid, dim3(64), 0, a.stream,
-                         a.out, a.part_m, a.part_l, a.part_o, a.seq_lens, a.num_heads, P,
-                         a.partition_tokens, 0, 0, 0);
-    } else {
-      hipLaunchKernelGGL((decode2_kernel<KV, KV, HEAD, BS, 4, false>), dim3(items * P),
-                         dim3(4 * kWave), 0, a.stream, p);
-      hipLaunchKernelGGL((lse_reduce_kernel<KV, KV, HEAD>), rgrid, dim3(64), 0, a.stream, a.out,
-                         a.part_m, a.part_l, a.part_o, a.seq_lens, a.num_heads, P,
-                         a.partition_tokens, 0, 0, 0);
-    }
+    hipLaunchKernelGGL((decode2_kernel<KV, Kind::F32, HEAD, BS, 4, false>), dim3(items * P),
+                       dim3(4 * kWave), 0, a.stream, p);
+    hipLaunchKernelGGL((lse_reduce_kernel<KV, Kind::F32, HEAD>), rgrid, dim3(64), 0, a.stream,
+                       a.out, a.part_m, a.part_l, a.part_o, a.seq_lens, a.num_heads, P,
+                       a.partition_tokens, 0, 0, 0);
   }
   return hipGetLastError() == hipSuccess ? 0 : 5;
 }
@@ -468,37 +468,41 @@ int launch_decode2(const DecodeLaunch& a) {
 template <Kind KV, Kind QK, int HEAD, int BS>
 int launch_gt(const DecodeLaunch& a) {
   const int group = a.num_heads / a.num_kv_heads;
-  if (a.use_generic == 0 &&
-      decode_uses_mfma(a.kv_dtype, a.num_heads, a.num_kv_heads, a.head_size, a.block_size)) {
-    const int rc = launch_decode_mfma(a);
-    if (rc != 3) return rc;
-  }
   if (group == 1) return launch_typed<KV, QK, HEAD, BS, 1>(a);
-  if constexpr ((KV == Kind::F16 || KV == Kind::BF16) && QK == KV && (HEAD == 64 || HEAD == 128)) {
-    if (a.use_generic == 0) return launch_decode2<KV, HEAD, BS>(a);
-  }
+  if constexpr ((KV == Kind::F16 || KV == Kind::BF16) && QK == KV && HEAD == 64)
+    return launch_decode2<KV, HEAD, BS>(a);
   return launch_typed<KV, QK, HEAD, BS, 4>(a);
 }
 
+// The shapes of the FMA kernels: head sizes 64 and 256 (every pool dtype),
+// 80 and 96 (2-byte pools), 128 for F32 pools; block size 16.  Head size
+// 128 with a 2-byte or FP8 pool runs on the matrix cores.
 template <Kind KV, Kind QK>
 int launch_shape(const DecodeLaunch& a) {
-  if (a.block_size == 16) {
-    if (a.head_size == 128) return launch_gt<KV, QK, 128, 16>(a);
-    if (a.head_size == 64) return launch_gt<KV, QK, 64, 16>(a);
-    if (a.head_size == 256) return launch_gt<KV, QK, 256, 16>(a);
-  } else if (a.block_size == 32) {
-    if (a.head_size == 128) return launch_gt<KV, QK, 128, 32>(a);
+  if (a.block_size != 16) return 3;
+  switch (a.head_size) {
+    case 64: return launch_gt<KV, QK, 64, 16>(a);
+    case 256: return launch_gt<KV, QK, 256, 16>(a);
+    case 80:
+      if constexpr (KV == Kind::F16 || KV == Kind::BF16) return launch_gt<KV, QK, 80, 16>(a);
+      return 3;
+    case 96:
+      if constexpr (KV == Kind::F16 || KV == Kind::BF16) return launch_gt<KV, QK, 96, 16>(a);
+      return 3;
+    case 128:
+      if constexpr (KV == Kind::F32) return launch_gt<KV, QK, 128, 16>(a);
+      return 3;
+    default: return 3;
   }
-  return 3;
 }
 
 }  // namespace
 
 int launch_lse_reduce(void* out, int q_dtype, const float* part_m, const float* part_l,
-                      const void* part_o, int part_o_dtype, const int32_t* seq_lens, int num_seqs,
+                      const void* part_o, const int32_t* seq_lens, int num_seqs,
                       int num_heads, int head_size, int num_partitions, int partition_tokens,
                       int kivi_residual, int kivi_pages, int kivi_max_pages, hipStream_t stream) {
-  if (head_size != 128 || part_o_dtype != 0) return 3;
+  if (head_size != 128) return 3;
   const dim3 grid((unsigned)(num_seqs * num_heads));
   if (q_dtype == (int)Kind::F16)
     hipLaunchKernelGGL((lse_reduce_kernel<Kind::F16, Kind::F32, 128>), grid, dim3(64), 0, stream, out,
@@ -515,12 +519,13 @@ int launch_lse_reduce(void* out, int q_dtype, const float* part_m, const float* 
 
 int launch_decode(const DecodeLaunch& a) {
   const Kind kv = (Kind)a.kv_dtype, qk = (Kind)a.q_dtype;
+  if (decode_uses_mfma(a.kv_dtype, a.num_heads, a.num_kv_heads, a.head_size, a.block_size))
+    return launch_decode_mfma(a);
   if (kv == Kind::F16 && qk == Kind::F16) return launch_shape<Kind::F16, Kind::F16>(a);
   if (kv == Kind::BF16 && qk == Kind::BF16) return launch_shape<Kind::BF16, Kind::BF16>(a);
   if (kv == Kind::FP8 && qk == Kind::F16) return launch_shape<Kind::FP8, Kind::F16>(a);
   if (kv == Kind::FP8 && qk == Kind::BF16) return launch_shape<Kind::FP8, Kind::BF16>(a);
-  if (kv == Kind::F32 && qk == Kind::F32 && a.block_size == 16 && a.head_size == 128)
-    return launch_gt<Kind::F32, Kind::F32, 128, 16>(a);
+  if (kv == Kind::F32 && qk == Kind::F32) return launch_shape<Kind::F32, Kind::F32>(a);
   return 3;
 }
 

@@ -1,5 +1,6 @@
 // tl_decode_mfma.hip -- paged-attention decode on the matrix cores
-// (head_size 128, block_size 16), for FP8 E4M3 KV and for 2-byte KV.
+// (head_size 128; block sizes 8 .. 256 for 2-byte KV, 16 .. 256 for FP8
+// E4M3 KV).
 //
 // The wavefronts are in tl_mfma_wave.hpp.  Why matrix cores for decode:
 //   * FP8: a byte is one element, so per byte of HBM traffic there are twice
@@ -41,34 +42,35 @@ __device__ __forceinline__ bool item_of(const Params& p, bool final, Item& w) {
   return true;
 }
 
-template <Kind QK, Kind PO, int NW, bool FINAL>
+template <Kind QK, Kind PO, int NW, bool FINAL, int BS>
 __global__ __launch_bounds__(NW * kWave) void fp8_decode_kernel(Params p) {
   __shared__ __attribute__((aligned(16))) float s_acc[NW * mw::kHeads * mw::kHead];
   __shared__ float s_m[NW * mw::kHeads], s_l[NW * mw::kHeads];
   Item w;
   if (!item_of(p, FINAL, w)) return;
-  mw::decode_workgroup<Kind::FP8, QK, PO, NW, FINAL>(p, w.seq, w.kvh, w.hs, w.part, w.t0, w.t1, s_acc, s_m, s_l);
+  mw::decode_workgroup<Kind::FP8, QK, PO, NW, FINAL, BS>(p, w.seq, w.kvh, w.hs, w.part, w.t0, w.t1, s_acc, s_m,
+                                                         s_l);
 }
 
-template <Kind KV, Kind PO, int NW, bool FINAL>
+template <Kind KV, Kind PO, int NW, bool FINAL, int BS>
 __global__ __launch_bounds__(NW * kWave) void mfma2_decode_kernel(Params p) {
   __shared__ __attribute__((aligned(16))) float s_acc[NW * mw::kHeads * mw::kHead];
   __shared__ float s_m[NW * mw::kHeads], s_l[NW * mw::kHeads];
   Item w;
   if (!item_of(p, FINAL, w)) return;
-  mw::decode_workgroup<KV, KV, PO, NW, FINAL>(p, w.seq, w.kvh, w.hs, w.part, w.t0, w.t1, s_acc, s_m, s_l);
+  mw::decode_workgroup<KV, KV, PO, NW, FINAL, BS>(p, w.seq, w.kvh, w.hs, w.part, w.t0, w.t1, s_acc, s_m, s_l);
 }
 
-template <Kind KV, Kind QK, int NW, bool FINAL>
+template <Kind KV, Kind QK, int NW, bool FINAL, int BS>
 void launch_kernel(const Params& p, unsigned grid, hipStream_t stream) {
   constexpr Kind PO = FINAL ? QK : Kind::F32;
   if constexpr (KV == Kind::FP8)
-    hipLaunchKernelGGL((fp8_decode_kernel<QK, PO, NW, FINAL>), dim3(grid), dim3(NW * kWave), 0, stream, p);
+    hipLaunchKernelGGL((fp8_decode_kernel<QK, PO, NW, FINAL, BS>), dim3(grid), dim3(NW * kWave), 0, stream, p);
   else
-    hipLaunchKernelGGL((mfma2_decode_kernel<KV, PO, NW, FINAL>), dim3(grid), dim3(NW * kWave), 0, stream, p);
+    hipLaunchKernelGGL((mfma2_decode_kernel<KV, PO, NW, FINAL, BS>), dim3(grid), dim3(NW * kWave), 0, stream, p);
 }
 
-template <Kind KV, Kind QK>
+template <Kind KV, Kind QK, int BS>
 int launch_typed(const DecodeLaunch& a) {
   Params p;
   p.out = a.out; p.q = a.q;
@@ -91,26 +93,41 @@ int launch_typed(const DecodeLaunch& a) {
     // grid of a large batch is resident in one round (B=64, ctx 4096:
     // 6.69 against 6.64 TB/s with 8)
     p.partition_tokens = 0x7fffffff;
-    launch_kernel<KV, QK, 4, true>(p, items, a.stream);
+    launch_kernel<KV, QK, 4, true, BS>(p, items, a.stream);
     return hipGetLastError() == hipSuccess ? 0 : 5;
   }
-  launch_kernel<KV, QK, 4, false>(p, items * P, a.stream);
+  launch_kernel<KV, QK, 4, false, BS>(p, items * P, a.stream);
   if (hipGetLastError() != hipSuccess) return 5;
-  return launch_lse_reduce(a.out, a.q_dtype, a.part_m, a.part_l, a.part_o, a.part_o_dtype, a.seq_lens,
+  return launch_lse_reduce(a.out, a.q_dtype, a.part_m, a.part_l, a.part_o, a.seq_lens,
                            a.num_seqs, a.num_heads, mw::kHead, P, a.partition_tokens, 0, 0, 0, a.stream);
+}
+
+template <Kind KV, Kind QK>
+int launch_bs(const DecodeLaunch& a) {
+  switch (a.block_size) {
+    case 8:
+      if constexpr (KV != Kind::FP8) return launch_typed<KV, QK, 8>(a);   // a 16-byte FP8 V run spans two blocks
+      return 3;
+    case 16: return launch_typed<KV, QK, 16>(a);
+    case 32: return launch_typed<KV, QK, 32>(a);
+    case 64: return launch_typed<KV, QK, 64>(a);
+    case 128: return launch_typed<KV, QK, 128>(a);
+    case 256: return launch_typed<KV, QK, 256>(a);
+    default: return 3;
+  }
 }
 
 }  // namespace
 
 int launch_decode_mfma(const DecodeLaunch& a) {
   const Kind kv = (Kind)a.kv_dtype, qk = (Kind)a.q_dtype;
-  if (a.head_size != mw::kHead || a.block_size != 16) return 3;
+  if (!decode_uses_mfma(a.kv_dtype, a.num_heads, a.num_kv_heads, a.head_size, a.block_size)) return 3;
   const int tpi = kv == Kind::FP8 ? mw::tokens_per_iteration<Kind::FP8>() : mw::tokens_per_iteration<Kind::F16>();
-  if (a.num_partitions > 1 && (a.partition_tokens % tpi || a.part_o_dtype != 0)) return 3;
-  if (kv == Kind::FP8 && qk == Kind::F16) return launch_typed<Kind::FP8, Kind::F16>(a);
-  if (kv == Kind::FP8 && qk == Kind::BF16) return launch_typed<Kind::FP8, Kind::BF16>(a);
-  if (kv == Kind::F16 && qk == Kind::F16) return launch_typed<Kind::F16, Kind::F16>(a);
-  if (kv == Kind::BF16 && qk == Kind::BF16) return launch_typed<Kind::BF16, Kind::BF16>(a);
+  if (a.num_partitions > 1 && a.partition_tokens % tpi) return 3;
+  if (kv == Kind::FP8 && qk == Kind::F16) return launch_bs<Kind::FP8, Kind::F16>(a);
+  if (kv == Kind::FP8 && qk == Kind::BF16) return launch_bs<Kind::FP8, Kind::BF16>(a);
+  if (kv == Kind::F16 && qk == Kind::F16) return launch_bs<Kind::F16, Kind::F16>(a);
+  if (kv == Kind::BF16 && qk == Kind::BF16) return launch_bs<Kind::BF16, Kind::BF16>(a);
   return 3;
 }
 

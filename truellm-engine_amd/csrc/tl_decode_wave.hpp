@@ -27,6 +27,9 @@ namespace tl {
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kWaveHeads = 4;   // q heads served per wavefront
+// words of one weight exchange area ([4][kWaveHeads][4]); bf16 keeps the
+// weights' low parts in a second area right after it
+constexpr int kLoWords = 4 * kWaveHeads * 4;
 
 struct Params {
   void* out;
@@ -102,7 +105,8 @@ __device__ __forceinline__ void load_v_rows(u32x4 (&vr)[VD], const char* blk, in
 
 // Runs one wavefront over its iterations and leaves its state in LDS:
 // s_acc_w [4][HEAD] unnormalised outputs, s_m_w [4] running max (log2 units),
-// s_l_w [4] sums.  s_p_w is the wavefront's [4][4][4] weight exchange area.
+// s_l_w [4] sums.  s_p_w is the wavefront's weight exchange area: [4][4][4]
+// words, twice that for bf16 (the weights' high and low bf16 parts).
 template <Kind KV, int HEAD, int BS>
 __device__ __forceinline__ void decode2_wave(const Params& p, int seq, int kvh, int hs, int first_it,
                                              int t1, int step, uint32_t* s_p_w, float* s_acc_w,
@@ -210,7 +214,14 @@ __device__ __forceinline__ void decode2_wave(const Params& p, int seq, int kvh, 
     const float p0 = ok0 ? __builtin_amdgcn_exp2f(sc0 - m_lane) : 0.f;
     const float p1 = ok1 ? __builtin_amdgcn_exp2f(sc1 - m_lane) : 0.f;
     l_lane += p0 + p1;
-    s_p_w[(tg * GT + g_lane) * 4 + tp] = D2::pack(p0, p1);
+    const uint32_t p01 = D2::pack(p0, p1);
+    s_p_w[(tg * GT + g_lane) * 4 + tp] = p01;
+    if constexpr (KV == Kind::BF16) {
+      // bf16 weights carry 8 mantissa bits (a short or peaked softmax would
+      // miss 2e-3 by up to 2^-9 max|v|): the rest goes in a second bf16
+      const float h0 = __builtin_bit_cast(float, p01 << 16), h1 = __builtin_bit_cast(float, p01 & 0xffff0000u);
+      s_p_w[kLoWords + (tg * GT + g_lane) * 4 + tp] = D2::pack(p0 - h0, p1 - h1);
+    }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -231,16 +242,22 @@ __device__ __forceinline__ void decode2_wave(const Params& p, int seq, int kvh, 
     }
 
     // ---- p.v over token pairs ----
-    u32x4 pp[GT];
+    u32x4 pp[GT], pl[GT];
 #pragma unroll
-    for (int g = 0; g < GT; ++g) pp[g] = *reinterpret_cast<const u32x4*>(&s_p_w[(tg * GT + g) * 4]);
+    for (int g = 0; g < GT; ++g) {
+      pp[g] = *reinterpret_cast<const u32x4*>(&s_p_w[(tg * GT + g) * 4]);
+      if constexpr (KV == Kind::BF16) pl[g] = *reinterpret_cast<const u32x4*>(&s_p_w[kLoWords + (tg * GT + g) * 4]);
+    }
 #pragma unroll
     for (int j = 0; j < VD; ++j)
 #pragma unroll
       for (int g = 0; g < GT; ++g) {
         float a = acc[g][j];
 #pragma unroll
-        for (int w = 0; w < 4; ++w) a = D2::dot(word(pp[g], w), word(vr[j], w), a);
+        for (int w = 0; w < 4; ++w) {
+          a = D2::dot(word(pp[g], w), word(vr[j], w), a);
+          if constexpr (KV == Kind::BF16) a = D2::dot(word(pl[g], w), word(vr[j], w), a);
+        }
         acc[g][j] = a;
       }
     if (has_next)

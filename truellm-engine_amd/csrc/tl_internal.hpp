@@ -22,14 +22,12 @@ struct DecodeLaunch {
   float* part_m;                // [S, H, P] (split-K only)
   float* part_l;                // [S, H, P]
   void* part_o;                 // [S, H, P, D]
-  int part_o_dtype;             // 0 = f32, else the q dtype
   int num_seqs, num_heads, num_kv_heads, head_size, block_size;
   int max_blocks_per_seq, num_blocks;
   int num_partitions;           // 1 = single pass
   int partition_tokens;         // multiple of kDecodeChunk when P > 1
   int q_dtype, kv_dtype, gqa_map;
   float scale, k_scale, v_scale;
-  int use_generic;              // 1 = force the generic (FMA) decode kernel
   hipStream_t stream;
 };
 
@@ -50,8 +48,10 @@ int launch_decode_mfma(const DecodeLaunch& a);
 // 3.0 TB/s).
 inline bool decode_uses_mfma(int kv_dtype, int num_heads, int num_kv_heads, int head_size, int block_size) {
   (void)num_heads;
-  if (head_size != 128 || block_size != 16 || num_kv_heads <= 0) return false;
-  return kv_dtype == 32 || kv_dtype == 1 || kv_dtype == 2;   // FP8 E4M3, f16, bf16
+  if (head_size != 128 || num_kv_heads <= 0) return false;
+  const bool pow2 = block_size > 0 && (block_size & (block_size - 1)) == 0 && block_size <= 256;
+  if (kv_dtype == 32) return pow2 && block_size >= 16;                   // FP8 E4M3
+  return (kv_dtype == 1 || kv_dtype == 2) && pow2 && block_size >= 8;     // f16, bf16
 }
 
 struct CacheLaunch {
@@ -123,7 +123,7 @@ int launch_block_copy(const BlockCopy& c, hipStream_t stream);
 // has are ceil(L / partition_tokens), or, for KIVI (kivi_pages > 0),
 // max(1, ceil(min(pages(L), kivi_max_pages) / kivi_pages)).
 int launch_lse_reduce(void* out, int q_dtype, const float* part_m, const float* part_l,
-                      const void* part_o, int part_o_dtype, const int32_t* seq_lens, int num_seqs,
+                      const void* part_o, const int32_t* seq_lens, int num_seqs,
                       int num_heads, int head_size, int num_partitions, int partition_tokens,
                       int kivi_residual, int kivi_pages, int kivi_max_pages, hipStream_t stream);
 

@@ -603,7 +603,7 @@ int launch_kivi_decode(const KiviDecodeLaunch& a) {
   } else {
     launch_decode<4, false>(k, append, items * a.num_partitions, a.stream);
     if (hipGetLastError() != hipSuccess) return 5;
-    return launch_lse_reduce(a.out, (int)Kind::F16, a.part_m, a.part_l, a.part_o, 0, a.seq_lens,
+    return launch_lse_reduce(a.out, (int)Kind::F16, a.part_m, a.part_l, a.part_o, a.seq_lens,
                              a.num_seqs, a.num_heads, kKiviHead, a.num_partitions, 0,
                              a.residual_length, a.partition_pages, a.max_pages_per_seq, a.stream);
   }

@@ -1,5 +1,8 @@
 // tl_mfma_wave.hpp -- decode wavefronts on the matrix cores for head_size
-// 128, block_size 16: FP8 E4M3 KV (fp8_wave) and 2-byte KV (mfma2_wave).
+// 128: FP8 E4M3 KV (fp8_wave, block sizes 16 .. 256) and 2-byte KV
+// (mfma2_wave, block sizes 8 .. 256).  An iteration covers 64 (FP8) or 32
+// (2-byte) consecutive tokens: several blocks when the block is smaller, a
+// part of one block (at the iteration's offset in it) when it is larger.
 //
 // Both put the q heads on the 16 columns of v_mfma_f32_16x16x32_{f16,bf16},
 // so one KV read serves up to 16 heads of a GQA group, and both keep the
@@ -8,9 +11,9 @@
 //   q.k, S^T[token][head] = K^T q^T.  The contraction runs over head dims,
 //     the pool keeps tokens contiguous ([D][BS] per block), so K is
 //     transposed in registers: a lane reads dwords of rows d = 4 j + kg
-//     (j < 32; for each j the wavefront reads rows 4 j .. 4 j + 3, 64 or 128
-//     contiguous bytes per block), and one v_perm_b32 per output dword pairs
-//     two rows per token.  MFMA step s (k = 32) holds head dim
+//     (j < 32; for each j the wavefront reads rows 4 j .. 4 j + 3 of the
+//     iteration's tokens), and one v_perm_b32 per output dword pairs two
+//     rows per token.  MFMA step s (k = 32) holds head dim
 //     32 s + 4 e + kg in slot e of lane group kg; q is loaded in that order.
 //   p.v, O^T[d][head] = V P^T.  A lane's score registers hold its head's
 //     weights for a contiguous run of tokens that is exactly one k group of
@@ -73,14 +76,22 @@ __device__ __forceinline__ float sum_kg(float v) {
   return swap16_add(v, v);
 }
 
+// The blocks an iteration of TPI tokens starting at token it touches: NB
+// blocks of BS tokens (BS < TPI), or the one block holding it (BS >= TPI).
+template <int BS, int TPI> constexpr int blocks_per_iteration() { return BS >= TPI ? 1 : TPI / BS; }
+// Byte offset of token it inside its block's rows (elements of E bytes):
+// non-zero only when a block holds more than one iteration.
+template <int BS, int TPI, int E>
+__device__ __forceinline__ int in_block_bytes(int it) { return BS > TPI ? E * (it % BS) : 0; }
+
 // Physical blocks of the NB blocks starting at token it (-1: hole, past t1
 // or outside the pool).
 template <int NB> struct Blocks { int e[NB]; };
-template <int NB>
+template <int NB, int BS>
 __device__ __forceinline__ Blocks<NB> table_blocks(const Params& p, const int32_t* table, int it, int t1) {
   Blocks<NB> b;
 #pragma unroll
-  for (int i = 0; i < NB; ++i) b.e[i] = table_entry_bs<16>(p, table, it + 16 * i, t1);
+  for (int i = 0; i < NB; ++i) b.e[i] = table_entry_bs<BS>(p, table, it + BS * i, t1);
   return b;
 }
 // Entry i (per lane) of a wave-uniform set.  Written as one nested select:
@@ -88,9 +99,10 @@ __device__ __forceinline__ Blocks<NB> table_blocks(const Params& p, const int32_
 // set in LDS.
 template <int NB>
 __device__ __forceinline__ int pick(const Blocks<NB>& b, int i) {
-  static_assert(NB == 2 || NB == 4, "2 or 4 blocks per iteration");
+  static_assert(NB == 1 || NB == 2 || NB == 4, "1, 2 or 4 blocks per iteration");
   if constexpr (NB == 4) return i == 0 ? b.e[0] : i == 1 ? b.e[1] : i == 2 ? b.e[2] : b.e[3];
-  else return i == 0 ? b.e[0] : b.e[1];
+  else if constexpr (NB == 2) return i == 0 ? b.e[0] : b.e[1];
+  else return b.e[0];
 }
 
 // Zeroes the bytes of tokens >= n (0 <= n <= 16) of a 16-token FP8 row.
@@ -152,26 +164,31 @@ struct State {
   }
 };
 
-// ---- FP8 E4M3 KV, f16 / bf16 q: 64 tokens (4 blocks) per iteration ----
+// ---- FP8 E4M3 KV, f16 / bf16 q: 64 tokens per iteration ----
 //
-// K: the A row m is token quad m (block m >> 2, tokens 4 (m & 3) .. +3) and
-// tile i takes token i of every quad.  Lane (m, kg) reads 32 dwords (64
-// contiguous bytes per block for each j); one v_perm_b32 stage pairs the
-// bytes of two rows per token, and the converter's (bytes 0,1) / (bytes
-// 2,3) halves are then exactly the f16 (d, d') pairs of one token: 1 perm
-// and 2 converts per 4 bytes.  v_cvt_scalef32_pk_f16_fp8 with scale 1 is
-// exact: every E4M3 value, subnormals and NaN included, is an f16 value.
-// Scores: lane (m, kg) holds head m, token 4 r + i of block kg.
-// V: lane (m, kg) loads 16 bytes, row d = 16 dt + m of block kg; MFMA h
+// K: the A row m is token quad m (iteration tokens 4 m .. 4 m + 3) and tile
+// i takes token i of every quad.  Lane (m, kg) reads 32 dwords, rows
+// 4 j + kg of its quad (at block size 16 the wavefront reads 64 contiguous
+// bytes per block for each j); one v_perm_b32 stage pairs the bytes of two
+// rows per token, and the converter's (bytes 0,1) / (bytes 2,3) halves are
+// then exactly the f16 (d, d') pairs of one token: 1 perm and 2 converts
+// per 4 bytes.  v_cvt_scalef32_pk_f16_fp8 with scale 1 is exact: every E4M3
+// value, subnormals and NaN included, is an f16 value.
+// Scores: lane (m, kg) holds head m, iteration token 16 kg + 4 r + i.
+// V: lane (m, kg) loads the 16 bytes of row d = 16 dt + m for iteration
+// tokens 16 kg .. 16 kg + 15 (one block row at block size 16); MFMA h
 // takes its tokens 8 h .. 8 h + 7.
 // bf16 q is brought into f16 range by a power of two per head (exact: max
 // |q| in [2^14, 2^15)); the factor returns in the score scale.  The
 // dequant scales fold into the score scale (k_scale) and the output
 // (v_scale).
-template <Kind QK>
+template <Kind QK, int BS>
 __device__ __forceinline__ void fp8_wave(const Params& p, int seq, int kvh, int hs, int first_it, int t1,
                                          int step, float* s_acc_w, float* s_m_w, float* s_l_w) {
-  constexpr int kBlockBytes = kHead * 16;
+  static_assert(BS >= 16 && (BS & (BS - 1)) == 0, "block size: a power of two >= 16");
+  constexpr int TPI = 64, RB = BS;           // tokens per iteration; bytes per head-dim row of a block
+  constexpr int kBlockBytes = kHead * RB;
+  constexpr int NB = blocks_per_iteration<BS, TPI>();
   const int lane = threadIdx.x % kWave;
   const int m = lane & 15, kg = lane >> 4;
 
@@ -215,32 +232,37 @@ __device__ __forceinline__ void fp8_wave(const Params& p, int seq, int kvh, int 
 
   const int32_t* table = p.block_tables + (int64_t)seq * p.max_blocks_per_seq;
   const int64_t pool_stride = (int64_t)p.num_kv_heads * kBlockBytes;
-  const char* kbase0 = p.k_cache + (int64_t)kvh * kBlockBytes + 16 * kg + 4 * (m & 3);
-  const char* vbase0 = p.v_cache + (int64_t)kvh * kBlockBytes + 16 * m;
-  const int kb = m >> 2;   // the block of this lane's K quad
+  // this lane's K quad and V run: their blocks within the iteration and
+  // their byte offsets in a block row (plus the iteration's own offset when
+  // a block holds several iterations)
+  const int kb = NB > 1 ? (4 * m) / BS : 0, vb = NB > 1 ? (16 * kg) / BS : 0;
+  const char* kbase0 = p.k_cache + (int64_t)kvh * kBlockBytes + RB * kg + (4 * m) % (NB > 1 ? BS : TPI);
+  const char* vbase0 = p.v_cache + (int64_t)kvh * kBlockBytes + RB * m + (16 * kg) % (NB > 1 ? BS : TPI);
   auto load_k = [&](uint32_t (&kw)[32], const char* base) {
 #pragma unroll
-    for (int j = 0; j < 32; ++j) kw[j] = ld_nt(base + 64 * j);
+    for (int j = 0; j < 32; ++j) kw[j] = ld_nt(base + 4 * RB * j);
   };
   auto load_v = [&](u32x4 (&vr)[8], const char* base) {
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) vr[dt] = load16_stream(base + 256 * dt);
+    for (int dt = 0; dt < 8; ++dt) vr[dt] = load16_stream(base + 16 * RB * dt);
   };
 
   int it = first_it;
-  Blocks<4> cur = table_blocks<4>(p, table, it, t1);
-  Blocks<4> nxt = table_blocks<4>(p, table, it + step, t1);
+  Blocks<NB> cur = table_blocks<NB, BS>(p, table, it, t1);
+  Blocks<NB> nxt = table_blocks<NB, BS>(p, table, it + step, t1);
   uint32_t kw[32];
   u32x4 vr[8];
   if (it < t1) {
-    load_k(kw, kbase0 + (int64_t)max(pick(cur, kb), 0) * pool_stride);
-    load_v(vr, vbase0 + (int64_t)max(pick(cur, kg), 0) * pool_stride);
+    const int ib = in_block_bytes<BS, TPI, 1>(it);
+    load_k(kw, kbase0 + ib + (int64_t)max(pick(cur, kb), 0) * pool_stride);
+    load_v(vr, vbase0 + ib + (int64_t)max(pick(cur, vb), 0) * pool_stride);
   }
 
 #pragma unroll 1
   for (; it < t1; it += step) {
-    const Blocks<4> nn = table_blocks<4>(p, table, it + 2 * step, t1);
+    const Blocks<NB> nn = table_blocks<NB, BS>(p, table, it + 2 * step, t1);
     const bool has_next = it + step < t1;
+    const int ib_next = in_block_bytes<BS, TPI, 1>(it + step);
 
     // ---- q.k: 4 tiles (token i of each quad) x 4 MFMA steps ----
     f4 s[4];
@@ -264,10 +286,10 @@ __device__ __forceinline__ void fp8_wave(const Params& p, int seq, int kvh, int 
 #pragma unroll
       for (int i = 0; i < 4; ++i) s[i] = mma<Kind::F16>(a[i][0], a[i][1], a[i][2], a[i][3], qb[sk], s[i]);
     }
-    if (has_next) load_k(kw, kbase0 + (int64_t)max(pick(nxt, kb), 0) * pool_stride);
+    if (has_next) load_k(kw, kbase0 + ib_next + (int64_t)max(pick(nxt, kb), 0) * pool_stride);
 
-    // ---- softmax: lane (m, kg) owns head m, tokens 4 r + i of block kg ----
-    const int ph_v = pick(cur, kg);
+    // ---- softmax: lane (m, kg) owns head m, iteration tokens 16 kg + 4 r + i ----
+    const int ph_v = pick(cur, vb);
     const int n_ok = ph_v < 0 ? 0 : min(max(t1 - (it + 16 * kg), 0), 16);
     float sc[4][4];
     float mx = -INFINITY;
@@ -310,27 +332,31 @@ __device__ __forceinline__ void fp8_wave(const Params& p, int seq, int kvh, int 
       st.o[dt] = mma<Kind::F16>(f8x2<false>(v.z), f8x2<true>(v.z), f8x2<false>(v.w), f8x2<true>(v.w), pb[1],
                                 st.o[dt]);
     }
-    if (has_next) load_v(vr, vbase0 + (int64_t)max(pick(nxt, kg), 0) * pool_stride);
+    if (has_next) load_v(vr, vbase0 + ib_next + (int64_t)max(pick(nxt, vb), 0) * pool_stride);
     cur = nxt;
     nxt = nn;
   }
   st.store(p.v_scale, m, kg, s_acc_w, s_m_w, s_l_w);
 }
 
-// ---- 2-byte KV (f16 / bf16, q of the same type): 32 tokens (2 blocks) per iteration ----
+// ---- 2-byte KV (f16 / bf16, q of the same type): 32 tokens per iteration ----
 //
-// K: the A row m is token pair m (block m >> 3, tokens 2 (m & 7), +1) and
-// tile i takes token i of every pair.  Lane (m, kg) reads 32 dwords (128
-// contiguous bytes per block for each j); v_perm_b32 of the dwords of rows
-// (e, e + 1) gives the (d, d') pair of the pair's first (low halves) or
-// second (high halves) token: 1 perm per operand dword.
-// Scores: lane (m, kg) holds head m, tokens 8 (kg & 1) + 2 r + i of block
-// kg >> 1, i.e. the run of 8 tokens that is k group kg of the p.v MFMA.
+// K: the A row m is token pair m (iteration tokens 2 m, 2 m + 1) and tile i
+// takes token i of every pair.  Lane (m, kg) reads 32 dwords, rows 4 j + kg
+// of its pair (at block size 16 the wavefront reads 128 contiguous bytes
+// per block for each j); v_perm_b32 of the dwords of rows (e, e + 1) gives
+// the (d, d') pair of the pair's first (low halves) or second (high halves)
+// token: 1 perm per operand dword.
+// Scores: lane (m, kg) holds head m, iteration tokens 8 kg + 2 r + i, i.e.
+// the run of 8 tokens that is k group kg of the p.v MFMA.
 // V: lane (m, kg) loads the 16 bytes of that run, row d = 16 dt + m.
-template <Kind KV>
+template <Kind KV, int BS>
 __device__ __forceinline__ void mfma2_wave(const Params& p, int seq, int kvh, int hs, int first_it, int t1,
                                            int step, float* s_acc_w, float* s_m_w, float* s_l_w) {
-  constexpr int kBlockBytes = kHead * 16 * 2;
+  static_assert(BS >= 8 && (BS & (BS - 1)) == 0, "block size: a power of two >= 8");
+  constexpr int TPI = 32, RB = 2 * BS;       // tokens per iteration; bytes per head-dim row of a block
+  constexpr int kBlockBytes = kHead * RB;
+  constexpr int NB = blocks_per_iteration<BS, TPI>();
   const int lane = threadIdx.x % kWave;
   const int m = lane & 15, kg = lane >> 4;
 
@@ -354,32 +380,37 @@ __device__ __forceinline__ void mfma2_wave(const Params& p, int seq, int kvh, in
 
   const int32_t* table = p.block_tables + (int64_t)seq * p.max_blocks_per_seq;
   const int64_t pool_stride = (int64_t)p.num_kv_heads * kBlockBytes;
-  const char* kbase0 = p.k_cache + (int64_t)kvh * kBlockBytes + 32 * kg + 4 * (m & 7);
-  const char* vbase0 = p.v_cache + (int64_t)kvh * kBlockBytes + 32 * m + 16 * (kg & 1);
-  const int kb = m >> 3, vb = kg >> 1;   // blocks of this lane's K pair and V run
+  // this lane's K pair and V run: their blocks within the iteration and
+  // their byte offsets in a block row (plus the iteration's own offset when
+  // a block holds several iterations)
+  const int kb = NB > 1 ? (2 * m) / BS : 0, vb = NB > 1 ? (8 * kg) / BS : 0;
+  const char* kbase0 = p.k_cache + (int64_t)kvh * kBlockBytes + RB * kg + 2 * ((2 * m) % (NB > 1 ? BS : TPI));
+  const char* vbase0 = p.v_cache + (int64_t)kvh * kBlockBytes + RB * m + 2 * ((8 * kg) % (NB > 1 ? BS : TPI));
   auto load_k = [&](uint32_t (&kw)[32], const char* base) {
 #pragma unroll
-    for (int j = 0; j < 32; ++j) kw[j] = ld_nt(base + 128 * j);
+    for (int j = 0; j < 32; ++j) kw[j] = ld_nt(base + 4 * RB * j);
   };
   auto load_v = [&](u32x4 (&vr)[8], const char* base) {
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) vr[dt] = load16_stream(base + 512 * dt);
+    for (int dt = 0; dt < 8; ++dt) vr[dt] = load16_stream(base + 16 * RB * dt);
   };
 
   int it = first_it;
-  Blocks<2> cur = table_blocks<2>(p, table, it, t1);
-  Blocks<2> nxt = table_blocks<2>(p, table, it + step, t1);
+  Blocks<NB> cur = table_blocks<NB, BS>(p, table, it, t1);
+  Blocks<NB> nxt = table_blocks<NB, BS>(p, table, it + step, t1);
   uint32_t kw[32];
   u32x4 vr[8];
   if (it < t1) {
-    load_k(kw, kbase0 + (int64_t)max(pick(cur, kb), 0) * pool_stride);
-    load_v(vr, vbase0 + (int64_t)max(pick(cur, vb), 0) * pool_stride);
+    const int ib = in_block_bytes<BS, TPI, 2>(it);
+    load_k(kw, kbase0 + ib + (int64_t)max(pick(cur, kb), 0) * pool_stride);
+    load_v(vr, vbase0 + ib + (int64_t)max(pick(cur, vb), 0) * pool_stride);
   }
 
 #pragma unroll 1
   for (; it < t1; it += step) {
-    const Blocks<2> nn = table_blocks<2>(p, table, it + 2 * step, t1);
+    const Blocks<NB> nn = table_blocks<NB, BS>(p, table, it + 2 * step, t1);
     const bool has_next = it + step < t1;
+    const int ib_next = in_block_bytes<BS, TPI, 2>(it + step);
 
     // ---- q.k: 2 tiles (token i of each pair) x 4 MFMA steps ----
     f4 s[2] = {f4{0.f, 0.f, 0.f, 0.f}, f4{0.f, 0.f, 0.f, 0.f}};
@@ -395,41 +426,49 @@ __device__ __forceinline__ void mfma2_wave(const Params& p, int seq, int kvh, in
 #pragma unroll
       for (int i = 0; i < 2; ++i) s[i] = mma<KV>(a[i][0], a[i][1], a[i][2], a[i][3], qb[sk], s[i]);
     }
-    if (has_next) load_k(kw, kbase0 + (int64_t)max(pick(nxt, kb), 0) * pool_stride);
+    if (has_next) load_k(kw, kbase0 + ib_next + (int64_t)max(pick(nxt, kb), 0) * pool_stride);
 
-    // ---- softmax: lane (m, kg) owns head m, tokens 8 (kg & 1) + 2 r + i of block kg >> 1 ----
+    // ---- softmax: lane (m, kg) owns head m, iteration tokens 8 kg + 2 r + i ----
     const int ph_v = pick(cur, vb);
-    const int n_ok = ph_v < 0 ? 0 : min(max(t1 - (it + 16 * vb), 0), 16);
-    const int run0 = 8 * (kg & 1);
+    const int n_run = ph_v < 0 ? 0 : min(max(t1 - (it + 8 * kg), 0), 8);   // valid tokens of the run
     float sc[2][4];
     float mx = -INFINITY;
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        sc[i][r] = (run0 + 2 * r + i < n_ok) ? s[i][r] * p.qk_scale : -INFINITY;
+        sc[i][r] = (2 * r + i < n_run) ? s[i][r] * p.qk_scale : -INFINITY;
         mx = fmaxf(mx, sc[i][r]);
       }
     st.update_max(mx);
-    u4v pb;
+    // bf16 weights carry 8 mantissa bits: a short or peaked softmax would
+    // miss 2e-3 by up to 2^-9 max|v|, so bf16 splits each weight into a
+    // bf16 high part and the bf16 rounding of the rest (relative 2^-18)
+    // and p.v takes both (f16 weights are exact enough alone)
+    u4v pb, pl;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const float p0 = (run0 + 2 * r < n_ok) ? __builtin_amdgcn_exp2f(sc[0][r] - st.m_run) : 0.f;
-      const float p1 = (run0 + 2 * r + 1 < n_ok) ? __builtin_amdgcn_exp2f(sc[1][r] - st.m_run) : 0.f;
+      const float p0 = (2 * r < n_run) ? __builtin_amdgcn_exp2f(sc[0][r] - st.m_run) : 0.f;
+      const float p1 = (2 * r + 1 < n_run) ? __builtin_amdgcn_exp2f(sc[1][r] - st.m_run) : 0.f;
       st.l_lane += p0 + p1;
       pb[r] = Dot2<KV>::pack(p0, p1);
+      if constexpr (KV == Kind::BF16) {
+        const float h0 = __builtin_bit_cast(float, pb[r] << 16), h1 = __builtin_bit_cast(float, pb[r] & 0xffff0000u);
+        pl[r] = Dot2<KV>::pack(p0 - h0, p1 - h1);
+      }
     }
 
     // ---- p.v: slots past t1 and holes may hold anything, NaN included ----
-    if (__builtin_amdgcn_ballot_w64(n_ok < 16) != 0) {
-      const int keep = min(max(n_ok - run0, 0), 8);
+    if (__builtin_amdgcn_ballot_w64(n_run < 8) != 0) {
 #pragma unroll
-      for (int dt = 0; dt < 8; ++dt) vr[dt] = keep_halves(vr[dt], keep);
+      for (int dt = 0; dt < 8; ++dt) vr[dt] = keep_halves(vr[dt], n_run);
     }
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt)
+    for (int dt = 0; dt < 8; ++dt) {
       st.o[dt] = mma<KV>(vr[dt].x, vr[dt].y, vr[dt].z, vr[dt].w, pb, st.o[dt]);
-    if (has_next) load_v(vr, vbase0 + (int64_t)max(pick(nxt, vb), 0) * pool_stride);
+      if constexpr (KV == Kind::BF16) st.o[dt] = mma<KV>(vr[dt].x, vr[dt].y, vr[dt].z, vr[dt].w, pl, st.o[dt]);
+    }
+    if (has_next) load_v(vr, vbase0 + ib_next + (int64_t)max(pick(nxt, vb), 0) * pool_stride);
     cur = nxt;
     nxt = nn;
   }
@@ -439,7 +478,7 @@ __device__ __forceinline__ void mfma2_wave(const Params& p, int seq, int kvh, in
 // One workgroup of NW wavefronts over (sequence, kv head, 16-head slice,
 // partition): the wavefronts stride over the partition's iterations and
 // are merged in LDS (smem: NW x 16 x 128 + 2 x NW x 16 floats).
-template <Kind KV, Kind QK, Kind PO, int NW, bool FINAL>
+template <Kind KV, Kind QK, Kind PO, int NW, bool FINAL, int BS = 16>
 __device__ __forceinline__ void decode_workgroup(const Params& p, int seq, int kvh, int hs, int part, int t0,
                                                  int t1, float* s_acc, float* s_m, float* s_l) {
   constexpr int TPI = tokens_per_iteration<KV>();
@@ -447,10 +486,11 @@ __device__ __forceinline__ void decode_workgroup(const Params& p, int seq, int k
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
   float* acc_w = s_acc + wave * kHeads * kHead;
   if constexpr (KV == Kind::FP8)
-    fp8_wave<QK>(p, seq, kvh, hs, t0 + wave * TPI, t1, NW * TPI, acc_w, s_m + wave * kHeads, s_l + wave * kHeads);
+    fp8_wave<QK, BS>(p, seq, kvh, hs, t0 + wave * TPI, t1, NW * TPI, acc_w, s_m + wave * kHeads,
+                     s_l + wave * kHeads);
   else
-    mfma2_wave<KV>(p, seq, kvh, hs, t0 + wave * TPI, t1, NW * TPI, acc_w, s_m + wave * kHeads,
-                   s_l + wave * kHeads);
+    mfma2_wave<KV, BS>(p, seq, kvh, hs, t0 + wave * TPI, t1, NW * TPI, acc_w, s_m + wave * kHeads,
+                       s_l + wave * kHeads);
   __syncthreads();
   combine_waves<QK, PO, kHead, FINAL, kHeads>(p, NW, s_m, s_l, s_acc, seq, kvh, hs, part, tid, NW * kWave);
 }
