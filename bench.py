@@ -13,14 +13,17 @@ Workloads (synthetic, seeded; q/K/V ~ N(0,1)):
 Two copies of every pool are rotated between steps so the 256 MiB Infinity
 Cache cannot serve a re-timed step.
 
-The timed steps are captured into one HIP graph and replayed (events on the
-replay stream), as a serving decode loop runs; warmup steps run eagerly.
+The --steps timed steps are captured into one HIP graph, as a serving decode
+loop runs (warmup steps run eagerly); after untimed replays bring the GPU to
+its sustained clocks the graph is replayed R times (R >= 5, at least 60
+steps in all), each replay timed with events on the replay stream, and a
+workload's ms per step is the median replay's.
 
 Prints one JSON line.  value = GB/s of algorithmic bytes (KV read once + q
-read + out write + block tables + seq_lens) per bf16 step over the timed
-steps; roofline = the same bytes over the decode launch's average duration
-(one launch per step) against 8 TB/s; cpu_baseline = the oracle's
-multithreaded fp32 decode on the host cores over a bounded sample.
+read + out write + block tables + seq_lens) per bf16 step; roofline = the
+same bytes over the decode launch's duration (one launch per step) against
+8 TB/s; cpu_baseline = the oracle's fp32 decode on the host cores over a
+bounded sample, one thread and all the cores of the GPU's CPU share.
 """
 import argparse
 import itertools
@@ -42,26 +45,34 @@ TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "decode_bf16_b64_ctx4096_hbm_tr
 
 
 def algorithmic_bytes(lens, elem):
+    """K+V read once, q read and out written, the block-table entries used
+    and seq_lens."""
     kv = sum(lens) * NKV * D * 2 * elem
-    qo = S * H * D * elem * 2
-    tables = sum((L + BS - 1) // BS for L in lens) * 4 + 4 * S
+    qo = len(lens) * H * D * elem * 2
+    tables = sum((L + BS - 1) // BS for L in lens) * 4 + 4 * len(lens)
     return kv + qo + tables
 
 
-def kivi_bytes(lens, R, appended_page):
+def config2b_lens():
+    """Batch 64, lengths uniform in [512, 8192] (seed 0x7E5E0002)."""
+    import numpy as np
+    return np.random.default_rng(0x7E5E0002).integers(512, 8193, size=S).tolist()
+
+
+def kivi_bytes(lens, R, completes_page):
     """KIVI bytes of one step: pages (160 B/token/kv head) + fp16 window
-    (512 B/token/kv head) + q/out + tables, plus the appended token and,
-    when a page completes, its quantisation (32 fp16 tokens read, 5 KiB
-    written per kv head)."""
+    (512 B/token/kv head) + q/out + tables, plus the appended token and, for
+    each sequence whose append completes a page, its quantisation (32 fp16
+    tokens read, 5 KiB written per kv head)."""
     tot = 0
-    for L in lens:
+    for L, page in zip(lens, completes_page):
         lq = 0 if L <= R else ((L - R) // 32) * 32
         tot += NKV * (lq * 160 + (L - lq) * 512)
         tot += (lq // 32 + (L - lq + BS - 1) // BS) * 4 + 4
-    tot += S * H * D * 2 * 2
-    tot += S * NKV * D * 2 * 2
-    if appended_page:
-        tot += S * NKV * (32 * 512 + 5120)
+        if page:
+            tot += NKV * (32 * 512 + 5120)
+    tot += len(lens) * H * D * 2 * 2
+    tot += len(lens) * NKV * D * 2 * 2
     return tot
 
 
@@ -73,7 +84,8 @@ def parse():
     p.add_argument("--partition-tokens", type=int, default=0)
     p.add_argument("--cpu-seconds", type=float, default=15.0)
     p.add_argument("--no-cpu", action="store_true")
-    p.add_argument("--only", default="all", choices=["all", "bf16", "fp16", "kivi", "fp8", "prefill", "blocks", "rope", "vq", "norm"])
+    p.add_argument("--only", default="all", choices=["all", "bf16", "fp16", "kivi", "fp8", "config2b", "v2",
+                                                     "prefill", "blocks", "rope", "vq", "norm"])
     p.add_argument("--no-graph", action="store_true",
                    help="launch the timed steps eagerly (for counter passes that cannot follow graphs)")
     p.add_argument("--copy-calibration", action="store_true",
@@ -88,93 +100,163 @@ USE_GRAPH = True
 WARM_MS = 30.0
 
 
-def timed(step, steps, warmup):
+POOL_ARENA = {}
+
+
+def pool_buffer(name, shape, dtype, g):
+    """A KV pool of the given shape and dtype, N(0, 1) from generator g, in a
+    device buffer allocated once for the whole run and shared by every
+    workload (pools 'k0', 'v0', 'k1', 'v1'): the workloads then stream the
+    same physical memory.  Pools allocated later in a run, after earlier
+    workloads' memory had been freed, were up to 4 % slower for the same
+    kernel (fp16 against bf16, the v2 operator against the library plan);
+    main() allocates the arena first, at the largest size any workload
+    needs."""
+    import torch
+    nbytes = math.prod(shape) * torch.empty((), dtype=dtype).element_size()
+    buf = POOL_ARENA.get(name)
+    if buf is None or buf.numel() < nbytes:
+        buf = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+        POOL_ARENA[name] = buf
+    t = buf[:nbytes].view(dtype).view(shape)
+    if dtype in (torch.float16, torch.bfloat16, torch.float32):
+        t.normal_(0.0, 1.0, generator=g)
+    return t
+
+
+def arena_bytes():
+    """Bytes of the largest pool any workload uses (per pool)."""
+    blocks_2a = math.ceil(1.25 * S * (CTX // BS))
+    blocks_2b = math.ceil(1.25 * sum((L + BS - 1) // BS for L in config2b_lens()))
+    blocks_kivi = S * ((CTX + 32 + 256 + BS - 1) // BS) + 8
+    return max(blocks_2a, blocks_2b, blocks_kivi) * NKV * D * BS * 2
+
+
+MIN_TIMED_STEPS, MIN_REPLAYS = 60, 5
+SPREAD = {}      # workload -> (min, max) ms per step over the timed replays
+
+
+def timed(step, steps, warmup, name=None):
     """Run `warmup` eager steps, capture the next `steps` steps into one HIP
     graph, replay it untimed until about WARM_MS of GPU work has run, then
-    time one replay with events on the replay stream.  Returns ms per step.
-    A serving decode loop runs the same way: the graph removes the per-launch
-    host cost, which otherwise exceeds a short step's GPU time, and the GPU
-    runs at the clocks of sustained load (from an idle GPU the first ~10 ms
-    of the KIVI decode ran up to 10 % slower)."""
+    time R = max(5, ceil(60 / steps)) replays one by one with events on the
+    replay stream.  Returns the median replay's ms per step (the spread goes
+    to SPREAD[name]).  A serving decode loop runs the same way: the graph
+    removes the per-launch host cost, which otherwise exceeds a short step's
+    GPU time, and the GPU runs at the clocks of sustained load (from an idle
+    GPU the first ~10 ms of the KIVI decode ran up to 10 % slower)."""
+    import statistics
+
     import torch
     stream = torch.cuda.current_stream()
     for i in range(warmup):
         step(i, stream)
     torch.cuda.synchronize()
+    reps = max(MIN_REPLAYS, -(-MIN_TIMED_STEPS // steps))
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    per = []
     if not USE_GRAPH:
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        for _ in range(reps):
+            e0.record(stream)
+            for i in range(steps):
+                step(warmup + i, stream)
+            e1.record(stream)
+            torch.cuda.synchronize()
+            per.append(e0.elapsed_time(e1) / steps)
+    else:
+        graph = torch.cuda.CUDAGraph()
+        cap = torch.cuda.Stream()
+        with torch.cuda.graph(graph, stream=cap):
+            for i in range(steps):
+                step(warmup + i, cap)
         e0.record(stream)
-        for i in range(steps):
-            step(warmup + i, stream)
+        graph.replay()
         e1.record(stream)
         torch.cuda.synchronize()
-        return e0.elapsed_time(e1) / steps
-    graph = torch.cuda.CUDAGraph()
-    cap = torch.cuda.Stream()
-    with torch.cuda.graph(graph, stream=cap):
-        for i in range(steps):
-            step(warmup + i, cap)
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
-    graph.replay()
-    e1.record(stream)
-    torch.cuda.synchronize()
-    for _ in range(min(50, int(WARM_MS / max(e0.elapsed_time(e1), 1e-3)))):
-        graph.replay()
-    torch.cuda.synchronize()
-    e0.record(stream)
-    graph.replay()
-    e1.record(stream)
-    torch.cuda.synchronize()
-    return e0.elapsed_time(e1) / steps
+        for _ in range(min(50, int(WARM_MS / max(e0.elapsed_time(e1), 1e-3)))):
+            graph.replay()
+        torch.cuda.synchronize()
+        for _ in range(reps):
+            e0.record(stream)
+            graph.replay()
+            e1.record(stream)
+            torch.cuda.synchronize()
+            per.append(e0.elapsed_time(e1) / steps)
+    if name:
+        SPREAD[name] = (min(per), max(per), reps, steps)
+    return statistics.median(per)
 
 
-def bench_decode(args, dtype, append=False):
-    """Single-pass (or split-K with --partition-tokens) decode at batch 64,
-    ctx 4096.  With append, every step first writes each sequence's newest
-    token (position ctx - 1) into the pool with reshape_and_cache, as an
-    engine's decode step does before attention: the fp16 counterpart of the
-    KIVI step, whose append is fused into its launch."""
+def bench_decode(args, dtype, append=False, lens=None, partition_tokens=None, v2=False, name=None):
+    """Decode of one layer over the given lengths (default: batch 64, every
+    context 4096) with the library plan (or partition_tokens), through
+    tl_paged_attention_decode or, with v2, the reference-named
+    tl_paged_attention_v2 on the engine's scratch sizes.  With append, every
+    step first writes each sequence's newest token (position L - 1) into the
+    pool with reshape_and_cache, as an engine's decode step does before
+    attention: the fp16 counterpart of the KIVI step, whose append is fused
+    into its launch."""
     import torch
 
     import tl_attn as tla
 
+
+    lens = [CTX] * S if lens is None else list(lens)
+    B = len(lens)
+    pt = args.partition_tokens if partition_tokens is None else partition_tokens
     tdt = torch.bfloat16 if dtype == "bf16" else torch.float16
-    nb = CTX // BS
-    N = math.ceil(1.25 * S * nb)
+    nbs = [(L + BS - 1) // BS for L in lens]
+    mb = max(nbs)
+    N = math.ceil(1.25 * sum(nbs))
     g = torch.Generator(device="cuda").manual_seed(0x7E5E0002)
     pools = []
     for _ in range(2):
-        k = torch.randn(N, NKV, D, BS, generator=g, device="cuda", dtype=tdt)
-        v = torch.randn(N, NKV, D, BS, generator=g, device="cuda", dtype=tdt)
-        perm = torch.randperm(N, generator=g, device="cuda").to(torch.int32)
-        pools.append((k, v, perm[: S * nb].view(S, nb).contiguous()))
-    q = torch.randn(S, H, D, generator=g, device="cuda", dtype=tdt)
-    sl = torch.full((S,), CTX, dtype=torch.int32, device="cuda")
+        k = pool_buffer(f"k{len(pools)}", (N, NKV, D, BS), tdt, g)
+        v = pool_buffer(f"v{len(pools)}", (N, NKV, D, BS), tdt, g)
+        perm = torch.randperm(N, generator=g, device="cuda").to(torch.int32).cpu()
+        tables = torch.full((B, mb), -1, dtype=torch.int32)
+        off = 0
+        for s_, nb in enumerate(nbs):
+            tables[s_, :nb] = perm[off:off + nb]
+            off += nb
+        pools.append((k, v, tables.cuda()))
+    q = torch.randn(B, H, D, generator=g, device="cuda", dtype=tdt)
+    sl = torch.tensor(lens, dtype=torch.int32, device="cuda")
+    max_ctx = max(lens)
     out = torch.empty_like(q)
-    desc = tla.make_decode_desc(q, pools[0][0], pools[0][2], NKV, 1.0 / math.sqrt(D),
-                                gqa_map=tla.GQA_GROUPED, partition_tokens=args.partition_tokens)
-    ws = torch.empty(max(16, tla.workspace_bytes(desc, CTX)), dtype=torch.uint8, device="cuda")
+    scale = 1.0 / math.sqrt(D)
+    desc = tla.make_decode_desc(q, pools[0][0], pools[0][2], NKV, scale, gqa_map=tla.GQA_GROUPED, partition_tokens=pt)
+    ws = torch.empty(max(16, tla.workspace_bytes(desc, max_ctx)), dtype=torch.uint8, device="cuda")
+    if v2:
+        P = tla.v2_num_partitions(max_ctx, BS)
+        es = torch.empty(B, H, P, dtype=torch.float32, device="cuda")
+        ml = torch.empty_like(es)
+        tmp = torch.empty(B, H, P, D, dtype=tdt, device="cuda")
 
     if append:
-        knew = torch.randn(S, NKV, D, generator=g, device="cuda", dtype=tdt)
-        vnew = torch.randn(S, NKV, D, generator=g, device="cuda", dtype=tdt)
-        pos = CTX - 1
-        slots = [(tables[:, pos // BS] * BS + pos % BS).to(torch.int32).contiguous() for _k, _v, tables in pools]
+        knew = torch.randn(B, NKV, D, generator=g, device="cuda", dtype=tdt)
+        vnew = torch.randn(B, NKV, D, generator=g, device="cuda", dtype=tdt)
+        pos = sl.long() - 1
+        rows = torch.arange(B, device="cuda")
+        slots = [(tables[rows, pos // BS] * BS + pos % BS).to(torch.int32).contiguous() for _k, _v, tables in pools]
 
     def step(i, stream):
         k, v, tables = pools[i % 2]
         if append:
             tla.reshape_and_cache_split(knew, vnew, k, v, slots[i % 2], stream)
-        tla.paged_attention_decode(desc, out, q, k, v, tables, sl, CTX, ws, stream)
+        if v2:
+            tla.paged_attention_v2(out, es, ml, tmp, q, k, v, tables, sl, NKV, scale, D, BS, max_ctx, stream,
+                                   gqa_map=tla.GQA_GROUPED)
+        else:
+            tla.paged_attention_decode(desc, out, q, k, v, tables, sl, max_ctx, ws, stream)
 
-    ms = timed(step, args.steps, args.warmup)
-    nbytes = algorithmic_bytes([CTX] * S, 2)
-    launch_ms = ms                      # one decode launch per step
+    ms = timed(step, args.steps, args.warmup, name)
+    nbytes = algorithmic_bytes(lens, 2)
     return {
-        "ms_per_step": ms, "gbs": nbytes / (ms * 1e-3) / 1e9, "tok_s": S / (ms * 1e-3),
-        "bytes": nbytes, "launch_ms": launch_ms, "pool_blocks": N,
-        "workspace_bytes": tla.workspace_bytes(desc, CTX),
+        "ms_per_step": ms, "gbs": nbytes / (ms * 1e-3) / 1e9, "tok_s": B / (ms * 1e-3),
+        "bytes": nbytes, "launch_ms": ms, "pool_blocks": N,            # one decode launch per step
+        "workspace_bytes": tla.workspace_bytes(desc, max_ctx),
+        "partitions": max(1, tla.workspace_bytes(desc, max_ctx) // (B * H * (D + 2) * 4)),
     }
 
 
@@ -187,23 +269,27 @@ def kivi_steps(steps):
     return max(64, (steps + 63) // 64 * 64)
 
 
-def bench_kivi(args, R=128):
+def bench_kivi(args, R=128, mixed=False, name=None):
+    """KIVI INT4 append + decode steps at batch 64 from context 4096 (mixed:
+    sequence s starts at 4096 + s mod 32 tokens, so two sequences complete a
+    page at every step instead of all 64 on one step in 32)."""
     import torch
 
     import tl_attn as tla
 
+
     n_timed = kivi_steps(args.steps)
     total_steps = args.warmup + n_timed
-    L0 = CTX
-    Lmax = L0 + total_steps
+    L0 = [CTX + (s_ % 32 if mixed else 0) for s_ in range(S)]
+    Lmax = max(L0) + total_steps
     nb = (Lmax + BS - 1) // BS
     N = S * nb + 8
     max_pages = Lmax // 32 + 1
     g = torch.Generator(device="cuda").manual_seed(0x7E5E0003)
     reps = []
     for _ in range(2):
-        k = torch.randn(N, NKV, D, BS, generator=g, device="cuda", dtype=torch.float16)
-        v = torch.randn(N, NKV, D, BS, generator=g, device="cuda", dtype=torch.float16)
+        k = pool_buffer(f"k{len(reps)}", (N, NKV, D, BS), torch.float16, g)
+        v = pool_buffer(f"v{len(reps)}", (N, NKV, D, BS), torch.float16, g)
         for h in range(NKV):                                  # 4 outlier K channels x8
             ch = torch.randperm(D, generator=g, device="cuda")[:4]
             k[:, h, ch, :] *= 8
@@ -219,43 +305,41 @@ def bench_kivi(args, R=128):
     vnew = torch.randn(S, NKV, D, generator=g, device="cuda", dtype=torch.float16)
     out = torch.empty_like(q)
     scale = 1.0 / math.sqrt(D)
-    # per replica: lengths before each of its appends, slots of the new token
-    lens_host = {0: L0, 1: L0}
+    # per replica: the lengths after each of its appends, slots of the new tokens
+    lens_host = {0: list(L0), 1: list(L0)}
     plan = []
     for i in range(total_steps):
         r = i % 2
-        L = lens_host[r] + 1
-        lens_host[r] = L
-        plan.append((r, L))
+        lens_host[r] = [L + 1 for L in lens_host[r]]
+        plan.append((r, list(lens_host[r])))
     sl_dev, slot_dev = [], []
     tables_host = [rep[2].cpu() for rep in reps]
-    for r, L in plan:
-        sl_dev.append(torch.full((S,), L, dtype=torch.int32, device="cuda"))
-        pos = L - 1
-        slot = tables_host[r][:, pos // BS] * BS + pos % BS
+    rows = torch.arange(S)
+    for r, lens in plan:
+        lt = torch.tensor(lens, dtype=torch.int64)
+        sl_dev.append(lt.to(torch.int32).cuda())
+        pos = lt - 1
+        slot = tables_host[r][rows, pos // BS] * BS + pos % BS
         slot_dev.append(slot.to(torch.int32).cuda())
     desc0 = tla.make_kivi_desc(q, reps[0][0], reps[0][2], reps[0][3], reps[0][5], NKV, scale,
                                residual_length=R, gqa_map=tla.GQA_GROUPED)
     ws = torch.empty(max(16, tla.kivi_workspace_bytes(desc0, Lmax)), dtype=torch.uint8, device="cuda")
     for rep in reps:
         d = tla.make_kivi_desc(q, rep[0], rep[2], rep[3], rep[5], NKV, scale, residual_length=R)
-        sl0 = torch.full((S,), L0, dtype=torch.int32, device="cuda")
-        tla.kivi_build_pages(d, rep[0], rep[1], rep[2], sl0, rep[3], rep[4], L0)
+        sl0 = torch.tensor(L0, dtype=torch.int32, device="cuda")
+        tla.kivi_build_pages(d, rep[0], rep[1], rep[2], sl0, rep[3], rep[4], max(L0))
     descs = [tla.make_kivi_desc(q, rep[0], rep[2], rep[3], rep[5], NKV, scale, residual_length=R)
              for rep in reps]
 
     def step(i, stream):
-        r, L = plan[i]
+        r, lens = plan[i]
         k, v, tables, ptables, pages, _ = reps[r]
         tla.kivi_decode_step(descs[r], out, q, knew, vnew, slot_dev[i], pages, ptables, k, v, tables,
-                             sl_dev[i], L, ws, stream)
+                             sl_dev[i], max(lens), ws, stream)
 
-    ms = timed(step, n_timed, args.warmup)
-    nbytes = []
-    for i in range(args.warmup, total_steps):
-        _, L = plan[i]
-        lq = lambda x: 0 if x <= R else ((x - R) // 32) * 32
-        nbytes.append(kivi_bytes([L] * S, R, lq(L) > lq(L - 1)))
+    ms = timed(step, n_timed, args.warmup, name)
+    lq = lambda x: 0 if x <= R else ((x - R) // 32) * 32
+    nbytes = [kivi_bytes(lens, R, [lq(L) > lq(L - 1) for L in lens]) for _, lens in plan[args.warmup:]]
     avg_bytes = sum(nbytes) / len(nbytes)
     return {"ms_per_step": ms, "gbs": avg_bytes / (ms * 1e-3) / 1e9, "tok_s": S / (ms * 1e-3),
             "bytes_per_step": avg_bytes, "residual_length": R, "group": 32, "steps": n_timed}
@@ -271,6 +355,7 @@ def bench_rope(args):
     import torch
 
     import tl_attn as tla
+
 
     g = torch.Generator(device="cuda").manual_seed(0x7E5E0007)
     N = S * (CTX // BS + 1)
@@ -328,6 +413,7 @@ def bench_norm_act(args):
 
     import tl_attn as tla
 
+
     g = torch.Generator(device="cuda").manual_seed(0x7E5E0009)
     x = torch.randn(NA_ROWS, NA_HID, generator=g, device="cuda", dtype=torch.bfloat16)
     res = torch.randn_like(x)
@@ -361,6 +447,7 @@ def bench_vq(args):
 
     import tl_attn as tla
 
+
     g = torch.Generator(device="cuda").manual_seed(0x7E5E0008)
     kv = torch.randn(VQ_N, D, generator=g, device="cuda", dtype=torch.float16)
     book = torch.randn(VQ_K, D, generator=g, device="cuda", dtype=torch.float16)
@@ -386,6 +473,7 @@ def bench_copy_blocks(args):
 
     import tl_attn as tla
 
+
     g = torch.Generator(device="cuda").manual_seed(0x7E5E0006)
     k = torch.randn(CB_BLOCKS, NKV, D, BS, generator=g, device="cuda", dtype=torch.float16)
     v = torch.randn_like(k)
@@ -400,15 +488,16 @@ def bench_copy_blocks(args):
     return {"ms": ms, "bytes": nbytes, "gbs": nbytes / (ms * 1e-3) / 1e9}
 
 
-def bench_fp8(args):
+def bench_fp8(args, partition_tokens=0, name=None):
     """FP8 E4M3 KV long-context decode: batch 16, 32 q / 8 kv heads, d 128,
     bs 16, every context 32768, per-tensor fp32 scales absmax/448 (K/V drawn
-    N(0,1) in fp16 and cast), bf16 q/out.  The library's own split-K plan
-    (partition_tokens 0) picks the partitions; the log-sum-exp reduce is in
-    the timed step."""
+    N(0,1) in fp16 and cast), bf16 q/out.  partition_tokens 0: the library's
+    own split-K plan; 512: the 64 partitions of 512 tokens the workload
+    names.  The log-sum-exp reduce is in the timed step."""
     import torch
 
     import tl_attn as tla
+
 
     nb = F8_CTX // BS
     N = math.ceil(1.25 * F8_S * nb)
@@ -416,10 +505,14 @@ def bench_fp8(args):
     pools = []
     for _ in range(2):
         kv = []
-        for _t in range(2):
+        for t_ in range(2):
             x = torch.randn(N, NKV, D, BS, generator=g, device="cuda", dtype=torch.float16)
             s = x.abs().max().float() / 448.0
-            kv.append(((x.float() / s).to(torch.float8_e4m3fn).view(torch.uint8), float(s)))
+            codes = pool_buffer(f"{'kv'[t_]}{len(pools)}", (N, NKV, D, BS), torch.uint8, g)
+            for c0 in range(0, N, 4096):
+                codes[c0:c0 + 4096].copy_((x[c0:c0 + 4096].float() / s).to(torch.float8_e4m3fn).view(torch.uint8))
+            kv.append((codes, float(s)))
+            del x
         perm = torch.randperm(N, generator=g, device="cuda").to(torch.int32)
         pools.append((kv[0], kv[1], perm[: F8_S * nb].view(F8_S, nb).contiguous()))
     q = torch.randn(F8_S, H, D, generator=g, device="cuda", dtype=torch.bfloat16)
@@ -428,14 +521,14 @@ def bench_fp8(args):
     descs = []
     for (kq, ks), (vq, vs), tables in pools:
         descs.append(tla.make_decode_desc(q, kq, tables, NKV, 1.0 / math.sqrt(D), gqa_map=tla.GQA_GROUPED,
-                                          partition_tokens=0, k_scale=ks, v_scale=vs))
+                                          partition_tokens=partition_tokens, k_scale=ks, v_scale=vs))
     ws = torch.empty(max(16, tla.workspace_bytes(descs[0], F8_CTX)), dtype=torch.uint8, device="cuda")
 
     def step(i, stream):
         (kq, _), (vq, _), tables = pools[i % 2]
         tla.paged_attention_decode(descs[i % 2], out, q, kq, vq, tables, sl, F8_CTX, ws, stream)
 
-    ms = timed(step, args.steps, args.warmup)
+    ms = timed(step, args.steps, args.warmup, name)
     kv_bytes = F8_S * F8_CTX * NKV * D * 2
     nbytes = kv_bytes + F8_S * H * D * 2 * 2 + F8_S * nb * 4 + F8_S * 4
     P = max(1, tla.workspace_bytes(descs[0], F8_CTX) // (F8_S * H * (D + 2) * 4))
@@ -465,14 +558,15 @@ def bench_prefill(args):
 
     import tl_attn as tla
 
+
     S = PF_SEQS + PF_DEC
     nb = PF_PROMPT // BS
     N = math.ceil(1.25 * S * nb)
     g = torch.Generator(device="cuda").manual_seed(0x7E5E0005)
     pools = []
     for _ in range(2):
-        k = torch.randn(N, PF_NKV, D, BS, generator=g, device="cuda", dtype=torch.bfloat16)
-        v = torch.randn(N, PF_NKV, D, BS, generator=g, device="cuda", dtype=torch.bfloat16)
+        k = pool_buffer(f"k{len(pools)}", (N, PF_NKV, D, BS), torch.bfloat16, g)
+        v = pool_buffer(f"v{len(pools)}", (N, PF_NKV, D, BS), torch.bfloat16, g)
         perm = torch.randperm(N, generator=g, device="cuda").to(torch.int32)
         pools.append((k, v, perm[: S * nb].view(S, nb).contiguous()))
     nq = PF_SEQS * PF_CHUNK + PF_DEC
@@ -510,28 +604,60 @@ def traffic_from_profile():
     return int(m.group(1)) if m else None
 
 
-def cpu_baseline(seconds, S_sample, threads):
+def cpu_info():
+    """nproc, the CPUs this process may run on, the cores the GPU's share of
+    the host gives it (OMP_NUM_THREADS where the host sets it) and the CPU
+    model from lscpu."""
+    import subprocess
+    info = {"nproc": os.cpu_count(), "affinity": len(os.sched_getaffinity(0))}
+    share = os.environ.get("OMP_NUM_THREADS", "")
+    info["threads_all_cores"] = min(int(share), info["affinity"]) if share.isdigit() and int(share) > 0 \
+        else info["affinity"]
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        m = re.search(r"^Model name:\s*(.+)$", out, re.M)
+        info["model"] = m.group(1).strip() if m else None
+    except (OSError, subprocess.SubprocessError):
+        info["model"] = None
+    return info
+
+
+def cpu_baseline(seconds, S_sample):
+    """The oracle's fp32 decode (threads over (sequence, kv head)) on a
+    sample of the headline batch, timed on one thread and on all the cores
+    of this GPU's CPU share; median of the timed runs, each config run for
+    about `seconds`."""
+    import statistics
+
     import inputs
     import oracle_lib as orc
 
+    info = cpu_info()
     lens = [CTX] * S_sample
     case = inputs.make_paged_case(inputs.SEEDS[1], S_sample, H, NKV, D, BS, lens, orc.BF16)
-    kv = sum(lens) * NKV * D * 2 * 2
-    nbytes = kv + S_sample * H * D * 2 * 2 + sum(L // BS for L in lens) * 4 + 4 * S_sample
-    reps, t_total = 0, 0.0
-    while t_total < seconds or reps < 2:
-        t0 = time.perf_counter()
-        orc.paged_attention_f32(case.q, orc.BF16, case.k_cache, case.v_cache, orc.BF16,
-                                case.tables, case.seq_lens, NKV, case.scale, orc.GROUPED,
-                                threads=threads)
-        t_total += time.perf_counter() - t0
-        reps += 1
-    per = t_total / reps
+    nbytes = algorithmic_bytes(lens, 2)
+
+    def run(threads):
+        times = []
+        while sum(times) < seconds or len(times) < 5:
+            t0 = time.perf_counter()
+            orc.paged_attention_f32(case.q, orc.BF16, case.k_cache, case.v_cache, orc.BF16,
+                                    case.tables, case.seq_lens, NKV, case.scale, orc.GROUPED,
+                                    threads=threads)
+            times.append(time.perf_counter() - t0)
+        return statistics.median(times), len(times)
+
+    t1, n1 = run(1)
+    ta, na = run(info["threads_all_cores"])
     return {
-        "value": round(nbytes / per / 1e9, 3), "unit": "GB/s", "tok_s": round(S_sample / per, 2),
-        "cores": threads, "kind": "port",
-        "sample": f"{S_sample} of the 64 sequences (ctx {CTX}, 32/8 heads, d 128, bf16 pool), "
-                  f"{reps} runs of the oracle's fp32 pthread decode, {per * 1e3:.2f} ms each",
+        "value": round(nbytes / ta / 1e9, 3), "unit": "GB/s", "tok_s": round(S_sample / ta, 2),
+        "cores": info["threads_all_cores"], "kind": "port",
+        "sample": f"{S_sample} of the 64 sequences (ctx {CTX}, 32/8 heads, d 128, bf16 pool); the oracle's fp32 "
+                  f"decode, median of {na} runs ({ta * 1e3:.2f} ms each) on {info['threads_all_cores']} threads "
+                  f"and of {n1} runs ({t1 * 1e3:.2f} ms) on one",
+        "single_thread": {"value": round(nbytes / t1 / 1e9, 3), "unit": "GB/s", "tok_s": round(S_sample / t1, 2),
+                          "ms_per_run": round(t1 * 1e3, 3)},
+        "nproc": info["nproc"], "affinity_cpus": info["affinity"], "cpu_model": info["model"],
     }
 
 
@@ -544,6 +670,8 @@ def main():
     import torch
 
     torch.cuda.set_device(0)
+    for name in ("k0", "v0", "k1", "v1"):             # the pool arena first (pool_buffer)
+        POOL_ARENA[name] = torch.empty(arena_bytes(), dtype=torch.uint8, device="cuda")
     global USE_GRAPH
     USE_GRAPH = not args.no_graph
     if args.copy_calibration:
@@ -559,14 +687,25 @@ def main():
            "warmup": args.warmup, "higher_is_better": True, "scaling": "weak",
            "vs_baseline": None, "dtype": "bf16", "data": "synthetic"}
     bf = fp = kv = None
-    if args.only in ("all", "bf16"):
-        bf = bench_decode(args, "bf16")
-    if args.only in ("all", "fp16"):
-        fp = bench_decode(args, "fp16")
-    if args.only in ("all", "kivi"):
-        kv = bench_kivi(args)
-    fpa = bench_decode(args, "fp16", append=True) if args.only in ("all", "kivi") else None
-    f8 = bench_fp8(args) if args.only in ("all", "fp8") else None
+    want = lambda *names: args.only == "all" or args.only in names
+    if want("bf16", "v2"):
+        bf = bench_decode(args, "bf16", name="bf16")
+    if want("fp16", "kivi"):
+        fp = bench_decode(args, "fp16", name="fp16")
+    if want("kivi"):
+        kv = bench_kivi(args, name="kivi")
+    kvm = bench_kivi(args, mixed=True, name="kivi_mixed") if want("kivi") else None
+    fpa = bench_decode(args, "fp16", append=True, name="fp16_append") if want("kivi") else None
+    f8 = bench_fp8(args, name="fp8") if want("fp8") else None
+    f8p = bench_fp8(args, 512, name="fp8_pt512") if want("fp8") else None
+    c2b = {}
+    if want("config2b"):
+        lens2b = config2b_lens()
+        for label, pt in (("auto", 0), ("single_pass", -1), ("split_k_512", 512)):
+            c2b[label] = bench_decode(args, "bf16", lens=lens2b, partition_tokens=pt, name=f"config2b_{label}")
+    v2a = bench_decode(args, "bf16", v2=True, name="v2") if want("v2") else None
+    v2one = bench_decode(args, "f16", lens=[CTX], v2=True, name="v2_one_seq") if want("v2") else None
+    one = bench_decode(args, "f16", lens=[CTX], name="auto_one_seq") if want("v2") else None
     pf = bench_prefill(args) if args.only in ("all", "prefill") else None
     cb = bench_copy_blocks(args) if args.only in ("all", "blocks") else None
     rp = bench_rope(args) if args.only in ("all", "rope") else None
@@ -601,10 +740,37 @@ def main():
         "kv_dtype": res["dtype"], "pools_rotated": 2,
         "partition_tokens": args.partition_tokens or "auto",
     }
+    res["timing"] = (f"ms_per_step = median over R replays of a HIP graph of --steps steps (R >= {MIN_REPLAYS}, "
+                     f">= {MIN_TIMED_STEPS} timed steps), after untimed replays to sustained clocks")
+    res["spread_ms_per_step"] = {k: {"min": round(v[0], 5), "max": round(v[1], 5), "replays": v[2], "steps": v[3]}
+                                 for k, v in SPREAD.items()}
     if fp is not None:
         res["fp16"] = {"gbs": round(fp["gbs"], 2), "ms_per_step": round(fp["ms_per_step"], 5),
                        "tok_s": round(fp["tok_s"], 1),
                        "pct_hbm_peak": round(100 * fp["gbs"] / HBM_PEAK_GBS, 2)}
+    if c2b:
+        res["config2b_variable_lengths"] = {
+            "workload": "bf16 decode, batch 64, lengths uniform in [512, 8192] (seed 0x7E5E0002), 32/8 heads, d 128, "
+                        f"bs 16; mean length {sum(config2b_lens()) / S:.0f}",
+            **{label: {"gbs": round(r["gbs"], 2), "pct_hbm_peak": round(100 * r["gbs"] / HBM_PEAK_GBS, 2),
+                       "ms_per_step": round(r["ms_per_step"], 5), "tok_s": round(r["tok_s"], 1),
+                       "partitions": r["partitions"], "bytes_per_step": r["bytes"]}
+               for label, r in c2b.items()}}
+    if v2a is not None:
+        res["paged_attention_v2_dropin"] = {
+            "workload": "tl_paged_attention_v2 (the operator the engine calls past 32 blocks) at batch 64, ctx 4096, "
+                        "bf16, with the engine's scratch sizes",
+            "gbs": round(v2a["gbs"], 2), "pct_hbm_peak": round(100 * v2a["gbs"] / HBM_PEAK_GBS, 2),
+            "ms_per_step": round(v2a["ms_per_step"], 5),
+            "vs_library_plan": round(bf["ms_per_step"] / v2a["ms_per_step"], 4) if bf else None}
+    if v2one is not None:
+        res["paged_attention_v2_one_sequence"] = {
+            "workload": "the engine's own call: one sequence, ctx 4096, 32/8 heads, d 128, f16, "
+                        "tl_paged_attention_v2 on the engine's scratch against tl_paged_attention_decode's plan",
+            "v2_us": round(v2one["ms_per_step"] * 1e3, 2), "v2_partitions": v2one["partitions"],
+            "v2_gbs": round(v2one["gbs"], 2),
+            "library_plan_us": round(one["ms_per_step"] * 1e3, 2) if one else None,
+            "library_plan_partitions": one["partitions"] if one else None}
     if kv is not None:
         res["kivi_int4"] = {"gbs": round(kv["gbs"], 2), "ms_per_step": round(kv["ms_per_step"], 5),
                             "tok_s": round(kv["tok_s"], 1),
@@ -621,6 +787,14 @@ def main():
             res["fp16_with_append"] = {"ms_per_step": round(fpa["ms_per_step"], 5),
                                        "tok_s": round(fpa["tok_s"], 1)}
             res["kivi_int4"]["speedup_vs_fp16_step_with_append"] = round(kv["tok_s"] / fpa["tok_s"], 3)
+    if kvm is not None:
+        res["kivi_int4_mixed_lengths"] = {
+            "workload": "as kivi_int4, sequence s starting at 4096 + s mod 32 tokens: two sequences complete a page "
+                        "at every step",
+            "gbs": round(kvm["gbs"], 2), "ms_per_step": round(kvm["ms_per_step"], 5), "tok_s": round(kvm["tok_s"], 1),
+            "pct_hbm_peak": round(100 * kvm["gbs"] / HBM_PEAK_GBS, 2), "bytes_per_step": int(kvm["bytes_per_step"])}
+        if fp is not None:
+            res["kivi_int4_mixed_lengths"]["speedup_vs_fp16_tok_s"] = round(kvm["tok_s"] / fp["tok_s"], 3)
     if f8 is not None:
         res["fp8_e4m3_long_context"] = {
             "workload": "decode, batch 16, ctx 32768, 32 q / 8 kv heads, d 128, FP8 E4M3 KV with per-tensor "
@@ -629,6 +803,13 @@ def main():
             "gbs": round(f8["gbs"], 2), "pct_hbm_peak": round(100 * f8["gbs"] / HBM_PEAK_GBS, 2),
             "ms_per_step": round(f8["ms_per_step"], 5), "tok_s": round(f8["tok_s"], 1),
             "bytes_per_step": f8["bytes"], "split_k_partial_bytes_not_counted": f8["partial_bytes"]}
+    if f8p is not None:
+        res["fp8_e4m3_long_context_512_token_partitions"] = {
+            "workload": "as fp8_e4m3_long_context, split-K into 64 partitions of 512 tokens (the workload's stated "
+                        "partitioning) + LSE reduce",
+            "gbs": round(f8p["gbs"], 2), "pct_hbm_peak": round(100 * f8p["gbs"] / HBM_PEAK_GBS, 2),
+            "ms_per_step": round(f8p["ms_per_step"], 5), "tok_s": round(f8p["tok_s"], 1),
+            "partitions": f8p["partitions"], "split_k_partial_bytes_not_counted": f8p["partial_bytes"]}
     if pf is not None:
         res["prefill"] = {
             "workload": "chunked prefill, 64 q / 8 kv heads, d 128, bf16: 8 prompts x 2048 tokens as 4 "
@@ -664,7 +845,7 @@ def main():
             "silu_and_mul_us": round(na["act_us"], 2),
             "silu_and_mul_gbs": round(na["act_bytes"] / (na["act_us"] * 1e-6) / 1e9, 2)}
     if not args.no_cpu:
-        res["cpu_baseline"] = cpu_baseline(args.cpu_seconds, 4, min(16, os.cpu_count() or 1))
+        res["cpu_baseline"] = cpu_baseline(args.cpu_seconds / 2, 4)
     print(json.dumps(res), flush=True)
 
 

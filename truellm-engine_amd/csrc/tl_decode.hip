@@ -115,8 +115,8 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(Params p) {
   } s_u;
 
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
-  int bid = blockIdx.x;
-  const int part = bid % p.num_partitions; bid /= p.num_partitions;
+  int part;
+  int bid = grid_item(p, part);
   const int hs = bid % p.head_slices;      bid /= p.head_slices;
   const int kvh = bid % p.num_kv_heads;
   const int seq = bid / p.num_kv_heads;
@@ -312,8 +312,8 @@ __global__ __launch_bounds__(NW * kWave) void decode2_kernel(Params p) {
   __shared__ float s_acc[NW][GT][HEAD];
 
   const int tid = threadIdx.x, wave = tid / kWave;
-  int bid = blockIdx.x;
-  const int part = bid % p.num_partitions; bid /= p.num_partitions;
+  int part;
+  int bid = grid_item(p, part);
   const int hs = bid % p.head_slices;      bid /= p.head_slices;
   const int kvh = bid % p.num_kv_heads;
   const int seq = bid / p.num_kv_heads;
@@ -327,6 +327,21 @@ __global__ __launch_bounds__(NW * kWave) void decode2_kernel(Params p) {
   __syncthreads();
   combine_waves<KV, PO, HEAD, FINAL>(p, NW, &s_m[0][0], &s_l[0][0], &s_acc[0][0][0], seq, kvh, hs,
                                      part, tid, NW * kWave);
+}
+
+// Partitions a sequence has in the merge: ceil(L / partition_tokens), or,
+// for KIVI (kivi_pages > 0), max(1, ceil(min(pages(L), kivi_max_pages) /
+// kivi_pages)); never more than num_partitions.
+__device__ __forceinline__ int merged_partitions(int L, int num_partitions, int partition_tokens, int kivi_residual,
+                                                 int kivi_pages, int kivi_max_pages) {
+  int np;
+  if (kivi_pages > 0) {
+    const int pages = min(kivi_quantized_len(L, kivi_residual) / kKiviPageTokens, kivi_max_pages);
+    np = max(1, (pages + kivi_pages - 1) / kivi_pages);
+  } else {
+    np = (L + partition_tokens - 1) / partition_tokens;
+  }
+  return min(np, num_partitions);
 }
 
 // Log-sum-exp merge of split-K partitions (paged_attention_v2.cu:131-170,
@@ -354,16 +369,10 @@ __global__ __launch_bounds__(64) void lse_reduce_kernel(
     for (int c = 0; c < CH; ++c)
       eo[i][c] = in ? load_scalar<PO>(part_o, (pb + i) * HEAD + threadIdx.x + 64 * c) : 0.f;
   }
-  const int L = seq_lens[seq];
-  int np;
-  if (kivi_pages > 0) {
-    // the page count of the decode kernel: clamped to the page table's width
-    const int pages = min(kivi_quantized_len(L, kivi_residual) / kKiviPageTokens, kivi_max_pages);
-    np = max(1, (pages + kivi_pages - 1) / kivi_pages);
-  } else {
-    np = (L + partition_tokens - 1) / partition_tokens;
-  }
-  np = min(np, num_partitions);
+  // the page count of a KIVI decode is clamped to the page table's width,
+  // as in the decode kernel
+  const int np = merged_partitions(seq_lens[seq], num_partitions, partition_tokens, kivi_residual, kivi_pages,
+                                   kivi_max_pages);
   if (kEarly > 0 && np <= kEarly) {
     float M = -INFINITY;
 #pragma unroll
@@ -400,6 +409,83 @@ __global__ __launch_bounds__(64) void lse_reduce_kernel(
   }
 }
 
+// Log-sum-exp merge for plans of more than 8 partitions (FP8 at 512-token
+// partitions: 64): one workgroup of 4 wavefronts per (sequence, head).  The
+// (max, sum) pairs are reduced over all threads; then wavefront w sums the
+// partial outputs of partitions w, w + 4, ... (lane: head dims lane + 64 c),
+// 4 partitions per round with their loads in flight together, and the 4
+// wavefronts' sums meet in LDS.
+template <Kind QK, int HEAD>
+__global__ __launch_bounds__(256) void lse_reduce_wide_kernel(
+    void* out, const float* part_m, const float* part_l, const float* part_o, const int32_t* seq_lens,
+    int num_heads, int num_partitions, int partition_tokens, int kivi_residual, int kivi_pages,
+    int kivi_max_pages) {
+  constexpr int CH = (HEAD + 63) / 64, U = 4;
+  __shared__ float s_red[2][4];
+  __shared__ float s_o[4][CH * 64];
+  const int sh = blockIdx.x, seq = sh / num_heads;
+  const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
+  const int64_t pb = (int64_t)sh * num_partitions;
+  const int np = merged_partitions(seq_lens[seq], num_partitions, partition_tokens, kivi_residual, kivi_pages,
+                                   kivi_max_pages);
+  float M = -INFINITY;
+  for (int i = tid; i < np; i += 256)
+    if (part_l[pb + i] > 0.f) M = fmaxf(M, part_m[pb + i]);
+  M = wave_max<32, 1>(M);
+  if (lane == 0) s_red[0][wave] = M;
+  __syncthreads();
+  M = fmaxf(fmaxf(s_red[0][0], s_red[0][1]), fmaxf(s_red[0][2], s_red[0][3]));
+  float W = 0.f;
+  for (int i = tid; i < np; i += 256) {
+    const float l = part_l[pb + i];
+    if (l > 0.f) W += l * __expf(part_m[pb + i] - M);
+  }
+  W = wave_sum<32, 1>(W);
+  if (lane == 0) s_red[1][wave] = W;
+  float o[CH];
+#pragma unroll
+  for (int c = 0; c < CH; ++c) o[c] = 0.f;
+  for (int i0 = wave; i0 < np; i0 += 4 * U) {
+    float coef[U], v[U][CH];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const bool in = i0 + 4 * u < np;
+      const int i = in ? i0 + 4 * u : 0;       // every load stays inside the partials
+      const float l = in ? part_l[pb + i] : 0.f;
+      coef[u] = l > 0.f ? l * __expf(part_m[pb + i] - M) : 0.f;
+#pragma unroll
+      for (int c = 0; c < CH; ++c) {
+        const int d = min(lane + 64 * c, HEAD - 1);
+        v[u][c] = (in && lane + 64 * c < HEAD) ? part_o[(pb + i) * HEAD + d] : 0.f;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int c = 0; c < CH; ++c) o[c] += coef[u] > 0.f ? coef[u] * v[u][c] : 0.f;
+  }
+#pragma unroll
+  for (int c = 0; c < CH; ++c) s_o[wave][lane + 64 * c] = o[c];
+  __syncthreads();
+  W = s_red[1][0] + s_red[1][1] + s_red[1][2] + s_red[1][3];
+  for (int d = tid; d < HEAD; d += 256) {
+    const float sum = s_o[0][d] + s_o[1][d] + s_o[2][d] + s_o[3][d];
+    store_scalar<QK>(out, (int64_t)sh * HEAD + d, W > 0.f ? sum / W : 0.f);
+  }
+}
+
+template <Kind QK, int HEAD>
+void launch_reduce(const DecodeLaunch& a) {
+  const int P = a.num_partitions;
+  const dim3 rgrid((unsigned)(a.num_seqs * a.num_heads));
+  if (P > 8)
+    hipLaunchKernelGGL((lse_reduce_wide_kernel<QK, HEAD>), rgrid, dim3(256), 0, a.stream, a.out, a.part_m,
+                       a.part_l, (const float*)a.part_o, a.seq_lens, a.num_heads, P, a.partition_tokens, 0, 0, 0);
+  else
+    hipLaunchKernelGGL((lse_reduce_kernel<QK, Kind::F32, HEAD>), rgrid, dim3(64), 0, a.stream, a.out, a.part_m,
+                       a.part_l, a.part_o, a.seq_lens, a.num_heads, P, a.partition_tokens, 0, 0, 0);
+}
+
 template <Kind KV, Kind QK, int HEAD, int BS, int GT>
 int launch_typed(const DecodeLaunch& a) {
   Params p;
@@ -423,12 +509,9 @@ int launch_typed(const DecodeLaunch& a) {
                        a.stream, p);
   } else {
     dim3 grid((unsigned)(a.num_seqs * a.num_kv_heads * p.head_slices * P));
-    dim3 rgrid((unsigned)(a.num_seqs * a.num_heads));
     hipLaunchKernelGGL((decode_kernel<KV, QK, Kind::F32, HEAD, BS, GT, false>), grid,
                        dim3(kThreads), 0, a.stream, p);
-    hipLaunchKernelGGL((lse_reduce_kernel<QK, Kind::F32, HEAD>), rgrid, dim3(64), 0, a.stream,
-                       a.out, a.part_m, a.part_l, a.part_o, a.seq_lens, a.num_heads, P,
-                       a.partition_tokens, 0, 0, 0);
+    launch_reduce<QK, HEAD>(a);
   }
   return hipGetLastError() == hipSuccess ? 0 : 5;
 }
@@ -455,12 +538,9 @@ int launch_decode2(const DecodeLaunch& a) {
     hipLaunchKernelGGL((decode2_kernel<KV, KV, HEAD, BS, 8, true>), dim3(items), dim3(8 * kWave), 0,
                        a.stream, p);
   } else {
-    dim3 rgrid((unsigned)(a.num_seqs * a.num_heads));
     hipLaunchKernelGGL((decode2_kernel<KV, Kind::F32, HEAD, BS, 4, false>), dim3(items * P),
                        dim3(4 * kWave), 0, a.stream, p);
-    hipLaunchKernelGGL((lse_reduce_kernel<KV, Kind::F32, HEAD>), rgrid, dim3(64), 0, a.stream,
-                       a.out, a.part_m, a.part_l, a.part_o, a.seq_lens, a.num_heads, P,
-                       a.partition_tokens, 0, 0, 0);
+    launch_reduce<KV, HEAD>(a);
   }
   return hipGetLastError() == hipSuccess ? 0 : 5;
 }
@@ -498,20 +578,33 @@ int launch_shape(const DecodeLaunch& a) {
 
 }  // namespace
 
+template <Kind QK>
+void launch_lse_reduce_q(void* out, const float* part_m, const float* part_l, const void* part_o,
+                         const int32_t* seq_lens, int num_seqs, int num_heads, int num_partitions,
+                         int partition_tokens, int kivi_residual, int kivi_pages, int kivi_max_pages,
+                         hipStream_t stream) {
+  const dim3 grid((unsigned)(num_seqs * num_heads));
+  if (num_partitions > 8)
+    hipLaunchKernelGGL((lse_reduce_wide_kernel<QK, 128>), grid, dim3(256), 0, stream, out, part_m, part_l,
+                       (const float*)part_o, seq_lens, num_heads, num_partitions, partition_tokens, kivi_residual,
+                       kivi_pages, kivi_max_pages);
+  else
+    hipLaunchKernelGGL((lse_reduce_kernel<QK, Kind::F32, 128>), grid, dim3(64), 0, stream, out, part_m, part_l,
+                       part_o, seq_lens, num_heads, num_partitions, partition_tokens, kivi_residual, kivi_pages,
+                       kivi_max_pages);
+}
+
 int launch_lse_reduce(void* out, int q_dtype, const float* part_m, const float* part_l,
                       const void* part_o, const int32_t* seq_lens, int num_seqs,
                       int num_heads, int head_size, int num_partitions, int partition_tokens,
                       int kivi_residual, int kivi_pages, int kivi_max_pages, hipStream_t stream) {
   if (head_size != 128) return 3;
-  const dim3 grid((unsigned)(num_seqs * num_heads));
   if (q_dtype == (int)Kind::F16)
-    hipLaunchKernelGGL((lse_reduce_kernel<Kind::F16, Kind::F32, 128>), grid, dim3(64), 0, stream, out,
-                       part_m, part_l, part_o, seq_lens, num_heads, num_partitions, partition_tokens,
-                       kivi_residual, kivi_pages, kivi_max_pages);
+    launch_lse_reduce_q<Kind::F16>(out, part_m, part_l, part_o, seq_lens, num_seqs, num_heads, num_partitions,
+                                   partition_tokens, kivi_residual, kivi_pages, kivi_max_pages, stream);
   else if (q_dtype == (int)Kind::BF16)
-    hipLaunchKernelGGL((lse_reduce_kernel<Kind::BF16, Kind::F32, 128>), grid, dim3(64), 0, stream, out,
-                       part_m, part_l, part_o, seq_lens, num_heads, num_partitions, partition_tokens,
-                       kivi_residual, kivi_pages, kivi_max_pages);
+    launch_lse_reduce_q<Kind::BF16>(out, part_m, part_l, part_o, seq_lens, num_seqs, num_heads, num_partitions,
+                                    partition_tokens, kivi_residual, kivi_pages, kivi_max_pages, stream);
   else
     return 3;
   return hipGetLastError() == hipSuccess ? 0 : 5;

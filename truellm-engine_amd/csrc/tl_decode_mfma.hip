@@ -15,6 +15,8 @@
 // scaled K/V are k_scale * code and v_scale * code).  Workgroups and the
 // split-K / log-sum-exp protocol are those of the 2-byte decode (NW
 // wavefronts stride over a partition's iterations and merge in LDS).
+#include <algorithm>
+
 #include "tl_device.hpp"
 #include "tl_internal.hpp"
 #include "tl_mfma_wave.hpp"
@@ -30,8 +32,7 @@ struct Item {
   int seq, kvh, hs, part, t0, t1;
 };
 __device__ __forceinline__ bool item_of(const Params& p, bool final, Item& w) {
-  int bid = blockIdx.x;
-  w.part = bid % p.num_partitions; bid /= p.num_partitions;
+  int bid = grid_item(p, w.part);
   w.hs = bid % p.head_slices;      bid /= p.head_slices;
   w.kvh = bid % p.num_kv_heads;
   w.seq = bid / p.num_kv_heads;
@@ -61,6 +62,42 @@ __global__ __launch_bounds__(NW * kWave) void mfma2_decode_kernel(Params p) {
   mw::decode_workgroup<KV, KV, PO, NW, FINAL, BS>(p, w.seq, w.kvh, w.hs, w.part, w.t0, w.t1, s_acc, s_m, s_l);
 }
 
+// Split-K, whole partitions per wavefront (mw::partitions_per_wave): the
+// grid is (group of 4 wavefronts' partition runs) x (sequence, kv head,
+// head slice), the group slowest; wavefront w of group g streams
+// partitions (4 g + w) k .. (4 g + w + 1) k - 1, k = parts_per_wave.
+// Three wavefronts per SIMD: left alone the compiler allocates ~192
+// registers (2 per SIMD), although 160 hold the FP8 wavefront without
+// spilling (at 4 per SIMD, 128 registers, it spills ~4 KiB per lane).
+template <Kind KV, Kind QK, int BS>
+__global__ __launch_bounds__(4 * kWave) __attribute__((amdgpu_waves_per_eu(3))) void wave_partition_kernel(
+    Params p) {
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int runs = (p.num_partitions + p.parts_per_wave - 1) / p.parts_per_wave;
+  const int groups = (runs + 3) / 4;
+  const int items = (int)gridDim.x / groups;
+  const int pg = (int)blockIdx.x / items;
+  int bid = (int)blockIdx.x - pg * items;
+  const int hs = bid % p.head_slices;      bid /= p.head_slices;
+  const int kvh = bid % p.num_kv_heads;
+  const int seq = bid / p.num_kv_heads;
+  mw::partitions_per_wave<KV, QK, BS>(p, seq, kvh, hs, (4 * pg + wave) * p.parts_per_wave);
+}
+
+// Whether split-K runs one partition per wavefront: when splitting a
+// partition over the 4 wavefronts of a workgroup would leave each at most
+// 4 iterations (FP8 at 512 / 1024 tokens: 2 / 4 iterations of 64 tokens;
+// 2-byte at 512: 4 of 32), and there are at least 4096 partitions to fill
+// the GPU's SIMDs.  Measured (FP8, batch 16, ctx 32768): 512-token
+// partitions 222 against 281 us, 1024-token 201 against 231 us; with only 4
+// partitions per sequence the 4-wavefront split wins (184 against 299 us),
+// and so it does for 1024-token partitions of 2-byte KV (8 iterations per
+// wavefront: 177 against 193 us).
+template <Kind KV>
+bool partition_per_wave(int partition_tokens, long partitions_total) {
+  return partition_tokens <= 16 * mw::tokens_per_iteration<KV>() && partitions_total >= 4096;
+}
+
 template <Kind KV, Kind QK, int NW, bool FINAL, int BS>
 void launch_kernel(const Params& p, unsigned grid, hipStream_t stream) {
   constexpr Kind PO = FINAL ? QK : Kind::F32;
@@ -83,6 +120,7 @@ int launch_typed(const DecodeLaunch& a) {
   p.group = a.num_heads / a.num_kv_heads;
   p.head_slices = (p.group + mw::kHeads - 1) / mw::kHeads;
   p.gqa_map = a.gqa_map;
+  p.parts_per_wave = 1;
   const bool fp8 = KV == Kind::FP8;
   p.qk_scale = a.scale * (fp8 ? a.k_scale : 1.f) * kLog2e;
   p.v_scale = fp8 ? a.v_scale : 1.f;
@@ -96,7 +134,16 @@ int launch_typed(const DecodeLaunch& a) {
     launch_kernel<KV, QK, 4, true, BS>(p, items, a.stream);
     return hipGetLastError() == hipSuccess ? 0 : 5;
   }
-  launch_kernel<KV, QK, 4, false, BS>(p, items * P, a.stream);
+  if (partition_per_wave<KV>(a.partition_tokens, (long)items * P)) {
+    // as many partitions per wavefront as keep >= 2048 wavefronts (one
+    // resident round at 2-3 per SIMD), at most 8
+    p.parts_per_wave = (int)std::max(1L, std::min(8L, (long)items * P / 2048));
+    const int runs = (P + p.parts_per_wave - 1) / p.parts_per_wave;
+    hipLaunchKernelGGL((wave_partition_kernel<KV, QK, BS>), dim3(items * ((runs + 3) / 4)), dim3(4 * kWave), 0,
+                       a.stream, p);
+  } else {
+    launch_kernel<KV, QK, 4, false, BS>(p, items * P, a.stream);
+  }
   if (hipGetLastError() != hipSuccess) return 5;
   return launch_lse_reduce(a.out, a.q_dtype, a.part_m, a.part_l, a.part_o, a.seq_lens,
                            a.num_seqs, a.num_heads, mw::kHead, P, a.partition_tokens, 0, 0, 0, a.stream);

@@ -43,10 +43,23 @@ struct Params {
   void* part_o;
   int num_heads, num_kv_heads, max_blocks_per_seq, num_blocks;
   int num_partitions, partition_tokens;
+  int parts_per_wave;   // split-K with a wavefront per partition run: partitions each wavefront streams
   int group, head_slices, gqa_map;
   float qk_scale;  // softmax scale * k dequant scale * log2(e)
   float v_scale;
 };
+
+// The work item of a decode workgroup: returns the index of its (sequence,
+// kv head, head slice) and sets its partition.  The partition is the
+// slowest index of the grid: the GPU deals workgroups round-robin to its 8
+// XCDs in dispatch order, and this way every XCD gets the same mix of
+// partitions (with the partition fastest, 4 partitions put partition 0 of
+// every sequence, the one that always has work, on XCDs 0 and 4 only).
+__device__ __forceinline__ int grid_item(const Params& p, int& part) {
+  const int items = (int)gridDim.x / p.num_partitions;
+  part = (int)blockIdx.x / items;
+  return (int)blockIdx.x - part * items;
+}
 
 __device__ __forceinline__ int head_of(const Params& p, int kvh, int gi) {
   return p.gqa_map ? kvh * p.group + gi : kvh + gi * p.num_kv_heads;

@@ -489,8 +489,8 @@ __global__ __launch_bounds__(NW * kWave, 2) void kivi_decode_kernel(KiviParams k
   const Params& p = k.base;
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);   // wave-uniform (SGPR)
-  int bid = blockIdx.x;
-  const int part = bid % p.num_partitions; bid /= p.num_partitions;
+  int part;
+  int bid = grid_item(p, part);
   const int hs = bid % p.head_slices;      bid /= p.head_slices;
   const int kvh = bid % p.num_kv_heads;
   const int seq = bid / p.num_kv_heads;

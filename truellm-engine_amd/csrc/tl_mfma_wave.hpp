@@ -164,6 +164,15 @@ struct State {
   }
 };
 
+// What a wavefront does at the boundaries of the partitions it streams:
+// nothing (NoFlush: the caller takes the state at the end), or hand the
+// finished partition's state to a sink and start the next one afresh.
+struct NoFlush {
+  static constexpr bool kActive = false;
+  int part_tokens = 1;
+  __device__ void operator()(const State&, int) const {}
+};
+
 // ---- FP8 E4M3 KV, f16 / bf16 q: 64 tokens per iteration ----
 //
 // K: the A row m is token quad m (iteration tokens 4 m .. 4 m + 3) and tile
@@ -182,9 +191,9 @@ struct State {
 // |q| in [2^14, 2^15)); the factor returns in the score scale.  The
 // dequant scales fold into the score scale (k_scale) and the output
 // (v_scale).
-template <Kind QK, int BS>
-__device__ __forceinline__ void fp8_wave(const Params& p, int seq, int kvh, int hs, int first_it, int t1,
-                                         int step, float* s_acc_w, float* s_m_w, float* s_l_w) {
+template <Kind QK, int BS, class Flush = NoFlush>
+__device__ __forceinline__ State fp8_wave(const Params& p, int seq, int kvh, int hs, int first_it, int t1,
+                                          int step, const Flush& flush = Flush()) {
   static_assert(BS >= 16 && (BS & (BS - 1)) == 0, "block size: a power of two >= 16");
   constexpr int TPI = 64, RB = BS;           // tokens per iteration; bytes per head-dim row of a block
   constexpr int kBlockBytes = kHead * RB;
@@ -260,6 +269,12 @@ __device__ __forceinline__ void fp8_wave(const Params& p, int seq, int kvh, int 
 
 #pragma unroll 1
   for (; it < t1; it += step) {
+    if constexpr (Flush::kActive) {
+      if (it != first_it && it % flush.part_tokens == 0) {   // a partition ends: its partials out, state afresh
+        flush(st, it / flush.part_tokens - 1);
+        st.init();
+      }
+    }
     const Blocks<NB> nn = table_blocks<NB, BS>(p, table, it + 2 * step, t1);
     const bool has_next = it + step < t1;
     const int ib_next = in_block_bytes<BS, TPI, 1>(it + step);
@@ -336,7 +351,7 @@ __device__ __forceinline__ void fp8_wave(const Params& p, int seq, int kvh, int 
     cur = nxt;
     nxt = nn;
   }
-  st.store(p.v_scale, m, kg, s_acc_w, s_m_w, s_l_w);
+  return st;
 }
 
 // ---- 2-byte KV (f16 / bf16, q of the same type): 32 tokens per iteration ----
@@ -350,9 +365,9 @@ __device__ __forceinline__ void fp8_wave(const Params& p, int seq, int kvh, int 
 // Scores: lane (m, kg) holds head m, iteration tokens 8 kg + 2 r + i, i.e.
 // the run of 8 tokens that is k group kg of the p.v MFMA.
 // V: lane (m, kg) loads the 16 bytes of that run, row d = 16 dt + m.
-template <Kind KV, int BS>
-__device__ __forceinline__ void mfma2_wave(const Params& p, int seq, int kvh, int hs, int first_it, int t1,
-                                           int step, float* s_acc_w, float* s_m_w, float* s_l_w) {
+template <Kind KV, int BS, class Flush = NoFlush>
+__device__ __forceinline__ State mfma2_wave(const Params& p, int seq, int kvh, int hs, int first_it, int t1,
+                                            int step, const Flush& flush = Flush()) {
   static_assert(BS >= 8 && (BS & (BS - 1)) == 0, "block size: a power of two >= 8");
   constexpr int TPI = 32, RB = 2 * BS;       // tokens per iteration; bytes per head-dim row of a block
   constexpr int kBlockBytes = kHead * RB;
@@ -408,6 +423,12 @@ __device__ __forceinline__ void mfma2_wave(const Params& p, int seq, int kvh, in
 
 #pragma unroll 1
   for (; it < t1; it += step) {
+    if constexpr (Flush::kActive) {
+      if (it != first_it && it % flush.part_tokens == 0) {   // a partition ends: its partials out, state afresh
+        flush(st, it / flush.part_tokens - 1);
+        st.init();
+      }
+    }
     const Blocks<NB> nn = table_blocks<NB, BS>(p, table, it + 2 * step, t1);
     const bool has_next = it + step < t1;
     const int ib_next = in_block_bytes<BS, TPI, 2>(it + step);
@@ -472,7 +493,75 @@ __device__ __forceinline__ void mfma2_wave(const Params& p, int seq, int kvh, in
     cur = nxt;
     nxt = nn;
   }
-  st.store(1.f, m, kg, s_acc_w, s_m_w, s_l_w);
+  return st;
+}
+
+template <Kind KV, Kind QK, int BS, class Flush = NoFlush>
+__device__ __forceinline__ State run_wave(const Params& p, int seq, int kvh, int hs, int first_it, int t1,
+                                          int step, const Flush& flush = Flush()) {
+  if constexpr (KV == Kind::FP8)
+    return fp8_wave<QK, BS>(p, seq, kvh, hs, first_it, t1, step, flush);
+  else
+    return mfma2_wave<KV, BS>(p, seq, kvh, hs, first_it, t1, step, flush);
+}
+
+// A wavefront that ran a whole split-K partition alone writes its
+// partials straight from registers: lane (m, kg) holds dims 16 dt + 4 kg +
+// r of head m, normalised by the head's sum; the (max, sum) pair in
+// natural-log units from the lanes of kg 0.  A head with no valid token
+// gets sum 0 (and max -inf), which the log-sum-exp merge skips.
+__device__ __forceinline__ void write_partial(const Params& p, const State& st, float v_scale, int seq, int kvh,
+                                              int hs, int part) {
+  const int lane = threadIdx.x % kWave;
+  const int m = lane & 15, kg = lane >> 4;
+  const float l_tot = sum_kg(st.l_lane);
+  const int gi = hs * kHeads + m;
+  if (gi >= p.group) return;
+  const int64_t pi = ((int64_t)seq * p.num_heads + head_of(p, kvh, gi)) * p.num_partitions + part;
+  const float f = l_tot > 0.f ? v_scale / l_tot : 0.f;
+  float* o = reinterpret_cast<float*>(p.part_o) + pi * kHead;
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt) *reinterpret_cast<f4*>(o + 16 * dt + 4 * kg) = st.o[dt] * f;
+  if (kg == 0) {
+    p.part_m[pi] = l_tot > 0.f ? st.m_run * (1.0f / kLog2e) : -INFINITY;
+    p.part_l[pi] = l_tot;
+  }
+}
+
+// The sink of a wavefront streaming several partitions: each finished
+// partition's partials go to the workspace.
+struct PartialSink {
+  static constexpr bool kActive = true;
+  const Params& p;
+  int part_tokens, seq, kvh, hs;
+  float v_scale;
+  __device__ void operator()(const State& st, int part) const {
+    write_partial(p, st, v_scale, seq, kvh, hs, part);
+  }
+};
+
+// Split-K with whole partitions per wavefront: wavefront w runs partitions
+// [first, first + parts_per_wave) of (sequence, kv head, 16-head slice)
+// alone, as one stream (q loaded once, the next iteration's loads in flight
+// across partition boundaries), writing each partition's partials when it
+// ends; no LDS, no merge inside the workgroup.  For short partitions (FP8
+// at 512 tokens: 8 iterations of 64 tokens) this pays the q prologue, the
+// first loads' latency and the tail once per run of partitions, where
+// splitting each partition over a workgroup pays them per quarter
+// partition.
+template <Kind KV, Kind QK, int BS>
+__device__ __forceinline__ void partitions_per_wave(const Params& p, int seq, int kvh, int hs, int first) {
+  constexpr int TPI = tokens_per_iteration<KV>();
+  if (first >= p.num_partitions) return;
+  const int L = p.seq_lens[seq];
+  const int t0 = first * p.partition_tokens;
+  if (t0 >= L) return;                       // merged only up to ceil(L / partition_tokens)
+  const int last = min(first + p.parts_per_wave, p.num_partitions);
+  const int t1 = min(last * p.partition_tokens, L);
+  const float vs = KV == Kind::FP8 ? p.v_scale : 1.f;
+  const PartialSink sink{p, p.partition_tokens, seq, kvh, hs, vs};
+  const State st = run_wave<KV, QK, BS>(p, seq, kvh, hs, t0, t1, TPI, sink);
+  write_partial(p, st, vs, seq, kvh, hs, (t1 - 1) / p.partition_tokens);
 }
 
 // One workgroup of NW wavefronts over (sequence, kv head, 16-head slice,
@@ -484,13 +573,10 @@ __device__ __forceinline__ void decode_workgroup(const Params& p, int seq, int k
   constexpr int TPI = tokens_per_iteration<KV>();
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
-  float* acc_w = s_acc + wave * kHeads * kHead;
-  if constexpr (KV == Kind::FP8)
-    fp8_wave<QK, BS>(p, seq, kvh, hs, t0 + wave * TPI, t1, NW * TPI, acc_w, s_m + wave * kHeads,
-                     s_l + wave * kHeads);
-  else
-    mfma2_wave<KV, BS>(p, seq, kvh, hs, t0 + wave * TPI, t1, NW * TPI, acc_w, s_m + wave * kHeads,
-                       s_l + wave * kHeads);
+  const int lane = tid % kWave;
+  const State st = run_wave<KV, QK, BS>(p, seq, kvh, hs, t0 + wave * TPI, t1, NW * TPI);
+  st.store(KV == Kind::FP8 ? p.v_scale : 1.f, lane & 15, lane >> 4, s_acc + wave * kHeads * kHead,
+           s_m + wave * kHeads, s_l + wave * kHeads);
   __syncthreads();
   combine_waves<QK, PO, kHead, FINAL, kHeads>(p, NW, s_m, s_l, s_acc, seq, kvh, hs, part, tid, NW * kWave);
 }
