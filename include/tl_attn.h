@@ -158,6 +158,14 @@ int tl_reshape_and_cache_fp8(const void* key, const void* value, int32_t src_dty
                              int32_t block_size, int32_t num_blocks, float k_scale,
                              float v_scale, void* stream);
 
+/* Replaces convert_fp8 (cache_kernels.cu:181-193, :286-295): out[i] =
+ * e4m3(float(in[i]) * scale) for i < n, round to nearest even with
+ * saturation to +-448 (NaN stays NaN), the conversion of
+ * half_to_fp8e4m3 (fp8_utils.cuh:47-53).  in: F16 (the reference's), BF16
+ * or F32; scale multiplies (pass 1 / s for a scale s = absmax / 448). */
+int tl_convert_fp8(uint8_t* out, const void* in, int32_t in_dtype, int64_t n, float scale,
+                   void* stream);
+
 /* Per-tensor E4M3 scale: *scale_out (device fp32) = absmax(x) / 448, the
  * convention of per_token_fp8_quant_kernel (fp8_gemm.cu:80-84) applied to a
  * whole tensor.  x: n elements of dtype F16, BF16 or F32. */

@@ -95,6 +95,11 @@ void copy_blocks(truellm::TrueBuffer& kv_cache, const truellm::TrueBuffer& block
 void swap_blocks(truellm::TrueBuffer& kv_cache, truellm::TrueBuffer& host_cache,
                  const truellm::TrueBuffer& block_mapping, int direction, hipStream_t stream);
 
+/* cache_kernels.cu:286-295 (built there for sm_89+ only): out (one byte per
+ * element, E4M3) = e4m3(in * scale) over every element of in's shape; in
+ * F16, BF16 or F32. */
+void convert_fp8(truellm::TrueBuffer& out, const truellm::TrueBuffer& in, float scale, hipStream_t stream);
+
 /* layernorm_kernels.cu:149-211 and activation_kernels.cu:104-132: x / out
  * [num_tokens, hidden] (shape[0], shape[1]), F32, F16 or BF16 (the
  * reference runs anything but F16 as f32). */

@@ -124,6 +124,18 @@ def test_v1_v2_reject_like_decode():
     assert rc == tla.ERR_INVALID_ARGUMENT
 
 
+def test_convert_fp8_rejects_bad_arguments():
+    L = tla.lib
+    L.tl_convert_fp8.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_float,
+                                 ctypes.c_void_p]
+    assert L.tl_convert_fp8(FAKE, FAKE, tla.F16, -1, 1.0, None) == tla.ERR_INVALID_ARGUMENT
+    assert L.tl_convert_fp8(FAKE, FAKE, tla.FP8_E4M3, 16, 1.0, None) == tla.ERR_INVALID_ARGUMENT
+    assert L.tl_convert_fp8(None, FAKE, tla.F16, 16, 1.0, None) == tla.ERR_INVALID_ARGUMENT
+    assert L.tl_convert_fp8(FAKE, ctypes.c_void_p(0x1001), tla.F16, 16, 1.0, None) == tla.ERR_INVALID_ARGUMENT
+    assert L.tl_convert_fp8(FAKE, ctypes.c_void_p(0x1002), tla.F32, 16, 1.0, None) == tla.ERR_INVALID_ARGUMENT
+    assert L.tl_convert_fp8(None, None, tla.F16, 0, 1.0, None) == tla.OK
+
+
 def test_reshape_rejects_bad_arguments():
     L = tla.lib
     assert L.tl_reshape_and_cache(FAKE, FAKE, FAKE, FAKE, FAKE, 4, 8, 100, 16, 10, tla.F16,
@@ -274,6 +286,7 @@ def test_exports_reference_named_operators():
         "truellm::kivi_decompress(unsigned char const*, __half*, int, int, int, int, ihipStream_t*)",
         "copy_blocks(truellm::TrueBuffer&, truellm::TrueBuffer const&, ihipStream_t*)",
         "swap_blocks(truellm::TrueBuffer&, truellm::TrueBuffer&, truellm::TrueBuffer const&, int, ihipStream_t*)",
+        "convert_fp8(truellm::TrueBuffer&, truellm::TrueBuffer const&, float, ihipStream_t*)",
         "truellm::vq_encode(__half const*, __half const*, unsigned short*, int, int, int, int, ihipStream_t*)",
         "truellm::vq_decode(__half*, __half const*, unsigned short const*, int, int, int, ihipStream_t*)",
         "truellm::codebook_init_kmeans(void const*, void*, int, int, int, int, ihipStream_t*)",

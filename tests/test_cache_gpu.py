@@ -134,3 +134,46 @@ def test_fp8_absmax_scale(code):
     tla.fp8_absmax_scale(zero, out)
     torch.cuda.synchronize()
     assert out.item() == 0.0
+
+
+@pytest.mark.parametrize("scale", [1.0, 0.5, 1.0 / 448.0, 3.7])
+def test_convert_fp8_every_f16_value(scale):
+    """convert_fp8 (cache_kernels.cu:286-295) over all 65 536 fp16 bit
+    patterns: e4m3(float(x) * scale) with RNE and saturation, NaN kept, as
+    the oracle's encoder (pinned against torch and by brute force)."""
+    bits = np.arange(65536, dtype=np.uint16)
+    want = np.empty(65536, np.uint8)
+    orc.lib.orc_convert(orc.ptr(bits), orc.F16, orc.ptr(want), orc.FP8, bits.size, scale)
+    x = dev(bits, orc.F16)
+    out = torch.full((65536,), 0xAB, dtype=torch.uint8, device="cuda")
+    print(f"case convert_fp8 f16 scale={scale}", flush=True)
+    tla.convert_fp8(out, x, scale)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    nan = (want & 0x7F) == 0x7F
+    assert np.array_equal(got[~nan], want[~nan])
+    assert ((got[nan] & 0x7F) == 0x7F).all()
+
+
+@pytest.mark.parametrize("code", [orc.BF16, orc.F32])
+def test_convert_fp8_other_sources_and_unaligned_tails(code):
+    """bf16 / f32 sources; a 16-byte-aligned call and calls at odd offsets
+    and lengths (the element-by-element path), bytes past n untouched."""
+    rng = np.random.default_rng(66)
+    x = (rng.standard_normal(10000) * np.float32(100.0)).astype(np.float32)
+    x[:6] = [np.inf, -np.inf, np.nan, 1e-9, -449.0, 600.0]
+    xb = inputs.encode(x, code)
+    xf = orc.bits_to_f32(xb, code) if code != orc.F32 else xb
+    want = orc.f32_to_e4m3(xf, np.float32(0.25))
+    xd = dev(xb, code)
+    for off, n in ((0, 10000), (1, 9997), (3, 33), (8, 17)):
+        out = torch.full((10016,), 0xAB, dtype=torch.uint8, device="cuda")
+        print(f"case convert_fp8 code={code} off={off} n={n}", flush=True)
+        tla.convert_fp8(out[off:], xd[off:], 0.25, n=n)
+        torch.cuda.synchronize()
+        got = out.cpu().numpy()
+        w = want[off:off + n]
+        g = got[off:off + n]
+        nan = (w & 0x7F) == 0x7F
+        assert np.array_equal(g[~nan], w[~nan]) and ((g[nan] & 0x7F) == 0x7F).all()
+        assert (got[:off] == 0xAB).all() and (got[off + n:] == 0xAB).all()

@@ -195,3 +195,19 @@ def test_block_shims_equal_c_abi():
     SB(tb(kv_a), tb(host), tb(sm), 0, _stream())
     torch.cuda.synchronize()
     assert torch.equal(host[2], kv_a[5].cpu()) and torch.equal(host[4], kv_a[90].cpu())
+
+
+CF8 = _fn("_Z11convert_fp8RN7truellm10TrueBufferERKS0_fP12ihipStream_t", [_R, _R, ctypes.c_float, _S])
+
+
+def test_convert_fp8_shim_equals_c_abi():
+    """The reference-named convert_fp8 over a [blocks, n_kv, d, bs] fp16
+    view (every element of the view's shape) gives the C ABI's bytes."""
+    x = (torch.randn(9, 4, 128, 16, device="cuda") * 50).to(torch.float16)
+    a = torch.zeros(x.numel(), dtype=torch.uint8, device="cuda")
+    b = torch.zeros_like(a)
+    print("case convert_fp8 shim", flush=True)
+    CF8(tb(a.view(9, 4, 128, 16)), tb(x), 1.0 / 3.0, _stream())
+    tla.convert_fp8(b, x, 1.0 / 3.0)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b) and (a != 0).any()

@@ -478,6 +478,18 @@ int tl_reshape_and_cache_fp8(const void* key, const void* value, int32_t src_dty
   return ok();
 }
 
+int tl_convert_fp8(uint8_t* out, const void* in, int32_t in_dtype, int64_t n, float scale, void* stream) {
+  if (n < 0) return fail(TL_ERR_INVALID_ARGUMENT, "n=%lld < 0", (long long)n);
+  if (!is_float_kind(in_dtype)) return fail(TL_ERR_INVALID_ARGUMENT, "in_dtype=%d is not F32/F16/BF16", in_dtype);
+  if (n == 0) return ok();
+  if (!out || !in) return fail(TL_ERR_INVALID_ARGUMENT, "NULL tensor pointer");
+  if (in_dtype != TL_DTYPE_F32 && ((uintptr_t)in & 1u)) return fail(TL_ERR_INVALID_ARGUMENT, "in misaligned");
+  if (in_dtype == TL_DTYPE_F32 && ((uintptr_t)in & 3u)) return fail(TL_ERR_INVALID_ARGUMENT, "in misaligned");
+  const int rc = tl::launch_convert_fp8(out, in, in_dtype, n, scale, (hipStream_t)stream);
+  if (rc) return fail(TL_ERR_BACKEND, "convert_fp8 launch failed");
+  return ok();
+}
+
 int tl_fp8_absmax_scale(const void* x, int32_t dtype, int64_t n, float* scale_out, void* stream) {
   if (n < 0 || !scale_out || (n > 0 && !x)) return fail(TL_ERR_INVALID_ARGUMENT, "bad arguments");
   if (!is_float_kind(dtype)) return fail(TL_ERR_INVALID_ARGUMENT, "dtype=%d", dtype);

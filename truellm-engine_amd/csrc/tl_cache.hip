@@ -25,6 +25,8 @@
 // dst}; a workgroup moves a slice of one block of one pool in 16-byte
 // chunks (bytes when the block or a base is not 16-byte aligned).  Ids
 // outside their pool skip the pair.
+#include <type_traits>
+
 #include "tl_device.hpp"
 #include "tl_internal.hpp"
 
@@ -185,6 +187,54 @@ __global__ __launch_bounds__(256) void reshape_fp8_kernel(
     k_cache[dst + (int64_t)i * block_size] = f32_to_fp8(kf[i] * k_mul);
     v_cache[dst + (int64_t)i * block_size] = f32_to_fp8(vf[i] * v_mul);
   }
+}
+
+// convert_fp8 (cache_kernels.cu:181-193, :286-295): out[i] = e4m3(float(in[i])
+// * scale), RNE with saturation to +-448 (NaN stays NaN).  VEC: 16 elements
+// per thread with 16-byte loads and one 16-byte store (both buffers 16-byte
+// aligned); otherwise element by element.
+__device__ __forceinline__ float fp8_sat(float v) {
+  const float c = __builtin_fminf(__builtin_fmaxf(v, -448.0f), 448.0f);
+  return (v != v) ? v : c;
+}
+__device__ __forceinline__ uint32_t pack4_fp8(float a, float b, float c, float d) {
+  uint32_t w = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(fp8_sat(a), fp8_sat(b), 0, false);
+  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(fp8_sat(c), fp8_sat(d), (int)w, true);
+}
+template <Kind SRC>
+__device__ __forceinline__ float load_elem(const void* p, int64_t i) {
+  if constexpr (SRC == Kind::F32) return reinterpret_cast<const float*>(p)[i];
+  else if constexpr (SRC == Kind::BF16) return bf16_to_f32(reinterpret_cast<const uint16_t*>(p)[i]);
+  else return f16_to_f32(reinterpret_cast<const uint16_t*>(p)[i]);
+}
+template <Kind SRC, bool VEC>
+__global__ __launch_bounds__(256) void convert_fp8_kernel(const void* __restrict__ in, uint8_t* __restrict__ out,
+                                                          int64_t n, float scale) {
+  const int64_t i0 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 16;
+  if (i0 >= n) return;
+  if (VEC && i0 + 16 <= n) {
+    float f[16];
+    if constexpr (SRC == Kind::F32) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const u32x4 v = load16(reinterpret_cast<const float*>(in) + i0 + 4 * c);
+        f[4 * c] = __builtin_bit_cast(float, v.x); f[4 * c + 1] = __builtin_bit_cast(float, v.y);
+        f[4 * c + 2] = __builtin_bit_cast(float, v.z); f[4 * c + 3] = __builtin_bit_cast(float, v.w);
+      }
+    } else {
+      load8<SRC>(in, i0, f);
+      load8<SRC>(in, i0 + 8, f + 8);
+    }
+    u32x4 o;
+    o.x = pack4_fp8(f[0] * scale, f[1] * scale, f[2] * scale, f[3] * scale);
+    o.y = pack4_fp8(f[4] * scale, f[5] * scale, f[6] * scale, f[7] * scale);
+    o.z = pack4_fp8(f[8] * scale, f[9] * scale, f[10] * scale, f[11] * scale);
+    o.w = pack4_fp8(f[12] * scale, f[13] * scale, f[14] * scale, f[15] * scale);
+    *reinterpret_cast<u32x4*>(out + i0) = o;
+    return;
+  }
+  const int64_t i1 = i0 + 16 < n ? i0 + 16 : n;
+  for (int64_t i = i0; i < i1; ++i) out[i] = f32_to_fp8(load_elem<SRC>(in, i) * scale);
 }
 
 // Element j of pair i within one head row: ADJACENT (2i + j), HALVES (i + j d/2).
@@ -481,6 +531,24 @@ int launch_block_copy(const BlockCopy& c, hipStream_t stream) {
     hipLaunchKernelGGL(block_copy_kernel<true>, dim3((unsigned)grid), dim3(256), 0, stream, k);
   else
     hipLaunchKernelGGL(block_copy_kernel<false>, dim3((unsigned)grid), dim3(256), 0, stream, k);
+  return hipGetLastError() == hipSuccess ? 0 : 5;
+}
+
+int launch_convert_fp8(uint8_t* out, const void* in, int dtype, int64_t n, float scale, hipStream_t stream) {
+  if (n <= 0) return 0;
+  const dim3 grid((unsigned)((n + 16 * 256 - 1) / (16 * 256)));
+  const bool vec = (((uintptr_t)out | (uintptr_t)in) % 16) == 0;
+  auto go = [&](auto tag) {
+    constexpr Kind K = decltype(tag)::value;
+    if (vec)
+      hipLaunchKernelGGL((convert_fp8_kernel<K, true>), grid, dim3(256), 0, stream, in, out, n, scale);
+    else
+      hipLaunchKernelGGL((convert_fp8_kernel<K, false>), grid, dim3(256), 0, stream, in, out, n, scale);
+  };
+  if (dtype == (int)Kind::F16) go(std::integral_constant<Kind, Kind::F16>());
+  else if (dtype == (int)Kind::BF16) go(std::integral_constant<Kind, Kind::BF16>());
+  else if (dtype == (int)Kind::F32) go(std::integral_constant<Kind, Kind::F32>());
+  else return 3;
   return hipGetLastError() == hipSuccess ? 0 : 5;
 }
 

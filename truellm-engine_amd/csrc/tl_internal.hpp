@@ -184,6 +184,9 @@ struct PrefillLaunch {
 };
 int launch_prefill(const PrefillLaunch& a);
 
+// out[i] = e4m3(float(in[i]) * scale) for i < n (in: F16, BF16 or F32).
+int launch_convert_fp8(uint8_t* out, const void* in, int dtype, int64_t n, float scale, hipStream_t stream);
+
 // absmax(x)/448 into *scale_out (1 when absmax is 0).
 int launch_fp8_scale(const void* x, int dtype, int64_t n, float* scale_out,
                      hipStream_t stream);

@@ -78,6 +78,12 @@ void swap_blocks(TrueBuffer& kv_cache, TrueBuffer& host_cache, const TrueBuffer&
                                        direction, stream));
 }
 
+void convert_fp8(TrueBuffer& out, const TrueBuffer& in, float scale, hipStream_t stream) {
+  int64_t n = 1;                                   // tb_numel: the product of the view's dims
+  for (int i = 0; i < in.ndim && i < 4; ++i) n *= in.shape[i];
+  report("convert_fp8", tl_convert_fp8((uint8_t*)out.data, in.data, tl_dtype_of(in), n, scale, stream));
+}
+
 void rms_norm(TrueBuffer& out, const TrueBuffer& x, const TrueBuffer& weight, float eps, hipStream_t stream) {
   report("rms_norm", tl_rms_norm(out.data, x.data, weight.data, dim(x, 0), dim(x, 1), eps, tl_dtype_of(x), stream));
 }

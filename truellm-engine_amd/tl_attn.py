@@ -120,6 +120,7 @@ _SIG = {
     "tl_copy_blocks": (ctypes.c_int, [_P, _P, _P, _I, _I, ctypes.c_int64, _P]),
     "tl_swap_blocks": (ctypes.c_int, [_P, _P, _P, _I, _I, _I, ctypes.c_int64, _I, _P]),
     "tl_fp8_absmax_scale": (ctypes.c_int, [_P, _I, ctypes.c_int64, _P, _P]),
+    "tl_convert_fp8": (ctypes.c_int, [_P, _P, _I, ctypes.c_int64, _F, _P]),
     "tl_kivi_compressed_bytes": (ctypes.c_size_t, [_I, _I, _I]),
     "tl_kivi_params_supported": (ctypes.c_int, [_I, _I, _I]),
     "tl_kivi_compress": (ctypes.c_int, [_P, _P, _I, _I, _I, _I, _P]),
@@ -242,6 +243,13 @@ def paged_attention_v2(out, exp_sums, max_logits, tmp_out, q, k_cache, v_cache, 
         _ptr(v_cache), _ptr(block_tables), _ptr(seq_lens), S, H, num_kv_heads, head_size,
         block_size, block_tables.shape[1], k_cache.shape[0], scale, dtype_code(q), gqa_map,
         max_context_len, _stream(stream)))
+
+
+def convert_fp8(out, inp, scale, stream=None, n=None):
+    """cache_kernels.cu:286: out (uint8 E4M3 codes) = e4m3(inp * scale), n
+    elements (default: all of inp)."""
+    n = inp.numel() if n is None else n
+    check(lib.tl_convert_fp8(_ptr(out), _ptr(inp), dtype_code(inp), n, scale, _stream(stream)))
 
 
 def v2_num_partitions(max_context_len: int, block_size: int) -> int:
