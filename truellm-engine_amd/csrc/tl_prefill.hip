@@ -10,10 +10,9 @@
 // block fetched serves all q heads of the group.  Per 64-key iteration:
 //   * the workgroup copies the keys' K (transposed to [key][channel], rows
 //     padded to 136 halves) and V ([channel][key slot], the key order of the
-//     PV operand, rows padded to 72 halves) into one of three LDS stages,
-//     two iterations ahead; each wavefront copies two 8-key runs for half
-//     of the channels, laid out so its LDS writes and the MFMA operand reads
-//     are free of bank conflicts;
+//     PV operand, rows padded to 72 halves) into LDS (two stages of each);
+//     each wavefront copies the 16 keys of one pool block for 64 channels,
+//     with loads that each read 1 KB contiguous in the pool;
 //   * each wavefront (32 rows) forms two 32-key tiles of S^T = K Q^T with
 //     v_mfma_f32_32x32x16_{bf16,f16}: A = K (rows: keys, k: channels) read
 //     from LDS, B = Q^T held in registers for the whole launch.  Lane l then
@@ -25,9 +24,13 @@
 //   * O += P V on the same MFMA: the weights leave the S^T accumulator of
 //     tile t as keys {32 t + 16 s + 4 g + i, 32 t + 16 s + 8 + 4 g + i} for
 //     lane group g, which is used as the k order of step s; V is read from
-//     LDS in that order;
-//   * the q.k MFMAs of the next iteration share a basic block with the
-//     exponentials and P V of the current one (software pipeline).
+//     LDS in that order.
+// The eight wavefronts form two groups with one wavefront of each on every
+// SIMD (wavefront w runs on SIMD w % 4); each wavefront alternates an MFMA
+// phase (P V of one iteration, S of the next) and a VALU phase (mask,
+// softmax, weight packing, staging), group 1 one phase behind group 0, with
+// a workgroup barrier after every phase, so that on each SIMD one
+// wavefront's matrix ops run beside the other's VALU work.
 // Decode rows run the decode wavefronts (tl_mfma_wave.hpp for block_size 16,
 // tl_decode_wave.hpp otherwise), one workgroup per (sequence, kv head, head
 // slice), as a second kernel of the same call on the same stream (one
@@ -66,9 +69,9 @@ __device__ __forceinline__ int v_slot(int k) {
   return (k & ~15) + 4 * (((q & 1) << 1) | (q >> 1)) + (k & 3);
 }
 constexpr float kLazyRescale = 8.f;  // log2 units
-// LDS stages: iteration i is staged in stage i % 3 two iterations ahead, so
-// its K is already visible during iteration i - 1
-constexpr int kStages = 3;
+// LDS stages of K and of V: iteration i uses stage i % 2 (the ping-pong
+// schedule of prefill_kernel writes each stage between its readers)
+constexpr int kStages = 2;
 
 template <Kind KV> struct Mfma32;
 // bf16 keeps 8 mantissa bits: the weights go to the PV product as two bf16
@@ -125,16 +128,20 @@ struct PrefillSmem {
 // behind every K/V load in flight.
 typedef const __attribute__((address_space(4))) int32_t* TableRow;
 
-// Physical block of block index lb of a table row, or -1.
-__device__ __forceinline__ int block_of(const Params& p, TableRow table, int lb) {
-  if (lb >= p.max_blocks_per_seq) return -1;
-  const int b = table[lb];
-  return (b < 0 || b >= p.num_blocks) ? -1 : b;
+// Table entry of block index lb (>= 0), read unconditionally (index
+// clamped to the row, max_blocks_per_seq >= 1); checked_block() turns it
+// into the physical block or -1.
+__device__ __forceinline__ int table_entry(const Params& p, TableRow table, int lb) {
+  return table[__builtin_amdgcn_readfirstlane(min(lb, p.max_blocks_per_seq - 1))];
+}
+__device__ __forceinline__ int checked_block(const Params& p, int lb, int entry) {
+  return (lb >= p.max_blocks_per_seq || entry < 0 || entry >= p.num_blocks) ? -1 : entry;
 }
 
 template <Kind KV, int BS, int NW>
 __global__ __launch_bounds__(NW * kWave) void prefill_kernel(PrefillParams pp) {
   static_assert(BS == 16 || BS == 32, "block size");
+  static_assert(NW == 8, "two groups of four wavefronts, one wavefront of each group per SIMD");
   constexpr int BPI = kPfKeys / BS;                    // pool blocks per iteration
   using M = Mfma32<KV>;
   __shared__ __attribute__((aligned(16))) PrefillSmem<NW, BS> sm;
@@ -143,6 +150,9 @@ __global__ __launch_bounds__(NW * kWave) void prefill_kernel(PrefillParams pp) {
   const int tid = threadIdx.x, lane = tid % kWave;
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
   const int g = lane >> 5, c32 = lane & 31;
+  // group 0 (wavefronts 0-3) leads, group 1 (4-7) runs one phase behind;
+  // wavefront w runs on SIMD w % 4, so every SIMD holds one of each
+  const int grp = wave >> 2;
 
   int b = blockIdx.x;
   const int items = pp.pf_seqs * p.num_kv_heads;
@@ -165,7 +175,8 @@ __global__ __launch_bounds__(NW * kWave) void prefill_kernel(PrefillParams pp) {
   const int qi = row_ok ? my_row / p.group : 0, gi = row_ok ? my_row % p.group : 0;
   const int pos = row_ok ? L - ql + qi : -1;           // keys 0 .. pos
   const int last_row = min(rows, row0 + NW * kPfRows) - 1;
-  const int kend = max(0, L - ql + last_row / p.group + 1);           // keys of the workgroup
+  // keys of the workgroup (wave-uniform: the division runs on the VALU)
+  const int kend = __builtin_amdgcn_readfirstlane(max(0, L - ql + last_row / p.group + 1));
   const int n_it = (kend + kPfKeys - 1) / kPfKeys;
 
   // B operand of S^T: row my_row, channels 16 ks + 8 g .. +7 (zero for padding rows)
@@ -187,41 +198,49 @@ __global__ __launch_bounds__(NW * kWave) void prefill_kernel(PrefillParams pp) {
   const uint16_t* kpool = (const uint16_t*)p.k_cache;
   const uint16_t* vpool = (const uint16_t*)p.v_cache;
 
-  // Staging: an iteration's 64 keys are 8 runs of 8 (run r: keys 8 r .. 8 r
-  // + 7 of the iteration).  Wavefront w copies runs (w >> 1) and (w >> 1) + 4
-  // for half of the channels.  K: channel 2 lane + (w & 1), so each
-  // transposed 2-byte LDS write of a wavefront hits 64 consecutive dwords;
-  // V: channel lane + 64 (w & 1).  Block ids are wave-uniform (scalar table
-  // reads).
-  constexpr int RPW = 2 * (kPfKeys / 8) / NW;          // runs per wavefront
-  static_assert(RPW * NW == 2 * (kPfKeys / 8), "runs x channel halves per wavefront");
-  const int k_ch = 2 * lane + (wave & 1), v_ch = lane + 64 * (wave & 1);
-  // nv: keys of the run that exist (the rest of its V is zeroed when staged,
-  // so that the loads are waited for only there)
-  struct Fetched { u32x4 k[RPW], v[RPW]; int nv[RPW]; };
-  auto run_key = [&](int j) { return 8 * ((wave >> 1) + (NW / 2) * j); };   // first key of run j
-  auto fetch = [&](int it, Fetched& f) {
-#pragma unroll
-    for (int j = 0; j < RPW; ++j) {
-      const int kb = run_key(j);
-      const int key0 = it * kPfKeys + kb;
-      // wave-uniform (the descriptor is built in scalar registers)
-      const int pb = __builtin_amdgcn_readfirstlane(key0 < kend ? block_of(p, table, it * BPI + kb / BS) : -1);
-      f.nv[j] = pb >= 0 ? min(max(L - key0, 0), 8) : 0;
-      // unconditional loads (a missing block has an empty range and reads
-      // zeros): no branch, so nothing waits for them before the staging
-      const int64_t row = pb >= 0 ? ((int64_t)pb * p.num_kv_heads + kvh) * head_stride : 0;
-      const unsigned bytes = pb >= 0 ? unsigned(head_stride * 2) : 0u;
-      f.k[j] = buffer_load16(buffer_rsrc(kpool + row, bytes), unsigned(2 * (k_ch * BS + kb % BS)));
-      f.v[j] = buffer_load16(buffer_rsrc(vpool + row, bytes), unsigned(2 * (v_ch * BS + kb % BS)));
-    }
+  // Staging: wavefront w copies the 16 keys kg = 16 (w >> 1) .. kg + 15 of
+  // an iteration (they lie in one pool block) for the 64 channels 64 (w & 1)
+  // .. + 63, as two units of 32 channels.  Lane l holds channel (l & 31) of
+  // the unit and keys kg + 8 (l >> 5) .. + 7 (16 bytes), so one load of a
+  // unit reads 1 KB that is contiguous in the pool.  The block id of the
+  // key group is wave-uniform (descriptors in scalar registers).
+  constexpr int kUnits = 2;                            // 32-channel units per wavefront
+  static_assert(NW == 2 * (kPfKeys / 16) && kUnits * 32 * 2 == kPfHead, "key groups x channel halves");
+  const int kg = 16 * (wave >> 1);                     // first key of the wavefront's group
+  const int tok = kg + 8 * g;                          // first key of the lane's 8
+  auto unit_ch = [&](int u) { return 64 * (wave & 1) + 32 * u + c32; };
+  // A phase's copy: K of one iteration and V of the one before (K is
+  // staged two phases ahead of its use, V one).  nv: keys of the lane's V
+  // run that exist (the rest is zeroed when staged, so that the loads are
+  // waited for only there).
+  struct Fetched { u32x4 k[kUnits], v[kUnits]; int nv; };
+  auto load_unit = [&](const uint16_t* pool, int pb, int ch) {
+    // unconditional loads (a missing block has an empty range and reads
+    // zeros): no branch, so nothing waits for them before the staging
+    const int64_t row = pb >= 0 ? ((int64_t)pb * p.num_kv_heads + kvh) * head_stride : 0;
+    const unsigned bytes = pb >= 0 ? unsigned(head_stride * 2) : 0u;
+    return buffer_load16(buffer_rsrc(pool + row, bytes), unsigned(2 * (ch * BS + tok % BS)));
   };
-  auto stage = [&](int st, const Fetched& f) {
+  // physical block of the wavefront's key group in iteration it from its
+  // table entry, or -1
+  auto group_block = [&](int it, int entry) {
+    const int key0 = it * kPfKeys + kg;
+    return __builtin_amdgcn_readfirstlane(key0 < kend && it >= 0 ? checked_block(p, it * BPI + kg / BS, entry) : -1);
+  };
+  auto fetch = [&](int it_k, int it_v, int ek, int ev, Fetched& f) {
+    const int pk = group_block(it_k, ek), pv = group_block(it_v, ev);
 #pragma unroll
-    for (int j = 0; j < RPW; ++j) {
-      const int kb = run_key(j);
-      uint16_t* kt = &sm.pf.kt[st][kb * kKtStride + k_ch];
-      const u4v kv = __builtin_bit_cast(u4v, f.k[j]);
+    for (int u = 0; u < kUnits; ++u) {
+      f.k[u] = load_unit(kpool, pk, unit_ch(u));
+      f.v[u] = load_unit(vpool, pv, unit_ch(u));
+    }
+    f.nv = pv >= 0 ? min(max(L - (it_v * kPfKeys + tok), 0), 8) : 0;
+  };
+  auto stage = [&](int it_k, int it_v, const Fetched& f) {
+#pragma unroll
+    for (int u = 0; u < kUnits; ++u) {
+      uint16_t* kt = &sm.pf.kt[it_k & 1][tok * kKtStride + unit_ch(u)];
+      const u4v kv = __builtin_bit_cast(u4v, f.k[u]);
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
         kt[(2 * w) * kKtStride] = (uint16_t)(kv[w] & 0xFFFFu);
@@ -229,16 +248,29 @@ __global__ __launch_bounds__(NW * kWave) void prefill_kernel(PrefillParams pp) {
       }
       // V slots at or past the sequence end may hold anything (NaN codes
       // too, and a zero weight times NaN is NaN): zero them
-      u4v v = __builtin_bit_cast(u4v, f.v[j]);
-      const int nv = f.nv[j];
+      u4v v = __builtin_bit_cast(u4v, f.v[u]);
+      const int nv = f.nv;
       if (nv < 8) {
 #pragma unroll
         for (int w = 0; w < 4; ++w) v[w] = 2 * w >= nv ? 0u : (2 * w + 1 >= nv ? v[w] & 0xFFFFu : v[w]);
       }
-      uint16_t* vrow = &sm.pf.v[st][v_ch * kVStride];
-      *reinterpret_cast<uint2*>(vrow + v_slot(kb)) = uint2{v[0], v[1]};
-      *reinterpret_cast<uint2*>(vrow + v_slot(kb + 4)) = uint2{v[2], v[3]};
+      uint16_t* vrow = &sm.pf.v[it_v & 1][unit_ch(u) * kVStride];
+      *reinterpret_cast<uint2*>(vrow + v_slot(tok)) = uint2{v[0], v[1]};
+      *reinterpret_cast<uint2*>(vrow + v_slot(tok + 4)) = uint2{v[2], v[3]};
     }
+  };
+  // Table entries are read two phases before their use by one vector load:
+  // lane 0 the K block of the fetch, lane 1 its V block, lane 2 + i block i
+  // of the mask.  A scalar table read would be waited for behind every LDS
+  // access in flight (one counter covers both).
+  const int32_t* table_v = p.block_tables + (int64_t)seq * p.max_blocks_per_seq;
+  const int t_lb = lane < 2 ? kg / BS : min(max(lane - 2, 0), BPI - 1);
+  const int t_it = lane == 0 ? 1 + grp : (lane == 1 ? grp : 0);   // iteration offset of the lane's entry
+  // entries of step jn: the fetch of MFMA phase X_jn (K of jn + 1 + grp, V
+  // of jn + grp, staged by Y_jn) and the mask of Y_jn
+  auto table_prefetch = [&](int jn) {
+    const int lb = max(jn + t_it, 0) * BPI + t_lb;
+    return table_v[min(lb, p.max_blocks_per_seq - 1)];
   };
 
   f16v o[4];
@@ -246,36 +278,47 @@ __global__ __launch_bounds__(NW * kWave) void prefill_kernel(PrefillParams pp) {
   for (int c = 0; c < 4; ++c) o[c] = f16v{};
   float m_used = -INFINITY, l_part = 0.f;
   float* s_row = &sm.pf.row[wave][0];
+  // Scores and weights of an iteration share registers: QK leaves the S^T
+  // tiles in sp (MFMA phase), SM turns tile t into its packed weights in
+  // place (VALU phase: words 8 s .. 8 s + 3 hold hi of step s, 8 s + 4 ..
+  // the lo terms), and PV of the next MFMA phase reads them before QK
+  // overwrites them.
+  // (__builtin_bit_cast of a vector element itself, v[i], reads element 0
+  // with this compiler: the elements go through a value conversion first.)
+  f16v sp[KT];
+  auto p_words = [&](int t, int s2, int part) {
+    const int w = 8 * s2 + 4 * part;
+    return u32x4{__builtin_bit_cast(unsigned, (float)sp[t][w]), __builtin_bit_cast(unsigned, (float)sp[t][w + 1]),
+                 __builtin_bit_cast(unsigned, (float)sp[t][w + 2]), __builtin_bit_cast(unsigned, (float)sp[t][w + 3])};
+  };
 
-  // Software pipeline.  Iteration it first masks its scores (computed
-  // during it - 1) and decides the rescale; then one branch-free block
-  // holds the q.k MFMAs of it + 1 (its K is staged two iterations ahead),
-  // the exponentials and weight packing of it and its P V MFMAs, which the
-  // compiler interleaves so the matrix cores and the VALU work at once.  A wavefront
-  // past its last keys runs the block on masked scores (weights 0).  Keys
-  // of an iteration entirely at or below the wavefront's first query
-  // position, in blocks that exist, need no mask.  The scores stay unscaled
-  // until the exponent (qk_scale > 0, so the max commutes with the scale).
-  const int wmin_pos = L - ql + wrow0 / p.group;
-  auto qk = [&](int it, f16v (&sa)[KT]) {
-    const uint16_t* kst = sm.pf.kt[it % kStages];
+  // ---- the two halves of an iteration ----
+  // QK(it): S^T tiles of iteration it (K stage it % 2)
+  auto qk = [&](int it) {
+    const uint16_t* kst = sm.pf.kt[it & 1];
 #pragma unroll
     for (int t = 0; t < KT; ++t) {
-      sa[t] = f16v{};
       const uint16_t* ktw = kst + (32 * t + c32) * kKtStride + 8 * g;
+      f16v acc = f16v{};
 #pragma unroll
       for (int ks = 0; ks < 8; ++ks)
-        sa[t] = M::mma(*reinterpret_cast<const u32x4*>(ktw + 16 * ks), qb[ks], sa[t]);
+        acc = M::mma(*reinterpret_cast<const u32x4*>(ktw + 16 * ks), qb[ks], acc);
+      sp[t] = acc;
     }
   };
-  // mask, row max and lazy rescale of iteration it; returns the exponent offset
-  auto prepare = [&](int it, f16v (&sa)[KT]) {
+  // SM(it): mask, row max, lazy rescale, exponentials and weight packing.
+  // Keys of an iteration entirely at or below the wavefront's first query
+  // position, in blocks that exist, need no mask.  The scores stay unscaled
+  // until the exponent (qk_scale > 0, so the max commutes with the scale).
+  const int wmin_pos = __builtin_amdgcn_readfirstlane(L - ql + wrow0 / p.group);
+  const int pos_g = pos - 4 * g;
+  auto softmax = [&](int it, int t_entries) {
     const int k0 = it * kPfKeys;
     bool blk_ok[BPI];
     bool all_ok = true;
 #pragma unroll
     for (int bi = 0; bi < BPI; ++bi) {
-      blk_ok[bi] = block_of(p, table, it * BPI + bi) >= 0;
+      blk_ok[bi] = checked_block(p, it * BPI + bi, __builtin_amdgcn_readlane(t_entries, 2 + bi)) >= 0;
       all_ok = all_ok && blk_ok[bi];
     }
     float mx = -INFINITY;
@@ -283,16 +326,19 @@ __global__ __launch_bounds__(NW * kWave) void prefill_kernel(PrefillParams pp) {
 #pragma unroll
       for (int t = 0; t < KT; ++t)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sa[t][r]);
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sp[t][r]);
     } else {
 #pragma unroll
       for (int t = 0; t < KT; ++t)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const int kk = 32 * t + 8 * (r >> 2) + 4 * g + (r & 3);
-          const bool ok = k0 + kk <= pos && blk_ok[kk / BS];
-          sa[t][r] = ok ? sa[t][r] : -INFINITY;
-          mx = fmaxf(mx, sa[t][r]);
+          // key k0 + kk, kk = 32 t + 8 (r >> 2) + 4 g + (r & 3): the
+          // comparison is written with the wave-uniform part on the left
+          // so that no per-lane value of each r is kept across the loop
+          const int kc = 32 * t + 8 * (r >> 2) + (r & 3);
+          const bool ok = k0 + kc <= pos_g && blk_ok[(kc + 4 * g) / BS];
+          sp[t][r] = ok ? sp[t][r] : -INFINITY;
+          mx = fmaxf(mx, sp[t][r]);
         }
     }
     {
@@ -323,72 +369,183 @@ __global__ __launch_bounds__(NW * kWave) void prefill_kernel(PrefillParams pp) {
       }
       __builtin_amdgcn_wave_barrier();
     }
-    return (m_used == -INFINITY) ? 0.f : m_used;
-  };
-  auto exp_pv = [&](int it, const f16v (&sa)[KT], float m_use) {
-    const uint16_t* vst = sm.pf.v[it % kStages];
+    const float m_use = (m_used == -INFINITY) ? 0.f : m_used;
 #pragma unroll
     for (int t = 0; t < KT; ++t) {
       float pw[16];
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        pw[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sa[t][r], p.qk_scale, -m_use));
+        pw[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sp[t][r], p.qk_scale, -m_use));
         l_part += pw[r];
       }
 #pragma unroll
-      for (int st2 = 0; st2 < 2; ++st2) {
-        const int r0 = 8 * st2;
+      for (int s2 = 0; s2 < 2; ++s2) {
+        const int r0 = 8 * s2;
         const u32x4 pa = {M::pack(pw[r0 + 0], pw[r0 + 1]), M::pack(pw[r0 + 2], pw[r0 + 3]),
                           M::pack(pw[r0 + 4], pw[r0 + 5]), M::pack(pw[r0 + 6], pw[r0 + 7])};
-        u32x4 pl = {0u, 0u, 0u, 0u};
+        const u4v pa4 = __builtin_bit_cast(u4v, pa);
+        u4v pl4 = {0u, 0u, 0u, 0u};
         if constexpr (M::kSplitP) {
+          // bf16 keeps 8 mantissa bits: the weights go to P V as two bf16
+          // terms, hi (taken straight from the packed pair, low half first)
+          // and lo = p - hi
+          const u4v h2 = __builtin_bit_cast(u4v, pa);
           float lo[8];
 #pragma unroll
-          for (int i = 0; i < 8; ++i) lo[i] = pw[r0 + i] - M::hi(pw[r0 + i]);
-          pl = u32x4{M::pack(lo[0], lo[1]), M::pack(lo[2], lo[3]), M::pack(lo[4], lo[5]), M::pack(lo[6], lo[7])};
+          for (int i = 0; i < 4; ++i) {
+            lo[2 * i] = pw[r0 + 2 * i] - __builtin_bit_cast(float, h2[i] << 16);
+            lo[2 * i + 1] = pw[r0 + 2 * i + 1] - __builtin_bit_cast(float, h2[i] & 0xFFFF0000u);
+          }
+          pl4 = u4v{M::pack(lo[0], lo[1]), M::pack(lo[2], lo[3]), M::pack(lo[4], lo[5]), M::pack(lo[6], lo[7])};
         }
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const int ch = 32 * c + c32;
-          // slots 0-3: keys 32 t + 16 st2 + 4 g + i, slots 4-7: the same + 8
-          const u32x4 vb = *reinterpret_cast<const u32x4*>(vst + ch * kVStride + 32 * t + 16 * st2 + 8 * g);
-          o[c] = M::mma(pa, vb, o[c]);
-          if constexpr (M::kSplitP) o[c] = M::mma(pl, vb, o[c]);
+        for (int i = 0; i < 4; ++i) {
+          sp[t][8 * s2 + i] = __builtin_bit_cast(float, (unsigned)pa4[i]);
+          sp[t][8 * s2 + 4 + i] = __builtin_bit_cast(float, (unsigned)pl4[i]);
         }
       }
     }
   };
 
-  // Fetches and stages run unconditionally: past the last iteration the
-  // blocks are missing (empty ranges, zeros), and a stage that no
-  // iteration reads takes them.  A conditional fetch would leave the loop's
-  // waits for one stage's loads unable to tell how many newer loads are in
-  // flight, and they would wait for all of them.
-  Fetched fs0, fs1;
-  f16v sa0[KT], sa1[KT];
-  fetch(0, fs0);
-  stage(0, fs0);
-  fetch(1, fs1);
-  stage(1, fs1);
-  fetch(2, fs0);
-  __syncthreads();
-  qk(0, sa0);
-  // f_stage holds it + 2 (staged at the end of it), f_free receives it + 3;
-  // s_cur holds the scores of it, s_next receives those of it + 1
-  auto iteration = [&](int it, Fetched& f_stage, Fetched& f_free, f16v (&s_cur)[KT], f16v (&s_next)[KT]) {
-    fetch(it + 3, f_free);
-    const float m_use = prepare(it, s_cur);
-    qk(it + 1, s_next);
-    exp_pv(it, s_cur, m_use);
-    stage((it + 2) % kStages, f_stage);
-    __syncthreads();
-  };
-#pragma unroll 1
-  for (int it = 0; it < n_it; it += 2) {
-    iteration(it, fs0, fs1, sa0, sa1);
-    if (it + 1 >= n_it) break;
-    iteration(it + 1, fs1, fs0, sa1, sa0);
+  // ---- ping-pong schedule ----
+  // A wavefront alternates MFMA phases X_j = {PV(j - 1), QK(j)} and VALU
+  // phases Y_j = {SM(j); stage K(j + 1 + grp), V(j + grp)}: X_0 Y_0 X_1 ...
+  // Y_{n-1} X_n, group 1 with a leading Y_{-1} (staging only).  Every phase
+  // ends at a workgroup barrier, so on each SIMD one wavefront's matrix ops
+  // run beside the other's VALU work.  K(k) is read at phases 2k and 2k + 1
+  // and written in [2k - 2, 2k - 1]; V(k) is read at 2k + 2 and 2k + 3 and
+  // written in [2k, 2k + 1]: two LDS stages of each suffice.  Stages of
+  // iterations past the last hold zeros (missing blocks) and are not read.
+  // The K/V loads of a VALU phase's staging are issued at the start of the
+  // MFMA phase before it (one register set, a phase of latency slack); the
+  // table entries they need were read by the VALU phase before that.
+  Fetched fs;
+  int t_ent, t_mask = 0;
+  {
+    // K(0) before the first barrier; group 1's Y_{-1} stages K(1), V(0)
+    const int e0 = table_entry(p, table, kg / BS), e1 = table_entry(p, table, BPI + kg / BS);
+    fetch(0, -1, e0, e0, fs);
+    stage(0, -1, fs);                   // K(0); V stage 1 gets zeros (iteration -1 is missing)
+    if (grp == 1) fetch(1, 0, e1, e0, fs);
+    t_ent = table_prefetch(0);
   }
+  __syncthreads();
+
+  // X_{j+1}: the loads of Y_{j+1}, P V of iteration j and S of iteration
+  // j + 1 (past the last iteration S is formed on a zero stage and not
+  // used: unconditional, so that no path carries scores or weights across a
+  // phase)
+  auto fetch_for = [&](int jn) {        // the loads staged by Y_jn
+    fetch(jn + 1 + grp, jn + grp, __builtin_amdgcn_readlane(t_ent, 0), __builtin_amdgcn_readlane(t_ent, 1), fs);
+  };
+  auto phase_x0 = [&]() {
+    fetch_for(0);
+    t_mask = t_ent;
+    t_ent = table_prefetch(1);
+    __builtin_amdgcn_s_setprio(1);
+    qk(0);
+    __builtin_amdgcn_s_setprio(0);
+  };
+  // PV(j) and QK(j + 1).  P V: the weights of tile t leave the S^T
+  // accumulator as keys 32 t + 16 s + 4 g + i (slots 0-3) and the same + 8
+  // (slots 4-7) for lane group g, the k order of step s.  The LDS operand
+  // reads are kept ahead of the matrix ops (the compiler alone keeps one or two in
+  // flight, and the phase then waits on LDS latency): P V in four groups
+  // (t, s2) of the four V operands of o[0..3], issued hi for all four, then
+  // lo, so that no MFMA waits for the one before it, with the next group's
+  // reads in flight; then S with both tiles' chains interleaved and the K
+  // reads of the next kQkAhead steps in flight.
+  auto pv_qk = [&](int j) {
+    const uint16_t* vst = sm.pf.v[j & 1];
+    const uint16_t* kst = sm.pf.kt[(j + 1) & 1];
+    auto v_op = [&](int grp4, int c) {
+      const int t = grp4 >> 1, s2 = grp4 & 1;
+      return *reinterpret_cast<const u32x4*>(vst + (32 * c + c32) * kVStride + 32 * t + 16 * s2 + 8 * g);
+    };
+    auto k_op = [&](int t, int ks) {
+      return *reinterpret_cast<const u32x4*>(kst + (32 * t + c32) * kKtStride + 8 * g + 16 * ks);
+    };
+    u32x4 vb[2][4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) vb[0][c] = v_op(0, c);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      if (q + 1 < 4) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) vb[(q + 1) & 1][c] = v_op(q + 1, c);
+      }
+      const int t = q >> 1, s2 = q & 1;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) o[c] = M::mma(p_words(t, s2, 0), vb[q & 1][c], o[c]);
+      if constexpr (M::kSplitP) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) o[c] = M::mma(p_words(t, s2, 1), vb[q & 1][c], o[c]);
+      }
+    }
+    constexpr int kQkAhead = 3;
+    u32x4 kb[kQkAhead + 1][KT];
+#pragma unroll
+    for (int ks = 0; ks < kQkAhead; ++ks)
+#pragma unroll
+      for (int t = 0; t < KT; ++t) kb[ks][t] = k_op(t, ks);
+    __builtin_amdgcn_sched_barrier(0);   // the reads stay issued ahead of their MFMAs
+    f16v acc[KT];
+#pragma unroll
+    for (int t = 0; t < KT; ++t) acc[t] = f16v{};
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) {
+      if (ks + kQkAhead < 8) {
+#pragma unroll
+        for (int t = 0; t < KT; ++t) kb[(ks + kQkAhead) % (kQkAhead + 1)][t] = k_op(t, ks + kQkAhead);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+      for (int t = 0; t < KT; ++t) acc[t] = M::mma(kb[ks % (kQkAhead + 1)][t], qb[ks], acc[t]);
+    }
+#pragma unroll
+    for (int t = 0; t < KT; ++t) sp[t] = acc[t];
+  };
+  // The loads are unconditional (past the last iteration the blocks are
+  // missing: empty ranges, no traffic), so that every path leaves the same
+  // loads in flight and the wait counts stay exact; a path without them
+  // makes the next phase wait for every load.  The table read of step
+  // jn + 1 goes out here too, two phases before its first use.
+  auto phase_x = [&](int j) {
+    fetch_for(j + 1);
+    t_mask = t_ent;                      // waited for by fetch_for: a plain copy
+    t_ent = table_prefetch(j + 2);
+    __builtin_amdgcn_s_setprio(1);
+    pv_qk(j);
+    __builtin_amdgcn_s_setprio(0);
+  };
+  // Y_j: SM(j) with the mask entries of step j and the staging of
+  // K(j + 1 + grp), V(j + grp)
+  auto phase_y = [&](int j) {
+    softmax(j, t_mask);
+    // the weights are formed here: the exponentials and packing are plain
+    // arithmetic, which the compiler would otherwise sink past the barrier
+    // into the MFMA phase that reads them
+#pragma unroll
+    for (int t = 0; t < KT; ++t) asm volatile("" ::"v"(sp[t]));
+    stage(j + 1 + grp, j + grp, fs);
+  };
+  // Group 0: X_0 at phase 0, Y_j at 2j + 1, X_{j+1} at 2j + 2, then one
+  // empty phase; group 1: Y_{-1} (staging only) at phase 0, X_0 at 1, Y_j
+  // at 2j + 2, X_{j+1} at 2j + 3.  Both pass 2 n + 2 barriers.
+  if (grp == 1) {
+    stage(1, 0, fs);
+    __syncthreads();
+  }
+  phase_x0();
+  __syncthreads();
+#pragma unroll 1
+  for (int j = 0; j < n_it; ++j) {
+    phase_y(j);
+    __syncthreads();
+    phase_x(j);
+    __syncthreads();
+  }
+  if (grp == 0) __syncthreads();
 
   // ---- normalise and store: lane holds rows 8 j + 4 g + i, channels 32 c + c32 ----
   {
