@@ -186,11 +186,7 @@ __global__ __launch_bounds__(NW * kWave) void prefill_kernel(PrefillParams pp) {
         ((int64_t)(q0 + qi) * p.num_heads + head_of(p, kvh, gi)) * kPfHead + 8 * g;
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) qb[ks] = row_ok ? load16(qrow + 16 * ks) : u32x4{0u, 0u, 0u, 0u};
-    // q is waited for here, on every path: otherwise the loop's first use
-    // of it waits for every load in flight, the K/V loads of later
-    // iterations included
-#pragma unroll
-    for (int ks = 0; ks < 8; ++ks) asm volatile("" ::"v"(qb[ks].x), "v"(qb[ks].y), "v"(qb[ks].z), "v"(qb[ks].w));
+    // waited for at its first use: the prologue's K/V loads go out meanwhile
   }
 
   const TableRow table = (TableRow)(p.block_tables + (int64_t)seq * p.max_blocks_per_seq);
@@ -227,14 +223,22 @@ __global__ __launch_bounds__(NW * kWave) void prefill_kernel(PrefillParams pp) {
     const int key0 = it * kPfKeys + kg;
     return __builtin_amdgcn_readfirstlane(key0 < kend && it >= 0 ? checked_block(p, it * BPI + kg / BS, entry) : -1);
   };
+  // the blocks of one copy; load(i) issues its i-th load (K unit i, then V
+  // unit i - kUnits), so that a phase can spread them over its matrix ops
+  struct FetchPlan { int pk, pv; };
+  auto plan = [&](int it_k, int it_v, int ek, int ev, Fetched& f) {
+    const FetchPlan fp = {group_block(it_k, ek), group_block(it_v, ev)};
+    f.nv = fp.pv >= 0 ? min(max(L - (it_v * kPfKeys + tok), 0), 8) : 0;
+    return fp;
+  };
+  auto load = [&](const FetchPlan& fp, int i, Fetched& f) {
+    if (i < kUnits) f.k[i] = load_unit(kpool, fp.pk, unit_ch(i));
+    else f.v[i - kUnits] = load_unit(vpool, fp.pv, unit_ch(i - kUnits));
+  };
   auto fetch = [&](int it_k, int it_v, int ek, int ev, Fetched& f) {
-    const int pk = group_block(it_k, ek), pv = group_block(it_v, ev);
+    const FetchPlan fp = plan(it_k, it_v, ek, ev, f);
 #pragma unroll
-    for (int u = 0; u < kUnits; ++u) {
-      f.k[u] = load_unit(kpool, pk, unit_ch(u));
-      f.v[u] = load_unit(vpool, pv, unit_ch(u));
-    }
-    f.nv = pv >= 0 ? min(max(L - (it_v * kPfKeys + tok), 0), 8) : 0;
+    for (int i = 0; i < 2 * kUnits; ++i) load(fp, i, f);
   };
   auto stage = [&](int it_k, int it_v, const Fetched& f) {
 #pragma unroll
@@ -372,12 +376,13 @@ __global__ __launch_bounds__(NW * kWave) void prefill_kernel(PrefillParams pp) {
     const float m_use = (m_used == -INFINITY) ? 0.f : m_used;
 #pragma unroll
     for (int t = 0; t < KT; ++t) {
-      float pw[16];
+      float pw[16], ls[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         pw[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sp[t][r], p.qk_scale, -m_use));
-        l_part += pw[r];
+        ls[r & 3] += pw[r];
       }
+      l_part += (ls[0] + ls[1]) + (ls[2] + ls[3]);
 #pragma unroll
       for (int s2 = 0; s2 < 2; ++s2) {
         const int r0 = 8 * s2;
@@ -422,12 +427,17 @@ __global__ __launch_bounds__(NW * kWave) void prefill_kernel(PrefillParams pp) {
   Fetched fs;
   int t_ent, t_mask = 0;
   {
-    // K(0) before the first barrier; group 1's Y_{-1} stages K(1), V(0)
+    // All of the prologue's loads go out together (q above, K(0), the copy
+    // of group 1's Y_{-1}, the first table entries), in the order in which
+    // they are waited for: K(0) is staged before the first barrier; group 1's
+    // Y_{-1} stages K(1), V(0) (group 0 loads its own copy again in X_0,
+    // unconditional so that the wait counts agree on every path)
     const int e0 = table_entry(p, table, kg / BS), e1 = table_entry(p, table, BPI + kg / BS);
-    fetch(0, -1, e0, e0, fs);
-    stage(0, -1, fs);                   // K(0); V stage 1 gets zeros (iteration -1 is missing)
-    if (grp == 1) fetch(1, 0, e1, e0, fs);
+    Fetched f0;
+    fetch(0, -1, e0, e0, f0);
+    fetch(1, 0, e1, e0, fs);
     t_ent = table_prefetch(0);
+    stage(0, -1, f0);                   // K(0); V stage 1 gets zeros (iteration -1 is missing)
   }
   __syncthreads();
 
@@ -455,7 +465,7 @@ __global__ __launch_bounds__(NW * kWave) void prefill_kernel(PrefillParams pp) {
   // lo, so that no MFMA waits for the one before it, with the next group's
   // reads in flight; then S with both tiles' chains interleaved and the K
   // reads of the next kQkAhead steps in flight.
-  auto pv_qk = [&](int j) {
+  auto pv_qk = [&](int j, const FetchPlan& fp) {
     const uint16_t* vst = sm.pf.v[j & 1];
     const uint16_t* kst = sm.pf.kt[(j + 1) & 1];
     auto v_op = [&](int grp4, int c) {
@@ -470,6 +480,8 @@ __global__ __launch_bounds__(NW * kWave) void prefill_kernel(PrefillParams pp) {
     for (int c = 0; c < 4; ++c) vb[0][c] = v_op(0, c);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
+      static_assert(2 * kUnits == 4, "one load per P V group");
+      load(fp, q, fs);
       if (q + 1 < 4) {
 #pragma unroll
         for (int c = 0; c < 4; ++c) vb[(q + 1) & 1][c] = v_op(q + 1, c);
@@ -511,11 +523,12 @@ __global__ __launch_bounds__(NW * kWave) void prefill_kernel(PrefillParams pp) {
   // makes the next phase wait for every load.  The table read of step
   // jn + 1 goes out here too, two phases before its first use.
   auto phase_x = [&](int j) {
-    fetch_for(j + 1);
-    t_mask = t_ent;                      // waited for by fetch_for: a plain copy
+    const FetchPlan fp = plan(j + 2 + grp, j + 1 + grp, __builtin_amdgcn_readlane(t_ent, 0),
+                              __builtin_amdgcn_readlane(t_ent, 1), fs);   // the copy staged by Y_{j+1}
+    t_mask = t_ent;                      // waited for by the readlanes: a plain copy
     t_ent = table_prefetch(j + 2);
     __builtin_amdgcn_s_setprio(1);
-    pv_qk(j);
+    pv_qk(j, fp);
     __builtin_amdgcn_s_setprio(0);
   };
   // Y_j: SM(j) with the mask entries of step j and the staging of
@@ -527,6 +540,7 @@ __global__ __launch_bounds__(NW * kWave) void prefill_kernel(PrefillParams pp) {
     // into the MFMA phase that reads them
 #pragma unroll
     for (int t = 0; t < KT; ++t) asm volatile("" ::"v"(sp[t]));
+    asm volatile("" ::"v"(l_part));
     stage(j + 1 + grp, j + grp, fs);
   };
   // Group 0: X_0 at phase 0, Y_j at 2j + 1, X_{j+1} at 2j + 2, then one
