@@ -59,18 +59,20 @@ def config2b_lens():
     return np.random.default_rng(0x7E5E0002).integers(512, 8193, size=S).tolist()
 
 
-def kivi_bytes(lens, R, completes_page):
-    """KIVI bytes of one step: pages (160 B/token/kv head) + fp16 window
-    (512 B/token/kv head) + q/out + tables, plus the appended token and, for
-    each sequence whose append completes a page, its quantisation (32 fp16
-    tokens read, 5 KiB written per kv head)."""
+def kivi_bytes(lens, R, completes_page, bits=4):
+    """KIVI bytes of one step: pages (INT4: 160 B/token/kv head, INT8: 288)
+    + fp16 window (512 B/token/kv head) + q/out + tables, plus the appended
+    token and, for each sequence whose append completes a page, its
+    quantisation (32 fp16 tokens read, one page of 5 KiB (INT4) or 9 KiB
+    (INT8) written per kv head)."""
+    page = 5120 if bits == 4 else 9216
     tot = 0
-    for L, page in zip(lens, completes_page):
+    for L, done in zip(lens, completes_page):
         lq = 0 if L <= R else ((L - R) // 32) * 32
-        tot += NKV * (lq * 160 + (L - lq) * 512)
+        tot += NKV * (lq * (page // 32) + (L - lq) * 512)
         tot += (lq // 32 + (L - lq + BS - 1) // BS) * 4 + 4
-        if page:
-            tot += NKV * (32 * 512 + 5120)
+        if done:
+            tot += NKV * (32 * 512 + page)
     tot += len(lens) * H * D * 2 * 2
     tot += len(lens) * NKV * D * 2 * 2
     return tot
@@ -269,10 +271,11 @@ def kivi_steps(steps):
     return max(64, (steps + 63) // 64 * 64)
 
 
-def bench_kivi(args, R=128, mixed=False, name=None):
-    """KIVI INT4 append + decode steps at batch 64 from context 4096 (mixed:
-    sequence s starts at 4096 + s mod 32 tokens, so two sequences complete a
-    page at every step instead of all 64 on one step in 32)."""
+def bench_kivi(args, R=128, mixed=False, name=None, bits=4):
+    """KIVI append + decode steps (INT4 pages, or INT8 with bits=8) at batch
+    64 from context 4096 (mixed: sequence s starts at 4096 + s mod 32 tokens,
+    so two sequences complete a page at every step instead of all 64 on one
+    step in 32)."""
     import torch
 
     import tl_attn as tla
@@ -298,7 +301,7 @@ def bench_kivi(args, R=128, mixed=False, name=None):
         num_pages = S * max_pages + 8
         pperm = torch.randperm(num_pages, generator=g, device="cuda").to(torch.int32)
         ptables = pperm[: S * max_pages].view(S, max_pages).contiguous()
-        pages = torch.zeros(num_pages, NKV, tla.KIVI_PAGE_BYTES, dtype=torch.uint8, device="cuda")
+        pages = torch.zeros(num_pages, NKV, tla.kivi_page_bytes(bits), dtype=torch.uint8, device="cuda")
         reps.append([k, v, tables, ptables, pages, num_pages])
     q = torch.randn(S, H, D, generator=g, device="cuda", dtype=torch.float16)
     knew = torch.randn(S, NKV, D, generator=g, device="cuda", dtype=torch.float16)
@@ -322,13 +325,13 @@ def bench_kivi(args, R=128, mixed=False, name=None):
         slot = tables_host[r][rows, pos // BS] * BS + pos % BS
         slot_dev.append(slot.to(torch.int32).cuda())
     desc0 = tla.make_kivi_desc(q, reps[0][0], reps[0][2], reps[0][3], reps[0][5], NKV, scale,
-                               residual_length=R, gqa_map=tla.GQA_GROUPED)
+                               residual_length=R, gqa_map=tla.GQA_GROUPED, bits=bits)
     ws = torch.empty(max(16, tla.kivi_workspace_bytes(desc0, Lmax)), dtype=torch.uint8, device="cuda")
     for rep in reps:
-        d = tla.make_kivi_desc(q, rep[0], rep[2], rep[3], rep[5], NKV, scale, residual_length=R)
+        d = tla.make_kivi_desc(q, rep[0], rep[2], rep[3], rep[5], NKV, scale, residual_length=R, bits=bits)
         sl0 = torch.tensor(L0, dtype=torch.int32, device="cuda")
         tla.kivi_build_pages(d, rep[0], rep[1], rep[2], sl0, rep[3], rep[4], max(L0))
-    descs = [tla.make_kivi_desc(q, rep[0], rep[2], rep[3], rep[5], NKV, scale, residual_length=R)
+    descs = [tla.make_kivi_desc(q, rep[0], rep[2], rep[3], rep[5], NKV, scale, residual_length=R, bits=bits)
              for rep in reps]
 
     def step(i, stream):
@@ -339,7 +342,7 @@ def bench_kivi(args, R=128, mixed=False, name=None):
 
     ms = timed(step, n_timed, args.warmup, name)
     lq = lambda x: 0 if x <= R else ((x - R) // 32) * 32
-    nbytes = [kivi_bytes(lens, R, [lq(L) > lq(L - 1) for L in lens]) for _, lens in plan[args.warmup:]]
+    nbytes = [kivi_bytes(lens, R, [lq(L) > lq(L - 1) for L in lens], bits) for _, lens in plan[args.warmup:]]
     avg_bytes = sum(nbytes) / len(nbytes)
     return {"ms_per_step": ms, "gbs": avg_bytes / (ms * 1e-3) / 1e9, "tok_s": S / (ms * 1e-3),
             "bytes_per_step": avg_bytes, "residual_length": R, "group": 32, "steps": n_timed}
@@ -695,6 +698,7 @@ def main():
     if want("kivi"):
         kv = bench_kivi(args, name="kivi")
     kvm = bench_kivi(args, mixed=True, name="kivi_mixed") if want("kivi") else None
+    kv8 = bench_kivi(args, name="kivi_int8", bits=8) if want("kivi") else None
     fpa = bench_decode(args, "fp16", append=True, name="fp16_append") if want("kivi") else None
     f8 = bench_fp8(args, name="fp8") if want("fp8") else None
     f8p = bench_fp8(args, 512, name="fp8_pt512") if want("fp8") else None
@@ -795,6 +799,13 @@ def main():
             "pct_hbm_peak": round(100 * kvm["gbs"] / HBM_PEAK_GBS, 2), "bytes_per_step": int(kvm["bytes_per_step"])}
         if fp is not None:
             res["kivi_int4_mixed_lengths"]["speedup_vs_fp16_tok_s"] = round(kvm["tok_s"] / fp["tok_s"], 3)
+    if kv8 is not None:
+        res["kivi_int8"] = {
+            "workload": "as kivi_int4 with INT8 pages (9216 B per 32 tokens per kv head)",
+            "gbs": round(kv8["gbs"], 2), "ms_per_step": round(kv8["ms_per_step"], 5), "tok_s": round(kv8["tok_s"], 1),
+            "pct_hbm_peak": round(100 * kv8["gbs"] / HBM_PEAK_GBS, 2), "bytes_per_step": int(kv8["bytes_per_step"])}
+        if fp is not None:
+            res["kivi_int8"]["speedup_vs_fp16_tok_s"] = round(kv8["tok_s"] / fp["tok_s"], 3)
     if f8 is not None:
         res["fp8_e4m3_long_context"] = {
             "workload": "decode, batch 16, ctx 32768, 32 q / 8 kv heads, d 128, FP8 E4M3 KV with per-tensor "

@@ -324,8 +324,8 @@ int tl_kivi_decompress(const uint8_t* in, void* kv_out, int32_t n_vecs, int32_t 
                        int32_t n_outliers, int32_t group_size, void* stream);
 
 /* ------------------------------------------------------------------------
- * Paged KIVI INT4 KV: K per channel and V per token, groups of 32, fp16
- * step/zero, nibbles two per byte, the most recent residual_length tokens
+ * Paged KIVI INT4 / INT8 KV: K per channel and V per token, groups of 32,
+ * fp16 step/zero, codes of desc->bits bits, the most recent residual_length tokens
  * (plus up to 31 more) kept in the fp16 pool (KiviConfig, config_schema.h:
  * 122-129, which the reference declares but never implements).
  * A sequence of length L holds its first
@@ -352,7 +352,15 @@ typedef struct tl_kivi_desc {
   int32_t gqa_map;
   int32_t partition_pages;     /* 0 = choose, -1 = single pass, else pages per partition */
   float scale;
+  int32_t bits;                /* code width of the pages (KiviConfig.bits, config_schema.h:124):
+                                  4 (also 0) or 8 */
 } tl_kivi_desc;
+
+/* Page bytes per kv head for a code width: 5120 (INT4, also bits 0) or 9216
+ * (INT8: the INT4 layout with every 16-byte code chunk widened to 32 bytes);
+ * 0 for any other width. */
+#define TL_KIVI_PAGE_BYTES_INT8 9216
+size_t tl_kivi_page_bytes(int32_t bits);
 
 int32_t tl_kivi_quantized_len(int32_t seq_len, int32_t residual_length);
 

@@ -819,53 +819,138 @@ static int vparam_off(int t, int g, int zero)
     return 4608 + (g * 4 + r) * 32 + zero * 16 + 2 * s;
 }
 
-void orc_kivi_page_quantize(const uint16_t* k_tok, const uint16_t* v_tok, uint8_t* page)
+/* ------------------------------------------------------------------------
+ * Paged KIVI INT8 page format (KiviConfig.bits = 8, config_schema.h:124):
+ * the INT4 page with every 16-byte code chunk widened to 32 bytes, so that a
+ * lane's chunk covers the same (token, channel) set:
+ *
+ *   [   0, 4096) K codes, 128 chunks of 32 B (chunk c as in INT4).  Dword
+ *                2m + h holds channels 8o + 4h + {0, 2, 1, 3} of octet
+ *                o = j + 4m in bytes 0..3 (a 0x00FF00FF mask then gives the
+ *                channel pairs (0, 1) and, after a shift by 8, (2, 3)).
+ *   [4096, 4608) K (step, zero) as the INT4 K params.
+ *   [4608, 8704) V codes, 128 chunks of 32 B (chunk c as in INT4).  Dword
+ *                2m + h holds token slots 4h + {0, 2, 1, 3} of channel
+ *                (4hh + m)*16 + u in bytes 0..3.
+ *   [8704, 9216) V (step, zero) as the INT4 V params.
+ * Codes are 8 bit: scale = 255 / range, clamp(rint((x - min) * scale), 0,
+ * 255); step = 1 / scale, zero = min, both fp16, as for INT4.
+ * ====================================================================== */
+
+static const int kb8_perm[4] = {0, 2, 1, 3};   /* byte k of a dword -> element 4h + perm[k] */
+
+static int kb8_byte(int t, int ch)             /* INT8 K code byte */
 {
-    memset(page, 0, ORC_KIVI_PAGE_BYTES);
+    int tt = t / 16, u = t % 16;
+    int o = ch / 8, j = o % 4, m = o / 4;
+    int e = ch % 8, h = e / 4, k = 0;
+    while (kb8_perm[k] != e % 4) ++k;
+    int c = tt * 64 + j * 16 + u;
+    return c * 32 + (2 * m + h) * 4 + k;
+}
+
+static int vb8_byte(int t, int ch)             /* INT8 V code byte */
+{
+    int r, s; v_slot_of(t, &r, &s);
+    int nt = ch / 16, u = ch % 16, hh = nt / 4, m = nt % 4;
+    int h = s / 4, k = 0;
+    while (kb8_perm[k] != s % 4) ++k;
+    int c = hh * 64 + r * 16 + u;
+    return 4608 + c * 32 + (2 * m + h) * 4 + k;
+}
+
+size_t orc_kivi_page_bytes(int bits)
+{
+    return bits == 8 ? ORC_KIVI_PAGE_BYTES_INT8 : ORC_KIVI_PAGE_BYTES;
+}
+
+/* The KIVI group quantiser with `levels` code steps (15: INT4, 255: INT8). */
+void orc_kivi_quant_group_levels(const float* x, int n, int levels, uint8_t* q, uint16_t* step,
+                                 uint16_t* zero)
+{
+    float gmin = FLT_MAX, gmax = -FLT_MAX;
+    for (int i = 0; i < n; ++i) {
+        if (x[i] < gmin) gmin = x[i];
+        if (x[i] > gmax) gmax = x[i];
+    }
+    float range = gmax - gmin;
+    int degenerate = !(range > 1e-6f);
+    float scale = degenerate ? 0.0f : ((float)levels / range);
+    for (int i = 0; i < n; ++i) {
+        float d = x[i] - gmin;
+        float r = rintf(d * scale);
+        q[i] = (uint8_t)(!(r >= 0.0f) ? 0 : (r > (float)levels ? levels : (int)r));
+    }
+    float st = degenerate ? 0.0f : (1.0f / scale);
+    int gmin_ok = (gmin == gmin) && (gmin > -FLT_MAX) && (gmin < FLT_MAX);
+    *step = orc_f32_to_f16(st);
+    *zero = orc_f32_to_f16(gmin_ok ? gmin : 0.0f);
+}
+
+static int k_params(int bits) { return bits == 8 ? 4096 : 2048; }
+static int v_params(int bits) { return bits == 8 ? 8704 : 4608; }
+
+void orc_kivi_page_quantize_bits(const uint16_t* k_tok, const uint16_t* v_tok, uint8_t* page, int bits)
+{
+    const int levels = bits == 8 ? 255 : 15;
+    memset(page, 0, orc_kivi_page_bytes(bits));
     float x[PG_D];
     uint8_t q[PG_D];
     uint16_t st, ze;
     /* K: per channel over the 32 tokens */
     for (int ch = 0; ch < PG_D; ++ch) {
         for (int t = 0; t < PG_T; ++t) x[t] = orc_f16_to_f32(k_tok[t * PG_D + ch]);
-        orc_kivi_quant_group(x, PG_T, q, &st, &ze);
+        orc_kivi_quant_group_levels(x, PG_T, levels, q, &st, &ze);
         for (int t = 0; t < PG_T; ++t) {
+            if (bits == 8) { page[kb8_byte(t, ch)] = q[t]; continue; }
             int byte; int sh = (int)kn_bitpos(t, ch, &byte);
             page[byte] |= (uint8_t)(q[t] << sh);
         }
-        memcpy(page + kparam_off(ch, 0), &st, 2);
-        memcpy(page + kparam_off(ch, 1), &ze, 2);
+        memcpy(page + kparam_off(ch, 0) - 2048 + k_params(bits), &st, 2);
+        memcpy(page + kparam_off(ch, 1) - 2048 + k_params(bits), &ze, 2);
     }
     /* V: per token over groups of 32 channels */
     for (int t = 0; t < PG_T; ++t)
         for (int g = 0; g < PG_D / 32; ++g) {
             for (int i = 0; i < 32; ++i) x[i] = orc_f16_to_f32(v_tok[t * PG_D + g * 32 + i]);
-            orc_kivi_quant_group(x, 32, q, &st, &ze);
+            orc_kivi_quant_group_levels(x, 32, levels, q, &st, &ze);
             for (int i = 0; i < 32; ++i) {
+                if (bits == 8) { page[vb8_byte(t, g * 32 + i)] = q[i]; continue; }
                 int byte; int sh = (int)vn_bitpos(t, g * 32 + i, &byte);
                 page[byte] |= (uint8_t)(q[i] << sh);
             }
-            memcpy(page + vparam_off(t, g, 0), &st, 2);
-            memcpy(page + vparam_off(t, g, 1), &ze, 2);
+            memcpy(page + vparam_off(t, g, 0) - 4608 + v_params(bits), &st, 2);
+            memcpy(page + vparam_off(t, g, 1) - 4608 + v_params(bits), &ze, 2);
         }
+}
+
+void orc_kivi_page_dequant_bits(const uint8_t* page, uint16_t* k_tok, uint16_t* v_tok, int bits)
+{
+    for (int t = 0; t < PG_T; ++t)
+        for (int ch = 0; ch < PG_D; ++ch) {
+            int n;
+            if (bits == 8) n = page[kb8_byte(t, ch)];
+            else { int byte; int sh = (int)kn_bitpos(t, ch, &byte); n = (page[byte] >> sh) & 0xf; }
+            uint16_t st, ze;
+            memcpy(&st, page + kparam_off(ch, 0) - 2048 + k_params(bits), 2);
+            memcpy(&ze, page + kparam_off(ch, 1) - 2048 + k_params(bits), 2);
+            k_tok[t * PG_D + ch] = orc_f32_to_f16(fmaf((float)n, orc_f16_to_f32(st), orc_f16_to_f32(ze)));
+            if (bits == 8) n = page[vb8_byte(t, ch)];
+            else { int byte; int sh = (int)vn_bitpos(t, ch, &byte); n = (page[byte] >> sh) & 0xf; }
+            memcpy(&st, page + vparam_off(t, ch / 32, 0) - 4608 + v_params(bits), 2);
+            memcpy(&ze, page + vparam_off(t, ch / 32, 1) - 4608 + v_params(bits), 2);
+            v_tok[t * PG_D + ch] = orc_f32_to_f16(fmaf((float)n, orc_f16_to_f32(st), orc_f16_to_f32(ze)));
+        }
+}
+
+void orc_kivi_page_quantize(const uint16_t* k_tok, const uint16_t* v_tok, uint8_t* page)
+{
+    orc_kivi_page_quantize_bits(k_tok, v_tok, page, 4);
 }
 
 void orc_kivi_page_dequant(const uint8_t* page, uint16_t* k_tok, uint16_t* v_tok)
 {
-    for (int t = 0; t < PG_T; ++t)
-        for (int ch = 0; ch < PG_D; ++ch) {
-            int byte; int sh = (int)kn_bitpos(t, ch, &byte);
-            int n = (page[byte] >> sh) & 0xf;
-            uint16_t st, ze;
-            memcpy(&st, page + kparam_off(ch, 0), 2);
-            memcpy(&ze, page + kparam_off(ch, 1), 2);
-            k_tok[t * PG_D + ch] = orc_f32_to_f16(fmaf((float)n, orc_f16_to_f32(st), orc_f16_to_f32(ze)));
-            sh = (int)vn_bitpos(t, ch, &byte);
-            n = (page[byte] >> sh) & 0xf;
-            memcpy(&st, page + vparam_off(t, ch / 32, 0), 2);
-            memcpy(&ze, page + vparam_off(t, ch / 32, 1), 2);
-            v_tok[t * PG_D + ch] = orc_f32_to_f16(fmaf((float)n, orc_f16_to_f32(st), orc_f16_to_f32(ze)));
-        }
+    orc_kivi_page_dequant_bits(page, k_tok, v_tok, 4);
 }
 
 int orc_kivi_quantized_len(int seq_len, int residual_length)
@@ -889,6 +974,19 @@ void orc_kivi_build_pages(const uint16_t* k_cache, const uint16_t* v_cache,
                           uint8_t* pages, const int32_t* page_tables, int max_pages,
                           int num_pages)
 {
+    orc_kivi_build_pages_bits(k_cache, v_cache, block_tables, max_blocks_per_seq, seq_lens, num_seqs,
+                              num_kv_heads, block_size, residual_length, pages, page_tables, max_pages,
+                              num_pages, 4);
+}
+
+void orc_kivi_build_pages_bits(const uint16_t* k_cache, const uint16_t* v_cache,
+                               const int32_t* block_tables, int max_blocks_per_seq,
+                               const int32_t* seq_lens, int num_seqs, int num_kv_heads,
+                               int block_size, int residual_length,
+                               uint8_t* pages, const int32_t* page_tables, int max_pages,
+                               int num_pages, int bits)
+{
+    const size_t page_bytes = orc_kivi_page_bytes(bits);
     uint16_t kt[PG_T * PG_D], vt[PG_T * PG_D];
     for (int s = 0; s < num_seqs; ++s) {
         int Lq = orc_kivi_quantized_len(seq_lens[s], residual_length);
@@ -901,7 +999,7 @@ void orc_kivi_build_pages(const uint16_t* k_cache, const uint16_t* v_cache,
                     gather_tok_f16(k_cache, row, p * PG_T + t, h, num_kv_heads, block_size, kt + t * PG_D);
                     gather_tok_f16(v_cache, row, p * PG_T + t, h, num_kv_heads, block_size, vt + t * PG_D);
                 }
-                orc_kivi_page_quantize(kt, vt, pages + ((int64_t)pid * num_kv_heads + h) * ORC_KIVI_PAGE_BYTES);
+                orc_kivi_page_quantize_bits(kt, vt, pages + ((int64_t)pid * num_kv_heads + h) * page_bytes, bits);
             }
         }
     }
@@ -923,6 +1021,21 @@ void orc_kivi_paged_attention(double* out, const void* q, int q_dtype,
                               int block_size, int residual_length, float scale,
                               int gqa_map)
 {
+    orc_kivi_paged_attention_bits(out, q, q_dtype, pages, page_tables, max_pages, num_pages, k_cache, v_cache,
+                                  block_tables, max_blocks_per_seq, seq_lens, num_seqs, num_heads, num_kv_heads,
+                                  block_size, residual_length, scale, gqa_map, 4);
+}
+
+void orc_kivi_paged_attention_bits(double* out, const void* q, int q_dtype,
+                                   const uint8_t* pages, const int32_t* page_tables,
+                                   int max_pages, int num_pages, const uint16_t* k_cache,
+                                   const uint16_t* v_cache, const int32_t* block_tables,
+                                   int max_blocks_per_seq, const int32_t* seq_lens,
+                                   int num_seqs, int num_heads, int num_kv_heads,
+                                   int block_size, int residual_length, float scale,
+                                   int gqa_map, int bits)
+{
+    const size_t page_bytes = orc_kivi_page_bytes(bits);
     int max_len = 0;
     for (int s = 0; s < num_seqs; ++s) if (seq_lens[s] > max_len) max_len = seq_lens[s];
     if (max_len == 0) max_len = 1;
@@ -941,7 +1054,7 @@ void orc_kivi_paged_attention(double* out, const void* q, int q_dtype,
                 int there = pid >= 0 && pid < num_pages;
                 for (int t = 0; t < PG_T; ++t) ok[p * PG_T + t] = (unsigned char)there;
                 if (!there) continue;
-                orc_kivi_page_dequant(pages + ((int64_t)pid * num_kv_heads + kvh) * ORC_KIVI_PAGE_BYTES, kt, vt);
+                orc_kivi_page_dequant_bits(pages + ((int64_t)pid * num_kv_heads + kvh) * page_bytes, kt, vt, bits);
                 for (int i = 0; i < PG_T * PG_D; ++i) {
                     K[(size_t)p * PG_T * PG_D + i] = orc_f16_to_f32(kt[i]);
                     V[(size_t)p * PG_T * PG_D + i] = orc_f16_to_f32(vt[i]);

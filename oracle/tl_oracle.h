@@ -145,6 +145,29 @@ void orc_kivi_page_dequant(const uint8_t* page, uint16_t* k_tok, uint16_t* v_tok
 /* Number of tokens held in pages for a sequence of length L. */
 int  orc_kivi_quantized_len(int seq_len, int residual_length);
 
+/* ---- paged KIVI INT8 (the INT4 page with 32-byte code chunks) --------- */
+#define ORC_KIVI_PAGE_BYTES_INT8 9216
+size_t orc_kivi_page_bytes(int bits);
+/* The group quantiser with `levels` code steps (15: INT4, 255: INT8). */
+void orc_kivi_quant_group_levels(const float* x, int n, int levels, uint8_t* q, uint16_t* step,
+                                 uint16_t* zero);
+void orc_kivi_page_quantize_bits(const uint16_t* k_tok, const uint16_t* v_tok, uint8_t* page, int bits);
+void orc_kivi_page_dequant_bits(const uint8_t* page, uint16_t* k_tok, uint16_t* v_tok, int bits);
+void orc_kivi_build_pages_bits(const uint16_t* k_cache, const uint16_t* v_cache,
+                               const int32_t* block_tables, int max_blocks_per_seq,
+                               const int32_t* seq_lens, int num_seqs, int num_kv_heads,
+                               int block_size, int residual_length,
+                               uint8_t* pages, const int32_t* page_tables, int max_pages,
+                               int num_pages, int bits);
+void orc_kivi_paged_attention_bits(double* out, const void* q, int q_dtype,
+                                   const uint8_t* pages, const int32_t* page_tables,
+                                   int max_pages, int num_pages, const uint16_t* k_cache,
+                                   const uint16_t* v_cache, const int32_t* block_tables,
+                                   int max_blocks_per_seq, const int32_t* seq_lens,
+                                   int num_seqs, int num_heads, int num_kv_heads,
+                                   int block_size, int residual_length, float scale,
+                                   int gqa_map, int bits);
+
 /* Build every page of a batch from an fp16 paged cache: pages
  * [num_pages][n_kv][5120]; page_tables [S, max_pages].  Page-table entries
  * outside [0, num_pages) are skipped; tokens whose block-table entry is

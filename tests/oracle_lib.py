@@ -16,6 +16,11 @@ LIB_PATH = os.path.join(ROOT, "oracle", "libtloracle.so")
 F32, F16, BF16, FP8 = 0, 1, 2, 32
 MODULO, GROUPED = 0, 1
 KIVI_PAGE_BYTES = 5120
+KIVI_PAGE_BYTES_INT8 = 9216
+
+
+def kivi_page_bytes(bits: int) -> int:
+    return KIVI_PAGE_BYTES_INT8 if bits == 8 else KIVI_PAGE_BYTES
 KIVI_PAGE_TOKENS = 32
 
 if not os.path.exists(LIB_PATH):
@@ -62,6 +67,14 @@ _lib.orc_kivi_quantized_len.restype = _I
 _lib.orc_kivi_quantized_len.argtypes = [_I, _I]
 _lib.orc_kivi_build_pages.argtypes = [_P, _P, _P, _I, _P, _I, _I, _I, _I, _P, _P, _I, _I]
 _lib.orc_kivi_paged_attention.argtypes = [_P, _P, _I, _P, _P, _I, _I, _P, _P, _P, _I, _P, _I, _I, _I, _I, _I, _F, _I]
+_lib.orc_kivi_page_bytes.restype = ctypes.c_size_t
+_lib.orc_kivi_page_bytes.argtypes = [_I]
+_lib.orc_kivi_quant_group_levels.argtypes = [_P, _I, _I, _P, _P, _P]
+_lib.orc_kivi_page_quantize_bits.argtypes = [_P, _P, _P, _I]
+_lib.orc_kivi_page_dequant_bits.argtypes = [_P, _P, _P, _I]
+_lib.orc_kivi_build_pages_bits.argtypes = [_P, _P, _P, _I, _P, _I, _I, _I, _I, _P, _P, _I, _I, _I]
+_lib.orc_kivi_paged_attention_bits.argtypes = [_P, _P, _I, _P, _P, _I, _I, _P, _P, _P, _I, _P, _I, _I, _I, _I, _I,
+                                               _F, _I, _I]
 
 lib = _lib
 
@@ -265,16 +278,31 @@ def kivi_quant_group(x: np.ndarray):
     return q, int(st[0]), int(ze[0])
 
 
-def kivi_page_quantize(k_tok_bits, v_tok_bits):
-    page = np.zeros(KIVI_PAGE_BYTES, np.uint8)
-    _lib.orc_kivi_page_quantize(ptr(k_tok_bits), ptr(v_tok_bits), ptr(page))
+def kivi_quant_group_levels(x: np.ndarray, levels: int):
+    x = np.ascontiguousarray(x, np.float32)
+    q = np.zeros(x.size, np.uint8)
+    st = np.zeros(1, np.uint16)
+    ze = np.zeros(1, np.uint16)
+    _lib.orc_kivi_quant_group_levels(ptr(x), x.size, levels, ptr(q), ptr(st), ptr(ze))
+    return q, int(st[0]), int(ze[0])
+
+
+def kivi_page_quantize(k_tok_bits, v_tok_bits, bits=4):
+    page = np.zeros(kivi_page_bytes(bits), np.uint8)
+    if bits == 4:
+        _lib.orc_kivi_page_quantize(ptr(k_tok_bits), ptr(v_tok_bits), ptr(page))
+    else:
+        _lib.orc_kivi_page_quantize_bits(ptr(k_tok_bits), ptr(v_tok_bits), ptr(page), bits)
     return page
 
 
-def kivi_page_dequant(page):
+def kivi_page_dequant(page, bits=4):
     k = np.zeros((32, 128), np.uint16)
     v = np.zeros((32, 128), np.uint16)
-    _lib.orc_kivi_page_dequant(ptr(page), ptr(k), ptr(v))
+    if bits == 4:
+        _lib.orc_kivi_page_dequant(ptr(page), ptr(k), ptr(v))
+    else:
+        _lib.orc_kivi_page_dequant_bits(ptr(page), ptr(k), ptr(v), bits)
     return k, v
 
 
@@ -282,20 +310,29 @@ def kivi_quantized_len(seq_len, residual_length) -> int:
     return _lib.orc_kivi_quantized_len(seq_len, residual_length)
 
 
-def kivi_build_pages(k_cache, v_cache, tables, seq_lens, residual_length, pages, page_tables):
-    _lib.orc_kivi_build_pages(ptr(k_cache), ptr(v_cache), ptr(tables), tables.shape[1],
-                              ptr(seq_lens), len(seq_lens), k_cache.shape[1], k_cache.shape[3],
-                              residual_length, ptr(pages), ptr(page_tables), page_tables.shape[1],
-                              pages.size // (k_cache.shape[1] * KIVI_PAGE_BYTES))
+def kivi_build_pages(k_cache, v_cache, tables, seq_lens, residual_length, pages, page_tables, bits=4):
+    num_pages = pages.size // (k_cache.shape[1] * kivi_page_bytes(bits))
+    if bits == 4:
+        _lib.orc_kivi_build_pages(ptr(k_cache), ptr(v_cache), ptr(tables), tables.shape[1],
+                                  ptr(seq_lens), len(seq_lens), k_cache.shape[1], k_cache.shape[3],
+                                  residual_length, ptr(pages), ptr(page_tables), page_tables.shape[1], num_pages)
+    else:
+        _lib.orc_kivi_build_pages_bits(ptr(k_cache), ptr(v_cache), ptr(tables), tables.shape[1],
+                                       ptr(seq_lens), len(seq_lens), k_cache.shape[1], k_cache.shape[3],
+                                       residual_length, ptr(pages), ptr(page_tables), page_tables.shape[1],
+                                       num_pages, bits)
 
 
 def kivi_paged_attention(q, q_code, pages, page_tables, k_cache, v_cache, tables, seq_lens,
-                         num_kv_heads, residual_length, scale, gqa_map=GROUPED):
+                         num_kv_heads, residual_length, scale, gqa_map=GROUPED, bits=4):
     S, H, D = q.shape
     out = np.zeros((S, H, D), np.float64)
-    _lib.orc_kivi_paged_attention(ptr(out), ptr(q), q_code, ptr(pages), ptr(page_tables),
-                                  page_tables.shape[1], pages.size // (num_kv_heads * KIVI_PAGE_BYTES),
-                                  ptr(k_cache), ptr(v_cache), ptr(tables),
-                                  tables.shape[1], ptr(seq_lens), S, H, num_kv_heads,
-                                  k_cache.shape[3], residual_length, scale, gqa_map)
+    num_pages = pages.size // (num_kv_heads * kivi_page_bytes(bits))
+    args = (ptr(out), ptr(q), q_code, ptr(pages), ptr(page_tables), page_tables.shape[1], num_pages,
+            ptr(k_cache), ptr(v_cache), ptr(tables), tables.shape[1], ptr(seq_lens), S, H, num_kv_heads,
+            k_cache.shape[3], residual_length, scale, gqa_map)
+    if bits == 4:
+        _lib.orc_kivi_paged_attention(*args)
+    else:
+        _lib.orc_kivi_paged_attention_bits(*args, bits)
     return out

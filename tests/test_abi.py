@@ -258,6 +258,17 @@ def test_kivi_decode_descriptor_checks_and_planning():
     # 4 x 8 items, 124 pages -> 16 partitions of 8 pages
     assert tla.kivi_workspace_bytes(_kdesc(num_seqs=4), 4096) == 4 * 32 * 16 * (128 * 4 + 8)
     assert call(_kdesc(num_seqs=4)) == tla.ERR_INVALID_ARGUMENT        # workspace missing
+    # page code widths: 4 (also 0) and 8; the workspace does not depend on them
+    assert call(_kdesc(bits=5)) == tla.ERR_NOT_IMPLEMENTED
+    assert call(_kdesc(bits=2)) == tla.ERR_NOT_IMPLEMENTED
+    assert tla.kivi_workspace_bytes(_kdesc(num_seqs=4, bits=8), 4096) == 4 * 32 * 16 * (128 * 4 + 8)
+
+
+def test_kivi_page_bytes():
+    assert tla.kivi_page_bytes(4) == tla.KIVI_PAGE_BYTES == 5120
+    assert tla.kivi_page_bytes(0) == 5120
+    assert tla.kivi_page_bytes(8) == tla.KIVI_PAGE_BYTES_INT8 == 9216
+    assert tla.kivi_page_bytes(3) == 0 and tla.kivi_page_bytes(16) == 0
 
 
 # ---- reference-named C++ operators (include/tl_truellm_ops.h) -------------

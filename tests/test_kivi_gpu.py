@@ -100,9 +100,11 @@ def test_vector_codec_unsupported_params_leave_output_untouched():
 class KiviCase:
     """fp16 pools for the given lengths plus a page table over a page pool."""
 
-    def __init__(self, seed, lens, H=32, n_kv=8, R=128, outliers=4, extra_blocks=4):
+    def __init__(self, seed, lens, H=32, n_kv=8, R=128, outliers=4, extra_blocks=4, bits=4):
         self.lens = np.asarray(lens, np.int32)
         self.R = R
+        self.bits = bits
+        self.page_bytes = orc.kivi_page_bytes(bits)
         S, D, BS = len(lens), 128, 16
         self.case = inputs.make_paged_case(seed, S, H, n_kv, D, BS,
                                            [L + extra_blocks * BS for L in lens], orc.F32)
@@ -123,15 +125,15 @@ class KiviCase:
         self.scale = 1 / math.sqrt(D)
 
     def oracle_pages(self, lens=None):
-        pages = np.zeros((self.num_pages, self.n_kv, orc.KIVI_PAGE_BYTES), np.uint8)
+        pages = np.zeros((self.num_pages, self.n_kv, self.page_bytes), np.uint8)
         orc.kivi_build_pages(self.k, self.v, self.tables, self.lens if lens is None else lens, self.R,
-                             pages, self.page_tables)
+                             pages, self.page_tables, self.bits)
         return pages
 
     def desc(self, qd, kd, btd, ptd, partition_pages=0, gqa=tla.GQA_GROUPED):
         return tla.make_kivi_desc(qd, kd, btd, ptd, self.num_pages, self.n_kv, self.scale,
                                   residual_length=self.R, gqa_map=gqa,
-                                  partition_pages=partition_pages)
+                                  partition_pages=partition_pages, bits=self.bits)
 
 
 def _used_pages(kc, lens):
@@ -142,14 +144,15 @@ def _used_pages(kc, lens):
     return sorted(used)
 
 
+@pytest.mark.parametrize("bits", [4, 8])
 @pytest.mark.parametrize("R", [128, 0, 40])
-def test_build_pages_bit_exact(R):
-    kc = KiviCase(51, [300, 1000, 161, 159, 0, 4096], R=R)
+def test_build_pages_bit_exact(R, bits):
+    kc = KiviCase(51, [300, 1000, 161, 159, 0, 4096], R=R, bits=bits)
     want = kc.oracle_pages()
     qd, kd, vd = dev(kc.q, orc.F16), dev(kc.k, orc.F16), dev(kc.v, orc.F16)
     btd, sld, ptd = dev(kc.tables), dev(kc.lens), dev(kc.page_tables)
-    pages = torch.zeros(kc.num_pages, kc.n_kv, tla.KIVI_PAGE_BYTES, dtype=torch.uint8, device="cuda")
-    print(f"case build pages R={R}", flush=True)
+    pages = torch.zeros(kc.num_pages, kc.n_kv, kc.page_bytes, dtype=torch.uint8, device="cuda")
+    print(f"case build pages R={R} bits={bits}", flush=True)
     tla.kivi_build_pages(kc.desc(qd, kd, btd, ptd), kd, vd, btd, sld, ptd, pages, int(kc.lens.max()))
     torch.cuda.synchronize()
     got = pages.cpu().numpy()
@@ -160,15 +163,17 @@ def test_build_pages_bit_exact(R):
     assert (got[unused] == 0).all()
 
 
-def test_append_quantises_on_page_boundaries():
+@pytest.mark.parametrize("bits", [4, 8])
+def test_append_quantises_on_page_boundaries(bits):
     """Append one token per step for 70 steps; pages and the fp16 pool match
     a rebuild from the final pool, and pages appear exactly when Lq grows."""
     start = np.array([150, 159, 160, 191, 200], np.int32)
     steps = 70
-    kc = KiviCase(52, start + steps, extra_blocks=1)
+    kc = KiviCase(52, start + steps, extra_blocks=1, bits=bits)
+    print(f"case kivi append bits={bits}", flush=True)
     qd, kd, vd = dev(kc.q, orc.F16), dev(kc.k, orc.F16), dev(kc.v, orc.F16)
     btd, ptd = dev(kc.tables), dev(kc.page_tables)
-    pages = torch.zeros(kc.num_pages, kc.n_kv, tla.KIVI_PAGE_BYTES, dtype=torch.uint8, device="cuda")
+    pages = torch.zeros(kc.num_pages, kc.n_kv, kc.page_bytes, dtype=torch.uint8, device="cuda")
     desc = kc.desc(qd, kd, btd, ptd)
     tla.kivi_build_pages(desc, kd, vd, btd, dev(start), ptd, pages, int(start.max()))
     rng = np.random.default_rng(9)
@@ -207,15 +212,16 @@ def _run_decode(kc, pages_np, partition_pages=0, gqa=tla.GQA_GROUPED):
 
 def _kivi_ref(kc, pages_np, gqa=orc.GROUPED):
     return orc.kivi_paged_attention(kc.q, orc.F16, pages_np, kc.page_tables, kc.k, kc.v, kc.tables,
-                                    kc.lens, kc.n_kv, kc.R, kc.scale, gqa)
+                                    kc.lens, kc.n_kv, kc.R, kc.scale, gqa, kc.bits)
 
 
+@pytest.mark.parametrize("bits", [4, 8])
 @pytest.mark.parametrize("pp", [-1, 0, 4, 1])
-def test_kivi_decode_matches_oracle(pp):
-    kc = KiviCase(53, [4096, 1000, 161, 159, 0, 1, 2047, 3000])
+def test_kivi_decode_matches_oracle(pp, bits):
+    kc = KiviCase(53, [4096, 1000, 161, 159, 0, 1, 2047, 3000], bits=bits)
     pages = kc.oracle_pages()
-    print(f"case kivi decode pp={pp}", flush=True)
-    assert_close(_run_decode(kc, pages, pp), _kivi_ref(kc, pages), orc.F16, ATOL_KIVI, f"pp={pp}")
+    print(f"case kivi decode pp={pp} bits={bits}", flush=True)
+    assert_close(_run_decode(kc, pages, pp), _kivi_ref(kc, pages), orc.F16, ATOL_KIVI, f"pp={pp} bits={bits}")
 
 
 @pytest.mark.parametrize("H,n_kv", [(16, 8), (64, 8), (8, 8)])
@@ -246,15 +252,15 @@ def _punch_holes(kc):
     pt[5, :] = -1                           # sequence 5: every page a hole (Lq = 544)
 
 
-@pytest.mark.parametrize("pp", [0, 4, -1])
-def test_kivi_decode_table_and_page_holes(pp):
+@pytest.mark.parametrize("pp,bits", [(0, 4), (4, 4), (-1, 4), (4, 8)])
+def test_kivi_decode_table_and_page_holes(pp, bits):
     """Holes in the block table (fp16 window) and the page table are skipped
     by the decode, as the oracle skips them; a hole inside a page's block
     range only zeroes the tokens the page was built from."""
-    kc = KiviCase(59, [4096, 1000, 300, 161, 2047, 700])
+    kc = KiviCase(59, [4096, 1000, 300, 161, 2047, 700], bits=bits)
     _punch_holes(kc)
     pages = kc.oracle_pages()
-    print(f"case kivi holes pp={pp}", flush=True)
+    print(f"case kivi holes pp={pp} bits={bits}", flush=True)
     assert_close(_run_decode(kc, pages, pp), _kivi_ref(kc, pages), orc.F16, ATOL_KIVI, f"holes pp={pp}")
 
 
@@ -283,23 +289,24 @@ def test_kivi_split_k_page_table_narrower_than_sequence():
     assert_close(out, _kivi_ref(kc, pages), orc.F16, ATOL_KIVI, "narrow page table")
 
 
-def test_build_pages_with_holes_bit_exact():
+@pytest.mark.parametrize("bits", [4, 8])
+def test_build_pages_with_holes_bit_exact(bits):
     """The GPU page build skips page-table holes (negative or past the pool)
     and quantises a block-table hole as zeros, byte for byte as the oracle."""
-    kc = KiviCase(60, [4096, 1000, 300, 161, 2047, 700])
+    kc = KiviCase(60, [4096, 1000, 300, 161, 2047, 700], bits=bits)
     _punch_holes(kc)
     want = kc.oracle_pages()
     qd, kd, vd = dev(kc.q, orc.F16), dev(kc.k, orc.F16), dev(kc.v, orc.F16)
     btd, sld, ptd = dev(kc.tables), dev(kc.lens), dev(kc.page_tables)
-    pages = torch.zeros(kc.num_pages, kc.n_kv, tla.KIVI_PAGE_BYTES, dtype=torch.uint8, device="cuda")
+    pages = torch.zeros(kc.num_pages, kc.n_kv, kc.page_bytes, dtype=torch.uint8, device="cuda")
     print("case build pages with holes", flush=True)
     tla.kivi_build_pages(kc.desc(qd, kd, btd, ptd), kd, vd, btd, sld, ptd, pages, int(kc.lens.max()))
     torch.cuda.synchronize()
     assert np.array_equal(pages.cpu().numpy(), want)
 
 
-@pytest.mark.parametrize("H,pp", [(32, 0), (64, 4)])
-def test_kivi_decode_step_matches_oracle_each_step(H, pp):
+@pytest.mark.parametrize("H,pp,bits", [(32, 0, 4), (64, 4, 4), (32, 0, 8), (64, 4, 8)])
+def test_kivi_decode_step_matches_oracle_each_step(H, pp, bits):
     """The fused tl_kivi_decode_step checked against the oracle itself at
     every step: the host pools receive each token through
     orc.reshape_and_cache, the pages are rebuilt by orc.kivi_build_pages at
@@ -308,12 +315,12 @@ def test_kivi_decode_step_matches_oracle_each_step(H, pp):
     window block of sequence 5 are holes."""
     start = np.array([150, 159, 160, 191, 33, 1000], np.int32)
     steps = 36
-    kc = KiviCase(61, start + steps, H=H, extra_blocks=1)
+    kc = KiviCase(61, start + steps, H=H, extra_blocks=1, bits=bits)
     kc.page_tables[0, 0] = -1
     kc.tables[5, (1000 - 60) // 16] = -1
     qd, kd, vd = dev(kc.q, orc.F16), dev(kc.k, orc.F16), dev(kc.v, orc.F16)
     btd, ptd = dev(kc.tables), dev(kc.page_tables)
-    pages = torch.zeros(kc.num_pages, kc.n_kv, tla.KIVI_PAGE_BYTES, dtype=torch.uint8, device="cuda")
+    pages = torch.zeros(kc.num_pages, kc.n_kv, kc.page_bytes, dtype=torch.uint8, device="cuda")
     desc = kc.desc(qd, kd, btd, ptd, pp)
     tla.kivi_build_pages(desc, kd, vd, btd, dev(start), ptd, pages, int(start.max()))
     rng = np.random.default_rng(12)
@@ -321,7 +328,7 @@ def test_kivi_decode_step_matches_oracle_each_step(H, pp):
     ws = torch.empty(max(16, tla.kivi_workspace_bytes(desc, max_ctx)), dtype=torch.uint8, device="cuda")
     lens = start.copy()
     k_host, v_host = kc.k.copy(), kc.v.copy()
-    print(f"case kivi step vs oracle H={H} pp={pp}", flush=True)
+    print(f"case kivi step vs oracle H={H} pp={pp} bits={bits}", flush=True)
     for step in range(steps):
         lens = lens + 1
         pos = lens - 1
@@ -364,7 +371,7 @@ def test_kivi_step_graph_replay_matches_eager(fused):
     kc = KiviCase(57, start + 1, extra_blocks=1)
     qd, kd, vd = dev(kc.q, orc.F16), dev(kc.k, orc.F16), dev(kc.v, orc.F16)
     btd, ptd = dev(kc.tables), dev(kc.page_tables)
-    pages = torch.zeros(kc.num_pages, kc.n_kv, tla.KIVI_PAGE_BYTES, dtype=torch.uint8, device="cuda")
+    pages = torch.zeros(kc.num_pages, kc.n_kv, kc.page_bytes, dtype=torch.uint8, device="cuda")
     desc = kc.desc(qd, kd, btd, ptd)
     tla.kivi_build_pages(desc, kd, vd, btd, dev(start), ptd, pages, int(start.max()))
     lens = start + 1
@@ -406,19 +413,19 @@ def test_kivi_step_graph_replay_matches_eager(fused):
         assert torch.equal(out, eager)
 
 
-@pytest.mark.parametrize("H,R,pp", [(32, 128, 0), (32, 0, 0), (64, 128, 0), (32, 128, 4), (64, 0, 4),
-                                    (32, 20, 0)])
-def test_decode_step_equals_append_then_decode(H, R, pp):
+@pytest.mark.parametrize("H,R,pp,bits", [(32, 128, 0, 4), (32, 0, 0, 4), (64, 128, 0, 4), (32, 128, 4, 4),
+                                         (64, 0, 4, 4), (32, 20, 0, 4), (32, 128, 0, 8), (64, 0, 4, 8)])
+def test_decode_step_equals_append_then_decode(H, R, pp, bits):
     """tl_kivi_decode_step gives the bytes of tl_kivi_append followed by
     tl_kivi_paged_attention_decode, over 40 steps that complete pages."""
     start = np.array([150, 159, 160, 191, 33, 1000], np.int32)
     steps = 40
     runs = []
     for fused in (False, True):
-        kc = KiviCase(58, start + steps, H=H, R=R, extra_blocks=1)
+        kc = KiviCase(58, start + steps, H=H, R=R, extra_blocks=1, bits=bits)
         qd, kd, vd = dev(kc.q, orc.F16), dev(kc.k, orc.F16), dev(kc.v, orc.F16)
         btd, ptd = dev(kc.tables), dev(kc.page_tables)
-        pages = torch.zeros(kc.num_pages, kc.n_kv, tla.KIVI_PAGE_BYTES, dtype=torch.uint8, device="cuda")
+        pages = torch.zeros(kc.num_pages, kc.n_kv, kc.page_bytes, dtype=torch.uint8, device="cuda")
         desc = kc.desc(qd, kd, btd, ptd, pp)
         tla.kivi_build_pages(desc, kd, vd, btd, dev(start), ptd, pages, int(start.max()))
         rng = np.random.default_rng(11)
@@ -426,7 +433,7 @@ def test_decode_step_equals_append_then_decode(H, R, pp):
         ws = torch.empty(max(16, tla.kivi_workspace_bytes(desc, max_ctx)), dtype=torch.uint8, device="cuda")
         lens = start.copy()
         outs = []
-        print(f"case kivi step H={H} R={R} pp={pp} fused={fused}", flush=True)
+        print(f"case kivi step H={H} R={R} pp={pp} bits={bits} fused={fused}", flush=True)
         for _ in range(steps):
             lens = lens + 1
             pos = lens - 1

@@ -468,6 +468,110 @@ def test_kivi_page_constant_is_exact_and_params_land_in_place():
     assert (vp[:, 0] == 0).all() and (vp[:, 1] == _f16(-0.75)[0]).all()
 
 
+# ---------------------------------------------------------------------------
+# paged KIVI INT8 page format (KiviConfig.bits = 8)
+# ---------------------------------------------------------------------------
+
+def test_kivi_quant_group_levels_rne_and_int4_agreement():
+    # 255 levels: 0..255 map to themselves; halfway cases round to even
+    q, st, ze = orc.kivi_quant_group_levels(np.arange(256, dtype=np.float32), 255)
+    assert list(q) == list(range(256)) and st == int(_f16(1.0)[0]) and ze == 0
+    x = np.array([0.0, 1.0, 3.0, 5.0, 510.0], np.float32)          # scale 255/510 = 0.5
+    q, _, _ = orc.kivi_quant_group_levels(x, 255)
+    assert list(q) == [0, 0, 2, 2, 255]                             # 0.5 -> 0, 1.5 -> 2, 2.5 -> 2
+    # 15 levels is the INT4 quantiser pinned above, bit for bit
+    rng = np.random.default_rng(3)
+    for n in (32, 7, 64):
+        x = (rng.standard_normal(n) * 3).astype(np.float32)
+        a, b = orc.kivi_quant_group_levels(x, 15), orc.kivi_quant_group(x)
+        assert np.array_equal(a[0], b[0]) and a[1:] == b[1:]
+
+
+def _byte8(w0, w1):
+    """The decode kernel's unpack of two code dwords: element order of the
+    four masked fp16 pairs (low half first)."""
+    out = []
+    for w in (w0, w1):
+        for sh in (0, 8):
+            y = (int(w) >> sh) & 0x00FF00FF
+            out += [y & 0xFF, y >> 16]
+    return out
+
+
+def test_kivi_int8_page_layout_matches_the_kernel_unpack():
+    """For every lane chunk of a page, the kernel's unpack (two dwords per
+    MFMA operand, 0x00FF00FF masks) yields the codes of the group quantiser
+    (pinned above, computed here independently of the page layout) in the
+    order the MFMA operands take them: K channels 8o .. 8o + 7 of token t for
+    octet o = j + 4m; V token slots 0..7 of channel (4hh + m)*16 + u."""
+    rng = np.random.default_rng(5)
+    k = _f16((rng.standard_normal((32, 128)) * 2).astype(np.float32)).reshape(32, 128)
+    v = _f16(rng.standard_normal((32, 128)).astype(np.float32)).reshape(32, 128)
+    page = orc.kivi_page_quantize(k, v, 8)
+    assert page.size == 9216
+    kf, vf = k.view(np.float16).astype(np.float32), v.view(np.float16).astype(np.float32)
+    kcode = np.stack([orc.kivi_quant_group_levels(kf[:, ch], 255)[0] for ch in range(128)])      # [ch][t]
+    vcode = np.zeros((32, 128), np.int64)
+    for t in range(32):
+        for g in range(4):
+            vcode[t, 32 * g:32 * g + 32] = orc.kivi_quant_group_levels(vf[t, 32 * g:32 * g + 32], 255)[0]
+    dw = page[:8704].view(np.uint32)
+    def v_token(r, s):
+        return 4 * r + s if s < 4 else 16 + 4 * r + s - 4
+    for c in range(128):
+        tt, j, u = c // 64, (c % 64) // 16, c % 16
+        t = tt * 16 + u
+        for m in range(4):
+            o = j + 4 * m
+            got = _byte8(dw[c * 8 + 2 * m], dw[c * 8 + 2 * m + 1])
+            assert got == [int(kcode[8 * o + e, t]) for e in range(8)], (c, m)
+        hh, r = c // 64, (c % 64) // 16
+        for m in range(4):
+            d = (4 * hh + m) * 16 + u
+            base = 4608 // 4 + c * 8 + 2 * m
+            got = _byte8(dw[base], dw[base + 1])
+            assert got == [int(vcode[v_token(r, s), d]) for s in range(8)], (c, m)
+
+
+def test_kivi_int8_page_roundtrip_error_bound():
+    rng = np.random.default_rng(23)
+    k = rng.standard_normal((32, 128)).astype(np.float32)
+    k[:, [3, 40, 77, 100]] *= 8
+    v = rng.standard_normal((32, 128)).astype(np.float32)
+    kb, vb = _f16(k).reshape(32, 128), _f16(v).reshape(32, 128)
+    kd, vd = orc.kivi_page_dequant(orc.kivi_page_quantize(kb, vb, 8), 8)
+    kd, vd = kd.view(np.float16).astype(np.float32), vd.view(np.float16).astype(np.float32)
+    kx, vx = kb.view(np.float16).astype(np.float32), vb.view(np.float16).astype(np.float32)
+    # x^ = fp16(n st + ze), st = fp16(range / 255), ze = fp16(min): the code
+    # error is at most step / 2, the fp16 step adds up to 255 step 2^-11, the
+    # fp16 zero |min| 2^-11 and the fp16 result |x| 2^-11
+    u = 2.0 ** -11
+    kmin, kstep = kx.min(0), (kx.max(0) - kx.min(0)) / 255
+    kbound = kstep * (0.5 + 255 * u) + np.abs(kmin) * u
+    assert (np.abs(kd - kx) <= kbound[None, :] + np.abs(kx) * u + 1e-6).all()
+    vg = vx.reshape(32, 4, 32)
+    vmin, vstep = vg.min(2), (vg.max(2) - vg.min(2)) / 255
+    vbound = vstep * (0.5 + 255 * u) + np.abs(vmin) * u
+    assert (np.abs(vd - vx).reshape(32, 4, 32) <= vbound[:, :, None] + np.abs(vg) * u + 1e-6).all()
+    # 16 times finer than the INT4 page on the same data
+    kd4, _ = orc.kivi_page_dequant(orc.kivi_page_quantize(kb, vb), 4)
+    e4 = np.abs(kd4.view(np.float16).astype(np.float32) - kx).max()
+    assert np.abs(kd - kx).max() < e4 / 8
+
+
+def test_kivi_int8_page_constant_is_exact_and_params_land_in_place():
+    k = np.full((32, 128), 1.5, np.float32)
+    v = np.full((32, 128), -0.75, np.float32)
+    page = orc.kivi_page_quantize(_f16(k).reshape(32, 128), _f16(v).reshape(32, 128), 8)
+    kd, vd = orc.kivi_page_dequant(page, 8)
+    assert (kd.view(np.float16) == 1.5).all() and (vd.view(np.float16) == -0.75).all()
+    assert (page[:4096] == 0).all() and (page[4608:8704] == 0).all()
+    kp = page[4096:4608].view(np.uint16).reshape(16, 2, 8)
+    assert (kp[:, 0] == 0).all() and (kp[:, 1] == _f16(1.5)[0]).all()
+    vp = page[8704:9216].view(np.uint16).reshape(16, 2, 8)
+    assert (vp[:, 0] == 0).all() and (vp[:, 1] == _f16(-0.75)[0]).all()
+
+
 def test_kivi_quantized_len():
     assert orc.kivi_quantized_len(0, 128) == 0
     assert orc.kivi_quantized_len(128, 128) == 0
@@ -529,7 +633,7 @@ def test_kivi_build_pages_equals_page_quantize_of_gathered_tokens():
     assert np.array_equal(pages, want)
 
 
-def _kivi_as_paged_pool(case, pages, ptab, num_pages, R):
+def _kivi_as_paged_pool(case, pages, ptab, num_pages, R, bits=4):
     """The pool a KIVI cache stands for: tokens below Lq dequantised from
     their page (a page hole: both of its blocks are table holes), the rest
     copied from the fp16 pool through the block table.  Each sequence gets
@@ -551,7 +655,7 @@ def _kivi_as_paged_pool(case, pages, ptab, num_pages, R):
                 if pid < 0 or pid >= num_pages:
                     continue
                 for h in range(n_kv):
-                    kd, vd = orc.kivi_page_dequant(np.ascontiguousarray(pages[pid, h]))
+                    kd, vd = orc.kivi_page_dequant(np.ascontiguousarray(pages[pid, h]), bits)
                     o = t0 % 32
                     kp[nxt, h] = kd[o:o + BS].T
                     vp[nxt, h] = vd[o:o + BS].T
@@ -566,8 +670,9 @@ def _kivi_as_paged_pool(case, pages, ptab, num_pages, R):
     return kp, vp, tables
 
 
+@pytest.mark.parametrize("bits", [4, 8])
 @pytest.mark.parametrize("gqa_map", [orc.MODULO, orc.GROUPED])
-def test_kivi_attention_equals_paged_attention_on_dequantised_prefix(gqa_map):
+def test_kivi_attention_equals_paged_attention_on_dequantised_prefix(gqa_map, bits):
     """orc_kivi_paged_attention = orc_paged_attention (pinned above) over the
     pool it stands for: pages dequantised by orc_kivi_page_dequant below Lq,
     the fp16 window above; page-table holes and block-table holes in the
@@ -581,18 +686,18 @@ def test_kivi_attention_equals_paged_attention_on_dequantised_prefix(gqa_map):
     case.tables[3, 9] = -1                 # in the window of sequence 3 (Lq = 64)
     ptab[0, 2] = -1
     ptab[3, 1] = num_pages                 # past the pool: a hole too
-    pages = np.zeros((num_pages, 2, orc.KIVI_PAGE_BYTES), np.uint8)
-    orc.kivi_build_pages(case.k_cache, case.v_cache, case.tables, case.seq_lens, R, pages, ptab)
+    pages = np.zeros((num_pages, 2, orc.kivi_page_bytes(bits)), np.uint8)
+    orc.kivi_build_pages(case.k_cache, case.v_cache, case.tables, case.seq_lens, R, pages, ptab, bits)
     got = orc.kivi_paged_attention(case.q, orc.F16, pages, ptab, case.k_cache, case.v_cache,
-                                   case.tables, case.seq_lens, 2, R, case.scale, gqa_map)
-    kp, vp, t2 = _kivi_as_paged_pool(case, pages, ptab, num_pages, R)
+                                   case.tables, case.seq_lens, 2, R, case.scale, gqa_map, bits)
+    kp, vp, t2 = _kivi_as_paged_pool(case, pages, ptab, num_pages, R, bits)
     want = orc.paged_attention(case.q, orc.F16, kp, vp, orc.F16, t2, case.seq_lens, 2, case.scale,
                                gqa_map)
     np.testing.assert_allclose(got, want, rtol=0, atol=1e-12)
     # the holes matter: without them the result changes
     full = orc.kivi_paged_attention(case.q, orc.F16, pages, np.where(ptab >= num_pages, 0, np.abs(ptab)).astype(np.int32),
                                     case.k_cache, case.v_cache, case.tables, case.seq_lens, 2, R, case.scale,
-                                    gqa_map)
+                                    gqa_map, bits)
     assert np.abs(full[0] - got[0]).max() > 1e-3 and np.abs(full[3] - got[3]).max() > 1e-3
 
 

@@ -560,7 +560,16 @@ static int check_kivi(const tl_kivi_desc* d) {
   if (d->gqa_map != TL_GQA_MODULO && d->gqa_map != TL_GQA_GROUPED)
     return fail(TL_ERR_INVALID_ARGUMENT, "gqa_map=%d", d->gqa_map);
   if (d->partition_pages < -1) return fail(TL_ERR_INVALID_ARGUMENT, "partition_pages=%d", d->partition_pages);
+  if (d->bits != 0 && d->bits != 4 && d->bits != 8)
+    return fail(TL_ERR_NOT_IMPLEMENTED, "paged KIVI bits=%d (built: 4, 8)", d->bits);
   return TL_OK;
+}
+
+static int kivi_bits(const tl_kivi_desc* d) { return d->bits == 8 ? 8 : 4; }
+
+size_t tl_kivi_page_bytes(int32_t bits) {
+  if (bits != 0 && bits != 4 && bits != 8) return 0;
+  return (size_t)tl::kivi_page_bytes(bits == 8 ? 8 : 4);
 }
 
 static tl::KiviPageLaunch page_launch(const tl_kivi_desc* d, const void* k_cache, const void* v_cache,
@@ -575,6 +584,7 @@ static tl::KiviPageLaunch page_launch(const tl_kivi_desc* d, const void* k_cache
   a.max_blocks_per_seq = d->max_blocks_per_seq; a.num_blocks = d->num_blocks;
   a.max_pages_per_seq = d->max_pages_per_seq; a.num_pages = d->num_pages;
   a.residual_length = d->residual_length;
+  a.bits = kivi_bits(d);
   a.stream = (hipStream_t)stream;
   return a;
 }
@@ -701,6 +711,7 @@ static int kivi_decode_impl(const tl_kivi_desc* desc, void* out, const void* q, 
   a.max_pages_per_seq = desc->max_pages_per_seq; a.num_pages = desc->num_pages;
   a.residual_length = desc->residual_length; a.gqa_map = desc->gqa_map;
   a.num_partitions = P; a.partition_pages = PP;
+  a.bits = kivi_bits(desc);
   a.scale = desc->scale;
   a.append = append;
   a.stream = (hipStream_t)stream;

@@ -137,9 +137,10 @@ struct KiviPageLaunch {
   const int32_t* block_tables;
   const int32_t* seq_lens;
   const int32_t* page_tables;   // [S, max_pages_per_seq]
-  void* pages;                  // [num_pages, n_kv, 5120]
+  void* pages;                  // [num_pages, n_kv, page bytes (5120 INT4, 9216 INT8)]
   int num_seqs, num_kv_heads, block_size, max_blocks_per_seq, num_blocks;
   int max_pages_per_seq, num_pages, residual_length;
+  int bits;                     // page code width: 4 or 8
   int max_pages_to_build;       // prefix build: page slots per sequence in the grid
   int append;                   // 1: write the new token, then build the page L completes
   const void* knew;             // append: new token per sequence [S, n_kv, 128] fp16
@@ -162,6 +163,7 @@ struct KiviDecodeLaunch {
   int num_seqs, num_heads, num_kv_heads, max_blocks_per_seq, num_blocks;
   int max_pages_per_seq, num_pages, residual_length, gqa_map;
   int num_partitions, partition_pages;
+  int bits;                     // page code width: 4 or 8
   float scale;
   const KiviPageLaunch* append;  // non-null: the step's append (token write, page build),
                                  // fused into the decode launch

@@ -1,5 +1,5 @@
-// tl_kivi.hpp -- paged KIVI INT4 page format shared by the codec and the
-// decode kernel.
+// tl_kivi.hpp -- paged KIVI page formats (INT4 and INT8) shared by the codec
+// and the decode kernel.
 //
 // A page holds 32 consecutive tokens of one kv head (head size 128):
 //   [   0, 2048) K nibbles, 128 chunks of 16 B.  Chunk c = tt*64 + j*16 + u
@@ -22,9 +22,34 @@
 //   [4608, 5120) V (step, zero): (channel group g, lane group r) -> 8 fp16
 //                steps then 8 fp16 zeros in slot order (per token over 32
 //                channels).
+//
+// The INT8 page (KiviConfig.bits = 8, config_schema.h:124) is the INT4 page
+// with every 16-byte code chunk widened to 32 bytes, so that a lane's chunk
+// covers the same (token, channel) set:
+//   [   0, 4096) K codes, 128 chunks of 32 B.  Dword 2m + h holds channels
+//                8o + 4h + {0, 2, 1, 3} of octet o = j + 4m in bytes 0..3;
+//                masked with 0x00FF00FF (and the same after a shift by 8) it
+//                gives channel pairs (0, 1) and (2, 3) as fp16 denormals.
+//   [4096, 4608) K (step, zero), as for INT4.
+//   [4608, 8704) V codes, 128 chunks of 32 B.  Dword 2m + h holds token
+//                slots 4h + {0, 2, 1, 3} of channel (4hh + m)*16 + u.
+//   [8704, 9216) V (step, zero), as for INT4.
+// Codes: scale = 255 / range, clamp(rint((x - min) * scale), 0, 255).
 #pragma once
 
 namespace tl {
+
+// Page geometry by code width: chunk bytes per lane, offsets, page size.
+template <int BITS> struct KiviFmt;
+template <> struct KiviFmt<4> {
+  static constexpr int kChunk = 16, kLevels = 15;
+  static constexpr int kKCodes = 0, kKParams = 2048, kVCodes = 2560, kVParams = 4608, kBytes = 5120;
+};
+template <> struct KiviFmt<8> {
+  static constexpr int kChunk = 32, kLevels = 255;
+  static constexpr int kKCodes = 0, kKParams = 4096, kVCodes = 4608, kVParams = 8704, kBytes = 9216;
+};
+inline int kivi_page_bytes(int bits) { return bits == 8 ? KiviFmt<8>::kBytes : KiviFmt<4>::kBytes; }
 
 constexpr int kKiviPageTokens = 32;
 constexpr int kKiviHead = 128;

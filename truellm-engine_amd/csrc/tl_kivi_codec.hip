@@ -128,8 +128,9 @@ __global__ __launch_bounds__(128) void kivi_vec_decompress_kernel(
 // Paged KIVI: build one page (32 tokens x 128 channels of one kv head) from
 // the fp16 pool [N, n_kv, 128, BS].
 // ---------------------------------------------------------------------------
+template <int BITS>
 __global__ __launch_bounds__(128) void kivi_page_kernel(PageJob j) {
-  __shared__ __attribute__((aligned(16))) KiviBuildSmem sm;
+  __shared__ __attribute__((aligned(16))) KiviBuildSmem<BITS> sm;
   const int tid = threadIdx.x;
   int bid = blockIdx.x;
   const int kvh = bid % j.num_kv_heads; bid /= j.num_kv_heads;
@@ -146,7 +147,7 @@ __global__ __launch_bounds__(128) void kivi_page_kernel(PageJob j) {
     page = pg;
     if (page >= lq / kKiviPageTokens) return;
   }
-  kivi_build_page<128>(sm, j, seq, kvh, page, L, tid);
+  kivi_build_page<128, BITS>(sm, j, seq, kvh, page, L, tid);
 }
 
 }  // namespace
@@ -167,7 +168,10 @@ int launch_kivi_pages(const KiviPageLaunch& a) {
   if (!a.append && a.max_pages_to_build <= 0) return 0;
   const PageJob j = make_page_job(a);
   const dim3 grid((unsigned)(a.num_seqs * j.pages_per_seq_grid * a.num_kv_heads));
-  hipLaunchKernelGGL(kivi_page_kernel, grid, dim3(128), 0, a.stream, j);
+  if (a.bits == 8)
+    hipLaunchKernelGGL(kivi_page_kernel<8>, grid, dim3(128), 0, a.stream, j);
+  else
+    hipLaunchKernelGGL(kivi_page_kernel<4>, grid, dim3(128), 0, a.stream, j);
   return hipGetLastError() == hipSuccess ? 0 : 5;
 }
 

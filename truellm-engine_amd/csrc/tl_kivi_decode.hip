@@ -1,14 +1,15 @@
-// tl_kivi_decode.hip -- paged-attention decode over KIVI INT4 KV (gfx950).
+// tl_kivi_decode.hip -- paged-attention decode over KIVI INT4 / INT8 KV (gfx950).
 //
 // A sequence of length L keeps its first Lq = kivi_quantized_len(L, R)
-// tokens in 32-token INT4 pages (tl_kivi.hpp) and the rest (R .. R+31
+// tokens in 32-token INT4 or INT8 pages (tl_kivi.hpp) and the rest (R .. R+31
 // tokens) in the fp16 paged pool.  One workgroup owns one (sequence, kv
 // head, partition of pages) and serves four q heads of the GQA group.
 //
-// Page wavefronts: per page a lane issues 20 16-byte loads (nibbles and
-// step/zero of K and V), unpacks nibbles in registers with the fp16 magic
-// number (0x6400 | n == 1024 + n), removes the 1024 and applies
-// n * step + zero with packed fp16 ops, which yields MFMA operands directly:
+// Page wavefronts: per page a lane issues 5 (INT4) or 9 (INT8) 16-byte loads
+// (codes and step/zero of K and V) and turns the codes into fp16 denormal
+// MFMA operands (n * 2^-24) with masks and shifts; step and zero go into
+// the other operand and a zero term, so that the MFMAs yield
+// n * step + zero:
 //   q.k: v_mfma_f32_16x16x32_f16, A = dequantised K (rows: 16 tokens,
 //        k: 32 channels), B = q (k: channels, columns: heads), 2 token tiles
 //        x 4 channel blocks per page;
@@ -56,6 +57,12 @@ __device__ __forceinline__ u32x4 nib8(uint32_t w) {
   return u32x4{w & 0x000F000Fu, w & 0x00F000F0u, y & 0x000F000Fu, y & 0x00F000F0u};
 }
 
+// Eight 8-bit codes n_j of two dwords (byte k of dword h holds element
+// 4h + {0, 2, 1, 3}[k]) as fp16 denormals n * 2^-24, in element order.
+__device__ __forceinline__ u32x4 byte8(uint32_t w0, uint32_t w1) {
+  return u32x4{w0 & 0x00FF00FFu, (w0 >> 8) & 0x00FF00FFu, w1 & 0x00FF00FFu, (w1 >> 8) & 0x00FF00FFu};
+}
+
 constexpr float kTwo24 = 16777216.0f, kTwoM24 = 1.0f / 16777216.0f;
 
 __device__ __forceinline__ h8 as_h8(const u32x4& c) {
@@ -75,11 +82,36 @@ __device__ __forceinline__ float swap32_max(float x) {
   return fmaxf(__builtin_bit_cast(float, (unsigned)r[0]), __builtin_bit_cast(float, (unsigned)r[1]));
 }
 
-// One page's raw bytes as a lane loads them: its K and V nibble chunks and
-// one 16-byte slice of the page's 1 KiB of (step, zero) parameters.
+// One page's raw bytes as a lane loads them: its K and V code chunks (16
+// bytes per token tile / channel half for INT4, 32 for INT8) and one
+// 16-byte slice of the page's 1 KiB of (step, zero) parameters.
+template <int BITS>
 struct PageRaw {
-  u32x4 kn[2], vn[2], par;
+  static constexpr int CW = KiviFmt<BITS>::kChunk / 16;
+  u32x4 kn[2 * CW], vn[2 * CW], par;
 };
+
+// The q.k A operand of token tile tt, k block m, and the p.v B operand of
+// channel tile nt, from a lane's code chunks.
+template <int BITS>
+__device__ __forceinline__ u32x4 k_codes(const PageRaw<BITS>& r, int tt, int m) {
+  if constexpr (BITS == 8) {
+    const u32x4& c = r.kn[2 * tt + m / 2];
+    return byte8(word(c, 2 * (m % 2)), word(c, 2 * (m % 2) + 1));
+  } else {
+    return nib8(word(r.kn[tt], m));
+  }
+}
+template <int BITS>
+__device__ __forceinline__ u32x4 v_codes(const PageRaw<BITS>& r, int nt) {
+  const int hh = nt / 4, m = nt % 4;
+  if constexpr (BITS == 8) {
+    const u32x4& c = r.vn[2 * hh + m / 2];
+    return byte8(word(c, 2 * (m % 2)), word(c, 2 * (m % 2) + 1));
+  } else {
+    return nib8(word(r.vn[hh], m));
+  }
+}
 
 // One page through a buffer descriptor (base = the page, 5120 bytes in
 // range, so the hardware also bounds every access) and per-lane 32-bit
@@ -88,13 +120,20 @@ struct PageRaw {
 // or a prefetch past the wavefront's last page) gets an empty range: its
 // loads return zeros without a memory request, while the number of loads
 // per iteration stays fixed.
-__device__ __forceinline__ void load_page(PageRaw& r, const uint8_t* page, bool there, unsigned off,
+template <int BITS>
+__device__ __forceinline__ void load_page(PageRaw<BITS>& r, const uint8_t* page, bool there, unsigned off,
                                           unsigned par_off) {
-  const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(page, there ? kKiviPageBytes : 0);
-  r.kn[0] = buffer_load16(rs, off);
-  r.kn[1] = buffer_load16(rs, 1024u + off);
-  r.vn[0] = buffer_load16(rs, unsigned(kKiviVNibOff) + off);
-  r.vn[1] = buffer_load16(rs, unsigned(kKiviVNibOff) + 1024u + off);
+  using F = KiviFmt<BITS>;
+  constexpr int CW = PageRaw<BITS>::CW;
+  constexpr unsigned kTile = 64u * F::kChunk;    // bytes of one token tile / channel half of codes
+  const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(page, there ? F::kBytes : 0);
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int w = 0; w < CW; ++w) {
+      r.kn[CW * t + w] = buffer_load16(rs, unsigned(F::kKCodes) + t * kTile + CW * off + 16u * w);
+      r.vn[CW * t + w] = buffer_load16(rs, unsigned(F::kVCodes) + t * kTile + CW * off + 16u * w);
+    }
   r.par = buffer_load16(rs, par_off);
 }
 
@@ -131,7 +170,8 @@ struct PageState {
 //   O[u][c] = 2^24 sum_t (p_ut slot_scale step_tg) (n_tc 2^-24) + sum_t p_ut zero_tg;
 // the first sum goes to acc (one MFMA per channel tile), the second to cz
 // (one MFMA per page: B column g holds zero_tg).
-__device__ __forceinline__ void page_pair(PageState& st, const PageRaw& ra, const PageRaw& rb, bool oka,
+template <int BITS>
+__device__ __forceinline__ void page_pair(PageState& st, const PageRaw<BITS>& ra, const PageRaw<BITS>& rb, bool oka,
                                           bool okb, const u32x4 (&qsc)[4], const u32x4 (&qss)[4],
                                           uint32_t* s_par_w, int lane, const h8& slot_scale) {
   constexpr int GT = kWaveHeads;
@@ -147,7 +187,7 @@ __device__ __forceinline__ void page_pair(PageState& st, const PageRaw& ra, cons
   f4 s[2][2];
 #pragma unroll
   for (int pi = 0; pi < 2; ++pi) {
-    const PageRaw& r = pi ? rb : ra;
+    const PageRaw<BITS>& r = pi ? rb : ra;
     const uint32_t* par = s_par_w + pi * 256;
     f4 zt = (f4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -160,8 +200,8 @@ __device__ __forceinline__ void page_pair(PageState& st, const PageRaw& ra, cons
     for (int m = 0; m < 4; ++m) {
       const u32x4* kp = reinterpret_cast<const u32x4*>(par + (grp + 4 * m) * 8);
       const h8 q2 = hmul(as_h8(qss[m]), kp[0]);
-      t0 = mfma(as_h8(nib8(word(r.kn[0], m))), q2, t0);
-      t1 = mfma(as_h8(nib8(word(r.kn[1], m))), q2, t1);
+      t0 = mfma(as_h8(k_codes(r, 0, m)), q2, t0);
+      t1 = mfma(as_h8(k_codes(r, 1, m)), q2, t1);
     }
     s[pi][0] = t0;
     s[pi][1] = t1;
@@ -207,7 +247,7 @@ __device__ __forceinline__ void page_pair(PageState& st, const PageRaw& ra, cons
   // ---- p.v (a hole's weights are zero) ----
 #pragma unroll
   for (int pi = 0; pi < 2; ++pi) {
-    const PageRaw& r = pi ? rb : ra;
+    const PageRaw<BITS>& r = pi ? rb : ra;
     const uint32_t* par = s_par_w + pi * 256 + 128;
     // zero term: B column u < 4 holds zero_tg of group g = u
     st.cz = mfma(pw[pi], as_h8(reinterpret_cast<const u32x4*>(par + ((u & 3) * 4 + grp) * 8)[1]), st.cz);
@@ -218,7 +258,7 @@ __device__ __forceinline__ void page_pair(PageState& st, const PageRaw& ra, cons
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const int nt = 2 * g + h;
-        st.acc[nt] = mfma(ps, as_h8(nib8(word(r.vn[nt / 4], nt % 4))), st.acc[nt]);
+        st.acc[nt] = mfma(ps, as_h8(v_codes(r, nt)), st.acc[nt]);
       }
     }
   }
@@ -233,6 +273,7 @@ __device__ __forceinline__ void page_pair(PageState& st, const PageRaw& ra, cons
 // kivi_decode_kernel).  early_ok: early_id is the table entry of page
 // pg_begin + lane * pg_step, read by the caller ahead of time (unchecked;
 // pages at or past pg_end and ids outside the pool are dropped here).
+template <int BITS>
 __device__ __forceinline__ void kivi_pages_wave(const KiviParams& k, int seq, int kvh, int hs,
                                                 int pg_begin, int pg_end, int pg_step,
                                                 uint32_t* s_par_w, float* s_acc_w, float* s_m_w,
@@ -244,7 +285,8 @@ __device__ __forceinline__ void kivi_pages_wave(const KiviParams& k, int seq, in
 
   // B operand of q.k: head u (real for u < GT), channels 32 m + 8 grp .. +7,
   // times scale * log2(e); zero for the padding heads
-  const _Float16 one = (_Float16)1.0f, sixteenth = (_Float16)0.0625f;
+  // INT4: the nibble pairs at bits 4 and 20 come out 16 times too large
+  const _Float16 one = (_Float16)1.0f, sixteenth = (_Float16)(BITS == 8 ? 1.0f : 0.0625f);
   const h8 slot_scale = {one, one, sixteenth, sixteenth, one, one, sixteenth, sixteenth};
   u32x4 qsc[4], qss[4];   // q * scale * log2(e); the same times slot_scale
   const int gi = hs * GT + u;
@@ -268,13 +310,14 @@ __device__ __forceinline__ void kivi_pages_wave(const KiviParams& k, int seq, in
   for (int nt = 0; nt < 8; ++nt) st.acc[nt] = (f4){0.f, 0.f, 0.f, 0.f};
 
   const int32_t* ptab = k.page_tables + (int64_t)seq * k.max_pages_per_seq;
-  const uint8_t* pool = k.pages + (int64_t)kvh * kKiviPageBytes;
-  const uint32_t pid_stride = uint32_t(p.num_kv_heads) * uint32_t(kKiviPageBytes);
-  // lane's 16 bytes of each 1 KiB nibble block; lanes 0-31 take the K params
-  // [2048, 2560), lanes 32-63 the V params [4608, 5120)
+  using F = KiviFmt<BITS>;
+  const uint8_t* pool = k.pages + (int64_t)kvh * F::kBytes;
+  const uint32_t pid_stride = uint32_t(p.num_kv_heads) * uint32_t(F::kBytes);
+  // lane's chunk of each code block (16 bytes per lane for INT4, 32 for
+  // INT8); lanes 0-31 take the K params, lanes 32-63 the V params
   const unsigned off = unsigned(lane) * 16u;
-  const unsigned par_off = lane < 32 ? unsigned(kKiviKParamOff) + off : unsigned(kKiviVParamOff) + off - 512u;
-  auto load = [&](PageRaw& ra, PageRaw& rb, int ia, int ib) {
+  const unsigned par_off = lane < 32 ? unsigned(F::kKParams) + off : unsigned(F::kVParams) + off - 512u;
+  auto load = [&](PageRaw<BITS>& ra, PageRaw<BITS>& rb, int ia, int ib) {
     // 32 x 32 -> 64-bit products keep the page base in scalar registers
     load_page(ra, pool + uint64_t(uint32_t(max(ia, 0))) * pid_stride, ia >= 0, off, par_off);
     load_page(rb, pool + uint64_t(uint32_t(max(ib, 0))) * pid_stride, ib >= 0, off, par_off);
@@ -287,7 +330,7 @@ __device__ __forceinline__ void kivi_pages_wave(const KiviParams& k, int seq, in
   // an empty range): a fixed number of loads per iteration lets the
   // compiler wait only for the pair about to be used, not for the prefetch.
   const int n_mine = pg_begin < pg_end ? (pg_end - pg_begin + pg_step - 1) / pg_step : 0;
-  PageRaw r0a, r0b, r1a, r1b;
+  PageRaw<BITS> r0a, r0b, r1a, r1b;
 #pragma unroll 1
   for (int c0 = 0; c0 < n_mine; c0 += kWave) {
     const int cn = min(kWave, n_mine - c0);
@@ -300,7 +343,7 @@ __device__ __forceinline__ void kivi_pages_wave(const KiviParams& k, int seq, in
     }
     auto id = [&](int o) { return o < cn ? __builtin_amdgcn_readlane(idv, o) : -1; };
     // the loads of pages o and o + 1
-    auto fetch = [&](PageRaw& ra, PageRaw& rb, int o) { load(ra, rb, id(o), id(o + 1)); };
+    auto fetch = [&](PageRaw<BITS>& ra, PageRaw<BITS>& rb, int o) { load(ra, rb, id(o), id(o + 1)); };
     fetch(r0a, r0b, 0);
 #pragma unroll 1
     for (int o = 0; o < cn; o += 4) {
@@ -479,10 +522,11 @@ struct KiviDecodeSmem {
 // Two wavefronts per SIMD (at most 256 registers, VGPRs and AGPRs together):
 // with 4-wavefront workgroups the compiler would otherwise take more and
 // halve the occupancy.
-template <int NW, bool FINAL, bool APPEND>
+template <int NW, bool FINAL, bool APPEND, int BITS>
 __global__ __launch_bounds__(NW * kWave, 2) void kivi_decode_kernel(KiviParams k) {
   using Smem = KiviDecodeSmem<NW>;
-  constexpr size_t kLds = (APPEND && sizeof(KiviBuildSmem) > sizeof(Smem)) ? sizeof(KiviBuildSmem) : sizeof(Smem);
+  using Build = KiviBuildSmem<BITS>;
+  constexpr size_t kLds = (APPEND && sizeof(Build) > sizeof(Smem)) ? sizeof(Build) : sizeof(Smem);
   __shared__ __attribute__((aligned(16))) unsigned char s_raw[kLds];
   Smem& sd = *reinterpret_cast<Smem*>(s_raw);
 
@@ -526,7 +570,7 @@ __global__ __launch_bounds__(NW * kWave, 2) void kivi_decode_kernel(KiviParams k
   // ends after the page wavefronts.)
   if constexpr (APPEND) {
     if (last && lq > 0 && lq != kivi_quantized_len(L - 1, k.residual_length)) {
-      kivi_build_page<NW * kWave>(*reinterpret_cast<KiviBuildSmem*>(s_raw), k.job, seq, kvh,
+      kivi_build_page<NW * kWave, BITS>(*reinterpret_cast<Build*>(s_raw), k.job, seq, kvh,
                                   lq / kKiviPageTokens - 1, L, tid);
       __syncthreads();   // the page is visible to the workgroup; the LDS is free again
     }
@@ -539,7 +583,7 @@ __global__ __launch_bounds__(NW * kWave, 2) void kivi_decode_kernel(KiviParams k
     // us at batch 64).  The second half's page wavefronts take the higher
     // priority on every other page pair, so both progress together (55.5
     // and 58.5 us).
-    kivi_pages_wave(k, seq, kvh, hs, pg0 + wave, pg1 - res_pages, page_waves, &sd.p[wave][0], &sd.acc[wave][0][0],
+    kivi_pages_wave<BITS>(k, seq, kvh, hs, pg0 + wave, pg1 - res_pages, page_waves, &sd.p[wave][0], &sd.acc[wave][0][0],
                     &sd.m[wave][0], &sd.l[wave][0], FINAL && blockIdx.x >= gridDim.x / 2,
                     FINAL && page_waves == NW - 1, early_id);
   } else {
@@ -555,7 +599,7 @@ __global__ __launch_bounds__(NW * kWave, 2) void kivi_decode_kernel(KiviParams k
     // the token's store, at the end of the window, off the page wavefronts'
     // path (the window ends halfway through the launch)
     if constexpr (APPEND) store_newest(k.job, nt, seq, kvh, lane);
-    kivi_pages_wave(k, seq, kvh, hs, pg1 - res_pages, pg1, 1, &sd.p[wave][0], &sd.acc[NW + 1][0][0],
+    kivi_pages_wave<BITS>(k, seq, kvh, hs, pg1 - res_pages, pg1, 1, &sd.p[wave][0], &sd.acc[NW + 1][0][0],
                     &sd.m[NW + 1][0], &sd.l[NW + 1][0], false, false, -1);
   }
   __syncthreads();
@@ -563,12 +607,17 @@ __global__ __launch_bounds__(NW * kWave, 2) void kivi_decode_kernel(KiviParams k
                                                         &sd.acc[0][0][0], seq, kvh, hs, part, tid, NW * kWave);
 }
 
-template <int NW, bool FINAL>
-void launch_decode(const KiviParams& k, bool append, unsigned grid, hipStream_t stream) {
+template <int NW, bool FINAL, int BITS>
+void launch_decode_bits(const KiviParams& k, bool append, unsigned grid, hipStream_t stream) {
   if (append)
-    hipLaunchKernelGGL((kivi_decode_kernel<NW, FINAL, true>), dim3(grid), dim3(NW * kWave), 0, stream, k);
+    hipLaunchKernelGGL((kivi_decode_kernel<NW, FINAL, true, BITS>), dim3(grid), dim3(NW * kWave), 0, stream, k);
   else
-    hipLaunchKernelGGL((kivi_decode_kernel<NW, FINAL, false>), dim3(grid), dim3(NW * kWave), 0, stream, k);
+    hipLaunchKernelGGL((kivi_decode_kernel<NW, FINAL, false, BITS>), dim3(grid), dim3(NW * kWave), 0, stream, k);
+}
+template <int NW, bool FINAL>
+void launch_decode(const KiviParams& k, bool append, int bits, unsigned grid, hipStream_t stream) {
+  if (bits == 8) launch_decode_bits<NW, FINAL, 8>(k, append, grid, stream);
+  else launch_decode_bits<NW, FINAL, 4>(k, append, grid, stream);
 }
 
 }  // namespace
@@ -599,9 +648,9 @@ int launch_kivi_decode(const KiviDecodeLaunch& a) {
   if (a.num_partitions == 1) {
     // 4 wavefronts per workgroup, two workgroups per CU: at batch 64 the
     // grid is resident in one round (65.1 against 67.1 us with 8)
-    launch_decode<4, true>(k, append, items, a.stream);
+    launch_decode<4, true>(k, append, a.bits, items, a.stream);
   } else {
-    launch_decode<4, false>(k, append, items * a.num_partitions, a.stream);
+    launch_decode<4, false>(k, append, a.bits, items * a.num_partitions, a.stream);
     if (hipGetLastError() != hipSuccess) return 5;
     return launch_lse_reduce(a.out, (int)Kind::F16, a.part_m, a.part_l, a.part_o, a.seq_lens,
                              a.num_seqs, a.num_heads, kKiviHead, a.num_partitions, 0,

@@ -18,11 +18,13 @@
 
 namespace tl {
 
-// __float2int_rn then the clamp to [0, 15] of kivi_cache.cu:109-112.
+// __float2int_rn then the clamp to [0, 15] of kivi_cache.cu:109-112 (to
+// [0, 255] for 8-bit codes).
+template <int LEVELS = 15>
 __device__ __forceinline__ int quant_nibble(float v) {
   const float r = __builtin_rintf(v);
   if (!(r >= 0.0f)) return 0;  // negative or NaN
-  if (r > 15.0f) return 15;
+  if (r > (float)LEVELS) return LEVELS;
   return (int)r;
 }
 
@@ -32,12 +34,13 @@ struct GroupQ {
   uint16_t step, zero;
 };
 
+template <int LEVELS = 15>
 __device__ __forceinline__ GroupQ group_params(float gmin, float gmax) {
   GroupQ g;
   const float range = gmax - gmin;
   const bool degenerate = !(range > 1e-6f);
   g.gmin = gmin;
-  g.scale = degenerate ? 0.0f : (15.0f / range);
+  g.scale = degenerate ? 0.0f : ((float)LEVELS / range);
   const float st = degenerate ? 0.0f : (1.0f / g.scale);
   const bool gmin_ok = (gmin == gmin) && (gmin > -FLT_MAX) && (gmin < FLT_MAX);
   g.step = f32_to_f16(st);
@@ -45,9 +48,10 @@ __device__ __forceinline__ GroupQ group_params(float gmin, float gmax) {
   return g;
 }
 
+template <int LEVELS = 15>
 __device__ __forceinline__ int quantise(float x, const GroupQ& g) {
   const float d = x - g.gmin;
-  return quant_nibble(d * g.scale);
+  return quant_nibble<LEVELS>(d * g.scale);
 }
 
 struct PageJob {
@@ -61,6 +65,7 @@ struct PageJob {
   int max_pages_per_seq, num_pages, residual_length;
   int pages_per_seq_grid;   // grid stride over page index (prefix build)
   int append;               // 1: write the new token, then the page that L completes, if any
+  int bits;                 // code width of the pages: 4 or 8
   const uint16_t* knew;     // append: new token per sequence [S, n_kv, 128]
   const uint16_t* vnew;
   const int32_t* slots;     // append: its slot in the fp16 pool
@@ -77,18 +82,20 @@ inline PageJob make_page_job(const KiviPageLaunch& a) {
   j.max_pages_per_seq = a.max_pages_per_seq; j.num_pages = a.num_pages;
   j.residual_length = a.residual_length;
   j.append = a.append;
+  j.bits = a.bits;
   j.knew = (const uint16_t*)a.knew; j.vnew = (const uint16_t*)a.vnew; j.slots = a.slots;
   j.pages_per_seq_grid = a.append ? 1 : (a.max_pages_to_build > 0 ? a.max_pages_to_build : 1);
   return j;
 }
 
-// LDS of one page build (30 KiB).
+// LDS of one page build (30 KiB for INT4 pages, 34 KiB for INT8).
+template <int BITS>
 struct KiviBuildSmem {
   uint16_t k[kKiviHead][kKiviPageTokens + 2];   // [channel][token] (+2 breaks bank conflicts)
   uint16_t v[kKiviPageTokens][kKiviHead + 2];   // [token][channel]
-  uint8_t qk[kKiviHead][kKiviPageTokens];       // K nibbles [channel][token]
-  uint8_t qv[kKiviPageTokens][kKiviHead];       // V nibbles [token][channel]
-  __attribute__((aligned(16))) uint8_t page[kKiviPageBytes];
+  uint8_t qk[kKiviHead][kKiviPageTokens];       // K codes [channel][token]
+  uint8_t qv[kKiviPageTokens][kKiviHead];       // V codes [token][channel]
+  __attribute__((aligned(16))) uint8_t page[KiviFmt<BITS>::kBytes];
 };
 
 // The new token (position L - 1) of (seq, kvh) into the fp16 pool, by NT
@@ -141,9 +148,11 @@ __device__ __forceinline__ void build_barrier() {
 
 // The group quantiser over unit u of a page: u < 128 is K channel u (its 32
 // tokens in order), u >= 128 is V (token, group of 32 channels) u - 128
-// (channels in order).  Nibbles go to qk / qv, step and zero to the page.
-__device__ __forceinline__ void quantise_unit(KiviBuildSmem& sm, int u) {
-  constexpr int T = kKiviPageTokens, D = kKiviHead;
+// (channels in order).  Codes go to qk / qv, step and zero to the page.
+template <int BITS>
+__device__ __forceinline__ void quantise_unit(KiviBuildSmem<BITS>& sm, int u) {
+  using F = KiviFmt<BITS>;
+  constexpr int T = kKiviPageTokens, D = kKiviHead, LV = F::kLevels;
   if (u < D) {
     const int c = u;
     float gmin = FLT_MAX, gmax = -FLT_MAX;
@@ -152,9 +161,9 @@ __device__ __forceinline__ void quantise_unit(KiviBuildSmem& sm, int u) {
       if (x < gmin) gmin = x;
       if (x > gmax) gmax = x;
     }
-    const GroupQ q = group_params(gmin, gmax);
-    for (int t = 0; t < T; ++t) sm.qk[c][t] = (uint8_t)quantise(f16_to_f32(sm.k[c][t]), q);
-    uint16_t* kp = reinterpret_cast<uint16_t*>(sm.page + kKiviKParamOff + (c / 8) * 32);
+    const GroupQ q = group_params<LV>(gmin, gmax);
+    for (int t = 0; t < T; ++t) sm.qk[c][t] = (uint8_t)quantise<LV>(f16_to_f32(sm.k[c][t]), q);
+    uint16_t* kp = reinterpret_cast<uint16_t*>(sm.page + F::kKParams + (c / 8) * 32);
     kp[c % 8] = q.step;
     kp[8 + c % 8] = q.zero;
   } else {
@@ -165,10 +174,10 @@ __device__ __forceinline__ void quantise_unit(KiviBuildSmem& sm, int u) {
       if (x < gmin) gmin = x;
       if (x > gmax) gmax = x;
     }
-    const GroupQ q = group_params(gmin, gmax);
-    for (int i = 0; i < 32; ++i) sm.qv[t][g * 32 + i] = (uint8_t)quantise(f16_to_f32(sm.v[t][g * 32 + i]), q);
+    const GroupQ q = group_params<LV>(gmin, gmax);
+    for (int i = 0; i < 32; ++i) sm.qv[t][g * 32 + i] = (uint8_t)quantise<LV>(f16_to_f32(sm.v[t][g * 32 + i]), q);
     const int r = kivi_v_group(t), s = kivi_v_slot(t);
-    uint16_t* vp = reinterpret_cast<uint16_t*>(sm.page + kKiviVParamOff + (g * 4 + r) * 32);
+    uint16_t* vp = reinterpret_cast<uint16_t*>(sm.page + F::kVParams + (g * 4 + r) * 32);
     vp[s] = q.step;
     vp[8 + s] = q.zero;
   }
@@ -180,9 +189,11 @@ __device__ __forceinline__ void quantise_unit(KiviBuildSmem& sm, int u) {
 // synchronises; the caller synchronises them again before it reuses the
 // LDS.  With j.append the token at position L - 1 is taken from the input
 // row.
-template <int NT>
-__device__ void kivi_build_page(KiviBuildSmem& sm, const PageJob& j, int seq, int kvh, int page, int L, int tid) {
+template <int NT, int BITS>
+__device__ void kivi_build_page(KiviBuildSmem<BITS>& sm, const PageJob& j, int seq, int kvh, int page, int L,
+                                int tid) {
   static_assert(NT % kWave == 0, "whole wavefronts");
+  using F = KiviFmt<BITS>;
   constexpr int T = kKiviPageTokens, D = kKiviHead;
   if (page >= j.max_pages_per_seq) return;
   const int pid = j.page_tables[(int64_t)seq * j.max_pages_per_seq + page];
@@ -252,11 +263,30 @@ __device__ void kivi_build_page(KiviBuildSmem& sm, const PageJob& j, int seq, in
   }
   build_barrier<NT>();
 
-  for (int u = tid; u < 2 * D; u += NT) quantise_unit(sm, u);
+  for (int u = tid; u < 2 * D; u += NT) quantise_unit<BITS>(sm, u);
   build_barrier<NT>();
 
-  // nibble dwords: 512 for K then 512 for V
   uint32_t* pw = reinterpret_cast<uint32_t*>(sm.page);
+  if constexpr (BITS == 8) {
+    // code dwords: 1024 for K then 1024 for V; byte k of dword 2m + h holds
+    // element 4h + {0, 2, 1, 3}[k] of its octet (K) or slot run (V)
+    for (int w = tid; w < 1024; w += NT) {
+      const int c = w / 8, dd = w % 8, m = dd / 2, h = dd % 2;
+      // K: chunk c = tt*64 + jj*16 + u holds token tt*16 + u, octet jj + 4m
+      const int t = (c / 64) * 16 + c % 16, o = (c % 64) / 16 + 4 * m;
+      const int kc = 8 * o + 4 * h;
+      pw[w] = (uint32_t)sm.qk[kc][t] | (uint32_t)sm.qk[kc + 2][t] << 8 | (uint32_t)sm.qk[kc + 1][t] << 16 |
+              (uint32_t)sm.qk[kc + 3][t] << 24;
+      // V: chunk c = hh*64 + r*16 + u, channel (4 hh + m)*16 + u, slots 4h ..
+      const int hh = c / 64, r = (c % 64) / 16, u = c % 16;
+      const int d = (4 * hh + m) * 16 + u;
+      pw[F::kVCodes / 4 + w] = (uint32_t)sm.qv[kivi_v_token(r, 4 * h)][d] |
+                               (uint32_t)sm.qv[kivi_v_token(r, 4 * h + 2)][d] << 8 |
+                               (uint32_t)sm.qv[kivi_v_token(r, 4 * h + 1)][d] << 16 |
+                               (uint32_t)sm.qv[kivi_v_token(r, 4 * h + 3)][d] << 24;
+    }
+  } else {
+  // nibble dwords: 512 for K then 512 for V
   for (int w = tid; w < 512; w += NT) {
     // K dword w: chunk c = w / 4 (= tt*64 + jj*16 + u), dword m = w % 4
     const int ch = w / 4, m = w % 4;
@@ -275,12 +305,13 @@ __device__ void kivi_build_page(KiviBuildSmem& sm, const PageJob& j, int seq, in
 #pragma unroll
     for (int s = 0; s < 8; ++s)
       y |= (uint32_t)sm.qv[kivi_v_token(r, s)][d] << (16 * (s & 1) + 4 * (s >> 1));
-    pw[kKiviVNibOff / 4 + w] = y;
+    pw[F::kVCodes / 4 + w] = y;
+  }
   }
   build_barrier<NT>();
 
-  uint8_t* dst = j.pages + ((int64_t)pid * j.num_kv_heads + kvh) * kKiviPageBytes;
-  for (int i = tid; i < kKiviPageBytes / 16; i += NT)
+  uint8_t* dst = j.pages + ((int64_t)pid * j.num_kv_heads + kvh) * F::kBytes;
+  for (int i = tid; i < F::kBytes / 16; i += NT)
     reinterpret_cast<u32x4*>(dst)[i] = reinterpret_cast<const u32x4*>(sm.page)[i];
 }
 

@@ -73,11 +73,18 @@ class KiviDesc(ctypes.Structure):
         ("gqa_map", ctypes.c_int32),
         ("partition_pages", ctypes.c_int32),
         ("scale", ctypes.c_float),
+        ("bits", ctypes.c_int32),
     ]
 
 
 KIVI_PAGE_TOKENS = 32
 KIVI_PAGE_BYTES = 5120
+KIVI_PAGE_BYTES_INT8 = 9216
+
+
+def kivi_page_bytes(bits: int = 4) -> int:
+    """Page bytes per kv head of a KIVI page pool (tl_kivi_page_bytes)."""
+    return int(lib.tl_kivi_page_bytes(bits))
 
 
 class PrefillDesc(ctypes.Structure):
@@ -126,6 +133,7 @@ _SIG = {
     "tl_kivi_compress": (ctypes.c_int, [_P, _P, _I, _I, _I, _I, _P]),
     "tl_kivi_decompress": (ctypes.c_int, [_P, _P, _I, _I, _I, _I, _P]),
     "tl_kivi_quantized_len": (ctypes.c_int32, [_I, _I]),
+    "tl_kivi_page_bytes": (ctypes.c_size_t, [_I]),
     "tl_kivi_build_pages": (ctypes.c_int, [ctypes.POINTER(KiviDesc), _P, _P, _P, _P, _P, _P, _I, _P]),
     "tl_kivi_append": (ctypes.c_int, [ctypes.POINTER(KiviDesc), _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
     "tl_kivi_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(KiviDesc), _I]),
@@ -440,9 +448,10 @@ def kivi_quantized_len(seq_len, residual_length) -> int:
 
 
 def make_kivi_desc(q, k_cache, block_tables, page_tables, num_pages, num_kv_heads, scale, *,
-                   residual_length=128, gqa_map=GQA_GROUPED, partition_pages=0):
+                   residual_length=128, gqa_map=GQA_GROUPED, partition_pages=0, bits=4):
     S, H, D = q.shape
     d = KiviDesc()
+    d.bits = bits
     d.num_seqs, d.num_heads, d.num_kv_heads, d.head_size = S, H, num_kv_heads, D
     d.block_size = k_cache.shape[3]
     d.max_blocks_per_seq, d.num_blocks = block_tables.shape[1], k_cache.shape[0]
