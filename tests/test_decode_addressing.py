@@ -21,13 +21,17 @@ D = 128
 
 
 def table_entry(table, tok, t1, max_blocks, num_blocks, BS):
-    """table_entry_bs: physical block of token tok, -1 for a hole, a token
-    at or past t1, a row entry past max_blocks or an id past the pool."""
+    """table_blocks: physical block of token tok, -1 for a hole, a token at
+    or past t1, a row entry past max_blocks or an id past the pool.  The
+    kernel reads the row entry at the index clamped to the row whatever the
+    token, so that read must stay inside the row."""
     lb = tok // BS
+    idx = min(lb, max_blocks - 1)
+    assert 0 <= idx < max_blocks and idx < table.shape[0]
+    e = int(table[idx])
     if tok >= t1 or lb >= max_blocks:
         return -1
-    ph = int(table[lb])
-    return -1 if ph >= num_blocks else ph
+    return -1 if e >= num_blocks else e
 
 
 def wave_loads(E, BS, table, t0, t1, first_it, step, max_blocks, num_blocks, n_kv, kvh):
@@ -65,12 +69,12 @@ def wave_loads(E, BS, table, t0, t1, first_it, step, max_blocks, num_blocks, n_k
             addr = vbase0 + ib(it) + vblk * pool_stride + 16 * RB * dt
             yield "v", dt, addr, 16
 
+    # the first iteration's loads and, in every iteration, the next one's
+    # are issued unconditionally (a missing iteration reads block 0)
     it = first_it
-    if it < t1:
-        yield from ((it, k, j, a, w) for k, j, a, w in loads(it, blocks(it)))
+    yield from ((it, k, j, a, w) for k, j, a, w in loads(it, blocks(it)))
     while it < t1:
-        if it + step < t1:
-            yield from ((it + step, k, j, a, w) for k, j, a, w in loads(it + step, blocks(it + step)))
+        yield from ((it + step, k, j, a, w) for k, j, a, w in loads(it + step, blocks(it + step)))
         it += step
 
 

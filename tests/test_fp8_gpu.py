@@ -172,3 +172,59 @@ def test_fp8_graph_replay_matches_eager():
         tla.paged_attention_decode(desc, out, qd, kd, vd, bt, sl, 4096, ws)
         torch.cuda.synchronize()
         assert torch.equal(out, eager)
+
+
+RAGGED = [32768, 1, 0, 511, 512, 513, 16385, 4097, 32767, 8191, 1025, 3, 12345, 30000, 64, 700]
+
+
+@pytest.mark.parametrize("kv", ["fp8", "bf16"])
+@pytest.mark.parametrize("H", [32, 64, 128])
+def test_whole_partitions_per_wavefront_ragged_lengths(kv, H):
+    """Split-K at 512-token partitions with at least 4096 partitions runs
+    whole partitions per wavefront (4 per wavefront here), the finished ones
+    kept in LDS until the wavefront's last loads (groups 4 and 8) or written
+    at once (group 16, whose slots would not fit): ragged lengths, empty and
+    one-token sequences, partition edges, against the single-pass kernel
+    (itself checked against the oracle by the tests above)."""
+    S, n_kv, D, BS = len(RAGGED), 8, 128, 16
+    g = torch.Generator(device="cuda").manual_seed(inputs.SEEDS[1] + H)
+    nbs = [(L + BS - 1) // BS for L in RAGGED]
+    mb = max(nbs)
+    N = sum(nbs) + 5
+    perm = torch.randperm(N, generator=g, device="cuda").to(torch.int32)
+    tables = torch.full((S, mb), -1, dtype=torch.int32, device="cuda")
+    off = 0
+    for s, nb in enumerate(nbs):
+        tables[s, :nb] = perm[off:off + nb]
+        off += nb
+    q = torch.randn(S, H, D, generator=g, device="cuda").to(torch.bfloat16)
+    if kv == "fp8":
+        kf = torch.randn(N, n_kv, D, BS, generator=g, device="cuda", dtype=torch.float16)
+        vf = torch.randn(N, n_kv, D, BS, generator=g, device="cuda", dtype=torch.float16)
+        ks, vs = kf.abs().max().item() / 448.0, vf.abs().max().item() / 448.0
+        k = (kf.float() / ks).to(torch.float8_e4m3fn).view(torch.uint8)
+        v = (vf.float() / vs).to(torch.float8_e4m3fn).view(torch.uint8)
+        del kf, vf
+        extra = dict(kv_dtype=tla.FP8_E4M3, k_scale=ks, v_scale=vs)
+        tol = ATOL_FP8
+    else:
+        k = torch.randn(N, n_kv, D, BS, generator=g, device="cuda").to(torch.bfloat16)
+        v = torch.randn(N, n_kv, D, BS, generator=g, device="cuda").to(torch.bfloat16)
+        extra = {}
+        tol = 2e-3
+    sl = torch.tensor(RAGGED, dtype=torch.int32, device="cuda")
+    L = max(RAGGED)
+    scale = 1 / math.sqrt(D)
+    outs = {}
+    for pt in (-1, 512):
+        desc = tla.make_decode_desc(q, k, tables, n_kv, scale, partition_tokens=pt, **extra)
+        ws = torch.empty(max(16, tla.workspace_bytes(desc, L)), dtype=torch.uint8, device="cuda")
+        out = torch.full_like(q, float("nan"))
+        print(f"case whole partitions kv={kv} H={H} pt={pt}", flush=True)
+        tla.paged_attention_decode(desc, out, q, k, v, tables, sl, L, ws)
+        torch.cuda.synchronize()
+        outs[pt] = out.float()
+    empty = torch.tensor(RAGGED, device="cuda") == 0
+    assert (outs[512][empty] == 0).all() and (outs[-1][empty] == 0).all()
+    assert torch.isfinite(outs[512]).all()
+    assert (outs[512] - outs[-1]).abs().max().item() <= 2 * tol

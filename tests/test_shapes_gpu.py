@@ -140,6 +140,46 @@ def test_reference_dispatch_shapes(D, code, H, n_kv):
         assert_close(_decode(case, gqa, 512), ref, code, ATOL, f"split-K D={D}")
 
 
+@pytest.mark.parametrize("D,code", [(96, orc.BF16), (256, orc.BF16), (128, orc.F16)])
+def test_merge_of_9_to_256_partitions(D, code):
+    """Split-K into 9-19 partitions of 512 tokens (the wide log-sum-exp
+    merge, whose loads all start before the sequence length is read):
+    ragged lengths with an empty sequence, holes and NaN tails, against the
+    oracle."""
+    lens = [9000, 1, 4600, 0, 513, 6001]
+    case = inputs.make_paged_case(300 + D, len(lens), 8, 2, D, 16, lens, code, holes=2)
+    _poison_tails(case, code)
+    for gqa in (tla.GQA_MODULO, tla.GQA_GROUPED):
+        print(f"case wide merge D={D} code={code} gqa={gqa}", flush=True)
+        assert_close(_decode(case, gqa, 512), _ref(case, gqa), code, ATOL, f"wide merge D={D}")
+
+
+def test_merge_of_more_than_256_partitions():
+    """One sequence of 133 000 tokens (32/8 heads, d 128, bf16): 260
+    partitions of 512 tokens (the long merge), 65 of 2048 (the wide merge)
+    and the single pass agree."""
+    L, H, n_kv, D, BS = 133000, 32, 8, 128, 16
+    g = torch.Generator(device="cuda").manual_seed(inputs.SEEDS[2])
+    nb = (L + BS - 1) // BS
+    N = nb + 7
+    tables = torch.randperm(N, generator=g, device="cuda").to(torch.int32)[:nb].view(1, nb).contiguous()
+    k = torch.randn(N, n_kv, D, BS, generator=g, device="cuda").to(torch.bfloat16)
+    v = torch.randn(N, n_kv, D, BS, generator=g, device="cuda").to(torch.bfloat16)
+    q = torch.randn(1, H, D, generator=g, device="cuda").to(torch.bfloat16)
+    sl = torch.tensor([L], dtype=torch.int32, device="cuda")
+    outs = {}
+    for pt in (-1, 512, 2048):
+        desc = tla.make_decode_desc(q, k, tables, n_kv, 1 / math.sqrt(D), partition_tokens=pt)
+        ws = torch.empty(max(16, tla.workspace_bytes(desc, L)), dtype=torch.uint8, device="cuda")
+        out = torch.full_like(q, float("nan"))
+        print(f"case long merge pt={pt}", flush=True)
+        tla.paged_attention_decode(desc, out, q, k, v, tables, sl, L, ws)
+        torch.cuda.synchronize()
+        outs[pt] = out.float()
+    for pt in (512, 2048):
+        assert (outs[pt] - outs[-1]).abs().max().item() <= 2 * ATOL, pt
+
+
 # ---------------------------------------------------------------------------
 # paged_attention_v2 drop-in
 # ---------------------------------------------------------------------------

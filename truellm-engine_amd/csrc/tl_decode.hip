@@ -409,14 +409,14 @@ __global__ __launch_bounds__(64) void lse_reduce_kernel(
   }
 }
 
-// Log-sum-exp merge for plans of more than 8 partitions (FP8 at 512-token
-// partitions: 64): one workgroup of 4 wavefronts per (sequence, head).  The
-// (max, sum) pairs are reduced over all threads; then wavefront w sums the
-// partial outputs of partitions w, w + 4, ... (lane: head dims lane + 64 c),
-// 4 partitions per round with their loads in flight together, and the 4
-// wavefronts' sums meet in LDS.
+// Log-sum-exp merge for plans of more than 256 partitions: one workgroup
+// of 4 wavefronts per (sequence, head).  The (max, sum) pairs are reduced
+// over all threads; then wavefront w sums the partial outputs of
+// partitions w, w + 4, ... (lane: head dims lane + 64 c), 4 partitions per
+// round with their loads in flight together, and the 4 wavefronts' sums
+// meet in LDS.
 template <Kind QK, int HEAD>
-__global__ __launch_bounds__(256) void lse_reduce_wide_kernel(
+__global__ __launch_bounds__(256) void lse_reduce_long_kernel(
     void* out, const float* part_m, const float* part_l, const float* part_o, const int32_t* seq_lens,
     int num_heads, int num_partitions, int partition_tokens, int kivi_residual, int kivi_pages,
     int kivi_max_pages) {
@@ -474,11 +474,87 @@ __global__ __launch_bounds__(256) void lse_reduce_wide_kernel(
   }
 }
 
+// Log-sum-exp merge for plans of 9-256 partitions (FP8 at 512-token
+// partitions: 64): one workgroup of 4 wavefronts per (sequence, head).
+// Every load is issued before the sequence length is known: thread i reads
+// the (max, sum) pair of partition i, and wavefront w the partial outputs
+// of partitions w, w + 4, ... (lane: head dims lane + 64 c), 16 at a time;
+// slots past the sequence's partitions are read and then dropped (their
+// weight is 0, and a select keeps stale values, NaN included, out of the
+// sums).  The pairs are reduced over the workgroup, each partition's weight
+// l exp(m - M) goes through LDS to the wavefront holding its outputs, and
+// the 4 wavefronts' sums meet in LDS: one memory round trip, where reading
+// the pairs, then the outputs round by round waited for each in turn
+// (64 partitions: 12.3 us).  Within a wavefront the partitions are summed
+// in ascending order.
+template <Kind QK, int HEAD>
+__global__ __launch_bounds__(256) void lse_reduce_wide_kernel(
+    void* out, const float* part_m, const float* part_l, const float* part_o, const int32_t* seq_lens,
+    int num_heads, int num_partitions, int partition_tokens, int kivi_residual, int kivi_pages,
+    int kivi_max_pages) {
+  constexpr int CH = (HEAD + 63) / 64, U = 16, kMaxParts = 256;
+  __shared__ float s_red[2][4];
+  __shared__ float s_coef[kMaxParts + 4 * U];
+  __shared__ float s_o[4][CH * 64];
+  const int sh = blockIdx.x, seq = sh / num_heads;
+  const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
+  const int P = num_partitions;              // 9 .. kMaxParts
+  const int64_t pb = (int64_t)sh * P;
+  const float m_i = tid < P ? part_m[pb + tid] : -INFINITY;
+  const float l_i = tid < P ? part_l[pb + tid] : 0.f;
+  auto load_round = [&](float (&v)[U][CH], int i0) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int i = min(i0 + 4 * u, P - 1);  // every load stays inside the partials
+#pragma unroll
+      for (int c = 0; c < CH; ++c) v[u][c] = part_o[(pb + i) * HEAD + min(lane + 64 * c, HEAD - 1)];
+    }
+  };
+  float v[U][CH];
+  load_round(v, wave);
+  const int np = merged_partitions(seq_lens[seq], P, partition_tokens, kivi_residual, kivi_pages, kivi_max_pages);
+  const bool ok = tid < np && l_i > 0.f;
+  float M = wave_max<32, 1>(ok ? m_i : -INFINITY);
+  if (lane == 0) s_red[0][wave] = M;
+  __syncthreads();
+  M = fmaxf(fmaxf(s_red[0][0], s_red[0][1]), fmaxf(s_red[0][2], s_red[0][3]));
+  const float coef = ok ? l_i * __expf(m_i - M) : 0.f;
+  s_coef[tid] = coef;
+  if (tid < 4 * U) s_coef[kMaxParts + tid] = 0.f;
+  const float W = wave_sum<32, 1>(coef);
+  if (lane == 0) s_red[1][wave] = W;
+  __syncthreads();
+  float o[CH];
+#pragma unroll
+  for (int c = 0; c < CH; ++c) o[c] = 0.f;
+  for (int i0 = wave; i0 < np; i0 += 4 * U) {
+    if (i0 != wave) load_round(v, i0);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const float cu = s_coef[min(i0 + 4 * u, kMaxParts + 4 * U - 1)];
+#pragma unroll
+      for (int c = 0; c < CH; ++c) o[c] += cu > 0.f ? cu * v[u][c] : 0.f;
+    }
+  }
+#pragma unroll
+  for (int c = 0; c < CH; ++c)
+    if (lane + 64 * c < HEAD) s_o[wave][lane + 64 * c] = o[c];
+  __syncthreads();
+  const float Wt = s_red[1][0] + s_red[1][1] + s_red[1][2] + s_red[1][3];
+  for (int d = tid; d < HEAD; d += 256) {
+    const float sum = s_o[0][d] + s_o[1][d] + s_o[2][d] + s_o[3][d];
+    store_scalar<QK>(out, (int64_t)sh * HEAD + d, Wt > 0.f ? sum / Wt : 0.f);
+  }
+}
+
 template <Kind QK, int HEAD>
 void launch_reduce(const DecodeLaunch& a) {
   const int P = a.num_partitions;
   const dim3 rgrid((unsigned)(a.num_seqs * a.num_heads));
-  if (P > 8)
+  if (P > 256)
+    hipLaunchKernelGGL((lse_reduce_long_kernel<QK, HEAD>), rgrid, dim3(256), 0, a.stream, a.out, a.part_m,
+                       a.part_l, (const float*)a.part_o, a.seq_lens, a.num_heads, P, a.partition_tokens, 0, 0, 0);
+  else if (P > 8)
     hipLaunchKernelGGL((lse_reduce_wide_kernel<QK, HEAD>), rgrid, dim3(256), 0, a.stream, a.out, a.part_m,
                        a.part_l, (const float*)a.part_o, a.seq_lens, a.num_heads, P, a.partition_tokens, 0, 0, 0);
   else
@@ -584,7 +660,11 @@ void launch_lse_reduce_q(void* out, const float* part_m, const float* part_l, co
                          int partition_tokens, int kivi_residual, int kivi_pages, int kivi_max_pages,
                          hipStream_t stream) {
   const dim3 grid((unsigned)(num_seqs * num_heads));
-  if (num_partitions > 8)
+  if (num_partitions > 256)
+    hipLaunchKernelGGL((lse_reduce_long_kernel<QK, 128>), grid, dim3(256), 0, stream, out, part_m, part_l,
+                       (const float*)part_o, seq_lens, num_heads, num_partitions, partition_tokens, kivi_residual,
+                       kivi_pages, kivi_max_pages);
+  else if (num_partitions > 8)
     hipLaunchKernelGGL((lse_reduce_wide_kernel<QK, 128>), grid, dim3(256), 0, stream, out, part_m, part_l,
                        (const float*)part_o, seq_lens, num_heads, num_partitions, partition_tokens, kivi_residual,
                        kivi_pages, kivi_max_pages);

@@ -81,7 +81,9 @@ __global__ __launch_bounds__(4 * kWave) __attribute__((amdgpu_waves_per_eu(3))) 
   const int hs = bid % p.head_slices;      bid /= p.head_slices;
   const int kvh = bid % p.num_kv_heads;
   const int seq = bid / p.num_kv_heads;
-  mw::partitions_per_wave<KV, QK, BS>(p, seq, kvh, hs, (4 * pg + wave) * p.parts_per_wave);
+  extern __shared__ __attribute__((aligned(16))) float stash[];
+  mw::partitions_per_wave<KV, QK, BS>(p, seq, kvh, hs, (4 * pg + wave) * p.parts_per_wave,
+                                      p.stash_floats ? stash + wave * p.stash_floats : nullptr);
 }
 
 // Whether split-K runs one partition per wavefront: when splitting a
@@ -139,8 +141,12 @@ int launch_typed(const DecodeLaunch& a) {
     // resident round at 2-3 per SIMD), at most 8
     p.parts_per_wave = (int)std::max(1L, std::min(8L, (long)items * P / 2048));
     const int runs = (P + p.parts_per_wave - 1) / p.parts_per_wave;
-    hipLaunchKernelGGL((wave_partition_kernel<KV, QK, BS>), dim3(items * ((runs + 3) / 4)), dim3(4 * kWave), 0,
-                       a.stream, p);
+    // a wavefront's finished partitions wait in LDS while that keeps two
+    // workgroups per CU (<= 64 KiB each)
+    const int stash = (p.parts_per_wave - 1) * mw::stash_floats(std::min(p.group, mw::kHeads));
+    p.stash_floats = 4 * stash * (int)sizeof(float) <= 64 * 1024 ? stash : 0;
+    hipLaunchKernelGGL((wave_partition_kernel<KV, QK, BS>), dim3(items * ((runs + 3) / 4)), dim3(4 * kWave),
+                       4 * p.stash_floats * sizeof(float), a.stream, p);
   } else {
     launch_kernel<KV, QK, 4, false, BS>(p, items * P, a.stream);
   }

@@ -44,6 +44,7 @@ struct Params {
   int num_heads, num_kv_heads, max_blocks_per_seq, num_blocks;
   int num_partitions, partition_tokens;
   int parts_per_wave;   // split-K with a wavefront per partition run: partitions each wavefront streams
+  int stash_floats = 0; // LDS floats per wavefront for its finished partitions (0: written at once)
   int group, head_slices, gqa_map;
   float qk_scale;  // softmax scale * k dequant scale * log2(e)
   float v_scale;

@@ -84,14 +84,27 @@ template <int BS, int TPI> constexpr int blocks_per_iteration() { return BS >= T
 template <int BS, int TPI, int E>
 __device__ __forceinline__ int in_block_bytes(int it) { return BS > TPI ? E * (it % BS) : 0; }
 
-// Physical blocks of the NB blocks starting at token it (-1: hole, past t1
-// or outside the pool).
+// A sequence's block-table row read through the constant address space:
+// the table is not written during the kernel, and with wave-uniform
+// indices the reads are scalar loads, waited for on their own counter, so
+// no K/V load in flight is waited for on account of a table entry.
+typedef const __attribute__((address_space(4))) int32_t* TableRow;
+
+// Physical blocks of the NB blocks starting at token it (< 0: hole, past t1
+// or outside the pool).  Every entry is read, at an index clamped to the
+// row (max_blocks_per_seq >= 1), and checked afterwards: a read under a
+// condition would make the compiler wait for every load in flight before
+// the entries are used.
 template <int NB> struct Blocks { int e[NB]; };
 template <int NB, int BS>
-__device__ __forceinline__ Blocks<NB> table_blocks(const Params& p, const int32_t* table, int it, int t1) {
+__device__ __forceinline__ Blocks<NB> table_blocks(const Params& p, TableRow table, int it, int t1) {
   Blocks<NB> b;
 #pragma unroll
-  for (int i = 0; i < NB; ++i) b.e[i] = table_entry_bs<BS>(p, table, it + BS * i, t1);
+  for (int i = 0; i < NB; ++i) {
+    const int tok = it + BS * i, lb = tok / BS;
+    const int e = table[__builtin_amdgcn_readfirstlane(min(lb, p.max_blocks_per_seq - 1))];
+    b.e[i] = (tok >= t1 || lb >= p.max_blocks_per_seq || e >= p.num_blocks) ? -1 : e;
+  }
   return b;
 }
 // Entry i (per lane) of a wave-uniform set.  Written as one nested select:
@@ -239,7 +252,7 @@ __device__ __forceinline__ State fp8_wave(const Params& p, int seq, int kvh, int
   State st;
   st.init();
 
-  const int32_t* table = p.block_tables + (int64_t)seq * p.max_blocks_per_seq;
+  const TableRow table = (TableRow)(p.block_tables + (int64_t)seq * p.max_blocks_per_seq);
   const int64_t pool_stride = (int64_t)p.num_kv_heads * kBlockBytes;
   // this lane's K quad and V run: their blocks within the iteration and
   // their byte offsets in a block row (plus the iteration's own offset when
@@ -261,9 +274,12 @@ __device__ __forceinline__ State fp8_wave(const Params& p, int seq, int kvh, int
   Blocks<NB> nxt = table_blocks<NB, BS>(p, table, it + step, t1);
   uint32_t kw[32];
   u32x4 vr[8];
-  if (it < t1) {
+  {
+    // in the loop's order (K, then V), so that the loop's waits can count
+    // the loads in flight from its first iteration on
     const int ib = in_block_bytes<BS, TPI, 1>(it);
     load_k(kw, kbase0 + ib + (int64_t)max(pick(cur, kb), 0) * pool_stride);
+    __builtin_amdgcn_sched_barrier(0);
     load_v(vr, vbase0 + ib + (int64_t)max(pick(cur, vb), 0) * pool_stride);
   }
 
@@ -276,7 +292,6 @@ __device__ __forceinline__ State fp8_wave(const Params& p, int seq, int kvh, int
       }
     }
     const Blocks<NB> nn = table_blocks<NB, BS>(p, table, it + 2 * step, t1);
-    const bool has_next = it + step < t1;
     const int ib_next = in_block_bytes<BS, TPI, 1>(it + step);
 
     // ---- q.k: 4 tiles (token i of each quad) x 4 MFMA steps ----
@@ -301,7 +316,10 @@ __device__ __forceinline__ State fp8_wave(const Params& p, int seq, int kvh, int
 #pragma unroll
       for (int i = 0; i < 4; ++i) s[i] = mma<Kind::F16>(a[i][0], a[i][1], a[i][2], a[i][3], qb[sk], s[i]);
     }
-    if (has_next) load_k(kw, kbase0 + ib_next + (int64_t)max(pick(nxt, kb), 0) * pool_stride);
+    // the next iteration's loads are issued whether or not it exists (a
+    // missing one reads block 0): under a condition the compiler would
+    // wait for them, too, before this iteration's V is used
+    load_k(kw, kbase0 + ib_next + (int64_t)max(pick(nxt, kb), 0) * pool_stride);
 
     // ---- softmax: lane (m, kg) owns head m, iteration tokens 16 kg + 4 r + i ----
     const int ph_v = pick(cur, vb);
@@ -347,7 +365,7 @@ __device__ __forceinline__ State fp8_wave(const Params& p, int seq, int kvh, int
       st.o[dt] = mma<Kind::F16>(f8x2<false>(v.z), f8x2<true>(v.z), f8x2<false>(v.w), f8x2<true>(v.w), pb[1],
                                 st.o[dt]);
     }
-    if (has_next) load_v(vr, vbase0 + ib_next + (int64_t)max(pick(nxt, vb), 0) * pool_stride);
+    load_v(vr, vbase0 + ib_next + (int64_t)max(pick(nxt, vb), 0) * pool_stride);
     cur = nxt;
     nxt = nn;
   }
@@ -393,7 +411,7 @@ __device__ __forceinline__ State mfma2_wave(const Params& p, int seq, int kvh, i
   State st;
   st.init();
 
-  const int32_t* table = p.block_tables + (int64_t)seq * p.max_blocks_per_seq;
+  const TableRow table = (TableRow)(p.block_tables + (int64_t)seq * p.max_blocks_per_seq);
   const int64_t pool_stride = (int64_t)p.num_kv_heads * kBlockBytes;
   // this lane's K pair and V run: their blocks within the iteration and
   // their byte offsets in a block row (plus the iteration's own offset when
@@ -415,9 +433,12 @@ __device__ __forceinline__ State mfma2_wave(const Params& p, int seq, int kvh, i
   Blocks<NB> nxt = table_blocks<NB, BS>(p, table, it + step, t1);
   uint32_t kw[32];
   u32x4 vr[8];
-  if (it < t1) {
+  {
+    // in the loop's order (K, then V), so that the loop's waits can count
+    // the loads in flight from its first iteration on
     const int ib = in_block_bytes<BS, TPI, 2>(it);
     load_k(kw, kbase0 + ib + (int64_t)max(pick(cur, kb), 0) * pool_stride);
+    __builtin_amdgcn_sched_barrier(0);
     load_v(vr, vbase0 + ib + (int64_t)max(pick(cur, vb), 0) * pool_stride);
   }
 
@@ -430,7 +451,6 @@ __device__ __forceinline__ State mfma2_wave(const Params& p, int seq, int kvh, i
       }
     }
     const Blocks<NB> nn = table_blocks<NB, BS>(p, table, it + 2 * step, t1);
-    const bool has_next = it + step < t1;
     const int ib_next = in_block_bytes<BS, TPI, 2>(it + step);
 
     // ---- q.k: 2 tiles (token i of each pair) x 4 MFMA steps ----
@@ -447,7 +467,10 @@ __device__ __forceinline__ State mfma2_wave(const Params& p, int seq, int kvh, i
 #pragma unroll
       for (int i = 0; i < 2; ++i) s[i] = mma<KV>(a[i][0], a[i][1], a[i][2], a[i][3], qb[sk], s[i]);
     }
-    if (has_next) load_k(kw, kbase0 + ib_next + (int64_t)max(pick(nxt, kb), 0) * pool_stride);
+    // the next iteration's loads are issued whether or not it exists (a
+    // missing one reads block 0): under a condition the compiler would
+    // wait for them, too, before this iteration's V is used
+    load_k(kw, kbase0 + ib_next + (int64_t)max(pick(nxt, kb), 0) * pool_stride);
 
     // ---- softmax: lane (m, kg) owns head m, iteration tokens 8 kg + 2 r + i ----
     const int ph_v = pick(cur, vb);
@@ -489,7 +512,7 @@ __device__ __forceinline__ State mfma2_wave(const Params& p, int seq, int kvh, i
       st.o[dt] = mma<KV>(vr[dt].x, vr[dt].y, vr[dt].z, vr[dt].w, pb, st.o[dt]);
       if constexpr (KV == Kind::BF16) st.o[dt] = mma<KV>(vr[dt].x, vr[dt].y, vr[dt].z, vr[dt].w, pl, st.o[dt]);
     }
-    if (has_next) load_v(vr, vbase0 + ib_next + (int64_t)max(pick(nxt, vb), 0) * pool_stride);
+    load_v(vr, vbase0 + ib_next + (int64_t)max(pick(nxt, vb), 0) * pool_stride);
     cur = nxt;
     nxt = nn;
   }
@@ -510,33 +533,90 @@ __device__ __forceinline__ State run_wave(const Params& p, int seq, int kvh, int
 // r of head m, normalised by the head's sum; the (max, sum) pair in
 // natural-log units from the lanes of kg 0.  A head with no valid token
 // gets sum 0 (and max -inf), which the log-sum-exp merge skips.
-__device__ __forceinline__ void write_partial(const Params& p, const State& st, float v_scale, int seq, int kvh,
-                                              int hs, int part) {
+struct Partial {
+  f4 o[8];
+  float m, l;
+};
+__device__ __forceinline__ Partial finish_partial(const State& st, float v_scale) {
+  const float l_tot = sum_kg(st.l_lane);
+  const float f = l_tot > 0.f ? v_scale / l_tot : 0.f;
+  Partial r;
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt) r.o[dt] = st.o[dt] * f;
+  r.m = l_tot > 0.f ? st.m_run * (1.0f / kLog2e) : -INFINITY;
+  r.l = l_tot;
+  return r;
+}
+__device__ __forceinline__ void store_partial(const Params& p, const Partial& r, int seq, int kvh, int hs,
+                                              int part) {
   const int lane = threadIdx.x % kWave;
   const int m = lane & 15, kg = lane >> 4;
-  const float l_tot = sum_kg(st.l_lane);
   const int gi = hs * kHeads + m;
   if (gi >= p.group) return;
   const int64_t pi = ((int64_t)seq * p.num_heads + head_of(p, kvh, gi)) * p.num_partitions + part;
-  const float f = l_tot > 0.f ? v_scale / l_tot : 0.f;
   float* o = reinterpret_cast<float*>(p.part_o) + pi * kHead;
 #pragma unroll
-  for (int dt = 0; dt < 8; ++dt) *reinterpret_cast<f4*>(o + 16 * dt + 4 * kg) = st.o[dt] * f;
+  for (int dt = 0; dt < 8; ++dt) *reinterpret_cast<f4*>(o + 16 * dt + 4 * kg) = r.o[dt];
   if (kg == 0) {
-    p.part_m[pi] = l_tot > 0.f ? st.m_run * (1.0f / kLog2e) : -INFINITY;
-    p.part_l[pi] = l_tot;
+    p.part_m[pi] = r.m;
+    p.part_l[pi] = r.l;
   }
 }
+__device__ __forceinline__ void write_partial(const Params& p, const State& st, float v_scale, int seq, int kvh,
+                                              int hs, int part) {
+  store_partial(p, finish_partial(st, v_scale), seq, kvh, hs, part);
+}
 
-// The sink of a wavefront streaming several partitions: each finished
-// partition's partials go to the workspace.
+// LDS floats per stashed partition of one wavefront: 8 f4 and (max, sum)
+// for each of the 4 kg lanes of up to `heads` head columns.
+__host__ __device__ constexpr int stash_floats(int heads) { return heads * 4 * (8 * 4 + 2); }
+
+// The sink of a wavefront streaming several partitions.  A finished
+// partition's partials either go to the workspace at once or, with a
+// stash, wait in LDS until the wavefront's last loads are done: a store
+// counts on the same in-order counter as the loads, so every later wait
+// for a K/V load would also wait for the store's acknowledgement, which a
+// read-saturated HBM returns late (64 x 512-token FP8 partitions: 217 us
+// with the stores in the stream, 189 us without three of the four).
 struct PartialSink {
   static constexpr bool kActive = true;
   const Params& p;
   int part_tokens, seq, kvh, hs;
   float v_scale;
+  float* stash;      // this wavefront's slots, or nullptr
+  int first;         // the wavefront's first partition (slot 0)
+  int heads;         // head columns a slot holds: min(group - 16 hs, 16)
   __device__ void operator()(const State& st, int part) const {
-    write_partial(p, st, v_scale, seq, kvh, hs, part);
+    const Partial r = finish_partial(st, v_scale);
+    if (stash == nullptr) {
+      store_partial(p, r, seq, kvh, hs, part);
+      return;
+    }
+    const int lane = threadIdx.x % kWave;
+    const int m = lane & 15, kg = lane >> 4;
+    if (m >= heads) return;
+    const int c = 4 * m + kg, nc = 4 * heads;   // compact lane index over the valid heads
+    float* slot = stash + (part - first) * stash_floats(heads);
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) *reinterpret_cast<f4*>(slot + 4 * (dt * nc + c)) = r.o[dt];
+    slot[32 * nc + c] = r.m;
+    slot[33 * nc + c] = r.l;
+  }
+  // The stashed partitions [first, first + n) to the workspace.
+  __device__ void drain(int n) const {
+    const int lane = threadIdx.x % kWave;
+    const int m = lane & 15, kg = lane >> 4;
+    if (stash == nullptr || m >= heads) return;
+    const int c = 4 * m + kg, nc = 4 * heads;
+    for (int k = 0; k < n; ++k) {
+      const float* slot = stash + k * stash_floats(heads);
+      Partial r;
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) r.o[dt] = *reinterpret_cast<const f4*>(slot + 4 * (dt * nc + c));
+      r.m = slot[32 * nc + c];
+      r.l = slot[33 * nc + c];
+      store_partial(p, r, seq, kvh, hs, first + k);
+    }
   }
 };
 
@@ -544,13 +624,14 @@ struct PartialSink {
 // [first, first + parts_per_wave) of (sequence, kv head, 16-head slice)
 // alone, as one stream (q loaded once, the next iteration's loads in flight
 // across partition boundaries), writing each partition's partials when it
-// ends; no LDS, no merge inside the workgroup.  For short partitions (FP8
-// at 512 tokens: 8 iterations of 64 tokens) this pays the q prologue, the
-// first loads' latency and the tail once per run of partitions, where
-// splitting each partition over a workgroup pays them per quarter
-// partition.
+// ends (or, with a stash, after its last loads); no merge inside the
+// workgroup.  For short partitions (FP8 at 512 tokens: 8 iterations of 64
+// tokens) this pays the q prologue, the first loads' latency and the tail
+// once per run of partitions, where splitting each partition over a
+// workgroup pays them per quarter partition.
 template <Kind KV, Kind QK, int BS>
-__device__ __forceinline__ void partitions_per_wave(const Params& p, int seq, int kvh, int hs, int first) {
+__device__ __forceinline__ void partitions_per_wave(const Params& p, int seq, int kvh, int hs, int first,
+                                                    float* stash) {
   constexpr int TPI = tokens_per_iteration<KV>();
   if (first >= p.num_partitions) return;
   const int L = p.seq_lens[seq];
@@ -559,9 +640,11 @@ __device__ __forceinline__ void partitions_per_wave(const Params& p, int seq, in
   const int last = min(first + p.parts_per_wave, p.num_partitions);
   const int t1 = min(last * p.partition_tokens, L);
   const float vs = KV == Kind::FP8 ? p.v_scale : 1.f;
-  const PartialSink sink{p, p.partition_tokens, seq, kvh, hs, vs};
+  const PartialSink sink{p, p.partition_tokens, seq, kvh, hs, vs, stash, first, min(p.group - hs * kHeads, kHeads)};
   const State st = run_wave<KV, QK, BS>(p, seq, kvh, hs, t0, t1, TPI, sink);
-  write_partial(p, st, vs, seq, kvh, hs, (t1 - 1) / p.partition_tokens);
+  const int part_last = (t1 - 1) / p.partition_tokens;
+  write_partial(p, st, vs, seq, kvh, hs, part_last);
+  sink.drain(part_last - first);
 }
 
 // One workgroup of NW wavefronts over (sequence, kv head, 16-head slice,
