@@ -408,6 +408,41 @@ int tl_kivi_decode_step(const tl_kivi_desc* desc, void* out, const void* q, cons
                         const int32_t* block_tables, const int32_t* seq_lens, int32_t max_context_len,
                         void* workspace, size_t workspace_bytes, void* stream);
 
+/* The KIVI decode step with RoPE first: RoPE (style TL_ROPE_ADJACENT or
+ * TL_ROPE_HALVES, fp32 tables [max_positions, 64], position positions[s])
+ * of q [S, H, 128] and of the new keys [S, n_kv, 128], then
+ * tl_kivi_decode_step on the rotated q and keys, which are stored and
+ * quantised rotated: the order KiviConfig.pre_rope_keys = false names
+ * (config_schema.h:128), and the order of the engine's decode step, whose
+ * ggml rope precedes reshape_and_cache (cuda_engine.cpp:1100-1130).  The
+ * rotation is that of tl_rope_reshape_and_cache; a position outside the
+ * tables leaves that sequence's q and key unrotated.  Two launches (the
+ * rotation into the workspace, then the step); the workspace holds the
+ * step's split-K partials and the rotated rows: see
+ * tl_kivi_rope_step_workspace_bytes. */
+size_t tl_kivi_rope_step_workspace_bytes(const tl_kivi_desc* desc, int32_t max_context_len);
+int tl_kivi_rope_decode_step(const tl_kivi_desc* desc, void* out, const void* q, const void* key,
+                             const void* value, const int32_t* positions, const float* cos_table,
+                             const float* sin_table, int32_t max_positions, int32_t style,
+                             const int32_t* slot_mapping, void* pages, const int32_t* page_tables,
+                             void* k_cache, void* v_cache, const int32_t* block_tables,
+                             const int32_t* seq_lens, int32_t max_context_len, void* workspace,
+                             size_t workspace_bytes, void* stream);
+
+/* KiviConfig (config_schema.h:122-129) onto a descriptor: bits (4 or 8) and
+ * residual_length go to desc->bits / desc->residual_length.  The pages hold
+ * keys per channel and values per token, so key_granularity must be
+ * "per_channel" and value_granularity "per_token" (the defaults); other
+ * strings return TL_ERR_NOT_IMPLEMENTED.  pre_rope_keys = 0 is the order of
+ * tl_kivi_rope_decode_step (and of any caller that stores rotated keys);
+ * pre_rope_keys != 0 (keys quantised before RoPE, each dequantised key then
+ * rotated by its position inside attention) is not built and returns
+ * TL_ERR_NOT_IMPLEMENTED.  The reference parses these fields
+ * (src/host/config/config.cpp:216-223) but no kernel of it reads them. */
+int tl_kivi_apply_config(tl_kivi_desc* desc, int32_t bits, int32_t residual_length,
+                         const char* key_granularity, const char* value_granularity,
+                         int32_t pre_rope_keys);
+
 /* ---- host-side helpers of the path's callers (no device work) ----------- */
 
 /* The engine's attention dispatch (cuda_engine.cpp:1138-1160): v2 iff

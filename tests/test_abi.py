@@ -271,6 +271,54 @@ def test_kivi_page_bytes():
     assert tla.kivi_page_bytes(3) == 0 and tla.kivi_page_bytes(16) == 0
 
 
+def test_kivi_apply_config_maps_kiviconfig_and_rejects_what_is_not_built():
+    """KiviConfig (config_schema.h:122-129): bits and residual_length land
+    in the descriptor; the default granularities are the pages' layout;
+    other granularities and pre_rope_keys = true are not built."""
+    d = _kdesc(bits=0, residual_length=5)
+    tla.kivi_apply_config(d, bits=8, residual_length=128)
+    assert d.bits == 8 and d.residual_length == 128
+    tla.kivi_apply_config(d, bits=4, residual_length=0)
+    assert d.bits == 4 and d.residual_length == 0
+    L = tla.lib
+    call = lambda b, r, kg, vg, pre: L.tl_kivi_apply_config(ctypes.byref(d), b, r, kg, vg, pre)
+    assert call(8, 128, b"per_channel", b"per_token", 1) == tla.ERR_NOT_IMPLEMENTED
+    assert "pre_rope_keys" in tla.last_error()
+    assert call(8, 128, b"per_token", b"per_token", 0) == tla.ERR_NOT_IMPLEMENTED
+    assert call(8, 128, b"per_channel", b"per_channel", 0) == tla.ERR_NOT_IMPLEMENTED
+    assert call(8, 128, None, b"per_token", 0) == tla.ERR_NOT_IMPLEMENTED
+    assert call(6, 128, b"per_channel", b"per_token", 0) == tla.ERR_INVALID_ARGUMENT
+    assert call(8, -1, b"per_channel", b"per_token", 0) == tla.ERR_INVALID_ARGUMENT
+    assert L.tl_kivi_apply_config(None, 8, 128, b"per_channel", b"per_token", 0) == tla.ERR_INVALID_ARGUMENT
+    assert d.bits == 4 and d.residual_length == 0          # a rejected call leaves the descriptor
+
+
+def test_kivi_rope_step_workspace_and_argument_checks():
+    d = _kdesc(num_seqs=64)
+    ws = tla.kivi_workspace_bytes(d, 4096)
+    q_bytes, k_bytes = 64 * 32 * 128 * 2, 64 * 8 * 128 * 2
+    a256 = lambda n: (n + 255) // 256 * 256
+    assert tla.kivi_rope_step_workspace_bytes(d, 4096) == a256(ws) + a256(q_bytes) + k_bytes
+    d16 = _kdesc(num_seqs=16)
+    assert tla.kivi_rope_step_workspace_bytes(d16, 40000) == (
+        a256(tla.kivi_workspace_bytes(d16, 40000)) + a256(16 * 32 * 128 * 2) + 16 * 8 * 128 * 2)
+    assert tla.kivi_rope_step_workspace_bytes(_kdesc(head_size=64), 4096) == 0
+    L = tla.lib
+    need = tla.kivi_rope_step_workspace_bytes(d, 4096)
+
+    def call(desc, max_pos=8192, style=0, ws_bytes=need, ws=FAKE, pos=FAKE):
+        return L.tl_kivi_rope_decode_step(ctypes.byref(desc), FAKE, FAKE, FAKE, FAKE, pos, FAKE, FAKE, max_pos,
+                                          style, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 4096, ws, ws_bytes, None)
+    assert call(d, ws_bytes=need - 1) == tla.ERR_INVALID_ARGUMENT
+    assert "workspace" in tla.last_error()
+    assert call(d, ws=None) == tla.ERR_INVALID_ARGUMENT
+    assert call(d, max_pos=0) == tla.ERR_INVALID_ARGUMENT
+    assert call(d, style=2) == tla.ERR_INVALID_ARGUMENT
+    assert call(d, pos=None) == tla.ERR_INVALID_ARGUMENT
+    assert call(_kdesc(head_size=64)) == tla.ERR_NOT_IMPLEMENTED
+    assert call(_kdesc(num_seqs=0), ws=None, ws_bytes=0) == tla.OK
+
+
 # ---- reference-named C++ operators (include/tl_truellm_ops.h) -------------
 
 def _demangled_exports():

@@ -349,6 +349,69 @@ def test_kivi_decode_step_matches_oracle_each_step(H, pp, bits):
     assert np.array_equal(pages.cpu().numpy()[used], want_pages[used])
 
 
+def _oracle_rotate(q, knew, vnew, pos, cos_t, sin_t, style):
+    """The oracle's RoPE of q [S, H, 128] and of the new keys at pos (a
+    position past the tables leaves the rows unrotated), by way of a scratch
+    pool that holds token t in slot t."""
+    S, n_kv, D = knew.shape
+    q_out = q.copy()
+    nb = (S + 15) // 16
+    kpool = np.zeros((nb, n_kv, D, 16), np.uint16)
+    vpool = np.zeros_like(kpool)
+    slots = np.arange(S, dtype=np.int32)
+    orc.reshape_and_cache(knew, vnew, kpool, vpool, slots)
+    orc.rope_reshape_and_cache(q, q_out, knew, vnew, kpool, vpool, slots, pos, cos_t, sin_t, orc.F16, style)
+    k_rot = np.ascontiguousarray(kpool.transpose(0, 3, 1, 2).reshape(nb * 16, n_kv, D)[:S])
+    return q_out, k_rot
+
+
+@pytest.mark.parametrize("style,bits", [(tla.ROPE_ADJACENT, 4), (tla.ROPE_HALVES, 8), (tla.ROPE_ADJACENT, 8)])
+def test_kivi_rope_step_matches_oracle_each_step(style, bits):
+    """tl_kivi_rope_decode_step (RoPE of q and the new keys, then the fused
+    step on the rotated rows) against the oracle at every step: the
+    oracle's RoPE, the rotated key into the host pools, the pages rebuilt
+    and orc.kivi_paged_attention with the rotated q.  Sequence 5 runs past
+    the 1024-position tables halfway (those tokens stay unrotated); pages
+    complete during the run.  At the end the pools and pages are the
+    oracle's bit for bit."""
+    from test_oracle import rope_tables
+    start = np.array([150, 159, 160, 191, 33, 1000], np.int32)
+    steps = 36
+    kc = KiviCase(71, start + steps, H=32, extra_blocks=1, bits=bits)
+    cos_t, sin_t = rope_tables(1024, 128)
+    q_base = kc.q.copy()
+    qd, kd, vd = dev(kc.q, orc.F16), dev(kc.k, orc.F16), dev(kc.v, orc.F16)
+    btd, ptd = dev(kc.tables), dev(kc.page_tables)
+    pages = torch.zeros(kc.num_pages, kc.n_kv, kc.page_bytes, dtype=torch.uint8, device="cuda")
+    desc = kc.desc(qd, kd, btd, ptd, 0)
+    tla.kivi_build_pages(desc, kd, vd, btd, dev(start), ptd, pages, int(start.max()))
+    rng = np.random.default_rng(13)
+    max_ctx = int(start.max()) + steps
+    ws = torch.empty(tla.kivi_rope_step_workspace_bytes(desc, max_ctx), dtype=torch.uint8, device="cuda")
+    cos_d, sin_d = dev(cos_t), dev(sin_t)
+    lens = start.copy()
+    k_host, v_host = kc.k.copy(), kc.v.copy()
+    print(f"case kivi rope step vs oracle style={style} bits={bits}", flush=True)
+    for step in range(steps):
+        lens = lens + 1
+        pos = (lens - 1).astype(np.int32)
+        slots = (kc.tables[np.arange(kc.S), pos // 16] * 16 + pos % 16).astype(np.int32)
+        knew = inputs.encode(rng.standard_normal((kc.S, kc.n_kv, 128), dtype=np.float32), orc.F16)
+        vnew = inputs.encode(rng.standard_normal((kc.S, kc.n_kv, 128), dtype=np.float32), orc.F16)
+        out = torch.full_like(qd, float("nan"))
+        tla.kivi_rope_decode_step(desc, out, qd, dev(knew, orc.F16), dev(vnew, orc.F16), dev(pos), cos_d, sin_d,
+                                  style, dev(slots), pages, ptd, kd, vd, btd, dev(lens), max_ctx, ws)
+        torch.cuda.synchronize()
+        q_rot, k_rot = _oracle_rotate(q_base, knew, vnew, pos, cos_t, sin_t, style)
+        orc.reshape_and_cache(k_rot, vnew, k_host, v_host, slots)
+        kc.q, kc.k, kc.v, kc.lens = q_rot, k_host, v_host, lens
+        want_pages = kc.oracle_pages()
+        assert_close(out, _kivi_ref(kc, want_pages), orc.F16, ATOL_KIVI, f"step {step}")
+    assert np.array_equal(host_bits(kd), k_host) and np.array_equal(host_bits(vd), v_host)
+    used = [p for p in _used_pages(kc, lens) if p >= 0]
+    assert np.array_equal(pages.cpu().numpy()[used], want_pages[used])
+
+
 def test_kivi_decode_residual_zero_and_nan_slots():
     """R = 0 (every whole page quantised) and NaN in unused fp16 slots."""
     kc = KiviCase(55, [96, 100, 33], R=0)

@@ -687,6 +687,75 @@ int tl_kivi_decode_step(const tl_kivi_desc* desc, void* out, const void* q, cons
                           max_context_len, workspace, workspace_bytes, stream, &a);
 }
 
+// The rope step's workspace: the step's split-K partials, then the rotated
+// q [S, H, 128] and keys [S, n_kv, 128] (fp16), each 256-byte aligned.
+static size_t align256(size_t n) { return (n + 255) / 256 * 256; }
+static size_t kivi_rope_q_offset(const tl_kivi_desc* d, int32_t max_ctx) {
+  return align256(tl_kivi_workspace_bytes(d, max_ctx));
+}
+
+size_t tl_kivi_rope_step_workspace_bytes(const tl_kivi_desc* desc, int32_t max_context_len) {
+  if (check_kivi(desc) != TL_OK || max_context_len < 0) return 0;
+  const size_t qb = (size_t)desc->num_seqs * desc->num_heads * desc->head_size * 2;
+  const size_t kb = (size_t)desc->num_seqs * desc->num_kv_heads * desc->head_size * 2;
+  return kivi_rope_q_offset(desc, max_context_len) + align256(qb) + kb;
+}
+
+int tl_kivi_rope_decode_step(const tl_kivi_desc* desc, void* out, const void* q, const void* key,
+                             const void* value, const int32_t* positions, const float* cos_table,
+                             const float* sin_table, int32_t max_positions, int32_t style,
+                             const int32_t* slot_mapping, void* pages, const int32_t* page_tables,
+                             void* k_cache, void* v_cache, const int32_t* block_tables,
+                             const int32_t* seq_lens, int32_t max_context_len, void* workspace,
+                             size_t workspace_bytes, void* stream) {
+  int rc = check_kivi(desc);
+  if (rc) return rc;
+  if (max_context_len < 0) return fail(TL_ERR_INVALID_ARGUMENT, "max_context_len < 0");
+  if (max_positions <= 0) return fail(TL_ERR_INVALID_ARGUMENT, "max_positions=%d", max_positions);
+  if (style != TL_ROPE_ADJACENT && style != TL_ROPE_HALVES) return fail(TL_ERR_INVALID_ARGUMENT, "style=%d", style);
+  if (desc->num_seqs == 0) return ok();
+  if (!q || !key || !value || !positions || !cos_table || !sin_table)
+    return fail(TL_ERR_INVALID_ARGUMENT, "NULL pointer");
+  const size_t need = tl_kivi_rope_step_workspace_bytes(desc, max_context_len);
+  if (!workspace || workspace_bytes < need)
+    return fail(TL_ERR_INVALID_ARGUMENT, "workspace of %zu bytes needed, %zu given", need, workspace_bytes);
+  if (!aligned16(workspace)) return fail(TL_ERR_INVALID_ARGUMENT, "workspace must be 16-byte aligned");
+  const size_t qoff = kivi_rope_q_offset(desc, max_context_len);
+  char* q_rot = (char*)workspace + qoff;
+  char* k_rot = q_rot + align256((size_t)desc->num_seqs * desc->num_heads * desc->head_size * 2);
+  tl::RopeCache r;
+  memset(&r, 0, sizeof r);
+  r.q = q; r.q_out = q_rot; r.key = key; r.k_out = k_rot;
+  r.positions = positions; r.cos_table = cos_table; r.sin_table = sin_table;
+  r.num_tokens = desc->num_seqs; r.num_heads = desc->num_heads; r.num_kv_heads = desc->num_kv_heads;
+  r.head_size = desc->head_size; r.block_size = desc->block_size; r.num_blocks = desc->num_blocks;
+  r.max_positions = max_positions; r.dtype = TL_DTYPE_F16; r.style = style;
+  if (tl::launch_rope_rows(r, (hipStream_t)stream)) return fail(TL_ERR_BACKEND, "rope launch failed");
+  return tl_kivi_decode_step(desc, out, q_rot, k_rot, value, slot_mapping, pages, page_tables, k_cache, v_cache,
+                             block_tables, seq_lens, max_context_len, workspace, qoff, stream);
+}
+
+int tl_kivi_apply_config(tl_kivi_desc* desc, int32_t bits, int32_t residual_length,
+                         const char* key_granularity, const char* value_granularity,
+                         int32_t pre_rope_keys) {
+  if (!desc) return fail(TL_ERR_INVALID_ARGUMENT, "desc is NULL");
+  if (bits != 4 && bits != 8) return fail(TL_ERR_INVALID_ARGUMENT, "bits=%d (KiviConfig: 4 or 8)", bits);
+  if (residual_length < 0) return fail(TL_ERR_INVALID_ARGUMENT, "residual_length=%d", residual_length);
+  if (!key_granularity || strcmp(key_granularity, "per_channel") != 0)
+    return fail(TL_ERR_NOT_IMPLEMENTED, "key_granularity '%s' (built: per_channel)",
+                key_granularity ? key_granularity : "(null)");
+  if (!value_granularity || strcmp(value_granularity, "per_token") != 0)
+    return fail(TL_ERR_NOT_IMPLEMENTED, "value_granularity '%s' (built: per_token)",
+                value_granularity ? value_granularity : "(null)");
+  if (pre_rope_keys)
+    return fail(TL_ERR_NOT_IMPLEMENTED,
+                "pre_rope_keys: keys quantised before RoPE are not built (keys are stored and quantised as "
+                "given; tl_kivi_rope_decode_step rotates them first)");
+  desc->bits = bits;
+  desc->residual_length = residual_length;
+  return ok();
+}
+
 static int kivi_decode_impl(const tl_kivi_desc* desc, void* out, const void* q, const void* pages,
                             const int32_t* page_tables, const void* k_cache, const void* v_cache,
                             const int32_t* block_tables, const int32_t* seq_lens, int32_t max_context_len,

@@ -247,14 +247,18 @@ template <Kind K, int STYLE>
 __global__ __launch_bounds__(256) void rope_cache_kernel(RopeCache a) {
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int half = a.head_size / 2, units = half / 8;           // 8 pairs per thread
-  const int rows = a.num_heads + (a.q_only ? 0 : 2 * a.num_kv_heads);   // q heads, k heads, v heads
+  // q heads, k heads, v heads (with k_out: q and k heads, written as rows)
+  const int rows = a.num_heads + (a.q_only ? 0 : (a.k_out ? 1 : 2) * a.num_kv_heads);
   const int64_t total = (int64_t)a.num_tokens * rows * units;
   if (idx >= total) return;
   const int u = (int)(idx % units);
   const int row = (int)((idx / units) % rows);
   const int t = (int)(idx / ((int64_t)units * rows));
   const int pos = a.positions[t];
-  if (pos < 0 || pos >= a.max_positions) return;               // token left as it is
+  // a position outside the tables leaves the token as it is (with k_out:
+  // copied unrotated)
+  const bool rot = pos >= 0 && pos < a.max_positions;
+  if (!rot && !a.k_out) return;
   const int i0 = 8 * u;
   float x[16];
   const void* src;
@@ -275,7 +279,7 @@ __global__ __launch_bounds__(256) void rope_cache_kernel(RopeCache a) {
     x[2 * p + 1] = load_scalar<K>(src, base + rope_dim<STYLE>(i0 + p, 1, half));
   }
   const bool is_v = row >= a.num_heads + a.num_kv_heads;
-  if (!is_v) {
+  if (!is_v && rot) {
     const float* cs = a.cos_table + (int64_t)pos * half + i0;
     const float* sn = a.sin_table + (int64_t)pos * half + i0;
 #pragma unroll
@@ -285,11 +289,12 @@ __global__ __launch_bounds__(256) void rope_cache_kernel(RopeCache a) {
       x[2 * p + 1] = __builtin_fmaf(x0, sv, x1 * c);
     }
   }
-  if (row < a.num_heads) {
+  if (row < a.num_heads || a.k_out) {
+    void* dst = row < a.num_heads ? a.q_out : a.k_out;
 #pragma unroll
     for (int p = 0; p < 8; ++p) {
-      store_scalar<K>(a.q_out, base + rope_dim<STYLE>(i0 + p, 0, half), x[2 * p]);
-      store_scalar<K>(a.q_out, base + rope_dim<STYLE>(i0 + p, 1, half), x[2 * p + 1]);
+      store_scalar<K>(dst, base + rope_dim<STYLE>(i0 + p, 0, half), x[2 * p]);
+      store_scalar<K>(dst, base + rope_dim<STYLE>(i0 + p, 1, half), x[2 * p + 1]);
     }
     return;
   }
@@ -512,6 +517,23 @@ int launch_rope_cache(const RopeCache& a_in, hipStream_t stream) {
   else if (k == Kind::F32) { if (a.style) TL_ROPE_LAUNCH(Kind::F32, 1); else TL_ROPE_LAUNCH(Kind::F32, 0); }
   else return 3;
 #undef TL_ROPE_LAUNCH
+  return hipGetLastError() == hipSuccess ? 0 : 5;
+}
+
+int launch_rope_rows(const RopeCache& a_in, hipStream_t stream) {
+  if (a_in.num_tokens == 0) return 0;
+  RopeCache a = a_in;
+  a.q_only = 0;
+  if (!a.k_out) return 3;
+  const int64_t total = (int64_t)a.num_tokens * (a.num_heads + a.num_kv_heads) * (a.head_size / 16);
+  const dim3 grid((unsigned)((total + 255) / 256));
+#define TL_ROPE_ROWS(K, S) hipLaunchKernelGGL((rope_cache_kernel<K, S>), grid, dim3(256), 0, stream, a)
+  const Kind k = (Kind)a.dtype;
+  if (k == Kind::F16) { if (a.style) TL_ROPE_ROWS(Kind::F16, 1); else TL_ROPE_ROWS(Kind::F16, 0); }
+  else if (k == Kind::BF16) { if (a.style) TL_ROPE_ROWS(Kind::BF16, 1); else TL_ROPE_ROWS(Kind::BF16, 0); }
+  else if (k == Kind::F32) { if (a.style) TL_ROPE_ROWS(Kind::F32, 1); else TL_ROPE_ROWS(Kind::F32, 0); }
+  else return 3;
+#undef TL_ROPE_ROWS
   return hipGetLastError() == hipSuccess ? 0 : 5;
 }
 

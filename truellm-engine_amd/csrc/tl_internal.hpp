@@ -78,8 +78,11 @@ struct RopeCache {
   int num_tokens, num_heads, num_kv_heads, head_size, block_size, num_blocks, max_positions;
   int dtype, style;             // style 0: pairs (2i, 2i+1); 1: (i, i + d/2)
   int q_only;                   // set by the launcher: k and v go through the row kernel
+  void* k_out;                  // launch_rope_rows: rotated keys [T, n_kv, d] (no pool writes)
 };
 int launch_rope_cache(const RopeCache& a, hipStream_t stream);
+// RoPE of q (into q_out) and of the keys (into k_out), nothing else written.
+int launch_rope_rows(const RopeCache& a, hipStream_t stream);
 
 // Norms and gated activations (residual == nullptr: plain RMSNorm).
 int launch_rms_norm(void* out, void* residual, const void* x, const void* w, int rows, int hidden, float eps,

@@ -146,6 +146,10 @@ _SIG = {
     "tl_kivi_pass_runs": (_I, [_I, _I, _I, _I, _I, ctypes.c_size_t]),
     "tl_chunked_prefill": (ctypes.c_int, [ctypes.POINTER(PrefillDesc), _P, _P, _P, _P, _P, _P, _P, _I, _I, _P]),
     "tl_kivi_paged_attention_decode": (ctypes.c_int, [ctypes.POINTER(KiviDesc), _P, _P, _P, _P, _P, _P, _P, _P, _I, _P, ctypes.c_size_t, _P]),
+    "tl_kivi_rope_step_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(KiviDesc), _I]),
+    "tl_kivi_rope_decode_step": (ctypes.c_int, [ctypes.POINTER(KiviDesc)] + [_P] * 7 + [_I, _I] + [_P] * 7
+                                 + [_I, _P, ctypes.c_size_t, _P]),
+    "tl_kivi_apply_config": (ctypes.c_int, [ctypes.POINTER(KiviDesc), _I, _I, ctypes.c_char_p, ctypes.c_char_p, _I]),
 }
 
 
@@ -488,6 +492,31 @@ def kivi_decode_step(desc, out, q, key, value, slot_mapping, pages, page_tables,
         ctypes.byref(desc), _ptr(out), _ptr(q), _ptr(key), _ptr(value), _ptr(slot_mapping), _ptr(pages),
         _ptr(page_tables), _ptr(k_cache), _ptr(v_cache), _ptr(block_tables), _ptr(seq_lens), max_context_len,
         _ptr(workspace), ws_bytes, _stream(stream)))
+
+
+def kivi_rope_step_workspace_bytes(desc, max_context_len) -> int:
+    return lib.tl_kivi_rope_step_workspace_bytes(ctypes.byref(desc), max_context_len)
+
+
+def kivi_rope_decode_step(desc, out, q, key, value, positions, cos_table, sin_table, style, slot_mapping, pages,
+                          page_tables, k_cache, v_cache, block_tables, seq_lens, max_context_len, workspace,
+                          stream=None):
+    """RoPE of q and the new keys at positions[s], then kivi_decode_step on the rotated rows (keys are
+    stored and quantised rotated)."""
+    ws_bytes = workspace.numel() * workspace.element_size()
+    check(lib.tl_kivi_rope_decode_step(
+        ctypes.byref(desc), _ptr(out), _ptr(q), _ptr(key), _ptr(value), _ptr(positions), _ptr(cos_table),
+        _ptr(sin_table), cos_table.shape[0], style, _ptr(slot_mapping), _ptr(pages), _ptr(page_tables),
+        _ptr(k_cache), _ptr(v_cache), _ptr(block_tables), _ptr(seq_lens), max_context_len, _ptr(workspace),
+        ws_bytes, _stream(stream)))
+
+
+def kivi_apply_config(desc, bits=8, residual_length=128, key_granularity="per_channel",
+                      value_granularity="per_token", pre_rope_keys=False):
+    """KiviConfig onto a descriptor (raises TLError for what is not built)."""
+    kg = None if key_granularity is None else key_granularity.encode()
+    vg = None if value_granularity is None else value_granularity.encode()
+    check(lib.tl_kivi_apply_config(ctypes.byref(desc), bits, residual_length, kg, vg, int(bool(pre_rope_keys))))
 
 
 def kivi_paged_attention_decode(desc, out, q, pages, page_tables, k_cache, v_cache, block_tables,
