@@ -8,9 +8,10 @@
 // Prefill work item: one workgroup per (sequence, kv head, tile of NW * 32
 // rows), a row being one (query, q head of the GQA group) pair, so every K/V
 // block fetched serves all q heads of the group.  Per 64-key iteration:
-//   * the workgroup copies the keys' K (transposed to [key][channel], rows
-//     padded to 136 halves) and V ([channel][key slot], the key order of the
-//     PV operand, rows padded to 72 halves) into LDS (two stages of each);
+//   * the workgroup copies the keys' K ([channel][key] as in the pool, rows
+//     padded to 80 halves; the q.k operand is read with the LDS transpose
+//     read) and V ([channel][key slot], the key order of the PV operand,
+//     rows padded to 72 halves) into LDS (two stages of each);
 //     each wavefront copies the 16 keys of one pool block for 64 channels,
 //     with loads that each read 1 KB contiguous in the pool;
 //   * each wavefront (32 rows) forms two 32-key tiles of S^T = K Q^T with
@@ -56,7 +57,7 @@ constexpr int kPfHead = 128;
 constexpr int kPfRows = 32;          // rows per wavefront
 constexpr int kPfKeys = 64;          // keys per iteration
 constexpr int KT = kPfKeys / 32;     // 32-key S tiles per iteration
-constexpr int kKtStride = 136;       // halves per key row of the transposed K stage
+constexpr int kKtStride = 80;        // halves per channel row of the K stage (64 keys + pad)
 constexpr int kVStride = 72;         // halves per channel row of the V stage (64 keys + pad)
 
 // Slot of key k (of an iteration's 64) in a V stage row: the middle two
@@ -116,7 +117,7 @@ struct PrefillParams {
 template <int NW, int BS>
 struct PrefillSmem {
   struct {
-    uint16_t kt[kStages][kPfKeys * kKtStride];    // [key][channel] (+8 pad)
+    uint16_t kt[kStages][kPfHead * kKtStride];    // [channel][key] (+16 pad)
     uint16_t v[kStages][kPfHead * kVStride];      // [channel][v_slot(key)] (+8 pad)
     float row[NW][kPfRows];                       // per-row exchange (alpha, l)
   } pf;
@@ -136,6 +137,26 @@ __device__ __forceinline__ int table_entry(const Params& p, TableRow table, int 
 }
 __device__ __forceinline__ int checked_block(const Params& p, int lb, int entry) {
   return (lb >= p.max_blocks_per_seq || entry < 0 || entry >= p.num_blocks) ? -1 : entry;
+}
+
+// The A operand of q.k step ks of S^T tile t (keys 32 t .. + 31, channels
+// 16 ks .. + 15) from the K stage [channel][key]: lane l needs channels
+// 16 ks + 8 (l >> 5) .. + 7 of key 32 t + (l & 31).  ds_read_b64_tr_b16
+// hands lane j of a 16-lane group element e = element j % 4 of the 8 bytes
+// that lane 4 e + j / 4 of the group addressed; so lane i addresses
+// channel c0 + i / 4, keys k0 + 4 (i % 4) .. + 3, and lane j receives
+// channels c0 .. c0 + 3 of key k0 + j.  Two reads give the 8 channels.  With
+// 160-byte rows the 4 channel rows of a group fall on disjoint banks.
+__device__ __forceinline__ u32x4 k_operand(const uint16_t* kst, int t, int ks, int lane) {
+  typedef short v4s __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) v4s* LdsV4;
+  const int i = lane & 15;
+  const int k0 = 32 * t + 16 * ((lane >> 4) & 1), c0 = 16 * ks + 8 * (lane >> 5);
+  const uint16_t* a = kst + (c0 + (i >> 2)) * kKtStride + k0 + 4 * (i & 3);
+  const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((LdsV4)(a));
+  const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((LdsV4)(a + 4 * kKtStride));
+  const uint2 l2 = __builtin_bit_cast(uint2, lo), h2 = __builtin_bit_cast(uint2, hi);
+  return u32x4{l2.x, l2.y, h2.x, h2.y};
 }
 
 template <Kind KV, int BS, int NW>
@@ -243,13 +264,9 @@ __global__ __launch_bounds__(NW * kWave) void prefill_kernel(PrefillParams pp) {
   auto stage = [&](int it_k, int it_v, const Fetched& f) {
 #pragma unroll
     for (int u = 0; u < kUnits; ++u) {
-      uint16_t* kt = &sm.pf.kt[it_k & 1][tok * kKtStride + unit_ch(u)];
-      const u4v kv = __builtin_bit_cast(u4v, f.k[u]);
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        kt[(2 * w) * kKtStride] = (uint16_t)(kv[w] & 0xFFFFu);
-        kt[(2 * w + 1) * kKtStride] = (uint16_t)(kv[w] >> 16);
-      }
+      // K as it lies in the pool: the lane's 8 keys of its channel, one
+      // 16-byte write (k_operand reads it transposed)
+      *reinterpret_cast<u32x4*>(&sm.pf.kt[it_k & 1][unit_ch(u) * kKtStride + tok]) = f.k[u];
       // V slots at or past the sequence end may hold anything (NaN codes
       // too, and a zero weight times NaN is NaN): zero them
       u4v v = __builtin_bit_cast(u4v, f.v[u]);
@@ -302,11 +319,9 @@ __global__ __launch_bounds__(NW * kWave) void prefill_kernel(PrefillParams pp) {
     const uint16_t* kst = sm.pf.kt[it & 1];
 #pragma unroll
     for (int t = 0; t < KT; ++t) {
-      const uint16_t* ktw = kst + (32 * t + c32) * kKtStride + 8 * g;
       f16v acc = f16v{};
 #pragma unroll
-      for (int ks = 0; ks < 8; ++ks)
-        acc = M::mma(*reinterpret_cast<const u32x4*>(ktw + 16 * ks), qb[ks], acc);
+      for (int ks = 0; ks < 8; ++ks) acc = M::mma(k_operand(kst, t, ks, lane), qb[ks], acc);
       sp[t] = acc;
     }
   };
@@ -472,9 +487,7 @@ __global__ __launch_bounds__(NW * kWave) void prefill_kernel(PrefillParams pp) {
       const int t = grp4 >> 1, s2 = grp4 & 1;
       return *reinterpret_cast<const u32x4*>(vst + (32 * c + c32) * kVStride + 32 * t + 16 * s2 + 8 * g);
     };
-    auto k_op = [&](int t, int ks) {
-      return *reinterpret_cast<const u32x4*>(kst + (32 * t + c32) * kKtStride + 8 * g + 16 * ks);
-    };
+    auto k_op = [&](int t, int ks) { return k_operand(kst, t, ks, lane); };
     u32x4 vb[2][4];
 #pragma unroll
     for (int c = 0; c < 4; ++c) vb[0][c] = v_op(0, c);
