@@ -69,6 +69,22 @@ def test_mixed_batch_matches_oracle(code, gqa):
     assert_close(pc.run(gqa), pc.ref(gqa), code, ATOL, "mixed")
 
 
+@pytest.mark.parametrize("scale_exp", [20, -12])
+def test_bf16_values_near_the_f16_stage_range(scale_exp):
+    """P V runs on f16, a bf16 V staged as 2^-7 v: V scaled by 2^20 (|v| up
+    to about 5 * 2^20, below the 2^23 limit) and by 2^-12 (below 2^-7, where
+    the f16 stage is subnormal) against the oracle.  The tolerance is the
+    usual one scaled with V where V is scaled up (the same relative bound:
+    2e-3 of the values' scale, plus half an output ulp), and the usual one
+    where V is scaled down."""
+    pc = PrefillCase(inputs.SEEDS[4] + scale_exp, MIXED, 16, 4, orc.BF16)
+    v = orc.bits_to_f32(pc.case.v_cache, orc.BF16) * np.float32(2.0 ** scale_exp)
+    pc.case.v_cache = inputs.encode(v, orc.BF16)
+    print(f"case bf16 V scaled by 2^{scale_exp}", flush=True)
+    atol = ATOL * 2.0 ** max(scale_exp, 0)
+    assert_close(pc.run(), pc.ref(), orc.BF16, atol, f"V x 2^{scale_exp}")
+
+
 @pytest.mark.parametrize("H,n_kv", [(16, 2), (4, 4), (12, 4)])
 def test_group_sizes(H, n_kv):
     pc = PrefillCase(inputs.SEEDS[4] + 1, [(70, 200), (1, 333), (40, 40)], H, n_kv, orc.BF16)

@@ -74,11 +74,25 @@ constexpr float kLazyRescale = 8.f;  // log2 units
 // schedule of prefill_kernel writes each stage between its readers)
 constexpr int kStages = 2;
 
+// P V runs on f16 for both input types: the weights in f16 (11 mantissa
+// bits; bf16's 8 would miss 2e-3 by up to 2^-9 max|v| on a short or peaked
+// row).  A bf16 V is converted to f16 as it is staged, scaled by 2^-7 so
+// that f16's range holds |v| < 2^23 (an f16 value 2^-7 v is exact down to
+// |v| = 2^-7, and below that off by at most 2^-17); the weights carry the
+// 2^7 instead (they stay below 2^8 by the lazy rescale, so below 2^15 in
+// f16), and the row sums are divided by it at the end.  |v| >= 2^23 in a
+// bf16 V overflows the f16 stage and the output is not finite.
+template <Kind KV> struct PvScale {
+  static constexpr float kV = 1.f, kP = 1.f;
+  static constexpr int kPExp = 0;
+};
+template <> struct PvScale<Kind::BF16> {
+  static constexpr float kV = 0.0078125f, kP = 128.f;
+  static constexpr int kPExp = 7;
+};
+
 template <Kind KV> struct Mfma32;
-// bf16 keeps 8 mantissa bits: the weights go to the PV product as two bf16
-// terms (hi = bf16(p), lo = bf16(p - hi)), fp16 weights (11 bits) as one.
 template <> struct Mfma32<Kind::BF16> {
-  static constexpr bool kSplitP = true;
   typedef __bf16 v8 __attribute__((ext_vector_type(8)));
   typedef __bf16 v2 __attribute__((ext_vector_type(2)));
   __device__ __forceinline__ static float hi(float x) { return (float)(__bf16)x; }
@@ -92,7 +106,6 @@ template <> struct Mfma32<Kind::BF16> {
   }
 };
 template <> struct Mfma32<Kind::F16> {
-  static constexpr bool kSplitP = false;
   typedef _Float16 v8 __attribute__((ext_vector_type(8)));
   typedef _Float16 v2 __attribute__((ext_vector_type(2)));
   __device__ __forceinline__ static float hi(float x) { return (float)(_Float16)x; }
@@ -164,7 +177,8 @@ __global__ __launch_bounds__(NW * kWave) void prefill_kernel(PrefillParams pp) {
   static_assert(BS == 16 || BS == 32, "block size");
   static_assert(NW == 8, "two groups of four wavefronts, one wavefront of each group per SIMD");
   constexpr int BPI = kPfKeys / BS;                    // pool blocks per iteration
-  using M = Mfma32<KV>;
+  using M = Mfma32<KV>;                                // q.k
+  using MP = Mfma32<Kind::F16>;                        // p.v (f16 for both types)
   __shared__ __attribute__((aligned(16))) PrefillSmem<NW, BS> sm;
 
   const Params& p = pp.base;
@@ -275,6 +289,15 @@ __global__ __launch_bounds__(NW * kWave) void prefill_kernel(PrefillParams pp) {
 #pragma unroll
         for (int w = 0; w < 4; ++w) v[w] = 2 * w >= nv ? 0u : (2 * w + 1 >= nv ? v[w] & 0xFFFFu : v[w]);
       }
+      if constexpr (KV == Kind::BF16) {
+        // bf16 -> f16, times 2^-7 (see PvScale)
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          const unsigned x = (unsigned)v[w];
+          v[w] = MP::pack(__builtin_bit_cast(float, x << 16) * PvScale<KV>::kV,
+                          __builtin_bit_cast(float, x & 0xFFFF0000u) * PvScale<KV>::kV);
+        }
+      }
       uint16_t* vrow = &sm.pf.v[it_v & 1][unit_ch(u) * kVStride];
       *reinterpret_cast<uint2*>(vrow + v_slot(tok)) = uint2{v[0], v[1]};
       *reinterpret_cast<uint2*>(vrow + v_slot(tok + 4)) = uint2{v[2], v[3]};
@@ -300,15 +323,14 @@ __global__ __launch_bounds__(NW * kWave) void prefill_kernel(PrefillParams pp) {
   float m_used = -INFINITY, l_part = 0.f;
   float* s_row = &sm.pf.row[wave][0];
   // Scores and weights of an iteration share registers: QK leaves the S^T
-  // tiles in sp (MFMA phase), SM turns tile t into its packed weights in
-  // place (VALU phase: words 8 s .. 8 s + 3 hold hi of step s, 8 s + 4 ..
-  // the lo terms), and PV of the next MFMA phase reads them before QK
-  // overwrites them.
+  // tiles in sp (MFMA phase), SM turns tile t into its packed f16 weights
+  // in place (VALU phase: words 8 s .. 8 s + 3 hold those of step s), and PV
+  // of the next MFMA phase reads them before QK overwrites them.
   // (__builtin_bit_cast of a vector element itself, v[i], reads element 0
   // with this compiler: the elements go through a value conversion first.)
   f16v sp[KT];
-  auto p_words = [&](int t, int s2, int part) {
-    const int w = 8 * s2 + 4 * part;
+  auto p_words = [&](int t, int s2) {
+    const int w = 8 * s2;
     return u32x4{__builtin_bit_cast(unsigned, (float)sp[t][w]), __builtin_bit_cast(unsigned, (float)sp[t][w + 1]),
                  __builtin_bit_cast(unsigned, (float)sp[t][w + 2]), __builtin_bit_cast(unsigned, (float)sp[t][w + 3])};
   };
@@ -388,7 +410,9 @@ __global__ __launch_bounds__(NW * kWave) void prefill_kernel(PrefillParams pp) {
       }
       __builtin_amdgcn_wave_barrier();
     }
-    const float m_use = (m_used == -INFINITY) ? 0.f : m_used;
+    // the weights carry 2^kPExp (see PvScale): a factor common to every
+    // weight and row sum, so the rounding of m_use - kPExp cancels
+    const float m_use = ((m_used == -INFINITY) ? 0.f : m_used) - (float)PvScale<KV>::kPExp;
 #pragma unroll
     for (int t = 0; t < KT; ++t) {
       float pw[16], ls[4] = {0.f, 0.f, 0.f, 0.f};
@@ -401,28 +425,11 @@ __global__ __launch_bounds__(NW * kWave) void prefill_kernel(PrefillParams pp) {
 #pragma unroll
       for (int s2 = 0; s2 < 2; ++s2) {
         const int r0 = 8 * s2;
-        const u32x4 pa = {M::pack(pw[r0 + 0], pw[r0 + 1]), M::pack(pw[r0 + 2], pw[r0 + 3]),
-                          M::pack(pw[r0 + 4], pw[r0 + 5]), M::pack(pw[r0 + 6], pw[r0 + 7])};
+        const u32x4 pa = {MP::pack(pw[r0 + 0], pw[r0 + 1]), MP::pack(pw[r0 + 2], pw[r0 + 3]),
+                          MP::pack(pw[r0 + 4], pw[r0 + 5]), MP::pack(pw[r0 + 6], pw[r0 + 7])};
         const u4v pa4 = __builtin_bit_cast(u4v, pa);
-        u4v pl4 = {0u, 0u, 0u, 0u};
-        if constexpr (M::kSplitP) {
-          // bf16 keeps 8 mantissa bits: the weights go to P V as two bf16
-          // terms, hi (taken straight from the packed pair, low half first)
-          // and lo = p - hi
-          const u4v h2 = __builtin_bit_cast(u4v, pa);
-          float lo[8];
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            lo[2 * i] = pw[r0 + 2 * i] - __builtin_bit_cast(float, h2[i] << 16);
-            lo[2 * i + 1] = pw[r0 + 2 * i + 1] - __builtin_bit_cast(float, h2[i] & 0xFFFF0000u);
-          }
-          pl4 = u4v{M::pack(lo[0], lo[1]), M::pack(lo[2], lo[3]), M::pack(lo[4], lo[5]), M::pack(lo[6], lo[7])};
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          sp[t][8 * s2 + i] = __builtin_bit_cast(float, (unsigned)pa4[i]);
-          sp[t][8 * s2 + 4 + i] = __builtin_bit_cast(float, (unsigned)pl4[i]);
-        }
+        for (int i = 0; i < 4; ++i) sp[t][8 * s2 + i] = __builtin_bit_cast(float, (unsigned)pa4[i]);
       }
     }
   };
@@ -501,11 +508,7 @@ __global__ __launch_bounds__(NW * kWave) void prefill_kernel(PrefillParams pp) {
       }
       const int t = q >> 1, s2 = q & 1;
 #pragma unroll
-      for (int c = 0; c < 4; ++c) o[c] = M::mma(p_words(t, s2, 0), vb[q & 1][c], o[c]);
-      if constexpr (M::kSplitP) {
-#pragma unroll
-        for (int c = 0; c < 4; ++c) o[c] = M::mma(p_words(t, s2, 1), vb[q & 1][c], o[c]);
-      }
+      for (int c = 0; c < 4; ++c) o[c] = MP::mma(p_words(t, s2), vb[q & 1][c], o[c]);
     }
     constexpr int kQkAhead = 3;
     u32x4 kb[kQkAhead + 1][KT];
@@ -591,7 +594,7 @@ __global__ __launch_bounds__(NW * kWave) void prefill_kernel(PrefillParams pp) {
       const int rl = 8 * j + 4 * g + i, row = wrow0 + rl;
       if (row >= rows) continue;
       const float l = s_row[rl];
-      const float inv = l > 0.f ? 1.f / l : 0.f;
+      const float inv = l > 0.f ? PvScale<KV>::kP / l : 0.f;   // the sums carry 2^kPExp
       const int qr = row / p.group, gr = row % p.group;
       const int64_t base = ((int64_t)(q0 + qr) * p.num_heads + head_of(p, kvh, gr)) * kPfHead;
 #pragma unroll
