@@ -412,6 +412,47 @@ def test_kivi_rope_step_matches_oracle_each_step(style, bits):
     assert np.array_equal(pages.cpu().numpy()[used], want_pages[used])
 
 
+def test_kivi_step_full_batch_mixed_lengths():
+    """The benchmark's KIVI step at full size: batch 64, 32/8 heads,
+    sequence s at 4096 + s mod 32 tokens, R = 128, one fused step (sequences
+    31 and 63 complete a page in it).  The pages of every sequence are the
+    oracle's bit for bit; the outputs of 16 sequences, those two included,
+    match the oracle."""
+    start = np.array([4096 + s % 32 for s in range(64)], np.int32)
+    kc = KiviCase(81, start + 1, H=32, extra_blocks=1)
+    qd, kd, vd = dev(kc.q, orc.F16), dev(kc.k, orc.F16), dev(kc.v, orc.F16)
+    btd, ptd = dev(kc.tables), dev(kc.page_tables)
+    pages = torch.zeros(kc.num_pages, kc.n_kv, kc.page_bytes, dtype=torch.uint8, device="cuda")
+    desc = kc.desc(qd, kd, btd, ptd, 0)
+    tla.kivi_build_pages(desc, kd, vd, btd, dev(start), ptd, pages, int(start.max()))
+    rng = np.random.default_rng(14)
+    lens = start + 1
+    pos = start
+    slots = (kc.tables[np.arange(kc.S), pos // 16] * 16 + pos % 16).astype(np.int32)
+    knew = inputs.encode(rng.standard_normal((kc.S, kc.n_kv, 128), dtype=np.float32), orc.F16)
+    vnew = inputs.encode(rng.standard_normal((kc.S, kc.n_kv, 128), dtype=np.float32), orc.F16)
+    max_ctx = int(lens.max())
+    ws = torch.empty(max(16, tla.kivi_workspace_bytes(desc, max_ctx)), dtype=torch.uint8, device="cuda")
+    out = torch.full_like(qd, float("nan"))
+    print("case kivi step full batch, mixed lengths", flush=True)
+    tla.kivi_decode_step(desc, out, qd, dev(knew, orc.F16), dev(vnew, orc.F16), dev(slots), pages, ptd, kd, vd, btd,
+                         dev(lens), max_ctx, ws)
+    torch.cuda.synchronize()
+    orc.reshape_and_cache(knew, vnew, kc.k, kc.v, slots)
+    kc.lens = lens
+    want_pages = kc.oracle_pages()
+    used = [p for p in _used_pages(kc, lens) if p >= 0]
+    assert np.array_equal(pages.cpu().numpy()[used], want_pages[used])
+    assert np.array_equal(host_bits(kd), kc.k) and np.array_equal(host_bits(vd), kc.v)
+    sub = np.array([0, 1, 5, 9, 15, 16, 22, 30, 31, 32, 40, 47, 50, 58, 62, 63])
+    want = orc.kivi_paged_attention(np.ascontiguousarray(kc.q[sub]), orc.F16, want_pages,
+                                    np.ascontiguousarray(kc.page_tables[sub]), kc.k, kc.v,
+                                    np.ascontiguousarray(kc.tables[sub]), np.ascontiguousarray(lens[sub]),
+                                    kc.n_kv, kc.R, kc.scale, orc.GROUPED, kc.bits)
+    assert_close(out[torch.from_numpy(sub).cuda()], want, orc.F16, ATOL_KIVI, "full batch")
+    assert torch.isfinite(out).all()
+
+
 def test_kivi_decode_residual_zero_and_nan_slots():
     """R = 0 (every whole page quantised) and NaN in unused fp16 slots."""
     kc = KiviCase(55, [96, 100, 33], R=0)

@@ -183,6 +183,40 @@ def test_config5_shape_spot_checks():
         assert_close(g, ref, orc.BF16, ATOL, f"seq {s}")
 
 
+def test_bench_chunk_full_size():
+    """The benchmark's launch at full size: 8 prompts' last 512-token chunk
+    at ctx 2048 plus 32 decode rows at ctx 2048, 64/8 heads, bf16, one call.
+    Every decode row, and rows spread over each chunk (first, last, both
+    sides of the 256-row tile edge, and others), against the oracle."""
+    shape = [(512, 2048)] * 8 + [(1, 2048)] * 32
+    pc = PrefillCase(inputs.SEEDS[4] + 9, shape, 64, 8, orc.BF16)
+    c = pc.case
+    q = dev(pc.q, orc.BF16)
+    k, v, bt, sl, cu = dev(c.k_cache, orc.BF16), dev(c.v_cache, orc.BF16), dev(c.tables), dev(pc.lens), dev(pc.cu)
+    out = torch.full_like(q, float("nan"))
+    desc = tla.make_prefill_desc(q, k, bt, pc.S, 8, c.scale, num_prefill_seqs=8)
+    print("case prefill bench chunk, full size", flush=True)
+    tla.chunked_prefill(desc, out, q, cu, k, v, bt, sl, 512)
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy()
+    # decode rows: one oracle call over the 32 of them
+    d0 = int(pc.cu[8])
+    ref = orc.chunked_prefill(np.ascontiguousarray(pc.q[d0:]), orc.BF16, np.arange(33, dtype=np.int32),
+                              c.k_cache, c.v_cache, orc.BF16, np.ascontiguousarray(c.tables[8:]),
+                              np.full(32, 2048, np.int32), 8, c.scale)
+    assert_close(torch.from_numpy(got[d0:]).to(torch.bfloat16), ref, orc.BF16, ATOL, "decode rows")
+    # prefill rows: each as a one-row call at its own position
+    for s in range(8):
+        for i in (0, 1, 31, 32, 37, 100, 255, 256, 300, 447, 510, 511):
+            row = int(pc.cu[s]) + i
+            pos = 2048 - 512 + i
+            ref = orc.chunked_prefill(np.ascontiguousarray(pc.q[row:row + 1]), orc.BF16, np.array([0, 1], np.int32),
+                                      c.k_cache, c.v_cache, orc.BF16, np.ascontiguousarray(c.tables[s:s + 1]),
+                                      np.array([pos + 1], np.int32), 8, c.scale)
+            assert_close(torch.from_numpy(got[row:row + 1]).to(torch.bfloat16), ref, orc.BF16, ATOL,
+                         f"seq {s} row {i}")
+
+
 def test_empty_and_invalid_arguments():
     q = torch.zeros(4, 8, 128, dtype=torch.bfloat16, device="cuda")
     k = torch.zeros(4, 2, 128, 16, dtype=torch.bfloat16, device="cuda")
