@@ -391,7 +391,6 @@ __global__ __launch_bounds__(64) void rope_rows_kernel(RopeCache a) {
   }
   const int cpc = a.block_size / PER;                  // chunks per channel
   const int chunks = a.head_size * cpc;
-#pragma unroll 4
   for (int j = lane; j < chunks; j += kWave) {
     u32x4 kc = load16(kr + (int64_t)j * 16), vc = load16(vr + (int64_t)j * 16);
     const int c = j / cpc, e = off - (j % cpc) * PER;
