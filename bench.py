@@ -271,11 +271,12 @@ def kivi_steps(steps):
     return max(64, (steps + 63) // 64 * 64)
 
 
-def bench_kivi(args, R=128, mixed=False, name=None, bits=4):
+def bench_kivi(args, R=128, mixed=False, name=None, bits=4, pre_rope=False):
     """KIVI append + decode steps (INT4 pages, or INT8 with bits=8) at batch
     64 from context 4096 (mixed: sequence s starts at 4096 + s mod 32 tokens,
     so two sequences complete a page at every step instead of all 64 on one
-    step in 32)."""
+    step in 32).  pre_rope: keys held before RoPE, each rotated at its
+    position inside attention (fp32 tables of 8192 positions)."""
     import torch
 
     import tl_attn as tla
@@ -331,14 +332,22 @@ def bench_kivi(args, R=128, mixed=False, name=None, bits=4):
         d = tla.make_kivi_desc(q, rep[0], rep[2], rep[3], rep[5], NKV, scale, residual_length=R, bits=bits)
         sl0 = torch.tensor(L0, dtype=torch.int32, device="cuda")
         tla.kivi_build_pages(d, rep[0], rep[1], rep[2], sl0, rep[3], rep[4], max(L0))
-    descs = [tla.make_kivi_desc(q, rep[0], rep[2], rep[3], rep[5], NKV, scale, residual_length=R, bits=bits)
-             for rep in reps]
+    descs = [tla.make_kivi_desc(q, rep[0], rep[2], rep[3], rep[5], NKV, scale, residual_length=R, bits=bits,
+                                pre_rope_keys=pre_rope) for rep in reps]
+    if pre_rope:
+        i = torch.arange(D // 2, dtype=torch.float32)
+        theta = torch.arange(8192, dtype=torch.float32)[:, None] / torch.pow(10000.0, 2.0 * i / D)
+        cos_t, sin_t = torch.cos(theta).cuda(), torch.sin(theta).cuda()
 
     def step(i, stream):
         r, lens = plan[i]
         k, v, tables, ptables, pages, _ = reps[r]
-        tla.kivi_decode_step(descs[r], out, q, knew, vnew, slot_dev[i], pages, ptables, k, v, tables,
-                             sl_dev[i], max(lens), ws, stream)
+        if pre_rope:
+            tla.kivi_decode_step_pre_rope(descs[r], out, q, knew, vnew, slot_dev[i], pages, ptables, k, v, tables,
+                                          sl_dev[i], max(lens), cos_t, sin_t, tla.ROPE_HALVES, ws, stream)
+        else:
+            tla.kivi_decode_step(descs[r], out, q, knew, vnew, slot_dev[i], pages, ptables, k, v, tables,
+                                 sl_dev[i], max(lens), ws, stream)
 
     ms = timed(step, n_timed, args.warmup, name)
     lq = lambda x: 0 if x <= R else ((x - R) // 32) * 32
@@ -699,6 +708,7 @@ def main():
         kv = bench_kivi(args, name="kivi")
     kvm = bench_kivi(args, mixed=True, name="kivi_mixed") if want("kivi") else None
     kv8 = bench_kivi(args, name="kivi_int8", bits=8) if want("kivi") else None
+    kvr = bench_kivi(args, name="kivi_pre_rope", pre_rope=True) if want("kivi") else None
     fpa = bench_decode(args, "fp16", append=True, name="fp16_append") if want("kivi") else None
     f8 = bench_fp8(args, name="fp8") if want("fp8") else None
     f8p = bench_fp8(args, 512, name="fp8_pt512") if want("fp8") else None
@@ -806,6 +816,15 @@ def main():
             "pct_hbm_peak": round(100 * kv8["gbs"] / HBM_PEAK_GBS, 2), "bytes_per_step": int(kv8["bytes_per_step"])}
         if fp is not None:
             res["kivi_int8"]["speedup_vs_fp16_tok_s"] = round(kv8["tok_s"] / fp["tok_s"], 3)
+    if kvr is not None:
+        res["kivi_int4_pre_rope_keys"] = {
+            "workload": "as kivi_int4 with the keys held before RoPE (pages and pool unrotated), every key rotated "
+                        "at its position inside attention (halves style, fp32 tables of 8192 positions)",
+            "gbs": round(kvr["gbs"], 2), "ms_per_step": round(kvr["ms_per_step"], 5), "tok_s": round(kvr["tok_s"], 1),
+            "pct_hbm_peak": round(100 * kvr["gbs"] / HBM_PEAK_GBS, 2), "bytes_per_step": int(kvr["bytes_per_step"]),
+            "rope_table_bytes_not_counted": True}
+        if kv is not None:
+            res["kivi_int4_pre_rope_keys"]["step_time_vs_rotated_keys"] = round(kvr["ms_per_step"] / kv["ms_per_step"], 3)
     if f8 is not None:
         res["fp8_e4m3_long_context"] = {
             "workload": "decode, batch 16, ctx 32768, 32 q / 8 kv heads, d 128, FP8 E4M3 KV with per-tensor "

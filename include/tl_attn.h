@@ -354,6 +354,10 @@ typedef struct tl_kivi_desc {
   float scale;
   int32_t bits;                /* code width of the pages (KiviConfig.bits, config_schema.h:124):
                                   4 (also 0) or 8 */
+  int32_t pre_rope_keys;       /* KiviConfig.pre_rope_keys (config_schema.h:128): 0 = keys are
+                                  stored and quantised as attention scores them; 1 = keys are held
+                                  before RoPE and rotated at their positions inside attention (the
+                                  _pre_rope entry points, which take the tables) */
 } tl_kivi_desc;
 
 /* Page bytes per kv head for a code width: 5120 (INT4, also bits 0) or 9216
@@ -419,7 +423,10 @@ int tl_kivi_decode_step(const tl_kivi_desc* desc, void* out, const void* q, cons
  * tables leaves that sequence's q and key unrotated.  Two launches (the
  * rotation into the workspace, then the step); the workspace holds the
  * step's split-K partials and the rotated rows: see
- * tl_kivi_rope_step_workspace_bytes. */
+ * tl_kivi_rope_step_workspace_bytes.  With desc->pre_rope_keys = 1 only q
+ * is rotated here and the step is tl_kivi_decode_step_pre_rope on the same
+ * tables (the keys stored unrotated, rotated at token position t inside
+ * attention), so positions[s] should be seq_lens[s] - 1. */
 size_t tl_kivi_rope_step_workspace_bytes(const tl_kivi_desc* desc, int32_t max_context_len);
 int tl_kivi_rope_decode_step(const tl_kivi_desc* desc, void* out, const void* q, const void* key,
                              const void* value, const int32_t* positions, const float* cos_table,
@@ -429,16 +436,43 @@ int tl_kivi_rope_decode_step(const tl_kivi_desc* desc, void* out, const void* q,
                              const int32_t* seq_lens, int32_t max_context_len, void* workspace,
                              size_t workspace_bytes, void* stream);
 
-/* KiviConfig (config_schema.h:122-129) onto a descriptor: bits (4 or 8) and
- * residual_length go to desc->bits / desc->residual_length.  The pages hold
- * keys per channel and values per token, so key_granularity must be
- * "per_channel" and value_granularity "per_token" (the defaults); other
- * strings return TL_ERR_NOT_IMPLEMENTED.  pre_rope_keys = 0 is the order of
- * tl_kivi_rope_decode_step (and of any caller that stores rotated keys);
- * pre_rope_keys != 0 (keys quantised before RoPE, each dequantised key then
- * rotated by its position inside attention) is not built and returns
- * TL_ERR_NOT_IMPLEMENTED.  The reference parses these fields
- * (src/host/config/config.cpp:216-223) but no kernel of it reads them. */
+/* Keys held before RoPE (desc->pre_rope_keys = 1): the decode and the
+ * decode step of tl_kivi_paged_attention_decode / tl_kivi_decode_step with
+ * every key rotated at its position in the sequence (token t of a sequence
+ * at position t, style TL_ROPE_ADJACENT or TL_ROPE_HALVES, fp32 tables
+ * [max_positions, 64], 16-byte aligned; t >= max_positions unrotated) as it
+ * is scored: a page key after its dequantisation, a window key as read from
+ * the fp16 pool, the step's new key as given.  Pages, pools and the appended
+ * token hold the keys unrotated.  q is taken as given (rotated by the caller
+ * at position seq_lens[s] - 1).  The standard entry points refuse a
+ * descriptor with pre_rope_keys set, since they would score unrotated keys. */
+int tl_kivi_paged_attention_decode_pre_rope(const tl_kivi_desc* desc, void* out, const void* q,
+                                            const void* pages, const int32_t* page_tables,
+                                            const void* k_cache, const void* v_cache,
+                                            const int32_t* block_tables, const int32_t* seq_lens,
+                                            int32_t max_context_len, const float* cos_table,
+                                            const float* sin_table, int32_t max_positions, int32_t style,
+                                            void* workspace, size_t workspace_bytes, void* stream);
+int tl_kivi_decode_step_pre_rope(const tl_kivi_desc* desc, void* out, const void* q, const void* key,
+                                 const void* value, const int32_t* slot_mapping, void* pages,
+                                 const int32_t* page_tables, void* k_cache, void* v_cache,
+                                 const int32_t* block_tables, const int32_t* seq_lens,
+                                 int32_t max_context_len, const float* cos_table, const float* sin_table,
+                                 int32_t max_positions, int32_t style, void* workspace,
+                                 size_t workspace_bytes, void* stream);
+
+/* KiviConfig (config_schema.h:122-129) onto a descriptor: bits (4 or 8),
+ * residual_length and pre_rope_keys (0 or 1) go to desc->bits /
+ * desc->residual_length / desc->pre_rope_keys.  The pages hold keys per
+ * channel and values per token, so key_granularity must be "per_channel"
+ * and value_granularity "per_token" (the defaults); other strings return
+ * TL_ERR_NOT_IMPLEMENTED.  pre_rope_keys = 0 is the order of
+ * tl_kivi_rope_decode_step without the flag (and of any caller that stores
+ * rotated keys); pre_rope_keys = 1 keeps keys unrotated in pages and pools
+ * and rotates them inside attention (the _pre_rope entry points, and
+ * tl_kivi_rope_decode_step with the flag).  The reference parses these
+ * fields (src/host/config/config.cpp:216-223) but no kernel of it reads
+ * them. */
 int tl_kivi_apply_config(tl_kivi_desc* desc, int32_t bits, int32_t residual_length,
                          const char* key_granularity, const char* value_granularity,
                          int32_t pre_rope_keys);

@@ -1026,14 +1026,21 @@ void orc_kivi_paged_attention(double* out, const void* q, int q_dtype,
                                   block_size, residual_length, scale, gqa_map, 4);
 }
 
-void orc_kivi_paged_attention_bits(double* out, const void* q, int q_dtype,
-                                   const uint8_t* pages, const int32_t* page_tables,
-                                   int max_pages, int num_pages, const uint16_t* k_cache,
-                                   const uint16_t* v_cache, const int32_t* block_tables,
-                                   int max_blocks_per_seq, const int32_t* seq_lens,
-                                   int num_seqs, int num_heads, int num_kv_heads,
-                                   int block_size, int residual_length, float scale,
-                                   int gqa_map, int bits)
+/* KIVI attention; with cos_t / sin_t the keys are held before RoPE (pages
+ * and fp16 window alike) and every key is rotated by its position (the
+ * token's index in the sequence) before the scores, in double: the
+ * KiviConfig.pre_rope_keys order (config_schema.h:128), with the rotation of
+ * rope_device.cuh:24-36 / the engine's NORM rope (style 0: pairs (2i, 2i+1),
+ * 1: (i, i + d/2)).  A position at or past max_pos is left unrotated. */
+static void kivi_attention_impl(double* out, const void* q, int q_dtype,
+                                const uint8_t* pages, const int32_t* page_tables,
+                                int max_pages, int num_pages, const uint16_t* k_cache,
+                                const uint16_t* v_cache, const int32_t* block_tables,
+                                int max_blocks_per_seq, const int32_t* seq_lens,
+                                int num_seqs, int num_heads, int num_kv_heads,
+                                int block_size, int residual_length, float scale,
+                                int gqa_map, int bits, const float* cos_t, const float* sin_t,
+                                int max_pos, int style)
 {
     const size_t page_bytes = orc_kivi_page_bytes(bits);
     int max_len = 0;
@@ -1071,6 +1078,20 @@ void orc_kivi_paged_attention_bits(double* out, const void* q, int q_dtype,
                     V[(size_t)t * PG_D + e] = orc_f16_to_f32(vt[e]);
                 }
             }
+            if (cos_t) {
+                const int half = PG_D / 2;
+                for (int t = 0; t < L && t < max_pos; ++t) {
+                    if (!ok[t]) continue;
+                    float* kr = K + (size_t)t * PG_D;
+                    for (int i = 0; i < half; ++i) {
+                        const int d0 = rope_dim(style, i, 0, half), d1 = rope_dim(style, i, 1, half);
+                        const double c = cos_t[(int64_t)t * half + i], sn = sin_t[(int64_t)t * half + i];
+                        const double x0 = kr[d0], x1 = kr[d1];
+                        kr[d0] = (float)(x0 * c - x1 * sn);
+                        kr[d1] = (float)(x0 * sn + x1 * c);
+                    }
+                }
+            }
             for (int h = 0; h < num_heads; ++h) {
                 if (kv_head_of(h, num_heads, num_kv_heads, gqa_map) != kvh) continue;
                 int64_t qoff = ((int64_t)s * num_heads + h) * PG_D;
@@ -1097,4 +1118,33 @@ void orc_kivi_paged_attention_bits(double* out, const void* q, int q_dtype,
         }
     }
     free(K); free(V); free(sc); free(ok);
+}
+
+void orc_kivi_paged_attention_bits(double* out, const void* q, int q_dtype,
+                                   const uint8_t* pages, const int32_t* page_tables,
+                                   int max_pages, int num_pages, const uint16_t* k_cache,
+                                   const uint16_t* v_cache, const int32_t* block_tables,
+                                   int max_blocks_per_seq, const int32_t* seq_lens,
+                                   int num_seqs, int num_heads, int num_kv_heads,
+                                   int block_size, int residual_length, float scale,
+                                   int gqa_map, int bits)
+{
+    kivi_attention_impl(out, q, q_dtype, pages, page_tables, max_pages, num_pages, k_cache, v_cache,
+                        block_tables, max_blocks_per_seq, seq_lens, num_seqs, num_heads, num_kv_heads,
+                        block_size, residual_length, scale, gqa_map, bits, NULL, NULL, 0, 0);
+}
+
+void orc_kivi_paged_attention_pre_rope(double* out, const void* q, int q_dtype,
+                                       const uint8_t* pages, const int32_t* page_tables,
+                                       int max_pages, int num_pages, const uint16_t* k_cache,
+                                       const uint16_t* v_cache, const int32_t* block_tables,
+                                       int max_blocks_per_seq, const int32_t* seq_lens,
+                                       int num_seqs, int num_heads, int num_kv_heads,
+                                       int block_size, int residual_length, float scale,
+                                       int gqa_map, int bits, const float* cos_t,
+                                       const float* sin_t, int max_pos, int style)
+{
+    kivi_attention_impl(out, q, q_dtype, pages, page_tables, max_pages, num_pages, k_cache, v_cache,
+                        block_tables, max_blocks_per_seq, seq_lens, num_seqs, num_heads, num_kv_heads,
+                        block_size, residual_length, scale, gqa_map, bits, cos_t, sin_t, max_pos, style);
 }

@@ -183,6 +183,18 @@ void orc_kivi_build_pages(const uint16_t* k_cache, const uint16_t* v_cache,
  * tokens < Lq, the fp16 paged cache for tokens >= Lq.  Page-table entries
  * outside [0, num_pages) and negative block-table entries are holes whose
  * tokens are skipped.  out double. */
+/* orc_kivi_paged_attention_bits with the keys held before RoPE: each key
+ * rotated by its position (fp32 tables [max_pos, 64], style 0 adjacent
+ * pairs, 1 halves) before the scores. */
+void orc_kivi_paged_attention_pre_rope(double* out, const void* q, int q_dtype,
+                                       const uint8_t* pages, const int32_t* page_tables,
+                                       int max_pages, int num_pages, const uint16_t* k_cache,
+                                       const uint16_t* v_cache, const int32_t* block_tables,
+                                       int max_blocks_per_seq, const int32_t* seq_lens,
+                                       int num_seqs, int num_heads, int num_kv_heads,
+                                       int block_size, int residual_length, float scale,
+                                       int gqa_map, int bits, const float* cos_t,
+                                       const float* sin_t, int max_pos, int style);
 void orc_kivi_paged_attention(double* out, const void* q, int q_dtype,
                               const uint8_t* pages, const int32_t* page_tables,
                               int max_pages, int num_pages, const uint16_t* k_cache,

@@ -75,6 +75,8 @@ _lib.orc_kivi_page_dequant_bits.argtypes = [_P, _P, _P, _I]
 _lib.orc_kivi_build_pages_bits.argtypes = [_P, _P, _P, _I, _P, _I, _I, _I, _I, _P, _P, _I, _I, _I]
 _lib.orc_kivi_paged_attention_bits.argtypes = [_P, _P, _I, _P, _P, _I, _I, _P, _P, _P, _I, _P, _I, _I, _I, _I, _I,
                                                _F, _I, _I]
+_lib.orc_kivi_paged_attention_pre_rope.argtypes = [_P, _P, _I, _P, _P, _I, _I, _P, _P, _P, _I, _P, _I, _I, _I, _I, _I,
+                                                  _F, _I, _I, _P, _P, _I, _I]
 
 lib = _lib
 
@@ -324,13 +326,19 @@ def kivi_build_pages(k_cache, v_cache, tables, seq_lens, residual_length, pages,
 
 
 def kivi_paged_attention(q, q_code, pages, page_tables, k_cache, v_cache, tables, seq_lens,
-                         num_kv_heads, residual_length, scale, gqa_map=GROUPED, bits=4):
+                         num_kv_heads, residual_length, scale, gqa_map=GROUPED, bits=4, pre_rope=None):
+    """pre_rope = (cos_t, sin_t, style): the keys are held before RoPE and
+    rotated by their positions inside attention."""
     S, H, D = q.shape
     out = np.zeros((S, H, D), np.float64)
     num_pages = pages.size // (num_kv_heads * kivi_page_bytes(bits))
     args = (ptr(out), ptr(q), q_code, ptr(pages), ptr(page_tables), page_tables.shape[1], num_pages,
             ptr(k_cache), ptr(v_cache), ptr(tables), tables.shape[1], ptr(seq_lens), S, H, num_kv_heads,
             k_cache.shape[3], residual_length, scale, gqa_map)
+    if pre_rope is not None:
+        cos_t, sin_t, style = pre_rope
+        _lib.orc_kivi_paged_attention_pre_rope(*args, bits, ptr(cos_t), ptr(sin_t), cos_t.shape[0], style)
+        return out
     if bits == 4:
         _lib.orc_kivi_paged_attention(*args)
     else:

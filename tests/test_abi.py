@@ -272,17 +272,17 @@ def test_kivi_page_bytes():
 
 
 def test_kivi_apply_config_maps_kiviconfig_and_rejects_what_is_not_built():
-    """KiviConfig (config_schema.h:122-129): bits and residual_length land
-    in the descriptor; the default granularities are the pages' layout;
-    other granularities and pre_rope_keys = true are not built."""
+    """KiviConfig (config_schema.h:122-129): bits, residual_length and
+    pre_rope_keys land in the descriptor; the default granularities are the
+    pages' layout; other granularities are not built."""
     d = _kdesc(bits=0, residual_length=5)
     tla.kivi_apply_config(d, bits=8, residual_length=128)
-    assert d.bits == 8 and d.residual_length == 128
-    tla.kivi_apply_config(d, bits=4, residual_length=0)
-    assert d.bits == 4 and d.residual_length == 0
+    assert d.bits == 8 and d.residual_length == 128 and d.pre_rope_keys == 0
+    tla.kivi_apply_config(d, bits=4, residual_length=0, pre_rope_keys=True)
+    assert d.bits == 4 and d.residual_length == 0 and d.pre_rope_keys == 1
     L = tla.lib
     call = lambda b, r, kg, vg, pre: L.tl_kivi_apply_config(ctypes.byref(d), b, r, kg, vg, pre)
-    assert call(8, 128, b"per_channel", b"per_token", 1) == tla.ERR_NOT_IMPLEMENTED
+    assert call(8, 128, b"per_channel", b"per_token", 2) == tla.ERR_INVALID_ARGUMENT
     assert "pre_rope_keys" in tla.last_error()
     assert call(8, 128, b"per_token", b"per_token", 0) == tla.ERR_NOT_IMPLEMENTED
     assert call(8, 128, b"per_channel", b"per_channel", 0) == tla.ERR_NOT_IMPLEMENTED
@@ -290,7 +290,45 @@ def test_kivi_apply_config_maps_kiviconfig_and_rejects_what_is_not_built():
     assert call(6, 128, b"per_channel", b"per_token", 0) == tla.ERR_INVALID_ARGUMENT
     assert call(8, -1, b"per_channel", b"per_token", 0) == tla.ERR_INVALID_ARGUMENT
     assert L.tl_kivi_apply_config(None, 8, 128, b"per_channel", b"per_token", 0) == tla.ERR_INVALID_ARGUMENT
-    assert d.bits == 4 and d.residual_length == 0          # a rejected call leaves the descriptor
+    # a rejected call leaves the descriptor
+    assert d.bits == 4 and d.residual_length == 0 and d.pre_rope_keys == 1
+
+
+def test_kivi_pre_rope_entry_points_check_their_arguments():
+    """Keys held before RoPE: the standard decode and step refuse a
+    descriptor with pre_rope_keys set (they would score unrotated keys); the
+    _pre_rope entry points check the tables (non-NULL, 16-byte aligned,
+    max_positions > 0, style 0 or 1) before any device work."""
+    L = tla.lib
+    d = _kdesc()
+    d.pre_rope_keys = 1
+    assert L.tl_kivi_paged_attention_decode(ctypes.byref(d), FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE,
+                                            4096, FAKE, 1 << 30, None) == tla.ERR_INVALID_ARGUMENT
+    assert "pre_rope_keys" in tla.last_error()
+    assert L.tl_kivi_decode_step(ctypes.byref(d), *([FAKE] * 11), 4096, FAKE, 1 << 30, None) == tla.ERR_INVALID_ARGUMENT
+    d.pre_rope_keys = 3
+    assert L.tl_kivi_paged_attention_decode_pre_rope(ctypes.byref(d), *([FAKE] * 8), 4096, FAKE, FAKE, 8192, 0, FAKE,
+                                                     1 << 30, None) == tla.ERR_INVALID_ARGUMENT
+    d.pre_rope_keys = 1
+
+    def dec(cos=FAKE, sin=FAKE, max_pos=8192, style=0):
+        return L.tl_kivi_paged_attention_decode_pre_rope(ctypes.byref(d), *([FAKE] * 8), 4096, cos, sin, max_pos,
+                                                         style, FAKE, 1 << 30, None)
+
+    def step(cos=FAKE, sin=FAKE, max_pos=8192, style=1):
+        return L.tl_kivi_decode_step_pre_rope(ctypes.byref(d), *([FAKE] * 11), 4096, cos, sin, max_pos, style, FAKE,
+                                              1 << 30, None)
+    for f in (dec, step):
+        assert f(cos=None) == tla.ERR_INVALID_ARGUMENT
+        assert f(sin=None) == tla.ERR_INVALID_ARGUMENT
+        assert f(cos=ctypes.c_void_p(0x1004)) == tla.ERR_INVALID_ARGUMENT
+        assert "aligned" in tla.last_error()
+        assert f(max_pos=0) == tla.ERR_INVALID_ARGUMENT
+        assert f(style=2) == tla.ERR_INVALID_ARGUMENT
+    z = _kdesc(num_seqs=0)
+    z.pre_rope_keys = 1
+    assert L.tl_kivi_paged_attention_decode_pre_rope(ctypes.byref(z), *([FAKE] * 8), 0, FAKE, FAKE, 8192, 0, None,
+                                                     0, None) == tla.OK
 
 
 def test_kivi_rope_step_workspace_and_argument_checks():

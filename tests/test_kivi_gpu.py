@@ -412,6 +412,99 @@ def test_kivi_rope_step_matches_oracle_each_step(style, bits):
     assert np.array_equal(pages.cpu().numpy()[used], want_pages[used])
 
 
+@pytest.mark.parametrize("style,bits,pp", [(tla.ROPE_ADJACENT, 4, 0), (tla.ROPE_HALVES, 4, -1),
+                                           (tla.ROPE_HALVES, 8, 4), (tla.ROPE_ADJACENT, 8, 1)])
+def test_kivi_pre_rope_decode_matches_oracle(style, bits, pp):
+    """Keys held before RoPE (tl_kivi_paged_attention_decode_pre_rope): each
+    page key rotated after its dequantisation and each window key as read,
+    at its token position, against the oracle's attention on the rotated
+    keys.  The tables hold 2048 positions, so the 3000- and 4096-token
+    sequences score their later keys unrotated; a page and a window block are
+    holes.  The same descriptor through the standard entry point is refused."""
+    from test_oracle import rope_tables
+    kc = KiviCase(57, [4096, 1000, 161, 159, 0, 1, 2047, 3000], bits=bits)
+    kc.page_tables[1, 3] = -1
+    kc.tables[6, (2047 - 60) // 16] = -1
+    pages_np = kc.oracle_pages()
+    cos_t, sin_t = rope_tables(2048, 128)
+    qd, kd, vd = dev(kc.q, orc.F16), dev(kc.k, orc.F16), dev(kc.v, orc.F16)
+    btd, sld, ptd = dev(kc.tables), dev(kc.lens), dev(kc.page_tables)
+    pages = torch.from_numpy(pages_np).cuda()
+    desc = kc.desc(qd, kd, btd, ptd, pp)
+    desc.pre_rope_keys = 1
+    max_ctx = int(kc.lens.max())
+    ws = torch.empty(max(16, tla.kivi_workspace_bytes(desc, max_ctx)), dtype=torch.uint8, device="cuda")
+    out = torch.full_like(qd, float("nan"))
+    print(f"case kivi pre-rope decode style={style} bits={bits} pp={pp}", flush=True)
+    tla.kivi_paged_attention_decode_pre_rope(desc, out, qd, pages, ptd, kd, vd, btd, sld, max_ctx, dev(cos_t),
+                                             dev(sin_t), style, ws)
+    torch.cuda.synchronize()
+    want = orc.kivi_paged_attention(kc.q, orc.F16, pages_np, kc.page_tables, kc.k, kc.v, kc.tables, kc.lens,
+                                    kc.n_kv, kc.R, kc.scale, orc.GROUPED, bits, pre_rope=(cos_t, sin_t, style))
+    assert_close(out, want, orc.F16, ATOL_KIVI, f"style={style} bits={bits} pp={pp}")
+    with pytest.raises(tla.TLError):
+        tla.kivi_paged_attention_decode(desc, out, qd, pages, ptd, kd, vd, btd, sld, max_ctx, ws)
+
+
+@pytest.mark.parametrize("style,bits,through_rope_step", [(tla.ROPE_ADJACENT, 4, True), (tla.ROPE_HALVES, 8, True),
+                                                          (tla.ROPE_HALVES, 4, False)])
+def test_kivi_pre_rope_step_matches_oracle_each_step(style, bits, through_rope_step):
+    """Keys held before RoPE through the fused step, checked against the
+    oracle at every step.  Through tl_kivi_rope_decode_step with the
+    descriptor's pre_rope_keys set, q is rotated at position seq_lens - 1 and
+    the new key goes to the pool as given; through
+    tl_kivi_decode_step_pre_rope, q is taken as given.  The host pools take
+    the unrotated keys, the pages are rebuilt from them, and the expected
+    output is the oracle's attention with every key rotated at its position.
+    Sequence 5 runs past the 1024-position tables halfway; pages complete
+    during the run.  At the end the pools and pages are the oracle's bit for
+    bit (unrotated keys)."""
+    from test_oracle import rope_tables
+    start = np.array([150, 159, 160, 191, 33, 1000], np.int32)
+    steps = 36
+    kc = KiviCase(73, start + steps, H=32, extra_blocks=1, bits=bits)
+    cos_t, sin_t = rope_tables(1024, 128)
+    q_base = kc.q.copy()
+    qd, kd, vd = dev(kc.q, orc.F16), dev(kc.k, orc.F16), dev(kc.v, orc.F16)
+    btd, ptd = dev(kc.tables), dev(kc.page_tables)
+    pages = torch.zeros(kc.num_pages, kc.n_kv, kc.page_bytes, dtype=torch.uint8, device="cuda")
+    desc = kc.desc(qd, kd, btd, ptd, 0)
+    tla.kivi_build_pages(desc, kd, vd, btd, dev(start), ptd, pages, int(start.max()))
+    tla.kivi_apply_config(desc, bits=bits, residual_length=kc.R, pre_rope_keys=True)
+    rng = np.random.default_rng(15)
+    max_ctx = int(start.max()) + steps
+    ws = torch.empty(max(16, tla.kivi_rope_step_workspace_bytes(desc, max_ctx)), dtype=torch.uint8, device="cuda")
+    cos_d, sin_d = dev(cos_t), dev(sin_t)
+    lens = start.copy()
+    k_host, v_host = kc.k.copy(), kc.v.copy()
+    print(f"case kivi pre-rope step style={style} bits={bits} rope_step={through_rope_step}", flush=True)
+    for step in range(steps):
+        lens = lens + 1
+        pos = (lens - 1).astype(np.int32)
+        slots = (kc.tables[np.arange(kc.S), pos // 16] * 16 + pos % 16).astype(np.int32)
+        knew = inputs.encode(rng.standard_normal((kc.S, kc.n_kv, 128), dtype=np.float32), orc.F16)
+        vnew = inputs.encode(rng.standard_normal((kc.S, kc.n_kv, 128), dtype=np.float32), orc.F16)
+        out = torch.full_like(qd, float("nan"))
+        if through_rope_step:
+            tla.kivi_rope_decode_step(desc, out, qd, dev(knew, orc.F16), dev(vnew, orc.F16), dev(pos), cos_d, sin_d,
+                                      style, dev(slots), pages, ptd, kd, vd, btd, dev(lens), max_ctx, ws)
+            q_use, _ = _oracle_rotate(q_base, knew, vnew, pos, cos_t, sin_t, style)
+        else:
+            tla.kivi_decode_step_pre_rope(desc, out, qd, dev(knew, orc.F16), dev(vnew, orc.F16), dev(slots), pages,
+                                          ptd, kd, vd, btd, dev(lens), max_ctx, cos_d, sin_d, style, ws)
+            q_use = q_base
+        torch.cuda.synchronize()
+        orc.reshape_and_cache(knew, vnew, k_host, v_host, slots)
+        kc.k, kc.v, kc.lens = k_host, v_host, lens
+        want_pages = kc.oracle_pages()
+        want = orc.kivi_paged_attention(q_use, orc.F16, want_pages, kc.page_tables, kc.k, kc.v, kc.tables, kc.lens,
+                                        kc.n_kv, kc.R, kc.scale, orc.GROUPED, bits, pre_rope=(cos_t, sin_t, style))
+        assert_close(out, want, orc.F16, ATOL_KIVI, f"step {step}")
+    assert np.array_equal(host_bits(kd), k_host) and np.array_equal(host_bits(vd), v_host)
+    used = [p for p in _used_pages(kc, lens) if p >= 0]
+    assert np.array_equal(pages.cpu().numpy()[used], want_pages[used])
+
+
 def test_kivi_step_full_batch_mixed_lengths():
     """The benchmark's KIVI step at full size: batch 64, 32/8 heads,
     sequence s at 4096 + s mod 32 tokens, R = 128, one fused step (sequences

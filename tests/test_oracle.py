@@ -701,6 +701,49 @@ def test_kivi_attention_equals_paged_attention_on_dequantised_prefix(gqa_map, bi
     assert np.abs(full[0] - got[0]).max() > 1e-3 and np.abs(full[3] - got[3]).max() > 1e-3
 
 
+@pytest.mark.parametrize("style,bits", [(0, 4), (1, 4), (0, 8), (1, 8)])
+def test_kivi_pre_rope_attention_is_attention_on_the_rotated_pool(style, bits):
+    """Keys held before RoPE (KiviConfig.pre_rope_keys): the oracle's KIVI
+    attention with the tables equals orc_paged_attention (pinned above) on
+    the pool the cache stands for (dequantised pages below Lq, the window
+    above) in fp32, each valid token's key rotated at its position by
+    orc_rope_reshape_and_cache (pinned by its own tests).  The tables stop
+    at 280: sequence 0's later tokens stay unrotated.  Holes in the page
+    table and in the window drop their tokens."""
+    R = 128
+    lens = [300, 161, 100, 223]
+    case, ptab, num_pages = _kivi_small_case(34, lens)
+    case.tables[0, 12] = -1
+    ptab[3, 1] = -1
+    pages = np.zeros((num_pages, 2, orc.kivi_page_bytes(bits)), np.uint8)
+    orc.kivi_build_pages(case.k_cache, case.v_cache, case.tables, case.seq_lens, R, pages, ptab, bits)
+    cos_t, sin_t = rope_tables(280, 128)
+    got = orc.kivi_paged_attention(case.q, orc.F16, pages, ptab, case.k_cache, case.v_cache, case.tables,
+                                   case.seq_lens, 2, R, case.scale, orc.GROUPED, bits, pre_rope=(cos_t, sin_t, style))
+    kp, vp, t2 = _kivi_as_paged_pool(case, pages, ptab, num_pages, R, bits)
+    f32 = lambda a: orc.bits_to_f32(a, orc.F16).astype(np.float32).view(np.uint32)
+    kp32, vp32 = np.ascontiguousarray(f32(kp)), np.ascontiguousarray(f32(vp))
+    rows_k, rows_v, slots, pos = [], [], [], []
+    for si, L in enumerate(case.seq_lens):
+        for t in range(int(L)):
+            blk = int(t2[si, t // 16])
+            if blk < 0:
+                continue
+            rows_k.append(kp32[blk, :, :, t % 16])
+            rows_v.append(vp32[blk, :, :, t % 16])
+            slots.append(blk * 16 + t % 16)
+            pos.append(t)
+    rk, rv = np.ascontiguousarray(np.stack(rows_k)), np.ascontiguousarray(np.stack(rows_v))
+    orc.rope_reshape_and_cache(None, None, rk, rv, kp32, vp32, np.array(slots, np.int32), np.array(pos, np.int32),
+                               cos_t, sin_t, orc.F32, style)
+    want = orc.paged_attention(case.q, orc.F16, kp32, vp32, orc.F32, t2, case.seq_lens, 2, case.scale,
+                               orc.GROUPED)
+    np.testing.assert_allclose(got, want, rtol=0, atol=2e-5)
+    plain = orc.kivi_paged_attention(case.q, orc.F16, pages, ptab, case.k_cache, case.v_cache, case.tables,
+                                     case.seq_lens, 2, R, case.scale, orc.GROUPED, bits)
+    assert np.abs(plain - got).max() > 1e-2
+
+
 def test_kivi_attention_without_pages_is_paged_attention_with_holes():
     """R >= L: no token is quantised, so KIVI attention is paged attention on
     the fp16 pool, holes skipped in both."""

@@ -562,7 +562,33 @@ static int check_kivi(const tl_kivi_desc* d) {
   if (d->partition_pages < -1) return fail(TL_ERR_INVALID_ARGUMENT, "partition_pages=%d", d->partition_pages);
   if (d->bits != 0 && d->bits != 4 && d->bits != 8)
     return fail(TL_ERR_NOT_IMPLEMENTED, "paged KIVI bits=%d (built: 4, 8)", d->bits);
+  if (d->pre_rope_keys != 0 && d->pre_rope_keys != 1)
+    return fail(TL_ERR_INVALID_ARGUMENT, "pre_rope_keys=%d", d->pre_rope_keys);
   return TL_OK;
+}
+
+// Keys held before RoPE: the tables the kernels rotate them with.
+struct KiviRope {
+  const float* cos_table;
+  const float* sin_table;
+  int32_t max_positions, style;
+};
+
+static int check_kivi_rope(const KiviRope& r) {
+  if (r.max_positions <= 0) return fail(TL_ERR_INVALID_ARGUMENT, "max_positions=%d", r.max_positions);
+  if (r.style != TL_ROPE_ADJACENT && r.style != TL_ROPE_HALVES)
+    return fail(TL_ERR_INVALID_ARGUMENT, "style=%d", r.style);
+  if (!r.cos_table || !r.sin_table) return fail(TL_ERR_INVALID_ARGUMENT, "NULL rope table");
+  if (((uintptr_t)r.cos_table | (uintptr_t)r.sin_table) % 16)
+    return fail(TL_ERR_INVALID_ARGUMENT, "rope tables must be 16-byte aligned");
+  return TL_OK;
+}
+
+static int refuse_pre_rope(const tl_kivi_desc* d) {
+  return d->pre_rope_keys ? fail(TL_ERR_INVALID_ARGUMENT,
+                                 "desc->pre_rope_keys: keys held before RoPE need the rope tables "
+                                 "(the _pre_rope entry points)")
+                          : TL_OK;
 }
 
 static int kivi_bits(const tl_kivi_desc* d) { return d->bits == 8 ? 8 : 4; }
@@ -658,7 +684,7 @@ static int kivi_decode_impl(const tl_kivi_desc* desc, void* out, const void* q, 
                             const int32_t* page_tables, const void* k_cache, const void* v_cache,
                             const int32_t* block_tables, const int32_t* seq_lens, int32_t max_context_len,
                             void* workspace, size_t workspace_bytes, void* stream,
-                            const tl::KiviPageLaunch* append);
+                            const tl::KiviPageLaunch* append, const KiviRope* rope);
 
 int tl_kivi_paged_attention_decode(const tl_kivi_desc* desc, void* out, const void* q,
                                    const void* pages, const int32_t* page_tables,
@@ -666,8 +692,39 @@ int tl_kivi_paged_attention_decode(const tl_kivi_desc* desc, void* out, const vo
                                    const int32_t* block_tables, const int32_t* seq_lens,
                                    int32_t max_context_len, void* workspace,
                                    size_t workspace_bytes, void* stream) {
+  int rc = check_kivi(desc);
+  if (rc || (rc = refuse_pre_rope(desc))) return rc;
   return kivi_decode_impl(desc, out, q, pages, page_tables, k_cache, v_cache, block_tables, seq_lens,
-                          max_context_len, workspace, workspace_bytes, stream, nullptr);
+                          max_context_len, workspace, workspace_bytes, stream, nullptr, nullptr);
+}
+
+int tl_kivi_paged_attention_decode_pre_rope(const tl_kivi_desc* desc, void* out, const void* q,
+                                            const void* pages, const int32_t* page_tables,
+                                            const void* k_cache, const void* v_cache,
+                                            const int32_t* block_tables, const int32_t* seq_lens,
+                                            int32_t max_context_len, const float* cos_table,
+                                            const float* sin_table, int32_t max_positions, int32_t style,
+                                            void* workspace, size_t workspace_bytes, void* stream) {
+  const KiviRope r{cos_table, sin_table, max_positions, style};
+  int rc = check_kivi(desc);
+  if (rc || (rc = check_kivi_rope(r))) return rc;
+  return kivi_decode_impl(desc, out, q, pages, page_tables, k_cache, v_cache, block_tables, seq_lens,
+                          max_context_len, workspace, workspace_bytes, stream, nullptr, &r);
+}
+
+static int kivi_step_impl(const tl_kivi_desc* desc, void* out, const void* q, const void* key,
+                          const void* value, const int32_t* slot_mapping, void* pages,
+                          const int32_t* page_tables, void* k_cache, void* v_cache,
+                          const int32_t* block_tables, const int32_t* seq_lens, int32_t max_context_len,
+                          void* workspace, size_t workspace_bytes, void* stream, const KiviRope* rope) {
+  if (desc->num_seqs == 0) return ok();
+  if (!key || !value || !slot_mapping) return fail(TL_ERR_INVALID_ARGUMENT, "NULL pointer");
+  if (!aligned16(key) || !aligned16(value)) return fail(TL_ERR_INVALID_ARGUMENT, "key/value must be 16-byte aligned");
+  tl::KiviPageLaunch a = page_launch(desc, k_cache, v_cache, block_tables, seq_lens, page_tables, pages, stream);
+  a.append = 1;
+  a.knew = key; a.vnew = value; a.slots = slot_mapping;
+  return kivi_decode_impl(desc, out, q, pages, page_tables, k_cache, v_cache, block_tables, seq_lens,
+                          max_context_len, workspace, workspace_bytes, stream, &a, rope);
 }
 
 int tl_kivi_decode_step(const tl_kivi_desc* desc, void* out, const void* q, const void* key,
@@ -676,15 +733,23 @@ int tl_kivi_decode_step(const tl_kivi_desc* desc, void* out, const void* q, cons
                         const int32_t* block_tables, const int32_t* seq_lens, int32_t max_context_len,
                         void* workspace, size_t workspace_bytes, void* stream) {
   int rc = check_kivi(desc);
-  if (rc) return rc;
-  if (desc->num_seqs == 0) return ok();
-  if (!key || !value || !slot_mapping) return fail(TL_ERR_INVALID_ARGUMENT, "NULL pointer");
-  if (!aligned16(key) || !aligned16(value)) return fail(TL_ERR_INVALID_ARGUMENT, "key/value must be 16-byte aligned");
-  tl::KiviPageLaunch a = page_launch(desc, k_cache, v_cache, block_tables, seq_lens, page_tables, pages, stream);
-  a.append = 1;
-  a.knew = key; a.vnew = value; a.slots = slot_mapping;
-  return kivi_decode_impl(desc, out, q, pages, page_tables, k_cache, v_cache, block_tables, seq_lens,
-                          max_context_len, workspace, workspace_bytes, stream, &a);
+  if (rc || (rc = refuse_pre_rope(desc))) return rc;
+  return kivi_step_impl(desc, out, q, key, value, slot_mapping, pages, page_tables, k_cache, v_cache, block_tables,
+                        seq_lens, max_context_len, workspace, workspace_bytes, stream, nullptr);
+}
+
+int tl_kivi_decode_step_pre_rope(const tl_kivi_desc* desc, void* out, const void* q, const void* key,
+                                 const void* value, const int32_t* slot_mapping, void* pages,
+                                 const int32_t* page_tables, void* k_cache, void* v_cache,
+                                 const int32_t* block_tables, const int32_t* seq_lens,
+                                 int32_t max_context_len, const float* cos_table, const float* sin_table,
+                                 int32_t max_positions, int32_t style, void* workspace,
+                                 size_t workspace_bytes, void* stream) {
+  const KiviRope r{cos_table, sin_table, max_positions, style};
+  int rc = check_kivi(desc);
+  if (rc || (rc = check_kivi_rope(r))) return rc;
+  return kivi_step_impl(desc, out, q, key, value, slot_mapping, pages, page_tables, k_cache, v_cache, block_tables,
+                        seq_lens, max_context_len, workspace, workspace_bytes, stream, &r);
 }
 
 // The rope step's workspace: the step's split-K partials, then the rotated
@@ -720,6 +785,8 @@ int tl_kivi_rope_decode_step(const tl_kivi_desc* desc, void* out, const void* q,
   if (!workspace || workspace_bytes < need)
     return fail(TL_ERR_INVALID_ARGUMENT, "workspace of %zu bytes needed, %zu given", need, workspace_bytes);
   if (!aligned16(workspace)) return fail(TL_ERR_INVALID_ARGUMENT, "workspace must be 16-byte aligned");
+  const KiviRope kr{cos_table, sin_table, max_positions, style};
+  if (desc->pre_rope_keys && (rc = check_kivi_rope(kr))) return rc;
   const size_t qoff = kivi_rope_q_offset(desc, max_context_len);
   char* q_rot = (char*)workspace + qoff;
   char* k_rot = q_rot + align256((size_t)desc->num_seqs * desc->num_heads * desc->head_size * 2);
@@ -727,12 +794,17 @@ int tl_kivi_rope_decode_step(const tl_kivi_desc* desc, void* out, const void* q,
   memset(&r, 0, sizeof r);
   r.q = q; r.q_out = q_rot; r.key = key; r.k_out = k_rot;
   r.positions = positions; r.cos_table = cos_table; r.sin_table = sin_table;
-  r.num_tokens = desc->num_seqs; r.num_heads = desc->num_heads; r.num_kv_heads = desc->num_kv_heads;
+  r.num_tokens = desc->num_seqs; r.num_heads = desc->num_heads;
+  // keys held before RoPE: q rows only, the keys go to the step as given
+  r.num_kv_heads = desc->pre_rope_keys ? 0 : desc->num_kv_heads;
   r.head_size = desc->head_size; r.block_size = desc->block_size; r.num_blocks = desc->num_blocks;
   r.max_positions = max_positions; r.dtype = TL_DTYPE_F16; r.style = style;
   if (tl::launch_rope_rows(r, (hipStream_t)stream)) return fail(TL_ERR_BACKEND, "rope launch failed");
-  return tl_kivi_decode_step(desc, out, q_rot, k_rot, value, slot_mapping, pages, page_tables, k_cache, v_cache,
-                             block_tables, seq_lens, max_context_len, workspace, qoff, stream);
+  if (desc->pre_rope_keys)
+    return kivi_step_impl(desc, out, q_rot, key, value, slot_mapping, pages, page_tables, k_cache, v_cache,
+                          block_tables, seq_lens, max_context_len, workspace, qoff, stream, &kr);
+  return kivi_step_impl(desc, out, q_rot, k_rot, value, slot_mapping, pages, page_tables, k_cache, v_cache,
+                        block_tables, seq_lens, max_context_len, workspace, qoff, stream, nullptr);
 }
 
 int tl_kivi_apply_config(tl_kivi_desc* desc, int32_t bits, int32_t residual_length,
@@ -747,12 +819,11 @@ int tl_kivi_apply_config(tl_kivi_desc* desc, int32_t bits, int32_t residual_leng
   if (!value_granularity || strcmp(value_granularity, "per_token") != 0)
     return fail(TL_ERR_NOT_IMPLEMENTED, "value_granularity '%s' (built: per_token)",
                 value_granularity ? value_granularity : "(null)");
-  if (pre_rope_keys)
-    return fail(TL_ERR_NOT_IMPLEMENTED,
-                "pre_rope_keys: keys quantised before RoPE are not built (keys are stored and quantised as "
-                "given; tl_kivi_rope_decode_step rotates them first)");
+  if (pre_rope_keys != 0 && pre_rope_keys != 1)
+    return fail(TL_ERR_INVALID_ARGUMENT, "pre_rope_keys=%d (0 or 1)", pre_rope_keys);
   desc->bits = bits;
   desc->residual_length = residual_length;
+  desc->pre_rope_keys = pre_rope_keys;
   return ok();
 }
 
@@ -760,7 +831,7 @@ static int kivi_decode_impl(const tl_kivi_desc* desc, void* out, const void* q, 
                             const int32_t* page_tables, const void* k_cache, const void* v_cache,
                             const int32_t* block_tables, const int32_t* seq_lens, int32_t max_context_len,
                             void* workspace, size_t workspace_bytes, void* stream,
-                            const tl::KiviPageLaunch* append) {
+                            const tl::KiviPageLaunch* append, const KiviRope* rope) {
   int rc = check_kivi(desc);
   if (rc) return rc;
   if (max_context_len < 0) return fail(TL_ERR_INVALID_ARGUMENT, "max_context_len < 0");
@@ -783,6 +854,10 @@ static int kivi_decode_impl(const tl_kivi_desc* desc, void* out, const void* q, 
   a.bits = kivi_bits(desc);
   a.scale = desc->scale;
   a.append = append;
+  if (rope) {
+    a.rope_cos = rope->cos_table; a.rope_sin = rope->sin_table;
+    a.rope_max_pos = rope->max_positions; a.rope_style = rope->style;
+  }
   a.stream = (hipStream_t)stream;
   if (P > 1) {
     const size_t sh = (size_t)desc->num_seqs * desc->num_heads * P;

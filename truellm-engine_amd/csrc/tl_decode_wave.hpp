@@ -117,14 +117,23 @@ __device__ __forceinline__ void load_v_rows(u32x4 (&vr)[VD], const char* blk, in
   for (int j = 0; j < VD; ++j) vr[j] = load16_stream(blk + ((16 * j + dl) * CPR + th) * 16);
 }
 
+// The key rotation hook of decode2_wave: called with the lane's K rows as
+// loaded (kr[j][r]: head-dim row 2 m + r, m = dl + 16 j, of its 8 tokens
+// tok0 .. tok0 + 7) before they enter q.k.  NoKeyRotation leaves them.
+struct NoKeyRotation {
+  static constexpr bool kActive = false;
+  template <int KP>
+  __device__ void operator()(u32x4 (&)[KP][2], int, int) const {}
+};
+
 // Runs one wavefront over its iterations and leaves its state in LDS:
 // s_acc_w [4][HEAD] unnormalised outputs, s_m_w [4] running max (log2 units),
 // s_l_w [4] sums.  s_p_w is the wavefront's weight exchange area: [4][4][4]
 // words, twice that for bf16 (the weights' high and low bf16 parts).
-template <Kind KV, int HEAD, int BS>
+template <Kind KV, int HEAD, int BS, class Rot = NoKeyRotation>
 __device__ __forceinline__ void decode2_wave(const Params& p, int seq, int kvh, int hs, int first_it,
                                              int t1, int step, uint32_t* s_p_w, float* s_acc_w,
-                                             float* s_m_w, float* s_l_w) {
+                                             float* s_m_w, float* s_l_w, const Rot& rot = Rot()) {
   constexpr int GT = kWaveHeads;
   constexpr int CPR = BS / 8;             // 16-byte chunks per head-dim row of a block
   constexpr int BPI = 4 / CPR;            // blocks per wave iteration
@@ -183,6 +192,7 @@ __device__ __forceinline__ void decode2_wave(const Params& p, int seq, int kvh, 
     const int ph_nn = table_entry_bs<BS>(p, table, it + 2 * step + blk_in * BS, t1);
     const bool has_next = it + step < t1;
     const int blk_tok = it + blk_in * BS;                // first token of this lane's block
+    if constexpr (Rot::kActive) rot(kr, blk_tok + th * 8, dl);
 
     // ---- q.k partials over this lane's dim pairs, 8 tokens x 4 heads ----
     float s[GT * 8];

@@ -170,6 +170,11 @@ struct KiviDecodeLaunch {
   float scale;
   const KiviPageLaunch* append;  // non-null: the step's append (token write, page build),
                                  // fused into the decode launch
+  // non-null: keys are held before RoPE and rotated at their positions
+  // while scored (fp32 tables [rope_max_pos, 64], style 0 or 1)
+  const float* rope_cos = nullptr;
+  const float* rope_sin = nullptr;
+  int rope_max_pos = 0, rope_style = 0;
   hipStream_t stream;
 };
 int launch_kivi_decode(const KiviDecodeLaunch& a);

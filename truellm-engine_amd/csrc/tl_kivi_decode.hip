@@ -44,7 +44,34 @@ struct KiviParams {
   const int32_t* page_tables;
   int max_pages_per_seq, num_pages, residual_length, partition_pages;
   PageJob job;                 // the step's append (kernels with APPEND)
+  // keys held before RoPE (kernels with ROPE): fp32 tables [rope_max_pos,
+  // 64], style 0 (pairs 2i, 2i + 1) or 1 (pairs i, i + 64)
+  const float* rope_cos;
+  const float* rope_sin;
+  int rope_max_pos, rope_style;
 };
+
+// RoPE of a key pair (x0, x1) at angle (c, s), as the oracle's rotation:
+// (x0 c - x1 s, x0 s + x1 c).
+__device__ __forceinline__ void rope_rotate(float& x0, float& x1, float c, float s) {
+  const float y0 = __builtin_fmaf(x0, c, -(x1 * s)), y1 = __builtin_fmaf(x0, s, x1 * c);
+  x0 = y0;
+  x1 = y1;
+}
+// cos / sin of pairs i .. i + 3 at position t (t past the tables: no
+// rotation).  i is a multiple of 4, the tables 16-byte aligned.
+__device__ __forceinline__ void rope_cs4(const KiviParams& k, int t, int i, f4& c, f4& s) {
+  const bool in = t >= 0 && t < k.rope_max_pos;
+  const int64_t o = (int64_t)(in ? t : 0) * (kKiviHead / 2) + i;
+  c = in ? *reinterpret_cast<const f4*>(k.rope_cos + o) : (f4){1.f, 1.f, 1.f, 1.f};
+  s = in ? *reinterpret_cast<const f4*>(k.rope_sin + o) : (f4){0.f, 0.f, 0.f, 0.f};
+}
+__device__ __forceinline__ void rope_cs1(const KiviParams& k, int t, int i, float& c, float& s) {
+  const bool in = t >= 0 && t < k.rope_max_pos;
+  const int64_t o = (int64_t)(in ? t : 0) * (kKiviHead / 2) + i;
+  c = in ? k.rope_cos[o] : 1.f;
+  s = in ? k.rope_sin[o] : 0.f;
+}
 
 // Eight nibbles n_j (slot j at bit 16 (j & 1) + 4 (j >> 1)) as fp16
 // denormals: a masked nibble pair is the fp16 pair (n * 2^-24, n' * 2^-24),
@@ -170,10 +197,15 @@ struct PageState {
 //   O[u][c] = 2^24 sum_t (p_ut slot_scale step_tg) (n_tc 2^-24) + sum_t p_ut zero_tg;
 // the first sum goes to acc (one MFMA per channel tile), the second to cz
 // (one MFMA per page: B column g holds zero_tg).
-template <int BITS>
+// ROPE (keys held before RoPE): a lane dequantises its A operand itself
+// (n step + zero in fp16, from the parameters in LDS), rotates it at the
+// token's position (page p holds tokens 32 p ..) and multiplies by qsc: the
+// tiles then hold S^T itself, and the zero tile and qss are not used.
+template <int BITS, bool ROPE>
 __device__ __forceinline__ void page_pair(PageState& st, const PageRaw<BITS>& ra, const PageRaw<BITS>& rb, bool oka,
                                           bool okb, const u32x4 (&qsc)[4], const u32x4 (&qss)[4],
-                                          uint32_t* s_par_w, int lane, const h8& slot_scale) {
+                                          uint32_t* s_par_w, int lane, const h8& slot_scale,
+                                          const KiviParams& k, int pga, int pgb) {
   constexpr int GT = kWaveHeads;
   const int grp = lane >> 4, u = lane & 15;
 
@@ -183,8 +215,66 @@ __device__ __forceinline__ void page_pair(PageState& st, const PageRaw<BITS>& ra
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-  // ---- q.k (tiles hold 2^-24 S^T) ----
+  // ---- q.k (tiles hold 2^-24 S^T; S^T with ROPE) ----
   f4 s[2][2];
+  if constexpr (ROPE) {
+#pragma unroll
+    for (int pi = 0; pi < 2; ++pi) {
+      const PageRaw<BITS>& r = pi ? rb : ra;
+      const uint32_t* par = s_par_w + pi * 256;
+      const int pg = pi ? pgb : pga;
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt) {
+        const int t = 32 * pg + 16 * tt + u;      // this lane's A row
+        h8 kk[4];                                 // channels 32 m + 8 grp + e
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          const u32x4* kp = reinterpret_cast<const u32x4*>(par + (grp + 4 * m) * 8);
+          const u32x4 raw = k_codes(r, tt, m);
+          // a code c in a half's low bits: 1024 + c as fp16, then c (16 n at
+          // the INT4 slots 2, 3, 6, 7, which slot_scale takes back)
+          const u32x4 biased = {raw.x | 0x64006400u, raw.y | 0x64006400u, raw.z | 0x64006400u,
+                                raw.w | 0x64006400u};
+          const h8 n = as_h8(biased) - (_Float16)1024.0f;
+          kk[m] = n * (slot_scale * as_h8(kp[0])) + as_h8(kp[1]);
+        }
+        if (k.rope_style == 0) {
+          // pairs (2i, 2i + 1): elements (2d, 2d + 1) of block m, i = 16 m + 4 grp + d
+#pragma unroll
+          for (int m = 0; m < 4; ++m) {
+            f4 c, sn;
+            rope_cs4(k, t, 16 * m + 4 * grp, c, sn);
+#pragma unroll
+            for (int d = 0; d < 4; ++d) {
+              float x0 = (float)kk[m][2 * d], x1 = (float)kk[m][2 * d + 1];
+              rope_rotate(x0, x1, c[d], sn[d]);
+              kk[m][2 * d] = (_Float16)x0;
+              kk[m][2 * d + 1] = (_Float16)x1;
+            }
+          }
+        } else {
+          // pairs (i, i + 64): element e of blocks m and m + 2, i = 32 m + 8 grp + e
+#pragma unroll
+          for (int m = 0; m < 2; ++m) {
+            f4 c0, s0, c1, s1;
+            rope_cs4(k, t, 32 * m + 8 * grp, c0, s0);
+            rope_cs4(k, t, 32 * m + 8 * grp + 4, c1, s1);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+              float x0 = (float)kk[m][e], x1 = (float)kk[m + 2][e];
+              rope_rotate(x0, x1, e < 4 ? c0[e & 3] : c1[e & 3], e < 4 ? s0[e & 3] : s1[e & 3]);
+              kk[m][e] = (_Float16)x0;
+              kk[m + 2][e] = (_Float16)x1;
+            }
+          }
+        }
+        f4 acc = (f4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int m = 0; m < 4; ++m) acc = mfma(kk[m], as_h8(qsc[m]), acc);
+        s[pi][tt] = acc;
+      }
+    }
+  } else {
 #pragma unroll
   for (int pi = 0; pi < 2; ++pi) {
     const PageRaw<BITS>& r = pi ? rb : ra;
@@ -206,6 +296,8 @@ __device__ __forceinline__ void page_pair(PageState& st, const PageRaw<BITS>& ra
     s[pi][0] = t0;
     s[pi][1] = t1;
   }
+  }
+  constexpr float kSc = ROPE ? 1.f : kTwo24;   // the tiles' scale of S^T
   // a hole's scores (its loads returned zeros) are dropped
   if (!oka) s[0][0] = s[0][1] = (f4){-INFINITY, -INFINITY, -INFINITY, -INFINITY};
   if (!okb) s[1][0] = s[1][1] = (f4){-INFINITY, -INFINITY, -INFINITY, -INFINITY};
@@ -215,7 +307,7 @@ __device__ __forceinline__ void page_pair(PageState& st, const PageRaw<BITS>& ra
                    fmaxf(fmaxf(s[0][1][0], s[0][1][1]), fmaxf(s[0][1][2], s[0][1][3])));
   mx = fmaxf(mx, fmaxf(fmaxf(fmaxf(s[1][0][0], s[1][0][1]), fmaxf(s[1][0][2], s[1][0][3])),
                        fmaxf(fmaxf(s[1][1][0], s[1][1][1]), fmaxf(s[1][1][2], s[1][1][3]))));
-  mx = swap32_max(swap16_max(mx)) * kTwo24;
+  mx = swap32_max(swap16_max(mx)) * kSc;
   const float m_new = fmaxf(st.m_run, mx);
   const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
   const float alpha = __builtin_amdgcn_exp2f(st.m_run - m_use);
@@ -226,7 +318,7 @@ __device__ __forceinline__ void page_pair(PageState& st, const PageRaw<BITS>& ra
   for (int pi = 0; pi < 2; ++pi) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(s[pi][i >> 2][i & 3], kTwo24, -m_use));
+      const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(s[pi][i >> 2][i & 3], kSc, -m_use));
       lsum += e;
       pw[pi][i] = (_Float16)e;
     }
@@ -273,7 +365,7 @@ __device__ __forceinline__ void page_pair(PageState& st, const PageRaw<BITS>& ra
 // kivi_decode_kernel).  early_ok: early_id is the table entry of page
 // pg_begin + lane * pg_step, read by the caller ahead of time (unchecked;
 // pages at or past pg_end and ids outside the pool are dropped here).
-template <int BITS>
+template <int BITS, bool ROPE>
 __device__ __forceinline__ void kivi_pages_wave(const KiviParams& k, int seq, int kvh, int hs,
                                                 int pg_begin, int pg_end, int pg_step,
                                                 uint32_t* s_par_w, float* s_acc_w, float* s_m_w,
@@ -342,6 +434,7 @@ __device__ __forceinline__ void kivi_pages_wave(const KiviParams& k, int seq, in
       idv = page_id(k, ptab, pg_begin + (c0 + lane) * pg_step, pg_end);
     }
     auto id = [&](int o) { return o < cn ? __builtin_amdgcn_readlane(idv, o) : -1; };
+    auto pg_of = [&](int o) { return pg_begin + (c0 + o) * pg_step; };   // page index (token position / 32)
     // the loads of pages o and o + 1
     auto fetch = [&](PageRaw<BITS>& ra, PageRaw<BITS>& rb, int o) { load(ra, rb, id(o), id(o + 1)); };
     fetch(r0a, r0b, 0);
@@ -349,11 +442,13 @@ __device__ __forceinline__ void kivi_pages_wave(const KiviParams& k, int seq, in
     for (int o = 0; o < cn; o += 4) {
       fetch(r1a, r1b, o + 2);
       if (share_simd) __builtin_amdgcn_s_setprio(1);
-      page_pair(st, r0a, r0b, id(o) >= 0, id(o + 1) >= 0, qsc, qss, s_par_w, lane, slot_scale);
+      page_pair<BITS, ROPE>(st, r0a, r0b, id(o) >= 0, id(o + 1) >= 0, qsc, qss, s_par_w, lane, slot_scale, k,
+                            pg_of(o), pg_of(o + 1));
       if (o + 2 >= cn) break;
       fetch(r0a, r0b, o + 4);
       if (share_simd) __builtin_amdgcn_s_setprio(0);
-      page_pair(st, r1a, r1b, id(o + 2) >= 0, id(o + 3) >= 0, qsc, qss, s_par_w, lane, slot_scale);
+      page_pair<BITS, ROPE>(st, r1a, r1b, id(o + 2) >= 0, id(o + 3) >= 0, qsc, qss, s_par_w, lane, slot_scale, k,
+                            pg_of(o + 2), pg_of(o + 3));
     }
   }
 
@@ -427,6 +522,89 @@ __device__ __forceinline__ float wave_sum(float x) {
   return x;
 }
 
+// Replace 16-bit element e (0..7) of a 16-byte chunk.
+__device__ __forceinline__ void put_half(u32x4& c, int e, uint32_t v) {
+  const uint32_t sh = 16 * (e & 1), keep = ~(0xFFFFu << sh), ins = (v & 0xFFFFu) << sh;
+  const int w = e / 2;
+  c.x = w == 0 ? (c.x & keep) | ins : c.x;
+  c.y = w == 1 ? (c.y & keep) | ins : c.y;
+  c.z = w == 2 ? (c.z & keep) | ins : c.z;
+  c.w = w == 3 ? (c.w & keep) | ins : c.w;
+}
+
+// The window's keys held before RoPE (decode2_wave's hook): each of the
+// lane's 8 tokens rotated at its position.  Style 0 pairs rows 2 m and
+// 2 m + 1 (pair m), style 1 rows c and c + 64 (kr[j] and kr[j + 2]).
+struct KiviWindowRope {
+  static constexpr bool kActive = true;
+  const KiviParams& k;
+  template <int KP>
+  __device__ void operator()(u32x4 (&kr)[KP][2], int tok0, int dl) const {
+    static_assert(KP == 4, "head size 128");
+    auto get = [](const u32x4& c, int e) { return f16_to_f32(uint16_t(word(c, e >> 1) >> (16 * (e & 1)))); };
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int t = tok0 + e;
+      if (k.rope_style == 0) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          float c, sn, x0 = get(kr[j][0], e), x1 = get(kr[j][1], e);
+          rope_cs1(k, t, dl + 16 * j, c, sn);
+          rope_rotate(x0, x1, c, sn);
+          put_half(kr[j][0], e, f32_to_f16(x0));
+          put_half(kr[j][1], e, f32_to_f16(x1));
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int r = 0; r < 2; ++r) {
+            float c, sn, x0 = get(kr[j][r], e), x1 = get(kr[j + 2][r], e);
+            rope_cs1(k, t, 2 * (dl + 16 * j) + r, c, sn);
+            rope_rotate(x0, x1, c, sn);
+            put_half(kr[j][r], e, f32_to_f16(x0));
+            put_half(kr[j + 2][r], e, f32_to_f16(x1));
+          }
+      }
+    }
+  }
+};
+
+// The newest token's key (lane: channels 2 lane, 2 lane + 1) rotated at
+// position t, for its score only (the pool keeps it as given).
+__device__ __forceinline__ uint32_t rope_newest_key(const KiviParams& k, uint32_t kb, int t, int lane) {
+  float x_lo = f16_to_f32(uint16_t(kb)), x_hi = f16_to_f32(uint16_t(kb >> 16));
+  if (k.rope_style == 0) {
+    float c, sn;
+    rope_cs1(k, t, lane, c, sn);
+    rope_rotate(x_lo, x_hi, c, sn);
+  } else {
+    // pairs (c, c + 64): lane l < 32 holds the first of pairs 2 l, 2 l + 1,
+    // lane l + 32 the second
+    const auto sw = __builtin_amdgcn_permlane32_swap(kb, kb, false, false);
+    const uint32_t pb = lane < 32 ? (uint32_t)sw[1] : (uint32_t)sw[0];
+    const float p_lo = f16_to_f32(uint16_t(pb)), p_hi = f16_to_f32(uint16_t(pb >> 16));
+    const int i = 2 * (lane & 31);
+    float c0, s0, c1, s1;
+    rope_cs1(k, t, i, c0, s0);
+    rope_cs1(k, t, i + 1, c1, s1);
+    if (lane < 32) {
+      float a = x_lo, b = p_lo, a1 = x_hi, b1 = p_hi;
+      rope_rotate(a, b, c0, s0);
+      rope_rotate(a1, b1, c1, s1);
+      x_lo = a;
+      x_hi = a1;
+    } else {
+      float a = p_lo, b = x_lo, a1 = p_hi, b1 = x_hi;
+      rope_rotate(a, b, c0, s0);
+      rope_rotate(a1, b1, c1, s1);
+      x_lo = b;
+      x_hi = b1;
+    }
+  }
+  return uint32_t(f32_to_f16(x_lo)) | (uint32_t(f32_to_f16(x_hi)) << 16);
+}
+
 // The single-token state of the wavefront's q heads: max = the score
 // (log2 units), sum = 1, unnormalised output = V.
 __device__ __forceinline__ void newest_state(const Params& p, const NewestToken& t, int seq, int kvh, int hs,
@@ -447,16 +625,6 @@ __device__ __forceinline__ void newest_state(const Params& p, const NewestToken&
     s_acc_w[g * kKiviHead + 2 * lane] = f16_to_f32(uint16_t(t.v));
     s_acc_w[g * kKiviHead + 2 * lane + 1] = f16_to_f32(uint16_t(t.v >> 16));
   }
-}
-
-// Replace 16-bit element e (0..7) of a 16-byte chunk.
-__device__ __forceinline__ void put_half(u32x4& c, int e, uint32_t v) {
-  const uint32_t sh = 16 * (e & 1), keep = ~(0xFFFFu << sh), ins = (v & 0xFFFFu) << sh;
-  const int w = e / 2;
-  c.x = w == 0 ? (c.x & keep) | ins : c.x;
-  c.y = w == 1 ? (c.y & keep) | ins : c.y;
-  c.z = w == 2 ? (c.z & keep) | ins : c.z;
-  c.w = w == 3 ? (c.w & keep) | ins : c.w;
 }
 
 // The new token into the fp16 pool, by one wavefront holding its channels
@@ -522,7 +690,7 @@ struct KiviDecodeSmem {
 // Two wavefronts per SIMD (at most 256 registers, VGPRs and AGPRs together):
 // with 4-wavefront workgroups the compiler would otherwise take more and
 // halve the occupancy.
-template <int NW, bool FINAL, bool APPEND, int BITS>
+template <int NW, bool FINAL, bool APPEND, int BITS, bool ROPE>
 __global__ __launch_bounds__(NW * kWave, 2) void kivi_decode_kernel(KiviParams k) {
   using Smem = KiviDecodeSmem<NW>;
   using Build = KiviBuildSmem<BITS>;
@@ -583,7 +751,7 @@ __global__ __launch_bounds__(NW * kWave, 2) void kivi_decode_kernel(KiviParams k
     // us at batch 64).  The second half's page wavefronts take the higher
     // priority on every other page pair, so both progress together (55.5
     // and 58.5 us).
-    kivi_pages_wave<BITS>(k, seq, kvh, hs, pg0 + wave, pg1 - res_pages, page_waves, &sd.p[wave][0], &sd.acc[wave][0][0],
+    kivi_pages_wave<BITS, ROPE>(k, seq, kvh, hs, pg0 + wave, pg1 - res_pages, page_waves, &sd.p[wave][0], &sd.acc[wave][0][0],
                     &sd.m[wave][0], &sd.l[wave][0], FINAL && blockIdx.x >= gridDim.x / 2,
                     FINAL && page_waves == NW - 1, early_id);
   } else {
@@ -593,13 +761,21 @@ __global__ __launch_bounds__(NW * kWave, 2) void kivi_decode_kernel(KiviParams k
       nt = k.job.slots[seq] >= 0 ? newest_from_row(k.job, seq, kvh, lane) : newest_from_pool(p, seq, kvh, L - 1, lane);
     else
       nt = newest_from_pool(p, seq, kvh, L - 1, lane);
-    decode2_wave<Kind::F16, kKiviHead, 16>(p, seq, kvh, hs, lq, L - 1, 32, &sd.p[wave][0],
-                                           &sd.acc[wave][0][0], &sd.m[wave][0], &sd.l[wave][0]);
-    newest_state(p, nt, seq, kvh, hs, lane, &sd.acc[NW][0][0], &sd.m[NW][0], &sd.l[NW][0]);
+    if constexpr (ROPE) {
+      decode2_wave<Kind::F16, kKiviHead, 16>(p, seq, kvh, hs, lq, L - 1, 32, &sd.p[wave][0], &sd.acc[wave][0][0],
+                                             &sd.m[wave][0], &sd.l[wave][0], KiviWindowRope{k});
+      NewestToken ntr = nt;
+      ntr.k = rope_newest_key(k, nt.k, L - 1, lane);
+      newest_state(p, ntr, seq, kvh, hs, lane, &sd.acc[NW][0][0], &sd.m[NW][0], &sd.l[NW][0]);
+    } else {
+      decode2_wave<Kind::F16, kKiviHead, 16>(p, seq, kvh, hs, lq, L - 1, 32, &sd.p[wave][0],
+                                             &sd.acc[wave][0][0], &sd.m[wave][0], &sd.l[wave][0]);
+      newest_state(p, nt, seq, kvh, hs, lane, &sd.acc[NW][0][0], &sd.m[NW][0], &sd.l[NW][0]);
+    }
     // the token's store, at the end of the window, off the page wavefronts'
     // path (the window ends halfway through the launch)
     if constexpr (APPEND) store_newest(k.job, nt, seq, kvh, lane);
-    kivi_pages_wave<BITS>(k, seq, kvh, hs, pg1 - res_pages, pg1, 1, &sd.p[wave][0], &sd.acc[NW + 1][0][0],
+    kivi_pages_wave<BITS, ROPE>(k, seq, kvh, hs, pg1 - res_pages, pg1, 1, &sd.p[wave][0], &sd.acc[NW + 1][0][0],
                     &sd.m[NW + 1][0], &sd.l[NW + 1][0], false, false, -1);
   }
   __syncthreads();
@@ -607,17 +783,23 @@ __global__ __launch_bounds__(NW * kWave, 2) void kivi_decode_kernel(KiviParams k
                                                         &sd.acc[0][0][0], seq, kvh, hs, part, tid, NW * kWave);
 }
 
-template <int NW, bool FINAL, int BITS>
+template <int NW, bool FINAL, int BITS, bool ROPE>
 void launch_decode_bits(const KiviParams& k, bool append, unsigned grid, hipStream_t stream) {
   if (append)
-    hipLaunchKernelGGL((kivi_decode_kernel<NW, FINAL, true, BITS>), dim3(grid), dim3(NW * kWave), 0, stream, k);
+    hipLaunchKernelGGL((kivi_decode_kernel<NW, FINAL, true, BITS, ROPE>), dim3(grid), dim3(NW * kWave), 0, stream, k);
   else
-    hipLaunchKernelGGL((kivi_decode_kernel<NW, FINAL, false, BITS>), dim3(grid), dim3(NW * kWave), 0, stream, k);
+    hipLaunchKernelGGL((kivi_decode_kernel<NW, FINAL, false, BITS, ROPE>), dim3(grid), dim3(NW * kWave), 0, stream, k);
 }
 template <int NW, bool FINAL>
 void launch_decode(const KiviParams& k, bool append, int bits, unsigned grid, hipStream_t stream) {
-  if (bits == 8) launch_decode_bits<NW, FINAL, 8>(k, append, grid, stream);
-  else launch_decode_bits<NW, FINAL, 4>(k, append, grid, stream);
+  const bool rope = k.rope_cos != nullptr;
+  if (bits == 8) {
+    if (rope) launch_decode_bits<NW, FINAL, 8, true>(k, append, grid, stream);
+    else launch_decode_bits<NW, FINAL, 8, false>(k, append, grid, stream);
+  } else {
+    if (rope) launch_decode_bits<NW, FINAL, 4, true>(k, append, grid, stream);
+    else launch_decode_bits<NW, FINAL, 4, false>(k, append, grid, stream);
+  }
 }
 
 }  // namespace
@@ -640,6 +822,8 @@ int launch_kivi_decode(const KiviDecodeLaunch& a) {
   k.pages = (const uint8_t*)a.pages; k.page_tables = a.page_tables;
   k.max_pages_per_seq = a.max_pages_per_seq; k.num_pages = a.num_pages;
   k.residual_length = a.residual_length; k.partition_pages = a.partition_pages;
+  k.rope_cos = a.rope_cos; k.rope_sin = a.rope_sin;
+  k.rope_max_pos = a.rope_max_pos; k.rope_style = a.rope_style;
   // the step's append (token write, quantise-on-append) is fused into the
   // decode launch
   const bool append = a.append != nullptr;

@@ -74,6 +74,7 @@ class KiviDesc(ctypes.Structure):
         ("partition_pages", ctypes.c_int32),
         ("scale", ctypes.c_float),
         ("bits", ctypes.c_int32),
+        ("pre_rope_keys", ctypes.c_int32),
     ]
 
 
@@ -149,6 +150,10 @@ _SIG = {
     "tl_kivi_rope_step_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(KiviDesc), _I]),
     "tl_kivi_rope_decode_step": (ctypes.c_int, [ctypes.POINTER(KiviDesc)] + [_P] * 7 + [_I, _I] + [_P] * 7
                                  + [_I, _P, ctypes.c_size_t, _P]),
+    "tl_kivi_paged_attention_decode_pre_rope": (ctypes.c_int, [ctypes.POINTER(KiviDesc)] + [_P] * 8
+                                                + [_I, _P, _P, _I, _I, _P, ctypes.c_size_t, _P]),
+    "tl_kivi_decode_step_pre_rope": (ctypes.c_int, [ctypes.POINTER(KiviDesc)] + [_P] * 11
+                                     + [_I, _P, _P, _I, _I, _P, ctypes.c_size_t, _P]),
     "tl_kivi_apply_config": (ctypes.c_int, [ctypes.POINTER(KiviDesc), _I, _I, ctypes.c_char_p, ctypes.c_char_p, _I]),
 }
 
@@ -452,10 +457,11 @@ def kivi_quantized_len(seq_len, residual_length) -> int:
 
 
 def make_kivi_desc(q, k_cache, block_tables, page_tables, num_pages, num_kv_heads, scale, *,
-                   residual_length=128, gqa_map=GQA_GROUPED, partition_pages=0, bits=4):
+                   residual_length=128, gqa_map=GQA_GROUPED, partition_pages=0, bits=4, pre_rope_keys=False):
     S, H, D = q.shape
     d = KiviDesc()
     d.bits = bits
+    d.pre_rope_keys = int(bool(pre_rope_keys))
     d.num_seqs, d.num_heads, d.num_kv_heads, d.head_size = S, H, num_kv_heads, D
     d.block_size = k_cache.shape[3]
     d.max_blocks_per_seq, d.num_blocks = block_tables.shape[1], k_cache.shape[0]
@@ -517,6 +523,31 @@ def kivi_apply_config(desc, bits=8, residual_length=128, key_granularity="per_ch
     kg = None if key_granularity is None else key_granularity.encode()
     vg = None if value_granularity is None else value_granularity.encode()
     check(lib.tl_kivi_apply_config(ctypes.byref(desc), bits, residual_length, kg, vg, int(bool(pre_rope_keys))))
+
+
+def kivi_paged_attention_decode_pre_rope(desc, out, q, pages, page_tables, k_cache, v_cache, block_tables,
+                                         seq_lens, max_context_len, cos_table, sin_table, style, workspace=None,
+                                         stream=None):
+    """kivi_paged_attention_decode with the keys held before RoPE: each key rotated at its position
+    (token index) as it is scored; q is taken as given."""
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    check(lib.tl_kivi_paged_attention_decode_pre_rope(
+        ctypes.byref(desc), _ptr(out), _ptr(q), _ptr(pages), _ptr(page_tables), _ptr(k_cache),
+        _ptr(v_cache), _ptr(block_tables), _ptr(seq_lens), max_context_len, _ptr(cos_table), _ptr(sin_table),
+        cos_table.shape[0], style, _ptr(workspace), ws_bytes, _stream(stream)))
+
+
+def kivi_decode_step_pre_rope(desc, out, q, key, value, slot_mapping, pages, page_tables, k_cache, v_cache,
+                              block_tables, seq_lens, max_context_len, cos_table, sin_table, style,
+                              workspace=None, stream=None):
+    """kivi_decode_step with the keys held before RoPE (stored and quantised unrotated, rotated at
+    their positions as they are scored); q is taken as given."""
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    check(lib.tl_kivi_decode_step_pre_rope(
+        ctypes.byref(desc), _ptr(out), _ptr(q), _ptr(key), _ptr(value), _ptr(slot_mapping), _ptr(pages),
+        _ptr(page_tables), _ptr(k_cache), _ptr(v_cache), _ptr(block_tables), _ptr(seq_lens), max_context_len,
+        _ptr(cos_table), _ptr(sin_table), cos_table.shape[0], style, _ptr(workspace), ws_bytes,
+        _stream(stream)))
 
 
 def kivi_paged_attention_decode(desc, out, q, pages, page_tables, k_cache, v_cache, block_tables,
