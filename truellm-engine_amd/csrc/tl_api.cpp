@@ -974,10 +974,15 @@ int tl_chunked_prefill(const tl_prefill_desc* d, void* out, const void* q, const
   if (d->num_seqs == 0 || total_q == 0) return ok();
   if (max_q_len > total_q)
     return fail(TL_ERR_INVALID_ARGUMENT, "max_q_len=%d > total_q=%d", max_q_len, total_q);
+  // the kernel's row -> (query, head) map is exact below 2^22 tile rows
+  if ((int64_t)max_q_len * (d->num_heads / d->num_kv_heads) > (1 << 22) - 256)
+    return fail(TL_ERR_NOT_IMPLEMENTED, "max_q_len=%d x group=%d (built: below 2^22 rows per kv head)", max_q_len,
+                d->num_heads / d->num_kv_heads);
   if (!out || !q || !cu_q_lens || !k_cache || !v_cache || !block_tables || !seq_lens)
     return fail(TL_ERR_INVALID_ARGUMENT, "NULL pointer");
   if (!aligned16(q) || !aligned16(k_cache) || !aligned16(v_cache))
     return fail(TL_ERR_INVALID_ARGUMENT, "q and the pools must be 16-byte aligned");
+  if ((uintptr_t)out & 3) return fail(TL_ERR_INVALID_ARGUMENT, "out must be 4-byte aligned");
   tl::PrefillLaunch a;
   memset(&a, 0, sizeof a);
   a.out = out; a.q = q; a.cu_q_lens = cu_q_lens; a.k_cache = k_cache; a.v_cache = v_cache;

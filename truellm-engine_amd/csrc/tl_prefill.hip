@@ -194,6 +194,12 @@ __global__ __launch_bounds__(NW * kWave) void prefill_kernel(PrefillParams pp) {
   const int tile = pp.row_tiles - 1 - b / items;       // longest (latest) tiles first
   b %= items;
   const int seq = b / p.num_kv_heads, kvh = b % p.num_kv_heads;
+  // The first two table entries of the wavefront's key group (see the
+  // staging below) are read with the lengths, before the exits that
+  // depend on them: one memory round trip for both.
+  const TableRow table = (TableRow)(p.block_tables + (int64_t)seq * p.max_blocks_per_seq);
+  const int kg = 16 * (wave >> 1);                     // first key of the wavefront's group
+  const int e0 = table_entry(p, table, kg / BS), e1 = table_entry(p, table, BPI + kg / BS);
   const int q0 = pp.cu_q_lens[seq], ql = pp.cu_q_lens[seq + 1] - q0;
   const int L = p.seq_lens[seq];
   if (ql <= 0) return;
@@ -224,7 +230,6 @@ __global__ __launch_bounds__(NW * kWave) void prefill_kernel(PrefillParams pp) {
     // waited for at its first use: the prologue's K/V loads go out meanwhile
   }
 
-  const TableRow table = (TableRow)(p.block_tables + (int64_t)seq * p.max_blocks_per_seq);
   const int64_t head_stride = (int64_t)kPfHead * BS;                  // elements per (block, kv head)
   const uint16_t* kpool = (const uint16_t*)p.k_cache;
   const uint16_t* vpool = (const uint16_t*)p.v_cache;
@@ -237,7 +242,6 @@ __global__ __launch_bounds__(NW * kWave) void prefill_kernel(PrefillParams pp) {
   // key group is wave-uniform (descriptors in scalar registers).
   constexpr int kUnits = 2;                            // 32-channel units per wavefront
   static_assert(NW == 2 * (kPfKeys / 16) && kUnits * 32 * 2 == kPfHead, "key groups x channel halves");
-  const int kg = 16 * (wave >> 1);                     // first key of the wavefront's group
   const int tok = kg + 8 * g;                          // first key of the lane's 8
   auto unit_ch = [&](int u) { return 64 * (wave & 1) + 32 * u + c32; };
   // A phase's copy: K of one iteration and V of the one before (K is
@@ -285,7 +289,9 @@ __global__ __launch_bounds__(NW * kWave) void prefill_kernel(PrefillParams pp) {
       // too, and a zero weight times NaN is NaN): zero them
       u4v v = __builtin_bit_cast(u4v, f.v[u]);
       const int nv = f.nv;
-      if (nv < 8) {
+      // a wave-uniform branch (the sequence's last iteration only): as a
+      // lane-divergent one it became selects run on every iteration
+      if (__builtin_amdgcn_ballot_w64(nv < 8)) {
 #pragma unroll
         for (int w = 0; w < 4; ++w) v[w] = 2 * w >= nv ? 0u : (2 * w + 1 >= nv ? v[w] & 0xFFFFu : v[w]);
       }
@@ -353,22 +359,34 @@ __global__ __launch_bounds__(NW * kWave) void prefill_kernel(PrefillParams pp) {
   // until the exponent (qk_scale > 0, so the max commutes with the scale).
   const int wmin_pos = __builtin_amdgcn_readfirstlane(L - ql + wrow0 / p.group);
   const int pos_g = pos - 4 * g;
-  auto softmax = [&](int it, int t_entries) {
-    const int k0 = it * kPfKeys;
-    bool blk_ok[BPI];
+  // Iterations [0, j_plain) lie at or below the wavefront's first query
+  // position: without holes they need no mask.
+  const int j_plain = min(n_it, (wmin_pos + 1) / kPfKeys);
+  auto blocks_ok = [&](int it, int t_entries, bool (&blk_ok)[BPI]) {
     bool all_ok = true;
 #pragma unroll
     for (int bi = 0; bi < BPI; ++bi) {
       blk_ok[bi] = checked_block(p, it * BPI + bi, __builtin_amdgcn_readlane(t_entries, 2 + bi)) >= 0;
       all_ok = all_ok && blk_ok[bi];
     }
+    return all_ok;
+  };
+  // MASK false: an iteration below j_plain whose blocks all exist.  The two
+  // forms run in separate loops, so that no path merges scores (a masked
+  // and an unmasked form of the same scores in one loop body cost 16 64-bit
+  // register copies per iteration).
+  auto softmax = [&](int it, int t_entries, auto mask_tag) {
+    constexpr bool MASK = decltype(mask_tag)::value;
+    const int k0 = it * kPfKeys;
     float mx = -INFINITY;
-    if (all_ok && k0 + kPfKeys - 1 <= wmin_pos) {
+    if constexpr (!MASK) {
 #pragma unroll
       for (int t = 0; t < KT; ++t)
 #pragma unroll
         for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sp[t][r]);
     } else {
+      bool blk_ok[BPI];
+      blocks_ok(it, t_entries, blk_ok);
 #pragma unroll
       for (int t = 0; t < KT; ++t)
 #pragma unroll
@@ -454,7 +472,6 @@ __global__ __launch_bounds__(NW * kWave) void prefill_kernel(PrefillParams pp) {
     // they are waited for: K(0) is staged before the first barrier; group 1's
     // Y_{-1} stages K(1), V(0) (group 0 loads its own copy again in X_0,
     // unconditional so that the wait counts agree on every path)
-    const int e0 = table_entry(p, table, kg / BS), e1 = table_entry(p, table, BPI + kg / BS);
     Fetched f0;
     fetch(0, -1, e0, e0, f0);
     fetch(1, 0, e1, e0, fs);
@@ -549,8 +566,8 @@ __global__ __launch_bounds__(NW * kWave) void prefill_kernel(PrefillParams pp) {
   };
   // Y_j: SM(j) with the mask entries of step j and the staging of
   // K(j + 1 + grp), V(j + grp)
-  auto phase_y = [&](int j) {
-    softmax(j, t_mask);
+  auto phase_y = [&](int j, auto mask_tag) {
+    softmax(j, t_mask, mask_tag);
     // the weights are formed here: the exponentials and packing are plain
     // arithmetic, which the compiler would otherwise sink past the barrier
     // into the MFMA phase that reads them
@@ -568,9 +585,21 @@ __global__ __launch_bounds__(NW * kWave) void prefill_kernel(PrefillParams pp) {
   }
   phase_x0();
   __syncthreads();
+  // The loops differ per wavefront only in where one ends and the other
+  // begins: every wavefront passes the same barriers.
+  int j = 0;
 #pragma unroll 1
-  for (int j = 0; j < n_it; ++j) {
-    phase_y(j);
+  for (; j < j_plain; ++j) {
+    bool blk_ok[BPI];
+    if (!blocks_ok(j, t_mask, blk_ok)) break;          // a hole: the masked loop takes over
+    phase_y(j, std::false_type{});
+    __syncthreads();
+    phase_x(j);
+    __syncthreads();
+  }
+#pragma unroll 1
+  for (; j < n_it; ++j) {
+    phase_y(j, std::true_type{});
     __syncthreads();
     phase_x(j);
     __syncthreads();
@@ -587,18 +616,46 @@ __global__ __launch_bounds__(NW * kWave) void prefill_kernel(PrefillParams pp) {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  // Output row of tile row r = qr group + gr (query q0 + qr, head
+  // head_of(gr)), in 128-element rows: q0 H + kvh group + r + qr (H - group)
+  // for the grouped map, q0 H + kvh + r n_kv for the modulo map (H = group
+  // n_kv).  qr = floor((r + 1/2) / group) as an fp32 product, exact for
+  // r < 2^22 (the launch checks): the half step keeps the rounding off the
+  // integers.
+  const float rg = 1.f / (float)p.group;
+  const int64_t obase = (int64_t)q0 * p.num_heads + (p.gqa_map ? kvh * p.group : kvh);
+  const int rmul = p.gqa_map ? 1 : p.num_kv_heads, qmul = p.gqa_map ? p.num_heads - p.group : 0;
+  const bool odd = (c32 & 1) != 0;
+  // Two channels per 4-byte store: lanes 2k and 2k + 1 swap one value, so
+  // that for rows (i, i + 1) the even lane stores row i at channels c32,
+  // c32 + 1 and the odd lane row i + 1 at c32 - 1, c32.
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
+    float inv[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int rl = 8 * j + 4 * g + i, row = wrow0 + rl;
-      if (row >= rows) continue;
-      const float l = s_row[rl];
-      const float inv = l > 0.f ? PvScale<KV>::kP / l : 0.f;   // the sums carry 2^kPExp
-      const int qr = row / p.group, gr = row % p.group;
-      const int64_t base = ((int64_t)(q0 + qr) * p.num_heads + head_of(p, kvh, gr)) * kPfHead;
+      const float l = s_row[8 * j + 4 * g + i];
+      inv[i] = l > 0.f ? PvScale<KV>::kP * __builtin_amdgcn_rcpf(l) : 0.f;   // the sums carry 2^kPExp
+    }
 #pragma unroll
-      for (int c = 0; c < 4; ++c) store_scalar<KV>(p.out, base + 32 * c + c32, o[c][4 * j + i] * inv);
+    for (int ip = 0; ip < 4; ip += 2) {
+      const int row = wrow0 + 8 * j + 4 * g + ip + (odd ? 1 : 0);
+      const int qr = (int)(((float)row + 0.5f) * rg);
+      uint32_t* dst = reinterpret_cast<uint32_t*>(
+          (uint16_t*)p.out + (obase + (int64_t)row * rmul + (int64_t)qr * qmul) * kPfHead + (c32 & ~1));
+      uint32_t w[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const float a = o[c][4 * j + ip] * inv[ip], b2 = o[c][4 * j + ip + 1] * inv[ip + 1];
+        const float send = odd ? a : b2;
+        const float got = __builtin_bit_cast(
+            float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, send), 0xB1, 0xF, 0xF, false));  // quad_perm 1,0,3,2
+        w[c] = odd ? M::pack(got, b2) : M::pack(a, got);
+      }
+      if (row < rows) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) dst[16 * c] = w[c];
+      }
     }
   }
 }
