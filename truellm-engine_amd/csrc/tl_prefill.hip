@@ -220,15 +220,17 @@ __global__ __launch_bounds__(NW * kWave) void prefill_kernel(PrefillParams pp) {
   const int kend = __builtin_amdgcn_readfirstlane(max(0, L - ql + last_row / p.group + 1));
   const int n_it = (kend + kPfKeys - 1) / kPfKeys;
 
-  // B operand of S^T: row my_row, channels 16 ks + 8 g .. +7 (zero for padding rows)
+  // B operand of S^T: row my_row, channels 16 ks + 8 g .. +7.  Padding
+  // rows (past the tile's rows) load query q0's first head: their scores
+  // stay in their own columns and are never stored.  Loaded in the
+  // prologue after K(0), so that staging K(0) does not wait for them.
   u32x4 qb[8];
-  {
+  auto load_q = [&]() {
     const uint16_t* qrow = (const uint16_t*)p.q +
         ((int64_t)(q0 + qi) * p.num_heads + head_of(p, kvh, gi)) * kPfHead + 8 * g;
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) qb[ks] = row_ok ? load16(qrow + 16 * ks) : u32x4{0u, 0u, 0u, 0u};
-    // waited for at its first use: the prologue's K/V loads go out meanwhile
-  }
+    for (int ks = 0; ks < 8; ++ks) qb[ks] = load16(qrow + 16 * ks);
+  };
 
   const int64_t head_stride = (int64_t)kPfHead * BS;                  // elements per (block, kv head)
   const uint16_t* kpool = (const uint16_t*)p.k_cache;
@@ -467,13 +469,15 @@ __global__ __launch_bounds__(NW * kWave) void prefill_kernel(PrefillParams pp) {
   Fetched fs;
   int t_ent, t_mask = 0;
   {
-    // All of the prologue's loads go out together (q above, K(0), the copy
-    // of group 1's Y_{-1}, the first table entries), in the order in which
-    // they are waited for: K(0) is staged before the first barrier; group 1's
-    // Y_{-1} stages K(1), V(0) (group 0 loads its own copy again in X_0,
-    // unconditional so that the wait counts agree on every path)
+    // All of the prologue's loads go out together (K(0), q, the copy of
+    // group 1's Y_{-1}, the first table entries), in the order in which
+    // they are waited for: K(0) is staged before the first barrier, q is
+    // read by X_0; group 1's Y_{-1} stages K(1), V(0) (group 0 loads its own
+    // copy again in X_0, unconditional so that the wait counts agree on
+    // every path)
     Fetched f0;
     fetch(0, -1, e0, e0, f0);
+    load_q();
     fetch(1, 0, e1, e0, fs);
     t_ent = table_prefetch(0);
     stage(0, -1, f0);                   // K(0); V stage 1 gets zeros (iteration -1 is missing)
