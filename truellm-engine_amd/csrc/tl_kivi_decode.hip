@@ -59,18 +59,23 @@ __device__ __forceinline__ void rope_rotate(float& x0, float& x1, float c, float
   x1 = y1;
 }
 // cos / sin of pairs i .. i + 3 at position t (t past the tables: no
-// rotation).  i is a multiple of 4, the tables 16-byte aligned.
+// rotation).  i is a multiple of 4, the tables 16-byte aligned.  The loads
+// are unconditional (at a clamped position, then a select): a load under a
+// lane-divergent branch makes the compiler wait for every load in flight,
+// the page loads included.
 __device__ __forceinline__ void rope_cs4(const KiviParams& k, int t, int i, f4& c, f4& s) {
   const bool in = t >= 0 && t < k.rope_max_pos;
-  const int64_t o = (int64_t)(in ? t : 0) * (kKiviHead / 2) + i;
-  c = in ? *reinterpret_cast<const f4*>(k.rope_cos + o) : (f4){1.f, 1.f, 1.f, 1.f};
-  s = in ? *reinterpret_cast<const f4*>(k.rope_sin + o) : (f4){0.f, 0.f, 0.f, 0.f};
+  const int64_t o = (int64_t)min(max(t, 0), k.rope_max_pos - 1) * (kKiviHead / 2) + i;
+  const f4 cv = *reinterpret_cast<const f4*>(k.rope_cos + o), sv = *reinterpret_cast<const f4*>(k.rope_sin + o);
+  c = in ? cv : (f4){1.f, 1.f, 1.f, 1.f};
+  s = in ? sv : (f4){0.f, 0.f, 0.f, 0.f};
 }
 __device__ __forceinline__ void rope_cs1(const KiviParams& k, int t, int i, float& c, float& s) {
   const bool in = t >= 0 && t < k.rope_max_pos;
-  const int64_t o = (int64_t)(in ? t : 0) * (kKiviHead / 2) + i;
-  c = in ? k.rope_cos[o] : 1.f;
-  s = in ? k.rope_sin[o] : 0.f;
+  const int64_t o = (int64_t)min(max(t, 0), k.rope_max_pos - 1) * (kKiviHead / 2) + i;
+  const float cv = k.rope_cos[o], sv = k.rope_sin[o];
+  c = in ? cv : 1.f;
+  s = in ? sv : 0.f;
 }
 
 // Eight nibbles n_j (slot j at bit 16 (j & 1) + 4 (j >> 1)) as fp16
