@@ -76,6 +76,22 @@ typedef struct tl_decode_desc {
   float k_scale, v_scale;      /* FP8 dequant scales (x = code * scale); else ignored */
 } tl_decode_desc;
 
+/* CudaEngineConfig's attention knobs (config_schema.h:67-83) onto a decode
+ * descriptor whose other fields are filled: paged_kv_block_size (a power
+ * of two) goes to desc->block_size; use_fp8_kv != 0 makes the pool FP8 E4M3
+ * (desc->kv_dtype; k_scale / v_scale <= 0 become 1), 0 makes it q's type;
+ * attention_layout "paged" and "flash_paged" both name the pool layout
+ * [N, n_kv, head_size, block_size] these kernels read, which already run an
+ * online softmax with split-K (the library's plan unless
+ * desc->partition_tokens says otherwise).  Other layout strings, and
+ * combinations no kernel is built for, return TL_ERR_NOT_IMPLEMENTED; a
+ * block size that is not a power of two TL_ERR_INVALID_ARGUMENT.  A rejected
+ * call leaves the descriptor unchanged.  The reference parses these fields
+ * (src/host/config/config.cpp:110-134); its engine passes block_size to the
+ * kernels and reads neither use_fp8_kv nor attention_layout there. */
+int tl_engine_apply_config(tl_decode_desc* desc, int32_t paged_kv_block_size, int32_t use_fp8_kv,
+                           const char* attention_layout);
+
 /* Bytes of fp32 workspace tl_paged_attention_decode needs for split-K at
  * max_context_len (0 when it will run single pass). */
 size_t tl_paged_attention_workspace_bytes(const tl_decode_desc* desc, int32_t max_context_len);

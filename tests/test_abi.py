@@ -271,6 +271,33 @@ def test_kivi_page_bytes():
     assert tla.kivi_page_bytes(3) == 0 and tla.kivi_page_bytes(16) == 0
 
 
+def test_engine_apply_config_maps_cudaengineconfig():
+    """CudaEngineConfig (config_schema.h:67-83): paged_kv_block_size, use_fp8_kv
+    and attention_layout onto a decode descriptor.  Both layouts name the
+    [N, n_kv, d, bs] pool; a rejected call leaves the descriptor as it was."""
+    d = _desc(q_dtype=tla.BF16, kv_dtype=tla.BF16)
+    tla.engine_apply_config(d, block_size=32)
+    assert d.block_size == 32 and d.kv_dtype == tla.BF16
+    d.k_scale = d.v_scale = 0.0
+    tla.engine_apply_config(d, block_size=16, use_fp8_kv=True, attention_layout="flash_paged")
+    assert d.block_size == 16 and d.kv_dtype == tla.FP8_E4M3 and d.k_scale == 1.0 and d.v_scale == 1.0
+    tla.engine_apply_config(d, block_size=64, use_fp8_kv=False)
+    assert d.block_size == 64 and d.kv_dtype == tla.BF16
+    L = tla.lib
+    call = lambda bs, fp8, lay: L.tl_engine_apply_config(ctypes.byref(d), bs, fp8, lay)
+    assert call(48, 0, b"paged") == tla.ERR_INVALID_ARGUMENT           # not a power of two
+    assert call(0, 0, b"paged") == tla.ERR_INVALID_ARGUMENT
+    assert call(16, 0, b"flash") == tla.ERR_NOT_IMPLEMENTED
+    assert "attention_layout" in tla.last_error()
+    assert call(16, 0, None) == tla.ERR_NOT_IMPLEMENTED
+    assert call(512, 0, b"paged") == tla.ERR_NOT_IMPLEMENTED           # no kernel for block size 512
+    assert call(8, 1, b"paged") == tla.ERR_NOT_IMPLEMENTED             # FP8 needs block size >= 16
+    assert L.tl_engine_apply_config(None, 16, 0, b"paged") == tla.ERR_INVALID_ARGUMENT
+    assert d.block_size == 64 and d.kv_dtype == tla.BF16              # unchanged by the rejected calls
+    f32 = _desc(q_dtype=tla.F32, kv_dtype=tla.F32)
+    assert L.tl_engine_apply_config(ctypes.byref(f32), 16, 1, b"paged") == tla.ERR_NOT_IMPLEMENTED  # FP8 needs 2-byte q
+
+
 def test_kivi_apply_config_maps_kiviconfig_and_rejects_what_is_not_built():
     """KiviConfig (config_schema.h:122-129): bits, residual_length and
     pre_rope_keys land in the descriptor; the default granularities are the

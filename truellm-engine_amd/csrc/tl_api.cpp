@@ -156,6 +156,27 @@ int tl_abi_version(void) { return TL_ABI_VERSION; }
 
 const char* tl_last_error_string(void) { return g_err; }
 
+int tl_engine_apply_config(tl_decode_desc* desc, int32_t paged_kv_block_size, int32_t use_fp8_kv,
+                           const char* attention_layout) {
+  if (!desc) return fail(TL_ERR_INVALID_ARGUMENT, "desc is NULL");
+  if (paged_kv_block_size <= 0 || (paged_kv_block_size & (paged_kv_block_size - 1)))
+    return fail(TL_ERR_INVALID_ARGUMENT, "paged_kv_block_size=%d (a power of two)", paged_kv_block_size);
+  if (!attention_layout || (strcmp(attention_layout, "paged") != 0 && strcmp(attention_layout, "flash_paged") != 0))
+    return fail(TL_ERR_NOT_IMPLEMENTED, "attention_layout '%s' (built: paged, flash_paged)",
+                attention_layout ? attention_layout : "(null)");
+  tl_decode_desc d = *desc;
+  d.block_size = paged_kv_block_size;
+  d.kv_dtype = use_fp8_kv ? TL_DTYPE_FP8_E4M3 : d.q_dtype;
+  if (use_fp8_kv) {
+    if (!(d.k_scale > 0.f)) d.k_scale = 1.f;
+    if (!(d.v_scale > 0.f)) d.v_scale = 1.f;
+  }
+  const int rc = check_decode(&d);
+  if (rc) return rc;
+  *desc = d;
+  return ok();
+}
+
 size_t tl_paged_attention_workspace_bytes(const tl_decode_desc* desc, int32_t max_context_len) {
   if (check_decode(desc) != TL_OK || max_context_len < 0) return 0;
   int P, PT;

@@ -154,6 +154,7 @@ _SIG = {
                                                 + [_I, _P, _P, _I, _I, _P, ctypes.c_size_t, _P]),
     "tl_kivi_decode_step_pre_rope": (ctypes.c_int, [ctypes.POINTER(KiviDesc)] + [_P] * 11
                                      + [_I, _P, _P, _I, _I, _P, ctypes.c_size_t, _P]),
+    "tl_engine_apply_config": (ctypes.c_int, [ctypes.POINTER(DecodeDesc), _I, _I, ctypes.c_char_p]),
     "tl_kivi_apply_config": (ctypes.c_int, [ctypes.POINTER(KiviDesc), _I, _I, ctypes.c_char_p, ctypes.c_char_p, _I]),
 }
 
@@ -515,6 +516,13 @@ def kivi_rope_decode_step(desc, out, q, key, value, positions, cos_table, sin_ta
         _ptr(sin_table), cos_table.shape[0], style, _ptr(slot_mapping), _ptr(pages), _ptr(page_tables),
         _ptr(k_cache), _ptr(v_cache), _ptr(block_tables), _ptr(seq_lens), max_context_len, _ptr(workspace),
         ws_bytes, _stream(stream)))
+
+
+def engine_apply_config(desc, block_size=16, use_fp8_kv=False, attention_layout="paged"):
+    """CudaEngineConfig's attention knobs onto a decode descriptor (raises TLError for what is not
+    built; the descriptor is left as it was then)."""
+    lay = None if attention_layout is None else attention_layout.encode()
+    check(lib.tl_engine_apply_config(ctypes.byref(desc), block_size, int(bool(use_fp8_kv)), lay))
 
 
 def kivi_apply_config(desc, bits=8, residual_length=128, key_granularity="per_channel",
