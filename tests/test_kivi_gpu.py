@@ -446,6 +446,32 @@ def test_kivi_pre_rope_decode_matches_oracle(style, bits, pp):
         tla.kivi_paged_attention_decode(desc, out, qd, pages, ptd, kd, vd, btd, sld, max_ctx, ws)
 
 
+@pytest.mark.parametrize("H,n_kv", [(16, 8), (64, 8), (8, 8)])
+@pytest.mark.parametrize("gqa", [tla.GQA_GROUPED, tla.GQA_MODULO])
+def test_kivi_pre_rope_decode_group_sizes(H, n_kv, gqa):
+    """Keys held before RoPE with GQA groups of 2, 8 and 1 under both head
+    maps (halves style, INT4, the library's partition plan)."""
+    from test_oracle import rope_tables
+    kc = KiviCase(58, [700, 300, 2000], H=H, n_kv=n_kv)
+    pages_np = kc.oracle_pages()
+    cos_t, sin_t = rope_tables(4096, 128)
+    qd, kd, vd = dev(kc.q, orc.F16), dev(kc.k, orc.F16), dev(kc.v, orc.F16)
+    btd, sld, ptd = dev(kc.tables), dev(kc.lens), dev(kc.page_tables)
+    desc = kc.desc(qd, kd, btd, ptd, 0, gqa)
+    desc.pre_rope_keys = 1
+    max_ctx = int(kc.lens.max())
+    ws = torch.empty(max(16, tla.kivi_workspace_bytes(desc, max_ctx)), dtype=torch.uint8, device="cuda")
+    out = torch.full_like(qd, float("nan"))
+    print(f"case kivi pre-rope H={H} n_kv={n_kv} gqa={gqa}", flush=True)
+    tla.kivi_paged_attention_decode_pre_rope(desc, out, qd, torch.from_numpy(pages_np).cuda(), ptd, kd, vd, btd, sld,
+                                             max_ctx, dev(cos_t), dev(sin_t), tla.ROPE_HALVES, ws)
+    torch.cuda.synchronize()
+    omap = orc.GROUPED if gqa == tla.GQA_GROUPED else orc.MODULO
+    want = orc.kivi_paged_attention(kc.q, orc.F16, pages_np, kc.page_tables, kc.k, kc.v, kc.tables, kc.lens,
+                                    kc.n_kv, kc.R, kc.scale, omap, kc.bits, pre_rope=(cos_t, sin_t, tla.ROPE_HALVES))
+    assert_close(out, want, orc.F16, ATOL_KIVI, f"H={H} gqa={gqa}")
+
+
 @pytest.mark.parametrize("style,bits,through_rope_step", [(tla.ROPE_ADJACENT, 4, True), (tla.ROPE_HALVES, 8, True),
                                                           (tla.ROPE_HALVES, 4, False)])
 def test_kivi_pre_rope_step_matches_oracle_each_step(style, bits, through_rope_step):

@@ -116,6 +116,44 @@ def test_fp8_block_sizes(BS, q_code, pt):
     assert_close(out, ref, q_code, ATOL_FP8, f"fp8 bs={BS}")
 
 
+@pytest.mark.parametrize("BS,fp8,layout", [(32, False, "paged"), (8, False, "flash_paged"), (64, True, "flash_paged")])
+def test_engine_config_descriptor_decodes(BS, fp8, layout):
+    """A decode descriptor set up by tl_engine_apply_config (CudaEngineConfig's
+    paged_kv_block_size, use_fp8_kv, attention_layout), run against the
+    oracle: the mapping gives the kernels the block size and pool type the
+    pool was built with."""
+    lens = [1, 64, 700, 2049]
+    base = inputs.make_paged_case(150 + BS, len(lens), 32, 8, 128, BS, lens, orc.F32 if fp8 else orc.BF16, holes=1)
+    bt, sl = dev(base.tables), dev(base.seq_lens)
+    if fp8:
+        ks = float(np.abs(base.k_cache).max()) / 448.0
+        vs = float(np.abs(base.v_cache).max()) / 448.0
+        k_np = orc.f32_to_e4m3(base.k_cache, np.float32(1.0) / np.float32(ks))
+        v_np = orc.f32_to_e4m3(base.v_cache, np.float32(1.0) / np.float32(vs))
+        q_np = inputs.encode(orc.bits_to_f32(base.q, orc.F32), orc.BF16)
+        ref = orc.paged_attention(q_np, orc.BF16, k_np, v_np, orc.FP8, base.tables, base.seq_lens, 8, base.scale,
+                                  orc.GROUPED, 0, ks, vs)
+        q, k, v = dev(q_np, orc.BF16), torch.from_numpy(k_np).cuda(), torch.from_numpy(v_np).cuda()
+    else:
+        ref = _ref(base, tla.GQA_GROUPED)
+        q, k, v = dev(base.q, orc.BF16), dev(base.k_cache, orc.BF16), dev(base.v_cache, orc.BF16)
+    # a descriptor made for a bf16 pool at block size 16, then the engine's knobs
+    desc = tla.make_decode_desc(q, dev(np.zeros((1, 8, 128, 16), np.uint16), orc.BF16), bt, 8, base.scale,
+                                gqa_map=tla.GQA_GROUPED)
+    desc.num_blocks = base.k_cache.shape[0]
+    tla.engine_apply_config(desc, block_size=BS, use_fp8_kv=fp8, attention_layout=layout)
+    assert desc.block_size == BS and desc.kv_dtype == (tla.FP8_E4M3 if fp8 else tla.BF16)
+    if fp8:
+        desc.k_scale, desc.v_scale = ks, vs
+    max_ctx = int(base.seq_lens.max())
+    ws = torch.empty(max(16, tla.workspace_bytes(desc, max_ctx)), dtype=torch.uint8, device="cuda")
+    out = torch.full_like(q, float("nan"))
+    print(f"case engine config bs={BS} fp8={fp8} layout={layout}", flush=True)
+    tla.paged_attention_decode(desc, out, q, k, v, bt, sl, max_ctx, ws)
+    torch.cuda.synchronize()
+    assert_close(out, ref, orc.BF16, ATOL_FP8 if fp8 else ATOL, f"engine config bs={BS}")
+
+
 @pytest.mark.parametrize("D,code", [(80, orc.F16), (96, orc.F16), (80, orc.BF16), (96, orc.BF16),
                                     (64, orc.F32), (256, orc.F32), (64, orc.BF16), (256, orc.BF16)])
 @pytest.mark.parametrize("H,n_kv", [(8, 2), (4, 4)])
