@@ -27,7 +27,9 @@
 extern "C" {
 #endif
 
-#define TL_ABI_VERSION 1
+/* Version of this C ABI (tl_abi_version).  2: tl_kivi_desc gained
+ * pre_rope_keys (after bits), for the _pre_rope entry points. */
+#define TL_ABI_VERSION 2
 
 /* Mirrors truellm::ErrorCode (include/truellm/types.h:20-32). */
 typedef enum tl_status {

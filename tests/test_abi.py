@@ -16,7 +16,7 @@ def test_exports_every_declared_function():
 
 
 def test_abi_version():
-    assert tla.lib.tl_abi_version() == 1
+    assert tla.lib.tl_abi_version() == 2 == tla.ABI_VERSION
 
 
 def _desc(**kw):

@@ -167,6 +167,9 @@ def _hip_runtimes() -> set:
         return set()
 
 
+ABI_VERSION = 2           # TL_ABI_VERSION of include/tl_attn.h
+
+
 def _load() -> ctypes.CDLL:
     if not os.path.exists(LIB_PATH):
         raise RuntimeError(f"{LIB_PATH} is not built; run __graft_entry__.build() (make -C truellm-engine_amd)")
@@ -182,6 +185,9 @@ def _load() -> ctypes.CDLL:
         fn = getattr(lib, name)
         fn.restype = res
         fn.argtypes = args
+    # the structures above mirror include/tl_attn.h at this version
+    if lib.tl_abi_version() != ABI_VERSION:
+        raise RuntimeError(f"{LIB_PATH} has C ABI version {lib.tl_abi_version()}, this binding {ABI_VERSION}")
     return lib
 
 
