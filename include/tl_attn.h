@@ -107,6 +107,20 @@ int tl_paged_attention_decode(const tl_decode_desc* desc, void* out, const void*
                               int32_t max_context_len, void* workspace,
                               size_t workspace_bytes, void* stream);
 
+/* The engine's decode step in one call: reshape_and_cache of the step's
+ * token then paged attention (cuda_engine.cpp:1100-1166), with the result
+ * of tl_reshape_and_cache (tl_reshape_and_cache_fp8 for an FP8 pool, with
+ * desc's scales) followed by tl_paged_attention_decode, as two launches on
+ * the stream: key/value [S, n_kv, head_size] in the pool type (q's type for
+ * an FP8 pool), slot_mapping[s] the pool slot of position seq_lens[s] - 1
+ * (seq_lens are the lengths after the append; a negative slot writes
+ * nothing).  Workspace as tl_paged_attention_workspace_bytes. */
+int tl_paged_attention_decode_step(const tl_decode_desc* desc, void* out, const void* q, const void* key,
+                                   const void* value, const int32_t* slot_mapping, void* k_cache,
+                                   void* v_cache, const int32_t* block_tables, const int32_t* seq_lens,
+                                   int32_t max_context_len, void* workspace, size_t workspace_bytes,
+                                   void* stream);
+
 /* No counterpart in the reference.  tl_paged_attention_decode for callers
  * that cannot allocate device memory (code under HIP graph capture, tight
  * serving loops, harnesses that forbid hipMalloc): the split-K workspace is

@@ -271,6 +271,22 @@ def test_kivi_page_bytes():
     assert tla.kivi_page_bytes(3) == 0 and tla.kivi_page_bytes(16) == 0
 
 
+def test_decode_step_argument_checks():
+    """tl_paged_attention_decode_step checks the decode's arguments and its
+    own (the token's rows and slots) before any device work."""
+    L = tla.lib
+    d = _desc()
+    def call(key=FAKE, value=FAKE, slots=FAKE, desc=d):
+        return L.tl_paged_attention_decode_step(ctypes.byref(desc), FAKE, FAKE, key, value, slots, FAKE, FAKE, FAKE,
+                                                FAKE, 1024, FAKE, 1 << 30, None)
+    assert call(key=None) == tla.ERR_INVALID_ARGUMENT
+    assert call(value=None) == tla.ERR_INVALID_ARGUMENT
+    assert call(slots=None) == tla.ERR_INVALID_ARGUMENT
+    assert call(key=ctypes.c_void_p(0x1008)) == tla.ERR_INVALID_ARGUMENT      # not 16-byte aligned
+    assert call(desc=_desc(head_size=100)) == tla.ERR_NOT_IMPLEMENTED
+    assert call(key=None, desc=_desc(num_seqs=0)) == tla.OK
+
+
 def test_engine_apply_config_maps_cudaengineconfig():
     """CudaEngineConfig (config_schema.h:67-83): paged_kv_block_size, use_fp8_kv
     and attention_layout onto a decode descriptor.  Both layouts name the

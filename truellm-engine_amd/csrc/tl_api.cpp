@@ -184,11 +184,12 @@ size_t tl_paged_attention_workspace_bytes(const tl_decode_desc* desc, int32_t ma
   return ws_bytes(desc, P);
 }
 
-int tl_paged_attention_decode(const tl_decode_desc* desc, void* out, const void* q,
-                              const void* k_cache, const void* v_cache,
-                              const int32_t* block_tables, const int32_t* seq_lens,
-                              int32_t max_context_len, void* workspace, size_t workspace_bytes,
-                              void* stream) {
+// The decode, and with key non-null the step: the token's append to the
+// pools at slots[s], then the decode.
+static int decode_impl(const tl_decode_desc* desc, void* out, const void* q, const void* k_cache,
+                       const void* v_cache, const int32_t* block_tables, const int32_t* seq_lens,
+                       int32_t max_context_len, void* workspace, size_t workspace_bytes, void* stream,
+                       const void* key, const void* value, const int32_t* slots) {
   int rc = check_decode(desc);
   if (rc) return rc;
   if (max_context_len < 0) return fail(TL_ERR_INVALID_ARGUMENT, "max_context_len < 0");
@@ -197,6 +198,9 @@ int tl_paged_attention_decode(const tl_decode_desc* desc, void* out, const void*
     return fail(TL_ERR_INVALID_ARGUMENT, "NULL tensor pointer");
   if (!aligned16(k_cache) || !aligned16(v_cache))
     return fail(TL_ERR_INVALID_ARGUMENT, "k_cache/v_cache must be 16-byte aligned");
+  if (key && (!value || !slots)) return fail(TL_ERR_INVALID_ARGUMENT, "NULL key/value/slot_mapping");
+  if (key && (!aligned16(key) || !aligned16(value)))
+    return fail(TL_ERR_INVALID_ARGUMENT, "key/value must be 16-byte aligned");
   int P, PT;
   plan_partitions(desc, max_context_len, &P, &PT);
   tl::DecodeLaunch a = make_launch(desc, out, q, k_cache, v_cache, block_tables, seq_lens, stream);
@@ -213,7 +217,36 @@ int tl_paged_attention_decode(const tl_decode_desc* desc, void* out, const void*
     a.num_partitions = P;
     a.partition_tokens = PT;
   }
+  if (key) {
+    rc = desc->kv_dtype == TL_DTYPE_FP8_E4M3
+             ? tl_reshape_and_cache_fp8(key, value, desc->q_dtype, (uint8_t*)k_cache, (uint8_t*)v_cache, slots,
+                                        desc->num_seqs, desc->num_kv_heads, desc->head_size, desc->block_size,
+                                        desc->num_blocks, desc->k_scale, desc->v_scale, stream)
+             : tl_reshape_and_cache(key, value, (void*)k_cache, (void*)v_cache, slots, desc->num_seqs,
+                                    desc->num_kv_heads, desc->head_size, desc->block_size, desc->num_blocks,
+                                    desc->kv_dtype, stream);
+    if (rc) return rc;
+  }
   return run(a);
+}
+
+int tl_paged_attention_decode(const tl_decode_desc* desc, void* out, const void* q,
+                              const void* k_cache, const void* v_cache,
+                              const int32_t* block_tables, const int32_t* seq_lens,
+                              int32_t max_context_len, void* workspace, size_t workspace_bytes,
+                              void* stream) {
+  return decode_impl(desc, out, q, k_cache, v_cache, block_tables, seq_lens, max_context_len, workspace,
+                     workspace_bytes, stream, nullptr, nullptr, nullptr);
+}
+
+int tl_paged_attention_decode_step(const tl_decode_desc* desc, void* out, const void* q, const void* key,
+                                   const void* value, const int32_t* slot_mapping, void* k_cache, void* v_cache,
+                                   const int32_t* block_tables, const int32_t* seq_lens, int32_t max_context_len,
+                                   void* workspace, size_t workspace_bytes, void* stream) {
+  if (desc && desc->num_seqs > 0 && (!key || !value || !slot_mapping))
+    return fail(TL_ERR_INVALID_ARGUMENT, "NULL key/value/slot_mapping");
+  return decode_impl(desc, out, q, k_cache, v_cache, block_tables, seq_lens, max_context_len, workspace,
+                     workspace_bytes, stream, key, value, slot_mapping);
 }
 
 int tl_paged_attention_v1(void* out, const void* q, const void* k_cache, const void* v_cache,

@@ -154,6 +154,8 @@ _SIG = {
                                                 + [_I, _P, _P, _I, _I, _P, ctypes.c_size_t, _P]),
     "tl_kivi_decode_step_pre_rope": (ctypes.c_int, [ctypes.POINTER(KiviDesc)] + [_P] * 11
                                      + [_I, _P, _P, _I, _I, _P, ctypes.c_size_t, _P]),
+    "tl_paged_attention_decode_step": (ctypes.c_int, [ctypes.POINTER(DecodeDesc)] + [_P] * 9
+                                       + [_I, _P, ctypes.c_size_t, _P]),
     "tl_engine_apply_config": (ctypes.c_int, [ctypes.POINTER(DecodeDesc), _I, _I, ctypes.c_char_p]),
     "tl_kivi_apply_config": (ctypes.c_int, [ctypes.POINTER(KiviDesc), _I, _I, ctypes.c_char_p, ctypes.c_char_p, _I]),
 }
@@ -407,6 +409,17 @@ def make_decode_desc(q, k_cache, block_tables, num_kv_heads, scale, *, kv_dtype=
     d.partition_tokens = partition_tokens
     d.scale, d.k_scale, d.v_scale = scale, k_scale, v_scale
     return d
+
+
+def paged_attention_decode_step(desc: DecodeDesc, out, q, key, value, slot_mapping, k_cache, v_cache, block_tables,
+                                seq_lens, max_context_len, workspace=None, stream=None):
+    """reshape_and_cache of the step's token, then the decode (seq_lens after the append), in one
+    call; slot_mapping[s] is the slot of position seq_lens[s] - 1."""
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    check(lib.tl_paged_attention_decode_step(
+        ctypes.byref(desc), _ptr(out), _ptr(q), _ptr(key), _ptr(value), _ptr(slot_mapping), _ptr(k_cache),
+        _ptr(v_cache), _ptr(block_tables), _ptr(seq_lens), max_context_len, _ptr(workspace), ws_bytes,
+        _stream(stream)))
 
 
 def workspace_bytes(desc: DecodeDesc, max_context_len: int) -> int:
