@@ -548,8 +548,9 @@ int32_t tl_kivi_pass_runs(int32_t seq_len, int32_t n_kv_heads, int32_t head_dim,
  * seq_lens[s] - q_len + i and attends causally to keys 0 .. that position.
  * q_len == 1 rows are decode rows (a second kernel on the same stream).
  * head_size 128, block_size 16 or 32,
- * dtype F16 or BF16 for q, out and the pool.  max_q_len (host) bounds the
- * grid; max_q_len x (num_heads / num_kv_heads) must stay below 2^22 - 256
+ * dtype F16 or BF16 for q, out and the pool; q and the pools 16-byte
+ * aligned, out 4-byte aligned.  max_q_len (host) bounds the grid;
+ * max_q_len x (num_heads / num_kv_heads) must stay below 2^22 - 256
  * (TL_ERR_NOT_IMPLEMENTED otherwise). */
 typedef struct tl_prefill_desc {
   int32_t num_seqs;
