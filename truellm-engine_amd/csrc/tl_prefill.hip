@@ -704,7 +704,9 @@ __global__ __launch_bounds__(NW * kWave) void prefill_decode_kernel(PrefillParam
 
 template <Kind KV, int BS>
 int launch_prefill_t(const PrefillParams& pp, unsigned grid, hipStream_t stream) {
-  constexpr int NW = 8, NWD = 8;
+  // decode rows: 4 wavefronts per workgroup (8: 926.2 against 916.8 us per
+  // 4-chunk step at 32 rows of ctx 2048, 64/8 heads; 12 and 16 slower still)
+  constexpr int NW = 8, NWD = 4;
   const Params& p = pp.base;
   constexpr int GT = decode_row_heads<BS>();
   const unsigned dgrid = (unsigned)((pp.num_seqs - pp.dec_first) * p.num_kv_heads * ((p.group + GT - 1) / GT));
