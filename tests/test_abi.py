@@ -271,6 +271,32 @@ def test_kivi_page_bytes():
     assert tla.kivi_page_bytes(3) == 0 and tla.kivi_page_bytes(16) == 0
 
 
+def test_chunked_prefill_argument_checks():
+    """tl_chunked_prefill: the arguments its kernels assume, checked before
+    any device work (out 4-byte aligned: the epilogue stores two channels per
+    4-byte store; max_q_len x group below 2^22 - 256: the kernel's
+    row -> (query, head) map is exact only there)."""
+    L = tla.lib
+    def desc(**kw):
+        d = tla.PrefillDesc()
+        d.num_seqs, d.num_heads, d.num_kv_heads, d.head_size, d.block_size = 2, 32, 8, 128, 16
+        d.max_blocks_per_seq, d.num_blocks, d.dtype, d.gqa_map, d.num_prefill_seqs = 64, 256, tla.BF16, 1, 0
+        d.scale = 0.088
+        for k, v in kw.items():
+            setattr(d, k, v)
+        return d
+    def call(d, out=FAKE, total_q=1024, max_q=512):
+        return L.tl_chunked_prefill(ctypes.byref(d), out, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, total_q, max_q, None)
+    assert call(desc(), out=ctypes.c_void_p(0x1002)) == tla.ERR_INVALID_ARGUMENT
+    assert "4-byte" in tla.last_error()
+    big = (1 << 22) // 4                       # group 4: max_q_len x 4 reaches 2^22
+    assert call(desc(), total_q=big, max_q=big) == tla.ERR_NOT_IMPLEMENTED
+    assert call(desc(dtype=tla.F32)) == tla.ERR_NOT_IMPLEMENTED
+    assert call(desc(head_size=64)) == tla.ERR_NOT_IMPLEMENTED
+    assert call(desc(), max_q=2048) == tla.ERR_INVALID_ARGUMENT      # max_q_len > total_q
+    assert call(desc(scale=0.0)) == tla.ERR_INVALID_ARGUMENT
+
+
 def test_decode_step_argument_checks():
     """tl_paged_attention_decode_step checks the decode's arguments and its
     own (the token's rows and slots) before any device work."""
