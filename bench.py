@@ -676,7 +676,7 @@ def cpu_baseline(seconds, S_sample):
 def main():
     args = parse()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1"}))
+        print(json.dumps({"error": "bench.py measures one GPU: --gpus must be 1 (the multi-GPU plan is design only)"}))
         sys.exit(2)
 
     import torch
