@@ -675,3 +675,51 @@ def test_decode_step_equals_append_then_decode(H, R, pp, bits):
         runs.append((torch.stack(outs), pages.clone(), kd.clone(), vd.clone()))
     for a, b in zip(runs[0], runs[1]):
         assert torch.equal(a.view(torch.uint8), b.view(torch.uint8))
+
+
+@pytest.mark.parametrize("style,bits,pp", [(tla.ROPE_HALVES, 4, 0), (tla.ROPE_ADJACENT, 8, 4), (tla.ROPE_HALVES, 4, -1)])
+def test_pre_rope_step_equals_append_then_pre_rope_decode(style, bits, pp):
+    """Keys held before RoPE: tl_kivi_decode_step_pre_rope gives the bytes of
+    tl_kivi_append followed by tl_kivi_paged_attention_decode_pre_rope
+    (outputs, pages and pools), over 40 steps that complete pages; sequence
+    5 crosses the end of the 1024-position tables."""
+    from test_oracle import rope_tables
+    start = np.array([150, 159, 160, 191, 33, 1000], np.int32)
+    steps = 40
+    cos_t, sin_t = rope_tables(1024, 128)
+    runs = []
+    for fused in (False, True):
+        kc = KiviCase(59, start + steps, H=32, extra_blocks=1, bits=bits)
+        qd, kd, vd = dev(kc.q, orc.F16), dev(kc.k, orc.F16), dev(kc.v, orc.F16)
+        btd, ptd = dev(kc.tables), dev(kc.page_tables)
+        cos_d, sin_d = dev(cos_t), dev(sin_t)
+        pages = torch.zeros(kc.num_pages, kc.n_kv, kc.page_bytes, dtype=torch.uint8, device="cuda")
+        desc = kc.desc(qd, kd, btd, ptd, pp)
+        tla.kivi_build_pages(desc, kd, vd, btd, dev(start), ptd, pages, int(start.max()))
+        desc.pre_rope_keys = 1
+        rng = np.random.default_rng(12)
+        max_ctx = int(start.max()) + steps
+        ws = torch.empty(max(16, tla.kivi_workspace_bytes(desc, max_ctx)), dtype=torch.uint8, device="cuda")
+        lens = start.copy()
+        outs = []
+        print(f"case kivi pre-rope step equivalence style={style} bits={bits} pp={pp} fused={fused}", flush=True)
+        for _ in range(steps):
+            lens = lens + 1
+            pos = lens - 1
+            slots = dev((kc.tables[np.arange(kc.S), pos // 16] * 16 + pos % 16).astype(np.int32))
+            knew = dev(inputs.encode(rng.standard_normal((kc.S, kc.n_kv, 128), dtype=np.float32), orc.F16), orc.F16)
+            vnew = dev(inputs.encode(rng.standard_normal((kc.S, kc.n_kv, 128), dtype=np.float32), orc.F16), orc.F16)
+            sld = dev(lens)
+            out = torch.full_like(qd, float("nan"))
+            if fused:
+                tla.kivi_decode_step_pre_rope(desc, out, qd, knew, vnew, slots, pages, ptd, kd, vd, btd, sld, max_ctx,
+                                              cos_d, sin_d, style, ws)
+            else:
+                tla.kivi_append(desc, knew, vnew, kd, vd, slots, btd, sld, ptd, pages)
+                tla.kivi_paged_attention_decode_pre_rope(desc, out, qd, pages, ptd, kd, vd, btd, sld, max_ctx, cos_d,
+                                                         sin_d, style, ws)
+            outs.append(out)
+        torch.cuda.synchronize()
+        runs.append((torch.stack(outs), pages.clone(), kd.clone(), vd.clone()))
+    for a, b in zip(runs[0], runs[1]):
+        assert torch.equal(a.view(torch.uint8), b.view(torch.uint8))
