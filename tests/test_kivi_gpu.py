@@ -723,3 +723,61 @@ def test_pre_rope_step_equals_append_then_pre_rope_decode(style, bits, pp):
         runs.append((torch.stack(outs), pages.clone(), kd.clone(), vd.clone()))
     for a, b in zip(runs[0], runs[1]):
         assert torch.equal(a.view(torch.uint8), b.view(torch.uint8))
+
+
+@pytest.mark.parametrize("through_rope_step", [False, True])
+def test_pre_rope_step_graph_replay_matches_eager(through_rope_step):
+    """Keys held before RoPE: the step (tl_kivi_decode_step_pre_rope, or
+    tl_kivi_rope_decode_step with the flag: the q rotation launch, then the
+    step) captured in a HIP graph and replayed three times with eager work
+    between replays: every replay matches the eager step bit for bit.
+    Sequence 1 (159 -> 160 tokens) completes a page in the step."""
+    from test_oracle import rope_tables
+    start = np.array([700, 159, 2000, 129], np.int32)
+    kc = KiviCase(60, start + 1, extra_blocks=1)
+    qd, kd, vd = dev(kc.q, orc.F16), dev(kc.k, orc.F16), dev(kc.v, orc.F16)
+    btd, ptd = dev(kc.tables), dev(kc.page_tables)
+    pages = torch.zeros(kc.num_pages, kc.n_kv, kc.page_bytes, dtype=torch.uint8, device="cuda")
+    desc = kc.desc(qd, kd, btd, ptd)
+    tla.kivi_build_pages(desc, kd, vd, btd, dev(start), ptd, pages, int(start.max()))
+    desc.pre_rope_keys = 1
+    cos_t, sin_t = rope_tables(4096, 128)
+    cos_d, sin_d = dev(cos_t), dev(sin_t)
+    lens = start + 1
+    pos = lens - 1
+    slots = dev((kc.tables[np.arange(kc.S), pos // 16] * 16 + pos % 16).astype(np.int32))
+    posd = dev(pos.astype(np.int32))
+    rng = np.random.default_rng(16)
+    knew = dev(inputs.encode(rng.standard_normal((kc.S, kc.n_kv, 128), dtype=np.float32), orc.F16), orc.F16)
+    vnew = dev(inputs.encode(rng.standard_normal((kc.S, kc.n_kv, 128), dtype=np.float32), orc.F16), orc.F16)
+    sld = dev(lens)
+    max_ctx = int(lens.max())
+    ws = torch.empty(max(16, tla.kivi_rope_step_workspace_bytes(desc, max_ctx)), dtype=torch.uint8, device="cuda")
+    out = torch.zeros_like(qd)
+
+    def step(stream):
+        if through_rope_step:
+            tla.kivi_rope_decode_step(desc, out, qd, knew, vnew, posd, cos_d, sin_d, tla.ROPE_HALVES, slots, pages, ptd,
+                                      kd, vd, btd, sld, max_ctx, ws, stream)
+        else:
+            tla.kivi_decode_step_pre_rope(desc, out, qd, knew, vnew, slots, pages, ptd, kd, vd, btd, sld, max_ctx,
+                                          cos_d, sin_d, tla.ROPE_HALVES, ws, stream)
+
+    print(f"case kivi pre-rope graph replay rope_step={through_rope_step}", flush=True)
+    step(torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    eager, eager_pages = out.clone(), pages.clone()
+    graph = torch.cuda.CUDAGraph()
+    cap = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    with torch.cuda.graph(graph, stream=cap):
+        step(cap)
+    for _ in range(3):
+        out.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
+        assert torch.equal(pages, eager_pages)
+        step(torch.cuda.current_stream())            # eager work between replays
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
