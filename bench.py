@@ -376,7 +376,11 @@ def bench_rope(args):
     v = torch.randn(S, NKV, D, generator=g, device="cuda", dtype=torch.bfloat16)
     kc = torch.zeros(N, NKV, D, BS, device="cuda", dtype=torch.bfloat16)
     vc = torch.zeros_like(kc)
-    slots = (torch.arange(S, device="cuda", dtype=torch.int32) * (CTX // BS + 1)) * BS + CTX % BS
+    # sequence s owns ctx/bs + 1 blocks of the pool in a random order (as an
+    # allocator's free list hands them out), and position ctx lands in its last
+    nbs = CTX // BS + 1
+    tables = torch.randperm(N, generator=g, device="cuda").to(torch.int32).view(S, nbs).contiguous()
+    slots = (tables[:, CTX // BS] * BS + CTX % BS).contiguous()
     pos = torch.full((S,), CTX, device="cuda", dtype=torch.int32)
     i = torch.arange(D // 2, device="cuda", dtype=torch.float32)
     theta = torch.arange(8192, device="cuda", dtype=torch.float32)[:, None] / torch.pow(10000.0, 2 * i / D)
@@ -392,10 +396,7 @@ def bench_rope(args):
     # the append's full cost shows in the decode that follows it (lines the
     # append left partly written are written back during the decode): the
     # append + decode step against the decode alone, over the same pools
-    # (sequence s owns blocks s (ctx/bs + 1) .. +ctx/bs, ctx + 1 tokens)
-    nbs = CTX // BS + 1
-    tables = (torch.arange(S, device="cuda", dtype=torch.int32)[:, None] * nbs +
-              torch.arange(nbs, device="cuda", dtype=torch.int32)[None, :]).contiguous()
+    # (ctx + 1 tokens per sequence)
     sl = torch.full((S,), CTX + 1, dtype=torch.int32, device="cuda")
     out = torch.empty_like(q)
     desc = tla.make_decode_desc(q_out, kc, tables, NKV, 1.0 / math.sqrt(D), gqa_map=tla.GQA_GROUPED,
