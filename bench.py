@@ -88,6 +88,9 @@ def parse():
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--only", default="all", choices=["all", "bf16", "fp16", "kivi", "fp8", "config2b", "v2",
                                                      "prefill", "blocks", "rope", "vq", "norm"])
+    p.add_argument("--block-size", type=int, default=16, choices=[8, 16, 32, 64, 128, 256],
+                   help="block size of the bf16 / fp16 / FP8 decode pools (with --only bf16, fp16 or fp8; "
+                        "FP8 from 16)")
     p.add_argument("--no-graph", action="store_true",
                    help="launch the timed steps eagerly (for counter passes that cannot follow graphs)")
     p.add_argument("--copy-calibration", action="store_true",
@@ -679,6 +682,11 @@ def main():
     if args.gpus != 1:
         print(json.dumps({"error": "bench.py measures one GPU: --gpus must be 1 (the multi-GPU plan is design only)"}))
         sys.exit(2)
+    if args.block_size != 16 and (args.only not in ("bf16", "fp16", "fp8") or (args.only == "fp8" and args.block_size < 16)):
+        print(json.dumps({"error": "--block-size other than 16 applies to --only bf16, fp16 (8-256) or fp8 (16-256)"}))
+        sys.exit(2)
+    global BS
+    BS = args.block_size
 
     import torch
 
