@@ -147,13 +147,16 @@ int tl_paged_attention_v1(void* out, const void* q, const void* k_cache, const v
 
 /* Replaces paged_attention_v2 (paged_attention_v2.cu:176-251).  The caller
  * provides scratch exp_sums / max_logits [S, H, P] fp32 and tmp_out
- * [S, H, P, head_size] in dtype, P = ceil(max_context_len / (32 *
- * block_size)) (the engine's sizing, cuda_engine.cpp:276-285,1144), and
+ * [S, H, P, head_size] in dtype, with P at least the partition count of the
+ * reference kernel, (max_context_len / block_size + 31) / 32
+ * (paged_attention_v2.cu:196); the engine's ceil(max_context_len / (32 *
+ * block_size)) (cuda_engine.cpp:276-285,1144) is never less.  The caller
  * reads none of it afterwards.  The call runs the library's own plan (as
  * tl_paged_attention_decode with partition_tokens 0): single pass when the
  * batch fills the GPU, else split-K with fp32 partials kept in that scratch
- * (at most P * sizeof(dtype) / 4 partitions).  The scratch's contents after
- * the call are not the reference's partials. */
+ * (at most P * sizeof(dtype) / 4 partitions, P the reference kernel's
+ * count).  The scratch's contents after the call are not the reference's
+ * partials. */
 int tl_paged_attention_v2(void* out, float* exp_sums, float* max_logits, void* tmp_out,
                           const void* q, const void* k_cache, const void* v_cache,
                           const int32_t* block_tables, const int32_t* seq_lens,

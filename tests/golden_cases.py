@@ -141,3 +141,31 @@ def kivi_page_tokens():
 
 KIVI_VEC_PARAMS = [(128, 8, 16), (64, 4, 16)]
 ATTENTION_SCALE = 1 / math.sqrt(128)
+
+
+# ---- KIVI vector codec: known answers derived by hand ---------------------
+
+# Records whose outliers the reference writes in selection-slot order
+# (kivi_cache.cu:50-60 replaces the first minimum of the slot array, strict
+# '>' on |x|; :73-78 write the slots in array order), derived by hand.
+KIVI_SLOT_ORDER_CASES = [
+    # x = [1, 5, 7, 0.5], O = 2, G = 2.  Scan: d0 -> slot 0 (min now slot 1
+    # at -1); d1 -> slot 1 (min slot 0 = 1); d2 (7 > 1) replaces slot 0;
+    # d3 (0.5 < 5) stays out.  Slots: (2, 7), (1, 5): neither channel order
+    # (1, 2) nor magnitude order (2, 1) read the other way.  Residual
+    # channels 0, 3 = [1, 0.5]: gmin 0.5, range 0.5, scale 30 -> codes 15, 0
+    # (byte 0x0F); step fp16(1/30) = 0x2844, zero fp16(0.5) = 0x3800.
+    ([1.0, 5.0, 7.0, 0.5], 2, 2,
+     [0x02, 0x00, 0x47, 0x01, 0x00, 0x45, 0x0F, 0x44, 0x28, 0x00, 0x38]),
+    # x = [3, 1, 4, 1.5, -5, 3], O = 3, G = 2.  Scan: d0 slot 0, d1 slot 1,
+    # d2 slot 2 (min slot 1 = 1); d3 (1.5 > 1) replaces slot 1 mid-scan
+    # (min slot 1 = 1.5); d4 (|-5| > 1.5) replaces slot 1 again (min slot 0
+    # = 3); d5 (3, a tie with the minimum) stays out.  Slots: (0, 3), (4, -5),
+    # (2, 4): channel order would be 0, 2, 4 and magnitude order 4, 2, 0.
+    # Residual channels 1, 3, 5 = [1, 1.5, 3]: group [1, 1.5] -> scale 30,
+    # codes 0, 15 (0xF0), step 0x2844, zero fp16(1) = 0x3C00; group [3]
+    # (one channel, degenerate) -> code 0, step 0, zero fp16(3) = 0x4200.
+    ([3.0, 1.0, 4.0, 1.5, -5.0, 3.0], 3, 2,
+     [0x00, 0x00, 0x42, 0x04, 0x00, 0xC5, 0x02, 0x00, 0x44,
+      0xF0, 0x44, 0x28, 0x00, 0x3C, 0x00, 0x00, 0x00, 0x00, 0x42]),
+]

@@ -246,6 +246,63 @@ def test_full_size_single_pass_equals_split_k_and_spot_checks():
         assert_close(outs[-1][s:s + 1].to(torch.bfloat16), ref, orc.BF16, ATOL, f"seq {s}")
 
 
+def _oracle_one_sequence(q, k, v, tables, s, L, n_kv, scale, code):
+    """The oracle on sequence s alone: its blocks gathered into a small pool."""
+    nb = (L + k.shape[3] - 1) // k.shape[3]
+    blocks = tables[s, :nb].tolist()
+    sub_k = k[blocks].contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+    sub_v = v[blocks].contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+    qs = q[s:s + 1].contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+    return orc.paged_attention(qs, code, sub_k, sub_v, code, np.arange(nb, dtype=np.int32)[None],
+                               np.array([L], np.int32), n_kv, scale, orc.GROUPED)
+
+
+def test_full_batch_variable_lengths_every_plan_against_oracle():
+    """The variable-length workload at its full size: batch 64, lengths
+    uniform in [512, 8192], 32/8 heads, d 128, bs 16, bf16, tables a shuffled
+    1.25x pool.  The library's own plan (4 partitions of 2048 tokens at this
+    batch), the reference's 512-token partitions and single pass all agree,
+    and 16 sequences spread over the batch (every fourth, the longest and the
+    shortest among them) match the oracle under each plan."""
+    S, H, n_kv, D, BS = 64, 32, 8, 128, 16
+    lens = inputs.uniform_lens(inputs.SEEDS[1], S, 512, 8192)
+    nbs = (lens + BS - 1) // BS
+    N = math.ceil(1.25 * int(nbs.sum()))
+    g = torch.Generator(device="cuda").manual_seed(inputs.SEEDS[1] + 2)
+    perm = torch.randperm(N, generator=g, device="cuda").to(torch.int32)
+    M = int(nbs.max())
+    tables = torch.full((S, M), -1, dtype=torch.int32, device="cuda")
+    off = 0
+    for s in range(S):
+        tables[s, : nbs[s]] = perm[off: off + nbs[s]]
+        off += int(nbs[s])
+    k = torch.randn(N, n_kv, D, BS, generator=g, device="cuda").to(torch.bfloat16)
+    v = torch.randn(N, n_kv, D, BS, generator=g, device="cuda").to(torch.bfloat16)
+    q = torch.randn(S, H, D, generator=g, device="cuda").to(torch.bfloat16)
+    sl = torch.tensor(lens, dtype=torch.int32, device="cuda")
+    scale = 1 / math.sqrt(D)
+    max_ctx = int(lens.max())
+    outs = {}
+    for pt in (0, 512, -1):
+        desc = tla.make_decode_desc(q, k, tables, n_kv, scale, partition_tokens=pt)
+        if pt == 0:
+            assert tla.workspace_bytes(desc, max_ctx) == S * H * 4 * (D + 2) * 4   # 4 partitions
+        ws = torch.empty(max(16, tla.workspace_bytes(desc, max_ctx)), dtype=torch.uint8, device="cuda")
+        out = torch.full_like(q, float("nan"))
+        print(f"case full-batch variable lengths pt={pt}", flush=True)
+        tla.paged_attention_decode(desc, out, q, k, v, tables, sl, max_ctx, ws)
+        torch.cuda.synchronize()
+        outs[pt] = out
+    for pt in (512, -1):
+        assert (outs[pt].float() - outs[0].float()).abs().max().item() <= 2 * ATOL
+    picks = sorted(set(range(0, S, 4)) | {int(np.argmax(lens)), int(np.argmin(lens))})
+    tb = tables.cpu().numpy()
+    for s in picks:
+        ref = _oracle_one_sequence(q, k, v, tb, s, int(lens[s]), n_kv, scale, orc.BF16)
+        for pt, out in outs.items():
+            assert_close(out[s:s + 1], ref, orc.BF16, ATOL, f"seq {s} L={lens[s]} pt={pt}")
+
+
 @pytest.mark.parametrize("pt", [-1, 512])
 def test_decode_graph_replay_matches_eager(pt):
     """Decode (single pass and split-K + reduce) captured in a HIP graph and

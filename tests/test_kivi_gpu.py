@@ -9,6 +9,7 @@ import numpy as np
 import pytest
 import torch
 
+import golden_cases
 import inputs
 import oracle_lib as orc
 import tl_attn as tla
@@ -58,6 +59,23 @@ def test_vector_codec_bit_exact(D, O, G):
     tla.kivi_decompress(rec, back, n, D, O, G)
     torch.cuda.synchronize()
     assert np.array_equal(host_bits(back).ravel(), orc.kivi_decompress(want, n, D, O, G))
+
+
+def test_vector_codec_hand_derived_slot_order():
+    """The kernel writes the outliers in the reference's selection-slot order
+    (kivi_cache.cu:50-78), byte for byte against records derived by hand
+    (not by the oracle): O = 2 and O = 3 with a mid-scan replacement, a
+    negative outlier and a tie with the running minimum."""
+    for x, O, G, want in golden_cases.KIVI_SLOT_ORDER_CASES:
+        D = len(x)
+        print(f"case vec codec hand-derived D={D} O={O} G={G}", flush=True)
+        rec = torch.full((len(want),), 0xAB, dtype=torch.uint8, device="cuda")
+        tla.kivi_compress(dev(_f16(x).reshape(1, D), orc.F16), rec, 1, D, O, G)
+        back = torch.zeros(1, D, dtype=torch.float16, device="cuda")
+        tla.kivi_decompress(rec, back, 1, D, O, G)
+        torch.cuda.synchronize()
+        assert [int(b) for b in rec.cpu().numpy()] == want
+        assert back.float().cpu().numpy().ravel().tolist() == x
 
 
 def test_vector_codec_reference_roundtrips():

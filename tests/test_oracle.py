@@ -19,6 +19,7 @@ import numpy as np
 import pytest
 import torch
 
+import golden_cases
 import inputs
 import oracle_lib as orc
 
@@ -402,6 +403,18 @@ def test_kivi_hand_derived_record():
     assert list(rec) == [0x01, 0x00, 0xC2, 0x05, 0x0F, 0x66, 0x2E, 0x00, 0x38]
     back = orc.kivi_decompress(rec, 1, 4, 1, 4).view(np.float16).astype(np.float32)
     assert list(back) == [1.0, -3.0, 0.5, 2.0]
+
+
+@pytest.mark.parametrize("x,O,G,want", golden_cases.KIVI_SLOT_ORDER_CASES)
+def test_kivi_hand_derived_records_keep_slot_order(x, O, G, want):
+    D = len(x)
+    assert orc.kivi_compressed_bytes(D, O, G) == len(want)
+    rec = orc.kivi_compress(_f16(x), D, O, G)
+    assert [int(b) for b in rec] == want
+    back = orc.kivi_decompress(rec, 1, D, O, G).view(np.float16).astype(np.float32)
+    # outliers verbatim; residual codes 0 / 15 at step 1/30 land within one
+    # fp16 ulp of the inputs (1 + 15 * fp16(1/30) = 1.49988 -> fp16 1.5)
+    assert list(back) == x
 
 
 def test_kivi_quant_group_nibbles_follow_rne():

@@ -225,16 +225,20 @@ def test_merge_of_more_than_256_partitions():
 GUARD = 4096
 
 
-def _v2_guarded(case, code, stream=None):
-    """tl_paged_attention_v2 with the engine's scratch sizes followed by
-    sentinel guards; returns (out, guards intact)."""
+def _v2_guarded(case, code, stream=None, kernel_sizing=False):
+    """tl_paged_attention_v2 with the engine's scratch sizes (or, with
+    kernel_sizing, the partition count the reference kernel itself writes,
+    paged_attention_v2.cu:196) followed by sentinel guards; returns (out,
+    guards intact)."""
     q, k, v, bt, sl = (dev(case.q, code), dev(case.k_cache, code), dev(case.v_cache, code), dev(case.tables),
                        dev(case.seq_lens))
     S, H, D = q.shape
     BS = k.shape[3]
     max_ctx = int(case.seq_lens.max())
-    P = tla.v2_num_partitions(max_ctx, BS)
+    P = (max_ctx // BS + 31) // 32 if kernel_sizing else tla.v2_num_partitions(max_ctx, BS)
     n = S * H * P
+    if n == 0:
+        n = 1
     es = torch.full((n + GUARD,), 7.25, dtype=torch.float32, device="cuda")
     ml = torch.full((n + GUARD,), -3.5, dtype=torch.float32, device="cuda")
     tmp = torch.full((n * D + GUARD,), 1.5, dtype=q.dtype, device="cuda")
@@ -274,6 +278,24 @@ def test_v2_split_k_stays_inside_the_callers_scratch(lens, code, BS):
     case = inputs.make_paged_case(110 + len(lens), len(lens), 32, 8, D, BS, lens, code)
     print(f"case v2 lens={lens} code={code} bs={BS}", flush=True)
     out, intact = _v2_guarded(case, code)
+    assert intact, "v2 wrote past the caller's scratch"
+    assert_close(out, _ref(case, orc.MODULO), code, ATOL, f"v2 {lens}")
+
+
+@pytest.mark.parametrize("lens,code,BS", [
+    ([1541], orc.F16, 16),            # engine count 4, kernel count 3
+    ([1541, 900], orc.F16, 16),
+    ([1537, 17], orc.BF16, 16),       # 4 against 3
+    ([1030], orc.F16, 32),            # 2 against 1: a single fp32 slot, single pass
+    ([4111], orc.F32, 16),            # 9 against 8, 4-byte tmp_out
+])
+def test_v2_stays_inside_scratch_sized_by_the_reference_kernel(lens, code, BS):
+    """A caller that sizes exp_sums / max_logits / tmp_out by the partition
+    count of the reference kernel, (max_ctx / bs + 31) / 32, which is one
+    less than the engine's ceiling count at these lengths."""
+    case = inputs.make_paged_case(130 + len(lens), len(lens), 32, 8, 128, BS, lens, code)
+    print(f"case v2 kernel-sized scratch lens={lens} code={code} bs={BS}", flush=True)
+    out, intact = _v2_guarded(case, code, kernel_sizing=True)
     assert intact, "v2 wrote past the caller's scratch"
     assert_close(out, _ref(case, orc.MODULO), code, ATOL, f"v2 {lens}")
 

@@ -116,3 +116,61 @@ def test_noalloc_fp8_and_single_pass():
     tla.paged_attention_decode(desc, b, q, k, v, bt, sl, 100)
     torch.cuda.synchronize()
     assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
+# A fresh process whose first call of the library on the GPU is
+# tl_paged_attention_decode_noalloc inside a stream capture: the scratch
+# address lookup happens there.  The graph is replayed three times with eager
+# work between, each replay checked bit for bit against the caller-workspace
+# entry point run eagerly after the capture.
+_FIRST_CALL_IN_CAPTURE = r"""
+import sys
+sys.path[:0] = sys.argv[1:3]
+import torch
+import inputs
+import oracle_lib as orc
+import tl_attn as tla
+from gpu_util import dev
+
+torch.cuda.set_device(0)
+case = inputs.make_paged_case(79, 8, 32, 8, 128, 16, [4096, 3000, 1, 700, 1025, 2048, 5, 4000], orc.BF16,
+                              holes=2)
+q, k, v = dev(case.q, orc.BF16), dev(case.k_cache, orc.BF16), dev(case.v_cache, orc.BF16)
+bt, sl = dev(case.tables), dev(case.seq_lens)
+max_ctx = int(case.seq_lens.max())
+desc = tla.make_decode_desc(q, k, bt, 8, case.scale, gqa_map=tla.GQA_GROUPED, partition_tokens=512)
+assert tla.workspace_bytes(desc, max_ctx) > 0
+out = torch.zeros_like(q)
+torch.cuda.synchronize()
+graph = torch.cuda.CUDAGraph()
+cap = torch.cuda.Stream()
+print("case noalloc first call inside a stream capture", flush=True)
+with torch.cuda.graph(graph, stream=cap):
+    tla.paged_attention_decode_noalloc(desc, out, q, k, v, bt, sl, max_ctx, cap)
+ws = torch.empty(tla.workspace_bytes(desc, max_ctx), dtype=torch.uint8, device="cuda")
+want = torch.full_like(q, float("nan"))
+tla.paged_attention_decode(desc, want, q, k, v, bt, sl, max_ctx, ws)
+torch.cuda.synchronize()
+for i in range(3):
+    out.zero_()
+    graph.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), want.view(torch.int16)), f"replay {i}"
+    tla.paged_attention_decode_noalloc(desc, out, q, k, v, bt, sl, max_ctx)   # eager, between replays
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), want.view(torch.int16)), f"eager {i}"
+print("first-call capture ok", flush=True)
+"""
+
+
+@pytest.mark.gpu
+def test_noalloc_first_call_inside_stream_capture():
+    import os
+    import subprocess
+    import sys
+    here = os.path.dirname(os.path.abspath(__file__))
+    pkg = os.path.join(os.path.dirname(here), "truellm-engine_amd")
+    r = subprocess.run([sys.executable, "-c", _FIRST_CALL_IN_CAPTURE, here, pkg], capture_output=True,
+                       text=True, timeout=300)
+    print(r.stdout[-2000:], r.stderr[-4000:], flush=True)
+    assert r.returncode == 0 and "first-call capture ok" in r.stdout

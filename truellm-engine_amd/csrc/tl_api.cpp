@@ -284,17 +284,20 @@ int tl_paged_attention_v2(void* out, float* exp_sums, float* max_logits, void* t
     return fail(TL_ERR_INVALID_ARGUMENT, "NULL tensor pointer");
   if (!aligned16(k_cache) || !aligned16(v_cache))
     return fail(TL_ERR_INVALID_ARGUMENT, "k_cache/v_cache must be 16-byte aligned");
-  // The caller's scratch holds Pc = ceil(max_context_len / (32 block_size))
-  // partitions (the engine's sizing, cuda_engine.cpp:273-285,1144):
-  // exp_sums / max_logits fp32 [S, H, Pc], tmp_out [S, H, Pc, head_size]
-  // in the call's dtype.  The engine reads none of it after the call, so
-  // it is used as the workspace of the library's own plan: fp32 partials,
-  // the (max, sum) pairs in max_logits / exp_sums and the partial outputs
-  // in tmp_out's bytes, which hold Pc * elem / 4 fp32 partitions.  Where the
-  // plan wants more partitions than that, they are made longer; where it
-  // wants one (a large batch), the call runs single pass.
-  const int64_t part_tokens = 32LL * block_size;
-  const int Pc = max_context_len > 0 ? (int)((max_context_len + part_tokens - 1) / part_tokens) : 1;
+  // The caller's scratch holds Pc partitions: exp_sums / max_logits fp32
+  // [S, H, Pc], tmp_out [S, H, Pc, head_size] in the call's dtype.  The
+  // engine sizes it as ceil(max_context_len / (32 block_size))
+  // (cuda_engine.cpp:273-285,1144); the reference kernel writes
+  // (max_context_len / block_size + 31) / 32 partitions
+  // (paged_attention_v2.cu:196), which is never more, so a caller that
+  // sized the scratch for the reference kernel has at least that many and
+  // Pc is taken as that count.  The engine reads none of it after the call,
+  // so it is used as the workspace of the library's own plan: fp32
+  // partials, the (max, sum) pairs in max_logits / exp_sums and the partial
+  // outputs in tmp_out's bytes, which hold Pc * elem / 4 fp32 partitions.
+  // Where the plan wants more partitions than that, they are made longer;
+  // where it wants one (a large batch), the call runs single pass.
+  const int Pc = (max_context_len / block_size + 31) / 32;
   const int elem = dtype == TL_DTYPE_F32 ? 4 : 2;
   const int cap = aligned16(tmp_out) ? Pc * elem / 4 : 1;
   int P, PT;
