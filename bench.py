@@ -638,41 +638,160 @@ def cpu_info():
     return info
 
 
-def cpu_baseline(seconds, S_sample):
-    """The oracle's fp32 decode (threads over (sequence, kv head)) on a
-    sample of the headline batch, timed on one thread and on all the cores
-    of this GPU's CPU share; median of the timed runs, each config run for
-    about `seconds`."""
+def _median_time(fn, seconds, min_runs=5, warm=2):
+    """Median wall time of fn() over at least min_runs runs (and about
+    `seconds` in all) after `warm` untimed runs."""
     import statistics
+    for _ in range(warm):
+        fn()
+    times = []
+    while sum(times) < seconds or len(times) < min_runs:
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times), len(times)
+
+
+def _host_u16(t):
+    import numpy as np
+    return t.contiguous().view(__import__("torch").int16).cpu().numpy().view(np.uint16)
+
+
+def cpu_baseline(seconds):
+    """The CPU path timed on the host cores beside the GPU, one entry per
+    decode workload: the oracle's fp32 decode (threads over (sequence, kv
+    head)) for the fp16 batch-4 workload (full size), the bf16 headline
+    (full size) and the FP8 long-context step (full size), and its fp32
+    paged-KIVI decode for the KIVI INT4 step (full size, one decode step).
+    Each runs on all the cores of this GPU's CPU share over the whole batch
+    and on one thread over a bounded sample of sequences; median of at least
+    5 runs after 2 untimed ones.  Inputs are generated as the GPU lines'
+    (same shapes, seeds and distributions; the large pools on the GPU, then
+    copied to the host)."""
+    import numpy as np
+    import torch
 
     import inputs
     import oracle_lib as orc
+    import tl_attn as tla
 
     info = cpu_info()
-    lens = [CTX] * S_sample
-    case = inputs.make_paged_case(inputs.SEEDS[1], S_sample, H, NKV, D, BS, lens, orc.BF16)
-    nbytes = algorithmic_bytes(lens, 2)
+    ncore = info["threads_all_cores"]
+    budget = max(0.5, seconds / 8)
+    out = {}
 
-    def run(threads):
-        times = []
-        while sum(times) < seconds or len(times) < 5:
-            t0 = time.perf_counter()
-            orc.paged_attention_f32(case.q, orc.BF16, case.k_cache, case.v_cache, orc.BF16,
-                                    case.tables, case.seq_lens, NKV, case.scale, orc.GROUPED,
-                                    threads=threads)
-            times.append(time.perf_counter() - t0)
-        return statistics.median(times), len(times)
+    def entry(name, workload, nbytes_all, nbytes_one, n_one, S_all, run_all, run_one):
+        ta, na = _median_time(run_all, budget)
+        t1, n1 = _median_time(run_one, budget)
+        out[name] = {
+            "workload": workload,
+            "all_cores": {"gbs": round(nbytes_all / ta / 1e9, 3), "tok_s": round(S_all / ta, 2),
+                          "ms_per_step": round(ta * 1e3, 3), "runs": na, "threads": ncore},
+            "single_thread": {"gbs": round(nbytes_one / t1 / 1e9, 3), "tok_s": round(n_one / t1, 2),
+                              "ms_per_run": round(t1 * 1e3, 3), "runs": n1, "sequences": n_one},
+        }
 
-    t1, n1 = run(1)
-    ta, na = run(info["threads_all_cores"])
+    # fp16 batch 4 (the reference CPU path's workload), full size
+    lens1 = inputs.uniform_lens(inputs.SEEDS[0], 4, 128, 1024)
+    c1 = inputs.make_paged_case(inputs.SEEDS[0], 4, H, NKV, D, 16, lens1, orc.F16, num_blocks=512, max_blocks=64)
+    b1 = 4096 * int(lens1.sum()) + 4 * H * D * 2 * 2
+    f1 = lambda th: (lambda: orc.paged_attention_f32(c1.q, orc.F16, c1.k_cache, c1.v_cache, orc.F16, c1.tables,
+                                                     c1.seq_lens, NKV, c1.scale, orc.GROUPED, threads=th))
+    entry("fp16_batch4", "fp16, batch 4, 32/8 heads, d 128, bs 16, lengths uniform in [128, 1024], 512-block pool",
+          b1, b1, 4, 4, f1(ncore), f1(1))
+
+    g = torch.Generator(device="cuda").manual_seed(inputs.SEEDS[1])
+
+    def pools(nblocks, dtype):
+        k = torch.randn(nblocks, NKV, D, 16, generator=g, device="cuda", dtype=torch.float32)
+        v = torch.randn(nblocks, NKV, D, 16, generator=g, device="cuda", dtype=torch.float32)
+        return k.to(dtype), v.to(dtype)
+
+    # bf16 headline: batch 64, ctx 4096, full size
+    nb = CTX // 16
+    N = math.ceil(1.25 * S * nb)
+    k, v = pools(N, torch.bfloat16)
+    tab = torch.randperm(N, generator=g, device="cuda").to(torch.int32)[: S * nb].view(S, nb).cpu().numpy()
+    q = _host_u16(torch.randn(S, H, D, generator=g, device="cuda").to(torch.bfloat16))
+    kh, vh = _host_u16(k), _host_u16(v)
+    del k, v
+    lens2 = np.full(S, CTX, np.int32)
+    n1 = 8
+    sc = 1.0 / math.sqrt(D)
+    f2 = lambda th, n: (lambda: orc.paged_attention_f32(q[:n], orc.BF16, kh, vh, orc.BF16, tab[:n], lens2[:n], NKV,
+                                                        sc, orc.GROUPED, threads=th))
+    entry("bf16_b64_ctx4096", "bf16, batch 64, ctx 4096, 32/8 heads, d 128, bs 16, shuffled 1.25x pool",
+          algorithmic_bytes([CTX] * S, 2), algorithmic_bytes([CTX] * n1, 2), n1, S, f2(ncore, S), f2(1, n1))
+    del kh, vh
+
+    # KIVI INT4 at ctx 4096 (pages of the first 3968 tokens, the fp16 window
+    # of the last 128), one decode step, full size
+    R = 128
+    L = CTX
+    max_pages = (L + 32) // 32 + 1
+    nbk = (L + 16 - 1) // 16 + 1
+    N3 = S * nbk + 8
+    k, v = pools(N3, torch.float16)
+    for h in range(NKV):
+        ch = torch.randperm(D, generator=g, device="cuda")[:4]
+        k[:, h, ch, :] *= 8
+    tab3 = torch.randperm(N3, generator=g, device="cuda").to(torch.int32)[: S * nbk].view(S, nbk).contiguous()
+    num_pages = S * max_pages + 8
+    ptab = torch.randperm(num_pages, generator=g, device="cuda").to(torch.int32)[: S * max_pages]
+    ptab = ptab.view(S, max_pages).contiguous()
+    pages = torch.zeros(num_pages, NKV, tla.kivi_page_bytes(4), dtype=torch.uint8, device="cuda")
+    q3 = torch.randn(S, H, D, generator=g, device="cuda", dtype=torch.float16)
+    sl3 = torch.full((S,), L, dtype=torch.int32, device="cuda")
+    d3 = tla.make_kivi_desc(q3, k, tab3, ptab, num_pages, NKV, sc, residual_length=R, bits=4)
+    tla.kivi_build_pages(d3, k, v, tab3, sl3, ptab, pages, L)
+    torch.cuda.synchronize()
+    kh, vh, q3h = _host_u16(k), _host_u16(v), _host_u16(q3)
+    pg, pt3, t3 = pages.cpu().numpy(), ptab.cpu().numpy(), tab3.cpu().numpy()
+    del k, v, pages
+    lens3 = np.full(S, L, np.int32)
+    kb = lambda n: kivi_bytes([L] * n, R, [False] * n) - n * NKV * D * 2 * 2   # no appended token
+    f3 = lambda th, n: (lambda: orc.kivi_paged_attention_f32(q3h[:n], pg, pt3[:n], kh, vh, t3[:n], lens3[:n], NKV,
+                                                             R, sc, orc.GROUPED, 4, threads=th))
+    entry("kivi_int4_b64_ctx4096", "KIVI INT4 pages (G 32, R 128), batch 64, ctx 4096, 32/8 heads, one decode step "
+          "(pages dequantised by the oracle's page routine, fp32 attention)",
+          kb(S), kb(n1), n1, S, f3(ncore, S), f3(1, n1))
+    del kh, vh, pg
+
+    # FP8 E4M3, batch 16, ctx 32768, per-tensor absmax / 448 scales, full size
+    nb4 = F8_CTX // 16
+    N4 = F8_S * nb4
+    k, v = pools(N4, torch.bfloat16)
+    ks = float(k.float().abs().max()) / 448
+    vs = float(v.float().abs().max()) / 448
+    k8 = torch.empty(k.shape, dtype=torch.uint8, device="cuda")
+    v8 = torch.empty_like(k8)
+    tla.convert_fp8(k8, k, 1.0 / ks)
+    tla.convert_fp8(v8, v, 1.0 / vs)
+    torch.cuda.synchronize()
+    del k, v
+    tab4 = torch.randperm(N4, generator=g, device="cuda").to(torch.int32).view(F8_S, nb4).cpu().numpy()
+    q4 = _host_u16(torch.randn(F8_S, H, D, generator=g, device="cuda").to(torch.bfloat16))
+    k8h, v8h = k8.cpu().numpy(), v8.cpu().numpy()
+    del k8, v8
+    lens4 = np.full(F8_S, F8_CTX, np.int32)
+    n4 = 2
+    f4 = lambda th, n: (lambda: orc.paged_attention_f32(q4[:n], orc.BF16, k8h, v8h, orc.FP8, tab4[:n], lens4[:n],
+                                                        NKV, sc, orc.GROUPED, threads=th, k_scale=ks, v_scale=vs))
+    b4 = lambda n: n * F8_CTX * NKV * D * 2 + n * H * D * 2 * 2 + n * (nb4 * 4 + 4)
+    entry("fp8_b16_ctx32768", "FP8 E4M3 KV (per-tensor scales), batch 16, ctx 32768, 32/8 heads, bf16 q",
+          b4(F8_S), b4(n4), n4, F8_S, f4(ncore, F8_S), f4(1, n4))
+    del k8h, v8h
+
+    head = out["bf16_b64_ctx4096"]
     return {
-        "value": round(nbytes / ta / 1e9, 3), "unit": "GB/s", "tok_s": round(S_sample / ta, 2),
-        "cores": info["threads_all_cores"], "kind": "port",
-        "sample": f"{S_sample} of the 64 sequences (ctx {CTX}, 32/8 heads, d 128, bf16 pool); the oracle's fp32 "
-                  f"decode, median of {na} runs ({ta * 1e3:.2f} ms each) on {info['threads_all_cores']} threads "
-                  f"and of {n1} runs ({t1 * 1e3:.2f} ms) on one",
-        "single_thread": {"value": round(nbytes / t1 / 1e9, 3), "unit": "GB/s", "tok_s": round(S_sample / t1, 2),
-                          "ms_per_run": round(t1 * 1e3, 3)},
+        "value": head["all_cores"]["gbs"], "unit": "GB/s", "tok_s": head["all_cores"]["tok_s"], "cores": ncore,
+        "kind": "port",
+        "sample": f"the headline workload at full size (batch 64, ctx 4096, bf16): the oracle's fp32 decode on "
+                  f"{ncore} threads, median of {head['all_cores']['runs']} runs; one thread over "
+                  f"{head['single_thread']['sequences']} of the 64 sequences. Per workload: 'configs'",
+        "single_thread": {"value": head["single_thread"]["gbs"], "unit": "GB/s",
+                          "tok_s": head["single_thread"]["tok_s"]},
+        "configs": out,
         "nproc": info["nproc"], "affinity_cpus": info["affinity"], "cpu_model": info["model"],
     }
 
@@ -884,7 +1003,7 @@ def main():
             "silu_and_mul_us": round(na["act_us"], 2),
             "silu_and_mul_gbs": round(na["act_bytes"] / (na["act_us"] * 1e-6) / 1e9, 2)}
     if not args.no_cpu:
-        res["cpu_baseline"] = cpu_baseline(args.cpu_seconds / 2, 4)
+        res["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(res), flush=True)
 
 

@@ -29,7 +29,7 @@ extern "C" {
 
 /* Version of this C ABI (tl_abi_version).  2: tl_kivi_desc gained
  * pre_rope_keys (after bits), for the _pre_rope entry points. */
-#define TL_ABI_VERSION 2
+#define TL_ABI_VERSION 3
 
 /* Mirrors truellm::ErrorCode (include/truellm/types.h:20-32). */
 typedef enum tl_status {
@@ -66,7 +66,7 @@ typedef struct tl_decode_desc {
   int32_t num_heads;           /* H (q heads); H % num_kv_heads == 0 */
   int32_t num_kv_heads;
   int32_t head_size;           /* 128; 64 / 256 (and 80 / 96 for F16 / BF16 KV) */
-  int32_t block_size;          /* head 128: a power of two 8..256 (FP8: 16..256),
+  int32_t block_size;          /* head 128: a power of two 8..256 (FP8 too),
                                   F32 KV and other heads: 16 */
   int32_t max_blocks_per_seq;  /* row stride of block_tables */
   int32_t num_blocks;          /* pool capacity N; table entries >= N are holes */
@@ -378,7 +378,7 @@ typedef struct tl_kivi_desc {
   int32_t num_heads;
   int32_t num_kv_heads;
   int32_t head_size;           /* 128 */
-  int32_t block_size;          /* 16 (fp16 pool) */
+  int32_t block_size;          /* fp16 pool block size: a power of two 8..256 */
   int32_t max_blocks_per_seq;
   int32_t num_blocks;
   int32_t max_pages_per_seq;
@@ -550,24 +550,28 @@ int32_t tl_kivi_pass_runs(int32_t seq_len, int32_t n_kv_heads, int32_t head_dim,
  * pool with tl_reshape_and_cache); query i sits at position
  * seq_lens[s] - q_len + i and attends causally to keys 0 .. that position.
  * q_len == 1 rows are decode rows (a second kernel on the same stream).
- * head_size 128, block_size 16 or 32,
- * dtype F16 or BF16 for q, out and the pool; q and the pools 16-byte
- * aligned, out 4-byte aligned.  max_q_len (host) bounds the grid;
- * max_q_len x (num_heads / num_kv_heads) must stay below 2^22 - 256
+ * head_size 128, block_size any power of two 8..256 (CudaEngineConfig's
+ * paged_kv_block_size, config_schema.h:68), dtype F16 or BF16 for q and out;
+ * the pool holds dtype, or FP8 E4M3 codes with per-tensor scales
+ * (use_fp8_kv, config_schema.h:72; cuda_allocator.h:179-182).  q and the
+ * pools 16-byte aligned, out 4-byte aligned.  max_q_len (host) bounds the
+ * grid; max_q_len x (num_heads / num_kv_heads) must stay below 2^22 - 256
  * (TL_ERR_NOT_IMPLEMENTED otherwise). */
 typedef struct tl_prefill_desc {
   int32_t num_seqs;
   int32_t num_heads;
   int32_t num_kv_heads;
   int32_t head_size;           /* 128 */
-  int32_t block_size;          /* 16 or 32 */
+  int32_t block_size;          /* a power of two 8..256 */
   int32_t max_blocks_per_seq;
   int32_t num_blocks;
-  int32_t dtype;               /* TL_DTYPE_F16 or TL_DTYPE_BF16 */
+  int32_t dtype;               /* TL_DTYPE_F16 or TL_DTYPE_BF16: q and out */
   int32_t gqa_map;
   int32_t num_prefill_seqs;    /* 0: any sequence may be either kind; n > 0: sequences
                                   0..n-1 hold every q_len > 1 row, n.. only q_len <= 1 */
   float scale;
+  int32_t kv_dtype;            /* the pool: 0 or dtype, or TL_DTYPE_FP8_E4M3 */
+  float k_scale, v_scale;      /* FP8 pools: the per-tensor dequant scales (> 0) */
 } tl_prefill_desc;
 
 int tl_chunked_prefill(const tl_prefill_desc* desc, void* out, const void* q,

@@ -159,3 +159,112 @@ void orc_paged_attention_f32(void* out, int out_dtype, const void* q, int q_dtyp
     worker(&jobs[0]);
     for (int i = 1; i < num_threads; ++i) pthread_join(th[i], NULL);
 }
+
+/* ---- paged KIVI (INT4 / INT8 pages + fp16 window), fp32 ------------------
+ * The same attention as orc_kivi_paged_attention_bits (tl_oracle.c: tokens
+ * [0, Lq) from the dequantised pages, [Lq, L) from the fp16 pool, page-table
+ * and block-table holes dropped) in fp32, threads over (seq, kv_head); the
+ * pages are dequantised by the oracle's own page routine. */
+typedef struct {
+    uint16_t* out; const uint16_t* q; const uint8_t* pages; const int32_t* page_tables;
+    int max_pages, num_pages; const uint16_t* k_cache; const uint16_t* v_cache;
+    const int32_t* block_tables; int mbps; const int32_t* seq_lens;
+    int num_seqs, num_heads, num_kv_heads, block_size, residual_length;
+    float scale; int gqa_map, bits, nthreads, tid, max_len;
+} kjob_t;
+
+enum { KD = 128, KT = 32 };
+
+static void* kivi_worker(void* arg)
+{
+    kjob_t* J = (kjob_t*)arg;
+    const int G = J->num_heads / J->num_kv_heads, BS = J->block_size;
+    const size_t page_bytes = orc_kivi_page_bytes(J->bits);
+    const size_t ml = J->max_len > 0 ? (size_t)J->max_len : 1;
+    float* K = (float*)malloc(sizeof(float) * ml * KD);
+    float* V = (float*)malloc(sizeof(float) * ml * KD);
+    float* sc = (float*)malloc(sizeof(float) * ml);
+    unsigned char* ok = (unsigned char*)malloc(ml);
+    uint16_t kt[KT * KD], vt[KT * KD];
+    float qv[KD], acc[KD];
+    const int items = J->num_seqs * J->num_kv_heads;
+    for (int it = J->tid; it < items; it += J->nthreads) {
+        const int s = it / J->num_kv_heads, kvh = it % J->num_kv_heads;
+        const int L = J->seq_lens[s], Lq = orc_kivi_quantized_len(L, J->residual_length);
+        const int32_t* row = J->block_tables + (int64_t)s * J->mbps;
+        for (int p = 0; p < Lq / KT; ++p) {
+            const int32_t pid = p < J->max_pages ? J->page_tables[(int64_t)s * J->max_pages + p] : -1;
+            const int there = pid >= 0 && pid < J->num_pages;
+            memset(ok + (size_t)p * KT, there, KT);
+            if (!there) continue;
+            orc_kivi_page_dequant_bits(J->pages + ((int64_t)pid * J->num_kv_heads + kvh) * page_bytes, kt, vt,
+                                       J->bits);
+            for (int i = 0; i < KT * KD; ++i) {
+                K[(size_t)p * KT * KD + i] = h2f(kt[i]);
+                V[(size_t)p * KT * KD + i] = h2f(vt[i]);
+            }
+        }
+        for (int t = Lq; t < L; ++t) {
+            const int lb = t / BS;
+            const int32_t ph = lb < J->mbps ? row[lb] : -1;
+            ok[t] = (unsigned char)(ph >= 0);
+            if (ph < 0) continue;
+            const int64_t base = ((int64_t)ph * J->num_kv_heads + kvh) * KD * BS + t % BS;
+            for (int e = 0; e < KD; ++e) {
+                K[(size_t)t * KD + e] = h2f(J->k_cache[base + (int64_t)e * BS]);
+                V[(size_t)t * KD + e] = h2f(J->v_cache[base + (int64_t)e * BS]);
+            }
+        }
+        for (int g = 0; g < G; ++g) {
+            const int h = (J->gqa_map == ORC_GQA_GROUPED) ? kvh * G + g : kvh + g * J->num_kv_heads;
+            const int64_t qoff = ((int64_t)s * J->num_heads + h) * KD;
+            for (int e = 0; e < KD; ++e) { qv[e] = h2f(J->q[qoff + e]) * J->scale; acc[e] = 0.f; }
+            float mx = -INFINITY, sum = 0.f;
+            for (int t = 0; t < L; ++t) {
+                if (!ok[t]) continue;
+                const float* kr = K + (size_t)t * KD;
+                float d = 0.f;
+                for (int e = 0; e < KD; ++e) d += qv[e] * kr[e];
+                sc[t] = d;
+                if (d > mx) mx = d;
+            }
+            for (int t = 0; t < L; ++t) {
+                if (!ok[t]) continue;
+                const float w = expf(sc[t] - mx);
+                const float* vr = V + (size_t)t * KD;
+                sum += w;
+                for (int e = 0; e < KD; ++e) acc[e] += w * vr[e];
+            }
+            const float inv = sum > 0.f ? 1.f / sum : 0.f;
+            for (int e = 0; e < KD; ++e) J->out[qoff + e] = orc_f32_to_f16(acc[e] * inv);
+        }
+    }
+    free(K); free(V); free(sc); free(ok);
+    return NULL;
+}
+
+void orc_kivi_paged_attention_f32(uint16_t* out, const uint16_t* q, const uint8_t* pages,
+                                  const int32_t* page_tables, int max_pages, int num_pages,
+                                  const uint16_t* k_cache, const uint16_t* v_cache,
+                                  const int32_t* block_tables, int max_blocks_per_seq,
+                                  const int32_t* seq_lens, int num_seqs, int num_heads,
+                                  int num_kv_heads, int block_size, int residual_length,
+                                  float scale, int gqa_map, int bits, int num_threads)
+{
+    if (num_kv_heads <= 0 || num_heads % num_kv_heads) return;
+    if (num_threads < 1) num_threads = 1;
+    if (num_threads > 256) num_threads = 256;
+    int max_len = 0;
+    for (int s = 0; s < num_seqs; ++s) if (seq_lens[s] > max_len) max_len = seq_lens[s];
+    pthread_t th[256];
+    kjob_t jobs[256];
+    for (int i = 0; i < num_threads; ++i) {
+        kjob_t J = { out, q, pages, page_tables, max_pages, num_pages, k_cache, v_cache, block_tables,
+                     max_blocks_per_seq, seq_lens, num_seqs, num_heads, num_kv_heads, block_size,
+                     residual_length, scale, gqa_map, bits, num_threads, i, max_len };
+        jobs[i] = J;
+    }
+    for (int i = 1; i < num_threads; ++i) pthread_create(&th[i], NULL, kivi_worker, &jobs[i]);
+    kivi_worker(&jobs[0]);
+    for (int i = 1; i < num_threads; ++i) pthread_join(th[i], NULL);
+}

@@ -100,6 +100,16 @@ void orc_paged_attention_f32(void* out, int out_dtype, const void* q, int q_dtyp
                              int num_kv_heads, int head_size, int block_size,
                              float scale, int gqa_map, int num_threads);
 
+/* The paged KIVI attention of orc_kivi_paged_attention_bits in fp32 (the
+ * CPU baseline), threads over (seq, kv_head); fp16 q and out. */
+void orc_kivi_paged_attention_f32(uint16_t* out, const uint16_t* q, const uint8_t* pages,
+                                  const int32_t* page_tables, int max_pages, int num_pages,
+                                  const uint16_t* k_cache, const uint16_t* v_cache,
+                                  const int32_t* block_tables, int max_blocks_per_seq,
+                                  const int32_t* seq_lens, int num_seqs, int num_heads,
+                                  int num_kv_heads, int block_size, int residual_length,
+                                  float scale, int gqa_map, int bits, int num_threads);
+
 /* Bug-for-bug restatement of paged_attention_v1 (paged_attention_v1.cu:31-135)
  * with fp32 arithmetic, used only to document how far the reference's
  * literal output is from attention.  out [S, H, d] float; untouched when

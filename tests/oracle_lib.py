@@ -52,6 +52,8 @@ _lib.orc_copy_blocks.argtypes = [_P, _P, _P, _I, _I, ctypes.c_int64]
 _lib.orc_swap_blocks.argtypes = [_P, _P, _P, _I, _I, _I, ctypes.c_int64, _I]
 _lib.orc_paged_attention.argtypes = [_P, _P, _I, _P, _P, _I, _F, _F, _P, _I, _P, _I, _I, _I, _I, _I, _F, _I, _I]
 _lib.orc_paged_attention_f32.argtypes = [_P, _I, _P, _I, _P, _P, _I, _F, _F, _P, _I, _P, _I, _I, _I, _I, _I, _F, _I, _I]
+_lib.orc_kivi_paged_attention_f32.argtypes = [_P, _P, _P, _P, _I, _I, _P, _P, _P, _I, _P, _I, _I, _I, _I, _I, _F,
+                                              _I, _I, _I]
 _lib.orc_paged_attention_literal_v1.argtypes = [_P, _P, _P, _P, _I, _P, _I, _P, _I, _I, _I, _I, _I, _F]
 _lib.orc_chunked_prefill.argtypes = [_P, _P, _I, _P, _P, _P, _I, _P, _I, _P, _I, _I, _I, _I, _I, _F, _I]
 _lib.orc_kivi_compressed_bytes.restype = ctypes.c_size_t
@@ -224,6 +226,20 @@ def paged_attention_f32(q, q_code, k_cache, v_cache, kv_code, tables, seq_lens, 
                                  kv_code, k_scale, v_scale, ptr(tables), tables.shape[1],
                                  ptr(seq_lens), S, H, num_kv_heads, D, k_cache.shape[3], scale,
                                  gqa_map, threads)
+    return out
+
+
+def kivi_paged_attention_f32(q, pages, page_tables, k_cache, v_cache, tables, seq_lens, num_kv_heads,
+                             residual_length, scale, gqa_map=GROUPED, bits=4, threads=1):
+    """The CPU baseline's paged KIVI decode (fp32, threads over (seq, kv
+    head)); fp16 q and output bits."""
+    S, H, D = q.shape
+    out = np.zeros((S, H, D), np.uint16)
+    num_pages = pages.size // (num_kv_heads * kivi_page_bytes(bits))
+    _lib.orc_kivi_paged_attention_f32(ptr(out), ptr(q), ptr(pages), ptr(page_tables), page_tables.shape[1],
+                                      num_pages, ptr(k_cache), ptr(v_cache), ptr(tables), tables.shape[1],
+                                      ptr(seq_lens), S, H, num_kv_heads, k_cache.shape[3], residual_length,
+                                      scale, gqa_map, bits, threads)
     return out
 
 

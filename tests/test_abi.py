@@ -16,7 +16,7 @@ def test_exports_every_declared_function():
 
 
 def test_abi_version():
-    assert tla.lib.tl_abi_version() == 2 == tla.ABI_VERSION
+    assert tla.lib.tl_abi_version() == 3 == tla.ABI_VERSION
 
 
 def _desc(**kw):
@@ -48,7 +48,6 @@ def _decode(d, out=FAKE, ws=None, ws_bytes=0, max_ctx=1024):
     (dict(head_size=64, block_size=8), tla.ERR_NOT_IMPLEMENTED),
     (dict(block_size=12), tla.ERR_NOT_IMPLEMENTED),
     (dict(block_size=512), tla.ERR_NOT_IMPLEMENTED),
-    (dict(block_size=8, kv_dtype=tla.FP8_E4M3), tla.ERR_NOT_IMPLEMENTED),
     (dict(block_size=32, q_dtype=tla.F32, kv_dtype=tla.F32), tla.ERR_NOT_IMPLEMENTED),
     (dict(q_dtype=7), tla.ERR_INVALID_ARGUMENT),
     (dict(kv_dtype=tla.BF16), tla.ERR_NOT_IMPLEMENTED),
@@ -64,13 +63,13 @@ def test_decode_rejects_bad_descriptors(kw, code):
 
 @pytest.mark.parametrize("kw", [
     dict(block_size=8), dict(block_size=32), dict(block_size=64), dict(block_size=128),
-    dict(block_size=256), dict(block_size=16, kv_dtype=tla.FP8_E4M3),
+    dict(block_size=256), dict(block_size=16, kv_dtype=tla.FP8_E4M3), dict(block_size=8, kv_dtype=tla.FP8_E4M3),
     dict(block_size=256, kv_dtype=tla.FP8_E4M3, q_dtype=tla.BF16), dict(head_size=80), dict(head_size=96),
     dict(head_size=96, q_dtype=tla.BF16, kv_dtype=tla.BF16), dict(head_size=64, q_dtype=tla.F32, kv_dtype=tla.F32),
     dict(head_size=256, q_dtype=tla.F32, kv_dtype=tla.F32), dict(head_size=256, kv_dtype=tla.FP8_E4M3),
 ])
 def test_decode_accepts_the_built_shapes(kw):
-    """Head 128 with any power-of-two block size 8..256 (FP8 16..256), the
+    """Head 128 with any power-of-two block size 8..256 (FP8 too), the
     reference's F16 heads 64/80/96/256 and F32 heads 64/128/256 at block
     size 16 (paged_attention_v1.cu:198-209): validation passes, so the
     split-K plan has a workspace size."""
@@ -251,7 +250,14 @@ def test_kivi_decode_descriptor_checks_and_planning():
     call = lambda d: L.tl_kivi_paged_attention_decode(ctypes.byref(d), FAKE, FAKE, FAKE, FAKE,
                                                       FAKE, FAKE, FAKE, FAKE, 4096, None, 0, None)
     assert call(_kdesc(head_size=64)) == tla.ERR_NOT_IMPLEMENTED
-    assert call(_kdesc(block_size=32)) == tla.ERR_NOT_IMPLEMENTED
+    # the fp16 pool's block size: any power of two 8..256 (CudaEngineConfig's
+    # paged_kv_block_size, config_schema.h:68); the checks pass and the call
+    # fails later on its missing workspace
+    for bs in (12, 4, 512, 0):
+        assert call(_kdesc(block_size=bs)) == tla.ERR_NOT_IMPLEMENTED
+    for bs in (8, 32, 64, 256):
+        assert tla.kivi_workspace_bytes(_kdesc(num_seqs=4, block_size=bs), 4096) == 4 * 32 * 16 * (128 * 4 + 8)
+        assert call(_kdesc(num_seqs=4, block_size=bs)) == tla.ERR_INVALID_ARGUMENT
     assert call(_kdesc(residual_length=-1)) == tla.ERR_INVALID_ARGUMENT
     assert call(_kdesc(num_pages=0)) == tla.ERR_INVALID_ARGUMENT
     assert tla.kivi_workspace_bytes(_kdesc(), 4096) == 0               # 512 items: single pass
@@ -293,6 +299,17 @@ def test_chunked_prefill_argument_checks():
     assert call(desc(), total_q=big, max_q=big) == tla.ERR_NOT_IMPLEMENTED
     assert call(desc(dtype=tla.F32)) == tla.ERR_NOT_IMPLEMENTED
     assert call(desc(head_size=64)) == tla.ERR_NOT_IMPLEMENTED
+    # the pool: the q type or FP8 E4M3 (positive finite scales), any
+    # power-of-two block size 8..256; the checks before the pointer checks
+    assert call(desc(kv_dtype=tla.F16)) == tla.ERR_NOT_IMPLEMENTED   # bf16 q over an f16 pool
+    assert call(desc(kv_dtype=tla.FP8_E4M3, k_scale=0.0, v_scale=1.0)) == tla.ERR_INVALID_ARGUMENT
+    assert call(desc(kv_dtype=tla.FP8_E4M3, k_scale=1.0, v_scale=float("inf"))) == tla.ERR_INVALID_ARGUMENT
+    for bs in (4, 12, 512):
+        assert call(desc(block_size=bs)) == tla.ERR_NOT_IMPLEMENTED
+    for bs in (8, 16, 32, 64, 128, 256):
+        for kw in (dict(), dict(kv_dtype=tla.FP8_E4M3, k_scale=0.5, v_scale=2.0)):
+            assert call(desc(block_size=bs, **kw), out=None) == tla.ERR_INVALID_ARGUMENT   # NULL out: checks passed
+            assert "NULL" in tla.last_error()
     assert call(desc(), max_q=2048) == tla.ERR_INVALID_ARGUMENT      # max_q_len > total_q
     assert call(desc(scale=0.0)) == tla.ERR_INVALID_ARGUMENT
 
@@ -333,9 +350,11 @@ def test_engine_apply_config_maps_cudaengineconfig():
     assert "attention_layout" in tla.last_error()
     assert call(16, 0, None) == tla.ERR_NOT_IMPLEMENTED
     assert call(512, 0, b"paged") == tla.ERR_NOT_IMPLEMENTED           # no kernel for block size 512
-    assert call(8, 1, b"paged") == tla.ERR_NOT_IMPLEMENTED             # FP8 needs block size >= 16
     assert L.tl_engine_apply_config(None, 16, 0, b"paged") == tla.ERR_INVALID_ARGUMENT
     assert d.block_size == 64 and d.kv_dtype == tla.BF16              # unchanged by the rejected calls
+    tla.engine_apply_config(d, block_size=8, use_fp8_kv=True)           # every power of two 8..256, FP8 too
+    assert d.block_size == 8 and d.kv_dtype == tla.FP8_E4M3
+    tla.engine_apply_config(d, block_size=64, use_fp8_kv=False)
     f32 = _desc(q_dtype=tla.F32, kv_dtype=tla.F32)
     assert L.tl_engine_apply_config(ctypes.byref(f32), 16, 1, b"paged") == tla.ERR_NOT_IMPLEMENTED  # FP8 needs 2-byte q
 

@@ -118,12 +118,13 @@ def test_vector_codec_unsupported_params_leave_output_untouched():
 class KiviCase:
     """fp16 pools for the given lengths plus a page table over a page pool."""
 
-    def __init__(self, seed, lens, H=32, n_kv=8, R=128, outliers=4, extra_blocks=4, bits=4):
+    def __init__(self, seed, lens, H=32, n_kv=8, R=128, outliers=4, extra_blocks=4, bits=4, BS=16):
         self.lens = np.asarray(lens, np.int32)
         self.R = R
         self.bits = bits
+        self.BS = BS
         self.page_bytes = orc.kivi_page_bytes(bits)
-        S, D, BS = len(lens), 128, 16
+        S, D = len(lens), 128
         self.case = inputs.make_paged_case(seed, S, H, n_kv, D, BS,
                                            [L + extra_blocks * BS for L in lens], orc.F32)
         rng = np.random.default_rng(seed + 1)
@@ -799,3 +800,60 @@ def test_pre_rope_step_graph_replay_matches_eager(through_rope_step):
         step(torch.cuda.current_stream())            # eager work between replays
         torch.cuda.synchronize()
         assert torch.equal(out, eager)
+
+
+@pytest.mark.parametrize("BS", [8, 32, 64, 256])
+def test_kivi_block_sizes_step_and_decode_against_oracle(BS):
+    """The fp16 pool at block sizes other than 16 (any power of two 8..256):
+    pages built bit-exact, the fused step against the oracle at every step
+    (the window and the newest token read at that block size, the token
+    stored into its block while the other slots keep their bytes: the pools
+    are compared bit for bit at the end), then the two-launch decode under
+    single pass and split-K, INT4 and INT8 pages.  A window block of
+    sequence 3 is a hole."""
+    start = np.array([150, 159, 190, 1000, 33, 700], np.int32)
+    steps = 34
+    for bits in (4, 8):
+        kc = KiviCase(62 + BS + bits, start + steps, H=32, extra_blocks=1, bits=bits, BS=BS)
+        hole_lb = (1000 - 60) // BS
+        kc.tables[3, hole_lb] = -1
+        qd, kd, vd = dev(kc.q, orc.F16), dev(kc.k, orc.F16), dev(kc.v, orc.F16)
+        btd, ptd = dev(kc.tables), dev(kc.page_tables)
+        pages = torch.zeros(kc.num_pages, kc.n_kv, kc.page_bytes, dtype=torch.uint8, device="cuda")
+        desc = kc.desc(qd, kd, btd, ptd, 0)
+        assert desc.block_size == BS
+        print(f"case kivi bs={BS} bits={bits} build", flush=True)
+        tla.kivi_build_pages(desc, kd, vd, btd, dev(start), ptd, pages, int(start.max()))
+        torch.cuda.synchronize()
+        kc.lens = start.copy()
+        want_pages = kc.oracle_pages()
+        used = [p for p in _used_pages(kc, start) if p >= 0]
+        assert np.array_equal(pages.cpu().numpy()[used], want_pages[used])
+        rng = np.random.default_rng(BS + bits)
+        max_ctx = int(start.max()) + steps
+        ws = torch.empty(max(16, tla.kivi_workspace_bytes(desc, max_ctx)), dtype=torch.uint8, device="cuda")
+        lens = start.copy()
+        k_host, v_host = kc.k.copy(), kc.v.copy()
+        print(f"case kivi bs={BS} bits={bits} steps", flush=True)
+        for step in range(steps):
+            lens = lens + 1
+            pos = lens - 1
+            ent = kc.tables[np.arange(kc.S), pos // BS]
+            slots = np.where(ent >= 0, ent * BS + pos % BS, -1).astype(np.int32)
+            knew = inputs.encode(rng.standard_normal((kc.S, kc.n_kv, 128), dtype=np.float32), orc.F16)
+            vnew = inputs.encode(rng.standard_normal((kc.S, kc.n_kv, 128), dtype=np.float32), orc.F16)
+            out = torch.full_like(qd, float("nan"))
+            tla.kivi_decode_step(desc, out, qd, dev(knew, orc.F16), dev(vnew, orc.F16), dev(slots), pages, ptd,
+                                 kd, vd, btd, dev(lens), max_ctx, ws)
+            torch.cuda.synchronize()
+            orc.reshape_and_cache(knew, vnew, k_host, v_host, slots)
+            kc.k, kc.v, kc.lens = k_host, v_host, lens
+            want_pages = kc.oracle_pages()
+            assert_close(out, _kivi_ref(kc, want_pages), orc.F16, ATOL_KIVI, f"bs={BS} bits={bits} step {step}")
+        assert np.array_equal(host_bits(kd), k_host) and np.array_equal(host_bits(vd), v_host)
+        used = [p for p in _used_pages(kc, lens) if p >= 0]
+        assert np.array_equal(pages.cpu().numpy()[used], want_pages[used])
+        for pp in (-1, 2):
+            print(f"case kivi bs={BS} bits={bits} decode pp={pp}", flush=True)
+            assert_close(_run_decode(kc, want_pages, pp), _kivi_ref(kc, want_pages), orc.F16, ATOL_KIVI,
+                         f"bs={BS} bits={bits} pp={pp}")

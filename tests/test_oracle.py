@@ -714,6 +714,28 @@ def test_kivi_attention_equals_paged_attention_on_dequantised_prefix(gqa_map, bi
     assert np.abs(full[0] - got[0]).max() > 1e-3 and np.abs(full[3] - got[3]).max() > 1e-3
 
 
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("gqa_map", [orc.MODULO, orc.GROUPED])
+def test_cpu_baseline_kivi_f32_matches_oracle(gqa_map, bits):
+    """The CPU baseline's paged KIVI decode (fp32, threads) against the fp64
+    oracle, holes of both kinds included: within an fp16 output ulp and the
+    fp32 sums' rounding."""
+    R = 128
+    case, ptab, num_pages = _kivi_small_case(33, [300, 161, 100, 223])
+    case.tables[0, 12] = -1
+    ptab[0, 2] = -1
+    ptab[3, 1] = num_pages
+    pages = np.zeros((num_pages, 2, orc.kivi_page_bytes(bits)), np.uint8)
+    orc.kivi_build_pages(case.k_cache, case.v_cache, case.tables, case.seq_lens, R, pages, ptab, bits)
+    want = orc.kivi_paged_attention(case.q, orc.F16, pages, ptab, case.k_cache, case.v_cache,
+                                    case.tables, case.seq_lens, 2, R, case.scale, gqa_map, bits)
+    got = orc.kivi_paged_attention_f32(case.q, pages, ptab, case.k_cache, case.v_cache, case.tables,
+                                       case.seq_lens, 2, R, case.scale, gqa_map, bits, threads=3)
+    got = got.view(np.float16).astype(np.float64)
+    np.testing.assert_allclose(got, want, rtol=0, atol=2e-5 + np.abs(want).max() * 2.0 ** -11)
+    assert np.abs(want).max() > 0.1
+
+
 @pytest.mark.parametrize("style,bits", [(0, 4), (1, 4), (0, 8), (1, 8)])
 def test_kivi_pre_rope_attention_is_attention_on_the_rotated_pool(style, bits):
     """Keys held before RoPE (KiviConfig.pre_rope_keys): the oracle's KIVI

@@ -243,3 +243,85 @@ def test_empty_and_invalid_arguments():
         with pytest.raises(tla.TLError) as e:
             tla.chunked_prefill(neg, out, q, cu, k, k, bt, sl, 4)
         assert e.value.code == tla.ERR_INVALID_ARGUMENT
+
+
+# ---------------------------------------------------------------------------
+# every power-of-two block size (CudaEngineConfig.paged_kv_block_size,
+# config_schema.h:68) and FP8 E4M3 pools (use_fp8_kv, config_schema.h:72)
+# ---------------------------------------------------------------------------
+
+BS_MIXED = [(96, 96), (130, 400), (1, 700), (33, 33), (2, 50), (1, 1), (257, 300), (1, 129), (70, 613)]
+
+
+@pytest.mark.parametrize("code", [orc.BF16, orc.F16])
+@pytest.mark.parametrize("BS", [8, 16, 32, 64, 128, 256])
+def test_block_sizes_with_holes_and_nan_unused_slots(BS, code):
+    """Prefill rows and decode rows at every block size: table holes (which
+    drop their keys) and NaN in the slots past each sequence's end."""
+    pc = PrefillCase(inputs.SEEDS[4] + 10 + BS, BS_MIXED, 16, 4, code, BS=BS, holes=4, nan_unused=True)
+    print(f"case prefill bs={BS} code={code}", flush=True)
+    assert_close(pc.run(), pc.ref(), code, ATOL, f"bs={BS}")
+
+
+def _fp8_case(seed, shape, H, n_kv, qcode, BS, holes=0):
+    """A PrefillCase whose pools are E4M3 codes with per-tensor absmax / 448
+    scales (fp8_gemm.cu:82-93), NaN codes in the slots past each sequence's
+    end; returns (case, k codes, v codes, k_scale, v_scale) with the case's
+    own pools replaced by the dequantised values in fp32 (what the oracle
+    attends over)."""
+    pc = PrefillCase(seed, shape, H, n_kv, orc.F32, BS=BS, holes=holes)
+    pc.q = inputs.encode(pc.q, qcode)
+    pc.code = qcode
+    c = pc.case
+    ks = float(np.abs(c.k_cache).max()) / 448
+    vs = float(np.abs(c.v_cache).max()) / 448
+    k8, v8 = orc.f32_to_e4m3(c.k_cache, 1 / ks), orc.f32_to_e4m3(c.v_cache, 1 / vs)
+    for s, L in enumerate(pc.lens):
+        if L % BS:
+            last = c.tables[s, (L - 1) // BS]
+            if last >= 0:
+                k8[last, :, :, L % BS:] = 0x7F
+                v8[last, :, :, L % BS:] = 0xFF
+    c.k_cache = orc.bits_to_f32(k8, orc.FP8) * np.float32(ks)
+    c.v_cache = orc.bits_to_f32(v8, orc.FP8) * np.float32(vs)
+    return pc, k8, v8, ks, vs
+
+
+def _run_fp8(pc, k8, v8, ks, vs, gqa=tla.GQA_GROUPED):
+    c = pc.case
+    q = dev(pc.q, pc.code)
+    k, v = dev(k8), dev(v8)
+    bt, sl, cu = dev(c.tables), dev(pc.lens), dev(pc.cu)
+    out = torch.full_like(q, float("nan"))
+    desc = tla.make_prefill_desc(q, k, bt, pc.S, pc.n_kv, c.scale, gqa_map=gqa, kv_dtype=tla.FP8_E4M3,
+                                 k_scale=ks, v_scale=vs)
+    tla.chunked_prefill(desc, out, q, cu, k, v, bt, sl, int(pc.q_lens.max()))
+    torch.cuda.synchronize()
+    return out
+
+
+def _ref_fp8(pc, gqa=orc.GROUPED):
+    c = pc.case
+    return orc.chunked_prefill(pc.q, pc.code, pc.cu, c.k_cache, c.v_cache, orc.F32, c.tables, pc.lens, pc.n_kv,
+                               c.scale, gqa)
+
+
+@pytest.mark.parametrize("qcode", [orc.BF16, orc.F16])
+@pytest.mark.parametrize("BS", [8, 16, 32, 256])
+def test_fp8_pool_against_the_dequantised_pool(BS, qcode):
+    """FP8 E4M3 pools (codes staged exactly as the q type for q.k and as f16
+    for p.v, k_scale in the score scale, v_scale on the output), prefill rows
+    and decode rows, against the oracle over the dequantised pool: max-abs
+    1e-2 (the FP8 bar).  Holes and NaN codes past the sequences' ends."""
+    pc, k8, v8, ks, vs = _fp8_case(inputs.SEEDS[4] + 20 + BS, BS_MIXED, 16, 4, qcode, BS, holes=3)
+    print(f"case prefill fp8 bs={BS} q={qcode}", flush=True)
+    assert_close(_run_fp8(pc, k8, v8, ks, vs), _ref_fp8(pc), qcode, 1e-2, f"fp8 bs={BS}")
+
+
+@pytest.mark.parametrize("gqa", [tla.GQA_GROUPED, tla.GQA_MODULO])
+def test_fp8_pool_group_sizes_and_head_maps(gqa):
+    for H, n_kv in ((8, 8), (32, 4)):
+        pc, k8, v8, ks, vs = _fp8_case(inputs.SEEDS[4] + 30 + H, [(80, 200), (1, 333), (40, 40)], H, n_kv,
+                                       orc.BF16, 16)
+        print(f"case prefill fp8 H={H} n_kv={n_kv} gqa={gqa}", flush=True)
+        assert_close(_run_fp8(pc, k8, v8, ks, vs, gqa), _ref_fp8(pc, gqa), orc.BF16, 1e-2, f"fp8 H={H}")

@@ -92,7 +92,7 @@ def test_head128_block_sizes_group_8_and_mha(BS):
                      f"bs={BS} H={H}")
 
 
-@pytest.mark.parametrize("BS", [32, 64, 128, 256])
+@pytest.mark.parametrize("BS", [8, 32, 64, 128, 256])
 @pytest.mark.parametrize("q_code", [orc.F16, orc.BF16])
 @pytest.mark.parametrize("pt", [-1, 512])
 def test_fp8_block_sizes(BS, q_code, pt):
@@ -116,7 +116,8 @@ def test_fp8_block_sizes(BS, q_code, pt):
     assert_close(out, ref, q_code, ATOL_FP8, f"fp8 bs={BS}")
 
 
-@pytest.mark.parametrize("BS,fp8,layout", [(32, False, "paged"), (8, False, "flash_paged"), (64, True, "flash_paged")])
+@pytest.mark.parametrize("BS,fp8,layout", [(32, False, "paged"), (8, False, "flash_paged"), (64, True, "flash_paged"),
+                                           (8, True, "paged")])
 def test_engine_config_descriptor_decodes(BS, fp8, layout):
     """A decode descriptor set up by tl_engine_apply_config (CudaEngineConfig's
     paged_kv_block_size, use_fp8_kv, attention_layout), run against the

@@ -55,7 +55,7 @@ int check_decode(const tl_decode_desc* d) {
   if (d->kv_dtype == TL_DTYPE_FP8_E4M3 && d->q_dtype == TL_DTYPE_F32)
     return fail(TL_ERR_NOT_IMPLEMENTED, "FP8 KV needs F16 or BF16 q");
   // head size 128: the matrix-core decode, any power-of-two block size
-  // 8 .. 256 (16 .. 256 for FP8); the FMA decode: head sizes 64 / 256 (and
+  // 8 .. 256 (FP8 too); the FMA decode: head sizes 64 / 256 (and
   // 80 / 96 for 2-byte pools) at block size 16; F32 pools: head sizes 64 /
   // 128 / 256 at block size 16 (the shapes of paged_attention_v1.cu:198-209)
   const int hs = d->head_size, bs = d->block_size;
@@ -72,7 +72,7 @@ int check_decode(const tl_decode_desc* d) {
     shape_ok = false;
   if (!shape_ok)
     return fail(TL_ERR_NOT_IMPLEMENTED,
-                "head_size=%d block_size=%d kv_dtype=%d (built: head 128 with block sizes 8..256, FP8 16..256; "
+                "head_size=%d block_size=%d kv_dtype=%d (built: head 128 with block sizes 8..256; "
                 "heads 64/256, and 80/96 for 2-byte KV, with block size 16; F32 KV heads 64/128/256 with "
                 "block size 16)",
                 hs, bs, d->kv_dtype);
@@ -609,8 +609,10 @@ static int check_kivi(const tl_kivi_desc* d) {
   if (d->num_seqs < 0) return fail(TL_ERR_INVALID_ARGUMENT, "num_seqs=%d", d->num_seqs);
   if (d->num_kv_heads <= 0 || d->num_heads <= 0 || d->num_heads % d->num_kv_heads)
     return fail(TL_ERR_INVALID_ARGUMENT, "num_heads=%d / num_kv_heads=%d", d->num_heads, d->num_kv_heads);
-  if (d->head_size != tl::kKiviHead || d->block_size != 16)
-    return fail(TL_ERR_NOT_IMPLEMENTED, "paged KIVI is built for head_size 128, block_size 16");
+  if (d->head_size != tl::kKiviHead)
+    return fail(TL_ERR_NOT_IMPLEMENTED, "paged KIVI is built for head_size 128");
+  if (d->block_size < 8 || d->block_size > 256 || (d->block_size & (d->block_size - 1)))
+    return fail(TL_ERR_NOT_IMPLEMENTED, "paged KIVI block_size=%d (built: powers of two 8 .. 256)", d->block_size);
   if (d->max_blocks_per_seq <= 0 || d->num_blocks <= 0 || d->max_pages_per_seq <= 0 || d->num_pages <= 0)
     return fail(TL_ERR_INVALID_ARGUMENT, "table and pool sizes must be > 0");
   if (d->residual_length < 0) return fail(TL_ERR_INVALID_ARGUMENT, "residual_length=%d", d->residual_length);
@@ -904,6 +906,7 @@ static int kivi_decode_impl(const tl_kivi_desc* desc, void* out, const void* q, 
   a.out = out; a.q = q; a.pages = pages; a.page_tables = page_tables;
   a.k_cache = k_cache; a.v_cache = v_cache; a.block_tables = block_tables; a.seq_lens = seq_lens;
   a.num_seqs = desc->num_seqs; a.num_heads = desc->num_heads; a.num_kv_heads = desc->num_kv_heads;
+  a.block_size = desc->block_size;
   a.max_blocks_per_seq = desc->max_blocks_per_seq; a.num_blocks = desc->num_blocks;
   a.max_pages_per_seq = desc->max_pages_per_seq; a.num_pages = desc->num_pages;
   a.residual_length = desc->residual_length; a.gqa_map = desc->gqa_map;
@@ -1019,8 +1022,16 @@ int tl_chunked_prefill(const tl_prefill_desc* d, void* out, const void* q, const
     return fail(TL_ERR_INVALID_ARGUMENT, "gqa_map=%d", d->gqa_map);
   if (d->dtype != TL_DTYPE_F16 && d->dtype != TL_DTYPE_BF16)
     return fail(TL_ERR_NOT_IMPLEMENTED, "prefill dtype=%d (built: F16, BF16)", d->dtype);
-  if (d->head_size != 128 || (d->block_size != 16 && d->block_size != 32))
-    return fail(TL_ERR_NOT_IMPLEMENTED, "prefill head_size=%d block_size=%d (built: 128 x 16/32)",
+  const int32_t kv_dtype = d->kv_dtype == 0 ? d->dtype : d->kv_dtype;
+  if (kv_dtype != d->dtype && kv_dtype != TL_DTYPE_FP8_E4M3)
+    return fail(TL_ERR_NOT_IMPLEMENTED, "prefill kv_dtype=%d with dtype=%d (built: the q type, FP8 E4M3)",
+                d->kv_dtype, d->dtype);
+  if (kv_dtype == TL_DTYPE_FP8_E4M3 &&
+      (!(d->k_scale > 0.f) || !(d->k_scale < INFINITY) || !(d->v_scale > 0.f) || !(d->v_scale < INFINITY)))
+    return fail(TL_ERR_INVALID_ARGUMENT, "FP8 pool scales k_scale=%g v_scale=%g must be positive and finite",
+                (double)d->k_scale, (double)d->v_scale);
+  if (d->head_size != 128 || d->block_size < 8 || d->block_size > 256 || (d->block_size & (d->block_size - 1)))
+    return fail(TL_ERR_NOT_IMPLEMENTED, "prefill head_size=%d block_size=%d (built: 128 x powers of two 8..256)",
                 d->head_size, d->block_size);
   if (d->num_prefill_seqs < 0 || d->num_prefill_seqs > d->num_seqs)
     return fail(TL_ERR_INVALID_ARGUMENT, "num_prefill_seqs=%d outside [0, %d]", d->num_prefill_seqs,
@@ -1046,11 +1057,16 @@ int tl_chunked_prefill(const tl_prefill_desc* d, void* out, const void* q, const
   a.block_tables = block_tables; a.seq_lens = seq_lens;
   a.num_seqs = d->num_seqs; a.num_heads = d->num_heads; a.num_kv_heads = d->num_kv_heads;
   a.block_size = d->block_size; a.max_blocks_per_seq = d->max_blocks_per_seq; a.num_blocks = d->num_blocks;
-  a.dtype = d->dtype;   // TL_DTYPE_F16 / TL_DTYPE_BF16 share the kernels' Kind codes
+  a.dtype = d->dtype;   // TL_DTYPE_F16 / BF16 / FP8_E4M3 share the kernels' Kind codes
+  a.kv_dtype = kv_dtype;
   a.gqa_map = d->gqa_map; a.max_q_len = max_q_len; a.scale = d->scale;
+  a.k_scale = kv_dtype == TL_DTYPE_FP8_E4M3 ? d->k_scale : 1.f;
+  a.v_scale = kv_dtype == TL_DTYPE_FP8_E4M3 ? d->v_scale : 1.f;
   a.num_prefill_seqs = d->num_prefill_seqs;
   a.stream = (hipStream_t)stream;
-  if (tl::launch_prefill(a)) return fail(TL_ERR_BACKEND, "prefill launch failed");
+  const int lrc = tl::launch_prefill(a);
+  if (lrc == 3) return fail(TL_ERR_NOT_IMPLEMENTED, "no prefill kernel for block_size=%d", d->block_size);
+  if (lrc) return fail(TL_ERR_BACKEND, "prefill launch failed");
   return ok();
 }
 

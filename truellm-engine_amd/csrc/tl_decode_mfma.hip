@@ -1,6 +1,5 @@
 // tl_decode_mfma.hip -- paged-attention decode on the matrix cores
-// (head_size 128; block sizes 8 .. 256 for 2-byte KV, 16 .. 256 for FP8
-// E4M3 KV).
+// (head_size 128; block sizes 8 .. 256 for 2-byte and FP8 E4M3 KV).
 //
 // The wavefronts are in tl_mfma_wave.hpp.  Why matrix cores for decode:
 //   * FP8: a byte is one element, so per byte of HBM traffic there are twice
@@ -158,9 +157,7 @@ int launch_typed(const DecodeLaunch& a) {
 template <Kind KV, Kind QK>
 int launch_bs(const DecodeLaunch& a) {
   switch (a.block_size) {
-    case 8:
-      if constexpr (KV != Kind::FP8) return launch_typed<KV, QK, 8>(a);   // a 16-byte FP8 V run spans two blocks
-      return 3;
+    case 8: return launch_typed<KV, QK, 8>(a);
     case 16: return launch_typed<KV, QK, 16>(a);
     case 32: return launch_typed<KV, QK, 32>(a);
     case 64: return launch_typed<KV, QK, 64>(a);

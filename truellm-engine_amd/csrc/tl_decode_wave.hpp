@@ -48,6 +48,7 @@ struct Params {
   int group, head_slices, gqa_map;
   float qk_scale;  // softmax scale * k dequant scale * log2(e)
   float v_scale;
+  int block_size = 0;   // pool block size, read by kernels built for any block size
 };
 
 // The work item of a decode workgroup: returns the index of its (sequence,
@@ -99,22 +100,23 @@ __device__ __forceinline__ int table_entry_bs(const Params& p, const int32_t* ta
 }
 
 // K of head-dim pairs (2m, 2m+1), m = dl + 16 j: rows 2m and 2m+1 of the
-// lane's 8-token run th of one block ([D][BS] layout, 16-byte chunks).
-template <int KP, int CPR>
-__device__ __forceinline__ void load_k_pairs(u32x4 (&kr)[KP][2], const char* blk, int dl, int th) {
+// lane's 8-token run th (the 16-byte chunk th of a row) of one block ([D][BS]
+// layout, cpr = BS / 8 chunks per row).
+template <int KP>
+__device__ __forceinline__ void load_k_pairs(u32x4 (&kr)[KP][2], const char* blk, int dl, int th, int cpr) {
 #pragma unroll
   for (int j = 0; j < KP; ++j) {
-    const int c = 2 * (dl + 16 * j) * CPR + th;
+    const int c = 2 * (dl + 16 * j) * cpr + th;
     kr[j][0] = load16_stream(blk + c * 16);
-    kr[j][1] = load16_stream(blk + (c + CPR) * 16);
+    kr[j][1] = load16_stream(blk + (c + cpr) * 16);
   }
 }
 
 // V rows d = 16 j + dl of the lane's 8-token run th of one block.
-template <int VD, int CPR>
-__device__ __forceinline__ void load_v_rows(u32x4 (&vr)[VD], const char* blk, int dl, int th) {
+template <int VD>
+__device__ __forceinline__ void load_v_rows(u32x4 (&vr)[VD], const char* blk, int dl, int th, int cpr) {
 #pragma unroll
-  for (int j = 0; j < VD; ++j) vr[j] = load16_stream(blk + ((16 * j + dl) * CPR + th) * 16);
+  for (int j = 0; j < VD; ++j) vr[j] = load16_stream(blk + ((16 * j + dl) * cpr + th) * 16);
 }
 
 // The key rotation hook of decode2_wave: called with the lane's K rows as
@@ -130,24 +132,44 @@ struct NoKeyRotation {
 // s_acc_w [4][HEAD] unnormalised outputs, s_m_w [4] running max (log2 units),
 // s_l_w [4] sums.  s_p_w is the wavefront's weight exchange area: [4][4][4]
 // words, twice that for bf16 (the weights' high and low bf16 parts).
+// An iteration is 32 consecutive tokens; token group tg is the 8-token run
+// it + 8 tg, which lies in one block for every block size (a power of two
+// >= 8): in block (it + 8 tg) / BS, chunk ((it + 8 tg) % BS) / 8 of its
+// rows.  BS is the block size, or 0 for p.block_size read at run time.
 template <Kind KV, int HEAD, int BS, class Rot = NoKeyRotation>
 __device__ __forceinline__ void decode2_wave(const Params& p, int seq, int kvh, int hs, int first_it,
                                              int t1, int step, uint32_t* s_p_w, float* s_acc_w,
                                              float* s_m_w, float* s_l_w, const Rot& rot = Rot()) {
   constexpr int GT = kWaveHeads;
-  constexpr int CPR = BS / 8;             // 16-byte chunks per head-dim row of a block
-  constexpr int BPI = 4 / CPR;            // blocks per wave iteration
-  constexpr int TPI = BPI * BS;           // tokens per wave iteration
   constexpr int KP = HEAD / 32;           // head-dim pairs per lane (q.k)
   constexpr int VD = HEAD / 16;           // head dims per lane (p.v)
-  constexpr int BLOCK_BYTES = HEAD * BS * 2;
-  static_assert(TPI == 32, "four 8-token groups per wave iteration");
+  // a block holds a whole number of iterations' runs: the lane's chunk in
+  // its block row is the same on every iteration
+  constexpr bool kFixedChunk = BS > 0 && BS <= 32;
+  static_assert(BS == 0 || (BS >= 8 && (BS & (BS - 1)) == 0), "block size: a power of two >= 8");
+  const int bs = BS > 0 ? BS : p.block_size;
+  const int lbs = BS > 0 ? __builtin_ctz(BS) : __builtin_ctz((unsigned)p.block_size);
+  const int cpr = bs >> 3;                // 16-byte chunks per head-dim row of a block
+  const int64_t block_bytes = (int64_t)HEAD * bs * 2;
   using D2 = Dot2<KV>;
 
   const int lane = threadIdx.x % kWave;
   const int tg = (lane >> 2) & 3, dl = (lane & 3) | ((lane >> 4) << 2);
-  const int blk_in = tg / CPR, th = tg % CPR;
   const int g_lane = lane >> 4, tp = lane & 3;
+  // the lane's run chunk in its block row for the iteration at token i
+  auto run_chunk = [&](int i) {
+    if constexpr (kFixedChunk) return tg % (BS / 8);
+    else return ((i + 8 * tg) & (bs - 1)) >> 3;
+  };
+  // physical block of the lane's run of the iteration at token i, or -1
+  // for a hole, a run at or past t1 or an entry outside the pool
+  auto run_block = [&](const int32_t* table, int i) {
+    if constexpr (kFixedChunk) return table_entry_bs<BS>(p, table, i + (tg / (BS / 8)) * BS, t1);
+    const int tok = i + 8 * tg, lb = tok >> lbs;
+    int ph = -1;
+    if (tok < t1 && lb < p.max_blocks_per_seq) ph = table[lb];
+    return (ph >= p.num_blocks) ? -1 : ph;
+  };
 
   // q as (dim 2m, 2m+1) pairs, m = dl + 16 j, straight from [S, H, D]
   uint32_t qp[GT][KP];
@@ -169,9 +191,9 @@ __device__ __forceinline__ void decode2_wave(const Params& p, int seq, int kvh, 
   }
 
   const int32_t* table = p.block_tables + (int64_t)seq * p.max_blocks_per_seq;
-  const int64_t pool_stride = (int64_t)p.num_kv_heads * BLOCK_BYTES;
-  const char* kbase0 = p.k_cache + (int64_t)kvh * BLOCK_BYTES;
-  const char* vbase0 = p.v_cache + (int64_t)kvh * BLOCK_BYTES;
+  const int64_t pool_stride = (int64_t)p.num_kv_heads * block_bytes;
+  const char* kbase0 = p.k_cache + (int64_t)kvh * block_bytes;
+  const char* vbase0 = p.v_cache + (int64_t)kvh * block_bytes;
 
   // Pipeline: the K loads of iteration i+1 are issued as soon as the scores
   // of iteration i are formed, the V loads of i+1 once p.v of i is done, and
@@ -179,20 +201,21 @@ __device__ __forceinline__ void decode2_wave(const Params& p, int seq, int kvh, 
   // keeps one iteration of K/V in flight while it computes.  Holes load
   // block 0 and are masked.
   int it = first_it;
-  int ph_cur = table_entry_bs<BS>(p, table, it + blk_in * BS, t1);
-  int ph_next = table_entry_bs<BS>(p, table, it + step + blk_in * BS, t1);
+  int ph_cur = run_block(table, it);
+  int ph_next = run_block(table, it + step);
   u32x4 kr[KP][2], vr[VD];
   if (it < t1) {
-    load_k_pairs<KP, CPR>(kr, kbase0 + (int64_t)max(ph_cur, 0) * pool_stride, dl, th);
-    load_v_rows<VD, CPR>(vr, vbase0 + (int64_t)max(ph_cur, 0) * pool_stride, dl, th);
+    load_k_pairs<KP>(kr, kbase0 + (int64_t)max(ph_cur, 0) * pool_stride, dl, run_chunk(it), cpr);
+    load_v_rows<VD>(vr, vbase0 + (int64_t)max(ph_cur, 0) * pool_stride, dl, run_chunk(it), cpr);
   }
 
 #pragma unroll 1
   for (; it < t1; it += step) {
-    const int ph_nn = table_entry_bs<BS>(p, table, it + 2 * step + blk_in * BS, t1);
+    const int ph_nn = run_block(table, it + 2 * step);
     const bool has_next = it + step < t1;
-    const int blk_tok = it + blk_in * BS;                // first token of this lane's block
-    if constexpr (Rot::kActive) rot(kr, blk_tok + th * 8, dl);
+    const int tok0 = it + 8 * tg;                        // first token of this lane's run
+    const int th_next = run_chunk(it + step);
+    if constexpr (Rot::kActive) rot(kr, tok0, dl);
 
     // ---- q.k partials over this lane's dim pairs, 8 tokens x 4 heads ----
     float s[GT * 8];
@@ -211,10 +234,10 @@ __device__ __forceinline__ void decode2_wave(const Params& p, int seq, int kvh, 
         }
       }
     if (has_next)
-      load_k_pairs<KP, CPR>(kr, kbase0 + (int64_t)max(ph_next, 0) * pool_stride, dl, th);
+      load_k_pairs<KP>(kr, kbase0 + (int64_t)max(ph_next, 0) * pool_stride, dl, th_next, cpr);
     transpose_reduce_5410<GT * 8>(s, lane);             // -> (head g_lane, tokens 2tp, 2tp+1)
 
-    const int tok = blk_tok + th * 8 + 2 * tp;
+    const int tok = tok0 + 2 * tp;
     const bool ok0 = ph_cur >= 0 && tok < t1, ok1 = ph_cur >= 0 && tok + 1 < t1;
     const float sc0 = ok0 ? s[0] * p.qk_scale : -INFINITY;
     const float sc1 = ok1 ? s[1] * p.qk_scale : -INFINITY;
@@ -251,13 +274,13 @@ __device__ __forceinline__ void decode2_wave(const Params& p, int seq, int kvh, 
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
     // ---- holes, and slots past the end of a partial block, may hold anything ----
-    if (ph_cur < 0 || blk_tok + BS > t1) {
+    if (ph_cur < 0 || tok0 + 8 > t1) {
 #pragma unroll
       for (int j = 0; j < VD; ++j) {
         uint32_t w4[4] = {vr[j].x, vr[j].y, vr[j].z, vr[j].w};
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
-          const int t = blk_tok + th * 8 + 2 * w;
+          const int t = tok0 + 2 * w;
           if (ph_cur < 0 || t >= t1) w4[w] = 0u;
           else if (t + 1 >= t1) w4[w] &= 0xffffu;
         }
@@ -285,7 +308,7 @@ __device__ __forceinline__ void decode2_wave(const Params& p, int seq, int kvh, 
         acc[g][j] = a;
       }
     if (has_next)
-      load_v_rows<VD, CPR>(vr, vbase0 + (int64_t)max(ph_next, 0) * pool_stride, dl, th);
+      load_v_rows<VD>(vr, vbase0 + (int64_t)max(ph_next, 0) * pool_stride, dl, th_next, cpr);
     ph_cur = ph_next;
     ph_next = ph_nn;
   }

@@ -50,8 +50,7 @@ inline bool decode_uses_mfma(int kv_dtype, int num_heads, int num_kv_heads, int 
   (void)num_heads;
   if (head_size != 128 || num_kv_heads <= 0) return false;
   const bool pow2 = block_size > 0 && (block_size & (block_size - 1)) == 0 && block_size <= 256;
-  if (kv_dtype == 32) return pow2 && block_size >= 16;                   // FP8 E4M3
-  return (kv_dtype == 1 || kv_dtype == 2) && pow2 && block_size >= 8;     // f16, bf16
+  return (kv_dtype == 32 || kv_dtype == 1 || kv_dtype == 2) && pow2 && block_size >= 8;   // FP8 E4M3, f16, bf16
 }
 
 struct CacheLaunch {
@@ -158,12 +157,12 @@ struct KiviDecodeLaunch {
   const void* q;                // [S, H, 128] fp16
   const void* pages;
   const int32_t* page_tables;
-  const void* k_cache;          // fp16 residual window, [N, n_kv, 128, 16]
+  const void* k_cache;          // fp16 residual window, [N, n_kv, 128, block_size]
   const void* v_cache;
   const int32_t* block_tables;
   const int32_t* seq_lens;
   float* part_m; float* part_l; void* part_o;   // fp32 split-K partials
-  int num_seqs, num_heads, num_kv_heads, max_blocks_per_seq, num_blocks;
+  int num_seqs, num_heads, num_kv_heads, block_size, max_blocks_per_seq, num_blocks;
   int max_pages_per_seq, num_pages, residual_length, gqa_map;
   int num_partitions, partition_pages;
   int bits;                     // page code width: 4 or 8
@@ -183,15 +182,17 @@ struct PrefillLaunch {
   void* out;                    // [total_q, H, 128], dtype
   const void* q;                // [total_q, H, 128], dtype
   const int32_t* cu_q_lens;     // [num_seqs + 1]
-  const void* k_cache;          // [N, n_kv, 128, bs], dtype
+  const void* k_cache;          // [N, n_kv, 128, bs], kv_dtype
   const void* v_cache;
   const int32_t* block_tables;
   const int32_t* seq_lens;
   int num_seqs, num_heads, num_kv_heads, block_size, max_blocks_per_seq, num_blocks;
   int dtype, gqa_map, max_q_len, num_prefill_seqs;
-  float scale;
+  int kv_dtype;                 // dtype, or FP8 E4M3 (k_scale, v_scale: the per-tensor scales)
+  float scale, k_scale, v_scale;
   hipStream_t stream;
 };
+// Returns 0, 3 (no kernel for the block size) or 5 (launch error).
 int launch_prefill(const PrefillLaunch& a);
 
 // out[i] = e4m3(float(in[i]) * scale) for i < n (in: F16, BF16 or F32).

@@ -497,19 +497,21 @@ struct NewestToken {
   bool ok;      // false: a hole in the block table (the token is masked)
 };
 
-// From the fp16 pool, at the token's block-table position.
+// From the fp16 pool, at the token's block-table position (BS: the block
+// size, or 0 for p.block_size).
+template <int BS>
 __device__ __forceinline__ NewestToken newest_from_pool(const Params& p, int seq, int kvh, int pos, int lane) {
-  constexpr int BS = 16;
-  const int lb = pos / BS;
+  const int bs = BS > 0 ? BS : p.block_size;
+  const int lb = pos / bs;
   int ph = (pos >= 0 && lb < p.max_blocks_per_seq) ? p.block_tables[(int64_t)seq * p.max_blocks_per_seq + lb] : -1;
   if (ph >= p.num_blocks) ph = -1;
   NewestToken t{0u, 0u, ph >= 0};
   if (ph >= 0) {
-    const int64_t off = (((int64_t)ph * p.num_kv_heads + kvh) * kKiviHead + 2 * lane) * BS + pos % BS;
+    const int64_t off = (((int64_t)ph * p.num_kv_heads + kvh) * kKiviHead + 2 * lane) * bs + pos % bs;
     const uint16_t* kp = (const uint16_t*)p.k_cache + off;
     const uint16_t* vp = (const uint16_t*)p.v_cache + off;
-    t.k = uint32_t(kp[0]) | (uint32_t(kp[BS]) << 16);
-    t.v = uint32_t(vp[0]) | (uint32_t(vp[BS]) << 16);
+    t.k = uint32_t(kp[0]) | (uint32_t(kp[bs]) << 16);
+    t.v = uint32_t(vp[0]) | (uint32_t(vp[bs]) << 16);
   }
   return t;
 }
@@ -634,17 +636,37 @@ __device__ __forceinline__ void newest_state(const Params& p, const NewestToken&
 
 // The new token into the fp16 pool, by one wavefront holding its channels
 // 2 lane and 2 lane + 1 (t).  A token's 128 channels are 2-byte elements
-// 32 bytes apart, and HBM3E has no byte masks: scattered 2-byte stores cost
-// a step at batch 64 about 4 us (left in L2) or 1.4 us (written through),
-// mostly in the memory's read-modify-writes.  So the block's rows of this
-// kv head (128 channels x 16 slots, 4 KiB each of K and V) are read, the
-// slot replaced, and the rows written back whole (about 0.3 us).  The other
-// slots keep their bytes; no other writer may touch the block during the
-// call (a block that a sequence appends to belongs to that sequence; the
-// other head slices of the same (seq, kv head) write the same bytes).
+// 2 BS bytes apart, and HBM3E has no byte masks: scattered 2-byte stores
+// cost a step at batch 64 (block size 16) about 4 us (left in L2) or 1.4 us
+// (written through), mostly in the memory's read-modify-writes.  So at
+// block size 16 the block's rows of this kv head (128 channels x 16 slots,
+// 4 KiB each of K and V) are read, the slot replaced, and the rows written
+// back whole (about 0.3 us).  At other block sizes (BS = 0: p.block_size)
+// each channel's 16-byte chunk holding the slot is rewritten (for block
+// size 8 that is the whole row).  The other slots keep their bytes; no
+// other writer may touch the block during the call (a block that a
+// sequence appends to belongs to that sequence; the other head slices of
+// the same (seq, kv head) write the same bytes).
+template <int BS>
 __device__ __forceinline__ void store_newest(const PageJob& j, const NewestToken& t, int seq, int kvh, int lane) {
-  constexpr int BS = 16;   // the paged KIVI calls take block_size 16 only
   const int32_t slot = j.slots[seq];
+  if constexpr (BS != 16) {
+    const int bs = j.block_size;
+    const int blk = slot >= 0 ? slot / bs : -1;
+    if (blk < 0 || blk >= j.num_blocks) return;
+    const int s = slot % bs;
+    const int64_t base = ((int64_t)blk * j.num_kv_heads + kvh) * kKiviHead * bs + (s & ~7);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int64_t off = base + (int64_t)(2 * lane + h) * bs;
+      u32x4 kc = load16(j.k_cache + off), vc = load16(j.v_cache + off);
+      put_half(kc, s & 7, h ? t.k >> 16 : t.k);
+      put_half(vc, s & 7, h ? t.v >> 16 : t.v);
+      *reinterpret_cast<u32x4*>(j.k_cache + off) = kc;
+      *reinterpret_cast<u32x4*>(j.v_cache + off) = vc;
+    }
+    return;
+  }
   const int blk = slot >= 0 ? slot / BS : -1;
   if (blk < 0 || blk >= j.num_blocks) return;
   const int64_t base = ((int64_t)blk * j.num_kv_heads + kvh) * kKiviHead * BS;
@@ -695,7 +717,9 @@ struct KiviDecodeSmem {
 // Two wavefronts per SIMD (at most 256 registers, VGPRs and AGPRs together):
 // with 4-wavefront workgroups the compiler would otherwise take more and
 // halve the occupancy.
-template <int NW, bool FINAL, bool APPEND, int BITS, bool ROPE>
+// BS: the fp16 pool's block size, 16, or 0 for any other (read from the
+// launch at run time).
+template <int NW, bool FINAL, bool APPEND, int BITS, bool ROPE, int BS>
 __global__ __launch_bounds__(NW * kWave, 2) void kivi_decode_kernel(KiviParams k) {
   using Smem = KiviDecodeSmem<NW>;
   using Build = KiviBuildSmem<BITS>;
@@ -747,7 +771,8 @@ __global__ __launch_bounds__(NW * kWave, 2) void kivi_decode_kernel(KiviParams k
                                   lq / kKiviPageTokens - 1, L, tid);
       __syncthreads();   // the page is visible to the workgroup; the LDS is free again
     }
-    if (last && !has_res && wave == 0) store_newest(k.job, newest_from_row(k.job, seq, kvh, tid), seq, kvh, tid);
+    if (last && !has_res && wave == 0)
+      store_newest<BS>(k.job, newest_from_row(k.job, seq, kvh, tid), seq, kvh, tid);
   }
   if (wave < page_waves) {
     // Single pass runs two workgroups per CU, b and b + grid/2 (dispatch
@@ -763,23 +788,24 @@ __global__ __launch_bounds__(NW * kWave, 2) void kivi_decode_kernel(KiviParams k
     const int lane = tid % kWave;
     NewestToken nt;
     if constexpr (APPEND)
-      nt = k.job.slots[seq] >= 0 ? newest_from_row(k.job, seq, kvh, lane) : newest_from_pool(p, seq, kvh, L - 1, lane);
+      nt = k.job.slots[seq] >= 0 ? newest_from_row(k.job, seq, kvh, lane)
+                                 : newest_from_pool<BS>(p, seq, kvh, L - 1, lane);
     else
-      nt = newest_from_pool(p, seq, kvh, L - 1, lane);
+      nt = newest_from_pool<BS>(p, seq, kvh, L - 1, lane);
     if constexpr (ROPE) {
-      decode2_wave<Kind::F16, kKiviHead, 16>(p, seq, kvh, hs, lq, L - 1, 32, &sd.p[wave][0], &sd.acc[wave][0][0],
+      decode2_wave<Kind::F16, kKiviHead, BS>(p, seq, kvh, hs, lq, L - 1, 32, &sd.p[wave][0], &sd.acc[wave][0][0],
                                              &sd.m[wave][0], &sd.l[wave][0], KiviWindowRope{k});
       NewestToken ntr = nt;
       ntr.k = rope_newest_key(k, nt.k, L - 1, lane);
       newest_state(p, ntr, seq, kvh, hs, lane, &sd.acc[NW][0][0], &sd.m[NW][0], &sd.l[NW][0]);
     } else {
-      decode2_wave<Kind::F16, kKiviHead, 16>(p, seq, kvh, hs, lq, L - 1, 32, &sd.p[wave][0],
+      decode2_wave<Kind::F16, kKiviHead, BS>(p, seq, kvh, hs, lq, L - 1, 32, &sd.p[wave][0],
                                              &sd.acc[wave][0][0], &sd.m[wave][0], &sd.l[wave][0]);
       newest_state(p, nt, seq, kvh, hs, lane, &sd.acc[NW][0][0], &sd.m[NW][0], &sd.l[NW][0]);
     }
     // the token's store, at the end of the window, off the page wavefronts'
     // path (the window ends halfway through the launch)
-    if constexpr (APPEND) store_newest(k.job, nt, seq, kvh, lane);
+    if constexpr (APPEND) store_newest<BS>(k.job, nt, seq, kvh, lane);
     kivi_pages_wave<BITS, ROPE>(k, seq, kvh, hs, pg1 - res_pages, pg1, 1, &sd.p[wave][0], &sd.acc[NW + 1][0][0],
                     &sd.m[NW + 1][0], &sd.l[NW + 1][0], false, false, -1);
   }
@@ -788,12 +814,19 @@ __global__ __launch_bounds__(NW * kWave, 2) void kivi_decode_kernel(KiviParams k
                                                         &sd.acc[0][0][0], seq, kvh, hs, part, tid, NW * kWave);
 }
 
+template <int NW, bool FINAL, int BITS, bool ROPE, int BS>
+void launch_decode_bs(const KiviParams& k, bool append, unsigned grid, hipStream_t stream) {
+  if (append)
+    hipLaunchKernelGGL((kivi_decode_kernel<NW, FINAL, true, BITS, ROPE, BS>), dim3(grid), dim3(NW * kWave), 0, stream,
+                       k);
+  else
+    hipLaunchKernelGGL((kivi_decode_kernel<NW, FINAL, false, BITS, ROPE, BS>), dim3(grid), dim3(NW * kWave), 0, stream,
+                       k);
+}
 template <int NW, bool FINAL, int BITS, bool ROPE>
 void launch_decode_bits(const KiviParams& k, bool append, unsigned grid, hipStream_t stream) {
-  if (append)
-    hipLaunchKernelGGL((kivi_decode_kernel<NW, FINAL, true, BITS, ROPE>), dim3(grid), dim3(NW * kWave), 0, stream, k);
-  else
-    hipLaunchKernelGGL((kivi_decode_kernel<NW, FINAL, false, BITS, ROPE>), dim3(grid), dim3(NW * kWave), 0, stream, k);
+  if (k.base.block_size == 16) launch_decode_bs<NW, FINAL, BITS, ROPE, 16>(k, append, grid, stream);
+  else launch_decode_bs<NW, FINAL, BITS, ROPE, 0>(k, append, grid, stream);
 }
 template <int NW, bool FINAL>
 void launch_decode(const KiviParams& k, bool append, int bits, unsigned grid, hipStream_t stream) {
@@ -824,6 +857,7 @@ int launch_kivi_decode(const KiviDecodeLaunch& a) {
   p.gqa_map = a.gqa_map;
   p.qk_scale = a.scale * kLog2e;
   p.v_scale = 1.f;
+  p.block_size = a.block_size;
   k.pages = (const uint8_t*)a.pages; k.page_tables = a.page_tables;
   k.max_pages_per_seq = a.max_pages_per_seq; k.num_pages = a.num_pages;
   k.residual_length = a.residual_length; k.partition_pages = a.partition_pages;

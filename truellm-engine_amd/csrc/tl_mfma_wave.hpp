@@ -1,6 +1,6 @@
 // tl_mfma_wave.hpp -- decode wavefronts on the matrix cores for head_size
-// 128: FP8 E4M3 KV (fp8_wave, block sizes 16 .. 256) and 2-byte KV
-// (mfma2_wave, block sizes 8 .. 256).  An iteration covers 64 (FP8) or 32
+// 128: FP8 E4M3 KV (fp8_wave) and 2-byte KV (mfma2_wave), block sizes
+// 8 .. 256.  An iteration covers 64 (FP8) or 32
 // (2-byte) consecutive tokens: several blocks when the block is smaller, a
 // part of one block (at the iteration's offset in it) when it is larger.
 //
@@ -112,8 +112,11 @@ __device__ __forceinline__ Blocks<NB> table_blocks(const Params& p, TableRow tab
 // set in LDS.
 template <int NB>
 __device__ __forceinline__ int pick(const Blocks<NB>& b, int i) {
-  static_assert(NB == 1 || NB == 2 || NB == 4, "1, 2 or 4 blocks per iteration");
-  if constexpr (NB == 4) return i == 0 ? b.e[0] : i == 1 ? b.e[1] : i == 2 ? b.e[2] : b.e[3];
+  static_assert(NB == 1 || NB == 2 || NB == 4 || NB == 8, "1, 2, 4 or 8 blocks per iteration");
+  if constexpr (NB == 8)
+    return i < 4 ? (i < 2 ? (i == 0 ? b.e[0] : b.e[1]) : (i == 2 ? b.e[2] : b.e[3]))
+                 : (i < 6 ? (i == 4 ? b.e[4] : b.e[5]) : (i == 6 ? b.e[6] : b.e[7]));
+  else if constexpr (NB == 4) return i == 0 ? b.e[0] : i == 1 ? b.e[1] : i == 2 ? b.e[2] : b.e[3];
   else if constexpr (NB == 2) return i == 0 ? b.e[0] : b.e[1];
   else return b.e[0];
 }
@@ -125,6 +128,18 @@ __device__ __forceinline__ u32x4 keep_bytes(const u32x4& v, int n) {
   for (int i = 0; i < 4; ++i) {
     const int k = n - 4 * i;   // bytes of this word to keep
     const uint32_t mask = k >= 4 ? 0xffffffffu : k <= 0 ? 0u : (0xffffffffu >> (32 - 8 * k));
+    w[i] &= mask;
+  }
+  return u32x4{w[0], w[1], w[2], w[3]};
+}
+// Keeps byte j of a 16-token FP8 row where bit j of keep is set.
+__device__ __forceinline__ u32x4 keep_byte_mask(const u32x4& v, uint32_t keep) {
+  uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    uint32_t mask = 0;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) mask |= ((keep >> (4 * i + b)) & 1u) ? (0xffu << (8 * b)) : 0u;
     w[i] &= mask;
   }
   return u32x4{w[0], w[1], w[2], w[3]};
@@ -198,8 +213,9 @@ struct NoFlush {
 // value, subnormals and NaN included, is an f16 value.
 // Scores: lane (m, kg) holds head m, iteration token 16 kg + 4 r + i.
 // V: lane (m, kg) loads the 16 bytes of row d = 16 dt + m for iteration
-// tokens 16 kg .. 16 kg + 15 (one block row at block size 16); MFMA h
-// takes its tokens 8 h .. 8 h + 7.
+// tokens 16 kg .. 16 kg + 15 (one block row at block size 16; at block size
+// 8 two 8-byte runs, one from each of the two blocks); MFMA h takes its
+// tokens 8 h .. 8 h + 7.
 // bf16 q is brought into f16 range by a power of two per head (exact: max
 // |q| in [2^14, 2^15)); the factor returns in the score scale.  The
 // dequant scales fold into the score scale (k_scale) and the output
@@ -207,8 +223,9 @@ struct NoFlush {
 template <Kind QK, int BS, class Flush = NoFlush>
 __device__ __forceinline__ State fp8_wave(const Params& p, int seq, int kvh, int hs, int first_it, int t1,
                                           int step, const Flush& flush = Flush()) {
-  static_assert(BS >= 16 && (BS & (BS - 1)) == 0, "block size: a power of two >= 16");
+  static_assert(BS >= 8 && (BS & (BS - 1)) == 0, "block size: a power of two >= 8");
   constexpr int TPI = 64, RB = BS;           // tokens per iteration; bytes per head-dim row of a block
+  constexpr bool kSplitRun = BS == 8;        // a lane's 16-token V run spans two blocks
   constexpr int kBlockBytes = kHead * RB;
   constexpr int NB = blocks_per_iteration<BS, TPI>();
   const int lane = threadIdx.x % kWave;
@@ -264,9 +281,24 @@ __device__ __forceinline__ State fp8_wave(const Params& p, int seq, int kvh, int
 #pragma unroll
     for (int j = 0; j < 32; ++j) kw[j] = ld_nt(base + 4 * RB * j);
   };
-  auto load_v = [&](u32x4 (&vr)[8], const char* base) {
+  // base: the run's block (its first 8 tokens' block at block size 8),
+  // base2: the block of tokens 8 .. 15 at block size 8 (unused otherwise)
+  auto load_v = [&](u32x4 (&vr)[8], const char* base, const char* base2) {
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) vr[dt] = load16_stream(base + 16 * RB * dt);
+    for (int dt = 0; dt < 8; ++dt) {
+      if constexpr (kSplitRun) {
+        typedef unsigned u2v __attribute__((ext_vector_type(2)));
+        const u2v lo = __builtin_nontemporal_load(reinterpret_cast<const u2v*>(base + 16 * RB * dt));
+        const u2v hi = __builtin_nontemporal_load(reinterpret_cast<const u2v*>(base2 + 16 * RB * dt));
+        vr[dt] = u32x4{lo.x, lo.y, hi.x, hi.y};
+      } else {
+        vr[dt] = load16_stream(base + 16 * RB * dt);
+      }
+    }
+  };
+  const int vb2 = kSplitRun ? vb + 1 : vb;
+  auto v_at = [&](const Blocks<NB>& b, int ib, int which) {
+    return vbase0 + ib + (int64_t)max(pick(b, which), 0) * pool_stride;
   };
 
   int it = first_it;
@@ -280,7 +312,7 @@ __device__ __forceinline__ State fp8_wave(const Params& p, int seq, int kvh, int
     const int ib = in_block_bytes<BS, TPI, 1>(it);
     load_k(kw, kbase0 + ib + (int64_t)max(pick(cur, kb), 0) * pool_stride);
     __builtin_amdgcn_sched_barrier(0);
-    load_v(vr, vbase0 + ib + (int64_t)max(pick(cur, vb), 0) * pool_stride);
+    load_v(vr, v_at(cur, ib, vb), v_at(cur, ib, vb2));
   }
 
 #pragma unroll 1
@@ -323,14 +355,23 @@ __device__ __forceinline__ State fp8_wave(const Params& p, int seq, int kvh, int
 
     // ---- softmax: lane (m, kg) owns head m, iteration tokens 16 kg + 4 r + i ----
     const int ph_v = pick(cur, vb);
-    const int n_ok = ph_v < 0 ? 0 : min(max(t1 - (it + 16 * kg), 0), 16);
+    int n_ok;
+    uint32_t keep = 0xffffu;   // block size 8: the run's tokens that exist (bit t: token 16 kg + t)
+    if constexpr (kSplitRun) {
+      n_ok = min(max(t1 - (it + 16 * kg), 0), 16);
+      keep = (n_ok >= 16 ? 0xffffu : ((1u << n_ok) - 1u)) & (ph_v < 0 ? 0xff00u : 0xffffu) &
+             (pick(cur, vb2) < 0 ? 0x00ffu : 0xffffu);
+    } else {
+      n_ok = ph_v < 0 ? 0 : min(max(t1 - (it + 16 * kg), 0), 16);
+    }
+    auto tok_ok = [&](int t) { return kSplitRun ? ((keep >> t) & 1u) != 0 : t < n_ok; };
     float sc[4][4];
     float mx = -INFINITY;
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        sc[i][r] = (4 * r + i < n_ok) ? s[i][r] * qk_scale : -INFINITY;
+        sc[i][r] = tok_ok(4 * r + i) ? s[i][r] * qk_scale : -INFINITY;
         mx = fmaxf(mx, sc[i][r]);
       }
     st.update_max(mx);
@@ -339,7 +380,7 @@ __device__ __forceinline__ State fp8_wave(const Params& p, int seq, int kvh, int
     for (int i = 0; i < 4; ++i)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        pw[i][r] = (4 * r + i < n_ok) ? __builtin_amdgcn_exp2f(sc[i][r] - st.m_run) : 0.f;
+        pw[i][r] = tok_ok(4 * r + i) ? __builtin_amdgcn_exp2f(sc[i][r] - st.m_run) : 0.f;
         st.l_lane += pw[i][r];
       }
     // P^T operands: MFMA h takes tokens 8 h .. 8 h + 7 = (r = 2 h, 2 h + 1) x (i = 0 .. 3)
@@ -353,7 +394,12 @@ __device__ __forceinline__ State fp8_wave(const Params& p, int seq, int kvh, int
     }
 
     // ---- p.v: tokens past t1 and holes may hold any byte (NaN codes too) ----
-    if (__builtin_amdgcn_ballot_w64(n_ok < 16) != 0) {
+    if constexpr (kSplitRun) {
+      if (__builtin_amdgcn_ballot_w64(keep != 0xffffu) != 0) {
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) vr[dt] = keep_byte_mask(vr[dt], keep);
+      }
+    } else if (__builtin_amdgcn_ballot_w64(n_ok < 16) != 0) {
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt) vr[dt] = keep_bytes(vr[dt], n_ok);
     }
@@ -365,7 +411,7 @@ __device__ __forceinline__ State fp8_wave(const Params& p, int seq, int kvh, int
       st.o[dt] = mma<Kind::F16>(f8x2<false>(v.z), f8x2<true>(v.z), f8x2<false>(v.w), f8x2<true>(v.w), pb[1],
                                 st.o[dt]);
     }
-    load_v(vr, vbase0 + ib_next + (int64_t)max(pick(nxt, vb), 0) * pool_stride);
+    load_v(vr, v_at(nxt, ib_next, vb), v_at(nxt, ib_next, vb2));
     cur = nxt;
     nxt = nn;
   }

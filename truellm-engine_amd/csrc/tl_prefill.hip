@@ -32,11 +32,15 @@
 // softmax, weight packing, staging), group 1 one phase behind group 0, with
 // a workgroup barrier after every phase, so that on each SIMD one
 // wavefront's matrix ops run beside the other's VALU work.
-// Decode rows run the decode wavefronts (tl_mfma_wave.hpp for block_size 16,
-// tl_decode_wave.hpp otherwise), one workgroup per (sequence, kv head, head
-// slice), as a second kernel of the same call on the same stream (one
-// kernel for both would be sized by the decode path's registers on top of
-// the prefill path's).
+// Decode rows run the matrix-core decode wavefronts (tl_mfma_wave.hpp), one
+// workgroup per (sequence, kv head, 16-head slice), as a second kernel of the
+// same call on the same stream (one kernel for both would be sized by the
+// decode path's registers on top of the prefill path's).
+// Pools: f16 / bf16 (the q type), or FP8 E4M3 with per-tensor k_scale /
+// v_scale (codes converted exactly to the q type for q.k and to f16 for
+// p.v as they are staged; k_scale folds into the score scale, v_scale into
+// the output).  Block sizes: any power of two 8 .. 256; a wavefront's 16-key
+// group lies in one block from 16 on, in two at 8 (one per lane half).
 //
 // Nearest reference analogues: the per-token prefill of cuda_engine.cpp:842-860
 // and the dense attention of megakernel.cu:267-351; the reference has no
@@ -120,14 +124,14 @@ template <> struct Mfma32<Kind::F16> {
 };
 
 struct PrefillParams {
-  Params base;                 // q, out, pools, tables, seq_lens, heads, group, qk_scale
+  Params base;                 // q, out, pools, tables, seq_lens, heads, group, qk_scale, v_scale
   const int32_t* cu_q_lens;    // [num_seqs + 1]
   int num_seqs, row_tiles;
   int pf_seqs;                 // sequences [0, pf_seqs) may be prefill rows
   int dec_first;               // sequences [dec_first, num_seqs) may be decode rows
 };
 
-template <int NW, int BS>
+template <int NW>
 struct PrefillSmem {
   struct {
     uint16_t kt[kStages][kPfHead * kKtStride];    // [channel][key] (+16 pad)
@@ -172,14 +176,35 @@ __device__ __forceinline__ u32x4 k_operand(const uint16_t* kst, int t, int ks, i
   return u32x4{l2.x, l2.y, h2.x, h2.y};
 }
 
-template <Kind KV, int BS, int NW>
+// Eight E4M3 codes (c.x: keys 0-3, c.y: keys 4-7) as eight 16-bit values of
+// type T, exactly (every E4M3 value, subnormals and NaN included, is an f16
+// and a bf16 value).
+template <Kind T>
+__device__ __forceinline__ u32x4 fp8x8_to(const u32x4& c) {
+  auto cvt = [](uint32_t w, bool hi) -> uint32_t {
+    if constexpr (T == Kind::BF16)
+      return hi ? __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, true))
+                : __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, false));
+    else
+      return hi ? __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, true))
+                : __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, false));
+  };
+  return u32x4{cvt(c.x, false), cvt(c.x, true), cvt(c.y, false), cvt(c.y, true)};
+}
+
+// Q: the q / out type (f16 or bf16); KV: the pool's, Q or FP8.
+template <Kind Q, Kind KV, int BS, int NW>
 __global__ __launch_bounds__(NW * kWave) void prefill_kernel(PrefillParams pp) {
-  static_assert(BS == 16 || BS == 32, "block size");
+  static_assert(BS >= 8 && BS <= 256 && (BS & (BS - 1)) == 0, "block size: a power of two 8 .. 256");
   static_assert(NW == 8, "two groups of four wavefronts, one wavefront of each group per SIMD");
-  constexpr int BPI = kPfKeys / BS;                    // pool blocks per iteration
-  using M = Mfma32<KV>;                                // q.k
-  using MP = Mfma32<Kind::F16>;                        // p.v (f16 for both types)
-  __shared__ __attribute__((aligned(16))) PrefillSmem<NW, BS> sm;
+  static_assert(KV == Q || KV == Kind::FP8, "a 2-byte pool holds the q type");
+  constexpr int BPI = BS >= kPfKeys ? 1 : kPfKeys / BS;   // pool blocks per iteration
+  constexpr int BSE = BS >= kPfKeys ? kPfKeys : BS;       // keys of an iteration per block
+  constexpr int NKE = BS == 8 ? 2 : 1;                    // blocks of a wavefront's 16-key group
+  constexpr int E = KV == Kind::FP8 ? 1 : 2;              // pool bytes per element
+  using M = Mfma32<Q>;                                 // q.k
+  using MP = Mfma32<Kind::F16>;                        // p.v (f16 for every type)
+  __shared__ __attribute__((aligned(16))) PrefillSmem<NW> sm;
 
   const Params& p = pp.base;
   const int tid = threadIdx.x, lane = tid % kWave;
@@ -194,12 +219,19 @@ __global__ __launch_bounds__(NW * kWave) void prefill_kernel(PrefillParams pp) {
   const int tile = pp.row_tiles - 1 - b / items;       // longest (latest) tiles first
   b %= items;
   const int seq = b / p.num_kv_heads, kvh = b % p.num_kv_heads;
-  // The first two table entries of the wavefront's key group (see the
-  // staging below) are read with the lengths, before the exits that
-  // depend on them: one memory round trip for both.
+  // The table entries of the wavefront's key group (see the staging below)
+  // in the first two iterations are read with the lengths, before the exits
+  // that depend on them: one memory round trip for all.
   const TableRow table = (TableRow)(p.block_tables + (int64_t)seq * p.max_blocks_per_seq);
   const int kg = 16 * (wave >> 1);                     // first key of the wavefront's group
-  const int e0 = table_entry(p, table, kg / BS), e1 = table_entry(p, table, BPI + kg / BS);
+  // logical block of key kk of iteration it (>= 0)
+  auto blk_of = [](int it, int kk) { return (int)((unsigned)(it * kPfKeys + kk) / BS); };
+  int e0[NKE], e1[NKE];
+#pragma unroll
+  for (int h = 0; h < NKE; ++h) {
+    e0[h] = table_entry(p, table, blk_of(0, kg + 8 * h));
+    e1[h] = table_entry(p, table, blk_of(1, kg + 8 * h));
+  }
   const int q0 = pp.cu_q_lens[seq], ql = pp.cu_q_lens[seq + 1] - q0;
   const int L = p.seq_lens[seq];
   if (ql <= 0) return;
@@ -232,16 +264,18 @@ __global__ __launch_bounds__(NW * kWave) void prefill_kernel(PrefillParams pp) {
     for (int ks = 0; ks < 8; ++ks) qb[ks] = load16(qrow + 16 * ks);
   };
 
-  const int64_t head_stride = (int64_t)kPfHead * BS;                  // elements per (block, kv head)
-  const uint16_t* kpool = (const uint16_t*)p.k_cache;
-  const uint16_t* vpool = (const uint16_t*)p.v_cache;
+  const int64_t head_bytes = (int64_t)kPfHead * BS * E;                // bytes per (block, kv head)
+  const char* kpool = p.k_cache;
+  const char* vpool = p.v_cache;
 
   // Staging: wavefront w copies the 16 keys kg = 16 (w >> 1) .. kg + 15 of
-  // an iteration (they lie in one pool block) for the 64 channels 64 (w & 1)
-  // .. + 63, as two units of 32 channels.  Lane l holds channel (l & 31) of
-  // the unit and keys kg + 8 (l >> 5) .. + 7 (16 bytes), so one load of a
-  // unit reads 1 KB that is contiguous in the pool.  The block id of the
-  // key group is wave-uniform (descriptors in scalar registers).
+  // an iteration for the 64 channels 64 (w & 1) .. + 63, as two units of 32
+  // channels.  Lane l holds channel (l & 31) of the unit and keys
+  // kg + 8 (l >> 5) .. + 7 (16 bytes; 8 for FP8), so one load of a unit
+  // reads 1 KB (512 B) that is contiguous in the pool at block sizes 16 and
+  // 32.  From block size 16 on the key group lies in one block, whose id is
+  // wave-uniform (descriptors in scalar registers); at block size 8 each
+  // lane half has a block of its own.
   constexpr int kUnits = 2;                            // 32-channel units per wavefront
   static_assert(NW == 2 * (kPfKeys / 16) && kUnits * 32 * 2 == kPfHead, "key groups x channel halves");
   const int tok = kg + 8 * g;                          // first key of the lane's 8
@@ -251,33 +285,68 @@ __global__ __launch_bounds__(NW * kWave) void prefill_kernel(PrefillParams pp) {
   // run that exist (the rest is zeroed when staged, so that the loads are
   // waited for only there).
   struct Fetched { u32x4 k[kUnits], v[kUnits]; int nv; };
-  auto load_unit = [&](const uint16_t* pool, int pb, int ch) {
-    // unconditional loads (a missing block has an empty range and reads
-    // zeros): no branch, so nothing waits for them before the staging
-    const int64_t row = pb >= 0 ? ((int64_t)pb * p.num_kv_heads + kvh) * head_stride : 0;
-    const unsigned bytes = pb >= 0 ? unsigned(head_stride * 2) : 0u;
-    return buffer_load16(buffer_rsrc(pool + row, bytes), unsigned(2 * (ch * BS + tok % BS)));
+  // unconditional loads (a missing block has an empty range and reads
+  // zeros): no branch, so nothing waits for them before the staging
+  auto rsrc_of = [&](const char* pool, int pb) {
+    const int64_t row = pb >= 0 ? ((int64_t)pb * p.num_kv_heads + kvh) * head_bytes : 0;
+    return buffer_rsrc(pool + row, pb >= 0 ? unsigned(head_bytes) : 0u);
   };
-  // physical block of the wavefront's key group in iteration it from its
-  // table entry, or -1
-  auto group_block = [&](int it, int entry) {
-    const int key0 = it * kPfKeys + kg;
-    return __builtin_amdgcn_readfirstlane(key0 < kend && it >= 0 ? checked_block(p, it * BPI + kg / BS, entry) : -1);
+  auto load_raw = [&](__amdgpu_buffer_rsrc_t r, unsigned off) -> u32x4 {
+    if constexpr (E == 2) {
+      return buffer_load16(r, off);
+    } else {
+      const auto w = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 2);
+      return u32x4{(uint32_t)w[0], (uint32_t)w[1], 0u, 0u};
+    }
+  };
+  // the lane's keys tok .. tok + 7 of channel ch in iteration it: a run of
+  // a block row, at the iteration's offset in the block
+  auto load_unit = [&](const char* pool, const int (&pb)[NKE], int it, int ch) -> u32x4 {
+    // (a block of at most 64 keys holds whole key groups at the same offset
+    // in every iteration)
+    const int in_blk = BS > kPfKeys ? (int)((unsigned)(it * kPfKeys) % BS) + tok : tok % BS;
+    const unsigned off = unsigned(E * (ch * BS + in_blk));
+    if constexpr (NKE == 1) {
+      return load_raw(rsrc_of(pool, pb[0]), off);
+    } else {
+      // each load serves one lane half; the other half's offset lies past
+      // the range (no memory request, zeros)
+      constexpr unsigned kPast = 0x40000000u;
+      const u32x4 a = load_raw(rsrc_of(pool, pb[0]), g == 0 ? off : kPast);
+      const u32x4 b = load_raw(rsrc_of(pool, pb[1]), g == 1 ? off : kPast);
+      return u32x4{a.x | b.x, a.y | b.y, a.z | b.z, a.w | b.w};
+    }
+  };
+  // physical block of half h of the wavefront's key group in iteration it
+  // from its table entry, or -1
+  auto group_block = [&](int it, int entry, int h) {
+    const int key0 = it * kPfKeys + kg + 8 * h;
+    return __builtin_amdgcn_readfirstlane(key0 < kend && it >= 0 ? checked_block(p, blk_of(it, kg + 8 * h), entry)
+                                                                 : -1);
   };
   // the blocks of one copy; load(i) issues its i-th load (K unit i, then V
   // unit i - kUnits), so that a phase can spread them over its matrix ops
-  struct FetchPlan { int pk, pv; };
-  auto plan = [&](int it_k, int it_v, int ek, int ev, Fetched& f) {
-    const FetchPlan fp = {group_block(it_k, ek), group_block(it_v, ev)};
-    f.nv = fp.pv >= 0 ? min(max(L - (it_v * kPfKeys + tok), 0), 8) : 0;
+  struct Entries { int k[NKE], v[NKE]; };
+  struct FetchPlan { int pk[NKE], pv[NKE], it_k, it_v; };
+  auto plan = [&](int it_k, int it_v, const Entries& e, Fetched& f) {
+    FetchPlan fp;
+    fp.it_k = it_k;
+    fp.it_v = it_v;
+#pragma unroll
+    for (int h = 0; h < NKE; ++h) {
+      fp.pk[h] = group_block(it_k, e.k[h], h);
+      fp.pv[h] = group_block(it_v, e.v[h], h);
+    }
+    const int pv_lane = NKE == 2 ? (g ? fp.pv[NKE - 1] : fp.pv[0]) : fp.pv[0];
+    f.nv = pv_lane >= 0 ? min(max(L - (it_v * kPfKeys + tok), 0), 8) : 0;
     return fp;
   };
   auto load = [&](const FetchPlan& fp, int i, Fetched& f) {
-    if (i < kUnits) f.k[i] = load_unit(kpool, fp.pk, unit_ch(i));
-    else f.v[i - kUnits] = load_unit(vpool, fp.pv, unit_ch(i - kUnits));
+    if (i < kUnits) f.k[i] = load_unit(kpool, fp.pk, fp.it_k, unit_ch(i));
+    else f.v[i - kUnits] = load_unit(vpool, fp.pv, fp.it_v, unit_ch(i - kUnits));
   };
-  auto fetch = [&](int it_k, int it_v, int ek, int ev, Fetched& f) {
-    const FetchPlan fp = plan(it_k, it_v, ek, ev, f);
+  auto fetch = [&](int it_k, int it_v, const Entries& e, Fetched& f) {
+    const FetchPlan fp = plan(it_k, it_v, e, f);
 #pragma unroll
     for (int i = 0; i < 2 * kUnits; ++i) load(fp, i, f);
   };
@@ -286,10 +355,11 @@ __global__ __launch_bounds__(NW * kWave) void prefill_kernel(PrefillParams pp) {
     for (int u = 0; u < kUnits; ++u) {
       // K as it lies in the pool: the lane's 8 keys of its channel, one
       // 16-byte write (k_operand reads it transposed)
-      *reinterpret_cast<u32x4*>(&sm.pf.kt[it_k & 1][unit_ch(u) * kKtStride + tok]) = f.k[u];
+      const u32x4 kq = KV == Kind::FP8 ? fp8x8_to<Q>(f.k[u]) : f.k[u];
+      *reinterpret_cast<u32x4*>(&sm.pf.kt[it_k & 1][unit_ch(u) * kKtStride + tok]) = kq;
       // V slots at or past the sequence end may hold anything (NaN codes
       // too, and a zero weight times NaN is NaN): zero them
-      u4v v = __builtin_bit_cast(u4v, f.v[u]);
+      u4v v = __builtin_bit_cast(u4v, KV == Kind::FP8 ? fp8x8_to<Kind::F16>(f.v[u]) : f.v[u]);
       const int nv = f.nv;
       // a wave-uniform branch (the sequence's last iteration only): as a
       // lane-divergent one it became selects run on every iteration
@@ -312,17 +382,26 @@ __global__ __launch_bounds__(NW * kWave) void prefill_kernel(PrefillParams pp) {
     }
   };
   // Table entries are read two phases before their use by one vector load:
-  // lane 0 the K block of the fetch, lane 1 its V block, lane 2 + i block i
-  // of the mask.  A scalar table read would be waited for behind every LDS
-  // access in flight (one counter covers both).
+  // lanes [0, NKE) the K blocks of the fetch, [NKE, 2 NKE) its V blocks,
+  // lane 2 NKE + i block i of the mask.  A scalar table read would be
+  // waited for behind every LDS access in flight (one counter covers both).
   const int32_t* table_v = p.block_tables + (int64_t)seq * p.max_blocks_per_seq;
-  const int t_lb = lane < 2 ? kg / BS : min(max(lane - 2, 0), BPI - 1);
-  const int t_it = lane == 0 ? 1 + grp : (lane == 1 ? grp : 0);   // iteration offset of the lane's entry
+  const int t_key = lane < 2 * NKE ? kg + 8 * (lane % NKE) : min(lane - 2 * NKE, BPI - 1) * BSE;
+  const int t_it = lane < NKE ? 1 + grp : (lane < 2 * NKE ? grp : 0);   // iteration offset of the lane's entry
   // entries of step jn: the fetch of MFMA phase X_jn (K of jn + 1 + grp, V
   // of jn + grp, staged by Y_jn) and the mask of Y_jn
   auto table_prefetch = [&](int jn) {
-    const int lb = max(jn + t_it, 0) * BPI + t_lb;
+    const int lb = blk_of(max(jn + t_it, 0), t_key);
     return table_v[min(lb, p.max_blocks_per_seq - 1)];
+  };
+  auto entries = [&](int t) {
+    Entries e;
+#pragma unroll
+    for (int h = 0; h < NKE; ++h) {
+      e.k[h] = __builtin_amdgcn_readlane(t, h);
+      e.v[h] = __builtin_amdgcn_readlane(t, NKE + h);
+    }
+    return e;
   };
 
   f16v o[4];
@@ -368,7 +447,7 @@ __global__ __launch_bounds__(NW * kWave) void prefill_kernel(PrefillParams pp) {
     bool all_ok = true;
 #pragma unroll
     for (int bi = 0; bi < BPI; ++bi) {
-      blk_ok[bi] = checked_block(p, it * BPI + bi, __builtin_amdgcn_readlane(t_entries, 2 + bi)) >= 0;
+      blk_ok[bi] = checked_block(p, blk_of(it, bi * BSE), __builtin_amdgcn_readlane(t_entries, 2 * NKE + bi)) >= 0;
       all_ok = all_ok && blk_ok[bi];
     }
     return all_ok;
@@ -397,7 +476,7 @@ __global__ __launch_bounds__(NW * kWave) void prefill_kernel(PrefillParams pp) {
           // comparison is written with the wave-uniform part on the left
           // so that no per-lane value of each r is kept across the loop
           const int kc = 32 * t + 8 * (r >> 2) + (r & 3);
-          const bool ok = k0 + kc <= pos_g && blk_ok[(kc + 4 * g) / BS];
+          const bool ok = k0 + kc <= pos_g && blk_ok[(kc + 4 * g) / BSE];
           sp[t][r] = ok ? sp[t][r] : -INFINITY;
           mx = fmaxf(mx, sp[t][r]);
         }
@@ -476,9 +555,15 @@ __global__ __launch_bounds__(NW * kWave) void prefill_kernel(PrefillParams pp) {
     // copy again in X_0, unconditional so that the wait counts agree on
     // every path)
     Fetched f0;
-    fetch(0, -1, e0, e0, f0);
+    Entries ea, eb;
+#pragma unroll
+    for (int h = 0; h < NKE; ++h) {
+      ea.k[h] = e0[h]; ea.v[h] = e0[h];
+      eb.k[h] = e1[h]; eb.v[h] = e0[h];
+    }
+    fetch(0, -1, ea, f0);
     load_q();
-    fetch(1, 0, e1, e0, fs);
+    fetch(1, 0, eb, fs);
     t_ent = table_prefetch(0);
     stage(0, -1, f0);                   // K(0); V stage 1 gets zeros (iteration -1 is missing)
   }
@@ -489,7 +574,7 @@ __global__ __launch_bounds__(NW * kWave) void prefill_kernel(PrefillParams pp) {
   // used: unconditional, so that no path carries scores or weights across a
   // phase)
   auto fetch_for = [&](int jn) {        // the loads staged by Y_jn
-    fetch(jn + 1 + grp, jn + grp, __builtin_amdgcn_readlane(t_ent, 0), __builtin_amdgcn_readlane(t_ent, 1), fs);
+    fetch(jn + 1 + grp, jn + grp, entries(t_ent), fs);
   };
   auto phase_x0 = [&]() {
     fetch_for(0);
@@ -560,8 +645,7 @@ __global__ __launch_bounds__(NW * kWave) void prefill_kernel(PrefillParams pp) {
   // makes the next phase wait for every load.  The table read of step
   // jn + 1 goes out here too, two phases before its first use.
   auto phase_x = [&](int j) {
-    const FetchPlan fp = plan(j + 2 + grp, j + 1 + grp, __builtin_amdgcn_readlane(t_ent, 0),
-                              __builtin_amdgcn_readlane(t_ent, 1), fs);   // the copy staged by Y_{j+1}
+    const FetchPlan fp = plan(j + 2 + grp, j + 1 + grp, entries(t_ent), fs);   // the copy staged by Y_{j+1}
     t_mask = t_ent;                      // waited for by the readlanes: a plain copy
     t_ent = table_prefetch(j + 2);
     __builtin_amdgcn_s_setprio(1);
@@ -640,6 +724,7 @@ __global__ __launch_bounds__(NW * kWave) void prefill_kernel(PrefillParams pp) {
     for (int i = 0; i < 4; ++i) {
       const float l = s_row[8 * j + 4 * g + i];
       inv[i] = l > 0.f ? PvScale<KV>::kP * __builtin_amdgcn_rcpf(l) : 0.f;   // the sums carry 2^kPExp
+      if constexpr (KV == Kind::FP8) inv[i] *= p.v_scale;
     }
 #pragma unroll
     for (int ip = 0; ip < 4; ip += 2) {
@@ -664,17 +749,13 @@ __global__ __launch_bounds__(NW * kWave) void prefill_kernel(PrefillParams pp) {
   }
 }
 
-// q heads per decode-row workgroup: the matrix-core wavefronts serve 16
-// (block_size 16), the dot-product wavefronts 4.
-template <int BS> constexpr int decode_row_heads() { return BS == 16 ? mw::kHeads : kWaveHeads; }
-
 // Decode rows (q_len == 1) of a mixed batch, one workgroup per (sequence,
-// kv head, head slice), q / out row cu_q_lens[s]: the matrix-core decode
-// wavefronts (tl_mfma_wave.hpp) for block_size 16, so a GQA group of up to
-// 16 heads reads its KV once, the 2-byte dot-product wavefronts otherwise.
-template <Kind KV, int BS, int NW>
+// kv head, 16-head slice), q / out row cu_q_lens[s]: the matrix-core decode
+// wavefronts (tl_mfma_wave.hpp), so a GQA group of up to 16 heads reads its
+// KV once, at every block size and for FP8 pools too.
+template <Kind Q, Kind KV, int BS, int NW>
 __global__ __launch_bounds__(NW * kWave) void prefill_decode_kernel(PrefillParams pp) {
-  constexpr int GT = decode_row_heads<BS>();
+  constexpr int GT = mw::kHeads;
   __shared__ __attribute__((aligned(16))) float s_acc[NW * GT * kPfHead];
   __shared__ float s_m[NW * GT], s_l[NW * GT];
   const Params& p = pp.base;
@@ -690,31 +771,35 @@ __global__ __launch_bounds__(NW * kWave) void prefill_decode_kernel(PrefillParam
   pd.q = (const char*)p.q + shift;
   pd.out = (char*)p.out + shift;
   pd.head_slices = slices;
-  if constexpr (BS == 16) {
-    mw::decode_workgroup<KV, KV, Kind::F32, NW, true>(pd, seq, kvh, hs, 0, 0, L, s_acc, s_m, s_l);
-  } else {
-    __shared__ __attribute__((aligned(16))) uint32_t s_p[NW][4][kWaveHeads][4];
-    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid / kWave);
-    decode2_wave<KV, kPfHead, BS>(pd, seq, kvh, hs, wave * 32, L, NW * 32, &s_p[wave][0][0][0],
-                                  &s_acc[wave * GT * kPfHead], &s_m[wave * GT], &s_l[wave * GT]);
-    __syncthreads();
-    combine_waves<KV, Kind::F32, kPfHead, true>(pd, NW, s_m, s_l, s_acc, seq, kvh, hs, 0, tid, NW * kWave);
-  }
+  mw::decode_workgroup<KV, Q, Kind::F32, NW, true, BS>(pd, seq, kvh, hs, 0, 0, L, s_acc, s_m, s_l);
 }
 
-template <Kind KV, int BS>
+template <Kind Q, Kind KV, int BS>
 int launch_prefill_t(const PrefillParams& pp, unsigned grid, hipStream_t stream) {
   // decode rows: 4 wavefronts per workgroup (8: 926.2 against 916.8 us per
   // 4-chunk step at 32 rows of ctx 2048, 64/8 heads; 12 and 16 slower still)
   constexpr int NW = 8, NWD = 4;
   const Params& p = pp.base;
-  constexpr int GT = decode_row_heads<BS>();
+  constexpr int GT = mw::kHeads;
   const unsigned dgrid = (unsigned)((pp.num_seqs - pp.dec_first) * p.num_kv_heads * ((p.group + GT - 1) / GT));
   if (dgrid > 0)
-    hipLaunchKernelGGL((prefill_decode_kernel<KV, BS, NWD>), dim3(dgrid), dim3(NWD * kWave), 0, stream, pp);
+    hipLaunchKernelGGL((prefill_decode_kernel<Q, KV, BS, NWD>), dim3(dgrid), dim3(NWD * kWave), 0, stream, pp);
   if (grid > 0)
-    hipLaunchKernelGGL((prefill_kernel<KV, BS, NW>), dim3(grid), dim3(NW * kWave), 0, stream, pp);
+    hipLaunchKernelGGL((prefill_kernel<Q, KV, BS, NW>), dim3(grid), dim3(NW * kWave), 0, stream, pp);
   return hipGetLastError() == hipSuccess ? 0 : 5;
+}
+
+template <Kind Q, Kind KV>
+int launch_prefill_bs(const PrefillParams& pp, int bs, unsigned grid, hipStream_t stream) {
+  switch (bs) {
+    case 8: return launch_prefill_t<Q, KV, 8>(pp, grid, stream);
+    case 16: return launch_prefill_t<Q, KV, 16>(pp, grid, stream);
+    case 32: return launch_prefill_t<Q, KV, 32>(pp, grid, stream);
+    case 64: return launch_prefill_t<Q, KV, 64>(pp, grid, stream);
+    case 128: return launch_prefill_t<Q, KV, 128>(pp, grid, stream);
+    case 256: return launch_prefill_t<Q, KV, 256>(pp, grid, stream);
+    default: return 3;
+  }
 }
 
 }  // namespace
@@ -733,8 +818,12 @@ int launch_prefill(const PrefillLaunch& a) {
   p.group = a.num_heads / a.num_kv_heads;
   p.head_slices = (p.group + kWaveHeads - 1) / kWaveHeads;
   p.gqa_map = a.gqa_map;
-  p.qk_scale = a.scale * kLog2e;
-  p.v_scale = 1.f;
+  const bool fp8 = a.kv_dtype == (int)Kind::FP8;
+  // FP8: the codes enter both products unscaled; k_scale scales the scores,
+  // v_scale the output
+  p.qk_scale = a.scale * (fp8 ? a.k_scale : 1.f) * kLog2e;
+  p.v_scale = fp8 ? a.v_scale : 1.f;
+  p.block_size = a.block_size;
   pp.cu_q_lens = a.cu_q_lens;
   pp.num_seqs = a.num_seqs;
   // with the prefill sequences first (num_prefill_seqs > 0) each kernel's grid
@@ -745,9 +834,11 @@ int launch_prefill(const PrefillLaunch& a) {
   pp.row_tiles = a.max_q_len > 1 ? (a.max_q_len * p.group + NW * kPfRows - 1) / (NW * kPfRows) : 0;
   const unsigned grid = (unsigned)(pp.row_tiles * pp.pf_seqs * a.num_kv_heads);
   const bool bf16 = a.dtype == (int)Kind::BF16;
-  if (a.block_size == 16)
-    return bf16 ? launch_prefill_t<Kind::BF16, 16>(pp, grid, a.stream) : launch_prefill_t<Kind::F16, 16>(pp, grid, a.stream);
-  return bf16 ? launch_prefill_t<Kind::BF16, 32>(pp, grid, a.stream) : launch_prefill_t<Kind::F16, 32>(pp, grid, a.stream);
+  if (fp8)
+    return bf16 ? launch_prefill_bs<Kind::BF16, Kind::FP8>(pp, a.block_size, grid, a.stream)
+                : launch_prefill_bs<Kind::F16, Kind::FP8>(pp, a.block_size, grid, a.stream);
+  return bf16 ? launch_prefill_bs<Kind::BF16, Kind::BF16>(pp, a.block_size, grid, a.stream)
+              : launch_prefill_bs<Kind::F16, Kind::F16>(pp, a.block_size, grid, a.stream);
 }
 
 }  // namespace tl

@@ -101,6 +101,9 @@ class PrefillDesc(ctypes.Structure):
         ("gqa_map", ctypes.c_int32),
         ("num_prefill_seqs", ctypes.c_int32),
         ("scale", ctypes.c_float),
+        ("kv_dtype", ctypes.c_int32),
+        ("k_scale", ctypes.c_float),
+        ("v_scale", ctypes.c_float),
     ]
 
 _P = ctypes.c_void_p
@@ -169,7 +172,7 @@ def _hip_runtimes() -> set:
         return set()
 
 
-ABI_VERSION = 2           # TL_ABI_VERSION of include/tl_attn.h
+ABI_VERSION = 3           # TL_ABI_VERSION of include/tl_attn.h
 
 
 def _load() -> ctypes.CDLL:
@@ -591,10 +594,11 @@ def kivi_paged_attention_decode(desc, out, q, pages, page_tables, k_cache, v_cac
 # ---------------------------------------------------------------------------
 
 def make_prefill_desc(q, k_cache, block_tables, num_seqs, num_kv_heads, scale, *,
-                      gqa_map=GQA_GROUPED, num_prefill_seqs=0):
+                      gqa_map=GQA_GROUPED, num_prefill_seqs=0, kv_dtype=None, k_scale=1.0, v_scale=1.0):
     """q [total_q, H, 128]; k_cache [N, n_kv, 128, bs]; block_tables [S, max_blocks].
     num_prefill_seqs > 0 declares sequences 0..n-1 the prefill ones (q_len > 1
-    only there), which keeps the decode rows out of the prefill grid."""
+    only there), which keeps the decode rows out of the prefill grid.
+    kv_dtype FP8_E4M3: a pool of E4M3 codes (uint8) with per-tensor scales."""
     d = PrefillDesc()
     d.num_seqs, d.num_heads, d.num_kv_heads, d.head_size = num_seqs, q.shape[1], num_kv_heads, q.shape[2]
     d.block_size = k_cache.shape[3]
@@ -603,6 +607,8 @@ def make_prefill_desc(q, k_cache, block_tables, num_seqs, num_kv_heads, scale, *
     d.gqa_map = gqa_map
     d.num_prefill_seqs = num_prefill_seqs
     d.scale = scale
+    d.kv_dtype = d.dtype if kv_dtype is None else kv_dtype
+    d.k_scale, d.v_scale = k_scale, v_scale
     return d
 
 
