@@ -108,7 +108,7 @@ WARM_MS = 30.0
 POOL_ARENA = {}
 
 
-def pool_buffer(name, shape, dtype, g):
+def pool_buffer(name, shape, dtype, g, index=0):
     """A KV pool of the given shape and dtype, N(0, 1) from generator g, in a
     device buffer allocated once for the whole run and shared by every
     workload (pools 'k0', 'v0', 'k1', 'v1'): the workloads then stream the
@@ -119,11 +119,12 @@ def pool_buffer(name, shape, dtype, g):
     needs."""
     import torch
     nbytes = math.prod(shape) * torch.empty((), dtype=dtype).element_size()
+    off = index * ((nbytes + 4095) // 4096 * 4096)      # pool `index` of this arena
     buf = POOL_ARENA.get(name)
-    if buf is None or buf.numel() < nbytes:
-        buf = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    if buf is None or buf.numel() < off + nbytes:
+        buf = torch.empty(off + nbytes, dtype=torch.uint8, device="cuda")
         POOL_ARENA[name] = buf
-    t = buf[:nbytes].view(dtype).view(shape)
+    t = buf[off:off + nbytes].view(dtype).view(shape)
     if dtype in (torch.float16, torch.bfloat16, torch.float32):
         t.normal_(0.0, 1.0, generator=g)
     return t
@@ -192,7 +193,7 @@ def timed(step, steps, warmup, name=None):
     return statistics.median(per)
 
 
-def bench_decode(args, dtype, append=False, lens=None, partition_tokens=None, v2=False, name=None):
+def bench_decode(args, dtype, append=False, lens=None, partition_tokens=None, v2=False, name=None, layers=2):
     """Decode of one layer over the given lengths (default: batch 64, every
     context 4096) with the library plan (or partition_tokens), through
     tl_paged_attention_decode or, with v2, the reference-named
@@ -200,7 +201,8 @@ def bench_decode(args, dtype, append=False, lens=None, partition_tokens=None, v2
     step first writes each sequence's newest token (position L - 1) into the
     pool with reshape_and_cache, as an engine's decode step does before
     attention: the fp16 counterpart of the KIVI step, whose append is fused
-    into its launch."""
+    into its launch.  Step i reads pool i % layers (layers pools of their
+    own, as the layers of a model keep theirs)."""
     import torch
 
     import tl_attn as tla
@@ -215,9 +217,9 @@ def bench_decode(args, dtype, append=False, lens=None, partition_tokens=None, v2
     N = math.ceil(1.25 * sum(nbs))
     g = torch.Generator(device="cuda").manual_seed(0x7E5E0002)
     pools = []
-    for _ in range(2):
-        k = pool_buffer(f"k{len(pools)}", (N, NKV, D, BS), tdt, g)
-        v = pool_buffer(f"v{len(pools)}", (N, NKV, D, BS), tdt, g)
+    for li in range(layers):
+        k = pool_buffer(f"k{li % 2}", (N, NKV, D, BS), tdt, g, li // 2)
+        v = pool_buffer(f"v{li % 2}", (N, NKV, D, BS), tdt, g, li // 2)
         perm = torch.randperm(N, generator=g, device="cuda").to(torch.int32).cpu()
         tables = torch.full((B, mb), -1, dtype=torch.int32)
         off = 0
@@ -234,6 +236,7 @@ def bench_decode(args, dtype, append=False, lens=None, partition_tokens=None, v2
     ws = torch.empty(max(16, tla.workspace_bytes(desc, max_ctx)), dtype=torch.uint8, device="cuda")
     if v2:
         P = tla.v2_num_partitions(max_ctx, BS)
+        v2_parts, v2_pt = tla.v2_plan(B, H, NKV, D, BS, tla.dtype_code(q), max_ctx)
         es = torch.empty(B, H, P, dtype=torch.float32, device="cuda")
         ml = torch.empty_like(es)
         tmp = torch.empty(B, H, P, D, dtype=tdt, device="cuda")
@@ -246,22 +249,25 @@ def bench_decode(args, dtype, append=False, lens=None, partition_tokens=None, v2
         slots = [(tables[rows, pos // BS] * BS + pos % BS).to(torch.int32).contiguous() for _k, _v, tables in pools]
 
     def step(i, stream):
-        k, v, tables = pools[i % 2]
+        k, v, tables = pools[i % layers]
         if append:
-            tla.reshape_and_cache_split(knew, vnew, k, v, slots[i % 2], stream)
+            tla.reshape_and_cache_split(knew, vnew, k, v, slots[i % layers], stream)
         if v2:
             tla.paged_attention_v2(out, es, ml, tmp, q, k, v, tables, sl, NKV, scale, D, BS, max_ctx, stream,
                                    gqa_map=tla.GQA_GROUPED)
         else:
             tla.paged_attention_decode(desc, out, q, k, v, tables, sl, max_ctx, ws, stream)
 
-    ms = timed(step, args.steps, args.warmup, name)
+    ms = timed(step, max(args.steps, layers), args.warmup, name)
     nbytes = algorithmic_bytes(lens, 2)
+    parts = max(1, tla.workspace_bytes(desc, max_ctx) // (B * H * (D + 2) * 4))
     return {
         "ms_per_step": ms, "gbs": nbytes / (ms * 1e-3) / 1e9, "tok_s": B / (ms * 1e-3),
         "bytes": nbytes, "launch_ms": ms, "pool_blocks": N,            # one decode launch per step
         "workspace_bytes": tla.workspace_bytes(desc, max_ctx),
-        "partitions": max(1, tla.workspace_bytes(desc, max_ctx) // (B * H * (D + 2) * 4)),
+        "partitions": v2_parts if v2 else parts,
+        "partition_tokens": v2_pt if v2 else (-(-max_ctx // parts) if parts == 1 else None),
+        "pool_bytes_all_layers": 2 * N * NKV * D * BS * 2 * layers,
     }
 
 
@@ -846,8 +852,10 @@ def main():
         for label, pt in (("auto", 0), ("single_pass", -1), ("split_k_512", 512)):
             c2b[label] = bench_decode(args, "bf16", lens=lens2b, partition_tokens=pt, name=f"config2b_{label}")
     v2a = bench_decode(args, "bf16", v2=True, name="v2") if want("v2") else None
-    v2one = bench_decode(args, "f16", lens=[CTX], v2=True, name="v2_one_seq") if want("v2") else None
-    one = bench_decode(args, "f16", lens=[CTX], name="auto_one_seq") if want("v2") else None
+    # the engine's call shape: one sequence per call, 32 layers each with a
+    # pool of its own (672 MB in all, beyond the 256 MiB Infinity Cache)
+    v2one = bench_decode(args, "f16", lens=[CTX], v2=True, name="v2_one_seq", layers=32) if want("v2") else None
+    one = bench_decode(args, "f16", lens=[CTX], name="auto_one_seq", layers=32) if want("v2") else None
     pf = bench_prefill(args) if args.only in ("all", "prefill") else None
     cb = bench_copy_blocks(args) if args.only in ("all", "blocks") else None
     rp = bench_rope(args) if args.only in ("all", "rope") else None
@@ -908,11 +916,14 @@ def main():
     if v2one is not None:
         res["paged_attention_v2_one_sequence"] = {
             "workload": "the engine's own call: one sequence, ctx 4096, 32/8 heads, d 128, f16, "
-                        "tl_paged_attention_v2 on the engine's scratch against tl_paged_attention_decode's plan",
+                        "tl_paged_attention_v2 on the engine's scratch against tl_paged_attention_decode's plan; "
+                        "32 layers with pools of their own (step i reads layer i % 32), "
+                        f"{v2one['pool_bytes_all_layers'] / 1e6:.0f} MB in all, beyond the 256 MiB Infinity Cache",
             "v2_us": round(v2one["ms_per_step"] * 1e3, 2), "v2_partitions": v2one["partitions"],
-            "v2_gbs": round(v2one["gbs"], 2),
+            "v2_partition_tokens": v2one["partition_tokens"], "v2_gbs": round(v2one["gbs"], 2),
             "library_plan_us": round(one["ms_per_step"] * 1e3, 2) if one else None,
-            "library_plan_partitions": one["partitions"] if one else None}
+            "library_plan_partitions": one["partitions"] if one else None,
+            "library_plan_gbs": round(one["gbs"], 2) if one else None}
     if kv is not None:
         res["kivi_int4"] = {"gbs": round(kv["gbs"], 2), "ms_per_step": round(kv["ms_per_step"], 5),
                             "tok_s": round(kv["tok_s"], 1),

@@ -153,10 +153,11 @@ int tl_paged_attention_v1(void* out, const void* q, const void* k_cache, const v
  * block_size)) (cuda_engine.cpp:276-285,1144) is never less.  The caller
  * reads none of it afterwards.  The call runs the library's own plan (as
  * tl_paged_attention_decode with partition_tokens 0): single pass when the
- * batch fills the GPU, else split-K with fp32 partials kept in that scratch
- * (at most P * sizeof(dtype) / 4 partitions, P the reference kernel's
- * count).  The scratch's contents after the call are not the reference's
- * partials. */
+ * batch fills the GPU, else split-K with the partials kept in that scratch:
+ * f16 partial outputs for f16 calls at head size 128 (at most P
+ * partitions, P the reference kernel's count), else fp32 (at most
+ * P * sizeof(dtype) / 4).  The scratch's contents after the call are not
+ * the reference's partials. */
 int tl_paged_attention_v2(void* out, float* exp_sums, float* max_logits, void* tmp_out,
                           const void* q, const void* k_cache, const void* v_cache,
                           const int32_t* block_tables, const int32_t* seq_lens,
@@ -164,6 +165,16 @@ int tl_paged_attention_v2(void* out, float* exp_sums, float* max_logits, void* t
                           int32_t head_size, int32_t block_size, int32_t max_blocks_per_seq,
                           int32_t num_blocks, float scale, int32_t dtype, int32_t gqa_map,
                           int32_t max_context_len, void* stream);
+
+/* The plan tl_paged_attention_v2 runs for a call of these sizes (16-byte
+ * aligned tmp_out): the number of partitions (1: single pass; -1: the
+ * sizes are refused) and, in *partition_tokens, their length (0 for single
+ * pass).  No counterpart in the reference (whose v2 always runs
+ * (max_context_len / block_size + 31) / 32 partitions of 32 blocks,
+ * paged_attention_v2.cu:196); for callers that report or size around it. */
+int32_t tl_paged_attention_v2_partitions(int32_t num_seqs, int32_t num_heads, int32_t num_kv_heads,
+                                         int32_t head_size, int32_t block_size, int32_t dtype,
+                                         int32_t max_context_len, int32_t* partition_tokens);
 
 /* ------------------------------------------------------------------------
  * KV-cache writes

@@ -100,6 +100,54 @@ def test_auto_partitioning_targets_many_workgroups():
     assert tla.workspace_bytes(_desc(num_seqs=4), 4096) == 4 * 32 * 8 * (128 * 4 + 8)
     # 16 x 8 items at 32768 tokens -> 4 partitions of 8192
     assert tla.workspace_bytes(_desc(num_seqs=16), 32768) == 16 * 32 * 4 * (128 * 4 + 8)
+    # fewer items than CUs even at 512 tokens (the engine's one-sequence
+    # call): partitions down to one iteration per wavefront of a 4-wavefront
+    # workgroup, so that about 256 workgroups share the context
+    assert tla.workspace_bytes(_desc(num_seqs=1), 4096) == 1 * 32 * 32 * (128 * 4 + 8)    # 32 x 128
+    assert tla.workspace_bytes(_desc(num_seqs=2), 4096) == 2 * 32 * 16 * (128 * 4 + 8)    # 16 x 256
+    assert tla.workspace_bytes(_desc(num_seqs=1, kv_dtype=tla.FP8_E4M3), 4096) == 32 * 16 * (128 * 4 + 8)
+    assert tla.workspace_bytes(_desc(num_seqs=1), 1024) == 32 * 8 * (128 * 4 + 8)         # 8 x 128
+    # 49 partitions of 2048 tokens already give 392 workgroups
+    assert tla.workspace_bytes(_desc(num_seqs=1), 100000) == 32 * 49 * (128 * 4 + 8)
+    assert tla.workspace_bytes(_desc(num_seqs=1), 512) == 0                              # single pass
+    # the dot-product decode (head 80) keeps kDecodeChunk partitions
+    assert tla.workspace_bytes(_desc(num_seqs=1, head_size=80), 4096) == 32 * 8 * (80 * 4 + 8)
+
+
+def test_v2_plan_inside_the_callers_scratch():
+    """tl_paged_attention_v2's plan: f16 at head 128 keeps f16 partials, one
+    partition per reference-kernel slot ((max_ctx / bs + 31) / 32); bf16 and
+    f32 keep fp32 partials (half as many for bf16); a batch that fills the
+    GPU runs single pass."""
+    plan = lambda S, dt, L, bs=16, hs=128: tla.v2_plan(S, 32, 8, hs, bs, dt, L)
+    assert plan(1, tla.F16, 4096) == (8, 512)           # the engine's call: 8 slots, the plan wants 32
+    assert plan(1, tla.BF16, 4096) == (4, 1024)         # fp32 partials: 4 of the 8 slots' bytes
+    assert plan(1, tla.F32, 4096) == (8, 512)
+    assert plan(1, tla.F16, 1541) == (3, 640)           # kernel count 3 (the engine's is 4)
+    assert plan(1, tla.F16, 600) == (2, 384)
+    assert plan(64, tla.F16, 4096) == (1, 0)            # single pass
+    assert plan(4, tla.F16, 4096) == (8, 512)           # the library plan fits
+    assert plan(1, tla.F16, 4096, hs=80)[0] == 4        # dot-product decode: fp32 partials
+    with pytest.raises(tla.TLError):
+        plan(1, tla.F16, 4096, bs=12)
+
+
+@pytest.mark.parametrize("kw,ok", [
+    (dict(partition_tokens=96), True), (dict(partition_tokens=32), True),
+    (dict(partition_tokens=96, kv_dtype=tla.FP8_E4M3), False), (dict(partition_tokens=192, kv_dtype=tla.FP8_E4M3), True),
+    (dict(partition_tokens=1024, head_size=80), True), (dict(partition_tokens=256, head_size=80), False),
+])
+def test_partition_tokens_granularity(kw, ok):
+    """Explicit partitions: a multiple of the matrix-core wavefront's
+    iteration (32 tokens of 2-byte KV, 64 of FP8) at head 128, of 512 for
+    the other kernels."""
+    d = _desc(**kw)
+    got = tla.workspace_bytes(d, 4096)
+    if ok:
+        P = -(-4096 // d.partition_tokens)
+        assert got == 4 * 32 * P * (d.head_size * 4 + 8)
+    else:
+        assert got == 0 and _decode(d, max_ctx=4096) == tla.ERR_INVALID_ARGUMENT
 
 
 def test_empty_batch_is_a_no_op():

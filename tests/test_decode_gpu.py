@@ -331,3 +331,47 @@ def test_decode_graph_replay_matches_eager(pt):
         tla.paged_attention_decode(desc, out, q, k, v, bt, sl, max_ctx, ws)
         torch.cuda.synchronize()
         assert torch.equal(out, eager)
+
+
+@pytest.mark.parametrize("lens,code,kv", [
+    ([4096], orc.F16, None), ([4097], orc.BF16, None), ([3000, 1200], orc.F16, None), ([1024], orc.F16, None),
+    ([700, 33], orc.BF16, None), ([8000], orc.BF16, "fp8"), ([2500], orc.F16, "fp8"),
+])
+def test_small_batch_plan_against_oracle(lens, code, kv):
+    """A batch too small to fill the GPU in 512-token partitions (the
+    engine's one-sequence call): the plan takes partitions down to one
+    iteration per wavefront (128 tokens of 2-byte KV, 256 of FP8) and merges
+    up to 32 of them.  Against the oracle, with holes; the same case through
+    the v2 operator with the engine's scratch (f16 partial outputs for f16)."""
+    S = len(lens)
+    if kv is None:
+        case = inputs.make_paged_case(170 + S, S, 32, 8, 128, 16, lens, code, holes=1)
+        q, k, v, bt, sl = _gpu_case(case)
+        desc = tla.make_decode_desc(q, k, bt, 8, case.scale, gqa_map=tla.GQA_GROUPED)
+        ref = _ref(case, tla.GQA_GROUPED)
+        atol = ATOL
+    else:
+        case = inputs.make_paged_case(180 + S, S, 32, 8, 128, 16, lens, orc.F32, holes=1)
+        ks = float(np.abs(case.k_cache).max()) / 448
+        vs = float(np.abs(case.v_cache).max()) / 448
+        k8, v8 = orc.f32_to_e4m3(case.k_cache, 1 / ks), orc.f32_to_e4m3(case.v_cache, 1 / vs)
+        qn = inputs.encode(orc.bits_to_f32(case.q, orc.F32), code)
+        ref = orc.paged_attention(qn, code, k8, v8, orc.FP8, case.tables, case.seq_lens, 8, case.scale, orc.GROUPED,
+                                  0, ks, vs)
+        q, k, v, bt, sl = dev(qn, code), dev(k8), dev(v8), dev(case.tables), dev(case.seq_lens)
+        desc = tla.make_decode_desc(q, k, bt, 8, case.scale, gqa_map=tla.GQA_GROUPED, kv_dtype=tla.FP8_E4M3,
+                                    k_scale=ks, v_scale=vs)
+        atol = ATOL_FP8
+    max_ctx = int(max(lens))
+    nbytes = tla.workspace_bytes(desc, max_ctx)
+    P = nbytes // (S * 32 * (128 + 2) * 4)
+    assert P > -(-max_ctx // 512), P                   # finer than 512-token partitions
+    ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device="cuda")
+    out = torch.full_like(q, float("nan"))
+    print(f"case small-batch plan lens={lens} code={code} kv={kv} P={P}", flush=True)
+    tla.paged_attention_decode(desc, out, q, k, v, bt, sl, max_ctx, ws)
+    torch.cuda.synchronize()
+    assert_close(out, ref, code, atol, f"small batch {lens}")
+    if kv is None:
+        o2 = run_v2(case, tla.GQA_GROUPED)
+        assert_close(o2, ref, code, ATOL, f"v2 small batch {lens}")

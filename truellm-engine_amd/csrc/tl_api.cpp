@@ -34,6 +34,19 @@ bool is_float_kind(int32_t d) {
   return d == TL_DTYPE_F32 || d == TL_DTYPE_F16 || d == TL_DTYPE_BF16;
 }
 
+bool uses_mfma(const tl_decode_desc* d) {
+  return tl::decode_uses_mfma(d->kv_dtype, d->num_heads, d->num_kv_heads, d->head_size, d->block_size);
+}
+
+// The token granularity of split-K partitions: the matrix-core kernels
+// split at any multiple of their wavefront iteration (32 tokens of 2-byte
+// KV, 64 of FP8), the others at kDecodeChunk (their scores of one chunk
+// live in LDS).
+int partition_grain(const tl_decode_desc* d) {
+  if (!uses_mfma(d)) return tl::kDecodeChunk;
+  return d->kv_dtype == TL_DTYPE_FP8_E4M3 ? 64 : 32;
+}
+
 int check_decode(const tl_decode_desc* d) {
   if (!d) return fail(TL_ERR_INVALID_ARGUMENT, "desc is NULL");
   if (d->num_seqs < 0) return fail(TL_ERR_INVALID_ARGUMENT, "num_seqs=%d < 0", d->num_seqs);
@@ -76,10 +89,11 @@ int check_decode(const tl_decode_desc* d) {
                 "heads 64/256, and 80/96 for 2-byte KV, with block size 16; F32 KV heads 64/128/256 with "
                 "block size 16)",
                 hs, bs, d->kv_dtype);
+  const int grain = partition_grain(d);
   if (d->partition_tokens != 0 && d->partition_tokens != -1 &&
-      (d->partition_tokens <= 0 || d->partition_tokens % tl::kDecodeChunk))
+      (d->partition_tokens <= 0 || d->partition_tokens % grain))
     return fail(TL_ERR_INVALID_ARGUMENT, "partition_tokens=%d must be 0, -1 or a multiple of %d",
-                d->partition_tokens, tl::kDecodeChunk);
+                d->partition_tokens, grain);
   return TL_OK;
 }
 
@@ -93,11 +107,14 @@ int check_decode(const tl_decode_desc* d) {
 // 200 us single pass; equal lengths of 4096 would lose 3.5 %).
 void plan_partitions(const tl_decode_desc* d, int32_t max_ctx, int* P, int* PT) {
   const int chunks = max_ctx > 0 ? (max_ctx + tl::kDecodeChunk - 1) / tl::kDecodeChunk : 1;
+  if (d->partition_tokens > 0) {
+    *PT = d->partition_tokens;
+    *P = max_ctx > 0 ? (int)(((int64_t)max_ctx + *PT - 1) / *PT) : 1;
+    return;
+  }
   int pt_chunks;
   if (d->partition_tokens == -1) {
     pt_chunks = chunks;
-  } else if (d->partition_tokens > 0) {
-    pt_chunks = d->partition_tokens / tl::kDecodeChunk;
   } else {
     const int group = d->num_heads / d->num_kv_heads;
     // q heads per workgroup: 16 for the matrix-core kernels, 4 otherwise
@@ -114,6 +131,27 @@ void plan_partitions(const tl_decode_desc* d, int32_t max_ctx, int* P, int* PT) 
   if (pt_chunks < 1) pt_chunks = 1;
   *P = (chunks + pt_chunks - 1) / pt_chunks;
   *PT = pt_chunks * tl::kDecodeChunk;
+  // A split batch too small to give every CU a workgroup even in
+  // kDecodeChunk partitions (the engine decodes one sequence per call,
+  // cuda_engine.cpp:1138-1159): the matrix-core kernels take shorter
+  // partitions, down to one iteration per wavefront of a 4-wavefront
+  // workgroup (128 tokens of 2-byte KV, 256 of FP8), so that about 256
+  // workgroups share the context.  (A context that the plan runs single
+  // pass stays so: the merge's launch would cost more than it saves.)
+  if (d->partition_tokens == 0 && uses_mfma(d) && *P > 1) {
+    const int group = d->num_heads / d->num_kv_heads;
+    const long items = (long)d->num_seqs * d->num_kv_heads * ((group + 15) / 16);
+    if (items > 0 && items * *P < 256) {
+      const int round = 4 * partition_grain(d);
+      const long want = (256 + items - 1) / items;
+      long pt = (max_ctx + want - 1) / want;
+      pt = (pt + round - 1) / round * round;
+      if (pt < *PT) {
+        *PT = (int)pt;
+        *P = (int)((max_ctx + pt - 1) / pt);
+      }
+    }
+  }
 }
 
 tl::DecodeLaunch make_launch(const tl_decode_desc* d, void* out, const void* q,
@@ -147,6 +185,46 @@ size_t ws_bytes(const tl_decode_desc* d, int P) {
 }
 
 }  // namespace
+
+// The plan of paged_attention_v2 inside the caller's scratch.  The scratch
+// holds Pc partitions: exp_sums / max_logits fp32 [S, H, Pc], tmp_out
+// [S, H, Pc, head_size] in the call's dtype.  The engine sizes it as
+// ceil(max_context_len / (32 block_size)) (cuda_engine.cpp:273-285,1144);
+// the reference kernel writes (max_context_len / block_size + 31) / 32
+// partitions (paged_attention_v2.cu:196), which is never more, so a caller
+// that sized the scratch for the reference kernel has at least that many
+// and Pc is taken as that count.  The engine reads none of it after the
+// call, so it is the workspace of the library's own plan: the (max, sum)
+// pairs in max_logits / exp_sums and the partial outputs in tmp_out.  f16
+// calls on the matrix-core kernels keep the partial outputs in f16, one
+// partition per tmp_out slot, as the reference's own tmp_out does
+// (paged_attention_v2.cu:61-63,111-124 store them in scalar_t): a partial
+// is a convex combination of f16 values, so it stays in f16's range, and
+// its rounding (half an ulp of a value below max |v|) is within the 2e-3
+// bar for the N(0, 1) values of the workloads.  bf16 and f32 keep fp32
+// partials (Pc * elem / 4 partitions in tmp_out's bytes).  Where the plan
+// wants more partitions than the scratch holds they are made longer; where
+// it wants one (a large batch) the call runs single pass.  d is the
+// descriptor of the call (partition_tokens 0) and may be changed.
+void v2_plan(tl_decode_desc* d, int32_t max_ctx, bool tmp_aligned, int* P, int* PT, bool* f16_parts) {
+  const int Pc = (max_ctx / d->block_size + 31) / 32;
+  const int elem = d->q_dtype == TL_DTYPE_F32 ? 4 : 2;
+  *f16_parts = d->q_dtype == TL_DTYPE_F16 && uses_mfma(d);
+  const int cap = tmp_aligned ? (*f16_parts ? Pc : Pc * elem / 4) : 1;
+  plan_partitions(d, max_ctx, P, PT);
+  if (*P > cap) {
+    if (cap <= 1) {
+      *P = 1;
+    } else {
+      // the longer partitions, in the kernels' granularity (a multiple of
+      // kDecodeChunk, or of a 4-wavefront round for the matrix-core kernels)
+      const int round = uses_mfma(d) ? 4 * partition_grain(d) : tl::kDecodeChunk;
+      const int64_t pt = ((int64_t)max_ctx + cap - 1) / cap;
+      d->partition_tokens = (int)((pt + round - 1) / round * round);
+      plan_partitions(d, max_ctx, P, PT);
+    }
+  }
+}
 
 int tl::report_error(int code, const char* msg) { return fail(code, "%s", msg); }
 
@@ -284,33 +362,9 @@ int tl_paged_attention_v2(void* out, float* exp_sums, float* max_logits, void* t
     return fail(TL_ERR_INVALID_ARGUMENT, "NULL tensor pointer");
   if (!aligned16(k_cache) || !aligned16(v_cache))
     return fail(TL_ERR_INVALID_ARGUMENT, "k_cache/v_cache must be 16-byte aligned");
-  // The caller's scratch holds Pc partitions: exp_sums / max_logits fp32
-  // [S, H, Pc], tmp_out [S, H, Pc, head_size] in the call's dtype.  The
-  // engine sizes it as ceil(max_context_len / (32 block_size))
-  // (cuda_engine.cpp:273-285,1144); the reference kernel writes
-  // (max_context_len / block_size + 31) / 32 partitions
-  // (paged_attention_v2.cu:196), which is never more, so a caller that
-  // sized the scratch for the reference kernel has at least that many and
-  // Pc is taken as that count.  The engine reads none of it after the call,
-  // so it is used as the workspace of the library's own plan: fp32
-  // partials, the (max, sum) pairs in max_logits / exp_sums and the partial
-  // outputs in tmp_out's bytes, which hold Pc * elem / 4 fp32 partitions.
-  // Where the plan wants more partitions than that, they are made longer;
-  // where it wants one (a large batch), the call runs single pass.
-  const int Pc = (max_context_len / block_size + 31) / 32;
-  const int elem = dtype == TL_DTYPE_F32 ? 4 : 2;
-  const int cap = aligned16(tmp_out) ? Pc * elem / 4 : 1;
   int P, PT;
-  plan_partitions(&d, max_context_len, &P, &PT);
-  if (P > cap) {
-    if (cap <= 1) {
-      P = 1;
-    } else {
-      const int chunks = (max_context_len + tl::kDecodeChunk - 1) / tl::kDecodeChunk;
-      d.partition_tokens = (chunks + cap - 1) / cap * tl::kDecodeChunk;
-      plan_partitions(&d, max_context_len, &P, &PT);
-    }
-  }
+  bool f16_parts;
+  v2_plan(&d, max_context_len, aligned16(tmp_out), &P, &PT, &f16_parts);
   tl::DecodeLaunch a = make_launch(&d, out, q, k_cache, v_cache, block_tables, seq_lens, stream);
   if (P > 1) {
     a.num_partitions = P;
@@ -318,8 +372,23 @@ int tl_paged_attention_v2(void* out, float* exp_sums, float* max_logits, void* t
     a.part_m = max_logits;
     a.part_l = exp_sums;
     a.part_o = tmp_out;
+    a.part_o_dtype = f16_parts ? TL_DTYPE_F16 : TL_DTYPE_F32;
   }
   return run(a);
+}
+
+int32_t tl_paged_attention_v2_partitions(int32_t num_seqs, int32_t num_heads, int32_t num_kv_heads,
+                                         int32_t head_size, int32_t block_size, int32_t dtype,
+                                         int32_t max_context_len, int32_t* partition_tokens) {
+  tl_decode_desc d = {num_seqs, num_heads, num_kv_heads, head_size, block_size, 1, 1,
+                      dtype, dtype, TL_GQA_MODULO, 0, 1.f, 1.f, 1.f};
+  if (check_decode(&d) != TL_OK || max_context_len < 0) return -1;
+  int P, PT;
+  bool f16_parts;
+  v2_plan(&d, max_context_len, true, &P, &PT, &f16_parts);
+  if (partition_tokens) *partition_tokens = P > 1 ? PT : 0;
+  ok();
+  return P;
 }
 
 int tl_reshape_and_cache(const void* key, const void* value, void* k_cache, void* v_cache,

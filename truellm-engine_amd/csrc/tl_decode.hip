@@ -415,9 +415,9 @@ __global__ __launch_bounds__(64) void lse_reduce_kernel(
 // partitions w, w + 4, ... (lane: head dims lane + 64 c), 4 partitions per
 // round with their loads in flight together, and the 4 wavefronts' sums
 // meet in LDS.
-template <Kind QK, int HEAD>
+template <Kind QK, int HEAD, Kind PO = Kind::F32>
 __global__ __launch_bounds__(256) void lse_reduce_long_kernel(
-    void* out, const float* part_m, const float* part_l, const float* part_o, const int32_t* seq_lens,
+    void* out, const float* part_m, const float* part_l, const void* part_o, const int32_t* seq_lens,
     int num_heads, int num_partitions, int partition_tokens, int kivi_residual, int kivi_pages,
     int kivi_max_pages) {
   constexpr int CH = (HEAD + 63) / 64, U = 4;
@@ -456,7 +456,7 @@ __global__ __launch_bounds__(256) void lse_reduce_long_kernel(
 #pragma unroll
       for (int c = 0; c < CH; ++c) {
         const int d = min(lane + 64 * c, HEAD - 1);
-        v[u][c] = (in && lane + 64 * c < HEAD) ? part_o[(pb + i) * HEAD + d] : 0.f;
+        v[u][c] = (in && lane + 64 * c < HEAD) ? load_scalar<PO>(part_o, (pb + i) * HEAD + d) : 0.f;
       }
     }
 #pragma unroll
@@ -487,9 +487,9 @@ __global__ __launch_bounds__(256) void lse_reduce_long_kernel(
 // the pairs, then the outputs round by round waited for each in turn
 // (64 partitions: 12.3 us).  Within a wavefront the partitions are summed
 // in ascending order.
-template <Kind QK, int HEAD>
+template <Kind QK, int HEAD, Kind PO = Kind::F32>
 __global__ __launch_bounds__(256) void lse_reduce_wide_kernel(
-    void* out, const float* part_m, const float* part_l, const float* part_o, const int32_t* seq_lens,
+    void* out, const float* part_m, const float* part_l, const void* part_o, const int32_t* seq_lens,
     int num_heads, int num_partitions, int partition_tokens, int kivi_residual, int kivi_pages,
     int kivi_max_pages) {
   constexpr int CH = (HEAD + 63) / 64, U = 16, kMaxParts = 256;
@@ -507,7 +507,7 @@ __global__ __launch_bounds__(256) void lse_reduce_wide_kernel(
     for (int u = 0; u < U; ++u) {
       const int i = min(i0 + 4 * u, P - 1);  // every load stays inside the partials
 #pragma unroll
-      for (int c = 0; c < CH; ++c) v[u][c] = part_o[(pb + i) * HEAD + min(lane + 64 * c, HEAD - 1)];
+      for (int c = 0; c < CH; ++c) v[u][c] = load_scalar<PO>(part_o, (pb + i) * HEAD + min(lane + 64 * c, HEAD - 1));
     }
   };
   float v[U][CH];
@@ -553,10 +553,10 @@ void launch_reduce(const DecodeLaunch& a) {
   const dim3 rgrid((unsigned)(a.num_seqs * a.num_heads));
   if (P > 256)
     hipLaunchKernelGGL((lse_reduce_long_kernel<QK, HEAD>), rgrid, dim3(256), 0, a.stream, a.out, a.part_m,
-                       a.part_l, (const float*)a.part_o, a.seq_lens, a.num_heads, P, a.partition_tokens, 0, 0, 0);
+                       a.part_l, a.part_o, a.seq_lens, a.num_heads, P, a.partition_tokens, 0, 0, 0);
   else if (P > 8)
     hipLaunchKernelGGL((lse_reduce_wide_kernel<QK, HEAD>), rgrid, dim3(256), 0, a.stream, a.out, a.part_m,
-                       a.part_l, (const float*)a.part_o, a.seq_lens, a.num_heads, P, a.partition_tokens, 0, 0, 0);
+                       a.part_l, a.part_o, a.seq_lens, a.num_heads, P, a.partition_tokens, 0, 0, 0);
   else
     hipLaunchKernelGGL((lse_reduce_kernel<QK, Kind::F32, HEAD>), rgrid, dim3(64), 0, a.stream, a.out, a.part_m,
                        a.part_l, a.part_o, a.seq_lens, a.num_heads, P, a.partition_tokens, 0, 0, 0);
@@ -654,22 +654,22 @@ int launch_shape(const DecodeLaunch& a) {
 
 }  // namespace
 
-template <Kind QK>
+template <Kind QK, Kind PO>
 void launch_lse_reduce_q(void* out, const float* part_m, const float* part_l, const void* part_o,
                          const int32_t* seq_lens, int num_seqs, int num_heads, int num_partitions,
                          int partition_tokens, int kivi_residual, int kivi_pages, int kivi_max_pages,
                          hipStream_t stream) {
   const dim3 grid((unsigned)(num_seqs * num_heads));
   if (num_partitions > 256)
-    hipLaunchKernelGGL((lse_reduce_long_kernel<QK, 128>), grid, dim3(256), 0, stream, out, part_m, part_l,
-                       (const float*)part_o, seq_lens, num_heads, num_partitions, partition_tokens, kivi_residual,
-                       kivi_pages, kivi_max_pages);
+    hipLaunchKernelGGL((lse_reduce_long_kernel<QK, 128, PO>), grid, dim3(256), 0, stream, out, part_m, part_l,
+                       part_o, seq_lens, num_heads, num_partitions, partition_tokens, kivi_residual, kivi_pages,
+                       kivi_max_pages);
   else if (num_partitions > 8)
-    hipLaunchKernelGGL((lse_reduce_wide_kernel<QK, 128>), grid, dim3(256), 0, stream, out, part_m, part_l,
-                       (const float*)part_o, seq_lens, num_heads, num_partitions, partition_tokens, kivi_residual,
-                       kivi_pages, kivi_max_pages);
+    hipLaunchKernelGGL((lse_reduce_wide_kernel<QK, 128, PO>), grid, dim3(256), 0, stream, out, part_m, part_l,
+                       part_o, seq_lens, num_heads, num_partitions, partition_tokens, kivi_residual, kivi_pages,
+                       kivi_max_pages);
   else
-    hipLaunchKernelGGL((lse_reduce_kernel<QK, Kind::F32, 128>), grid, dim3(64), 0, stream, out, part_m, part_l,
+    hipLaunchKernelGGL((lse_reduce_kernel<QK, PO, 128>), grid, dim3(64), 0, stream, out, part_m, part_l,
                        part_o, seq_lens, num_heads, num_partitions, partition_tokens, kivi_residual, kivi_pages,
                        kivi_max_pages);
 }
@@ -677,14 +677,23 @@ void launch_lse_reduce_q(void* out, const float* part_m, const float* part_l, co
 int launch_lse_reduce(void* out, int q_dtype, const float* part_m, const float* part_l,
                       const void* part_o, const int32_t* seq_lens, int num_seqs,
                       int num_heads, int head_size, int num_partitions, int partition_tokens,
-                      int kivi_residual, int kivi_pages, int kivi_max_pages, hipStream_t stream) {
+                      int kivi_residual, int kivi_pages, int kivi_max_pages, hipStream_t stream,
+                      int part_o_dtype) {
   if (head_size != 128) return 3;
-  if (q_dtype == (int)Kind::F16)
-    launch_lse_reduce_q<Kind::F16>(out, part_m, part_l, part_o, seq_lens, num_seqs, num_heads, num_partitions,
-                                   partition_tokens, kivi_residual, kivi_pages, kivi_max_pages, stream);
+  if (q_dtype == (int)Kind::F16 && part_o_dtype == (int)Kind::F16)
+    launch_lse_reduce_q<Kind::F16, Kind::F16>(out, part_m, part_l, part_o, seq_lens, num_seqs, num_heads,
+                                              num_partitions, partition_tokens, kivi_residual, kivi_pages,
+                                              kivi_max_pages, stream);
+  else if (part_o_dtype != (int)Kind::F32)
+    return 3;
+  else if (q_dtype == (int)Kind::F16)
+    launch_lse_reduce_q<Kind::F16, Kind::F32>(out, part_m, part_l, part_o, seq_lens, num_seqs, num_heads,
+                                              num_partitions, partition_tokens, kivi_residual, kivi_pages,
+                                              kivi_max_pages, stream);
   else if (q_dtype == (int)Kind::BF16)
-    launch_lse_reduce_q<Kind::BF16>(out, part_m, part_l, part_o, seq_lens, num_seqs, num_heads, num_partitions,
-                                    partition_tokens, kivi_residual, kivi_pages, kivi_max_pages, stream);
+    launch_lse_reduce_q<Kind::BF16, Kind::F32>(out, part_m, part_l, part_o, seq_lens, num_seqs, num_heads,
+                                               num_partitions, partition_tokens, kivi_residual, kivi_pages,
+                                               kivi_max_pages, stream);
   else
     return 3;
   return hipGetLastError() == hipSuccess ? 0 : 5;

@@ -99,9 +99,10 @@ bool partition_per_wave(int partition_tokens, long partitions_total) {
   return partition_tokens <= 16 * mw::tokens_per_iteration<KV>() && partitions_total >= 4096;
 }
 
-template <Kind KV, Kind QK, int NW, bool FINAL, int BS>
+// PO_SPLIT: the split-K partial outputs' type (F32, or F16 for f16 q)
+template <Kind KV, Kind QK, int NW, bool FINAL, int BS, Kind PO_SPLIT = Kind::F32>
 void launch_kernel(const Params& p, unsigned grid, hipStream_t stream) {
-  constexpr Kind PO = FINAL ? QK : Kind::F32;
+  constexpr Kind PO = FINAL ? QK : PO_SPLIT;
   if constexpr (KV == Kind::FP8)
     hipLaunchKernelGGL((fp8_decode_kernel<QK, PO, NW, FINAL, BS>), dim3(grid), dim3(NW * kWave), 0, stream, p);
   else
@@ -135,7 +136,10 @@ int launch_typed(const DecodeLaunch& a) {
     launch_kernel<KV, QK, 4, true, BS>(p, items, a.stream);
     return hipGetLastError() == hipSuccess ? 0 : 5;
   }
-  if (partition_per_wave<KV>(a.partition_tokens, (long)items * P)) {
+  // f16 partials: 2-byte f16 KV only, one partition per workgroup
+  const bool f16_parts = a.part_o_dtype == (int)Kind::F16;
+  if (f16_parts && KV != Kind::F16) return 3;
+  if (!f16_parts && partition_per_wave<KV>(a.partition_tokens, (long)items * P)) {
     // as many partitions per wavefront as keep >= 2048 wavefronts (one
     // resident round at 2-3 per SIMD), at most 8
     p.parts_per_wave = (int)std::max(1L, std::min(8L, (long)items * P / 2048));
@@ -146,12 +150,25 @@ int launch_typed(const DecodeLaunch& a) {
     p.stash_floats = 4 * stash * (int)sizeof(float) <= 64 * 1024 ? stash : 0;
     hipLaunchKernelGGL((wave_partition_kernel<KV, QK, BS>), dim3(items * ((runs + 3) / 4)), dim3(4 * kWave),
                        4 * p.stash_floats * sizeof(float), a.stream, p);
+  } else if (items * P <= 128) {
+    // a grid of at most half the CUs (the engine's one-sequence call inside
+    // the v2 scratch: 8 partitions x 8 kv heads): 8 wavefronts per
+    // workgroup (two per SIMD: the wavefront keeps its 256 registers), so
+    // that each streams two of a 512-token partition's iterations
+    if (f16_parts) {
+      if constexpr (KV == Kind::F16) launch_kernel<KV, QK, 8, false, BS, Kind::F16>(p, items * P, a.stream);
+    } else {
+      launch_kernel<KV, QK, 8, false, BS>(p, items * P, a.stream);
+    }
+  } else if (f16_parts) {
+    if constexpr (KV == Kind::F16) launch_kernel<KV, QK, 4, false, BS, Kind::F16>(p, items * P, a.stream);
   } else {
     launch_kernel<KV, QK, 4, false, BS>(p, items * P, a.stream);
   }
   if (hipGetLastError() != hipSuccess) return 5;
   return launch_lse_reduce(a.out, a.q_dtype, a.part_m, a.part_l, a.part_o, a.seq_lens,
-                           a.num_seqs, a.num_heads, mw::kHead, P, a.partition_tokens, 0, 0, 0, a.stream);
+                           a.num_seqs, a.num_heads, mw::kHead, P, a.partition_tokens, 0, 0, 0, a.stream,
+                           a.part_o_dtype);
 }
 
 template <Kind KV, Kind QK>

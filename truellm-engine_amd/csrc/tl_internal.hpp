@@ -28,6 +28,7 @@ struct DecodeLaunch {
   int partition_tokens;         // multiple of kDecodeChunk when P > 1
   int q_dtype, kv_dtype, gqa_map;
   float scale, k_scale, v_scale;
+  int part_o_dtype;             // split-K partial outputs: F32 (0), or F16 (f16 q and KV, head 128)
   hipStream_t stream;
 };
 
@@ -127,7 +128,8 @@ int launch_block_copy(const BlockCopy& c, hipStream_t stream);
 int launch_lse_reduce(void* out, int q_dtype, const float* part_m, const float* part_l,
                       const void* part_o, const int32_t* seq_lens, int num_seqs,
                       int num_heads, int head_size, int num_partitions, int partition_tokens,
-                      int kivi_residual, int kivi_pages, int kivi_max_pages, hipStream_t stream);
+                      int kivi_residual, int kivi_pages, int kivi_max_pages, hipStream_t stream,
+                      int part_o_dtype = 0);
 
 // ---- KIVI ------------------------------------------------------------------
 int launch_kivi_vec(const void* in, void* out, int n_vecs, int head_dim, int n_outliers,

@@ -117,6 +117,7 @@ _SIG = {
     "tl_paged_attention_decode_noalloc": (ctypes.c_int, [ctypes.POINTER(DecodeDesc), _P, _P, _P, _P, _P, _P, _I, _P]),
     "tl_paged_attention_v1": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F, _I, _I, _P]),
     "tl_paged_attention_v2": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F, _I, _I, _I, _P]),
+    "tl_paged_attention_v2_partitions": (_I, [_I, _I, _I, _I, _I, _I, _I, _P]),
     "tl_reshape_and_cache": (ctypes.c_int, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P]),
     "tl_reshape_and_cache_fp8": (ctypes.c_int, [_P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _I, _F, _F, _P]),
     "tl_rope_reshape_and_cache": (ctypes.c_int, [_P] * 10 + [_I] * 9 + [_P]),
@@ -279,6 +280,17 @@ def convert_fp8(out, inp, scale, stream=None, n=None):
     elements (default: all of inp)."""
     n = inp.numel() if n is None else n
     check(lib.tl_convert_fp8(_ptr(out), _ptr(inp), dtype_code(inp), n, scale, _stream(stream)))
+
+
+def v2_plan(num_seqs, num_heads, num_kv_heads, head_size, block_size, dtype, max_context_len):
+    """(partitions, partition_tokens) of tl_paged_attention_v2 for a call of
+    these sizes."""
+    pt = ctypes.c_int32(0)
+    P = lib.tl_paged_attention_v2_partitions(num_seqs, num_heads, num_kv_heads, head_size, block_size, dtype,
+                                             max_context_len, ctypes.byref(pt))
+    if P < 0:
+        raise TLError(ERR_INVALID_ARGUMENT, "tl_paged_attention_v2_partitions: sizes refused")
+    return P, pt.value
 
 
 def v2_num_partitions(max_context_len: int, block_size: int) -> int:
