@@ -843,6 +843,9 @@ def main():
     kvm = bench_kivi(args, mixed=True, name="kivi_mixed") if want("kivi") else None
     kv8 = bench_kivi(args, name="kivi_int8", bits=8) if want("kivi") else None
     kvr = bench_kivi(args, name="kivi_pre_rope", pre_rope=True) if want("kivi") else None
+    # the reference's default KiviConfig (config_schema.h:124,128): bits 8,
+    # keys held before RoPE
+    kvd = bench_kivi(args, name="kivi_default_config", bits=8, pre_rope=True) if want("kivi") else None
     fpa = bench_decode(args, "fp16", append=True, name="fp16_append") if want("kivi") else None
     f8 = bench_fp8(args, name="fp8") if want("fp8") else None
     f8p = bench_fp8(args, 512, name="fp8_pt512") if want("fp8") else None
@@ -964,6 +967,18 @@ def main():
             "rope_table_bytes_not_counted": True}
         if kv is not None:
             res["kivi_int4_pre_rope_keys"]["step_time_vs_rotated_keys"] = round(kvr["ms_per_step"] / kv["ms_per_step"], 3)
+        if fp is not None:
+            res["kivi_int4_pre_rope_keys"]["speedup_vs_fp16_tok_s"] = round(kvr["tok_s"] / fp["tok_s"], 3)
+    if kvd is not None:
+        res["kivi_default_config"] = {
+            "workload": "the reference's default KiviConfig (bits 8, pre_rope_keys true; config_schema.h:124,128): "
+                        "INT8 pages, keys held before RoPE and rotated at their positions inside attention, "
+                        "batch 64, ctx 4096, one appended token per step",
+            "gbs": round(kvd["gbs"], 2), "ms_per_step": round(kvd["ms_per_step"], 5), "tok_s": round(kvd["tok_s"], 1),
+            "pct_hbm_peak": round(100 * kvd["gbs"] / HBM_PEAK_GBS, 2), "bytes_per_step": int(kvd["bytes_per_step"]),
+            "rope_table_bytes_not_counted": True}
+        if fp is not None:
+            res["kivi_default_config"]["speedup_vs_fp16_tok_s"] = round(kvd["tok_s"] / fp["tok_s"], 3)
     if f8 is not None:
         res["fp8_e4m3_long_context"] = {
             "workload": "decode, batch 16, ctx 32768, 32 q / 8 kv heads, d 128, FP8 E4M3 KV with per-tensor "

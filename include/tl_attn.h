@@ -486,12 +486,17 @@ int tl_kivi_rope_decode_step(const tl_kivi_desc* desc, void* out, const void* q,
  * decode step of tl_kivi_paged_attention_decode / tl_kivi_decode_step with
  * every key rotated at its position in the sequence (token t of a sequence
  * at position t, style TL_ROPE_ADJACENT or TL_ROPE_HALVES, fp32 tables
- * [max_positions, 64], 16-byte aligned; t >= max_positions unrotated) as it
- * is scored: a page key after its dequantisation, a window key as read from
- * the fp16 pool, the step's new key as given.  Pages, pools and the appended
- * token hold the keys unrotated.  q is taken as given (rotated by the caller
- * at position seq_lens[s] - 1).  The standard entry points refuse a
- * descriptor with pre_rope_keys set, since they would score unrotated keys. */
+ * [max_positions, 64], 16-byte aligned, covering every position:
+ * max_positions >= max_context_len, else TL_ERR_INVALID_ARGUMENT) as it is
+ * scored: a page key after its dequantisation, a window key as read from
+ * the fp16 pool, the step's new key as given.  A page key of position
+ * t = 32 p + j is scored with the rotation of 32 p applied to q and that of
+ * j to the key (R_t = R_32p R_j: exact for tables of angles linear in the
+ * position, as RoPE's theta_i t are; the products run in f16).  Pages,
+ * pools and the appended token hold the keys unrotated.  q is taken as
+ * given (rotated by the caller at position seq_lens[s] - 1).  The standard
+ * entry points refuse a descriptor with pre_rope_keys set, since they would
+ * score unrotated keys. */
 int tl_kivi_paged_attention_decode_pre_rope(const tl_kivi_desc* desc, void* out, const void* q,
                                             const void* pages, const int32_t* page_tables,
                                             const void* k_cache, const void* v_cache,

@@ -434,7 +434,8 @@ def test_kivi_pre_rope_entry_points_check_their_arguments():
     """Keys held before RoPE: the standard decode and step refuse a
     descriptor with pre_rope_keys set (they would score unrotated keys); the
     _pre_rope entry points check the tables (non-NULL, 16-byte aligned,
-    max_positions > 0, style 0 or 1) before any device work."""
+    max_positions > 0 and covering max_context_len, style 0 or 1) before any
+    device work."""
     L = tla.lib
     d = _kdesc()
     d.pre_rope_keys = 1
@@ -460,6 +461,8 @@ def test_kivi_pre_rope_entry_points_check_their_arguments():
         assert f(cos=ctypes.c_void_p(0x1004)) == tla.ERR_INVALID_ARGUMENT
         assert "aligned" in tla.last_error()
         assert f(max_pos=0) == tla.ERR_INVALID_ARGUMENT
+        assert f(max_pos=4095) == tla.ERR_INVALID_ARGUMENT           # tables short of max_context_len 4096
+        assert "cover" in tla.last_error()
         assert f(style=2) == tla.ERR_INVALID_ARGUMENT
     z = _kdesc(num_seqs=0)
     z.pre_rope_keys = 1

@@ -437,15 +437,15 @@ def test_kivi_pre_rope_decode_matches_oracle(style, bits, pp):
     """Keys held before RoPE (tl_kivi_paged_attention_decode_pre_rope): each
     page key rotated after its dequantisation and each window key as read,
     at its token position, against the oracle's attention on the rotated
-    keys.  The tables hold 2048 positions, so the 3000- and 4096-token
-    sequences score their later keys unrotated; a page and a window block are
-    holes.  The same descriptor through the standard entry point is refused."""
+    keys; a page and a window block are holes.  The same descriptor through
+    the standard entry point is refused, and so are tables that do not cover
+    every position (2048 positions for a 4096-token sequence)."""
     from test_oracle import rope_tables
     kc = KiviCase(57, [4096, 1000, 161, 159, 0, 1, 2047, 3000], bits=bits)
     kc.page_tables[1, 3] = -1
     kc.tables[6, (2047 - 60) // 16] = -1
     pages_np = kc.oracle_pages()
-    cos_t, sin_t = rope_tables(2048, 128)
+    cos_t, sin_t = rope_tables(4096, 128)
     qd, kd, vd = dev(kc.q, orc.F16), dev(kc.k, orc.F16), dev(kc.v, orc.F16)
     btd, sld, ptd = dev(kc.tables), dev(kc.lens), dev(kc.page_tables)
     pages = torch.from_numpy(pages_np).cuda()
@@ -463,6 +463,10 @@ def test_kivi_pre_rope_decode_matches_oracle(style, bits, pp):
     assert_close(out, want, orc.F16, ATOL_KIVI, f"style={style} bits={bits} pp={pp}")
     with pytest.raises(tla.TLError):
         tla.kivi_paged_attention_decode(desc, out, qd, pages, ptd, kd, vd, btd, sld, max_ctx, ws)
+    short_c, short_s = dev(cos_t[:2048].copy()), dev(sin_t[:2048].copy())
+    with pytest.raises(tla.TLError):
+        tla.kivi_paged_attention_decode_pre_rope(desc, out, qd, pages, ptd, kd, vd, btd, sld, max_ctx, short_c,
+                                                 short_s, style, ws)
 
 
 @pytest.mark.parametrize("H,n_kv", [(16, 8), (64, 8), (8, 8)])
@@ -501,14 +505,13 @@ def test_kivi_pre_rope_step_matches_oracle_each_step(style, bits, through_rope_s
     tl_kivi_decode_step_pre_rope, q is taken as given.  The host pools take
     the unrotated keys, the pages are rebuilt from them, and the expected
     output is the oracle's attention with every key rotated at its position.
-    Sequence 5 runs past the 1024-position tables halfway; pages complete
-    during the run.  At the end the pools and pages are the oracle's bit for
-    bit (unrotated keys)."""
+    Pages complete during the run.  At the end the pools and pages are the
+    oracle's bit for bit (unrotated keys)."""
     from test_oracle import rope_tables
     start = np.array([150, 159, 160, 191, 33, 1000], np.int32)
     steps = 36
     kc = KiviCase(73, start + steps, H=32, extra_blocks=1, bits=bits)
-    cos_t, sin_t = rope_tables(1024, 128)
+    cos_t, sin_t = rope_tables(1040, 128)
     q_base = kc.q.copy()
     qd, kd, vd = dev(kc.q, orc.F16), dev(kc.k, orc.F16), dev(kc.v, orc.F16)
     btd, ptd = dev(kc.tables), dev(kc.page_tables)
@@ -700,12 +703,11 @@ def test_decode_step_equals_append_then_decode(H, R, pp, bits):
 def test_pre_rope_step_equals_append_then_pre_rope_decode(style, bits, pp):
     """Keys held before RoPE: tl_kivi_decode_step_pre_rope gives the bytes of
     tl_kivi_append followed by tl_kivi_paged_attention_decode_pre_rope
-    (outputs, pages and pools), over 40 steps that complete pages; sequence
-    5 crosses the end of the 1024-position tables."""
+    (outputs, pages and pools), over 40 steps that complete pages."""
     from test_oracle import rope_tables
     start = np.array([150, 159, 160, 191, 33, 1000], np.int32)
     steps = 40
-    cos_t, sin_t = rope_tables(1024, 128)
+    cos_t, sin_t = rope_tables(1040, 128)
     runs = []
     for fused in (False, True):
         kc = KiviCase(59, start + steps, H=32, extra_blocks=1, bits=bits)

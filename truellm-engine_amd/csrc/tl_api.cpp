@@ -702,8 +702,15 @@ struct KiviRope {
   int32_t max_positions, style;
 };
 
-static int check_kivi_rope(const KiviRope& r) {
+// The decode scores a key of position t = 32 p + j (page p) with the
+// rotation of t0 = 32 p on q and that of j on the key (R_t = R_t0 R_j, the
+// tables' angles being linear in the position), so the tables must cover
+// every position the call scores.
+static int check_kivi_rope(const KiviRope& r, int32_t max_context_len) {
   if (r.max_positions <= 0) return fail(TL_ERR_INVALID_ARGUMENT, "max_positions=%d", r.max_positions);
+  if (r.max_positions < max_context_len)
+    return fail(TL_ERR_INVALID_ARGUMENT, "rope tables of max_positions=%d do not cover max_context_len=%d",
+                r.max_positions, max_context_len);
   if (r.style != TL_ROPE_ADJACENT && r.style != TL_ROPE_HALVES)
     return fail(TL_ERR_INVALID_ARGUMENT, "style=%d", r.style);
   if (!r.cos_table || !r.sin_table) return fail(TL_ERR_INVALID_ARGUMENT, "NULL rope table");
@@ -835,7 +842,7 @@ int tl_kivi_paged_attention_decode_pre_rope(const tl_kivi_desc* desc, void* out,
                                             void* workspace, size_t workspace_bytes, void* stream) {
   const KiviRope r{cos_table, sin_table, max_positions, style};
   int rc = check_kivi(desc);
-  if (rc || (rc = check_kivi_rope(r))) return rc;
+  if (rc || (rc = check_kivi_rope(r, max_context_len))) return rc;
   return kivi_decode_impl(desc, out, q, pages, page_tables, k_cache, v_cache, block_tables, seq_lens,
                           max_context_len, workspace, workspace_bytes, stream, nullptr, &r);
 }
@@ -875,7 +882,7 @@ int tl_kivi_decode_step_pre_rope(const tl_kivi_desc* desc, void* out, const void
                                  size_t workspace_bytes, void* stream) {
   const KiviRope r{cos_table, sin_table, max_positions, style};
   int rc = check_kivi(desc);
-  if (rc || (rc = check_kivi_rope(r))) return rc;
+  if (rc || (rc = check_kivi_rope(r, max_context_len))) return rc;
   return kivi_step_impl(desc, out, q, key, value, slot_mapping, pages, page_tables, k_cache, v_cache, block_tables,
                         seq_lens, max_context_len, workspace, workspace_bytes, stream, &r);
 }
@@ -914,7 +921,7 @@ int tl_kivi_rope_decode_step(const tl_kivi_desc* desc, void* out, const void* q,
     return fail(TL_ERR_INVALID_ARGUMENT, "workspace of %zu bytes needed, %zu given", need, workspace_bytes);
   if (!aligned16(workspace)) return fail(TL_ERR_INVALID_ARGUMENT, "workspace must be 16-byte aligned");
   const KiviRope kr{cos_table, sin_table, max_positions, style};
-  if (desc->pre_rope_keys && (rc = check_kivi_rope(kr))) return rc;
+  if (desc->pre_rope_keys && (rc = check_kivi_rope(kr, max_context_len))) return rc;
   const size_t qoff = kivi_rope_q_offset(desc, max_context_len);
   char* q_rot = (char*)workspace + qoff;
   char* k_rot = q_rot + align256((size_t)desc->num_seqs * desc->num_heads * desc->head_size * 2);

@@ -78,6 +78,61 @@ __device__ __forceinline__ void rope_cs1(const KiviParams& k, int t, int i, floa
   s = in ? sv : 0.f;
 }
 
+// Rotations of a lane's 32 channels 32 m + 8 grp + e (block m, element e:
+// the channels of its q.k A and B operands) in packed f16.  Per channel, C
+// = cos of the channel's pair and S = -sin for the pair's first channel,
+// +sin for its second; then R x = C x + S partner(x) and R^T x = C x - S
+// partner(x), where partner(x) is the pair's other channel: the neighbour
+// in the same dword (style 0, pairs 2 i, 2 i + 1) or the same element of
+// block m + 2 (style 1, pairs i, i + 64, blocks m and m + 2 together).
+// The blocks one call rotates: style 0 block m, style 1 blocks m, m + 2.
+template <bool TRANSPOSE>
+__device__ __forceinline__ void rope_pair_blocks(h8& a, h8& b, const h8& ca, const h8& sa, const h8& cb,
+                                                 const h8& sb) {
+  const h8 a0 = a, b0 = b;
+  a = TRANSPOSE ? a0 * ca - b0 * sa : a0 * ca + b0 * sa;
+  b = TRANSPOSE ? b0 * cb - a0 * sb : b0 * cb + a0 * sb;
+}
+template <bool TRANSPOSE>
+__device__ __forceinline__ void rope_one_block(h8& a, const h8& c, const h8& s) {
+  const h8 pt = __builtin_shufflevector(a, a, 1, 0, 3, 2, 5, 4, 7, 6);
+  a = TRANSPOSE ? a * c - pt * s : a * c + pt * s;
+}
+// C and S of block m (style 0: pairs 16 m + 4 grp + d, each twice) or of
+// blocks m and m + 2 (style 1: pairs 32 m + 8 grp + e) at position t, from
+// the fp32 tables.
+__device__ __forceinline__ void rope_coef_block0(const KiviParams& k, int t, int m, int grp, h8& c, h8& s) {
+  f4 cv, sv;
+  rope_cs4(k, t, 16 * m + 4 * grp, cv, sv);
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    c[2 * d] = c[2 * d + 1] = (_Float16)cv[d];
+    s[2 * d] = (_Float16)(-sv[d]);
+    s[2 * d + 1] = (_Float16)sv[d];
+  }
+}
+__device__ __forceinline__ void rope_coef_block1(const KiviParams& k, int t, int m, int grp, h8& c, h8& sa,
+                                                 h8& sb) {
+  f4 c0, s0, c1, s1;
+  rope_cs4(k, t, 32 * m + 8 * grp, c0, s0);
+  rope_cs4(k, t, 32 * m + 8 * grp + 4, c1, s1);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    c[e] = (_Float16)(e < 4 ? c0[e & 3] : c1[e & 3]);
+    sb[e] = (_Float16)(e < 4 ? s0[e & 3] : s1[e & 3]);
+    sa[e] = -sb[e];
+  }
+}
+// The rotations of positions 0 .. 31 (a page's offsets) in LDS, per
+// channel: [C or S][offset j][channel].
+constexpr int kRopeRows = kKiviPageTokens;
+struct RopeTable {
+  uint16_t cs[2][kRopeRows][kKiviHead];
+};
+__device__ __forceinline__ h8 rope_lds(const RopeTable& tb, int which, int j, int m, int grp) {
+  return *reinterpret_cast<const h8*>(&tb.cs[which][j][32 * m + 8 * grp]);
+}
+
 // Eight nibbles n_j (slot j at bit 16 (j & 1) + 4 (j >> 1)) as fp16
 // denormals: a masked nibble pair is the fp16 pair (n * 2^-24, n' * 2^-24),
 // or 16 n * 2^-24 for the pairs at bits 4 and 20 (slots 2, 3, 6, 7; the
@@ -203,14 +258,15 @@ struct PageState {
 // the first sum goes to acc (one MFMA per channel tile), the second to cz
 // (one MFMA per page: B column g holds zero_tg).
 // ROPE (keys held before RoPE): a lane dequantises its A operand itself
-// (n step + zero in fp16, from the parameters in LDS), rotates it at the
-// token's position (page p holds tokens 32 p ..) and multiplies by qsc: the
-// tiles then hold S^T itself, and the zero tile and qss are not used.
+// (n step + zero in fp16, from the parameters in LDS) and rotates it by its
+// row's offset in the page (packed f16 arithmetic), while q takes the
+// page's own rotation: the tiles then hold S^T itself, and the zero tile
+// and qss are not used.
 template <int BITS, bool ROPE>
 __device__ __forceinline__ void page_pair(PageState& st, const PageRaw<BITS>& ra, const PageRaw<BITS>& rb, bool oka,
                                           bool okb, const u32x4 (&qsc)[4], const u32x4 (&qss)[4],
                                           uint32_t* s_par_w, int lane, const h8& slot_scale,
-                                          const KiviParams& k, int pga, int pgb) {
+                                          const KiviParams& k, int pga, int pgb, const RopeTable* s_rope) {
   constexpr int GT = kWaveHeads;
   const int grp = lane >> 4, u = lane & 15;
 
@@ -223,14 +279,40 @@ __device__ __forceinline__ void page_pair(PageState& st, const PageRaw<BITS>& ra
   // ---- q.k (tiles hold 2^-24 S^T; S^T with ROPE) ----
   f4 s[2][2];
   if constexpr (ROPE) {
+    // Token t = t0 + j of page pg (t0 = 32 pg, j = 16 tt + u: this lane's A
+    // row) is rotated by R_t = R_t0 R_j, so q . R_t k = (R_t0^T q) . (R_j k):
+    // the page's rotation goes onto q, once per page, and R_j, the same for
+    // every page, comes from the LDS table (exact for tables of angles
+    // linear in the position, theta_i t, as RoPE's are; the launch requires
+    // tables covering every position).  Coefficients are taken block by
+    // block, so that few are live at a time.
+    const int style = k.rope_style;
 #pragma unroll
     for (int pi = 0; pi < 2; ++pi) {
       const PageRaw<BITS>& r = pi ? rb : ra;
       const uint32_t* par = s_par_w + pi * 256;
-      const int pg = pi ? pgb : pga;
+      const int t0 = 32 * (pi ? pgb : pga);
+      h8 qp[4];
+#pragma unroll
+      for (int m = 0; m < 4; ++m) qp[m] = as_h8(qsc[m]);
+      if (style == 0) {
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          h8 c, sn;
+          rope_coef_block0(k, t0, m, grp, c, sn);
+          rope_one_block<true>(qp[m], c, sn);
+        }
+      } else {
+#pragma unroll
+        for (int m = 0; m < 2; ++m) {
+          h8 c, sa, sb;
+          rope_coef_block1(k, t0, m, grp, c, sa, sb);
+          rope_pair_blocks<true>(qp[m], qp[m + 2], c, sa, c, sb);
+        }
+      }
 #pragma unroll
       for (int tt = 0; tt < 2; ++tt) {
-        const int t = 32 * pg + 16 * tt + u;      // this lane's A row
+        const int j = 16 * tt + u;
         h8 kk[4];                                 // channels 32 m + 8 grp + e
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
@@ -243,40 +325,25 @@ __device__ __forceinline__ void page_pair(PageState& st, const PageRaw<BITS>& ra
           const h8 n = as_h8(biased) - (_Float16)1024.0f;
           kk[m] = n * (slot_scale * as_h8(kp[0])) + as_h8(kp[1]);
         }
-        if (k.rope_style == 0) {
-          // pairs (2i, 2i + 1): elements (2d, 2d + 1) of block m, i = 16 m + 4 grp + d
+        if (style == 0) {
 #pragma unroll
           for (int m = 0; m < 4; ++m) {
-            f4 c, sn;
-            rope_cs4(k, t, 16 * m + 4 * grp, c, sn);
-#pragma unroll
-            for (int d = 0; d < 4; ++d) {
-              float x0 = (float)kk[m][2 * d], x1 = (float)kk[m][2 * d + 1];
-              rope_rotate(x0, x1, c[d], sn[d]);
-              kk[m][2 * d] = (_Float16)x0;
-              kk[m][2 * d + 1] = (_Float16)x1;
-            }
+            rope_one_block<false>(kk[m], rope_lds(*s_rope, 0, j, m, grp), rope_lds(*s_rope, 1, j, m, grp));
           }
         } else {
-          // pairs (i, i + 64): element e of blocks m and m + 2, i = 32 m + 8 grp + e
 #pragma unroll
           for (int m = 0; m < 2; ++m) {
-            f4 c0, s0, c1, s1;
-            rope_cs4(k, t, 32 * m + 8 * grp, c0, s0);
-            rope_cs4(k, t, 32 * m + 8 * grp + 4, c1, s1);
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-              float x0 = (float)kk[m][e], x1 = (float)kk[m + 2][e];
-              rope_rotate(x0, x1, e < 4 ? c0[e & 3] : c1[e & 3], e < 4 ? s0[e & 3] : s1[e & 3]);
-              kk[m][e] = (_Float16)x0;
-              kk[m + 2][e] = (_Float16)x1;
-            }
+            rope_pair_blocks<false>(kk[m], kk[m + 2], rope_lds(*s_rope, 0, j, m, grp), rope_lds(*s_rope, 1, j, m, grp),
+                                    rope_lds(*s_rope, 0, j, m + 2, grp), rope_lds(*s_rope, 1, j, m + 2, grp));
           }
         }
         f4 acc = (f4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int m = 0; m < 4; ++m) acc = mfma(kk[m], as_h8(qsc[m]), acc);
+        for (int m = 0; m < 4; ++m) acc = mfma(kk[m], qp[m], acc);
         s[pi][tt] = acc;
+        // one tile at a time: interleaved, the tiles' operands and
+        // coefficients do not fit the wavefront's registers
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
   } else {
@@ -374,7 +441,8 @@ template <int BITS, bool ROPE>
 __device__ __forceinline__ void kivi_pages_wave(const KiviParams& k, int seq, int kvh, int hs,
                                                 int pg_begin, int pg_end, int pg_step,
                                                 uint32_t* s_par_w, float* s_acc_w, float* s_m_w,
-                                                float* s_l_w, bool share_simd, bool early_ok, int early_id) {
+                                                float* s_l_w, bool share_simd, bool early_ok, int early_id,
+                                                const RopeTable* s_rope) {
   constexpr int GT = kWaveHeads;
   const Params& p = k.base;
   const int lane = threadIdx.x % kWave;
@@ -448,12 +516,12 @@ __device__ __forceinline__ void kivi_pages_wave(const KiviParams& k, int seq, in
       fetch(r1a, r1b, o + 2);
       if (share_simd) __builtin_amdgcn_s_setprio(1);
       page_pair<BITS, ROPE>(st, r0a, r0b, id(o) >= 0, id(o + 1) >= 0, qsc, qss, s_par_w, lane, slot_scale, k,
-                            pg_of(o), pg_of(o + 1));
+                            pg_of(o), pg_of(o + 1), s_rope);
       if (o + 2 >= cn) break;
       fetch(r0a, r0b, o + 4);
       if (share_simd) __builtin_amdgcn_s_setprio(0);
       page_pair<BITS, ROPE>(st, r1a, r1b, id(o + 2) >= 0, id(o + 3) >= 0, qsc, qss, s_par_w, lane, slot_scale, k,
-                            pg_of(o + 2), pg_of(o + 3));
+                            pg_of(o + 2), pg_of(o + 3), s_rope);
     }
   }
 
@@ -730,6 +798,29 @@ __global__ __launch_bounds__(NW * kWave, 2) void kivi_decode_kernel(KiviParams k
   const Params& p = k.base;
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);   // wave-uniform (SGPR)
+  // keys held before RoPE: the rotations of a page's 32 offsets, built
+  // once per workgroup (a few L2 reads per thread, all issued together)
+  const RopeTable* s_rope = nullptr;
+  if constexpr (ROPE) {
+    __shared__ __attribute__((aligned(16))) RopeTable s_rope_tb;
+    constexpr int kN = kRopeRows * kKiviHead / (NW * kWave);
+    static_assert(kRopeRows * kKiviHead % (NW * kWave) == 0, "whole rounds");
+    float cv[kN], sv[kN];
+#pragma unroll
+    for (int r = 0; r < kN; ++r) {
+      const int i = tid + r * NW * kWave, j = i / kKiviHead, c = i % kKiviHead;
+      rope_cs1(k, j, k.rope_style == 0 ? c >> 1 : c & 63, cv[r], sv[r]);
+    }
+#pragma unroll
+    for (int r = 0; r < kN; ++r) {
+      const int i = tid + r * NW * kWave, j = i / kKiviHead, c = i % kKiviHead;
+      const bool first = k.rope_style == 0 ? (c & 1) == 0 : c < 64;
+      s_rope_tb.cs[0][j][c] = __builtin_bit_cast(uint16_t, (_Float16)cv[r]);
+      s_rope_tb.cs[1][j][c] = __builtin_bit_cast(uint16_t, (_Float16)(first ? -sv[r] : sv[r]));
+    }
+    __syncthreads();
+    s_rope = &s_rope_tb;
+  }
   int part;
   int bid = grid_item(p, part);
   const int hs = bid % p.head_slices;      bid /= p.head_slices;
@@ -783,7 +874,7 @@ __global__ __launch_bounds__(NW * kWave, 2) void kivi_decode_kernel(KiviParams k
     // and 58.5 us).
     kivi_pages_wave<BITS, ROPE>(k, seq, kvh, hs, pg0 + wave, pg1 - res_pages, page_waves, &sd.p[wave][0], &sd.acc[wave][0][0],
                     &sd.m[wave][0], &sd.l[wave][0], FINAL && blockIdx.x >= gridDim.x / 2,
-                    FINAL && page_waves == NW - 1, early_id);
+                    FINAL && page_waves == NW - 1, early_id, s_rope);
   } else {
     const int lane = tid % kWave;
     NewestToken nt;
@@ -807,7 +898,7 @@ __global__ __launch_bounds__(NW * kWave, 2) void kivi_decode_kernel(KiviParams k
     // path (the window ends halfway through the launch)
     if constexpr (APPEND) store_newest<BS>(k.job, nt, seq, kvh, lane);
     kivi_pages_wave<BITS, ROPE>(k, seq, kvh, hs, pg1 - res_pages, pg1, 1, &sd.p[wave][0], &sd.acc[NW + 1][0][0],
-                    &sd.m[NW + 1][0], &sd.l[NW + 1][0], false, false, -1);
+                    &sd.m[NW + 1][0], &sd.l[NW + 1][0], false, false, -1, s_rope);
   }
   __syncthreads();
   combine_waves<Kind::F16, Kind::F32, kKiviHead, FINAL>(p, has_res ? NW + 2 : NW, &sd.m[0][0], &sd.l[0][0],
