@@ -341,10 +341,13 @@ __device__ __forceinline__ void page_pair(PageState& st, const PageRaw<BITS>& ra
 #pragma unroll
         for (int m = 0; m < 4; ++m) acc = mfma(kk[m], qp[m], acc);
         s[pi][tt] = acc;
-        // one tile at a time: interleaved, the tiles' operands and
-        // coefficients do not fit the wavefront's registers
-        __builtin_amdgcn_sched_barrier(0);
+        // INT8 pages hold twice the code registers: one tile at a time
+        if constexpr (BITS == 8) __builtin_amdgcn_sched_barrier(0);
       }
+      // one page at a time (INT4, 4-wavefront workgroups at two per SIMD:
+      // 112.5 against 118.5 us per step with one tile at a time; with both
+      // pages interleaved the operands and coefficients spill)
+      __builtin_amdgcn_sched_barrier(0);
     }
   } else {
 #pragma unroll
