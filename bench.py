@@ -280,12 +280,14 @@ def kivi_steps(steps):
     return max(64, (steps + 63) // 64 * 64)
 
 
-def bench_kivi(args, R=128, mixed=False, name=None, bits=4, pre_rope=False):
+def bench_kivi(args, R=128, mixed=False, name=None, bits=4, pre_rope=False, build_ahead=False):
     """KIVI append + decode steps (INT4 pages, or INT8 with bits=8) at batch
     64 from context 4096 (mixed: sequence s starts at 4096 + s mod 32 tokens,
     so two sequences complete a page at every step instead of all 64 on one
     step in 32).  pre_rope: keys held before RoPE, each rotated at its
-    position inside attention (fp32 tables of 8192 positions)."""
+    position inside attention (fp32 tables of 8192 positions).  build_ahead:
+    each page written in eighths by the 8 steps before the one that
+    completes it (the page tables are set up front)."""
     import torch
 
     import tl_attn as tla
@@ -338,11 +340,12 @@ def bench_kivi(args, R=128, mixed=False, name=None, bits=4, pre_rope=False):
                                residual_length=R, gqa_map=tla.GQA_GROUPED, bits=bits)
     ws = torch.empty(max(16, tla.kivi_workspace_bytes(desc0, Lmax)), dtype=torch.uint8, device="cuda")
     for rep in reps:
-        d = tla.make_kivi_desc(q, rep[0], rep[2], rep[3], rep[5], NKV, scale, residual_length=R, bits=bits)
+        d = tla.make_kivi_desc(q, rep[0], rep[2], rep[3], rep[5], NKV, scale, residual_length=R, bits=bits,
+                               build_ahead=build_ahead)
         sl0 = torch.tensor(L0, dtype=torch.int32, device="cuda")
         tla.kivi_build_pages(d, rep[0], rep[1], rep[2], sl0, rep[3], rep[4], max(L0))
     descs = [tla.make_kivi_desc(q, rep[0], rep[2], rep[3], rep[5], NKV, scale, residual_length=R, bits=bits,
-                                pre_rope_keys=pre_rope) for rep in reps]
+                                pre_rope_keys=pre_rope, build_ahead=build_ahead) for rep in reps]
     if pre_rope:
         i = torch.arange(D // 2, dtype=torch.float32)
         theta = torch.arange(8192, dtype=torch.float32)[:, None] / torch.pow(10000.0, 2.0 * i / D)
@@ -363,7 +366,8 @@ def bench_kivi(args, R=128, mixed=False, name=None, bits=4, pre_rope=False):
     nbytes = [kivi_bytes(lens, R, [lq(L) > lq(L - 1) for L in lens], bits) for _, lens in plan[args.warmup:]]
     avg_bytes = sum(nbytes) / len(nbytes)
     return {"ms_per_step": ms, "gbs": avg_bytes / (ms * 1e-3) / 1e9, "tok_s": S / (ms * 1e-3),
-            "bytes_per_step": avg_bytes, "residual_length": R, "group": 32, "steps": n_timed}
+            "bytes_per_step": avg_bytes, "residual_length": R, "group": 32, "steps": n_timed,
+            "build_ahead": int(bool(build_ahead))}
 
 
 F8_S, F8_CTX = 16, 32768
@@ -841,6 +845,10 @@ def main():
     if want("kivi"):
         kv = bench_kivi(args, name="kivi")
     kvm = bench_kivi(args, mixed=True, name="kivi_mixed") if want("kivi") else None
+    # the same two workloads with each page written in eighths over the 8
+    # steps before the one that completes it (tl_kivi_desc.build_ahead)
+    kva = bench_kivi(args, name="kivi_build_ahead", build_ahead=True) if want("kivi") else None
+    kvma = bench_kivi(args, mixed=True, name="kivi_mixed_build_ahead", build_ahead=True) if want("kivi") else None
     kv8 = bench_kivi(args, name="kivi_int8", bits=8) if want("kivi") else None
     kvr = bench_kivi(args, name="kivi_pre_rope", pre_rope=True) if want("kivi") else None
     # the reference's default KiviConfig (config_schema.h:124,128): bits 8,
@@ -951,6 +959,12 @@ def main():
             "pct_hbm_peak": round(100 * kvm["gbs"] / HBM_PEAK_GBS, 2), "bytes_per_step": int(kvm["bytes_per_step"])}
         if fp is not None:
             res["kivi_int4_mixed_lengths"]["speedup_vs_fp16_tok_s"] = round(kvm["tok_s"] / fp["tok_s"], 3)
+    for key, r_ in (("kivi_int4", kva), ("kivi_int4_mixed_lengths", kvma)):
+        if r_ is not None and key in res:
+            res[key]["build_ahead"] = {"ms_per_step": round(r_["ms_per_step"], 5), "tok_s": round(r_["tok_s"], 1),
+                                       "gbs": round(r_["gbs"], 2)}
+            if fp is not None:
+                res[key]["build_ahead"]["speedup_vs_fp16_tok_s"] = round(r_["tok_s"] / fp["tok_s"], 3)
     if kv8 is not None:
         res["kivi_int8"] = {
             "workload": "as kivi_int4 with INT8 pages (9216 B per 32 tokens per kv head)",

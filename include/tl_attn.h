@@ -28,8 +28,10 @@ extern "C" {
 #endif
 
 /* Version of this C ABI (tl_abi_version).  2: tl_kivi_desc gained
- * pre_rope_keys (after bits), for the _pre_rope entry points. */
-#define TL_ABI_VERSION 3
+ * pre_rope_keys (after bits), for the _pre_rope entry points.  3:
+ * tl_prefill_desc gained kv_dtype, k_scale, v_scale.  4: tl_kivi_desc
+ * gained build_ahead (after pre_rope_keys). */
+#define TL_ABI_VERSION 4
 
 /* Mirrors truellm::ErrorCode (include/truellm/types.h:20-32). */
 typedef enum tl_status {
@@ -404,6 +406,17 @@ typedef struct tl_kivi_desc {
                                   stored and quantised as attention scores them; 1 = keys are held
                                   before RoPE and rotated at their positions inside attention (the
                                   _pre_rope entry points, which take the tables) */
+  int32_t build_ahead;         /* 0: a step (tl_kivi_decode_step*, tl_kivi_append) whose length
+                                  completes a page quantises the whole page.  1 (used when
+                                  residual_length > 8): each of the 8 steps before that one
+                                  writes an eighth of it (K channels of 4 octets, or V tokens of
+                                  one lane group), so no step quantises a whole page, and
+                                  tl_kivi_build_pages also builds the next page once its first
+                                  eighth is due.  The bytes are the same.  Contract: the page
+                                  table entry of a sequence's next page is set from the first
+                                  of those calls on (a page allocated later than that stays
+                                  incomplete), and every call that appends to the sequence
+                                  uses the same setting. */
 } tl_kivi_desc;
 
 /* Page bytes per kv head for a code width: 5120 (INT4, also bits 0) or 9216

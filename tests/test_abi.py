@@ -16,7 +16,7 @@ def test_exports_every_declared_function():
 
 
 def test_abi_version():
-    assert tla.lib.tl_abi_version() == 3 == tla.ABI_VERSION
+    assert tla.lib.tl_abi_version() == 4 == tla.ABI_VERSION
 
 
 def _desc(**kw):
@@ -316,6 +316,12 @@ def test_kivi_decode_descriptor_checks_and_planning():
     assert call(_kdesc(bits=5)) == tla.ERR_NOT_IMPLEMENTED
     assert call(_kdesc(bits=2)) == tla.ERR_NOT_IMPLEMENTED
     assert tla.kivi_workspace_bytes(_kdesc(num_seqs=4, bits=8), 4096) == 4 * 32 * 16 * (128 * 4 + 8)
+    # build_ahead: 0 or 1 (with any residual length: below 9 it builds on completion)
+    for ba in (2, -1):
+        assert call(_kdesc(build_ahead=ba)) == tla.ERR_INVALID_ARGUMENT
+    for ba, R in ((1, 128), (1, 4), (0, 128)):
+        assert call(_kdesc(num_seqs=4, build_ahead=ba, residual_length=R)) == tla.ERR_INVALID_ARGUMENT  # workspace
+    assert ctypes.sizeof(tla.KiviDesc) == 16 * 4
 
 
 def test_kivi_page_bytes():

@@ -859,3 +859,176 @@ def test_kivi_block_sizes_step_and_decode_against_oracle(BS):
             print(f"case kivi bs={BS} bits={bits} decode pp={pp}", flush=True)
             assert_close(_run_decode(kc, want_pages, pp), _kivi_ref(kc, want_pages), orc.F16, ATOL_KIVI,
                          f"bs={BS} bits={bits} pp={pp}")
+
+
+# ---------------------------------------------------------------------------
+# build-ahead: pages written in eighths over the steps before they complete
+# ---------------------------------------------------------------------------
+
+# (L0 - R) mod 32 of the starting lengths: the next page's first eighth due
+# one step ago (31, 24: the prefix build writes the page whole), at the first
+# step (23), in mid window (27: five eighths due), later (16, 0)
+_AHEAD_PHASES = [31, 24, 23, 27, 16, 0]
+
+
+def _signed_zero_page(kc, s, L0):
+    """Sequence s's next page to be quantised: every present token gets
+    zeros of random sign in K channels 0-7 (octet 0) and V channels 32-63
+    (group 1), so that each of those groups' min and max is a tie whose sign
+    only the sequential scan order fixes."""
+    P = orc.kivi_quantized_len(int(L0), kc.R) // 32
+    rng = np.random.default_rng(1000 + s)
+    for t in range(32 * P, min(32 * P + 32, int(L0))):
+        blk = kc.tables[s, t // kc.BS]
+        if blk < 0:
+            continue
+        for h in range(kc.n_kv):
+            kc.k[blk, h, 0:8, t % kc.BS] = rng.choice([0x0000, 0x8000], 8)
+            kc.v[blk, h, 32:64, t % kc.BS] = rng.choice([0x0000, 0x8000], 32)
+
+
+@pytest.mark.parametrize("mode,bits,BS,R", [
+    ("step", 4, 16, 128), ("step", 8, 16, 128), ("step", 4, 8, 9), ("step", 8, 64, 40), ("step", 4, 256, 128),
+    ("append", 4, 16, 128), ("append", 8, 32, 9), ("alternate", 4, 16, 40), ("step", 4, 16, 8),
+])
+def test_build_ahead_pages_bit_exact_at_every_step(mode, bits, BS, R):
+    """desc.build_ahead = 1 against the oracle, which quantises each page
+    whole when the length completes it.  The starting lengths put every
+    sequence at a different phase of its next page's eighths (the prefix
+    build writes that page whole when its first eighth is already due); then
+    40 appends through the fused step ('step'), through tl_kivi_append and
+    the decode ('append'), or the two in turn ('alternate').  After every
+    step the pages of every sequence are the oracle's bit for bit and the
+    output matches the oracle.  With R = 8 the setting builds on completion.
+    Signed zeros fill some groups of each sequence's next page; a window
+    block of sequence 2 is a hole."""
+    steps = 40
+    start = np.array([R + 32 * k + o for k, o in zip([4, 2, 7, 0, 3, 1], _AHEAD_PHASES)], np.int32)
+    kc = KiviCase(90 + BS + R + bits, start + steps, H=32, extra_blocks=1, bits=bits, BS=BS, R=R)
+    for s, L0 in enumerate(start):
+        _signed_zero_page(kc, s, L0)
+    hole_lb = (int(start[2]) + 5) // BS
+    kc.tables[2, hole_lb] = -1
+    qd, kd, vd = dev(kc.q, orc.F16), dev(kc.k, orc.F16), dev(kc.v, orc.F16)
+    btd, ptd = dev(kc.tables), dev(kc.page_tables)
+    pages = torch.zeros(kc.num_pages, kc.n_kv, kc.page_bytes, dtype=torch.uint8, device="cuda")
+    desc = tla.make_kivi_desc(qd, kd, btd, ptd, kc.num_pages, kc.n_kv, kc.scale, residual_length=R,
+                              bits=bits, build_ahead=True)
+    assert desc.build_ahead == 1 and desc.block_size == BS
+    print(f"case build-ahead {mode} bits={bits} bs={BS} R={R}", flush=True)
+    tla.kivi_build_pages(desc, kd, vd, btd, dev(start), ptd, pages, int(start.max()))
+    rng = np.random.default_rng(BS * 7 + R + bits)
+    max_ctx = int(start.max()) + steps
+    ws = torch.empty(max(16, tla.kivi_workspace_bytes(desc, max_ctx)), dtype=torch.uint8, device="cuda")
+    lens = start.copy()
+    k_host, v_host = kc.k.copy(), kc.v.copy()
+    for step in range(steps):
+        lens = lens + 1
+        pos = lens - 1
+        ent = kc.tables[np.arange(kc.S), pos // BS]
+        slots = np.where(ent >= 0, ent * BS + pos % BS, -1).astype(np.int32)
+        knew = inputs.encode(rng.standard_normal((kc.S, kc.n_kv, 128), dtype=np.float32), orc.F16)
+        vnew = inputs.encode(rng.standard_normal((kc.S, kc.n_kv, 128), dtype=np.float32), orc.F16)
+        out = torch.full_like(qd, float("nan"))
+        fused = mode == "step" or (mode == "alternate" and step % 2 == 0)
+        if fused:
+            tla.kivi_decode_step(desc, out, qd, dev(knew, orc.F16), dev(vnew, orc.F16), dev(slots), pages, ptd,
+                                 kd, vd, btd, dev(lens), max_ctx, ws)
+        else:
+            tla.kivi_append(desc, dev(knew, orc.F16), dev(vnew, orc.F16), kd, vd, dev(slots), btd, dev(lens),
+                            ptd, pages)
+            tla.kivi_paged_attention_decode(desc, out, qd, pages, ptd, kd, vd, btd, dev(lens), max_ctx, ws)
+        torch.cuda.synchronize()
+        orc.reshape_and_cache(knew, vnew, k_host, v_host, slots)
+        kc.k, kc.v, kc.lens = k_host, v_host, lens
+        want_pages = kc.oracle_pages()
+        used = [p for p in _used_pages(kc, lens) if p >= 0]
+        assert np.array_equal(pages.cpu().numpy()[used], want_pages[used]), f"pages after step {step}"
+        assert_close(out, _kivi_ref(kc, want_pages), orc.F16, ATOL_KIVI, f"{mode} step {step}")
+    assert np.array_equal(host_bits(kd), k_host) and np.array_equal(host_bits(vd), v_host)
+
+
+@pytest.mark.parametrize("style,bits", [(tla.ROPE_HALVES, 4), (tla.ROPE_ADJACENT, 8)])
+def test_build_ahead_pre_rope_step(style, bits):
+    """build_ahead with the keys held before RoPE (tl_kivi_decode_step_pre_rope):
+    the pages hold unrotated keys, bit for bit the oracle's at every step."""
+    from test_oracle import rope_tables
+    steps, R = 36, 128
+    start = np.array([R + 32 * k + o for k, o in zip([4, 2, 7, 0, 3, 1], _AHEAD_PHASES)], np.int32)
+    kc = KiviCase(77 + bits, start + steps, H=32, extra_blocks=1, bits=bits, R=R)
+    cos_t, sin_t = rope_tables(1040, 128)
+    qd, kd, vd = dev(kc.q, orc.F16), dev(kc.k, orc.F16), dev(kc.v, orc.F16)
+    btd, ptd = dev(kc.tables), dev(kc.page_tables)
+    pages = torch.zeros(kc.num_pages, kc.n_kv, kc.page_bytes, dtype=torch.uint8, device="cuda")
+    desc = tla.make_kivi_desc(qd, kd, btd, ptd, kc.num_pages, kc.n_kv, kc.scale, residual_length=R,
+                              bits=bits, pre_rope_keys=True, build_ahead=True)
+    print(f"case build-ahead pre-rope style={style} bits={bits}", flush=True)
+    tla.kivi_build_pages(desc, kd, vd, btd, dev(start), ptd, pages, int(start.max()))
+    rng = np.random.default_rng(33 + bits)
+    max_ctx = int(start.max()) + steps
+    ws = torch.empty(max(16, tla.kivi_workspace_bytes(desc, max_ctx)), dtype=torch.uint8, device="cuda")
+    cos_d, sin_d = dev(cos_t), dev(sin_t)
+    lens = start.copy()
+    k_host, v_host = kc.k.copy(), kc.v.copy()
+    for step in range(steps):
+        lens = lens + 1
+        pos = (lens - 1).astype(np.int32)
+        slots = (kc.tables[np.arange(kc.S), pos // 16] * 16 + pos % 16).astype(np.int32)
+        knew = inputs.encode(rng.standard_normal((kc.S, kc.n_kv, 128), dtype=np.float32), orc.F16)
+        vnew = inputs.encode(rng.standard_normal((kc.S, kc.n_kv, 128), dtype=np.float32), orc.F16)
+        out = torch.full_like(qd, float("nan"))
+        tla.kivi_decode_step_pre_rope(desc, out, qd, dev(knew, orc.F16), dev(vnew, orc.F16), dev(slots), pages,
+                                      ptd, kd, vd, btd, dev(lens), max_ctx, cos_d, sin_d, style, ws)
+        torch.cuda.synchronize()
+        orc.reshape_and_cache(knew, vnew, k_host, v_host, slots)
+        kc.k, kc.v, kc.lens = k_host, v_host, lens
+        want_pages = kc.oracle_pages()
+        used = [p for p in _used_pages(kc, lens) if p >= 0]
+        assert np.array_equal(pages.cpu().numpy()[used], want_pages[used]), f"pages after step {step}"
+        want = orc.kivi_paged_attention(kc.q, orc.F16, want_pages, kc.page_tables, kc.k, kc.v, kc.tables, kc.lens,
+                                        kc.n_kv, kc.R, kc.scale, orc.GROUPED, bits, pre_rope=(cos_t, sin_t, style))
+        assert_close(out, want, orc.F16, ATOL_KIVI, f"step {step}")
+
+
+def test_build_ahead_full_batch_mixed_lengths():
+    """The benchmark's mixed-length workload (batch 64, sequence s at
+    4096 + s mod 32 tokens, R = 128) with build_ahead, over 40 fused steps:
+    at each step a quarter of the sequences write an eighth of a page and
+    two complete one.  Pages of every sequence bit for bit at the end;
+    outputs of 16 sequences against the oracle at the last step."""
+    steps = 40
+    start = np.array([4096 + s % 32 for s in range(64)], np.int32)
+    kc = KiviCase(82, start + steps, H=32, extra_blocks=1)
+    qd, kd, vd = dev(kc.q, orc.F16), dev(kc.k, orc.F16), dev(kc.v, orc.F16)
+    btd, ptd = dev(kc.tables), dev(kc.page_tables)
+    pages = torch.zeros(kc.num_pages, kc.n_kv, kc.page_bytes, dtype=torch.uint8, device="cuda")
+    desc = tla.make_kivi_desc(qd, kd, btd, ptd, kc.num_pages, kc.n_kv, kc.scale, residual_length=kc.R,
+                              build_ahead=True)
+    tla.kivi_build_pages(desc, kd, vd, btd, dev(start), ptd, pages, int(start.max()))
+    rng = np.random.default_rng(16)
+    max_ctx = int(start.max()) + steps
+    ws = torch.empty(max(16, tla.kivi_workspace_bytes(desc, max_ctx)), dtype=torch.uint8, device="cuda")
+    lens = start.copy()
+    print("case build-ahead full batch, mixed lengths", flush=True)
+    for step in range(steps):
+        lens = lens + 1
+        pos = lens - 1
+        slots = (kc.tables[np.arange(kc.S), pos // 16] * 16 + pos % 16).astype(np.int32)
+        knew = inputs.encode(rng.standard_normal((kc.S, kc.n_kv, 128), dtype=np.float32), orc.F16)
+        vnew = inputs.encode(rng.standard_normal((kc.S, kc.n_kv, 128), dtype=np.float32), orc.F16)
+        out = torch.full_like(qd, float("nan"))
+        tla.kivi_decode_step(desc, out, qd, dev(knew, orc.F16), dev(vnew, orc.F16), dev(slots), pages, ptd, kd, vd,
+                             btd, dev(lens), max_ctx, ws)
+        orc.reshape_and_cache(knew, vnew, kc.k, kc.v, slots)
+    torch.cuda.synchronize()
+    kc.lens = lens
+    want_pages = kc.oracle_pages()
+    used = [p for p in _used_pages(kc, lens) if p >= 0]
+    assert np.array_equal(pages.cpu().numpy()[used], want_pages[used])
+    assert np.array_equal(host_bits(kd), kc.k) and np.array_equal(host_bits(vd), kc.v)
+    sub = np.array([0, 1, 5, 9, 15, 16, 22, 23, 24, 31, 40, 47, 50, 55, 56, 63])
+    want = orc.kivi_paged_attention(np.ascontiguousarray(kc.q[sub]), orc.F16, want_pages,
+                                    np.ascontiguousarray(kc.page_tables[sub]), kc.k, kc.v,
+                                    np.ascontiguousarray(kc.tables[sub]), np.ascontiguousarray(lens[sub]),
+                                    kc.n_kv, kc.R, kc.scale, orc.GROUPED, kc.bits)
+    assert_close(out[torch.from_numpy(sub).cuda()], want, orc.F16, ATOL_KIVI, "full batch")

@@ -692,6 +692,8 @@ static int check_kivi(const tl_kivi_desc* d) {
     return fail(TL_ERR_NOT_IMPLEMENTED, "paged KIVI bits=%d (built: 4, 8)", d->bits);
   if (d->pre_rope_keys != 0 && d->pre_rope_keys != 1)
     return fail(TL_ERR_INVALID_ARGUMENT, "pre_rope_keys=%d", d->pre_rope_keys);
+  if (d->build_ahead != 0 && d->build_ahead != 1)
+    return fail(TL_ERR_INVALID_ARGUMENT, "build_ahead=%d", d->build_ahead);
   return TL_OK;
 }
 
@@ -746,6 +748,7 @@ static tl::KiviPageLaunch page_launch(const tl_kivi_desc* d, const void* k_cache
   a.max_pages_per_seq = d->max_pages_per_seq; a.num_pages = d->num_pages;
   a.residual_length = d->residual_length;
   a.bits = kivi_bits(d);
+  a.build_ahead = d->build_ahead && d->residual_length >= tl::kKiviAheadMinResidual;
   a.stream = (hipStream_t)stream;
   return a;
 }
@@ -763,6 +766,7 @@ int tl_kivi_build_pages(const tl_kivi_desc* desc, const void* k_cache, const voi
   if (!aligned16(pages)) return fail(TL_ERR_INVALID_ARGUMENT, "pages must be 16-byte aligned");
   tl::KiviPageLaunch a = page_launch(desc, k_cache, v_cache, block_tables, seq_lens, page_tables, pages, stream);
   a.max_pages_to_build = tl::kivi_quantized_len(max_context_len, desc->residual_length) / tl::kKiviPageTokens;
+  a.max_pages_to_build += a.build_ahead;   // the next page, once its first piece is due
   if (a.max_pages_to_build > desc->max_pages_per_seq) a.max_pages_to_build = desc->max_pages_per_seq;
   if (tl::launch_kivi_pages(a)) return fail(TL_ERR_BACKEND, "KIVI page launch failed");
   return ok();

@@ -147,6 +147,7 @@ struct KiviPageLaunch {
   int bits;                     // page code width: 4 or 8
   int max_pages_to_build;       // prefix build: page slots per sequence in the grid
   int append;                   // 1: write the new token, then build the page L completes
+  int build_ahead;              // 1: pages built in pieces over the steps before they complete
   const void* knew;             // append: new token per sequence [S, n_kv, 128] fp16
   const void* vnew;
   const int32_t* slots;         // append: its slot in the fp16 pool

@@ -60,6 +60,11 @@ constexpr int kKiviVParamOff = 4608;
 constexpr int kKiviMaxHeadDim = 128;   // KIVI_MAX_HEAD_DIM, kivi_cache.cuh:27
 constexpr int kKiviMaxOutliers = 64;   // KIVI_MAX_OUTLIERS, kivi_cache.cuh:28
 constexpr int kKiviMaxWgPages = 1024;  // pages one decode workgroup takes (ids staged in LDS)
+// Build-ahead: a page is written in kKiviPieces pieces by the steps before
+// the one that quantises it; with R > kKiviPieces the newest token of those
+// steps lies past the page.
+constexpr int kKiviPieces = 8;
+constexpr int kKiviAheadMinResidual = kKiviPieces + 1;
 
 // Tokens of a sequence of length L held in pages: whole pages of the prefix
 // that leaves at least residual_length tokens in the fp16 pool.

@@ -139,13 +139,24 @@ __global__ __launch_bounds__(128) void kivi_page_kernel(PageJob j) {
   const int L = j.seq_lens[seq];
   const int lq = kivi_quantized_len(L, j.residual_length);
   int page;
+  int ahead_page;
+  const int piece = j.build_ahead ? kivi_ahead_piece(L, j.residual_length, ahead_page) : -1;
   if (j.append) {
     kivi_append_token<128>(j, seq, kvh, tid);
+    if (j.build_ahead) {
+      // the pages this append completes were written in pieces by the
+      // appends before it; this one writes its piece of the next page
+      if (piece >= 0 && tid < kWave)
+        kivi_build_piece<BITS>(j, seq, kvh, ahead_page, piece, tid, &sm.qk[0][0]);
+      return;
+    }
     if (lq == 0 || lq == kivi_quantized_len(L - 1, j.residual_length)) return;
     page = lq / kKiviPageTokens - 1;
   } else {
     page = pg;
-    if (page >= lq / kKiviPageTokens) return;
+    // build-ahead: the next page too once its first piece is due (every
+    // piece written so far and the rest ahead of time: the same bytes)
+    if (page >= lq / kKiviPageTokens && !(piece >= 0 && page == ahead_page)) return;
   }
   kivi_build_page<128, BITS>(sm, j, seq, kvh, page, L, tid);
 }

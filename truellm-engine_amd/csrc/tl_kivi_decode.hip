@@ -765,6 +765,7 @@ __device__ __forceinline__ void store_newest(const PageJob& j, const NewestToken
 template <int NW>
 struct KiviDecodeSmem {
   uint32_t p[NW][512];                       // per wave: weights or page params
+  int piece_pid;                             // build-ahead: the piece's page slot, or -1
   float m[NW + 2][kWaveHeads], l[NW + 2][kWaveHeads];
   float acc[NW + 2][kWaveHeads][kKiviHead];
 };
@@ -790,6 +791,10 @@ struct KiviDecodeSmem {
 // halve the occupancy.
 // BS: the fp16 pool's block size, 16, or 0 for any other (read from the
 // launch at run time).
+// Pages the residual wavefront leaves to the page wavefronts in a step in
+// which it writes a build-ahead piece.
+constexpr int kPieceResPages = 0;
+
 template <int NW, bool FINAL, bool APPEND, int BITS, bool ROPE, int BS>
 __global__ __launch_bounds__(NW * kWave, 2) void kivi_decode_kernel(KiviParams k) {
   using Smem = KiviDecodeSmem<NW>;
@@ -852,7 +857,10 @@ __global__ __launch_bounds__(NW * kWave, 2) void kivi_decode_kernel(KiviParams k
   // wavefronts end their pages (batch 64, ctx 4096), so it also runs the
   // range's last pages, 1/30 of them: 4 of 124 at ctx 4096 gave 63.9 us
   // per step against 64.5 us (2 pages: 64.7, 3: 64.1, 6: 64.9).
-  const int res_pages = has_res ? (pg1 - pg0) / 30 : 0;
+  int ahead_page = 0;
+  const int ahead = APPEND ? kivi_ahead_piece(L, k.residual_length, ahead_page) : -1;
+  const bool piece_due = APPEND && k.job.build_ahead && hs == 0 && has_res && ahead >= 0;
+  const int res_pages = has_res ? max(0, (pg1 - pg0) / 30 - (piece_due ? kPieceResPages : 0)) : 0;
 
   // The page that L completes, if any (APPEND), by the whole workgroup
   // before the page wavefronts start.  (Built by the residual wavefront
@@ -860,7 +868,8 @@ __global__ __launch_bounds__(NW * kWave, 2) void kivi_decode_kernel(KiviParams k
   // on average: one wavefront takes far longer over the build and then
   // ends after the page wavefronts.)
   if constexpr (APPEND) {
-    if (last && lq > 0 && lq != kivi_quantized_len(L - 1, k.residual_length)) {
+    // (with build-ahead the steps before this one wrote the page in pieces)
+    if (!k.job.build_ahead && last && lq > 0 && lq != kivi_quantized_len(L - 1, k.residual_length)) {
       kivi_build_page<NW * kWave, BITS>(*reinterpret_cast<Build*>(s_raw), k.job, seq, kvh,
                                   lq / kKiviPageTokens - 1, L, tid);
       __syncthreads();   // the page is visible to the workgroup; the LDS is free again
@@ -880,6 +889,14 @@ __global__ __launch_bounds__(NW * kWave, 2) void kivi_decode_kernel(KiviParams k
                     FINAL && page_waves == NW - 1, early_id, s_rope);
   } else {
     const int lane = tid % kWave;
+    // build-ahead: this step's piece of the next page (one head slice
+    // writes it).  Its table entries are read here, its fp16 after the
+    // window, and it is quantised and written after the wavefront's last
+    // loads, which its stores would otherwise hold up.
+    KiviPiece piece;
+    piece.piece = -1;
+    if constexpr (APPEND)
+      if (piece_due) piece = kivi_piece_plan(k.job, seq, ahead_page, ahead, lane);
     NewestToken nt;
     if constexpr (APPEND)
       nt = k.job.slots[seq] >= 0 ? newest_from_row(k.job, seq, kvh, lane)
@@ -900,12 +917,36 @@ __global__ __launch_bounds__(NW * kWave, 2) void kivi_decode_kernel(KiviParams k
     // the token's store, at the end of the window, off the page wavefronts'
     // path (the window ends halfway through the launch)
     if constexpr (APPEND) store_newest<BS>(k.job, nt, seq, kvh, lane);
+    if constexpr (APPEND) kivi_piece_load(k.job, piece, kvh, ahead_page, lane);
     kivi_pages_wave<BITS, ROPE>(k, seq, kvh, hs, pg1 - res_pages, pg1, 1, &sd.p[wave][0], &sd.acc[NW + 1][0][0],
                     &sd.m[NW + 1][0], &sd.l[NW + 1][0], false, false, -1, s_rope);
+    // the piece's fp16 for the quarters after the merge
+    if constexpr (APPEND) {
+      if (piece_due) {
+        kivi_piece_stage(piece, lane, reinterpret_cast<uint16_t*>(&sd.p[wave][0]));
+        if (lane == 0) sd.piece_pid = piece.piece >= 0 ? piece.pid : -1;
+      }
+    }
   }
   __syncthreads();
+  // build-ahead: wavefront q quantises quarter q of the piece, last, after
+  // every load; its staged values are read before the merge
+  static_assert(!APPEND || NW == 4, "a quarter of the piece per wavefront");
+  uint2 qv = {0u, 0u};
+  int piece_pid = -1;
+  if constexpr (APPEND) {
+    if (piece_due) {
+      piece_pid = sd.piece_pid;
+      qv = kivi_piece_quarter_values(ahead, wave, tid % kWave, reinterpret_cast<const uint16_t*>(&sd.p[NW - 1][0]));
+    }
+  }
   combine_waves<Kind::F16, Kind::F32, kKiviHead, FINAL>(p, has_res ? NW + 2 : NW, &sd.m[0][0], &sd.l[0][0],
                                                         &sd.acc[0][0][0], seq, kvh, hs, part, tid, NW * kWave);
+  if constexpr (APPEND) {
+    if (piece_pid >= 0)
+      kivi_piece_quarter<BITS>(k.job, piece_pid, ahead, kvh, wave, tid % kWave, qv,
+                               reinterpret_cast<uint8_t*>(&sd.p[0][0]) + 256 * wave);
+  }
 }
 
 template <int NW, bool FINAL, int BITS, bool ROPE, int BS>

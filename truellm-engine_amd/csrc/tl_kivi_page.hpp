@@ -66,6 +66,7 @@ struct PageJob {
   int pages_per_seq_grid;   // grid stride over page index (prefix build)
   int append;               // 1: write the new token, then the page that L completes, if any
   int bits;                 // code width of the pages: 4 or 8
+  int build_ahead;          // 1: the steps build the next page in pieces (residual_length > 8)
   const uint16_t* knew;     // append: new token per sequence [S, n_kv, 128]
   const uint16_t* vnew;
   const int32_t* slots;     // append: its slot in the fp16 pool
@@ -83,6 +84,7 @@ inline PageJob make_page_job(const KiviPageLaunch& a) {
   j.residual_length = a.residual_length;
   j.append = a.append;
   j.bits = a.bits;
+  j.build_ahead = a.build_ahead;
   j.knew = (const uint16_t*)a.knew; j.vnew = (const uint16_t*)a.vnew; j.slots = a.slots;
   j.pages_per_seq_grid = a.append ? 1 : (a.max_pages_to_build > 0 ? a.max_pages_to_build : 1);
   return j;
@@ -313,6 +315,388 @@ __device__ void kivi_build_page(KiviBuildSmem<BITS>& sm, const PageJob& j, int s
   uint8_t* dst = j.pages + ((int64_t)pid * j.num_kv_heads + kvh) * F::kBytes;
   for (int i = tid; i < F::kBytes / 16; i += NT)
     reinterpret_cast<u32x4*>(dst)[i] = reinterpret_cast<const u32x4*>(sm.page)[i];
+}
+
+// ---- build ahead: a page in pieces over the steps before it completes ----
+//
+// Page p of a sequence is quantised at the step whose length reaches
+// 32 (p + 1) + R; its 32 tokens are all in the fp16 pool R steps earlier.
+// With build-ahead the kKiviPieces steps before that one each write one
+// piece of it, so that no step builds a whole page:
+//   * piece i < 4: K channels of octets i, i + 4, i + 8, i + 12 (their codes
+//     are the chunks 64 tt + 16 i + u, two runs of 16 chunks, and their
+//     (step, zero) rows);
+//   * piece 4 + r: V tokens of lane group r (4 r .. 4 r + 3 and
+//     16 + 4 r .. 16 + 4 r + 3: chunks 64 hh + 16 r + u, and the (step,
+//     zero) rows of (g, r)).
+// A piece holds exactly the bytes that kivi_build_page writes there: each
+// group's min / max is the sequential scan's (first occurrence on ties,
+// NaN skipped), combined in scan order, and the quantiser is the same.
+// Piece to build at length L, or -1: the next page to be quantised, d steps
+// before the step that quantises it, builds piece kKiviPieces - d.
+__device__ __forceinline__ int kivi_ahead_piece(int L, int residual_length, int& page) {
+  page = kivi_quantized_len(L, residual_length) / kKiviPageTokens;
+  const int d = kKiviPageTokens * (page + 1) + residual_length - L;
+  return (d >= 1 && d <= kKiviPieces) ? kKiviPieces - d : -1;
+}
+
+// The sequential scans' combination of two partial scans, lo over earlier
+// elements than hi: the earlier value wins ties (x < gmin / x > gmax).
+__device__ __forceinline__ void scan_combine(float& mn, float& mx, float mn_hi, float mx_hi) {
+  mn = mn_hi < mn ? mn_hi : mn;
+  mx = mx_hi > mx ? mx_hi : mx;
+}
+// The value of lane lane ^ M: row permutations (no LDS round trip) up to
+// M = 8 (4: the quad reversal of the half-row mirror, 8: the half-row
+// mirror of the row mirror), an LDS-unit shuffle beyond.
+constexpr int kDppQuadReverse = 0x1B;  // quad_perm [3,2,1,0]
+template <int M>
+__device__ __forceinline__ float lane_xor(float v) {
+  if constexpr (M == 1) return dpp<kDppXor1>(v);
+  else if constexpr (M == 2) return dpp<kDppXor2>(v);
+  else if constexpr (M == 4) return dpp<kDppQuadReverse>(dpp<kDppHalfMirror>(v));
+  else if constexpr (M == 8) return dpp<kDppHalfMirror>(dpp<kDppMirror>(v));
+  else return shfl_xor(v, M);
+}
+template <int M>
+__device__ __forceinline__ uint32_t lane_xor_u(uint32_t v) {
+  return __builtin_bit_cast(uint32_t, lane_xor<M>(__builtin_bit_cast(float, v)));
+}
+
+// The same over lanes: xor butterfly over masks FIRST, 2 FIRST, .., LAST,
+// the lane of lower index holding the earlier elements.
+template <int FIRST, int LAST>
+__device__ __forceinline__ void scan_combine_lanes(float& mn, float& mx, int lane) {
+  if constexpr (FIRST <= LAST) {
+    const float omn = lane_xor<FIRST>(mn), omx = lane_xor<FIRST>(mx);
+    if (lane & FIRST) {
+      float a = omn, b = omx;
+      scan_combine(a, b, mn, mx);
+      mn = a;
+      mx = b;
+    } else {
+      scan_combine(mn, mx, omn, omx);
+    }
+    scan_combine_lanes<FIRST * 2, LAST>(mn, mx, lane);
+  }
+}
+
+// A piece in three phases, so that a wavefront can spread it over other
+// work: plan (the page slot and the pool blocks: table reads), load (the
+// 2 KiB of fp16 it quantises), finish (quantise, then write).  Stores count
+// on the same in-order counter as loads, so a wavefront that still has
+// loads to wait for writes its piece after them.
+// K piece: lane = channel cl = lane / 2 of the piece (octet piece + 4 m,
+// m = cl / 8, channel ci = cl % 8 of it) over tokens 16 th .. 16 th + 15
+// (th = lane % 2), two runs of 8, each inside one block.  V piece: lane =
+// channels lane and lane + 64 (index lane % 32 of groups lane / 32 and
+// 2 + lane / 32) over the 8 token slots of lane group r, two runs of 4.
+struct KiviPiece {
+  int piece;        // -1: nothing to write
+  int pid;          // page table entry (checked by the load phase)
+  int phys[2];      // table entries of the blocks of the lane's two runs (checked by the load phase)
+  uint32_t w[8];    // K: two runs of 8 halves; V: [channel half][run] 4 halves
+};
+
+__device__ __forceinline__ KiviPiece kivi_piece_plan(const PageJob& j, int seq, int page, int piece, int lane) {
+  // the entries are only read here (the checks that use them come in the
+  // load phase), so that nothing waits for them yet
+  KiviPiece pc;
+  pc.piece = (piece < 0 || page >= j.max_pages_per_seq) ? -1 : piece;
+  if (pc.piece < 0) return pc;
+  pc.pid = j.page_tables[(int64_t)seq * j.max_pages_per_seq + page];
+  const int32_t* btab = j.block_tables + (int64_t)seq * j.max_blocks_per_seq;
+  const int t_page = page * kKiviPageTokens;
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const int tok = piece < 4 ? t_page + 16 * (lane & 1) + 8 * r : t_page + 16 * r + 4 * (piece - 4);
+    const int lb = min(tok / j.block_size, j.max_blocks_per_seq - 1);
+    pc.phys[r] = tok / j.block_size < j.max_blocks_per_seq ? btab[lb] : -1;
+  }
+  return pc;
+}
+
+__device__ __forceinline__ void kivi_piece_load(const PageJob& j, KiviPiece& pc, int kvh, int page, int lane) {
+  if (pc.piece < 0) return;
+  if (pc.pid < 0 || pc.pid >= j.num_pages) {
+    pc.piece = -1;                      // a page table hole: nothing to write
+    return;
+  }
+#pragma unroll
+  for (int r = 0; r < 2; ++r)
+    if (pc.phys[r] < 0 || pc.phys[r] >= j.num_blocks) pc.phys[r] = -1;
+  const int t_page = page * kKiviPageTokens;
+  auto off_of = [&](int phys, int c, int tok) {
+    return (((int64_t)phys * j.num_kv_heads + kvh) * kKiviHead + c) * j.block_size + tok % j.block_size;
+  };
+  if (pc.piece < 4) {
+    const int cl = lane >> 1, c = 8 * (pc.piece + 4 * (cl >> 3)) + (cl & 7);
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int tok = t_page + 16 * (lane & 1) + 8 * r;
+      const u32x4 v = pc.phys[r] >= 0 ? load16(j.k_cache + off_of(pc.phys[r], c, tok)) : u32x4{0u, 0u, 0u, 0u};
+      pc.w[4 * r] = v.x; pc.w[4 * r + 1] = v.y; pc.w[4 * r + 2] = v.z; pc.w[4 * r + 3] = v.w;
+    }
+  } else {
+#pragma unroll
+    for (int h2 = 0; h2 < 2; ++h2)
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        const int tok = t_page + 16 * r + 4 * (pc.piece - 4);
+        const uint2 v = pc.phys[r] >= 0
+                            ? *reinterpret_cast<const uint2*>(j.v_cache + off_of(pc.phys[r], lane + 64 * h2, tok))
+                            : uint2{0u, 0u};
+        pc.w[4 * h2 + 2 * r] = v.x;
+        pc.w[4 * h2 + 2 * r + 1] = v.y;
+      }
+  }
+}
+
+// Quantise and write (scratch: 1 KiB of the wavefront's own LDS).
+template <int BITS>
+__device__ void kivi_piece_finish(const PageJob& j, const KiviPiece& pc, int kvh, int lane, uint8_t* scratch) {
+  using F = KiviFmt<BITS>;
+  constexpr int LV = F::kLevels;
+  if (pc.piece < 0) return;
+  uint8_t* dst = j.pages + ((int64_t)pc.pid * j.num_kv_heads + kvh) * F::kBytes;
+  const int piece = pc.piece;
+  auto half = [&](int e) { return f16_to_f32((uint16_t)(pc.w[e >> 1] >> (16 * (e & 1)))); };
+  if (piece < 4) {
+    const int cl = lane >> 1, th = lane & 1, m = cl >> 3, ci = cl & 7;
+    const int o = piece + 4 * m;
+    float x[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) x[e] = half(e);
+    float mn = FLT_MAX, mx = -FLT_MAX;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      if (x[e] < mn) mn = x[e];
+      if (x[e] > mx) mx = x[e];
+    }
+    scan_combine_lanes<1, 1>(mn, mx, lane);
+    const GroupQ q = group_params<LV>(mn, mx);
+#pragma unroll
+    for (int e = 0; e < 16; ++e) scratch[(16 * th + e) * 32 + cl] = (uint8_t)quantise<LV>(x[e], q);
+    if (th == 0) {
+      uint16_t* kp = reinterpret_cast<uint16_t*>(dst + F::kKParams + o * 32);
+      kp[ci] = q.step;
+      kp[8 + ci] = q.zero;
+    }
+    build_barrier<kWave>();
+    // code dwords of chunks 64 tt + 16 piece + u: row t = 16 tt + u of the
+    // scratch holds the piece's 32 channels, octet piece + 4 m at bytes 8 m
+    constexpr int kWords = F::kChunk / 4;               // dwords per chunk
+    constexpr int kPerLane = 2 * 16 * kWords / kWave;   // 2 (INT4) or 4 (INT8)
+#pragma unroll
+    for (int e = 0; e < kPerLane; ++e) {
+      const int w = kPerLane * lane + e;
+      const int tt = w / (16 * kWords), u = (w / kWords) % 16, dd = w % kWords;
+      const int t = 16 * tt + u;
+      uint32_t x4;
+      if constexpr (BITS == 8) {
+        // dword 2 m + h: channels 8 o + 4 h + {0, 2, 1, 3}
+        const uint8_t* b = scratch + t * 32 + 8 * (dd >> 1) + 4 * (dd & 1);
+        x4 = (uint32_t)b[0] | (uint32_t)b[2] << 8 | (uint32_t)b[1] << 16 | (uint32_t)b[3] << 24;
+      } else {
+        // dword m: channel 8 o + 2 i + hb at bit 16 hb + 4 i
+        const uint8_t* b = scratch + t * 32 + 8 * dd;
+        x4 = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) x4 |= (uint32_t)b[2 * i] << (4 * i) | (uint32_t)b[2 * i + 1] << (16 + 4 * i);
+      }
+      const int chunk = 64 * tt + 16 * piece + u;
+      *reinterpret_cast<uint32_t*>(dst + F::kKCodes + chunk * F::kChunk + 4 * dd) = x4;
+    }
+    build_barrier<kWave>();   // the scratch may be reused
+  } else {
+    // V: the 8 tokens' fp16 go to the scratch as [slot][channel]; lane
+    // 4 s + g (< 32) scans group g of slot s in channel order as
+    // kivi_build_page does, writes its (step, zero) and its 32 codes as
+    // [channel][slot] bytes over the fp16 it has read (the wavefront's
+    // reads all come before its writes); then every lane packs the 8 slots
+    // of channels lane and lane + 64.
+    const int r = piece - 4;
+    uint16_t* xs = reinterpret_cast<uint16_t*>(scratch);
+#pragma unroll
+    for (int h2 = 0; h2 < 2; ++h2)
+#pragma unroll
+      for (int sl = 0; sl < 8; ++sl) xs[sl * kKiviHead + lane + 64 * h2] = (uint16_t)(pc.w[4 * h2 + (sl >> 1)] >> (16 * (sl & 1)));
+    build_barrier<kWave>();
+    if (lane < 32) {
+      const int sl = lane >> 2, g = lane & 3;
+      u32x4 raw[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) raw[i] = *reinterpret_cast<const u32x4*>(xs + sl * kKiviHead + 32 * g + 8 * i);
+      float x[32];
+#pragma unroll
+      for (int i = 0; i < 32; ++i) x[i] = f16_to_f32((uint16_t)(word(raw[i >> 3], (i & 7) >> 1) >> (16 * (i & 1))));
+      float mn = FLT_MAX, mx = -FLT_MAX;
+#pragma unroll
+      for (int i = 0; i < 32; ++i) {
+        if (x[i] < mn) mn = x[i];
+        if (x[i] > mx) mx = x[i];
+      }
+      const GroupQ q = group_params<LV>(mn, mx);
+      uint16_t* vp = reinterpret_cast<uint16_t*>(dst + F::kVParams + (g * 4 + r) * 32);
+      vp[sl] = q.step;
+      vp[8 + sl] = q.zero;
+#pragma unroll
+      for (int i = 0; i < 32; ++i) scratch[(32 * g + i) * 8 + sl] = (uint8_t)quantise<LV>(x[i], q);
+    }
+    build_barrier<kWave>();
+    // channel c = (4 hh + m) 16 + u: chunk 64 hh + 16 r + u
+    const int m = (lane >> 4) & 3, u = lane & 15;
+#pragma unroll
+    for (int h2 = 0; h2 < 2; ++h2) {
+      const uint2 cw = *reinterpret_cast<const uint2*>(scratch + (lane + 64 * h2) * 8);
+      auto cd = [&](int sl) { return (uint32_t)(((sl < 4 ? cw.x : cw.y) >> (8 * (sl & 3))) & 0xFFu); };
+      uint8_t* chunk = dst + F::kVCodes + (64 * h2 + 16 * r + u) * F::kChunk;
+      if constexpr (BITS == 8) {
+        // dword 2 m + h: slots 4 h + {0, 2, 1, 3}
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          *reinterpret_cast<uint32_t*>(chunk + 4 * (2 * m + h)) =
+              cd(4 * h) | cd(4 * h + 2) << 8 | cd(4 * h + 1) << 16 | cd(4 * h + 3) << 24;
+      } else {
+        // slot s at bit 16 (s & 1) + 4 (s >> 1)
+        uint32_t y = 0;
+#pragma unroll
+        for (int sl = 0; sl < 8; ++sl) y |= cd(sl) << (16 * (sl & 1) + 4 * (sl >> 1));
+        *reinterpret_cast<uint32_t*>(chunk + 4 * m) = y;
+      }
+    }
+    build_barrier<kWave>();   // the scratch may be reused
+  }
+}
+
+// A workgroup's way through a piece: one wavefront plans and loads it and
+// stages its fp16 in LDS (K: [channel of the piece][token], 32 x 32; V:
+// [slot][channel], 8 x 128), then, after a workgroup barrier, each of four
+// wavefronts quantises and writes a quarter: K octet piece + 4 q, or V
+// channel group q.  A quarter is 256 values, 4 per lane, so each group's
+// scan is 4 elements in order and then 3 combines across lanes.
+__device__ __forceinline__ void kivi_piece_stage(const KiviPiece& pc, int lane, uint16_t* raw) {
+  if (pc.piece < 0) return;
+  if (pc.piece < 4) {
+    u32x4* d = reinterpret_cast<u32x4*>(raw + (lane >> 1) * 32 + 16 * (lane & 1));
+    d[0] = u32x4{pc.w[0], pc.w[1], pc.w[2], pc.w[3]};
+    d[1] = u32x4{pc.w[4], pc.w[5], pc.w[6], pc.w[7]};
+  } else {
+#pragma unroll
+    for (int h2 = 0; h2 < 2; ++h2)
+#pragma unroll
+      for (int sl = 0; sl < 8; ++sl)
+        raw[sl * kKiviHead + lane + 64 * h2] = (uint16_t)(pc.w[4 * h2 + (sl >> 1)] >> (16 * (sl & 1)));
+  }
+}
+
+// The lane's 4 staged values of quarter q: K, channel ci = lane % 8 of octet
+// piece + 4 q at tokens 4 tq .. 4 tq + 3 (tq = lane / 8); V, slot lane / 8
+// at channels 32 q + 4 (lane % 8) .. + 3.
+__device__ __forceinline__ uint2 kivi_piece_quarter_values(int piece, int q, int lane, const uint16_t* raw) {
+  return piece < 4 ? *reinterpret_cast<const uint2*>(raw + (8 * q + (lane & 7)) * 32 + 4 * (lane >> 3))
+                   : *reinterpret_cast<const uint2*>(raw + (lane >> 3) * kKiviHead + 32 * q + 4 * (lane & 7));
+}
+
+// Quarter q of piece `piece` of the page in slot pid, from the lane's staged
+// values (scratch: 256 B of the wavefront's own LDS).
+template <int BITS>
+__device__ void kivi_piece_quarter(const PageJob& j, int pid, int piece, int kvh, int q, int lane, uint2 rw,
+                                   uint8_t* scratch) {
+  using F = KiviFmt<BITS>;
+  constexpr int LV = F::kLevels;
+  uint8_t* dst = j.pages + ((int64_t)pid * j.num_kv_heads + kvh) * F::kBytes;
+  float x[4];
+  if (piece < 4) {
+    // lane: channel ci of octet o = piece + 4 q, tokens 4 tq .. 4 tq + 3
+    const int ci = lane & 7, tq = lane >> 3, o = piece + 4 * q;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) x[i] = f16_to_f32((uint16_t)((i < 2 ? rw.x : rw.y) >> (16 * (i & 1))));
+    float mn = FLT_MAX, mx = -FLT_MAX;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (x[i] < mn) mn = x[i];
+      if (x[i] > mx) mx = x[i];
+    }
+    scan_combine_lanes<8, 32>(mn, mx, lane);
+    const GroupQ g = group_params<LV>(mn, mx);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) scratch[(4 * tq + i) * 8 + ci] = (uint8_t)quantise<LV>(x[i], g);
+    if (tq == 0) {
+      uint16_t* kp = reinterpret_cast<uint16_t*>(dst + F::kKParams + o * 32);
+      kp[ci] = g.step;
+      kp[8 + ci] = g.zero;
+    }
+    build_barrier<kWave>();
+    if (lane < 32) {
+      // token t = lane: the octet's 8 codes
+      const uint2 cb = *reinterpret_cast<const uint2*>(scratch + lane * 8);
+      auto b = [&](int c) { return (uint32_t)(((c < 4 ? cb.x : cb.y) >> (8 * (c & 3))) & 0xFFu); };
+      uint8_t* chunk = dst + F::kKCodes + (64 * (lane >> 4) + 16 * piece + (lane & 15)) * F::kChunk;
+      if constexpr (BITS == 8) {
+        // dword 2 q + h: channels 4 h + {0, 2, 1, 3} of the octet
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          *reinterpret_cast<uint32_t*>(chunk + 4 * (2 * q + h)) =
+              b(4 * h) | b(4 * h + 2) << 8 | b(4 * h + 1) << 16 | b(4 * h + 3) << 24;
+      } else {
+        // dword q: channel 2 i + hb at bit 16 hb + 4 i
+        uint32_t x4 = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) x4 |= b(2 * i) << (4 * i) | b(2 * i + 1) << (16 + 4 * i);
+        *reinterpret_cast<uint32_t*>(chunk + 4 * q) = x4;
+      }
+    }
+  } else {
+    // lane: slot sl, channels 32 q + 4 cq .. + 3 (group q)
+    const int r = piece - 4, sl = lane >> 3, cq = lane & 7;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) x[i] = f16_to_f32((uint16_t)((i < 2 ? rw.x : rw.y) >> (16 * (i & 1))));
+    float mn = FLT_MAX, mx = -FLT_MAX;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (x[i] < mn) mn = x[i];
+      if (x[i] > mx) mx = x[i];
+    }
+    scan_combine_lanes<1, 4>(mn, mx, lane);
+    const GroupQ g = group_params<LV>(mn, mx);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) scratch[(4 * cq + i) * 8 + sl] = (uint8_t)quantise<LV>(x[i], g);
+    if (cq == 0) {
+      uint16_t* vp = reinterpret_cast<uint16_t*>(dst + F::kVParams + (q * 4 + r) * 32);
+      vp[sl] = g.step;
+      vp[8 + sl] = g.zero;
+    }
+    build_barrier<kWave>();
+    if (lane < 32) {
+      // channel c = 32 q + lane = (4 hh + m) 16 + u: its 8 slots
+      const int c = 32 * q + lane, hh = c >> 6, m = (c >> 4) & 3, u = c & 15;
+      const uint2 cw = *reinterpret_cast<const uint2*>(scratch + lane * 8);
+      auto cd = [&](int s2) { return (uint32_t)(((s2 < 4 ? cw.x : cw.y) >> (8 * (s2 & 3))) & 0xFFu); };
+      uint8_t* chunk = dst + F::kVCodes + (64 * hh + 16 * r + u) * F::kChunk;
+      if constexpr (BITS == 8) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          *reinterpret_cast<uint32_t*>(chunk + 4 * (2 * m + h)) =
+              cd(4 * h) | cd(4 * h + 2) << 8 | cd(4 * h + 1) << 16 | cd(4 * h + 3) << 24;
+      } else {
+        uint32_t y = 0;
+#pragma unroll
+        for (int s2 = 0; s2 < 8; ++s2) y |= cd(s2) << (16 * (s2 & 1) + 4 * (s2 >> 1));
+        *reinterpret_cast<uint32_t*>(chunk + 4 * m) = y;
+      }
+    }
+  }
+}
+
+// The three phases in a row, for a wavefront with nothing else to do.  Every
+// token of the page must be in the pool.
+template <int BITS>
+__device__ void kivi_build_piece(const PageJob& j, int seq, int kvh, int page, int piece, int lane,
+                                 uint8_t* scratch) {
+  KiviPiece pc = kivi_piece_plan(j, seq, page, piece, lane);
+  kivi_piece_load(j, pc, kvh, page, lane);
+  kivi_piece_finish<BITS>(j, pc, kvh, lane, scratch);
 }
 
 }  // namespace tl

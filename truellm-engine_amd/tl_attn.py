@@ -75,6 +75,7 @@ class KiviDesc(ctypes.Structure):
         ("scale", ctypes.c_float),
         ("bits", ctypes.c_int32),
         ("pre_rope_keys", ctypes.c_int32),
+        ("build_ahead", ctypes.c_int32),
     ]
 
 
@@ -173,7 +174,7 @@ def _hip_runtimes() -> set:
         return set()
 
 
-ABI_VERSION = 3           # TL_ABI_VERSION of include/tl_attn.h
+ABI_VERSION = 4           # TL_ABI_VERSION of include/tl_attn.h
 
 
 def _load() -> ctypes.CDLL:
@@ -492,11 +493,13 @@ def kivi_quantized_len(seq_len, residual_length) -> int:
 
 
 def make_kivi_desc(q, k_cache, block_tables, page_tables, num_pages, num_kv_heads, scale, *,
-                   residual_length=128, gqa_map=GQA_GROUPED, partition_pages=0, bits=4, pre_rope_keys=False):
+                   residual_length=128, gqa_map=GQA_GROUPED, partition_pages=0, bits=4, pre_rope_keys=False,
+                   build_ahead=False):
     S, H, D = q.shape
     d = KiviDesc()
     d.bits = bits
     d.pre_rope_keys = int(bool(pre_rope_keys))
+    d.build_ahead = int(bool(build_ahead))
     d.num_seqs, d.num_heads, d.num_kv_heads, d.head_size = S, H, num_kv_heads, D
     d.block_size = k_cache.shape[3]
     d.max_blocks_per_seq, d.num_blocks = block_tables.shape[1], k_cache.shape[0]
