@@ -791,10 +791,6 @@ struct KiviDecodeSmem {
 // halve the occupancy.
 // BS: the fp16 pool's block size, 16, or 0 for any other (read from the
 // launch at run time).
-// Pages the residual wavefront leaves to the page wavefronts in a step in
-// which it writes a build-ahead piece.
-constexpr int kPieceResPages = 0;
-
 template <int NW, bool FINAL, bool APPEND, int BITS, bool ROPE, int BS>
 __global__ __launch_bounds__(NW * kWave, 2) void kivi_decode_kernel(KiviParams k) {
   using Smem = KiviDecodeSmem<NW>;
@@ -860,7 +856,7 @@ __global__ __launch_bounds__(NW * kWave, 2) void kivi_decode_kernel(KiviParams k
   int ahead_page = 0;
   const int ahead = APPEND ? kivi_ahead_piece(L, k.residual_length, ahead_page) : -1;
   const bool piece_due = APPEND && k.job.build_ahead && hs == 0 && has_res && ahead >= 0;
-  const int res_pages = has_res ? max(0, (pg1 - pg0) / 30 - (piece_due ? kPieceResPages : 0)) : 0;
+  const int res_pages = has_res ? (pg1 - pg0) / 30 : 0;
 
   // The page that L completes, if any (APPEND), by the whole workgroup
   // before the page wavefronts start.  (Built by the residual wavefront
