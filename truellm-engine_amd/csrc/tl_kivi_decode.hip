@@ -207,7 +207,8 @@ __device__ __forceinline__ u32x4 v_codes(const PageRaw<BITS>& r, int nt) {
 // or a prefetch past the wavefront's last page) gets an empty range: its
 // loads return zeros without a memory request, while the number of loads
 // per iteration stays fixed.
-template <int BITS>
+// KV: 1 loads the K codes and the parameters, 2 the V codes, 3 both.
+template <int BITS, int KV = 3>
 __device__ __forceinline__ void load_page(PageRaw<BITS>& r, const uint8_t* page, bool there, unsigned off,
                                           unsigned par_off) {
   using F = KiviFmt<BITS>;
@@ -218,10 +219,10 @@ __device__ __forceinline__ void load_page(PageRaw<BITS>& r, const uint8_t* page,
   for (int t = 0; t < 2; ++t)
 #pragma unroll
     for (int w = 0; w < CW; ++w) {
-      r.kn[CW * t + w] = buffer_load16(rs, unsigned(F::kKCodes) + t * kTile + CW * off + 16u * w);
-      r.vn[CW * t + w] = buffer_load16(rs, unsigned(F::kVCodes) + t * kTile + CW * off + 16u * w);
+      if constexpr (KV & 1) r.kn[CW * t + w] = buffer_load16(rs, unsigned(F::kKCodes) + t * kTile + CW * off + 16u * w);
+      if constexpr (KV & 2) r.vn[CW * t + w] = buffer_load16(rs, unsigned(F::kVCodes) + t * kTile + CW * off + 16u * w);
     }
-  r.par = buffer_load16(rs, par_off);
+  if constexpr (KV & 1) r.par = buffer_load16(rs, par_off);
 }
 
 // Physical page of page index pg, or -1 (hole / past the end / outside the pool).
@@ -485,10 +486,16 @@ __device__ __forceinline__ void kivi_pages_wave(const KiviParams& k, int seq, in
   // INT8); lanes 0-31 take the K params, lanes 32-63 the V params
   const unsigned off = unsigned(lane) * 16u;
   const unsigned par_off = lane < 32 ? unsigned(F::kKParams) + off : unsigned(F::kVParams) + off - 512u;
-  auto load = [&](PageRaw<BITS>& ra, PageRaw<BITS>& rb, int ia, int ib) {
+  // Keys held before RoPE at INT8: a pair's V codes are loaded just before
+  // its own q.k (the rotation hides their latency) instead of with its K
+  // one pair ahead, so that two pairs' V codes are never held together.
+  constexpr bool kLateV = ROPE && BITS == 8;
+  constexpr int kAhead = kLateV ? 1 : 3;    // what a pair's early fetch loads
+  auto load_kv = [&](auto kv_tag, PageRaw<BITS>& ra, PageRaw<BITS>& rb, int ia, int ib) {
+    constexpr int KV = decltype(kv_tag)::value;
     // 32 x 32 -> 64-bit products keep the page base in scalar registers
-    load_page(ra, pool + uint64_t(uint32_t(max(ia, 0))) * pid_stride, ia >= 0, off, par_off);
-    load_page(rb, pool + uint64_t(uint32_t(max(ib, 0))) * pid_stride, ib >= 0, off, par_off);
+    load_page<BITS, KV>(ra, pool + uint64_t(uint32_t(max(ia, 0))) * pid_stride, ia >= 0, off, par_off);
+    load_page<BITS, KV>(rb, pool + uint64_t(uint32_t(max(ib, 0))) * pid_stride, ib >= 0, off, par_off);
   };
 
   // The wavefront's pages are pg_begin + o * pg_step, o = 0 .. n_mine - 1.
@@ -511,16 +518,24 @@ __device__ __forceinline__ void kivi_pages_wave(const KiviParams& k, int seq, in
     }
     auto id = [&](int o) { return o < cn ? __builtin_amdgcn_readlane(idv, o) : -1; };
     auto pg_of = [&](int o) { return pg_begin + (c0 + o) * pg_step; };   // page index (token position / 32)
-    // the loads of pages o and o + 1
-    auto fetch = [&](PageRaw<BITS>& ra, PageRaw<BITS>& rb, int o) { load(ra, rb, id(o), id(o + 1)); };
+    // the loads of pages o and o + 1 (with kLateV, fetch_v loads their V
+    // codes just before they are used)
+    auto fetch = [&](PageRaw<BITS>& ra, PageRaw<BITS>& rb, int o) {
+      load_kv(std::integral_constant<int, kAhead>{}, ra, rb, id(o), id(o + 1));
+    };
+    auto fetch_v = [&](PageRaw<BITS>& ra, PageRaw<BITS>& rb, int o) {
+      if constexpr (kLateV) load_kv(std::integral_constant<int, 2>{}, ra, rb, id(o), id(o + 1));
+    };
     fetch(r0a, r0b, 0);
 #pragma unroll 1
     for (int o = 0; o < cn; o += 4) {
+      fetch_v(r0a, r0b, o);
       fetch(r1a, r1b, o + 2);
       if (share_simd) __builtin_amdgcn_s_setprio(1);
       page_pair<BITS, ROPE>(st, r0a, r0b, id(o) >= 0, id(o + 1) >= 0, qsc, qss, s_par_w, lane, slot_scale, k,
                             pg_of(o), pg_of(o + 1), s_rope);
       if (o + 2 >= cn) break;
+      fetch_v(r1a, r1b, o + 2);
       fetch(r0a, r0b, o + 4);
       if (share_simd) __builtin_amdgcn_s_setprio(0);
       page_pair<BITS, ROPE>(st, r1a, r1b, id(o + 2) >= 0, id(o + 3) >= 0, qsc, qss, s_par_w, lane, slot_scale, k,
@@ -886,12 +901,14 @@ __global__ __launch_bounds__(NW * kWave, 2) void kivi_decode_kernel(KiviParams k
   } else {
     const int lane = tid % kWave;
     // build-ahead: this step's piece of the next page (one head slice
-    // writes it).  Its table entries are read here, its fp16 after the
-    // window, and it is quantised and written after the wavefront's last
-    // loads, which its stores would otherwise hold up.
+    // writes it).  Its table entries are read here and its fp16 after the
+    // window (with keys held before RoPE, both after the wavefront's last
+    // pages: its registers are short there), it is staged in LDS, and the
+    // four wavefronts quantise and write it after the merge, so that no
+    // load of the launch waits behind its stores.
     KiviPiece piece;
     piece.piece = -1;
-    if constexpr (APPEND)
+    if constexpr (APPEND && !ROPE)
       if (piece_due) piece = kivi_piece_plan(k.job, seq, ahead_page, ahead, lane);
     NewestToken nt;
     if constexpr (APPEND)
@@ -913,12 +930,16 @@ __global__ __launch_bounds__(NW * kWave, 2) void kivi_decode_kernel(KiviParams k
     // the token's store, at the end of the window, off the page wavefronts'
     // path (the window ends halfway through the launch)
     if constexpr (APPEND) store_newest<BS>(k.job, nt, seq, kvh, lane);
-    if constexpr (APPEND) kivi_piece_load(k.job, piece, kvh, ahead_page, lane);
+    if constexpr (APPEND && !ROPE) kivi_piece_load(k.job, piece, kvh, ahead_page, lane);
     kivi_pages_wave<BITS, ROPE>(k, seq, kvh, hs, pg1 - res_pages, pg1, 1, &sd.p[wave][0], &sd.acc[NW + 1][0][0],
                     &sd.m[NW + 1][0], &sd.l[NW + 1][0], false, false, -1, s_rope);
     // the piece's fp16 for the quarters after the merge
     if constexpr (APPEND) {
       if (piece_due) {
+        if constexpr (ROPE) {
+          piece = kivi_piece_plan(k.job, seq, ahead_page, ahead, lane);
+          kivi_piece_load(k.job, piece, kvh, ahead_page, lane);
+        }
         kivi_piece_stage(piece, lane, reinterpret_cast<uint16_t*>(&sd.p[wave][0]));
         if (lane == 0) sd.piece_pid = piece.piece >= 0 ? piece.pid : -1;
       }
