@@ -486,10 +486,12 @@ __device__ __forceinline__ void kivi_pages_wave(const KiviParams& k, int seq, in
   // INT8); lanes 0-31 take the K params, lanes 32-63 the V params
   const unsigned off = unsigned(lane) * 16u;
   const unsigned par_off = lane < 32 ? unsigned(F::kKParams) + off : unsigned(F::kVParams) + off - 512u;
-  // Keys held before RoPE at INT8: a pair's V codes are loaded just before
-  // its own q.k (the rotation hides their latency) instead of with its K
-  // one pair ahead, so that two pairs' V codes are never held together.
-  constexpr bool kLateV = ROPE && BITS == 8;
+  // Keys held before RoPE: a pair's V codes are loaded just before its own
+  // q.k (the rotation hides their latency) instead of with its K one pair
+  // ahead, so that two pairs' V codes are never held together (INT8: 190.5
+  // -> 158.9 us per step, 38-46 registers spilled before; INT4: 112.7 ->
+  // 111.9 us).
+  constexpr bool kLateV = ROPE;
   constexpr int kAhead = kLateV ? 1 : 3;    // what a pair's early fetch loads
   auto load_kv = [&](auto kv_tag, PageRaw<BITS>& ra, PageRaw<BITS>& rb, int ia, int ib) {
     constexpr int KV = decltype(kv_tag)::value;
