@@ -1032,3 +1032,98 @@ def test_build_ahead_full_batch_mixed_lengths():
                                     np.ascontiguousarray(kc.tables[sub]), np.ascontiguousarray(lens[sub]),
                                     kc.n_kv, kc.R, kc.scale, orc.GROUPED, kc.bits)
     assert_close(out[torch.from_numpy(sub).cuda()], want, orc.F16, ATOL_KIVI, "full batch")
+
+
+@pytest.mark.parametrize("H,n_kv,pp", [(32, 1, 0), (32, 1, 4), (64, 8, 4), (48, 2, -1)])
+def test_build_ahead_head_slices_and_split_k(H, n_kv, pp):
+    """build_ahead with GQA groups wider than one wavefront's 16 heads (two
+    or more workgroups per (sequence, kv head), of which one writes the
+    piece) and with split-K plans (the piece written by the last
+    partition's workgroup): pages bit for bit and outputs against the
+    oracle after each of 36 fused steps."""
+    steps, R = 36, 128
+    start = np.array([R + 32 * k + o for k, o in zip([4, 2, 7, 0, 3, 1], _AHEAD_PHASES)], np.int32)
+    kc = KiviCase(95 + H + n_kv + pp, start + steps, H=H, n_kv=n_kv, extra_blocks=1, R=R)
+    qd, kd, vd = dev(kc.q, orc.F16), dev(kc.k, orc.F16), dev(kc.v, orc.F16)
+    btd, ptd = dev(kc.tables), dev(kc.page_tables)
+    pages = torch.zeros(kc.num_pages, kc.n_kv, kc.page_bytes, dtype=torch.uint8, device="cuda")
+    desc = tla.make_kivi_desc(qd, kd, btd, ptd, kc.num_pages, kc.n_kv, kc.scale, residual_length=R,
+                              partition_pages=pp, build_ahead=True)
+    print(f"case build-ahead H={H} n_kv={n_kv} pp={pp}", flush=True)
+    tla.kivi_build_pages(desc, kd, vd, btd, dev(start), ptd, pages, int(start.max()))
+    rng = np.random.default_rng(H * 3 + n_kv + pp)
+    max_ctx = int(start.max()) + steps
+    ws = torch.empty(max(16, tla.kivi_workspace_bytes(desc, max_ctx)), dtype=torch.uint8, device="cuda")
+    lens = start.copy()
+    k_host, v_host = kc.k.copy(), kc.v.copy()
+    for step in range(steps):
+        lens = lens + 1
+        pos = lens - 1
+        slots = (kc.tables[np.arange(kc.S), pos // 16] * 16 + pos % 16).astype(np.int32)
+        knew = inputs.encode(rng.standard_normal((kc.S, kc.n_kv, 128), dtype=np.float32), orc.F16)
+        vnew = inputs.encode(rng.standard_normal((kc.S, kc.n_kv, 128), dtype=np.float32), orc.F16)
+        out = torch.full_like(qd, float("nan"))
+        tla.kivi_decode_step(desc, out, qd, dev(knew, orc.F16), dev(vnew, orc.F16), dev(slots), pages, ptd,
+                             kd, vd, btd, dev(lens), max_ctx, ws)
+        torch.cuda.synchronize()
+        orc.reshape_and_cache(knew, vnew, k_host, v_host, slots)
+        kc.k, kc.v, kc.lens = k_host, v_host, lens
+        want_pages = kc.oracle_pages()
+        used = [p for p in _used_pages(kc, lens) if p >= 0]
+        assert np.array_equal(pages.cpu().numpy()[used], want_pages[used]), f"pages after step {step}"
+        assert_close(out, _kivi_ref(kc, want_pages), orc.F16, ATOL_KIVI, f"H={H} n_kv={n_kv} pp={pp} step {step}")
+
+
+def test_build_ahead_step_graph_replay_matches_eager():
+    """The fused step with build_ahead captured in a HIP graph: 40 replays
+    (each its own step, lengths and slots advanced through device buffers)
+    give the eager run's pages and outputs bit for bit."""
+    steps, R = 40, 128
+    start = np.array([R + 32 * k + o for k, o in zip([4, 2, 7, 0, 3, 1], _AHEAD_PHASES)], np.int32)
+    rng = np.random.default_rng(71)
+    knew = [inputs.encode(rng.standard_normal((6, 8, 128), dtype=np.float32), orc.F16) for _ in range(steps)]
+    vnew = [inputs.encode(rng.standard_normal((6, 8, 128), dtype=np.float32), orc.F16) for _ in range(steps)]
+    results = []
+    for graphed in (False, True):
+        kc = KiviCase(97, start + steps, H=32, extra_blocks=1, R=R)
+        qd, kd, vd = dev(kc.q, orc.F16), dev(kc.k, orc.F16), dev(kc.v, orc.F16)
+        btd, ptd = dev(kc.tables), dev(kc.page_tables)
+        pages = torch.zeros(kc.num_pages, kc.n_kv, kc.page_bytes, dtype=torch.uint8, device="cuda")
+        desc = tla.make_kivi_desc(qd, kd, btd, ptd, kc.num_pages, kc.n_kv, kc.scale, residual_length=R,
+                                  build_ahead=True)
+        tla.kivi_build_pages(desc, kd, vd, btd, dev(start), ptd, pages, int(start.max()))
+        max_ctx = int(start.max()) + steps
+        ws = torch.empty(max(16, tla.kivi_workspace_bytes(desc, max_ctx)), dtype=torch.uint8, device="cuda")
+        sl = dev(start)
+        slot_d = torch.zeros(kc.S, dtype=torch.int32, device="cuda")
+        kn = torch.zeros(kc.S, kc.n_kv, 128, dtype=torch.float16, device="cuda")
+        vn = torch.zeros_like(kn)
+        out = torch.zeros_like(qd)
+        outs = []
+        stream = torch.cuda.Stream()
+        graph = None
+        print(f"case build-ahead graph={graphed}", flush=True)
+        for step in range(steps):
+            lens = start + step + 1
+            pos = lens - 1
+            sl.copy_(dev(lens))
+            slot_d.copy_(dev((kc.tables[np.arange(kc.S), pos // 16] * 16 + pos % 16).astype(np.int32)))
+            kn.copy_(dev(knew[step], orc.F16))
+            vn.copy_(dev(vnew[step], orc.F16))
+            torch.cuda.synchronize()
+            if graphed:
+                if graph is None:
+                    graph = torch.cuda.CUDAGraph()
+                    with torch.cuda.graph(graph, stream=stream):
+                        tla.kivi_decode_step(desc, out, qd, kn, vn, slot_d, pages, ptd, kd, vd, btd, sl, max_ctx, ws,
+                                             torch.cuda.current_stream())
+                graph.replay()
+            else:
+                tla.kivi_decode_step(desc, out, qd, kn, vn, slot_d, pages, ptd, kd, vd, btd, sl, max_ctx, ws)
+            torch.cuda.synchronize()
+            outs.append(out.clone())
+        results.append((outs, pages.clone(), kd.clone(), vd.clone()))
+    (o0, p0, k0, v0), (o1, p1, k1, v1) = results
+    assert torch.equal(p0, p1) and torch.equal(k0, k1) and torch.equal(v0, v1)
+    for step in range(steps):
+        assert torch.equal(o0[step], o1[step]), f"step {step}"
