@@ -193,7 +193,8 @@ def timed(step, steps, warmup, name=None):
     return statistics.median(per)
 
 
-def bench_decode(args, dtype, append=False, lens=None, partition_tokens=None, v2=False, name=None, layers=2):
+def bench_decode(args, dtype, append=False, lens=None, partition_tokens=None, v2=False, name=None, layers=2,
+                 v2_capacity=None):
     """Decode of one layer over the given lengths (default: batch 64, every
     context 4096) with the library plan (or partition_tokens), through
     tl_paged_attention_decode or, with v2, the reference-named
@@ -235,8 +236,11 @@ def bench_decode(args, dtype, append=False, lens=None, partition_tokens=None, v2
     desc = tla.make_decode_desc(q, pools[0][0], pools[0][2], NKV, scale, gqa_map=tla.GQA_GROUPED, partition_tokens=pt)
     ws = torch.empty(max(16, tla.workspace_bytes(desc, max_ctx)), dtype=torch.uint8, device="cuda")
     if v2:
-        P = tla.v2_num_partitions(max_ctx, BS)
-        v2_parts, v2_pt = tla.v2_plan(B, H, NKV, D, BS, tla.dtype_code(q), max_ctx)
+        # v2_capacity: the scratch allocated for that many partitions (the
+        # engine sizes it for its training context) and passed through
+        # tl_paged_attention_v2_capacity
+        P = tla.v2_num_partitions(max_ctx, BS) if v2_capacity is None else v2_capacity
+        v2_parts, v2_pt = tla.v2_plan(B, H, NKV, D, BS, tla.dtype_code(q), max_ctx, scratch_partitions=v2_capacity)
         es = torch.empty(B, H, P, dtype=torch.float32, device="cuda")
         ml = torch.empty_like(es)
         tmp = torch.empty(B, H, P, D, dtype=tdt, device="cuda")
@@ -254,7 +258,7 @@ def bench_decode(args, dtype, append=False, lens=None, partition_tokens=None, v2
             tla.reshape_and_cache_split(knew, vnew, k, v, slots[i % layers], stream)
         if v2:
             tla.paged_attention_v2(out, es, ml, tmp, q, k, v, tables, sl, NKV, scale, D, BS, max_ctx, stream,
-                                   gqa_map=tla.GQA_GROUPED)
+                                   gqa_map=tla.GQA_GROUPED, scratch_partitions=v2_capacity)
         else:
             tla.paged_attention_decode(desc, out, q, k, v, tables, sl, max_ctx, ws, stream)
 
@@ -866,6 +870,10 @@ def main():
     # the engine's call shape: one sequence per call, 32 layers each with a
     # pool of its own (672 MB in all, beyond the 256 MiB Infinity Cache)
     v2one = bench_decode(args, "f16", lens=[CTX], v2=True, name="v2_one_seq", layers=32) if want("v2") else None
+    # the same with the engine's whole v2 scratch: allocated once for
+    # ceil(n_ctx_train / 512) partitions, 16 for a model trained at 8192
+    v2cap = (bench_decode(args, "f16", lens=[CTX], v2=True, name="v2_one_seq_cap16", layers=32, v2_capacity=16)
+             if want("v2") else None)
     one = bench_decode(args, "f16", lens=[CTX], name="auto_one_seq", layers=32) if want("v2") else None
     pf = bench_prefill(args) if args.only in ("all", "prefill") else None
     cb = bench_copy_blocks(args) if args.only in ("all", "blocks") else None
@@ -935,6 +943,12 @@ def main():
             "library_plan_us": round(one["ms_per_step"] * 1e3, 2) if one else None,
             "library_plan_partitions": one["partitions"] if one else None,
             "library_plan_gbs": round(one["gbs"], 2) if one else None}
+        if v2cap is not None:
+            res["paged_attention_v2_one_sequence"]["v2_engine_allocation"] = {
+                "workload": "tl_paged_attention_v2_capacity with the scratch the engine allocates once for a "
+                            "model trained at 8192 tokens (16 partitions, cuda_engine.cpp:273-285)",
+                "us": round(v2cap["ms_per_step"] * 1e3, 2), "partitions": v2cap["partitions"],
+                "partition_tokens": v2cap["partition_tokens"], "gbs": round(v2cap["gbs"], 2)}
     if kv is not None:
         res["kivi_int4"] = {"gbs": round(kv["gbs"], 2), "ms_per_step": round(kv["ms_per_step"], 5),
                             "tok_s": round(kv["tok_s"], 1),

@@ -30,8 +30,9 @@ extern "C" {
 /* Version of this C ABI (tl_abi_version).  2: tl_kivi_desc gained
  * pre_rope_keys (after bits), for the _pre_rope entry points.  3:
  * tl_prefill_desc gained kv_dtype, k_scale, v_scale.  4: tl_kivi_desc
- * gained build_ahead (after pre_rope_keys). */
-#define TL_ABI_VERSION 4
+ * gained build_ahead (after pre_rope_keys).  5: tl_paged_attention_v2_capacity
+ * and its plan query. */
+#define TL_ABI_VERSION 5
 
 /* Mirrors truellm::ErrorCode (include/truellm/types.h:20-32). */
 typedef enum tl_status {
@@ -177,6 +178,28 @@ int tl_paged_attention_v2(void* out, float* exp_sums, float* max_logits, void* t
 int32_t tl_paged_attention_v2_partitions(int32_t num_seqs, int32_t num_heads, int32_t num_kv_heads,
                                          int32_t head_size, int32_t block_size, int32_t dtype,
                                          int32_t max_context_len, int32_t* partition_tokens);
+
+/* No counterpart in the reference.  tl_paged_attention_v2 for a caller
+ * whose scratch holds more partitions than the call's context needs: the
+ * engine allocates exp_sums / max_logits / tmp_out once, for
+ * ceil(n_ctx_train / (32 * block_size)) partitions (cuda_engine.cpp:273-285),
+ * and passes that count as scratch_partitions (at least the reference
+ * kernel's count for max_context_len, else TL_ERR_INVALID_ARGUMENT).  The
+ * plan may then use up to that many partitions, which a short batch (the
+ * engine's one sequence per call) turns into shorter partitions over more
+ * CUs.  Results as tl_paged_attention_v2. */
+int tl_paged_attention_v2_capacity(void* out, float* exp_sums, float* max_logits, void* tmp_out,
+                                   const void* q, const void* k_cache, const void* v_cache,
+                                   const int32_t* block_tables, const int32_t* seq_lens,
+                                   int32_t num_seqs, int32_t num_heads, int32_t num_kv_heads,
+                                   int32_t head_size, int32_t block_size, int32_t max_blocks_per_seq,
+                                   int32_t num_blocks, float scale, int32_t dtype, int32_t gqa_map,
+                                   int32_t max_context_len, int32_t scratch_partitions, void* stream);
+/* Its plan, as tl_paged_attention_v2_partitions (-1: refused sizes). */
+int32_t tl_paged_attention_v2_capacity_partitions(int32_t num_seqs, int32_t num_heads, int32_t num_kv_heads,
+                                                  int32_t head_size, int32_t block_size, int32_t dtype,
+                                                  int32_t max_context_len, int32_t scratch_partitions,
+                                                  int32_t* partition_tokens);
 
 /* ------------------------------------------------------------------------
  * KV-cache writes

@@ -16,7 +16,7 @@ def test_exports_every_declared_function():
 
 
 def test_abi_version():
-    assert tla.lib.tl_abi_version() == 4 == tla.ABI_VERSION
+    assert tla.lib.tl_abi_version() == 5 == tla.ABI_VERSION
 
 
 def _desc(**kw):
@@ -130,6 +130,28 @@ def test_v2_plan_inside_the_callers_scratch():
     assert plan(1, tla.F16, 4096, hs=80)[0] == 4        # dot-product decode: fp32 partials
     with pytest.raises(tla.TLError):
         plan(1, tla.F16, 4096, bs=12)
+
+
+def test_v2_capacity_plan_uses_the_callers_allocation():
+    """tl_paged_attention_v2_capacity: a scratch allocated for more
+    partitions than the call's context needs (the engine's, sized for its
+    training context) lets the one-sequence plan take shorter partitions;
+    a count below the reference kernel's for the call is refused."""
+    plan = lambda S, dt, L, cap: tla.v2_plan(S, 32, 8, 128, 16, dt, L, scratch_partitions=cap)
+    assert plan(1, tla.F16, 4096, 8) == (8, 512)          # as tl_paged_attention_v2
+    assert plan(1, tla.F16, 4096, 16) == (16, 256)        # n_ctx_train 8192: 16 slots
+    assert plan(1, tla.F16, 4096, 64) == (32, 128)        # the library plan fits
+    assert plan(1, tla.BF16, 4096, 16) == (8, 512)        # fp32 partials: 8 of the 16 slots' bytes
+    assert plan(64, tla.F16, 4096, 16) == (1, 0)          # single pass
+    with pytest.raises(tla.TLError):
+        plan(1, tla.F16, 4096, 7)                           # below the 8 the call needs
+    with pytest.raises(tla.TLError):
+        plan(1, tla.F16, 4096, 0)
+    call = lambda cap: tla.lib.tl_paged_attention_v2_capacity(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE,
+                                                              1, 32, 8, 128, 16, 256, 512, 0.088, tla.F16,
+                                                              tla.GQA_GROUPED, 4096, cap, None)
+    assert call(7) == tla.ERR_INVALID_ARGUMENT and "scratch_partitions" in tla.last_error()
+    assert call(0) == tla.ERR_INVALID_ARGUMENT
 
 
 @pytest.mark.parametrize("kw,ok", [

@@ -226,17 +226,20 @@ def test_merge_of_more_than_256_partitions():
 GUARD = 4096
 
 
-def _v2_guarded(case, code, stream=None, kernel_sizing=False):
+def _v2_guarded(case, code, stream=None, kernel_sizing=False, capacity=None):
     """tl_paged_attention_v2 with the engine's scratch sizes (or, with
     kernel_sizing, the partition count the reference kernel itself writes,
-    paged_attention_v2.cu:196) followed by sentinel guards; returns (out,
-    guards intact)."""
+    paged_attention_v2.cu:196; with capacity, a scratch of that many
+    partitions through tl_paged_attention_v2_capacity) followed by sentinel
+    guards; returns (out, guards intact)."""
     q, k, v, bt, sl = (dev(case.q, code), dev(case.k_cache, code), dev(case.v_cache, code), dev(case.tables),
                        dev(case.seq_lens))
     S, H, D = q.shape
     BS = k.shape[3]
     max_ctx = int(case.seq_lens.max())
     P = (max_ctx // BS + 31) // 32 if kernel_sizing else tla.v2_num_partitions(max_ctx, BS)
+    if capacity is not None:
+        P = capacity
     n = S * H * P
     if n == 0:
         n = 1
@@ -245,7 +248,7 @@ def _v2_guarded(case, code, stream=None, kernel_sizing=False):
     tmp = torch.full((n * D + GUARD,), 1.5, dtype=q.dtype, device="cuda")
     out = torch.full_like(q, float("nan"))
     tla.paged_attention_v2(out, es, ml, tmp, q, k, v, bt, sl, case.num_kv_heads, case.scale, D, BS, max_ctx,
-                           stream, gqa_map=tla.GQA_MODULO)
+                           stream, gqa_map=tla.GQA_MODULO, scratch_partitions=capacity)
     torch.cuda.synchronize()
     intact = bool((es[n:] == 7.25).all() and (ml[n:] == -3.5).all() and (tmp[n * D:] == 1.5).all())
     return out, intact
@@ -299,6 +302,25 @@ def test_v2_stays_inside_scratch_sized_by_the_reference_kernel(lens, code, BS):
     out, intact = _v2_guarded(case, code, kernel_sizing=True)
     assert intact, "v2 wrote past the caller's scratch"
     assert_close(out, _ref(case, orc.MODULO), code, ATOL, f"v2 {lens}")
+
+
+@pytest.mark.parametrize("lens,code,cap", [
+    ([4096], orc.F16, 16),            # the engine's scratch for n_ctx_train 8192: 16 x 256 tokens
+    ([4096], orc.F16, 64),            # room for the library plan: 32 x 128
+    ([4097], orc.BF16, 16),           # fp32 partials in 16 slots' bytes
+    ([3000, 1200], orc.F16, 40),
+    ([700], orc.F32, 9),
+])
+def test_v2_capacity_stays_inside_the_allocated_scratch(lens, code, cap):
+    """tl_paged_attention_v2_capacity with a scratch allocated for cap
+    partitions (more than the call's context needs): against the oracle,
+    the guards past the allocation intact, and the plan the one reported."""
+    case = inputs.make_paged_case(140 + len(lens) + cap, len(lens), 32, 8, 128, 16, lens, code)
+    P, _ = tla.v2_plan(len(lens), 32, 8, 128, 16, code, int(max(lens)), scratch_partitions=cap)
+    print(f"case v2 capacity lens={lens} code={code} cap={cap} P={P}", flush=True)
+    out, intact = _v2_guarded(case, code, capacity=cap)
+    assert intact, "v2 wrote past the allocated scratch"
+    assert_close(out, _ref(case, orc.MODULO), code, ATOL, f"v2 capacity {lens}")
 
 
 def test_v2_misaligned_scratch_runs_single_pass():

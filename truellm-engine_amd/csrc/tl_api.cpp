@@ -206,8 +206,11 @@ size_t ws_bytes(const tl_decode_desc* d, int P) {
 // wants more partitions than the scratch holds they are made longer; where
 // it wants one (a large batch) the call runs single pass.  d is the
 // descriptor of the call (partition_tokens 0) and may be changed.
-void v2_plan(tl_decode_desc* d, int32_t max_ctx, bool tmp_aligned, int* P, int* PT, bool* f16_parts) {
-  const int Pc = (max_ctx / d->block_size + 31) / 32;
+// Pc: tmp_out's partition slots (0: the reference kernel's count for
+// max_ctx; a caller that allocated the scratch for a longer context passes
+// its own count).
+void v2_plan(tl_decode_desc* d, int32_t max_ctx, bool tmp_aligned, int* P, int* PT, bool* f16_parts, int Pc = 0) {
+  if (Pc <= 0) Pc = (max_ctx / d->block_size + 31) / 32;
   const int elem = d->q_dtype == TL_DTYPE_F32 ? 4 : 2;
   *f16_parts = d->q_dtype == TL_DTYPE_F16 && uses_mfma(d);
   const int cap = tmp_aligned ? (*f16_parts ? Pc : Pc * elem / 4) : 1;
@@ -344,18 +347,19 @@ int tl_paged_attention_v1(void* out, const void* q, const void* k_cache, const v
   return run(make_launch(&d, out, q, k_cache, v_cache, block_tables, seq_lens, stream));
 }
 
-int tl_paged_attention_v2(void* out, float* exp_sums, float* max_logits, void* tmp_out,
-                          const void* q, const void* k_cache, const void* v_cache,
-                          const int32_t* block_tables, const int32_t* seq_lens, int32_t num_seqs,
-                          int32_t num_heads, int32_t num_kv_heads, int32_t head_size,
-                          int32_t block_size, int32_t max_blocks_per_seq, int32_t num_blocks,
-                          float scale, int32_t dtype, int32_t gqa_map, int32_t max_context_len,
-                          void* stream) {
+static int v2_impl(void* out, float* exp_sums, float* max_logits, void* tmp_out, const void* q,
+                   const void* k_cache, const void* v_cache, const int32_t* block_tables, const int32_t* seq_lens,
+                   int32_t num_seqs, int32_t num_heads, int32_t num_kv_heads, int32_t head_size,
+                   int32_t block_size, int32_t max_blocks_per_seq, int32_t num_blocks, float scale, int32_t dtype,
+                   int32_t gqa_map, int32_t max_context_len, int32_t scratch_partitions, void* stream) {
   tl_decode_desc d = {num_seqs, num_heads, num_kv_heads, head_size, block_size, max_blocks_per_seq,
                       num_blocks, dtype, dtype, gqa_map, 0, scale, 1.f, 1.f};
   int rc = check_decode(&d);
   if (rc) return rc;
   if (max_context_len < 0) return fail(TL_ERR_INVALID_ARGUMENT, "max_context_len < 0");
+  if (scratch_partitions > 0 && scratch_partitions < (max_context_len / block_size + 31) / 32)
+    return fail(TL_ERR_INVALID_ARGUMENT, "scratch_partitions=%d below the %d partitions of max_context_len=%d",
+                scratch_partitions, (max_context_len / block_size + 31) / 32, max_context_len);
   if (num_seqs == 0) return ok();
   if (!out || !q || !k_cache || !v_cache || !block_tables || !seq_lens || !exp_sums ||
       !max_logits || !tmp_out)
@@ -364,7 +368,7 @@ int tl_paged_attention_v2(void* out, float* exp_sums, float* max_logits, void* t
     return fail(TL_ERR_INVALID_ARGUMENT, "k_cache/v_cache must be 16-byte aligned");
   int P, PT;
   bool f16_parts;
-  v2_plan(&d, max_context_len, aligned16(tmp_out), &P, &PT, &f16_parts);
+  v2_plan(&d, max_context_len, aligned16(tmp_out), &P, &PT, &f16_parts, scratch_partitions);
   tl::DecodeLaunch a = make_launch(&d, out, q, k_cache, v_cache, block_tables, seq_lens, stream);
   if (P > 1) {
     a.num_partitions = P;
@@ -377,18 +381,60 @@ int tl_paged_attention_v2(void* out, float* exp_sums, float* max_logits, void* t
   return run(a);
 }
 
-int32_t tl_paged_attention_v2_partitions(int32_t num_seqs, int32_t num_heads, int32_t num_kv_heads,
-                                         int32_t head_size, int32_t block_size, int32_t dtype,
-                                         int32_t max_context_len, int32_t* partition_tokens) {
+int tl_paged_attention_v2(void* out, float* exp_sums, float* max_logits, void* tmp_out,
+                          const void* q, const void* k_cache, const void* v_cache,
+                          const int32_t* block_tables, const int32_t* seq_lens, int32_t num_seqs,
+                          int32_t num_heads, int32_t num_kv_heads, int32_t head_size,
+                          int32_t block_size, int32_t max_blocks_per_seq, int32_t num_blocks,
+                          float scale, int32_t dtype, int32_t gqa_map, int32_t max_context_len,
+                          void* stream) {
+  return v2_impl(out, exp_sums, max_logits, tmp_out, q, k_cache, v_cache, block_tables, seq_lens, num_seqs,
+                 num_heads, num_kv_heads, head_size, block_size, max_blocks_per_seq, num_blocks, scale, dtype,
+                 gqa_map, max_context_len, 0, stream);
+}
+
+int tl_paged_attention_v2_capacity(void* out, float* exp_sums, float* max_logits, void* tmp_out,
+                                   const void* q, const void* k_cache, const void* v_cache,
+                                   const int32_t* block_tables, const int32_t* seq_lens, int32_t num_seqs,
+                                   int32_t num_heads, int32_t num_kv_heads, int32_t head_size,
+                                   int32_t block_size, int32_t max_blocks_per_seq, int32_t num_blocks,
+                                   float scale, int32_t dtype, int32_t gqa_map, int32_t max_context_len,
+                                   int32_t scratch_partitions, void* stream) {
+  if (scratch_partitions <= 0) return fail(TL_ERR_INVALID_ARGUMENT, "scratch_partitions=%d", scratch_partitions);
+  return v2_impl(out, exp_sums, max_logits, tmp_out, q, k_cache, v_cache, block_tables, seq_lens, num_seqs,
+                 num_heads, num_kv_heads, head_size, block_size, max_blocks_per_seq, num_blocks, scale, dtype,
+                 gqa_map, max_context_len, scratch_partitions, stream);
+}
+
+static int32_t v2_partitions_impl(int32_t num_seqs, int32_t num_heads, int32_t num_kv_heads, int32_t head_size,
+                                  int32_t block_size, int32_t dtype, int32_t max_context_len,
+                                  int32_t scratch_partitions, int32_t* partition_tokens) {
   tl_decode_desc d = {num_seqs, num_heads, num_kv_heads, head_size, block_size, 1, 1,
                       dtype, dtype, TL_GQA_MODULO, 0, 1.f, 1.f, 1.f};
   if (check_decode(&d) != TL_OK || max_context_len < 0) return -1;
+  if (scratch_partitions > 0 && scratch_partitions < (max_context_len / block_size + 31) / 32) return -1;
   int P, PT;
   bool f16_parts;
-  v2_plan(&d, max_context_len, true, &P, &PT, &f16_parts);
+  v2_plan(&d, max_context_len, true, &P, &PT, &f16_parts, scratch_partitions);
   if (partition_tokens) *partition_tokens = P > 1 ? PT : 0;
   ok();
   return P;
+}
+
+int32_t tl_paged_attention_v2_partitions(int32_t num_seqs, int32_t num_heads, int32_t num_kv_heads,
+                                         int32_t head_size, int32_t block_size, int32_t dtype,
+                                         int32_t max_context_len, int32_t* partition_tokens) {
+  return v2_partitions_impl(num_seqs, num_heads, num_kv_heads, head_size, block_size, dtype, max_context_len, 0,
+                            partition_tokens);
+}
+
+int32_t tl_paged_attention_v2_capacity_partitions(int32_t num_seqs, int32_t num_heads, int32_t num_kv_heads,
+                                                  int32_t head_size, int32_t block_size, int32_t dtype,
+                                                  int32_t max_context_len, int32_t scratch_partitions,
+                                                  int32_t* partition_tokens) {
+  if (scratch_partitions <= 0) return -1;
+  return v2_partitions_impl(num_seqs, num_heads, num_kv_heads, head_size, block_size, dtype, max_context_len,
+                            scratch_partitions, partition_tokens);
 }
 
 int tl_reshape_and_cache(const void* key, const void* value, void* k_cache, void* v_cache,

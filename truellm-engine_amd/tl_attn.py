@@ -118,7 +118,10 @@ _SIG = {
     "tl_paged_attention_decode_noalloc": (ctypes.c_int, [ctypes.POINTER(DecodeDesc), _P, _P, _P, _P, _P, _P, _I, _P]),
     "tl_paged_attention_v1": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F, _I, _I, _P]),
     "tl_paged_attention_v2": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F, _I, _I, _I, _P]),
+    "tl_paged_attention_v2_capacity": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F, _I,
+                                                      _I, _I, _I, _P]),
     "tl_paged_attention_v2_partitions": (_I, [_I, _I, _I, _I, _I, _I, _I, _P]),
+    "tl_paged_attention_v2_capacity_partitions": (_I, [_I, _I, _I, _I, _I, _I, _I, _I, _P]),
     "tl_reshape_and_cache": (ctypes.c_int, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P]),
     "tl_reshape_and_cache_fp8": (ctypes.c_int, [_P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _I, _F, _F, _P]),
     "tl_rope_reshape_and_cache": (ctypes.c_int, [_P] * 10 + [_I] * 9 + [_P]),
@@ -174,7 +177,7 @@ def _hip_runtimes() -> set:
         return set()
 
 
-ABI_VERSION = 4           # TL_ABI_VERSION of include/tl_attn.h
+ABI_VERSION = 5           # TL_ABI_VERSION of include/tl_attn.h
 
 
 def _load() -> ctypes.CDLL:
@@ -265,15 +268,20 @@ def paged_attention_v1(out, q, k_cache, v_cache, block_tables, seq_lens, num_kv_
 
 def paged_attention_v2(out, exp_sums, max_logits, tmp_out, q, k_cache, v_cache, block_tables,
                        seq_lens, num_kv_heads, scale, head_size, block_size, max_context_len,
-                       stream=None, gqa_map=GQA_MODULO):
+                       stream=None, gqa_map=GQA_MODULO, scratch_partitions=None):
     """paged_attention_v2.cu:176: scratch exp_sums/max_logits [S, H, P] fp32,
-    tmp_out [S, H, P, D] in q's dtype, P = ceil(max_context_len / (32 * BS))."""
+    tmp_out [S, H, P, D] in q's dtype, P = ceil(max_context_len / (32 * BS)).
+    scratch_partitions: the P the scratch was allocated for, when larger
+    (tl_paged_attention_v2_capacity)."""
     S, H = q.shape[0], q.shape[1]
-    check(lib.tl_paged_attention_v2(
-        _ptr(out), _ptr(exp_sums), _ptr(max_logits), _ptr(tmp_out), _ptr(q), _ptr(k_cache),
-        _ptr(v_cache), _ptr(block_tables), _ptr(seq_lens), S, H, num_kv_heads, head_size,
-        block_size, block_tables.shape[1], k_cache.shape[0], scale, dtype_code(q), gqa_map,
-        max_context_len, _stream(stream)))
+    args = [_ptr(out), _ptr(exp_sums), _ptr(max_logits), _ptr(tmp_out), _ptr(q), _ptr(k_cache),
+            _ptr(v_cache), _ptr(block_tables), _ptr(seq_lens), S, H, num_kv_heads, head_size,
+            block_size, block_tables.shape[1], k_cache.shape[0], scale, dtype_code(q), gqa_map,
+            max_context_len]
+    if scratch_partitions is None:
+        check(lib.tl_paged_attention_v2(*args, _stream(stream)))
+    else:
+        check(lib.tl_paged_attention_v2_capacity(*args, scratch_partitions, _stream(stream)))
 
 
 def convert_fp8(out, inp, scale, stream=None, n=None):
@@ -283,12 +291,19 @@ def convert_fp8(out, inp, scale, stream=None, n=None):
     check(lib.tl_convert_fp8(_ptr(out), _ptr(inp), dtype_code(inp), n, scale, _stream(stream)))
 
 
-def v2_plan(num_seqs, num_heads, num_kv_heads, head_size, block_size, dtype, max_context_len):
-    """(partitions, partition_tokens) of tl_paged_attention_v2 for a call of
+def v2_plan(num_seqs, num_heads, num_kv_heads, head_size, block_size, dtype, max_context_len,
+            scratch_partitions=None):
+    """(partitions, partition_tokens) of tl_paged_attention_v2 (with
+    scratch_partitions, of tl_paged_attention_v2_capacity) for a call of
     these sizes."""
     pt = ctypes.c_int32(0)
-    P = lib.tl_paged_attention_v2_partitions(num_seqs, num_heads, num_kv_heads, head_size, block_size, dtype,
-                                             max_context_len, ctypes.byref(pt))
+    if scratch_partitions is None:
+        P = lib.tl_paged_attention_v2_partitions(num_seqs, num_heads, num_kv_heads, head_size, block_size, dtype,
+                                                 max_context_len, ctypes.byref(pt))
+    else:
+        P = lib.tl_paged_attention_v2_capacity_partitions(num_seqs, num_heads, num_kv_heads, head_size, block_size,
+                                                          dtype, max_context_len, scratch_partitions,
+                                                          ctypes.byref(pt))
     if P < 0:
         raise TLError(ERR_INVALID_ARGUMENT, "tl_paged_attention_v2_partitions: sizes refused")
     return P, pt.value
