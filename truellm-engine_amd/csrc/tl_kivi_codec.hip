@@ -145,9 +145,25 @@ __global__ __launch_bounds__(128) void kivi_page_kernel(PageJob j) {
     kivi_append_token<128>(j, seq, kvh, tid);
     if (j.build_ahead) {
       // the pages this append completes were written in pieces by the
-      // appends before it; this one writes its piece of the next page
-      if (piece >= 0 && tid < kWave)
-        kivi_build_piece<BITS>(j, seq, kvh, ahead_page, piece, tid, &sm.qk[0][0]);
+      // appends before it; this one writes its piece of the next page:
+      // wavefront 0 stages its fp16, then each wavefront quantises two of
+      // its quarters
+      if (piece < 0) return;
+      __shared__ int s_pid;
+      uint16_t* raw = reinterpret_cast<uint16_t*>(&sm.qk[0][0]);
+      const int lane = tid % kWave, wave = tid / kWave;
+      if (wave == 0) {
+        KiviPiece pc = kivi_piece_plan(j, seq, ahead_page, piece, lane);
+        kivi_piece_load(j, pc, kvh, ahead_page, lane);
+        kivi_piece_stage(pc, lane, raw);
+        if (lane == 0) s_pid = pc.piece >= 0 ? pc.pid : -1;
+      }
+      __syncthreads();
+      const int pid = s_pid;
+      if (pid < 0) return;
+      for (int q = wave; q < 4; q += 128 / kWave)
+        kivi_piece_quarter<BITS>(j, pid, piece, kvh, q, lane, kivi_piece_quarter_values(piece, q, lane, raw),
+                                 &sm.qv[0][0] + 256 * q);
       return;
     }
     if (lq == 0 || lq == kivi_quantized_len(L - 1, j.residual_length)) return;

@@ -381,16 +381,16 @@ __device__ __forceinline__ void scan_combine_lanes(float& mn, float& mx, int lan
   }
 }
 
-// A piece in three phases, so that a wavefront can spread it over other
-// work: plan (the page slot and the pool blocks: table reads), load (the
-// 2 KiB of fp16 it quantises), finish (quantise, then write).  Stores count
-// on the same in-order counter as loads, so a wavefront that still has
-// loads to wait for writes its piece after them.
-// K piece: lane = channel cl = lane / 2 of the piece (octet piece + 4 m,
-// m = cl / 8, channel ci = cl % 8 of it) over tokens 16 th .. 16 th + 15
-// (th = lane % 2), two runs of 8, each inside one block.  V piece: lane =
-// channels lane and lane + 64 (index lane % 32 of groups lane / 32 and
-// 2 + lane / 32) over the 8 token slots of lane group r, two runs of 4.
+// A piece in phases that a workgroup can spread over other work: one
+// wavefront plans it (the page slot and the pool blocks: table reads),
+// loads the 2 KiB of fp16 it quantises and stages them in LDS; after a
+// workgroup barrier each of four quarters is quantised and written by one
+// wavefront.  Stores count on the same in-order counter as loads, so a
+// wavefront that still has loads to wait for writes its quarter after them.
+// Loads: K piece: lane = channel cl = lane / 2 of the piece over tokens
+// 16 th .. 16 th + 15 (th = lane % 2), two runs of 8, each inside one
+// block.  V piece: lane = channels lane and lane + 64 over the 8 token
+// slots of lane group r, two runs of 4.
 struct KiviPiece {
   int piece;        // -1: nothing to write
   int pid;          // page table entry (checked by the load phase)
@@ -449,123 +449,6 @@ __device__ __forceinline__ void kivi_piece_load(const PageJob& j, KiviPiece& pc,
         pc.w[4 * h2 + 2 * r] = v.x;
         pc.w[4 * h2 + 2 * r + 1] = v.y;
       }
-  }
-}
-
-// Quantise and write (scratch: 1 KiB of the wavefront's own LDS).
-template <int BITS>
-__device__ void kivi_piece_finish(const PageJob& j, const KiviPiece& pc, int kvh, int lane, uint8_t* scratch) {
-  using F = KiviFmt<BITS>;
-  constexpr int LV = F::kLevels;
-  if (pc.piece < 0) return;
-  uint8_t* dst = j.pages + ((int64_t)pc.pid * j.num_kv_heads + kvh) * F::kBytes;
-  const int piece = pc.piece;
-  auto half = [&](int e) { return f16_to_f32((uint16_t)(pc.w[e >> 1] >> (16 * (e & 1)))); };
-  if (piece < 4) {
-    const int cl = lane >> 1, th = lane & 1, m = cl >> 3, ci = cl & 7;
-    const int o = piece + 4 * m;
-    float x[16];
-#pragma unroll
-    for (int e = 0; e < 16; ++e) x[e] = half(e);
-    float mn = FLT_MAX, mx = -FLT_MAX;
-#pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      if (x[e] < mn) mn = x[e];
-      if (x[e] > mx) mx = x[e];
-    }
-    scan_combine_lanes<1, 1>(mn, mx, lane);
-    const GroupQ q = group_params<LV>(mn, mx);
-#pragma unroll
-    for (int e = 0; e < 16; ++e) scratch[(16 * th + e) * 32 + cl] = (uint8_t)quantise<LV>(x[e], q);
-    if (th == 0) {
-      uint16_t* kp = reinterpret_cast<uint16_t*>(dst + F::kKParams + o * 32);
-      kp[ci] = q.step;
-      kp[8 + ci] = q.zero;
-    }
-    build_barrier<kWave>();
-    // code dwords of chunks 64 tt + 16 piece + u: row t = 16 tt + u of the
-    // scratch holds the piece's 32 channels, octet piece + 4 m at bytes 8 m
-    constexpr int kWords = F::kChunk / 4;               // dwords per chunk
-    constexpr int kPerLane = 2 * 16 * kWords / kWave;   // 2 (INT4) or 4 (INT8)
-#pragma unroll
-    for (int e = 0; e < kPerLane; ++e) {
-      const int w = kPerLane * lane + e;
-      const int tt = w / (16 * kWords), u = (w / kWords) % 16, dd = w % kWords;
-      const int t = 16 * tt + u;
-      uint32_t x4;
-      if constexpr (BITS == 8) {
-        // dword 2 m + h: channels 8 o + 4 h + {0, 2, 1, 3}
-        const uint8_t* b = scratch + t * 32 + 8 * (dd >> 1) + 4 * (dd & 1);
-        x4 = (uint32_t)b[0] | (uint32_t)b[2] << 8 | (uint32_t)b[1] << 16 | (uint32_t)b[3] << 24;
-      } else {
-        // dword m: channel 8 o + 2 i + hb at bit 16 hb + 4 i
-        const uint8_t* b = scratch + t * 32 + 8 * dd;
-        x4 = 0;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) x4 |= (uint32_t)b[2 * i] << (4 * i) | (uint32_t)b[2 * i + 1] << (16 + 4 * i);
-      }
-      const int chunk = 64 * tt + 16 * piece + u;
-      *reinterpret_cast<uint32_t*>(dst + F::kKCodes + chunk * F::kChunk + 4 * dd) = x4;
-    }
-    build_barrier<kWave>();   // the scratch may be reused
-  } else {
-    // V: the 8 tokens' fp16 go to the scratch as [slot][channel]; lane
-    // 4 s + g (< 32) scans group g of slot s in channel order as
-    // kivi_build_page does, writes its (step, zero) and its 32 codes as
-    // [channel][slot] bytes over the fp16 it has read (the wavefront's
-    // reads all come before its writes); then every lane packs the 8 slots
-    // of channels lane and lane + 64.
-    const int r = piece - 4;
-    uint16_t* xs = reinterpret_cast<uint16_t*>(scratch);
-#pragma unroll
-    for (int h2 = 0; h2 < 2; ++h2)
-#pragma unroll
-      for (int sl = 0; sl < 8; ++sl) xs[sl * kKiviHead + lane + 64 * h2] = (uint16_t)(pc.w[4 * h2 + (sl >> 1)] >> (16 * (sl & 1)));
-    build_barrier<kWave>();
-    if (lane < 32) {
-      const int sl = lane >> 2, g = lane & 3;
-      u32x4 raw[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) raw[i] = *reinterpret_cast<const u32x4*>(xs + sl * kKiviHead + 32 * g + 8 * i);
-      float x[32];
-#pragma unroll
-      for (int i = 0; i < 32; ++i) x[i] = f16_to_f32((uint16_t)(word(raw[i >> 3], (i & 7) >> 1) >> (16 * (i & 1))));
-      float mn = FLT_MAX, mx = -FLT_MAX;
-#pragma unroll
-      for (int i = 0; i < 32; ++i) {
-        if (x[i] < mn) mn = x[i];
-        if (x[i] > mx) mx = x[i];
-      }
-      const GroupQ q = group_params<LV>(mn, mx);
-      uint16_t* vp = reinterpret_cast<uint16_t*>(dst + F::kVParams + (g * 4 + r) * 32);
-      vp[sl] = q.step;
-      vp[8 + sl] = q.zero;
-#pragma unroll
-      for (int i = 0; i < 32; ++i) scratch[(32 * g + i) * 8 + sl] = (uint8_t)quantise<LV>(x[i], q);
-    }
-    build_barrier<kWave>();
-    // channel c = (4 hh + m) 16 + u: chunk 64 hh + 16 r + u
-    const int m = (lane >> 4) & 3, u = lane & 15;
-#pragma unroll
-    for (int h2 = 0; h2 < 2; ++h2) {
-      const uint2 cw = *reinterpret_cast<const uint2*>(scratch + (lane + 64 * h2) * 8);
-      auto cd = [&](int sl) { return (uint32_t)(((sl < 4 ? cw.x : cw.y) >> (8 * (sl & 3))) & 0xFFu); };
-      uint8_t* chunk = dst + F::kVCodes + (64 * h2 + 16 * r + u) * F::kChunk;
-      if constexpr (BITS == 8) {
-        // dword 2 m + h: slots 4 h + {0, 2, 1, 3}
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-          *reinterpret_cast<uint32_t*>(chunk + 4 * (2 * m + h)) =
-              cd(4 * h) | cd(4 * h + 2) << 8 | cd(4 * h + 1) << 16 | cd(4 * h + 3) << 24;
-      } else {
-        // slot s at bit 16 (s & 1) + 4 (s >> 1)
-        uint32_t y = 0;
-#pragma unroll
-        for (int sl = 0; sl < 8; ++sl) y |= cd(sl) << (16 * (sl & 1) + 4 * (sl >> 1));
-        *reinterpret_cast<uint32_t*>(chunk + 4 * m) = y;
-      }
-    }
-    build_barrier<kWave>();   // the scratch may be reused
   }
 }
 
@@ -687,16 +570,6 @@ __device__ void kivi_piece_quarter(const PageJob& j, int pid, int piece, int kvh
       }
     }
   }
-}
-
-// The three phases in a row, for a wavefront with nothing else to do.  Every
-// token of the page must be in the pool.
-template <int BITS>
-__device__ void kivi_build_piece(const PageJob& j, int seq, int kvh, int page, int piece, int lane,
-                                 uint8_t* scratch) {
-  KiviPiece pc = kivi_piece_plan(j, seq, page, piece, lane);
-  kivi_piece_load(j, pc, kvh, page, lane);
-  kivi_piece_finish<BITS>(j, pc, kvh, lane, scratch);
 }
 
 }  // namespace tl
