@@ -437,6 +437,19 @@ __device__ __forceinline__ void page_pair(PageState& st, const PageRaw<BITS>& ra
 // loads in flight while a pair is computed (two register sets, alternating).
 // The pair's parameters go through the wavefront's 2 KiB LDS slot s_par_w
 // (page a at 0, page b at 256 dwords; K params first, V params at 128).
+// The page wavefronts' q operand as loaded: lane (grp, u) holds q[head u of
+// the slice] at channels 32 m + 8 grp .. + 7, zero for the padding heads.
+__device__ __forceinline__ void load_q_operand(const Params& p, int seq, int kvh, int hs, int lane,
+                                               u32x4 (&q_raw)[4]) {
+  const int grp = lane >> 4, u = lane & 15;
+  const int gi = hs * kWaveHeads + u;
+  const bool real = u < kWaveHeads && gi < p.group;
+  const uint16_t* qrow = (const uint16_t*)p.q +
+      ((int64_t)seq * p.num_heads + (real ? head_of(p, kvh, gi) : 0)) * kKiviHead;
+#pragma unroll
+  for (int m = 0; m < 4; ++m) q_raw[m] = real ? load16(qrow + 32 * m + 8 * grp) : u32x4{0u, 0u, 0u, 0u};
+}
+
 // share_simd: raise the wavefront's priority on every other page pair (see
 // kivi_decode_kernel).  early_ok: early_id is the table entry of page
 // pg_begin + lane * pg_step, read by the caller ahead of time (unchecked;
@@ -446,27 +459,21 @@ __device__ __forceinline__ void kivi_pages_wave(const KiviParams& k, int seq, in
                                                 int pg_begin, int pg_end, int pg_step,
                                                 uint32_t* s_par_w, float* s_acc_w, float* s_m_w,
                                                 float* s_l_w, bool share_simd, bool early_ok, int early_id,
-                                                const RopeTable* s_rope) {
+                                                const RopeTable* s_rope, const u32x4 (&q_raw)[4]) {
   constexpr int GT = kWaveHeads;
   const Params& p = k.base;
   const int lane = threadIdx.x % kWave;
   const int grp = lane >> 4, u = lane & 15;     // lane group (k slots), row / column index
 
-  // B operand of q.k: head u (real for u < GT), channels 32 m + 8 grp .. +7,
-  // times scale * log2(e); zero for the padding heads
+  // B operand of q.k (q_raw: load_q_operand) times scale * log2(e)
   // INT4: the nibble pairs at bits 4 and 20 come out 16 times too large
   const _Float16 one = (_Float16)1.0f, sixteenth = (_Float16)(BITS == 8 ? 1.0f : 0.0625f);
   const h8 slot_scale = {one, one, sixteenth, sixteenth, one, one, sixteenth, sixteenth};
   u32x4 qsc[4], qss[4];   // q * scale * log2(e); the same times slot_scale
-  const int gi = hs * GT + u;
-  const bool real = u < GT && gi < p.group;
-  const uint16_t* qrow = (const uint16_t*)p.q +
-      ((int64_t)seq * p.num_heads + (real ? head_of(p, kvh, gi) : 0)) * kKiviHead;
   const _Float16 qs = (_Float16)p.qk_scale;
 #pragma unroll
   for (int m = 0; m < 4; ++m) {
-    const u32x4 raw = real ? load16(qrow + 32 * m + 8 * grp) : u32x4{0u, 0u, 0u, 0u};
-    const h8 v = as_h8(raw) * qs;
+    const h8 v = as_h8(q_raw[m]) * qs;
     qsc[m] = __builtin_bit_cast(u32x4, v);
     qss[m] = __builtin_bit_cast(u32x4, v * slot_scale);
   }
@@ -851,6 +858,15 @@ __global__ __launch_bounds__(NW * kWave, 2) void kivi_decode_kernel(KiviParams k
   // are read before L is known, for the usual split (NW - 1 page
   // wavefronts, the last one on the window), so the first page loads wait
   // for one memory round trip instead of two.
+  // The q operand is loaded here, with the length and the table entries,
+  // so that the first page loads wait for one memory round trip, not for q
+  // after the length (interleaved A/B, us per step: INT4 65.0 -> 64.6, mixed
+  // lengths 67.6 -> 66.7, INT8 113.3 -> 112.9, INT4 keys before RoPE 111.9
+  // -> 111.4).  INT8 with keys before RoPE loads it where it is used: its
+  // registers are short, and 16 more held from here cost it 1.1 us.
+  constexpr bool kQEarly = !(BITS == 8 && ROPE);
+  u32x4 q_raw[4];
+  if constexpr (kQEarly) load_q_operand(p, seq, kvh, hs, tid % kWave, q_raw);
   int early_id = -1;
   if constexpr (FINAL) {
     const int pg = wave + (tid % kWave) * (NW - 1);
@@ -891,6 +907,7 @@ __global__ __launch_bounds__(NW * kWave, 2) void kivi_decode_kernel(KiviParams k
       store_newest<BS>(k.job, newest_from_row(k.job, seq, kvh, tid), seq, kvh, tid);
   }
   if (wave < page_waves) {
+    if constexpr (!kQEarly) load_q_operand(p, seq, kvh, hs, tid % kWave, q_raw);
     // Single pass runs two workgroups per CU, b and b + grid/2 (dispatch
     // order), and the SIMDs issue the oldest wavefront first: left alone
     // workgroup b finishes about 10 us before b + grid/2 (48.5 against 59.4
@@ -899,7 +916,7 @@ __global__ __launch_bounds__(NW * kWave, 2) void kivi_decode_kernel(KiviParams k
     // and 58.5 us).
     kivi_pages_wave<BITS, ROPE>(k, seq, kvh, hs, pg0 + wave, pg1 - res_pages, page_waves, &sd.p[wave][0], &sd.acc[wave][0][0],
                     &sd.m[wave][0], &sd.l[wave][0], FINAL && blockIdx.x >= gridDim.x / 2,
-                    FINAL && page_waves == NW - 1, early_id, s_rope);
+                    FINAL && page_waves == NW - 1, early_id, s_rope, q_raw);
   } else {
     const int lane = tid % kWave;
     // build-ahead: this step's piece of the next page (one head slice
@@ -933,8 +950,9 @@ __global__ __launch_bounds__(NW * kWave, 2) void kivi_decode_kernel(KiviParams k
     // path (the window ends halfway through the launch)
     if constexpr (APPEND) store_newest<BS>(k.job, nt, seq, kvh, lane);
     if constexpr (APPEND && !ROPE) kivi_piece_load(k.job, piece, kvh, ahead_page, lane);
+    if constexpr (!kQEarly) load_q_operand(p, seq, kvh, hs, lane, q_raw);
     kivi_pages_wave<BITS, ROPE>(k, seq, kvh, hs, pg1 - res_pages, pg1, 1, &sd.p[wave][0], &sd.acc[NW + 1][0][0],
-                    &sd.m[NW + 1][0], &sd.l[NW + 1][0], false, false, -1, s_rope);
+                    &sd.m[NW + 1][0], &sd.l[NW + 1][0], false, false, -1, s_rope, q_raw);
     // the piece's fp16 for the quarters after the merge
     if constexpr (APPEND) {
       if (piece_due) {
