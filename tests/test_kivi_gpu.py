@@ -469,6 +469,35 @@ def test_kivi_pre_rope_decode_matches_oracle(style, bits, pp):
                                                  short_s, style, ws)
 
 
+@pytest.mark.parametrize("style", [tla.ROPE_ADJACENT, tla.ROPE_HALVES])
+@pytest.mark.parametrize("bits", [4, 8])
+def test_kivi_pre_rope_long_single_pass(style, bits):
+    """A workgroup takes the rotations of its first pages (128 at INT4, 112
+    at INT8) from LDS and those of later pages from the tables: single-pass
+    sequences of 155, 135 and 114 pages use both, against the oracle; a page
+    past the LDS rows is a hole."""
+    from test_oracle import rope_tables
+    kc = KiviCase(58, [5100, 4460, 3800, 900], bits=bits)
+    kc.page_tables[0, 140] = -1
+    pages_np = kc.oracle_pages()
+    cos_t, sin_t = rope_tables(5100, 128)
+    qd, kd, vd = dev(kc.q, orc.F16), dev(kc.k, orc.F16), dev(kc.v, orc.F16)
+    btd, sld, ptd = dev(kc.tables), dev(kc.lens), dev(kc.page_tables)
+    pages = torch.from_numpy(pages_np).cuda()
+    desc = kc.desc(qd, kd, btd, ptd, -1)
+    desc.pre_rope_keys = 1
+    max_ctx = int(kc.lens.max())
+    ws = torch.empty(max(16, tla.kivi_workspace_bytes(desc, max_ctx)), dtype=torch.uint8, device="cuda")
+    out = torch.full_like(qd, float("nan"))
+    print(f"case kivi pre-rope long single pass style={style} bits={bits}", flush=True)
+    tla.kivi_paged_attention_decode_pre_rope(desc, out, qd, pages, ptd, kd, vd, btd, sld, max_ctx, dev(cos_t),
+                                             dev(sin_t), style, ws)
+    torch.cuda.synchronize()
+    want = orc.kivi_paged_attention(kc.q, orc.F16, pages_np, kc.page_tables, kc.k, kc.v, kc.tables, kc.lens,
+                                    kc.n_kv, kc.R, kc.scale, orc.GROUPED, bits, pre_rope=(cos_t, sin_t, style))
+    assert_close(out, want, orc.F16, ATOL_KIVI, f"style={style} bits={bits} long single pass")
+
+
 @pytest.mark.parametrize("H,n_kv", [(16, 8), (64, 8), (8, 8)])
 @pytest.mark.parametrize("gqa", [tla.GQA_GROUPED, tla.GQA_MODULO])
 def test_kivi_pre_rope_decode_group_sizes(H, n_kv, gqa):

@@ -133,6 +133,37 @@ __device__ __forceinline__ h8 rope_lds(const RopeTable& tb, int which, int j, in
   return *reinterpret_cast<const h8*>(&tb.cs[which][j][32 * m + 8 * grp]);
 }
 
+// The page rotations R_{32 p} of a workgroup's pages first .. first + count
+// - 1 in LDS, filled at its start: cs[p - first][cos | sin][pair] in f16,
+// converted as rope_coef_block0/1 convert the table rows (so both give the
+// same bits).  The q rotation of a page then reads LDS; read from the
+// tables where it is used, it waited for every page load in flight (the
+// next pair's included), one memory round trip per page: INT4 with keys
+// before RoPE took 111.7 us per step, 88.1-88.6 with the coefficients
+// taken as constants (timing only).
+struct PageRot {
+  const uint16_t* cs;   // [count][2][64]
+  int first, count;
+};
+// pages the table holds: what leaves two workgroups per CU (at most 80 KiB
+// of LDS each) beside the rest of the kernel's LDS
+template <int BITS> constexpr int kivi_page_rot_cap() { return BITS == 8 ? 112 : 128; }
+
+// rope_coef_block0/1 from the LDS row of a page
+__device__ __forceinline__ void rope_coef_row0(const uint16_t* row, int m, int grp, h8& c, h8& s) {
+  typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+  const h4 cv = __builtin_bit_cast(h4, *reinterpret_cast<const uint2*>(row + 16 * m + 4 * grp));
+  const h4 sv = __builtin_bit_cast(h4, *reinterpret_cast<const uint2*>(row + kKiviHead / 2 + 16 * m + 4 * grp));
+  const h4 ns = -sv;
+  c = __builtin_shufflevector(cv, cv, 0, 0, 1, 1, 2, 2, 3, 3);
+  s = __builtin_shufflevector(ns, sv, 0, 4, 1, 5, 2, 6, 3, 7);
+}
+__device__ __forceinline__ void rope_coef_row1(const uint16_t* row, int m, int grp, h8& c, h8& sa, h8& sb) {
+  c = *reinterpret_cast<const h8*>(row + 32 * m + 8 * grp);
+  sb = *reinterpret_cast<const h8*>(row + kKiviHead / 2 + 32 * m + 8 * grp);
+  sa = -sb;
+}
+
 // Eight nibbles n_j (slot j at bit 16 (j & 1) + 4 (j >> 1)) as fp16
 // denormals: a masked nibble pair is the fp16 pair (n * 2^-24, n' * 2^-24),
 // or 16 n * 2^-24 for the pairs at bits 4 and 20 (slots 2, 3, 6, 7; the
@@ -267,7 +298,8 @@ template <int BITS, bool ROPE>
 __device__ __forceinline__ void page_pair(PageState& st, const PageRaw<BITS>& ra, const PageRaw<BITS>& rb, bool oka,
                                           bool okb, const u32x4 (&qsc)[4], const u32x4 (&qss)[4],
                                           uint32_t* s_par_w, int lane, const h8& slot_scale,
-                                          const KiviParams& k, int pga, int pgb, const RopeTable* s_rope) {
+                                          const KiviParams& k, int pga, int pgb, const RopeTable* s_rope,
+                                          const PageRot& prot) {
   constexpr int GT = kWaveHeads;
   const int grp = lane >> 4, u = lane & 15;
 
@@ -292,7 +324,11 @@ __device__ __forceinline__ void page_pair(PageState& st, const PageRaw<BITS>& ra
     for (int pi = 0; pi < 2; ++pi) {
       const PageRaw<BITS>& r = pi ? rb : ra;
       const uint32_t* par = s_par_w + pi * 256;
-      const int t0 = 32 * (pi ? pgb : pga);
+      const int pg = pi ? pgb : pga;
+      const int t0 = 32 * pg;
+      const int ci = pg - prot.first;               // wave-uniform
+      const bool from_lds = ci >= 0 && ci < prot.count;
+      const uint16_t* row = prot.cs + (int64_t)(from_lds ? ci : 0) * kKiviHead;
       h8 qp[4];
 #pragma unroll
       for (int m = 0; m < 4; ++m) qp[m] = as_h8(qsc[m]);
@@ -300,14 +336,16 @@ __device__ __forceinline__ void page_pair(PageState& st, const PageRaw<BITS>& ra
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
           h8 c, sn;
-          rope_coef_block0(k, t0, m, grp, c, sn);
+          if (from_lds) rope_coef_row0(row, m, grp, c, sn);
+          else rope_coef_block0(k, t0, m, grp, c, sn);
           rope_one_block<true>(qp[m], c, sn);
         }
       } else {
 #pragma unroll
         for (int m = 0; m < 2; ++m) {
           h8 c, sa, sb;
-          rope_coef_block1(k, t0, m, grp, c, sa, sb);
+          if (from_lds) rope_coef_row1(row, m, grp, c, sa, sb);
+          else rope_coef_block1(k, t0, m, grp, c, sa, sb);
           rope_pair_blocks<true>(qp[m], qp[m + 2], c, sa, c, sb);
         }
       }
@@ -459,7 +497,8 @@ __device__ __forceinline__ void kivi_pages_wave(const KiviParams& k, int seq, in
                                                 int pg_begin, int pg_end, int pg_step,
                                                 uint32_t* s_par_w, float* s_acc_w, float* s_m_w,
                                                 float* s_l_w, bool share_simd, bool early_ok, int early_id,
-                                                const RopeTable* s_rope, const u32x4 (&q_raw)[4]) {
+                                                const RopeTable* s_rope, const PageRot& prot,
+                                                const u32x4 (&q_raw)[4]) {
   constexpr int GT = kWaveHeads;
   const Params& p = k.base;
   const int lane = threadIdx.x % kWave;
@@ -542,13 +581,13 @@ __device__ __forceinline__ void kivi_pages_wave(const KiviParams& k, int seq, in
       fetch(r1a, r1b, o + 2);
       if (share_simd) __builtin_amdgcn_s_setprio(1);
       page_pair<BITS, ROPE>(st, r0a, r0b, id(o) >= 0, id(o + 1) >= 0, qsc, qss, s_par_w, lane, slot_scale, k,
-                            pg_of(o), pg_of(o + 1), s_rope);
+                            pg_of(o), pg_of(o + 1), s_rope, prot);
       if (o + 2 >= cn) break;
       fetch_v(r1a, r1b, o + 2);
       fetch(r0a, r0b, o + 4);
       if (share_simd) __builtin_amdgcn_s_setprio(0);
       page_pair<BITS, ROPE>(st, r1a, r1b, id(o + 2) >= 0, id(o + 3) >= 0, qsc, qss, s_par_w, lane, slot_scale, k,
-                            pg_of(o + 2), pg_of(o + 3), s_rope);
+                            pg_of(o + 2), pg_of(o + 3), s_rope, prot);
     }
   }
 
@@ -826,13 +865,35 @@ __global__ __launch_bounds__(NW * kWave, 2) void kivi_decode_kernel(KiviParams k
   const Params& p = k.base;
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);   // wave-uniform (SGPR)
-  // keys held before RoPE: the rotations of a page's 32 offsets, built
-  // once per workgroup (a few L2 reads per thread, all issued together)
+  int part;
+  int bid = grid_item(p, part);
+  // keys held before RoPE: the rotations of a page's 32 offsets and of the
+  // workgroup's pages, built once per workgroup (L2 reads, all issued
+  // together)
   const RopeTable* s_rope = nullptr;
+  PageRot prot{nullptr, 0, 0};
   if constexpr (ROPE) {
     __shared__ __attribute__((aligned(16))) RopeTable s_rope_tb;
+    constexpr int kCap = kivi_page_rot_cap<BITS>();
+    __shared__ __attribute__((aligned(16))) uint16_t s_prot[kCap][2][kKiviHead / 2];
     constexpr int kN = kRopeRows * kKiviHead / (NW * kWave);
     static_assert(kRopeRows * kKiviHead % (NW * kWave) == 0, "whole rounds");
+    // the page rotations: rows 32 p of pages pg_first .. pg_first + kCap - 1,
+    // 16 bytes of one table per load (kQ per row)
+    constexpr int kQ = kKiviHead / 2 / 4;
+    constexpr int kPR = kCap * 2 * kQ / (NW * kWave);
+    static_assert(kCap * 2 * kQ % (NW * kWave) == 0, "whole rounds");
+    const int pg_first = FINAL ? 0 : part * k.partition_pages;
+    f4 rv[kPR];
+#pragma unroll
+    for (int r = 0; r < kPR; ++r) {
+      const int i = tid + r * NW * kWave, pgi = i / (2 * kQ), w = i % (2 * kQ), tab = w / kQ, q4 = w % kQ;
+      const int t = 32 * (pg_first + pgi);
+      const bool in = t < k.rope_max_pos;
+      const int64_t o = (int64_t)min(t, k.rope_max_pos - 1) * (kKiviHead / 2) + 4 * q4;
+      const f4 v = *reinterpret_cast<const f4*>((tab ? k.rope_sin : k.rope_cos) + o);
+      rv[r] = in ? v : (tab ? (f4){0.f, 0.f, 0.f, 0.f} : (f4){1.f, 1.f, 1.f, 1.f});
+    }
     float cv[kN], sv[kN];
 #pragma unroll
     for (int r = 0; r < kN; ++r) {
@@ -846,11 +907,17 @@ __global__ __launch_bounds__(NW * kWave, 2) void kivi_decode_kernel(KiviParams k
       s_rope_tb.cs[0][j][c] = __builtin_bit_cast(uint16_t, (_Float16)cv[r]);
       s_rope_tb.cs[1][j][c] = __builtin_bit_cast(uint16_t, (_Float16)(first ? -sv[r] : sv[r]));
     }
+#pragma unroll
+    for (int r = 0; r < kPR; ++r) {
+      const int i = tid + r * NW * kWave, pgi = i / (2 * kQ), w = i % (2 * kQ), tab = w / kQ, q4 = w % kQ;
+      typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+      const h4 hv = {(_Float16)rv[r][0], (_Float16)rv[r][1], (_Float16)rv[r][2], (_Float16)rv[r][3]};
+      *reinterpret_cast<uint2*>(&s_prot[pgi][tab][4 * q4]) = __builtin_bit_cast(uint2, hv);
+    }
     __syncthreads();
     s_rope = &s_rope_tb;
+    prot = PageRot{&s_prot[0][0][0], pg_first, kCap};
   }
-  int part;
-  int bid = grid_item(p, part);
   const int hs = bid % p.head_slices;      bid /= p.head_slices;
   const int kvh = bid % p.num_kv_heads;
   const int seq = bid / p.num_kv_heads;
@@ -916,7 +983,7 @@ __global__ __launch_bounds__(NW * kWave, 2) void kivi_decode_kernel(KiviParams k
     // and 58.5 us).
     kivi_pages_wave<BITS, ROPE>(k, seq, kvh, hs, pg0 + wave, pg1 - res_pages, page_waves, &sd.p[wave][0], &sd.acc[wave][0][0],
                     &sd.m[wave][0], &sd.l[wave][0], FINAL && blockIdx.x >= gridDim.x / 2,
-                    FINAL && page_waves == NW - 1, early_id, s_rope, q_raw);
+                    FINAL && page_waves == NW - 1, early_id, s_rope, prot, q_raw);
   } else {
     const int lane = tid % kWave;
     // build-ahead: this step's piece of the next page (one head slice
@@ -952,7 +1019,7 @@ __global__ __launch_bounds__(NW * kWave, 2) void kivi_decode_kernel(KiviParams k
     if constexpr (APPEND && !ROPE) kivi_piece_load(k.job, piece, kvh, ahead_page, lane);
     if constexpr (!kQEarly) load_q_operand(p, seq, kvh, hs, lane, q_raw);
     kivi_pages_wave<BITS, ROPE>(k, seq, kvh, hs, pg1 - res_pages, pg1, 1, &sd.p[wave][0], &sd.acc[NW + 1][0][0],
-                    &sd.m[NW + 1][0], &sd.l[NW + 1][0], false, false, -1, s_rope, q_raw);
+                    &sd.m[NW + 1][0], &sd.l[NW + 1][0], false, false, -1, s_rope, prot, q_raw);
     // the piece's fp16 for the quarters after the merge
     if constexpr (APPEND) {
       if (piece_due) {
