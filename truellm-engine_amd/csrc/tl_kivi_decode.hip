@@ -356,11 +356,25 @@ __device__ __forceinline__ void page_pair(PageState& st, const PageRaw<BITS>& ra
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
           const u32x4* kp = reinterpret_cast<const u32x4*>(par + (grp + 4 * m) * 8);
-          const u32x4 raw = k_codes(r, tt, m);
           // a code c in a half's low bits: 1024 + c as fp16, then c (16 n at
           // the INT4 slots 2, 3, 6, 7, which slot_scale takes back)
-          const u32x4 biased = {raw.x | 0x64006400u, raw.y | 0x64006400u, raw.z | 0x64006400u,
-                                raw.w | 0x64006400u};
+          u32x4 biased;
+          if constexpr (BITS == 4) {
+            // mask and bias in one v_and_or_b32 (the bias in a VGPR: one
+            // scalar operand per instruction)
+            const uint32_t w = word(r.kn[tt], m), y = w >> 8;
+            auto and_or = [](uint32_t x, uint32_t mask) {
+              uint32_t o;
+              const uint32_t bias = 0x64006400u;
+              asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(o) : "v"(x), "s"(mask), "v"(bias));
+              return o;
+            };
+            biased = u32x4{and_or(w, 0x000F000Fu), and_or(w, 0x00F000F0u), and_or(y, 0x000F000Fu),
+                           and_or(y, 0x00F000F0u)};
+          } else {
+            const u32x4 raw = k_codes(r, tt, m);
+            biased = u32x4{raw.x | 0x64006400u, raw.y | 0x64006400u, raw.z | 0x64006400u, raw.w | 0x64006400u};
+          }
           const h8 n = as_h8(biased) - (_Float16)1024.0f;
           kk[m] = n * (slot_scale * as_h8(kp[0])) + as_h8(kp[1]);
         }
@@ -372,8 +386,11 @@ __device__ __forceinline__ void page_pair(PageState& st, const PageRaw<BITS>& ra
         } else {
 #pragma unroll
           for (int m = 0; m < 2; ++m) {
-            rope_pair_blocks<false>(kk[m], kk[m + 2], rope_lds(*s_rope, 0, j, m, grp), rope_lds(*s_rope, 1, j, m, grp),
-                                    rope_lds(*s_rope, 0, j, m + 2, grp), rope_lds(*s_rope, 1, j, m + 2, grp));
+            // blocks m and m + 2 hold the same pairs: one cosine row, and
+            // sines that differ only in sign (INT4, with the bias below:
+            // 94.4 -> 82.4 us per step)
+            const h8 c = rope_lds(*s_rope, 0, j, m + 2, grp), sn = rope_lds(*s_rope, 1, j, m + 2, grp);
+            rope_pair_blocks<false>(kk[m], kk[m + 2], c, -sn, c, sn);
           }
         }
         f4 acc = (f4){0.f, 0.f, 0.f, 0.f};
