@@ -124,7 +124,8 @@ __device__ __forceinline__ void rope_coef_block1(const KiviParams& k, int t, int
   }
 }
 // The rotations of positions 0 .. 31 (a page's offsets) in LDS, per
-// channel: [C or S][offset j][channel].
+// channel: [C or S][offset j][channel]; for style 0, [0] holds each pair's
+// (C, S) in its two channels' dword (see rope_rot_adjacent).
 constexpr int kRopeRows = kKiviPageTokens;
 struct RopeTable {
   uint16_t cs[2][kRopeRows][kKiviHead];
@@ -157,6 +158,24 @@ __device__ __forceinline__ void rope_coef_row0(const uint16_t* row, int m, int g
   const h4 ns = -sv;
   c = __builtin_shufflevector(cv, cv, 0, 0, 1, 1, 2, 2, 3, 3);
   s = __builtin_shufflevector(ns, sv, 0, 4, 1, 5, 2, 6, 3, 7);
+}
+// R x of the 4 adjacent pairs (x0, x1) of a block (style 0), dword d of cs
+// holding (cos, sin) of pair d: (x0 c - x1 s, x1 c + x0 s) as rope_one_block
+// rounds it (the product x c, then one fma), with the halves selected and
+// negated by the packed ops' operand modifiers instead of a swap.
+__device__ __forceinline__ void rope_rot_adjacent(h8& a, const u32x4& cs) {
+  const u32x4 x = __builtin_bit_cast(u32x4, a);
+  uint32_t o[4];
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    uint32_t t;
+    // t = (x0 c, x1 c)
+    asm("v_pk_mul_f16 %0, %1, %2 op_sel_hi:[1,0]" : "=v"(t) : "v"(word(x, d)), "v"(word(cs, d)));
+    // (x1 (-s) + x0 c, x0 s + x1 c)
+    asm("v_pk_fma_f16 %0, %1, %2, %3 op_sel:[1,1,0] op_sel_hi:[0,1,1] neg_lo:[0,1,0]"
+        : "=v"(o[d]) : "v"(word(x, d)), "v"(word(cs, d)), "v"(t));
+  }
+  a = __builtin_bit_cast(h8, u32x4{o[0], o[1], o[2], o[3]});
 }
 __device__ __forceinline__ void rope_coef_row1(const uint16_t* row, int m, int grp, h8& c, h8& sa, h8& sb) {
   c = *reinterpret_cast<const h8*>(row + 32 * m + 8 * grp);
@@ -380,9 +399,7 @@ __device__ __forceinline__ void page_pair(PageState& st, const PageRaw<BITS>& ra
         }
         if (style == 0) {
 #pragma unroll
-          for (int m = 0; m < 4; ++m) {
-            rope_one_block<false>(kk[m], rope_lds(*s_rope, 0, j, m, grp), rope_lds(*s_rope, 1, j, m, grp));
-          }
+          for (int m = 0; m < 4; ++m) rope_rot_adjacent(kk[m], __builtin_bit_cast(u32x4, rope_lds(*s_rope, 0, j, m, grp)));
         } else {
 #pragma unroll
           for (int m = 0; m < 2; ++m) {
@@ -921,7 +938,9 @@ __global__ __launch_bounds__(NW * kWave, 2) void kivi_decode_kernel(KiviParams k
     for (int r = 0; r < kN; ++r) {
       const int i = tid + r * NW * kWave, j = i / kKiviHead, c = i % kKiviHead;
       const bool first = k.rope_style == 0 ? (c & 1) == 0 : c < 64;
-      s_rope_tb.cs[0][j][c] = __builtin_bit_cast(uint16_t, (_Float16)cv[r]);
+      // style 0: cs[0] holds (cos, sin) of pair c / 2 in the dword of
+      // channels c, c + 1 (rope_rot_adjacent); cs[1] is not read
+      s_rope_tb.cs[0][j][c] = __builtin_bit_cast(uint16_t, (_Float16)(k.rope_style == 0 && (c & 1) ? sv[r] : cv[r]));
       s_rope_tb.cs[1][j][c] = __builtin_bit_cast(uint16_t, (_Float16)(first ? -sv[r] : sv[r]));
     }
 #pragma unroll
