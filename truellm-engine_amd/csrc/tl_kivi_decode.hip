@@ -135,10 +135,11 @@ __device__ __forceinline__ h8 rope_lds(const RopeTable& tb, int which, int j, in
 }
 
 // The page rotations R_{32 p} of a workgroup's pages first .. first + count
-// - 1 in LDS, filled at its start: cs[p - first][cos | sin][pair] in f16,
-// converted as rope_coef_block0/1 convert the table rows (so both give the
-// same bits).  The q rotation of a page then reads LDS; read from the
-// tables where it is used, it waited for every page load in flight (the
+// - 1 in LDS, filled at its start, in f16 converted as rope_coef_block0/1
+// convert the table rows (so both give the same bits): per page, style 1
+// [cos | sin][pair], style 0 (cos, sin) of each pair in one dword.  The q
+// rotation of a page then reads LDS; read from the tables where it is
+// used, it waited for every page load in flight (the
 // next pair's included), one memory round trip per page: INT4 with keys
 // before RoPE took 111.7 us per step, 88.1-88.6 with the coefficients
 // taken as constants (timing only).
@@ -150,15 +151,6 @@ struct PageRot {
 // of LDS each) beside the rest of the kernel's LDS
 template <int BITS> constexpr int kivi_page_rot_cap() { return BITS == 8 ? 112 : 128; }
 
-// rope_coef_block0/1 from the LDS row of a page
-__device__ __forceinline__ void rope_coef_row0(const uint16_t* row, int m, int grp, h8& c, h8& s) {
-  typedef _Float16 h4 __attribute__((ext_vector_type(4)));
-  const h4 cv = __builtin_bit_cast(h4, *reinterpret_cast<const uint2*>(row + 16 * m + 4 * grp));
-  const h4 sv = __builtin_bit_cast(h4, *reinterpret_cast<const uint2*>(row + kKiviHead / 2 + 16 * m + 4 * grp));
-  const h4 ns = -sv;
-  c = __builtin_shufflevector(cv, cv, 0, 0, 1, 1, 2, 2, 3, 3);
-  s = __builtin_shufflevector(ns, sv, 0, 4, 1, 5, 2, 6, 3, 7);
-}
 // R x of the 4 adjacent pairs (x0, x1) of a block (style 0), dword d of cs
 // holding (cos, sin) of pair d: (x0 c - x1 s, x1 c + x0 s) as rope_one_block
 // rounds it (the product x c, then one fma), with the halves selected and
@@ -177,6 +169,20 @@ __device__ __forceinline__ void rope_rot_adjacent(h8& a, const u32x4& cs) {
   }
   a = __builtin_bit_cast(h8, u32x4{o[0], o[1], o[2], o[3]});
 }
+// R^T x of the same: (x0 c + x1 s, x1 c - x0 s)
+__device__ __forceinline__ void rope_rot_adjacent_t(h8& a, const u32x4& cs) {
+  const u32x4 x = __builtin_bit_cast(u32x4, a);
+  uint32_t o[4];
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    uint32_t t;
+    asm("v_pk_mul_f16 %0, %1, %2 op_sel_hi:[1,0]" : "=v"(t) : "v"(word(x, d)), "v"(word(cs, d)));
+    asm("v_pk_fma_f16 %0, %1, %2, %3 op_sel:[1,1,0] op_sel_hi:[0,1,1] neg_hi:[0,1,0]"
+        : "=v"(o[d]) : "v"(word(x, d)), "v"(word(cs, d)), "v"(t));
+  }
+  a = __builtin_bit_cast(h8, u32x4{o[0], o[1], o[2], o[3]});
+}
+// rope_coef_block1 from the LDS row of a page (style 1)
 __device__ __forceinline__ void rope_coef_row1(const uint16_t* row, int m, int grp, h8& c, h8& sa, h8& sb) {
   c = *reinterpret_cast<const h8*>(row + 32 * m + 8 * grp);
   sb = *reinterpret_cast<const h8*>(row + kKiviHead / 2 + 32 * m + 8 * grp);
@@ -354,10 +360,14 @@ __device__ __forceinline__ void page_pair(PageState& st, const PageRaw<BITS>& ra
       if (style == 0) {
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
-          h8 c, sn;
-          if (from_lds) rope_coef_row0(row, m, grp, c, sn);
-          else rope_coef_block0(k, t0, m, grp, c, sn);
-          rope_one_block<true>(qp[m], c, sn);
+          if (from_lds) {
+            // pairs 16 m + 4 grp .. + 3
+            rope_rot_adjacent_t(qp[m], *reinterpret_cast<const u32x4*>(row + 32 * m + 8 * grp));
+          } else {
+            h8 c, sn;
+            rope_coef_block0(k, t0, m, grp, c, sn);
+            rope_one_block<true>(qp[m], c, sn);
+          }
         }
       } else {
 #pragma unroll
@@ -948,7 +958,19 @@ __global__ __launch_bounds__(NW * kWave, 2) void kivi_decode_kernel(KiviParams k
       const int i = tid + r * NW * kWave, pgi = i / (2 * kQ), w = i % (2 * kQ), tab = w / kQ, q4 = w % kQ;
       typedef _Float16 h4 __attribute__((ext_vector_type(4)));
       const h4 hv = {(_Float16)rv[r][0], (_Float16)rv[r][1], (_Float16)rv[r][2], (_Float16)rv[r][3]};
-      *reinterpret_cast<uint2*>(&s_prot[pgi][tab][4 * q4]) = __builtin_bit_cast(uint2, hv);
+      if (k.rope_style == 0) {
+        // pair 4 q4 + e: (cos, sin) in halves 2 (4 q4 + e), + 1
+        uint16_t* rowp = &s_prot[pgi][0][0];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          // (a scalar first: __builtin_bit_cast of a vector element itself
+          // reads element 0 with this compiler)
+          const _Float16 he = (_Float16)rv[r][e];
+          rowp[2 * (4 * q4 + e) + tab] = __builtin_bit_cast(uint16_t, he);
+        }
+      } else {
+        *reinterpret_cast<uint2*>(&s_prot[pgi][tab][4 * q4]) = __builtin_bit_cast(uint2, hv);
+      }
     }
     __syncthreads();
     s_rope = &s_rope_tb;
