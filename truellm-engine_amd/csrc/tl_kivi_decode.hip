@@ -720,13 +720,76 @@ __device__ __forceinline__ void put_half(u32x4& c, int e, uint32_t v) {
 // The window's keys held before RoPE (decode2_wave's hook): each of the
 // lane's 8 tokens rotated at its position.  Style 0 pairs rows 2 m and
 // 2 m + 1 (pair m), style 1 rows c and c + 64 (kr[j] and kr[j + 2]).
+// The window's rotation rows: (cos, sin) in f16 of each pair at the first
+// position of the window's first kWinRows pages, filled by the residual
+// wavefront once it knows the length.
+constexpr int kWinRows = 8;
+
 struct KiviWindowRope {
   static constexpr bool kActive = true;
   const KiviParams& k;
+  const RopeTable* offs = nullptr;     // the offset rotations R_j (LDS)
+  const uint32_t* wrows = nullptr;     // [kWinRows][64] page rotations R_{32 p}, p = wp0 + row (LDS)
+  int wp0 = 0;
   template <int KP>
   __device__ void operator()(u32x4 (&kr)[KP][2], int tok0, int dl) const {
     static_assert(KP == 4, "head size 128");
     auto get = [](const u32x4& c, int e) { return f16_to_f32(uint16_t(word(c, e >> 1) >> (16 * (e & 1)))); };
+    auto f2 = [](uint32_t w, float& lo, float& hi) {
+      lo = f16_to_f32(uint16_t(w));
+      hi = f16_to_f32(uint16_t(w >> 16));
+    };
+    // An iteration's 32 tokens are one page (the window starts on a page
+    // boundary), so rp is wave-uniform.  Token t = 32 p + j is rotated by
+    // R_{32 p} R_j, composed in fp32 from the two LDS tables (angles linear
+    // in the position), instead of its table row read from memory, which
+    // waited for every load in flight (INT8 with keys before RoPE: the
+    // window was the residual wavefront's critical path).
+    const int rp = (tok0 >> 5) - wp0;
+    if (wrows != nullptr && rp >= 0 && rp < kWinRows) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int jj = (tok0 + e) & 31;
+        if (k.rope_style == 0) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int m = dl + 16 * j;
+            float cp, sp, cj, sj;
+            f2(wrows[rp * 64 + m], cp, sp);
+            f2(*reinterpret_cast<const uint32_t*>(&offs->cs[0][jj][2 * m]), cj, sj);
+            const float c = __builtin_fmaf(cp, cj, -(sp * sj)), sn = __builtin_fmaf(sp, cj, cp * sj);
+            float x0 = get(kr[j][0], e), x1 = get(kr[j][1], e);
+            rope_rotate(x0, x1, c, sn);
+            put_half(kr[j][0], e, f32_to_f16(x0));
+            put_half(kr[j][1], e, f32_to_f16(x1));
+            // one pair's reads and products at a time: held together across
+            // the tokens they spill inside the window loop
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        } else {
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            // pairs pi, pi + 1: one dword of cosines, one of (positive) sines
+            const int pi = 2 * (dl + 16 * j);
+            float cj[2], sj[2];
+            f2(*reinterpret_cast<const uint32_t*>(&offs->cs[0][jj][pi]), cj[0], cj[1]);
+            f2(*reinterpret_cast<const uint32_t*>(&offs->cs[1][jj][pi + 64]), sj[0], sj[1]);
+#pragma unroll
+            for (int r = 0; r < 2; ++r) {
+              float cp, sp;
+              f2(wrows[rp * 64 + pi + r], cp, sp);
+              const float c = __builtin_fmaf(cp, cj[r], -(sp * sj[r])), sn = __builtin_fmaf(sp, cj[r], cp * sj[r]);
+              float x0 = get(kr[j][r], e), x1 = get(kr[j + 2][r], e);
+              rope_rotate(x0, x1, c, sn);
+              put_half(kr[j][r], e, f32_to_f16(x0));
+              put_half(kr[j + 2][r], e, f32_to_f16(x1));
+            }
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        }
+      }
+      return;
+    }
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const int t = tok0 + e;
@@ -916,10 +979,13 @@ __global__ __launch_bounds__(NW * kWave, 2) void kivi_decode_kernel(KiviParams k
   // together)
   const RopeTable* s_rope = nullptr;
   PageRot prot{nullptr, 0, 0};
+  uint32_t* s_wrot = nullptr;          // the window's page rotations (residual wavefront)
   if constexpr (ROPE) {
     __shared__ __attribute__((aligned(16))) RopeTable s_rope_tb;
     constexpr int kCap = kivi_page_rot_cap<BITS>();
     __shared__ __attribute__((aligned(16))) uint16_t s_prot[kCap][2][kKiviHead / 2];
+    __shared__ __attribute__((aligned(16))) uint32_t s_wrot_tb[kWinRows][kKiviHead / 2];
+    s_wrot = &s_wrot_tb[0][0];
     constexpr int kN = kRopeRows * kKiviHead / (NW * kWave);
     static_assert(kRopeRows * kKiviHead % (NW * kWave) == 0, "whole rounds");
     // the page rotations: rows 32 p of pages pg_first .. pg_first + kCap - 1,
@@ -1061,8 +1127,22 @@ __global__ __launch_bounds__(NW * kWave, 2) void kivi_decode_kernel(KiviParams k
     else
       nt = newest_from_pool<BS>(p, seq, kvh, L - 1, lane);
     if constexpr (ROPE) {
+      // the window's page rotations: lane l holds pair l of rows 32 (wp0 + r)
+      const int wp0 = lq / kKiviPageTokens;
+      float wc[kWinRows], ws[kWinRows];
+#pragma unroll
+      for (int r = 0; r < kWinRows; ++r) rope_cs1(k, kKiviPageTokens * (wp0 + r), lane, wc[r], ws[r]);
+#pragma unroll
+      for (int r = 0; r < kWinRows; ++r) {
+        typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+        const h2 v = {(_Float16)wc[r], (_Float16)ws[r]};
+        s_wrot[r * (kKiviHead / 2) + lane] = __builtin_bit_cast(uint32_t, v);
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
       decode2_wave<Kind::F16, kKiviHead, BS>(p, seq, kvh, hs, lq, L - 1, 32, &sd.p[wave][0], &sd.acc[wave][0][0],
-                                             &sd.m[wave][0], &sd.l[wave][0], KiviWindowRope{k});
+                                             &sd.m[wave][0], &sd.l[wave][0], KiviWindowRope{k, s_rope, s_wrot, wp0});
       NewestToken ntr = nt;
       ntr.k = rope_newest_key(k, nt.k, L - 1, lane);
       newest_state(p, ntr, seq, kvh, hs, lane, &sd.acc[NW][0][0], &sd.m[NW][0], &sd.l[NW][0]);
