@@ -139,10 +139,10 @@ __device__ __forceinline__ h8 rope_lds(const RopeTable& tb, int which, int j, in
 // convert the table rows (so both give the same bits): per page, style 1
 // [cos | sin][pair], style 0 (cos, sin) of each pair in one dword.  The q
 // rotation of a page then reads LDS; read from the tables where it is
-// used, it waited for every page load in flight (the
-// next pair's included), one memory round trip per page: INT4 with keys
-// before RoPE took 111.7 us per step, 88.1-88.6 with the coefficients
-// taken as constants (timing only).
+// used, it waited for every page load in flight (the next pair's
+// included), one memory round trip per page: INT4 with keys before RoPE
+// took 111.7 us per step, 88.1-88.6 with the coefficients taken as
+// constants (timing only).
 struct PageRot {
   const uint16_t* cs;   // [count][2][64]
   int first, count;
