@@ -421,7 +421,10 @@ typedef struct tl_kivi_desc {
   int32_t num_pages;
   int32_t residual_length;     /* R >= 0 */
   int32_t gqa_map;
-  int32_t partition_pages;     /* 0 = choose, -1 = single pass, else pages per partition */
+  int32_t partition_pages;     /* 0 = choose, -1 = single pass, else pages per partition; the
+                                  _pre_rope entry points take at most 160 pages per partition
+                                  at INT4, 144 at INT8 (the page rotations a workgroup holds in
+                                  LDS), a single pass included */
   float scale;
   int32_t bits;                /* code width of the pages (KiviConfig.bits, config_schema.h:124):
                                   4 (also 0) or 8 */
@@ -466,6 +469,10 @@ int tl_kivi_append(const tl_kivi_desc* desc, const void* key, const void* value,
                    const int32_t* seq_lens, const int32_t* page_tables, void* pages,
                    void* stream);
 
+/* Split-K partials of the decode and the step: 0 when the plan runs a
+ * single pass.  Sized for the _pre_rope entry points' plan (as many
+ * partitions as the other one, or more past 160 / 144 pages), so one size
+ * serves every entry point. */
 size_t tl_kivi_workspace_bytes(const tl_kivi_desc* desc, int32_t max_context_len);
 
 /* Decode attention over pages (tokens < Lq) and the fp16 pool (tokens >= Lq).

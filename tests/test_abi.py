@@ -334,10 +334,19 @@ def test_kivi_decode_descriptor_checks_and_planning():
     # 4 x 8 items, 124 pages -> 16 partitions of 8 pages
     assert tla.kivi_workspace_bytes(_kdesc(num_seqs=4), 4096) == 4 * 32 * 16 * (128 * 4 + 8)
     assert call(_kdesc(num_seqs=4)) == tla.ERR_INVALID_ARGUMENT        # workspace missing
-    # page code widths: 4 (also 0) and 8; the workspace does not depend on them
+    # page code widths: 4 (also 0) and 8; at 4096 tokens the workspace does
+    # not depend on them
     assert call(_kdesc(bits=5)) == tla.ERR_NOT_IMPLEMENTED
     assert call(_kdesc(bits=2)) == tla.ERR_NOT_IMPLEMENTED
     assert tla.kivi_workspace_bytes(_kdesc(num_seqs=4, bits=8), 4096) == 4 * 32 * 16 * (128 * 4 + 8)
+    # the _pre_rope entry points give a workgroup at most 160 (INT4) / 144
+    # (INT8) pages, their rotations held in LDS: the 300 pages of 9728 tokens
+    # run in 2 / 3 partitions, a single pass asked for included, and the
+    # workspace is sized for that plan
+    for pp in (0, -1):
+        assert tla.kivi_workspace_bytes(_kdesc(partition_pages=pp), 9728) == 64 * 32 * 2 * (128 * 4 + 8)
+        assert tla.kivi_workspace_bytes(_kdesc(partition_pages=pp, bits=8), 9728) == 64 * 32 * 3 * (128 * 4 + 8)
+    assert tla.kivi_workspace_bytes(_kdesc(partition_pages=-1), 4096) == 0
     # build_ahead: 0 or 1 (with any residual length: below 9 it builds on completion)
     for ba in (2, -1):
         assert call(_kdesc(build_ahead=ba)) == tla.ERR_INVALID_ARGUMENT

@@ -472,15 +472,17 @@ def test_kivi_pre_rope_decode_matches_oracle(style, bits, pp):
 @pytest.mark.parametrize("style", [tla.ROPE_ADJACENT, tla.ROPE_HALVES])
 @pytest.mark.parametrize("bits", [4, 8])
 def test_kivi_pre_rope_long_single_pass(style, bits):
-    """A workgroup takes the rotations of its first pages (128 at INT4, 112
-    at INT8) from LDS and those of later pages from the tables: single-pass
-    sequences of 155, 135 and 114 pages use both, against the oracle; a page
-    past the LDS rows is a hole."""
+    """A workgroup holds the rotations of at most 160 (INT4) / 144 (INT8)
+    pages in LDS, so a single pass asked for over sequences of 180, 135 and
+    114 pages runs in two partitions (at INT8 the 135-page sequence fits one
+    partition, the 180-page one spans both), against the oracle; a page in
+    each partition is a hole."""
     from test_oracle import rope_tables
-    kc = KiviCase(58, [5100, 4460, 3800, 900], bits=bits)
+    kc = KiviCase(58, [5900, 4460, 3800, 900], bits=bits)
     kc.page_tables[0, 140] = -1
+    kc.page_tables[0, 170] = -1
     pages_np = kc.oracle_pages()
-    cos_t, sin_t = rope_tables(5100, 128)
+    cos_t, sin_t = rope_tables(5900, 128)
     qd, kd, vd = dev(kc.q, orc.F16), dev(kc.k, orc.F16), dev(kc.v, orc.F16)
     btd, sld, ptd = dev(kc.tables), dev(kc.lens), dev(kc.page_tables)
     pages = torch.from_numpy(pages_np).cuda()

@@ -836,7 +836,9 @@ int tl_kivi_append(const tl_kivi_desc* desc, const void* key, const void* value,
   return ok();
 }
 
-static void kivi_plan(const tl_kivi_desc* d, int32_t max_ctx, int* P, int* PP) {
+// rope: the _pre_rope entry points, whose workgroups take at most
+// tl::kivi_page_rot_cap(bits) pages
+static void kivi_plan(const tl_kivi_desc* d, int32_t max_ctx, bool rope, int* P, int* PP) {
   const int pages = tl::kivi_quantized_len(max_ctx, d->residual_length) / tl::kKiviPageTokens;
   int pp;
   if (d->partition_pages == -1 || pages == 0) {
@@ -852,14 +854,17 @@ static void kivi_plan(const tl_kivi_desc* d, int32_t max_ctx, int* P, int* PP) {
     pp = (int)((pages + want - 1) / want);
   }
   if (pp > tl::kKiviMaxWgPages) pp = tl::kKiviMaxWgPages;   // a workgroup stages its page ids in LDS
+  if (rope && pp > tl::kivi_page_rot_cap(kivi_bits(d))) pp = tl::kivi_page_rot_cap(kivi_bits(d));
   *PP = pp;
   *P = pages > 0 ? (pages + pp - 1) / pp : 1;
 }
 
 size_t tl_kivi_workspace_bytes(const tl_kivi_desc* desc, int32_t max_context_len) {
   if (check_kivi(desc) != TL_OK || max_context_len < 0) return 0;
+  // the plan of the _pre_rope entry points: at least as many partitions as
+  // the other one, so the size serves both
   int P, PP;
-  kivi_plan(desc, max_context_len, &P, &PP);
+  kivi_plan(desc, max_context_len, true, &P, &PP);
   if (P <= 1) return 0;
   const size_t sh = (size_t)desc->num_seqs * desc->num_heads * P;
   return sh * desc->head_size * 4 + 2 * sh * 4;
@@ -1026,7 +1031,7 @@ static int kivi_decode_impl(const tl_kivi_desc* desc, void* out, const void* q, 
   if (!aligned16(q) || !aligned16(pages) || !aligned16(k_cache) || !aligned16(v_cache))
     return fail(TL_ERR_INVALID_ARGUMENT, "q, pages and pools must be 16-byte aligned");
   int P, PP;
-  kivi_plan(desc, max_context_len, &P, &PP);
+  kivi_plan(desc, max_context_len, rope != nullptr, &P, &PP);
   tl::KiviDecodeLaunch a;
   memset(&a, 0, sizeof a);
   a.out = out; a.q = q; a.pages = pages; a.page_tables = page_tables;

@@ -60,6 +60,11 @@ constexpr int kKiviVParamOff = 4608;
 constexpr int kKiviMaxHeadDim = 128;   // KIVI_MAX_HEAD_DIM, kivi_cache.cuh:27
 constexpr int kKiviMaxOutliers = 64;   // KIVI_MAX_OUTLIERS, kivi_cache.cuh:28
 constexpr int kKiviMaxWgPages = 1024;  // pages one decode workgroup takes (ids staged in LDS)
+// Pages one decode workgroup takes with the keys held before RoPE: the
+// rotations of its pages' first positions are LDS rows filled at its start,
+// as many as fit beside the rest of the kernel's LDS at two workgroups per
+// CU; the plan splits longer sequences.
+__host__ __device__ constexpr int kivi_page_rot_cap(int bits) { return bits == 8 ? 144 : 160; }
 // Build-ahead: a page is written in kKiviPieces pieces by the steps before
 // the one that quantises it; with R > kKiviPieces the newest token of those
 // steps lies past the page.

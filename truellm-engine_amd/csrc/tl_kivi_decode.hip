@@ -58,18 +58,7 @@ __device__ __forceinline__ void rope_rotate(float& x0, float& x1, float c, float
   x0 = y0;
   x1 = y1;
 }
-// cos / sin of pairs i .. i + 3 at position t (t past the tables: no
-// rotation).  i is a multiple of 4, the tables 16-byte aligned.  The loads
-// are unconditional (at a clamped position, then a select): a load under a
-// lane-divergent branch makes the compiler wait for every load in flight,
-// the page loads included.
-__device__ __forceinline__ void rope_cs4(const KiviParams& k, int t, int i, f4& c, f4& s) {
-  const bool in = t >= 0 && t < k.rope_max_pos;
-  const int64_t o = (int64_t)min(max(t, 0), k.rope_max_pos - 1) * (kKiviHead / 2) + i;
-  const f4 cv = *reinterpret_cast<const f4*>(k.rope_cos + o), sv = *reinterpret_cast<const f4*>(k.rope_sin + o);
-  c = in ? cv : (f4){1.f, 1.f, 1.f, 1.f};
-  s = in ? sv : (f4){0.f, 0.f, 0.f, 0.f};
-}
+// cos / sin of pair i at position t (t past the tables: no rotation)
 __device__ __forceinline__ void rope_cs1(const KiviParams& k, int t, int i, float& c, float& s) {
   const bool in = t >= 0 && t < k.rope_max_pos;
   const int64_t o = (int64_t)min(max(t, 0), k.rope_max_pos - 1) * (kKiviHead / 2) + i;
@@ -93,67 +82,39 @@ __device__ __forceinline__ void rope_pair_blocks(h8& a, h8& b, const h8& ca, con
   a = TRANSPOSE ? a0 * ca - b0 * sa : a0 * ca + b0 * sa;
   b = TRANSPOSE ? b0 * cb - a0 * sb : b0 * cb + a0 * sb;
 }
-template <bool TRANSPOSE>
-__device__ __forceinline__ void rope_one_block(h8& a, const h8& c, const h8& s) {
-  const h8 pt = __builtin_shufflevector(a, a, 1, 0, 3, 2, 5, 4, 7, 6);
-  a = TRANSPOSE ? a * c - pt * s : a * c + pt * s;
-}
-// C and S of block m (style 0: pairs 16 m + 4 grp + d, each twice) or of
-// blocks m and m + 2 (style 1: pairs 32 m + 8 grp + e) at position t, from
-// the fp32 tables.
-__device__ __forceinline__ void rope_coef_block0(const KiviParams& k, int t, int m, int grp, h8& c, h8& s) {
-  f4 cv, sv;
-  rope_cs4(k, t, 16 * m + 4 * grp, cv, sv);
-#pragma unroll
-  for (int d = 0; d < 4; ++d) {
-    c[2 * d] = c[2 * d + 1] = (_Float16)cv[d];
-    s[2 * d] = (_Float16)(-sv[d]);
-    s[2 * d + 1] = (_Float16)sv[d];
-  }
-}
-__device__ __forceinline__ void rope_coef_block1(const KiviParams& k, int t, int m, int grp, h8& c, h8& sa,
-                                                 h8& sb) {
-  f4 c0, s0, c1, s1;
-  rope_cs4(k, t, 32 * m + 8 * grp, c0, s0);
-  rope_cs4(k, t, 32 * m + 8 * grp + 4, c1, s1);
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    c[e] = (_Float16)(e < 4 ? c0[e & 3] : c1[e & 3]);
-    sb[e] = (_Float16)(e < 4 ? s0[e & 3] : s1[e & 3]);
-    sa[e] = -sb[e];
-  }
-}
-// The rotations of positions 0 .. 31 (a page's offsets) in LDS, per
-// channel: [C or S][offset j][channel]; for style 0, [0] holds each pair's
-// (C, S) in its two channels' dword (see rope_rot_adjacent).
+// The rotations of positions 0 .. 31 (a page's offsets) in LDS, one row per
+// offset j in the layout of the page rows below: style 1 [cos | sin][pair],
+// style 0 (cos, sin) of each pair in one dword (rope_rot_adjacent).  Each
+// pair's cosine and sine once: 8 KiB, which leaves room for 32 more page
+// rows than a table per channel.
 constexpr int kRopeRows = kKiviPageTokens;
 struct RopeTable {
-  uint16_t cs[2][kRopeRows][kKiviHead];
+  uint16_t cs[kRopeRows][kKiviHead];
 };
-__device__ __forceinline__ h8 rope_lds(const RopeTable& tb, int which, int j, int m, int grp) {
-  return *reinterpret_cast<const h8*>(&tb.cs[which][j][32 * m + 8 * grp]);
+// halves off .. off + 7 of offset j's row
+__device__ __forceinline__ h8 rope_lds(const RopeTable& tb, int j, int off) {
+  return *reinterpret_cast<const h8*>(&tb.cs[j][off]);
 }
 
 // The page rotations R_{32 p} of a workgroup's pages first .. first + count
-// - 1 in LDS, filled at its start, in f16 converted as rope_coef_block0/1
-// convert the table rows (so both give the same bits): per page, style 1
-// [cos | sin][pair], style 0 (cos, sin) of each pair in one dword.  The q
-// rotation of a page then reads LDS; read from the tables where it is
-// used, it waited for every page load in flight (the next pair's
-// included), one memory round trip per page: INT4 with keys before RoPE
-// took 111.7 us per step, 88.1-88.6 with the coefficients taken as
-// constants (timing only).
+// - 1 in LDS, filled at its start, the table rows converted to f16: per
+// page, style 1 [cos | sin][pair], style 0 (cos, sin) of each pair in one
+// dword.  The plan gives a workgroup at most kivi_page_rot_cap(bits) pages
+// (tl_kivi.hpp), so every page's rotation is in the table.  Read from the
+// tables where it is used, the q rotation waited for every page load in
+// flight (the next pair's included), one memory round trip per page: INT4
+// with keys before RoPE took 111.7 us per step, 88.1-88.6 with the
+// coefficients taken as constants (timing only); and a fallback to the
+// tables for pages past the LDS rows, never taken at 4096 tokens, still
+// cost 2-3 us per step (the branch splits the q rotation's block).
 struct PageRot {
   const uint16_t* cs;   // [count][2][64]
   int first, count;
 };
-// pages the table holds: what leaves two workgroups per CU (at most 80 KiB
-// of LDS each) beside the rest of the kernel's LDS
-template <int BITS> constexpr int kivi_page_rot_cap() { return BITS == 8 ? 112 : 128; }
 
 // R x of the 4 adjacent pairs (x0, x1) of a block (style 0), dword d of cs
-// holding (cos, sin) of pair d: (x0 c - x1 s, x1 c + x0 s) as rope_one_block
-// rounds it (the product x c, then one fma), with the halves selected and
+// holding (cos, sin) of pair d: (x0 c - x1 s, x1 c + x0 s), rounded as the
+// product x c, then one fma, with the halves selected and
 // negated by the packed ops' operand modifiers instead of a swap.
 __device__ __forceinline__ void rope_rot_adjacent(h8& a, const u32x4& cs) {
   const u32x4 x = __builtin_bit_cast(u32x4, a);
@@ -182,7 +143,8 @@ __device__ __forceinline__ void rope_rot_adjacent_t(h8& a, const u32x4& cs) {
   }
   a = __builtin_bit_cast(h8, u32x4{o[0], o[1], o[2], o[3]});
 }
-// rope_coef_block1 from the LDS row of a page (style 1)
+// C, -S and S of blocks m and m + 2 (style 1: pairs 32 m + 8 grp + e) from
+// the LDS row of a page
 __device__ __forceinline__ void rope_coef_row1(const uint16_t* row, int m, int grp, h8& c, h8& sa, h8& sb) {
   c = *reinterpret_cast<const h8*>(row + 32 * m + 8 * grp);
   sb = *reinterpret_cast<const h8*>(row + kKiviHead / 2 + 32 * m + 8 * grp);
@@ -350,31 +312,22 @@ __device__ __forceinline__ void page_pair(PageState& st, const PageRaw<BITS>& ra
       const PageRaw<BITS>& r = pi ? rb : ra;
       const uint32_t* par = s_par_w + pi * 256;
       const int pg = pi ? pgb : pga;
-      const int t0 = 32 * pg;
-      const int ci = pg - prot.first;               // wave-uniform
-      const bool from_lds = ci >= 0 && ci < prot.count;
-      const uint16_t* row = prot.cs + (int64_t)(from_lds ? ci : 0) * kKiviHead;
+      // wave-uniform; in the table by the plan (the clamp keeps a page
+      // past it, which the plan never gives, inside LDS)
+      const int ci = min(max(pg - prot.first, 0), prot.count - 1);
+      const uint16_t* row = prot.cs + ci * kKiviHead;
       h8 qp[4];
 #pragma unroll
       for (int m = 0; m < 4; ++m) qp[m] = as_h8(qsc[m]);
       if (style == 0) {
 #pragma unroll
-        for (int m = 0; m < 4; ++m) {
-          if (from_lds) {
-            // pairs 16 m + 4 grp .. + 3
-            rope_rot_adjacent_t(qp[m], *reinterpret_cast<const u32x4*>(row + 32 * m + 8 * grp));
-          } else {
-            h8 c, sn;
-            rope_coef_block0(k, t0, m, grp, c, sn);
-            rope_one_block<true>(qp[m], c, sn);
-          }
-        }
+        for (int m = 0; m < 4; ++m)   // pairs 16 m + 4 grp .. + 3
+          rope_rot_adjacent_t(qp[m], *reinterpret_cast<const u32x4*>(row + 32 * m + 8 * grp));
       } else {
 #pragma unroll
         for (int m = 0; m < 2; ++m) {
           h8 c, sa, sb;
-          if (from_lds) rope_coef_row1(row, m, grp, c, sa, sb);
-          else rope_coef_block1(k, t0, m, grp, c, sa, sb);
+          rope_coef_row1(row, m, grp, c, sa, sb);
           rope_pair_blocks<true>(qp[m], qp[m + 2], c, sa, c, sb);
         }
       }
@@ -409,14 +362,15 @@ __device__ __forceinline__ void page_pair(PageState& st, const PageRaw<BITS>& ra
         }
         if (style == 0) {
 #pragma unroll
-          for (int m = 0; m < 4; ++m) rope_rot_adjacent(kk[m], __builtin_bit_cast(u32x4, rope_lds(*s_rope, 0, j, m, grp)));
+          for (int m = 0; m < 4; ++m)
+            rope_rot_adjacent(kk[m], __builtin_bit_cast(u32x4, rope_lds(*s_rope, j, 32 * m + 8 * grp)));
         } else {
 #pragma unroll
           for (int m = 0; m < 2; ++m) {
             // blocks m and m + 2 hold the same pairs: one cosine row, and
             // sines that differ only in sign (INT4, with the bias below:
             // 94.4 -> 82.4 us per step)
-            const h8 c = rope_lds(*s_rope, 0, j, m + 2, grp), sn = rope_lds(*s_rope, 1, j, m + 2, grp);
+            const h8 c = rope_lds(*s_rope, j, 32 * m + 8 * grp), sn = rope_lds(*s_rope, j, 64 + 32 * m + 8 * grp);
             rope_pair_blocks<false>(kk[m], kk[m + 2], c, -sn, c, sn);
           }
         }
@@ -756,7 +710,7 @@ struct KiviWindowRope {
             const int m = dl + 16 * j;
             float cp, sp, cj, sj;
             f2(wrows[rp * 64 + m], cp, sp);
-            f2(*reinterpret_cast<const uint32_t*>(&offs->cs[0][jj][2 * m]), cj, sj);
+            f2(*reinterpret_cast<const uint32_t*>(&offs->cs[jj][2 * m]), cj, sj);
             const float c = __builtin_fmaf(cp, cj, -(sp * sj)), sn = __builtin_fmaf(sp, cj, cp * sj);
             float x0 = get(kr[j][0], e), x1 = get(kr[j][1], e);
             rope_rotate(x0, x1, c, sn);
@@ -772,8 +726,8 @@ struct KiviWindowRope {
             // pairs pi, pi + 1: one dword of cosines, one of (positive) sines
             const int pi = 2 * (dl + 16 * j);
             float cj[2], sj[2];
-            f2(*reinterpret_cast<const uint32_t*>(&offs->cs[0][jj][pi]), cj[0], cj[1]);
-            f2(*reinterpret_cast<const uint32_t*>(&offs->cs[1][jj][pi + 64]), sj[0], sj[1]);
+            f2(*reinterpret_cast<const uint32_t*>(&offs->cs[jj][pi]), cj[0], cj[1]);
+            f2(*reinterpret_cast<const uint32_t*>(&offs->cs[jj][pi + 64]), sj[0], sj[1]);
 #pragma unroll
             for (int r = 0; r < 2; ++r) {
               float cp, sp;
@@ -982,12 +936,12 @@ __global__ __launch_bounds__(NW * kWave, 2) void kivi_decode_kernel(KiviParams k
   uint32_t* s_wrot = nullptr;          // the window's page rotations (residual wavefront)
   if constexpr (ROPE) {
     __shared__ __attribute__((aligned(16))) RopeTable s_rope_tb;
-    constexpr int kCap = kivi_page_rot_cap<BITS>();
+    constexpr int kCap = kivi_page_rot_cap(BITS);
     __shared__ __attribute__((aligned(16))) uint16_t s_prot[kCap][2][kKiviHead / 2];
     __shared__ __attribute__((aligned(16))) uint32_t s_wrot_tb[kWinRows][kKiviHead / 2];
     s_wrot = &s_wrot_tb[0][0];
-    constexpr int kN = kRopeRows * kKiviHead / (NW * kWave);
-    static_assert(kRopeRows * kKiviHead % (NW * kWave) == 0, "whole rounds");
+    constexpr int kN = kRopeRows * (kKiviHead / 2) / (NW * kWave);
+    static_assert(kRopeRows * (kKiviHead / 2) % (NW * kWave) == 0, "whole rounds");
     // the page rotations: rows 32 p of pages pg_first .. pg_first + kCap - 1,
     // 16 bytes of one table per load (kQ per row)
     constexpr int kQ = kKiviHead / 2 / 4;
@@ -1007,17 +961,16 @@ __global__ __launch_bounds__(NW * kWave, 2) void kivi_decode_kernel(KiviParams k
     float cv[kN], sv[kN];
 #pragma unroll
     for (int r = 0; r < kN; ++r) {
-      const int i = tid + r * NW * kWave, j = i / kKiviHead, c = i % kKiviHead;
-      rope_cs1(k, j, k.rope_style == 0 ? c >> 1 : c & 63, cv[r], sv[r]);
+      const int i = tid + r * NW * kWave, j = i / (kKiviHead / 2), pr = i % (kKiviHead / 2);
+      rope_cs1(k, j, pr, cv[r], sv[r]);
     }
 #pragma unroll
     for (int r = 0; r < kN; ++r) {
-      const int i = tid + r * NW * kWave, j = i / kKiviHead, c = i % kKiviHead;
-      const bool first = k.rope_style == 0 ? (c & 1) == 0 : c < 64;
-      // style 0: cs[0] holds (cos, sin) of pair c / 2 in the dword of
-      // channels c, c + 1 (rope_rot_adjacent); cs[1] is not read
-      s_rope_tb.cs[0][j][c] = __builtin_bit_cast(uint16_t, (_Float16)(k.rope_style == 0 && (c & 1) ? sv[r] : cv[r]));
-      s_rope_tb.cs[1][j][c] = __builtin_bit_cast(uint16_t, (_Float16)(first ? -sv[r] : sv[r]));
+      const int i = tid + r * NW * kWave, j = i / (kKiviHead / 2), pr = i % (kKiviHead / 2);
+      const int oc = k.rope_style == 0 ? 2 * pr : pr, os = k.rope_style == 0 ? 2 * pr + 1 : kKiviHead / 2 + pr;
+      const _Float16 ch = (_Float16)cv[r], sh = (_Float16)sv[r];
+      s_rope_tb.cs[j][oc] = __builtin_bit_cast(uint16_t, ch);
+      s_rope_tb.cs[j][os] = __builtin_bit_cast(uint16_t, sh);
     }
 #pragma unroll
     for (int r = 0; r < kPR; ++r) {
@@ -1245,6 +1198,8 @@ int launch_kivi_decode(const KiviDecodeLaunch& a) {
   const bool append = a.append != nullptr;
   if (append) k.job = make_page_job(*a.append);
   const unsigned items = (unsigned)(a.num_seqs * a.num_kv_heads * p.head_slices);
+  // keys held before RoPE: every page rotation of a workgroup in its LDS rows
+  if (a.rope_cos && a.partition_pages > kivi_page_rot_cap(a.bits)) return 3;
   if (a.num_partitions == 1) {
     // 4 wavefronts per workgroup, two workgroups per CU: at batch 64 the
     // grid is resident in one round (65.1 against 67.1 us with 8)
