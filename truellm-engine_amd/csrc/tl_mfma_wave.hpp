@@ -62,6 +62,18 @@ __device__ __forceinline__ uint32_t ld_nt(const char* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(p));
 }
 
+// FP8 K at block sizes 8 and 16: lanes m and m ^ 1 (same kg) load rows
+// 4 (2 j2) + kg and 4 (2 j2 + 1) + kg of their block, 8 bytes each: both
+// lanes' token quads of that row (the even lane's quad first).  One dword
+// each way (DPP, adjacent lanes) leaves each lane its own quad of both
+// rows, r0 of the first and r1 of the second.
+__device__ __forceinline__ void k8_pair(uint32_t x, uint32_t y, bool odd, uint32_t& r0, uint32_t& r1) {
+  const uint32_t send = odd ? x : y;
+  const uint32_t recv = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)send, 0xB1, 0xF, 0xF, false);  // [1,0,3,2]
+  r0 = odd ? recv : x;
+  r1 = odd ? y : recv;
+}
+
 // Max / sum over the lanes l, l ^ 16, l ^ 32, l ^ 48.
 __device__ __forceinline__ float max_kg(float v) {
   auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, v), __builtin_bit_cast(unsigned, v),
@@ -274,12 +286,28 @@ __device__ __forceinline__ State fp8_wave(const Params& p, int seq, int kvh, int
   // this lane's K quad and V run: their blocks within the iteration and
   // their byte offsets in a block row (plus the iteration's own offset when
   // a block holds several iterations)
+  // Block sizes 8 and 16 load K 8 bytes per lane (k8_pair), so that each
+  // load instruction reads whole 128-byte lines of a block (4-byte loads
+  // read 64-byte halves of four blocks' lines).
+  constexpr bool kK8 = BS <= 16;
+  const bool odd = (m & 1) != 0;
   const int kb = NB > 1 ? (4 * m) / BS : 0, vb = NB > 1 ? (16 * kg) / BS : 0;
-  const char* kbase0 = p.k_cache + (int64_t)kvh * kBlockBytes + RB * kg + (4 * m) % (NB > 1 ? BS : TPI);
+  const char* kbase0 = kK8 ? p.k_cache + (int64_t)kvh * kBlockBytes + RB * kg + (4 * (m & ~1)) % BS + 4 * RB * (m & 1)
+                           : p.k_cache + (int64_t)kvh * kBlockBytes + RB * kg + (4 * m) % (NB > 1 ? BS : TPI);
   const char* vbase0 = p.v_cache + (int64_t)kvh * kBlockBytes + RB * m + (16 * kg) % (NB > 1 ? BS : TPI);
   auto load_k = [&](uint32_t (&kw)[32], const char* base) {
+    if constexpr (kK8) {
+      typedef unsigned u2v __attribute__((ext_vector_type(2)));
 #pragma unroll
-    for (int j = 0; j < 32; ++j) kw[j] = ld_nt(base + 4 * RB * j);
+      for (int j2 = 0; j2 < 16; ++j2) {
+        const u2v w = __builtin_nontemporal_load(reinterpret_cast<const u2v*>(base + 8 * RB * j2));
+        kw[2 * j2] = w.x;
+        kw[2 * j2 + 1] = w.y;
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 32; ++j) kw[j] = ld_nt(base + 4 * RB * j);
+    }
   };
   // base: the run's block (its first 8 tokens' block at block size 8),
   // base2: the block of tokens 8 .. 15 at block size 8 (unused otherwise)
@@ -335,7 +363,15 @@ __device__ __forceinline__ State fp8_wave(const Params& p, int seq, int kvh, int
       uint32_t a[4][4];   // [tile][f16 pair]
 #pragma unroll
       for (int hf = 0; hf < 2; ++hf) {
-        const uint32_t* w = &kw[8 * sk + 4 * hf];   // rows 32 sk + 16 hf + 4 c + kg
+        const int j0 = 8 * sk + 4 * hf;             // rows 32 sk + 16 hf + 4 c + kg
+        uint32_t w[4];
+        if constexpr (kK8) {
+          k8_pair(kw[j0], kw[j0 + 1], odd, w[0], w[1]);
+          k8_pair(kw[j0 + 2], kw[j0 + 3], odd, w[2], w[3]);
+        } else {
+#pragma unroll
+          for (int c = 0; c < 4; ++c) w[c] = kw[j0 + c];
+        }
         const uint32_t x0 = __builtin_amdgcn_perm(w[1], w[0], 0x05010400u);  // tokens 0, 1
         const uint32_t x1 = __builtin_amdgcn_perm(w[1], w[0], 0x07030602u);  // tokens 2, 3
         const uint32_t y0 = __builtin_amdgcn_perm(w[3], w[2], 0x05010400u);
