@@ -62,9 +62,10 @@ __device__ __forceinline__ uint32_t ld_nt(const char* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(p));
 }
 
-// FP8 K at block sizes 8 and 16: lanes m and m ^ 1 (same kg) load rows
-// 4 (2 j2) + kg and 4 (2 j2 + 1) + kg of their block, 8 bytes each: both
-// lanes' token quads of that row (the even lane's quad first).  One dword
+// K of FP8 at block sizes 8 and 16 and of 2-byte KV at block size 8: lanes
+// m and m ^ 1 (same kg) load rows 4 (2 j2) + kg and 4 (2 j2 + 1) + kg of
+// their block, 8 bytes each: both lanes' token quads (FP8) or pairs (2-byte)
+// of that row, the even lane's first.  One dword
 // each way (DPP, adjacent lanes) leaves each lane its own quad of both
 // rows, r0 of the first and r1 of the second.
 __device__ __forceinline__ void k8_pair(uint32_t x, uint32_t y, bool odd, uint32_t& r0, uint32_t& r1) {
@@ -498,12 +499,29 @@ __device__ __forceinline__ State mfma2_wave(const Params& p, int seq, int kvh, i
   // this lane's K pair and V run: their blocks within the iteration and
   // their byte offsets in a block row (plus the iteration's own offset when
   // a block holds several iterations)
+  // Block size 8 loads K 8 bytes per lane (two token pairs of a row, lanes
+  // m and m ^ 1 on alternate rows: k8_pair), so that each load instruction
+  // reads whole 128-byte lines of a block (4-byte loads read 64-byte halves
+  // of four blocks' lines there).
+  constexpr bool kK8 = BS == 8;
+  const bool odd = (m & 1) != 0;
   const int kb = NB > 1 ? (2 * m) / BS : 0, vb = NB > 1 ? (8 * kg) / BS : 0;
-  const char* kbase0 = p.k_cache + (int64_t)kvh * kBlockBytes + RB * kg + 2 * ((2 * m) % (NB > 1 ? BS : TPI));
+  const char* kbase0 = kK8 ? p.k_cache + (int64_t)kvh * kBlockBytes + RB * kg + 2 * ((2 * (m & ~1)) % BS) + 4 * RB * (m & 1)
+                           : p.k_cache + (int64_t)kvh * kBlockBytes + RB * kg + 2 * ((2 * m) % (NB > 1 ? BS : TPI));
   const char* vbase0 = p.v_cache + (int64_t)kvh * kBlockBytes + RB * m + 2 * ((8 * kg) % (NB > 1 ? BS : TPI));
   auto load_k = [&](uint32_t (&kw)[32], const char* base) {
+    if constexpr (kK8) {
+      typedef unsigned u2v __attribute__((ext_vector_type(2)));
 #pragma unroll
-    for (int j = 0; j < 32; ++j) kw[j] = ld_nt(base + 4 * RB * j);
+      for (int j2 = 0; j2 < 16; ++j2) {
+        const u2v w = __builtin_nontemporal_load(reinterpret_cast<const u2v*>(base + 8 * RB * j2));
+        kw[2 * j2] = w.x;
+        kw[2 * j2 + 1] = w.y;
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 32; ++j) kw[j] = ld_nt(base + 4 * RB * j);
+    }
   };
   auto load_v = [&](u32x4 (&vr)[8], const char* base) {
 #pragma unroll
@@ -539,7 +557,14 @@ __device__ __forceinline__ State mfma2_wave(const Params& p, int seq, int kvh, i
     f4 s[2] = {f4{0.f, 0.f, 0.f, 0.f}, f4{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
     for (int sk = 0; sk < 4; ++sk) {
-      const uint32_t* w = &kw[8 * sk];            // rows 32 sk + 4 e + kg
+      uint32_t w[8];                              // rows 32 sk + 4 e + kg
+      if constexpr (kK8) {
+#pragma unroll
+        for (int e2 = 0; e2 < 4; ++e2) k8_pair(kw[8 * sk + 2 * e2], kw[8 * sk + 2 * e2 + 1], odd, w[2 * e2], w[2 * e2 + 1]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) w[e] = kw[8 * sk + e];
+      }
       uint32_t a[2][4];
 #pragma unroll
       for (int e2 = 0; e2 < 4; ++e2) {
