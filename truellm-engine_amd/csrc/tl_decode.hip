@@ -325,7 +325,7 @@ __global__ __launch_bounds__(NW * kWave) void decode2_kernel(Params p) {
   decode2_wave<KV, HEAD, BS>(p, seq, kvh, hs, t0 + wave * 32, t1, NW * 32, &s_p[wave][0][0][0][0],
                              &s_acc[wave][0][0], &s_m[wave][0], &s_l[wave][0]);
   __syncthreads();
-  combine_waves<KV, PO, HEAD, FINAL>(p, NW, &s_m[0][0], &s_l[0][0], &s_acc[0][0][0], seq, kvh, hs,
+  combine_waves<KV, PO, HEAD, FINAL, kWaveHeads, NW>(p, NW, &s_m[0][0], &s_l[0][0], &s_acc[0][0][0], seq, kvh, hs,
                                      part, tid, NW * kWave);
 }
 

@@ -327,25 +327,39 @@ __device__ __forceinline__ void decode2_wave(const Params& p, int seq, int kvh, 
 }
 
 // Merges the nw wavefront states (s_m [nw][GT], s_l [nw][GT], s_acc
-// [nw][GT][HEAD], GT q heads per wavefront) and writes the workgroup's
-// result: the normalised output (FINAL) or the partition's (max, sum,
-// normalised partial) for the log-sum-exp merge.
-template <Kind QK, Kind PO, int HEAD, bool FINAL, int GT = kWaveHeads>
+// [nw][GT][HEAD], GT q heads per wavefront; nw <= MAXW) and writes the
+// workgroup's result: the normalised output (FINAL) or the partition's
+// (max, sum, normalised partial) for the log-sum-exp merge.
+template <Kind QK, Kind PO, int HEAD, bool FINAL, int GT = kWaveHeads, int MAXW = 8>
 __device__ __forceinline__ void combine_waves(const Params& p, int nw, const float* s_m,
                                               const float* s_l, const float* s_acc, int seq, int kvh,
                                               int hs, int part, int tid, int nthreads) {
   for (int i = tid; i < GT * HEAD; i += nthreads) {
     const int g = i / HEAD, d = i % HEAD, gi = hs * GT + g;
     if (gi >= p.group) continue;
+    // every state's reads at once (rows clamped to nw - 1, the extra ones
+    // unused); a loop over the run-time count waited for one LDS round
+    // trip per state and value
+    float mw[MAXW], lw[MAXW], aw[MAXW];
+#pragma unroll
+    for (int w = 0; w < MAXW; ++w) {
+      const int r = min(w, nw - 1);
+      mw[w] = s_m[r * GT + g];
+      lw[w] = s_l[r * GT + g];
+      aw[w] = s_acc[(r * GT + g) * HEAD + d];
+    }
     float M = -INFINITY;
-    for (int w = 0; w < nw; ++w) M = fmaxf(M, s_m[w * GT + g]);
+#pragma unroll
+    for (int w = 0; w < MAXW; ++w) M = fmaxf(M, mw[w]);
     float num = 0.f, den = 0.f;
     if (M != -INFINITY) {
-      for (int w = 0; w < nw; ++w) {
-        const float mw = s_m[w * GT + g];
-        const float f = (mw == -INFINITY) ? 0.f : exp2f(mw - M);
-        num += f * s_acc[(w * GT + g) * HEAD + d];
-        den += f * s_l[w * GT + g];
+#pragma unroll
+      for (int w = 0; w < MAXW; ++w) {
+        if (w < nw) {
+          const float f = (mw[w] == -INFINITY) ? 0.f : exp2f(mw[w] - M);
+          num += f * aw[w];
+          den += f * lw[w];
+        }
       }
     }
     const float val = (den > 0.f) ? num / den : 0.f;

@@ -1135,7 +1135,7 @@ __global__ __launch_bounds__(NW * kWave, 2) void kivi_decode_kernel(KiviParams k
       qv = kivi_piece_quarter_values(ahead, wave, tid % kWave, reinterpret_cast<const uint16_t*>(&sd.p[NW - 1][0]));
     }
   }
-  combine_waves<Kind::F16, Kind::F32, kKiviHead, FINAL>(p, has_res ? NW + 2 : NW, &sd.m[0][0], &sd.l[0][0],
+  combine_waves<Kind::F16, Kind::F32, kKiviHead, FINAL, kWaveHeads, NW + 2>(p, has_res ? NW + 2 : NW, &sd.m[0][0], &sd.l[0][0],
                                                         &sd.acc[0][0][0], seq, kvh, hs, part, tid, NW * kWave);
   if constexpr (APPEND) {
     if (piece_pid >= 0)

@@ -768,7 +768,7 @@ __device__ __forceinline__ void decode_workgroup(const Params& p, int seq, int k
   st.store(KV == Kind::FP8 ? p.v_scale : 1.f, lane & 15, lane >> 4, s_acc + wave * kHeads * kHead,
            s_m + wave * kHeads, s_l + wave * kHeads);
   __syncthreads();
-  combine_waves<QK, PO, kHead, FINAL, kHeads>(p, NW, s_m, s_l, s_acc, seq, kvh, hs, part, tid, NW * kWave);
+  combine_waves<QK, PO, kHead, FINAL, kHeads, NW>(p, NW, s_m, s_l, s_acc, seq, kvh, hs, part, tid, NW * kWave);
 }
 
 }  // namespace mw
