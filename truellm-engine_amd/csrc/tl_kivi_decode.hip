@@ -614,11 +614,16 @@ __device__ __forceinline__ void kivi_pages_wave(const KiviParams& k, int seq, in
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   if (grp == 0) {
+    // all of cz first: read between the stores (which may alias it, for
+    // the compiler) each read waited for the LDS
+    f4 cz[GT];
+#pragma unroll
+    for (int r = 0; r < GT; ++r) cz[r] = *reinterpret_cast<const f4*>(s_cz + r * 4);
 #pragma unroll
     for (int nt = 0; nt < 8; ++nt)
 #pragma unroll
       for (int r = 0; r < GT; ++r)
-        s_acc_w[r * kKiviHead + nt * 16 + u] = __builtin_fmaf(st.acc[nt][r], kTwo24, s_cz[r * 4 + nt / 2]);
+        s_acc_w[r * kKiviHead + nt * 16 + u] = __builtin_fmaf(st.acc[nt][r], kTwo24, cz[r][nt / 2]);
   }
 }
 
