@@ -9,6 +9,7 @@
 // per token over groups of 32 channels, then lays the nibbles out as in
 // tl_kivi.hpp.
 #pragma once
+#include <cstddef>
 
 #include "tl_device.hpp"
 #include "tl_internal.hpp"
@@ -151,33 +152,56 @@ __device__ __forceinline__ void build_barrier() {
 // The group quantiser over unit u of a page: u < 128 is K channel u (its 32
 // tokens in order), u >= 128 is V (token, group of 32 channels) u - 128
 // (channels in order).  Codes go to qk / qv, step and zero to the page.
+// The unit's 32 values are read once, as 16 dwords (every row of k and v
+// starts 4-byte aligned), scanned in order (ties and signed zeros keep
+// the first occurrence, as the reference's scan), and the codes are
+// written as 8 dwords: read back per code between byte stores, each read
+// waited for the LDS.
 template <int BITS>
 __device__ __forceinline__ void quantise_unit(KiviBuildSmem<BITS>& sm, int u) {
   using F = KiviFmt<BITS>;
   constexpr int T = kKiviPageTokens, D = kKiviHead, LV = F::kLevels;
+  static_assert(T == 32, "32 values per unit");
+  static_assert(offsetof(KiviBuildSmem<BITS>, v) % 4 == 0 && offsetof(KiviBuildSmem<BITS>, qk) % 4 == 0 &&
+                    offsetof(KiviBuildSmem<BITS>, qv) % 4 == 0 && sizeof(sm.k[0]) % 4 == 0 && sizeof(sm.v[0]) % 4 == 0,
+                "rows of k, v, qk and qv start 4-byte aligned");
+  const uint16_t* src;
+  uint8_t* dst;
+  if (u < D) {
+    src = &sm.k[u][0];
+    dst = &sm.qk[u][0];
+  } else {
+    const int t = (u - D) / 4, g = (u - D) % 4;
+    src = &sm.v[t][g * 32];
+    dst = &sm.qv[t][g * 32];
+  }
+  uint32_t w[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) w[i] = reinterpret_cast<const uint32_t*>(src)[i];
+  float x[32];
+#pragma unroll
+  for (int i = 0; i < 32; ++i) x[i] = f16_to_f32(uint16_t(w[i / 2] >> (16 * (i & 1))));
+  float gmin = FLT_MAX, gmax = -FLT_MAX;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) {
+    if (x[i] < gmin) gmin = x[i];
+    if (x[i] > gmax) gmax = x[i];
+  }
+  const GroupQ q = group_params<LV>(gmin, gmax);
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    uint32_t c = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) c |= (uint32_t)quantise<LV>(x[4 * k + e], q) << (8 * e);
+    reinterpret_cast<uint32_t*>(dst)[k] = c;
+  }
   if (u < D) {
     const int c = u;
-    float gmin = FLT_MAX, gmax = -FLT_MAX;
-    for (int t = 0; t < T; ++t) {
-      const float x = f16_to_f32(sm.k[c][t]);
-      if (x < gmin) gmin = x;
-      if (x > gmax) gmax = x;
-    }
-    const GroupQ q = group_params<LV>(gmin, gmax);
-    for (int t = 0; t < T; ++t) sm.qk[c][t] = (uint8_t)quantise<LV>(f16_to_f32(sm.k[c][t]), q);
     uint16_t* kp = reinterpret_cast<uint16_t*>(sm.page + F::kKParams + (c / 8) * 32);
     kp[c % 8] = q.step;
     kp[8 + c % 8] = q.zero;
   } else {
     const int t = (u - D) / 4, g = (u - D) % 4;
-    float gmin = FLT_MAX, gmax = -FLT_MAX;
-    for (int i = 0; i < 32; ++i) {
-      const float x = f16_to_f32(sm.v[t][g * 32 + i]);
-      if (x < gmin) gmin = x;
-      if (x > gmax) gmax = x;
-    }
-    const GroupQ q = group_params<LV>(gmin, gmax);
-    for (int i = 0; i < 32; ++i) sm.qv[t][g * 32 + i] = (uint8_t)quantise<LV>(f16_to_f32(sm.v[t][g * 32 + i]), q);
     const int r = kivi_v_group(t), s = kivi_v_slot(t);
     uint16_t* vp = reinterpret_cast<uint16_t*>(sm.page + F::kVParams + (g * 4 + r) * 32);
     vp[s] = q.step;
