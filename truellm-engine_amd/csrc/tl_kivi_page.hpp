@@ -222,8 +222,10 @@ __device__ void kivi_build_page(KiviBuildSmem<BITS>& sm, const PageJob& j, int s
   using F = KiviFmt<BITS>;
   constexpr int T = kKiviPageTokens, D = kKiviHead;
   if (page >= j.max_pages_per_seq) return;
+  // the page's slot is checked only before its store, so that the block
+  // table and pool loads do not wait for it (one memory round trip fewer
+  // before a build; a hole just skips the store)
   const int pid = j.page_tables[(int64_t)seq * j.max_pages_per_seq + page];
-  if (pid < 0 || pid >= j.num_pages) return;
   const int64_t new_off = ((int64_t)seq * j.num_kv_heads + kvh) * D;
 
   // gather the 32 tokens: element (token t, channel c) of the fp16 pool; the
@@ -336,6 +338,7 @@ __device__ void kivi_build_page(KiviBuildSmem<BITS>& sm, const PageJob& j, int s
   }
   build_barrier<NT>();
 
+  if (pid < 0 || pid >= j.num_pages) return;
   uint8_t* dst = j.pages + ((int64_t)pid * j.num_kv_heads + kvh) * F::kBytes;
   for (int i = tid; i < F::kBytes / 16; i += NT)
     reinterpret_cast<u32x4*>(dst)[i] = reinterpret_cast<const u32x4*>(sm.page)[i];
