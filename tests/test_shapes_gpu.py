@@ -2,7 +2,7 @@
 
 - Head size 128 with every power-of-two block size the engine's
   `paged_kv_block_size` may take (config_schema.h:68): 8 .. 256 for 2-byte
-  pools, 16 .. 256 for FP8 pools.
+  and FP8 pools (FP8 at 16 in test_fp8_gpu.py).
 - The reference's other dispatch shapes (paged_attention_v1.cu:198-209): F16
   heads 80 and 96, F32 heads 64 and 256, at block size 16.
 - tl_paged_attention_v2 runs the library's plan inside the caller's scratch:
