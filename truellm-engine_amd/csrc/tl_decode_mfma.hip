@@ -26,39 +26,56 @@ namespace {
 
 // Work item of a decode workgroup: (sequence, kv head, head slice,
 // partition) and the partition's token range [t0, t1); false when the
-// partition starts past the sequence (split-K only).
+// partition starts past the sequence (split-K only).  With late_exit (and
+// for the single pass) the item is always returned, t1 is the partition's
+// end and len the sequence's length, applied by the wavefronts after their
+// first loads: the block-table
+// reads and the first K/V loads are then issued together with the length
+// read instead of after it, and a partition past the end exits once they
+// are done (decode_workgroup).
 struct Item {
-  int seq, kvh, hs, part, t0, t1;
+  int seq, kvh, hs, part, t0, t1, len;
 };
-__device__ __forceinline__ bool item_of(const Params& p, bool final, Item& w) {
+__device__ __forceinline__ bool item_of(const Params& p, bool final, bool late_exit, Item& w) {
   int bid = grid_item(p, w.part);
   w.hs = bid % p.head_slices;      bid /= p.head_slices;
   w.kvh = bid % p.num_kv_heads;
   w.seq = bid / p.num_kv_heads;
   const int L = p.seq_lens[w.seq];
   w.t0 = w.part * p.partition_tokens;
+  if (late_exit || final) {           // final: one partition, t0 = 0
+    w.t1 = w.t0 + p.partition_tokens;
+    w.len = L;
+    return true;
+  }
   if (!final && w.t0 >= L) return false;
   w.t1 = min(w.t0 + p.partition_tokens, L);
+  w.len = 0x7fffffff;
   return true;
 }
 
-template <Kind QK, Kind PO, int NW, bool FINAL, int BS>
+// LATE: split-K items past the sequence's end exit after their first loads
+// (item_of's late_exit), for grids that fit the GPU in one round, where the
+// launch is a chain of round trips (length, table, K/V, partials) and the
+// loads of an exiting workgroup cost nothing.
+template <Kind QK, Kind PO, int NW, bool FINAL, int BS, bool LATE = false>
 __global__ __launch_bounds__(NW * kWave) void fp8_decode_kernel(Params p) {
   __shared__ __attribute__((aligned(16))) float s_acc[NW * mw::kHeads * mw::kHead];
   __shared__ float s_m[NW * mw::kHeads], s_l[NW * mw::kHeads];
   Item w;
-  if (!item_of(p, FINAL, w)) return;
-  mw::decode_workgroup<Kind::FP8, QK, PO, NW, FINAL, BS>(p, w.seq, w.kvh, w.hs, w.part, w.t0, w.t1, s_acc, s_m,
-                                                         s_l);
+  if (!item_of(p, FINAL, LATE, w)) return;
+  mw::decode_workgroup<Kind::FP8, QK, PO, NW, FINAL, BS, LATE>(p, w.seq, w.kvh, w.hs, w.part, w.t0, w.t1, s_acc,
+                                                               s_m, s_l, w.len);
 }
 
-template <Kind KV, Kind PO, int NW, bool FINAL, int BS>
+template <Kind KV, Kind PO, int NW, bool FINAL, int BS, bool LATE = false>
 __global__ __launch_bounds__(NW * kWave) void mfma2_decode_kernel(Params p) {
   __shared__ __attribute__((aligned(16))) float s_acc[NW * mw::kHeads * mw::kHead];
   __shared__ float s_m[NW * mw::kHeads], s_l[NW * mw::kHeads];
   Item w;
-  if (!item_of(p, FINAL, w)) return;
-  mw::decode_workgroup<KV, KV, PO, NW, FINAL, BS>(p, w.seq, w.kvh, w.hs, w.part, w.t0, w.t1, s_acc, s_m, s_l);
+  if (!item_of(p, FINAL, LATE, w)) return;
+  mw::decode_workgroup<KV, KV, PO, NW, FINAL, BS, LATE>(p, w.seq, w.kvh, w.hs, w.part, w.t0, w.t1, s_acc, s_m,
+                                                        s_l, w.len);
 }
 
 // Split-K, whole partitions per wavefront (mw::partitions_per_wave): the
@@ -100,13 +117,15 @@ bool partition_per_wave(int partition_tokens, long partitions_total) {
 }
 
 // PO_SPLIT: the split-K partial outputs' type (F32, or F16 for f16 q)
-template <Kind KV, Kind QK, int NW, bool FINAL, int BS, Kind PO_SPLIT = Kind::F32>
+template <Kind KV, Kind QK, int NW, bool FINAL, int BS, Kind PO_SPLIT = Kind::F32, bool LATE = false>
 void launch_kernel(const Params& p, unsigned grid, hipStream_t stream) {
   constexpr Kind PO = FINAL ? QK : PO_SPLIT;
   if constexpr (KV == Kind::FP8)
-    hipLaunchKernelGGL((fp8_decode_kernel<QK, PO, NW, FINAL, BS>), dim3(grid), dim3(NW * kWave), 0, stream, p);
+    hipLaunchKernelGGL((fp8_decode_kernel<QK, PO, NW, FINAL, BS, LATE>), dim3(grid), dim3(NW * kWave), 0, stream,
+                       p);
   else
-    hipLaunchKernelGGL((mfma2_decode_kernel<KV, PO, NW, FINAL, BS>), dim3(grid), dim3(NW * kWave), 0, stream, p);
+    hipLaunchKernelGGL((mfma2_decode_kernel<KV, PO, NW, FINAL, BS, LATE>), dim3(grid), dim3(NW * kWave), 0, stream,
+                       p);
 }
 
 template <Kind KV, Kind QK, int BS>
@@ -156,9 +175,17 @@ int launch_typed(const DecodeLaunch& a) {
     // workgroup (two per SIMD: the wavefront keeps its 256 registers), so
     // that each streams two of a 512-token partition's iterations
     if (f16_parts) {
-      if constexpr (KV == Kind::F16) launch_kernel<KV, QK, 8, false, BS, Kind::F16>(p, items * P, a.stream);
+      if constexpr (KV == Kind::F16) launch_kernel<KV, QK, 8, false, BS, Kind::F16, true>(p, items * P, a.stream);
     } else {
-      launch_kernel<KV, QK, 8, false, BS>(p, items * P, a.stream);
+      launch_kernel<KV, QK, 8, false, BS, Kind::F32, true>(p, items * P, a.stream);
+    }
+  } else if (items * P <= 256) {
+    // one workgroup per CU at most (one sequence in 32 partitions of 128
+    // tokens x 8 kv heads): the items past the end exit late
+    if (f16_parts) {
+      if constexpr (KV == Kind::F16) launch_kernel<KV, QK, 4, false, BS, Kind::F16, true>(p, items * P, a.stream);
+    } else {
+      launch_kernel<KV, QK, 4, false, BS, Kind::F32, true>(p, items * P, a.stream);
     }
   } else if (f16_parts) {
     if constexpr (KV == Kind::F16) launch_kernel<KV, QK, 4, false, BS, Kind::F16>(p, items * P, a.stream);

@@ -482,8 +482,13 @@ __device__ __forceinline__ void load_q_operand(const Params& p, int seq, int kvh
   const bool real = u < kWaveHeads && gi < p.group;
   const uint16_t* qrow = (const uint16_t*)p.q +
       ((int64_t)seq * p.num_heads + (real ? head_of(p, kvh, gi) : 0)) * kKiviHead;
+  // loaded by every lane (a padding head reads head 0's row), then masked:
+  // loads under the lane's condition each wait on their own
 #pragma unroll
-  for (int m = 0; m < 4; ++m) q_raw[m] = real ? load16(qrow + 32 * m + 8 * grp) : u32x4{0u, 0u, 0u, 0u};
+  for (int m = 0; m < 4; ++m) q_raw[m] = load16(qrow + 32 * m + 8 * grp);
+#pragma unroll
+  for (int m = 0; m < 4; ++m)
+    if (!real) q_raw[m] = u32x4{0u, 0u, 0u, 0u};
 }
 
 // share_simd: raise the wavefront's priority on every other page pair (see

@@ -108,17 +108,29 @@ typedef const __attribute__((address_space(4))) int32_t* TableRow;
 // row (max_blocks_per_seq >= 1), and checked afterwards: a read under a
 // condition would make the compiler wait for every load in flight before
 // the entries are used.
+// table_raw issues the reads, table_check applies the checks: split, the
+// reads of a prologue can all be in flight before the first is used.
 template <int NB> struct Blocks { int e[NB]; };
 template <int NB, int BS>
-__device__ __forceinline__ Blocks<NB> table_blocks(const Params& p, TableRow table, int it, int t1) {
+__device__ __forceinline__ Blocks<NB> table_raw(const Params& p, TableRow table, int it) {
   Blocks<NB> b;
+#pragma unroll
+  for (int i = 0; i < NB; ++i)
+    b.e[i] = table[__builtin_amdgcn_readfirstlane(min((it + BS * i) / BS, p.max_blocks_per_seq - 1))];
+  return b;
+}
+template <int NB, int BS>
+__device__ __forceinline__ Blocks<NB> table_check(const Params& p, Blocks<NB> b, int it, int t1) {
 #pragma unroll
   for (int i = 0; i < NB; ++i) {
     const int tok = it + BS * i, lb = tok / BS;
-    const int e = table[__builtin_amdgcn_readfirstlane(min(lb, p.max_blocks_per_seq - 1))];
-    b.e[i] = (tok >= t1 || lb >= p.max_blocks_per_seq || e >= p.num_blocks) ? -1 : e;
+    b.e[i] = (tok >= t1 || lb >= p.max_blocks_per_seq || b.e[i] >= p.num_blocks) ? -1 : b.e[i];
   }
   return b;
+}
+template <int NB, int BS>
+__device__ __forceinline__ Blocks<NB> table_blocks(const Params& p, TableRow table, int it, int t1) {
+  return table_check<NB, BS>(p, table_raw<NB, BS>(p, table, it), it, t1);
 }
 // Entry i (per lane) of a wave-uniform set.  Written as one nested select:
 // a select loop over k is turned back into an indexed load, which puts the
@@ -235,8 +247,9 @@ struct NoFlush {
 // (v_scale).
 template <Kind QK, int BS, class Flush = NoFlush>
 __device__ __forceinline__ State fp8_wave(const Params& p, int seq, int kvh, int hs, int first_it, int t1,
-                                          int step, const Flush& flush = Flush()) {
+                                          int step, const Flush& flush = Flush(), int len = 0x7fffffff) {
   static_assert(BS >= 8 && (BS & (BS - 1)) == 0, "block size: a power of two >= 8");
+  t1 = min(t1, len);
   constexpr int TPI = 64, RB = BS;           // tokens per iteration; bytes per head-dim row of a block
   constexpr bool kSplitRun = BS == 8;        // a lane's 16-token V run spans two blocks
   constexpr int kBlockBytes = kHead * RB;
@@ -249,13 +262,22 @@ __device__ __forceinline__ State fp8_wave(const Params& p, int seq, int kvh, int
   const bool hv = gi < p.group;
   const int head = hv ? head_of(p, kvh, gi) : 0;
   const uint16_t* qrow = (const uint16_t*)p.q + ((int64_t)seq * p.num_heads + head) * kHead;
+  // the loads under one condition, used after it: loads under a condition
+  // of their own were each a branch with a wait, 32 round trips in a row
+  uint16_t qh[32] = {};
+  if (hv) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qh[8 * s + e] = qrow[32 * s + 4 * e + kg];
+  }
   float qf[32];
   float qmax = 0.f;
 #pragma unroll
   for (int s = 0; s < 4; ++s)
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const uint16_t bits = hv ? qrow[32 * s + 4 * e + kg] : (uint16_t)0;
+      const uint16_t bits = qh[8 * s + e];
       const float v = QK == Kind::BF16 ? bf16_to_f32(bits) : f16_to_f32(bits);
       qf[8 * s + e] = v;
       qmax = fmaxf(qmax, fabsf(v));
@@ -467,8 +489,10 @@ __device__ __forceinline__ State fp8_wave(const Params& p, int seq, int kvh, int
 // the run of 8 tokens that is k group kg of the p.v MFMA.
 // V: lane (m, kg) loads the 16 bytes of that run, row d = 16 dt + m.
 template <Kind KV, int BS, class Flush = NoFlush>
+// len: the sequence's length when t1 does not include it yet (the token
+// range is [first_it, min(t1, len)); the prologue's loads do not wait for it).
 __device__ __forceinline__ State mfma2_wave(const Params& p, int seq, int kvh, int hs, int first_it, int t1,
-                                            int step, const Flush& flush = Flush()) {
+                                            int step, const Flush& flush = Flush(), int len = 0x7fffffff) {
   static_assert(BS >= 8 && (BS & (BS - 1)) == 0, "block size: a power of two >= 8");
   constexpr int TPI = 32, RB = 2 * BS;       // tokens per iteration; bytes per head-dim row of a block
   constexpr int kBlockBytes = kHead * RB;
@@ -481,15 +505,6 @@ __device__ __forceinline__ State mfma2_wave(const Params& p, int seq, int kvh, i
   const bool hv = gi < p.group;
   const int head = hv ? head_of(p, kvh, gi) : 0;
   const uint16_t* qrow = (const uint16_t*)p.q + ((int64_t)seq * p.num_heads + head) * kHead;
-  u4v qb[4];
-#pragma unroll
-  for (int s = 0; s < 4; ++s)
-#pragma unroll
-    for (int e2 = 0; e2 < 4; ++e2) {
-      const uint32_t lo = hv ? qrow[32 * s + 8 * e2 + kg] : 0u;
-      const uint32_t hi = hv ? qrow[32 * s + 8 * e2 + 4 + kg] : 0u;
-      qb[s][e2] = lo | (hi << 16);
-    }
 
   State st;
   st.init();
@@ -528,9 +543,27 @@ __device__ __forceinline__ State mfma2_wave(const Params& p, int seq, int kvh, i
     for (int dt = 0; dt < 8; ++dt) vr[dt] = load16_stream(base + 16 * RB * dt);
   };
 
+  // The prologue in the order of its round trips: the table entries (all
+  // in flight together), q (the loads under one condition, used after it:
+  // loads under a condition of their own were each a branch with a wait),
+  // the first K/V, and q is packed while they fly.  Entries past len may be loaded: in bounds, and
+  // masked by the scores' valid-token count.
   int it = first_it;
-  Blocks<NB> cur = table_blocks<NB, BS>(p, table, it, t1);
-  Blocks<NB> nxt = table_blocks<NB, BS>(p, table, it + step, t1);
+  const Blocks<NB> cur_raw = table_raw<NB, BS>(p, table, it);
+  const Blocks<NB> nxt_raw = table_raw<NB, BS>(p, table, it + step);
+  __builtin_amdgcn_sched_barrier(0);
+  Blocks<NB> cur = table_check<NB, BS>(p, cur_raw, it, t1);
+  Blocks<NB> nxt = table_check<NB, BS>(p, nxt_raw, it + step, t1);
+  uint32_t qlo[16] = {}, qhi[16] = {};
+  if (hv) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int e2 = 0; e2 < 4; ++e2) {
+        qlo[4 * s + e2] = qrow[32 * s + 8 * e2 + kg];
+        qhi[4 * s + e2] = qrow[32 * s + 8 * e2 + 4 + kg];
+      }
+  }
   uint32_t kw[32];
   u32x4 vr[8];
   {
@@ -540,7 +573,18 @@ __device__ __forceinline__ State mfma2_wave(const Params& p, int seq, int kvh, i
     load_k(kw, kbase0 + ib + (int64_t)max(pick(cur, kb), 0) * pool_stride);
     __builtin_amdgcn_sched_barrier(0);
     load_v(vr, vbase0 + ib + (int64_t)max(pick(cur, vb), 0) * pool_stride);
+    __builtin_amdgcn_sched_barrier(0);
   }
+  t1 = min(t1, len);
+  // q's registers are opaque from here: otherwise the compiler packs them
+  // inside the condition, and waits for q there, before K/V are issued
+#pragma unroll
+  for (int i = 0; i < 16; ++i) asm volatile("" : "+v"(qlo[i]), "+v"(qhi[i]));
+  u4v qb[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s)
+#pragma unroll
+    for (int e2 = 0; e2 < 4; ++e2) qb[s][e2] = qlo[4 * s + e2] | (qhi[4 * s + e2] << 16);
 
 #pragma unroll 1
   for (; it < t1; it += step) {
@@ -628,11 +672,11 @@ __device__ __forceinline__ State mfma2_wave(const Params& p, int seq, int kvh, i
 
 template <Kind KV, Kind QK, int BS, class Flush = NoFlush>
 __device__ __forceinline__ State run_wave(const Params& p, int seq, int kvh, int hs, int first_it, int t1,
-                                          int step, const Flush& flush = Flush()) {
+                                          int step, const Flush& flush = Flush(), int len = 0x7fffffff) {
   if constexpr (KV == Kind::FP8)
-    return fp8_wave<QK, BS>(p, seq, kvh, hs, first_it, t1, step, flush);
+    return fp8_wave<QK, BS>(p, seq, kvh, hs, first_it, t1, step, flush, len);
   else
-    return mfma2_wave<KV, BS>(p, seq, kvh, hs, first_it, t1, step, flush);
+    return mfma2_wave<KV, BS>(p, seq, kvh, hs, first_it, t1, step, flush, len);
 }
 
 // A wavefront that ran a whole split-K partition alone writes its
@@ -756,15 +800,20 @@ __device__ __forceinline__ void partitions_per_wave(const Params& p, int seq, in
 
 // One workgroup of NW wavefronts over (sequence, kv head, 16-head slice,
 // partition): the wavefronts stride over the partition's iterations and
-// are merged in LDS (smem: NW x 16 x 128 + 2 x NW x 16 floats).
-template <Kind KV, Kind QK, Kind PO, int NW, bool FINAL, int BS = 16>
+// are merged in LDS (smem: NW x 16 x 128 + 2 x NW x 16 floats).  LATE:
+// the range is [t0, min(t1, len)), len applied after the wavefronts' first
+// loads; a partition past the end (len <= t0, the same for the whole
+// workgroup) returns then, writing nothing.
+template <Kind KV, Kind QK, Kind PO, int NW, bool FINAL, int BS = 16, bool LATE = false>
 __device__ __forceinline__ void decode_workgroup(const Params& p, int seq, int kvh, int hs, int part, int t0,
-                                                 int t1, float* s_acc, float* s_m, float* s_l) {
+                                                 int t1, float* s_acc, float* s_m, float* s_l,
+                                                 int len = 0x7fffffff) {
   constexpr int TPI = tokens_per_iteration<KV>();
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
   const int lane = tid % kWave;
-  const State st = run_wave<KV, QK, BS>(p, seq, kvh, hs, t0 + wave * TPI, t1, NW * TPI);
+  const State st = run_wave<KV, QK, BS>(p, seq, kvh, hs, t0 + wave * TPI, t1, NW * TPI, NoFlush(), len);
+  if (LATE && len <= t0) return;
   st.store(KV == Kind::FP8 ? p.v_scale : 1.f, lane & 15, lane >> 4, s_acc + wave * kHeads * kHead,
            s_m + wave * kHeads, s_l + wave * kHeads);
   __syncthreads();
