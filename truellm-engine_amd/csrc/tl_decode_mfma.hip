@@ -68,14 +68,15 @@ __global__ __launch_bounds__(NW * kWave) void fp8_decode_kernel(Params p) {
                                                                s_m, s_l, w.len);
 }
 
-template <Kind KV, Kind PO, int NW, bool FINAL, int BS, bool LATE = false>
+// ONE: partitions of at most one iteration per wavefront (mw::mfma2_wave).
+template <Kind KV, Kind PO, int NW, bool FINAL, int BS, bool LATE = false, bool ONE = false>
 __global__ __launch_bounds__(NW * kWave) void mfma2_decode_kernel(Params p) {
   __shared__ __attribute__((aligned(16))) float s_acc[NW * mw::kHeads * mw::kHead];
   __shared__ float s_m[NW * mw::kHeads], s_l[NW * mw::kHeads];
   Item w;
   if (!item_of(p, FINAL, LATE, w)) return;
-  mw::decode_workgroup<KV, KV, PO, NW, FINAL, BS, LATE>(p, w.seq, w.kvh, w.hs, w.part, w.t0, w.t1, s_acc, s_m,
-                                                        s_l, w.len);
+  mw::decode_workgroup<KV, KV, PO, NW, FINAL, BS, LATE, ONE>(p, w.seq, w.kvh, w.hs, w.part, w.t0, w.t1, s_acc, s_m,
+                                                             s_l, w.len);
 }
 
 // Split-K, whole partitions per wavefront (mw::partitions_per_wave): the
@@ -117,15 +118,26 @@ bool partition_per_wave(int partition_tokens, long partitions_total) {
 }
 
 // PO_SPLIT: the split-K partial outputs' type (F32, or F16 for f16 q)
-template <Kind KV, Kind QK, int NW, bool FINAL, int BS, Kind PO_SPLIT = Kind::F32, bool LATE = false>
+template <Kind KV, Kind QK, int NW, bool FINAL, int BS, Kind PO_SPLIT = Kind::F32, bool LATE = false,
+          bool ONE = false>
 void launch_kernel(const Params& p, unsigned grid, hipStream_t stream) {
   constexpr Kind PO = FINAL ? QK : PO_SPLIT;
   if constexpr (KV == Kind::FP8)
     hipLaunchKernelGGL((fp8_decode_kernel<QK, PO, NW, FINAL, BS, LATE>), dim3(grid), dim3(NW * kWave), 0, stream,
                        p);
   else
-    hipLaunchKernelGGL((mfma2_decode_kernel<KV, PO, NW, FINAL, BS, LATE>), dim3(grid), dim3(NW * kWave), 0, stream,
-                       p);
+    hipLaunchKernelGGL((mfma2_decode_kernel<KV, PO, NW, FINAL, BS, LATE, ONE>), dim3(grid), dim3(NW * kWave), 0,
+                       stream, p);
+}
+
+// The split-K kernels of small grids (LATE); ONE when no wavefront has a
+// second iteration (a partition at most NW iterations long).
+template <Kind KV, Kind QK, int NW, int BS, Kind PO_SPLIT>
+void launch_late(const Params& p, unsigned grid, hipStream_t stream) {
+  if (KV != Kind::FP8 && p.partition_tokens <= NW * mw::tokens_per_iteration<KV>())
+    launch_kernel<KV, QK, NW, false, BS, PO_SPLIT, true, true>(p, grid, stream);
+  else
+    launch_kernel<KV, QK, NW, false, BS, PO_SPLIT, true, false>(p, grid, stream);
 }
 
 template <Kind KV, Kind QK, int BS>
@@ -175,17 +187,17 @@ int launch_typed(const DecodeLaunch& a) {
     // workgroup (two per SIMD: the wavefront keeps its 256 registers), so
     // that each streams two of a 512-token partition's iterations
     if (f16_parts) {
-      if constexpr (KV == Kind::F16) launch_kernel<KV, QK, 8, false, BS, Kind::F16, true>(p, items * P, a.stream);
+      if constexpr (KV == Kind::F16) launch_late<KV, QK, 8, BS, Kind::F16>(p, items * P, a.stream);
     } else {
-      launch_kernel<KV, QK, 8, false, BS, Kind::F32, true>(p, items * P, a.stream);
+      launch_late<KV, QK, 8, BS, Kind::F32>(p, items * P, a.stream);
     }
   } else if (items * P <= 256) {
     // one workgroup per CU at most (one sequence in 32 partitions of 128
     // tokens x 8 kv heads): the items past the end exit late
     if (f16_parts) {
-      if constexpr (KV == Kind::F16) launch_kernel<KV, QK, 4, false, BS, Kind::F16, true>(p, items * P, a.stream);
+      if constexpr (KV == Kind::F16) launch_late<KV, QK, 4, BS, Kind::F16>(p, items * P, a.stream);
     } else {
-      launch_kernel<KV, QK, 4, false, BS, Kind::F32, true>(p, items * P, a.stream);
+      launch_late<KV, QK, 4, BS, Kind::F32>(p, items * P, a.stream);
     }
   } else if (f16_parts) {
     if constexpr (KV == Kind::F16) launch_kernel<KV, QK, 4, false, BS, Kind::F16>(p, items * P, a.stream);

@@ -488,9 +488,11 @@ __device__ __forceinline__ State fp8_wave(const Params& p, int seq, int kvh, int
 // Scores: lane (m, kg) holds head m, iteration tokens 8 kg + 2 r + i, i.e.
 // the run of 8 tokens that is k group kg of the p.v MFMA.
 // V: lane (m, kg) loads the 16 bytes of that run, row d = 16 dt + m.
-template <Kind KV, int BS, class Flush = NoFlush>
 // len: the sequence's length when t1 does not include it yet (the token
 // range is [first_it, min(t1, len)); the prologue's loads do not wait for it).
+// ONE: the wavefront runs at most one iteration (the plan's partitions are
+// at most one step long): no next-iteration table reads or loads.
+template <Kind KV, int BS, class Flush = NoFlush, bool ONE = false>
 __device__ __forceinline__ State mfma2_wave(const Params& p, int seq, int kvh, int hs, int first_it, int t1,
                                             int step, const Flush& flush = Flush(), int len = 0x7fffffff) {
   static_assert(BS >= 8 && (BS & (BS - 1)) == 0, "block size: a power of two >= 8");
@@ -550,7 +552,7 @@ __device__ __forceinline__ State mfma2_wave(const Params& p, int seq, int kvh, i
   // masked by the scores' valid-token count.
   int it = first_it;
   const Blocks<NB> cur_raw = table_raw<NB, BS>(p, table, it);
-  const Blocks<NB> nxt_raw = table_raw<NB, BS>(p, table, it + step);
+  const Blocks<NB> nxt_raw = ONE ? cur_raw : table_raw<NB, BS>(p, table, it + step);
   __builtin_amdgcn_sched_barrier(0);
   Blocks<NB> cur = table_check<NB, BS>(p, cur_raw, it, t1);
   Blocks<NB> nxt = table_check<NB, BS>(p, nxt_raw, it + step, t1);
@@ -594,7 +596,7 @@ __device__ __forceinline__ State mfma2_wave(const Params& p, int seq, int kvh, i
         st.init();
       }
     }
-    const Blocks<NB> nn = table_blocks<NB, BS>(p, table, it + 2 * step, t1);
+    const Blocks<NB> nn = ONE ? cur : table_blocks<NB, BS>(p, table, it + 2 * step, t1);
     const int ib_next = in_block_bytes<BS, TPI, 2>(it + step);
 
     // ---- q.k: 2 tiles (token i of each pair) x 4 MFMA steps ----
@@ -621,7 +623,7 @@ __device__ __forceinline__ State mfma2_wave(const Params& p, int seq, int kvh, i
     // the next iteration's loads are issued whether or not it exists (a
     // missing one reads block 0): under a condition the compiler would
     // wait for them, too, before this iteration's V is used
-    load_k(kw, kbase0 + ib_next + (int64_t)max(pick(nxt, kb), 0) * pool_stride);
+    if constexpr (!ONE) load_k(kw, kbase0 + ib_next + (int64_t)max(pick(nxt, kb), 0) * pool_stride);
 
     // ---- softmax: lane (m, kg) owns head m, iteration tokens 8 kg + 2 r + i ----
     const int ph_v = pick(cur, vb);
@@ -663,20 +665,20 @@ __device__ __forceinline__ State mfma2_wave(const Params& p, int seq, int kvh, i
       st.o[dt] = mma<KV>(vr[dt].x, vr[dt].y, vr[dt].z, vr[dt].w, pb, st.o[dt]);
       if constexpr (KV == Kind::BF16) st.o[dt] = mma<KV>(vr[dt].x, vr[dt].y, vr[dt].z, vr[dt].w, pl, st.o[dt]);
     }
-    load_v(vr, vbase0 + ib_next + (int64_t)max(pick(nxt, vb), 0) * pool_stride);
+    if constexpr (!ONE) load_v(vr, vbase0 + ib_next + (int64_t)max(pick(nxt, vb), 0) * pool_stride);
     cur = nxt;
     nxt = nn;
   }
   return st;
 }
 
-template <Kind KV, Kind QK, int BS, class Flush = NoFlush>
+template <Kind KV, Kind QK, int BS, class Flush = NoFlush, bool ONE = false>
 __device__ __forceinline__ State run_wave(const Params& p, int seq, int kvh, int hs, int first_it, int t1,
                                           int step, const Flush& flush = Flush(), int len = 0x7fffffff) {
   if constexpr (KV == Kind::FP8)
     return fp8_wave<QK, BS>(p, seq, kvh, hs, first_it, t1, step, flush, len);
   else
-    return mfma2_wave<KV, BS>(p, seq, kvh, hs, first_it, t1, step, flush, len);
+    return mfma2_wave<KV, BS, Flush, ONE>(p, seq, kvh, hs, first_it, t1, step, flush, len);
 }
 
 // A wavefront that ran a whole split-K partition alone writes its
@@ -804,7 +806,7 @@ __device__ __forceinline__ void partitions_per_wave(const Params& p, int seq, in
 // the range is [t0, min(t1, len)), len applied after the wavefronts' first
 // loads; a partition past the end (len <= t0, the same for the whole
 // workgroup) returns then, writing nothing.
-template <Kind KV, Kind QK, Kind PO, int NW, bool FINAL, int BS = 16, bool LATE = false>
+template <Kind KV, Kind QK, Kind PO, int NW, bool FINAL, int BS = 16, bool LATE = false, bool ONE = false>
 __device__ __forceinline__ void decode_workgroup(const Params& p, int seq, int kvh, int hs, int part, int t0,
                                                  int t1, float* s_acc, float* s_m, float* s_l,
                                                  int len = 0x7fffffff) {
@@ -812,7 +814,7 @@ __device__ __forceinline__ void decode_workgroup(const Params& p, int seq, int k
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
   const int lane = tid % kWave;
-  const State st = run_wave<KV, QK, BS>(p, seq, kvh, hs, t0 + wave * TPI, t1, NW * TPI, NoFlush(), len);
+  const State st = run_wave<KV, QK, BS, NoFlush, ONE>(p, seq, kvh, hs, t0 + wave * TPI, t1, NW * TPI, NoFlush(), len);
   if (LATE && len <= t0) return;
   st.store(KV == Kind::FP8 ? p.v_scale : 1.f, lane & 15, lane >> 4, s_acc + wave * kHeads * kHead,
            s_m + wave * kHeads, s_l + wave * kHeads);
