@@ -68,14 +68,14 @@ __global__ __launch_bounds__(NW * kWave) void fp8_decode_kernel(Params p) {
                                                                s_m, s_l, w.len);
 }
 
-// ONE: partitions of at most one iteration per wavefront (mw::mfma2_wave).
-template <Kind KV, Kind PO, int NW, bool FINAL, int BS, bool LATE = false, bool ONE = false>
+// ITERS: 1 or 2 when no wavefront has more iterations (mw::mfma2_wave).
+template <Kind KV, Kind PO, int NW, bool FINAL, int BS, bool LATE = false, int ITERS = 0>
 __global__ __launch_bounds__(NW * kWave) void mfma2_decode_kernel(Params p) {
   __shared__ __attribute__((aligned(16))) float s_acc[NW * mw::kHeads * mw::kHead];
   __shared__ float s_m[NW * mw::kHeads], s_l[NW * mw::kHeads];
   Item w;
   if (!item_of(p, FINAL, LATE, w)) return;
-  mw::decode_workgroup<KV, KV, PO, NW, FINAL, BS, LATE, ONE>(p, w.seq, w.kvh, w.hs, w.part, w.t0, w.t1, s_acc, s_m,
+  mw::decode_workgroup<KV, KV, PO, NW, FINAL, BS, LATE, ITERS>(p, w.seq, w.kvh, w.hs, w.part, w.t0, w.t1, s_acc, s_m,
                                                              s_l, w.len);
 }
 
@@ -119,25 +119,28 @@ bool partition_per_wave(int partition_tokens, long partitions_total) {
 
 // PO_SPLIT: the split-K partial outputs' type (F32, or F16 for f16 q)
 template <Kind KV, Kind QK, int NW, bool FINAL, int BS, Kind PO_SPLIT = Kind::F32, bool LATE = false,
-          bool ONE = false>
+          int ITERS = 0>
 void launch_kernel(const Params& p, unsigned grid, hipStream_t stream) {
   constexpr Kind PO = FINAL ? QK : PO_SPLIT;
   if constexpr (KV == Kind::FP8)
     hipLaunchKernelGGL((fp8_decode_kernel<QK, PO, NW, FINAL, BS, LATE>), dim3(grid), dim3(NW * kWave), 0, stream,
                        p);
   else
-    hipLaunchKernelGGL((mfma2_decode_kernel<KV, PO, NW, FINAL, BS, LATE, ONE>), dim3(grid), dim3(NW * kWave), 0,
+    hipLaunchKernelGGL((mfma2_decode_kernel<KV, PO, NW, FINAL, BS, LATE, ITERS>), dim3(grid), dim3(NW * kWave), 0,
                        stream, p);
 }
 
-// The split-K kernels of small grids (LATE); ONE when no wavefront has a
-// second iteration (a partition at most NW iterations long).
+// The split-K kernels of small grids (LATE), by the most iterations a
+// wavefront has (a partition of at most NW or 2 NW iterations).
 template <Kind KV, Kind QK, int NW, int BS, Kind PO_SPLIT>
 void launch_late(const Params& p, unsigned grid, hipStream_t stream) {
-  if (KV != Kind::FP8 && p.partition_tokens <= NW * mw::tokens_per_iteration<KV>())
-    launch_kernel<KV, QK, NW, false, BS, PO_SPLIT, true, true>(p, grid, stream);
+  const int step = NW * mw::tokens_per_iteration<KV>();
+  if (KV != Kind::FP8 && p.partition_tokens <= step)
+    launch_kernel<KV, QK, NW, false, BS, PO_SPLIT, true, 1>(p, grid, stream);
+  else if (KV != Kind::FP8 && p.partition_tokens <= 2 * step)
+    launch_kernel<KV, QK, NW, false, BS, PO_SPLIT, true, 2>(p, grid, stream);
   else
-    launch_kernel<KV, QK, NW, false, BS, PO_SPLIT, true, false>(p, grid, stream);
+    launch_kernel<KV, QK, NW, false, BS, PO_SPLIT, true, 0>(p, grid, stream);
 }
 
 template <Kind KV, Kind QK, int BS>

@@ -490,9 +490,11 @@ __device__ __forceinline__ State fp8_wave(const Params& p, int seq, int kvh, int
 // V: lane (m, kg) loads the 16 bytes of that run, row d = 16 dt + m.
 // len: the sequence's length when t1 does not include it yet (the token
 // range is [first_it, min(t1, len)); the prologue's loads do not wait for it).
-// ONE: the wavefront runs at most one iteration (the plan's partitions are
-// at most one step long): no next-iteration table reads or loads.
-template <Kind KV, int BS, class Flush = NoFlush, bool ONE = false>
+// ITERS 1 or 2: the wavefront runs at most that many iterations (the
+// plan's partitions are at most ITERS steps long): their K/V are all loaded
+// in the prologue, and no table entry or K/V past them is read (64 more
+// registers for 2).  0: any number, one iteration's loads ahead.
+template <Kind KV, int BS, class Flush = NoFlush, int ITERS = 0>
 __device__ __forceinline__ State mfma2_wave(const Params& p, int seq, int kvh, int hs, int first_it, int t1,
                                             int step, const Flush& flush = Flush(), int len = 0x7fffffff) {
   static_assert(BS >= 8 && (BS & (BS - 1)) == 0, "block size: a power of two >= 8");
@@ -552,7 +554,7 @@ __device__ __forceinline__ State mfma2_wave(const Params& p, int seq, int kvh, i
   // masked by the scores' valid-token count.
   int it = first_it;
   const Blocks<NB> cur_raw = table_raw<NB, BS>(p, table, it);
-  const Blocks<NB> nxt_raw = ONE ? cur_raw : table_raw<NB, BS>(p, table, it + step);
+  const Blocks<NB> nxt_raw = ITERS == 1 ? cur_raw : table_raw<NB, BS>(p, table, it + step);
   __builtin_amdgcn_sched_barrier(0);
   Blocks<NB> cur = table_check<NB, BS>(p, cur_raw, it, t1);
   Blocks<NB> nxt = table_check<NB, BS>(p, nxt_raw, it + step, t1);
@@ -577,6 +579,16 @@ __device__ __forceinline__ State mfma2_wave(const Params& p, int seq, int kvh, i
     load_v(vr, vbase0 + ib + (int64_t)max(pick(cur, vb), 0) * pool_stride);
     __builtin_amdgcn_sched_barrier(0);
   }
+  // ITERS 2: the second iteration's K/V in a set of their own
+  uint32_t kw2[ITERS == 2 ? 32 : 1];
+  u32x4 vr2[ITERS == 2 ? 8 : 1];
+  if constexpr (ITERS == 2) {
+    const int ib = in_block_bytes<BS, TPI, 2>(it + step);
+    load_k(kw2, kbase0 + ib + (int64_t)max(pick(nxt, kb), 0) * pool_stride);
+    __builtin_amdgcn_sched_barrier(0);
+    load_v(vr2, vbase0 + ib + (int64_t)max(pick(nxt, vb), 0) * pool_stride);
+    __builtin_amdgcn_sched_barrier(0);
+  }
   t1 = min(t1, len);
   // q's registers are opaque from here: otherwise the compiler packs them
   // inside the condition, and waits for q there, before K/V are issued
@@ -588,97 +600,113 @@ __device__ __forceinline__ State mfma2_wave(const Params& p, int seq, int kvh, i
 #pragma unroll
     for (int e2 = 0; e2 < 4; ++e2) qb[s][e2] = qlo[4 * s + e2] | (qhi[4 * s + e2] << 16);
 
-#pragma unroll 1
-  for (; it < t1; it += step) {
-    if constexpr (Flush::kActive) {
-      if (it != first_it && it % flush.part_tokens == 0) {   // a partition ends: its partials out, state afresh
-        flush(st, it / flush.part_tokens - 1);
-        st.init();
+  // One iteration at token it on (kwA, vrA); with reload, their K/V are
+  // then loaded with the iteration of table entries ld (in-block offset
+  // ib_ld).
+  auto iterate = [&](uint32_t (&kwA)[32], u32x4 (&vrA)[8], const Blocks<NB>& c, const Blocks<NB>& ld,
+                     int ib_ld, bool reload) {
+      // ---- q.k: 2 tiles (token i of each pair) x 4 MFMA steps ----
+      f4 s[2] = {f4{0.f, 0.f, 0.f, 0.f}, f4{0.f, 0.f, 0.f, 0.f}};
+  #pragma unroll
+      for (int sk = 0; sk < 4; ++sk) {
+        uint32_t w[8];                              // rows 32 sk + 4 e + kg
+        if constexpr (kK8) {
+  #pragma unroll
+          for (int e2 = 0; e2 < 4; ++e2) k8_pair(kwA[8 * sk + 2 * e2], kwA[8 * sk + 2 * e2 + 1], odd, w[2 * e2], w[2 * e2 + 1]);
+        } else {
+  #pragma unroll
+          for (int e = 0; e < 8; ++e) w[e] = kwA[8 * sk + e];
+        }
+        uint32_t a[2][4];
+  #pragma unroll
+        for (int e2 = 0; e2 < 4; ++e2) {
+          a[0][e2] = __builtin_amdgcn_perm(w[2 * e2 + 1], w[2 * e2], 0x05040100u);  // first token
+          a[1][e2] = __builtin_amdgcn_perm(w[2 * e2 + 1], w[2 * e2], 0x07060302u);  // second token
+        }
+  #pragma unroll
+        for (int i = 0; i < 2; ++i) s[i] = mma<KV>(a[i][0], a[i][1], a[i][2], a[i][3], qb[sk], s[i]);
       }
-    }
-    const Blocks<NB> nn = ONE ? cur : table_blocks<NB, BS>(p, table, it + 2 * step, t1);
-    const int ib_next = in_block_bytes<BS, TPI, 2>(it + step);
+      // the next iteration's loads are issued whether or not it exists (a
+      // missing one reads block 0): under a condition the compiler would
+      // wait for them, too, before this iteration's V is used
+      if (reload) load_k(kwA, kbase0 + ib_ld + (int64_t)max(pick(ld, kb), 0) * pool_stride);
 
-    // ---- q.k: 2 tiles (token i of each pair) x 4 MFMA steps ----
-    f4 s[2] = {f4{0.f, 0.f, 0.f, 0.f}, f4{0.f, 0.f, 0.f, 0.f}};
-#pragma unroll
-    for (int sk = 0; sk < 4; ++sk) {
-      uint32_t w[8];                              // rows 32 sk + 4 e + kg
-      if constexpr (kK8) {
-#pragma unroll
-        for (int e2 = 0; e2 < 4; ++e2) k8_pair(kw[8 * sk + 2 * e2], kw[8 * sk + 2 * e2 + 1], odd, w[2 * e2], w[2 * e2 + 1]);
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) w[e] = kw[8 * sk + e];
-      }
-      uint32_t a[2][4];
-#pragma unroll
-      for (int e2 = 0; e2 < 4; ++e2) {
-        a[0][e2] = __builtin_amdgcn_perm(w[2 * e2 + 1], w[2 * e2], 0x05040100u);  // first token
-        a[1][e2] = __builtin_amdgcn_perm(w[2 * e2 + 1], w[2 * e2], 0x07060302u);  // second token
-      }
-#pragma unroll
-      for (int i = 0; i < 2; ++i) s[i] = mma<KV>(a[i][0], a[i][1], a[i][2], a[i][3], qb[sk], s[i]);
-    }
-    // the next iteration's loads are issued whether or not it exists (a
-    // missing one reads block 0): under a condition the compiler would
-    // wait for them, too, before this iteration's V is used
-    if constexpr (!ONE) load_k(kw, kbase0 + ib_next + (int64_t)max(pick(nxt, kb), 0) * pool_stride);
-
-    // ---- softmax: lane (m, kg) owns head m, iteration tokens 8 kg + 2 r + i ----
-    const int ph_v = pick(cur, vb);
-    const int n_run = ph_v < 0 ? 0 : min(max(t1 - (it + 8 * kg), 0), 8);   // valid tokens of the run
-    float sc[2][4];
-    float mx = -INFINITY;
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
+      // ---- softmax: lane (m, kg) owns head m, iteration tokens 8 kg + 2 r + i ----
+      const int ph_v = pick(c, vb);
+      const int n_run = ph_v < 0 ? 0 : min(max(t1 - (it + 8 * kg), 0), 8);   // valid tokens of the run
+      float sc[2][4];
+      float mx = -INFINITY;
+  #pragma unroll
+      for (int i = 0; i < 2; ++i)
+  #pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          sc[i][r] = (2 * r + i < n_run) ? s[i][r] * p.qk_scale : -INFINITY;
+          mx = fmaxf(mx, sc[i][r]);
+        }
+      st.update_max(mx);
+      // bf16 weights carry 8 mantissa bits: a short or peaked softmax would
+      // miss 2e-3 by up to 2^-9 max|v|, so bf16 splits each weight into a
+      // bf16 high part and the bf16 rounding of the rest (relative 2^-18)
+      // and p.v takes both (f16 weights are exact enough alone)
+      u4v pb, pl;
+  #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        sc[i][r] = (2 * r + i < n_run) ? s[i][r] * p.qk_scale : -INFINITY;
-        mx = fmaxf(mx, sc[i][r]);
+        const float p0 = (2 * r < n_run) ? __builtin_amdgcn_exp2f(sc[0][r] - st.m_run) : 0.f;
+        const float p1 = (2 * r + 1 < n_run) ? __builtin_amdgcn_exp2f(sc[1][r] - st.m_run) : 0.f;
+        st.l_lane += p0 + p1;
+        pb[r] = Dot2<KV>::pack(p0, p1);
+        if constexpr (KV == Kind::BF16) {
+          const float h0 = __builtin_bit_cast(float, pb[r] << 16), h1 = __builtin_bit_cast(float, pb[r] & 0xffff0000u);
+          pl[r] = Dot2<KV>::pack(p0 - h0, p1 - h1);
+        }
       }
-    st.update_max(mx);
-    // bf16 weights carry 8 mantissa bits: a short or peaked softmax would
-    // miss 2e-3 by up to 2^-9 max|v|, so bf16 splits each weight into a
-    // bf16 high part and the bf16 rounding of the rest (relative 2^-18)
-    // and p.v takes both (f16 weights are exact enough alone)
-    u4v pb, pl;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const float p0 = (2 * r < n_run) ? __builtin_amdgcn_exp2f(sc[0][r] - st.m_run) : 0.f;
-      const float p1 = (2 * r + 1 < n_run) ? __builtin_amdgcn_exp2f(sc[1][r] - st.m_run) : 0.f;
-      st.l_lane += p0 + p1;
-      pb[r] = Dot2<KV>::pack(p0, p1);
-      if constexpr (KV == Kind::BF16) {
-        const float h0 = __builtin_bit_cast(float, pb[r] << 16), h1 = __builtin_bit_cast(float, pb[r] & 0xffff0000u);
-        pl[r] = Dot2<KV>::pack(p0 - h0, p1 - h1);
-      }
-    }
 
-    // ---- p.v: slots past t1 and holes may hold anything, NaN included ----
-    if (__builtin_amdgcn_ballot_w64(n_run < 8) != 0) {
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt) vr[dt] = keep_halves(vr[dt], n_run);
+      // ---- p.v: slots past t1 and holes may hold anything, NaN included ----
+      if (__builtin_amdgcn_ballot_w64(n_run < 8) != 0) {
+  #pragma unroll
+        for (int dt = 0; dt < 8; ++dt) vrA[dt] = keep_halves(vrA[dt], n_run);
+      }
+  #pragma unroll
+      for (int dt = 0; dt < 8; ++dt) {
+        st.o[dt] = mma<KV>(vrA[dt].x, vrA[dt].y, vrA[dt].z, vrA[dt].w, pb, st.o[dt]);
+        if constexpr (KV == Kind::BF16) st.o[dt] = mma<KV>(vrA[dt].x, vrA[dt].y, vrA[dt].z, vrA[dt].w, pl, st.o[dt]);
+      }
+      if (reload) load_v(vrA, vbase0 + ib_ld + (int64_t)max(pick(ld, vb), 0) * pool_stride);
+  };
+
+  if constexpr (ITERS > 0) {
+    static_assert(!Flush::kActive, "partition flushes stream whole partitions");
+    if (it < t1) {
+      iterate(kw, vr, cur, cur, 0, false);
+      it += step;
+      if constexpr (ITERS == 2)
+        if (it < t1) iterate(kw2, vr2, nxt, nxt, 0, false);
     }
-#pragma unroll
-    for (int dt = 0; dt < 8; ++dt) {
-      st.o[dt] = mma<KV>(vr[dt].x, vr[dt].y, vr[dt].z, vr[dt].w, pb, st.o[dt]);
-      if constexpr (KV == Kind::BF16) st.o[dt] = mma<KV>(vr[dt].x, vr[dt].y, vr[dt].z, vr[dt].w, pl, st.o[dt]);
+  } else {
+#pragma unroll 1
+    for (; it < t1; it += step) {
+      if constexpr (Flush::kActive) {
+        if (it != first_it && it % flush.part_tokens == 0) {   // a partition ends: its partials out, state afresh
+          flush(st, it / flush.part_tokens - 1);
+          st.init();
+        }
+      }
+      const Blocks<NB> nn = table_blocks<NB, BS>(p, table, it + 2 * step, t1);
+      iterate(kw, vr, cur, nxt, in_block_bytes<BS, TPI, 2>(it + step), true);
+      cur = nxt;
+      nxt = nn;
     }
-    if constexpr (!ONE) load_v(vr, vbase0 + ib_next + (int64_t)max(pick(nxt, vb), 0) * pool_stride);
-    cur = nxt;
-    nxt = nn;
   }
   return st;
 }
 
-template <Kind KV, Kind QK, int BS, class Flush = NoFlush, bool ONE = false>
+template <Kind KV, Kind QK, int BS, class Flush = NoFlush, int ITERS = 0>
 __device__ __forceinline__ State run_wave(const Params& p, int seq, int kvh, int hs, int first_it, int t1,
                                           int step, const Flush& flush = Flush(), int len = 0x7fffffff) {
   if constexpr (KV == Kind::FP8)
     return fp8_wave<QK, BS>(p, seq, kvh, hs, first_it, t1, step, flush, len);
   else
-    return mfma2_wave<KV, BS, Flush, ONE>(p, seq, kvh, hs, first_it, t1, step, flush, len);
+    return mfma2_wave<KV, BS, Flush, ITERS>(p, seq, kvh, hs, first_it, t1, step, flush, len);
 }
 
 // A wavefront that ran a whole split-K partition alone writes its
@@ -806,7 +834,7 @@ __device__ __forceinline__ void partitions_per_wave(const Params& p, int seq, in
 // the range is [t0, min(t1, len)), len applied after the wavefronts' first
 // loads; a partition past the end (len <= t0, the same for the whole
 // workgroup) returns then, writing nothing.
-template <Kind KV, Kind QK, Kind PO, int NW, bool FINAL, int BS = 16, bool LATE = false, bool ONE = false>
+template <Kind KV, Kind QK, Kind PO, int NW, bool FINAL, int BS = 16, bool LATE = false, int ITERS = 0>
 __device__ __forceinline__ void decode_workgroup(const Params& p, int seq, int kvh, int hs, int part, int t0,
                                                  int t1, float* s_acc, float* s_m, float* s_l,
                                                  int len = 0x7fffffff) {
@@ -814,7 +842,7 @@ __device__ __forceinline__ void decode_workgroup(const Params& p, int seq, int k
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
   const int lane = tid % kWave;
-  const State st = run_wave<KV, QK, BS, NoFlush, ONE>(p, seq, kvh, hs, t0 + wave * TPI, t1, NW * TPI, NoFlush(), len);
+  const State st = run_wave<KV, QK, BS, NoFlush, ITERS>(p, seq, kvh, hs, t0 + wave * TPI, t1, NW * TPI, NoFlush(), len);
   if (LATE && len <= t0) return;
   st.store(KV == Kind::FP8 ? p.v_scale : 1.f, lane & 15, lane >> 4, s_acc + wave * kHeads * kHead,
            s_m + wave * kHeads, s_l + wave * kHeads);
