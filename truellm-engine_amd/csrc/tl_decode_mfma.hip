@@ -57,7 +57,7 @@ __device__ __forceinline__ bool item_of(const Params& p, bool final, bool late_e
 // LATE: split-K items past the sequence's end exit after their first loads
 // (item_of's late_exit), for grids that fit the GPU in one round, where the
 // launch is a chain of round trips (length, table, K/V, partials) and the
-// loads of an exiting workgroup cost nothing.
+// few loads of an exiting workgroup cost less than a round trip.
 template <Kind QK, Kind PO, int NW, bool FINAL, int BS, bool LATE = false>
 __global__ __launch_bounds__(NW * kWave) void fp8_decode_kernel(Params p) {
   __shared__ __attribute__((aligned(16))) float s_acc[NW * mw::kHeads * mw::kHead];
